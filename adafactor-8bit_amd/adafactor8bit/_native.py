@@ -1,0 +1,113 @@
+"""ctypes binding of ``libadafactor8bit_amd.so`` (the HIP C ABI).
+
+The library is built in-tree by ``adafactor-8bit_amd/build.py`` for gfx950 and
+declared in ``include/adafactor8bit_amd.h``.  There is no fallback: every
+optimizer step runs through this library, and a missing or unloadable library
+raises immediately.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libadafactor8bit_amd.so")
+
+F32, BF16, F16 = 0, 1, 2
+MODE_NOCLIP, MODE_NORM, MODE_APPLY, MODE_LAG = 0, 1, 2, 3
+
+_c_vp = ctypes.c_void_p
+_c_i = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_u64 = ctypes.c_uint64
+_c_f = ctypes.c_float
+_c_d = ctypes.c_double
+
+
+class Tensor1D(ctypes.Structure):
+    """Mirror of ``a8_tensor1d``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
+                ("v_q", _c_vp), ("v_scale", _c_vp), ("v_min_log", _c_vp), ("v_buf", _c_vp),
+                ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
+                ("numel", _c_i64), ("sr_seed", _c_u64)]
+
+
+class TensorFull(ctypes.Structure):
+    """Mirror of ``a8_tensor_full``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("variance", _c_vp), ("m", _c_vp),
+                ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
+                ("numel", _c_i64)]
+
+
+_SIGS = {
+    "a8_last_error": (ctypes.c_char_p, []),
+    "a8_version": (ctypes.c_char_p, []),
+    "a8_set_qmap": (_c_i, [_c_vp, _c_vp]),
+    "a8_fused_update_1d": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_u64, _c_u64, _c_d, _c_d,
+                                  _c_f, _c_i, _c_f, _c_f, _c_f, _c_i64, _c_i, _c_i, _c_i, _c_i,
+                                  _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_vp]),
+    "a8_fused_update_1d_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(Tensor1D), _c_i, _c_vp,
+                                        _c_i64, _c_d, _c_d, _c_f, _c_i, _c_f, _c_f, _c_f, _c_i, _c_i,
+                                        _c_i, _c_i, _c_f, _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i,
+                                        _c_vp]),
+    "a8_table_bytes_1d": (_c_i64, [_c_i]),
+    "a8_fused_update_1d_full": (_c_i, [_c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                       _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,
+                                       _c_f, _c_f, _c_i, _c_vp]),
+    "a8_fused_update_1d_full_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(TensorFull), _c_i, _c_vp,
+                                             _c_i64, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_f, _c_i,
+                                             _c_f, _c_f, _c_i, _c_i, _c_vp]),
+    "a8_table_bytes_full": (_c_i64, [_c_i]),
+    "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
+}
+
+_LIB = None
+
+
+def lib():
+    """Load the library once; raise if it is missing (no CPU fallback exists)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"adafactor8bit: HIP library not found at {LIB_PATH}; build it with "
+                "`python adafactor-8bit_amd/build.py` (there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, what: str = ""):
+    if rc != 0:
+        msg = lib().a8_last_error().decode(errors="replace")
+        raise RuntimeError(f"adafactor8bit HIP call {what} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    """Device address of a tensor (None for None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    if dt == torch.float16:
+        return F16
+    raise TypeError(f"adafactor8bit: unsupported parameter dtype {dt}")
+
+
+def exported_symbols():
+    return sorted(_SIGS)

@@ -1,0 +1,659 @@
+"""Adafactor8Bit for MI355X: host side of the fused block-quantised optimizer step.
+
+Mirrors the reference optimizer's public interface (adafactor8bit/optimizer.py:
+``Adafactor8Bit.__init__`` 1313-1461, ``state_dict``/``load_state_dict``
+1463-1553, ``_init_group`` 1618-1864, ``step`` 1866-1938): the same keyword
+arguments and validation, the same per-parameter state keys, dtypes, shapes
+and padding, the same scalar preparation (bias correction, epsilon, alpha,
+weight decay).  The arithmetic of every step runs in the hand-written HIP
+library ``libadafactor8bit_amd.so`` (see ``_native.py``); there is no CPU or
+PyTorch fallback.  Quantised codes follow the reference's PyTorch numerics
+(optimizer.py:299-353, 504-532), so a run matches the reference's CPU results.
+
+Parameters that share a step counter and hyper-parameters are updated by one
+multi-tensor launch per group instead of one launch per parameter.
+"""
+import logging
+import math
+from typing import Any, Dict, Iterable, Optional, Tuple, Union
+
+import numpy as np
+import torch
+from torch import Tensor
+from torch.optim import Optimizer
+
+from . import _native as nat
+from . import _state as S
+
+__all__ = ["Adafactor8Bit"]
+
+logger = logging.getLogger(__name__)
+
+_LOG_QUANT_FLOOR = 1.17549435e-38
+_VALID_M_QUANT_TYPES = ("uf4", "uf8", "d4", "d8", "fp32")
+_VALID_V_QUANT_TYPES = ("al8", "al16", "fp32")
+_AL_FLOOR = -126.0   # min_log floor of the reference's AL quantiser (optimizer.py:299)
+
+_F32 = np.float32
+
+
+def _f32(x) -> float:
+    return float(_F32(x))
+
+
+class Adafactor8Bit(Optimizer):
+    """8-bit Adafactor / AdamW / CAME / RMSprop / SGD with block-quantised states.
+
+    Keyword arguments, defaults and semantics are those of the reference
+    ``Adafactor8Bit`` (adafactor8bit/optimizer.py:1176-1360).  ``use_cuda_kernel``
+    is accepted for compatibility; the step always runs on the HIP library and
+    parameters must live on a ROCm device.
+    """
+
+    def __init__(
+        self,
+        params: Iterable[Union[Tensor, Dict[str, Any]]],
+        lr: float = 1e-2,
+        beta1: Optional[float] = None,
+        beta2: Optional[float] = None,
+        beta2_decay: Optional[float] = -0.8,
+        beta3: Optional[float] = None,
+        eps_came: float = 1e-16,
+        eps: Tuple[Optional[float], float] = (1e-30, 1e-3),
+        weight_decay: float = 0.0,
+        d: float = 1.0,
+        maximize: bool = False,
+        relative_step: bool = True,
+        scale_parameter: bool = True,
+        factored: bool = True,
+        quantize: bool = True,
+        block_size: int = 2048,
+        m_block_size: int = 256,
+        m_quant_type: str = "uf8",
+        v_quant_type: str = "al8",
+        c_quant_type: Optional[str] = None,
+        min_8bit_size: int = 4096,
+        use_cuda_kernel: bool = True,
+        stochastic_round_writeback: bool = False,
+        apollo_rank: int = 0,
+        apollo_update_proj_gap: int = 200,
+        apollo_scale_type: str = "channel",
+        apollo_scale: float = 1.0,
+        apollo_scale_front: bool = False,
+        apollo_eps: float = 1e-6,
+        apollo_factorize: bool = False,
+        apollo_cache_proj: bool = False,
+        enable_fira_for_apollo: bool = True,
+        scale_weight_decay: bool = True,
+        enable_fira_for_adafactor: bool = False,
+        fira_margin: float = 0.01,
+        lag_norm: bool = False,
+        momentum_only_1d: Optional[bool] = None,
+        bias_correction: Optional[bool] = None,
+        warmup_multiplier: float = 0.0,
+    ):
+        # argument validation: optimizer.py:1362-1432 (same conditions and messages)
+        if lr < 0.0:
+            raise ValueError(f"Invalid lr: {lr}, must be >= 0.0")
+        if beta1 is not None and (beta1 < 0.0 or beta1 >= 1.0):
+            raise ValueError(f"Invalid beta1: {beta1}, must be in [0.0, 1.0)")
+        if beta2_decay is not None and beta2_decay > 0.0:
+            raise ValueError(f"Invalid beta2_decay: {beta2_decay}, must be <= 0.0")
+        if beta2 is None and beta2_decay is None:
+            if relative_step:
+                raise ValueError(
+                    "When `beta2` and `beta2_decay` are both None, `relative_step` must be False. "
+                    "Please set `relative_step=False` for standard SGD, or specify `beta2`/`beta2_decay` "
+                    "to use adaptive optimizers.")
+            if apollo_rank > 0:
+                raise ValueError("APOLLO requires a second-moment estimate (`beta2` or `beta2_decay`), "
+                                 "but both are currently None.")
+            if beta3 is not None:
+                raise ValueError("CAME (`beta3`) requires both `beta1` and `beta2`, but `beta2` is "
+                                 "currently None.")
+        eps1, eps2 = eps
+        if eps1 is None:
+            eps1 = 1e-30
+        if eps1 < 0.0:
+            raise ValueError(f"Invalid eps1: {eps1}, must be >= 0.0")
+        if eps2 < 0.0:
+            raise ValueError(f"Invalid eps2: {eps2}, must be >= 0.0")
+        if d < 0.0:
+            raise ValueError(f"Invalid d: {d}, must be >= 0.0. d=0 disables RMS clipping.")
+        if weight_decay < 0.0:
+            raise ValueError(f"Invalid weight_decay: {weight_decay}, must be >= 0.0")
+        if beta2 is not None and (beta2 < 0.0 or beta2 >= 1.0):
+            raise ValueError(f"Invalid beta2: {beta2}, must be in [0.0, 1.0)")
+        if quantize and (block_size < 128 or block_size % 128 != 0):
+            raise ValueError(f"block_size must be >= 128 and a multiple of 128, but got {block_size}.")
+        if m_block_size < 32 or m_block_size % 4 != 0:
+            raise ValueError(f"m_block_size must be a multiple of 4 and >= 32, but got {m_block_size}.")
+        if m_quant_type not in _VALID_M_QUANT_TYPES:
+            raise ValueError(f"m_quant_type must be one of {_VALID_M_QUANT_TYPES}, got '{m_quant_type}'.")
+        if v_quant_type not in _VALID_V_QUANT_TYPES:
+            raise ValueError(f"v_quant_type must be one of {_VALID_V_QUANT_TYPES}, got '{v_quant_type}'.")
+        if c_quant_type is not None and c_quant_type not in _VALID_V_QUANT_TYPES:
+            raise ValueError(f"c_quant_type must be one of {_VALID_V_QUANT_TYPES} or None, "
+                             f"got '{c_quant_type}'.")
+        if quantize and beta1 is not None and m_quant_type != "fp32" and block_size % m_block_size != 0:
+            raise ValueError(
+                f"For the fused 1D kernel, block_size must be a multiple of m_block_size "
+                f"(got block_size={block_size}, m_block_size={m_block_size}).")
+        if apollo_rank > 0 and apollo_scale_type not in ("channel", "tensor"):
+            raise ValueError(f"apollo_scale_type must be 'channel' or 'tensor', got {apollo_scale_type}.")
+        if apollo_scale < 0.0:
+            raise ValueError(f"Invalid apollo_scale: {apollo_scale}, must be >= 0.0")
+        if fira_margin < 0.0:
+            raise ValueError(f"Invalid fira_margin: {fira_margin}, must be >= 0.0")
+        if beta3 is not None:
+            if beta3 < 0.0 or beta3 >= 1.0:
+                raise ValueError(f"Invalid beta3: {beta3}, must be in [0.0, 1.0)")
+            if beta1 is None:
+                raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update "
+                                 "instability.")
+            if apollo_rank == 0 and not factored:
+                raise ValueError("CAME (beta3) requires factored=True (2D row/col factorization). It is "
+                                 "not supported for 1D full-rank paths.")
+
+        defaults = dict(
+            lr=lr, beta1=beta1, beta2=beta2, beta2_decay=beta2_decay, beta3=beta3, eps_came=eps_came,
+            eps=eps, weight_decay=weight_decay, d=d, maximize=maximize,
+            relative_step=relative_step, scale_parameter=scale_parameter, factored=factored,
+            quantize=quantize, block_size=block_size, m_block_size=m_block_size,
+            m_quant_type=m_quant_type, v_quant_type=v_quant_type, c_quant_type=c_quant_type,
+            min_8bit_size=min_8bit_size, use_cuda_kernel=use_cuda_kernel,
+            stochastic_round_writeback=stochastic_round_writeback,
+            apollo_rank=apollo_rank, apollo_update_proj_gap=apollo_update_proj_gap,
+            apollo_scale_type=apollo_scale_type, apollo_scale=apollo_scale,
+            apollo_scale_front=apollo_scale_front, apollo_eps=apollo_eps,
+            apollo_factorize=apollo_factorize, apollo_cache_proj=apollo_cache_proj,
+            enable_fira_for_apollo=enable_fira_for_apollo,
+            scale_weight_decay=scale_weight_decay,
+            enable_fira_for_adafactor=enable_fira_for_adafactor, fira_margin=fira_margin,
+            lag_norm=lag_norm, momentum_only_1d=momentum_only_1d, bias_correction=bias_correction,
+            warmup_multiplier=warmup_multiplier,
+        )
+        super().__init__(params, defaults)
+        self._apollo_seed_counter = 1
+        self._sr_seed_counter = 1
+        self._ws = {}   # device workspaces (tensor tables, norm buffers, v_buf)
+
+    # ------------------------------------------------------------------ checkpoint
+    def state_dict(self):
+        sd = super().state_dict()
+        sd["_apollo_seed_counter"] = self._apollo_seed_counter
+        sd["_sr_seed_counter"] = self._sr_seed_counter
+        return sd
+
+    def load_state_dict(self, state_dict):
+        """optimizer.py:1467-1553: keep quantised/fp32 state dtypes, restore type tags."""
+        state_dict = state_dict.copy()
+        state_dict["state"] = {
+            idx: ({k: v for k, v in st.items() if k not in ("m", "m_q", "m_scale")}
+                  if isinstance(st, dict) and "apollo_seed" in st else st)
+            for idx, st in state_dict.get("state", {}).items()
+        }
+        old_vqt, old_mqt, old_cqt, saved_tensors = {}, {}, {}, {}
+        for idx, st in state_dict.get("state", {}).items():
+            if isinstance(st, dict):
+                old_vqt[idx] = st.get("v_quant_type", "al8")
+                old_mqt[idx] = st.get("m_quant_type", "uf8")
+                old_cqt[idx] = st.get("c_quant_type", old_vqt[idx])
+                saved_tensors[idx] = {k: v for k, v in st.items() if torch.is_tensor(v) and k != "step"}
+        saved_ids = [i for g in state_dict.get("param_groups", []) for i in g.get("params", [])]
+        self._apollo_seed_counter = state_dict.get("_apollo_seed_counter", 0)
+        self._sr_seed_counter = state_dict.get("_sr_seed_counter", 0)
+        sr_policy = [g.get("stochastic_round_writeback", False) for g in self.param_groups]
+        sr_missing = [("stochastic_round_writeback" not in sg) if isinstance(sg, dict) else True
+                      for sg in state_dict.get("param_groups", [])]
+        super().load_state_dict(state_dict)
+        if len(self.param_groups) == len(sr_missing):
+            for g, miss, pol in zip(self.param_groups, sr_missing, sr_policy):
+                if miss:
+                    g["stochastic_round_writeback"] = pol
+        cur = [p for g in self.param_groups for p in g["params"]]
+        if len(saved_ids) == len(cur):
+            id_map = dict(zip(saved_ids, cur))
+            for sid, tensors in saved_tensors.items():
+                p = id_map.get(sid)
+                if p is None or p not in self.state:
+                    continue
+                st = self.state[p]
+                for k, v in tensors.items():
+                    st[k] = v.detach().to(device=p.device, dtype=v.dtype, copy=True).contiguous()
+        i = 0
+        for g in self.param_groups:
+            for p in g["params"]:
+                if p in self.state:
+                    st = self.state[p]
+                    st["v_quant_type"] = old_vqt.get(i, "al8")
+                    st["m_quant_type"] = old_mqt.get(i, "uf8")
+                    st["c_quant_type"] = old_cqt.get(i, st["v_quant_type"])
+                    s = st.get("step")
+                    if torch.is_tensor(s):
+                        st["step"] = int(s)
+                i += 1
+        self._ws.clear()
+
+    def _warmup_allocator(self):
+        """optimizer.py:1592-1616: optional allocate-and-free of a large block."""
+        mult = self.param_groups[0].get("warmup_multiplier", 0.0)
+        if mult <= 0.0 or not torch.cuda.is_available():
+            return
+        biggest = {}
+        for g in self.param_groups:
+            for p in g["params"]:
+                if p.is_cuda and p.numel() > biggest.get(p.device, 0):
+                    biggest[p.device] = p.numel()
+        for dev, n in biggest.items():
+            tmp = torch.empty(int(n * mult), device=dev, dtype=torch.float32)
+            del tmp
+
+    # ------------------------------------------------------------------ state init
+    def _init_group(self, group, params_with_grad, grads, states):
+        S.init_group(self, group, params_with_grad, grads, states)
+
+    # ------------------------------------------------------------------ step
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        if not hasattr(self, "_allocator_warmed_up"):
+            self._warmup_allocator()
+            self._allocator_warmed_up = True
+        for group in self.param_groups:
+            params, grads, states = [], [], []
+            self._init_group(group, params, grads, states)
+            if not params:
+                continue
+            for p in params:
+                if not p.is_cuda:
+                    raise RuntimeError("adafactor8bit (MI355X build): parameters must be on a ROCm "
+                                       "device; there is no CPU path")
+            S.ensure_qmap(params[0].device)
+            sr_on = group.get("stochastic_round_writeback", False)
+            for p, st in zip(params, states):
+                if sr_on and p.dtype in (torch.bfloat16, torch.float16) and "sr_seed" not in st:
+                    st["sr_seed"] = self._sr_seed_counter
+                    self._sr_seed_counter += 1
+            self._step_group(group, params, grads, states)
+        return loss
+
+    # ------------------------------------------------------------------ dispatch
+    def _step_group(self, group, params, grads, states):
+        apollo_rank = group.get("apollo_rank", 0)
+        batches: Dict[tuple, list] = {}
+        for p, g, st in zip(params, grads, states):
+            if apollo_rank > 0 and "apollo_seed" in st:
+                raise NotImplementedError("APOLLO path is not available in this build yet")
+            plan = _plan_param(p, g, st, group)
+            key = plan.batch_key()
+            if key is None:
+                _run_single(self, plan)
+            else:
+                batches.setdefault(key, []).append(plan)
+        for key, plans in batches.items():
+            _run_batch(self, key, plans)
+
+
+# ====================================================================== planning
+class _Plan:
+    """Host-side scalar preparation of one parameter's step (optimizer.py:1944-2040)."""
+    __slots__ = ("p", "g", "st", "group", "path", "step", "beta_val", "alpha_val", "alpha_t",
+                 "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
+                 "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
+                 "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize")
+
+    def batch_key(self):
+        if self.path not in ("q1d", "f1d"):
+            return None
+        if self.alpha_t is not None or self.decay_t is not None:
+            return None
+        if self.d > 0 or self.fira or self.sr or self.maximize:
+            return None
+        if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
+            return None
+        return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.vqt,
+                self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
+                self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
+                self.alpha_val, self.decay_val)
+
+
+def _plan_param(p, grad, st, group) -> _Plan:
+    P = _Plan()
+    P.p, P.st, P.group = p, st, group
+    beta1, beta2, beta2_decay, beta3 = group.get("beta1"), group["beta2"], group["beta2_decay"], group.get("beta3")
+    eps1, eps2 = group["eps"]
+    eps1 = 1e-30 if eps1 is None else eps1
+    d = group["d"]
+    factored = group.get("factored", True)
+    sgd = beta2 is None and beta2_decay is None
+    full_rank = grad.dim() < 2 or not factored or sgd
+    P.eps1, P.eps2 = eps1, eps2
+    P.eps_sq = max(eps1 * eps1, _LOG_QUANT_FLOOR)
+    P.log_eps_sq = math.log2(P.eps_sq)
+    P.adam_denom = (not factored) and (beta2 is not None) and (beta3 is None)
+    P.eps_d = eps1 if P.adam_denom else 0.0
+    P.eps_g = eps1 if not P.adam_denom else 0.0
+    mo = group.get("momentum_only_1d")
+    P.mom_only = (not P.adam_denom) if mo is None else bool(mo)
+    P.maximize = group["maximize"]
+    g = grad if grad.is_contiguous() else grad.contiguous()
+    if P.maximize:
+        g = g.neg()
+    P.g = g
+    P.quant = st.get("is_quantized", False)
+    P.vqt = st.get("v_quant_type", "al8")
+    P.bs = st.get("block_size", group.get("block_size", 2048))
+    P.has_m = beta1 is not None
+    P.mbs = st.get("m_block_size", group.get("m_block_size", 256)) if P.has_m else 0
+    P.mqt = st.get("m_quant_type", "uf8") if P.has_m else "uf8"
+    P.beta1 = beta1
+    P.d = d
+    P.fira = group.get("enable_fira_for_adafactor", False)
+    P.margin = group.get("fira_margin", 0.01)
+    P.lag = group.get("lag_norm", False)
+
+    step = st["step"] + 1
+    st["step"] = step
+    P.step = step
+    if sgd:
+        P.beta_val = 0.0
+    elif beta2 is not None:
+        P.beta_val = 1.0 - beta2
+    else:
+        P.beta_val = math.pow(step, beta2_decay)
+
+    # alpha / rho: optimizer.py:832-856 (+ bias correction 2020-2030)
+    lr = group["lr"]
+    P.alpha_t = P.rho_t = None
+    relative_step, scale_parameter = group["relative_step"], group["scale_parameter"]
+    if isinstance(lr, Tensor):
+        rho_t = lr.to(device=p.device, dtype=torch.float32)
+        if relative_step:
+            rho_t = torch.minimum(torch.tensor(float(step), device=p.device).rsqrt(), rho_t)
+        P.rho_t, P.rho_val = rho_t, None
+    else:
+        P.rho_val = _f32(min(lr, 1.0 / math.sqrt(step)) if relative_step else lr)
+    if scale_parameter:
+        rms = torch.linalg.vector_norm(p, ord=2, dtype=torch.float32) / math.sqrt(p.numel())
+        rho = P.rho_t if P.rho_t is not None else P.rho_val
+        P.alpha_t = torch.clamp(rms, min=eps2) * rho
+        P.alpha_val = None
+    elif P.rho_t is not None:
+        P.alpha_t, P.alpha_val = P.rho_t, None
+    else:
+        P.alpha_val = P.rho_val
+    if beta1 is not None and not relative_step and not sgd:
+        bc_on = P.adam_denom if group.get("bias_correction") is None else group.get("bias_correction")
+        if bc_on:
+            bc1 = 1.0 - beta1 ** step
+            if beta2 is not None:
+                bc2 = 1.0 - beta2 ** step
+                fac = math.sqrt(bc2) / bc1
+                if P.alpha_t is not None:
+                    P.alpha_t = P.alpha_t * fac
+                else:
+                    P.alpha_val = _f32(_F32(P.alpha_val) * _F32(fac))
+                if P.adam_denom:
+                    P.eps_d = eps1 * math.sqrt(bc2)
+            else:
+                if P.alpha_t is not None:
+                    P.alpha_t = P.alpha_t / bc1
+                else:
+                    P.alpha_val = _f32(_F32(P.alpha_val) / _F32(bc1))
+
+    # weight decay: optimizer.py:2032-2039 (fused into the kernels as p*decay)
+    wd = group["weight_decay"]
+    P.sr = group.get("stochastic_round_writeback", False) and p.dtype in (torch.bfloat16, torch.float16)
+    P.decay_val, P.decay_t = None, None
+    if wd != 0:
+        use_alpha = group.get("scale_weight_decay", True)
+        if use_alpha:
+            if P.alpha_t is not None:
+                P.decay_t = 1.0 - (P.alpha_t * wd)
+            else:
+                P.decay_val = _f32(_F32(1.0) - _F32(_F32(P.alpha_val) * _F32(wd)))
+        else:
+            if P.rho_t is not None:
+                P.decay_t = 1.0 - (P.rho_t * wd)
+            else:
+                P.decay_val = _f32(_F32(1.0) - _F32(_F32(P.rho_val) * _F32(wd)))
+
+    if sgd:
+        P.path = "sgd"
+    elif full_rank:
+        if P.quant and P.vqt != "fp32":
+            P.path = "q1d" if (not P.has_m or P.mqt != "fp32") else "q1d_fp32m"
+        else:
+            P.path = "f1d" if (not P.has_m or not P.quant or P.mqt == "fp32") else "f1d_qm"
+    else:
+        P.path = "factored"
+    return P
+
+
+def _dev_scalar(opt, device, key, value):
+    ws = opt._ws.setdefault((device, "scalars"), {})
+    t = ws.get(key)
+    if t is None:
+        t = torch.empty((), dtype=torch.float32, device=device)
+        ws[key] = t
+    t.fill_(value)
+    return t
+
+
+def _v_buf(opt, device, numel):
+    key = (device, "v_buf")
+    b = opt._ws.get(key)
+    if b is None or b.numel() < numel:
+        b = torch.empty(numel, dtype=torch.float32, device=device)
+        opt._ws[key] = b
+    return b[:numel]
+
+
+def _norm_buf(opt, device):
+    key = (device, "norm_buf")
+    b = opt._ws.get(key)
+    if b is None:
+        b = torch.zeros(1, dtype=torch.float32, device=device)
+        opt._ws[key] = b
+    else:
+        b.zero_()
+    return b
+
+
+def _alpha_args(P):
+    if P.alpha_t is not None:
+        a = P.alpha_t.reshape(()).to(torch.float32)
+        return a, 0.0
+    return None, P.alpha_val
+
+
+def _decay_args(P):
+    if P.decay_t is not None:
+        return P.decay_t.reshape(()).to(torch.float32), 1.0, 1
+    if P.decay_val is not None:
+        return None, P.decay_val, 1
+    return None, 1.0, 0
+
+
+def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, v_buf=None):
+    L = nat.lib()
+    st, p, g = P.st, P.p, P.g
+    dec_t, dec_val, has_dec = _decay_args(P)
+    if P.path == "q1d":
+        vq = st["variance_q"]
+        m_q = st["m_q"] if P.has_m else None
+        m_scale = st["m_scale"] if P.has_m else None
+        m_bits = S.m_bits(P.mqt) if P.has_m else 0
+        m_mode = S.m_mode(P.mqt) if P.has_m else 0
+        rc = L.a8_fused_update_1d(
+            mode, int(P.sr), nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(m_q),
+            nat.ptr(m_scale), nat.ptr(vq), nat.ptr(st["variance_scale"]), nat.ptr(st["variance_min_log"]),
+            nat.ptr(v_buf), nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
+            int(st.get("sr_seed", 0)), int(P.step), P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_d,
+            int(P.adam_denom), _AL_FLOOR, P.eps_g, P.eps_sq, p.numel(), P.bs,
+            P.mbs if P.has_m else P.bs, m_bits, m_mode, P.d, 16 if P.vqt == "al16" else 8,
+            int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
+            nat.stream_of(p.device))
+        nat.check(rc, "a8_fused_update_1d")
+        if mode != nat.MODE_APPLY:
+            _block_view(st, "variance", P.bs)
+    else:
+        m = st.get("m") if P.has_m else None
+        if m is not None and not m.is_contiguous():
+            m = m.contiguous()
+            st["m"] = m
+        var = st["variance"]
+        if not var.is_contiguous():
+            var = var.contiguous()
+            st["variance"] = var
+        rc = L.a8_fused_update_1d_full(
+            mode, nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(var), nat.ptr(m),
+            nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
+            P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
+            p.numel(), P.d, int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
+            nat.stream_of(p.device))
+        nat.check(rc, "a8_fused_update_1d_full")
+
+
+def _block_view(st, prefix, bs):
+    """After a re-quantisation the reference stores V codes as [nblocks, block_size]
+    (the block view returned by _log_quantize_nonneg, optimizer.py:302-324)."""
+    q = st[f"{prefix}_q"]
+    if q.dim() == 1:
+        st[f"{prefix}_q"] = q.view(-1, bs)
+
+
+def _fira_apply(opt, st, norm_buf, alpha_t, alpha_val, margin, device):
+    """NORM -> Fira -> APPLY glue of _apply_fira_cuda (optimizer.py:785-793)."""
+    if alpha_t is None:
+        alpha_t = _dev_scalar(opt, device, "fira_alpha", alpha_val)
+    prev = st.get("fira_prev_norm")
+    out = torch.empty(3, dtype=torch.float32, device=device)
+    if prev is not None and not torch.is_tensor(prev):
+        prev = torch.tensor(prev, dtype=torch.float32, device=device)
+    rc = nat.lib().a8_fira_scalar(nat.ptr(norm_buf), nat.ptr(prev), nat.ptr(alpha_t), nat.ptr(out), 1,
+                                  int(prev is not None), 1, _f32(1.0 + margin), nat.stream_of(device))
+    nat.check(rc, "a8_fira_scalar")
+    st["fira_prev_norm"] = out[1].view(())
+    return out[0].view(()), out[2].view(1)
+
+
+def _fira_scale_only(opt, st, x, margin, device, key):
+    prev = st.get(key)
+    out = torch.empty(3, dtype=torch.float32, device=device)
+    x1 = x.reshape(1).to(torch.float32)
+    if prev is not None and not torch.is_tensor(prev):
+        prev = torch.tensor(prev, dtype=torch.float32, device=device)
+    rc = nat.lib().a8_fira_scalar(nat.ptr(x1), nat.ptr(prev), None, nat.ptr(out), 1,
+                                  int(prev is not None), 0, _f32(1.0 + margin), nat.stream_of(device))
+    nat.check(rc, "a8_fira_scalar")
+    st[key] = out[1].view(x.shape if prev is not None else ())
+    return out[0].view(())
+
+
+def _run_single(opt, P):
+    if P.path not in ("q1d", "f1d"):
+        raise NotImplementedError(f"adafactor8bit: '{P.path}' update path is not available in this build yet")
+    alpha_t, alpha_val = _alpha_args(P)
+    dev = P.p.device
+    need_norm = P.d > 0.0 or P.fira
+    if not need_norm:
+        _launch_1d(opt, P, nat.MODE_NOCLIP, alpha_t, alpha_val)
+        return
+    st = P.st
+    if P.lag:  # _dispatch_cuda_clip, lag branch (optimizer.py:1057-1073)
+        if "prev_update_norm" not in st:
+            st["prev_update_norm"] = torch.zeros(1, device=dev, dtype=torch.float32)
+        if P.fira and st.get("lag_fira_scale") is not None:
+            if alpha_t is None:
+                alpha_t = _dev_scalar(opt, dev, "lag_alpha", alpha_val)
+            alpha_t = alpha_t * st["lag_fira_scale"]
+        nb = _norm_buf(opt, dev)
+        _launch_1d(opt, P, nat.MODE_LAG, alpha_t, alpha_val, norm_buf=nb, prev_norm=st["prev_update_norm"])
+        curr = nb.sqrt()
+        st["prev_update_norm"] = curr
+        if P.fira:
+            st["lag_fira_scale"] = _fira_scale_only(opt, st, curr.view(()), P.margin, dev, "fira_prev_norm")
+        return
+    nb = _norm_buf(opt, dev)
+    vb = _v_buf(opt, dev, P.p.numel()) if P.path == "q1d" else None
+    _launch_1d(opt, P, nat.MODE_NORM, None, 0.0, norm_buf=nb, v_buf=vb)
+    if P.fira:
+        alpha_t, nb = _fira_apply(opt, st, nb, alpha_t, alpha_val, P.margin, dev)
+    _launch_1d(opt, P, nat.MODE_APPLY, alpha_t, alpha_val, norm_buf=nb, v_buf=vb)
+
+
+def _run_batch(opt, key, plans):
+    path = key[0]
+    if len(plans) == 1:
+        _run_single(opt, plans[0])
+        return
+    P0 = plans[0]
+    dev = P0.p.device
+    L = nat.lib()
+    n = len(plans)
+    ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr()) for pl in plans)
+    cache_key = (key, ptrs)
+    ws = opt._ws.setdefault((dev, "tables"), {})
+    ent = ws.get(cache_key)
+    upload = 0
+    if ent is None:
+        if path == "q1d":
+            arr = (nat.Tensor1D * n)()
+            for i, pl in enumerate(plans):
+                st = pl.st
+                arr[i] = nat.Tensor1D(
+                    pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(st.get("m_q") if pl.has_m else None),
+                    nat.ptr(st.get("m_scale") if pl.has_m else None), st["variance_q"].data_ptr(),
+                    st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), None, None, None,
+                    None, None, pl.p.numel(), int(st.get("sr_seed", 0)))
+            nbytes = L.a8_table_bytes_1d(n)
+        else:
+            arr = (nat.TensorFull * n)()
+            for i, pl in enumerate(plans):
+                st = pl.st
+                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), st["variance"].data_ptr(),
+                                        nat.ptr(st.get("m") if pl.has_m else None), None, None, None,
+                                        None, pl.p.numel())
+            nbytes = L.a8_table_bytes_full(n)
+        table = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
+        # state tensors referenced by the table must stay the same objects
+        refs = None
+        ent = [arr, table, nbytes, refs]
+        if len(ws) > 64:
+            ws.clear()
+        ws[cache_key] = ent
+        upload = 1
+    else:
+        refs = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+        if refs != ent[3]:
+            ws.pop(cache_key)
+            return _run_batch(opt, key, plans)
+    arr, table, nbytes, _ = ent
+    has_dec = int(P0.decay_val is not None)
+    dec_val = P0.decay_val if has_dec else 1.0
+    strm = nat.stream_of(dev)
+    if path == "q1d":
+        rc = L.a8_fused_update_1d_multi(
+            nat.MODE_NOCLIP, 0, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,
+            P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
+            S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
+            16 if P0.vqt == "al16" else 8, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
+            float(dec_val), has_dec, upload, strm)
+        nat.check(rc, "a8_fused_update_1d_multi")
+        for pl in plans:
+            _block_view(pl.st, "variance", pl.bs)
+        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+    else:
+        rc = L.a8_fused_update_1d_full_multi(
+            nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom),
+            P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, upload,
+            strm)
+        nat.check(rc, "a8_fused_update_1d_full_multi")
+        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]

@@ -1,0 +1,33 @@
+// Internal glue between the kernels and the C ABI: error state, checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string>
+#include <vector>
+
+#include "../../include/adafactor8bit_amd.h"
+
+namespace a8 {
+
+void set_error_msg(const char* msg);
+
+inline int set_error(int code, const char* msg) {
+  set_error_msg(msg);
+  return code;
+}
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof buf, "%s launch failed: %s", what, hipGetErrorString(e));
+    set_error_msg(buf);
+    return A8_ERR_HIP;
+  }
+  return 0;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace a8

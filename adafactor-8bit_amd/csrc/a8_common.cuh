@@ -1,0 +1,192 @@
+// Device helpers shared by the adafactor8bit MI355X kernels (gfx950, wave64).
+//
+// Numerics contract ("reference numerics"): every value that is stored as a
+// quantised code is decided exactly as the reference's PyTorch path decides it
+// (adafactor8bit/optimizer.py:299-353, 504-532, 690-700):
+//   * EMA      lerp(s, e, w) = fma(w, e - s, s) for |w| < 0.5, else fma(w - 1, e - s, e)
+//   * AL code  q = clamp(rint(((log2(max(v,1e-38)) - lmin) / s) * (L-2)) + 1, 1, L-1), q=0 <=> v=0
+//   * UF code  q = clamp(rint((m / absmax) * 2^(b-1)), -2^(b-1), 2^(b-1)-1) + 2^(b-1)
+// with IEEE float32 division and correctly rounded log2 / exp2.  A fast path
+// (hardware v_log_f32 / v_rcp_f32) decides a code whenever the rounding
+// argument lies farther from a half-integer than a proven error margin; the
+// rare remaining elements are recomputed exactly (double-precision log2, IEEE
+// division).  Parameters are not re-quantised, so the update direction may use
+// the hardware sqrt/rcp (<= 2 ulp) without changing any code.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace a8 {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kFltMin = 1.17549435e-38f;   // FP32 smallest normal
+constexpr float kLogClampIn = 1e-38f;        // clamp(min=1e-38) before log2 (optimizer.py:309)
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float lerp_ref(float s, float e, float w) {
+  // torch.lerp on CPU (vectorised): fma(coeff, e - s, base)
+  return (fabsf(w) < 0.5f) ? __builtin_fmaf(w, e - s, s) : __builtin_fmaf(w - 1.0f, e - s, e);
+}
+
+__device__ __forceinline__ float log2_exact(float x) {   // x > 0, correctly rounded to fp32
+  return (float)::log2((double)x);
+}
+
+__device__ __forceinline__ float exp2_exact(float x) {
+  return (float)::exp2((double)x);
+}
+
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+
+// Non-finite gradients are treated as zero (the reference's GPU kernels do the
+// same, kernels.cu:43-46; its CPU path has no defined result for them).
+__device__ __forceinline__ float scrub(float g) {
+  return (__builtin_isfinite(g)) ? g : 0.0f;
+}
+
+// Per-block constants of the AL refit.
+struct ALFit {
+  float lmin;     // new min_log
+  float s;        // new scale
+  float rs;       // ~1/s
+  float kmar;     // margin slope: (L-2) * rs * 2^-20
+};
+
+// Refit from the block's max v and min non-zero v (optimizer.py:308-318):
+// l = log2(max(v, 1e-38)); lmax over all, lmin over v != 0, floored, lmin := lmax-1
+// if lmin >= lmax, scale = max(lmax - lmin, 1e-12).
+__device__ __forceinline__ ALFit al_refit(float vmax, float vmin_nz, float floor_, float levels_m2) {
+  ALFit f;
+  float lmax = log2_exact(fmaxf(vmax, kLogClampIn));
+  float lmin = (vmin_nz == __builtin_inff()) ? __builtin_inff()
+                                              : log2_exact(fmaxf(vmin_nz, kLogClampIn));
+  lmin = fmaxf(lmin, floor_);
+  if (lmin >= lmax) lmin = lmax - 1.0f;
+  float s = fmaxf(lmax - lmin, 1e-12f);
+  f.lmin = lmin;
+  f.s = s;
+  f.rs = fast_rcp(s);
+  f.kmar = levels_m2 * f.rs * 0x1p-20f;
+  return f;
+}
+
+// AL code of a non-negative value; LM2 = levels - 2 (254 or 65534).
+template <int LM2>
+__device__ __forceinline__ uint32_t al_code(float v, const ALFit& f) {
+  if (v == 0.0f) return 0u;
+  float x = fmaxf(v, kLogClampIn);
+  float r = 0.0f;
+  bool done = false;
+  if (LM2 == 254 && x >= kFltMin) {
+    float lf = __builtin_amdgcn_logf(x);
+    float t = ((lf - f.lmin) * f.rs) * 254.0f;
+    r = rintf(t);
+    float margin = fmaxf(fabsf(lf), 1.0f) * f.kmar + 1.25e-4f;
+    done = fabsf(fabsf(t - r) - 0.5f) > margin;
+  }
+  if (!done) {
+    float le = log2_exact(x);
+    float t = ((le - f.lmin) / f.s) * (float)LM2;
+    r = rintf(t);
+  }
+  float q = fminf(fmaxf(r + 1.0f, 1.0f), (float)(LM2 + 1));
+  return (uint32_t)q;
+}
+
+// UF code (b = 8 or 4): rint((m / amax) * H) clamped to [-H, H-1] plus H.
+template <int H>
+__device__ __forceinline__ uint32_t uf_code(float m, float amax, float ramax) {
+  float t = (m * ramax) * (float)H;
+  float r = rintf(t);
+  if (!(fabsf(fabsf(t - r) - 0.5f) > 1.25e-4f)) {
+    r = rintf((m / amax) * (float)H);
+  }
+  r = fminf(fmaxf(r, (float)(-H)), (float)(H - 1));
+  return (uint32_t)(int)(r + (float)H);
+}
+
+// ---------------------------------------------------------------- dtypes
+template <typename T> __device__ __forceinline__ float to_f(T x);
+template <> __device__ __forceinline__ float to_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ float to_f<__hip_bfloat16>(__hip_bfloat16 x) {
+  return __bfloat162float(x);
+}
+template <> __device__ __forceinline__ float to_f<__half>(__half x) { return __half2float(x); }
+
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f<__hip_bfloat16>(float x) {
+  return __float2bfloat16(x);
+}
+template <> __device__ __forceinline__ __half from_f<__half>(float x) { return __float2half(x); }
+
+// Load / store 8 consecutive elements (aligned fast path when fully in range).
+template <typename T>
+__device__ __forceinline__ void load8(const T* base, int64_t i0, int64_t n, float* out) {
+  if (i0 + 8 <= n) {
+    if constexpr (sizeof(T) == 4) {
+      const f32x4* p = reinterpret_cast<const f32x4*>(base + i0);
+      f32x4 a = __builtin_nontemporal_load(p);
+      f32x4 b = __builtin_nontemporal_load(p + 1);
+      out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+      out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    } else {
+      u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + i0));
+      const T* h = reinterpret_cast<const T*>(&a);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) out[k] = to_f<T>(h[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = (i0 + k < n) ? to_f<T>(base[i0 + k]) : 0.0f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const float* v) {
+  if (i0 + 8 <= n) {
+    if constexpr (sizeof(T) == 4) {
+      f32x4* p = reinterpret_cast<f32x4*>(base + i0);
+      f32x4 a = {v[0], v[1], v[2], v[3]};
+      f32x4 b = {v[4], v[5], v[6], v[7]};
+      __builtin_nontemporal_store(a, p);
+      __builtin_nontemporal_store(b, p + 1);
+    } else {
+      u32x4 a;
+      T* h = reinterpret_cast<T*>(&a);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) h[k] = from_f<T>(v[k]);
+      __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(base + i0));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (i0 + k < n) base[i0 + k] = from_f<T>(v[k]);
+  }
+}
+
+// ---------------------------------------------------------------- reductions
+// Butterfly reductions over aligned groups of G lanes (G power of two <= 64).
+__device__ __forceinline__ float grp_max(float x, int G) {
+  for (int o = 1; o < G; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ float grp_min(float x, int G) {
+  for (int o = 1; o < G; o <<= 1) x = fminf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ float grp_sum(float x, int G) {
+  for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+__device__ __forceinline__ double grp_sum_d(double x, int G) {
+  for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+}  // namespace a8

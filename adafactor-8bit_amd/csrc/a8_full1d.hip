@@ -1,0 +1,280 @@
+// Full-precision (fp32 V, optional fp32 M) 1-D step and the Fira scalar.
+//
+// Tensors below min_8bit_size keep fp32 state (optimizer.py:1640-1641); the
+// reference steps them with fused_update_1d_full_kernel (kernels.cu:1261-1372)
+// on the GPU and with mul_/addcmul_/lerp_ (optimizer.py:2186-2191, 886-917) on
+// the CPU.  This kernel follows the CPU arithmetic:
+//   v = fma(RN(bv*g), g, RN(v*(1-bv))) [+ bv*eps_g],  m = lerp(m, x, 1-beta1)
+// Element-wise, 8 elements per lane, tensor-table capable like the
+// quantised kernel.  Fira (kernels.cu:3030-3053, optimizer.py:760-782) is a
+// one-lane-per-tensor scalar kernel.
+#include "a8_common.cuh"
+#include "a8_abi_impl.h"
+
+namespace a8 {
+
+struct DescFull {
+  void* param;
+  const void* grad;
+  float* v;
+  float* m;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  int64_t numel;
+  int64_t wg_begin;
+  uint64_t sr_seed;
+};
+
+struct HyperFull {
+  float w_m;        // (float)(1 - beta1)
+  float bv;         // (float)beta_val
+  float v_keep;     // (float)(1 - beta_val)
+  float eps_add;    // (float)(beta_val * eps_g), added when eps_g > 0
+  float eps_d;
+  float eps_sq;
+  float d;
+  int has_eps_add;
+  int adam_denom;
+  int momentum_only;
+  float alpha_val;
+  float decay_val;
+  int has_decay;
+  uint64_t sr_step;
+};
+
+constexpr int kFLanes = 256;
+constexpr int kFElems = kFLanes * 8;
+
+__device__ __forceinline__ const DescFull* find_full(const DescFull* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const DescFull* __restrict__ table,
+                                                         int ntab, HyperFull h) {
+  const DescFull D = table ? *find_full(table, ntab, (int64_t)blockIdx.x) : one;
+  const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
+  const int lane = threadIdx.x;
+  const int64_t n = D.numel;
+  const int64_t e0 = wl * kFElems + (int64_t)lane * 8;
+  float sq = 0.0f;
+  float step = 0.0f, ut_clip = 1.0f;
+  if constexpr (MODE != 1) {
+    const float a = D.alpha ? *D.alpha : h.alpha_val;
+    if constexpr (MODE == 0) {
+      step = a;
+    } else {
+      float denom = 1.0f;
+      if (h.d > 0.0f) {
+        const float nrm = (MODE == 2) ? sqrtf(*D.norm_buf) : *D.prev_norm;
+        // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
+        // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
+        if (h.momentum_only && D.m)
+          denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
+        else
+          denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));
+      }
+      if (h.momentum_only && D.m) { step = a; ut_clip = denom; }
+      else { step = a / denom; }
+    }
+  }
+  if (e0 < n) {
+    const int cnt = (n - e0) < 8 ? (int)(n - e0) : 8;
+    const T* G = reinterpret_cast<const T*>(D.grad);
+    T* P = reinterpret_cast<T*>(D.param);
+    for (int k = 0; k < cnt; ++k) {
+      const int64_t i = e0 + k;
+      const float g = scrub(to_f<T>(G[i]));
+      float v;
+      if (MODE == 2) {
+        v = D.v[i];
+      } else {
+        v = __builtin_fmaf(h.bv * g, g, D.v[i] * h.v_keep);
+        if (h.has_eps_add) v = v + h.eps_add;
+        D.v[i] = v;
+      }
+      float inv = h.adam_denom ? 1.0f / (sqrtf(v) + h.eps_d) : 1.0f / sqrtf(fmaxf(v, h.eps_sq));
+      float u;
+      if (D.m) {
+        float mo = D.m[i];
+        if (h.momentum_only) {
+          const float ut = g * inv;
+          if (MODE == 1 || MODE == 3) sq += ut * ut;
+          if (MODE != 1) {
+            const float m = lerp_ref(mo, ut_clip != 1.0f ? ut / ut_clip : ut, h.w_m);
+            D.m[i] = m;
+            u = m;
+          } else {
+            u = ut;
+          }
+        } else {
+          float m;
+          if (MODE == 2) {
+            m = mo;  // written by the NORM pass
+          } else {
+            m = lerp_ref(mo, g, h.w_m);
+            D.m[i] = m;
+          }
+          u = m * inv;
+          if (MODE == 1 || MODE == 3) sq += u * u;
+        }
+      } else {
+        u = h.adam_denom ? g / (sqrtf(v) + h.eps_d) : g * inv;
+        if (MODE == 1 || MODE == 3) sq += u * u;
+      }
+      if (MODE != 1) {
+        float p = to_f<T>(P[i]);
+        if (D.decay) p = p * *D.decay;
+        else if (h.has_decay) p = p * h.decay_val;
+        P[i] = from_f<T>(__builtin_fmaf(-step, u, p));
+      }
+    }
+  }
+  if constexpr (MODE == 1 || MODE == 3) {
+    float t = grp_sum(sq, 64);
+    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+  }
+}
+
+template <typename T>
+static int launch_full(int mode, const DescFull& one, const DescFull* tab, int ntab, int64_t nwg,
+                       const HyperFull& h, hipStream_t st) {
+  if (nwg <= 0) return 0;
+  switch (mode) {
+    case 0: hipLaunchKernelGGL((k_update1d_full<T, 0>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 1: hipLaunchKernelGGL((k_update1d_full<T, 1>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 2: hipLaunchKernelGGL((k_update1d_full<T, 2>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    default: hipLaunchKernelGGL((k_update1d_full<T, 3>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+  }
+  return check_launch("k_update1d_full");
+}
+
+static int launch_full_any(int dtype, int mode, const DescFull& one, const DescFull* tab, int ntab,
+                           int64_t nwg, const HyperFull& h, hipStream_t st) {
+  switch (dtype) {
+    case A8_F32: return launch_full<float>(mode, one, tab, ntab, nwg, h, st);
+    case A8_BF16: return launch_full<__hip_bfloat16>(mode, one, tab, ntab, nwg, h, st);
+    case A8_F16: return launch_full<__half>(mode, one, tab, ntab, nwg, h, st);
+    default: return set_error(A8_ERR_DTYPE, "unsupported param dtype");
+  }
+}
+
+static HyperFull make_hf(double beta1, double beta_val, float eps_sq, float eps_d, int adam,
+                         float eps_g, float d, int mom_only, uint64_t sr_step, float alpha_val,
+                         float decay_val, int has_decay) {
+  HyperFull h{};
+  h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
+  h.w_m = (float)(1.0 - beta1);
+  h.bv = (float)beta_val;
+  h.v_keep = (float)(1.0 - beta_val);
+  h.eps_add = (float)(beta_val * (double)eps_g);
+  h.has_eps_add = eps_g > 0.0f;
+  h.eps_d = eps_d; h.eps_sq = eps_sq; h.d = d;
+  h.adam_denom = adam; h.momentum_only = mom_only; h.sr_step = sr_step;
+  return h;
+}
+
+// ------------------------------------------------------------ Fira scalar
+// out[i] = scale (or alpha*scale), out[n+i] = next prev-norm, out[2n+i] = finite(x) ? x : 0
+__global__ void k_fira(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
+                       float margin, int apply, int has_prev) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float in = x[i];
+  const float nrm = apply ? sqrtf(in) : in;
+  const bool fin = __builtin_isfinite(nrm);
+  const float curr = fin ? nrm : 0.0f;
+  float scale = 1.0f, next = curr;
+  if (has_prev) {
+    const float p = prev[i];
+    const float ratio = curr / (p + 1.0e-8f);
+    const float lim = (ratio != ratio ? ratio : fmaxf(ratio, margin)) / margin;
+    const bool reset = p < 1.0e-6f;
+    scale = reset ? 1.0f : 1.0f / lim;
+    next = reset ? curr : curr * scale;
+  }
+  out[i] = apply ? alpha[i] * scale : scale;
+  out[n + i] = next;
+  out[2 * n + i] = fin ? in : 0.0f;
+}
+
+}  // namespace a8
+
+using namespace a8;
+
+extern "C" {
+
+int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
+                            float* m, float* norm_buf, const float* alpha, const float* prev_norm,
+                            const float* decay, double beta1, double beta_val, float eps_sq,
+                            float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
+                            int64_t numel, float d, int momentum_only, float alpha_val,
+                            float decay_val, int has_decay, void* stream) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (!param && mode != 1) return set_error(A8_ERR_ARG, "null param");
+  if (!grad || !variance) return set_error(A8_ERR_ARG, "null grad/variance");
+  if ((mode == 1 || mode == 2 || mode == 3) && !norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
+  if (mode == 3 && !prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
+  DescFull D{};
+  D.param = param; D.grad = grad; D.v = variance; D.m = m; D.norm_buf = norm_buf;
+  D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel;
+  HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
+                        momentum_only, 0, alpha_val, decay_val, has_decay);
+  return launch_full_any(dtype, mode, D, nullptr, 0, (numel + kFElems - 1) / kFElems, h,
+                         (hipStream_t)stream);
+}
+
+int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* tensors, int ntensors,
+                                  void* table_dev, int64_t table_bytes, double beta1, double beta_val,
+                                  float eps_sq, float eps_for_denom, int use_adam_denom,
+                                  float eps_for_grad_sq, float d, int momentum_only,
+                                  float alpha_val, float decay_val, int has_decay, int upload,
+                                  void* stream) {
+  if (ntensors <= 0) return 0;
+  if ((int64_t)sizeof(DescFull) * ntensors > table_bytes)
+    return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_full(ntensors)");
+  std::vector<DescFull> tab((size_t)ntensors);
+  int64_t wg = 0;
+  const bool has_m = tensors[0].m != nullptr;
+  for (int i = 0; i < ntensors; ++i) {
+    const a8_tensor_full& t = tensors[i];
+    if ((t.m != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    DescFull& D = tab[(size_t)i];
+    D.param = t.param; D.grad = t.grad; D.v = t.variance; D.m = t.m; D.norm_buf = t.norm_buf;
+    D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay; D.numel = t.numel;
+    D.wg_begin = wg;
+    wg += (t.numel + kFElems - 1) / kFElems;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(DescFull) * (size_t)ntensors,
+                               hipMemcpyHostToDevice, st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
+                        momentum_only, 0, alpha_val, decay_val, has_decay);
+  DescFull none{};
+  return launch_full_any(dtype, mode, none, reinterpret_cast<const DescFull*>(table_dev), ntensors, wg,
+                         h, st);
+}
+
+int64_t a8_table_bytes_full(int ntensors) { return (int64_t)sizeof(DescFull) * (int64_t)ntensors; }
+
+int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
+                   int has_prev, int apply, float margin, void* stream) {
+  if (n < 0) return set_error(A8_ERR_SIZE, "n < 0");
+  if (n == 0) return 0;
+  if (!x || !out || (has_prev && !prev) || (apply && !alpha)) return set_error(A8_ERR_ARG, "null pointer");
+  const int threads = 128;
+  const int64_t blocks = (n + threads - 1) / threads;
+  hipLaunchKernelGGL(k_fira, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, x, prev, alpha,
+                     out, n, margin, apply, has_prev);
+  return check_launch("k_fira");
+}
+
+}  // extern "C"

@@ -1,0 +1,655 @@
+// Fused full-rank (1-D) optimizer step for MI355X (gfx950).
+//
+// One launch streams every element once: decode V (AL8/AL16) and M (UF8/UF4/
+// D8/D4), EMA both, compute the update, write the parameter, refit the V block
+// [l_min, l_max] and the M block absmax, and write the new codes.  Follows the
+// reference's fused_update_1d kernels (kernels.cu:594-822 with M,
+// kernels.cu:998-1098 without M) and, for the numbers it produces, the CPU
+// path of _update_param_8bit (optimizer.py:2115-2123, 886-917).
+//
+// Layout: a 256-lane workgroup owns 2048 consecutive elements, 8 per lane held
+// in VGPRs (two 16-byte loads of fp32 p/g, one 8-byte load of each code
+// stream).  A V block of B_V elements is B_V/8 consecutive lanes and an M block
+// of B_M elements is B_M/8 lanes, so both block reductions are butterfly
+// shuffles inside a wave, plus one LDS exchange when B_V/8 > 64.  AL8 decode is
+// a per-block 256-entry table in LDS (one exp2 per code instead of one per
+// element).  A tensor table lets one launch cover many tensors.
+#include "a8_common.cuh"
+#include "a8_abi_impl.h"
+
+namespace a8 {
+
+struct Desc1D {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  void* v_q;
+  float* v_scale;
+  float* v_min_log;
+  float* v_buf;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  int64_t numel;
+  int64_t wg_begin;
+  uint64_t sr_seed;
+};
+
+struct Hyper1D {
+  float beta1;     // M EMA decay (kernel-rule arithmetic)
+  float w_m;       // lerp weight of M: (float)(1 - beta1)
+  float bv;        // lerp weight of V
+  float eps_d;     // Adam denominator epsilon
+  float eps_g;     // added to g^2
+  float eps_sq;    // rsqrt floor
+  float floor_;    // AL l_min floor
+  float d;         // RMS clip threshold (APPLY/LAG)
+  int block_size;
+  int m_block_size;
+  int mk;          // momentum codec
+  int adam_denom;
+  int momentum_only;
+  float alpha_val;  // used when a tensor's alpha pointer is NULL
+  float decay_val;  // used when a tensor's decay pointer is NULL and has_decay
+  int has_decay;
+  uint64_t sr_step;
+};
+
+__constant__ float c_qmap8[256];
+__constant__ float c_qmap4[16];
+
+// ------------------------------------------------------------ SR writeback
+// SplitMix64 counter stream keyed by (seed, step, element) and the bf16/fp16
+// stochastic rounding rules of the reference (kernels.cu:48-161).
+__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64_t idx) {
+  uint64_t z = seed * 0x9E3779B97F4A7C15ULL + step * 0xD1B54A32D192ED03ULL + idx;
+  z += 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  z ^= z >> 31;
+  return (uint32_t)(z >> 32);
+}
+
+__device__ __forceinline__ float sr_uniform(uint64_t seed, uint64_t step, uint64_t idx) {
+  return (float)(sr_bits(seed, step, idx) >> 8) * (1.0f / 16777216.0f);
+}
+
+__device__ __forceinline__ uint16_t sr_bf16(float x, float u) {
+  uint32_t b = __float_as_uint(x);
+  const bool nan = ((b & 0x7F800000u) == 0x7F800000u) && (b & 0x007FFFFFu);
+  if (nan) return (uint16_t)(((b & 0x80000000u) | 0x7FC00000u) >> 16);
+  uint32_t lo = b & 0xFFFF0000u;
+  uint32_t rem = b & 0x0000FFFFu;
+  uint32_t hi = lo + 0x00010000u;
+  bool lo_inf = (lo & 0x7F800000u) == 0x7F800000u;
+  bool hi_inf = ((hi & 0x7F800000u) == 0x7F800000u) && !(hi & 0x007FFFFFu);
+  bool up_ok = rem && !lo_inf && !hi_inf;
+  float prob = up_ok ? (float)rem * (1.0f / 65536.0f) : 0.0f;
+  return (uint16_t)(((up_ok && u < prob) ? hi : lo) >> 16);
+}
+
+__device__ __forceinline__ uint16_t h_next_up(uint16_t h) {
+  if (h == 0x7C00u) return h;
+  if (h == 0x8000u) return 0x0001u;
+  return (h & 0x8000u) ? (uint16_t)(h - 1u) : (uint16_t)(h + 1u);
+}
+__device__ __forceinline__ uint16_t h_next_down(uint16_t h) {
+  if (h == 0xFC00u) return h;
+  if (h == 0x0000u) return 0x8001u;
+  return (h & 0x8000u) ? (uint16_t)(h + 1u) : (uint16_t)(h - 1u);
+}
+
+__device__ __forceinline__ uint16_t sr_fp16(float x, float u) {
+  uint32_t b = __float_as_uint(x);
+  uint16_t sign = (b & 0x80000000u) ? 0x8000u : 0u;
+  if ((b & 0x7F800000u) == 0x7F800000u) return (b & 0x007FFFFFu) ? (sign | 0x7E00u) : (sign | 0x7C00u);
+  if (fabsf(x) > 65504.0f) return sign | 0x7BFFu;
+  __half nh = __float2half_rn(x);
+  uint16_t qb = __half_as_ushort(nh);
+  float q = __half2float(nh);
+  if (q == x) return qb;
+  uint16_t lo, hi;
+  if (q < x) { lo = qb; hi = h_next_up(qb); } else { hi = qb; lo = h_next_down(qb); }
+  float flo = __half2float(__ushort_as_half(lo));
+  float fhi = __half2float(__ushort_as_half(hi));
+  float prob = (x - flo) / (fhi - flo);
+  return (u < prob) ? hi : lo;
+}
+
+template <typename T>
+__device__ __forceinline__ T sr_round(float x, uint64_t seed, uint64_t step, uint64_t idx) {
+  float u = sr_uniform(seed, step, idx);
+  if constexpr (sizeof(T) == 2 && std::is_same<T, __hip_bfloat16>::value) {
+    return __ushort_as_bfloat16(sr_bf16(x, u));
+  } else if constexpr (sizeof(T) == 2) {
+    return __ushort_as_half(sr_fp16(x, u));
+  } else {
+    return x;
+  }
+}
+
+// ------------------------------------------------------------ M codecs
+__device__ __forceinline__ float m_decode(int mk, uint32_t q, float s) {
+  switch (mk) {
+    case 1: return ((float)q - 128.0f) * (s / 128.0f);
+    case 2: return ((float)q - 8.0f) * (s / 8.0f);
+    case 3: return c_qmap8[q] * s;
+    default: return c_qmap4[q] * s;
+  }
+}
+
+// Nearest codebook entry with searchsorted semantics and sign fix
+// (optimizer.py:454-476), on x = m / absmax computed with IEEE division.
+template <int N>
+__device__ __forceinline__ uint32_t d_code(float m, float amax) {
+  const float* qm = (N == 256) ? c_qmap8 : c_qmap4;
+  float x = m / amax;
+  int lo = 0, hi = N;  // first index with qm[i] >= x
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (qm[mid] < x) lo = mid + 1; else hi = mid;
+  }
+  int idx = lo > N - 1 ? N - 1 : lo;
+  int prev = idx - 1 < 0 ? 0 : idx - 1;
+  if (fabsf(x - qm[prev]) < fabsf(x - qm[idx])) idx = prev;
+  float sx = (x > 0.0f) ? 1.0f : ((x < 0.0f) ? -1.0f : 0.0f);
+  float v = qm[idx];
+  float sq = (v > 0.0f) ? 1.0f : ((v < 0.0f) ? -1.0f : 0.0f);
+  if (sx != sq && sx != 0.0f) {
+    if (sx > 0.0f && idx < N - 1) idx += 1;
+    else if (sx < 0.0f && idx > 0) idx -= 1;
+  }
+  return (uint32_t)idx;
+}
+
+__device__ __forceinline__ uint32_t m_encode(int mk, float m, float amax, float ramax) {
+  switch (mk) {
+    case 1: return uf_code<128>(m, amax, ramax);
+    case 2: return uf_code<8>(m, amax, ramax);
+    case 3: return d_code<256>(m, amax);
+    default: return d_code<16>(m, amax);
+  }
+}
+
+// ------------------------------------------------------------ main kernel
+constexpr int kLanes = 256;
+constexpr int kEPT = 8;
+constexpr int kWGElems = kLanes * kEPT;
+
+__device__ __forceinline__ const Desc1D* find_desc(const Desc1D* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+template <typename T, int VB, int MODE, bool SR>
+__global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* __restrict__ table,
+                                                   int ntab, Hyper1D h) {
+  extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | [8] cross-wave partials
+  const Desc1D D = table ? *find_desc(table, ntab, (int64_t)blockIdx.x) : one;
+  const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
+  const int lane = threadIdx.x;
+  const int64_t n = D.numel;
+  const int BV = h.block_size, BM = h.m_block_size;
+  const int VL = BV >> 3;                       // lanes per V block (16..256)
+  const int ML = BM >> 3;                       // lanes per M block (4..256)
+  const int nv_wg = kWGElems / BV;              // V blocks per workgroup
+  const int64_t e0 = wl * kWGElems + (int64_t)lane * kEPT;
+  const int64_t nvb = (n + BV - 1) / BV;
+  const int64_t nmb = (n + BM - 1) / BM;
+  const int64_t vb = e0 / BV;
+  const int64_t mb = e0 / BM;
+  const bool v_ok = vb < nvb;
+  const bool has_m = h.mk != 0;
+  const bool m_ok = has_m && (mb < nmb);
+  const int vloc = lane / VL;                    // V block index inside the workgroup
+  float* tabs = s_lds;                           // AL8 decode tables
+  float* xw = s_lds + (VB == 8 && MODE != 2 ? nv_wg * 256 : 0);  // 4 waves x 4 floats
+
+  // ---- AL8 decode tables for this workgroup's V blocks
+  if constexpr (VB == 8 && MODE != 2) {
+    const int64_t vb0 = wl * nv_wg;
+    for (int k = lane; k < nv_wg * 256; k += kLanes) {
+      const int64_t b = vb0 + (k >> 8);
+      const int c = k & 255;
+      float val = 0.0f;
+      if (b < nvb && c != 0) {
+        const float s = D.v_scale[b], lm = D.v_min_log[b];
+        val = exp2_exact(((float)(c - 1) * s) / 254.0f + lm);
+      }
+      tabs[k] = val;
+    }
+    __syncthreads();
+  }
+
+  // ---- step scale
+  float step = 0.0f, ut_clip = 1.0f;
+  if constexpr (MODE != 1) {
+    const float a = D.alpha ? *D.alpha : h.alpha_val;
+    if constexpr (MODE == 0) {
+      step = a;
+    } else {
+      float denom = 1.0f;
+      if (h.d > 0.0f) {
+        const float nrm = (MODE == 2) ? sqrtf(*D.norm_buf) : *D.prev_norm;
+        // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
+        // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
+        if (h.momentum_only && has_m)
+          denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
+        else
+          denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));
+      }
+      if (h.momentum_only && has_m) { step = a; ut_clip = denom; }
+      else { step = a / denom; }
+    }
+  }
+
+  float g[kEPT], vn[kEPT], mn[kEPT];
+  float vmax = 0.0f, vmin = __builtin_inff(), amax = 0.0f, sq = 0.0f;
+
+  if (v_ok) {
+    load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) g[k] = (e0 + k < n) ? scrub(g[k]) : 0.0f;
+
+    // ---- V: decode + EMA (or the exact V of the NORM pass)
+    if constexpr (MODE == 2) {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) vn[k] = (e0 + k < n) ? D.v_buf[e0 + k] : 0.0f;
+    } else {
+      float vo[kEPT];
+      const float s_old = D.v_scale[vb], lm_old = D.v_min_log[vb];
+      if constexpr (VB == 8) {
+        const uint2 qv = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0);
+        const float* tb = tabs + vloc * 256;
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          uint32_t c = ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu;
+          vo[k] = tb[c];
+        }
+      } else {
+        const uint4 qv = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0);
+        const uint32_t w4[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          uint32_t c = (w4[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+          vo[k] = c ? exp2_exact(((float)(c - 1) * s_old) / 65534.0f + lm_old) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) {
+        const float gsq = g[k] * g[k] + h.eps_g;
+        const float v = lerp_ref(vo[k], gsq, h.bv);
+        vn[k] = (e0 + k < n) ? v : 0.0f;
+      }
+      if constexpr (MODE == 1) {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k)
+          if (e0 + k < n) D.v_buf[e0 + k] = vn[k];
+      }
+    }
+
+    // ---- M decode + EMA, update direction
+    float mo[kEPT];
+    if (m_ok) {
+      const float ms = D.m_scale[mb];
+      if (h.mk == 2 || h.mk == 4) {
+        const uint32_t qw = *reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1));
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
+          const uint32_t c = (k & 1) ? (byte & 0x0Fu) : (byte >> 4);
+          mo[k] = m_decode(h.mk, c, ms);
+        }
+      } else {
+        const uint2 qw = *reinterpret_cast<const uint2*>(D.m_q + e0);
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          const uint32_t c = ((k < 4 ? qw.x : qw.y) >> (8 * (k & 3))) & 0xFFu;
+          mo[k] = m_decode(h.mk, c, ms);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) mo[k] = 0.0f;
+    }
+
+    float u[kEPT];
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) {
+      const bool in = e0 + k < n;
+      float inv;
+      if (h.adam_denom) {
+        inv = fast_rcp(fast_sqrt(vn[k]) + h.eps_d);
+      } else {
+        // feeds the momentum codes when momentum_only: IEEE sqrt then division,
+        // as torch's rsqrt on the CPU (optimizer.py:893)
+        inv = 1.0f / sqrtf(fmaxf(vn[k], h.eps_sq));
+      }
+      float uu;
+      if (has_m) {
+        float x;
+        if (h.momentum_only) {
+          float ut = g[k] * inv;
+          if (MODE == 1) { sq += in ? ut * ut : 0.0f; }
+          x = (ut_clip != 1.0f) ? ut / ut_clip : ut;
+        } else {
+          x = g[k];
+        }
+        const float m = lerp_ref(mo[k], x, h.w_m);
+        mn[k] = in ? m : 0.0f;
+        uu = h.momentum_only ? m : m * inv;
+        if (!h.momentum_only && (MODE == 1 || MODE == 3)) sq += in ? uu * uu : 0.0f;
+        if (h.momentum_only && MODE == 3) { const float ut = g[k] * inv; sq += in ? ut * ut : 0.0f; }
+      } else {
+        mn[k] = 0.0f;
+        uu = h.adam_denom ? g[k] * inv : g[k] * inv;
+        if (MODE == 1 || MODE == 3) sq += in ? uu * uu : 0.0f;
+      }
+      u[k] = in ? uu : 0.0f;
+      vmax = fmaxf(vmax, vn[k]);
+      if (vn[k] > 0.0f) vmin = fminf(vmin, vn[k]);
+      amax = fmaxf(amax, fabsf(mn[k]));
+    }
+
+    // ---- parameter write
+    if constexpr (MODE != 1) {
+      T* P = reinterpret_cast<T*>(D.param);
+      const bool has_dec = D.decay || h.has_decay;
+      const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
+      if constexpr (SR) {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          if (e0 + k < n) {
+            const float pv = to_f<T>(P[e0 + k]);
+            P[e0 + k] = sr_round<T>(pv * dec - step * u[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
+          }
+        }
+      } else {
+        float p[kEPT];
+        load8<T>(P, e0, n, p);
+        if (has_dec) {  // decoupled weight decay: p*decay rounded, then the update (optimizer.py:2039)
+#pragma unroll
+          for (int k = 0; k < kEPT; ++k) p[k] = p[k] * dec;
+        }
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) p[k] = __builtin_fmaf(-step, u[k], p[k]);
+        store8<T>(P, e0, n, p);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) { vn[k] = 0.0f; mn[k] = 0.0f; }
+  }
+
+  const int wave = lane >> 6;
+
+  // ---- V refit + codes
+  if constexpr (MODE != 2) {
+    float bmax = grp_max(vmax, VL < 64 ? VL : 64);
+    float bmin = grp_min(vmin, VL < 64 ? VL : 64);
+    if (VL > 64) {
+      if ((lane & 63) == 0) { xw[wave * 4 + 0] = bmax; xw[wave * 4 + 1] = bmin; }
+      __syncthreads();
+      const int w0 = (lane / VL) * (VL >> 6);
+      bmax = xw[w0 * 4]; bmin = xw[w0 * 4 + 1];
+      for (int w = 1; w < (VL >> 6); ++w) {
+        bmax = fmaxf(bmax, xw[(w0 + w) * 4]);
+        bmin = fminf(bmin, xw[(w0 + w) * 4 + 1]);
+      }
+    }
+    if (v_ok) {
+      const ALFit f = al_refit(bmax, bmin, h.floor_, VB == 8 ? 254.0f : 65534.0f);
+      if constexpr (VB == 8) {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w0 |= al_code<254>(vn[k], f) << (8 * k);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w1 |= al_code<254>(vn[k + 4], f) << (8 * k);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0) = make_uint2(w0, w1);
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = al_code<65534>(vn[2 * j], f) | (al_code<65534>(vn[2 * j + 1], f) << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(D.v_q) + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      if ((lane % VL) == 0) { D.v_scale[vb] = f.s; D.v_min_log[vb] = f.lmin; }
+    }
+  }
+
+  // ---- M refit + codes
+  if constexpr (MODE != 1) {
+    if (has_m) {
+      float bam = grp_max(amax, ML < 64 ? ML : 64);
+      if (ML > 64) {
+        __syncthreads();
+        if ((lane & 63) == 0) xw[wave * 4 + 2] = bam;
+        __syncthreads();
+        const int w0 = (lane / ML) * (ML >> 6);
+        bam = xw[w0 * 4 + 2];
+        for (int w = 1; w < (ML >> 6); ++w) bam = fmaxf(bam, xw[(w0 + w) * 4 + 2]);
+      }
+      if (m_ok) {
+        const float am = fmaxf(bam, 1e-12f);
+        const float ram = fast_rcp(am);
+        if (h.mk == 2 || h.mk == 4) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t hi = m_encode(h.mk, mn[2 * j], am, ram);
+            const uint32_t lo = m_encode(h.mk, mn[2 * j + 1], am, ram);
+            w |= ((hi << 4) | lo) << (8 * j);
+          }
+          *reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1)) = w;
+        } else {
+          uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) w0 |= m_encode(h.mk, mn[k], am, ram) << (8 * k);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) w1 |= m_encode(h.mk, mn[k + 4], am, ram) << (8 * k);
+          *reinterpret_cast<uint2*>(D.m_q + e0) = make_uint2(w0, w1);
+        }
+        if ((lane % ML) == 0) D.m_scale[mb] = am;
+      }
+    }
+  }
+
+  // ---- sum of squares for NORM / LAG
+  if constexpr (MODE == 1 || MODE == 3) {
+    float t = grp_sum(sq, 64);
+    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+  }
+}
+
+// ------------------------------------------------------------ launch glue
+static bool fast_shape_ok(int bv, int bm) {
+  auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
+  return pow2(bv) && bv >= 128 && bv <= 2048 && pow2(bm) && bm >= 32 && bm <= bv;
+}
+
+template <typename T, int VB, int MODE, bool SR>
+static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
+                    hipStream_t st) {
+  const int nv_wg = kWGElems / h.block_size;
+  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 16 * sizeof(float);
+  if (nwg <= 0) return 0;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,
+                     table, ntab, h);
+  return check_launch("k_update1d");
+}
+
+template <typename T, bool SR>
+static int launch_dispatch(int vbits, int mode, const Desc1D& one, const Desc1D* table, int ntab,
+                           int64_t nwg, const Hyper1D& h, hipStream_t st) {
+#define A8_L(VB, MO) return launch_t<T, VB, MO, SR>(one, table, ntab, nwg, h, st)
+  if (vbits == 8) {
+    switch (mode) { case 0: A8_L(8, 0); case 1: A8_L(8, 1); case 2: A8_L(8, 2); default: A8_L(8, 3); }
+  } else {
+    switch (mode) { case 0: A8_L(16, 0); case 1: A8_L(16, 1); case 2: A8_L(16, 2); default: A8_L(16, 3); }
+  }
+#undef A8_L
+}
+
+static int launch_any(int dtype, int sr, int vbits, int mode, const Desc1D& one, const Desc1D* table,
+                      int ntab, int64_t nwg, const Hyper1D& h, hipStream_t st) {
+  if (mode == 1 && sr) sr = 0;
+  switch (dtype) {
+    case A8_F32: return launch_dispatch<float, false>(vbits, mode, one, table, ntab, nwg, h, st);
+    case A8_BF16:
+      return sr ? launch_dispatch<__hip_bfloat16, true>(vbits, mode, one, table, ntab, nwg, h, st)
+                : launch_dispatch<__hip_bfloat16, false>(vbits, mode, one, table, ntab, nwg, h, st);
+    case A8_F16:
+      return sr ? launch_dispatch<__half, true>(vbits, mode, one, table, ntab, nwg, h, st)
+                : launch_dispatch<__half, false>(vbits, mode, one, table, ntab, nwg, h, st);
+    default: return set_error(A8_ERR_DTYPE, "unsupported param dtype");
+  }
+}
+
+static int check_common(int dtype, int64_t numel, int bv, int bm, int mbits, int mmode, int vbits,
+                        bool has_m) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (vbits != 8 && vbits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
+  if (!has_m) bm = bv;
+  if (!fast_shape_ok(bv, bm))
+    return set_error(A8_ERR_BLOCK, "block_size must be a power of two in [128, 2048] and "
+                                   "m_block_size a power of two in [32, block_size]");
+  if (has_m && !((mbits == 8 || mbits == 4) && (mmode == 0 || mmode == 1)))
+    return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
+  return 0;
+}
+
+static int mk_of(int mbits, int mmode) {
+  if (mmode == 0) return mbits == 8 ? 1 : 2;
+  return mbits == 8 ? 3 : 4;
+}
+
+}  // namespace a8
+
+using namespace a8;
+
+// ============================================================== C-ABI
+static int update1d_entry(int mode, int sr, int dtype, void* param, const void* grad, uint8_t* m_q,
+                          float* m_scale, void* v_q, float* v_scale, float* v_min_log, float* v_buf,
+                          float* norm_buf, const float* alpha, const float* prev_norm,
+                          const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
+                          double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
+                          float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
+                          int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                          int momentum_only, float alpha_val, float decay_val, int has_decay,
+                          void* stream) {
+  const bool has_m = m_q != nullptr;
+  int rc = check_common(dtype, numel, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
+  if (rc) return rc;
+  if (!v_q || !v_scale || !v_min_log || !grad) return set_error(A8_ERR_ARG, "null state pointer");
+  if (mode != 1 && !param) return set_error(A8_ERR_ARG, "null param");
+  if ((mode == 1 || mode == 2) && !v_buf) return set_error(A8_ERR_ARG, "NORM/APPLY need v_buf");
+  if ((mode == 1 || mode == 3) && !norm_buf) return set_error(A8_ERR_ARG, "NORM/LAG need norm_buf");
+  if (mode == 2 && !norm_buf) return set_error(A8_ERR_ARG, "APPLY needs norm_buf");
+  if (mode == 3 && !prev_norm) return set_error(A8_ERR_ARG, "LAG needs prev_norm");
+  if (!aligned16(param) || !aligned16(grad) || !aligned16(v_q) || (has_m && !aligned16(m_q)))
+    return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
+  Desc1D D{};
+  D.param = param; D.grad = grad; D.m_q = m_q; D.m_scale = m_scale;
+  D.v_q = v_q; D.v_scale = v_scale; D.v_min_log = v_min_log; D.v_buf = v_buf;
+  D.norm_buf = norm_buf; D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay;
+  D.numel = numel; D.wg_begin = 0; D.sr_seed = sr_seed;
+  Hyper1D h{};
+  h.beta1 = (float)beta1;
+  h.w_m = (float)(1.0 - beta1);
+  h.bv = (float)beta_val;
+  h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
+  h.floor_ = log_floor; h.d = d;
+  h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
+  h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
+  h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
+  h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
+  h.sr_step = sr_step;
+  const int64_t nwg = (numel + kWGElems - 1) / kWGElems;
+  return launch_any(dtype, sr, v_bits, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
+}
+
+extern "C" {
+
+int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
+                       uint8_t* m_q, float* m_scale, void* v_q, float* v_scale, float* v_min_log,
+                       float* v_buf, float* norm_buf, const float* alpha, const float* prev_norm,
+                       const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
+                       double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
+                       float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
+                       int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                       int momentum_only, float alpha_val, float decay_val, int has_decay,
+                       void* stream) {
+  return update1d_entry(mode, stochastic, dtype, param, grad, m_q, m_scale, v_q, v_scale, v_min_log,
+                        v_buf, norm_buf, alpha, prev_norm, decay, sr_seed, sr_step, beta1, beta_val,
+                        eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, numel,
+                        block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only, alpha_val,
+                        decay_val, has_decay, stream);
+}
+
+int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
+                             int ntensors, void* table_dev, int64_t table_bytes, double beta1,
+                             double beta_val, float eps_for_denom, int use_adam_denom,
+                             float log_floor, float eps_for_grad_sq, float eps_sq, int block_size,
+                             int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                             int momentum_only, uint64_t sr_step, float alpha_val,
+                             float decay_val, int has_decay, int upload, void* stream) {
+  if (ntensors <= 0) return 0;
+  const bool has_m = tensors[0].m_q != nullptr;
+  int rc = check_common(dtype, 0, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
+  if (rc) return rc;
+  if ((int64_t)sizeof(Desc1D) * ntensors > table_bytes)
+    return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_1d(ntensors)");
+  std::vector<Desc1D> tab((size_t)ntensors);
+  int64_t wg = 0;
+  for (int i = 0; i < ntensors; ++i) {
+    const a8_tensor1d& t = tensors[i];
+    if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.v_q) || (has_m && !aligned16(t.m_q)))
+      return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
+    if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+    Desc1D& D = tab[(size_t)i];
+    D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
+    D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
+    D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
+    D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed;
+    wg += (t.numel + kWGElems - 1) / kWGElems;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(Desc1D) * (size_t)ntensors,
+                               hipMemcpyHostToDevice, st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  Hyper1D h{};
+  h.beta1 = (float)beta1;
+  h.w_m = (float)(1.0 - beta1);
+  h.bv = (float)beta_val;
+  h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
+  h.floor_ = log_floor; h.d = d;
+  h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
+  h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
+  h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
+  h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
+  h.sr_step = sr_step;
+  Desc1D none{};
+  return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev),
+                    ntensors, wg, h, st);
+}
+
+int64_t a8_table_bytes_1d(int ntensors) { return (int64_t)sizeof(Desc1D) * (int64_t)ntensors; }
+
+int a8_set_qmap(const float* qmap8_host, const float* qmap4_host) {
+  if (hipMemcpyToSymbol(HIP_SYMBOL(c_qmap8), qmap8_host, 256 * sizeof(float)) != hipSuccess)
+    return set_error(A8_ERR_HIP, "qmap8 upload failed");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(c_qmap4), qmap4_host, 16 * sizeof(float)) != hipSuccess)
+    return set_error(A8_ERR_HIP, "qmap4 upload failed");
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+/* adafactor8bit_amd — C ABI of the MI355X (gfx950) fused optimizer-step library.
+ *
+ * Every entry point takes raw device pointers, element counts, float scalars
+ * and a hipStream_t passed as void*, launches asynchronously on that stream and
+ * returns 0 or a negative A8_ERR_* code (message: a8_last_error()).  No torch
+ * types cross this boundary.  Buffers are caller-owned; kernels update state in
+ * place exactly where the reference's kernels do.
+ *
+ * The reference binds its kernels as the pybind11 module "adafactor8bit_cuda"
+ * (adafactor8bit/kernels.cu:3089-3150), loaded by _load_cuda_module
+ * (adafactor8bit/optimizer.py:61-106).  Each function below names the
+ * binding(s) it replaces.  The Python mirror of that module
+ * (adafactor-8bit_amd/adafactor8bit/adafactor8bit_cuda.py) keeps the
+ * reference's names and positional signatures and calls these functions.
+ *
+ * Numerics: quantised codes are decided as the reference's PyTorch path
+ * decides them (optimizer.py:299-353, 504-532), see DESIGN.md.
+ */
+#ifndef ADAFACTOR8BIT_AMD_H
+#define ADAFACTOR8BIT_AMD_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define A8_OK 0
+#define A8_ERR_ARG (-1)
+#define A8_ERR_DTYPE (-2)
+#define A8_ERR_BLOCK (-3)
+#define A8_ERR_SIZE (-4)
+#define A8_ERR_ALIGN (-5)
+#define A8_ERR_HIP (-6)
+
+/* parameter / gradient element types */
+#define A8_F32 0
+#define A8_BF16 1
+#define A8_F16 2
+
+/* kernel modes (kernels.cu:19-24): single pass, norm pass, apply pass, lagged norm */
+#define A8_MODE_NOCLIP 0
+#define A8_MODE_NORM 1
+#define A8_MODE_APPLY 2
+#define A8_MODE_LAG 3
+
+const char* a8_last_error(void);
+const char* a8_version(void);
+
+/* Replaces set_qmap (kernels.cu:32-37; called by _ensure_qmap, optimizer.py:109-133).
+ * Uploads the 256- and 16-entry signed dynamic codebooks (host fp32 arrays)
+ * to the current device. */
+int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
+
+/* Replaces fused_update_1d_{noclip,norm,apply,lag}[_sr] (kernels.cu:826-990)
+ * and, with m_q == NULL, fused_update_1d_vonly_{noclip,norm,apply,lag}[_sr]
+ * (kernels.cu:1100-1255); called from _dispatch_1d_cuda (optimizer.py:1080-1170).
+ *   mode        A8_MODE_*; stochastic = SR writeback for bf16/fp16 params
+ *   param/grad  numel elements of `dtype`, 16-byte aligned
+ *   m_q/m_scale momentum codes (uf8/d8: 1 byte, uf4/d4: packed nibbles) padded to
+ *               m_block_size, fp32 absmax per m block; NULL for no momentum
+ *   v_q         AL8 uint8 / AL16 int16 codes padded to block_size; v_scale,
+ *               v_min_log fp32 per block
+ *   v_buf       fp32[numel] exact V written by NORM, read by APPLY
+ *   norm_buf    fp32[1] sum of squares accumulated by NORM/LAG, read by APPLY
+ *   alpha, prev_norm, decay: device fp32 scalars; alpha == NULL uses alpha_val,
+ *               decay == NULL uses decay_val when has_decay (p := p*decay before
+ *               the update, the decoupled weight decay of optimizer.py:2034-2039)
+ *   beta1, beta_val  EMA coefficients as the host's doubles: the lerp weights are
+ *               (float)(1 - beta1) and (float)beta_val, as torch.lerp_ receives them
+ *   log_floor   lower bound of a block's l_min (-126 for the reference numerics)
+ * block_size must be a power of two in [128, 2048], m_block_size a power of two
+ * in [32, block_size]. */
+int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
+                       uint8_t* m_q, float* m_scale, void* v_q, float* v_scale, float* v_min_log,
+                       float* v_buf, float* norm_buf, const float* alpha, const float* prev_norm,
+                       const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
+                       double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
+                       float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
+                       int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                       int momentum_only, float alpha_val, float decay_val, int has_decay,
+                       void* stream);
+
+/* One tensor of a multi-tensor launch. */
+typedef struct a8_tensor1d {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  void* v_q;
+  float* v_scale;
+  float* v_min_log;
+  float* v_buf;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  int64_t numel;
+  uint64_t sr_seed;
+} a8_tensor1d;
+
+/* Multi-tensor form of a8_fused_update_1d: one launch over `ntensors` tensors
+ * that share hyper-parameters (the reference launches once per tensor from
+ * its per-parameter loop, optimizer.py:1887).  `table_dev` is a device buffer
+ * of at least a8_table_bytes_1d(ntensors) bytes that receives the tensor table
+ * (stream-ordered upload) when `upload` is non-zero; with upload == 0 the table
+ * already there from an earlier call with the same tensors is reused. */
+int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
+                             int ntensors, void* table_dev, int64_t table_bytes, double beta1,
+                             double beta_val, float eps_for_denom, int use_adam_denom,
+                             float log_floor, float eps_for_grad_sq, float eps_sq, int block_size,
+                             int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                             int momentum_only, uint64_t sr_step, float alpha_val,
+                             float decay_val, int has_decay, int upload, void* stream);
+int64_t a8_table_bytes_1d(int ntensors);
+
+/* Replaces fused_update_1d_full_{noclip,norm,apply,lag} (kernels.cu:1374-1515;
+ * called at optimizer.py:2147-2183): fp32 V (and optional fp32 M, NULL for none)
+ * for tensors below min_8bit_size or with quantize=False.  NORM writes V (and M
+ * unless momentum_only) and accumulates sum(u^2) into norm_buf; APPLY reads them. */
+int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
+                            float* m, float* norm_buf, const float* alpha, const float* prev_norm,
+                            const float* decay, double beta1, double beta_val, float eps_sq,
+                            float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
+                            int64_t numel, float d, int momentum_only, float alpha_val,
+                            float decay_val, int has_decay, void* stream);
+
+typedef struct a8_tensor_full {
+  void* param;
+  const void* grad;
+  float* variance;
+  float* m;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  int64_t numel;
+} a8_tensor_full;
+
+/* Multi-tensor form of a8_fused_update_1d_full (one launch per group). */
+int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* tensors, int ntensors,
+                                  void* table_dev, int64_t table_bytes, double beta1, double beta_val,
+                                  float eps_sq, float eps_for_denom, int use_adam_denom,
+                                  float eps_for_grad_sq, float d, int momentum_only,
+                                  float alpha_val, float decay_val, int has_decay, int upload,
+                                  void* stream);
+int64_t a8_table_bytes_full(int ntensors);
+
+/* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,
+ * optimizer.py:735-757).  For i < n: norm = apply ? sqrt(x[i]) : x[i], zeroed when
+ * non-finite; with a previous norm p: ratio = norm/(p+1e-8),
+ * limiter = max(ratio, margin)/margin, scale = p < 1e-6 ? 1 : 1/limiter.
+ * out[i] = apply ? alpha[i]*scale : scale; out[n+i] = next previous norm;
+ * out[2n+i] = x[i] if finite else 0.  margin = 1 + fira_margin. */
+int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
+                   int has_prev, int apply, float margin, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,50 @@
+"""The C-ABI library loads on a CPU-only host and exports every declared symbol."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for f in os.listdir(inc):
+        if f.endswith(".h"):
+            src = open(os.path.join(inc, f)).read()
+            names |= set(re.findall(r"^(?:int|int64_t|const char\*)\s+(a8_\w+)\s*\(", src, re.M))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "a8_fused_update_1d" in names and len(names) >= 8, names
+
+
+def test_library_exports_declared_symbols():
+    from adafactor8bit import _native as nat
+    L = nat.lib()
+    for n in _declared():
+        assert hasattr(L, n), f"symbol {n} declared in include/ but not exported"
+    assert L.a8_version().startswith(b"adafactor8bit_amd")
+
+
+def test_ctypes_signatures_cover_header():
+    from adafactor8bit import _native as nat
+    assert set(_declared()) <= set(nat.exported_symbols())
+
+
+def test_argument_errors_without_gpu():
+    """Shape/dtype validation happens on the host and returns an error code."""
+    from adafactor8bit import _native as nat
+    L = nat.lib()
+    rc = L.a8_fused_update_1d(0, 0, 0, None, None, None, None, None, None, None, None, None, None,
+                              None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 100,
+                              256, 8, 0, 0.0, 8, 0, 1e-4, 1.0, 0, None)
+    assert rc == -3, rc  # block_size 100 rejected
+    assert b"block_size" in L.a8_last_error()
+    rc = L.a8_fused_update_1d(0, 0, 7, None, None, None, None, None, None, None, None, None, None,
+                              None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 2048,
+                              256, 8, 0, 0.0, 8, 0, 1e-4, 1.0, 0, None)
+    assert rc == -2, rc

@@ -1,0 +1,75 @@
+"""HIP path vs the reference's own trajectories (golden fixtures), on the GPU.
+
+Tolerance: quantised codes equal except at most 0.01% of them (plus one code per
+tensor for tensors under 10^4 codes), where the reference's CPU decode
+(torch.pow, faithfully but not correctly rounded) and the correctly rounded HIP
+decode give values one ulp apart; per-block scale/min_log within rtol 1e-5;
+fp32 states within rtol 2e-6; parameters within rtol 1e-5.  Step 1 from fresh
+state involves no decode and is compared bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import golden_util as gu
+
+SUPPORTED = ["adamw_uf8_al8", "adamw_uf8_al16", "adamw_uf4_al8", "adamw_d8_al8", "adamw_d4_al8",
+             "adamw_bv256_mb128", "adamw_clip_fira_wd", "adamw_fp32_state", "rmsprop_al8",
+             "adafactor_mom1d"]
+
+CODE_KEYS = ("_q",)
+
+
+def _cmp_state(name, key, st, z, zkeys, report):
+    for k in zkeys:
+        ref = z[f"{key}/{k}"]
+        assert k in st, f"{name} {key}: missing state {k}"
+        mine = st[k]
+        mine = mine.detach().cpu().numpy() if torch.is_tensor(mine) else np.asarray(mine)
+        assert mine.dtype == ref.dtype and mine.shape == ref.shape, (name, key, k, mine.dtype, ref.dtype)
+        first = key.startswith("s1/")
+        if k.endswith("_q"):
+            frac, mx = gu.code_mismatch(mine, ref)
+            report.append((key, k, frac, mx))
+            allowed = 0.0 if first else 1e-4 + 1.0 / max(mine.size, 1)
+            assert mx <= 2 and frac <= allowed, f"{name} {key}/{k}: {frac:.2e} codes differ, max {mx}"
+        elif k in ("step",):
+            assert int(mine) == int(ref)
+        elif k.endswith("_scale") or k.endswith("_min_log"):
+            if first:
+                np.testing.assert_array_equal(mine, ref, err_msg=f"{name} {key}/{k}")
+            else:
+                np.testing.assert_allclose(mine, ref, rtol=1e-5, atol=0, err_msg=f"{name} {key}/{k}")
+        else:
+            np.testing.assert_allclose(mine, ref, rtol=2e-6, atol=1e-30, err_msg=f"{name} {key}/{k}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", SUPPORTED)
+@pytest.mark.parametrize("multi", [True, False])
+def test_hip_matches_golden(name, multi):
+    from adafactor8bit import Adafactor8Bit
+    meta, kw, z = gu.load(name)
+    print(f"[golden] {name} multi={multi}", flush=True)
+    params = gu.init_params(meta, device="cuda")
+    if multi:
+        opt = Adafactor8Bit(params, **kw)
+    else:  # one group per parameter: no multi-tensor batching
+        opt = Adafactor8Bit([{"params": [p]} for p in params], **kw)
+    report = []
+    for t in range(1, meta["steps"] + 1):
+        for p, g in zip(params, gu.grads_for(meta, params, t)):
+            p.grad = g.cuda()
+        opt.step()
+        if t not in meta["save_steps"]:
+            continue
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            key = f"s{t}/p{i}"
+            ref_p = z[f"{key}/param"]
+            np.testing.assert_allclose(p.detach().cpu().numpy(), ref_p, rtol=1e-5, atol=1e-8,
+                                       err_msg=f"{name} {key} param")
+            zkeys = [k[len(key) + 1:] for k in z.files if k.startswith(key + "/") and
+                     not k.endswith("/param")]
+            _cmp_state(name, key, opt.state[p], z, zkeys, report)
+    print(report)

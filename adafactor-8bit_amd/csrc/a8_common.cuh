@@ -20,8 +20,18 @@
 
 namespace a8 {
 
+// Global-memory (address space 1) view of a pointer: descriptor-table pointers
+// would otherwise be generic (flat), costing flat_load/flat_store and combined
+// vmcnt/lgkmcnt waits against LDS traffic.
+#define A8_G __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ A8_G T* gp(T* p) { return (A8_G T*)p; }
+template <typename T>
+__device__ __forceinline__ const A8_G T* gp(const T* p) { return (const A8_G T*)p; }
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kFltMin = 1.17549435e-38f;   // FP32 smallest normal
 constexpr float kLogClampIn = 1e-38f;        // clamp(min=1e-38) before log2 (optimizer.py:309)
@@ -53,8 +63,8 @@ __device__ __forceinline__ float scrub(float g) {
 struct ALFit {
   float lmin;     // new min_log
   float s;        // new scale
-  float rs;       // ~1/s
-  float kmar;     // margin slope: (L-2) * rs * 2^-20
+  float k;        // ~ (L-2)/s
+  float kmar;     // fast-path margin slope: k * 2^-22
 };
 
 // Refit from the block's max v and min non-zero v (optimizer.py:308-318):
@@ -62,52 +72,74 @@ struct ALFit {
 // if lmin >= lmax, scale = max(lmax - lmin, 1e-12).
 __device__ __forceinline__ ALFit al_refit(float vmax, float vmin_nz, float floor_, float levels_m2) {
   ALFit f;
-  float lmax = log2_exact(fmaxf(vmax, kLogClampIn));
+  const float lmax = log2_exact(fmaxf(vmax, kLogClampIn));
   float lmin = (vmin_nz == __builtin_inff()) ? __builtin_inff()
                                               : log2_exact(fmaxf(vmin_nz, kLogClampIn));
   lmin = fmaxf(lmin, floor_);
   if (lmin >= lmax) lmin = lmax - 1.0f;
-  float s = fmaxf(lmax - lmin, 1e-12f);
+  const float s = fmaxf(lmax - lmin, 1e-12f);
   f.lmin = lmin;
   f.s = s;
-  f.rs = fast_rcp(s);
-  f.kmar = levels_m2 * f.rs * 0x1p-20f;
+  f.k = levels_m2 * fast_rcp(s);
+  f.kmar = f.k * 0x1p-22f;
   return f;
 }
 
-// AL code of a non-negative value; LM2 = levels - 2 (254 or 65534).
+// Exact AL rounding argument: correctly rounded log2 and IEEE division, in the
+// reference's operation order ((log2(max(v,1e-38)) - lmin) / s) * (L-2).
 template <int LM2>
-__device__ __forceinline__ uint32_t al_code(float v, const ALFit& f) {
-  if (v == 0.0f) return 0u;
-  float x = fmaxf(v, kLogClampIn);
-  float r = 0.0f;
-  bool done = false;
-  if (LM2 == 254 && x >= kFltMin) {
-    float lf = __builtin_amdgcn_logf(x);
-    float t = ((lf - f.lmin) * f.rs) * 254.0f;
-    r = rintf(t);
-    float margin = fmaxf(fabsf(lf), 1.0f) * f.kmar + 1.25e-4f;
-    done = fabsf(fabsf(t - r) - 0.5f) > margin;
-  }
-  if (!done) {
-    float le = log2_exact(x);
-    float t = ((le - f.lmin) / f.s) * (float)LM2;
-    r = rintf(t);
-  }
-  float q = fminf(fmaxf(r + 1.0f, 1.0f), (float)(LM2 + 1));
-  return (uint32_t)q;
+__device__ __forceinline__ float al_round_exact(float v, const ALFit& f) {
+  const float le = log2_exact(fmaxf(v, kLogClampIn));
+  return rintf(((le - f.lmin) / f.s) * (float)LM2);
 }
 
-// UF code (b = 8 or 4): rint((m / amax) * H) clamped to [-H, H-1] plus H.
+// Fast AL8 rounding argument from the hardware log2 (faithful: |error| <= |l|*2^-23,
+// measured on gfx950) and k ~ 254/s.  |t_fast - t_exact| <= |l|*k*2^-23 + 1.2e-4
+// (the rounding of the difference, the reciprocal and the two products, t <= 255),
+// so the rounded value is the exact one whenever t lies farther than the margin
+// |l|*k*2^-22 + 1.5e-4 from a half-integer.  ok=false flags the rest (and
+// subnormal inputs) for al_round_exact; v == 0 needs no rounding (code 0).
+__device__ __forceinline__ float al8_round_fast(float v, const ALFit& f, bool& ok) {
+  const float lf = __builtin_amdgcn_logf(v);
+  const float t = (lf - f.lmin) * f.k;
+  const float r = rintf(t);
+  const float e = fabsf(fabsf(t - r) - 0.5f);
+  ok = (v == 0.0f) || ((v >= kFltMin) && (e > __builtin_fmaf(fabsf(lf), f.kmar, 1.5e-4f)));
+  return r;
+}
+
+template <int LM2>
+__device__ __forceinline__ uint32_t al_finish(float v, float r) {
+  const float q = __builtin_amdgcn_fmed3f(r + 1.0f, 1.0f, (float)(LM2 + 1));
+  return (v == 0.0f) ? 0u : (uint32_t)q;
+}
+
+// Fast UF rounding argument: t = m * (H/absmax) with a faithful reciprocal;
+// |t_fast - t_exact| <= H*2^-22 (t = (m/absmax)*H exactly scaled by H = 2^k).
+template <int H>
+__device__ __forceinline__ float uf_round_fast(float m, float kam, bool& ok) {
+  const float t = m * kam;
+  const float r = rintf(t);
+  ok = fabsf(fabsf(t - r) - 0.5f) > (float)H * 0x1p-20f;
+  return r;
+}
+
+template <int H>
+__device__ __forceinline__ float uf_round_exact(float m, float amax) {
+  return rintf((m / amax) * (float)H);
+}
+
+template <int H>
+__device__ __forceinline__ uint32_t uf_finish(float r) {
+  return (uint32_t)(__builtin_amdgcn_fmed3f(r, (float)(-H), (float)(H - 1)) + (float)H);
+}
+
 template <int H>
 __device__ __forceinline__ uint32_t uf_code(float m, float amax, float ramax) {
-  float t = (m * ramax) * (float)H;
-  float r = rintf(t);
-  if (!(fabsf(fabsf(t - r) - 0.5f) > 1.25e-4f)) {
-    r = rintf((m / amax) * (float)H);
-  }
-  r = fminf(fmaxf(r, (float)(-H)), (float)(H - 1));
-  return (uint32_t)(int)(r + (float)H);
+  bool ok;
+  float r = uf_round_fast<H>(m, (float)H * ramax, ok);
+  if (!ok) r = uf_round_exact<H>(m, amax);
+  return uf_finish<H>(r);
 }
 
 // ---------------------------------------------------------------- dtypes
@@ -125,25 +157,50 @@ template <> __device__ __forceinline__ __hip_bfloat16 from_f<__hip_bfloat16>(flo
 }
 template <> __device__ __forceinline__ __half from_f<__half>(float x) { return __float2half(x); }
 
+// Single-element global load / store of a param-typed value (16-bit types go
+// through their bit pattern: class types cannot be bound in address space 1).
+template <typename T>
+__device__ __forceinline__ float ld1(const T* p, int64_t i) {
+  if constexpr (sizeof(T) == 4) {
+    return gp(reinterpret_cast<const float*>(p))[i];
+  } else {
+    const uint16_t b = gp(reinterpret_cast<const uint16_t*>(p))[i];
+    T t;
+    __builtin_memcpy(&t, &b, 2);
+    return to_f<T>(t);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st1(T* p, int64_t i, float v) {
+  if constexpr (sizeof(T) == 4) {
+    gp(reinterpret_cast<float*>(p))[i] = v;
+  } else {
+    const T t = from_f<T>(v);
+    uint16_t b;
+    __builtin_memcpy(&b, &t, 2);
+    gp(reinterpret_cast<uint16_t*>(p))[i] = b;
+  }
+}
+
 // Load / store 8 consecutive elements (aligned fast path when fully in range).
 template <typename T>
 __device__ __forceinline__ void load8(const T* base, int64_t i0, int64_t n, float* out) {
   if (i0 + 8 <= n) {
     if constexpr (sizeof(T) == 4) {
-      const f32x4* p = reinterpret_cast<const f32x4*>(base + i0);
+      const A8_G f32x4* p = gp(reinterpret_cast<const f32x4*>(base + i0));
       f32x4 a = __builtin_nontemporal_load(p);
       f32x4 b = __builtin_nontemporal_load(p + 1);
       out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
       out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
     } else {
-      u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + i0));
+      u32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const u32x4*>(base + i0)));
       const T* h = reinterpret_cast<const T*>(&a);
 #pragma unroll
       for (int k = 0; k < 8; ++k) out[k] = to_f<T>(h[k]);
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = (i0 + k < n) ? to_f<T>(base[i0 + k]) : 0.0f;
+    for (int k = 0; k < 8; ++k) out[k] = (i0 + k < n) ? ld1<T>(base, i0 + k) : 0.0f;
   }
 }
 
@@ -151,7 +208,7 @@ template <typename T>
 __device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const float* v) {
   if (i0 + 8 <= n) {
     if constexpr (sizeof(T) == 4) {
-      f32x4* p = reinterpret_cast<f32x4*>(base + i0);
+      A8_G f32x4* p = gp(reinterpret_cast<f32x4*>(base + i0));
       f32x4 a = {v[0], v[1], v[2], v[3]};
       f32x4 b = {v[4], v[5], v[6], v[7]};
       __builtin_nontemporal_store(a, p);
@@ -161,12 +218,12 @@ __device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const flo
       T* h = reinterpret_cast<T*>(&a);
 #pragma unroll
       for (int k = 0; k < 8; ++k) h[k] = from_f<T>(v[k]);
-      __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(base + i0));
+      __builtin_nontemporal_store(a, gp(reinterpret_cast<u32x4*>(base + i0)));
     }
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (i0 + k < n) base[i0 + k] = from_f<T>(v[k]);
+      if (i0 + k < n) st1<T>(base, i0 + k, v[k]);
   }
 }
 

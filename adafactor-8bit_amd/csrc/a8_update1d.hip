@@ -51,6 +51,8 @@ struct Hyper1D {
   int mk;          // momentum codec
   int adam_denom;
   int momentum_only;
+  int lbv;          // log2(block_size)
+  int lbm;          // log2(m_block_size)
   float alpha_val;  // used when a tensor's alpha pointer is NULL
   float decay_val;  // used when a tensor's decay pointer is NULL and has_decay
   int has_decay;
@@ -187,29 +189,44 @@ __device__ __forceinline__ const Desc1D* find_desc(const Desc1D* tab, int n, int
   return tab + lo;
 }
 
-template <typename T, int VB, int MODE, bool SR>
+// Integer view of a non-negative float minus one: for v >= 0 the unsigned
+// order of these keys is the float order, and v == 0 maps to 0xFFFFFFFF, so an
+// unsigned min over keys is the minimum over the non-zero entries.
+__device__ __forceinline__ uint32_t nz_key(float v) { return __float_as_uint(v) - 1u; }
+__device__ __forceinline__ uint32_t grp_umin(uint32_t x, int G) {
+  for (int o = 1; o < G; o <<= 1) x = min(x, (uint32_t)__shfl_xor((int)x, o, 64));
+  return x;
+}
+
+// MK: 0 no momentum, 1 UF8 (specialised), 2 UF4/D8/D4 (codec chosen by h.mk).
+template <typename T, int VB, int MODE, bool SR, int MK>
 __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* __restrict__ table,
                                                    int ntab, Hyper1D h) {
-  extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | [8] cross-wave partials
+  extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | [16] cross-wave partials
+  constexpr bool kHasM = MK != 0;
   const Desc1D D = table ? *find_desc(table, ntab, (int64_t)blockIdx.x) : one;
   const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
   const int64_t n = D.numel;
-  const int BV = h.block_size, BM = h.m_block_size;
-  const int VL = BV >> 3;                       // lanes per V block (16..256)
-  const int ML = BM >> 3;                       // lanes per M block (4..256)
-  const int nv_wg = kWGElems / BV;              // V blocks per workgroup
+  // block sizes are powers of two: all block arithmetic is shifts and masks
+  const int lbv = h.lbv, lbm = h.lbm;
+  const int BV = 1 << lbv, BM = 1 << lbm;
+  const int VL = BV >> 3;                        // lanes per V block (16..256)
+  const int ML = BM >> 3;                        // lanes per M block (4..256)
+  const int nv_wg = kWGElems >> lbv;             // V blocks per workgroup
   const int64_t e0 = wl * kWGElems + (int64_t)lane * kEPT;
-  const int64_t nvb = (n + BV - 1) / BV;
-  const int64_t nmb = (n + BM - 1) / BM;
-  const int64_t vb = e0 / BV;
-  const int64_t mb = e0 / BM;
+  const int64_t nvb = (n + BV - 1) >> lbv;
+  const int64_t nmb = (n + BM - 1) >> lbm;
+  const int64_t vb = e0 >> lbv;
+  const int64_t mb = e0 >> lbm;
   const bool v_ok = vb < nvb;
-  const bool has_m = h.mk != 0;
-  const bool m_ok = has_m && (mb < nmb);
-  const int vloc = lane / VL;                    // V block index inside the workgroup
-  float* tabs = s_lds;                           // AL8 decode tables
-  float* xw = s_lds + (VB == 8 && MODE != 2 ? nv_wg * 256 : 0);  // 4 waves x 4 floats
+  const bool m_ok = kHasM && (mb < nmb);
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= kEPT ? kEPT : (int)rem);   // valid elements of this lane
+  const int vloc = lane >> (lbv - 3);
+  const int mk = (MK == 1) ? 1 : h.mk;
+  float* tabs = s_lds;
+  float* xw = s_lds + ((VB == 8 && MODE != 2) ? nv_wg * 256 : 0);  // 4 waves x 4 floats
 
   // ---- AL8 decode tables for this workgroup's V blocks
   if constexpr (VB == 8 && MODE != 2) {
@@ -219,8 +236,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       const int c = k & 255;
       float val = 0.0f;
       if (b < nvb && c != 0) {
-        const float s = D.v_scale[b], lm = D.v_min_log[b];
-        val = exp2_exact(((float)(c - 1) * s) / 254.0f + lm);
+        const float sc = gp(D.v_scale)[b], lm = gp(D.v_min_log)[b];
+        val = exp2_exact(((float)(c - 1) * sc) / 254.0f + lm);
       }
       tabs[k] = val;
     }
@@ -230,130 +247,151 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   // ---- step scale
   float step = 0.0f, ut_clip = 1.0f;
   if constexpr (MODE != 1) {
-    const float a = D.alpha ? *D.alpha : h.alpha_val;
+    const float a = D.alpha ? *gp(D.alpha) : h.alpha_val;
     if constexpr (MODE == 0) {
       step = a;
     } else {
       float denom = 1.0f;
       if (h.d > 0.0f) {
-        const float nrm = (MODE == 2) ? sqrtf(*D.norm_buf) : *D.prev_norm;
+        const float nrm = (MODE == 2) ? sqrtf(*gp(D.norm_buf)) : *gp(D.prev_norm);
         // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
         // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
-        if (h.momentum_only && has_m)
+        if (h.momentum_only && kHasM)
           denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
         else
           denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));
       }
-      if (h.momentum_only && has_m) { step = a; ut_clip = denom; }
+      if (h.momentum_only && kHasM) { step = a; ut_clip = denom; }
       else { step = a / denom; }
     }
   }
 
-  float g[kEPT], vn[kEPT], mn[kEPT];
-  float vmax = 0.0f, vmin = __builtin_inff(), amax = 0.0f, sq = 0.0f;
+  float vn[kEPT], mn[kEPT];
+  float vmax = 0.0f, amax = 0.0f, sq = 0.0f;
+  uint32_t vkey = 0xFFFFFFFFu;
 
   if (v_ok) {
+    float g[kEPT];
     load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
+    {  // non-finite gradients become 0 (kernels.cu:43-46); one test per lane
+      float t = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+      if (!__builtin_isfinite(t)) {
 #pragma unroll
-    for (int k = 0; k < kEPT; ++k) g[k] = (e0 + k < n) ? scrub(g[k]) : 0.0f;
+        for (int k = 0; k < kEPT; ++k) g[k] = scrub(g[k]);
+      }
+    }
 
-    // ---- V: decode + EMA (or the exact V of the NORM pass)
+    // ---- V: decode + EMA (APPLY reads the exact V of the NORM pass)
     if constexpr (MODE == 2) {
 #pragma unroll
-      for (int k = 0; k < kEPT; ++k) vn[k] = (e0 + k < n) ? D.v_buf[e0 + k] : 0.0f;
+      for (int k = 0; k < kEPT; ++k) vn[k] = (k < cnt) ? gp(D.v_buf)[e0 + k] : 0.0f;
     } else {
       float vo[kEPT];
-      const float s_old = D.v_scale[vb], lm_old = D.v_min_log[vb];
       if constexpr (VB == 8) {
-        const uint2 qv = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0);
+        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
         const float* tb = tabs + vloc * 256;
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          uint32_t c = ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu;
-          vo[k] = tb[c];
-        }
+        for (int k = 0; k < kEPT; ++k) vo[k] = tb[((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu];
       } else {
-        const uint4 qv = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0);
+        const float s_old = gp(D.v_scale)[vb], lm_old = gp(D.v_min_log)[vb];
+        const u32x4 qv = *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0));
         const uint32_t w4[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
-          uint32_t c = (w4[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+          const uint32_t c = (w4[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
           vo[k] = c ? exp2_exact(((float)(c - 1) * s_old) / 65534.0f + lm_old) : 0.0f;
         }
       }
+      float gsq[kEPT];
 #pragma unroll
-      for (int k = 0; k < kEPT; ++k) {
-        const float gsq = g[k] * g[k] + h.eps_g;
-        const float v = lerp_ref(vo[k], gsq, h.bv);
-        vn[k] = (e0 + k < n) ? v : 0.0f;
-      }
-      if constexpr (MODE == 1) {
+      for (int k = 0; k < kEPT; ++k) gsq[k] = g[k] * g[k];
+      if (h.eps_g != 0.0f) {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k)
-          if (e0 + k < n) D.v_buf[e0 + k] = vn[k];
+        for (int k = 0; k < kEPT; ++k) gsq[k] = gsq[k] + h.eps_g;
       }
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) vn[k] = lerp_ref(vo[k], gsq[k], h.bv);
     }
 
-    // ---- M decode + EMA, update direction
+    // ---- M decode
     float mo[kEPT];
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) mo[k] = 0.0f;
     if (m_ok) {
-      const float ms = D.m_scale[mb];
-      if (h.mk == 2 || h.mk == 4) {
-        const uint32_t qw = *reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1));
+      const float ms = gp(D.m_scale)[mb];
+      if (MK == 1) {
+        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+        const float s128 = ms / 128.0f, b128 = -128.0f * s128;   // (q-128)*s128 == fma(q, s128, -128*s128)
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k)
+          mo[k] = __builtin_fmaf((float)(((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu), s128, b128);
+      } else if (mk == 2 || mk == 4) {
+        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
           const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
-          const uint32_t c = (k & 1) ? (byte & 0x0Fu) : (byte >> 4);
-          mo[k] = m_decode(h.mk, c, ms);
+          mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
         }
       } else {
-        const uint2 qw = *reinterpret_cast<const uint2*>(D.m_q + e0);
+        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          const uint32_t c = ((k < 4 ? qw.x : qw.y) >> (8 * (k & 3))) & 0xFFu;
-          mo[k] = m_decode(h.mk, c, ms);
-        }
+        for (int k = 0; k < kEPT; ++k)
+          mo[k] = m_decode(mk, ((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < kEPT; ++k) mo[k] = 0.0f;
     }
 
-    float u[kEPT];
+    // ---- M EMA and update direction
+    float uu[kEPT];
+    const bool exact_inv = !h.adam_denom && h.momentum_only && kHasM;
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) {
-      const bool in = e0 + k < n;
       float inv;
       if (h.adam_denom) {
         inv = fast_rcp(fast_sqrt(vn[k]) + h.eps_d);
-      } else {
-        // feeds the momentum codes when momentum_only: IEEE sqrt then division,
-        // as torch's rsqrt on the CPU (optimizer.py:893)
+      } else if (exact_inv) {
+        // feeds the momentum codes: IEEE sqrt then division, as torch's rsqrt on the CPU
+        // (optimizer.py:893)
         inv = 1.0f / sqrtf(fmaxf(vn[k], h.eps_sq));
+      } else {
+        inv = __builtin_amdgcn_rsqf(fmaxf(vn[k], h.eps_sq));
       }
-      float uu;
-      if (has_m) {
-        float x;
+      if constexpr (kHasM) {
+        float x = g[k];
         if (h.momentum_only) {
-          float ut = g[k] * inv;
-          if (MODE == 1) { sq += in ? ut * ut : 0.0f; }
+          const float ut = g[k] * inv;
+          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(ut, ut, sq);
           x = (ut_clip != 1.0f) ? ut / ut_clip : ut;
+          mn[k] = lerp_ref(mo[k], x, h.w_m);
+          uu[k] = mn[k];
         } else {
-          x = g[k];
+          mn[k] = lerp_ref(mo[k], x, h.w_m);
+          uu[k] = mn[k] * inv;
+          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
         }
-        const float m = lerp_ref(mo[k], x, h.w_m);
-        mn[k] = in ? m : 0.0f;
-        uu = h.momentum_only ? m : m * inv;
-        if (!h.momentum_only && (MODE == 1 || MODE == 3)) sq += in ? uu * uu : 0.0f;
-        if (h.momentum_only && MODE == 3) { const float ut = g[k] * inv; sq += in ? ut * ut : 0.0f; }
       } else {
         mn[k] = 0.0f;
-        uu = h.adam_denom ? g[k] * inv : g[k] * inv;
-        if (MODE == 1 || MODE == 3) sq += in ? uu * uu : 0.0f;
+        uu[k] = g[k] * inv;
+        if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
       }
-      u[k] = in ? uu : 0.0f;
+    }
+    if (cnt < kEPT) {  // the last lane of a tensor: padding elements hold zero state
+      sq = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) {
+        if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; uu[k] = 0.0f; }
+        const float ut = (kHasM && h.momentum_only) ? g[k] * (1.0f / sqrtf(fmaxf(vn[k], h.eps_sq))) : uu[k];
+        if ((MODE == 1 || MODE == 3) && k < cnt) sq = __builtin_fmaf(ut, ut, sq);
+      }
+    }
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k)
+        if (k < cnt) gp(D.v_buf)[e0 + k] = vn[k];
+    }
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) {
       vmax = fmaxf(vmax, vn[k]);
-      if (vn[k] > 0.0f) vmin = fminf(vmin, vn[k]);
+      vkey = min(vkey, nz_key(vn[k]));
       amax = fmaxf(amax, fabsf(mn[k]));
     }
 
@@ -361,13 +399,13 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     if constexpr (MODE != 1) {
       T* P = reinterpret_cast<T*>(D.param);
       const bool has_dec = D.decay || h.has_decay;
-      const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
+      const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
       if constexpr (SR) {
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
-          if (e0 + k < n) {
+          if (k < cnt) {
             const float pv = to_f<T>(P[e0 + k]);
-            P[e0 + k] = sr_round<T>(pv * dec - step * u[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
+            P[e0 + k] = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
           }
         }
       } else {
@@ -378,7 +416,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
           for (int k = 0; k < kEPT; ++k) p[k] = p[k] * dec;
         }
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) p[k] = __builtin_fmaf(-step, u[k], p[k]);
+        for (int k = 0; k < kEPT; ++k) p[k] = __builtin_fmaf(-step, uu[k], p[k]);
         store8<T>(P, e0, n, p);
       }
     }
@@ -392,77 +430,110 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   // ---- V refit + codes
   if constexpr (MODE != 2) {
     float bmax = grp_max(vmax, VL < 64 ? VL : 64);
-    float bmin = grp_min(vmin, VL < 64 ? VL : 64);
+    uint32_t bkey = grp_umin(vkey, VL < 64 ? VL : 64);
     if (VL > 64) {
-      if ((lane & 63) == 0) { xw[wave * 4 + 0] = bmax; xw[wave * 4 + 1] = bmin; }
+      if ((lane & 63) == 0) { xw[wave * 4 + 0] = bmax; xw[wave * 4 + 1] = __uint_as_float(bkey); }
       __syncthreads();
-      const int w0 = (lane / VL) * (VL >> 6);
-      bmax = xw[w0 * 4]; bmin = xw[w0 * 4 + 1];
+      const int w0 = (lane >> (lbv - 3)) * (VL >> 6);
+      bmax = xw[w0 * 4];
+      bkey = __float_as_uint(xw[w0 * 4 + 1]);
       for (int w = 1; w < (VL >> 6); ++w) {
         bmax = fmaxf(bmax, xw[(w0 + w) * 4]);
-        bmin = fminf(bmin, xw[(w0 + w) * 4 + 1]);
+        bkey = min(bkey, __float_as_uint(xw[(w0 + w) * 4 + 1]));
       }
     }
     if (v_ok) {
+      const float bmin = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
       const ALFit f = al_refit(bmax, bmin, h.floor_, VB == 8 ? 254.0f : 65534.0f);
+      uint32_t q[kEPT];
       if constexpr (VB == 8) {
-        uint32_t w0 = 0, w1 = 0;
+        float r[kEPT];
+        uint32_t need = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w0 |= al_code<254>(vn[k], f) << (8 * k);
+        for (int k = 0; k < kEPT; ++k) {
+          bool ok;
+          r[k] = al8_round_fast(vn[k], f, ok);
+          need |= ok ? 0u : (1u << k);
+        }
+        if (need) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w1 |= al_code<254>(vn[k + 4], f) << (8 * k);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0) = make_uint2(w0, w1);
+          for (int k = 0; k < kEPT; ++k)
+            if (need & (1u << k)) r[k] = al_round_exact<254>(vn[k], f);
+        }
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) q[k] = al_finish<254>(vn[k], r[k]);
+        const uint32_t w0 = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+        const uint32_t w1 = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) = u32x2{w0, w1};
       } else {
-        uint32_t w[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[j] = al_code<65534>(vn[2 * j], f) | (al_code<65534>(vn[2 * j + 1], f) << 16);
-        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(D.v_q) + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+        for (int k = 0; k < kEPT; ++k) q[k] = al_finish<65534>(vn[k], al_round_exact<65534>(vn[k], f));
+        *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(D.v_q) + e0)) =
+            u32x4{q[0] | (q[1] << 16), q[2] | (q[3] << 16), q[4] | (q[5] << 16), q[6] | (q[7] << 16)};
       }
-      if ((lane % VL) == 0) { D.v_scale[vb] = f.s; D.v_min_log[vb] = f.lmin; }
+      if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }
     }
   }
 
   // ---- M refit + codes
-  if constexpr (MODE != 1) {
-    if (has_m) {
-      float bam = grp_max(amax, ML < 64 ? ML : 64);
-      if (ML > 64) {
-        __syncthreads();
-        if ((lane & 63) == 0) xw[wave * 4 + 2] = bam;
-        __syncthreads();
-        const int w0 = (lane / ML) * (ML >> 6);
-        bam = xw[w0 * 4 + 2];
-        for (int w = 1; w < (ML >> 6); ++w) bam = fmaxf(bam, xw[(w0 + w) * 4 + 2]);
-      }
-      if (m_ok) {
-        const float am = fmaxf(bam, 1e-12f);
-        const float ram = fast_rcp(am);
-        if (h.mk == 2 || h.mk == 4) {
-          uint32_t w = 0;
+  if constexpr (MODE != 1 && kHasM) {
+    float bam = grp_max(amax, ML < 64 ? ML : 64);
+    if (ML > 64) {
+      __syncthreads();
+      if ((lane & 63) == 0) xw[wave * 4 + 2] = bam;
+      __syncthreads();
+      const int w0 = (lane >> (lbm - 3)) * (ML >> 6);
+      bam = xw[w0 * 4 + 2];
+      for (int w = 1; w < (ML >> 6); ++w) bam = fmaxf(bam, xw[(w0 + w) * 4 + 2]);
+    }
+    if (m_ok) {
+      const float am = fmaxf(bam, 1e-12f);
+      const float ram = fast_rcp(am);
+      if (MK == 1) {
+        const float kam = 128.0f * ram;
+        float r[kEPT];
+        uint32_t need = 0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t hi = m_encode(h.mk, mn[2 * j], am, ram);
-            const uint32_t lo = m_encode(h.mk, mn[2 * j + 1], am, ram);
-            w |= ((hi << 4) | lo) << (8 * j);
-          }
-          *reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1)) = w;
-        } else {
-          uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) w0 |= m_encode(h.mk, mn[k], am, ram) << (8 * k);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) w1 |= m_encode(h.mk, mn[k + 4], am, ram) << (8 * k);
-          *reinterpret_cast<uint2*>(D.m_q + e0) = make_uint2(w0, w1);
+        for (int k = 0; k < kEPT; ++k) {
+          bool ok;
+          r[k] = uf_round_fast<128>(mn[k], kam, ok);
+          need |= ok ? 0u : (1u << k);
         }
-        if ((lane % ML) == 0) D.m_scale[mb] = am;
+        if (need) {
+#pragma unroll
+          for (int k = 0; k < kEPT; ++k)
+            if (need & (1u << k)) r[k] = uf_round_exact<128>(mn[k], am);
+        }
+        uint32_t q[kEPT];
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) q[k] = uf_finish<128>(r[k]);
+        const uint32_t w0 = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+        const uint32_t w1 = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
+      } else if (mk == 2 || mk == 4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t hi = m_encode(mk, mn[2 * j], am, ram);
+          const uint32_t lo = m_encode(mk, mn[2 * j + 1], am, ram);
+          w |= ((hi << 4) | lo) << (8 * j);
+        }
+        *gp(reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1))) = w;
+      } else {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w0 |= m_encode(mk, mn[k], am, ram) << (8 * k);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w1 |= m_encode(mk, mn[k + 4], am, ram) << (8 * k);
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
       }
+      if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
     }
   }
 
   // ---- sum of squares for NORM / LAG
   if constexpr (MODE == 1 || MODE == 3) {
-    float t = grp_sum(sq, 64);
+    const float t = grp_sum(sq, 64);
     if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
   }
 }
@@ -473,28 +544,38 @@ static bool fast_shape_ok(int bv, int bm) {
   return pow2(bv) && bv >= 128 && bv <= 2048 && pow2(bm) && bm >= 32 && bm <= bv;
 }
 
-template <typename T, int VB, int MODE, bool SR>
+template <typename T, int VB, int MODE, bool SR, int MK>
 static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
                     hipStream_t st) {
   const int nv_wg = kWGElems / h.block_size;
   size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 16 * sizeof(float);
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
-  hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,
+  hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,
                      table, ntab, h);
   return check_launch("k_update1d");
 }
 
-template <typename T, bool SR>
-static int launch_dispatch(int vbits, int mode, const Desc1D& one, const Desc1D* table, int ntab,
-                           int64_t nwg, const Hyper1D& h, hipStream_t st) {
-#define A8_L(VB, MO) return launch_t<T, VB, MO, SR>(one, table, ntab, nwg, h, st)
+template <typename T, bool SR, int MK>
+static int launch_mode(int vbits, int mode, const Desc1D& one, const Desc1D* table, int ntab,
+                       int64_t nwg, const Hyper1D& h, hipStream_t st) {
+#define A8_L(VB, MO) return launch_t<T, VB, MO, SR, MK>(one, table, ntab, nwg, h, st)
   if (vbits == 8) {
     switch (mode) { case 0: A8_L(8, 0); case 1: A8_L(8, 1); case 2: A8_L(8, 2); default: A8_L(8, 3); }
   } else {
     switch (mode) { case 0: A8_L(16, 0); case 1: A8_L(16, 1); case 2: A8_L(16, 2); default: A8_L(16, 3); }
   }
 #undef A8_L
+}
+
+template <typename T, bool SR>
+static int launch_dispatch(int vbits, int mode, const Desc1D& one, const Desc1D* table, int ntab,
+                           int64_t nwg, const Hyper1D& h, hipStream_t st) {
+  switch (h.mk) {
+    case 0: return launch_mode<T, SR, 0>(vbits, mode, one, table, ntab, nwg, h, st);
+    case 1: return launch_mode<T, SR, 1>(vbits, mode, one, table, ntab, nwg, h, st);
+    default: return launch_mode<T, SR, 2>(vbits, mode, one, table, ntab, nwg, h, st);
+  }
 }
 
 static int launch_any(int dtype, int sr, int vbits, int mode, const Desc1D& one, const Desc1D* table,
@@ -524,6 +605,12 @@ static int check_common(int dtype, int64_t numel, int bv, int bm, int mbits, int
     return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
   return 0;
+}
+
+static int ilog2(int x) {
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
 }
 
 static int mk_of(int mbits, int mmode) {
@@ -568,6 +655,7 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
   h.floor_ = log_floor; h.d = d;
   h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
+  h.lbv = ilog2(h.block_size); h.lbm = ilog2(h.m_block_size);
   h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
   h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
   h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
@@ -633,6 +721,7 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
   h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
   h.floor_ = log_floor; h.d = d;
   h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
+  h.lbv = ilog2(h.block_size); h.lbm = ilog2(h.m_block_size);
   h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
   h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
   h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;

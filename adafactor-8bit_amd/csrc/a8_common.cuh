@@ -85,6 +85,27 @@ __device__ __forceinline__ ALFit al_refit(float vmax, float vmin_nz, float floor
   return f;
 }
 
+// Same refit, with the two correctly rounded logarithms of a block computed in
+// one call per wave: even lanes take log2 of the block max, odd lanes of the
+// block min, and every lane reads its block's pair back.  Requires that the
+// block's lanes hold the same (vmax, vmin_nz) and span at least two lanes.
+__device__ __forceinline__ ALFit al_refit_pair(float vmax, float vmin_nz, float floor_, float levels_m2,
+                                               int lane) {
+  const float x = (lane & 1) ? vmin_nz : vmax;   // inf (no non-zero entry) stays inf
+  const float l = log2_exact(fmaxf(x, kLogClampIn));
+  const float lmax = __shfl(l, lane & ~1, 64);
+  float lmin = __shfl(l, lane | 1, 64);
+  ALFit f;
+  lmin = fmaxf(lmin, floor_);
+  if (lmin >= lmax) lmin = lmax - 1.0f;
+  const float s = fmaxf(lmax - lmin, 1e-12f);
+  f.lmin = lmin;
+  f.s = s;
+  f.k = levels_m2 * fast_rcp(s);
+  f.kmar = f.k * 0x1p-22f;
+  return f;
+}
+
 // Exact AL rounding argument: correctly rounded log2 and IEEE division, in the
 // reference's operation order ((log2(max(v,1e-38)) - lmin) / s) * (L-2).
 template <int LM2>
@@ -99,12 +120,15 @@ __device__ __forceinline__ float al_round_exact(float v, const ALFit& f) {
 // so the rounded value is the exact one whenever t lies farther than the margin
 // |l|*k*2^-22 + 1.5e-4 from a half-integer.  ok=false flags the rest (and
 // subnormal inputs) for al_round_exact; v == 0 needs no rounding (code 0).
-__device__ __forceinline__ float al8_round_fast(float v, const ALFit& f, bool& ok) {
+__device__ __forceinline__ float al8_round_fast(float v, const ALFit& f, uint32_t& bad) {
   const float lf = __builtin_amdgcn_logf(v);
   const float t = (lf - f.lmin) * f.k;
   const float r = rintf(t);
   const float e = fabsf(fabsf(t - r) - 0.5f);
-  ok = (v == 0.0f) || ((v >= kFltMin) && (e > __builtin_fmaf(fabsf(lf), f.kmar, 1.5e-4f)));
+  // branch-free: bad = 1 when neither "v == 0" nor "normal and outside the margin"
+  const uint32_t good = (uint32_t)(v == 0.0f) |
+                        ((uint32_t)(v >= kFltMin) & (uint32_t)(e > __builtin_fmaf(fabsf(lf), f.kmar, 1.5e-4f)));
+  bad = good ^ 1u;
   return r;
 }
 
@@ -117,10 +141,10 @@ __device__ __forceinline__ uint32_t al_finish(float v, float r) {
 // Fast UF rounding argument: t = m * (H/absmax) with a faithful reciprocal;
 // |t_fast - t_exact| <= H*2^-22 (t = (m/absmax)*H exactly scaled by H = 2^k).
 template <int H>
-__device__ __forceinline__ float uf_round_fast(float m, float kam, bool& ok) {
+__device__ __forceinline__ float uf_round_fast(float m, float kam, uint32_t& bad) {
   const float t = m * kam;
   const float r = rintf(t);
-  ok = fabsf(fabsf(t - r) - 0.5f) > (float)H * 0x1p-20f;
+  bad = (uint32_t)!(fabsf(fabsf(t - r) - 0.5f) > (float)H * 0x1p-20f);
   return r;
 }
 
@@ -136,9 +160,9 @@ __device__ __forceinline__ uint32_t uf_finish(float r) {
 
 template <int H>
 __device__ __forceinline__ uint32_t uf_code(float m, float amax, float ramax) {
-  bool ok;
-  float r = uf_round_fast<H>(m, (float)H * ramax, ok);
-  if (!ok) r = uf_round_exact<H>(m, amax);
+  uint32_t bad;
+  float r = uf_round_fast<H>(m, (float)H * ramax, bad);
+  if (bad) r = uf_round_exact<H>(m, amax);
   return uf_finish<H>(r);
 }
 

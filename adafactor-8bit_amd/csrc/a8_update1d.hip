@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   const int vloc = lane >> (lbv - 3);
   const int mk = (MK == 1) ? 1 : h.mk;
   float* tabs = s_lds;
-  float* xw = s_lds + ((VB == 8 && MODE != 2) ? nv_wg * 256 : 0);  // 4 waves x 4 floats
+  float* xw = s_lds + ((VB == 8 && MODE != 2) ? nv_wg * 256 : 0);  // 4 waves x 4 | 4 fits x 4
 
   // ---- AL8 decode tables for this workgroup's V blocks
   if constexpr (VB == 8 && MODE != 2) {
@@ -267,7 +267,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   }
 
   float vn[kEPT], mn[kEPT];
-  float vmax = 0.0f, amax = 0.0f, sq = 0.0f;
+  float sq = 0.0f;
+  uint32_t vmaxb = 0u, amaxb = 0u;   // max of non-negative floats as integer bit patterns
   uint32_t vkey = 0xFFFFFFFFu;
 
   if (v_ok) {
@@ -309,8 +310,15 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) gsq[k] = gsq[k] + h.eps_g;
       }
+      // torch.lerp: fma(w, e - s, s) for |w| < 0.5, else fma(w - 1, e - s, e)
+      if (fabsf(h.bv) < 0.5f) {
 #pragma unroll
-      for (int k = 0; k < kEPT; ++k) vn[k] = lerp_ref(vo[k], gsq[k], h.bv);
+        for (int k = 0; k < kEPT; ++k) vn[k] = __builtin_fmaf(h.bv, gsq[k] - vo[k], vo[k]);
+      } else {
+        const float c = h.bv - 1.0f;
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) vn[k] = __builtin_fmaf(c, gsq[k] - vo[k], gsq[k]);
+      }
     }
 
     // ---- M decode
@@ -340,37 +348,64 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       }
     }
 
+    // ---- inverse second-moment denominators (uniform choice, hoisted)
+    const bool mom = kHasM && h.momentum_only;
+    float inv[kEPT];
+    if (mom) {
+      // feeds the momentum codes: IEEE sqrt then division, as torch's
+      // variance.clamp(min=eps_sq).rsqrt() on the CPU (optimizer.py:893)
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) inv[k] = 1.0f / sqrtf(fmaxf(vn[k], h.eps_sq));
+    } else if (h.adam_denom) {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) inv[k] = fast_rcp(fast_sqrt(vn[k]) + h.eps_d);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) inv[k] = __builtin_amdgcn_rsqf(fmaxf(vn[k], h.eps_sq));
+    }
+
     // ---- M EMA and update direction
     float uu[kEPT];
-    const bool exact_inv = !h.adam_denom && h.momentum_only && kHasM;
+    if constexpr (kHasM) {
+      float x[kEPT];
+      if (mom) {
 #pragma unroll
-    for (int k = 0; k < kEPT; ++k) {
-      float inv;
-      if (h.adam_denom) {
-        inv = fast_rcp(fast_sqrt(vn[k]) + h.eps_d);
-      } else if (exact_inv) {
-        // feeds the momentum codes: IEEE sqrt then division, as torch's rsqrt on the CPU
-        // (optimizer.py:893)
-        inv = 1.0f / sqrtf(fmaxf(vn[k], h.eps_sq));
-      } else {
-        inv = __builtin_amdgcn_rsqf(fmaxf(vn[k], h.eps_sq));
-      }
-      if constexpr (kHasM) {
-        float x = g[k];
-        if (h.momentum_only) {
-          const float ut = g[k] * inv;
+        for (int k = 0; k < kEPT; ++k) {
+          const float ut = g[k] * inv[k];
           if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(ut, ut, sq);
-          x = (ut_clip != 1.0f) ? ut / ut_clip : ut;
-          mn[k] = lerp_ref(mo[k], x, h.w_m);
-          uu[k] = mn[k];
-        } else {
-          mn[k] = lerp_ref(mo[k], x, h.w_m);
-          uu[k] = mn[k] * inv;
-          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
+          x[k] = ut;
+        }
+        if (ut_clip != 1.0f) {
+#pragma unroll
+          for (int k = 0; k < kEPT; ++k) x[k] = x[k] / ut_clip;
         }
       } else {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) x[k] = g[k];
+      }
+      if (fabsf(h.w_m) < 0.5f) {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) mn[k] = __builtin_fmaf(h.w_m, x[k] - mo[k], mo[k]);
+      } else {
+        const float c = h.w_m - 1.0f;
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) mn[k] = __builtin_fmaf(c, x[k] - mo[k], x[k]);
+      }
+      if (mom) {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) uu[k] = mn[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) {
+          uu[k] = mn[k] * inv[k];
+          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) {
         mn[k] = 0.0f;
-        uu[k] = g[k] * inv;
+        uu[k] = g[k] * inv[k];
         if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
       }
     }
@@ -379,7 +414,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
       for (int k = 0; k < kEPT; ++k) {
         if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; uu[k] = 0.0f; }
-        const float ut = (kHasM && h.momentum_only) ? g[k] * (1.0f / sqrtf(fmaxf(vn[k], h.eps_sq))) : uu[k];
+        const float ut = mom ? g[k] * inv[k] : uu[k];
         if ((MODE == 1 || MODE == 3) && k < cnt) sq = __builtin_fmaf(ut, ut, sq);
       }
     }
@@ -390,9 +425,9 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     }
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) {
-      vmax = fmaxf(vmax, vn[k]);
+      vmaxb = max(vmaxb, __float_as_uint(vn[k]));
       vkey = min(vkey, nz_key(vn[k]));
-      amax = fmaxf(amax, fabsf(mn[k]));
+      amaxb = max(amaxb, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
     }
 
     // ---- parameter write
@@ -404,8 +439,11 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
           if (k < cnt) {
-            const float pv = to_f<T>(P[e0 + k]);
-            P[e0 + k] = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
+            const float pv = ld1<T>(P, e0 + k);
+            const T r = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
+            uint16_t bits;
+            __builtin_memcpy(&bits, &r, 2);
+            gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = bits;
           }
         }
       } else {
@@ -424,6 +462,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) { vn[k] = 0.0f; mn[k] = 0.0f; }
   }
+  const float vmax = __uint_as_float(vmaxb);
+  const float amax = __uint_as_float(amaxb);
 
   const int wave = lane >> 6;
 
@@ -431,29 +471,48 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   if constexpr (MODE != 2) {
     float bmax = grp_max(vmax, VL < 64 ? VL : 64);
     uint32_t bkey = grp_umin(vkey, VL < 64 ? VL : 64);
+    const float lm2 = VB == 8 ? 254.0f : 65534.0f;
+    ALFit f;
     if (VL > 64) {
+      // a V block spans VL/64 waves: wave 0 refits every block of the workgroup
+      // (lane pair 2j, 2j+1 for block j) and shares the fit through LDS, so
+      // the other waves do not repeat the correctly rounded logarithms.
       if ((lane & 63) == 0) { xw[wave * 4 + 0] = bmax; xw[wave * 4 + 1] = __uint_as_float(bkey); }
       __syncthreads();
-      const int w0 = (lane >> (lbv - 3)) * (VL >> 6);
-      bmax = xw[w0 * 4];
-      bkey = __float_as_uint(xw[w0 * 4 + 1]);
-      for (int w = 1; w < (VL >> 6); ++w) {
-        bmax = fmaxf(bmax, xw[(w0 + w) * 4]);
-        bkey = min(bkey, __float_as_uint(xw[(w0 + w) * 4 + 1]));
+      if (wave == 0) {
+        const int j = (lane >> 1) < nv_wg ? (lane >> 1) : 0;
+        const int wpb = VL >> 6;   // waves per block
+        float mx = xw[(j * wpb) * 4];
+        uint32_t ky = __float_as_uint(xw[(j * wpb) * 4 + 1]);
+        for (int w = 1; w < wpb; ++w) {
+          mx = fmaxf(mx, xw[(j * wpb + w) * 4]);
+          ky = min(ky, __float_as_uint(xw[(j * wpb + w) * 4 + 1]));
+        }
+        const float mn_ = (ky == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(ky + 1u);
+        const ALFit g = al_refit_pair(mx, mn_, h.floor_, lm2, lane);
+        if ((lane & 1) == 0 && (lane >> 1) < nv_wg) {
+          float* xf = xw + 16 + (lane >> 1) * 4;
+          xf[0] = g.lmin; xf[1] = g.s; xf[2] = g.k; xf[3] = g.kmar;
+        }
       }
-    }
-    if (v_ok) {
+      __syncthreads();
+      const float* xf = xw + 16 + vloc * 4;
+      f.lmin = xf[0]; f.s = xf[1]; f.k = xf[2]; f.kmar = xf[3];
+    } else {
       const float bmin = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
-      const ALFit f = al_refit(bmax, bmin, h.floor_, VB == 8 ? 254.0f : 65534.0f);
+      f = al_refit_pair(bmax, bmin, h.floor_, lm2, lane);
+    }
+    {
+      if (v_ok) {
       uint32_t q[kEPT];
       if constexpr (VB == 8) {
         float r[kEPT];
         uint32_t need = 0;
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
-          bool ok;
-          r[k] = al8_round_fast(vn[k], f, ok);
-          need |= ok ? 0u : (1u << k);
+          uint32_t bad;
+          r[k] = al8_round_fast(vn[k], f, bad);
+          need |= bad << k;
         }
         if (need) {
 #pragma unroll
@@ -472,6 +531,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
             u32x4{q[0] | (q[1] << 16), q[2] | (q[3] << 16), q[4] | (q[5] << 16), q[6] | (q[7] << 16)};
       }
       if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }
+      }
     }
   }
 
@@ -495,9 +555,9 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
         uint32_t need = 0;
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
-          bool ok;
-          r[k] = uf_round_fast<128>(mn[k], kam, ok);
-          need |= ok ? 0u : (1u << k);
+          uint32_t bad;
+          r[k] = uf_round_fast<128>(mn[k], kam, bad);
+          need |= bad << k;
         }
         if (need) {
 #pragma unroll
@@ -548,7 +608,7 @@ template <typename T, int VB, int MODE, bool SR, int MK>
 static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
                     hipStream_t st) {
   const int nv_wg = kWGElems / h.block_size;
-  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 16 * sizeof(float);
+  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 32 * sizeof(float);
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
   hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,

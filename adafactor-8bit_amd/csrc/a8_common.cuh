@@ -64,8 +64,17 @@ struct ALFit {
   float lmin;     // new min_log
   float s;        // new scale
   float k;        // ~ (L-2)/s
-  float kmar;     // fast-path margin slope: k * 2^-22
+  float c1;       // 1 - lmin*k: t1 = fma(log2 v, k, c1) ~ ((log2 v - lmin)/s)*(L-2) + 1
+  float kmar;     // fast-path margin: kmar*|log2 v| + cmar
+  float cmar;
 };
+
+__device__ __forceinline__ void al_fit_consts(ALFit& f, float levels_m2) {
+  f.k = levels_m2 * fast_rcp(f.s);
+  f.c1 = 1.0f - f.lmin * f.k;
+  f.kmar = f.k * 0x1p-22f;
+  f.cmar = __builtin_fmaf(fabsf(f.lmin), f.kmar, 2e-4f);
+}
 
 // Refit from the block's max v and min non-zero v (optimizer.py:308-318):
 // l = log2(max(v, 1e-38)); lmax over all, lmin over v != 0, floored, lmin := lmax-1
@@ -80,8 +89,7 @@ __device__ __forceinline__ ALFit al_refit(float vmax, float vmin_nz, float floor
   const float s = fmaxf(lmax - lmin, 1e-12f);
   f.lmin = lmin;
   f.s = s;
-  f.k = levels_m2 * fast_rcp(s);
-  f.kmar = f.k * 0x1p-22f;
+  al_fit_consts(f, levels_m2);
   return f;
 }
 
@@ -101,69 +109,88 @@ __device__ __forceinline__ ALFit al_refit_pair(float vmax, float vmin_nz, float 
   const float s = fmaxf(lmax - lmin, 1e-12f);
   f.lmin = lmin;
   f.s = s;
-  f.k = levels_m2 * fast_rcp(s);
-  f.kmar = f.k * 0x1p-22f;
+  al_fit_consts(f, levels_m2);
   return f;
 }
 
-// Exact AL rounding argument: correctly rounded log2 and IEEE division, in the
-// reference's operation order ((log2(max(v,1e-38)) - lmin) / s) * (L-2).
+// Exact AL code argument (before clamping): rint(((log2(max(v,1e-38)) - lmin) / s)
+// * (L-2)) + 1 with a correctly rounded log2 and IEEE division, in the
+// reference's operation order (optimizer.py:310-321).
 template <int LM2>
 __device__ __forceinline__ float al_round_exact(float v, const ALFit& f) {
   const float le = log2_exact(fmaxf(v, kLogClampIn));
-  return rintf(((le - f.lmin) / f.s) * (float)LM2);
+  return rintf(((le - f.lmin) / f.s) * (float)LM2) + 1.0f;
 }
 
-// Fast AL8 rounding argument from the hardware log2 (faithful: |error| <= |l|*2^-23,
-// measured on gfx950) and k ~ 254/s.  |t_fast - t_exact| <= |l|*k*2^-23 + 1.2e-4
-// (the rounding of the difference, the reciprocal and the two products, t <= 255),
-// so the rounded value is the exact one whenever t lies farther than the margin
-// |l|*k*2^-22 + 1.5e-4 from a half-integer.  ok=false flags the rest (and
-// subnormal inputs) for al_round_exact; v == 0 needs no rounding (code 0).
-__device__ __forceinline__ float al8_round_fast(float v, const ALFit& f, uint32_t& bad) {
+// Fast AL8 code argument from the hardware log2 (faithful: |error| <= |l|*2^-23,
+// measured on gfx950): t1 = fma(lf, k, 1 - lmin*k).  Against the exact argument
+// t* + 1 the error is at most (|l| + |lmin|)*k*2^-23 (log error, rounding of
+// lmin*k and of c1) + 1.3e-4 (reciprocal, the fma, and t*'s own three roundings,
+// t <= 255), so rint(t1) is exact whenever t1 lies farther than
+// (|l| + |lmin|)*k*2^-22 + 2e-4 from a half-integer.  bad=true flags the rest
+// (and subnormal inputs) for al_round_exact; v == 0 needs no rounding (code 0).
+__device__ __forceinline__ float al8_round_fast(float v, const ALFit& f, bool& bad) {
   const float lf = __builtin_amdgcn_logf(v);
-  const float t = (lf - f.lmin) * f.k;
-  const float r = rintf(t);
-  const float e = fabsf(fabsf(t - r) - 0.5f);
-  // branch-free: bad = 1 when neither "v == 0" nor "normal and outside the margin"
-  const uint32_t good = (uint32_t)(v == 0.0f) |
-                        ((uint32_t)(v >= kFltMin) & (uint32_t)(e > __builtin_fmaf(fabsf(lf), f.kmar, 1.5e-4f)));
-  bad = good ^ 1u;
+  const float t1 = __builtin_fmaf(lf, f.k, f.c1);
+  const float r = rintf(t1);
+  const float e = fabsf(fabsf(t1 - r) - 0.5f);
+  const bool good = (v == 0.0f) | ((v >= kFltMin) & (e > __builtin_fmaf(fabsf(lf), f.kmar, f.cmar)));
+  bad = !good;
   return r;
+}
+
+// Code value from the argument: 0 for v == 0, else clamp to [1, L-1].
+template <int LM2>
+__device__ __forceinline__ float al_clamp(float v, float r1) {
+  return (v == 0.0f) ? 0.0f : __builtin_amdgcn_fmed3f(r1, 1.0f, (float)(LM2 + 1));
 }
 
 template <int LM2>
-__device__ __forceinline__ uint32_t al_finish(float v, float r) {
-  const float q = __builtin_amdgcn_fmed3f(r + 1.0f, 1.0f, (float)(LM2 + 1));
-  return (v == 0.0f) ? 0u : (uint32_t)q;
+__device__ __forceinline__ uint32_t al_finish(float v, float r1) {
+  return (uint32_t)al_clamp<LM2>(v, r1);
 }
 
-// Fast UF rounding argument: t = m * (H/absmax) with a faithful reciprocal;
-// |t_fast - t_exact| <= H*2^-22 (t = (m/absmax)*H exactly scaled by H = 2^k).
+// Fast UF code argument: t' = fma(m, H/absmax, H) ~ (m/absmax)*H + H with a
+// faithful reciprocal; against the exact argument the error is at most
+// H*3*2^-24 + ulp(2H)/2 (< 4e-5 for H = 128), margin 1e-4.
 template <int H>
-__device__ __forceinline__ float uf_round_fast(float m, float kam, uint32_t& bad) {
-  const float t = m * kam;
+__device__ __forceinline__ float uf_round_fast(float m, float kam, bool& bad) {
+  const float t = __builtin_fmaf(m, kam, (float)H);
   const float r = rintf(t);
-  bad = (uint32_t)!(fabsf(fabsf(t - r) - 0.5f) > (float)H * 0x1p-20f);
+  bad = !(fabsf(fabsf(t - r) - 0.5f) > 1e-4f);
   return r;
 }
 
+// Exact UF code argument: rint((m / absmax) * H) + H (optimizer.py:516-518).
 template <int H>
 __device__ __forceinline__ float uf_round_exact(float m, float amax) {
-  return rintf((m / amax) * (float)H);
+  return rintf((m / amax) * (float)H) + (float)H;
+}
+
+template <int H>
+__device__ __forceinline__ float uf_clamp(float r) {
+  return __builtin_amdgcn_fmed3f(r, 0.0f, (float)(2 * H - 1));
 }
 
 template <int H>
 __device__ __forceinline__ uint32_t uf_finish(float r) {
-  return (uint32_t)(__builtin_amdgcn_fmed3f(r, (float)(-H), (float)(H - 1)) + (float)H);
+  return (uint32_t)uf_clamp<H>(r);
 }
 
 template <int H>
 __device__ __forceinline__ uint32_t uf_code(float m, float amax, float ramax) {
-  uint32_t bad;
+  bool bad;
   float r = uf_round_fast<H>(m, (float)H * ramax, bad);
   if (bad) r = uf_round_exact<H>(m, amax);
   return uf_finish<H>(r);
+}
+
+// Pack four integer-valued floats in [0, 255] into one dword, byte k from x[k].
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+  uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(a, 0, 0u);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(b, 1, w);
+  w = __builtin_amdgcn_cvt_pk_u8_f32(c, 2, w);
+  return __builtin_amdgcn_cvt_pk_u8_f32(d, 3, w);
 }
 
 // ---------------------------------------------------------------- dtypes

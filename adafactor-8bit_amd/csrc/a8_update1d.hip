@@ -491,40 +491,33 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
         const float mn_ = (ky == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(ky + 1u);
         const ALFit g = al_refit_pair(mx, mn_, h.floor_, lm2, lane);
         if ((lane & 1) == 0 && (lane >> 1) < nv_wg) {
-          float* xf = xw + 16 + (lane >> 1) * 4;
-          xf[0] = g.lmin; xf[1] = g.s; xf[2] = g.k; xf[3] = g.kmar;
+          float* xf = xw + 16 + (lane >> 1) * 8;
+          xf[0] = g.lmin; xf[1] = g.s; xf[2] = g.k; xf[3] = g.c1; xf[4] = g.kmar; xf[5] = g.cmar;
         }
       }
       __syncthreads();
-      const float* xf = xw + 16 + vloc * 4;
-      f.lmin = xf[0]; f.s = xf[1]; f.k = xf[2]; f.kmar = xf[3];
+      const float* xf = xw + 16 + vloc * 8;
+      f.lmin = xf[0]; f.s = xf[1]; f.k = xf[2]; f.c1 = xf[3]; f.kmar = xf[4]; f.cmar = xf[5];
     } else {
       const float bmin = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
       f = al_refit_pair(bmax, bmin, h.floor_, lm2, lane);
     }
     {
       if (v_ok) {
-      uint32_t q[kEPT];
       if constexpr (VB == 8) {
         float r[kEPT];
-        uint32_t need = 0;
+        bool bad[kEPT];
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          uint32_t bad;
-          r[k] = al8_round_fast(vn[k], f, bad);
-          need |= bad << k;
-        }
-        if (need) {
+        for (int k = 0; k < kEPT; ++k) r[k] = al8_round_fast(vn[k], f, bad[k]);
 #pragma unroll
-          for (int k = 0; k < kEPT; ++k)
-            if (need & (1u << k)) r[k] = al_round_exact<254>(vn[k], f);
-        }
+        for (int k = 0; k < kEPT; ++k)
+          if (bad[k]) r[k] = al_round_exact<254>(vn[k], f);
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) q[k] = al_finish<254>(vn[k], r[k]);
-        const uint32_t w0 = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        const uint32_t w1 = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
-        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) = u32x2{w0, w1};
+        for (int k = 0; k < kEPT; ++k) r[k] = al_clamp<254>(vn[k], r[k]);
+        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) =
+            u32x2{pack4(r[0], r[1], r[2], r[3]), pack4(r[4], r[5], r[6], r[7])};
       } else {
+        uint32_t q[kEPT];
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) q[k] = al_finish<65534>(vn[k], al_round_exact<65534>(vn[k], f));
         *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(D.v_q) + e0)) =
@@ -552,24 +545,16 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       if (MK == 1) {
         const float kam = 128.0f * ram;
         float r[kEPT];
-        uint32_t need = 0;
+        bool bad[kEPT];
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          uint32_t bad;
-          r[k] = uf_round_fast<128>(mn[k], kam, bad);
-          need |= bad << k;
-        }
-        if (need) {
+        for (int k = 0; k < kEPT; ++k) r[k] = uf_round_fast<128>(mn[k], kam, bad[k]);
 #pragma unroll
-          for (int k = 0; k < kEPT; ++k)
-            if (need & (1u << k)) r[k] = uf_round_exact<128>(mn[k], am);
-        }
-        uint32_t q[kEPT];
+        for (int k = 0; k < kEPT; ++k)
+          if (bad[k]) r[k] = uf_round_exact<128>(mn[k], am);
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) q[k] = uf_finish<128>(r[k]);
-        const uint32_t w0 = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        const uint32_t w1 = q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24);
-        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
+        for (int k = 0; k < kEPT; ++k) r[k] = uf_clamp<128>(r[k]);
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) =
+            u32x2{pack4(r[0], r[1], r[2], r[3]), pack4(r[4], r[5], r[6], r[7])};
       } else if (mk == 2 || mk == 4) {
         uint32_t w = 0;
 #pragma unroll
@@ -608,7 +593,7 @@ template <typename T, int VB, int MODE, bool SR, int MK>
 static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
                     hipStream_t st) {
   const int nv_wg = kWGElems / h.block_size;
-  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 32 * sizeof(float);
+  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 48 * sizeof(float);
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
   hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,

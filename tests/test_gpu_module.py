@@ -1,0 +1,89 @@
+"""The reference-named module (``adafactor8bit_cuda``) on the GPU, against the CPU oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from inputs import make_grad, make_param
+
+ADAMW = dict(beta1=0.9, beta2=0.999, beta2_decay=None, factored=False, relative_step=False,
+             scale_parameter=False, scale_weight_decay=False, d=0.0, eps=(1e-8, 1e-3), lr=1e-4)
+
+
+@pytest.mark.gpu
+def test_fira_scalar_truth_table():
+    """fira_scalar (kernels.cu:3030-3084) against the oracle's limiter (optimizer.py:760-782)."""
+    from adafactor8bit import adafactor8bit_cuda as K
+    from oracle.fallback import fira_scale
+    print("[module] fira_scalar", flush=True)
+    mu = 0.01
+    cases = [  # (squared norm, previous norm or None)
+        (4.0, None), (1.005 ** 2, 1.0), (16.0, 1.0), (25.0, 1e-7), (float("nan"), 1.0),
+        (float("inf"), 2.0), (0.0, 3.0), (9.0, 0.5),
+    ]
+    for x, prev in cases:
+        xt = torch.tensor([x], dtype=torch.float32, device="cuda")
+        alpha = torch.tensor([0.125], dtype=torch.float32, device="cuda")
+        pt = torch.tensor([prev if prev is not None else 0.0], dtype=torch.float32, device="cuda")
+        out = K.fira_scalar(xt, pt, alpha, prev is not None, True, 1.0 + mu, 1.0 / (1.0 + mu)).cpu()
+        st = {} if prev is None else {"fira_prev_norm": torch.tensor(prev, dtype=torch.float32)}
+        curr = torch.tensor(x, dtype=torch.float32).sqrt()
+        fs = fira_scale(st, curr, mu)
+        assert out[0].item() == pytest.approx(0.125 * fs.item(), rel=2e-7), (x, prev)
+        assert out[1].item() == pytest.approx(st["fira_prev_norm"].item(), rel=2e-7), (x, prev)
+        assert out[2].item() == (x if math.isfinite(x) else 0.0), (x, prev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mqt,vbits", [("uf8", 8), ("uf4", 8), ("d8", 8), ("uf8", 16)])
+def test_module_noclip_step_matches_oracle(mqt, vbits):
+    """fused_update_1d_noclip through the reference's positional signature: one AdamW step on a
+    (61, 1003) fp32 param; codes bit-exact, metadata and param within rtol 3e-7 / 1e-6."""
+    from adafactor8bit import adafactor8bit_cuda as K
+    from adafactor8bit import _state as S
+    from oracle.fallback import OracleOptimizer
+    print(f"[module] noclip {mqt} al{vbits}", flush=True)
+    shape, bs, mbs = (61, 1003), 2048, 256
+    vqt = "al8" if vbits == 8 else "al16"
+    kw = dict(ADAMW, m_quant_type=mqt, v_quant_type=vqt, block_size=bs, m_block_size=mbs)
+    pc = torch.nn.Parameter(make_param(shape, 0, 3))
+    oc = OracleOptimizer([pc], **kw)
+    g = make_grad(shape, 0, 1, 3)
+    pc.grad = g
+    pg = pc.detach().clone().cuda()
+    oc.step()
+
+    K.set_qmap(*[q.cuda() for q in K.qmaps()])
+    st = {}
+    S.init_v_state(st, "variance", shape, bs, "cuda", vqt)
+    S.m_init_state(st, pg.numel(), mbs, mqt, "cuda", shape=shape)
+    bc1, bc2 = 1.0 - 0.9, 1.0 - 0.999
+    alpha = (torch.tensor(1e-4, dtype=torch.float32) * (math.sqrt(bc2) / bc1)).reshape(1).cuda()
+    eps1 = 1e-8
+    K.fused_update_1d_noclip(
+        pg, g.cuda(), st["m_q"], st["m_scale"], st["variance_q"], st["variance_scale"],
+        st["variance_min_log"], alpha, 0.9, 1.0 - 0.999, eps1 * math.sqrt(bc2), True,
+        math.log2(max(eps1 * eps1, 1.17549435e-38)), 0.0, pg.numel(), bs, mbs, S.m_bits(mqt),
+        S.m_mode(mqt), vbits, False)
+    torch.cuda.synchronize()
+    so = oc.state[id(pc)]
+    for k in ("variance_q", "m_q"):
+        a = so[k].reshape(-1).numpy()
+        b = st[k].reshape(-1).cpu().numpy()
+        assert np.array_equal(a, b), f"{k}: {(a != b).sum()} codes differ"
+    for k in ("variance_scale", "variance_min_log", "m_scale"):
+        np.testing.assert_allclose(st[k].cpu().numpy(), so[k].reshape(-1).numpy(), rtol=3e-7, atol=0)
+    np.testing.assert_allclose(pg.cpu().numpy(), pc.detach().numpy(), rtol=1e-6, atol=0)
+
+
+@pytest.mark.gpu
+def test_module_rejects_wrong_code_dtype():
+    from adafactor8bit import adafactor8bit_cuda as K
+    print("[module] dtype check", flush=True)
+    z = torch.zeros(4096, device="cuda")
+    vq = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    one = torch.ones(2, device="cuda")
+    with pytest.raises(RuntimeError, match="v_bits=16"):
+        K.fused_update_1d_vonly_noclip(z, z, vq, one, one, one, 0.001, 1e-8, True, -53.0, 0.0,
+                                       4096, 2048, 16)

@@ -56,7 +56,7 @@ def set_qmap(qmap_8, qmap_4):
 
 def _u1d(mode, sr, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha,
          prev_norm, decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom,
-         eps_for_grad_sq, numel, block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only):
+         log_eps_sq, eps_for_grad_sq, numel, block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only):
     _vbits_check(v_q, v_bits)
     ref = grad
     if sr and (param is None or param.dtype not in (torch.bfloat16, torch.float16)
@@ -86,7 +86,7 @@ def fused_update_1d_noclip(param, grad, m_q, m_scale, v_q, v_scale, v_min_log, a
                            eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
                            block_size, m_block_size, m_bits, m_mode, v_bits, momentum_only):
     _u1d(0, False, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, None, None, alpha, None, None,
-         0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          m_block_size, m_bits, m_mode, 0.0, v_bits, momentum_only)
 
 
@@ -94,7 +94,7 @@ def fused_update_1d_norm(grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, nor
                          eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
                          m_block_size, m_bits, m_mode, v_bits, momentum_only):
     _u1d(1, False, None, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, norm_buf, None, None, None,
-         0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          m_block_size, m_bits, m_mode, 0.0, v_bits, momentum_only)
 
 
@@ -102,7 +102,7 @@ def fused_update_1d_apply(param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_
                           beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq,
                           numel, block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only):
     _u1d(2, False, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha, None,
-         None, 0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         None, 0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          m_block_size, m_bits, m_mode, d, v_bits, momentum_only)
 
 
@@ -110,7 +110,7 @@ def fused_update_1d_lag(param, grad, m_q, m_scale, v_q, v_scale, v_min_log, norm
                         beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq,
                         numel, block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only):
     _u1d(3, False, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, None, norm_buf, alpha, prev_norm,
-         None, 0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         None, 0, 0, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          m_block_size, m_bits, m_mode, d, v_bits, momentum_only)
 
 
@@ -119,7 +119,7 @@ def fused_update_1d_noclip_sr(param, grad, m_q, m_scale, v_q, v_scale, v_min_log
                               eps_for_grad_sq, numel, block_size, m_block_size, m_bits, m_mode, v_bits,
                               momentum_only):
     _u1d(0, True, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, None, None, alpha, None, decay,
-         sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, m_block_size, m_bits, m_mode, 0.0, v_bits, momentum_only)
 
 
@@ -128,7 +128,7 @@ def fused_update_1d_apply_sr(param, grad, m_q, m_scale, v_q, v_scale, v_min_log,
                              log_eps_sq, eps_for_grad_sq, numel, block_size, m_block_size, m_bits, m_mode,
                              d, v_bits, momentum_only):
     _u1d(2, True, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha, None,
-         decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only)
 
 
@@ -137,7 +137,7 @@ def fused_update_1d_lag_sr(param, grad, m_q, m_scale, v_q, v_scale, v_min_log, n
                            use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size, m_block_size,
                            m_bits, m_mode, d, v_bits, momentum_only):
     _u1d(3, True, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, None, norm_buf, alpha, prev_norm,
-         decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only)
 
 
@@ -145,14 +145,14 @@ def fused_update_1d_lag_sr(param, grad, m_q, m_scale, v_q, v_scale, v_min_log, n
 def fused_update_1d_vonly_noclip(param, grad, v_q, v_scale, v_min_log, alpha, beta_val, eps_for_denom,
                                  use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size, v_bits):
     _u1d(0, False, param, grad, None, None, v_q, v_scale, v_min_log, None, None, alpha, None, None, 0, 0,
-         0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size, block_size, 0,
+         0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size, block_size, 0,
          0, 0.0, v_bits, False)
 
 
 def fused_update_1d_vonly_norm(grad, v_q, v_scale, v_min_log, v_buf, norm_buf, beta_val, eps_for_denom,
                                use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size, v_bits):
     _u1d(1, False, None, grad, None, None, v_q, v_scale, v_min_log, v_buf, norm_buf, None, None, None, 0,
-         0, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size, block_size,
+         0, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size, block_size,
          0, 0, 0.0, v_bits, False)
 
 
@@ -160,7 +160,7 @@ def fused_update_1d_vonly_apply(param, grad, v_q, v_scale, v_min_log, v_buf, nor
                                 eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
                                 block_size, d, v_bits):
     _u1d(2, False, param, grad, None, None, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha, None, None,
-         0, 0, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         0, 0, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          block_size, 0, 0, d, v_bits, False)
 
 
@@ -168,7 +168,7 @@ def fused_update_1d_vonly_lag(param, grad, v_q, v_scale, v_min_log, norm_buf, al
                               eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
                               block_size, d, v_bits):
     _u1d(3, False, param, grad, None, None, v_q, v_scale, v_min_log, None, norm_buf, alpha, prev_norm,
-         None, 0, 0, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, block_size,
+         None, 0, 0, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel, block_size,
          block_size, 0, 0, d, v_bits, False)
 
 
@@ -176,7 +176,7 @@ def fused_update_1d_vonly_noclip_sr(param, grad, v_q, v_scale, v_min_log, alpha,
                                     beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq,
                                     numel, block_size, v_bits):
     _u1d(0, True, param, grad, None, None, v_q, v_scale, v_min_log, None, None, alpha, None, decay,
-         sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, block_size, 0, 0, 0.0, v_bits, False)
 
 
@@ -184,7 +184,7 @@ def fused_update_1d_vonly_apply_sr(param, grad, v_q, v_scale, v_min_log, v_buf, 
                                    sr_seed, sr_step, beta_val, eps_for_denom, use_adam_denom, log_eps_sq,
                                    eps_for_grad_sq, numel, block_size, d, v_bits):
     _u1d(2, True, param, grad, None, None, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha, None, decay,
-         sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, block_size, 0, 0, d, v_bits, False)
 
 
@@ -192,7 +192,7 @@ def fused_update_1d_vonly_lag_sr(param, grad, v_q, v_scale, v_min_log, norm_buf,
                                  sr_seed, sr_step, beta_val, eps_for_denom, use_adam_denom, log_eps_sq,
                                  eps_for_grad_sq, numel, block_size, d, v_bits):
     _u1d(3, True, param, grad, None, None, v_q, v_scale, v_min_log, None, norm_buf, alpha, prev_norm,
-         decay, sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+         decay, sr_seed, sr_step, 0.0, beta_val, eps_for_denom, use_adam_denom, log_eps_sq, eps_for_grad_sq, numel,
          block_size, block_size, 0, 0, d, v_bits, False)
 
 

@@ -18,7 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "adafactor8bit", "libadafactor8bit_amd.so")
-SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip"]
+SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip", "a8_factored.hip"]
 ARCH = os.environ.get("A8_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

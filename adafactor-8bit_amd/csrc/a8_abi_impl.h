@@ -31,3 +31,8 @@ inline int check_launch(const char* what) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace a8
+
+namespace a8 {
+// Codebook upload of the factored-step translation unit (called by a8_set_qmap).
+hipError_t factored_upload_qmap(const float* q8, const float* q4);
+}  // namespace a8

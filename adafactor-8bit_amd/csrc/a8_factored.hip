@@ -1,0 +1,740 @@
+// Factored (Adafactor row/column) optimizer step for MI355X (gfx950).
+//
+// One group step is three or five launches over every tensor of the group:
+//   k_fstats   2-D tiles of 32 rows x 1024 columns: row sums and column sums of
+//              g^2 (and sum p^2 for the relative step size), written as
+//              per-tile partials -- no atomics, so the result is deterministic;
+//   k_ffinish  one workgroup per (tensor, row|column): reduce the partials in a
+//              fixed order, EMA the row/column second moment, refit and
+//              re-encode its AL blocks, and produce inv_row / inv_col and the
+//              tensor's step size and weight-decay factor;
+//   k_fupdate  flat 2048-element units (8 per lane, as the 1-D step): the
+//              update u = (x * inv_row) * inv_col with x = g or the momentum
+//              EMA, the parameter write and the momentum re-encode.  With RMS
+//              clipping or Fira it runs twice: first for sum(u^2) per unit,
+//              then (after k_fnorm) to apply;
+//   k_fnorm    one workgroup per tensor: ||u||, the Fira limiter and the step.
+// Numbers follow the reference's PyTorch path (optimizer.py:2198-2252 and
+// _fallback_2d_update 920-970): means are sum/count of the fp32 squares,
+// inv_row = 1/sqrt(row/r) and inv_col = 1/sqrt(col) with IEEE division and
+// square root, and u is formed as (x * inv_row) * inv_col.
+#include "a8_common.cuh"
+#include "a8_mcodec.cuh"
+#include "a8_abi_impl.h"
+
+namespace a8 {
+
+constexpr int kTR = 32;      // rows per statistics tile
+constexpr int kTC = 1024;    // columns per statistics tile (256 lanes x 4)
+constexpr int kUnit = 2048;  // elements per update workgroup
+constexpr int kScal = 8;     // per-tensor scalars in the workspace
+
+// Per-tensor workspace layout (floats).
+struct FWs {
+  int64_t rowpart;   // [nchunk][B*R]      row partial sums
+  int64_t colpart;   // [B][nstrip][C]     column partial sums
+  int64_t p2;        // [ntile]            partial sum p^2
+  int64_t invr;      // [B*R]              new row V, then inv_row
+  int64_t invc;      // [B*C]              new column V, then inv_col
+  int64_t npart;     // [nunit]            partial sum u^2
+  int64_t scal;      // [8]: alpha, step, fira scale, decay
+  int64_t total;
+  int64_t nchunk, nstrip, ntile, nunit;
+};
+
+__host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
+  FWs w;
+  w.nchunk = (C + kTC - 1) / kTC;
+  w.nstrip = (R + kTR - 1) / kTR;
+  w.ntile = B * w.nstrip * w.nchunk;
+  w.nunit = (B * R * C + kUnit - 1) / kUnit;
+  w.rowpart = 0;
+  w.colpart = w.rowpart + w.nchunk * B * R;
+  w.p2 = w.colpart + B * w.nstrip * C;
+  w.invr = w.p2 + w.ntile;
+  w.invc = w.invr + B * R;
+  w.npart = w.invc + B * C;
+  w.scal = w.npart + w.nunit;
+  w.total = w.scal + kScal;
+  return w;
+}
+
+struct DescF {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  void* row_q;
+  float* row_scale;
+  float* row_min_log;
+  float* row_var;
+  void* col_q;
+  float* col_scale;
+  float* col_min_log;
+  float* col_var;
+  float* ws;
+  const float* lr;
+  float* fira_prev;
+  int64_t B, R, C, numel;
+  int64_t tile_begin;
+  int64_t unit_begin;
+  uint64_t sr_seed;
+  int has_fira_prev;
+  int vec4;            // rows start 16-byte aligned for fp32 (8-byte for 16-bit types)
+};
+
+struct HyperF {
+  float bv;            // V lerp weight
+  float eps1;
+  float eps2;
+  float lr_val;
+  float bias_factor;
+  float wd;
+  float d;
+  float margin;        // 1 + fira_margin
+  float floor_;
+  float w_m;           // momentum lerp weight (1 - beta1)
+  int bias_mode;
+  int scale_param;
+  int wd_mode;
+  int fira;
+  int block_size;      // V block size
+  int mk;              // momentum codec (0 none, 1 UF8, 2 UF4, 3 D8, 4 D4)
+  int lbm;             // log2(m_block_size)
+  uint64_t sr_step;
+};
+
+__device__ __forceinline__ const DescF* find_tile(const DescF* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].tile_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+__device__ __forceinline__ const DescF* find_unit(const DescF* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].unit_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+// Workgroup-wide reductions (256 lanes, 4 waves) through 4 LDS slots; every
+// lane gets the result.  The cross-wave order is fixed.
+__device__ __forceinline__ double wg_sum_d(double x, double* s4) {
+  x = grp_sum_d(x, 64);
+  const int lane = threadIdx.x;
+  __syncthreads();
+  if ((lane & 63) == 0) s4[lane >> 6] = x;
+  __syncthreads();
+  return ((s4[0] + s4[1]) + s4[2]) + s4[3];
+}
+
+__device__ __forceinline__ float wg_sum_f(float x, float* s4) {
+  x = grp_sum(x, 64);
+  const int lane = threadIdx.x;
+  __syncthreads();
+  if ((lane & 63) == 0) s4[lane >> 6] = x;
+  __syncthreads();
+  return ((s4[0] + s4[1]) + s4[2]) + s4[3];
+}
+
+__device__ __forceinline__ uint32_t nz_key_f(float v) { return __float_as_uint(v) - 1u; }
+
+__device__ __forceinline__ void wg_maxkey(float& mx, uint32_t& key, float* s8) {
+  mx = grp_max(mx, 64);
+  for (int o = 1; o < 64; o <<= 1) key = min(key, (uint32_t)__shfl_xor((int)key, o, 64));
+  const int lane = threadIdx.x;
+  __syncthreads();
+  if ((lane & 63) == 0) {
+    s8[lane >> 6] = mx;
+    s8[4 + (lane >> 6)] = __uint_as_float(key);
+  }
+  __syncthreads();
+  mx = fmaxf(fmaxf(s8[0], s8[1]), fmaxf(s8[2], s8[3]));
+  key = min(min(__float_as_uint(s8[4]), __float_as_uint(s8[5])),
+            min(__float_as_uint(s8[6]), __float_as_uint(s8[7])));
+}
+
+// Four consecutive row elements starting at column c0 (zero beyond C).
+template <typename T>
+__device__ __forceinline__ void load4(const T* base, int64_t rowbase, int64_t c0, int64_t C, bool vec,
+                                      float* out) {
+  if (vec && c0 + 4 <= C) {
+    if constexpr (sizeof(T) == 4) {
+      const f32x4 a = *gp(reinterpret_cast<const f32x4*>(base + rowbase + c0));
+      out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    } else {
+      const u32x2 a = *gp(reinterpret_cast<const u32x2*>(base + rowbase + c0));
+      const T* h = reinterpret_cast<const T*>(&a);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[k] = to_f<T>(h[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = (c0 + k < C) ? ld1<T>(base, rowbase + c0 + k) : 0.0f;
+  }
+}
+
+// ------------------------------------------------------------ statistics
+template <typename T, bool PSQ>
+__global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table, int ntab) {
+  __shared__ float s_col[4 * kTC];
+  __shared__ float s4[4];
+  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
+  const int64_t R = D.R, C = D.C;
+  const int64_t ch = t % W.nchunk;
+  const int64_t bs = t / W.nchunk;
+  const int64_t s = bs % W.nstrip;
+  const int64_t b = bs / W.nstrip;
+  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
+  const int64_t r_lo = s * kTR;
+  const int64_t r_hi = (r_lo + kTR < R) ? r_lo + kTR : R;
+  const int64_t c_base = ch * kTC;
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  const T* P = reinterpret_cast<const T*>(D.param);
+  float* ws = D.ws;
+  const bool vec = D.vec4 != 0;
+  float acc[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+  float psq = 0.0f;
+  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
+    const int64_t rowbase = (b * R + r) * C;
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c0 = c_base + 4 * wl + 256 * j;
+      float g4[4];
+      load4<T>(G, rowbase, c0, C, vec, g4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gg = scrub(g4[e]);
+        const float sq = gg * gg;
+        rs += sq;
+        acc[j * 4 + e] += sq;
+      }
+      if constexpr (PSQ) {
+        float p4[4];
+        load4<T>(P, rowbase, c0, C, vec, p4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) psq = __builtin_fmaf(p4[e], p4[e], psq);
+      }
+    }
+    rs = grp_sum(rs, 64);
+    if (wl == 0) gp(ws)[W.rowpart + ch * (D.B * R) + b * R + r] = rs;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_col[wave * kTC + 4 * wl + 256 * j + e] = acc[j * 4 + e];
+  __syncthreads();
+  for (int q = lane; q < kTC; q += 256) {
+    const int64_t c = c_base + q;
+    if (c < C) {
+      const float v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
+      gp(ws)[W.colpart + (b * W.nstrip + s) * C + c] = v;
+    }
+  }
+  if constexpr (PSQ) {
+    const float tot = wg_sum_f(psq, s4);
+    if (lane == 0) gp(ws)[W.p2 + t] = tot;
+  }
+}
+
+// ------------------------------------------------------------ row/column V EMA
+template <int VB>
+__device__ __forceinline__ float fv_decode(const void* q, const float* sc, const float* ml, int64_t i,
+                                           int64_t bsz) {
+  if constexpr (VB == 8) {
+    const uint32_t c = gp(reinterpret_cast<const uint8_t*>(q))[i];
+    if (!c) return 0.0f;
+    const int64_t bi = i / bsz;
+    return exp2_exact(((float)(c - 1) * gp(sc)[bi]) / 254.0f + gp(ml)[bi]);
+  } else {
+    const uint32_t c = gp(reinterpret_cast<const uint16_t*>(q))[i];
+    if (!c) return 0.0f;
+    const int64_t bi = i / bsz;
+    return exp2_exact(((float)(c - 1) * gp(sc)[bi]) / 65534.0f + gp(ml)[bi]);
+  }
+}
+
+// grid (ntab, 2): y = 0 row state (+ per-tensor scalars), y = 1 column state.
+template <int VB>
+__global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table, HyperF h) {
+  __shared__ double sd[4];
+  __shared__ float sf[8];
+  const DescF D = table[blockIdx.x];
+  const bool is_row = blockIdx.y == 0;
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int lane = threadIdx.x;
+  const int64_t B = D.B, R = D.R, C = D.C;
+  const int64_t n = is_row ? B * R : B * C;
+  float* ws = D.ws;
+  float* vec = ws + (is_row ? W.invr : W.invc);
+  void* q = is_row ? D.row_q : D.col_q;
+  float* sc = is_row ? D.row_scale : D.col_scale;
+  float* ml = is_row ? D.row_min_log : D.col_min_log;
+  float* fst = is_row ? D.row_var : D.col_var;
+  const float cnt = is_row ? (float)C : (float)R;
+  const int64_t bsz = h.block_size;
+
+  // 1. means of g^2 (sum / count + eps1), EMA with the decoded state
+  for (int64_t i = lane; i < n; i += 256) {
+    double sum = 0.0;
+    if (is_row) {
+      for (int64_t k = 0; k < W.nchunk; ++k) sum += (double)gp(ws)[W.rowpart + k * n + i];
+    } else {
+      const int64_t b = i / C, c = i - b * C;
+      for (int64_t k = 0; k < W.nstrip; ++k) sum += (double)gp(ws)[W.colpart + (b * W.nstrip + k) * C + c];
+    }
+    const float mean = (float)sum / cnt + h.eps1;
+    float old;
+    if constexpr (VB == 0) old = gp(fst)[i];
+    else old = fv_decode<VB>(q, sc, ml, i, bsz);
+    const float nv = lerp_ref(old, mean, h.bv);
+    gp(vec)[i] = nv;
+    if constexpr (VB == 0) gp(fst)[i] = nv;
+  }
+  __syncthreads();
+
+  // 2. refit and re-encode every AL block of the flattened vector (zero padding -> code 0)
+  if constexpr (VB != 0) {
+    constexpr int LM2 = VB == 8 ? 254 : 65534;
+    const int64_t nb = (n + bsz - 1) / bsz;
+    for (int64_t bi = 0; bi < nb; ++bi) {
+      float mx = 0.0f;
+      uint32_t key = 0xFFFFFFFFu;
+      for (int64_t k = lane; k < bsz; k += 256) {
+        const int64_t i = bi * bsz + k;
+        const float v = i < n ? gp(vec)[i] : 0.0f;
+        mx = fmaxf(mx, v);
+        key = min(key, nz_key_f(v));
+      }
+      wg_maxkey(mx, key, sf);
+      const float mnz = (key == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(key + 1u);
+      const ALFit f = al_refit(mx, mnz, h.floor_, (float)LM2);
+      for (int64_t k = lane; k < bsz; k += 256) {
+        const int64_t i = bi * bsz + k;
+        const float v = i < n ? gp(vec)[i] : 0.0f;
+        const uint32_t code = al_finish<LM2>(v, al_round_exact<LM2>(v, f));
+        if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[i] = (uint8_t)code;
+        else gp(reinterpret_cast<uint16_t*>(q))[i] = (uint16_t)code;
+      }
+      if (lane == 0) { gp(sc)[bi] = f.s; gp(ml)[bi] = f.lmin; }
+    }
+  }
+  __syncthreads();
+
+  // 3. inverse square roots (optimizer.py:818-821)
+  if (is_row) {
+    for (int64_t b = 0; b < B; ++b) {
+      double s = 0.0;
+      for (int64_t r = lane; r < R; r += 256) s += (double)gp(vec)[b * R + r];
+      s = wg_sum_d(s, sd);
+      const float rmv = fmaxf((float)s / (float)R, h.eps1);
+      for (int64_t r = lane; r < R; r += 256) {
+        const int64_t i = b * R + r;
+        gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i] / rmv);
+      }
+    }
+  } else {
+    for (int64_t i = lane; i < n; i += 256) gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i]);
+  }
+
+  // 4. step size and weight decay (optimizer.py:832-856, 2020-2039)
+  if (is_row) {
+    const float rho = D.lr ? *gp(D.lr) : h.lr_val;
+    float alpha = rho;
+    if (h.scale_param) {
+      double s = 0.0;
+      for (int64_t k = lane; k < W.ntile; k += 256) s += (double)gp(ws)[W.p2 + k];
+      s = wg_sum_d(s, sd);
+      const float nrm = sqrtf((float)s);
+      const float rms = nrm / (float)sqrt((double)D.numel);
+      alpha = fmaxf(rms, h.eps2) * rho;
+    }
+    if (h.bias_mode == 1) alpha = alpha * h.bias_factor;
+    else if (h.bias_mode == 2) alpha = alpha / h.bias_factor;
+    if (lane == 0) {
+      float* sl = ws + W.scal;
+      gp(sl)[0] = alpha;
+      gp(sl)[1] = alpha;
+      gp(sl)[2] = 1.0f;
+      float dec = 1.0f;
+      if (h.wd_mode == 1) dec = 1.0f - alpha * h.wd;
+      else if (h.wd_mode == 2) dec = 1.0f - rho * h.wd;
+      gp(sl)[3] = dec;
+    }
+  }
+}
+
+// ------------------------------------------------------------ update
+// MODE 0: write with step = alpha; 1: sum(u^2) per unit; 2: write with the
+// step and Fira scale of k_fnorm.  MK: 0 no momentum, 1 UF8, 2 other codecs.
+template <typename T, int MODE, bool SR, int MK>
+__global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table, int ntab, HyperF h) {
+  __shared__ float s4[8];
+  constexpr bool kHasM = MK != 0;
+  const DescF D = *find_unit(table, ntab, (int64_t)blockIdx.x);
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int64_t wl = (int64_t)blockIdx.x - D.unit_begin;
+  const int lane = threadIdx.x;
+  const int64_t n = D.numel;
+  const int64_t e0 = wl * kUnit + (int64_t)lane * 8;
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
+  const int64_t R = D.R, C = D.C;
+  const float* ws = D.ws;
+  const float* invr = ws + W.invr;
+  const float* invc = ws + W.invc;
+  const float* sl = ws + W.scal;
+  const int lbm = h.lbm;
+  const int BM = 1 << lbm;
+  const int ML = BM >> 3;
+  const int64_t mb = e0 >> lbm;
+  const int mk = (MK == 1) ? 1 : h.mk;
+
+  float g[8], mn[8], u[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) { g[k] = 0.0f; mn[k] = 0.0f; u[k] = 0.0f; }
+  float sq = 0.0f;
+  uint32_t amaxb = 0u;
+  if (cnt > 0) {
+    load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = scrub(g[k]);
+    float x[8];
+    if constexpr (kHasM) {
+      float mo[8];
+      const float ms = gp(D.m_scale)[mb];
+      if (MK == 1) {
+        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+        const float s128 = ms / 128.0f, b128 = -128.0f * s128;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          mo[k] = __builtin_fmaf((float)(((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu), s128, b128);
+      } else if (mk == 2 || mk == 4) {
+        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
+          mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+        }
+      } else {
+        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mn[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = mn[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = g[k];
+    }
+    // element (row, column): row = e / C, column index b*C + c with b = row / R
+    int64_t row = e0 / C;
+    int64_t c = e0 - row * C;
+    int64_t b = row / R;
+    int64_t rr = row - b * R;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < cnt) {
+        u[k] = (x[k] * gp(invr)[row]) * gp(invc)[b * C + c];
+        if (MODE == 1) sq = __builtin_fmaf(u[k], u[k], sq);
+      }
+      if (++c == C) {
+        c = 0;
+        ++row;
+        if (++rr == R) { rr = 0; ++b; }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) amaxb = max(amaxb, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
+
+    if constexpr (MODE != 1) {
+      const float step = (MODE == 0) ? gp(sl)[0] : gp(sl)[1];
+      const float fs = (MODE == 2) ? gp(sl)[2] : 1.0f;
+      const float dec = gp(sl)[3];
+      const bool has_dec = h.wd_mode != 0;
+      if (MODE == 2) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) u[k] = u[k] * fs;
+      }
+      T* P = reinterpret_cast<T*>(D.param);
+      if constexpr (SR) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (k < cnt) {
+            const float pv = ld1<T>(P, e0 + k);
+            const T r = sr_round<T>((has_dec ? pv * dec : pv) - step * u[k], D.sr_seed, h.sr_step,
+                                    (uint64_t)(e0 + k));
+            uint16_t bits;
+            __builtin_memcpy(&bits, &r, 2);
+            gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = bits;
+          }
+        }
+      } else {
+        float p[8];
+        load8<T>(P, e0, n, p);
+        if (has_dec) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) p[k] = p[k] * dec;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) p[k] = __builtin_fmaf(-step, u[k], p[k]);
+        store8<T>(P, e0, n, p);
+      }
+    }
+  }
+
+  if constexpr (MODE == 1) {
+    const float tot = wg_sum_f(sq, s4);
+    if (lane == 0) gp(const_cast<float*>(ws))[W.npart + wl] = tot;
+  }
+
+  // momentum re-encode: absmax over B_M elements = ML lanes
+  if constexpr (MODE != 1 && kHasM) {
+    const int wave = lane >> 6;
+    float bam = grp_max(__uint_as_float(amaxb), ML < 64 ? ML : 64);
+    if (ML > 64) {
+      __syncthreads();
+      if ((lane & 63) == 0) s4[wave] = bam;
+      __syncthreads();
+      const int w0 = (lane >> (lbm - 3)) * (ML >> 6);
+      bam = s4[w0];
+      for (int w = 1; w < (ML >> 6); ++w) bam = fmaxf(bam, s4[w0 + w]);
+    }
+    if (cnt > 0) {
+      const float am = fmaxf(bam, 1e-12f);
+      const float ram = fast_rcp(am);
+      if (MK == 1) {
+        const float kam = 128.0f * ram;
+        float r[8];
+        bool bad[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = uf_round_fast<128>(mn[k], kam, bad[k]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (bad[k]) r[k] = uf_round_exact<128>(mn[k], am);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = uf_clamp<128>(r[k]);
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{pack4(r[0], r[1], r[2], r[3]), pack4(r[4], r[5], r[6], r[7])};
+      } else if (mk == 2 || mk == 4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t hi = m_encode(mk, mn[2 * j], am, ram);
+          const uint32_t lo = m_encode(mk, mn[2 * j + 1], am, ram);
+          w |= ((hi << 4) | lo) << (8 * j);
+        }
+        *gp(reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1))) = w;
+      } else {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w0 |= m_encode(mk, mn[k], am, ram) << (8 * k);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w1 |= m_encode(mk, mn[k + 4], am, ram) << (8 * k);
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
+      }
+      if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
+    }
+  }
+}
+
+// ------------------------------------------------------------ norm, Fira, step
+// _apply_update_pytorch with Fira (optimizer.py:796-810, 859-875).
+__global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, HyperF h) {
+  __shared__ double sd[4];
+  const DescF D = table[blockIdx.x];
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  float* ws = D.ws;
+  double s = 0.0;
+  for (int64_t k = threadIdx.x; k < W.nunit; k += 256) s += (double)gp(ws)[W.npart + k];
+  s = wg_sum_d(s, sd);
+  if (threadIdx.x == 0) {
+    float* sl = ws + W.scal;
+    float nrm = sqrtf((float)s);
+    float fs = 1.0f;
+    if (h.fira) {
+      const bool fin = __builtin_isfinite(nrm);
+      if (!fin) nrm = 0.0f;            // u.zero_(); norm.zero_()
+      float next = nrm;
+      if (D.has_fira_prev) {
+        const float p = *gp(D.fira_prev);
+        const float ratio = nrm / (p + 1e-8f);
+        const float lim = (ratio != ratio ? ratio : fmaxf(ratio, h.margin)) / h.margin;
+        const bool reset = p < 1e-6f;
+        fs = reset ? 1.0f : 1.0f / lim;
+        next = reset ? nrm : nrm * fs;
+      }
+      *gp(D.fira_prev) = next;
+      if (!fin) fs = 0.0f;
+    }
+    float denom = 1.0f;
+    if (h.d > 0.0f) denom = fmaxf(nrm / (float)(sqrt((double)D.numel) * (double)h.d), 1.0f);
+    const float alpha = gp(sl)[0];
+    gp(sl)[1] = alpha / denom;
+    gp(sl)[2] = fs;
+  }
+}
+
+hipError_t factored_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
+
+// ------------------------------------------------------------ launch glue
+template <typename T>
+static int launch_stats(bool psq, const DescF* tab, int ntab, int64_t ntiles, hipStream_t st) {
+  if (psq) hipLaunchKernelGGL((k_fstats<T, true>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab);
+  else hipLaunchKernelGGL((k_fstats<T, false>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab);
+  return check_launch("k_fstats");
+}
+
+template <typename T, int MODE, bool SR>
+static int launch_update_m(int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h, hipStream_t st) {
+  switch (mk) {
+    case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
+    case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
+    default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
+  }
+  return check_launch("k_fupdate");
+}
+
+template <typename T, bool SR>
+static int launch_update(int mode, int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h,
+                         hipStream_t st) {
+  switch (mode) {
+    case 0: return launch_update_m<T, 0, SR>(mk, tab, ntab, nunits, h, st);
+    case 1: return launch_update_m<T, 1, false>(mk, tab, ntab, nunits, h, st);
+    default: return launch_update_m<T, 2, SR>(mk, tab, ntab, nunits, h, st);
+  }
+}
+
+template <typename T, bool SR>
+static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int vbits, bool clip,
+                     const HyperF& h, hipStream_t st) {
+  int rc = launch_stats<T>(h.scale_param != 0, tab, ntab, ntiles, st);
+  if (rc) return rc;
+  switch (vbits) {
+    case 8: hipLaunchKernelGGL((k_ffinish<8>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
+    case 16: hipLaunchKernelGGL((k_ffinish<16>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
+    default: hipLaunchKernelGGL((k_ffinish<0>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
+  }
+  if ((rc = check_launch("k_ffinish"))) return rc;
+  if (!clip) return launch_update<T, SR>(0, h.mk, tab, ntab, nunits, h, st);
+  if ((rc = launch_update<T, false>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
+  hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
+  if ((rc = check_launch("k_fnorm"))) return rc;
+  return launch_update<T, SR>(2, h.mk, tab, ntab, nunits, h, st);
+}
+
+static int mk_code(int mbits, int mmode) {
+  if (mmode == 0) return mbits == 8 ? 1 : 2;
+  return mbits == 8 ? 3 : 4;
+}
+
+}  // namespace a8
+
+using namespace a8;
+
+extern "C" {
+
+int64_t a8_factored_workspace_floats(int64_t batch, int64_t rows, int64_t cols) {
+  if (batch <= 0 || rows <= 0 || cols <= 0) return 0;
+  return fws_layout(batch, rows, cols).total;
+}
+
+int64_t a8_table_bytes_2d(int ntensors) { return (int64_t)sizeof(DescF) * (int64_t)ntensors; }
+
+int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int ntensors,
+                     void* table_dev, int64_t table_bytes, int upload, double beta_val, float eps1,
+                     float eps2, float lr_val, int scale_parameter, int bias_mode, float bias_factor,
+                     float weight_decay, int wd_mode, float d, int fira, float fira_margin,
+                     float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
+                     int m_bits, int m_mode, uint64_t sr_step, void* stream) {
+  if (ntensors <= 0) return 0;
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
+  if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
+  if (block_size <= 0) return set_error(A8_ERR_BLOCK, "block_size must be positive");
+  if ((int64_t)sizeof(DescF) * ntensors > table_bytes)
+    return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_2d(ntensors)");
+  const bool has_m = tensors[0].m_q != nullptr;
+  int lbm = 0;
+  if (has_m) {
+    if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
+      return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
+    if (m_block_size < 32 || m_block_size > kUnit || (m_block_size & (m_block_size - 1)))
+      return set_error(A8_ERR_BLOCK, "m_block_size must be a power of two in [32, 2048]");
+    while ((1 << lbm) < m_block_size) ++lbm;
+  } else {
+    lbm = 5;
+  }
+  if (stochastic && dtype == A8_F32) stochastic = 0;
+  std::vector<DescF> tab((size_t)ntensors);
+  int64_t tiles = 0, units = 0;
+  const size_t esz = dtype == A8_F32 ? 4 : 2;
+  for (int i = 0; i < ntensors; ++i) {
+    const a8_tensor2d& t = tensors[i];
+    if (t.batch <= 0 || t.rows <= 0 || t.cols <= 0) return set_error(A8_ERR_SIZE, "empty factored tensor");
+    if (!t.param || !t.grad || !t.workspace) return set_error(A8_ERR_ARG, "null param/grad/workspace");
+    if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if (v_bits ? !(t.row_q && t.col_q && t.row_scale && t.col_scale && t.row_min_log && t.col_min_log)
+               : !(t.row_var && t.col_var))
+      return set_error(A8_ERR_ARG, "row/column state missing");
+    if (fira && !t.fira_prev_norm) return set_error(A8_ERR_ARG, "fira needs fira_prev_norm");
+    if (!aligned16(t.param) || !aligned16(t.grad) || (has_m && !aligned16(t.m_q)))
+      return set_error(A8_ERR_ALIGN, "param/grad/momentum buffers must be 16-byte aligned");
+    const int64_t numel = t.batch * t.rows * t.cols;
+    if (numel >= ((int64_t)1 << 40)) return set_error(A8_ERR_SIZE, "tensor too large");
+    DescF& D = tab[(size_t)i];
+    D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
+    D.row_q = t.row_q; D.row_scale = t.row_scale; D.row_min_log = t.row_min_log; D.row_var = t.row_var;
+    D.col_q = t.col_q; D.col_scale = t.col_scale; D.col_min_log = t.col_min_log; D.col_var = t.col_var;
+    D.ws = t.workspace; D.lr = t.lr; D.fira_prev = t.fira_prev_norm; D.has_fira_prev = t.has_fira_prev;
+    D.B = t.batch; D.R = t.rows; D.C = t.cols; D.numel = numel;
+    D.sr_seed = t.sr_seed;
+    D.vec4 = ((t.cols * esz) % 16 == 0) ? 1 : 0;
+    const FWs W = fws_layout(t.batch, t.rows, t.cols);
+    D.tile_begin = tiles;
+    D.unit_begin = units;
+    tiles += W.ntile;
+    units += W.nunit;
+  }
+  if (tiles > 0x7FFFFFFF || units > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  hipStream_t st = (hipStream_t)stream;
+  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(DescF) * (size_t)ntensors,
+                               hipMemcpyHostToDevice, st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  HyperF h{};
+  h.bv = (float)beta_val;
+  h.eps1 = eps1; h.eps2 = eps2; h.lr_val = lr_val;
+  h.bias_factor = bias_factor; h.bias_mode = bias_mode;
+  h.scale_param = scale_parameter;
+  h.wd = weight_decay; h.wd_mode = wd_mode;
+  h.d = d; h.fira = fira; h.margin = (float)(1.0 + (double)fira_margin);
+  h.floor_ = log_floor;
+  h.w_m = (float)(1.0 - beta1);
+  h.block_size = block_size;
+  h.mk = has_m ? mk_code(m_bits, m_mode) : 0;
+  h.lbm = lbm;
+  h.sr_step = sr_step;
+  const bool clip = d > 0.0f || fira;
+  const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
+  switch (dtype) {
+    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+    case A8_BF16:
+      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, v_bits, clip, h, st)
+                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+    default:
+      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, v_bits, clip, h, st)
+                        : run_group<__half, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+  }
+}
+
+}  // extern "C"

@@ -15,6 +15,7 @@
 // a per-block 256-entry table in LDS (one exp2 per code instead of one per
 // element).  A tensor table lets one launch cover many tensors.
 #include "a8_common.cuh"
+#include "a8_mcodec.cuh"
 #include "a8_abi_impl.h"
 
 namespace a8 {
@@ -58,122 +59,6 @@ struct Hyper1D {
   int has_decay;
   uint64_t sr_step;
 };
-
-__constant__ float c_qmap8[256];
-__constant__ float c_qmap4[16];
-
-// ------------------------------------------------------------ SR writeback
-// SplitMix64 counter stream keyed by (seed, step, element) and the bf16/fp16
-// stochastic rounding rules of the reference (kernels.cu:48-161).
-__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64_t idx) {
-  uint64_t z = seed * 0x9E3779B97F4A7C15ULL + step * 0xD1B54A32D192ED03ULL + idx;
-  z += 0x9E3779B97F4A7C15ULL;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-  z ^= z >> 31;
-  return (uint32_t)(z >> 32);
-}
-
-__device__ __forceinline__ float sr_uniform(uint64_t seed, uint64_t step, uint64_t idx) {
-  return (float)(sr_bits(seed, step, idx) >> 8) * (1.0f / 16777216.0f);
-}
-
-__device__ __forceinline__ uint16_t sr_bf16(float x, float u) {
-  uint32_t b = __float_as_uint(x);
-  const bool nan = ((b & 0x7F800000u) == 0x7F800000u) && (b & 0x007FFFFFu);
-  if (nan) return (uint16_t)(((b & 0x80000000u) | 0x7FC00000u) >> 16);
-  uint32_t lo = b & 0xFFFF0000u;
-  uint32_t rem = b & 0x0000FFFFu;
-  uint32_t hi = lo + 0x00010000u;
-  bool lo_inf = (lo & 0x7F800000u) == 0x7F800000u;
-  bool hi_inf = ((hi & 0x7F800000u) == 0x7F800000u) && !(hi & 0x007FFFFFu);
-  bool up_ok = rem && !lo_inf && !hi_inf;
-  float prob = up_ok ? (float)rem * (1.0f / 65536.0f) : 0.0f;
-  return (uint16_t)(((up_ok && u < prob) ? hi : lo) >> 16);
-}
-
-__device__ __forceinline__ uint16_t h_next_up(uint16_t h) {
-  if (h == 0x7C00u) return h;
-  if (h == 0x8000u) return 0x0001u;
-  return (h & 0x8000u) ? (uint16_t)(h - 1u) : (uint16_t)(h + 1u);
-}
-__device__ __forceinline__ uint16_t h_next_down(uint16_t h) {
-  if (h == 0xFC00u) return h;
-  if (h == 0x0000u) return 0x8001u;
-  return (h & 0x8000u) ? (uint16_t)(h + 1u) : (uint16_t)(h - 1u);
-}
-
-__device__ __forceinline__ uint16_t sr_fp16(float x, float u) {
-  uint32_t b = __float_as_uint(x);
-  uint16_t sign = (b & 0x80000000u) ? 0x8000u : 0u;
-  if ((b & 0x7F800000u) == 0x7F800000u) return (b & 0x007FFFFFu) ? (sign | 0x7E00u) : (sign | 0x7C00u);
-  if (fabsf(x) > 65504.0f) return sign | 0x7BFFu;
-  __half nh = __float2half_rn(x);
-  uint16_t qb = __half_as_ushort(nh);
-  float q = __half2float(nh);
-  if (q == x) return qb;
-  uint16_t lo, hi;
-  if (q < x) { lo = qb; hi = h_next_up(qb); } else { hi = qb; lo = h_next_down(qb); }
-  float flo = __half2float(__ushort_as_half(lo));
-  float fhi = __half2float(__ushort_as_half(hi));
-  float prob = (x - flo) / (fhi - flo);
-  return (u < prob) ? hi : lo;
-}
-
-template <typename T>
-__device__ __forceinline__ T sr_round(float x, uint64_t seed, uint64_t step, uint64_t idx) {
-  float u = sr_uniform(seed, step, idx);
-  if constexpr (sizeof(T) == 2 && std::is_same<T, __hip_bfloat16>::value) {
-    return __ushort_as_bfloat16(sr_bf16(x, u));
-  } else if constexpr (sizeof(T) == 2) {
-    return __ushort_as_half(sr_fp16(x, u));
-  } else {
-    return x;
-  }
-}
-
-// ------------------------------------------------------------ M codecs
-__device__ __forceinline__ float m_decode(int mk, uint32_t q, float s) {
-  switch (mk) {
-    case 1: return ((float)q - 128.0f) * (s / 128.0f);
-    case 2: return ((float)q - 8.0f) * (s / 8.0f);
-    case 3: return c_qmap8[q] * s;
-    default: return c_qmap4[q] * s;
-  }
-}
-
-// Nearest codebook entry with searchsorted semantics and sign fix
-// (optimizer.py:454-476), on x = m / absmax computed with IEEE division.
-template <int N>
-__device__ __forceinline__ uint32_t d_code(float m, float amax) {
-  const float* qm = (N == 256) ? c_qmap8 : c_qmap4;
-  float x = m / amax;
-  int lo = 0, hi = N;  // first index with qm[i] >= x
-  while (lo < hi) {
-    int mid = (lo + hi) >> 1;
-    if (qm[mid] < x) lo = mid + 1; else hi = mid;
-  }
-  int idx = lo > N - 1 ? N - 1 : lo;
-  int prev = idx - 1 < 0 ? 0 : idx - 1;
-  if (fabsf(x - qm[prev]) < fabsf(x - qm[idx])) idx = prev;
-  float sx = (x > 0.0f) ? 1.0f : ((x < 0.0f) ? -1.0f : 0.0f);
-  float v = qm[idx];
-  float sq = (v > 0.0f) ? 1.0f : ((v < 0.0f) ? -1.0f : 0.0f);
-  if (sx != sq && sx != 0.0f) {
-    if (sx > 0.0f && idx < N - 1) idx += 1;
-    else if (sx < 0.0f && idx > 0) idx -= 1;
-  }
-  return (uint32_t)idx;
-}
-
-__device__ __forceinline__ uint32_t m_encode(int mk, float m, float amax, float ramax) {
-  switch (mk) {
-    case 1: return uf_code<128>(m, amax, ramax);
-    case 2: return uf_code<8>(m, amax, ramax);
-    case 3: return d_code<256>(m, amax);
-    default: return d_code<16>(m, amax);
-  }
-}
 
 // ------------------------------------------------------------ main kernel
 constexpr int kLanes = 256;
@@ -779,10 +664,10 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
 int64_t a8_table_bytes_1d(int ntensors) { return (int64_t)sizeof(Desc1D) * (int64_t)ntensors; }
 
 int a8_set_qmap(const float* qmap8_host, const float* qmap4_host) {
-  if (hipMemcpyToSymbol(HIP_SYMBOL(c_qmap8), qmap8_host, 256 * sizeof(float)) != hipSuccess)
-    return set_error(A8_ERR_HIP, "qmap8 upload failed");
-  if (hipMemcpyToSymbol(HIP_SYMBOL(c_qmap4), qmap4_host, 16 * sizeof(float)) != hipSuccess)
-    return set_error(A8_ERR_HIP, "qmap4 upload failed");
+  if (!qmap8_host || !qmap4_host) return set_error(A8_ERR_ARG, "null codebook");
+  if (upload_qmap_tu(qmap8_host, qmap4_host) != hipSuccess ||
+      a8::factored_upload_qmap(qmap8_host, qmap4_host) != hipSuccess)
+    return set_error(A8_ERR_HIP, "codebook upload failed");
   return 0;
 }
 

@@ -155,6 +155,58 @@ int64_t a8_table_bytes_full(int ntensors);
 int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
                    int has_prev, int apply, float margin, void* stream);
 
+/* ---- Factored second moment (Adafactor row/column statistics) ------------
+ * One parameter of shape [batch, rows, cols] (leading dimensions flattened
+ * into batch) with row/column V state.  V state is AL8/AL16 codes with
+ * per-block scale/min_log over the flattened [batch*rows] (resp. [batch*cols])
+ * vector, or fp32 vectors (row_var/col_var) when unquantised. */
+typedef struct a8_tensor2d {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;            /* optional momentum codes (NULL: beta1 is None) */
+  float* m_scale;
+  void* row_q;             /* AL codes (NULL when row_var holds fp32 state) */
+  float* row_scale;
+  float* row_min_log;
+  float* row_var;          /* fp32 row state, [batch*rows], or NULL */
+  void* col_q;
+  float* col_scale;
+  float* col_min_log;
+  float* col_var;
+  float* workspace;        /* a8_factored_workspace_floats(batch, rows, cols) floats */
+  const float* lr;         /* device learning rate, or NULL for lr_val */
+  float* fira_prev_norm;   /* 0-dim fp32 state when fira is on; written every step */
+  int has_fira_prev;       /* 0 on the first Fira step (the state is created) */
+  int64_t batch, rows, cols;
+  uint64_t sr_seed;
+} a8_tensor2d;
+
+/* Replaces the factored branch of one optimizer step for a group of tensors
+ * (optimizer.py:2198-2252 statistics and V EMA, 2534-2552 with
+ * _fallback_2d_update 920-970 for the update; kernels: compute_factored_sums
+ * kernels.cu:1925-1944, fused_log_quantize_lerp 340-480, fused_update_2d
+ * 1523-1647).  Per tensor:
+ *   row_mean = mean_c(g^2) + eps1, col_mean = mean_r(g^2) + eps1 (deterministic);
+ *   row/col V: decode, lerp(v, mean, beta_val), refit + re-encode (or fp32 state);
+ *   r = mean_r(row V) clamped at eps1 per batch; inv_row = 1/sqrt(row/r), inv_col = 1/sqrt(col);
+ *   alpha = lr (* max(rms(p), eps2) when scale_parameter) (* or / bias_factor);
+ *   u = (x * inv_row) * inv_col with x = g, or the momentum EMA lerp(m, g, 1-beta1);
+ *   d > 0 or fira: one extra pass for ||u||, Fira limiter, denom = max(1, ||u||/(sqrt(n) d));
+ *   p <- p * (1 - wd*alpha | 1 - wd*lr) - (alpha/denom) * u   (SR for bf16/fp16 if stochastic).
+ * bias_mode: 0 none, 1 alpha *= bias_factor, 2 alpha /= bias_factor.
+ * wd_mode: 0 none, 1 decay uses alpha, 2 decay uses lr.
+ * v_bits: 8 / 16 (codes) or 0 (fp32 row_var/col_var).  block_size: V block
+ * (any positive size).  m_block_size: power of two in [32, 2048].
+ * table_dev: device buffer of a8_table_bytes_2d(ntensors) bytes (uploaded when upload != 0). */
+int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int ntensors,
+                     void* table_dev, int64_t table_bytes, int upload, double beta_val, float eps1,
+                     float eps2, float lr_val, int scale_parameter, int bias_mode, float bias_factor,
+                     float weight_decay, int wd_mode, float d, int fira, float fira_margin,
+                     float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
+                     int m_bits, int m_mode, uint64_t sr_step, void* stream);
+int64_t a8_factored_workspace_floats(int64_t batch, int64_t rows, int64_t cols);
+int64_t a8_table_bytes_2d(int ntensors);
+
 #ifdef __cplusplus
 }
 #endif

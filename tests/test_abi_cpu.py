@@ -48,3 +48,19 @@ def test_argument_errors_without_gpu():
                               None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 2048,
                               256, 8, 0, 0.0, 8, 0, 1e-4, 1.0, 0, None)
     assert rc == -2, rc
+
+
+def test_module_signatures_match_reference():
+    """Every name the reference-named module provides has the reference's positional parameters
+    (fixture written from kernels.cu:3089-3150 by tests/golden/gen_signatures.py)."""
+    import inspect
+    import json
+    import os
+    from adafactor8bit import adafactor8bit_cuda as K
+    path = os.path.join(os.path.dirname(__file__), "golden", "module_signatures.json")
+    with open(path) as f:
+        ref = json.load(f)
+    assert len(ref) == 61
+    for name in K.__all__:
+        assert name in ref, name
+        assert list(inspect.signature(getattr(K, name)).parameters) == ref[name], name

@@ -39,6 +39,15 @@ class TensorFull(ctypes.Structure):
                 ("numel", _c_i64)]
 
 
+class Tensor2D(ctypes.Structure):
+    """Mirror of ``a8_tensor2d``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
+                ("row_q", _c_vp), ("row_scale", _c_vp), ("row_min_log", _c_vp), ("row_var", _c_vp),
+                ("col_q", _c_vp), ("col_scale", _c_vp), ("col_min_log", _c_vp), ("col_var", _c_vp),
+                ("workspace", _c_vp), ("lr", _c_vp), ("fira_prev_norm", _c_vp), ("has_fira_prev", _c_i),
+                ("batch", _c_i64), ("rows", _c_i64), ("cols", _c_i64), ("sr_seed", _c_u64)]
+
+
 _SIGS = {
     "a8_last_error": (ctypes.c_char_p, []),
     "a8_version": (ctypes.c_char_p, []),
@@ -60,6 +69,11 @@ _SIGS = {
                                              _c_f, _c_f, _c_i, _c_i, _c_vp]),
     "a8_table_bytes_full": (_c_i64, [_c_i]),
     "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
+    "a8_factored_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(Tensor2D), _c_i, _c_vp, _c_i64, _c_i, _c_d,
+                                _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_f, _c_i, _c_f, _c_f,
+                                _c_i, _c_i, _c_d, _c_i, _c_i, _c_i, _c_u64, _c_vp]),
+    "a8_factored_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "a8_table_bytes_2d": (_c_i64, [_c_i]),
 }
 
 _LIB = None

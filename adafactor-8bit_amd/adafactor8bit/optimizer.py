@@ -304,9 +304,13 @@ class _Plan:
     __slots__ = ("p", "g", "st", "group", "path", "step", "beta_val", "alpha_val", "alpha_t",
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
-                 "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize")
+                 "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
+                 "bias_mode", "bias_fac", "wd", "wd_mode")
 
     def batch_key(self):
+        if self.path == "factored":
+            return ("factored", self.p.device, self.p.dtype, self.g.dtype, self.step, self.quant,
+                    self.vqt, self.bs, self.has_m, self.mqt, self.mbs, self.sr, self.beta3)
         if self.path not in ("q1d", "f1d"):
             return None
         if self.alpha_t is not None or self.decay_t is not None:
@@ -356,6 +360,17 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P.margin = group.get("fira_margin", 0.01)
     P.lag = group.get("lag_norm", False)
 
+    P.beta3 = beta3
+    if sgd:
+        P.path = "sgd"
+    elif full_rank:
+        if P.quant and P.vqt != "fp32":
+            P.path = "q1d" if (not P.has_m or P.mqt != "fp32") else "q1d_fp32m"
+        else:
+            P.path = "f1d" if (not P.has_m or not P.quant or P.mqt == "fp32") else "f1d_qm"
+    else:
+        P.path = "factored"
+
     step = st["step"] + 1
     st["step"] = step
     P.step = step
@@ -365,6 +380,11 @@ def _plan_param(p, grad, st, group) -> _Plan:
         P.beta_val = 1.0 - beta2
     else:
         P.beta_val = math.pow(step, beta2_decay)
+
+    P.sr = group.get("stochastic_round_writeback", False) and p.dtype in (torch.bfloat16, torch.float16)
+    if P.path == "factored":
+        _plan_factored(P, group, beta1, beta2, sgd)
+        return P
 
     # alpha / rho: optimizer.py:832-856 (+ bias correction 2020-2030)
     lr = group["lr"]
@@ -407,7 +427,6 @@ def _plan_param(p, grad, st, group) -> _Plan:
 
     # weight decay: optimizer.py:2032-2039 (fused into the kernels as p*decay)
     wd = group["weight_decay"]
-    P.sr = group.get("stochastic_round_writeback", False) and p.dtype in (torch.bfloat16, torch.float16)
     P.decay_val, P.decay_t = None, None
     if wd != 0:
         use_alpha = group.get("scale_weight_decay", True)
@@ -422,16 +441,38 @@ def _plan_param(p, grad, st, group) -> _Plan:
             else:
                 P.decay_val = _f32(_F32(1.0) - _F32(_F32(P.rho_val) * _F32(wd)))
 
-    if sgd:
-        P.path = "sgd"
-    elif full_rank:
-        if P.quant and P.vqt != "fp32":
-            P.path = "q1d" if (not P.has_m or P.mqt != "fp32") else "q1d_fp32m"
-        else:
-            P.path = "f1d" if (not P.has_m or not P.quant or P.mqt == "fp32") else "f1d_qm"
-    else:
-        P.path = "factored"
     return P
+
+
+def _plan_factored(P, group, beta1, beta2, sgd):
+    """Scalar preparation of the factored path: the step size itself (relative
+    step, RMS scaling, bias correction, optimizer.py:832-856, 2020-2030) and the
+    weight-decay factor (2032-2039) are formed on the device from these inputs."""
+    lr = group["lr"]
+    relative_step = group["relative_step"]
+    P.scale_param = bool(group["scale_parameter"])
+    if isinstance(lr, Tensor):
+        rho_t = lr.to(device=P.p.device, dtype=torch.float32).reshape(())
+        if relative_step:
+            rho_t = torch.minimum(torch.tensor(float(P.step), device=P.p.device).rsqrt(), rho_t)
+        P.rho_t, P.rho_val = rho_t.contiguous(), 0.0
+    else:
+        P.rho_t = None
+        P.rho_val = _f32(min(lr, 1.0 / math.sqrt(P.step)) if relative_step else lr)
+    P.alpha_t, P.alpha_val = None, None
+    P.bias_mode, P.bias_fac = 0, 1.0
+    if beta1 is not None and not relative_step and not sgd:
+        bc_on = P.adam_denom if group.get("bias_correction") is None else group.get("bias_correction")
+        if bc_on:
+            bc1 = 1.0 - beta1 ** P.step
+            if beta2 is not None:
+                P.bias_mode, P.bias_fac = 1, _f32(math.sqrt(1.0 - beta2 ** P.step) / bc1)
+            else:
+                P.bias_mode, P.bias_fac = 2, _f32(bc1)
+    wd = group["weight_decay"]
+    P.wd = _f32(wd)
+    P.wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
+    P.decay_val, P.decay_t = None, None
 
 
 def _dev_scalar(opt, device, key, value):
@@ -556,6 +597,9 @@ def _fira_scale_only(opt, st, x, margin, device, key):
 
 
 def _run_single(opt, P):
+    if P.path == "factored":
+        _run_factored(opt, [P])
+        return
     if P.path not in ("q1d", "f1d"):
         raise NotImplementedError(f"adafactor8bit: '{P.path}' update path is not available in this build yet")
     alpha_t, alpha_val = _alpha_args(P)
@@ -589,6 +633,9 @@ def _run_single(opt, P):
 
 def _run_batch(opt, key, plans):
     path = key[0]
+    if path == "factored":
+        _run_factored(opt, plans)
+        return
     if len(plans) == 1:
         _run_single(opt, plans[0])
         return
@@ -657,3 +704,104 @@ def _run_batch(opt, key, plans):
             strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+
+
+def _run_factored(opt, plans):
+    """One factored step for a group of matrices (optimizer.py:2198-2252, 920-970):
+    statistics, row/column V EMA, update (and the norm pass for RMS clipping or
+    Fira) in a8_factored_step's few launches."""
+    P0 = plans[0]
+    if P0.beta3 is not None:
+        raise NotImplementedError("adafactor8bit: the CAME path is not available in this build yet")
+    vbits = 0 if (not P0.quant or P0.vqt == "fp32") else (16 if P0.vqt == "al16" else 8)
+    for pl in plans:
+        if pl.has_m and (not pl.quant or pl.mqt == "fp32"):
+            raise NotImplementedError("adafactor8bit: factored path with fp32 momentum is not available "
+                                      "in this build yet")
+        if not pl.p.is_contiguous():
+            raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
+        if pl.g.dtype != pl.p.dtype:
+            if pl.p.dtype == torch.float32:
+                pl.g = pl.g.float()
+            else:
+                raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    dev = P0.p.device
+    L = nat.lib()
+    n = len(plans)
+    fira = bool(P0.fira)
+    has_prev = []
+    for pl in plans:
+        st = pl.st
+        if fira:
+            prev = st.get("fira_prev_norm")
+            if prev is None:
+                st["fira_prev_norm"] = torch.zeros((), dtype=torch.float32, device=dev)
+                has_prev.append(0)
+            else:
+                if not torch.is_tensor(prev) or prev.device != dev or prev.dtype != torch.float32:
+                    prev = torch.as_tensor(prev, dtype=torch.float32).to(dev).reshape(())
+                    st["fira_prev_norm"] = prev
+                has_prev.append(1)
+        else:
+            has_prev.append(0)
+        if vbits == 0:
+            for k in ("row_var", "col_var"):
+                if not st[k].is_contiguous():
+                    st[k] = st[k].contiguous()
+
+    sig = tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(pl.rho_t), hp,
+                 tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)))
+                for pl, hp in zip(plans, has_prev))
+    wsd = opt._ws.setdefault((dev, "tables2d"), {})
+    shapes = tuple(tuple(pl.g.shape) for pl in plans)
+    ent = wsd.get(shapes)
+    upload = 0
+    if ent is None or ent["sig"] != sig:
+        sizes = []
+        for pl in plans:
+            sh = pl.g.shape
+            R, C = int(sh[-2]), int(sh[-1])
+            B = pl.g.numel() // (R * C)
+            sizes.append((B, R, C, int(L.a8_factored_workspace_floats(B, R, C))))
+        offs, tot = [], 0
+        for (_, _, _, w) in sizes:
+            offs.append(tot)
+            tot += (w + 63) // 64 * 64
+        if ent is not None and ent["ws"].numel() >= tot and ent["n"] == n:
+            wbuf, table = ent["ws"], ent["table"]
+        else:
+            wbuf = torch.empty(max(tot, 1), dtype=torch.float32, device=dev)
+            table = torch.empty(int(L.a8_table_bytes_2d(n)), dtype=torch.uint8, device=dev)
+        arr = (nat.Tensor2D * n)()
+        base = wbuf.data_ptr()
+        for i, (pl, (B, R, C, _)) in enumerate(zip(plans, sizes)):
+            st = pl.st
+            q = vbits != 0
+            arr[i] = nat.Tensor2D(
+                pl.p.data_ptr(), pl.g.data_ptr(),
+                nat.ptr(st.get("m_q") if pl.has_m else None), nat.ptr(st.get("m_scale") if pl.has_m else None),
+                nat.ptr(st["row_var_q"]) if q else None, nat.ptr(st["row_var_scale"]) if q else None,
+                nat.ptr(st["row_var_min_log"]) if q else None, None if q else st["row_var"].data_ptr(),
+                nat.ptr(st["col_var_q"]) if q else None, nat.ptr(st["col_var_scale"]) if q else None,
+                nat.ptr(st["col_var_min_log"]) if q else None, None if q else st["col_var"].data_ptr(),
+                base + 4 * offs[i], nat.ptr(pl.rho_t),
+                nat.ptr(st.get("fira_prev_norm")) if fira else None, has_prev[i],
+                B, R, C, int(st.get("sr_seed", 0)))
+        ent = {"sig": sig, "arr": arr, "ws": wbuf, "table": table, "n": n}
+        if len(wsd) > 64:
+            wsd.clear()
+        wsd[shapes] = ent
+        upload = 1
+    arr, table = ent["arr"], ent["table"]
+    rc = L.a8_factored_step(
+        nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), table.numel(), upload,
+        P0.beta_val, _f32(P0.eps1), _f32(P0.eps2), float(P0.rho_val), int(P0.scale_param),
+        int(P0.bias_mode), float(P0.bias_fac), float(P0.wd), int(P0.wd_mode), float(P0.d), int(fira),
+        float(P0.margin), _AL_FLOOR, vbits, int(P0.bs), P0.beta1 if P0.has_m else 0.0,
+        int(P0.mbs) if P0.has_m else 32, S.m_bits(P0.mqt) if P0.has_m else 8,
+        S.m_mode(P0.mqt) if P0.has_m else 0, int(P0.step), nat.stream_of(dev))
+    nat.check(rc, "a8_factored_step")
+    if vbits:
+        for pl in plans:
+            _block_view(pl.st, "row_var", pl.bs)
+            _block_view(pl.st, "col_var", pl.bs)

@@ -17,7 +17,14 @@ import golden_util as gu
 
 SUPPORTED = ["adamw_uf8_al8", "adamw_uf8_al16", "adamw_uf4_al8", "adamw_d8_al8", "adamw_d4_al8",
              "adamw_bv256_mb128", "adamw_clip_fira_wd", "adamw_fp32_state", "rmsprop_al8",
-             "adafactor_mom1d"]
+             "adafactor_mom1d", "adafactor_factored_al8", "adafactor_factored_emb",
+             "adafactor_factored_m_uf8"]
+
+# Row/column statistics are sums over a matrix: the HIP path reduces them in a
+# fixed order of its own (fp32 tiles, double across tiles), the reference in
+# torch's CPU order, so a mean may differ by an ulp and a row/column code next
+# to a rounding boundary may flip even at step 1.
+FACTORED = ("adafactor_factored",)
 
 CODE_KEYS = ("_q",)
 
@@ -30,10 +37,11 @@ def _cmp_state(name, key, st, z, zkeys, report):
         mine = mine.detach().cpu().numpy() if torch.is_tensor(mine) else np.asarray(mine)
         assert mine.dtype == ref.dtype and mine.shape == ref.shape, (name, key, k, mine.dtype, ref.dtype)
         first = key.startswith("s1/")
+        factored_stat = name.startswith(FACTORED) and (k.startswith("row_var") or k.startswith("col_var"))
         if k.endswith("_q"):
             frac, mx = gu.code_mismatch(mine, ref)
             report.append((key, k, frac, mx))
-            allowed = 0.0 if first else 1e-4 + 1.0 / max(mine.size, 1)
+            allowed = 0.0 if (first and not factored_stat) else 1e-4 + 1.0 / max(mine.size, 1)
             assert mx <= 2 and frac <= allowed, f"{name} {key}/{k}: {frac:.2e} codes differ, max {mx}"
         elif k in ("step",):
             assert int(mine) == int(ref)

@@ -14,7 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadafactor8bit_amd.so")
 
 F32, BF16, F16 = 0, 1, 2
-MODE_NOCLIP, MODE_NORM, MODE_APPLY, MODE_LAG = 0, 1, 2, 3
+MODE_NOCLIP, MODE_NORM, MODE_APPLY, MODE_LAG, MODE_MNORM = 0, 1, 2, 3, 4
 
 _c_vp = ctypes.c_void_p
 _c_i = ctypes.c_int
@@ -44,7 +44,10 @@ class Tensor2D(ctypes.Structure):
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
                 ("row_q", _c_vp), ("row_scale", _c_vp), ("row_min_log", _c_vp), ("row_var", _c_vp),
                 ("col_q", _c_vp), ("col_scale", _c_vp), ("col_min_log", _c_vp), ("col_var", _c_vp),
-                ("workspace", _c_vp), ("lr", _c_vp), ("fira_prev_norm", _c_vp), ("has_fira_prev", _c_i),
+                ("conf_row_q", _c_vp), ("conf_row_scale", _c_vp), ("conf_row_min_log", _c_vp),
+                ("conf_row", _c_vp), ("conf_col_q", _c_vp), ("conf_col_scale", _c_vp),
+                ("conf_col_min_log", _c_vp), ("conf_col", _c_vp), ("workspace", _c_vp),
+                ("lr", _c_vp), ("fira_prev_norm", _c_vp), ("has_fira_prev", _c_i),
                 ("batch", _c_i64), ("rows", _c_i64), ("cols", _c_i64), ("sr_seed", _c_u64)]
 
 
@@ -71,7 +74,8 @@ _SIGS = {
     "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_factored_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(Tensor2D), _c_i, _c_vp, _c_i64, _c_i, _c_d,
                                 _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_f, _c_i, _c_f, _c_f,
-                                _c_i, _c_i, _c_d, _c_i, _c_i, _c_i, _c_u64, _c_vp]),
+                                _c_i, _c_i, _c_d, _c_i, _c_i, _c_i, _c_u64, _c_i, _c_d, _c_f, _c_i,
+                                _c_vp]),
     "a8_factored_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "a8_table_bytes_2d": (_c_i64, [_c_i]),
 }

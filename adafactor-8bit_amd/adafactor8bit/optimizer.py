@@ -494,8 +494,8 @@ def _v_buf(opt, device, numel):
     return b[:numel]
 
 
-def _norm_buf(opt, device):
-    key = (device, "norm_buf")
+def _norm_buf(opt, device, which="norm_buf"):
+    key = (device, which)
     b = opt._ws.get(key)
     if b is None:
         b = torch.zeros(1, dtype=torch.float32, device=device)
@@ -626,7 +626,13 @@ def _run_single(opt, P):
     nb = _norm_buf(opt, dev)
     vb = _v_buf(opt, dev, P.p.numel()) if P.path == "q1d" else None
     _launch_1d(opt, P, nat.MODE_NORM, None, 0.0, norm_buf=nb, v_buf=vb)
-    if P.fira:
+    if P.fira and P.has_m and P.mom_only:
+        # momentum-only: the U-clip uses ||U|| (NORM), Fira the new momentum's
+        # norm ||M'|| (optimizer.py:890-896, _apply_update_pytorch 866-875)
+        nbm = _norm_buf(opt, dev, "norm_buf_m")
+        _launch_1d(opt, P, nat.MODE_MNORM, None, 0.0, norm_buf=nbm, prev_norm=nb, v_buf=vb)
+        alpha_t, _ = _fira_apply(opt, st, nbm, alpha_t, alpha_val, P.margin, dev)
+    elif P.fira:
         alpha_t, nb = _fira_apply(opt, st, nb, alpha_t, alpha_val, P.margin, dev)
     _launch_1d(opt, P, nat.MODE_APPLY, alpha_t, alpha_val, norm_buf=nb, v_buf=vb)
 
@@ -711,9 +717,12 @@ def _run_factored(opt, plans):
     statistics, row/column V EMA, update (and the norm pass for RMS clipping or
     Fira) in a8_factored_step's few launches."""
     P0 = plans[0]
-    if P0.beta3 is not None:
-        raise NotImplementedError("adafactor8bit: the CAME path is not available in this build yet")
+    came = P0.beta3 is not None and P0.has_m
     vbits = 0 if (not P0.quant or P0.vqt == "fp32") else (16 if P0.vqt == "al16" else 8)
+    cbits = 0
+    if came:
+        cqt = P0.st.get("c_quant_type") or P0.vqt
+        cbits = 0 if (not P0.quant or cqt == "fp32") else (16 if cqt == "al16" else 8)
     for pl in plans:
         if pl.has_m and (not pl.quant or pl.mqt == "fp32"):
             raise NotImplementedError("adafactor8bit: factored path with fp32 momentum is not available "
@@ -748,6 +757,10 @@ def _run_factored(opt, plans):
             for k in ("row_var", "col_var"):
                 if not st[k].is_contiguous():
                     st[k] = st[k].contiguous()
+        if came and cbits == 0:
+            for k in ("conf_row", "conf_col"):
+                if not st[k].is_contiguous():
+                    st[k] = st[k].contiguous()
 
     sig = tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(pl.rho_t), hp,
                  tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)))
@@ -777,6 +790,17 @@ def _run_factored(opt, plans):
         for i, (pl, (B, R, C, _)) in enumerate(zip(plans, sizes)):
             st = pl.st
             q = vbits != 0
+            cq = cbits != 0
+            conf = [None] * 8
+            if came:
+                conf = [nat.ptr(st["conf_row_q"]) if cq else None,
+                        nat.ptr(st["conf_row_scale"]) if cq else None,
+                        nat.ptr(st["conf_row_min_log"]) if cq else None,
+                        None if cq else st["conf_row"].data_ptr(),
+                        nat.ptr(st["conf_col_q"]) if cq else None,
+                        nat.ptr(st["conf_col_scale"]) if cq else None,
+                        nat.ptr(st["conf_col_min_log"]) if cq else None,
+                        None if cq else st["conf_col"].data_ptr()]
             arr[i] = nat.Tensor2D(
                 pl.p.data_ptr(), pl.g.data_ptr(),
                 nat.ptr(st.get("m_q") if pl.has_m else None), nat.ptr(st.get("m_scale") if pl.has_m else None),
@@ -784,7 +808,7 @@ def _run_factored(opt, plans):
                 nat.ptr(st["row_var_min_log"]) if q else None, None if q else st["row_var"].data_ptr(),
                 nat.ptr(st["col_var_q"]) if q else None, nat.ptr(st["col_var_scale"]) if q else None,
                 nat.ptr(st["col_var_min_log"]) if q else None, None if q else st["col_var"].data_ptr(),
-                base + 4 * offs[i], nat.ptr(pl.rho_t),
+                *conf, base + 4 * offs[i], nat.ptr(pl.rho_t),
                 nat.ptr(st.get("fira_prev_norm")) if fira else None, has_prev[i],
                 B, R, C, int(st.get("sr_seed", 0)))
         ent = {"sig": sig, "arr": arr, "ws": wbuf, "table": table, "n": n}
@@ -799,9 +823,15 @@ def _run_factored(opt, plans):
         int(P0.bias_mode), float(P0.bias_fac), float(P0.wd), int(P0.wd_mode), float(P0.d), int(fira),
         float(P0.margin), _AL_FLOOR, vbits, int(P0.bs), P0.beta1 if P0.has_m else 0.0,
         int(P0.mbs) if P0.has_m else 32, S.m_bits(P0.mqt) if P0.has_m else 8,
-        S.m_mode(P0.mqt) if P0.has_m else 0, int(P0.step), nat.stream_of(dev))
+        S.m_mode(P0.mqt) if P0.has_m else 0, int(P0.step), int(came),
+        float(P0.beta3) if came else 0.0, _f32(P0.group.get("eps_came", 1e-16)), cbits,
+        nat.stream_of(dev))
     nat.check(rc, "a8_factored_step")
     if vbits:
         for pl in plans:
             _block_view(pl.st, "row_var", pl.bs)
             _block_view(pl.st, "col_var", pl.bs)
+    if cbits:
+        for pl in plans:
+            _block_view(pl.st, "conf_row", pl.bs)
+            _block_view(pl.st, "conf_col", pl.bs)

@@ -1,6 +1,6 @@
 // Factored (Adafactor row/column) optimizer step for MI355X (gfx950).
 //
-// One group step is three or five launches over every tensor of the group:
+// One group step is a few launches over every tensor of the group:
 //   k_fstats   2-D tiles of 32 rows x 1024 columns: row sums and column sums of
 //              g^2 (and sum p^2 for the relative step size), written as
 //              per-tile partials -- no atomics, so the result is deterministic;
@@ -14,6 +14,14 @@
 //              clipping or Fira it runs twice: first for sum(u^2) per unit,
 //              then (after k_fnorm) to apply;
 //   k_fnorm    one workgroup per tensor: ||u||, the Fira limiter and the step.
+// CAME (beta3) adds, between k_ffinish and the update:
+//   k_fclip    the RMS clip factor of U = (g * inv_row) * inv_col (after a
+//              k_fupdate norm pass over U, only when d > 0);
+//   k_came1    the same 2-D tiles as k_fstats: U / clip, the momentum EMA M',
+//              and row/column sums of the residual (U - M')^2 + eps_came;
+//   k_ffinish  again, on the residual sums: the confidence EMA, its AL
+//              re-encode and inv_conf_row / inv_conf_col;
+// and the update becomes (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
 // Numbers follow the reference's PyTorch path (optimizer.py:2198-2252 and
 // _fallback_2d_update 920-970): means are sum/count of the fp32 squares,
 // inv_row = 1/sqrt(row/r) and inv_col = 1/sqrt(col) with IEEE division and
@@ -36,8 +44,10 @@ struct FWs {
   int64_t p2;        // [ntile]            partial sum p^2
   int64_t invr;      // [B*R]              new row V, then inv_row
   int64_t invc;      // [B*C]              new column V, then inv_col
+  int64_t icr;       // [B*R]              CAME: new row confidence, then its inverse root
+  int64_t icc;       // [B*C]              CAME: new column confidence, then its inverse root
   int64_t npart;     // [nunit]            partial sum u^2
-  int64_t scal;      // [8]: alpha, step, fira scale, decay
+  int64_t scal;      // [8]: alpha, step, fira scale, decay, CAME clip factor
   int64_t total;
   int64_t nchunk, nstrip, ntile, nunit;
 };
@@ -53,7 +63,9 @@ __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
   w.p2 = w.colpart + B * w.nstrip * C;
   w.invr = w.p2 + w.ntile;
   w.invc = w.invr + B * R;
-  w.npart = w.invc + B * C;
+  w.icr = w.invc + B * C;
+  w.icc = w.icr + B * R;
+  w.npart = w.icc + B * C;
   w.scal = w.npart + w.nunit;
   w.total = w.scal + kScal;
   return w;
@@ -72,6 +84,14 @@ struct DescF {
   float* col_scale;
   float* col_min_log;
   float* col_var;
+  void* crow_q;        // CAME confidence state (codes or fp32), as row/col V
+  float* crow_scale;
+  float* crow_min_log;
+  float* crow_var;
+  void* ccol_q;
+  float* ccol_scale;
+  float* ccol_min_log;
+  float* ccol_var;
   float* ws;
   const float* lr;
   float* fira_prev;
@@ -94,6 +114,9 @@ struct HyperF {
   float margin;        // 1 + fira_margin
   float floor_;
   float w_m;           // momentum lerp weight (1 - beta1)
+  float w_c;           // CAME confidence lerp weight (1 - beta3)
+  float eps_came;
+  int came;
   int bias_mode;
   int scale_param;
   int wd_mode;
@@ -247,6 +270,121 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
   }
 }
 
+// ------------------------------------------------------------ CAME residual statistics
+// Old momentum of the element at flat index e (codec mk: 1 UF8, 2 UF4, 3 D8,
+// 4 D4; UF4/D4 keep the even element in the high nibble).
+__device__ __forceinline__ float m_old_at(int mk, const uint8_t* mq, const float* msc, int64_t e, int lbm) {
+  const float ms = gp(msc)[e >> lbm];
+  uint32_t q;
+  if (mk == 2 || mk == 4) {
+    const uint32_t byte = gp(mq)[e >> 1];
+    q = (e & 1) ? (byte & 0x0Fu) : (byte >> 4);
+  } else {
+    q = gp(mq)[e];
+  }
+  return m_decode(mk, q, ms);
+}
+
+// Old momentum of four consecutive elements e .. e+3 of one row (zero beyond
+// `avail`).  The vector form needs e % 4 == 0 (the four share an M block).
+template <int MK>
+__device__ __forceinline__ void m_old4(int mkr, const uint8_t* mq, const float* msc, int64_t e, int64_t avail,
+                                       bool vec, int lbm, float* out) {
+  const int mk = MK == 1 ? 1 : mkr;
+  if (vec && avail >= 4) {
+    const float ms = gp(msc)[e >> lbm];
+    if (mk == 2 || mk == 4) {
+      const uint32_t w = *gp(reinterpret_cast<const uint16_t*>(mq + (e >> 1)));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t byte = (w >> (8 * (k >> 1))) & 0xFFu;
+        out[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+      }
+    } else {
+      const uint32_t w = *gp(reinterpret_cast<const uint32_t*>(mq + e));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[k] = m_decode(mk, (w >> (8 * k)) & 0xFFu, ms);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = (k < avail) ? m_old_at(mk, mq, msc, e + k, lbm) : 0.0f;
+  }
+}
+
+// CAME pass 1 (optimizer.py:929-937): U = ((g * inv_row) * inv_col) / clip,
+// M' = lerp(M, U, 1 - beta1), res = (U - M')^2 + eps_came; row and column sums
+// of res as per-tile partials in the g^2 partial arrays (consumed by then).
+template <typename T, int MK>
+__global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, int ntab, HyperF h) {
+  __shared__ float s_col[4 * kTC];
+  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
+  const int64_t R = D.R, C = D.C;
+  const int64_t ch = t % W.nchunk;
+  const int64_t bs = t / W.nchunk;
+  const int64_t s = bs % W.nstrip;
+  const int64_t b = bs / W.nstrip;
+  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
+  const int64_t r_lo = s * kTR;
+  const int64_t r_hi = (r_lo + kTR < R) ? r_lo + kTR : R;
+  const int64_t c_base = ch * kTC;
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  float* ws = D.ws;
+  const bool vec = D.vec4 != 0;
+  const float clip = gp(ws)[W.scal + 4];
+  float icol[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t c = c_base + 4 * wl + 256 * j + e;
+      icol[j * 4 + e] = (c < C) ? gp(ws)[W.invc + b * C + c] : 0.0f;
+    }
+  float acc[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
+    const int64_t rowbase = (b * R + r) * C;
+    const float ir = gp(ws)[W.invr + b * R + r];
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c0 = c_base + 4 * wl + 256 * j;
+      if (c0 < C) {
+        float g4[4], m4[4];
+        load4<T>(G, rowbase, c0, C, vec, g4);
+        m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, m4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (c0 + e < C) {
+            const float ug = ((scrub(g4[e]) * ir) * icol[j * 4 + e]) / clip;
+            const float mn = lerp_ref(m4[e], ug, h.w_m);
+            const float dd = ug - mn;
+            const float res = dd * dd + h.eps_came;
+            rs += res;
+            acc[j * 4 + e] += res;
+          }
+        }
+      }
+    }
+    rs = grp_sum(rs, 64);
+    if (wl == 0) gp(ws)[W.rowpart + ch * (D.B * R) + b * R + r] = rs;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_col[wave * kTC + 4 * wl + 256 * j + e] = acc[j * 4 + e];
+  __syncthreads();
+  for (int q = lane; q < kTC; q += 256) {
+    const int64_t c = c_base + q;
+    if (c < C) {
+      const float v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
+      gp(ws)[W.colpart + (b * W.nstrip + s) * C + c] = v;
+    }
+  }
+}
+
 // ------------------------------------------------------------ row/column V EMA
 template <int VB>
 __device__ __forceinline__ float fv_decode(const void* q, const float* sc, const float* ml, int64_t i,
@@ -265,7 +403,12 @@ __device__ __forceinline__ float fv_decode(const void* q, const float* sc, const
 }
 
 // grid (ntab, 2): y = 0 row state (+ per-tensor scalars), y = 1 column state.
-template <int VB>
+// CONF = false: the second moment from the g^2 sums (mean + eps1, lerp weight
+// 1 - beta2 or step^decay), then inv_row / inv_col and the step size.
+// CONF = true (CAME): the confidence from the residual sums written by k_came1
+// (mean, lerp weight 1 - beta3), then inv_conf_row / inv_conf_col
+// (optimizer.py:941-953).  VB is the state's codec (8 / 16 bits, 0 = fp32).
+template <int VB, bool CONF>
 __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table, HyperF h) {
   __shared__ double sd[4];
   __shared__ float sf[8];
@@ -276,15 +419,27 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
   const int64_t B = D.B, R = D.R, C = D.C;
   const int64_t n = is_row ? B * R : B * C;
   float* ws = D.ws;
-  float* vec = ws + (is_row ? W.invr : W.invc);
-  void* q = is_row ? D.row_q : D.col_q;
-  float* sc = is_row ? D.row_scale : D.col_scale;
-  float* ml = is_row ? D.row_min_log : D.col_min_log;
-  float* fst = is_row ? D.row_var : D.col_var;
+  float* vec;
+  void* q;
+  float *sc, *ml, *fst;
+  if constexpr (CONF) {
+    vec = ws + (is_row ? W.icr : W.icc);
+    q = is_row ? D.crow_q : D.ccol_q;
+    sc = is_row ? D.crow_scale : D.ccol_scale;
+    ml = is_row ? D.crow_min_log : D.ccol_min_log;
+    fst = is_row ? D.crow_var : D.ccol_var;
+  } else {
+    vec = ws + (is_row ? W.invr : W.invc);
+    q = is_row ? D.row_q : D.col_q;
+    sc = is_row ? D.row_scale : D.col_scale;
+    ml = is_row ? D.row_min_log : D.col_min_log;
+    fst = is_row ? D.row_var : D.col_var;
+  }
   const float cnt = is_row ? (float)C : (float)R;
   const int64_t bsz = h.block_size;
+  const float w = CONF ? h.w_c : h.bv;
 
-  // 1. means of g^2 (sum / count + eps1), EMA with the decoded state
+  // 1. means (g^2: sum / count + eps1; residual: sum / count), EMA with the decoded state
   for (int64_t i = lane; i < n; i += 256) {
     double sum = 0.0;
     if (is_row) {
@@ -293,11 +448,12 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
       const int64_t b = i / C, c = i - b * C;
       for (int64_t k = 0; k < W.nstrip; ++k) sum += (double)gp(ws)[W.colpart + (b * W.nstrip + k) * C + c];
     }
-    const float mean = (float)sum / cnt + h.eps1;
+    float mean = (float)sum / cnt;
+    if constexpr (!CONF) mean = mean + h.eps1;
     float old;
     if constexpr (VB == 0) old = gp(fst)[i];
     else old = fv_decode<VB>(q, sc, ml, i, bsz);
-    const float nv = lerp_ref(old, mean, h.bv);
+    const float nv = lerp_ref(old, mean, w);
     gp(vec)[i] = nv;
     if constexpr (VB == 0) gp(fst)[i] = nv;
   }
@@ -331,7 +487,7 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
   }
   __syncthreads();
 
-  // 3. inverse square roots (optimizer.py:818-821)
+  // 3. inverse square roots (optimizer.py:818-821; the same form for the confidence, 951-953)
   if (is_row) {
     for (int64_t b = 0; b < B; ++b) {
       double s = 0.0;
@@ -348,7 +504,7 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
   }
 
   // 4. step size and weight decay (optimizer.py:832-856, 2020-2039)
-  if (is_row) {
+  if (!CONF && is_row) {
     const float rho = D.lr ? *gp(D.lr) : h.lr_val;
     float alpha = rho;
     if (h.scale_param) {
@@ -370,6 +526,7 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
       if (h.wd_mode == 1) dec = 1.0f - alpha * h.wd;
       else if (h.wd_mode == 2) dec = 1.0f - rho * h.wd;
       gp(sl)[3] = dec;
+      gp(sl)[4] = 1.0f;   // CAME clip factor unless k_fclip sets it
     }
   }
 }
@@ -377,8 +534,11 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
 // ------------------------------------------------------------ update
 // MODE 0: write with step = alpha; 1: sum(u^2) per unit; 2: write with the
 // step and Fira scale of k_fnorm.  MK: 0 no momentum, 1 UF8, 2 other codecs.
-template <typename T, int MODE, bool SR, int MK>
+// CM (CAME): the momentum EMA runs on U = ((g * inv_row) * inv_col) / clip and
+// the update is (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
+template <typename T, int MODE, bool SR, int MK, bool CM>
 __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table, int ntab, HyperF h) {
+  static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s4[8];
   constexpr bool kHasM = MK != 0;
   const DescF D = *find_unit(table, ntab, (int64_t)blockIdx.x);
@@ -393,6 +553,8 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   const float* ws = D.ws;
   const float* invr = ws + W.invr;
   const float* invc = ws + W.invc;
+  const float* icr = ws + W.icr;
+  const float* icc = ws + W.icc;
   const float* sl = ws + W.scal;
   const int lbm = h.lbm;
   const int BM = 1 << lbm;
@@ -400,18 +562,16 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   const int64_t mb = e0 >> lbm;
   const int mk = (MK == 1) ? 1 : h.mk;
 
-  float g[8], mn[8], u[8];
+  float g[8], mn[8], u[8], mo[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) { g[k] = 0.0f; mn[k] = 0.0f; u[k] = 0.0f; }
+  for (int k = 0; k < 8; ++k) { g[k] = 0.0f; mn[k] = 0.0f; u[k] = 0.0f; mo[k] = 0.0f; }
   float sq = 0.0f;
   uint32_t amaxb = 0u;
   if (cnt > 0) {
     load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
 #pragma unroll
     for (int k = 0; k < 8; ++k) g[k] = scrub(g[k]);
-    float x[8];
     if constexpr (kHasM) {
-      float mo[8];
       const float ms = gp(D.m_scale)[mb];
       if (MK == 1) {
         const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
@@ -431,14 +591,12 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 #pragma unroll
         for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }
+      if constexpr (!CM) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) mn[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = mn[k];
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) x[k] = g[k];
+        for (int k = 0; k < 8; ++k) mn[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
+      }
     }
+    const float clip = CM ? gp(sl)[4] : 1.0f;
     // element (row, column): row = e / C, column index b*C + c with b = row / R
     int64_t row = e0 / C;
     int64_t c = e0 - row * C;
@@ -447,7 +605,14 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if (k < cnt) {
-        u[k] = (x[k] * gp(invr)[row]) * gp(invc)[b * C + c];
+        if constexpr (CM) {
+          const float ug = ((g[k] * gp(invr)[row]) * gp(invc)[b * C + c]) / clip;
+          mn[k] = lerp_ref(mo[k], ug, h.w_m);
+          u[k] = (mn[k] * gp(icr)[row]) * gp(icc)[b * C + c];
+        } else {
+          const float x = kHasM ? mn[k] : g[k];
+          u[k] = (x * gp(invr)[row]) * gp(invc)[b * C + c];
+        }
         if (MODE == 1) sq = __builtin_fmaf(u[k], u[k], sq);
       }
       if (++c == C) {
@@ -578,11 +743,27 @@ __global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, 
       *gp(D.fira_prev) = next;
       if (!fin) fs = 0.0f;
     }
-    float denom = 1.0f;
-    if (h.d > 0.0f) denom = fmaxf(nrm / (float)(sqrt((double)D.numel) * (double)h.d), 1.0f);
+    float denom = 1.0f;   // CAME applies its update unclipped (optimizer.py:955)
+    if (h.d > 0.0f && !h.came) denom = fmaxf(nrm / (float)(sqrt((double)D.numel) * (double)h.d), 1.0f);
     const float alpha = gp(sl)[0];
     gp(sl)[1] = alpha / denom;
     gp(sl)[2] = fs;
+  }
+}
+
+// CAME clip factor of U = (g * inv_row) * inv_col (optimizer.py:824-829):
+// clip = max((||U|| / sqrt(n)) / d, 1), from the norm pass's unit partials.
+__global__ __launch_bounds__(256) void k_fclip(const DescF* __restrict__ table, HyperF h) {
+  __shared__ double sd[4];
+  const DescF D = table[blockIdx.x];
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  float* ws = D.ws;
+  double s = 0.0;
+  for (int64_t k = threadIdx.x; k < W.nunit; k += 256) s += (double)gp(ws)[W.npart + k];
+  s = wg_sum_d(s, sd);
+  if (threadIdx.x == 0) {
+    const float rms = sqrtf((float)s) / (float)sqrt((double)D.numel);
+    gp(ws)[W.scal + 4] = fmaxf(rms / h.d, 1.0f);
   }
 }
 
@@ -596,42 +777,74 @@ static int launch_stats(bool psq, const DescF* tab, int ntab, int64_t ntiles, hi
   return check_launch("k_fstats");
 }
 
-template <typename T, int MODE, bool SR>
+template <typename T, int MODE, bool SR, bool CM>
 static int launch_update_m(int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h, hipStream_t st) {
-  switch (mk) {
-    case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
-    case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
-    default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2>), dim3((unsigned)nunits), dim3(256), 0, st, tab, ntab, h); break;
+  const dim3 g((unsigned)nunits), b(256);
+  if constexpr (CM) {
+    if (mk == 1) hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
+    else hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
+  } else {
+    switch (mk) {
+      case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
+      case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
+      default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
+    }
   }
   return check_launch("k_fupdate");
 }
 
-template <typename T, bool SR>
+template <typename T, bool SR, bool CM>
 static int launch_update(int mode, int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h,
                          hipStream_t st) {
   switch (mode) {
-    case 0: return launch_update_m<T, 0, SR>(mk, tab, ntab, nunits, h, st);
-    case 1: return launch_update_m<T, 1, false>(mk, tab, ntab, nunits, h, st);
-    default: return launch_update_m<T, 2, SR>(mk, tab, ntab, nunits, h, st);
+    case 0: return launch_update_m<T, 0, SR, CM>(mk, tab, ntab, nunits, h, st);
+    case 1: return launch_update_m<T, 1, false, CM>(mk, tab, ntab, nunits, h, st);
+    default: return launch_update_m<T, 2, SR, CM>(mk, tab, ntab, nunits, h, st);
   }
 }
 
+template <bool CONF>
+static int launch_finish(int bits, const DescF* tab, int ntab, const HyperF& h, hipStream_t st) {
+  const dim3 g((unsigned)ntab, 2), b(256);
+  switch (bits) {
+    case 8: hipLaunchKernelGGL((k_ffinish<8, CONF>), g, b, 0, st, tab, h); break;
+    case 16: hipLaunchKernelGGL((k_ffinish<16, CONF>), g, b, 0, st, tab, h); break;
+    default: hipLaunchKernelGGL((k_ffinish<0, CONF>), g, b, 0, st, tab, h); break;
+  }
+  return check_launch("k_ffinish");
+}
+
+// Launch sequence of one group step.  Plain factored: stats, finish, then the
+// update (with a norm pass + k_fnorm first when clipping or Fira is on).  CAME:
+// stats, finish, [U norm + k_fclip when d > 0], k_came1, confidence finish,
+// [update norm + k_fnorm with Fira], update.
 template <typename T, bool SR>
-static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int vbits, bool clip,
-                     const HyperF& h, hipStream_t st) {
+static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int vbits, int cbits,
+                     bool clip, const HyperF& h, hipStream_t st) {
   int rc = launch_stats<T>(h.scale_param != 0, tab, ntab, ntiles, st);
   if (rc) return rc;
-  switch (vbits) {
-    case 8: hipLaunchKernelGGL((k_ffinish<8>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
-    case 16: hipLaunchKernelGGL((k_ffinish<16>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
-    default: hipLaunchKernelGGL((k_ffinish<0>), dim3((unsigned)ntab, 2), dim3(256), 0, st, tab, h); break;
+  if ((rc = launch_finish<false>(vbits, tab, ntab, h, st))) return rc;
+  if (h.came) {
+    if (h.d > 0.0f) {
+      if ((rc = launch_update<T, false, false>(1, 0, tab, ntab, nunits, h, st))) return rc;
+      hipLaunchKernelGGL(k_fclip, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
+      if ((rc = check_launch("k_fclip"))) return rc;
+    }
+    if (h.mk == 1) hipLaunchKernelGGL((k_came1<T, 1>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
+    else hipLaunchKernelGGL((k_came1<T, 2>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
+    if ((rc = check_launch("k_came1"))) return rc;
+    if ((rc = launch_finish<true>(cbits, tab, ntab, h, st))) return rc;
+    if (!h.fira) return launch_update<T, SR, true>(0, h.mk, tab, ntab, nunits, h, st);
+    if ((rc = launch_update<T, false, true>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
+    hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
+    if ((rc = check_launch("k_fnorm"))) return rc;
+    return launch_update<T, SR, true>(2, h.mk, tab, ntab, nunits, h, st);
   }
-  if ((rc = check_launch("k_ffinish"))) return rc;
-  if (!clip) return launch_update<T, SR>(0, h.mk, tab, ntab, nunits, h, st);
-  if ((rc = launch_update<T, false>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
+  if (!clip) return launch_update<T, SR, false>(0, h.mk, tab, ntab, nunits, h, st);
+  if ((rc = launch_update<T, false, false>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
   hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
   if ((rc = check_launch("k_fnorm"))) return rc;
-  return launch_update<T, SR>(2, h.mk, tab, ntab, nunits, h, st);
+  return launch_update<T, SR, false>(2, h.mk, tab, ntab, nunits, h, st);
 }
 
 static int mk_code(int mbits, int mmode) {
@@ -657,10 +870,12 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                      float eps2, float lr_val, int scale_parameter, int bias_mode, float bias_factor,
                      float weight_decay, int wd_mode, float d, int fira, float fira_margin,
                      float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
-                     int m_bits, int m_mode, uint64_t sr_step, void* stream) {
+                     int m_bits, int m_mode, uint64_t sr_step, int came, double beta3, float eps_came,
+                     int c_bits, void* stream) {
   if (ntensors <= 0) return 0;
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
+  if (came && c_bits != 0 && c_bits != 8 && c_bits != 16) return set_error(A8_ERR_ARG, "c_bits must be 0, 8 or 16");
   if (block_size <= 0) return set_error(A8_ERR_BLOCK, "block_size must be positive");
   if ((int64_t)sizeof(DescF) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_2d(ntensors)");
@@ -675,6 +890,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   } else {
     lbm = 5;
   }
+  if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum codes (m_q)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
   int64_t tiles = 0, units = 0;
@@ -688,6 +904,10 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                : !(t.row_var && t.col_var))
       return set_error(A8_ERR_ARG, "row/column state missing");
     if (fira && !t.fira_prev_norm) return set_error(A8_ERR_ARG, "fira needs fira_prev_norm");
+    if (came && (c_bits ? !(t.conf_row_q && t.conf_col_q && t.conf_row_scale && t.conf_col_scale &&
+                            t.conf_row_min_log && t.conf_col_min_log)
+                        : !(t.conf_row && t.conf_col)))
+      return set_error(A8_ERR_ARG, "CAME confidence state missing");
     if (!aligned16(t.param) || !aligned16(t.grad) || (has_m && !aligned16(t.m_q)))
       return set_error(A8_ERR_ALIGN, "param/grad/momentum buffers must be 16-byte aligned");
     const int64_t numel = t.batch * t.rows * t.cols;
@@ -696,6 +916,9 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
     D.row_q = t.row_q; D.row_scale = t.row_scale; D.row_min_log = t.row_min_log; D.row_var = t.row_var;
     D.col_q = t.col_q; D.col_scale = t.col_scale; D.col_min_log = t.col_min_log; D.col_var = t.col_var;
+    D.crow_q = t.conf_row_q; D.crow_scale = t.conf_row_scale; D.crow_min_log = t.conf_row_min_log;
+    D.crow_var = t.conf_row; D.ccol_q = t.conf_col_q; D.ccol_scale = t.conf_col_scale;
+    D.ccol_min_log = t.conf_col_min_log; D.ccol_var = t.conf_col;
     D.ws = t.workspace; D.lr = t.lr; D.fira_prev = t.fira_prev_norm; D.has_fira_prev = t.has_fira_prev;
     D.B = t.batch; D.R = t.rows; D.C = t.cols; D.numel = numel;
     D.sr_seed = t.sr_seed;
@@ -720,6 +943,9 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.d = d; h.fira = fira; h.margin = (float)(1.0 + (double)fira_margin);
   h.floor_ = log_floor;
   h.w_m = (float)(1.0 - beta1);
+  h.came = came ? 1 : 0;
+  h.w_c = (float)(1.0 - beta3);
+  h.eps_came = eps_came;
   h.block_size = block_size;
   h.mk = has_m ? mk_code(m_bits, m_mode) : 0;
   h.lbm = lbm;
@@ -727,13 +953,13 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   const bool clip = d > 0.0f || fira;
   const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
   switch (dtype) {
-    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
     case A8_BF16:
-      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, v_bits, clip, h, st)
-                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st)
+                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
     default:
-      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, v_bits, clip, h, st)
-                        : run_group<__half, false>(dt, ntensors, tiles, units, v_bits, clip, h, st);
+      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st)
+                        : run_group<__half, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
   }
 }
 

@@ -56,6 +56,9 @@ __device__ __forceinline__ const DescFull* find_full(const DescFull* tab, int n,
   return tab + lo;
 }
 
+// MODE: 0 single pass, 1 NORM (writes V, sums u^2 or U^2), 2 APPLY (reads V,
+// writes M and p), 3 LAG, 4 MNORM (momentum-only: reads V, clips U by the NORM
+// pass's sum of U^2 in prev_norm and sums M'^2 for Fira; writes nothing).
 template <typename T, int MODE>
 __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const DescFull* __restrict__ table,
                                                          int ntab, HyperFull h) {
@@ -73,7 +76,8 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
     } else {
       float denom = 1.0f;
       if (h.d > 0.0f) {
-        const float nrm = (MODE == 2) ? sqrtf(*D.norm_buf) : *D.prev_norm;
+        const float nrm = (MODE == 2) ? sqrtf(*D.norm_buf)
+                          : (MODE == 4 ? sqrtf(*D.prev_norm) : *D.prev_norm);
         // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
         // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
         if (h.momentum_only && D.m)
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       const int64_t i = e0 + k;
       const float g = scrub(to_f<T>(G[i]));
       float v;
-      if (MODE == 2) {
+      if (MODE == 2 || MODE == 4) {
         v = D.v[i];
       } else {
         v = __builtin_fmaf(h.bv * g, g, D.v[i] * h.v_keep);
@@ -109,7 +113,8 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
           if (MODE == 1 || MODE == 3) sq += ut * ut;
           if (MODE != 1) {
             const float m = lerp_ref(mo, ut_clip != 1.0f ? ut / ut_clip : ut, h.w_m);
-            D.m[i] = m;
+            if (MODE == 4) sq += m * m;
+            else D.m[i] = m;
             u = m;
           } else {
             u = ut;
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
         u = h.adam_denom ? g / (sqrtf(v) + h.eps_d) : g * inv;
         if (MODE == 1 || MODE == 3) sq += u * u;
       }
-      if (MODE != 1) {
+      if (MODE != 1 && MODE != 4) {
         float p = to_f<T>(P[i]);
         if (D.decay) p = p * *D.decay;
         else if (h.has_decay) p = p * h.decay_val;
@@ -137,7 +142,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       }
     }
   }
-  if constexpr (MODE == 1 || MODE == 3) {
+  if constexpr (MODE == 1 || MODE == 3 || MODE == 4) {
     float t = grp_sum(sq, 64);
     if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
   }
@@ -151,6 +156,7 @@ static int launch_full(int mode, const DescFull& one, const DescFull* tab, int n
     case 0: hipLaunchKernelGGL((k_update1d_full<T, 0>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
     case 1: hipLaunchKernelGGL((k_update1d_full<T, 1>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
     case 2: hipLaunchKernelGGL((k_update1d_full<T, 2>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 4: hipLaunchKernelGGL((k_update1d_full<T, 4>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
     default: hipLaunchKernelGGL((k_update1d_full<T, 3>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
   }
   return check_launch("k_update1d_full");
@@ -218,10 +224,12 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
                             int64_t numel, float d, int momentum_only, float alpha_val,
                             float decay_val, int has_decay, void* stream) {
   if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
-  if (!param && mode != 1) return set_error(A8_ERR_ARG, "null param");
+  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
+  if (!param && mode != 1 && mode != 4) return set_error(A8_ERR_ARG, "null param");
   if (!grad || !variance) return set_error(A8_ERR_ARG, "null grad/variance");
-  if ((mode == 1 || mode == 2 || mode == 3) && !norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
-  if (mode == 3 && !prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
+  if (mode != 0 && !norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
+  if ((mode == 3 || mode == 4) && !prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
+  if (mode == 4 && !(m && momentum_only)) return set_error(A8_ERR_ARG, "MNORM needs momentum and momentum_only");
   DescFull D{};
   D.param = param; D.grad = grad; D.v = variance; D.m = m; D.norm_buf = norm_buf;
   D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel;
@@ -240,12 +248,19 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
   if (ntensors <= 0) return 0;
   if ((int64_t)sizeof(DescFull) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_full(ntensors)");
+  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
   std::vector<DescFull> tab((size_t)ntensors);
   int64_t wg = 0;
   const bool has_m = tensors[0].m != nullptr;
+  if (mode == 4 && !(has_m && momentum_only)) return set_error(A8_ERR_ARG, "MNORM needs momentum and momentum_only");
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor_full& t = tensors[i];
     if ((t.m != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+    if (!t.grad || !t.variance) return set_error(A8_ERR_ARG, "null grad/variance");
+    if (!t.param && mode != 1 && mode != 4) return set_error(A8_ERR_ARG, "null param");
+    if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
+    if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
     DescFull& D = tab[(size_t)i];
     D.param = t.param; D.grad = t.grad; D.v = t.variance; D.m = t.m; D.norm_buf = t.norm_buf;
     D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay; D.numel = t.numel;

@@ -84,11 +84,18 @@ __device__ __forceinline__ uint32_t grp_umin(uint32_t x, int G) {
 }
 
 // MK: 0 no momentum, 1 UF8 (specialised), 2 UF4/D8/D4 (codec chosen by h.mk).
+// MODE: 0 single pass, 1 NORM (V codes + v_buf, sum of squares), 2 APPLY (reads
+// v_buf, writes M and p), 3 LAG (single pass clipped by the previous norm),
+// 4 MNORM (momentum-only: reads v_buf, clips U by the NORM pass's sum of U^2 in
+// prev_norm, and sums M'^2 for Fira; writes no state).
 template <typename T, int VB, int MODE, bool SR, int MK>
 __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* __restrict__ table,
                                                    int ntab, Hyper1D h) {
   extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | [16] cross-wave partials
   constexpr bool kHasM = MK != 0;
+  constexpr bool kVbuf = MODE == 2 || MODE == 4;     // V comes from the NORM pass
+  constexpr bool kSq = MODE == 1 || MODE == 3 || MODE == 4;
+  constexpr bool kWrite = MODE == 0 || MODE == 2 || MODE == 3;   // p and M
   const Desc1D D = table ? *find_desc(table, ntab, (int64_t)blockIdx.x) : one;
   const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
@@ -111,10 +118,10 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   const int vloc = lane >> (lbv - 3);
   const int mk = (MK == 1) ? 1 : h.mk;
   float* tabs = s_lds;
-  float* xw = s_lds + ((VB == 8 && MODE != 2) ? nv_wg * 256 : 0);  // 4 waves x 4 | 4 fits x 4
+  float* xw = s_lds + ((VB == 8 && !kVbuf) ? nv_wg * 256 : 0);  // 4 waves x 4 | 4 fits x 4
 
   // ---- AL8 decode tables for this workgroup's V blocks
-  if constexpr (VB == 8 && MODE != 2) {
+  if constexpr (VB == 8 && !kVbuf) {
     const int64_t vb0 = wl * nv_wg;
     for (int k = lane; k < nv_wg * 256; k += kLanes) {
       const int64_t b = vb0 + (k >> 8);
@@ -138,7 +145,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     } else {
       float denom = 1.0f;
       if (h.d > 0.0f) {
-        const float nrm = (MODE == 2) ? sqrtf(*gp(D.norm_buf)) : *gp(D.prev_norm);
+        const float nrm = (MODE == 2) ? sqrtf(*gp(D.norm_buf))
+                          : (MODE == 4 ? sqrtf(*gp(D.prev_norm)) : *gp(D.prev_norm));
         // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
         // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
         if (h.momentum_only && kHasM)
@@ -168,7 +176,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     }
 
     // ---- V: decode + EMA (APPLY reads the exact V of the NORM pass)
-    if constexpr (MODE == 2) {
+    if constexpr (kVbuf) {
 #pragma unroll
       for (int k = 0; k < kEPT; ++k) vn[k] = (k < cnt) ? gp(D.v_buf)[e0 + k] : 0.0f;
     } else {
@@ -278,7 +286,10 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       }
       if (mom) {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) uu[k] = mn[k];
+        for (int k = 0; k < kEPT; ++k) {
+          uu[k] = mn[k];
+          if (MODE == 4) sq = __builtin_fmaf(mn[k], mn[k], sq);
+        }
       } else {
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
@@ -299,8 +310,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
       for (int k = 0; k < kEPT; ++k) {
         if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; uu[k] = 0.0f; }
-        const float ut = mom ? g[k] * inv[k] : uu[k];
-        if ((MODE == 1 || MODE == 3) && k < cnt) sq = __builtin_fmaf(ut, ut, sq);
+        const float ut = (MODE == 4) ? mn[k] : (mom ? g[k] * inv[k] : uu[k]);
+        if (kSq && k < cnt) sq = __builtin_fmaf(ut, ut, sq);
       }
     }
     if constexpr (MODE == 1) {
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     }
 
     // ---- parameter write
-    if constexpr (MODE != 1) {
+    if constexpr (kWrite) {
       T* P = reinterpret_cast<T*>(D.param);
       const bool has_dec = D.decay || h.has_decay;
       const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
@@ -353,7 +364,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   const int wave = lane >> 6;
 
   // ---- V refit + codes
-  if constexpr (MODE != 2) {
+  if constexpr (!kVbuf) {
     float bmax = grp_max(vmax, VL < 64 ? VL : 64);
     uint32_t bkey = grp_umin(vkey, VL < 64 ? VL : 64);
     const float lm2 = VB == 8 ? 254.0f : 65534.0f;
@@ -414,7 +425,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   }
 
   // ---- M refit + codes
-  if constexpr (MODE != 1 && kHasM) {
+  if constexpr (kWrite && kHasM) {
     float bam = grp_max(amax, ML < 64 ? ML : 64);
     if (ML > 64) {
       __syncthreads();
@@ -461,8 +472,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     }
   }
 
-  // ---- sum of squares for NORM / LAG
-  if constexpr (MODE == 1 || MODE == 3) {
+  // ---- sum of squares for NORM / LAG / MNORM
+  if constexpr (kSq) {
     const float t = grp_sum(sq, 64);
     if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
   }
@@ -478,7 +489,8 @@ template <typename T, int VB, int MODE, bool SR, int MK>
 static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
                     hipStream_t st) {
   const int nv_wg = kWGElems / h.block_size;
-  size_t lds = ((VB == 8 && MODE != 2) ? (size_t)nv_wg * 256 : 0) * sizeof(float) + 48 * sizeof(float);
+  size_t lds = ((VB == 8 && MODE != 2 && MODE != 4) ? (size_t)nv_wg * 256 : 0) * sizeof(float) +
+               48 * sizeof(float);
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
   hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,
@@ -490,6 +502,14 @@ template <typename T, bool SR, int MK>
 static int launch_mode(int vbits, int mode, const Desc1D& one, const Desc1D* table, int ntab,
                        int64_t nwg, const Hyper1D& h, hipStream_t st) {
 #define A8_L(VB, MO) return launch_t<T, VB, MO, SR, MK>(one, table, ntab, nwg, h, st)
+  if (mode == 4) {
+    if constexpr (MK == 0 || SR) {
+      return set_error(A8_ERR_ARG, "MNORM needs momentum codes");
+    } else {
+      if (vbits == 8) A8_L(8, 4);
+      A8_L(16, 4);
+    }
+  }
   if (vbits == 8) {
     switch (mode) { case 0: A8_L(8, 0); case 1: A8_L(8, 1); case 2: A8_L(8, 2); default: A8_L(8, 3); }
   } else {
@@ -510,7 +530,7 @@ static int launch_dispatch(int vbits, int mode, const Desc1D& one, const Desc1D*
 
 static int launch_any(int dtype, int sr, int vbits, int mode, const Desc1D& one, const Desc1D* table,
                       int ntab, int64_t nwg, const Hyper1D& h, hipStream_t st) {
-  if (mode == 1 && sr) sr = 0;
+  if ((mode == 1 || mode == 4) && sr) sr = 0;
   switch (dtype) {
     case A8_F32: return launch_dispatch<float, false>(vbits, mode, one, table, ntab, nwg, h, st);
     case A8_BF16:
@@ -565,9 +585,13 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   const bool has_m = m_q != nullptr;
   int rc = check_common(dtype, numel, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
   if (rc) return rc;
-  if (!v_q || !v_scale || !v_min_log || !grad) return set_error(A8_ERR_ARG, "null state pointer");
-  if (mode != 1 && !param) return set_error(A8_ERR_ARG, "null param");
-  if ((mode == 1 || mode == 2) && !v_buf) return set_error(A8_ERR_ARG, "NORM/APPLY need v_buf");
+  if (!v_q || !v_scale || !v_min_log || !grad || (has_m && !m_scale))
+    return set_error(A8_ERR_ARG, "null state pointer");
+  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
+  if (mode != 1 && mode != 4 && !param) return set_error(A8_ERR_ARG, "null param");
+  if ((mode == 1 || mode == 2 || mode == 4) && !v_buf) return set_error(A8_ERR_ARG, "NORM/APPLY/MNORM need v_buf");
+  if (mode == 4 && !(norm_buf && prev_norm && has_m && momentum_only))
+    return set_error(A8_ERR_ARG, "MNORM needs momentum codes, momentum_only, norm_buf and prev_norm");
   if ((mode == 1 || mode == 3) && !norm_buf) return set_error(A8_ERR_ARG, "NORM/LAG need norm_buf");
   if (mode == 2 && !norm_buf) return set_error(A8_ERR_ARG, "APPLY needs norm_buf");
   if (mode == 3 && !prev_norm) return set_error(A8_ERR_ARG, "LAG needs prev_norm");
@@ -625,11 +649,21 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
   if (rc) return rc;
   if ((int64_t)sizeof(Desc1D) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_1d(ntensors)");
+  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
+  if (mode == 4 && !momentum_only) return set_error(A8_ERR_ARG, "MNORM needs momentum_only");
   std::vector<Desc1D> tab((size_t)ntensors);
   int64_t wg = 0;
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor1d& t = tensors[i];
     if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if (!t.grad || !t.v_q || !t.v_scale || !t.v_min_log || (has_m && !t.m_scale))
+      return set_error(A8_ERR_ARG, "null state pointer");
+    if (mode != 1 && mode != 4 && !t.param) return set_error(A8_ERR_ARG, "null param");
+    if ((mode == 1 || mode == 2 || mode == 4) && !t.v_buf)
+      return set_error(A8_ERR_ARG, "NORM/APPLY/MNORM need v_buf");
+    if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "NORM/APPLY/LAG/MNORM need norm_buf");
+    if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "LAG/MNORM need prev_norm");
+    if (mode == 4 && !has_m) return set_error(A8_ERR_ARG, "MNORM needs momentum codes");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.v_q) || (has_m && !aligned16(t.m_q)))
       return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
     if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");

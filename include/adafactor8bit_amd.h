@@ -43,6 +43,12 @@ extern "C" {
 #define A8_MODE_NORM 1
 #define A8_MODE_APPLY 2
 #define A8_MODE_LAG 3
+/* momentum-only norm of the new momentum M' for Fira (no counterpart in the
+ * reference's kernels, whose CUDA path applies Fira to ||U||; its PyTorch path,
+ * optimizer.py:890-896 with _apply_update_pytorch 866-875, applies it to ||M'||):
+ * reads v_buf, clips U by sqrt(*prev_norm) (the NORM pass's sum of U^2) and
+ * accumulates sum(M'^2) into norm_buf; writes no state. */
+#define A8_MODE_MNORM 4
 
 const char* a8_last_error(void);
 const char* a8_version(void);
@@ -173,6 +179,14 @@ typedef struct a8_tensor2d {
   float* col_scale;
   float* col_min_log;
   float* col_var;
+  void* conf_row_q;        /* CAME confidence state, as row/col V (codes or fp32 conf_row/conf_col) */
+  float* conf_row_scale;
+  float* conf_row_min_log;
+  float* conf_row;
+  void* conf_col_q;
+  float* conf_col_scale;
+  float* conf_col_min_log;
+  float* conf_col;
   float* workspace;        /* a8_factored_workspace_floats(batch, rows, cols) floats */
   const float* lr;         /* device learning rate, or NULL for lr_val */
   float* fira_prev_norm;   /* 0-dim fp32 state when fira is on; written every step */
@@ -197,13 +211,26 @@ typedef struct a8_tensor2d {
  * wd_mode: 0 none, 1 decay uses alpha, 2 decay uses lr.
  * v_bits: 8 / 16 (codes) or 0 (fp32 row_var/col_var).  block_size: V block
  * (any positive size).  m_block_size: power of two in [32, 2048].
- * table_dev: device buffer of a8_table_bytes_2d(ntensors) bytes (uploaded when upload != 0). */
+ * table_dev: device buffer of a8_table_bytes_2d(ntensors) bytes (uploaded when upload != 0).
+ *
+ * came != 0 selects CAME (beta3; _fallback_2d_update optimizer.py:929-956, kernels
+ * compute_ut_rms kernels.cu:1962-1984, fused_came_pass1 2003-2094, fused_came_pass2
+ * 2097-2221, called at optimizer.py:2265-2340).  Momentum codes are required.  After the
+ * row/column V step:
+ *   U = ((g * inv_row) * inv_col) / clip, clip = max((||U0|| / sqrt(n)) / d, 1) (1 when d == 0);
+ *   M' = lerp(M, U, 1 - beta1), res = (U - M')^2 + eps_came;
+ *   conf_row/conf_col: lerp(conf, mean of res over columns/rows, 1 - beta3), re-encoded
+ *   with c_bits (8 / 16 codes, 0 = fp32 state);
+ *   u = (M' * inv_conf_row) * inv_conf_col with inv_conf_row = 1/sqrt(conf_row / r_c),
+ *   r_c = mean_r(conf_row) clamped at eps1; Fira (when on) scales u; no RMS denominator;
+ *   p <- p * decay - alpha * u, M' re-encoded. */
 int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int ntensors,
                      void* table_dev, int64_t table_bytes, int upload, double beta_val, float eps1,
                      float eps2, float lr_val, int scale_parameter, int bias_mode, float bias_factor,
                      float weight_decay, int wd_mode, float d, int fira, float fira_margin,
                      float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
-                     int m_bits, int m_mode, uint64_t sr_step, void* stream);
+                     int m_bits, int m_mode, uint64_t sr_step, int came, double beta3, float eps_came,
+                     int c_bits, void* stream);
 int64_t a8_factored_workspace_floats(int64_t batch, int64_t rows, int64_t cols);
 int64_t a8_table_bytes_2d(int ntensors);
 

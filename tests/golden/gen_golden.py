@@ -62,6 +62,9 @@ CONFIGS = [
     ("rmsprop_al8", dict(RMSPROP, lr=1e-4), P_SMALL, "normal_zeros", 4, (1, 4)),
     ("adafactor_mom1d", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False), P_SMALL,
      "student_t", 4, (1, 4)),
+    ("adafactor_mom1d_fira", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False,
+                                  enable_fira_for_adafactor=True, fira_margin=0.01), P_SMALL,
+     "logscale", 5, (1, 5)),
     ("adafactor_factored_al8", dict(ADAFACTOR, lr=1e-3, block_size=256), P_FACT, "student_t",
      10, (1, 2, 10)),
     ("adafactor_factored_emb", dict(ADAFACTOR, lr=1e-3, block_size=256), P_EMB, "sparse_rows",

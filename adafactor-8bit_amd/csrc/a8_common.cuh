@@ -29,6 +29,13 @@ __device__ __forceinline__ A8_G T* gp(T* p) { return (A8_G T*)p; }
 template <typename T>
 __device__ __forceinline__ const A8_G T* gp(const T* p) { return (const A8_G T*)p; }
 
+// Constant-address-space (address space 4) view for data that is uniform across
+// a workgroup and not written during the launch: loads go through the scalar
+// cache into SGPRs.
+#define A8_C __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const A8_C T* cp(const T* p) { return (const A8_C T*)p; }
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -65,13 +65,26 @@ constexpr int kLanes = 256;
 constexpr int kEPT = 8;
 constexpr int kWGElems = kLanes * kEPT;
 
-__device__ __forceinline__ const Desc1D* find_desc(const Desc1D* tab, int n, int64_t wg) {
+// Tensor table in device memory: ntab descriptors, then one int32 first
+// workgroup per tensor.  It is uniform per workgroup and read-only during the
+// launch, so it is read through the scalar cache (constant address space): the
+// search probes a compact 4-byte array and the descriptor arrives in SGPRs.
+__device__ __forceinline__ Desc1D load_desc(const Desc1D* tab, int n, int wg) {
+  const A8_C Desc1D* ct = cp(tab);
+  const A8_C int32_t* wb = (const A8_C int32_t*)(ct + n);
   int lo = 0, hi = n - 1;
   while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    const int mid = (lo + hi + 1) >> 1;
+    if (wb[mid] <= wg) lo = mid; else hi = mid - 1;
   }
-  return tab + lo;
+  static_assert(sizeof(Desc1D) % 8 == 0, "descriptor is loaded as 64-bit words");
+  const A8_C uint64_t* w = (const A8_C uint64_t*)(ct + lo);
+  uint64_t buf[sizeof(Desc1D) / 8];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(Desc1D) / 8); ++i) buf[i] = w[i];
+  Desc1D d;
+  __builtin_memcpy(&d, buf, sizeof(Desc1D));
+  return d;
 }
 
 // Integer view of a non-negative float minus one: for v >= 0 the unsigned
@@ -96,7 +109,9 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   constexpr bool kVbuf = MODE == 2 || MODE == 4;     // V comes from the NORM pass
   constexpr bool kSq = MODE == 1 || MODE == 3 || MODE == 4;
   constexpr bool kWrite = MODE == 0 || MODE == 2 || MODE == 3;   // p and M
-  const Desc1D D = table ? *find_desc(table, ntab, (int64_t)blockIdx.x) : one;
+  Desc1D D;
+  if (table != nullptr) D = load_desc(table, ntab, (int)blockIdx.x);
+  else D = one;
   const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
   const int64_t n = D.numel;
@@ -120,18 +135,55 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   float* tabs = s_lds;
   float* xw = s_lds + ((VB == 8 && !kVbuf) ? nv_wg * 256 : 0);  // 4 waves x 4 | 4 fits x 4
 
+  // ---- stream loads, issued before the decode table and its barrier so that
+  // their latency overlaps the table build
+  float g[kEPT], pin[kEPT];
+  u32x2 vq8 = {0u, 0u}, mq8 = {0u, 0u};
+  u32x4 vq16 = {0u, 0u, 0u, 0u};
+  uint32_t mq4 = 0u;
+  float ms = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k) { g[k] = 0.0f; pin[k] = 0.0f; }
+  if (v_ok) {
+    load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
+    if constexpr (!kVbuf) {
+      if constexpr (VB == 8) vq8 = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
+      else vq16 = *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0));
+    }
+    if (m_ok) {
+      ms = gp(D.m_scale)[mb];
+      if (MK == 1 || !(mk == 2 || mk == 4)) mq8 = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+      else mq4 = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
+    }
+    if constexpr (kWrite && !SR) load8<T>(reinterpret_cast<const T*>(D.param), e0, n, pin);
+  }
+
   // ---- AL8 decode tables for this workgroup's V blocks
   if constexpr (VB == 8 && !kVbuf) {
     const int64_t vb0 = wl * nv_wg;
-    for (int k = lane; k < nv_wg * 256; k += kLanes) {
-      const int64_t b = vb0 + (k >> 8);
-      const int c = k & 255;
+    if (nv_wg == 1) {
+      // one block per workgroup: its scale and min_log are uniform, read
+      // through the scalar cache (each block's metadata is read here once and
+      // rewritten at the end of this workgroup only)
+      const int c = lane;
       float val = 0.0f;
-      if (b < nvb && c != 0) {
-        const float sc = gp(D.v_scale)[b], lm = gp(D.v_min_log)[b];
+      if (vb0 < nvb && c != 0) {
+        const float sc = cp(D.v_scale)[vb0];
+        const float lm = cp(D.v_min_log)[vb0];
         val = exp2_exact(((float)(c - 1) * sc) / 254.0f + lm);
       }
-      tabs[k] = val;
+      tabs[c] = val;
+    } else {
+      for (int k = lane; k < nv_wg * 256; k += kLanes) {
+        const int64_t b = vb0 + (k >> 8);
+        const int c = k & 255;
+        float val = 0.0f;
+        if (b < nvb && c != 0) {
+          const float sc = gp(D.v_scale)[b], lm = gp(D.v_min_log)[b];
+          val = exp2_exact(((float)(c - 1) * sc) / 254.0f + lm);
+        }
+        tabs[k] = val;
+      }
     }
     __syncthreads();
   }
@@ -165,8 +217,6 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
   uint32_t vkey = 0xFFFFFFFFu;
 
   if (v_ok) {
-    float g[kEPT];
-    load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
     {  // non-finite gradients become 0 (kernels.cu:43-46); one test per lane
       float t = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
       if (!__builtin_isfinite(t)) {
@@ -182,13 +232,13 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     } else {
       float vo[kEPT];
       if constexpr (VB == 8) {
-        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
+        const u32x2 qv = vq8;
         const float* tb = tabs + vloc * 256;
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) vo[k] = tb[((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu];
       } else {
         const float s_old = gp(D.v_scale)[vb], lm_old = gp(D.v_min_log)[vb];
-        const u32x4 qv = *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0));
+        const u32x4 qv = vq16;
         const uint32_t w4[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
@@ -219,22 +269,21 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) mo[k] = 0.0f;
     if (m_ok) {
-      const float ms = gp(D.m_scale)[mb];
       if (MK == 1) {
-        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+        const u32x2 q = mq8;
         const float s128 = ms / 128.0f, b128 = -128.0f * s128;   // (q-128)*s128 == fma(q, s128, -128*s128)
 #pragma unroll
         for (int k = 0; k < kEPT; ++k)
           mo[k] = __builtin_fmaf((float)(((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu), s128, b128);
       } else if (mk == 2 || mk == 4) {
-        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
+        const uint32_t qw = mq4;
 #pragma unroll
         for (int k = 0; k < kEPT; ++k) {
           const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
           mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
         }
       } else {
-        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+        const u32x2 q = mq8;
 #pragma unroll
         for (int k = 0; k < kEPT; ++k)
           mo[k] = m_decode(mk, ((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu, ms);
@@ -344,7 +393,8 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
         }
       } else {
         float p[kEPT];
-        load8<T>(P, e0, n, p);
+#pragma unroll
+        for (int k = 0; k < kEPT; ++k) p[k] = pin[k];
         if (has_dec) {  // decoupled weight decay: p*decay rounded, then the update (optimizer.py:2039)
 #pragma unroll
           for (int k = 0; k < kEPT; ++k) p[k] = p[k] * dec;
@@ -647,11 +697,12 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
   const bool has_m = tensors[0].m_q != nullptr;
   int rc = check_common(dtype, 0, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
   if (rc) return rc;
-  if ((int64_t)sizeof(Desc1D) * ntensors > table_bytes)
+  if (a8_table_bytes_1d(ntensors) > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_1d(ntensors)");
   if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
   if (mode == 4 && !momentum_only) return set_error(A8_ERR_ARG, "MNORM needs momentum_only");
   std::vector<Desc1D> tab((size_t)ntensors);
+  std::vector<int32_t> first((size_t)ntensors);
   int64_t wg = 0;
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor1d& t = tensors[i];
@@ -672,12 +723,19 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
     D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
     D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
     D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed;
+    first[(size_t)i] = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
     wg += (t.numel + kWGElems - 1) / kWGElems;
   }
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
   hipStream_t st = (hipStream_t)stream;
-  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(Desc1D) * (size_t)ntensors,
-                               hipMemcpyHostToDevice, st) != hipSuccess)
-    return set_error(A8_ERR_HIP, "table upload failed");
+  if (upload) {
+    // one staging copy: descriptors followed by the first-workgroup array
+    std::vector<char> blob((size_t)a8_table_bytes_1d(ntensors));
+    std::memcpy(blob.data(), tab.data(), sizeof(Desc1D) * (size_t)ntensors);
+    std::memcpy(blob.data() + sizeof(Desc1D) * (size_t)ntensors, first.data(), sizeof(int32_t) * (size_t)ntensors);
+    if (hipMemcpyAsync(table_dev, blob.data(), blob.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "table upload failed");
+  }
   Hyper1D h{};
   h.beta1 = (float)beta1;
   h.w_m = (float)(1.0 - beta1);
@@ -695,7 +753,9 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                     ntensors, wg, h, st);
 }
 
-int64_t a8_table_bytes_1d(int ntensors) { return (int64_t)sizeof(Desc1D) * (int64_t)ntensors; }
+int64_t a8_table_bytes_1d(int ntensors) {
+  return ((int64_t)sizeof(Desc1D) + (int64_t)sizeof(int32_t)) * (int64_t)ntensors;
+}
 
 int a8_set_qmap(const float* qmap8_host, const float* qmap4_host) {
   if (!qmap8_host || !qmap4_host) return set_error(A8_ERR_ARG, "null codebook");

@@ -285,6 +285,60 @@ __device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const flo
   }
 }
 
+// Load / store 4 consecutive elements (one 16-byte fp32 or 8-byte 16-bit
+// access per lane when fully in range).
+template <typename T>
+__device__ __forceinline__ void load4n(const T* base, int64_t i0, int64_t n, float* out) {
+  if (i0 + 4 <= n) {
+    if constexpr (sizeof(T) == 4) {
+      const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(base + i0)));
+      out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    } else {
+      const u32x2 a = __builtin_nontemporal_load(gp(reinterpret_cast<const u32x2*>(base + i0)));
+      const T* h = reinterpret_cast<const T*>(&a);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[k] = to_f<T>(h[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = (i0 + k < n) ? ld1<T>(base, i0 + k) : 0.0f;
+  }
+}
+
+// Unchecked form of load4n for a window known to lie inside the tensor.
+template <typename T>
+__device__ __forceinline__ void load4v(const T* base, int64_t i0, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(base + i0)));
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  } else {
+    const u32x2 a = __builtin_nontemporal_load(gp(reinterpret_cast<const u32x2*>(base + i0)));
+    const T* h = reinterpret_cast<const T*>(&a);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = to_f<T>(h[k]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4n(T* base, int64_t i0, int64_t n, const float* v) {
+  if (i0 + 4 <= n) {
+    if constexpr (sizeof(T) == 4) {
+      const f32x4 a = {v[0], v[1], v[2], v[3]};
+      __builtin_nontemporal_store(a, gp(reinterpret_cast<f32x4*>(base + i0)));
+    } else {
+      u32x2 a;
+      T* h = reinterpret_cast<T*>(&a);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) h[k] = from_f<T>(v[k]);
+      __builtin_nontemporal_store(a, gp(reinterpret_cast<u32x2*>(base + i0)));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (i0 + k < n) st1<T>(base, i0 + k, v[k]);
+  }
+}
+
 // ---------------------------------------------------------------- reductions
 // Butterfly reductions over aligned groups of G lanes (G power of two <= 64).
 __device__ __forceinline__ float grp_max(float x, int G) {

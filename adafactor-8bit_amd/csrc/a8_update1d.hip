@@ -7,13 +7,15 @@
 // kernels.cu:998-1098 without M) and, for the numbers it produces, the CPU
 // path of _update_param_8bit (optimizer.py:2115-2123, 886-917).
 //
-// Layout: a 256-lane workgroup owns 2048 consecutive elements, 8 per lane held
-// in VGPRs (two 16-byte loads of fp32 p/g, one 8-byte load of each code
-// stream).  A V block of B_V elements is B_V/8 consecutive lanes and an M block
-// of B_M elements is B_M/8 lanes, so both block reductions are butterfly
-// shuffles inside a wave, plus one LDS exchange when B_V/8 > 64.  AL8 decode is
-// a per-block 256-entry table in LDS (one exp2 per code instead of one per
-// element).  A tensor table lets one launch cover many tensors.
+// Layout: a 256-lane workgroup owns 2048 consecutive elements as two halves of
+// 1024; lane t holds elements 4t..4t+3 of each half in VGPRs, so every
+// wave-wide access (16 bytes of fp32 p/g, 4 bytes of each code stream per lane)
+// covers one contiguous span.  A V block of B_V <= 1024 elements is B_V/4
+// consecutive lanes of a half and an M block B_M/4 lanes, so block reductions
+// are butterfly shuffles inside a wave, plus one LDS exchange when a block
+// spans several waves.  AL8 decode is a per-block 256-entry table in LDS (one
+// exp2 per code instead of one per element).  A tensor table lets one launch
+// cover many tensors.
 #include "a8_common.cuh"
 #include "a8_mcodec.cuh"
 #include "a8_abi_impl.h"
@@ -64,6 +66,7 @@ struct Hyper1D {
 constexpr int kLanes = 256;
 constexpr int kEPT = 8;
 constexpr int kWGElems = kLanes * kEPT;
+constexpr int kHalf = kWGElems / 2;
 
 // Tensor table in device memory: ntab descriptors, then one int32 first
 // workgroup per tensor.  It is uniform per workgroup and read-only during the
@@ -101,66 +104,104 @@ __device__ __forceinline__ uint32_t grp_umin(uint32_t x, int G) {
 // v_buf, writes M and p), 3 LAG (single pass clipped by the previous norm),
 // 4 MNORM (momentum-only: reads v_buf, clips U by the NORM pass's sum of U^2 in
 // prev_norm, and sums M'^2 for Fira; writes no state).
-template <typename T, int VB, int MODE, bool SR, int MK>
-__global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* __restrict__ table,
-                                                   int ntab, Hyper1D h) {
-  extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | [16] cross-wave partials
+//
+// Lane t of a workgroup holds elements j*1024 + 4t + i of its 2048-element
+// unit (half j = 0, 1; i = 0..3), at register index k = 4j + i: every
+// wave-wide 16-byte access covers 1 KB of contiguous memory.  A V block of
+// B_V <= 1024 elements is B_V/4 consecutive lanes in each half (so a lane holds
+// two blocks, one per half); B_V = 2048 is the whole workgroup.  M blocks map
+// the same way with B_M.
+//
+// FULL: the unit lies entirely inside the tensor (every unit but a tensor's
+// last): no lane is partial or outside the tensor's blocks, so every load is
+// unconditional; the workgroup chooses its body once, and the two bodies never
+// rejoin.
+template <typename T, int VB, int MODE, bool SR, int MK, bool FULL>
+__device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int64_t wl, float* s_lds) {
   constexpr bool kHasM = MK != 0;
   constexpr bool kVbuf = MODE == 2 || MODE == 4;     // V comes from the NORM pass
   constexpr bool kSq = MODE == 1 || MODE == 3 || MODE == 4;
   constexpr bool kWrite = MODE == 0 || MODE == 2 || MODE == 3;   // p and M
-  Desc1D D;
-  if (table != nullptr) D = load_desc(table, ntab, (int)blockIdx.x);
-  else D = one;
-  const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
+  const int wave = lane >> 6;
   const int64_t n = D.numel;
   // block sizes are powers of two: all block arithmetic is shifts and masks
   const int lbv = h.lbv, lbm = h.lbm;
   const int BV = 1 << lbv, BM = 1 << lbm;
-  const int VL = BV >> 3;                        // lanes per V block (16..256)
-  const int ML = BM >> 3;                        // lanes per M block (4..256)
+  const bool vwhole = BV == kWGElems;            // one V block spans the workgroup
+  const bool mwhole = BM == kWGElems;
+  const int VLh = vwhole ? kLanes : (BV >> 2);   // lanes per V block in one half
+  const int MLh = mwhole ? kLanes : (BM >> 2);   // lanes per M block in one half
   const int nv_wg = kWGElems >> lbv;             // V blocks per workgroup
-  const int64_t e0 = wl * kWGElems + (int64_t)lane * kEPT;
+  // Addresses are a uniform (SGPR) base of this unit plus a 32-bit lane offset,
+  // so the loads and stores use SGPR-based addressing and no 64-bit VGPR pairs.
+  const int64_t ub = wl * kWGElems;              // first element of the unit
   const int64_t nvb = (n + BV - 1) >> lbv;
   const int64_t nmb = (n + BM - 1) >> lbm;
-  const int64_t vb = e0 >> lbv;
-  const int64_t mb = e0 >> lbm;
-  const bool v_ok = vb < nvb;
-  const bool m_ok = kHasM && (mb < nmb);
-  const int64_t rem = n - e0;
-  const int cnt = rem <= 0 ? 0 : (rem >= kEPT ? kEPT : (int)rem);   // valid elements of this lane
-  const int vloc = lane >> (lbv - 3);
+  const int64_t vb_u = ub >> lbv, mb_u = ub >> lbm;
+  const int64_t rem64 = n - ub;
+  const uint32_t nrem = FULL ? (uint32_t)kWGElems
+                             : (rem64 <= 0 ? 0u : (rem64 >= kWGElems ? (uint32_t)kWGElems : (uint32_t)rem64));
+  const int64_t nvr = nvb - vb_u, nmr = nmb - mb_u;   // blocks from this unit on
+  uint32_t lo[2];
+  int cnth[2], vloc[2], mloc[2];
+  bool vok[2], mok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    lo[j] = (uint32_t)(j * kHalf + 4 * lane);
+    vloc[j] = (int)(lo[j] >> lbv);
+    mloc[j] = (int)(lo[j] >> lbm);
+    cnth[j] = FULL ? 4 : (lo[j] >= nrem ? 0 : ((nrem - lo[j]) >= 4u ? 4 : (int)(nrem - lo[j])));
+    vok[j] = FULL || vloc[j] < nvr;
+    mok[j] = kHasM && (FULL || mloc[j] < nmr);
+  }
+  const T* Gu = reinterpret_cast<const T*>(D.grad) + ub;
+  T* Pu = reinterpret_cast<T*>(D.param) + ub;
+  uint8_t* V8u = reinterpret_cast<uint8_t*>(D.v_q) + ub;
+  uint16_t* V16u = reinterpret_cast<uint16_t*>(D.v_q) + ub;
+  uint8_t* Mu8 = kHasM ? D.m_q + ub : nullptr;
+  uint8_t* Mu4 = kHasM ? D.m_q + (ub >> 1) : nullptr;
+  float* MSu = kHasM ? D.m_scale + mb_u : nullptr;
+  float* VSu = D.v_scale + vb_u;
+  float* VLu = D.v_min_log + vb_u;
+  float* VBu = (kVbuf || MODE == 1) ? D.v_buf + ub : nullptr;
   const int mk = (MK == 1) ? 1 : h.mk;
   float* tabs = s_lds;
-  float* xw = s_lds + ((VB == 8 && !kVbuf) ? nv_wg * 256 : 0);  // 4 waves x 4 | 4 fits x 4
+  float* xw = s_lds + ((VB == 8 && !kVbuf) ? nv_wg * 256 : 0);  // [0,16) partials, [16,32) fit
 
   // ---- stream loads, issued before the decode table and its barrier so that
   // their latency overlaps the table build
   float g[kEPT], pin[kEPT];
-  u32x2 vq8 = {0u, 0u}, mq8 = {0u, 0u};
-  u32x4 vq16 = {0u, 0u, 0u, 0u};
-  uint32_t mq4 = 0u;
-  float ms = 0.0f;
+  uint32_t vq8[2] = {0u, 0u}, mq8[2] = {0u, 0u}, mq4[2] = {0u, 0u};
+  u32x2 vq16[2] = {{0u, 0u}, {0u, 0u}};
+  float ms[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int k = 0; k < kEPT; ++k) { g[k] = 0.0f; pin[k] = 0.0f; }
-  if (v_ok) {
-    load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
-    if constexpr (!kVbuf) {
-      if constexpr (VB == 8) vq8 = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
-      else vq16 = *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(D.v_q) + e0));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (vok[j]) {
+      if constexpr (!kVbuf) {
+        if constexpr (VB == 8) vq8[j] = *gp(reinterpret_cast<const uint32_t*>(V8u + lo[j]));
+        else vq16[j] = *gp(reinterpret_cast<const u32x2*>(V16u + lo[j]));
+      }
+      if (mok[j]) {
+        ms[j] = gp(MSu)[mloc[j]];
+        if (MK == 1 || !(mk == 2 || mk == 4)) mq8[j] = *gp(reinterpret_cast<const uint32_t*>(Mu8 + lo[j]));
+        else mq4[j] = *gp(reinterpret_cast<const uint16_t*>(Mu4 + (lo[j] >> 1)));
+      }
+      if constexpr (FULL) {
+        load4v<T>(Gu, lo[j], g + 4 * j);
+        if constexpr (kWrite && !SR) load4v<T>(Pu, lo[j], pin + 4 * j);
+      } else {
+        load4n<T>(Gu, lo[j], nrem, g + 4 * j);
+        if constexpr (kWrite && !SR) load4n<T>(Pu, lo[j], nrem, pin + 4 * j);
+      }
     }
-    if (m_ok) {
-      ms = gp(D.m_scale)[mb];
-      if (MK == 1 || !(mk == 2 || mk == 4)) mq8 = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
-      else mq4 = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
-    }
-    if constexpr (kWrite && !SR) load8<T>(reinterpret_cast<const T*>(D.param), e0, n, pin);
   }
 
   // ---- AL8 decode tables for this workgroup's V blocks
   if constexpr (VB == 8 && !kVbuf) {
-    const int64_t vb0 = wl * nv_wg;
+    const int64_t vb0 = vb_u;
     if (nv_wg == 1) {
       // one block per workgroup: its scale and min_log are uniform, read
       // through the scalar cache (each block's metadata is read here once and
@@ -213,10 +254,14 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
 
   float vn[kEPT], mn[kEPT];
   float sq = 0.0f;
-  uint32_t vmaxb = 0u, amaxb = 0u;   // max of non-negative floats as integer bit patterns
-  uint32_t vkey = 0xFFFFFFFFu;
+  // per-half block statistics: max of non-negative floats as integer bit
+  // patterns, and the non-zero minimum key
+  uint32_t vmaxb[2] = {0u, 0u}, amaxb[2] = {0u, 0u};
+  uint32_t vkey[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k) { vn[k] = 0.0f; mn[k] = 0.0f; }
 
-  if (v_ok) {
+  if (vok[0]) {   // vok[1] implies vok[0]
     {  // non-finite gradients become 0 (kernels.cu:43-46); one test per lane
       float t = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
       if (!__builtin_isfinite(t)) {
@@ -228,22 +273,23 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     // ---- V: decode + EMA (APPLY reads the exact V of the NORM pass)
     if constexpr (kVbuf) {
 #pragma unroll
-      for (int k = 0; k < kEPT; ++k) vn[k] = (k < cnt) ? gp(D.v_buf)[e0 + k] : 0.0f;
+      for (int k = 0; k < kEPT; ++k) vn[k] = (k & 3) < cnth[k >> 2] ? gp(VBu)[lo[k >> 2] + (k & 3)] : 0.0f;
     } else {
       float vo[kEPT];
       if constexpr (VB == 8) {
-        const u32x2 qv = vq8;
-        const float* tb = tabs + vloc * 256;
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) vo[k] = tb[((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu];
+        for (int k = 0; k < kEPT; ++k)
+          vo[k] = tabs[vloc[k >> 2] * 256 + ((vq8[k >> 2] >> (8 * (k & 3))) & 0xFFu)];
       } else {
-        const float s_old = gp(D.v_scale)[vb], lm_old = gp(D.v_min_log)[vb];
-        const u32x4 qv = vq16;
-        const uint32_t w4[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          const uint32_t c = (w4[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-          vo[k] = c ? exp2_exact(((float)(c - 1) * s_old) / 65534.0f + lm_old) : 0.0f;
+        for (int j = 0; j < 2; ++j) {
+          float s_old = 0.0f, lm_old = 0.0f;
+          if (vok[j]) { s_old = gp(VSu)[vloc[j]]; lm_old = gp(VLu)[vloc[j]]; }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t c = ((i < 2 ? vq16[j].x : vq16[j].y) >> (16 * (i & 1))) & 0xFFFFu;
+            vo[4 * j + i] = c ? exp2_exact(((float)(c - 1) * s_old) / 65534.0f + lm_old) : 0.0f;
+          }
         }
       }
       float gsq[kEPT];
@@ -268,25 +314,24 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     float mo[kEPT];
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) mo[k] = 0.0f;
-    if (m_ok) {
-      if (MK == 1) {
-        const u32x2 q = mq8;
-        const float s128 = ms / 128.0f, b128 = -128.0f * s128;   // (q-128)*s128 == fma(q, s128, -128*s128)
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k)
-          mo[k] = __builtin_fmaf((float)(((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu), s128, b128);
-      } else if (mk == 2 || mk == 4) {
-        const uint32_t qw = mq4;
+    for (int j = 0; j < 2; ++j) {
+      if (mok[j]) {
+        if (MK == 1) {
+          const float s128 = ms[j] / 128.0f, b128 = -128.0f * s128;   // (q-128)*s128 == fma(q, s128, -128*s128)
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
-          mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+          for (int i = 0; i < 4; ++i)
+            mo[4 * j + i] = __builtin_fmaf((float)((mq8[j] >> (8 * i)) & 0xFFu), s128, b128);
+        } else if (mk == 2 || mk == 4) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t byte = (mq4[j] >> (8 * (i >> 1))) & 0xFFu;
+            mo[4 * j + i] = m_decode(mk, (i & 1) ? (byte & 0x0Fu) : (byte >> 4), ms[j]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mo[4 * j + i] = m_decode(mk, (mq8[j] >> (8 * i)) & 0xFFu, ms[j]);
         }
-      } else {
-        const u32x2 q = mq8;
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k)
-          mo[k] = m_decode(mk, ((k < 4 ? q.x : q.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }
     }
 
@@ -312,11 +357,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       float x[kEPT];
       if (mom) {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          const float ut = g[k] * inv[k];
-          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(ut, ut, sq);
-          x[k] = ut;
-        }
+        for (int k = 0; k < kEPT; ++k) x[k] = g[k] * inv[k];
         if (ut_clip != 1.0f) {
 #pragma unroll
           for (int k = 0; k < kEPT; ++k) x[k] = x[k] / ut_clip;
@@ -335,190 +376,242 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
       }
       if (mom) {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          uu[k] = mn[k];
-          if (MODE == 4) sq = __builtin_fmaf(mn[k], mn[k], sq);
-        }
+        for (int k = 0; k < kEPT; ++k) uu[k] = mn[k];
       } else {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          uu[k] = mn[k] * inv[k];
-          if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
-        }
+        for (int k = 0; k < kEPT; ++k) uu[k] = mn[k] * inv[k];
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < kEPT; ++k) {
-        mn[k] = 0.0f;
-        uu[k] = g[k] * inv[k];
-        if (MODE == 1 || MODE == 3) sq = __builtin_fmaf(uu[k], uu[k], sq);
-      }
+      for (int k = 0; k < kEPT; ++k) uu[k] = g[k] * inv[k];
     }
-    if (cnt < kEPT) {  // the last lane of a tensor: padding elements hold zero state
-      sq = 0.0f;
+    // elements beyond the tensor (the zero padding of its last blocks) hold zero state
+#pragma unroll
+    for (int k = 0; k < kEPT; ++k) {
+      if ((k & 3) >= cnth[k >> 2]) { vn[k] = 0.0f; mn[k] = 0.0f; uu[k] = 0.0f; }
+    }
+    if constexpr (kSq) {
+      // NORM / LAG: the update (momentum-only: U = g*inv before clipping); MNORM: M'
 #pragma unroll
       for (int k = 0; k < kEPT; ++k) {
-        if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; uu[k] = 0.0f; }
-        const float ut = (MODE == 4) ? mn[k] : (mom ? g[k] * inv[k] : uu[k]);
-        if (kSq && k < cnt) sq = __builtin_fmaf(ut, ut, sq);
+        const float t = (MODE == 4) ? mn[k] : ((mom && (k & 3) < cnth[k >> 2]) ? g[k] * inv[k] : uu[k]);
+        sq = __builtin_fmaf(t, t, sq);
       }
     }
     if constexpr (MODE == 1) {
 #pragma unroll
       for (int k = 0; k < kEPT; ++k)
-        if (k < cnt) gp(D.v_buf)[e0 + k] = vn[k];
+        if ((k & 3) < cnth[k >> 2]) gp(VBu)[lo[k >> 2] + (k & 3)] = vn[k];
     }
 #pragma unroll
     for (int k = 0; k < kEPT; ++k) {
-      vmaxb = max(vmaxb, __float_as_uint(vn[k]));
-      vkey = min(vkey, nz_key(vn[k]));
-      amaxb = max(amaxb, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
+      const int j = k >> 2;
+      vmaxb[j] = max(vmaxb[j], __float_as_uint(vn[k]));
+      vkey[j] = min(vkey[j], nz_key(vn[k]));
+      amaxb[j] = max(amaxb[j], __float_as_uint(mn[k]) & 0x7FFFFFFFu);
     }
 
     // ---- parameter write
     if constexpr (kWrite) {
-      T* P = reinterpret_cast<T*>(D.param);
       const bool has_dec = D.decay || h.has_decay;
       const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
-      if constexpr (SR) {
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) {
-          if (k < cnt) {
-            const float pv = ld1<T>(P, e0 + k);
-            const T r = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(e0 + k));
-            uint16_t bits;
-            __builtin_memcpy(&bits, &r, 2);
-            gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = bits;
+      for (int j = 0; j < 2; ++j) {
+        if (!vok[j]) continue;
+        if constexpr (SR) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (i < cnth[j]) {
+              const uint32_t e = lo[j] + i;
+              const float pv = ld1<T>(Pu, e);
+              const T r = sr_round<T>(pv * dec - step * uu[4 * j + i], D.sr_seed, h.sr_step,
+                                      (uint64_t)(ub + (int64_t)e));
+              uint16_t bits;
+              __builtin_memcpy(&bits, &r, 2);
+              gp(reinterpret_cast<uint16_t*>(Pu))[e] = bits;
+            }
           }
+        } else {
+          float p[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[i] = pin[4 * j + i];
+          if (has_dec) {  // decoupled weight decay: p*decay rounded, then the update (optimizer.py:2039)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = p[i] * dec;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[i] = __builtin_fmaf(-step, uu[4 * j + i], p[i]);
+          store4n<T>(Pu, lo[j], nrem, p);
         }
-      } else {
-        float p[kEPT];
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k) p[k] = pin[k];
-        if (has_dec) {  // decoupled weight decay: p*decay rounded, then the update (optimizer.py:2039)
-#pragma unroll
-          for (int k = 0; k < kEPT; ++k) p[k] = p[k] * dec;
-        }
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k) p[k] = __builtin_fmaf(-step, uu[k], p[k]);
-        store8<T>(P, e0, n, p);
       }
     }
-  } else {
-#pragma unroll
-    for (int k = 0; k < kEPT; ++k) { vn[k] = 0.0f; mn[k] = 0.0f; }
   }
-  const float vmax = __uint_as_float(vmaxb);
-  const float amax = __uint_as_float(amaxb);
-
-  const int wave = lane >> 6;
 
   // ---- V refit + codes
   if constexpr (!kVbuf) {
-    float bmax = grp_max(vmax, VL < 64 ? VL : 64);
-    uint32_t bkey = grp_umin(vkey, VL < 64 ? VL : 64);
     const float lm2 = VB == 8 ? 254.0f : 65534.0f;
-    ALFit f;
-    if (VL > 64) {
-      // a V block spans VL/64 waves: wave 0 refits every block of the workgroup
-      // (lane pair 2j, 2j+1 for block j) and shares the fit through LDS, so
-      // the other waves do not repeat the correctly rounded logarithms.
+    ALFit f[2];
+    if (vwhole) {
+      // one block per workgroup: reduce over all lanes and both halves; wave 0
+      // computes the fit (lane pair 0/1) and shares it through LDS, so the
+      // other waves do not repeat the correctly rounded logarithms
+      float bmax = grp_max(__uint_as_float(max(vmaxb[0], vmaxb[1])), 64);
+      uint32_t bkey = grp_umin(min(vkey[0], vkey[1]), 64);
       if ((lane & 63) == 0) { xw[wave * 4 + 0] = bmax; xw[wave * 4 + 1] = __uint_as_float(bkey); }
       __syncthreads();
       if (wave == 0) {
-        const int j = (lane >> 1) < nv_wg ? (lane >> 1) : 0;
-        const int wpb = VL >> 6;   // waves per block
-        float mx = xw[(j * wpb) * 4];
-        uint32_t ky = __float_as_uint(xw[(j * wpb) * 4 + 1]);
-        for (int w = 1; w < wpb; ++w) {
-          mx = fmaxf(mx, xw[(j * wpb + w) * 4]);
-          ky = min(ky, __float_as_uint(xw[(j * wpb + w) * 4 + 1]));
-        }
+        const float mx = fmaxf(fmaxf(xw[0], xw[4]), fmaxf(xw[8], xw[12]));
+        const uint32_t ky = min(min(__float_as_uint(xw[1]), __float_as_uint(xw[5])),
+                                min(__float_as_uint(xw[9]), __float_as_uint(xw[13])));
         const float mn_ = (ky == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(ky + 1u);
-        const ALFit g = al_refit_pair(mx, mn_, h.floor_, lm2, lane);
-        if ((lane & 1) == 0 && (lane >> 1) < nv_wg) {
-          float* xf = xw + 16 + (lane >> 1) * 8;
-          xf[0] = g.lmin; xf[1] = g.s; xf[2] = g.k; xf[3] = g.c1; xf[4] = g.kmar; xf[5] = g.cmar;
+        const ALFit ft = al_refit_pair(mx, mn_, h.floor_, lm2, lane);
+        if (lane == 0) {
+          float* xf = xw + 16;
+          xf[0] = ft.lmin; xf[1] = ft.s; xf[2] = ft.k; xf[3] = ft.c1; xf[4] = ft.kmar; xf[5] = ft.cmar;
         }
       }
       __syncthreads();
-      const float* xf = xw + 16 + vloc * 8;
-      f.lmin = xf[0]; f.s = xf[1]; f.k = xf[2]; f.c1 = xf[3]; f.kmar = xf[4]; f.cmar = xf[5];
+      const float* xf = xw + 16;
+      f[0].lmin = xf[0]; f[0].s = xf[1]; f[0].k = xf[2]; f[0].c1 = xf[3]; f[0].kmar = xf[4]; f[0].cmar = xf[5];
+      f[1] = f[0];
     } else {
-      const float bmin = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
-      f = al_refit_pair(bmax, bmin, h.floor_, lm2, lane);
-    }
-    {
-      if (v_ok) {
-      if constexpr (VB == 8) {
-        float r[kEPT];
-        bool bad[kEPT];
+      float bmax[2];
+      uint32_t bkey[2];
+      const int G = VLh < 64 ? VLh : 64;
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) r[k] = al8_round_fast(vn[k], f, bad[k]);
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k)
-          if (bad[k]) r[k] = al_round_exact<254>(vn[k], f);
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k) r[k] = al_clamp<254>(vn[k], r[k]);
-        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) =
-            u32x2{pack4(r[0], r[1], r[2], r[3]), pack4(r[4], r[5], r[6], r[7])};
-      } else {
-        uint32_t q[kEPT];
-#pragma unroll
-        for (int k = 0; k < kEPT; ++k) q[k] = al_finish<65534>(vn[k], al_round_exact<65534>(vn[k], f));
-        *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(D.v_q) + e0)) =
-            u32x4{q[0] | (q[1] << 16), q[2] | (q[3] << 16), q[4] | (q[5] << 16), q[6] | (q[7] << 16)};
+      for (int j = 0; j < 2; ++j) {
+        bmax[j] = grp_max(__uint_as_float(vmaxb[j]), G);
+        bkey[j] = grp_umin(vkey[j], G);
       }
-      if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }
+      if (VLh > 64) {
+        // a block spans VLh/64 waves of one half: exchange one partial per wave and half
+        if ((lane & 63) == 0) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) { xw[wave * 4 + 2 * j] = bmax[j]; xw[wave * 4 + 2 * j + 1] = __uint_as_float(bkey[j]); }
+        }
+        __syncthreads();
+        const int wpb = VLh >> 6;                 // waves per block
+        const int w0 = (wave / wpb) * wpb;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float mx = xw[w0 * 4 + 2 * j];
+          uint32_t ky = __float_as_uint(xw[w0 * 4 + 2 * j + 1]);
+          for (int w = 1; w < wpb; ++w) {
+            mx = fmaxf(mx, xw[(w0 + w) * 4 + 2 * j]);
+            ky = min(ky, __float_as_uint(xw[(w0 + w) * 4 + 2 * j + 1]));
+          }
+          bmax[j] = mx;
+          bkey[j] = ky;
+        }
+      }
+      // the two fits of a lane's blocks: lanes 4q+0/1 take log2 of half 0's max/min,
+      // 4q+2/3 of half 1's (a block spans >= 32 lanes, so the quad shares both)
+      const float mn0 = (bkey[0] == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey[0] + 1u);
+      const float mn1 = (bkey[1] == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey[1] + 1u);
+      const int qs = lane & 3;
+      const float x = qs == 0 ? bmax[0] : (qs == 1 ? mn0 : (qs == 2 ? bmax[1] : mn1));
+      const float l = log2_exact(fmaxf(x, kLogClampIn));
+      const int qb = lane & ~3;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float lmax = __shfl(l, qb + 2 * j, 64);
+        float lmin = __shfl(l, qb + 2 * j + 1, 64);
+        lmin = fmaxf(lmin, h.floor_);
+        if (lmin >= lmax) lmin = lmax - 1.0f;
+        f[j].lmin = lmin;
+        f[j].s = fmaxf(lmax - lmin, 1e-12f);
+        al_fit_consts(f[j], lm2);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!vok[j]) continue;
+      if constexpr (VB == 8) {
+        float r[4];
+        bool bad[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = al8_round_fast(vn[4 * j + i], f[j], bad[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (bad[i]) r[i] = al_round_exact<254>(vn[4 * j + i], f[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = al_clamp<254>(vn[4 * j + i], r[i]);
+        *gp(reinterpret_cast<uint32_t*>(V8u + lo[j])) = pack4(r[0], r[1], r[2], r[3]);
+      } else {
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = al_finish<65534>(vn[4 * j + i], al_round_exact<65534>(vn[4 * j + i], f[j]));
+        *gp(reinterpret_cast<u32x2*>(V16u + lo[j])) =
+            u32x2{q[0] | (q[1] << 16), q[2] | (q[3] << 16)};
+      }
+      if ((lane & (VLh - 1)) == 0 && (vwhole ? j == 0 : true)) {
+        gp(VSu)[vloc[j]] = f[j].s;
+        gp(VLu)[vloc[j]] = f[j].lmin;
       }
     }
   }
 
   // ---- M refit + codes
   if constexpr (kWrite && kHasM) {
-    float bam = grp_max(amax, ML < 64 ? ML : 64);
-    if (ML > 64) {
+    float bam[2];
+    if (mwhole) {
+      float a = grp_max(__uint_as_float(max(amaxb[0], amaxb[1])), 64);
       __syncthreads();
-      if ((lane & 63) == 0) xw[wave * 4 + 2] = bam;
+      if ((lane & 63) == 0) xw[wave * 4 + 2] = a;
       __syncthreads();
-      const int w0 = (lane >> (lbm - 3)) * (ML >> 6);
-      bam = xw[w0 * 4 + 2];
-      for (int w = 1; w < (ML >> 6); ++w) bam = fmaxf(bam, xw[(w0 + w) * 4 + 2]);
+      a = fmaxf(fmaxf(xw[2], xw[6]), fmaxf(xw[10], xw[14]));
+      bam[0] = bam[1] = a;
+    } else {
+      const int G = MLh < 64 ? MLh : 64;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bam[j] = grp_max(__uint_as_float(amaxb[j]), G);
+      if (MLh > 64) {
+        __syncthreads();
+        if ((lane & 63) == 0) { xw[wave * 4 + 2] = bam[0]; xw[wave * 4 + 3] = bam[1]; }
+        __syncthreads();
+        const int wpb = MLh >> 6;
+        const int w0 = (wave / wpb) * wpb;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float a = xw[w0 * 4 + 2 + j];
+          for (int w = 1; w < wpb; ++w) a = fmaxf(a, xw[(w0 + w) * 4 + 2 + j]);
+          bam[j] = a;
+        }
+      }
     }
-    if (m_ok) {
-      const float am = fmaxf(bam, 1e-12f);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!mok[j]) continue;
+      const float am = fmaxf(bam[j], 1e-12f);
       const float ram = fast_rcp(am);
       if (MK == 1) {
         const float kam = 128.0f * ram;
-        float r[kEPT];
-        bool bad[kEPT];
+        float r[4];
+        bool bad[4];
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) r[k] = uf_round_fast<128>(mn[k], kam, bad[k]);
+        for (int i = 0; i < 4; ++i) r[i] = uf_round_fast<128>(mn[4 * j + i], kam, bad[i]);
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k)
-          if (bad[k]) r[k] = uf_round_exact<128>(mn[k], am);
+        for (int i = 0; i < 4; ++i)
+          if (bad[i]) r[i] = uf_round_exact<128>(mn[4 * j + i], am);
 #pragma unroll
-        for (int k = 0; k < kEPT; ++k) r[k] = uf_clamp<128>(r[k]);
-        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) =
-            u32x2{pack4(r[0], r[1], r[2], r[3]), pack4(r[4], r[5], r[6], r[7])};
+        for (int i = 0; i < 4; ++i) r[i] = uf_clamp<128>(r[i]);
+        *gp(reinterpret_cast<uint32_t*>(Mu8 + lo[j])) = pack4(r[0], r[1], r[2], r[3]);
       } else if (mk == 2 || mk == 4) {
         uint32_t w = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t hi = m_encode(mk, mn[2 * j], am, ram);
-          const uint32_t lo = m_encode(mk, mn[2 * j + 1], am, ram);
-          w |= ((hi << 4) | lo) << (8 * j);
+        for (int q = 0; q < 2; ++q) {
+          const uint32_t hi = m_encode(mk, mn[4 * j + 2 * q], am, ram);
+          const uint32_t lo = m_encode(mk, mn[4 * j + 2 * q + 1], am, ram);
+          w |= ((hi << 4) | lo) << (8 * q);
         }
-        *gp(reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1))) = w;
+        *gp(reinterpret_cast<uint16_t*>(Mu4 + (lo[j] >> 1))) = (uint16_t)w;
       } else {
-        uint32_t w0 = 0, w1 = 0;
+        uint32_t w = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w0 |= m_encode(mk, mn[k], am, ram) << (8 * k);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) w1 |= m_encode(mk, mn[k + 4], am, ram) << (8 * k);
-        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
+        for (int i = 0; i < 4; ++i) w |= m_encode(mk, mn[4 * j + i], am, ram) << (8 * i);
+        *gp(reinterpret_cast<uint32_t*>(Mu8 + lo[j])) = w;
       }
-      if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
+      if ((lane & (MLh - 1)) == 0 && (mwhole ? j == 0 : true)) gp(MSu)[mloc[j]] = am;
     }
   }
 
@@ -527,6 +620,20 @@ __global__ __launch_bounds__(kLanes) void k_update1d(Desc1D one, const Desc1D* _
     const float t = grp_sum(sq, 64);
     if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
   }
+}
+
+// Occupancy 7 waves per SIMD (at most 72 VGPRs): measured best on MI355X for
+// this streaming step (more resident waves hide the HBM latency of the loads).
+template <typename T, int VB, int MODE, bool SR, int MK>
+__global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(7)))
+void k_update1d(Desc1D one, const Desc1D* __restrict__ table, int ntab, Hyper1D h) {
+  extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | cross-wave partials and fits
+  Desc1D D;
+  if (table != nullptr) D = load_desc(table, ntab, (int)blockIdx.x);
+  else D = one;
+  const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
+  if (D.numel - wl * kWGElems >= kWGElems) unit_step<T, VB, MODE, SR, MK, true>(D, h, wl, s_lds);
+  else unit_step<T, VB, MODE, SR, MK, false>(D, h, wl, s_lds);
 }
 
 // ------------------------------------------------------------ launch glue

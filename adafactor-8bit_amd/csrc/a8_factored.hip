@@ -1,25 +1,27 @@
 // Factored (Adafactor row/column) optimizer step for MI355X (gfx950).
 //
 // One group step is a few launches over every tensor of the group:
-//   k_fstats   2-D tiles of 32 rows x 1024 columns: row sums and column sums of
-//              g^2 (and sum p^2 for the relative step size), written as
-//              per-tile partials -- no atomics, so the result is deterministic;
-//   k_ffinish  one workgroup per (tensor, row|column): reduce the partials in a
-//              fixed order, EMA the row/column second moment, refit and
-//              re-encode its AL blocks, and produce inv_row / inv_col and the
-//              tensor's step size and weight-decay factor;
+//   k_fstats   2-D tiles of tr rows x 1024 columns (tr = 32, taller for tall
+//              matrices): row sums and column sums of g^2 (and sum p^2 for the
+//              relative step size), written as per-tile partials -- no atomics,
+//              so the result is deterministic;
+//   k_fblock   one workgroup per AL block of each row/column vector: reduce the
+//              partials in a fixed order, EMA the second moment, refit and
+//              re-encode the block (columns: inv_col in place);
+//   k_frows    one workgroup per tensor: the row mean, inv_row, the step size
+//              and the weight-decay factor;
 //   k_fupdate  flat 2048-element units (8 per lane, as the 1-D step): the
 //              update u = (x * inv_row) * inv_col with x = g or the momentum
 //              EMA, the parameter write and the momentum re-encode.  With RMS
 //              clipping or Fira it runs twice: first for sum(u^2) per unit,
 //              then (after k_fnorm) to apply;
 //   k_fnorm    one workgroup per tensor: ||u||, the Fira limiter and the step.
-// CAME (beta3) adds, between k_ffinish and the update:
+// CAME (beta3) adds, between k_frows and the update:
 //   k_fclip    the RMS clip factor of U = (g * inv_row) * inv_col (after a
 //              k_fupdate norm pass over U, only when d > 0);
 //   k_came1    the same 2-D tiles as k_fstats: U / clip, the momentum EMA M',
 //              and row/column sums of the residual (U - M')^2 + eps_came;
-//   k_ffinish  again, on the residual sums: the confidence EMA, its AL
+//   k_fblock / k_frows again, on the residual sums: the confidence EMA, its AL
 //              re-encode and inv_conf_row / inv_conf_col;
 // and the update becomes (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
 // Numbers follow the reference's PyTorch path (optimizer.py:2198-2252 and
@@ -32,7 +34,7 @@
 
 namespace a8 {
 
-constexpr int kTR = 32;      // rows per statistics tile
+constexpr int kTR = 32;      // minimum rows per statistics tile
 constexpr int kTC = 1024;    // columns per statistics tile (256 lanes x 4)
 constexpr int kUnit = 2048;  // elements per update workgroup
 constexpr int kScal = 8;     // per-tensor scalars in the workspace
@@ -50,12 +52,23 @@ struct FWs {
   int64_t scal;      // [8]: alpha, step, fira scale, decay, CAME clip factor
   int64_t total;
   int64_t nchunk, nstrip, ntile, nunit;
+  int64_t tr;        // rows per statistics tile
 };
+
+// Rows per statistics tile: 32, taller for tall matrices so that a column has at
+// most ~64 strip partials to reduce (the tile kernels carry column partials in
+// registers across rows, so a taller tile costs nothing there).
+__host__ __device__ inline int64_t fws_tile_rows(int64_t R) {
+  int64_t tr = (R + 63) / 64;
+  tr = (tr + kTR - 1) / kTR * kTR;
+  return tr < kTR ? kTR : (tr > 1024 ? 1024 : tr);
+}
 
 __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
   FWs w;
   w.nchunk = (C + kTC - 1) / kTC;
-  w.nstrip = (R + kTR - 1) / kTR;
+  w.tr = fws_tile_rows(R);
+  w.nstrip = (R + w.tr - 1) / w.tr;
   w.ntile = B * w.nstrip * w.nchunk;
   w.nunit = (B * R * C + kUnit - 1) / kUnit;
   w.rowpart = 0;
@@ -98,6 +111,8 @@ struct DescF {
   int64_t B, R, C, numel;
   int64_t tile_begin;
   int64_t unit_begin;
+  int64_t fblk_begin;  // first k_fblock workgroup of this tensor
+  int64_t nbr;         // AL blocks of the row vector (the column vector follows)
   uint64_t sr_seed;
   int has_fira_prev;
   int vec4;            // rows start 16-byte aligned for fp32 (8-byte for 16-bit types)
@@ -216,8 +231,8 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
   const int64_t s = bs % W.nstrip;
   const int64_t b = bs / W.nstrip;
   const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  const int64_t r_lo = s * kTR;
-  const int64_t r_hi = (r_lo + kTR < R) ? r_lo + kTR : R;
+  const int64_t r_lo = s * W.tr;
+  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
   const int64_t c_base = ch * kTC;
   const T* G = reinterpret_cast<const T*>(D.grad);
   const T* P = reinterpret_cast<const T*>(D.param);
@@ -326,8 +341,8 @@ __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, 
   const int64_t s = bs % W.nstrip;
   const int64_t b = bs / W.nstrip;
   const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  const int64_t r_lo = s * kTR;
-  const int64_t r_hi = (r_lo + kTR < R) ? r_lo + kTR : R;
+  const int64_t r_lo = s * W.tr;
+  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
   const int64_t c_base = ch * kTC;
   const T* G = reinterpret_cast<const T*>(D.grad);
   float* ws = D.ws;
@@ -402,19 +417,32 @@ __device__ __forceinline__ float fv_decode(const void* q, const float* sc, const
   }
 }
 
-// grid (ntab, 2): y = 0 row state (+ per-tensor scalars), y = 1 column state.
-// CONF = false: the second moment from the g^2 sums (mean + eps1, lerp weight
-// 1 - beta2 or step^decay), then inv_row / inv_col and the step size.
-// CONF = true (CAME): the confidence from the residual sums written by k_came1
-// (mean, lerp weight 1 - beta3), then inv_conf_row / inv_conf_col
-// (optimizer.py:941-953).  VB is the state's codec (8 / 16 bits, 0 = fp32).
+__device__ __forceinline__ const DescF* find_fblk(const DescF* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].fblk_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+// Row/column second moment (CONF = false) or CAME confidence (CONF = true), one
+// workgroup per AL block of the flattened row or column vector of a tensor:
+// reduce the statistics tiles' partials in a fixed order (double), mean (g^2:
+// sum/count + eps1; residual: sum/count), EMA with the decoded state (lerp
+// weight 1 - beta2 / step^decay, or 1 - beta3), refit and re-encode the block
+// (optimizer.py:2204-2238, 941-948).  The new values go to the workspace vector;
+// on the column side they are replaced by inv_col = 1/sqrt(v) (optimizer.py:818-821,
+// 951-953).  VB is the state's codec (8 / 16 bits, 0 = fp32 state, blocks of the
+// same size only partition the work).
 template <int VB, bool CONF>
-__global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table, HyperF h) {
-  __shared__ double sd[4];
+__global__ __launch_bounds__(256) void k_fblock(const DescF* __restrict__ table, int ntab, HyperF h) {
   __shared__ float sf[8];
-  const DescF D = table[blockIdx.x];
-  const bool is_row = blockIdx.y == 0;
+  const DescF D = *find_fblk(table, ntab, (int64_t)blockIdx.x);
   const FWs W = fws_layout(D.B, D.R, D.C);
+  const int64_t lb = (int64_t)blockIdx.x - D.fblk_begin;
+  const bool is_row = lb < D.nbr;
+  const int64_t bi = is_row ? lb : lb - D.nbr;
   const int lane = threadIdx.x;
   const int64_t B = D.B, R = D.R, C = D.C;
   const int64_t n = is_row ? B * R : B * C;
@@ -438,15 +466,28 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
   const float cnt = is_row ? (float)C : (float)R;
   const int64_t bsz = h.block_size;
   const float w = CONF ? h.w_c : h.bv;
+  const int64_t i0 = bi * bsz;
+  const int64_t i1 = (i0 + bsz < n) ? i0 + bsz : n;
 
-  // 1. means (g^2: sum / count + eps1; residual: sum / count), EMA with the decoded state
-  for (int64_t i = lane; i < n; i += 256) {
+  // 1. means and EMA (each lane keeps its own entries for step 2)
+  float mx = 0.0f;
+  uint32_t key = 0xFFFFFFFFu;
+  for (int64_t i = i0 + lane; i < i1; i += 256) {
     double sum = 0.0;
     if (is_row) {
       for (int64_t k = 0; k < W.nchunk; ++k) sum += (double)gp(ws)[W.rowpart + k * n + i];
     } else {
       const int64_t b = i / C, c = i - b * C;
-      for (int64_t k = 0; k < W.nstrip; ++k) sum += (double)gp(ws)[W.colpart + (b * W.nstrip + k) * C + c];
+      const float* cp0 = ws + W.colpart + b * W.nstrip * C + c;
+      int64_t k = 0;
+      for (; k + 8 <= W.nstrip; k += 8) {   // eight loads in flight, summed in order
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = gp(cp0)[(k + u) * C];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum += (double)t[u];
+      }
+      for (; k < W.nstrip; ++k) sum += (double)gp(cp0)[k * C];
     }
     float mean = (float)sum / cnt;
     if constexpr (!CONF) mean = mean + h.eps1;
@@ -455,56 +496,56 @@ __global__ __launch_bounds__(256) void k_ffinish(const DescF* __restrict__ table
     else old = fv_decode<VB>(q, sc, ml, i, bsz);
     const float nv = lerp_ref(old, mean, w);
     gp(vec)[i] = nv;
-    if constexpr (VB == 0) gp(fst)[i] = nv;
+    if constexpr (VB == 0) {
+      gp(fst)[i] = nv;
+      if (!is_row) gp(vec)[i] = 1.0f / sqrtf(nv);
+    }
+    mx = fmaxf(mx, nv);
+    key = min(key, nz_key_f(nv));
   }
-  __syncthreads();
 
-  // 2. refit and re-encode every AL block of the flattened vector (zero padding -> code 0)
+  // 2. refit and re-encode the block (zero padding beyond n -> code 0)
   if constexpr (VB != 0) {
     constexpr int LM2 = VB == 8 ? 254 : 65534;
-    const int64_t nb = (n + bsz - 1) / bsz;
-    for (int64_t bi = 0; bi < nb; ++bi) {
-      float mx = 0.0f;
-      uint32_t key = 0xFFFFFFFFu;
-      for (int64_t k = lane; k < bsz; k += 256) {
-        const int64_t i = bi * bsz + k;
-        const float v = i < n ? gp(vec)[i] : 0.0f;
-        mx = fmaxf(mx, v);
-        key = min(key, nz_key_f(v));
-      }
-      wg_maxkey(mx, key, sf);
-      const float mnz = (key == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(key + 1u);
-      const ALFit f = al_refit(mx, mnz, h.floor_, (float)LM2);
-      for (int64_t k = lane; k < bsz; k += 256) {
-        const int64_t i = bi * bsz + k;
-        const float v = i < n ? gp(vec)[i] : 0.0f;
-        const uint32_t code = al_finish<LM2>(v, al_round_exact<LM2>(v, f));
-        if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[i] = (uint8_t)code;
-        else gp(reinterpret_cast<uint16_t*>(q))[i] = (uint16_t)code;
-      }
-      if (lane == 0) { gp(sc)[bi] = f.s; gp(ml)[bi] = f.lmin; }
+    wg_maxkey(mx, key, sf);
+    const float mnz = (key == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(key + 1u);
+    const ALFit f = al_refit(mx, mnz, h.floor_, (float)LM2);
+    for (int64_t k = lane; k < bsz; k += 256) {
+      const int64_t i = i0 + k;
+      const float v = i < n ? gp(vec)[i] : 0.0f;
+      const uint32_t code = al_finish<LM2>(v, al_round_exact<LM2>(v, f));
+      if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[i] = (uint8_t)code;
+      else gp(reinterpret_cast<uint16_t*>(q))[i] = (uint16_t)code;
+      if (!is_row && i < n) gp(vec)[i] = 1.0f / sqrtf(v);
+    }
+    if (lane == 0) { gp(sc)[bi] = f.s; gp(ml)[bi] = f.lmin; }
+  }
+}
+
+// One workgroup per tensor: r = max(mean_r(row), eps1) per batch and
+// inv_row = 1/sqrt(row / r) (optimizer.py:2221, 818-821; the confidence's r_c,
+// 951-952), then (CONF = false) the step size and weight-decay factor
+// (optimizer.py:832-856, 2020-2039).
+template <bool CONF>
+__global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, HyperF h) {
+  __shared__ double sd[4];
+  const DescF D = table[blockIdx.x];
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int lane = threadIdx.x;
+  const int64_t B = D.B, R = D.R;
+  float* ws = D.ws;
+  float* vec = ws + (CONF ? W.icr : W.invr);
+  for (int64_t b = 0; b < B; ++b) {
+    double s = 0.0;
+    for (int64_t r = lane; r < R; r += 256) s += (double)gp(vec)[b * R + r];
+    s = wg_sum_d(s, sd);
+    const float rmv = fmaxf((float)s / (float)R, h.eps1);
+    for (int64_t r = lane; r < R; r += 256) {
+      const int64_t i = b * R + r;
+      gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i] / rmv);
     }
   }
-  __syncthreads();
-
-  // 3. inverse square roots (optimizer.py:818-821; the same form for the confidence, 951-953)
-  if (is_row) {
-    for (int64_t b = 0; b < B; ++b) {
-      double s = 0.0;
-      for (int64_t r = lane; r < R; r += 256) s += (double)gp(vec)[b * R + r];
-      s = wg_sum_d(s, sd);
-      const float rmv = fmaxf((float)s / (float)R, h.eps1);
-      for (int64_t r = lane; r < R; r += 256) {
-        const int64_t i = b * R + r;
-        gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i] / rmv);
-      }
-    }
-  } else {
-    for (int64_t i = lane; i < n; i += 256) gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i]);
-  }
-
-  // 4. step size and weight decay (optimizer.py:832-856, 2020-2039)
-  if (!CONF && is_row) {
+  if constexpr (!CONF) {
     const float rho = D.lr ? *gp(D.lr) : h.lr_val;
     float alpha = rho;
     if (h.scale_param) {
@@ -804,14 +845,18 @@ static int launch_update(int mode, int mk, const DescF* tab, int ntab, int64_t n
 }
 
 template <bool CONF>
-static int launch_finish(int bits, const DescF* tab, int ntab, const HyperF& h, hipStream_t st) {
-  const dim3 g((unsigned)ntab, 2), b(256);
+static int launch_finish(int bits, const DescF* tab, int ntab, int64_t nfblk, const HyperF& h,
+                         hipStream_t st) {
+  const dim3 g((unsigned)nfblk), b(256);
   switch (bits) {
-    case 8: hipLaunchKernelGGL((k_ffinish<8, CONF>), g, b, 0, st, tab, h); break;
-    case 16: hipLaunchKernelGGL((k_ffinish<16, CONF>), g, b, 0, st, tab, h); break;
-    default: hipLaunchKernelGGL((k_ffinish<0, CONF>), g, b, 0, st, tab, h); break;
+    case 8: hipLaunchKernelGGL((k_fblock<8, CONF>), g, b, 0, st, tab, ntab, h); break;
+    case 16: hipLaunchKernelGGL((k_fblock<16, CONF>), g, b, 0, st, tab, ntab, h); break;
+    default: hipLaunchKernelGGL((k_fblock<0, CONF>), g, b, 0, st, tab, ntab, h); break;
   }
-  return check_launch("k_ffinish");
+  int rc = check_launch("k_fblock");
+  if (rc) return rc;
+  hipLaunchKernelGGL((k_frows<CONF>), dim3((unsigned)ntab), b, 0, st, tab, h);
+  return check_launch("k_frows");
 }
 
 // Launch sequence of one group step.  Plain factored: stats, finish, then the
@@ -819,11 +864,11 @@ static int launch_finish(int bits, const DescF* tab, int ntab, const HyperF& h, 
 // stats, finish, [U norm + k_fclip when d > 0], k_came1, confidence finish,
 // [update norm + k_fnorm with Fira], update.
 template <typename T, bool SR>
-static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int vbits, int cbits,
-                     bool clip, const HyperF& h, hipStream_t st) {
+static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int64_t nfblk, int vbits,
+                     int cbits, bool clip, const HyperF& h, hipStream_t st) {
   int rc = launch_stats<T>(h.scale_param != 0, tab, ntab, ntiles, st);
   if (rc) return rc;
-  if ((rc = launch_finish<false>(vbits, tab, ntab, h, st))) return rc;
+  if ((rc = launch_finish<false>(vbits, tab, ntab, nfblk, h, st))) return rc;
   if (h.came) {
     if (h.d > 0.0f) {
       if ((rc = launch_update<T, false, false>(1, 0, tab, ntab, nunits, h, st))) return rc;
@@ -833,7 +878,7 @@ static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits,
     if (h.mk == 1) hipLaunchKernelGGL((k_came1<T, 1>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     else hipLaunchKernelGGL((k_came1<T, 2>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     if ((rc = check_launch("k_came1"))) return rc;
-    if ((rc = launch_finish<true>(cbits, tab, ntab, h, st))) return rc;
+    if ((rc = launch_finish<true>(cbits, tab, ntab, nfblk, h, st))) return rc;
     if (!h.fira) return launch_update<T, SR, true>(0, h.mk, tab, ntab, nunits, h, st);
     if ((rc = launch_update<T, false, true>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
     hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
@@ -893,7 +938,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum codes (m_q)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
-  int64_t tiles = 0, units = 0;
+  int64_t tiles = 0, units = 0, fblks = 0;
   const size_t esz = dtype == A8_F32 ? 4 : 2;
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor2d& t = tensors[i];
@@ -926,10 +971,14 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     const FWs W = fws_layout(t.batch, t.rows, t.cols);
     D.tile_begin = tiles;
     D.unit_begin = units;
+    D.fblk_begin = fblks;
+    D.nbr = (t.batch * t.rows + block_size - 1) / block_size;
     tiles += W.ntile;
     units += W.nunit;
+    fblks += D.nbr + (t.batch * t.cols + block_size - 1) / block_size;
   }
-  if (tiles > 0x7FFFFFFF || units > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  if (tiles > 0x7FFFFFFF || units > 0x7FFFFFFF || fblks > 0x7FFFFFFF)
+    return set_error(A8_ERR_SIZE, "too many workgroups");
   hipStream_t st = (hipStream_t)stream;
   if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(DescF) * (size_t)ntensors,
                                hipMemcpyHostToDevice, st) != hipSuccess)
@@ -953,13 +1002,13 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   const bool clip = d > 0.0f || fira;
   const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
   switch (dtype) {
-    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
+    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
     case A8_BF16:
-      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st)
-                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st)
+                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
     default:
-      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st)
-                        : run_group<__half, false>(dt, ntensors, tiles, units, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st)
+                        : run_group<__half, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
   }
 }
 

@@ -1,6 +1,6 @@
 """Benchmark: fused AL8/UF8 AdamW optimizer step over a TinyLlama-1.1B-shaped fp32 model.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload NAME]
 
 One "step" is one ``Adafactor8Bit.step()`` (adamw preset: beta=(0.9, 0.999),
 eps=(1e-8, 1e-3), d=0, lr=1e-4, UF8 momentum with 256-element blocks, AL8 second
@@ -12,6 +12,14 @@ grads and states are resident in HBM before timing; grads are synthetic
 Prints one JSON line: whole-step params/s, the dominant kernel's roofline
 (algorithmic bytes per launch / average launch time from HIP events on the
 launch stream) and a CPU baseline (the CPU oracle timed on the host cores).
+
+``--workload`` also measures two other BASELINE configurations on the same
+shapes (they are parity cases of the headline metric, reported for their own
+kernels): ``adafactor`` (C2: factored AL8, B_V 256, no beta1, Student-t grads,
+90% zero embedding rows) and ``came`` (C3: UF8 M, AL16 V and confidence, B_V
+2048, Fira on, per-tensor log-uniform gradient scales).  For those the
+roofline is the whole step's algorithmic bytes over its GPU time (HIP events
+around ``step()``).
 """
 import argparse
 import json
@@ -29,6 +37,15 @@ ADAMW = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=Fals
              relative_step=False, scale_parameter=False, scale_weight_decay=False, d=0.0,
              eps=(1e-8, 1e-3), lr=1e-4, block_size=2048, m_block_size=256, m_quant_type="uf8",
              v_quant_type="al8")
+
+
+ADAFACTOR = dict(beta1=None, beta2=None, beta2_decay=-0.8, beta3=None, factored=True,
+                 relative_step=False, lr=1e-3, block_size=256, v_quant_type="al8")
+CAME = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True,
+            relative_step=False, scale_parameter=False, scale_weight_decay=False, d=1.0,
+            eps_came=1e-16, lr=1e-4, block_size=2048, m_block_size=256, m_quant_type="uf8",
+            v_quant_type="al16", c_quant_type="al16", enable_fira_for_adafactor=True,
+            fira_margin=0.01)
 
 
 def tinyllama_shapes():
@@ -54,6 +71,42 @@ def step_bytes(shapes, bv=2048, bm=256, min8=4096):
         else:
             q += 16 * n + 16 * (-(-n // bv)) + 8 * (-(-n // bm))
     return q, f
+
+
+def factored_step_bytes(shapes, workload):
+    """Algorithmic bytes of one factored step: per matrix element, adafactor (C2:
+    scale_parameter, d = 1) reads g+p for the statistics, g for the norm pass and
+    g+p and writes p in the update = 24 B; came with Fira (C3) reads g (statistics),
+    g (U norm), g+M (pass 1), g+M (Fira norm), g+M+p and writes M+p (update) = 32 B,
+    plus the M scale per 256 elements.  The 1-D vectors keep fp32 state: 28 B."""
+    mat = vec = 0
+    for s in shapes:
+        n = 1
+        for x in s:
+            n *= x
+        if len(s) >= 2:
+            mat += n
+        else:
+            vec += n
+    per = 24.0 if workload == "adafactor" else 32.0 + 3 * 4.0 / 256
+    return mat * per + vec * 28.0
+
+
+def make_grad(kind, shape, gen, dev, i, embed):
+    if kind == "adamw":
+        g = torch.randn(shape, device=dev, generator=gen) * 1e-3
+        return g * (torch.rand(shape, device=dev, generator=gen) >= 0.05)
+    if kind == "adafactor":  # Student-t df=3 scaled 1e-3; embedding rows 90% zero
+        z = torch.randn(shape, device=dev, generator=gen)
+        chi = sum(torch.randn(shape, device=dev, generator=gen) ** 2 for _ in range(3))
+        g = 1e-3 * z * torch.sqrt(3.0 / chi)
+        if embed:
+            keep = (torch.rand(shape[0], device=dev, generator=gen) >= 0.9).float()
+            g = g * keep[:, None]
+        return g
+    # came: N(0, 1e-3) with a per-tensor scale 10^U(-5, -2)
+    sc = 10.0 ** (-5.0 + 3.0 * torch.rand((), device=dev, generator=gen))
+    return torch.randn(shape, device=dev, generator=gen) * 1e-3 * sc
 
 
 def cpu_baseline(seconds_budget=20.0):
@@ -96,6 +149,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="after timing, run a plain 256 MiB fp32 copy (for counter calibration)")
+    ap.add_argument("--workload", default="adamw", choices=["adamw", "adafactor", "came"],
+                    help="adamw (default, the headline metric), adafactor (C2) or came (C3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU boxes; no collectives); "
@@ -110,17 +165,18 @@ def main():
     params = []
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    for s in shapes:
+    for i, s in enumerate(shapes):
         if len(s) == 1:
             p = torch.ones(s, device=dev)
         else:
             p = torch.randn(s, device=dev, generator=gen) * 0.02
-        g = torch.randn(s, device=dev, generator=gen) * 1e-3
-        g *= (torch.rand(s, device=dev, generator=gen) >= 0.05)
+        g = make_grad(args.workload, s, gen, dev, i, embed=(i == 0))
         p = torch.nn.Parameter(p)
         p.grad = g
         params.append(p)
     nparams = sum(p.numel() for p in params)
+    if args.workload != "adamw":
+        return bench_factored(args, params, nparams, shapes, Adafactor8Bit)
     opt = Adafactor8Bit(params, **ADAMW)
     for _ in range(args.warmup):
         opt.step()
@@ -191,6 +247,43 @@ def main():
                      "kernel": "k_update1d<float,8,0,false> (multi-tensor, 156 tensors)",
                      "kernel_ms_avg": k_avg, "kernel_ms_min": kms[0], "bytes_per_launch": qbytes},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
+    kw = ADAFACTOR if args.workload == "adafactor" else CAME
+    opt = Adafactor8Bit(params, **kw)
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        opt.step()
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall / args.steps * 1e3
+    gms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    nbytes = factored_step_bytes(shapes, args.workload)
+    achieved = nbytes / (gms * 1e-3) / 1e9
+    name = {"adafactor": "adafactor_factored_al8_bv256", "came": "came_uf8_al16_al16_fira_bv2048"}[args.workload]
+    out = {
+        "metric": "fused step params/sec + achieved HBM GB/s (% of peak), " + args.workload + " @1.1B params",
+        "value": nparams / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": name + "_tinyllama_1.1b_fp32", "params": nparams, "tensors": len(params),
+                   "step_bytes": nbytes},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "whole step (all launches of one step, HIP events around step())",
+                     "gpu_ms_per_step": gms, "bytes_per_step": nbytes},
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
 

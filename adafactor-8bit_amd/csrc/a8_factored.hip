@@ -48,7 +48,7 @@ struct FWs {
   int64_t invc;      // [B*C]              new column V, then inv_col
   int64_t icr;       // [B*R]              CAME: new row confidence, then its inverse root
   int64_t icc;       // [B*C]              CAME: new column confidence, then its inverse root
-  int64_t npart;     // [nunit]            partial sum u^2
+  int64_t npart;     // [max(nunit, ntile)] partial sums u^2 (per unit or per tile)
   int64_t scal;      // [8]: alpha, step, fira scale, decay, CAME clip factor
   int64_t total;
   int64_t nchunk, nstrip, ntile, nunit;
@@ -79,7 +79,7 @@ __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
   w.icr = w.invc + B * C;
   w.icc = w.icr + B * R;
   w.npart = w.icc + B * C;
-  w.scal = w.npart + w.nunit;
+  w.scal = w.npart + (w.nunit > w.ntile ? w.nunit : w.ntile);
   w.total = w.scal + kScal;
   return w;
 }
@@ -116,6 +116,7 @@ struct DescF {
   uint64_t sr_seed;
   int has_fira_prev;
   int vec4;            // rows start 16-byte aligned for fp32 (8-byte for 16-bit types)
+  int tiled;           // update runs on the statistics tiles (k_fupdt), else flat units
 };
 
 struct HyperF {
@@ -583,6 +584,7 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   __shared__ float s4[8];
   constexpr bool kHasM = MK != 0;
   const DescF D = *find_unit(table, ntab, (int64_t)blockIdx.x);
+  if (D.tiled) return;   // updated by k_fupdt
   const FWs W = fws_layout(D.B, D.R, D.C);
   const int64_t wl = (int64_t)blockIdx.x - D.unit_begin;
   const int lane = threadIdx.x;
@@ -755,6 +757,181 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   }
 }
 
+// Tiled form of k_fupdate for tensors whose columns allow it (C % 4 == 0 and,
+// with momentum, B_M <= 256 dividing C): the statistics tiles (tr rows x 1024
+// columns), each wave walking rows, lanes holding 4 consecutive columns of each
+// 256-column chunk (1 KB-contiguous accesses).  The tile's inv_col (and CAME
+// inv_conf_col) are staged in LDS once, a row's inv_row arrives through a scalar
+// load, and an M block is B_M/4 lanes of one chunk of one row.  Same arithmetic
+// and operation order as k_fupdate; MODE 1 writes one partial per tile.
+template <typename T, int MODE, bool SR, int MK, bool CM>
+__global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, int ntab, HyperF h) {
+  static_assert(!CM || MK != 0, "CAME needs momentum");
+  __shared__ float s_ic[2 * kTC];
+  __shared__ float s4[8];
+  constexpr bool kHasM = MK != 0;
+  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
+  if (!D.tiled) return;   // updated by k_fupdate
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
+  const int64_t R = D.R, C = D.C;
+  const int64_t ch = t % W.nchunk;
+  const int64_t bs = t / W.nchunk;
+  const int64_t s = bs % W.nstrip;
+  const int64_t b = bs / W.nstrip;
+  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
+  const int64_t r_lo = s * W.tr;
+  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
+  const int64_t c_base = ch * kTC;
+  float* ws = D.ws;
+  for (int q = lane; q < kTC; q += 256) {
+    const int64_t c = c_base + q;
+    s_ic[q] = c < C ? gp(ws)[W.invc + b * C + c] : 0.0f;
+    if constexpr (CM) s_ic[kTC + q] = c < C ? gp(ws)[W.icc + b * C + c] : 0.0f;
+  }
+  __syncthreads();
+  const float* sl = ws + W.scal;
+  const int lbm = h.lbm;
+  const int G = (1 << lbm) >> 2;          // lanes per M block
+  const int mk = (MK == 1) ? 1 : h.mk;
+  const float clip = CM ? cp(sl)[4] : 1.0f;
+  float step = 0.0f, fs = 1.0f, dec = 1.0f;
+  if constexpr (MODE != 1) {
+    step = (MODE == 0) ? cp(sl)[0] : cp(sl)[1];
+    fs = (MODE == 2) ? cp(sl)[2] : 1.0f;
+    dec = cp(sl)[3];
+  }
+  const bool has_dec = h.wd_mode != 0;
+  const T* G0 = reinterpret_cast<const T*>(D.grad);
+  T* P0 = reinterpret_cast<T*>(D.param);
+  float sq = 0.0f;
+  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
+    const int64_t rowbase = (b * R + r) * C;
+    const float ir = cp(ws)[W.invr + b * R + r];
+    const float icrr = CM ? cp(ws)[W.icr + b * R + r] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (c_base + 256 * j >= C) break;     // uniform: chunk beyond the matrix
+      const int q0 = 256 * j + 4 * wl;
+      const int64_t c0 = c_base + q0;
+      const bool act = c0 < C;            // C % 4 == 0: all four columns or none
+      const int64_t e = rowbase + c0;
+      float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (act) {
+        load4v<T>(G0, e, g);
+        if constexpr (kHasM) {
+          const float ms = gp(D.m_scale)[e >> lbm];
+          if (MK == 1) {
+            const uint32_t qv = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
+            const float s128 = ms / 128.0f, b128 = -128.0f * s128;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mo[i] = __builtin_fmaf((float)((qv >> (8 * i)) & 0xFFu), s128, b128);
+          } else if (mk == 2 || mk == 4) {
+            const uint32_t qv = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t byte = (qv >> (8 * (i >> 1))) & 0xFFu;
+              mo[i] = m_decode(mk, (i & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+            }
+          } else {
+            const uint32_t qv = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mo[i] = m_decode(mk, (qv >> (8 * i)) & 0xFFu, ms);
+          }
+        }
+        if constexpr (MODE != 1 && !SR) load4v<T>(P0, e, pv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gi = scrub(g[i]);
+          const float ic = s_ic[q0 + i];
+          if constexpr (CM) {
+            const float ug = ((gi * ir) * ic) / clip;
+            mn[i] = lerp_ref(mo[i], ug, h.w_m);
+            u[i] = (mn[i] * icrr) * s_ic[kTC + q0 + i];
+          } else {
+            float x = gi;
+            if constexpr (kHasM) { mn[i] = lerp_ref(mo[i], gi, h.w_m); x = mn[i]; }
+            u[i] = (x * ir) * ic;
+          }
+          if (MODE == 1) sq = __builtin_fmaf(u[i], u[i], sq);
+        }
+      }
+      if constexpr (MODE != 1) {
+        if (act) {
+          if (MODE == 2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[i] = u[i] * fs;
+          }
+          if constexpr (SR) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p = ld1<T>(P0, e + i);
+              const T rr = sr_round<T>((has_dec ? p * dec : p) - step * u[i], D.sr_seed, h.sr_step,
+                                       (uint64_t)(e + i));
+              uint16_t bits;
+              __builtin_memcpy(&bits, &rr, 2);
+              gp(reinterpret_cast<uint16_t*>(P0))[e + i] = bits;
+            }
+          } else {
+            if (has_dec) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pv[i] = pv[i] * dec;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[i] = __builtin_fmaf(-step, u[i], pv[i]);
+            store4n<T>(P0, e, e + 4, pv);
+          }
+        }
+        if constexpr (kHasM) {
+          // momentum re-encode: absmax over the block's G lanes (inactive lanes hold 0)
+          uint32_t ab = 0u;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ab = max(ab, __float_as_uint(mn[i]) & 0x7FFFFFFFu);
+          const float bam = grp_max(__uint_as_float(ab), G);
+          if (act) {
+            const float am = fmaxf(bam, 1e-12f);
+            const float ram = fast_rcp(am);
+            if (MK == 1) {
+              const float kam = 128.0f * ram;
+              float rr[4];
+              bool bad[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) rr[i] = uf_round_fast<128>(mn[i], kam, bad[i]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (bad[i]) rr[i] = uf_round_exact<128>(mn[i], am);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) rr[i] = uf_clamp<128>(rr[i]);
+              *gp(reinterpret_cast<uint32_t*>(D.m_q + e)) = pack4(rr[0], rr[1], rr[2], rr[3]);
+            } else if (mk == 2 || mk == 4) {
+              uint32_t w = 0;
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                const uint32_t hi = m_encode(mk, mn[2 * q], am, ram);
+                const uint32_t lo = m_encode(mk, mn[2 * q + 1], am, ram);
+                w |= ((hi << 4) | lo) << (8 * q);
+              }
+              *gp(reinterpret_cast<uint16_t*>(D.m_q + (e >> 1))) = (uint16_t)w;
+            } else {
+              uint32_t w = 0;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) w |= m_encode(mk, mn[i], am, ram) << (8 * i);
+              *gp(reinterpret_cast<uint32_t*>(D.m_q + e)) = w;
+            }
+            if ((wl & (G - 1)) == 0) gp(D.m_scale)[e >> lbm] = am;
+          }
+        }
+      }
+    }
+  }
+  if constexpr (MODE == 1) {
+    const float tot = wg_sum_f(sq, s4);
+    if (lane == 0) gp(ws)[W.npart + t] = tot;
+  }
+}
+
 // ------------------------------------------------------------ norm, Fira, step
 // _apply_update_pytorch with Fira (optimizer.py:796-810, 859-875).
 __global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, HyperF h) {
@@ -763,7 +940,8 @@ __global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, 
   const FWs W = fws_layout(D.B, D.R, D.C);
   float* ws = D.ws;
   double s = 0.0;
-  for (int64_t k = threadIdx.x; k < W.nunit; k += 256) s += (double)gp(ws)[W.npart + k];
+  const int64_t np = D.tiled ? W.ntile : W.nunit;
+  for (int64_t k = threadIdx.x; k < np; k += 256) s += (double)gp(ws)[W.npart + k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
     float* sl = ws + W.scal;
@@ -800,7 +978,8 @@ __global__ __launch_bounds__(256) void k_fclip(const DescF* __restrict__ table, 
   const FWs W = fws_layout(D.B, D.R, D.C);
   float* ws = D.ws;
   double s = 0.0;
-  for (int64_t k = threadIdx.x; k < W.nunit; k += 256) s += (double)gp(ws)[W.npart + k];
+  const int64_t np = D.tiled ? W.ntile : W.nunit;
+  for (int64_t k = threadIdx.x; k < np; k += 256) s += (double)gp(ws)[W.npart + k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
     const float rms = sqrtf((float)s) / (float)sqrt((double)D.numel);
@@ -818,29 +997,56 @@ static int launch_stats(bool psq, const DescF* tab, int ntab, int64_t ntiles, hi
   return check_launch("k_fstats");
 }
 
+// Work split of the update passes: tensors with the tiled layout (k_fupdt,
+// over the statistics tiles) and the rest (k_fupdate, over flat units).
+struct UpdGrid {
+  int64_t ntiles, nunits;
+  bool any_tiled, any_flat;
+};
+
 template <typename T, int MODE, bool SR, bool CM>
-static int launch_update_m(int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h, hipStream_t st) {
-  const dim3 g((unsigned)nunits), b(256);
-  if constexpr (CM) {
-    if (mk == 1) hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
-    else hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
-  } else {
-    switch (mk) {
-      case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
-      case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
-      default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
+static int launch_update_m(int mk, const DescF* tab, int ntab, const UpdGrid& ug, const HyperF& h,
+                           hipStream_t st) {
+  const dim3 b(256);
+  if (ug.any_tiled) {
+    const dim3 g((unsigned)ug.ntiles);
+    if constexpr (CM) {
+      if (mk == 1) hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
+      else hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
+    } else {
+      switch (mk) {
+        case 0: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
+        case 1: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
+        default: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
+      }
     }
+    int rc = check_launch("k_fupdt");
+    if (rc) return rc;
   }
-  return check_launch("k_fupdate");
+  if (ug.any_flat) {
+    const dim3 g((unsigned)ug.nunits);
+    if constexpr (CM) {
+      if (mk == 1) hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
+      else hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
+    } else {
+      switch (mk) {
+        case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
+        case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
+        default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
+      }
+    }
+    return check_launch("k_fupdate");
+  }
+  return 0;
 }
 
 template <typename T, bool SR, bool CM>
-static int launch_update(int mode, int mk, const DescF* tab, int ntab, int64_t nunits, const HyperF& h,
+static int launch_update(int mode, int mk, const DescF* tab, int ntab, const UpdGrid& ug, const HyperF& h,
                          hipStream_t st) {
   switch (mode) {
-    case 0: return launch_update_m<T, 0, SR, CM>(mk, tab, ntab, nunits, h, st);
-    case 1: return launch_update_m<T, 1, false, CM>(mk, tab, ntab, nunits, h, st);
-    default: return launch_update_m<T, 2, SR, CM>(mk, tab, ntab, nunits, h, st);
+    case 0: return launch_update_m<T, 0, SR, CM>(mk, tab, ntab, ug, h, st);
+    case 1: return launch_update_m<T, 1, false, CM>(mk, tab, ntab, ug, h, st);
+    default: return launch_update_m<T, 2, SR, CM>(mk, tab, ntab, ug, h, st);
   }
 }
 
@@ -864,14 +1070,14 @@ static int launch_finish(int bits, const DescF* tab, int ntab, int64_t nfblk, co
 // stats, finish, [U norm + k_fclip when d > 0], k_came1, confidence finish,
 // [update norm + k_fnorm with Fira], update.
 template <typename T, bool SR>
-static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits, int64_t nfblk, int vbits,
+static int run_group(const DescF* tab, int ntab, int64_t ntiles, const UpdGrid& ug, int64_t nfblk, int vbits,
                      int cbits, bool clip, const HyperF& h, hipStream_t st) {
   int rc = launch_stats<T>(h.scale_param != 0, tab, ntab, ntiles, st);
   if (rc) return rc;
   if ((rc = launch_finish<false>(vbits, tab, ntab, nfblk, h, st))) return rc;
   if (h.came) {
     if (h.d > 0.0f) {
-      if ((rc = launch_update<T, false, false>(1, 0, tab, ntab, nunits, h, st))) return rc;
+      if ((rc = launch_update<T, false, false>(1, 0, tab, ntab, ug, h, st))) return rc;
       hipLaunchKernelGGL(k_fclip, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
       if ((rc = check_launch("k_fclip"))) return rc;
     }
@@ -879,17 +1085,17 @@ static int run_group(const DescF* tab, int ntab, int64_t ntiles, int64_t nunits,
     else hipLaunchKernelGGL((k_came1<T, 2>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     if ((rc = check_launch("k_came1"))) return rc;
     if ((rc = launch_finish<true>(cbits, tab, ntab, nfblk, h, st))) return rc;
-    if (!h.fira) return launch_update<T, SR, true>(0, h.mk, tab, ntab, nunits, h, st);
-    if ((rc = launch_update<T, false, true>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
+    if (!h.fira) return launch_update<T, SR, true>(0, h.mk, tab, ntab, ug, h, st);
+    if ((rc = launch_update<T, false, true>(1, h.mk, tab, ntab, ug, h, st))) return rc;
     hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
     if ((rc = check_launch("k_fnorm"))) return rc;
-    return launch_update<T, SR, true>(2, h.mk, tab, ntab, nunits, h, st);
+    return launch_update<T, SR, true>(2, h.mk, tab, ntab, ug, h, st);
   }
-  if (!clip) return launch_update<T, SR, false>(0, h.mk, tab, ntab, nunits, h, st);
-  if ((rc = launch_update<T, false, false>(1, h.mk, tab, ntab, nunits, h, st))) return rc;
+  if (!clip) return launch_update<T, SR, false>(0, h.mk, tab, ntab, ug, h, st);
+  if ((rc = launch_update<T, false, false>(1, h.mk, tab, ntab, ug, h, st))) return rc;
   hipLaunchKernelGGL(k_fnorm, dim3((unsigned)ntab), dim3(256), 0, st, tab, h);
   if ((rc = check_launch("k_fnorm"))) return rc;
-  return launch_update<T, SR, false>(2, h.mk, tab, ntab, nunits, h, st);
+  return launch_update<T, SR, false>(2, h.mk, tab, ntab, ug, h, st);
 }
 
 static int mk_code(int mbits, int mmode) {
@@ -939,6 +1145,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
   int64_t tiles = 0, units = 0, fblks = 0;
+  bool any_tiled = false, any_flat = false;
   const size_t esz = dtype == A8_F32 ? 4 : 2;
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor2d& t = tensors[i];
@@ -968,6 +1175,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     D.B = t.batch; D.R = t.rows; D.C = t.cols; D.numel = numel;
     D.sr_seed = t.sr_seed;
     D.vec4 = ((t.cols * esz) % 16 == 0) ? 1 : 0;
+    D.tiled = (t.cols % 4 == 0) && (!has_m || (m_block_size <= 256 && t.cols % m_block_size == 0)) ? 1 : 0;
+    (D.tiled ? any_tiled : any_flat) = true;
     const FWs W = fws_layout(t.batch, t.rows, t.cols);
     D.tile_begin = tiles;
     D.unit_begin = units;
@@ -1001,14 +1210,15 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.sr_step = sr_step;
   const bool clip = d > 0.0f || fira;
   const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
+  const UpdGrid ug{tiles, units, any_tiled, any_flat};
   switch (dtype) {
-    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
+    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
     case A8_BF16:
-      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st)
-                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st)
+                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
     default:
-      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st)
-                        : run_group<__half, false>(dt, ntensors, tiles, units, fblks, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st)
+                        : run_group<__half, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
   }
 }
 

@@ -337,7 +337,47 @@ DEFAULTS = dict(lr=1e-2, beta1=None, beta2=None, beta2_decay=-0.8, beta3=None, e
                 scale_parameter=True, factored=True, quantize=True, block_size=2048,
                 m_block_size=256, m_quant_type="uf8", v_quant_type="al8", c_quant_type=None,
                 min_8bit_size=4096, scale_weight_decay=True, enable_fira_for_adafactor=False,
-                fira_margin=0.01, lag_norm=False, momentum_only_1d=None, bias_correction=None)
+                fira_margin=0.01, lag_norm=False, momentum_only_1d=None, bias_correction=None,
+                apollo_rank=0, apollo_update_proj_gap=200, apollo_scale_type="channel",
+                apollo_scale=1.0, apollo_scale_front=False, apollo_eps=1e-6, apollo_factorize=False,
+                apollo_cache_proj=False, enable_fira_for_apollo=True,
+                stochastic_round_writeback=False)
+
+ADV_DEFAULT = 0xF   # optimizer.py:26
+
+
+def stable_randn(shape, seed, device=None, dtype=torch.float32):
+    """optimizer.py:139-149 (the tests install inputs.make_proj in its place)."""
+    dev = device if device is not None else torch.device("cpu")
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(shape, generator=gen, device=dev, dtype=dtype)
+
+
+def next_seed(seed: int, adv: int = ADV_DEFAULT) -> int:
+    """optimizer.py:152-155."""
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(0, torch.iinfo(torch.int64).max, (adv,), generator=gen).tolist()[-1]
+
+
+def apollo_proj_T(st, shape, step, cache):
+    """_get_apollo_proj_matrix, optimizer.py:2557-2584."""
+    rank, gap = int(st["apollo_rank"]), int(st["apollo_update_proj_gap"])
+    last = int(st.get("last_proj_step", -gap))
+    refresh = (step - last) >= gap
+    if not refresh and cache and st.get("apollo_proj_matrix_T") is not None:
+        return st["apollo_proj_matrix_T"]
+    if refresh:
+        st["current_proj_seed"] = int(st["apollo_seed"])
+        st["apollo_seed"] = next_seed(st["current_proj_seed"])
+        st["last_proj_step"] = step
+    R, C = shape[-2], shape[-1]
+    m_shape = (rank, C) if R >= C else (R, rank)
+    seed = st.get("current_proj_seed", st["apollo_seed"])
+    proj = stable_randn(m_shape, seed=seed, device=torch.device("cpu"), dtype=torch.float32) / math.sqrt(rank)
+    proj_T = proj.T.to(torch.float32).contiguous()
+    if cache:
+        st["apollo_proj_matrix_T"] = proj_T
+    return proj_T
 
 
 class OracleOptimizer:
@@ -356,6 +396,7 @@ class OracleOptimizer:
                 raise KeyError(k)
             self.hp[k] = v
         self.state: Dict[Any, Dict[str, Any]] = {id(p): {} for p in self.params}
+        self.apollo_seed_counter = 1
 
     # optimizer.py:1618-1743 (fresh-state branch only)
     def _init_state(self, p, st):
@@ -373,6 +414,20 @@ class OracleOptimizer:
             if h["beta1"] is not None:
                 init_m(st, p.numel(), p.shape, h["m_block_size"], mqt, use_quant)
             return
+        if h["apollo_rank"] > 0 and p.dim() >= 2:   # optimizer.py:1725-1745
+            gap = h["apollo_update_proj_gap"]
+            st["apollo_seed"] = self.apollo_seed_counter
+            self.apollo_seed_counter += 1
+            st["apollo_rank"] = h["apollo_rank"]
+            st["apollo_factorize"] = h["apollo_factorize"]
+            st["beta3"] = h["beta3"]
+            st["apollo_update_proj_gap"] = gap
+            st["last_proj_step"] = -gap
+            st["apollo_proj_matrix_T"] = None
+            st["m_quant_type"] = mqt
+            for k in ("v_low_q", "v_low_scale", "v_low_min_log", "v_low_shape", "v_low_pad", "v_low"):
+                st[k] = None
+            return
         if p.dim() >= 2 and h["factored"]:
             R, C = p.shape[-2], p.shape[-1]
             rs = list(p.shape[:-2]) + [R, 1]
@@ -389,6 +444,9 @@ class OracleOptimizer:
             if h["beta1"] is not None:
                 init_m(st, p.numel(), p.shape, h["m_block_size"], mqt, use_quant)
 
+    def _update_apollo(self, p, grad, st):
+        apollo_update(self, p, grad, st)
+
     @torch.no_grad()
     def step(self):
         for p in self.params:
@@ -397,7 +455,10 @@ class OracleOptimizer:
             st = self.state[id(p)]
             if not st:
                 self._init_state(p, st)
-            self._update(p, p.grad, st)
+            if self.hp["apollo_rank"] > 0 and "apollo_seed" in st:
+                self._update_apollo(p, p.grad, st)
+            else:
+                self._update(p, p.grad, st)
 
     def _update(self, p, grad, st):  # optimizer.py:1944-2552, CPU branches
         h = self.hp
@@ -568,6 +629,144 @@ class OracleOptimizer:
             u = g32 * inv_row
             u.mul_(inv_col)
             apply_update(p, u, alpha, st, d, fira, margin)
+
+
+def m_ema_prefix(st, x, beta1, mqt, m_block, prefix):
+    """``_m_ema_pytorch`` with a state prefix (optimizer.py:690-700)."""
+    qk, sk = f"{prefix}_q", f"{prefix}_scale"
+    if qk in st and st[qk] is not None:
+        m = m_dequantize(st[qk], st[sk], x.numel(), m_block, mqt).view(x.shape)
+    else:
+        m = torch.zeros_like(x)
+    m.lerp_(x, 1.0 - beta1)
+    st[qk], st[sk] = m_quantize(m, mqt, m_block)
+    return m
+
+
+def init_m_prefix(st, numel, m_block, mqt, prefix):
+    """``_m_init_state`` with a prefix (optimizer.py:574-590), quantised codecs."""
+    padded = ((numel + m_block - 1) // m_block) * m_block
+    if m_bits_of(mqt) == 4:
+        st[f"{prefix}_q"] = torch.full((padded // 2,), 0x88 if mqt == "uf4" else 0x77, dtype=torch.uint8)
+    else:
+        st[f"{prefix}_q"] = torch.full((padded,), 128 if mqt == "uf8" else 127, dtype=torch.uint8)
+    st[f"{prefix}_scale"] = torch.ones(padded // m_block, dtype=torch.float32)
+    st["m_block_size"] = m_block
+    st["m_quant_type"] = mqt
+
+
+@torch.no_grad()
+def apollo_update(opt, p, grad, st):
+    """``_update_param_apollo`` (optimizer.py:2587-3084), CPU branches, for the
+    non-factorised path without CAME (apollo_factorize=False, beta3=None) and
+    deterministic writeback."""
+    h = opt.hp
+    beta1, beta2, beta2_decay = h["beta1"], h["beta2"], h["beta2_decay"]
+    if h["apollo_factorize"] or h["beta3"] is not None:
+        raise NotImplementedError("oracle: factorised / CAME APOLLO")
+    if h["stochastic_round_writeback"] and p.dtype in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("oracle: SR writeback (its CPU RNG stream is not the GPU's)")
+    d, lr = h["d"], h["lr"]
+    eps2 = h["eps"][1]
+    gw = grad.float()
+    if gw.data_ptr() == grad.data_ptr():
+        gw = gw.clone()
+    if h["maximize"]:
+        gw.neg_()
+    torch.nan_to_num_(gw, nan=0.0, posinf=0.0, neginf=0.0)
+    pw = p.data
+    if pw.dim() > 2:
+        pw = pw.reshape(pw.shape[0], -1)
+        gw = gw.reshape(gw.shape[0], -1)
+    step = st["step"] + 1
+    st["step"] = step
+    vqt = st.get("v_quant_type", "al8")
+    mqt = st.get("m_quant_type", "uf8") if beta1 is not None else "uf8"
+    bv = 1.0 - beta2 if beta2 is not None else math.pow(step, beta2_decay)
+    alpha, rho = compute_alpha(pw, lr, step, h["relative_step"], h["scale_parameter"], eps2)
+    projT = apollo_proj_T(st, gw.shape, step, h["apollo_cache_proj"])
+    R, C = gw.shape[-2], gw.shape[-1]
+    right = R >= C
+    fira = h["enable_fira_for_apollo"]
+    need_norm = fira or d > 0
+    glow = (torch.matmul(gw, projT) if right else torch.matmul(projT, gw)).float()
+
+    first = st.get("v_low_q") is None and st.get("v_low") is None
+    quant = st.get("is_quantized", False)
+    bs = st.get("block_size", h["block_size"])
+    aeps = h["apollo_eps"]
+    eps_sq = max(aeps * aeps, LOG_QUANT_FLOOR)
+    lf = math.log2(eps_sq)
+    if first:
+        vinit = glow.flatten().square() * bv
+        if quant and vqt != "fp32":
+            quant_v(st, "v_low", vinit, bs, vqt)
+        else:
+            st["v_low"] = vinit
+        vdeq = vinit
+    elif quant and vqt != "fp32":
+        vd = deq_v(st, "v_low")
+        vd.lerp_(glow.flatten().square(), bv)
+        quant_v(st, "v_low", vd, bs, vqt, floor=lf)
+        vdeq = vd
+    else:
+        st["v_low"].lerp_(glow.flatten().square(), bv)
+        vdeq = st["v_low"]
+
+    if beta1 is not None:
+        if not quant or mqt == "fp32":
+            if st.get("m_low") is None:
+                st["m_low"] = torch.zeros_like(glow)
+            st["m_low"].lerp_(glow, 1.0 - beta1)
+            mdeq = st["m_low"]
+        else:
+            mbs = st.get("m_block_size", h["m_block_size"])
+            if st.get("m_low_q") is None:
+                init_m_prefix(st, glow.numel(), mbs, mqt, "m_low")
+            mdeq = m_ema_prefix(st, glow, beta1, mqt, mbs, "m_low")
+        upd = mdeq / (torch.sqrt(vdeq.view_as(glow)) + aeps)
+    else:
+        upd = glow / (torch.sqrt(vdeq).view_as(glow) + aeps)
+
+    channel = h["apollo_scale_type"] == "channel"
+    nd = -1 if right else -2
+    if channel:
+        s = upd.norm(dim=nd, keepdim=True) / (glow.norm(dim=nd, keepdim=True) + 1e-8)
+    else:
+        s = upd.norm() / (glow.norm() + 1e-8)
+    sv = math.sqrt(h["apollo_scale"])
+    if h["apollo_scale_front"]:
+        s = s * sv
+    if need_norm:
+        if channel:
+            ngsq = torch.linalg.vector_norm(gw, ord=2, dim=nd, keepdim=True, dtype=torch.float32).square()
+            nun = torch.sqrt((ngsq * s.square()).sum())
+        else:
+            nun = torch.linalg.vector_norm(gw, ord=2, dtype=torch.float32) * s
+    if fira:
+        final = s * fira_scale(st, nun, h["fira_margin"], key="scaled_grad_norm_prev")
+    else:
+        final = s
+    if not h["apollo_scale_front"]:
+        final = final * sv
+    denom = torch.clamp_min(nun / (math.sqrt(pw.numel()) * d), 1.0) if d > 0 else _one()
+    wd = h["weight_decay"]
+    decay = (1.0 - ((alpha if h["scale_weight_decay"] else rho) * wd)) if wd != 0 else None
+    us = -alpha / denom
+    if beta1 is not None and not h["relative_step"]:
+        bc_on = True if h["bias_correction"] is None else h["bias_correction"]
+        if bc_on:
+            bc1 = 1.0 - beta1 ** step
+            if beta2 is not None:
+                us = us * (math.sqrt(1.0 - beta2 ** step) / bc1)
+            else:
+                us = us / bc1
+    if decay is not None:
+        pw.mul_(decay)
+    if channel:
+        pw.addcmul_(gw, final.to(gw.dtype), value=us)
+    else:
+        pw.add_(gw, alpha=us * final)
 
 
 def reference_adamw_block_bytes(numel: int, block_size: int = 2048, m_block: int = 256) -> float:

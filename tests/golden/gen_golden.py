@@ -22,7 +22,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
-from inputs import make_grad, make_param  # noqa: E402
+from inputs import make_grad, make_param, make_proj  # noqa: E402
 
 ADAMW = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=False,
              relative_step=False, scale_parameter=False, scale_weight_decay=False,
@@ -46,6 +46,15 @@ P_FACT = [((64, 300), "normal"), ((300, 64), "normal"), ((2, 40, 130), "normal")
           ((64,), "ones")]
 P_EMB = [((500, 64), "normal"), ((64, 48), "normal")]
 P_CAME = [((64, 300), "normal"), ((128, 64), "normal"), ((64,), "ones")]
+# APOLLO: a right-side (R >= C) and a left-side (R < C) matrix, and a vector that
+# takes the full-rank route of the same group.
+P_APOLLO = [((128, 96), "normal"), ((64, 160), "normal"), ((96,), "ones")]
+APOLLO = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=False,
+              relative_step=False, scale_parameter=False, scale_weight_decay=False, d=0.0,
+              eps=(1e-6, 1e-3), apollo_eps=1e-6, apollo_factorize=False, apollo_update_proj_gap=3,
+              apollo_scale_type="channel", apollo_scale=1.0, apollo_scale_front=False,
+              apollo_cache_proj=True, enable_fira_for_apollo=True, apollo_rank=16,
+              block_size=128, m_block_size=32)
 
 CONFIGS = [
     # name, kwargs, params, grad kind, steps, save steps
@@ -76,6 +85,14 @@ CONFIGS = [
      "logscale", 10, (1, 2, 10)),
     ("came_uf8_al8", dict(CAME, lr=1e-4), P_CAME, "normal_zeros", 4, (1, 4)),
     ("sgd_momentum_uf8", dict(SGD, lr=1e-2, beta1=0.9), P_SMALL, "normal_zeros", 4, (1, 4)),
+    ("apollo_uf8_al8", dict(APOLLO, lr=1e-3), P_APOLLO, "normal_zeros", 7, (1, 3, 4, 7)),
+    ("apollo_tensor_clip_wd", dict(APOLLO, lr=1e-3, apollo_scale_type="tensor", d=1.0,
+                                   weight_decay=0.1, scale_weight_decay=True, apollo_scale=2.0,
+                                   apollo_scale_front=True, enable_fira_for_apollo=False,
+                                   apollo_cache_proj=False, m_quant_type="uf4"),
+     P_APOLLO, "student_t", 5, (1, 5)),
+    ("apollo_fp32_states", dict(APOLLO, lr=1e-3, quantize=False), P_APOLLO, "logscale", 4, (1, 4)),
+    ("apollo_bf16_det", dict(APOLLO, lr=1e-3), P_APOLLO, "normal_zeros", 4, (1, 4), "bf16"),
 ]
 
 
@@ -86,22 +103,23 @@ def _to_np(v):
     return v.detach().cpu().contiguous().numpy().copy()
 
 
-def run_config(mod, name, kwargs, pspecs, gkind, steps, save_steps, outdir, seed=0):
+def run_config(mod, name, kwargs, pspecs, gkind, steps, save_steps, pdtype="f32", outdir=".", seed=0):
+    dt = torch.bfloat16 if pdtype == "bf16" else torch.float32
     params = []
     for i, (shape, init) in enumerate(pspecs):
-        params.append(torch.nn.Parameter(make_param(shape, i, seed, kind=init)))
+        params.append(torch.nn.Parameter(make_param(shape, i, seed, kind=init).to(dt)))
     opt = mod.Adafactor8Bit(params, use_cuda_kernel=False, **kwargs)
     arrays = {}
     meta = {"config": name, "kwargs": {k: (list(v) if isinstance(v, tuple) else v)
                                        for k, v in kwargs.items()},
             "params": [[list(s), init] for s, init in pspecs], "grad_kind": gkind,
-            "seed": seed, "steps": steps, "save_steps": list(save_steps),
+            "seed": seed, "steps": steps, "save_steps": list(save_steps), "dtype": pdtype,
             "torch": torch.__version__, "scalars": {}}
     for i, p in enumerate(params):
         arrays[f"init/p{i}"] = _to_np(p.data)
     for t in range(1, steps + 1):
         for i, p in enumerate(params):
-            p.grad = make_grad(tuple(p.shape), i, t, seed, kind=gkind)
+            p.grad = make_grad(tuple(p.shape), i, t, seed, kind=gkind).to(dt)
         opt.step()
         if t in save_steps:
             for i, p in enumerate(params):
@@ -125,6 +143,8 @@ def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     sys.path.insert(0, ref)
     import adafactor8bit.optimizer as mod  # the reference package
+    # APOLLO projections from a host-independent generator (see inputs.make_proj)
+    mod.stable_randn = make_proj
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     outdir = HERE
     only = set(sys.argv[2:])

@@ -66,3 +66,16 @@ def make_grad(shape, idx: int, step: int, seed: int = 0, kind: str = "normal_zer
         raise ValueError(kind)
     x = np.ascontiguousarray(x.astype(np.float32))
     return torch.from_numpy(x).to(dtype)
+
+
+def make_proj(shape, seed: int, device=None, dtype=torch.float32):
+    """Stand-in for the reference's ``stable_randn(shape, seed, device, dtype)``
+    (optimizer.py:139-149) with a host-independent stream: N(0, 1) from PCG64
+    keyed by the 64-bit seed.  The golden generator and the tests install it in
+    place of the torch-generator version, whose CPU and GPU streams differ, so
+    the reference's trajectories and this build's see the same projection."""
+    s = int(seed) & 0xFFFFFFFFFFFFFFFF
+    rng = np.random.Generator(np.random.PCG64([s & 0xFFFFFFFF, s >> 32, 0xA9]))
+    x = np.ascontiguousarray(rng.standard_normal(size=tuple(shape), dtype=np.float32))
+    t = torch.from_numpy(x).to(dtype)
+    return t if device is None else t.to(device)

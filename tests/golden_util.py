@@ -25,7 +25,12 @@ def load(name):
     return meta, kw, z
 
 
-def init_params(meta, device="cpu", dtype=torch.float32):
+def param_dtype(meta):
+    return torch.bfloat16 if meta.get("dtype", "f32") == "bf16" else torch.float32
+
+
+def init_params(meta, device="cpu", dtype=None):
+    dtype = param_dtype(meta) if dtype is None else dtype
     out = []
     for i, (shape, init) in enumerate(meta["params"]):
         out.append(torch.nn.Parameter(make_param(tuple(shape), i, meta["seed"], kind=init)
@@ -34,7 +39,7 @@ def init_params(meta, device="cpu", dtype=torch.float32):
 
 
 def grads_for(meta, params, step):
-    return [make_grad(tuple(p.shape), i, step, meta["seed"], kind=meta["grad_kind"])
+    return [make_grad(tuple(p.shape), i, step, meta["seed"], kind=meta["grad_kind"]).to(param_dtype(meta))
             for i, p in enumerate(params)]
 
 

@@ -51,6 +51,15 @@ class Tensor2D(ctypes.Structure):
                 ("batch", _c_i64), ("rows", _c_i64), ("cols", _c_i64), ("sr_seed", _c_u64)]
 
 
+class ApolloTensor(ctypes.Structure):
+    """Mirror of ``a8_apollo_tensor``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("rows", _c_i64), ("cols", _c_i64),
+                ("proj_t", _c_vp), ("rank", _c_i64), ("v_q", _c_vp), ("v_scale", _c_vp),
+                ("v_min_log", _c_vp), ("v_fp32", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
+                ("m_fp32", _c_vp), ("fira_prev", _c_vp), ("has_fira_prev", _c_i), ("lr", _c_vp),
+                ("workspace", _c_vp), ("sr_seed", _c_u64)]
+
+
 _SIGS = {
     "a8_last_error": (ctypes.c_char_p, []),
     "a8_version": (ctypes.c_char_p, []),
@@ -78,6 +87,10 @@ _SIGS = {
                                 _c_vp]),
     "a8_factored_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "a8_table_bytes_2d": (_c_i64, [_c_i]),
+    "a8_apollo_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_i, _c_d, _c_d, _c_i, _c_f,
+                              _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i, _c_f, _c_f,
+                              _c_f, _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_u64, _c_vp]),
+    "a8_apollo_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
 }
 
 _LIB = None

@@ -13,6 +13,7 @@ PyTorch fallback.  Quantised codes follow the reference's PyTorch numerics
 Parameters that share a step counter and hyper-parameters are updated by one
 multi-tensor launch per group instead of one launch per parameter.
 """
+import ctypes
 import logging
 import math
 from typing import Any, Dict, Iterable, Optional, Tuple, Union
@@ -39,6 +40,24 @@ _F32 = np.float32
 
 def _f32(x) -> float:
     return float(_F32(x))
+
+
+_ADV_DEFAULT = 0xF   # optimizer.py:26
+
+
+def stable_randn(shape, seed: int, device=None, dtype=torch.float32) -> Tensor:
+    """optimizer.py:139-149: a reproducible N(0, 1) tensor from a torch generator
+    seeded on ``device`` (the projection matrices of APOLLO)."""
+    if device is None:
+        device = torch.device("cuda" if torch.cuda.is_available() else "cpu")
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return torch.randn(shape, generator=gen, device=device, dtype=dtype)
+
+
+def next_seed(seed: int, adv: int = _ADV_DEFAULT) -> int:
+    """optimizer.py:152-155: advance a seed by consuming ``adv`` random integers."""
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(0, torch.iinfo(torch.int64).max, (adv,), generator=gen).tolist()[-1]
 
 
 class Adafactor8Bit(Optimizer):
@@ -287,7 +306,8 @@ class Adafactor8Bit(Optimizer):
         batches: Dict[tuple, list] = {}
         for p, g, st in zip(params, grads, states):
             if apollo_rank > 0 and "apollo_seed" in st:
-                raise NotImplementedError("APOLLO path is not available in this build yet")
+                _run_apollo(self, p, g, st, group)
+                continue
             plan = _plan_param(p, g, st, group)
             key = plan.batch_key()
             if key is None:
@@ -710,6 +730,147 @@ def _run_batch(opt, key, plans):
             strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+
+
+def _apollo_proj(st, shape, step, device, cache):
+    """_get_apollo_proj_matrix (optimizer.py:2557-2584): the projection P^T of this
+    step and whether it was (re)generated."""
+    rank = int(st["apollo_rank"])
+    gap = int(st["apollo_update_proj_gap"])
+    last = int(st.get("last_proj_step", -gap))
+    refresh = (step - last) >= gap
+    if not refresh and cache and st.get("apollo_proj_matrix_T") is not None:
+        return st["apollo_proj_matrix_T"], False
+    if refresh:
+        st["current_proj_seed"] = int(st["apollo_seed"])
+        st["apollo_seed"] = next_seed(st["current_proj_seed"])
+        st["last_proj_step"] = step
+    R, C = shape[-2], shape[-1]
+    m_shape = (rank, C) if R >= C else (R, rank)
+    seed = st.get("current_proj_seed", st["apollo_seed"])
+    proj = stable_randn(m_shape, seed=seed, device=device, dtype=torch.float32)
+    # IEEE division by a device scalar (a Python scalar would become a reciprocal multiply)
+    proj = proj / torch.tensor(math.sqrt(rank), dtype=torch.float32, device=device)
+    proj_T = proj.T.to(torch.float32).contiguous()
+    if cache:
+        st["apollo_proj_matrix_T"] = proj_T
+    return proj_T, True
+
+
+def _run_apollo(opt, p, grad, st, group):
+    """One APOLLO parameter (optimizer.py:2587-3084, non-factorised, beta3 = None):
+    host scalars and state, then a8_apollo_step (projection GEMM, low-rank V/M,
+    channel scale, Fira, full-rank writeback)."""
+    beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
+    if group.get("apollo_factorize", False) or group.get("beta3") is not None:
+        raise NotImplementedError("adafactor8bit: factorised / CAME APOLLO is not available in this build yet")
+    if p.dtype not in (torch.float32, torch.bfloat16):
+        raise NotImplementedError("adafactor8bit: APOLLO needs fp32 or bf16 parameters")
+    if not p.is_contiguous():
+        raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
+    g = grad if grad.is_contiguous() else grad.contiguous()
+    if g.dtype != p.dtype:
+        if p.dtype == torch.float32:
+            g = g.float()
+        else:
+            raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    if group["maximize"]:
+        g = g.neg()
+    dev = p.device
+    R = p.shape[0]
+    C = p.numel() // R
+    rank = int(st["apollo_rank"])
+    step = st["step"] + 1
+    st["step"] = step
+    vqt = st.get("v_quant_type", "al8")
+    mqt = st.get("m_quant_type", "uf8") if beta1 is not None else "uf8"
+    beta_val = 1.0 - beta2 if beta2 is not None else math.pow(step, beta2_decay)
+    lr = group["lr"]
+    rho_t = None
+    if isinstance(lr, Tensor):
+        rho_t = lr.to(device=dev, dtype=torch.float32).reshape(())
+        if group["relative_step"]:
+            rho_t = torch.minimum(torch.tensor(float(step), device=dev).rsqrt(), rho_t)
+        rho_t = rho_t.contiguous()
+        rho_val = 0.0
+    else:
+        rho_val = _f32(min(lr, 1.0 / math.sqrt(step)) if group["relative_step"] else lr)
+    proj_T, fresh = _apollo_proj(st, (R, C), step, dev, group.get("apollo_cache_proj", False))
+    right = R >= C
+    n_low = R * rank if right else rank * C
+    quant = st.get("is_quantized", False)
+    bs = st.get("block_size", group.get("block_size", 2048))
+    first = st.get("v_low_q") is None and st.get("v_low") is None
+    aeps = group.get("apollo_eps", 1e-6)
+    eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
+    vbits = 0 if (not quant or vqt == "fp32") else (16 if vqt == "al16" else 8)
+    if first:   # optimizer.py:2770-2779 creates the low-rank V state on the first step
+        if vbits:
+            S.init_v_state(st, "v_low", (n_low,), bs, dev, vqt)
+        else:
+            st["v_low"] = torch.zeros(n_low, dtype=torch.float32, device=dev)
+    has_m = beta1 is not None
+    m_fp32 = has_m and (not quant or mqt == "fp32")
+    mbs = st.get("m_block_size", group.get("m_block_size", 256))
+    if has_m:
+        if m_fp32:
+            if st.get("m_low") is None:
+                st["m_low"] = torch.zeros((R, rank) if right else (rank, C), dtype=torch.float32, device=dev)
+        elif st.get("m_low_q") is None:
+            S.m_init_state(st, n_low, mbs, mqt, dev, prefix="m_low")
+    fira = bool(group.get("enable_fira_for_apollo", True))
+    has_prev = 0
+    if fira:
+        prev = st.get("scaled_grad_norm_prev")
+        if prev is None:
+            st["scaled_grad_norm_prev"] = torch.zeros((), dtype=torch.float32, device=dev)
+        else:
+            if not torch.is_tensor(prev) or prev.device != dev or prev.dtype != torch.float32:
+                st["scaled_grad_norm_prev"] = torch.as_tensor(prev, dtype=torch.float32).to(dev).reshape(())
+            has_prev = 1
+    channel = group.get("apollo_scale_type", "channel") == "channel"
+    bias_mode, bias_fac = 0, 1.0
+    if has_m and not group["relative_step"]:
+        bc_on = True if group.get("bias_correction") is None else group.get("bias_correction")
+        if bc_on:
+            bc1 = 1.0 - beta1 ** step
+            if beta2 is not None:
+                bias_mode, bias_fac = 1, _f32(math.sqrt(1.0 - beta2 ** step) / bc1)
+            else:
+                bias_mode, bias_fac = 2, _f32(bc1)
+    wd = group["weight_decay"]
+    wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
+    L = nat.lib()
+    key = (dev, "apollo", id(p))
+    ent = opt._ws.get(key)
+    nws = int(L.a8_apollo_workspace_floats(R, C, rank, int(channel)))
+    if ent is None or ent["ws"].numel() < nws:
+        ent = {"ws": torch.empty(nws, dtype=torch.float32, device=dev), "proj": None}
+        opt._ws[key] = ent
+    if ent["proj"] is None or ent["proj"] != (proj_T.data_ptr(), proj_T._version):
+        fresh = True
+    ent["proj"] = (proj_T.data_ptr(), proj_T._version)
+    sr = group.get("stochastic_round_writeback", False) and p.dtype == torch.bfloat16
+    t = nat.ApolloTensor(
+        p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank,
+        nat.ptr(st.get("v_low_q")) if vbits else None, nat.ptr(st.get("v_low_scale")) if vbits else None,
+        nat.ptr(st.get("v_low_min_log")) if vbits else None, None if vbits else st["v_low"].data_ptr(),
+        nat.ptr(st.get("m_low_q")) if (has_m and not m_fp32) else None,
+        nat.ptr(st.get("m_low_scale")) if (has_m and not m_fp32) else None,
+        st["m_low"].data_ptr() if m_fp32 else None,
+        nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
+        nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)))
+    rc = L.a8_apollo_step(
+        nat.dtype_code(p.dtype), int(sr), ctypes.byref(t), int(first), int(fresh), float(beta_val),
+        float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), vbits, int(bs),
+        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs),
+        int(channel), float(group.get("apollo_scale", 1.0)), int(bool(group.get("apollo_scale_front", False))),
+        int(fira), float(group.get("fira_margin", 0.01)), float(group["d"]), float(rho_val),
+        _f32(group["eps"][1]), int(bool(group["scale_parameter"])), bias_mode, float(bias_fac), _f32(wd),
+        wd_mode, int(step), nat.stream_of(dev))
+    nat.check(rc, "a8_apollo_step")
+    if vbits:
+        _block_view(st, "v_low", bs)
 
 
 def _run_factored(opt, plans):

@@ -18,7 +18,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "adafactor8bit", "libadafactor8bit_amd.so")
-SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip", "a8_factored.hip"]
+SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip", "a8_factored.hip", "a8_apollo.hip"]
+LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = os.environ.get("A8_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -49,7 +50,7 @@ def build(verbose: bool = True) -> str:
         if p.wait() != 0:
             raise RuntimeError(f"hipcc failed on {src}")
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp] + objs
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp] + objs + LIBS
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.check_call(cmd)

@@ -36,4 +36,5 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 namespace a8 {
 // Codebook upload of the factored-step translation unit (called by a8_set_qmap).
 hipError_t factored_upload_qmap(const float* q8, const float* q4);
+hipError_t apollo_upload_qmap(const float* q8, const float* q4);
 }  // namespace a8

@@ -234,6 +234,50 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
 int64_t a8_factored_workspace_floats(int64_t batch, int64_t rows, int64_t cols);
 int64_t a8_table_bytes_2d(int ntensors);
 
+/* ---- APOLLO (low-rank projected AdamW) ------------------------------------
+ * One full-rank matrix (a 2-D view: rows x cols; higher-rank parameters are
+ * viewed as [shape[0], -1]) per call. */
+typedef struct a8_apollo_tensor {
+  void* param;             /* fp32 or bf16, rows x cols */
+  const void* grad;        /* same dtype as param */
+  int64_t rows, cols;
+  const float* proj_t;     /* projection P^T, fp32: right side (rows >= cols) [cols x rank],
+                              left side [rank x rows] (P = stable_randn / sqrt(rank)) */
+  int64_t rank;
+  void* v_q;               /* low-rank V: AL8 uint8 / AL16 int16 codes ... */
+  float* v_scale;
+  float* v_min_log;
+  float* v_fp32;           /* ... or fp32 v_low (NULL when coded) */
+  uint8_t* m_q;            /* low-rank M: codes + scale, or fp32 m_low */
+  float* m_scale;
+  float* m_fp32;
+  float* fira_prev;        /* scaled_grad_norm_prev (0-dim fp32 state) when Fira is on */
+  int has_fira_prev;       /* 0 on the first Fira step */
+  const float* lr;         /* device learning rate, or NULL for lr_val */
+  float* workspace;        /* a8_apollo_workspace_floats(rows, cols, rank, channel) floats */
+  uint64_t sr_seed;
+} a8_apollo_tensor;
+
+/* Replaces the APOLLO update of one parameter (_update_param_apollo,
+ * optimizer.py:2587-3084, non-factorised, beta3 = None; kernels
+ * fused_m_quantize_lerp kernels.cu:523-588, fused_log_quantize_lerp 340-517,
+ * compute_apollo_norms 2410-2453, apollo_apply_* 2638-3000; the projection GEMM
+ * torch.matmul at optimizer.py:2678-2681).  first_step: V initialised as
+ * g_low^2 * beta_val (AL floor -126); later steps lerp with floor log_floor
+ * (log2(max(apollo_eps^2, FLT_MIN))).  proj_fresh: P^T changed since the last
+ * call for this workspace (its bf16 split is recomputed).  has_m: beta1 is set;
+ * m_fp32 selects fp32 m_low.  channel: apollo_scale_type "channel" (else
+ * "tensor").  bias_mode 0/1/2: none / step *= bias_factor / step /= bias_factor.
+ * wd_mode 0/1/2: none / decay uses alpha / decay uses lr.  V block_size and
+ * m_block_size are powers of two (V: 128..2048, M: 32..2048). */
+int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int first_step, int proj_fresh,
+                   double beta_val, double beta1, int has_m, float apollo_eps, float log_floor, int v_bits,
+                   int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
+                   float apollo_scale, int scale_front, int fira, float fira_margin, float d, float lr_val,
+                   float eps2, int scale_parameter, int bias_mode, float bias_factor, float weight_decay,
+                   int wd_mode, uint64_t sr_step, void* stream);
+int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int channel);
+
 #ifdef __cplusplus
 }
 #endif

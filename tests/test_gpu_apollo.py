@@ -1,0 +1,288 @@
+"""APOLLO (low-rank projected Adafactor) on the GPU, against the reference.
+
+Golden trajectories (apollo_* fixtures, made by the reference's own
+``_update_param_apollo`` with the projection generator replaced by
+``inputs.make_proj``, which the test installs in the same place).
+
+The projection g_low = G P^T (right side, R >= C) or P^T G (left side) is a
+GEMM: the HIP path sums its K products in rocBLAS's order, the reference in
+its CPU BLAS's order.  On the right-side matrices of these fixtures the two
+orders agree bit for bit.  On the left side the two results differ at the
+ulp level.  That is why the tolerances below are looser than the 1-D path's:
+
+* V codes (AL8, low rank): every decoded value within two code steps
+  (2^(2 s / 254) - 1, relative) of the reference's decoded value.  At most 2%
+  of codes may differ, by at most 2.  The block's range is set by its smallest
+  nonzero g_low^2, which can be a cancelling sum with a large relative error.
+  So block scale / min_log are held to 2e-2 absolute (log2 units).
+* M codes: at most 2% differ, by at most 2.  Block scales within rtol 1e-5.
+* Parameters (fp32): within 1e-5 relative plus 2e-3 of the largest
+  displacement the reference's own steps made.  A flipped code moves one
+  element of the low-rank update by a code step.  That moves its channel's
+  norm ratio, which scales the whole channel's update.
+* Parameters (bf16, deterministic writeback): within two bf16 ulps of the
+  larger of the two values plus the fp32 bound (for values small next to their
+  update), and at most 1% of them not bit-equal.  An fp32 pre-rounding value a
+  few ulps off lands on the neighbouring bf16 value when it sits next to a
+  rounding midpoint.  Such a flip persists, and a later step can flip the
+  same element again: after 4 steps 0.3% of the elements differ, at most by 2
+  ulps.
+* Norms (scaled_grad_norm_prev): rtol 3e-5.  fp32 low-rank states: rtol 2e-6
+  plus 1e-6 of the state's largest magnitude.  The projection matrix:
+  bit-exact.
+
+The GEMM itself is pinned separately: g_low from the library is held to the
+deterministic error bound of a K-term fp32 dot product, (K + 2) u sum |g||p|,
+against an fp64 product.  For bf16 gradients the bound is three times that:
+P^T is split into three bf16 terms, each a GEMM of its own.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import golden_util as gu
+import inputs
+
+APOLLO = ["apollo_uf8_al8", "apollo_tensor_clip_wd", "apollo_fp32_states", "apollo_bf16_det"]
+
+
+@pytest.fixture
+def det_proj(monkeypatch):
+    import adafactor8bit.optimizer as O
+    monkeypatch.setattr(O, "stable_randn", inputs.make_proj)
+
+
+def _f32(a):
+    a = np.asarray(a)
+    if a.dtype == np.int16:   # bf16 stored as its bit pattern
+        return (a.view(np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+    return a
+
+
+def _t2np(t):
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy()
+    return t.numpy()
+
+
+def _al8_decode(q, scale, min_log):
+    q = np.asarray(q).astype(np.int64).reshape(scale.size, -1)
+    v = np.exp2((q - 1) * (scale.astype(np.float64)[:, None] / 254.0) + min_log.astype(np.float64)[:, None])
+    return np.where(q == 0, 0.0, v)
+
+
+def _cmp_params(name, key, mine, ref, init):
+    disp = float(np.abs(_f32(ref).astype(np.float64) - _f32(init)).max())
+    if ref.dtype == np.int16:
+        m, r = _f32(mine).astype(np.float64), _f32(ref).astype(np.float64)
+        big = np.maximum(np.maximum(np.abs(m), np.abs(r)), 1e-38)
+        ulp = np.exp2(np.floor(np.log2(big)) - 7)
+        # two bf16 ulps, plus the fp32 bound for values small next to their update
+        assert np.all(np.abs(m - r) <= 2 * ulp + 2e-3 * disp), f"{name} {key}: bf16 param beyond two ulps"
+        assert (mine != ref).mean() <= 1e-2, f"{name} {key}: {(mine != ref).mean():.2e} bf16 params differ"
+    else:
+        np.testing.assert_allclose(mine, ref, rtol=1e-5, atol=1e-8 + 2e-3 * disp, err_msg=f"{name} {key} param")
+
+
+def _cmp_state(name, key, st, z, zkeys):
+    for k in zkeys:
+        ref = z[f"{key}/{k}"]
+        assert k in st and st[k] is not None, f"{name} {key}: missing state {k}"
+        mine = st[k]
+        mine = mine.detach().cpu().numpy() if torch.is_tensor(mine) else np.asarray(mine)
+        assert mine.dtype == ref.dtype and mine.shape == ref.shape, (name, key, k, mine.dtype, ref.dtype)
+        msg = f"{name} {key}/{k}"
+        if k == "apollo_proj_matrix_T":
+            assert np.array_equal(mine, ref), msg
+        elif k.endswith("_q"):
+            frac, mx = gu.code_mismatch(mine, ref)
+            low_rank = k.startswith(("v_low", "m_low"))
+            allowed = 2e-2 if low_rank else 1e-4 + 1.0 / max(mine.size, 1)
+            assert mx <= 2 and frac <= allowed, f"{msg}: {frac:.2e} codes differ, max {mx}"
+            if k == "v_low_q":
+                dm = _al8_decode(mine, st["v_low_scale"].cpu().numpy(), st["v_low_min_log"].cpu().numpy())
+                dr = _al8_decode(ref, z[f"{key}/v_low_scale"], z[f"{key}/v_low_min_log"])
+                step2 = np.exp2(2.0 * z[f"{key}/v_low_scale"].astype(np.float64) / 254.0)[:, None] - 1.0
+                assert np.all(np.abs(dm - dr) <= step2 * np.abs(dr) + 1e-37), f"{msg}: decoded V"
+        elif k.startswith("v_low_") and (k.endswith("_scale") or k.endswith("_min_log")):
+            np.testing.assert_allclose(mine, ref, rtol=0, atol=2e-2, err_msg=msg)
+        elif k.endswith("_scale") or k.endswith("_min_log"):
+            np.testing.assert_allclose(mine, ref, rtol=1e-5, atol=0, err_msg=msg)
+        elif "norm" in k:
+            np.testing.assert_allclose(mine, ref, rtol=3e-5, atol=1e-30, err_msg=msg)
+        elif k == "step":
+            assert int(mine) == int(ref), msg
+        else:
+            floor = 1e-6 * float(np.abs(ref).max()) if ref.size else 0.0
+            np.testing.assert_allclose(mine, ref, rtol=2e-6, atol=1e-30 + floor, err_msg=msg)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", APOLLO)
+@pytest.mark.parametrize("multi", [True, False])
+def test_apollo_matches_golden(name, multi, det_proj):
+    from adafactor8bit import Adafactor8Bit
+    meta, kw, z = gu.load(name)
+    print(f"[apollo golden] {name} multi={multi}", flush=True)
+    params = gu.init_params(meta, device="cuda")
+    opt = Adafactor8Bit(params if multi else [{"params": [p]} for p in params], **kw)
+    for t in range(1, meta["steps"] + 1):
+        for p, g in zip(params, gu.grads_for(meta, params, t)):
+            p.grad = g.cuda()
+        opt.step()
+        if t not in meta["save_steps"]:
+            continue
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            key = f"s{t}/p{i}"
+            _cmp_params(name, key, _t2np(p), z[f"{key}/param"], z[f"init/p{i}"])
+            zkeys = [k[len(key) + 1:] for k in z.files if k.startswith(key + "/") and not k.endswith("/param")]
+            _cmp_state(name, key, opt.state[p], z, zkeys)
+
+
+def _apollo_kw(**over):
+    kw = dict(lr=1e-3, beta1=0.9, beta2=0.999, relative_step=False, scale_parameter=False, apollo_rank=32,
+              apollo_update_proj_gap=200, apollo_cache_proj=True, block_size=128, m_block_size=32)
+    kw.update(over)
+    return kw
+
+
+def _ws(opt, p):
+    ent = opt._ws[(p.device, "apollo", id(p))]
+    return ent["ws"].cpu().numpy()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(300, 200), (96, 260), (513, 7), (5, 1030)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_apollo_projection_error_bound(shape, dtype, det_proj):
+    """g_low from the library against an fp64 product of the same G and P^T."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[apollo gemm] {shape} {dtype}", flush=True)
+    R, C = shape
+    r = 32 if min(R, C) > 32 else 4
+    p = torch.nn.Parameter(inputs.make_param(shape, 0, 11).to("cuda", dtype))
+    g = inputs.make_grad(shape, 0, 1, 11, kind="student_t").to(dtype)
+    opt = Adafactor8Bit([p], **_apollo_kw(apollo_rank=r))
+    p.grad = g.cuda()
+    opt.step()
+    torch.cuda.synchronize()
+    pt = opt.state[p]["apollo_proj_matrix_T"].double().cpu().numpy()
+    G = g.double().numpy()
+    right = R >= C
+    exact = G @ pt if right else pt @ G
+    absb = np.abs(G) @ np.abs(pt) if right else np.abs(pt) @ np.abs(G)
+    K = C if right else R
+    n_low = exact.size
+    glow = _ws(opt, p)[:n_low].reshape(exact.shape).astype(np.float64)
+    terms = 1 if dtype == torch.float32 else 3
+    bound = terms * (K + 2) * 2.0 ** -24 * absb
+    assert np.all(np.abs(glow - exact) <= bound + 1e-30), float(np.max(np.abs(glow - exact) / (absb + 1e-30)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(128, 96), (64, 160)])
+def test_apollo_nonfinite_grad_equals_scrubbed(shape, det_proj):
+    """NaN / +-Inf gradient entries count as zero (optimizer.py:2606)."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[apollo nonfinite] {shape}", flush=True)
+    res = []
+    for bad in (True, False):
+        p = torch.nn.Parameter(inputs.make_param(shape, 0, 5).cuda())
+        opt = Adafactor8Bit([p], **_apollo_kw(apollo_rank=16))
+        for t in range(1, 4):
+            g = inputs.make_grad(shape, 0, t, 5)
+            flat = g.view(-1)
+            idx = torch.arange(t, flat.numel(), 97)
+            if bad:
+                flat[idx[0::3]] = float("nan")
+                flat[idx[1::3]] = float("inf")
+                flat[idx[2::3]] = float("-inf")
+            else:
+                flat[idx] = 0.0
+            p.grad = g.cuda()
+            opt.step()
+        torch.cuda.synchronize()
+        res.append((p.detach().cpu().numpy(), opt.state[p]["scaled_grad_norm_prev"].item()))
+    (pb, nb), (pg, ng) = res
+    init = inputs.make_param(shape, 0, 5).numpy()
+    disp = float(np.abs(pg - init).max())
+    assert np.all(np.isfinite(pb)) and math.isfinite(nb)
+    np.testing.assert_allclose(pb, pg, rtol=1e-5, atol=1e-8 + 2e-3 * disp)
+    np.testing.assert_allclose(nb, ng, rtol=3e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,channel", [((256, 64), True), ((48, 300), True), ((200, 100), False)])
+def test_apollo_bf16_sr_writeback_bits(shape, channel, det_proj):
+    """SR writeback (optimizer.py:3058-3063): x = (p * decay) + (G * f) * step in
+    fp32, rounded with the stream of kernels.cu:48-87, bit for bit against the
+    CPU restatement given the step's scalars from the library's workspace."""
+    from adafactor8bit import Adafactor8Bit
+    from oracle import sr
+    print(f"[apollo sr] {shape} channel={channel}", flush=True)
+    R, C = shape
+    p = torch.nn.Parameter(inputs.make_param(shape, 0, 9).to("cuda", torch.bfloat16))
+    opt = Adafactor8Bit([p], **_apollo_kw(apollo_rank=16, weight_decay=0.1, stochastic_round_writeback=True,
+                                          apollo_scale_type="channel" if channel else "tensor"))
+    for t in range(1, 3):
+        p_old = _f32(_t2np(p)).reshape(-1).astype(np.float32)
+        g = inputs.make_grad(shape, 0, t, 9).to(torch.bfloat16)
+        p.grad = g.cuda()
+        opt.step()
+        torch.cuda.synchronize()
+        st = opt.state[p]
+        L = __import__("adafactor8bit._native", fromlist=["lib"]).lib()
+        total = int(L.a8_apollo_workspace_floats(R, C, 16, int(channel)))
+        ws = _ws(opt, p)
+        step_s, dec = np.float32(ws[total - 16]), np.float32(ws[total - 15])
+        n_low = (R * 16) if R >= C else (16 * C)
+        nch = (R if R >= C else C) if channel else 1
+        fin = 2 * n_low + nch
+        gf = _f32(_t2np(g)).reshape(R, C).astype(np.float32)
+        if channel:
+            f = ws[fin:fin + nch].astype(np.float32)
+            fm = np.broadcast_to(f[:, None] if R >= C else f[None, :], (R, C))
+        else:
+            fm = np.full((R, C), np.float32(ws[total - 13]), dtype=np.float32)
+        x = (p_old * dec) + ((gf * fm) * step_s).reshape(-1)
+        want = sr.sr_round_bf16(x.astype(np.float32), seed=int(st["sr_seed"]), step=int(st["step"]))
+        got = _t2np(p).reshape(-1).view(np.uint16)
+        assert np.array_equal(got, want), f"step {t}: {(got != want).mean():.2e} differ"
+
+
+@pytest.mark.gpu
+def test_1d_bf16_sr_writeback_stream():
+    """1-D fused step with SR writeback: the bf16 result is the stochastic rounding
+    of the fp32 result under the reference's stream.  The fp32 run writes
+    fma(-step, u, p) and the SR path rounds (p - step * u), one fp32 rounding
+    apart, which moves the round-up probability by 2^-16: at most 0.1% of the
+    elements may land on the other bf16 neighbour."""
+    from adafactor8bit import Adafactor8Bit
+    from oracle import sr
+    meta, kw, _ = gu.load("adamw_uf8_al8")
+    shapes = [(700, 300), (4097,), (64, 64)]
+    print("[1d sr]", flush=True)
+    p16 = [torch.nn.Parameter(inputs.make_param(s, i, 3).to("cuda", torch.bfloat16)) for i, s in enumerate(shapes)]
+    p32 = [torch.nn.Parameter(p.detach().float()) for p in p16]
+    o16 = Adafactor8Bit(p16, **dict(kw, stochastic_round_writeback=True))
+    o32 = Adafactor8Bit(p32, **kw)
+    for i, s in enumerate(shapes):
+        g = inputs.make_grad(s, i, 1, 3).to(torch.bfloat16).cuda()
+        p16[i].grad = g
+        p32[i].grad = g.float()
+    o16.step()
+    o32.step()
+    torch.cuda.synchronize()
+    for p, q in zip(p16, p32):
+        x = q.detach().cpu().numpy().reshape(-1)
+        want = sr.sr_round_bf16(x, seed=int(o16.state[p]["sr_seed"]), step=int(o16.state[p]["step"]))
+        got = _t2np(p).reshape(-1).view(np.uint16)
+        diff = got != want
+        assert diff.mean() <= 1e-3, diff.mean()
+        # where they differ, both are neighbours of x
+        lo = (x.view(np.uint32) & np.uint32(0xFFFF0000)) >> np.uint32(16)
+        assert np.all(np.isin(got[diff].astype(np.int64) - lo[diff].astype(np.int64), [0, 1]))

@@ -57,7 +57,8 @@ class ApolloTensor(ctypes.Structure):
                 ("proj_t", _c_vp), ("rank", _c_i64), ("v_q", _c_vp), ("v_scale", _c_vp),
                 ("v_min_log", _c_vp), ("v_fp32", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
                 ("m_fp32", _c_vp), ("fira_prev", _c_vp), ("has_fira_prev", _c_i), ("lr", _c_vp),
-                ("workspace", _c_vp), ("sr_seed", _c_u64)]
+                ("workspace", _c_vp), ("sr_seed", _c_u64), ("first_step", _c_i), ("proj_fresh", _c_i),
+                ("step", _c_u64), ("bias_factor", _c_f)]
 
 
 _SIGS = {
@@ -91,6 +92,10 @@ _SIGS = {
                               _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i, _c_f, _c_f,
                               _c_f, _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_u64, _c_vp]),
     "a8_apollo_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
+    "a8_apollo_step_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_vp, _c_i64, _c_d, _c_d,
+                                    _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i,
+                                    _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_i, _c_vp]),
+    "a8_apollo_table_bytes": (_c_i64, [_c_i]),
 }
 
 _LIB = None

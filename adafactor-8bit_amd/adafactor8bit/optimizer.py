@@ -304,9 +304,11 @@ class Adafactor8Bit(Optimizer):
     def _step_group(self, group, params, grads, states):
         apollo_rank = group.get("apollo_rank", 0)
         batches: Dict[tuple, list] = {}
+        ap_batches: Dict[tuple, list] = {}
         for p, g, st in zip(params, grads, states):
             if apollo_rank > 0 and "apollo_seed" in st:
-                _run_apollo(self, p, g, st, group)
+                bkey, rec, fin = _apollo_prep(self, p, g, st, group)
+                ap_batches.setdefault(bkey, []).append((rec, fin))
                 continue
             plan = _plan_param(p, g, st, group)
             key = plan.batch_key()
@@ -316,6 +318,8 @@ class Adafactor8Bit(Optimizer):
                 batches.setdefault(key, []).append(plan)
         for key, plans in batches.items():
             _run_batch(self, key, plans)
+        for bkey, items in ap_batches.items():
+            _run_apollo_batch(self, group, bkey, items)
 
 
 # ====================================================================== planning
@@ -757,10 +761,11 @@ def _apollo_proj(st, shape, step, device, cache):
     return proj_T, True
 
 
-def _run_apollo(opt, p, grad, st, group):
-    """One APOLLO parameter (optimizer.py:2587-3084, non-factorised, beta3 = None):
-    host scalars and state, then a8_apollo_step (projection GEMM, low-rank V/M,
-    channel scale, Fira, full-rank writeback)."""
+def _apollo_prep(opt, p, grad, st, group):
+    """Host side of one APOLLO parameter's step (optimizer.py:2587-3084,
+    non-factorised, beta3 = None): step counter, projection refresh, lazy
+    low-rank state, per-step scalars.  Returns (batch key, tensor record, finish)
+    for the grouped launch."""
     beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
     if group.get("apollo_factorize", False) or group.get("beta3") is not None:
         raise NotImplementedError("adafactor8bit: factorised / CAME APOLLO is not available in this build yet")
@@ -801,8 +806,6 @@ def _run_apollo(opt, p, grad, st, group):
     quant = st.get("is_quantized", False)
     bs = st.get("block_size", group.get("block_size", 2048))
     first = st.get("v_low_q") is None and st.get("v_low") is None
-    aeps = group.get("apollo_eps", 1e-6)
-    eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
     vbits = 0 if (not quant or vqt == "fp32") else (16 if vqt == "al16" else 8)
     if first:   # optimizer.py:2770-2779 creates the low-rank V state on the first step
         if vbits:
@@ -828,7 +831,6 @@ def _run_apollo(opt, p, grad, st, group):
             if not torch.is_tensor(prev) or prev.device != dev or prev.dtype != torch.float32:
                 st["scaled_grad_norm_prev"] = torch.as_tensor(prev, dtype=torch.float32).to(dev).reshape(())
             has_prev = 1
-    channel = group.get("apollo_scale_type", "channel") == "channel"
     bias_mode, bias_fac = 0, 1.0
     if has_m and not group["relative_step"]:
         bc_on = True if group.get("bias_correction") is None else group.get("bias_correction")
@@ -838,19 +840,16 @@ def _run_apollo(opt, p, grad, st, group):
                 bias_mode, bias_fac = 1, _f32(math.sqrt(1.0 - beta2 ** step) / bc1)
             else:
                 bias_mode, bias_fac = 2, _f32(bc1)
-    wd = group["weight_decay"]
-    wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
-    L = nat.lib()
     key = (dev, "apollo", id(p))
     ent = opt._ws.get(key)
-    nws = int(L.a8_apollo_workspace_floats(R, C, rank, int(channel)))
+    nws = int(nat.lib().a8_apollo_workspace_floats(R, C, rank, 1))
     if ent is None or ent["ws"].numel() < nws:
         ent = {"ws": torch.empty(nws, dtype=torch.float32, device=dev), "proj": None}
         opt._ws[key] = ent
     if ent["proj"] is None or ent["proj"] != (proj_T.data_ptr(), proj_T._version):
         fresh = True
     ent["proj"] = (proj_T.data_ptr(), proj_T._version)
-    sr = group.get("stochastic_round_writeback", False) and p.dtype == torch.bfloat16
+    sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype == torch.bfloat16
     t = nat.ApolloTensor(
         p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank,
         nat.ptr(st.get("v_low_q")) if vbits else None, nat.ptr(st.get("v_low_scale")) if vbits else None,
@@ -859,18 +858,45 @@ def _run_apollo(opt, p, grad, st, group):
         nat.ptr(st.get("m_low_scale")) if (has_m and not m_fp32) else None,
         st["m_low"].data_ptr() if m_fp32 else None,
         nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
-        nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)))
-    rc = L.a8_apollo_step(
-        nat.dtype_code(p.dtype), int(sr), ctypes.byref(t), int(first), int(fresh), float(beta_val),
+        nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)),
+        int(first), int(fresh), int(step), float(bias_fac))
+    bkey = (p.dtype, sr, vbits, has_m, m_fp32, mqt, int(mbs), int(bs), float(beta_val), float(rho_val), bias_mode)
+    keep = (g, proj_T, rho_t)   # alive until the launch is queued
+    return bkey, t, (st, vbits, bs, keep)
+
+
+def _run_apollo_batch(opt, group, bkey, items):
+    """One a8_apollo_step_multi launch sequence for the APOLLO matrices of a group
+    that share dtype, state formats and step scalars."""
+    pdt, sr, vbits, has_m, m_fp32, mqt, mbs, bs, beta_val, rho_val, bias_mode = bkey
+    n = len(items)
+    arr = (nat.ApolloTensor * n)(*[t for t, _ in items])
+    L = nat.lib()
+    pdev = items[0][1][3][0].device   # the first record's gradient
+    tkey = (pdev, "ap_table")
+    need = int(L.a8_apollo_table_bytes(n))
+    tab = opt._ws.get(tkey)
+    if tab is None or tab.numel() < need:
+        tab = torch.empty(max(need, 4096), dtype=torch.uint8, device=pdev)
+        opt._ws[tkey] = tab
+    beta1 = group.get("beta1")
+    aeps = group.get("apollo_eps", 1e-6)
+    eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
+    wd = group["weight_decay"]
+    wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
+    fira = bool(group.get("enable_fira_for_apollo", True))
+    rc = L.a8_apollo_step_multi(
+        nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
         float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), vbits, int(bs),
         S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs),
-        int(channel), float(group.get("apollo_scale", 1.0)), int(bool(group.get("apollo_scale_front", False))),
-        int(fira), float(group.get("fira_margin", 0.01)), float(group["d"]), float(rho_val),
-        _f32(group["eps"][1]), int(bool(group["scale_parameter"])), bias_mode, float(bias_fac), _f32(wd),
-        wd_mode, int(step), nat.stream_of(dev))
-    nat.check(rc, "a8_apollo_step")
+        int(group.get("apollo_scale_type", "channel") == "channel"), float(group.get("apollo_scale", 1.0)),
+        int(bool(group.get("apollo_scale_front", False))), int(fira), float(group.get("fira_margin", 0.01)),
+        float(group["d"]), float(rho_val), _f32(group["eps"][1]), int(bool(group["scale_parameter"])), bias_mode,
+        _f32(wd), wd_mode, nat.stream_of(pdev))
+    nat.check(rc, "a8_apollo_step_multi")
     if vbits:
-        _block_view(st, "v_low", bs)
+        for _, (st, vb, bsz, _keep) in items:
+            _block_view(st, "v_low", bsz)
 
 
 def _run_factored(opt, plans):

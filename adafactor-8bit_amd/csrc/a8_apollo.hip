@@ -1,9 +1,10 @@
-// APOLLO optimizer step for MI355X (gfx950): one full-rank matrix per call.
+// APOLLO optimizer step for MI355X (gfx950), all matrices of a group per launch.
 //
 // Follows _update_param_apollo (optimizer.py:2587-3084) on its non-factorised
 // path without CAME (apollo_factorize=False, beta3=None):
 //   G (R x C) is projected to rank r: right side (R >= C) g_low = G P^T (R x r),
 //   left side g_low = P^T G (r x C), P the seeded Gaussian / sqrt(r);
+//   NaN / Inf gradient entries count as zero (optimizer.py:2606);
 //   low-rank V: first step v = g_low^2 * beta_v (AL floor -126), later
 //   v = lerp(v, g_low^2, beta_v) (floor log2(eps^2)); low-rank M: lerp(m, g_low, 1-beta1);
 //   u = m / (sqrt(v) + eps) (or g_low / (...) without beta1);
@@ -11,71 +12,83 @@
 //   columns (left), or one tensor scale; Fira on sqrt(sum ||G_ch||^2 s^2) (or
 //   ||G|| s); p <- p * decay + (step * G) * final_scale, step = -alpha / denom
 //   with bias correction.
-// Launches: [split of P^T into three bf16 terms when P changed] -> projection
-// GEMM (rocBLAS gemm_ex: bf16 G times the three terms, accumulated in fp32,
-// which carries P's 24 bits; fp32 G: one fp32 GEMM) -> k_ap_gnorm (norms of G)
-// -> k_ap_low (low-rank V/M EMA, re-encode, u) -> k_ap_scale (channel norms of
-// u and g_low) -> k_ap_scalars (Fira, step, final scales) -> k_ap_apply.
+//
+// One step of a group of matrices is five launches over a device table of
+// per-matrix descriptors (each kernel finds its matrix by a binary search of a
+// compact first-workgroup array):
+//   k_ap_proj    bf16 G: MFMA projection (v_mfma_f32_32x32x16_bf16) of 64-row
+//                (right) or 64-column (left) tiles of G against P^T split into
+//                three bf16 terms (3 x 8 significand bits carry fp32's 24; all
+//                products land in one fp32 accumulator), reading G once: the
+//                same pass scrubs non-finite entries and accumulates the channel
+//                norms of G (and of p for scale_parameter).  fp32 G: rocBLAS
+//                sgemm plus a norm pass per matrix.
+//   k_ap_low     low-rank V/M EMA and re-encode, u
+//   k_ap_scale   channel (or tensor) norms of u and g_low, per-workgroup partials
+//   k_ap_scalars one workgroup per matrix: alpha, Fira, step, decay
+//   k_ap_apply   full-rank writeback (deterministic or stochastic rounding)
 #include <rocblas/rocblas.h>
+#include <vector>
 #include "a8_common.cuh"
 #include "a8_mcodec.cuh"
 #include "a8_abi_impl.h"
 
 namespace a8 {
 
-constexpr int kApUnit = 2048;   // low-rank elements per k_ap_low workgroup (8 per lane)
-constexpr int kApNP = 1024;     // maximum workgroups of the partial-sum passes
-constexpr int kApSc = 16;       // per-tensor scalars
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Workspace of one tensor (offsets in floats; partial arrays are doubles).
-struct ApWs {
-  int64_t glow;      // [n_low]   projected gradient
-  int64_t u;         // [n_low]   low-rank update direction
-  int64_t ngsq;      // [nch]     ||G_ch||^2
-  int64_t fin;       // [nch]     s, then the final scale
-  int64_t gpart;     // double[kApNP]   ||G||^2 per k_ap_gnorm workgroup
-  int64_t ppart;     // double[kApNP]   sum p^2 per k_ap_gnorm workgroup
-  int64_t spart;     // double[2 kApNP] scale pass: sum ngsq s^2 | sum u^2, sum g_low^2
-  int64_t nfpart;    // int[kApNP]      k_ap_gnorm workgroup saw a non-finite gradient
-  int64_t gcol;      // double[nrc C]   left side: column sums of G^2 per row chunk
-  int64_t split;     // bf16[3 r K]     P^T in three terms
-  int64_t scal;      // [16]
-  int64_t total;
-  int64_t n_low, nch, K;
-  int64_t rcr, nrc, ncc;   // left side: rows per chunk, row chunks, 2048-column chunks
+constexpr int kApTile = 64;     // G rows (right) / G columns (left) per projection tile
+constexpr int kApPass = 256;    // low-rank outputs per projection pass (4 waves x 64)
+constexpr int kApUnit = 2048;   // low-rank elements per k_ap_low workgroup (8 per lane)
+constexpr int kApScR = 16;      // right side: g_low rows per k_ap_scale workgroup
+constexpr int kApScL = 64;      // left side: g_low columns per k_ap_scale workgroup
+constexpr int kApApp = 2048;    // matrix elements per k_ap_apply workgroup (8 per lane)
+constexpr int kApLS = 40;       // LDS row stride (halves) of the transposed G tile
+
+// Workspace of one matrix (offsets in floats; partial arrays hold doubles).
+struct ApL {
+  int64_t n_low, nchg, K, Kp, rp, ntr, npass, ntile, nunit, nsc, napp;
+  int64_t glow, u, ngsq, fin, scal, gpart, ppart, spart, nfpart, psplit, total;
 };
 
-__host__ __device__ inline ApWs ap_layout(int64_t R, int64_t C, int64_t r, int channel) {
-  ApWs w;
+__host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
+  ApL w;
   const bool right = R >= C;
-  w.n_low = right ? R * r : r * C;
-  w.nch = channel ? (right ? R : C) : 1;
-  w.K = right ? C : R;
+  w.n_low = (right ? R : C) * r;
+  w.nchg = right ? R : C;                  // channels of G: rows (right) / columns (left)
+  w.K = right ? C : R;                     // reduction length of the projection
+  w.Kp = (w.K + 31) / 32 * 32;
+  w.rp = (r + 31) / 32 * 32;
+  w.ntr = (w.nchg + kApTile - 1) / kApTile;
+  w.npass = (w.rp + kApPass - 1) / kApPass;
+  w.ntile = w.ntr * w.npass;
+  w.nunit = (w.n_low + kApUnit - 1) / kApUnit;
+  w.nsc = right ? (R + kApScR - 1) / kApScR : (C + kApScL - 1) / kApScL;
+  w.napp = (R * C + kApApp - 1) / kApApp;
   w.glow = 0;
   w.u = w.glow + w.n_low;
-  w.ngsq = w.u + w.n_low;
-  w.fin = w.ngsq + w.nch;
-  w.gpart = (w.fin + w.nch + 1) / 2 * 2;
-  w.ppart = w.gpart + 2 * kApNP;
-  w.spart = w.ppart + 2 * kApNP;
-  w.ncc = (C + 2047) / 2048;
-  w.rcr = 64;
-  while (w.ncc * ((R + w.rcr - 1) / w.rcr) > kApNP) w.rcr *= 2;
-  w.nrc = (R + w.rcr - 1) / w.rcr;
-  w.nfpart = w.spart + 4 * kApNP;
-  w.gcol = w.nfpart + kApNP;
-  w.split = (w.gcol + (right ? 0 : 2 * w.nrc * C) + 63) / 64 * 64;
-  w.scal = w.split + (3 * r * w.K + 1) / 2;
-  w.total = w.scal + kApSc;
+  w.ngsq = w.u + w.n_low;                  // ||G_ch||^2
+  w.fin = w.ngsq + w.nchg;                 // channel scale s
+  w.scal = w.fin + w.nchg;                 // 16 per-matrix scalars
+  w.gpart = (w.scal + 16 + 1) / 2 * 2;     // double[ntr]  ||G||^2 per tile
+  w.ppart = w.gpart + 2 * w.ntr;           // double[ntr]  ||p||^2 per tile
+  w.spart = w.ppart + 2 * w.ntr;           // double[3 nsc] sum ngsq s^2, sum u^2, sum g_low^2
+  w.nfpart = w.spart + 6 * w.nsc;          // int[ntr]     non-finite G seen (fp32 path)
+  w.psplit = (w.nfpart + w.ntr + 63) / 64 * 64;   // bf16[3][rp][Kp]  P rows, three terms
+  w.total = w.psplit + (3 * w.rp * w.Kp + 1) / 2;
   return w;
 }
 
-// Scalars: [0] step (-alpha/denom, bias-corrected), [1] decay, [2] has decay,
+// Scalars in ApL::scal: [0] step (-alpha/denom, bias-corrected), [1] decay,
 // [3] tensor final scale, [4] alpha, [5] norm_unscaled, [6] fira scale.
-struct ApArgs {
-  void* param;
+
+// One matrix.  Read through the scalar cache: 8-byte words only.
+struct ApDesc {
   const void* grad;
-  int64_t R, C, r;
+  void* param;
+  float* ws;
+  const float* proj_t;
   void* v_q;
   float* v_scale;
   float* v_min_log;
@@ -85,32 +98,50 @@ struct ApArgs {
   float* m_fp32;
   float* fira_prev;
   const float* lr;
-  float* ws;
-  uint64_t sr_seed;
-  float bv, w_m, aeps, floor_, lr_val, eps2, bias_factor, wd, d, margin, sv;
-  int has_fira_prev, first, has_m, mk, vb, lbv, lbm, channel, front, fira, scale_param, bias_mode, wd_mode;
-  int ngn, nsc;   // workgroups of k_ap_gnorm and k_ap_scale
-  int valign;     // rows of G start 16-byte aligned (C % 8 == 0, or C % 4 == 0 for fp32)
-  uint64_t sr_step;
+  int64_t R, C, r;
+  uint64_t sr_seed, step;
+  float bias_factor;
+  int32_t first, has_prev, valign;
+  int32_t tile_begin, unit_begin, sc_begin, app_begin;
+};
+static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
+
+struct ApHyp {
+  float bv, w_m, aeps, log_floor, lr_val, eps2, wd, d, margin, sv;
+  int lbv, lbm, mk, channel, front, fira, scale_param, bias_mode, wd_mode;
 };
 
-__device__ __forceinline__ double ws_d(float* ws, int64_t off, int64_t i) {
-  return gp(reinterpret_cast<double*>(ws + off))[i];
+// Table: ntab descriptors, then four int32 first-workgroup arrays (projection
+// tiles, low units, scale workgroups, apply workgroups).  Without a table the
+// single descriptor comes as a kernel argument.
+__device__ __forceinline__ ApDesc ap_pick(const ApDesc& one, const ApDesc* tab, int ntab, int which, int wg,
+                                          int& local) {
+  if (tab == nullptr) {
+    local = wg;
+    return one;
+  }
+  const A8_C ApDesc* ct = cp(tab);
+  const A8_C int32_t* fb = (const A8_C int32_t*)(ct + ntab) + (int64_t)which * ntab;
+  int lo = 0, hi = ntab - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (fb[mid] <= wg) lo = mid; else hi = mid - 1;
+  }
+  const A8_C uint64_t* w = (const A8_C uint64_t*)(ct + lo);
+  uint64_t buf[sizeof(ApDesc) / 8];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(ApDesc) / 8); ++i) buf[i] = w[i];
+  ApDesc d;
+  __builtin_memcpy(&d, buf, sizeof(ApDesc));
+  local = wg - fb[lo];
+  return d;
+}
+
+__device__ __forceinline__ double ws_d(const float* ws, int64_t off, int64_t i) {
+  return gp(reinterpret_cast<const double*>(ws + off))[i];
 }
 __device__ __forceinline__ void ws_d_set(float* ws, int64_t off, int64_t i, double v) {
   gp(reinterpret_cast<double*>(ws + off))[i] = v;
-}
-
-// Eight consecutive elements of one row (16-byte vector loads when rows start
-// aligned, i.e. C % 8 == 0; element loads otherwise or at the row's end).
-template <typename T>
-__device__ __forceinline__ void ld8_row(const T* rowp, int64_t c, int64_t C, int aligned, float* out) {
-  if (aligned) {
-    load8<T>(rowp, c, C, out);
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = (c + k < C) ? ld1<T>(rowp, c + k) : 0.0f;
-  }
 }
 
 // Workgroup sum of a double (256 lanes), fixed order; every lane gets it.
@@ -123,139 +154,373 @@ __device__ __forceinline__ double ap_wg_sum(double x, double* s4) {
   return ((s4[0] + s4[1]) + s4[2]) + s4[3];
 }
 
+// ------------------------------------------------------------ bf16 helpers
+// Eight bf16 of a row: one 16-byte load when all eight are in range and the row
+// is 16-byte aligned, element loads otherwise (cnt in 0..8, the rest zero).
+__device__ __forceinline__ u32x4 ldg8(const uint16_t* base, int64_t off, int cnt, int vec) {
+  if (vec && cnt == 8) return *gp(reinterpret_cast<const u32x4*>(base + off));
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < cnt) w[j >> 1] |= (uint32_t)gp(base)[off + j] << (16 * (j & 1));
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+// NaN / Inf (exponent all ones) -> +0 in both halves of a word.
+__device__ __forceinline__ uint32_t scrub2(uint32_t w) {
+  const uint32_t lo = ((w & 0x7F80u) == 0x7F80u) ? 0u : (w & 0xFFFFu);
+  const uint32_t hi = ((w & 0x7F800000u) == 0x7F800000u) ? 0u : (w & 0xFFFF0000u);
+  return lo | hi;
+}
+__device__ __forceinline__ u32x4 scrub8(u32x4 q) {
+  return u32x4{scrub2(q.x), scrub2(q.y), scrub2(q.z), scrub2(q.w)};
+}
+// Sum of squares of eight (scrubbed) bf16 values: the products are exact in fp32.
+__device__ __forceinline__ double sq8(u32x4 q) {
+  double s = 0.0;
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xFFFF0000u);
+    s += (double)(a * a);
+    s += (double)(b * b);
+  }
+  return s;
+}
+__device__ __forceinline__ bf16x8 as_bf8(u32x4 q) { return __builtin_bit_cast(bf16x8, q); }
+__device__ __forceinline__ bf16x8 ldp8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *gp(reinterpret_cast<const u32x4*>(p)));
+}
+__device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// ||G_ch||^2 as torch.linalg.vector_norm(...).square(): the norm rounded to fp32, squared.
+__device__ __forceinline__ float norm_sq(double s) {
+  const float nrm = sqrtf((float)s);
+  return nrm * nrm;
+}
+
 // ------------------------------------------------------------ P^T split
-// P^T = hi + mid + lo, each term rounded to bf16: 3 x 8 significand bits carry
-// fp32's 24, so bf16 products of an exact bf16 G with the three terms, summed
-// in fp32, give the fp32 GEMM to fp32 rounding.
-__global__ __launch_bounds__(256) void k_ap_split(const float* __restrict__ pt, int64_t n,
-                                                 __hip_bfloat16* __restrict__ out) {
+// Rows of P (the B operand on the right side, A on the left), three bf16 terms
+// hi + mid + lo = the fp32 value exactly, zero padded to rp x Kp.
+__global__ __launch_bounds__(256) void k_ap_split(const float* __restrict__ pt, int64_t r, int64_t K, int right,
+                                                 int64_t rp, int64_t Kp, uint16_t* __restrict__ out) {
+  const int64_t n = rp * Kp;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const float x = gp(pt)[i];
+    const int64_t row = i / Kp, k = i - row * Kp;
+    float x = 0.0f;
+    if (row < r && k < K) x = right ? gp(pt)[k * r + row] : gp(pt)[row * K + k];
     const __hip_bfloat16 h = __float2bfloat16(x);
     const float r1 = x - __bfloat162float(h);
     const __hip_bfloat16 m = __float2bfloat16(r1);
-    const float r2 = r1 - __bfloat162float(m);
-    out[i] = h;
-    out[n + i] = m;
-    out[2 * n + i] = __float2bfloat16(r2);
+    const __hip_bfloat16 l = __float2bfloat16(r1 - __bfloat162float(m));
+    uint16_t bh, bm, bl;
+    __builtin_memcpy(&bh, &h, 2);
+    __builtin_memcpy(&bm, &m, 2);
+    __builtin_memcpy(&bl, &l, 2);
+    gp(out)[i] = bh;
+    gp(out)[n + i] = bm;
+    gp(out)[2 * n + i] = bl;
   }
 }
 
-// ------------------------------------------------------------ norms of G (and p^2)
-// Channel norms: right side one wave per row of G, left side lanes over
-// columns walking the rows; sums of fp32 squares in double, fixed order;
-// ngsq = (sqrt(sum))^2 as torch.linalg.vector_norm(...).square().  Per
-// workgroup partials of ||G||^2 (tensor scale) and p^2 (scale_parameter).
-template <typename T>
-__global__ __launch_bounds__(256) void k_ap_gnorm(ApArgs a) {
-  __shared__ double sd[4];
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  const int64_t R = a.R, C = a.C;
-  const bool right = R >= C;
-  const T* G = reinterpret_cast<const T*>(a.grad);
-  const T* P = reinterpret_cast<const T*>(a.param);
-  float* ws = a.ws;
-  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  double psq = 0.0, gsq = 0.0;
-  bool nonfin = false;
-  if (right) {
-    // one wave per row, 8 elements per lane per step
-    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < R; row += (int64_t)gridDim.x * 4) {
-      double s = 0.0, sp = 0.0;
-      for (int64_t c = (int64_t)wl * 8; c < C; c += 512) {
-        float g[8];
-        ld8_row<T>(G + row * C, c, C, a.valign, g);
+// ------------------------------------------------------------ MFMA projection (bf16)
+// 32x32x16 lane layout (gfx950): A: lane l holds row l%32, k = 8(l/32)..+8;
+// B: column l%32, same k; D: column l%32, acc v at row 8(v/4) + 4(l/32) + v%4.
+__device__ __forceinline__ void store_acc(const f32x16& acc, float* out, int64_t ld, int64_t row0, int64_t col,
+                                          int64_t nrow, int64_t ncol, int hi) {
+  if (col >= ncol) return;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          nonfin |= !__builtin_isfinite(g[k]);
-          const float gk = scrub(g[k]);
-          s += (double)(gk * gk);
+  for (int v = 0; v < 16; ++v) {
+    const int64_t row = row0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+    if (row < nrow) gp(out)[row * ld + col] = acc[v];
+  }
+}
+
+// Right side: tile = 64 rows of G x 256 outputs (one pass); wave w owns outputs
+// [64w, 64w + 64) of the pass as two 32-column blocks.  All waves read the same
+// G rows (the A operand); wave 0 also sums their squares, wave 1 those of p.
+__device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int tile, int scale_param) {
+  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int pass = (int)(tile / L.ntr);
+  const int64_t rt = tile - (int64_t)pass * L.ntr;
+  const int64_t R = D.R, C = D.C, r = D.r, K = C, Kp = L.Kp, rp = L.rp;
+  const int64_t row0 = rt * kApTile;
+  const int64_t cb0 = (int64_t)pass * kApPass + w * 64;
+  const bool act0 = cb0 < rp, act1 = cb0 + 32 < rp;
+  const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
+  const uint16_t* PP = reinterpret_cast<const uint16_t*>(D.param);
+  const uint16_t* Pm = reinterpret_cast<const uint16_t*>(D.ws + L.psplit);
+  const int64_t tstride = rp * Kp;
+  const uint16_t* pb0 = Pm + (cb0 + l32) * Kp + 8 * hi;
+  const uint16_t* pb1 = pb0 + 32 * Kp;
+  const int64_t ra = row0 + l32, rb = row0 + 32 + l32;
+  const bool gnorm = pass == 0 && w == 0, pnorm = pass == 0 && w == 1 && scale_param;
+  f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
+  double n0 = 0.0, n1 = 0.0, ps = 0.0;
+  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    const int64_t k = k0 + 8 * hi;
+    const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
+    const u32x4 q0 = scrub8(ldg8(G, ra * C + k, ra < R ? cnt : 0, D.valign));
+    const u32x4 q1 = scrub8(ldg8(G, rb * C + k, rb < R ? cnt : 0, D.valign));
+    if (gnorm) {
+      n0 += sq8(q0);
+      n1 += sq8(q1);
+    }
+    if (pnorm) {
+      ps += sq8(ldg8(PP, ra * C + k, ra < R ? cnt : 0, D.valign));
+      ps += sq8(ldg8(PP, rb * C + k, rb < R ? cnt : 0, D.valign));
+    }
+    if (act0 || act1) {
+      const bf16x8 x0 = as_bf8(q0), x1 = as_bf8(q1);
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        if (act0) {
+          const bf16x8 b = ldp8(pb0 + t * tstride + k0);
+          a00 = mfma(x0, b, a00);
+          a10 = mfma(x1, b, a10);
         }
-        if (a.scale_param) {
-          float p[8];
-          ld8_row<T>(P + row * C, c, C, a.valign, p);
+        if (act1) {
+          const bf16x8 b = ldp8(pb1 + t * tstride + k0);
+          a01 = mfma(x0, b, a01);
+          a11 = mfma(x1, b, a11);
+        }
+      }
+    }
+  }
+  float* glow = D.ws + L.glow;
+  if (act0) {
+    store_acc(a00, glow, r, row0, cb0 + l32, R, r, hi);
+    store_acc(a10, glow, r, row0 + 32, cb0 + l32, R, r, hi);
+  }
+  if (act1) {
+    store_acc(a01, glow, r, row0, cb0 + 32 + l32, R, r, hi);
+    store_acc(a11, glow, r, row0 + 32, cb0 + 32 + l32, R, r, hi);
+  }
+  if (pass != 0) return;
+  if (w == 0) {   // lanes l and l + 32 hold the two k halves of one row
+    n0 += __shfl_xor(n0, 32, 64);
+    n1 += __shfl_xor(n1, 32, 64);
+    double t = 0.0;
+    if (hi == 0) {
+      if (ra < R) { gp(D.ws + L.ngsq)[ra] = norm_sq(n0); t += n0; }
+      if (rb < R) { gp(D.ws + L.ngsq)[rb] = norm_sq(n1); t += n1; }
+    }
+    t = grp_sum_d(t, 64);
+    if (l == 0) ws_d_set(D.ws, L.gpart, rt, t);
+  } else if (w == 1) {
+    ps = grp_sum_d(ps, 64);
+    if (l == 0) ws_d_set(D.ws, L.ppart, rt, ps);
+  }
+}
+
+// Left side: tile = 64 columns of G x 256 outputs (one pass).  The A operand is
+// P (rows of the low-rank output); the B operand needs 8 consecutive rows of G
+// per lane, so each 32-row slab of the tile is loaded with 16-byte row loads
+// and stored transposed to LDS.  The loading lanes also sum squares per column.
+__device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int tile, int scale_param,
+                                          uint16_t* ldsT, double* sred) {
+  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int pass = (int)(tile / L.ntr);
+  const int64_t ct = tile - (int64_t)pass * L.ntr;
+  const int64_t R = D.R, C = D.C, r = D.r, K = R, Kp = L.Kp, rp = L.rp;
+  const int64_t n0 = ct * kApTile;
+  const int64_t mb0 = (int64_t)pass * kApPass + w * 64;
+  const bool act0 = mb0 < rp, act1 = mb0 + 32 < rp;
+  const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
+  const uint16_t* PP = reinterpret_cast<const uint16_t*>(D.param);
+  const uint16_t* Pm = reinterpret_cast<const uint16_t*>(D.ws + L.psplit);
+  const int64_t tstride = rp * Kp;
+  const uint16_t* pa0 = Pm + (mb0 + l32) * Kp + 8 * hi;
+  const uint16_t* pa1 = pa0 + 32 * Kp;
+  const int lrow = lane >> 3, lcol = (lane & 7) * 8;
+  const int64_t gc = n0 + lcol;
+  const int ccnt = C - gc >= 8 ? 8 : (C - gc > 0 ? (int)(C - gc) : 0);
+  const bool norms = pass == 0;
+  f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
+  double cs[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) sp += (double)(p[k] * p[k]);
+  for (int j = 0; j < 8; ++j) cs[j] = 0.0;
+  double ps = 0.0;
+  for (int64_t k0 = 0; k0 < K; k0 += 32) {
+    const int64_t grow = k0 + lrow;
+    const int cnt = grow < K ? ccnt : 0;
+    const u32x4 q = scrub8(ldg8(G, grow * C + gc, cnt, D.valign));
+    const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+    if (norms) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = __uint_as_float((j & 1) ? (wv[j >> 1] & 0xFFFF0000u) : (wv[j >> 1] << 16));
+        cs[j] += (double)(x * x);
+      }
+      if (scale_param) ps += sq8(ldg8(PP, grow * C + gc, cnt, D.valign));
+    }
+    __syncthreads();   // the previous slab's readers are done
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      ldsT[(lcol + j) * kApLS + lrow] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+    __syncthreads();
+    if (act0 || act1) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 b0 =
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&ldsT[l32 * kApLS + s * 16 + 8 * hi]));
+        const bf16x8 b1 =
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&ldsT[(32 + l32) * kApLS + s * 16 + 8 * hi]));
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          if (act0) {
+            const bf16x8 a = ldp8(pa0 + t * tstride + k0 + s * 16);
+            a00 = mfma(a, b0, a00);
+            a01 = mfma(a, b1, a01);
+          }
+          if (act1) {
+            const bf16x8 a = ldp8(pa1 + t * tstride + k0 + s * 16);
+            a10 = mfma(a, b0, a10);
+            a11 = mfma(a, b1, a11);
+          }
+        }
+      }
+    }
+  }
+  float* glow = D.ws + L.glow;
+  if (act0) {
+    store_acc(a00, glow, C, mb0, n0 + l32, r, C, hi);
+    store_acc(a01, glow, C, mb0, n0 + 32 + l32, r, C, hi);
+  }
+  if (act1) {
+    store_acc(a10, glow, C, mb0 + 32, n0 + l32, r, C, hi);
+    store_acc(a11, glow, C, mb0 + 32, n0 + 32 + l32, r, C, hi);
+  }
+  if (!norms) return;
+  // column sums: lanes with equal (lane & 7) share columns; xor over 8, 16, 32
+  // within the wave, then the four waves through LDS
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    double x = cs[j];
+    x += __shfl_xor(x, 8, 64);
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
+    cs[j] = x;
+  }
+  if (l < 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sred[w * 64 + l * 8 + j] = cs[j];
+  }
+  __syncthreads();
+  double t = 0.0;
+  if (w == 0) {
+    const double s = ((sred[l] + sred[64 + l]) + sred[128 + l]) + sred[192 + l];
+    if (n0 + l < C) {
+      gp(D.ws + L.ngsq)[n0 + l] = norm_sq(s);
+      t = s;
+    }
+    t = grp_sum_d(t, 64);
+  }
+  const double tp = scale_param ? ap_wg_sum(ps, sred + 256) : 0.0;
+  if (lane == 0) {
+    ws_d_set(D.ws, L.gpart, ct, t);
+    ws_d_set(D.ws, L.ppart, ct, tp);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_ap_proj(ApDesc one, const ApDesc* tab, int ntab, int scale_param) {
+  __shared__ __attribute__((aligned(16))) uint16_t ldsT[kApTile * kApLS];
+  __shared__ double sred[4 * 64 + 4];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 0, (int)blockIdx.x, local);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  if (D.R >= D.C) proj_right(D, L, local, scale_param);
+  else proj_left(D, L, local, scale_param, ldsT, sred);
+}
+
+// ------------------------------------------------------------ fp32 G: norms and flags
+// One workgroup per 64 rows (right) / 64 columns (left): ||G_ch||^2, ||G||^2 and
+// ||p||^2 partials, and whether a non-finite entry was seen (the library GEMM
+// reads G as given; k_ap_fixlow then recomputes g_low from the scrubbed G).
+__global__ __launch_bounds__(256) void k_ap_norm32(ApDesc D, int scale_param) {
+  __shared__ double sd[4 * 64 + 4];
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t R = D.R, C = D.C;
+  const float* G = reinterpret_cast<const float*>(D.grad);
+  const float* P = reinterpret_cast<const float*>(D.param);
+  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63;
+  const int64_t t = blockIdx.x;
+  bool nonfin = false;
+  double tg = 0.0, tp = 0.0;
+  if (R >= C) {
+    for (int i = 0; i < kApTile / 4; ++i) {
+      const int64_t row = t * kApTile + w * (kApTile / 4) + i;
+      if (row >= R) break;
+      double s = 0.0, sp = 0.0;
+      for (int64_t c = l; c < C; c += 64) {
+        const float g = gp(G)[row * C + c];
+        nonfin |= !__builtin_isfinite(g);
+        const float gs = scrub(g);
+        s += (double)(gs * gs);
+        if (scale_param) {
+          const float p = gp(P)[row * C + c];
+          sp += (double)(p * p);
         }
       }
       s = grp_sum_d(s, 64);
-      sp = grp_sum_d(sp, 64);
-      if (a.channel && wl == 0) {
-        const float nrm = sqrtf((float)s);
-        gp(ws)[W.ngsq + row] = nrm * nrm;
-      }
-      if (wl == 0) { gsq += s; psq += sp; }
+      if (l == 0) gp(D.ws + L.ngsq)[row] = norm_sq(s);
+      tg += (l == 0) ? s : 0.0;
+      tp += sp;
     }
   } else {
-    // 2-D grid: x = 2048-column chunk, y = chunk of rcr rows; column partials in double
-    const int64_t c0 = (int64_t)blockIdx.x * 2048 + (int64_t)lane * 8;
-    const int64_t r0 = (int64_t)blockIdx.y * W.rcr;
-    const int64_t r1 = (r0 + W.rcr < R) ? r0 + W.rcr : R;
-    double s[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) s[k] = 0.0;
-    if (c0 < C) {
-      for (int64_t row = r0; row < r1; ++row) {
-        float g[8];
-        ld8_row<T>(G + row * C, c0, C, a.valign, g);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          nonfin |= !__builtin_isfinite(g[k]);
-          const float gk = scrub(g[k]);
-          s[k] += (double)(gk * gk);
-        }
-        if (a.scale_param) {
-          float p[8];
-          ld8_row<T>(P + row * C, c0, C, a.valign, p);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) psq += (double)(p[k] * p[k]);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (c0 + k < C) {
-          ws_d_set(ws, W.gcol, (int64_t)blockIdx.y * C + c0 + k, s[k]);
-          gsq += s[k];
+    const int64_t c = t * kApTile + l;
+    double s = 0.0;
+    if (c < C) {
+      for (int64_t row = w; row < R; row += 4) {
+        const float g = gp(G)[row * C + c];
+        nonfin |= !__builtin_isfinite(g);
+        const float gs = scrub(g);
+        s += (double)(gs * gs);
+        if (scale_param) {
+          const float p = gp(P)[row * C + c];
+          tp += (double)(p * p);
         }
       }
     }
+    sd[w * 64 + l] = s;
+    __syncthreads();
+    if (w == 0 && c < C) {
+      const double cs = ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
+      gp(D.ws + L.ngsq)[c] = norm_sq(cs);
+      tg = cs;
+    }
+    __syncthreads();
   }
-  const double tg = ap_wg_sum(gsq, sd);
-  const double tp = ap_wg_sum(psq, sd);
+  const double sg = ap_wg_sum(tg, sd + 256);
+  const double sp = ap_wg_sum(tp, sd + 256);
   const int nf = __syncthreads_or(nonfin ? 1 : 0);
   if (lane == 0) {
-    const int64_t wg = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-    ws_d_set(ws, W.gpart, wg, tg);
-    ws_d_set(ws, W.ppart, wg, tp);
-    gp(reinterpret_cast<int*>(ws + W.nfpart))[wg] = nf ? 1 : 0;
+    ws_d_set(D.ws, L.gpart, t, sg);
+    ws_d_set(D.ws, L.ppart, t, sp);
+    gp(reinterpret_cast<int*>(D.ws + L.nfpart))[t] = nf ? 1 : 0;
   }
 }
 
-// ------------------------------------------------------------ non-finite gradients
-// The reference zeroes NaN / Inf gradient entries before the projection
-// (optimizer.py:2606); the library GEMM reads G as given, so when k_ap_gnorm
-// flagged a non-finite entry this pass recomputes g_low from the scrubbed G with
-// plain fp32 dot products (one element per lane).  With a finite G every
-// workgroup returns after reading the flags.
-template <typename T>
-__global__ __launch_bounds__(256) void k_ap_fixlow(ApArgs a, const float* __restrict__ pt) {
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
+// With a finite G every workgroup returns after reading the flags.
+__global__ __launch_bounds__(256) void k_ap_fixlow(ApDesc D) {
+  const ApL L = ap_layout(D.R, D.C, D.r);
   const int lane = threadIdx.x;
   int f = 0;
-  for (int k = lane; k < a.ngn; k += 256) f |= gp(reinterpret_cast<const int*>(a.ws + W.nfpart))[k];
+  for (int64_t k = lane; k < L.ntr; k += 256) f |= gp(reinterpret_cast<const int*>(D.ws + L.nfpart))[k];
   if (!__syncthreads_or(f)) return;
-  const int64_t R = a.R, C = a.C, r = a.r;
-  const T* G = reinterpret_cast<const T*>(a.grad);
-  for (int64_t i = (int64_t)blockIdx.x * 256 + lane; i < W.n_low; i += (int64_t)gridDim.x * 256) {
+  const int64_t R = D.R, C = D.C, r = D.r;
+  const float* G = reinterpret_cast<const float*>(D.grad);
+  const float* pt = D.proj_t;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + lane; i < L.n_low; i += (int64_t)gridDim.x * 256) {
     float acc = 0.0f;
     if (R >= C) {
       const int64_t row = i / r, k = i - row * r;
-      for (int64_t c = 0; c < C; ++c) acc = __builtin_fmaf(scrub(ld1<T>(G, row * C + c)), gp(pt)[c * r + k], acc);
+      for (int64_t c = 0; c < C; ++c) acc = __builtin_fmaf(scrub(gp(G)[row * C + c]), gp(pt)[c * r + k], acc);
     } else {
       const int64_t k = i / C, j = i - k * C;
-      for (int64_t q = 0; q < R; ++q) acc = __builtin_fmaf(gp(pt)[k * R + q], scrub(ld1<T>(G, q * C + j)), acc);
+      for (int64_t q = 0; q < R; ++q) acc = __builtin_fmaf(gp(pt)[k * R + q], scrub(gp(G)[q * C + j]), acc);
     }
-    gp(a.ws)[W.glow + i] = acc;
+    gp(D.ws + L.glow)[i] = acc;
   }
 }
 
@@ -267,14 +532,16 @@ __global__ __launch_bounds__(256) void k_ap_fixlow(ApArgs a, const float* __rest
 // lerp_): v = first ? g^2 * bv : lerp(v, g^2, bv); m = lerp(m, g, 1 - beta1);
 // u = m / (sqrt(v) + eps) with IEEE sqrt and division.
 template <int VB, int MK>
-__global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
+__global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   __shared__ float xw[16];
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  const int64_t n = W.n_low;
-  float* ws = a.ws;
+  int unit;
+  const ApDesc D = ap_pick(one, tab, ntab, 1, (int)blockIdx.x, unit);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t n = L.n_low;
+  float* ws = D.ws;
   const int lane = threadIdx.x, wave = lane >> 6;
-  const int64_t e0 = (int64_t)blockIdx.x * kApUnit + (int64_t)lane * 8;
-  const int lbv = a.lbv, lbm = a.lbm;
+  const int64_t e0 = (int64_t)unit * kApUnit + (int64_t)lane * 8;
+  const int lbv = h.lbv, lbm = h.lbm;
   const int VL = (1 << lbv) >> 3, ML = (1 << lbm) >> 3;
   const int64_t nvb = VB ? (n + (1 << lbv) - 1) >> lbv : 0;
   const int64_t nmb = (n + (1 << lbm) - 1) >> lbm;
@@ -283,29 +550,31 @@ __global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
   const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
   const bool v_ok = VB ? vb < nvb : cnt > 0;
   const bool m_ok = (MK == 1 || MK == 2) && mb < nmb;   // codes padded to whole M blocks
-  const int mk = MK == 1 ? 1 : a.mk;
+  const int mk = MK == 1 ? 1 : h.mk;
+  const bool first = D.first != 0;
+  const float floor_ = first ? -126.0f : h.log_floor;
   float g[8], v[8], m[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) { g[k] = 0.0f; v[k] = 0.0f; m[k] = 0.0f; }
 #pragma unroll
   for (int k = 0; k < 8; ++k)
-    if (k < cnt) g[k] = gp(ws)[W.glow + e0 + k];
+    if (k < cnt) g[k] = gp(ws)[L.glow + e0 + k];
   // ---- V
   float vo[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) vo[k] = 0.0f;
-  if (!a.first) {
+  if (!first) {
     if constexpr (VB == 0) {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < cnt) vo[k] = gp(a.v_fp32)[e0 + k];
+        if (k < cnt) vo[k] = gp(D.v_fp32)[e0 + k];
     } else if (v_ok) {
-      const float s_old = gp(a.v_scale)[vb], lm_old = gp(a.v_min_log)[vb];
+      const float s_old = gp(D.v_scale)[vb], lm_old = gp(D.v_min_log)[vb];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         uint32_t c;
-        if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(a.v_q))[e0 + k];
-        else c = gp(reinterpret_cast<const uint16_t*>(a.v_q))[e0 + k];
+        if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(D.v_q))[e0 + k];
+        else c = gp(reinterpret_cast<const uint16_t*>(D.v_q))[e0 + k];
         const float lm2 = VB == 8 ? 254.0f : 65534.0f;
         vo[k] = c ? exp2_exact(((float)(c - 1) * s_old) / lm2 + lm_old) : 0.0f;
       }
@@ -314,7 +583,7 @@ __global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const float g2 = g[k] * g[k];
-    v[k] = a.first ? g2 * a.bv : lerp_ref(vo[k], g2, a.bv);
+    v[k] = first ? g2 * h.bv : lerp_ref(vo[k], g2, h.bv);
     if (k >= cnt) v[k] = 0.0f;
   }
   // ---- M
@@ -325,38 +594,38 @@ __global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
     if (MK == 3) {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < cnt) mo[k] = gp(a.m_fp32)[e0 + k];
+        if (k < cnt) mo[k] = gp(D.m_fp32)[e0 + k];
     } else if (m_ok) {
-      const float ms = gp(a.m_scale)[mb];
+      const float ms = gp(D.m_scale)[mb];
       if (mk == 2 || mk == 4) {
-        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(a.m_q + (e0 >> 1)));
+        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
           mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
         }
       } else {
-        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(a.m_q + e0));
+        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
 #pragma unroll
         for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], a.w_m) : 0.0f;
+    for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
   }
   // ---- u
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (k < cnt) {
       const float x = MK != 0 ? m[k] : g[k];
-      gp(ws)[W.u + e0 + k] = x / (sqrtf(v[k]) + a.aeps);
+      gp(ws)[L.u + e0 + k] = x / (sqrtf(v[k]) + h.aeps);
     }
   }
   // ---- V state
   if constexpr (VB == 0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (k < cnt) gp(a.v_fp32)[e0 + k] = v[k];
+      if (k < cnt) gp(D.v_fp32)[e0 + k] = v[k];
   } else {
     uint32_t vmaxb = 0u, vkey = 0xFFFFFFFFu;
 #pragma unroll
@@ -373,29 +642,29 @@ __global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
       const int wpb = VL >> 6, w0 = (wave / wpb) * wpb;
       bmax = xw[w0 * 2];
       bkey = __float_as_uint(xw[w0 * 2 + 1]);
-      for (int w = 1; w < wpb; ++w) {
-        bmax = fmaxf(bmax, xw[(w0 + w) * 2]);
-        bkey = min(bkey, __float_as_uint(xw[(w0 + w) * 2 + 1]));
+      for (int ww = 1; ww < wpb; ++ww) {
+        bmax = fmaxf(bmax, xw[(w0 + ww) * 2]);
+        bkey = min(bkey, __float_as_uint(xw[(w0 + ww) * 2 + 1]));
       }
     }
     const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
     constexpr int LM2 = VB == 8 ? 254 : 65534;
-    const ALFit f = al_refit(bmax, mnz, a.floor_, (float)LM2);
+    const ALFit f = al_refit(bmax, mnz, floor_, (float)LM2);
     if (v_ok) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t code = al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f));
-        if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(a.v_q))[e0 + k] = (uint8_t)code;
-        else gp(reinterpret_cast<uint16_t*>(a.v_q))[e0 + k] = (uint16_t)code;
+        if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(D.v_q))[e0 + k] = (uint8_t)code;
+        else gp(reinterpret_cast<uint16_t*>(D.v_q))[e0 + k] = (uint16_t)code;
       }
-      if ((lane & (VL - 1)) == 0) { gp(a.v_scale)[vb] = f.s; gp(a.v_min_log)[vb] = f.lmin; }
+      if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }
     }
   }
   // ---- M state
   if constexpr (MK == 3) {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (k < cnt) gp(a.m_fp32)[e0 + k] = m[k];
+      if (k < cnt) gp(D.m_fp32)[e0 + k] = m[k];
   } else if constexpr (MK != 0) {
     uint32_t ab = 0u;
 #pragma unroll
@@ -407,195 +676,216 @@ __global__ __launch_bounds__(256) void k_ap_low(ApArgs a) {
       __syncthreads();
       const int wpb = ML >> 6, w0 = (wave / wpb) * wpb;
       bam = xw[8 + w0];
-      for (int w = 1; w < wpb; ++w) bam = fmaxf(bam, xw[8 + w0 + w]);
+      for (int ww = 1; ww < wpb; ++ww) bam = fmaxf(bam, xw[8 + w0 + ww]);
     }
     if (m_ok) {
       const float am = fmaxf(bam, 1e-12f);
       const float ram = fast_rcp(am);
       if (mk == 2 || mk == 4) {
-        uint32_t w = 0;
+        uint32_t wq = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t hi = m_encode(mk, m[2 * j], am, ram);
-          const uint32_t lo = m_encode(mk, m[2 * j + 1], am, ram);
-          w |= ((hi << 4) | lo) << (8 * j);
+          const uint32_t hi4 = m_encode(mk, m[2 * j], am, ram);
+          const uint32_t lo4 = m_encode(mk, m[2 * j + 1], am, ram);
+          wq |= ((hi4 << 4) | lo4) << (8 * j);
         }
-        *gp(reinterpret_cast<uint32_t*>(a.m_q + (e0 >> 1))) = w;
+        *gp(reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1))) = wq;
       } else {
         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) w0 |= m_encode(mk, m[k], am, ram) << (8 * k);
 #pragma unroll
         for (int k = 0; k < 4; ++k) w1 |= m_encode(mk, m[k + 4], am, ram) << (8 * k);
-        *gp(reinterpret_cast<u32x2*>(a.m_q + e0)) = u32x2{w0, w1};
+        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
       }
-      if ((lane & (ML - 1)) == 0) gp(a.m_scale)[mb] = am;
+      if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
     }
   }
 }
 
 // ------------------------------------------------------------ scale
-// s_ch = ||u_ch|| / (||g_low_ch|| + 1e-8) (optimizer.py:2997-3001): right side one
-// wave per row of g_low, left side one lane per column walking the r rows;
-// norms as sqrt of fp32 sums accumulated in double.  Partials per workgroup:
-// channel sum(ngsq * s^2); tensor sum(u^2), sum(g_low^2).
-__global__ __launch_bounds__(256) void k_ap_scale(ApArgs a) {
-  __shared__ double sd[4];
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  const int64_t R = a.R, C = a.C, r = a.r;
-  const bool right = R >= C;
-  float* ws = a.ws;
-  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  double acc0 = 0.0, acc1 = 0.0;
-  if (!a.channel) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + lane; i < W.n_low; i += (int64_t)gridDim.x * 256) {
-      const float u = gp(ws)[W.u + i], g = gp(ws)[W.glow + i];
-      acc0 += (double)(u * u);
-      acc1 += (double)(g * g);
-    }
-  } else if (right) {
-    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < R; row += (int64_t)gridDim.x * 4) {
+// s_ch = ||u_ch|| / (||g_low_ch|| + 1e-8) (optimizer.py:2997-3001), norms as
+// sqrt of fp32 squares summed in double.  Right side: one wave per g_low row
+// (16 rows per workgroup); left side: one lane per g_low column walking a
+// quarter of the r rows, the four waves combined in LDS (64 columns per
+// workgroup).  Partials per workgroup: sum ngsq * s^2 (channel) or sum u^2 and
+// sum g_low^2 (tensor).
+__global__ __launch_bounds__(256) void k_ap_scale(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
+  __shared__ double sd[2 * 256 + 4];
+  int wg;
+  const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, wg);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t R = D.R, C = D.C, r = D.r;
+  const float* U = D.ws + L.u;
+  const float* GL = D.ws + L.glow;
+  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63;
+  double a0 = 0.0, a1 = 0.0, a2 = 0.0;
+  if (R >= C) {
+#pragma unroll 1
+    for (int i = 0; i < kApScR / 4; ++i) {
+      const int64_t row = (int64_t)wg * kApScR + w * (kApScR / 4) + i;
+      if (row >= R) break;
       double su = 0.0, sg = 0.0;
-      for (int64_t k = wl; k < r; k += 64) {
-        const float u = gp(ws)[W.u + row * r + k], g = gp(ws)[W.glow + row * r + k];
+      for (int64_t k = l; k < r; k += 64) {
+        const float u = gp(U)[row * r + k], g = gp(GL)[row * r + k];
         su += (double)(u * u);
         sg += (double)(g * g);
       }
       su = grp_sum_d(su, 64);
       sg = grp_sum_d(sg, 64);
-      if (wl == 0) {
-        float s = sqrtf((float)su) / (sqrtf((float)sg) + 1e-8f);
-        if (a.front) s = s * a.sv;
-        gp(ws)[W.fin + row] = s;
-        const float ng = gp(ws)[W.ngsq + row];
-        acc0 += (double)(ng * (s * s));
+      if (l == 0) {
+        if (h.channel) {
+          float s = sqrtf((float)su) / (sqrtf((float)sg) + 1e-8f);
+          if (h.front) s = s * h.sv;
+          gp(D.ws + L.fin)[row] = s;
+          a0 += (double)(gp(D.ws + L.ngsq)[row] * (s * s));
+        } else {
+          a1 += su;
+          a2 += sg;
+        }
       }
     }
   } else {
-    for (int64_t c = (int64_t)blockIdx.x * 256 + lane; c < C; c += (int64_t)gridDim.x * 256) {
-      double gc = 0.0;
-      for (int64_t q = 0; q < W.nrc; ++q) gc += ws_d(ws, W.gcol, q * C + c);
-      const float gn = sqrtf((float)gc);
-      gp(ws)[W.ngsq + c] = gn * gn;
-      double su = 0.0, sg = 0.0;
-      for (int64_t k = 0; k < r; ++k) {
-        const float u = gp(ws)[W.u + k * C + c], g = gp(ws)[W.glow + k * C + c];
+    const int64_t c = (int64_t)wg * kApScL + l;
+    double su = 0.0, sg = 0.0;
+    if (c < C) {
+#pragma unroll 4
+      for (int64_t k = w; k < r; k += 4) {
+        const float u = gp(U)[k * C + c], g = gp(GL)[k * C + c];
         su += (double)(u * u);
         sg += (double)(g * g);
       }
-      float s = sqrtf((float)su) / (sqrtf((float)sg) + 1e-8f);
-      if (a.front) s = s * a.sv;
-      gp(ws)[W.fin + c] = s;
-      const float ng = gp(ws)[W.ngsq + c];
-      acc0 += (double)(ng * (s * s));
+    }
+    sd[w * 64 + l] = su;
+    sd[256 + w * 64 + l] = sg;
+    __syncthreads();
+    if (w == 0 && c < C) {
+      su = ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
+      sg = ((sd[256 + l] + sd[320 + l]) + sd[384 + l]) + sd[448 + l];
+      if (h.channel) {
+        float s = sqrtf((float)su) / (sqrtf((float)sg) + 1e-8f);
+        if (h.front) s = s * h.sv;
+        gp(D.ws + L.fin)[c] = s;
+        a0 = (double)(gp(D.ws + L.ngsq)[c] * (s * s));
+      } else {
+        a1 = su;
+        a2 = sg;
+      }
     }
   }
-  const double t0 = ap_wg_sum(acc0, sd);
-  const double t1 = ap_wg_sum(acc1, sd);
+  const double t0 = ap_wg_sum(a0, sd + 512);
+  const double t1 = ap_wg_sum(a1, sd + 512);
+  const double t2 = ap_wg_sum(a2, sd + 512);
   if (lane == 0) {
-    ws_d_set(ws, W.spart, blockIdx.x, t0);
-    ws_d_set(ws, W.spart, kApNP + blockIdx.x, t1);
+    ws_d_set(D.ws, L.spart, 3 * (int64_t)wg, t0);
+    ws_d_set(D.ws, L.spart, 3 * (int64_t)wg + 1, t1);
+    ws_d_set(D.ws, L.spart, 3 * (int64_t)wg + 2, t2);
   }
 }
 
-// ------------------------------------------------------------ per-tensor scalars
-// One workgroup: alpha (optimizer.py:832-856), norm_unscaled and Fira on it
-// (optimizer.py:3003-3024, 760-782 with the key scaled_grad_norm_prev), the
-// final channel scales s * fira (* sqrt(apollo_scale) at the back), the RMS
-// denominator, the step -alpha/denom with bias correction, and the decay.
-__global__ __launch_bounds__(256) void k_ap_scalars(ApArgs a) {
+// ------------------------------------------------------------ per-matrix scalars
+// One workgroup per matrix: alpha (optimizer.py:832-856), norm_unscaled and Fira
+// on it (optimizer.py:3003-3024, 760-782 with the key scaled_grad_norm_prev),
+// the RMS denominator, the step -alpha/denom with bias correction, the decay.
+__global__ __launch_bounds__(256) void k_ap_scalars(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   __shared__ double sd[4];
-  __shared__ float sh[2];
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  float* ws = a.ws;
+  ApDesc D;
+  if (tab == nullptr) {
+    D = one;
+  } else {
+    const A8_C uint64_t* wsrc = (const A8_C uint64_t*)(cp(tab) + blockIdx.x);
+    uint64_t buf[sizeof(ApDesc) / 8];
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(ApDesc) / 8); ++i) buf[i] = wsrc[i];
+    __builtin_memcpy(&D, buf, sizeof(ApDesc));
+  }
+  (void)ntab;
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  float* ws = D.ws;
   const int lane = threadIdx.x;
-  double pg = 0.0, pp = 0.0, s0 = 0.0, s1 = 0.0;
-  for (int k = lane; k < a.ngn; k += 256) { pg += ws_d(ws, W.gpart, k); pp += ws_d(ws, W.ppart, k); }
-  for (int k = lane; k < a.nsc; k += 256) { s0 += ws_d(ws, W.spart, k); s1 += ws_d(ws, W.spart, kApNP + k); }
+  double pg = 0.0, pp = 0.0, s0 = 0.0, s1 = 0.0, s2 = 0.0;
+  for (int64_t k = lane; k < L.ntr; k += 256) { pg += ws_d(ws, L.gpart, k); pp += ws_d(ws, L.ppart, k); }
+  for (int64_t k = lane; k < L.nsc; k += 256) {
+    s0 += ws_d(ws, L.spart, 3 * k);
+    s1 += ws_d(ws, L.spart, 3 * k + 1);
+    s2 += ws_d(ws, L.spart, 3 * k + 2);
+  }
   pg = ap_wg_sum(pg, sd);
   pp = ap_wg_sum(pp, sd);
   s0 = ap_wg_sum(s0, sd);
   s1 = ap_wg_sum(s1, sd);
-  const int64_t numel = a.R * a.C;
-  if (lane == 0) {
-    const float rho = a.lr ? *gp(a.lr) : a.lr_val;
-    float alpha = rho;
-    if (a.scale_param) {
-      const float rms = sqrtf((float)pp) / (float)sqrt((double)numel);
-      alpha = fmaxf(rms, a.eps2) * rho;
-    }
-    float s_t = 1.0f;                 // tensor scale
-    float nun;                        // norm_unscaled
-    if (a.channel) {
-      nun = sqrtf((float)s0);
-    } else {
-      s_t = sqrtf((float)s0) / (sqrtf((float)s1) + 1e-8f);
-      if (a.front) s_t = s_t * a.sv;
-      nun = sqrtf((float)pg) * s_t;
-    }
-    float fs = 1.0f;
-    if (a.fira) {
-      const float curr = __builtin_isfinite(nun) ? nun : 0.0f;
-      float next = curr;
-      if (a.has_fira_prev) {
-        const float p = *gp(a.fira_prev);
-        const float ratio = curr / (p + 1e-8f);
-        const float lim = (ratio != ratio ? ratio : fmaxf(ratio, a.margin)) / a.margin;
-        const bool reset = p < 1e-6f;
-        fs = reset ? 1.0f : 1.0f / lim;
-        next = reset ? curr : curr * fs;
-      }
-      *gp(a.fira_prev) = next;
-    }
-    float denom = 1.0f;
-    if (a.d > 0.0f) denom = fmaxf(nun / (float)(sqrt((double)numel) * (double)a.d), 1.0f);
-    float step = -alpha / denom;
-    if (a.bias_mode == 1) step = step * a.bias_factor;
-    else if (a.bias_mode == 2) step = step / a.bias_factor;
-    float dec = 1.0f;
-    if (a.wd_mode == 1) dec = 1.0f - alpha * a.wd;
-    else if (a.wd_mode == 2) dec = 1.0f - rho * a.wd;
-    float fin_t = s_t;
-    if (a.fira) fin_t = fin_t * fs;
-    if (!a.front) fin_t = fin_t * a.sv;
-    float* sl = ws + W.scal;
-    gp(sl)[0] = step;
-    gp(sl)[1] = dec;
-    gp(sl)[3] = fin_t;
-    gp(sl)[4] = alpha;
-    gp(sl)[5] = nun;
-    gp(sl)[6] = fs;
-    sh[0] = fs;
+  s2 = ap_wg_sum(s2, sd);
+  if (lane != 0) return;
+  const int64_t numel = D.R * D.C;
+  const float rho = D.lr ? *gp(D.lr) : h.lr_val;
+  float alpha = rho;
+  if (h.scale_param) {
+    const float rms = sqrtf((float)pp) / (float)sqrt((double)numel);
+    alpha = fmaxf(rms, h.eps2) * rho;
   }
-  __syncthreads();
-  if (a.channel) {
-    const float fs = sh[0];
-    for (int64_t c = lane; c < W.nch; c += 256) {
-      float f = gp(ws)[W.fin + c];
-      if (a.fira) f = f * fs;
-      if (!a.front) f = f * a.sv;
-      gp(ws)[W.fin + c] = f;
-    }
+  float s_t = 1.0f;   // tensor scale
+  float nun;          // norm_unscaled
+  if (h.channel) {
+    nun = sqrtf((float)s0);
+  } else {
+    s_t = sqrtf((float)s1) / (sqrtf((float)s2) + 1e-8f);
+    if (h.front) s_t = s_t * h.sv;
+    nun = sqrtf((float)pg) * s_t;
   }
+  float fs = 1.0f;
+  if (h.fira) {
+    const float curr = __builtin_isfinite(nun) ? nun : 0.0f;
+    float next = curr;
+    if (D.has_prev) {
+      const float p = *gp(D.fira_prev);
+      const float ratio = curr / (p + 1e-8f);
+      const float lim = (ratio != ratio ? ratio : fmaxf(ratio, h.margin)) / h.margin;
+      const bool reset = p < 1e-6f;
+      fs = reset ? 1.0f : 1.0f / lim;
+      next = reset ? curr : curr * fs;
+    }
+    *gp(D.fira_prev) = next;
+  }
+  float denom = 1.0f;
+  if (h.d > 0.0f) denom = fmaxf(nun / (float)(sqrt((double)numel) * (double)h.d), 1.0f);
+  float step = -alpha / denom;
+  if (h.bias_mode == 1) step = step * D.bias_factor;
+  else if (h.bias_mode == 2) step = step / D.bias_factor;
+  float dec = 1.0f;
+  if (h.wd_mode == 1) dec = 1.0f - alpha * h.wd;
+  else if (h.wd_mode == 2) dec = 1.0f - rho * h.wd;
+  float fin_t = s_t;
+  if (h.fira) fin_t = fin_t * fs;
+  if (!h.front) fin_t = fin_t * h.sv;
+  float* sl = ws + L.scal;
+  gp(sl)[0] = step;
+  gp(sl)[1] = dec;
+  gp(sl)[3] = fin_t;
+  gp(sl)[4] = alpha;
+  gp(sl)[5] = nun;
+  gp(sl)[6] = fs;
 }
 
 // ------------------------------------------------------------ full-rank writeback
 // Deterministic (optimizer.py:3071-3077): p := p * decay (rounded to T), then
 // channel p + (step * G) * f_ch (addcmul) or tensor fma(step * f, G, p) (add_),
-// rounded to T.  SR (optimizer.py:3058-3063 with the stream of kernels.cu:48-87):
+// rounded to T; f_ch = (s_ch * fira) * sqrt(apollo_scale) at the back.  SR
+// (optimizer.py:3058-3063 with the stream of kernels.cu:48-87):
 // x = (p * decay) + (G * f) * step in fp32, stochastically rounded.
 template <typename T, bool SR>
-__global__ __launch_bounds__(256) void k_ap_apply(ApArgs a) {
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  const int64_t R = a.R, C = a.C, n = R * C;
+__global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
+  int unit;
+  const ApDesc D = ap_pick(one, tab, ntab, 3, (int)blockIdx.x, unit);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t R = D.R, C = D.C, n = R * C;
   const bool right = R >= C;
-  const float* ws = a.ws;
-  const float* sl = ws + W.scal;
-  const float step = gp(sl)[0], dec = gp(sl)[1], fin_t = gp(sl)[3];
-  const bool has_dec = a.wd_mode != 0;
-  T* P = reinterpret_cast<T*>(a.param);
-  const T* G = reinterpret_cast<const T*>(a.grad);
-  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  const float* ws = D.ws;
+  const float* sl = ws + L.scal;
+  const float step = gp(sl)[0], dec = gp(sl)[1], fin_t = gp(sl)[3], fs = gp(sl)[6];
+  const bool has_dec = h.wd_mode != 0;
+  T* P = reinterpret_cast<T*>(D.param);
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  const int64_t e0 = (int64_t)unit * kApApp + (int64_t)threadIdx.x * 8;
   if (e0 >= n) return;
   float g[8], p[8];
   load8<T>(G, e0, n, g);
@@ -603,23 +893,33 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApArgs a) {
   int64_t row = e0 / C;
   int64_t col = e0 - row * C;
   const float ts = step * fin_t;   // tensor: alpha = step * final_scale
+  float f = fin_t;
+  int64_t fch = -1;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (e0 + k < n) {
       const float gk = scrub(g[k]);
-      const float f = a.channel ? gp(ws)[W.fin + (right ? row : col)] : fin_t;
+      if (h.channel) {
+        const int64_t ch = right ? row : col;
+        if (ch != fch) {
+          f = gp(ws + L.fin)[ch];
+          if (h.fira) f = f * fs;
+          if (!h.front) f = f * h.sv;
+          fch = ch;
+        }
+      }
       if constexpr (SR) {
         float x = ld1<T>(P, e0 + k);
         if (has_dec) x = x * dec;
         x = x + (gk * f) * step;
-        const T rr = sr_round<T>(x, a.sr_seed, a.sr_step, (uint64_t)(e0 + k));
+        const T rr = sr_round<T>(x, D.sr_seed, D.step, (uint64_t)(e0 + k));
         uint16_t bits;
         __builtin_memcpy(&bits, &rr, 2);
         gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = bits;
       } else {
         float x = p[k];
         if (has_dec) x = to_f<T>(from_f<T>(x * dec));
-        if (a.channel) x = x + (step * gk) * f;
+        if (h.channel) x = x + (step * gk) * f;
         else x = __builtin_fmaf(ts, gk, x);
         p[k] = x;
       }
@@ -631,7 +931,7 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApArgs a) {
 
 hipError_t apollo_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
 
-// ------------------------------------------------------------ rocBLAS
+// ------------------------------------------------------------ rocBLAS (fp32 G)
 static rocblas_handle g_blas[64];
 
 static int blas_handle(rocblas_handle* out) {
@@ -648,63 +948,154 @@ static int blas_handle(rocblas_handle* out) {
 
 // g_low = G P^T (right) or P^T G (left), row-major, through column-major GEMMs:
 // right: g_low^T (r x R) = PT^T (r x C) . G^T (C x R); left: g_low^T (C x r) = G^T . PT^T.
-static int ap_gemm(rocblas_handle hb, int dtype, const ApArgs& a, const ApWs& W, const float* pt,
-                   int split_fresh, hipStream_t st) {
-  const bool right = a.R >= a.C;
-  const int64_t R = a.R, C = a.C, r = a.r;
-  float* glow = a.ws + W.glow;
+static int ap_sgemm(rocblas_handle hb, const ApDesc& D, const ApL& L, hipStream_t st) {
+  const int64_t R = D.R, C = D.C, r = D.r;
   const float one = 1.0f, zero = 0.0f;
+  float* glow = D.ws + L.glow;
   rocblas_set_stream(hb, st);
-  if (dtype == A8_F32) {
-    rocblas_status s;
-    if (right)
-      s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)r, (rocblas_int)R,
-                        (rocblas_int)C, &one, pt, (rocblas_int)r, reinterpret_cast<const float*>(a.grad),
-                        (rocblas_int)C, &zero, glow, (rocblas_int)r);
-    else
-      s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)C, (rocblas_int)r,
-                        (rocblas_int)R, &one, reinterpret_cast<const float*>(a.grad), (rocblas_int)C, pt,
-                        (rocblas_int)R, &zero, glow, (rocblas_int)C);
-    return s == rocblas_status_success ? 0 : set_error(A8_ERR_HIP, "rocblas_sgemm failed");
-  }
-  // bf16 G: three bf16 GEMMs against the split P^T, accumulated in fp32
-  __hip_bfloat16* sp = reinterpret_cast<__hip_bfloat16*>(a.ws + W.split);
-  const int64_t np = r * W.K;
-  if (split_fresh) {
-    const int64_t nb = (np + 255) / 256;
-    hipLaunchKernelGGL(k_ap_split, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, pt, np, sp);
-    int rc = check_launch("k_ap_split");
-    if (rc) return rc;
-  }
-  for (int t = 0; t < 3; ++t) {
-    const void* pterm = sp + t * np;
-    const float* beta = t == 0 ? &zero : &one;
-    rocblas_status s;
-    if (right)
-      s = rocblas_gemm_ex(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)r, (rocblas_int)R,
-                          (rocblas_int)C, &one, pterm, rocblas_datatype_bf16_r, (rocblas_int)r, a.grad,
-                          rocblas_datatype_bf16_r, (rocblas_int)C, beta, glow, rocblas_datatype_f32_r,
-                          (rocblas_int)r, glow, rocblas_datatype_f32_r, (rocblas_int)r, rocblas_datatype_f32_r,
-                          rocblas_gemm_algo_standard, 0, 0);
-    else
-      s = rocblas_gemm_ex(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)C, (rocblas_int)r,
-                          (rocblas_int)R, &one, a.grad, rocblas_datatype_bf16_r, (rocblas_int)C, pterm,
-                          rocblas_datatype_bf16_r, (rocblas_int)R, beta, glow, rocblas_datatype_f32_r,
-                          (rocblas_int)C, glow, rocblas_datatype_f32_r, (rocblas_int)C, rocblas_datatype_f32_r,
-                          rocblas_gemm_algo_standard, 0, 0);
-    if (s != rocblas_status_success) return set_error(A8_ERR_HIP, "rocblas_gemm_ex (bf16) failed");
-  }
-  return 0;
+  rocblas_status s;
+  if (R >= C)
+    s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)r, (rocblas_int)R,
+                      (rocblas_int)C, &one, D.proj_t, (rocblas_int)r, reinterpret_cast<const float*>(D.grad),
+                      (rocblas_int)C, &zero, glow, (rocblas_int)r);
+  else
+    s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)C, (rocblas_int)r,
+                      (rocblas_int)R, &one, reinterpret_cast<const float*>(D.grad), (rocblas_int)C, D.proj_t,
+                      (rocblas_int)R, &zero, glow, (rocblas_int)C);
+  return s == rocblas_status_success ? 0 : set_error(A8_ERR_HIP, "rocblas_sgemm failed");
 }
 
 template <int VB>
-static void launch_low(int mkt, unsigned nb, const ApArgs& a, hipStream_t st) {
+static void launch_low(int mkt, unsigned nb, const ApDesc& one, const ApDesc* tab, int ntab, const ApHyp& h,
+                       hipStream_t st) {
   switch (mkt) {
-    case 0: hipLaunchKernelGGL((k_ap_low<VB, 0>), dim3(nb), dim3(256), 0, st, a); break;
-    case 1: hipLaunchKernelGGL((k_ap_low<VB, 1>), dim3(nb), dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((k_ap_low<VB, 3>), dim3(nb), dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((k_ap_low<VB, 2>), dim3(nb), dim3(256), 0, st, a); break;
+    case 0: hipLaunchKernelGGL((k_ap_low<VB, 0>), dim3(nb), dim3(256), 0, st, one, tab, ntab, h); break;
+    case 1: hipLaunchKernelGGL((k_ap_low<VB, 1>), dim3(nb), dim3(256), 0, st, one, tab, ntab, h); break;
+    case 3: hipLaunchKernelGGL((k_ap_low<VB, 3>), dim3(nb), dim3(256), 0, st, one, tab, ntab, h); break;
+    default: hipLaunchKernelGGL((k_ap_low<VB, 2>), dim3(nb), dim3(256), 0, st, one, tab, ntab, h); break;
   }
+}
+
+static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 4 * sizeof(int32_t)); }
+
+static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int n, void* table_dev,
+                      int64_t tbytes, double beta_val, double beta1, int has_m, float apollo_eps, float log_floor,
+                      int v_bits, int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
+                      float apollo_scale, int scale_front, int fira, float fira_margin, float d, float lr_val,
+                      float eps2, int scale_parameter, int bias_mode, float weight_decay, int wd_mode,
+                      void* stream) {
+  if (n <= 0) return 0;
+  if (!ts) return set_error(A8_ERR_ARG, "null tensor list");
+  if (dtype != A8_F32 && dtype != A8_BF16) return set_error(A8_ERR_DTYPE, "APOLLO supports fp32 and bf16 params");
+  if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
+  auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
+  if (v_bits && !(pow2(block_size) && block_size >= 128 && block_size <= 2048))
+    return set_error(A8_ERR_BLOCK, "APOLLO V block_size must be a power of two in [128, 2048]");
+  if (has_m && !m_fp32 && !(pow2(m_block_size) && m_block_size >= 32 && m_block_size <= 2048))
+    return set_error(A8_ERR_BLOCK, "APOLLO m_block_size must be a power of two in [32, 2048]");
+  if (n > 1 && (!table_dev || tbytes < table_bytes(n)))
+    return set_error(A8_ERR_SIZE, "table_dev too small: need a8_apollo_table_bytes(n)");
+  if (stochastic && dtype == A8_F32) stochastic = 0;
+  std::vector<ApDesc> tab((size_t)n);
+  std::vector<int32_t> first((size_t)4 * n);
+  int64_t ntile = 0, nunit = 0, nsc = 0, napp = 0;
+  for (int i = 0; i < n; ++i) {
+    const a8_apollo_tensor& t = ts[i];
+    if (!t.param || !t.grad || !t.proj_t || !t.workspace) return set_error(A8_ERR_ARG, "null pointer");
+    if (t.rows <= 0 || t.cols <= 0 || t.rank <= 0) return set_error(A8_ERR_SIZE, "empty APOLLO tensor");
+    if (t.rows * t.cols >= ((int64_t)1 << 31)) return set_error(A8_ERR_SIZE, "APOLLO tensor too large");
+    if (v_bits ? !(t.v_q && t.v_scale && t.v_min_log) : !t.v_fp32)
+      return set_error(A8_ERR_ARG, "APOLLO V state missing");
+    if (has_m && (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale))) return set_error(A8_ERR_ARG, "APOLLO M state missing");
+    if (fira && !t.fira_prev) return set_error(A8_ERR_ARG, "APOLLO Fira needs scaled_grad_norm_prev");
+    if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.workspace))
+      return set_error(A8_ERR_ALIGN, "APOLLO param, grad and workspace must be 16-byte aligned");
+    const ApL L = ap_layout(t.rows, t.cols, t.rank);
+    ApDesc& D = tab[(size_t)i];
+    D.grad = t.grad; D.param = t.param; D.ws = t.workspace; D.proj_t = t.proj_t;
+    D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_fp32 = t.v_fp32;
+    D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
+    D.fira_prev = t.fira_prev; D.lr = t.lr;
+    D.R = t.rows; D.C = t.cols; D.r = t.rank;
+    D.sr_seed = t.sr_seed; D.step = t.step; D.bias_factor = t.bias_factor;
+    D.first = t.first_step ? 1 : 0; D.has_prev = t.has_fira_prev ? 1 : 0;
+    D.valign = (t.cols % (dtype == A8_F32 ? 4 : 8)) == 0 ? 1 : 0;
+    D.tile_begin = (int32_t)ntile; D.unit_begin = (int32_t)nunit; D.sc_begin = (int32_t)nsc;
+    D.app_begin = (int32_t)napp;
+    first[(size_t)i] = D.tile_begin;
+    first[(size_t)n + i] = D.unit_begin;
+    first[(size_t)2 * n + i] = D.sc_begin;
+    first[(size_t)3 * n + i] = D.app_begin;
+    ntile += L.ntile; nunit += L.nunit; nsc += L.nsc; napp += L.napp;
+    if (ntile > 0x7FFFFFFF || nunit > 0x7FFFFFFF || nsc > 0x7FFFFFFF || napp > 0x7FFFFFFF)
+      return set_error(A8_ERR_SIZE, "too many workgroups");
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const ApDesc* dtab = nullptr;
+  if (n > 1) {
+    std::vector<char> blob((size_t)table_bytes(n));
+    std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
+    std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 4 * (size_t)n);
+    if (hipMemcpyAsync(table_dev, blob.data(), blob.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "table upload failed");
+    dtab = reinterpret_cast<const ApDesc*>(table_dev);
+  }
+  const ApDesc& one = tab[0];
+  ApHyp h{};
+  h.bv = (float)beta_val; h.w_m = (float)(1.0 - beta1); h.aeps = apollo_eps; h.log_floor = log_floor;
+  h.lr_val = lr_val; h.eps2 = eps2; h.wd = weight_decay; h.d = d;
+  h.margin = (float)(1.0 + (double)fira_margin); h.sv = (float)sqrt((double)apollo_scale);
+  int lbv = 0, lbm = 0;
+  while ((1 << lbv) < (v_bits ? block_size : 2048)) ++lbv;
+  while ((1 << lbm) < ((has_m && !m_fp32) ? m_block_size : 32)) ++lbm;
+  h.lbv = lbv; h.lbm = lbm;
+  h.mk = has_m && !m_fp32 ? (m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4)) : 0;
+  h.channel = channel ? 1 : 0; h.front = scale_front ? 1 : 0; h.fira = fira ? 1 : 0;
+  h.scale_param = scale_parameter ? 1 : 0; h.bias_mode = bias_mode; h.wd_mode = wd_mode;
+  int rc;
+  // projection (+ channel norms of G)
+  if (dtype == A8_BF16) {
+    for (int i = 0; i < n; ++i) {
+      if (!ts[i].proj_fresh) continue;
+      const ApDesc& D = tab[(size_t)i];
+      const ApL L = ap_layout(D.R, D.C, D.r);
+      const int64_t nb = (L.rp * L.Kp + 255) / 256;
+      hipLaunchKernelGGL(k_ap_split, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, D.proj_t, D.r, L.K,
+                         (int)(D.R >= D.C), L.rp, L.Kp, reinterpret_cast<uint16_t*>(D.ws + L.psplit));
+      if ((rc = check_launch("k_ap_split"))) return rc;
+    }
+    hipLaunchKernelGGL(k_ap_proj, dim3((unsigned)ntile), dim3(256), 0, st, one, dtab, n, h.scale_param);
+    if ((rc = check_launch("k_ap_proj"))) return rc;
+  } else {
+    rocblas_handle hb;
+    if ((rc = blas_handle(&hb))) return rc;
+    for (int i = 0; i < n; ++i) {
+      const ApDesc& D = tab[(size_t)i];
+      const ApL L = ap_layout(D.R, D.C, D.r);
+      if ((rc = ap_sgemm(hb, D, L, st))) return rc;
+      hipLaunchKernelGGL(k_ap_norm32, dim3((unsigned)L.ntr), dim3(256), 0, st, D, h.scale_param);
+      if ((rc = check_launch("k_ap_norm32"))) return rc;
+      const int64_t nf = (L.n_low + 255) / 256;
+      hipLaunchKernelGGL(k_ap_fixlow, dim3((unsigned)(nf < 1024 ? nf : 1024)), dim3(256), 0, st, D);
+      if ((rc = check_launch("k_ap_fixlow"))) return rc;
+    }
+  }
+  const int mkt = !has_m ? 0 : (m_fp32 ? 3 : (h.mk == 1 ? 1 : 2));
+  if (v_bits == 8) launch_low<8>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+  else if (v_bits == 16) launch_low<16>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+  else launch_low<0>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+  if ((rc = check_launch("k_ap_low"))) return rc;
+  hipLaunchKernelGGL(k_ap_scale, dim3((unsigned)nsc), dim3(256), 0, st, one, dtab, n, h);
+  if ((rc = check_launch("k_ap_scale"))) return rc;
+  hipLaunchKernelGGL(k_ap_scalars, dim3((unsigned)n), dim3(256), 0, st, one, dtab, n, h);
+  if ((rc = check_launch("k_ap_scalars"))) return rc;
+  if (dtype == A8_F32)
+    hipLaunchKernelGGL((k_ap_apply<float, false>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  else if (stochastic)
+    hipLaunchKernelGGL((k_ap_apply<__hip_bfloat16, true>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  else
+    hipLaunchKernelGGL((k_ap_apply<__hip_bfloat16, false>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  return check_launch("k_ap_apply");
 }
 
 }  // namespace a8
@@ -714,9 +1105,12 @@ using namespace a8;
 extern "C" {
 
 int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int channel) {
+  (void)channel;
   if (rows <= 0 || cols <= 0 || rank <= 0) return 0;
-  return ap_layout(rows, cols, rank, channel ? 1 : 0).total;
+  return ap_layout(rows, cols, rank).total;
 }
+
+int64_t a8_apollo_table_bytes(int ntensors) { return ntensors > 0 ? table_bytes(ntensors) : 0; }
 
 int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int first_step, int proj_fresh,
                    double beta_val, double beta1, int has_m, float apollo_eps, float log_floor, int v_bits,
@@ -724,81 +1118,27 @@ int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int fir
                    float apollo_scale, int scale_front, int fira, float fira_margin, float d, float lr_val,
                    float eps2, int scale_parameter, int bias_mode, float bias_factor, float weight_decay,
                    int wd_mode, uint64_t sr_step, void* stream) {
-  if (!t || !t->param || !t->grad || !t->proj_t || !t->workspace) return set_error(A8_ERR_ARG, "null pointer");
-  if (dtype != A8_F32 && dtype != A8_BF16) return set_error(A8_ERR_DTYPE, "APOLLO supports fp32 and bf16 params");
-  if (t->rows <= 0 || t->cols <= 0 || t->rank <= 0) return set_error(A8_ERR_SIZE, "empty APOLLO tensor");
-  if (t->rows * t->cols >= ((int64_t)1 << 31)) return set_error(A8_ERR_SIZE, "APOLLO tensor too large");
-  if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
-  auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
-  if (v_bits && !(pow2(block_size) && block_size >= 128 && block_size <= 2048))
-    return set_error(A8_ERR_BLOCK, "APOLLO V block_size must be a power of two in [128, 2048]");
-  if (has_m && !m_fp32 && !(pow2(m_block_size) && m_block_size >= 32 && m_block_size <= 2048))
-    return set_error(A8_ERR_BLOCK, "APOLLO m_block_size must be a power of two in [32, 2048]");
-  if (v_bits ? !(t->v_q && t->v_scale && t->v_min_log) : !t->v_fp32)
-    return set_error(A8_ERR_ARG, "APOLLO V state missing");
-  if (has_m && (m_fp32 ? !t->m_fp32 : !(t->m_q && t->m_scale))) return set_error(A8_ERR_ARG, "APOLLO M state missing");
-  if (fira && !t->fira_prev) return set_error(A8_ERR_ARG, "APOLLO Fira needs scaled_grad_norm_prev");
-  if ((reinterpret_cast<uintptr_t>(t->param) | reinterpret_cast<uintptr_t>(t->grad)) & 15)
-    return set_error(A8_ERR_ARG, "APOLLO param and grad must be 16-byte aligned");
-  if (stochastic && dtype == A8_F32) stochastic = 0;
-  hipStream_t st = (hipStream_t)stream;
-  ApArgs a{};
-  a.param = t->param; a.grad = t->grad; a.R = t->rows; a.C = t->cols; a.r = t->rank;
-  a.v_q = t->v_q; a.v_scale = t->v_scale; a.v_min_log = t->v_min_log; a.v_fp32 = t->v_fp32;
-  a.m_q = t->m_q; a.m_scale = t->m_scale; a.m_fp32 = t->m_fp32;
-  a.fira_prev = t->fira_prev; a.has_fira_prev = t->has_fira_prev; a.lr = t->lr; a.ws = t->workspace;
-  a.sr_seed = t->sr_seed; a.sr_step = sr_step;
-  a.bv = (float)beta_val; a.w_m = (float)(1.0 - beta1); a.aeps = apollo_eps;
-  a.floor_ = first_step ? -126.0f : log_floor;
-  a.lr_val = lr_val; a.eps2 = eps2; a.bias_factor = bias_factor; a.bias_mode = bias_mode;
-  a.wd = weight_decay; a.wd_mode = wd_mode; a.d = d; a.margin = (float)(1.0 + (double)fira_margin);
-  a.sv = (float)sqrt((double)apollo_scale);
-  a.first = first_step; a.has_m = has_m; a.vb = v_bits; a.channel = channel ? 1 : 0; a.front = scale_front;
-  a.fira = fira; a.scale_param = scale_parameter;
-  int lbv = 0, lbm = 0;
-  while ((1 << lbv) < (v_bits ? block_size : 2048)) ++lbv;
-  while ((1 << lbm) < ((has_m && !m_fp32) ? m_block_size : 32)) ++lbm;
-  a.lbv = lbv; a.lbm = lbm;
-  a.mk = has_m && !m_fp32 ? (m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4)) : 0;
-  const ApWs W = ap_layout(a.R, a.C, a.r, a.channel);
-  const bool right = a.R >= a.C;
-  int64_t ngn = right ? (a.R + 3) / 4 : W.ncc * W.nrc;
-  ngn = ngn < kApNP ? ngn : kApNP;
-  int64_t nsc = !a.channel ? (W.n_low + 255) / 256 : (right ? (a.R + 3) / 4 : (a.C + 255) / 256);
-  nsc = nsc < kApNP ? nsc : kApNP;
-  a.ngn = (int)ngn; a.nsc = (int)nsc;
-  a.valign = (a.C % (dtype == A8_F32 ? 4 : 8)) == 0 ? 1 : 0;
+  if (!t) return set_error(A8_ERR_ARG, "null pointer");
+  a8_apollo_tensor one = *t;
+  one.first_step = first_step;
+  one.proj_fresh = proj_fresh;
+  one.step = sr_step;
+  one.bias_factor = bias_factor;
+  return apollo_run(dtype, stochastic, &one, 1, nullptr, 0, beta_val, beta1, has_m, apollo_eps, log_floor, v_bits,
+                    block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale, scale_front, fira,
+                    fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay, wd_mode, stream);
+}
 
-  rocblas_handle hb;
-  int rc = blas_handle(&hb);
-  if (rc) return rc;
-  if ((rc = ap_gemm(hb, dtype, a, W, t->proj_t, proj_fresh, st))) return rc;
-  const dim3 ggn = right ? dim3((unsigned)ngn) : dim3((unsigned)W.ncc, (unsigned)W.nrc);
-  if (dtype == A8_F32) hipLaunchKernelGGL((k_ap_gnorm<float>), ggn, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((k_ap_gnorm<__hip_bfloat16>), ggn, dim3(256), 0, st, a);
-  if ((rc = check_launch("k_ap_gnorm"))) return rc;
-  {
-    const int64_t nf = (W.n_low + 255) / 256;
-    const unsigned nfb = (unsigned)(nf < 1024 ? nf : 1024);
-    if (dtype == A8_F32) hipLaunchKernelGGL((k_ap_fixlow<float>), dim3(nfb), dim3(256), 0, st, a, t->proj_t);
-    else hipLaunchKernelGGL((k_ap_fixlow<__hip_bfloat16>), dim3(nfb), dim3(256), 0, st, a, t->proj_t);
-    if ((rc = check_launch("k_ap_fixlow"))) return rc;
-  }
-  const unsigned nlow = (unsigned)((W.n_low + kApUnit - 1) / kApUnit);
-  const int mkt = !has_m ? 0 : (m_fp32 ? 3 : (a.mk == 1 ? 1 : 2));
-  if (v_bits == 8) launch_low<8>(mkt, nlow, a, st);
-  else if (v_bits == 16) launch_low<16>(mkt, nlow, a, st);
-  else launch_low<0>(mkt, nlow, a, st);
-  if ((rc = check_launch("k_ap_low"))) return rc;
-  hipLaunchKernelGGL(k_ap_scale, dim3((unsigned)nsc), dim3(256), 0, st, a);
-  if ((rc = check_launch("k_ap_scale"))) return rc;
-  hipLaunchKernelGGL(k_ap_scalars, dim3(1), dim3(256), 0, st, a);
-  if ((rc = check_launch("k_ap_scalars"))) return rc;
-  const unsigned napp = (unsigned)((a.R * a.C + 2047) / 2048);
-  if (dtype == A8_F32) hipLaunchKernelGGL((k_ap_apply<float, false>), dim3(napp), dim3(256), 0, st, a);
-  else if (stochastic) hipLaunchKernelGGL((k_ap_apply<__hip_bfloat16, true>), dim3(napp), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((k_ap_apply<__hip_bfloat16, false>), dim3(napp), dim3(256), 0, st, a);
-  return check_launch("k_ap_apply");
+int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* ts, int ntensors, void* table_dev,
+                         int64_t table_bytes_, double beta_val, double beta1, int has_m, float apollo_eps,
+                         float log_floor, int v_bits, int block_size, int m_bits, int m_mode, int m_fp32,
+                         int m_block_size, int channel, float apollo_scale, int scale_front, int fira,
+                         float fira_margin, float d, float lr_val, float eps2, int scale_parameter, int bias_mode,
+                         float weight_decay, int wd_mode, void* stream) {
+  return apollo_run(dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m, apollo_eps,
+                    log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale,
+                    scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay,
+                    wd_mode, stream);
 }
 
 }  // extern "C"

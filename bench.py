@@ -13,13 +13,15 @@ Prints one JSON line: whole-step params/s, the dominant kernel's roofline
 (algorithmic bytes per launch / average launch time from HIP events on the
 launch stream) and a CPU baseline (the CPU oracle timed on the host cores).
 
-``--workload`` also measures two other BASELINE configurations on the same
+``--workload`` also measures the other BASELINE configurations on the same
 shapes (they are parity cases of the headline metric, reported for their own
 kernels): ``adafactor`` (C2: factored AL8, B_V 256, no beta1, Student-t grads,
-90% zero embedding rows) and ``came`` (C3: UF8 M, AL16 V and confidence, B_V
-2048, Fira on, per-tensor log-uniform gradient scales).  For those the
-roofline is the whole step's algorithmic bytes over its GPU time (HIP events
-around ``step()``).
+90% zero embedding rows), ``came`` (C3: UF8 M, AL16 V and confidence, B_V
+2048, Fira on, per-tensor log-uniform gradient scales) and ``apollo`` (C4:
+bf16 params and grads 1e-3*N(0,1), the reference's apollo preset at rank 256,
+gap 200, channel scale, Fira, UF8 M / AL8 V low-rank states, SR writeback).
+For those the roofline is the whole step's algorithmic bytes over its GPU time
+(HIP events around ``step()``); apollo also reports the projection's flops.
 """
 import argparse
 import json
@@ -73,6 +75,33 @@ def step_bytes(shapes, bv=2048, bm=256, min8=4096):
     return q, f
 
 
+APOLLO = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=False, relative_step=False,
+              scale_parameter=False, scale_weight_decay=False, d=0.0, eps=(1e-6, 1e-3), apollo_eps=1e-6,
+              apollo_factorize=False, apollo_update_proj_gap=200, apollo_scale_type="channel", apollo_scale=1.0,
+              apollo_scale_front=False, apollo_cache_proj=True, enable_fira_for_apollo=True, apollo_rank=256,
+              lr=1e-3, block_size=2048, m_block_size=256, m_quant_type="uf8", v_quant_type="al8",
+              stochastic_round_writeback=True)
+
+
+def apollo_step_bytes_flops(shapes, rank=256, bs=2048, mbs=256):
+    """Algorithmic bytes and projection flops of one APOLLO step (C4, bf16).
+    Per matrix element: g read by the projection and by the writeback, p read
+    and written = 8 B.  Per low-rank element (R*r or r*C): V code r+w and M code
+    r+w = 4 B, plus their block scales; per matrix the fp32 P^T (4 r K B).  The
+    projection is 2 R C r flops.  The 1-D vectors (bf16 p, fp32 V and M): 22 B."""
+    nbytes = flops = 0.0
+    for s in shapes:
+        if len(s) < 2:
+            nbytes += 22.0 * s[0]
+            continue
+        R, C = s
+        right = R >= C
+        n_low = (R if right else C) * rank
+        nbytes += 8.0 * R * C + 4.0 * n_low + n_low * (8.0 / bs + 8.0 / mbs) + 4.0 * rank * (C if right else R)
+        flops += 2.0 * R * C * rank
+    return nbytes, flops
+
+
 def factored_step_bytes(shapes, workload):
     """Algorithmic bytes of one factored step: per matrix element, adafactor (C2:
     scale_parameter, d = 1) reads g+p for the statistics, g for the norm pass and
@@ -93,6 +122,8 @@ def factored_step_bytes(shapes, workload):
 
 
 def make_grad(kind, shape, gen, dev, i, embed):
+    if kind == "apollo":
+        return torch.randn(shape, device=dev, generator=gen) * 1e-3
     if kind == "adamw":
         g = torch.randn(shape, device=dev, generator=gen) * 1e-3
         return g * (torch.rand(shape, device=dev, generator=gen) >= 0.05)
@@ -149,8 +180,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="after timing, run a plain 256 MiB fp32 copy (for counter calibration)")
-    ap.add_argument("--workload", default="adamw", choices=["adamw", "adafactor", "came"],
-                    help="adamw (default, the headline metric), adafactor (C2) or came (C3)")
+    ap.add_argument("--workload", default="adamw", choices=["adamw", "adafactor", "came", "apollo"],
+                    help="adamw (default, the headline metric), adafactor (C2), came (C3) or apollo (C4)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU boxes; no collectives); "
@@ -165,13 +196,14 @@ def main():
     params = []
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
+    pdt = torch.bfloat16 if args.workload == "apollo" else torch.float32
     for i, s in enumerate(shapes):
         if len(s) == 1:
             p = torch.ones(s, device=dev)
         else:
             p = torch.randn(s, device=dev, generator=gen) * 0.02
-        g = make_grad(args.workload, s, gen, dev, i, embed=(i == 0))
-        p = torch.nn.Parameter(p)
+        g = make_grad(args.workload, s, gen, dev, i, embed=(i == 0)).to(pdt)
+        p = torch.nn.Parameter(p.to(pdt))
         p.grad = g
         params.append(p)
     nparams = sum(p.numel() for p in params)
@@ -252,7 +284,7 @@ def main():
 
 
 def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
-    kw = ADAFACTOR if args.workload == "adafactor" else CAME
+    kw = {"adafactor": ADAFACTOR, "came": CAME, "apollo": APOLLO}[args.workload]
     opt = Adafactor8Bit(params, **kw)
     for _ in range(args.warmup):
         opt.step()
@@ -269,15 +301,21 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
     wall = time.perf_counter() - t0
     ms = wall / args.steps * 1e3
     gms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
-    nbytes = factored_step_bytes(shapes, args.workload)
+    flops = None
+    if args.workload == "apollo":
+        nbytes, flops = apollo_step_bytes_flops(shapes)
+    else:
+        nbytes = factored_step_bytes(shapes, args.workload)
     achieved = nbytes / (gms * 1e-3) / 1e9
-    name = {"adafactor": "adafactor_factored_al8_bv256", "came": "came_uf8_al16_al16_fira_bv2048"}[args.workload]
+    name = {"adafactor": "adafactor_factored_al8_bv256", "came": "came_uf8_al16_al16_fira_bv2048",
+            "apollo": "apollo_r256_uf8_al8_sr"}[args.workload]
+    dt = "bf16" if args.workload == "apollo" else "fp32"
     out = {
         "metric": "fused step params/sec + achieved HBM GB/s (% of peak), " + args.workload + " @1.1B params",
         "value": nparams / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": name + "_tinyllama_1.1b_fp32", "params": nparams, "tensors": len(params),
+        "config": {"workload": name + "_tinyllama_1.1b_" + dt, "params": nparams, "tensors": len(params),
                    "step_bytes": nbytes},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
@@ -285,6 +323,8 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
                      "gpu_ms_per_step": gms, "bytes_per_step": nbytes},
         "cpu_baseline": None,
     }
+    if flops is not None:
+        out["projection"] = {"flops_per_step": flops, "TFLOPs_at_step_time": flops / (gms * 1e-3) / 1e12}
     print(json.dumps(out), flush=True)
 
 

@@ -254,8 +254,14 @@ typedef struct a8_apollo_tensor {
   float* fira_prev;        /* scaled_grad_norm_prev (0-dim fp32 state) when Fira is on */
   int has_fira_prev;       /* 0 on the first Fira step */
   const float* lr;         /* device learning rate, or NULL for lr_val */
-  float* workspace;        /* a8_apollo_workspace_floats(rows, cols, rank, channel) floats */
+  float* workspace;        /* a8_apollo_workspace_floats(rows, cols, rank, channel) floats, kept
+                              across steps (it caches the bf16 split of P^T) */
   uint64_t sr_seed;
+  /* per-step fields, read by a8_apollo_step_multi (a8_apollo_step takes them as arguments) */
+  int first_step;          /* V initialised as g_low^2 * beta_val (no low-rank state yet) */
+  int proj_fresh;          /* P^T changed since the last call for this workspace */
+  uint64_t step;           /* optimizer step (stochastic-rounding stream) */
+  float bias_factor;       /* see bias_mode */
 } a8_apollo_tensor;
 
 /* Replaces the APOLLO update of one parameter (_update_param_apollo,
@@ -277,6 +283,21 @@ int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int fir
                    float eps2, int scale_parameter, int bias_mode, float bias_factor, float weight_decay,
                    int wd_mode, uint64_t sr_step, void* stream);
 int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int channel);
+
+/* The APOLLO update of every matrix of a parameter group in five launches over a
+ * device descriptor table (the reference loops _update_param_apollo per
+ * parameter, optimizer.py:1886-1898; this batching has no counterpart there).
+ * Same hyper-parameters as a8_apollo_step; per-matrix step, first_step,
+ * proj_fresh and bias_factor come from the tensor records.  table_dev: device
+ * memory of a8_apollo_table_bytes(ntensors) bytes, written by this call (stream
+ * ordered).  Calls that share a table_dev must not overlap. */
+int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tensors, int ntensors,
+                         void* table_dev, int64_t table_bytes, double beta_val, double beta1, int has_m,
+                         float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits, int m_mode,
+                         int m_fp32, int m_block_size, int channel, float apollo_scale, int scale_front, int fira,
+                         float fira_margin, float d, float lr_val, float eps2, int scale_parameter, int bias_mode,
+                         float weight_decay, int wd_mode, void* stream);
+int64_t a8_apollo_table_bytes(int ntensors);
 
 #ifdef __cplusplus
 }

@@ -44,7 +44,6 @@ constexpr int kApUnit = 2048;   // low-rank elements per k_ap_low workgroup (8 p
 constexpr int kApScR = 16;      // right side: g_low rows per k_ap_scale workgroup
 constexpr int kApScL = 64;      // left side: g_low columns per k_ap_scale workgroup
 constexpr int kApApp = 2048;    // matrix elements per k_ap_apply workgroup (8 per lane)
-constexpr int kApLS = 40;       // LDS row stride (halves) of the transposed G tile
 
 // Workspace of one matrix (offsets in floats; partial arrays hold doubles).
 struct ApL {
@@ -58,7 +57,7 @@ __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
   w.n_low = (right ? R : C) * r;
   w.nchg = right ? R : C;                  // channels of G: rows (right) / columns (left)
   w.K = right ? C : R;                     // reduction length of the projection
-  w.Kp = (w.K + 31) / 32 * 32;
+  w.Kp = (w.K + 63) / 64 * 64;
   w.rp = (r + 31) / 32 * 32;
   w.ntr = (w.nchg + kApTile - 1) / kApTile;
   w.npass = (w.rp + kApPass - 1) / kApPass;
@@ -102,7 +101,7 @@ struct ApDesc {
   uint64_t sr_seed, step;
   float bias_factor;
   int32_t first, has_prev, valign;
-  int32_t tile_begin, unit_begin, sc_begin, app_begin;
+  int32_t rtile_begin, ltile_begin, unit_begin, sc_begin, app_begin, pad_;
 };
 static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
 
@@ -111,9 +110,11 @@ struct ApHyp {
   int lbv, lbm, mk, channel, front, fira, scale_param, bias_mode, wd_mode;
 };
 
-// Table: ntab descriptors, then four int32 first-workgroup arrays (projection
-// tiles, low units, scale workgroups, apply workgroups).  Without a table the
-// single descriptor comes as a kernel argument.
+// Table: ntab descriptors, then five int32 first-workgroup arrays (right-side
+// projection tiles, left-side projection tiles, low units, scale workgroups,
+// apply workgroups); a matrix without work of a kind repeats the next first
+// index, and the search takes the last match.  Without a table the single
+// descriptor comes as a kernel argument.
 __device__ __forceinline__ ApDesc ap_pick(const ApDesc& one, const ApDesc* tab, int ntab, int which, int wg,
                                           int& local) {
   if (tab == nullptr) {
@@ -187,6 +188,11 @@ __device__ __forceinline__ double sq8(u32x4 q) {
   return s;
 }
 __device__ __forceinline__ bf16x8 as_bf8(u32x4 q) { return __builtin_bit_cast(bf16x8, q); }
+// 16 bytes at a workgroup-uniform base plus a 32-bit per-lane byte offset (the
+// address form that keeps the base in SGPRs).
+__device__ __forceinline__ u32x4 ldu(const void* base, uint32_t off) {
+  return *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + off));
+}
 __device__ __forceinline__ bf16x8 ldp8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, *gp(reinterpret_cast<const u32x4*>(p)));
 }
@@ -200,26 +206,48 @@ __device__ __forceinline__ float norm_sq(double s) {
 }
 
 // ------------------------------------------------------------ P^T split
-// Rows of P (the B operand on the right side, A on the left), three bf16 terms
-// hi + mid + lo = the fp32 value exactly, zero padded to rp x Kp.
+// The projection's P operand (rows of P: output index n, reduction index k) in
+// three bf16 terms hi + mid + lo = the fp32 value exactly, stored in MFMA
+// fragment order so that one wave's fragment load is 1 KB of contiguous memory:
+// 16-byte unit u = (((t * nblk + blk) * nkc + kc) * 2 + j) * 64 + l holds
+// P[32 blk + l % 32][32 kc + 16 (l / 32) + 8 j .. +8] of term t (zero padded to
+// rp x Kp).  With lane half hi = l / 32 holding k = 16 hi + 8 j, sub-step j of
+// a 32-k chunk takes the same k permutation on both operands, which leaves the
+// sum unchanged.
+__device__ __forceinline__ int64_t psw_unit(int64_t t, int64_t blk, int64_t kc, int j, int l, int64_t nblk,
+                                            int64_t nkc) {
+  return (((t * nblk + blk) * nkc + kc) * 2 + j) * 64 + l;
+}
+
 __global__ __launch_bounds__(256) void k_ap_split(const float* __restrict__ pt, int64_t r, int64_t K, int right,
-                                                 int64_t rp, int64_t Kp, uint16_t* __restrict__ out) {
-  const int64_t n = rp * Kp;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / Kp, k = i - row * Kp;
-    float x = 0.0f;
-    if (row < r && k < K) x = right ? gp(pt)[k * r + row] : gp(pt)[row * K + k];
-    const __hip_bfloat16 h = __float2bfloat16(x);
-    const float r1 = x - __bfloat162float(h);
-    const __hip_bfloat16 m = __float2bfloat16(r1);
-    const __hip_bfloat16 l = __float2bfloat16(r1 - __bfloat162float(m));
-    uint16_t bh, bm, bl;
-    __builtin_memcpy(&bh, &h, 2);
-    __builtin_memcpy(&bm, &m, 2);
-    __builtin_memcpy(&bl, &l, 2);
-    gp(out)[i] = bh;
-    gp(out)[n + i] = bm;
-    gp(out)[2 * n + i] = bl;
+                                                 int64_t rp, int64_t Kp, u32x4* __restrict__ out) {
+  const int64_t nblk = rp / 32, nkc = Kp / 32;
+  const int64_t nu = nblk * nkc * 128;   // units per term
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < nu; u += (int64_t)gridDim.x * 256) {
+    const int l = (int)(u & 63), j = (int)((u >> 6) & 1);
+    const int64_t c = u >> 7, kc = c % nkc, blk = c / nkc;
+    const int64_t row = 32 * blk + (l & 31), k0 = 32 * kc + 16 * (l >> 5) + 8 * j;
+    uint32_t w[3][4] = {};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t k = k0 + e;
+      float x = 0.0f;
+      if (row < r && k < K) x = right ? gp(pt)[k * r + row] : gp(pt)[row * K + k];
+      const __hip_bfloat16 h = __float2bfloat16(x);
+      const float r1 = x - __bfloat162float(h);
+      const __hip_bfloat16 m = __float2bfloat16(r1);
+      const __hip_bfloat16 lo = __float2bfloat16(r1 - __bfloat162float(m));
+      uint16_t bh, bm, bl;
+      __builtin_memcpy(&bh, &h, 2);
+      __builtin_memcpy(&bm, &m, 2);
+      __builtin_memcpy(&bl, &lo, 2);
+      w[0][e >> 1] |= (uint32_t)bh << (16 * (e & 1));
+      w[1][e >> 1] |= (uint32_t)bm << (16 * (e & 1));
+      w[2][e >> 1] |= (uint32_t)bl << (16 * (e & 1));
+    }
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      gp(out)[psw_unit(t, blk, kc, j, l, nblk, nkc)] = u32x4{w[t][0], w[t][1], w[t][2], w[t][3]};
   }
 }
 
@@ -229,6 +257,11 @@ __global__ __launch_bounds__(256) void k_ap_split(const float* __restrict__ pt, 
 __device__ __forceinline__ void store_acc(const f32x16& acc, float* out, int64_t ld, int64_t row0, int64_t col,
                                           int64_t nrow, int64_t ncol, int hi) {
   if (col >= ncol) return;
+  if (row0 + 32 <= nrow) {   // the whole 32-row block exists
+#pragma unroll
+    for (int v = 0; v < 16; ++v) gp(out)[(row0 + 8 * (v >> 2) + 4 * hi + (v & 3)) * ld + col] = acc[v];
+    return;
+  }
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int64_t row = row0 + 8 * (v >> 2) + 4 * hi + (v & 3);
@@ -236,162 +269,245 @@ __device__ __forceinline__ void store_acc(const f32x16& acc, float* out, int64_t
   }
 }
 
+// Eight squares of a scrubbed bf16 fragment: exact products, an 8-term fp32 sum.
+__device__ __forceinline__ float sq8f(u32x4 q) {
+  float s = 0.0f;
+  const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __uint_as_float(wv[i] << 16), b = __uint_as_float(wv[i] & 0xFFFF0000u);
+    s = __builtin_fmaf(a, a, s);
+    s = __builtin_fmaf(b, b, s);
+  }
+  return s;
+}
+
+constexpr int kApGS = 72;   // LDS row stride (halves) of the right side's 64-row x 64-k G slab
+constexpr int kApTS = 40;   // LDS row stride (halves) of the left side's transposed 32-row slab
+
 // Right side: tile = 64 rows of G x 256 outputs (one pass); wave w owns outputs
-// [64w, 64w + 64) of the pass as two 32-column blocks.  All waves read the same
-// G rows (the A operand); wave 0 also sums their squares, wave 1 those of p.
-__device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int tile, int scale_param) {
-  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63, l32 = l & 31, hi = l >> 5;
+// [64w, 64w + 64) of the pass as two 32-column blocks (NB of them active).
+// Each 64-k slab of the tile's G rows is loaded once per workgroup with row
+// loads (eight lanes per 128-byte row segment, two rows per lane), scrubbed,
+// squared into the row norms and stored to LDS (double buffered); the MFMA A
+// fragments come from LDS, the B fragments (P) from the fragment-ordered split.
+// FULL: all 64 rows exist, K % 64 == 0 and rows are 16-byte aligned.
+template <bool FULL, int NB>
+__device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int tile, uint16_t* lds, double* sred) {
+  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
   const int pass = (int)(tile / L.ntr);
   const int64_t rt = tile - (int64_t)pass * L.ntr;
-  const int64_t R = D.R, C = D.C, r = D.r, K = C, Kp = L.Kp, rp = L.rp;
+  const int64_t R = D.R, C = D.C, r = D.r, K = C;
   const int64_t row0 = rt * kApTile;
   const int64_t cb0 = (int64_t)pass * kApPass + w * 64;
-  const bool act0 = cb0 < rp, act1 = cb0 + 32 < rp;
+  constexpr bool act1 = NB >= 2;
+  const int64_t nblk = L.rp / 32, nkc = L.Kp / 32;
+  const int64_t blk0 = cb0 / 32;
   const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
-  const uint16_t* PP = reinterpret_cast<const uint16_t*>(D.param);
-  const uint16_t* Pm = reinterpret_cast<const uint16_t*>(D.ws + L.psplit);
-  const int64_t tstride = rp * Kp;
-  const uint16_t* pb0 = Pm + (cb0 + l32) * Kp + 8 * hi;
-  const uint16_t* pb1 = pb0 + 32 * Kp;
-  const int64_t ra = row0 + l32, rb = row0 + 32 + l32;
-  const bool gnorm = pass == 0 && w == 0, pnorm = pass == 0 && w == 1 && scale_param;
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: rows lr and lr + 32, k chunk lc
+  const int64_t ga = row0 + lr, gb = row0 + lr + 32;
+  const bool pass0 = pass == 0;
   f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
-  double n0 = 0.0, n1 = 0.0, ps = 0.0;
-  for (int64_t k0 = 0; k0 < K; k0 += 16) {
-    const int64_t k = k0 + 8 * hi;
-    const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
-    const u32x4 q0 = scrub8(ldg8(G, ra * C + k, ra < R ? cnt : 0, D.valign));
-    const u32x4 q1 = scrub8(ldg8(G, rb * C + k, rb < R ? cnt : 0, D.valign));
-    if (gnorm) {
-      n0 += sq8(q0);
-      n1 += sq8(q1);
+  double na = 0.0, nb = 0.0;
+  auto ldG = [&](int64_t k0, u32x4& x, u32x4& y) {
+    if constexpr (FULL) {
+      x = ldu(G + k0, (uint32_t)((ga * C + lc) * 2));
+      y = ldu(G + k0, (uint32_t)((gb * C + lc) * 2));
+    } else {
+      const int64_t k = k0 + lc;
+      const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
+      x = ldg8(G, ga * C + k, ga < R ? cnt : 0, D.valign);
+      y = ldg8(G, gb * C + k, gb < R ? cnt : 0, D.valign);
     }
-    if (pnorm) {
-      ps += sq8(ldg8(PP, ra * C + k, ra < R ? cnt : 0, D.valign));
-      ps += sq8(ldg8(PP, rb * C + k, rb < R ? cnt : 0, D.valign));
-    }
-    if (act0 || act1) {
-      const bf16x8 x0 = as_bf8(q0), x1 = as_bf8(q1);
+  };
+  auto ldB = [&](int64_t kc, int t, u32x4* x0, u32x4* x1) {
 #pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        if (act0) {
-          const bf16x8 b = ldp8(pb0 + t * tstride + k0);
-          a00 = mfma(x0, b, a00);
-          a10 = mfma(x1, b, a10);
+    for (int j = 0; j < 2; ++j) {
+      x0[j] = gp(Ps)[psw_unit(t, blk0, kc, j, l, nblk, nkc)];
+      if constexpr (act1) x1[j] = gp(Ps)[psw_unit(t, blk0 + 1, kc, j, l, nblk, nkc)];
+    }
+  };
+  u32x4 fx, fy;   // the next slab's G, prefetched
+  ldG(0, fx, fy);
+  u32x4 b0[2], b1[2], c0[2], c1[2];
+  if constexpr (NB > 0) ldB(0, 0, b0, b1);
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += 64) {
+    const u32x4 x = scrub8(fx), y = scrub8(fy);
+    if (k0 + 64 < K) ldG(k0 + 64, fx, fy);
+    if (pass0) {
+      na += (double)sq8f(x);
+      nb += (double)sq8f(y);
+    }
+    uint16_t* sl = lds + buf * (kApTile * kApGS);
+    *reinterpret_cast<u32x4*>(&sl[lr * kApGS + lc]) = x;
+    *reinterpret_cast<u32x4*>(&sl[(lr + 32) * kApGS + lc]) = y;
+    __syncthreads();   // the slab is in LDS; the other buffer's readers finished a barrier ago
+    if constexpr (NB > 0) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int64_t kcg = k0 / 32 + kc;
+        u32x4 ar0[2], ar1[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          ar0[j] = *reinterpret_cast<const u32x4*>(&sl[l32 * kApGS + 32 * kc + 16 * hi + 8 * j]);
+          ar1[j] = *reinterpret_cast<const u32x4*>(&sl[(32 + l32) * kApGS + 32 * kc + 16 * hi + 8 * j]);
         }
-        if (act1) {
-          const bf16x8 b = ldp8(pb1 + t * tstride + k0);
-          a01 = mfma(x0, b, a01);
-          a11 = mfma(x1, b, a11);
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          // the next term's (or the next chunk's first term's) P fragments
+          const bool last = kc == 1 && t == 2;
+          if (t < 2) ldB(kcg, t + 1, c0, c1);
+          else if (!last || k0 + 64 < K) ldB(kcg + 1, 0, c0, c1);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            a00 = mfma(as_bf8(ar0[j]), as_bf8(b0[j]), a00);
+            a10 = mfma(as_bf8(ar1[j]), as_bf8(b0[j]), a10);
+            if constexpr (act1) {
+              a01 = mfma(as_bf8(ar0[j]), as_bf8(b1[j]), a01);
+              a11 = mfma(as_bf8(ar1[j]), as_bf8(b1[j]), a11);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            b0[j] = c0[j];
+            if constexpr (act1) b1[j] = c1[j];
+          }
         }
       }
     }
+    buf ^= 1;
   }
   float* glow = D.ws + L.glow;
-  if (act0) {
+  if constexpr (NB > 0) {
     store_acc(a00, glow, r, row0, cb0 + l32, R, r, hi);
     store_acc(a10, glow, r, row0 + 32, cb0 + l32, R, r, hi);
   }
-  if (act1) {
+  if constexpr (act1) {
     store_acc(a01, glow, r, row0, cb0 + 32 + l32, R, r, hi);
     store_acc(a11, glow, r, row0 + 32, cb0 + 32 + l32, R, r, hi);
   }
-  if (pass != 0) return;
-  if (w == 0) {   // lanes l and l + 32 hold the two k halves of one row
-    n0 += __shfl_xor(n0, 32, 64);
-    n1 += __shfl_xor(n1, 32, 64);
-    double t = 0.0;
-    if (hi == 0) {
-      if (ra < R) { gp(D.ws + L.ngsq)[ra] = norm_sq(n0); t += n0; }
-      if (rb < R) { gp(D.ws + L.ngsq)[rb] = norm_sq(n1); t += n1; }
-    }
-    t = grp_sum_d(t, 64);
-    if (l == 0) ws_d_set(D.ws, L.gpart, rt, t);
-  } else if (w == 1) {
-    ps = grp_sum_d(ps, 64);
-    if (l == 0) ws_d_set(D.ws, L.ppart, rt, ps);
+  if (!pass0) return;
+  // row norms: the eight lanes of a row (consecutive lanes) combine
+  na += __shfl_xor(na, 1, 64);
+  na += __shfl_xor(na, 2, 64);
+  na += __shfl_xor(na, 4, 64);
+  nb += __shfl_xor(nb, 1, 64);
+  nb += __shfl_xor(nb, 2, 64);
+  nb += __shfl_xor(nb, 4, 64);
+  double t = 0.0;
+  if ((lane & 7) == 0) {
+    if (ga < R) { gp(D.ws + L.ngsq)[ga] = norm_sq(na); t += na; }
+    if (gb < R) { gp(D.ws + L.ngsq)[gb] = norm_sq(nb); t += nb; }
   }
+  t = ap_wg_sum(t, sred);
+  if (lane == 0) ws_d_set(D.ws, L.gpart, rt, t);
 }
 
 // Left side: tile = 64 columns of G x 256 outputs (one pass).  The A operand is
-// P (rows of the low-rank output); the B operand needs 8 consecutive rows of G
-// per lane, so each 32-row slab of the tile is loaded with 16-byte row loads
-// and stored transposed to LDS.  The loading lanes also sum squares per column.
-__device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int tile, int scale_param,
-                                          uint16_t* ldsT, double* sred) {
-  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63, l32 = l & 31, hi = l >> 5;
+// P (rows of the low-rank output, from the fragment-ordered split); the B
+// operand needs consecutive rows of G per lane, so each 32-row slab of the tile
+// is loaded with row loads (eight lanes per 128-byte row segment) and stored
+// transposed to LDS (double buffered).  The loading lanes also sum squares per
+// column.  FULL: all 64 columns exist, K % 32 == 0 and rows are 16-byte aligned.
+template <bool FULL, int NB>
+__device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int tile, uint16_t* ldsT, double* sred) {
+  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
   const int pass = (int)(tile / L.ntr);
   const int64_t ct = tile - (int64_t)pass * L.ntr;
-  const int64_t R = D.R, C = D.C, r = D.r, K = R, Kp = L.Kp, rp = L.rp;
+  const int64_t C = D.C, r = D.r, K = D.R;
   const int64_t n0 = ct * kApTile;
   const int64_t mb0 = (int64_t)pass * kApPass + w * 64;
-  const bool act0 = mb0 < rp, act1 = mb0 + 32 < rp;
+  constexpr bool act1 = NB >= 2;
+  const int64_t nblk = L.rp / 32, nkc = L.Kp / 32;
+  const int64_t blk0 = mb0 / 32;
   const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
-  const uint16_t* PP = reinterpret_cast<const uint16_t*>(D.param);
-  const uint16_t* Pm = reinterpret_cast<const uint16_t*>(D.ws + L.psplit);
-  const int64_t tstride = rp * Kp;
-  const uint16_t* pa0 = Pm + (mb0 + l32) * Kp + 8 * hi;
-  const uint16_t* pa1 = pa0 + 32 * Kp;
-  const int lrow = lane >> 3, lcol = (lane & 7) * 8;
-  const int64_t gc = n0 + lcol;
-  const int ccnt = C - gc >= 8 ? 8 : (C - gc > 0 ? (int)(C - gc) : 0);
-  const bool norms = pass == 0;
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: row lr of the slab, 8 columns
+  const int64_t gc = n0 + lc;
+  const int cc = C - gc >= 8 ? 8 : (C - gc > 0 ? (int)(C - gc) : 0);
+  const bool pass0 = pass == 0;
   f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
   double cs[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) cs[j] = 0.0;
-  double ps = 0.0;
+  auto ldG = [&](int64_t row) {
+    if constexpr (FULL) return ldu(G, (uint32_t)((row * C + gc) * 2));
+    else return ldg8(G, row * C + gc, row < K ? cc : 0, D.valign);
+  };
+  auto ldA = [&](int64_t kc, int t, u32x4* x0, u32x4* x1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      x0[j] = gp(Ps)[psw_unit(t, blk0, kc, j, l, nblk, nkc)];
+      if constexpr (act1) x1[j] = gp(Ps)[psw_unit(t, blk0 + 1, kc, j, l, nblk, nkc)];
+    }
+  };
+  u32x4 f = ldG(lr);   // the next slab's row, prefetched
+  u32x4 p0[2], p1[2], q0[2], q1[2];
+  if constexpr (NB > 0) ldA(0, 0, p0, p1);
+  int buf = 0;
   for (int64_t k0 = 0; k0 < K; k0 += 32) {
-    const int64_t grow = k0 + lrow;
-    const int cnt = grow < K ? ccnt : 0;
-    const u32x4 q = scrub8(ldg8(G, grow * C + gc, cnt, D.valign));
+    const u32x4 q = scrub8(f);
+    if (k0 + 32 < K) f = ldG(k0 + 32 + lr);
     const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
-    if (norms) {
+    if (pass0) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float x = __uint_as_float((j & 1) ? (wv[j >> 1] & 0xFFFF0000u) : (wv[j >> 1] << 16));
         cs[j] += (double)(x * x);
       }
-      if (scale_param) ps += sq8(ldg8(PP, grow * C + gc, cnt, D.valign));
     }
-    __syncthreads();   // the previous slab's readers are done
+    uint16_t* sl = ldsT + buf * (kApTile * kApTS);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      ldsT[(lcol + j) * kApLS + lrow] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-    __syncthreads();
-    if (act0 || act1) {
+    for (int j = 0; j < 8; ++j) sl[(lc + j) * kApTS + lr] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+    __syncthreads();   // the slab is in LDS; the other buffer's readers finished a barrier ago
+    if constexpr (NB > 0) {
+      const int64_t kcg = k0 / 32;
+      u32x4 bc0[2], bc1[2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const bf16x8 b0 =
-            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&ldsT[l32 * kApLS + s * 16 + 8 * hi]));
-        const bf16x8 b1 =
-            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&ldsT[(32 + l32) * kApLS + s * 16 + 8 * hi]));
+      for (int j = 0; j < 2; ++j) {
+        bc0[j] = *reinterpret_cast<const u32x4*>(&sl[l32 * kApTS + 16 * hi + 8 * j]);
+        bc1[j] = *reinterpret_cast<const u32x4*>(&sl[(32 + l32) * kApTS + 16 * hi + 8 * j]);
+      }
 #pragma unroll
-        for (int t = 0; t < 3; ++t) {
-          if (act0) {
-            const bf16x8 a = ldp8(pa0 + t * tstride + k0 + s * 16);
-            a00 = mfma(a, b0, a00);
-            a01 = mfma(a, b1, a01);
+      for (int t = 0; t < 3; ++t) {
+        if (t < 2) ldA(kcg, t + 1, q0, q1);
+        else if (k0 + 32 < K) ldA(kcg + 1, 0, q0, q1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          a00 = mfma(as_bf8(p0[j]), as_bf8(bc0[j]), a00);
+          a01 = mfma(as_bf8(p0[j]), as_bf8(bc1[j]), a01);
+          if constexpr (act1) {
+            a10 = mfma(as_bf8(p1[j]), as_bf8(bc0[j]), a10);
+            a11 = mfma(as_bf8(p1[j]), as_bf8(bc1[j]), a11);
           }
-          if (act1) {
-            const bf16x8 a = ldp8(pa1 + t * tstride + k0 + s * 16);
-            a10 = mfma(a, b0, a10);
-            a11 = mfma(a, b1, a11);
-          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          p0[j] = q0[j];
+          if constexpr (act1) p1[j] = q1[j];
         }
       }
     }
+    buf ^= 1;
   }
   float* glow = D.ws + L.glow;
-  if (act0) {
+  if constexpr (NB > 0) {
     store_acc(a00, glow, C, mb0, n0 + l32, r, C, hi);
     store_acc(a01, glow, C, mb0, n0 + 32 + l32, r, C, hi);
   }
-  if (act1) {
+  if constexpr (act1) {
     store_acc(a10, glow, C, mb0 + 32, n0 + l32, r, C, hi);
     store_acc(a11, glow, C, mb0 + 32, n0 + 32 + l32, r, C, hi);
   }
-  if (!norms) return;
+  if (!pass0) return;
   // column sums: lanes with equal (lane & 7) share columns; xor over 8, 16, 32
   // within the wave, then the four waves through LDS
 #pragma unroll
@@ -416,21 +532,84 @@ __device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int til
     }
     t = grp_sum_d(t, 64);
   }
-  const double tp = scale_param ? ap_wg_sum(ps, sred + 256) : 0.0;
-  if (lane == 0) {
-    ws_d_set(D.ws, L.gpart, ct, t);
-    ws_d_set(D.ws, L.ppart, ct, tp);
+  if (lane == 0) ws_d_set(D.ws, L.gpart, ct, t);
+}
+
+// Workgroups are dealt to the 8 XCDs round-robin by index, each XCD with its own
+// L2.  Consecutive projection tiles of a matrix share its P split (3 x 2 r K
+// bytes, ~3 MB at r = 256, K = 2048), so tile order is remapped to give each XCD
+// one contiguous range of tiles: its resident workgroups then work on one or two
+// matrices at a time and re-read P from their L2.
+__device__ __forceinline__ int xcd_order(int b, int nwg) {
+  constexpr int kXcd = 8;
+  const int x = b % kXcd, slot = b / kXcd;
+  const int q = nwg / kXcd, rem = nwg % kXcd;
+  return x < rem ? x * (q + 1) + slot : rem * (q + 1) + (x - rem) * q + slot;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_ap_proj_r(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kApTile * kApGS];
+  __shared__ double sred[8];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 0, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t row0 = (local % L.ntr) * kApTile;
+  const bool full = D.valign && row0 + kApTile <= D.R && D.C % 64 == 0;
+  const int64_t cb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
+  const int nb = cb0 + 32 < L.rp ? 2 : (cb0 < L.rp ? 1 : 0);   // uniform per wave
+  // every wave runs the slab loop (it holds the workgroup barriers)
+  if (full) {
+    if (nb == 2) proj_right<true, 2>(D, L, local, lds, sred);
+    else if (nb == 1) proj_right<true, 1>(D, L, local, lds, sred);
+    else proj_right<true, 0>(D, L, local, lds, sred);
+  } else {
+    if (nb == 2) proj_right<false, 2>(D, L, local, lds, sred);
+    else if (nb == 1) proj_right<false, 1>(D, L, local, lds, sred);
+    else proj_right<false, 0>(D, L, local, lds, sred);
   }
 }
 
-__global__ __launch_bounds__(256) void k_ap_proj(ApDesc one, const ApDesc* tab, int ntab, int scale_param) {
-  __shared__ __attribute__((aligned(16))) uint16_t ldsT[kApTile * kApLS];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t ldsT[2 * kApTile * kApTS];
   __shared__ double sred[4 * 64 + 4];
   int local;
-  const ApDesc D = ap_pick(one, tab, ntab, 0, (int)blockIdx.x, local);
+  const ApDesc D = ap_pick(one, tab, ntab, 1, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
   const ApL L = ap_layout(D.R, D.C, D.r);
-  if (D.R >= D.C) proj_right(D, L, local, scale_param);
-  else proj_left(D, L, local, scale_param, ldsT, sred);
+  const int64_t n0 = (local % L.ntr) * kApTile;
+  const bool full = D.valign && n0 + kApTile <= D.C && D.R % 32 == 0;
+  const int64_t mb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
+  const int nb = mb0 + 32 < L.rp ? 2 : (mb0 < L.rp ? 1 : 0);   // uniform per wave
+  if (full) {
+    if (nb == 2) proj_left<true, 2>(D, L, local, ldsT, sred);
+    else if (nb == 1) proj_left<true, 1>(D, L, local, ldsT, sred);
+    else proj_left<true, 0>(D, L, local, ldsT, sred);
+  } else {
+    if (nb == 2) proj_left<false, 2>(D, L, local, ldsT, sred);
+    else if (nb == 1) proj_left<false, 1>(D, L, local, ldsT, sred);
+    else proj_left<false, 0>(D, L, local, ldsT, sred);
+  }
+}
+
+// ------------------------------------------------------------ ||p||^2 (scale_parameter)
+// ntr workgroups per matrix, each summing a contiguous share of p^2 in double;
+// only the total (k_ap_scalars) is used.
+template <typename T>
+__global__ __launch_bounds__(256) void k_ap_psq(ApDesc D) {
+  __shared__ double sd[4];
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t n = D.R * D.C;
+  const int64_t chunk = (n + L.ntr - 1) / L.ntr;
+  const int64_t b = (int64_t)blockIdx.x * chunk, e = b + chunk < n ? b + chunk : n;
+  const T* P = reinterpret_cast<const T*>(D.param);
+  double s = 0.0;
+  for (int64_t i = b + threadIdx.x; i < e; i += 256) {
+    const float p = ld1<T>(P, i);
+    s += (double)(p * p);
+  }
+  s = ap_wg_sum(s, sd);
+  if (threadIdx.x == 0) ws_d_set(D.ws, L.ppart, blockIdx.x, s);
 }
 
 // ------------------------------------------------------------ fp32 G: norms and flags
@@ -535,7 +714,7 @@ template <int VB, int MK>
 __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   __shared__ float xw[16];
   int unit;
-  const ApDesc D = ap_pick(one, tab, ntab, 1, (int)blockIdx.x, unit);
+  const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, unit);
   const ApL L = ap_layout(D.R, D.C, D.r);
   const int64_t n = L.n_low;
   float* ws = D.ws;
@@ -713,7 +892,7 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
 __global__ __launch_bounds__(256) void k_ap_scale(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   __shared__ double sd[2 * 256 + 4];
   int wg;
-  const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, wg);
+  const ApDesc D = ap_pick(one, tab, ntab, 3, (int)blockIdx.x, wg);
   const ApL L = ap_layout(D.R, D.C, D.r);
   const int64_t R = D.R, C = D.C, r = D.r;
   const float* U = D.ws + L.u;
@@ -871,62 +1050,88 @@ __global__ __launch_bounds__(256) void k_ap_scalars(ApDesc one, const ApDesc* ta
 // channel p + (step * G) * f_ch (addcmul) or tensor fma(step * f, G, p) (add_),
 // rounded to T; f_ch = (s_ch * fira) * sqrt(apollo_scale) at the back.  SR
 // (optimizer.py:3058-3063 with the stream of kernels.cu:48-87):
-// x = (p * decay) + (G * f) * step in fp32, stochastically rounded.
+// x = (p * decay) + (G * f) * step in fp32, stochastically rounded.  Eight
+// consecutive elements per lane (16-byte loads and stores for 16-bit types);
+// with C % 8 == 0 they share one row, so one channel scale (right side) or
+// eight consecutive ones (left side).
+template <typename T>
+__device__ __forceinline__ float ap_fch(const float* fin, int64_t ch, float fs, const ApHyp& h) {
+  float f = gp(fin)[ch];
+  if (h.fira) f = f * fs;
+  if (!h.front) f = f * h.sv;
+  return f;
+}
+
 template <typename T, bool SR>
 __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   int unit;
-  const ApDesc D = ap_pick(one, tab, ntab, 3, (int)blockIdx.x, unit);
+  const ApDesc D = ap_pick(one, tab, ntab, 4, (int)blockIdx.x, unit);
   const ApL L = ap_layout(D.R, D.C, D.r);
-  const int64_t R = D.R, C = D.C, n = R * C;
+  const uint32_t R = (uint32_t)D.R, C = (uint32_t)D.C, n = R * C;   // n < 2^31
   const bool right = R >= C;
   const float* ws = D.ws;
+  const float* fin = ws + L.fin;
   const float* sl = ws + L.scal;
   const float step = gp(sl)[0], dec = gp(sl)[1], fin_t = gp(sl)[3], fs = gp(sl)[6];
   const bool has_dec = h.wd_mode != 0;
   T* P = reinterpret_cast<T*>(D.param);
   const T* G = reinterpret_cast<const T*>(D.grad);
-  const int64_t e0 = (int64_t)unit * kApApp + (int64_t)threadIdx.x * 8;
+  const uint32_t e0 = (uint32_t)unit * kApApp + threadIdx.x * 8u;
   if (e0 >= n) return;
-  float g[8], p[8];
+  float g[8], p[8], f[8];
   load8<T>(G, e0, n, g);
-  if constexpr (!SR) load8<T>(P, e0, n, p);
-  int64_t row = e0 / C;
-  int64_t col = e0 - row * C;
-  const float ts = step * fin_t;   // tensor: alpha = step * final_scale
-  float f = fin_t;
-  int64_t fch = -1;
+  load8<T>(P, e0, n, p);
+  const uint32_t row = e0 / C, col = e0 - row * C;
+  if (!h.channel) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (e0 + k < n) {
-      const float gk = scrub(g[k]);
-      if (h.channel) {
-        const int64_t ch = right ? row : col;
-        if (ch != fch) {
-          f = gp(ws + L.fin)[ch];
-          if (h.fira) f = f * fs;
-          if (!h.front) f = f * h.sv;
-          fch = ch;
-        }
-      }
-      if constexpr (SR) {
-        float x = ld1<T>(P, e0 + k);
-        if (has_dec) x = x * dec;
-        x = x + (gk * f) * step;
-        const T rr = sr_round<T>(x, D.sr_seed, D.step, (uint64_t)(e0 + k));
-        uint16_t bits;
-        __builtin_memcpy(&bits, &rr, 2);
-        gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = bits;
-      } else {
-        float x = p[k];
-        if (has_dec) x = to_f<T>(from_f<T>(x * dec));
-        if (h.channel) x = x + (step * gk) * f;
-        else x = __builtin_fmaf(ts, gk, x);
-        p[k] = x;
-      }
+    for (int k = 0; k < 8; ++k) f[k] = fin_t;
+  } else if (D.valign && e0 + 8 <= n) {   // all eight in one row
+    if (right) {
+      const float fr = ap_fch<T>(fin, row, fs, h);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] = fr;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] = ap_fch<T>(fin, col + k, fs, h);
     }
-    if (++col == C) { col = 0; ++row; }
+  } else {
+    uint32_t rr = row, cc = col;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      f[k] = (e0 + k < n) ? ap_fch<T>(fin, right ? rr : cc, fs, h) : 0.0f;
+      if (++cc == C) { cc = 0; ++rr; }
+    }
   }
-  if constexpr (!SR) store8<T>(P, e0, n, p);
+  const float ts = step * fin_t;   // tensor: alpha = step * final_scale
+  if constexpr (SR) {
+    const uint64_t base = sr_base(D.sr_seed, D.step);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float x = p[k];
+      if (has_dec) x = x * dec;
+      x = x + (scrub(g[k]) * f[k]) * step;
+      w[k >> 1] |= (uint32_t)sr_bf16_bits(x, sr_bits_at(base, (uint64_t)(e0 + k))) << (16 * (k & 1));
+    }
+    if (e0 + 8 <= n) {
+      *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P) + e0)) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (e0 + k < n) gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float gk = scrub(g[k]);
+      float x = p[k];
+      if (has_dec) x = to_f<T>(from_f<T>(x * dec));
+      if (h.channel) x = x + (step * gk) * f[k];
+      else x = __builtin_fmaf(ts, gk, x);
+      p[k] = x;
+    }
+    store8<T>(P, e0, n, p);
+  }
 }
 
 hipError_t apollo_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
@@ -976,7 +1181,7 @@ static void launch_low(int mkt, unsigned nb, const ApDesc& one, const ApDesc* ta
   }
 }
 
-static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 4 * sizeof(int32_t)); }
+static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 5 * sizeof(int32_t)); }
 
 static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int n, void* table_dev,
                       int64_t tbytes, double beta_val, double beta1, int has_m, float apollo_eps, float log_floor,
@@ -997,8 +1202,8 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_apollo_table_bytes(n)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<ApDesc> tab((size_t)n);
-  std::vector<int32_t> first((size_t)4 * n);
-  int64_t ntile = 0, nunit = 0, nsc = 0, napp = 0;
+  std::vector<int32_t> first((size_t)5 * n);
+  int64_t nrt = 0, nlt = 0, nunit = 0, nsc = 0, napp = 0;
   for (int i = 0; i < n; ++i) {
     const a8_apollo_tensor& t = ts[i];
     if (!t.param || !t.grad || !t.proj_t || !t.workspace) return set_error(A8_ERR_ARG, "null pointer");
@@ -1020,14 +1225,16 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
     D.sr_seed = t.sr_seed; D.step = t.step; D.bias_factor = t.bias_factor;
     D.first = t.first_step ? 1 : 0; D.has_prev = t.has_fira_prev ? 1 : 0;
     D.valign = (t.cols % (dtype == A8_F32 ? 4 : 8)) == 0 ? 1 : 0;
-    D.tile_begin = (int32_t)ntile; D.unit_begin = (int32_t)nunit; D.sc_begin = (int32_t)nsc;
-    D.app_begin = (int32_t)napp;
-    first[(size_t)i] = D.tile_begin;
-    first[(size_t)n + i] = D.unit_begin;
-    first[(size_t)2 * n + i] = D.sc_begin;
-    first[(size_t)3 * n + i] = D.app_begin;
-    ntile += L.ntile; nunit += L.nunit; nsc += L.nsc; napp += L.napp;
-    if (ntile > 0x7FFFFFFF || nunit > 0x7FFFFFFF || nsc > 0x7FFFFFFF || napp > 0x7FFFFFFF)
+    D.rtile_begin = (int32_t)nrt; D.ltile_begin = (int32_t)nlt; D.unit_begin = (int32_t)nunit;
+    D.sc_begin = (int32_t)nsc; D.app_begin = (int32_t)napp; D.pad_ = 0;
+    first[(size_t)i] = D.rtile_begin;
+    first[(size_t)n + i] = D.ltile_begin;
+    first[(size_t)2 * n + i] = D.unit_begin;
+    first[(size_t)3 * n + i] = D.sc_begin;
+    first[(size_t)4 * n + i] = D.app_begin;
+    if (t.rows >= t.cols) nrt += L.ntile; else nlt += L.ntile;
+    nunit += L.nunit; nsc += L.nsc; napp += L.napp;
+    if (nrt > 0x7FFFFFFF || nlt > 0x7FFFFFFF || nunit > 0x7FFFFFFF || nsc > 0x7FFFFFFF || napp > 0x7FFFFFFF)
       return set_error(A8_ERR_SIZE, "too many workgroups");
   }
   hipStream_t st = (hipStream_t)stream;
@@ -1035,7 +1242,7 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
   if (n > 1) {
     std::vector<char> blob((size_t)table_bytes(n));
     std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
-    std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 4 * (size_t)n);
+    std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 5 * (size_t)n);
     if (hipMemcpyAsync(table_dev, blob.data(), blob.size(), hipMemcpyHostToDevice, st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
     dtab = reinterpret_cast<const ApDesc*>(table_dev);
@@ -1059,13 +1266,26 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
       if (!ts[i].proj_fresh) continue;
       const ApDesc& D = tab[(size_t)i];
       const ApL L = ap_layout(D.R, D.C, D.r);
-      const int64_t nb = (L.rp * L.Kp + 255) / 256;
+      const int64_t nb = (L.rp * L.Kp / 8 + 255) / 256;
       hipLaunchKernelGGL(k_ap_split, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, D.proj_t, D.r, L.K,
-                         (int)(D.R >= D.C), L.rp, L.Kp, reinterpret_cast<uint16_t*>(D.ws + L.psplit));
+                         (int)(D.R >= D.C), L.rp, L.Kp, reinterpret_cast<u32x4*>(D.ws + L.psplit));
       if ((rc = check_launch("k_ap_split"))) return rc;
     }
-    hipLaunchKernelGGL(k_ap_proj, dim3((unsigned)ntile), dim3(256), 0, st, one, dtab, n, h.scale_param);
-    if ((rc = check_launch("k_ap_proj"))) return rc;
+    if (nrt > 0) {
+      hipLaunchKernelGGL(k_ap_proj_r, dim3((unsigned)nrt), dim3(256), 0, st, one, dtab, n);
+      if ((rc = check_launch("k_ap_proj_r"))) return rc;
+    }
+    if (nlt > 0) {
+      hipLaunchKernelGGL(k_ap_proj_l, dim3((unsigned)nlt), dim3(256), 0, st, one, dtab, n);
+      if ((rc = check_launch("k_ap_proj_l"))) return rc;
+    }
+    if (h.scale_param) {
+      for (int i = 0; i < n; ++i) {
+        const ApDesc& D = tab[(size_t)i];
+        hipLaunchKernelGGL(k_ap_psq<__hip_bfloat16>, dim3((unsigned)ap_layout(D.R, D.C, D.r).ntr), dim3(256), 0, st, D);
+        if ((rc = check_launch("k_ap_psq"))) return rc;
+      }
+    }
   } else {
     rocblas_handle hb;
     if ((rc = blas_handle(&hb))) return rc;

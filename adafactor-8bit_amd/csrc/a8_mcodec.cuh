@@ -30,6 +30,35 @@ __device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64
   return (uint32_t)(z >> 32);
 }
 
+// The same stream from a precomputed counter base (seed * gamma + step * K): the
+// element's 32 random bits.
+__device__ __forceinline__ uint32_t sr_bits_at(uint64_t base, uint64_t idx) {
+  uint64_t z = base + idx + 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  z ^= z >> 31;
+  return (uint32_t)(z >> 32);
+}
+__device__ __forceinline__ uint64_t sr_base(uint64_t seed, uint64_t step) {
+  return seed * 0x9E3779B97F4A7C15ULL + step * 0xD1B54A32D192ED03ULL;
+}
+
+// bf16 stochastic rounding decided in integers: u < rem / 2^16 with
+// u = (bits >> 8) / 2^24 is (bits >> 8) < rem * 2^8 exactly (both sides are
+// exact in fp32), so the result equals sr_bf16(x, u).
+__device__ __forceinline__ uint16_t sr_bf16_bits(float x, uint32_t bits) {
+  const uint32_t b = __float_as_uint(x);
+  const bool nan = ((b & 0x7F800000u) == 0x7F800000u) && (b & 0x007FFFFFu);
+  const uint32_t lo = b & 0xFFFF0000u;
+  const uint32_t rem = b & 0x0000FFFFu;
+  const uint32_t hi = lo + 0x00010000u;
+  const bool lo_inf = (lo & 0x7F800000u) == 0x7F800000u;
+  const bool hi_inf = ((hi & 0x7F800000u) == 0x7F800000u) && !(hi & 0x007FFFFFu);
+  const bool up = rem && !lo_inf && !hi_inf && ((bits >> 8) < (rem << 8));
+  const uint32_t r = nan ? ((b & 0x80000000u) | 0x7FC00000u) : (up ? hi : lo);
+  return (uint16_t)(r >> 16);
+}
+
 __device__ __forceinline__ float sr_uniform(uint64_t seed, uint64_t step, uint64_t idx) {
   return (float)(sr_bits(seed, step, idx) >> 8) * (1.0f / 16777216.0f);
 }

@@ -196,14 +196,17 @@ def fused_update_1d_vonly_lag_sr(param, grad, v_q, v_scale, v_min_log, norm_buf,
          block_size, block_size, 0, 0, d, v_bits, False)
 
 
-# ---- fused_update_1d_full_* (kernels.cu:1374-1515): fp32 state
+# ---- fused_update_1d_full_*[_sr] (kernels.cu:1374-1515): fp32 state
 def _full(mode, param, grad, variance, m, norm_buf, alpha, prev_norm, beta1, beta_val, eps_sq,
-          eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, d, momentum_only):
+          eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, d, momentum_only, decay=None, sr_seed=None,
+          sr_step=0):
+    sr = sr_seed is not None and param is not None and param.dtype in (torch.bfloat16, torch.float16)
     rc = nat.lib().a8_fused_update_1d_full(
         mode, nat.dtype_code(grad.dtype), nat.ptr(param), nat.ptr(grad), nat.ptr(variance), nat.ptr(m),
-        nat.ptr(norm_buf), nat.ptr(alpha), nat.ptr(prev_norm), None, float(beta1), float(beta_val),
+        nat.ptr(norm_buf), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(decay), float(beta1), float(beta_val),
         float(eps_sq), float(eps_for_denom), int(bool(use_adam_denom)), float(eps_for_grad_sq),
-        int(numel), float(d), int(bool(momentum_only)), 0.0, 1.0, 0, _stream(grad))
+        int(numel), float(d), int(bool(momentum_only)), 0.0, 1.0, 0, int(sr), int(sr_seed or 0), int(sr_step),
+        _stream(grad))
     nat.check(rc, "fused_update_1d_full")
 
 
@@ -230,6 +233,26 @@ def fused_update_1d_full_lag(param, grad, variance, m, norm_buf, alpha, prev_nor
                              momentum_only):
     _full(3, param, grad, variance, m, norm_buf, alpha, prev_norm, beta1, beta_val, eps_sq, eps_for_denom,
           use_adam_denom, eps_for_grad_sq, numel, d, momentum_only)
+
+
+def fused_update_1d_full_noclip_sr(param, grad, variance, m, alpha, decay, sr_seed, sr_step, beta1, beta_val,
+                                   eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, momentum_only):
+    _full(0, param, grad, variance, m, None, alpha, None, beta1, beta_val, eps_sq, eps_for_denom,
+          use_adam_denom, eps_for_grad_sq, numel, 0.0, momentum_only, decay, sr_seed, sr_step)
+
+
+def fused_update_1d_full_apply_sr(param, grad, variance, m, norm_buf, alpha, decay, sr_seed, sr_step, beta1,
+                                  beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, d,
+                                  momentum_only):
+    _full(2, param, grad, variance, m, norm_buf, alpha, None, beta1, beta_val, eps_sq, eps_for_denom,
+          use_adam_denom, eps_for_grad_sq, numel, d, momentum_only, decay, sr_seed, sr_step)
+
+
+def fused_update_1d_full_lag_sr(param, grad, variance, m, norm_buf, alpha, prev_norm, decay, sr_seed, sr_step,
+                                beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, numel,
+                                d, momentum_only):
+    _full(3, param, grad, variance, m, norm_buf, alpha, prev_norm, beta1, beta_val, eps_sq, eps_for_denom,
+          use_adam_denom, eps_for_grad_sq, numel, d, momentum_only, decay, sr_seed, sr_step)
 
 
 # ---- fira_scalar (kernels.cu:3055-3084)

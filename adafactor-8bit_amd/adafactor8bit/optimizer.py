@@ -339,11 +339,11 @@ class _Plan:
             return None
         if self.alpha_t is not None or self.decay_t is not None:
             return None
-        if self.d > 0 or self.fira or self.sr or self.maximize:
+        if self.d > 0 or self.fira or self.maximize:
             return None
         if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
-        return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.vqt,
+        return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
                 self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                 self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                 self.alpha_val, self.decay_val)
@@ -580,7 +580,7 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
             nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
             P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
             p.numel(), P.d, int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
-            nat.stream_of(p.device))
+            int(P.sr), int(st.get("sr_seed", 0)), int(P.step), nat.stream_of(p.device))
         nat.check(rc, "a8_fused_update_1d_full")
 
 
@@ -695,7 +695,7 @@ def _run_batch(opt, key, plans):
                 st = pl.st
                 arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), st["variance"].data_ptr(),
                                         nat.ptr(st.get("m") if pl.has_m else None), None, None, None,
-                                        None, pl.p.numel())
+                                        None, pl.p.numel(), int(st.get("sr_seed", 0)))
             nbytes = L.a8_table_bytes_full(n)
         table = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         # state tensors referenced by the table must stay the same objects
@@ -716,7 +716,7 @@ def _run_batch(opt, key, plans):
     strm = nat.stream_of(dev)
     if path == "q1d":
         rc = L.a8_fused_update_1d_multi(
-            nat.MODE_NOCLIP, 0, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
+            nat.MODE_NOCLIP, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,
             P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
             S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
@@ -730,8 +730,8 @@ def _run_batch(opt, key, plans):
         rc = L.a8_fused_update_1d_full_multi(
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom),
-            P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, upload,
-            strm)
+            P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr),
+            int(P0.step), upload, strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
 

@@ -709,13 +709,13 @@ __global__ __launch_bounds__(256) void k_ap_fixlow(ApDesc D) {
 // block is B/8 consecutive lanes.  Arithmetic as optimizer.py:2765-2790, 2911-2951
 // (quantised states through _quant_v / _m_ema_pytorch, fp32 states through
 // lerp_): v = first ? g^2 * bv : lerp(v, g^2, bv); m = lerp(m, g, 1 - beta1);
-// u = m / (sqrt(v) + eps) with IEEE sqrt and division.
-template <int VB, int MK>
-__global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
-  __shared__ float xw[16];
-  int unit;
-  const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, unit);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+// u = m / (sqrt(v) + eps) with IEEE sqrt and division.  FULL: the unit lies
+// inside g_low and u is 16-byte aligned, so every access is a vector access.
+// AL8 blocks of >= 512 elements decode through an LDS table of the block's
+// 255 code values (one correctly rounded exp2 per lane per block).
+template <int VB, int MK, bool FULL>
+__device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int unit, const ApHyp& h, float* xw,
+                                            float* dtab) {
   const int64_t n = L.n_low;
   float* ws = D.ws;
   const int lane = threadIdx.x, wave = lane >> 6;
@@ -735,9 +735,15 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
   float g[8], v[8], m[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) { g[k] = 0.0f; v[k] = 0.0f; m[k] = 0.0f; }
+  if constexpr (FULL) {
+    const f32x4 a = *gp(reinterpret_cast<const f32x4*>(ws + L.glow + e0));
+    const f32x4 b = *gp(reinterpret_cast<const f32x4*>(ws + L.glow + e0 + 4));
+    g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w; g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+  } else {
 #pragma unroll
-  for (int k = 0; k < 8; ++k)
-    if (k < cnt) g[k] = gp(ws)[L.glow + e0 + k];
+    for (int k = 0; k < 8; ++k)
+      if (k < cnt) g[k] = gp(ws)[L.glow + e0 + k];
+  }
   // ---- V
   float vo[8];
 #pragma unroll
@@ -747,6 +753,29 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         if (k < cnt) vo[k] = gp(D.v_fp32)[e0 + k];
+    } else if (VB == 8 && VL >= 64) {
+      // one block per VL lanes (VL / 64 waves); its 255 decoded values into LDS
+      const int bw = lane / VL;   // block of this unit
+      const int64_t vbb = (int64_t)unit * (kApUnit >> lbv) + bw;
+      const bool bok = vbb < nvb;   // a tail unit may end before its last block slot
+      const float s_old = bok ? gp(D.v_scale)[vbb] : 0.0f, lm_old = bok ? gp(D.v_min_log)[vbb] : 0.0f;
+      for (int c = lane % VL; c < 256; c += VL)
+        dtab[bw * 256 + c] = c ? exp2_exact(((float)(c - 1) * s_old) / 254.0f + lm_old) : 0.0f;
+      __syncthreads();
+      uint32_t cw[2];
+      if constexpr (FULL) {
+        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
+        cw[0] = q.x; cw[1] = q.y;
+      } else {
+        cw[0] = cw[1] = 0u;
+        if (v_ok) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            cw[k >> 2] |= (uint32_t)gp(reinterpret_cast<const uint8_t*>(D.v_q))[e0 + k] << (8 * (k & 3));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) vo[k] = dtab[bw * 256 + ((cw[k >> 2] >> (8 * (k & 3))) & 0xFFu)];
     } else if (v_ok) {
       const float s_old = gp(D.v_scale)[vb], lm_old = gp(D.v_min_log)[vb];
 #pragma unroll
@@ -793,11 +822,19 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
     for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
   }
   // ---- u
+  if constexpr (FULL) {
+    float uu[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if (k < cnt) {
-      const float x = MK != 0 ? m[k] : g[k];
-      gp(ws)[L.u + e0 + k] = x / (sqrtf(v[k]) + h.aeps);
+    for (int k = 0; k < 8; ++k) uu[k] = (MK != 0 ? m[k] : g[k]) / (sqrtf(v[k]) + h.aeps);
+    *gp(reinterpret_cast<f32x4*>(ws + L.u + e0)) = f32x4{uu[0], uu[1], uu[2], uu[3]};
+    *gp(reinterpret_cast<f32x4*>(ws + L.u + e0 + 4)) = f32x4{uu[4], uu[5], uu[6], uu[7]};
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < cnt) {
+        const float x = MK != 0 ? m[k] : g[k];
+        gp(ws)[L.u + e0 + k] = x / (sqrtf(v[k]) + h.aeps);
+      }
     }
   }
   // ---- V state
@@ -830,11 +867,18 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
     constexpr int LM2 = VB == 8 ? 254 : 65534;
     const ALFit f = al_refit(bmax, mnz, floor_, (float)LM2);
     if (v_ok) {
+      if constexpr (FULL && VB == 8) {
+        uint32_t cw[2] = {0u, 0u};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t code = al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f));
-        if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(D.v_q))[e0 + k] = (uint8_t)code;
-        else gp(reinterpret_cast<uint16_t*>(D.v_q))[e0 + k] = (uint16_t)code;
+        for (int k = 0; k < 8; ++k) cw[k >> 2] |= al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f)) << (8 * (k & 3));
+        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) = u32x2{cw[0], cw[1]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t code = al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f));
+          if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(D.v_q))[e0 + k] = (uint8_t)code;
+          else gp(reinterpret_cast<uint16_t*>(D.v_q))[e0 + k] = (uint16_t)code;
+        }
       }
       if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }
     }
@@ -880,6 +924,17 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
       if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
     }
   }
+}
+
+template <int VB, int MK>
+__global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
+  __shared__ float xw[16];
+  __shared__ float dtab[4 * 256];
+  int unit;
+  const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, unit);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  if ((int64_t)(unit + 1) * kApUnit <= L.n_low && (L.u & 3) == 0) ap_low_unit<VB, MK, true>(D, L, unit, h, xw, dtab);
+  else ap_low_unit<VB, MK, false>(D, L, unit, h, xw, dtab);
 }
 
 // ------------------------------------------------------------ scale

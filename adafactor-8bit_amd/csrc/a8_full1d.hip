@@ -9,6 +9,7 @@
 // quantised kernel.  Fira (kernels.cu:3030-3053, optimizer.py:760-782) is a
 // one-lane-per-tensor scalar kernel.
 #include "a8_common.cuh"
+#include "a8_mcodec.cuh"
 #include "a8_abi_impl.h"
 
 namespace a8 {
@@ -59,7 +60,10 @@ __device__ __forceinline__ const DescFull* find_full(const DescFull* tab, int n,
 // MODE: 0 single pass, 1 NORM (writes V, sums u^2 or U^2), 2 APPLY (reads V,
 // writes M and p), 3 LAG, 4 MNORM (momentum-only: reads V, clips U by the NORM
 // pass's sum of U^2 in prev_norm and sums M'^2 for Fira; writes nothing).
-template <typename T, int MODE>
+// SR: the parameter write is p * decay - step * u in fp32, stochastically
+// rounded to T with the stream of kernels.cu:48-87 (write_param_update,
+// kernels.cu:149-161), element index within the tensor.
+template <typename T, int MODE, bool SR>
 __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const DescFull* __restrict__ table,
                                                          int ntab, HyperFull h) {
   const DescFull D = table ? *find_full(table, ntab, (int64_t)blockIdx.x) : one;
@@ -136,9 +140,14 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       }
       if (MODE != 1 && MODE != 4) {
         float p = to_f<T>(P[i]);
-        if (D.decay) p = p * *D.decay;
-        else if (h.has_decay) p = p * h.decay_val;
-        P[i] = from_f<T>(__builtin_fmaf(-step, u, p));
+        if constexpr (SR) {
+          const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
+          P[i] = sr_round<T>(p * dec - step * u, D.sr_seed, h.sr_step, (uint64_t)i);
+        } else {
+          if (D.decay) p = p * *D.decay;
+          else if (h.has_decay) p = p * h.decay_val;
+          P[i] = from_f<T>(__builtin_fmaf(-step, u, p));
+        }
       }
     }
   }
@@ -148,26 +157,30 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
   }
 }
 
-template <typename T>
+template <typename T, bool SR>
 static int launch_full(int mode, const DescFull& one, const DescFull* tab, int ntab, int64_t nwg,
                        const HyperFull& h, hipStream_t st) {
   if (nwg <= 0) return 0;
   switch (mode) {
-    case 0: hipLaunchKernelGGL((k_update1d_full<T, 0>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
-    case 1: hipLaunchKernelGGL((k_update1d_full<T, 1>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
-    case 2: hipLaunchKernelGGL((k_update1d_full<T, 2>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
-    case 4: hipLaunchKernelGGL((k_update1d_full<T, 4>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
-    default: hipLaunchKernelGGL((k_update1d_full<T, 3>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 0: hipLaunchKernelGGL((k_update1d_full<T, 0, SR>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 1: hipLaunchKernelGGL((k_update1d_full<T, 1, SR>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 2: hipLaunchKernelGGL((k_update1d_full<T, 2, SR>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    case 4: hipLaunchKernelGGL((k_update1d_full<T, 4, SR>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
+    default: hipLaunchKernelGGL((k_update1d_full<T, 3, SR>), dim3((unsigned)nwg), dim3(kFLanes), 0, st, one, tab, ntab, h); break;
   }
   return check_launch("k_update1d_full");
 }
 
-static int launch_full_any(int dtype, int mode, const DescFull& one, const DescFull* tab, int ntab,
-                           int64_t nwg, const HyperFull& h, hipStream_t st) {
+static int launch_full_any(int dtype, int stochastic, int mode, const DescFull& one, const DescFull* tab,
+                           int ntab, int64_t nwg, const HyperFull& h, hipStream_t st) {
   switch (dtype) {
-    case A8_F32: return launch_full<float>(mode, one, tab, ntab, nwg, h, st);
-    case A8_BF16: return launch_full<__hip_bfloat16>(mode, one, tab, ntab, nwg, h, st);
-    case A8_F16: return launch_full<__half>(mode, one, tab, ntab, nwg, h, st);
+    case A8_F32: return launch_full<float, false>(mode, one, tab, ntab, nwg, h, st);
+    case A8_BF16:
+      return stochastic ? launch_full<__hip_bfloat16, true>(mode, one, tab, ntab, nwg, h, st)
+                        : launch_full<__hip_bfloat16, false>(mode, one, tab, ntab, nwg, h, st);
+    case A8_F16:
+      return stochastic ? launch_full<__half, true>(mode, one, tab, ntab, nwg, h, st)
+                        : launch_full<__half, false>(mode, one, tab, ntab, nwg, h, st);
     default: return set_error(A8_ERR_DTYPE, "unsupported param dtype");
   }
 }
@@ -222,7 +235,8 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
                             const float* decay, double beta1, double beta_val, float eps_sq,
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
-                            float decay_val, int has_decay, void* stream) {
+                            float decay_val, int has_decay, int stochastic, uint64_t sr_seed,
+                            uint64_t sr_step, void* stream) {
   if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
   if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
   if (!param && mode != 1 && mode != 4) return set_error(A8_ERR_ARG, "null param");
@@ -232,10 +246,10 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
   if (mode == 4 && !(m && momentum_only)) return set_error(A8_ERR_ARG, "MNORM needs momentum and momentum_only");
   DescFull D{};
   D.param = param; D.grad = grad; D.v = variance; D.m = m; D.norm_buf = norm_buf;
-  D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel;
+  D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
-                        momentum_only, 0, alpha_val, decay_val, has_decay);
-  return launch_full_any(dtype, mode, D, nullptr, 0, (numel + kFElems - 1) / kFElems, h,
+                        momentum_only, sr_step, alpha_val, decay_val, has_decay);
+  return launch_full_any(dtype, stochastic, mode, D, nullptr, 0, (numel + kFElems - 1) / kFElems, h,
                          (hipStream_t)stream);
 }
 
@@ -243,8 +257,8 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   void* table_dev, int64_t table_bytes, double beta1, double beta_val,
                                   float eps_sq, float eps_for_denom, int use_adam_denom,
                                   float eps_for_grad_sq, float d, int momentum_only,
-                                  float alpha_val, float decay_val, int has_decay, int upload,
-                                  void* stream) {
+                                  float alpha_val, float decay_val, int has_decay, int stochastic,
+                                  uint64_t sr_step, int upload, void* stream) {
   if (ntensors <= 0) return 0;
   if ((int64_t)sizeof(DescFull) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_full(ntensors)");
@@ -264,6 +278,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
     DescFull& D = tab[(size_t)i];
     D.param = t.param; D.grad = t.grad; D.v = t.variance; D.m = t.m; D.norm_buf = t.norm_buf;
     D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay; D.numel = t.numel;
+    D.sr_seed = t.sr_seed;
     D.wg_begin = wg;
     wg += (t.numel + kFElems - 1) / kFElems;
   }
@@ -272,10 +287,10 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                hipMemcpyHostToDevice, st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
-                        momentum_only, 0, alpha_val, decay_val, has_decay);
+                        momentum_only, sr_step, alpha_val, decay_val, has_decay);
   DescFull none{};
-  return launch_full_any(dtype, mode, none, reinterpret_cast<const DescFull*>(table_dev), ntensors, wg,
-                         h, st);
+  return launch_full_any(dtype, stochastic, mode, none, reinterpret_cast<const DescFull*>(table_dev),
+                         ntensors, wg, h, st);
 }
 
 int64_t a8_table_bytes_full(int ntensors) { return (int64_t)sizeof(DescFull) * (int64_t)ntensors; }

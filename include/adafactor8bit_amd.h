@@ -120,16 +120,19 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                              float decay_val, int has_decay, int upload, void* stream);
 int64_t a8_table_bytes_1d(int ntensors);
 
-/* Replaces fused_update_1d_full_{noclip,norm,apply,lag} (kernels.cu:1374-1515;
+/* Replaces fused_update_1d_full_{noclip,norm,apply,lag}[_sr] (kernels.cu:1374-1515;
  * called at optimizer.py:2147-2183): fp32 V (and optional fp32 M, NULL for none)
  * for tensors below min_8bit_size or with quantize=False.  NORM writes V (and M
- * unless momentum_only) and accumulates sum(u^2) into norm_buf; APPLY reads them. */
+ * unless momentum_only) and accumulates sum(u^2) into norm_buf; APPLY reads them.
+ * stochastic (16-bit params): p * decay - step * u rounded with the (sr_seed,
+ * sr_step, element index) stream of kernels.cu:48-87. */
 int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
                             float* m, float* norm_buf, const float* alpha, const float* prev_norm,
                             const float* decay, double beta1, double beta_val, float eps_sq,
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
-                            float decay_val, int has_decay, void* stream);
+                            float decay_val, int has_decay, int stochastic, uint64_t sr_seed,
+                            uint64_t sr_step, void* stream);
 
 typedef struct a8_tensor_full {
   void* param;
@@ -141,6 +144,7 @@ typedef struct a8_tensor_full {
   const float* prev_norm;
   const float* decay;
   int64_t numel;
+  uint64_t sr_seed;        /* stochastic rounding seed (16-bit params) */
 } a8_tensor_full;
 
 /* Multi-tensor form of a8_fused_update_1d_full (one launch per group). */
@@ -148,8 +152,8 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   void* table_dev, int64_t table_bytes, double beta1, double beta_val,
                                   float eps_sq, float eps_for_denom, int use_adam_denom,
                                   float eps_for_grad_sq, float d, int momentum_only,
-                                  float alpha_val, float decay_val, int has_decay, int upload,
-                                  void* stream);
+                                  float alpha_val, float decay_val, int has_decay, int stochastic,
+                                  uint64_t sr_step, int upload, void* stream);
 int64_t a8_table_bytes_full(int ntensors);
 
 /* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,

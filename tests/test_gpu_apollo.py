@@ -261,15 +261,17 @@ def test_apollo_bf16_sr_writeback_bits(shape, channel, det_proj):
 
 @pytest.mark.gpu
 def test_1d_bf16_sr_writeback_stream():
-    """1-D fused step with SR writeback: the bf16 result is the stochastic rounding
-    of the fp32 result under the reference's stream.  The fp32 run writes
+    """1-D fused steps with SR writeback (quantised and fp32 state): the bf16
+    result is the stochastic rounding of the fp32 result under the reference's
+    stream.  The fp32 run writes
     fma(-step, u, p) and the SR path rounds (p - step * u), one fp32 rounding
     apart, which moves the round-up probability by 2^-16: at most 0.1% of the
     elements may land on the other bf16 neighbour."""
     from adafactor8bit import Adafactor8Bit
     from oracle import sr
     meta, kw, _ = gu.load("adamw_uf8_al8")
-    shapes = [(700, 300), (4097,), (64, 64)]
+    # quantised-state tensors and, below min_8bit_size (4096), fp32-state ones
+    shapes = [(700, 300), (4097,), (64, 64), (2048,), (1000,), (3,)]
     print("[1d sr]", flush=True)
     p16 = [torch.nn.Parameter(inputs.make_param(s, i, 3).to("cuda", torch.bfloat16)) for i, s in enumerate(shapes)]
     p32 = [torch.nn.Parameter(p.detach().float()) for p in p16]
@@ -287,7 +289,7 @@ def test_1d_bf16_sr_writeback_stream():
         want = sr.sr_round_bf16(x, seed=int(o16.state[p]["sr_seed"]), step=int(o16.state[p]["step"]))
         got = _t2np(p).reshape(-1).view(np.uint16)
         diff = got != want
-        assert diff.mean() <= 1e-3, diff.mean()
+        assert diff.sum() <= max(1, 1e-3 * diff.size), diff.mean()
         # where they differ, both are neighbours of x
         lo = (x.view(np.uint32) & np.uint32(0xFFFF0000)) >> np.uint32(16)
         assert np.all(np.isin(got[diff].astype(np.int64) - lo[diff].astype(np.int64), [0, 1]))

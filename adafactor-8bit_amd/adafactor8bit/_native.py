@@ -96,6 +96,8 @@ _SIGS = {
                                     _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i,
                                     _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_i, _c_vp]),
     "a8_apollo_table_bytes": (_c_i64, [_c_i]),
+    "a8_dequantize_log_nonneg": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
+    "a8_dequantize_dynamic": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
 }
 
 _LIB = None

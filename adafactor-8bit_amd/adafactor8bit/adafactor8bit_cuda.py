@@ -255,6 +255,25 @@ def fused_update_1d_full_lag_sr(param, grad, variance, m, norm_buf, alpha, prev_
           use_adam_denom, eps_for_grad_sq, numel, d, momentum_only, decay, sr_seed, sr_step)
 
 
+# ---- decode utilities (kernels.cu:2571-2632)
+def dequantize_log_nonneg(output, q, scale, min_log, numel, block_size, v_bits):
+    if int(v_bits) == 8 and q.dtype != torch.uint8:
+        raise RuntimeError("v_bits=8 requires q to be torch.uint8")
+    if int(v_bits) == 16 and q.dtype != torch.int16:
+        raise RuntimeError("v_bits=16 requires q to be torch.int16")
+    if scale.dtype != torch.float32 or min_log.dtype != torch.float32:
+        raise RuntimeError("scale and min_log must be torch.float32")
+    rc = nat.lib().a8_dequantize_log_nonneg(nat.ptr(output), nat.ptr(q), nat.ptr(scale), nat.ptr(min_log),
+                                            int(numel), int(block_size), int(v_bits), _stream(output))
+    nat.check(rc, "dequantize_log_nonneg")
+
+
+def dequantize_dynamic(output, q, scale, numel, block_size, m_bits):
+    rc = nat.lib().a8_dequantize_dynamic(nat.ptr(output), nat.ptr(q), nat.ptr(scale), int(numel),
+                                         int(block_size), int(m_bits), _stream(output))
+    nat.check(rc, "dequantize_dynamic")
+
+
 # ---- fira_scalar (kernels.cu:3055-3084)
 def fira_scalar(x, prev, alpha, has_prev, apply, margin, inv_margin):
     """Returns [3n] fp32: scale (or alpha*scale), next previous norm, cleaned input."""

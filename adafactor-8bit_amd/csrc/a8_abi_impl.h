@@ -37,4 +37,5 @@ namespace a8 {
 // Codebook upload of the factored-step translation unit (called by a8_set_qmap).
 hipError_t factored_upload_qmap(const float* q8, const float* q4);
 hipError_t apollo_upload_qmap(const float* q8, const float* q4);
+hipError_t decode_upload_qmap(const float* q8, const float* q4);
 }  // namespace a8

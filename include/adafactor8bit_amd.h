@@ -303,6 +303,22 @@ int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tens
                          float weight_decay, int wd_mode, void* stream);
 int64_t a8_apollo_table_bytes(int ntensors);
 
+/* Replaces dequantize_log_nonneg (kernels.cu:2593-2632; called by
+ * _log_dequantize_nonneg, optimizer.py:328-338): output[i] = 0 for code 0, else
+ * 2^(((q-1) * scale[b]) / (L-2) + min_log[b]) with b = i / block_size, L = 256
+ * (v_bits 8, uint8 codes) or 65536 (v_bits 16, int16 codes read as unsigned), in
+ * the fallback's numerics (optimizer.py:340-353: division, correctly rounded
+ * exp2).  output: fp32, 16-byte aligned. */
+int a8_dequantize_log_nonneg(float* output, const void* q, const float* scale, const float* min_log,
+                             int64_t numel, int block_size, int v_bits, void* stream);
+
+/* Replaces dequantize_dynamic (kernels.cu:2571-2590; called by
+ * _dequantize_dynamic_pytorch, optimizer.py:483-488): output[i] = qmap[q_i] *
+ * scale[i / block_size] with the codebook of a8_set_qmap; m_bits 8 (one code per
+ * byte) or 4 (two per byte, even element in the high nibble). */
+int a8_dequantize_dynamic(float* output, const uint8_t* q, const float* scale, int64_t numel, int block_size,
+                          int m_bits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -140,17 +140,28 @@ def make_grad(kind, shape, gen, dev, i, embed):
     return torch.randn(shape, device=dev, generator=gen) * 1e-3 * sc
 
 
-def cpu_baseline(seconds_budget=20.0):
-    """The CPU oracle (torch CPU restatement of the reference's fallback) on C1's
-    4096x4096 AdamW UF8/AL8 step, 1 warm-up + timed steps within the budget."""
+def cpu_baseline(workload="adamw", seconds_budget=20.0):
+    """The CPU oracle (torch CPU restatement of the reference's fallback) on a
+    bounded sample of the workload, 1 warm-up + timed steps within the budget:
+    adamw (C1): one 4096x4096 fp32 AdamW UF8/AL8 step; adafactor / came (C2, C3):
+    one 2048x2048 fp32 matrix of the config; apollo (C4): one 2048x2048 bf16
+    matrix at rank 256 (deterministic writeback: the reference's CPU stochastic
+    rounding draws from torch's CPU generator, a different stream)."""
     from inputs import make_grad, make_param
-    from oracle.fallback import OracleOptimizer
+    import oracle.fallback as F
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    shape = (4096, 4096)
-    p = torch.nn.Parameter(make_param(shape, 0, 0))
-    opt = OracleOptimizer([p], **{k: v for k, v in ADAMW.items()})
-    grads = [make_grad(shape, 0, t, 0) for t in (1, 2)]
+    shape, pdt, gk = (4096, 4096), torch.float32, "normal_zeros"
+    kw = dict(ADAMW)
+    if workload == "adafactor":
+        shape, gk, kw = (2048, 2048), "student_t", dict(ADAFACTOR)
+    elif workload == "came":
+        shape, gk, kw = (2048, 2048), "logscale", dict(CAME)
+    elif workload == "apollo":
+        shape, pdt, kw = (2048, 2048), torch.bfloat16, dict(APOLLO, stochastic_round_writeback=False)
+    p = torch.nn.Parameter(make_param(shape, 0, 0).to(pdt))
+    opt = F.OracleOptimizer([p], **kw)
+    grads = [make_grad(shape, 0, t, 0, kind=gk).to(pdt) for t in (1, 2)]
     p.grad = grads[0]
     opt.step()
     times = []
@@ -167,9 +178,12 @@ def cpu_baseline(seconds_budget=20.0):
     times.sort()
     med = times[len(times) // 2]
     n = shape[0] * shape[1]
+    what = {"adamw": "C1: one 4096x4096 fp32 AdamW UF8/AL8 step",
+            "adafactor": "C2: one 2048x2048 fp32 factored Adafactor AL8 step",
+            "came": "C3: one 2048x2048 fp32 CAME UF8/AL16/AL16+Fira step",
+            "apollo": "C4: one 2048x2048 bf16 APOLLO r=256 UF8/AL8 step (deterministic writeback)"}[workload]
     return {"value": n / med, "unit": "params/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"C1: one 4096x4096 fp32 AdamW UF8/AL8 step, median of {len(times)} after 1 warm-up",
-            "ms_per_step": med * 1e3}
+            "sample": f"{what}, median of {len(times)} after 1 warm-up", "ms_per_step": med * 1e3}
 
 
 def main():
@@ -278,7 +292,7 @@ def main():
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "kernel": "k_update1d<float,8,0,false> (multi-tensor, 156 tensors)",
                      "kernel_ms_avg": k_avg, "kernel_ms_min": kms[0], "bytes_per_launch": qbytes},
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline("adamw"),
     }
     print(json.dumps(out), flush=True)
 
@@ -321,7 +335,7 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
                      "kernel": "whole step (all launches of one step, HIP events around step())",
                      "gpu_ms_per_step": gms, "bytes_per_step": nbytes},
-        "cpu_baseline": None,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.workload),
     }
     if flops is not None:
         out["projection"] = {"flops_per_step": flops, "TFLOPs_at_step_time": flops / (gms * 1e-3) / 1e12}

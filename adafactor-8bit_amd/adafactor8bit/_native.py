@@ -39,6 +39,13 @@ class TensorFull(ctypes.Structure):
                 ("numel", _c_i64), ("sr_seed", _c_u64)]
 
 
+class TensorSgd(ctypes.Structure):
+    """Mirror of ``a8_tensor_sgd``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp), ("m", _c_vp),
+                ("norm_buf", _c_vp), ("fira", _c_vp), ("alpha", _c_vp), ("decay", _c_vp),
+                ("numel", _c_i64), ("sr_seed", _c_u64)]
+
+
 class Tensor2D(ctypes.Structure):
     """Mirror of ``a8_tensor2d``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
@@ -98,6 +105,12 @@ _SIGS = {
     "a8_apollo_table_bytes": (_c_i64, [_c_i]),
     "a8_dequantize_log_nonneg": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_dequantize_dynamic": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
+    "a8_sgd_step": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                           _c_i64, _c_d, _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_u64, _c_vp]),
+    "a8_sgd_step_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(TensorSgd), _c_i, _c_vp, _c_i64, _c_d, _c_i,
+                                 _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_i, _c_vp]),
+    "a8_table_bytes_sgd": (_c_i64, [_c_i]),
+    "a8_m_quantize_lerp": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i, _c_vp, _c_d, _c_i, _c_i64, _c_i, _c_i, _c_vp]),
 }
 
 _LIB = None

@@ -27,7 +27,9 @@ __all__ = [
     "fused_update_1d_vonly_lag", "fused_update_1d_vonly_noclip_sr", "fused_update_1d_vonly_apply_sr",
     "fused_update_1d_vonly_lag_sr",
     "fused_update_1d_full_noclip", "fused_update_1d_full_norm", "fused_update_1d_full_apply",
-    "fused_update_1d_full_lag",
+    "fused_update_1d_full_lag", "fused_update_1d_full_noclip_sr", "fused_update_1d_full_apply_sr",
+    "fused_update_1d_full_lag_sr",
+    "fused_m_quantize_lerp", "dequantize_log_nonneg", "dequantize_dynamic",
 ]
 
 _AL_FLOOR = -126.0
@@ -272,6 +274,20 @@ def dequantize_dynamic(output, q, scale, numel, block_size, m_bits):
     rc = nat.lib().a8_dequantize_dynamic(nat.ptr(output), nat.ptr(q), nat.ptr(scale), int(numel),
                                          int(block_size), int(m_bits), _stream(output))
     nat.check(rc, "dequantize_dynamic")
+
+
+# ---- fused_m_quantize_lerp (kernels.cu:574-588)
+def fused_m_quantize_lerp(q, scale, new_val, fp32_out, beta, block_size, N, m_bits, m_mode):
+    """Momentum EMA in place: m' = lerp(deq(q, scale), new_val, 1 - beta), requantised
+    per block; fp32_out (optional) receives m'."""
+    if q.dtype != torch.uint8 or scale.dtype != torch.float32:
+        raise RuntimeError("q must be torch.uint8 and scale torch.float32")
+    if fp32_out is not None and fp32_out.dtype != torch.float32:
+        raise RuntimeError("fp32_out must be torch.float32")
+    rc = nat.lib().a8_m_quantize_lerp(nat.ptr(q), nat.ptr(scale), nat.ptr(new_val), nat.dtype_code(new_val.dtype),
+                                      nat.ptr(fp32_out), float(beta), int(block_size), int(N), int(m_bits),
+                                      int(m_mode), _stream(new_val))
+    nat.check(rc, "fused_m_quantize_lerp")
 
 
 # ---- fira_scalar (kernels.cu:3055-3084)

@@ -335,7 +335,7 @@ class _Plan:
         if self.path == "factored":
             return ("factored", self.p.device, self.p.dtype, self.g.dtype, self.step, self.quant,
                     self.vqt, self.bs, self.has_m, self.mqt, self.mbs, self.sr, self.beta3)
-        if self.path not in ("q1d", "f1d"):
+        if self.path not in ("q1d", "f1d", "sgd"):
             return None
         if self.alpha_t is not None or self.decay_t is not None:
             return None
@@ -343,6 +343,10 @@ class _Plan:
             return None
         if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
+        if self.path == "sgd":
+            mq = self.has_m and self.quant and self.mqt != "fp32" and "m_q" in self.st
+            return ("sgd", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m, mq,
+                    self.mqt if mq else None, self.mbs if mq else 0, self.beta1, self.alpha_val, self.decay_val)
         return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
                 self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                 self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
@@ -620,9 +624,66 @@ def _fira_scale_only(opt, st, x, margin, device, key):
     return out[0].view(())
 
 
+def _sgd_momentum(P):
+    """Momentum buffers of an SGD step: (m_q, m_scale, m_fp32, kind) with kind 0
+    none, 1 quantised, 2 fp32 (optimizer.py:2046-2068)."""
+    if not P.has_m:
+        return None, None, None, 0
+    st = P.st
+    if P.quant and P.mqt != "fp32" and "m_q" in st:
+        return st["m_q"], st["m_scale"], None, 1
+    if "m" not in st:
+        st["m"] = torch.zeros_like(P.g, dtype=torch.float32)
+    if not st["m"].is_contiguous():
+        st["m"] = st["m"].contiguous()
+    return None, None, st["m"], 2
+
+
+def _run_sgd(opt, P):
+    """SGD branch of _update_param_8bit (optimizer.py:2045-2077): one pass, or
+    NORM -> (Fira) -> APPLY when the update is clipped (d > 0) or Fira is on."""
+    L = nat.lib()
+    st, dev = P.st, P.p.device
+    m_q, m_scale, m, kind = _sgd_momentum(P)
+    m_bits = S.m_bits(P.mqt) if kind == 1 else 0
+    m_mode = S.m_mode(P.mqt) if kind == 1 else 0
+    alpha_t, alpha_val = _alpha_args(P)
+    dec_t, dec_val, has_dec = _decay_args(P)
+    strm = nat.stream_of(dev)
+
+    def launch(mode, norm_buf=None, fira=None):
+        rc = L.a8_sgd_step(mode, nat.dtype_code(P.p.dtype), int(P.sr), nat.ptr(P.p), nat.ptr(P.g), nat.ptr(m_q),
+                           nat.ptr(m_scale), nat.ptr(m), nat.ptr(norm_buf), nat.ptr(fira), nat.ptr(alpha_t),
+                           nat.ptr(dec_t), P.p.numel(), P.beta1 if P.has_m else 0.0, m_bits, m_mode,
+                           P.mbs if kind == 1 else 32, P.d, float(alpha_val), float(dec_val), has_dec,
+                           int(st.get("sr_seed", 0)), int(P.step), strm)
+        nat.check(rc, "a8_sgd_step")
+
+    if not (P.d > 0.0 or P.fira):
+        launch(nat.MODE_NOCLIP)
+        return
+    nb = _norm_buf(opt, dev)
+    launch(nat.MODE_NORM, norm_buf=nb)
+    fira = None
+    if P.fira:
+        # _apply_fira_pytorch (optimizer.py:796-810): scale from ||u||, prev-norm state
+        prev = st.get("fira_prev_norm")
+        if prev is not None and not torch.is_tensor(prev):
+            prev = torch.tensor(prev, dtype=torch.float32, device=dev)
+        fira = torch.empty(3, dtype=torch.float32, device=dev)
+        rc = L.a8_fira_scalar(nat.ptr(nb), nat.ptr(prev), nat.ptr(_dev_scalar(opt, dev, "one", 1.0)),
+                              nat.ptr(fira), 1, int(prev is not None), 1, _f32(1.0 + P.margin), strm)
+        nat.check(rc, "a8_fira_scalar")
+        st["fira_prev_norm"] = fira[1].view(())
+    launch(nat.MODE_APPLY, norm_buf=nb, fira=fira)
+
+
 def _run_single(opt, P):
     if P.path == "factored":
         _run_factored(opt, [P])
+        return
+    if P.path == "sgd":
+        _run_sgd(opt, P)
         return
     if P.path not in ("q1d", "f1d"):
         raise NotImplementedError(f"adafactor8bit: '{P.path}' update path is not available in this build yet")
@@ -679,7 +740,15 @@ def _run_batch(opt, key, plans):
     ent = ws.get(cache_key)
     upload = 0
     if ent is None:
-        if path == "q1d":
+        if path == "sgd":
+            arr = (nat.TensorSgd * n)()
+            for i, pl in enumerate(plans):
+                m_q, m_scale, m, _ = _sgd_momentum(pl)
+                arr[i] = nat.TensorSgd(pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(m_q), nat.ptr(m_scale),
+                                       nat.ptr(m), None, None, None, None, pl.p.numel(),
+                                       int(pl.st.get("sr_seed", 0)))
+            nbytes = L.a8_table_bytes_sgd(n)
+        elif path == "q1d":
             arr = (nat.Tensor1D * n)()
             for i, pl in enumerate(plans):
                 st = pl.st
@@ -714,7 +783,16 @@ def _run_batch(opt, key, plans):
     has_dec = int(P0.decay_val is not None)
     dec_val = P0.decay_val if has_dec else 1.0
     strm = nat.stream_of(dev)
-    if path == "q1d":
+    if path == "sgd":
+        kind = 0 if not P0.has_m else (1 if key[7] else 2)
+        rc = L.a8_sgd_step_multi(
+            nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), nbytes,
+            P0.beta1 if P0.has_m else 0.0, kind, S.m_bits(P0.mqt) if kind == 1 else 0,
+            S.m_mode(P0.mqt) if kind == 1 else 0, P0.mbs if kind == 1 else 32, P0.d, float(P0.alpha_val),
+            float(dec_val), has_dec, int(P0.step), upload, strm)
+        nat.check(rc, "a8_sgd_step_multi")
+        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+    elif path == "q1d":
         rc = L.a8_fused_update_1d_multi(
             nat.MODE_NOCLIP, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,

@@ -14,7 +14,7 @@
  * reference's names and positional signatures and calls these functions.
  *
  * Numerics: quantised codes are decided as the reference's PyTorch path
- * decides them (optimizer.py:299-353, 504-532), see DESIGN.md.
+ * decides them (optimizer.py:299-353, 504-532).
  */
 #ifndef ADAFACTOR8BIT_AMD_H
 #define ADAFACTOR8BIT_AMD_H
@@ -318,6 +318,56 @@ int a8_dequantize_log_nonneg(float* output, const void* q, const float* scale, c
  * byte) or 4 (two per byte, even element in the high nibble). */
 int a8_dequantize_dynamic(float* output, const uint8_t* q, const float* scale, int64_t numel, int block_size,
                           int m_bits, void* stream);
+
+/* Replaces the SGD branch of _update_param_8bit (optimizer.py:2045-2077; beta2 and
+ * beta2_decay both None), whose CUDA path calls fused_m_quantize_lerp
+ * (kernels.cu:523-588) and then _apply_update_pytorch (optimizer.py:866-881).
+ * Fallback arithmetic: m' = lerp(deq(m), g, 1 - beta1); u = m' / (1 - beta1), or
+ * u = g without momentum; p = fma(-alpha/denom, u * s, p * decay) with
+ * denom = max(1, sqrt(sum u^2) / (sqrt(numel) d)) for d > 0 and the Fira scale s
+ * (1 without Fira); M is requantised from the fp32 m'.
+ * mode 0: one pass, no clip, no Fira.  mode 1 (NORM): accumulates sum(u^2) into
+ * *norm_buf (zeroed by the caller), writes nothing.  mode 2 (APPLY): reads
+ * *norm_buf, and fira = the 3-float output of a8_fira_scalar(norm_buf, prev, one,
+ * apply=1) when Fira is on (else null); a non-finite norm then zeroes the update
+ * (optimizer.py:797-800).  Momentum: m_q/m_scale (codes padded to whole
+ * m_block_size blocks, m_bits/m_mode as in a8_fused_update_1d), or fp32 m, or
+ * neither.  stochastic: 16-bit params written with the kernels.cu:48-87 stream. */
+int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* grad, uint8_t* m_q, float* m_scale,
+                float* m, float* norm_buf, const float* fira, const float* alpha, const float* decay, int64_t numel,
+                double beta1, int m_bits, int m_mode, int m_block_size, float d, float alpha_val, float decay_val,
+                int has_decay, uint64_t sr_seed, uint64_t sr_step, void* stream);
+
+typedef struct a8_tensor_sgd {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  float* m;
+  float* norm_buf;
+  const float* fira;
+  const float* alpha;
+  const float* decay;
+  int64_t numel;
+  uint64_t sr_seed;
+} a8_tensor_sgd;
+
+/* Multi-tensor form of a8_sgd_step: one launch per group.  m_kind: 0 none,
+ * 1 quantised (m_q, m_scale), 2 fp32 (m). */
+int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* tensors, int ntensors,
+                      void* table_dev, int64_t table_bytes, double beta1, int m_kind, int m_bits, int m_mode,
+                      int m_block_size, float d, float alpha_val, float decay_val, int has_decay, uint64_t sr_step,
+                      int upload, void* stream);
+int64_t a8_table_bytes_sgd(int ntensors);
+
+/* Replaces fused_m_quantize_lerp (kernels.cu:523-588; called by
+ * _m_fused_quantize_lerp, optimizer.py:563-571) with the arithmetic of its twin
+ * _m_ema_pytorch (optimizer.py:690-701): m' = lerp(deq(m), x, 1 - beta) per
+ * element (non-finite x read as 0), then one absmax per block and requantised
+ * codes; fp32_out (optional) receives m'.  x: x_dtype (A8_F32/BF16/F16).
+ * block_size: a power of two in [32, 2048]. */
+int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype, float* fp32_out, double beta,
+                       int block_size, int64_t numel, int m_bits, int m_mode, void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,17 @@ class TensorSgd(ctypes.Structure):
                 ("numel", _c_i64), ("sr_seed", _c_u64)]
 
 
+class FactoredPrimArgs(ctypes.Structure):
+    """Mirror of ``a8_factored_prim_args``."""
+    _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp), ("m", _c_vp),
+                ("row", _c_vp), ("col", _c_vp), ("row_mean", _c_vp), ("conf_row", _c_vp), ("conf_col", _c_vp),
+                ("conf_row_mean", _c_vp), ("row_sum", _c_vp), ("col_sum", _c_vp), ("norm_buf", _c_vp),
+                ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp), ("clip", _c_vp), ("rows", _c_i64),
+                ("cols", _c_i64), ("numel", _c_i64), ("beta1", _c_d), ("eps_came", _c_f), ("d", _c_f),
+                ("m_bits", _c_i), ("m_mode", _c_i), ("m_block_size", _c_i), ("sr_seed", _c_u64),
+                ("sr_step", _c_u64)]
+
+
 class Tensor2D(ctypes.Structure):
     """Mirror of ``a8_tensor2d``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
@@ -111,6 +122,16 @@ _SIGS = {
                                  _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_i, _c_vp]),
     "a8_table_bytes_sgd": (_c_i64, [_c_i]),
     "a8_m_quantize_lerp": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i, _c_vp, _c_d, _c_i, _c_i64, _c_i, _c_i, _c_vp]),
+    "a8_log_quantize_lerp": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i, _c_vp, _c_d, _c_i, _c_i, _c_f, _c_i64, _c_f,
+                                    _c_i, _c_vp]),
+    "a8_factored_prim": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(FactoredPrimArgs), _c_vp]),
+    "a8_apollo_norms": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_f,
+                               _c_i, _c_vp]),
+    "a8_apollo_came_rms": (_c_i, [_c_vp, _c_vp, _c_vp, _c_f, _c_i64, _c_vp]),
+    "a8_apollo_came_m_res": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_d, _c_d, _c_f, _c_f,
+                                    _c_i, _c_i64, _c_i, _c_i, _c_vp]),
+    "a8_apollo_writeback": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i, _c_i, _c_i, _c_u64,
+                                   _c_u64, _c_i64, _c_i64, _c_vp]),
 }
 
 _LIB = None

@@ -10,9 +10,7 @@ Numerics follow the reference's PyTorch path (optimizer.py:299-353, 504-532):
 the AL floor of the 1-D kernels is the CPU quantiser's -126, so the
 ``log_eps_sq`` argument only supplies eps1 for the Adam denominator's momentum clamp.
 
-Names of the reference module not listed in ``__all__`` are not provided yet;
-looking one up raises ``AttributeError``, which the reference's own
-``hasattr`` probes (optimizer.py:738, 2621-2628) treat as "absent".
+Every one of the reference module's 61 functions is provided.
 """
 import torch
 
@@ -30,6 +28,18 @@ __all__ = [
     "fused_update_1d_full_lag", "fused_update_1d_full_noclip_sr", "fused_update_1d_full_apply_sr",
     "fused_update_1d_full_lag_sr",
     "fused_m_quantize_lerp", "dequantize_log_nonneg", "dequantize_dynamic",
+    "fused_log_quantize_lerp",
+    "fused_update_2d_noclip", "fused_update_2d_norm", "fused_update_2d_apply", "fused_update_2d_lag",
+    "fused_update_2d_noclip_sr", "fused_update_2d_apply_sr", "fused_update_2d_lag_sr",
+    "fused_update_2d_full_noclip", "fused_update_2d_full_norm", "fused_update_2d_full_apply",
+    "fused_update_2d_full_lag", "fused_update_2d_full_noclip_sr", "fused_update_2d_full_apply_sr",
+    "fused_update_2d_full_lag_sr", "compute_factored_sums", "compute_ut_rms",
+    "fused_came_pass1", "fused_came_pass2_norm", "fused_came_pass2", "fused_came_pass2_sr",
+    "fused_came_full_pass1", "fused_came_full_pass2", "fused_came_full_pass2_sr",
+    "compute_apollo_norms", "compute_apollo_came_rms", "apollo_came_compute_m_res",
+    "apollo_came_compute_update_norms", "apollo_apply_bf16_det", "apollo_apply_bf16_sr", "apollo_apply_fp16_sr",
+    "apollo_apply_bf16_det_native", "apollo_apply_fp16_det_native", "apollo_apply_bf16_sr_native",
+    "apollo_apply_fp16_sr_native",
 ]
 
 _AL_FLOOR = -126.0
@@ -288,6 +298,302 @@ def fused_m_quantize_lerp(q, scale, new_val, fp32_out, beta, block_size, N, m_bi
                                       nat.ptr(fp32_out), float(beta), int(block_size), int(N), int(m_bits),
                                       int(m_mode), _stream(new_val))
     nat.check(rc, "fused_m_quantize_lerp")
+
+
+# ---- fused_log_quantize_lerp (kernels.cu:332-368)
+def fused_log_quantize_lerp(q, scale, min_log_out, new_val, fp32_out, beta, block_size, square_input, eps1, N,
+                            log_floor, v_bits):
+    """V EMA in place: v' = lerp(deq(q), x, beta) with x = new_val (squared + eps1
+    when square_input), AL-requantised per block; fp32_out (optional) receives v'."""
+    _vbits_check(q, v_bits)
+    if scale.dtype != torch.float32 or min_log_out.dtype != torch.float32:
+        raise RuntimeError("scale and min_log_out must be torch.float32")
+    rc = nat.lib().a8_log_quantize_lerp(nat.ptr(q), nat.ptr(scale), nat.ptr(min_log_out), nat.ptr(new_val),
+                                        nat.dtype_code(new_val.dtype), nat.ptr(fp32_out), float(beta),
+                                        int(block_size), int(bool(square_input)), float(eps1), int(N),
+                                        float(log_floor), int(v_bits), _stream(new_val))
+    nat.check(rc, "fused_log_quantize_lerp")
+
+
+# ---- factored element primitives (kernels.cu:1523-2400)
+_F_NOCLIP, _F_NORM, _F_APPLY, _F_LAG, _F_SUMS, _F_CAME1, _F_CAME2N, _F_CAME2 = range(8)
+
+
+def _fprim(op, ref, stochastic=False, **kw):
+    """One a8_factored_prim call; ``ref`` is the tensor whose dtype and device
+    select the kernel (the gradient, or the parameter)."""
+    a = nat.FactoredPrimArgs()
+    for k, v in kw.items():
+        if torch.is_tensor(v):
+            setattr(a, k, v.data_ptr())
+        elif v is None:
+            setattr(a, k, None)
+        else:
+            setattr(a, k, v)
+    rc = nat.lib().a8_factored_prim(op, nat.dtype_code(ref.dtype), int(bool(stochastic)), a, _stream(ref))
+    nat.check(rc, "factored primitive")
+
+
+def _sr_check(param, grad):
+    if param.dtype not in (torch.bfloat16, torch.float16) or (grad is not None and grad.dtype != param.dtype):
+        raise RuntimeError("SR writeback requires matching FP16/BF16 param and grad")
+
+
+def _u2d(op, param, grad, m_q, m_scale, m, row, col, rm, norm_buf, alpha, prev_norm, decay, sr_seed, sr_step,
+         beta1, R, C, numel, m_block_size, m_bits, m_mode, d, sr):
+    if sr:
+        _sr_check(param, grad)
+    _fprim(op, grad, sr, param=param, grad=grad, m_q=m_q, m_scale=m_scale, m=m, row=row, col=col,
+           row_mean=rm, norm_buf=norm_buf, alpha=alpha, prev_norm=prev_norm, decay=decay, rows=int(R),
+           cols=int(C), numel=int(numel), beta1=float(beta1), d=float(d), m_bits=int(m_bits), m_mode=int(m_mode),
+           m_block_size=int(m_block_size), sr_seed=int(sr_seed), sr_step=int(sr_step))
+
+
+def fused_update_2d_noclip(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, alpha, beta1, R, C, numel,
+                           m_block_size, m_bits, m_mode):
+    _u2d(_F_NOCLIP, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, None, alpha, None, None, 0, 0,
+         beta1, R, C, numel, m_block_size, m_bits, m_mode, 0.0, False)
+
+
+def fused_update_2d_norm(grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, norm_buf, beta1, R, C, numel,
+                         m_block_size, m_bits, m_mode):
+    _u2d(_F_NORM, None, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, norm_buf, None, None, None, 0, 0,
+         beta1, R, C, numel, m_block_size, m_bits, m_mode, 0.0, False)
+
+
+def fused_update_2d_apply(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, beta1, R, C,
+                          numel, m_block_size, m_bits, m_mode, d):
+    _u2d(_F_APPLY, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, None, None, 0,
+         0, beta1, R, C, numel, m_block_size, m_bits, m_mode, d, False)
+
+
+def fused_update_2d_lag(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm,
+                        beta1, R, C, numel, m_block_size, m_bits, m_mode, d):
+    _u2d(_F_LAG, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, None,
+         0, 0, beta1, R, C, numel, m_block_size, m_bits, m_mode, d, False)
+
+
+def fused_update_2d_noclip_sr(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, alpha, decay, sr_seed,
+                              sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode):
+    _u2d(_F_NOCLIP, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, None, alpha, None, decay,
+         sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, 0.0, True)
+
+
+def fused_update_2d_apply_sr(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, decay,
+                             sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, d):
+    _u2d(_F_APPLY, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, None, decay,
+         sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, d, True)
+
+
+def fused_update_2d_lag_sr(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm,
+                           decay, sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, d):
+    _u2d(_F_LAG, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, decay,
+         sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, d, True)
+
+
+def fused_update_2d_full_noclip(param, grad, m, row_fp32, col_fp32, row_mean_val, alpha, beta1, R, C, numel,
+                                m_block_size):
+    _u2d(_F_NOCLIP, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, None, alpha, None, None, 0, 0,
+         beta1, R, C, numel, m_block_size, 8, 0, 0.0, False)
+
+
+def fused_update_2d_full_norm(grad, m, row_fp32, col_fp32, row_mean_val, norm_buf, beta1, R, C, numel, m_block_size):
+    _u2d(_F_NORM, None, grad, None, None, m, row_fp32, col_fp32, row_mean_val, norm_buf, None, None, None, 0, 0,
+         beta1, R, C, numel, m_block_size, 8, 0, 0.0, False)
+
+
+def fused_update_2d_full_apply(param, grad, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, beta1, R, C,
+                               numel, m_block_size, d):
+    _u2d(_F_APPLY, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, None, None, 0, 0,
+         beta1, R, C, numel, m_block_size, 8, 0, d, False)
+
+
+def fused_update_2d_full_lag(param, grad, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, beta1, R,
+                             C, numel, m_block_size, d):
+    _u2d(_F_LAG, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, None, 0, 0,
+         beta1, R, C, numel, m_block_size, 8, 0, d, False)
+
+
+def fused_update_2d_full_noclip_sr(param, grad, m, row_fp32, col_fp32, row_mean_val, alpha, decay, sr_seed, sr_step,
+                                   beta1, R, C, numel, m_block_size):
+    _u2d(_F_NOCLIP, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, None, alpha, None, decay, sr_seed,
+         sr_step, beta1, R, C, numel, m_block_size, 8, 0, 0.0, True)
+
+
+def fused_update_2d_full_apply_sr(param, grad, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, decay, sr_seed,
+                                  sr_step, beta1, R, C, numel, m_block_size, d):
+    _u2d(_F_APPLY, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, None, decay,
+         sr_seed, sr_step, beta1, R, C, numel, m_block_size, 8, 0, d, True)
+
+
+def fused_update_2d_full_lag_sr(param, grad, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, decay,
+                                sr_seed, sr_step, beta1, R, C, numel, m_block_size, d):
+    _u2d(_F_LAG, param, grad, None, None, m, row_fp32, col_fp32, row_mean_val, norm_buf, alpha, prev_norm, decay,
+         sr_seed, sr_step, beta1, R, C, numel, m_block_size, 8, 0, d, True)
+
+
+def compute_factored_sums(grad, row_sum, col_sum, R, C, numel):
+    _fprim(_F_SUMS, grad, grad=grad, row_sum=row_sum, col_sum=col_sum, rows=int(R), cols=int(C), numel=int(numel))
+
+
+def compute_ut_rms(grad, row_fp32, col_fp32, row_mean_val, ut_sq_sum, R, C, numel):
+    _fprim(_F_NORM, grad, grad=grad, row=row_fp32, col=col_fp32, row_mean=row_mean_val, norm_buf=ut_sq_sum,
+           rows=int(R), cols=int(C), numel=int(numel))
+
+
+def fused_came_pass1(grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, res_row_sum, res_col_sum, clip_factor,
+                     beta1, eps_came, R, C, numel, m_block_size, m_bits, m_mode):
+    _fprim(_F_CAME1, grad, grad=grad, m_q=m_q, m_scale=m_scale, row=row_fp32, col=col_fp32, row_mean=row_mean_val,
+           row_sum=res_row_sum, col_sum=res_col_sum, clip=clip_factor, beta1=float(beta1), eps_came=float(eps_came),
+           rows=int(R), cols=int(C), numel=int(numel), m_block_size=int(m_block_size), m_bits=int(m_bits),
+           m_mode=int(m_mode))
+
+
+def _came2(op, param, grad, m_q, m_scale, m, row, col, rm, crow, ccol, crm, clip, norm_buf, alpha, decay, sr_seed,
+           sr_step, beta1, R, C, numel, m_block_size, m_bits, m_mode, sr):
+    ref = grad if grad is not None else m
+    if sr:
+        _sr_check(param, grad)
+    _fprim(op, param if (param is not None and op == _F_CAME2) else ref, sr, param=param, grad=grad, m_q=m_q,
+           m_scale=m_scale, m=m, row=row, col=col, row_mean=rm, conf_row=crow, conf_col=ccol, conf_row_mean=crm,
+           clip=clip, norm_buf=norm_buf, alpha=alpha, decay=decay, sr_seed=int(sr_seed), sr_step=int(sr_step),
+           beta1=float(beta1), rows=int(R), cols=int(C), numel=int(numel), m_block_size=int(m_block_size),
+           m_bits=int(m_bits), m_mode=int(m_mode))
+
+
+def fused_came_pass2_norm(grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+                          conf_row_mean, clip_factor, norm_buf, beta1, R, C, numel, m_block_size, m_bits, m_mode):
+    _came2(_F_CAME2N, None, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+           conf_row_mean, clip_factor, norm_buf, None, None, 0, 0, beta1, R, C, numel, m_block_size, m_bits, m_mode,
+           False)
+
+
+def fused_came_pass2(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+                     conf_row_mean, clip_factor, alpha, beta1, R, C, numel, m_block_size, m_bits, m_mode):
+    _came2(_F_CAME2, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+           conf_row_mean, clip_factor, None, alpha, None, 0, 0, beta1, R, C, numel, m_block_size, m_bits, m_mode,
+           False)
+
+
+def fused_came_pass2_sr(param, grad, m_q, m_scale, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+                        conf_row_mean, clip_factor, alpha, decay, sr_seed, sr_step, beta1, R, C, numel, m_block_size,
+                        m_bits, m_mode):
+    _came2(_F_CAME2, param, grad, m_q, m_scale, None, row_fp32, col_fp32, row_mean_val, conf_row_fp32, conf_col_fp32,
+           conf_row_mean, clip_factor, None, alpha, decay, sr_seed, sr_step, beta1, R, C, numel, m_block_size, m_bits,
+           m_mode, True)
+
+
+def fused_came_full_pass1(grad, m, row_fp32, col_fp32, row_mean_val, res_row_sum, res_col_sum, clip_factor, beta1,
+                          eps_came, R, C, numel, m_block_size):
+    _fprim(_F_CAME1, grad, grad=grad, m=m, row=row_fp32, col=col_fp32, row_mean=row_mean_val, row_sum=res_row_sum,
+           col_sum=res_col_sum, clip=clip_factor, beta1=float(beta1), eps_came=float(eps_came), rows=int(R),
+           cols=int(C), numel=int(numel), m_block_size=int(m_block_size))
+
+
+def fused_came_full_pass2(param, m, conf_row_fp32, conf_col_fp32, conf_row_mean, norm_buf, alpha, R, C, numel,
+                          m_block_size, norm_only):
+    op = _F_CAME2N if norm_only else _F_CAME2
+    if norm_only and norm_buf is None:
+        raise RuntimeError("fused_came_full_pass2: norm_only needs norm_buf")
+    _fprim(op, param, param=None if norm_only else param, m=m, conf_row=conf_row_fp32, conf_col=conf_col_fp32,
+           conf_row_mean=conf_row_mean, norm_buf=norm_buf, alpha=alpha, rows=int(R), cols=int(C), numel=int(numel),
+           m_block_size=int(m_block_size))
+
+
+def fused_came_full_pass2_sr(param, m, conf_row_fp32, conf_col_fp32, conf_row_mean, alpha, decay, sr_seed, sr_step,
+                             R, C, numel, m_block_size):
+    _sr_check(param, None)
+    _fprim(_F_CAME2, param, True, param=param, m=m, conf_row=conf_row_fp32, conf_col=conf_col_fp32,
+           conf_row_mean=conf_row_mean, alpha=alpha, decay=decay, sr_seed=int(sr_seed), sr_step=int(sr_step),
+           rows=int(R), cols=int(C), numel=int(numel), m_block_size=int(m_block_size))
+
+
+# ---- APOLLO primitives (kernels.cu:2410-2570, 2638-3000)
+def compute_apollo_norms(m_fp32, v_fp32, grad_low, norm_update, norm_grad, N, D, stride_N, stride_D, apollo_eps):
+    rc = nat.lib().a8_apollo_norms(nat.ptr(m_fp32), nat.ptr(v_fp32), nat.ptr(grad_low), nat.ptr(norm_update),
+                                   nat.ptr(norm_grad), int(N), int(D), int(stride_N), int(stride_D),
+                                   int(m_fp32.numel()), float(apollo_eps), 0, _stream(m_fp32))
+    nat.check(rc, "compute_apollo_norms")
+
+
+def compute_apollo_came_rms(grad_low, v_fp32, sum_u2, eps_sq, numel):
+    rc = nat.lib().a8_apollo_came_rms(nat.ptr(grad_low), nat.ptr(v_fp32), nat.ptr(sum_u2), float(eps_sq),
+                                      int(numel), _stream(grad_low))
+    nat.check(rc, "compute_apollo_came_rms")
+
+
+def apollo_came_compute_m_res(grad_low, v_fp32, m_q_old, m_scale_old, res_fp32_old, m_temp, res_temp, clip_factor,
+                              beta1, beta3, eps_came, eps_sq, m_block_size, numel, m_bits, m_mode):
+    rc = nat.lib().a8_apollo_came_m_res(nat.ptr(grad_low), nat.ptr(v_fp32), nat.ptr(m_q_old), nat.ptr(m_scale_old),
+                                        nat.ptr(res_fp32_old), nat.ptr(m_temp), nat.ptr(res_temp),
+                                        nat.ptr(clip_factor), float(beta1), float(beta3), float(eps_came),
+                                        float(eps_sq), int(m_block_size), int(numel), int(m_bits), int(m_mode),
+                                        _stream(grad_low))
+    nat.check(rc, "apollo_came_compute_m_res")
+
+
+def apollo_came_compute_update_norms(m_fp32_new, res_fp32_new, grad_low, norm_update, norm_grad, eps_sq, N, D,
+                                     stride_N, stride_D, numel):
+    rc = nat.lib().a8_apollo_norms(nat.ptr(m_fp32_new), nat.ptr(res_fp32_new), nat.ptr(grad_low),
+                                   nat.ptr(norm_update), nat.ptr(norm_grad), int(N), int(D), int(stride_N),
+                                   int(stride_D), int(numel), float(eps_sq), 1, _stream(m_fp32_new))
+    nat.check(rc, "apollo_came_compute_update_norms")
+
+
+def _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, native, sr, maximize=False,
+          sr_seed=0, sr_step=0, want=None):
+    if want is not None and param.dtype != want:
+        raise RuntimeError(f"param must be {want}")
+    if param.dim() != 2 or not param.is_contiguous() or not grad.is_contiguous():
+        raise RuntimeError("param must be 2D; param and grad must be contiguous")
+    if native and grad.dtype != param.dtype:
+        raise RuntimeError("param and grad dtypes must match")
+    if not native and grad.dtype != torch.float32:
+        raise RuntimeError("grad must be float32")
+    if final_scale.dtype != torch.float32:
+        raise RuntimeError("final_scale must be float32")
+    dec = decay if (decay is not None and decay.numel()) else None
+    rc = nat.lib().a8_apollo_writeback(nat.dtype_code(param.dtype), int(native), int(sr), nat.ptr(param),
+                                       nat.ptr(grad), nat.ptr(final_scale), nat.ptr(dec), nat.ptr(update_scale),
+                                       int(bool(side_right)), int(bool(is_channel)), int(bool(maximize)),
+                                       int(sr_seed), int(sr_step), param.shape[0], param.shape[1], _stream(param))
+    nat.check(rc, "apollo_apply")
+
+
+def apollo_apply_bf16_det(param, grad, final_scale, decay, update_scale, side_right, is_channel):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, False, False, want=torch.bfloat16)
+
+
+def apollo_apply_bf16_sr(param, grad, final_scale, decay, update_scale, side_right, is_channel, sr_seed, sr_step):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, False, True, sr_seed=sr_seed,
+          sr_step=sr_step, want=torch.bfloat16)
+
+
+def apollo_apply_fp16_sr(param, grad, final_scale, decay, update_scale, side_right, is_channel, sr_seed, sr_step):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, False, True, sr_seed=sr_seed,
+          sr_step=sr_step, want=torch.float16)
+
+
+def apollo_apply_bf16_det_native(param, grad, final_scale, decay, update_scale, side_right, is_channel, maximize):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, True, False, maximize,
+          want=torch.bfloat16)
+
+
+def apollo_apply_fp16_det_native(param, grad, final_scale, decay, update_scale, side_right, is_channel, maximize):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, True, False, maximize,
+          want=torch.float16)
+
+
+def apollo_apply_bf16_sr_native(param, grad, final_scale, decay, update_scale, side_right, is_channel, maximize,
+                                sr_seed, sr_step):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, True, True, maximize, sr_seed,
+          sr_step, want=torch.bfloat16)
+
+
+def apollo_apply_fp16_sr_native(param, grad, final_scale, decay, update_scale, side_right, is_channel, maximize,
+                                sr_seed, sr_step):
+    _apwb(param, grad, final_scale, decay, update_scale, side_right, is_channel, True, True, maximize, sr_seed,
+          sr_step, want=torch.float16)
 
 
 # ---- fira_scalar (kernels.cu:3055-3084)

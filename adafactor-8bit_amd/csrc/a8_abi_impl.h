@@ -39,4 +39,5 @@ hipError_t factored_upload_qmap(const float* q8, const float* q4);
 hipError_t apollo_upload_qmap(const float* q8, const float* q4);
 hipError_t decode_upload_qmap(const float* q8, const float* q4);
 hipError_t sgd_upload_qmap(const float* q8, const float* q4);
+hipError_t prims_upload_qmap(const float* q8, const float* q4);
 }  // namespace a8

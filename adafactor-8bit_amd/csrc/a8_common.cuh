@@ -213,7 +213,15 @@ template <> __device__ __forceinline__ float from_f<float>(float x) { return x; 
 template <> __device__ __forceinline__ __hip_bfloat16 from_f<__hip_bfloat16>(float x) {
   return __float2bfloat16(x);
 }
-template <> __device__ __forceinline__ __half from_f<__half>(float x) { return __float2half(x); }
+// x as a materialised fp32 value: the empty asm stops instruction selection from
+// fusing the conversion that follows with the multiply or fma that produced x
+// into one v_fma_mix*_f16, which rounds the exact result to fp16 once instead of
+// rounding to fp32 first, as the reference and its PyTorch path do.
+__device__ __forceinline__ float f32_value(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+template <> __device__ __forceinline__ __half from_f<__half>(float x) { return __float2half(f32_value(x)); }
 
 // Single-element global load / store of a param-typed value (16-bit types go
 // through their bit pattern: class types cannot be bound in address space 1).

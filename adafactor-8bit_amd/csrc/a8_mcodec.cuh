@@ -160,4 +160,69 @@ __device__ __forceinline__ uint32_t m_encode(int mk, float m, float amax, float 
   }
 }
 
+// ------------------------------------------------------------ lane codecs
+// Momentum of elements e0..e0+7 (one lane; e0 a multiple of 8) from codes
+// padded to whole blocks of 2^lbm elements.  mb = e0 >> lbm; m_ok says the
+// lane's block exists (mb < number of blocks).
+__device__ __forceinline__ void mq_decode8(int mk, const uint8_t* m_q, const float* m_scale, int64_t e0,
+                                           int64_t mb, bool m_ok, float* mo) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mo[k] = 0.0f;
+  if (!m_ok) return;
+  const float ms = gp(m_scale)[mb];
+  if (mk == 2 || mk == 4) {
+    const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(m_q + (e0 >> 1)));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
+      mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+    }
+  } else {
+    const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(m_q + e0));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
+  }
+}
+
+// Requantise the lane's 8 values m[] (zero beyond the tensor): absmax over the
+// ML = B_M / 8 lanes of a block (across waves through xw[4] when ML > 64),
+// codes and the block scale.  Every lane of the 256-lane workgroup calls it.
+__device__ __forceinline__ void mq_encode8(int mk, uint8_t* m_q, float* m_scale, int64_t e0, int64_t mb, bool m_ok,
+                                           const float* m, int ML, float* xw) {
+  const int lane = threadIdx.x, wave = lane >> 6;
+  uint32_t ab = 0u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) ab = max(ab, __float_as_uint(m[k]) & 0x7FFFFFFFu);
+  float bam = __uint_as_float(ab);
+  for (int o = 1; o < (ML < 64 ? ML : 64); o <<= 1) bam = fmaxf(bam, __shfl_xor(bam, o, 64));
+  if (ML > 64) {
+    if ((lane & 63) == 0) xw[wave] = bam;
+    __syncthreads();
+    const int wpb = ML >> 6, w0 = (wave / wpb) * wpb;
+    bam = xw[w0];
+    for (int ww = 1; ww < wpb; ++ww) bam = fmaxf(bam, xw[w0 + ww]);
+  }
+  if (!m_ok) return;
+  const float am = fmaxf(bam, 1e-12f);
+  const float ram = __builtin_amdgcn_rcpf(am);
+  if (mk == 2 || mk == 4) {
+    uint32_t wq = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t hi4 = m_encode(mk, m[2 * j], am, ram);
+      const uint32_t lo4 = m_encode(mk, m[2 * j + 1], am, ram);
+      wq |= ((hi4 << 4) | lo4) << (8 * j);
+    }
+    *gp(reinterpret_cast<uint32_t*>(m_q + (e0 >> 1))) = wq;
+  } else {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w0 |= m_encode(mk, m[k], am, ram) << (8 * k);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w1 |= m_encode(mk, m[k + 4], am, ram) << (8 * k);
+    *gp(reinterpret_cast<u32x2*>(m_q + e0)) = u32x2{w0, w1};
+  }
+  if ((lane & (ML - 1)) == 0) gp(m_scale)[mb] = am;
+}
+
 }  // namespace a8

@@ -1,0 +1,598 @@
+// Stand-alone step primitives of the reference's module (gfx950).
+//
+// The reference's optimizer drives its factored, CAME and APOLLO steps as
+// sequences of small kernels (kernels.cu:340-480, 1523-2440, 2638-3000).  This
+// build's own optimizer fuses those sequences (a8_factored.hip, a8_apollo.hip);
+// the kernels here give the same primitives one by one, so the reference's
+// optimizer can run on this library through the reference-named module.
+//
+// Arithmetic follows the reference's PyTorch twins of each primitive:
+//   V EMA        lerp(deq(v), x, beta) with x = g^2 + eps1 when squared, AL codes
+//                refit per block from the non-zero values (optimizer.py:2232-2238)
+//   2-D update   inv_row = 1/sqrt(row / row_mean), inv_col = 1/sqrt(col),
+//                u = (x * inv_row) * inv_col with x = lerp(m, g, 1 - beta1) or g,
+//                p = fma(-step, u, p)                (optimizer.py:818-821, 958-970)
+//   CAME         U = ((g * inv_row) * inv_col) / clip, M = lerp(M, U, 1 - beta1),
+//                res = (U - M)^2 + eps_came; update (M * inv_crow) * inv_ccol with
+//                the confidence factors              (optimizer.py:929-956)
+// and the reference's kernels where no twin exists (APOLLO norms and writeback,
+// kernels.cu:2410-2570, 2638-3000).
+//
+// Layout: the element kernels give each lane 8 consecutive elements and a
+// 256-lane workgroup 2048, a whole number of momentum blocks; the row / column
+// of each element is stepped from the lane's first element.
+#include "a8_common.cuh"
+#include "a8_mcodec.cuh"
+#include "a8_abi_impl.h"
+
+namespace a8 {
+
+constexpr int kPElems = 2048;
+
+// ============================================================ V EMA
+template <int VB, typename T>
+__global__ __launch_bounds__(256) void k_vema(void* __restrict__ q, float* __restrict__ scale,
+                                              float* __restrict__ min_log, const T* __restrict__ x,
+                                              float* __restrict__ out, int64_t n, int64_t nblk, int lbv, float w,
+                                              int square, float eps1, float floor_) {
+  __shared__ float xw[8];
+  const int lane = threadIdx.x, wave = lane >> 6;
+  const int64_t e0 = (int64_t)blockIdx.x * kPElems + (int64_t)lane * 8;
+  const int VL = (1 << lbv) >> 3;
+  const int64_t vb = e0 >> lbv;
+  const bool v_ok = vb < nblk;
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
+  constexpr float LM2 = VB == 8 ? 254.0f : 65534.0f;
+  float xv[8];
+  load8<T>(x, e0, n, xv);
+  float v[8];
+  const float s_old = v_ok ? gp(scale)[vb] : 0.0f, lm_old = v_ok ? gp(min_log)[vb] : 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float xi = xv[k];
+    if (square) xi = xi * xi + eps1;
+    xi = scrub(xi);
+    float vo = 0.0f;
+    if (k < cnt) {
+      uint32_t c;
+      if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(q))[e0 + k];
+      else c = gp(reinterpret_cast<const uint16_t*>(q))[e0 + k];
+      vo = c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f;
+    }
+    v[k] = (k < cnt) ? lerp_ref(vo, xi, w) : 0.0f;   // padding quantises as zero
+  }
+  if (out) store8<float>(out, e0, n, v);
+  uint32_t vmaxb = 0u, vkey = 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    vmaxb = max(vmaxb, __float_as_uint(v[k]));
+    vkey = min(vkey, __float_as_uint(v[k]) - 1u);   // zero wraps to the largest key
+  }
+  const int G = VL < 64 ? VL : 64;
+  float bmax = grp_max(__uint_as_float(vmaxb), G);
+  uint32_t bkey = vkey;
+  for (int o = 1; o < G; o <<= 1) bkey = min(bkey, (uint32_t)__shfl_xor((int)bkey, o, 64));
+  if (VL > 64) {
+    if ((lane & 63) == 0) { xw[wave * 2] = bmax; xw[wave * 2 + 1] = __uint_as_float(bkey); }
+    __syncthreads();
+    const int wpb = VL >> 6, w0 = (wave / wpb) * wpb;
+    bmax = xw[w0 * 2];
+    bkey = __float_as_uint(xw[w0 * 2 + 1]);
+    for (int ww = 1; ww < wpb; ++ww) {
+      bmax = fmaxf(bmax, xw[(w0 + ww) * 2]);
+      bkey = min(bkey, __float_as_uint(xw[(w0 + ww) * 2 + 1]));
+    }
+  }
+  if (!v_ok) return;
+  const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
+  constexpr int L2 = VB == 8 ? 254 : 65534;
+  const ALFit f = al_refit(bmax, mnz, floor_, (float)L2);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t code = al_finish<L2>(v[k], al_round_exact<L2>(v[k], f));
+    if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[e0 + k] = (uint8_t)code;
+    else gp(reinterpret_cast<uint16_t*>(q))[e0 + k] = (uint16_t)code;
+  }
+  if ((lane & (VL - 1)) == 0) { gp(scale)[vb] = f.s; gp(min_log)[vb] = f.lmin; }
+}
+
+// ============================================================ factored element kernel
+enum { F_NOCLIP = 0, F_NORM = 1, F_APPLY = 2, F_LAG = 3, F_SUMS = 4, F_CAME1 = 5, F_CAME2N = 6, F_CAME2 = 7 };
+
+struct F2 {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  float* m;
+  const float* row;       // b*R + r
+  const float* col;       // b*C + c
+  const float* rmean;     // b
+  const float* crow;
+  const float* ccol;
+  const float* crmean;
+  float* row_sum;
+  float* col_sum;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  const float* clip;
+  int64_t R, C, n;
+  uint64_t sr_seed, sr_step;
+  float w_m;        // (float)(1 - beta1)
+  float eps_came;
+  float d;
+  float sqrt_nd;    // (float)(sqrt(n) * d)
+  int mq;           // momentum: 0 none, 1 quantised, 2 fp32
+  int mk;           // codec of quantised momentum (1 UF8, 2 UF4, 3 D8, 4 D4)
+  int lbm;          // log2 of the momentum block
+  int sr;
+};
+
+template <typename T>
+__device__ __forceinline__ void f2_write(const F2& a, int64_t e0, int cnt, float step, const float* u) {
+  float p[8];
+  load8<T>(reinterpret_cast<const T*>(a.param), e0, a.n, p);
+  if (a.sr) {
+    const float dec = a.decay ? *a.decay : 1.0f;
+    T* P = reinterpret_cast<T*>(a.param);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < cnt) P[e0 + k] = sr_round<T>(__builtin_fmaf(-step, u[k], p[k] * dec), a.sr_seed, a.sr_step,
+                                           (uint64_t)(e0 + k));
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) p[k] = __builtin_fmaf(-step, u[k], p[k]);
+    store8<T>(reinterpret_cast<T*>(a.param), e0, a.n, p);
+  }
+}
+
+__device__ __forceinline__ void f2_sum_add(float* buf, float v) {
+  const float t = grp_sum(v, 64);
+  if ((threadIdx.x & 63) == 0 && t != 0.0f) atomicAdd(buf, t);
+}
+
+// Row sums: one atomic per row segment of the lane; column sums: one per element.
+__device__ __forceinline__ void f2_rowcol_add(const F2& a, int cnt, const int64_t* ri, const int64_t* ci,
+                                              const float* val) {
+  float acc = 0.0f;
+  int64_t cur = ri[0];
+  for (int k = 0; k < cnt; ++k) {
+    if (ri[k] != cur) {
+      atomicAdd(a.row_sum + cur, acc);
+      acc = 0.0f;
+      cur = ri[k];
+    }
+    acc += val[k];
+    atomicAdd(a.col_sum + ci[k], val[k]);
+  }
+  if (cnt > 0) atomicAdd(a.row_sum + cur, acc);
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void k_f2d(F2 a) {
+  __shared__ float xw[4];
+  const int lane = threadIdx.x;
+  const int64_t n = a.n;
+  const int64_t e0 = (int64_t)blockIdx.x * kPElems + (int64_t)lane * 8;
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
+
+  // row (b*R + r), column (b*C + c) and batch of each element
+  int64_t ri[8], ci[8], bi[8];
+  {
+    const int64_t RC = a.R * a.C;
+    const int64_t s = e0 < n ? e0 : 0;
+    int64_t b = s / RC, r = (s - b * RC) / a.C, c = s - b * RC - r * a.C;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      ri[k] = b * a.R + r; ci[k] = b * a.C + c; bi[k] = b;
+      if (++c == a.C) { c = 0; if (++r == a.R) { r = 0; ++b; } }
+    }
+  }
+  const bool need_g = !((OP == F_CAME2N || OP == F_CAME2) && a.mq == 2);
+  float g[8];
+  if (need_g) {
+    load8<T>(reinterpret_cast<const T*>(a.grad), e0, n, g);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = scrub(g[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = 0.0f;
+  }
+
+  if constexpr (OP == F_SUMS) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = g[k] * g[k];
+    f2_rowcol_add(a, cnt, ri, ci, v);
+    return;
+  }
+
+  // x: what the momentum averages (g, or U = ((g * inv_row) * inv_col) / clip for CAME)
+  float x[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = g[k];
+  if constexpr (OP == F_CAME1 || OP == F_CAME2N || OP == F_CAME2) {
+    if (need_g) {
+      const float clip = a.clip ? *a.clip : 1.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (k < cnt) {
+          const float ir = 1.0f / sqrtf(gp(a.row)[ri[k]] / gp(a.rmean)[bi[k]]);
+          const float ic = 1.0f / sqrtf(gp(a.col)[ci[k]]);
+          x[k] = ((g[k] * ir) * ic) / clip;
+        }
+      }
+    }
+  }
+
+  // momentum
+  const int ML = (1 << a.lbm) >> 3;
+  const int64_t mb = e0 >> a.lbm;
+  const bool m_ok = a.mq == 1 && mb < ((n + (1 << a.lbm) - 1) >> a.lbm);
+  float m[8];
+  const bool fresh_m = a.mq == 1 || (a.mq == 2 && OP != F_CAME2N && OP != F_CAME2);
+  if (a.mq == 1) {
+    mq_decode8(a.mk, a.m_q, a.m_scale, e0, mb, m_ok, m);
+  } else if (a.mq == 2) {
+    load8<float>(a.m, e0, n, m);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = 0.0f;
+  }
+  if (fresh_m) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(m[k], x[k], a.w_m) : 0.0f;
+  }
+
+  if constexpr (OP == F_CAME1) {
+    float res[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float dd = x[k] - m[k];
+      res[k] = dd * dd + a.eps_came;
+    }
+    f2_rowcol_add(a, cnt, ri, ci, res);
+    if (a.mq == 2) store8<float>(a.m, e0, n, m);
+    return;
+  }
+
+  // update
+  float u[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    u[k] = 0.0f;
+    if (k < cnt) {
+      const float y = a.mq ? m[k] : x[k];
+      if constexpr (OP == F_CAME2N || OP == F_CAME2) {
+        const float icr = 1.0f / sqrtf(gp(a.crow)[ri[k]] / gp(a.crmean)[bi[k]]);
+        const float icc = 1.0f / sqrtf(gp(a.ccol)[ci[k]]);
+        u[k] = (y * icr) * icc;
+      } else {
+        const float ir = 1.0f / sqrtf(gp(a.row)[ri[k]] / gp(a.rmean)[bi[k]]);
+        const float ic = 1.0f / sqrtf(gp(a.col)[ci[k]]);
+        u[k] = (y * ir) * ic;
+      }
+    }
+  }
+  if constexpr (OP == F_NORM || OP == F_LAG || OP == F_CAME2N) {
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sq += u[k] * u[k];
+    f2_sum_add(a.norm_buf, sq);
+  }
+  if constexpr (OP == F_NOCLIP || OP == F_APPLY || OP == F_LAG || OP == F_CAME2) {
+    const float al = *a.alpha;
+    float step = al;
+    if constexpr (OP == F_APPLY) {
+      if (a.d > 0.0f) step = al / fmaxf(1.0f, sqrtf(*a.norm_buf) / a.sqrt_nd);
+    } else if constexpr (OP == F_LAG) {
+      if (a.d > 0.0f) step = al / fmaxf(1.0f, *a.prev_norm / a.sqrt_nd);
+    }
+    f2_write<T>(a, e0, cnt, step, u);
+    if (a.mq == 2 && OP != F_CAME2) store8<float>(a.m, e0, n, m);
+  }
+  const bool writes_m = OP == F_NOCLIP || OP == F_APPLY || OP == F_LAG || OP == F_CAME2;
+  if (writes_m && a.mq == 1) mq_encode8(a.mk, a.m_q, a.m_scale, e0, mb, m_ok, m, ML, xw);
+}
+
+// ============================================================ APOLLO primitives
+// Channel norms of u = m / (sqrt(v) + eps) (or m * rsqrt(max(res, eps_sq)) for
+// CAME) and of the low-rank gradient, one workgroup per channel.
+template <bool CAME>
+__global__ __launch_bounds__(256) void k_apnorm(const float* __restrict__ m, const float* __restrict__ v,
+                                                const float* __restrict__ gl, float* __restrict__ nu,
+                                                float* __restrict__ ng, int64_t N, int64_t D, int64_t sN,
+                                                int64_t sD, int64_t numel, float eps) {
+  __shared__ double sd[8];
+  const int64_t row = blockIdx.x;
+  double su = 0.0, sg = 0.0;
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    const int64_t gi = row * sN + i * sD;
+    if (CAME && gi >= numel) break;
+    float uu;
+    if constexpr (CAME) uu = gp(m)[gi] * (1.0f / sqrtf(fmaxf(gp(v)[gi], eps)));
+    else uu = gp(m)[gi] / (sqrtf(gp(v)[gi]) + eps);
+    const float gg = CAME ? scrub(gp(gl)[gi]) : gp(gl)[gi];
+    su += (double)(uu * uu);
+    sg += (double)(gg * gg);
+  }
+  su = grp_sum_d(su, 64);
+  sg = grp_sum_d(sg, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sd[wave] = su; sd[4 + wave] = sg; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    nu[row] = sqrtf((float)(sd[0] + sd[1] + sd[2] + sd[3]));
+    ng[row] = sqrtf((float)(sd[4] + sd[5] + sd[6] + sd[7]));
+  }
+}
+
+__global__ __launch_bounds__(256) void k_apcrms(const float* __restrict__ gl, const float* __restrict__ v,
+                                                float* __restrict__ out, int64_t n, float eps_sq) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  float sq = 0.0f;
+  if (i < n) {
+    const float u = scrub(gp(gl)[i]) * (1.0f / sqrtf(fmaxf(gp(v)[i], eps_sq)));
+    sq = u * u;
+  }
+  f2_sum_add(out, sq);
+}
+
+__global__ __launch_bounds__(256) void k_apres(const float* __restrict__ gl, const float* __restrict__ v,
+                                               const uint8_t* __restrict__ mq, const float* __restrict__ ms,
+                                               const float* __restrict__ res_old, float* __restrict__ m_out,
+                                               float* __restrict__ res_out, const float* __restrict__ clip,
+                                               float w1, float w3, float eps_came, float eps_sq, int64_t bs,
+                                               int64_t n, int mk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float ut = (scrub(gp(gl)[i]) * (1.0f / sqrtf(fmaxf(gp(v)[i], eps_sq)))) / *clip;
+  uint32_t c;
+  if (mk == 2 || mk == 4) {
+    const uint32_t byte = gp(mq)[i >> 1];
+    c = (i & 1) ? (byte & 0x0Fu) : (byte >> 4);
+  } else {
+    c = gp(mq)[i];
+  }
+  const float mo = m_decode(mk, c, gp(ms)[i / bs]);
+  const float mn = lerp_ref(mo, ut, w1);
+  gp(m_out)[i] = mn;
+  const float dd = ut - mn;
+  gp(res_out)[i] = fmaxf(lerp_ref(gp(res_old)[i], dd * dd + eps_came, w3), kFltMin);
+}
+
+// Writeback p <- p * decay + (g * scale) * update_scale (kernels.cu:2638-3000).
+// DET: the decayed value and the sum are each rounded to the parameter type;
+// SR: the fp32 sum is rounded with the kernels.cu:48-87 stream.  GT: the
+// gradient's element type (fp32, or the parameter's for the native forms, whose
+// gradient is scrubbed and optionally negated).
+template <typename T, typename GT, bool SR>
+__global__ __launch_bounds__(256) void k_apwb(T* __restrict__ param, const GT* __restrict__ grad,
+                                              const float* __restrict__ fs, const float* __restrict__ decay,
+                                              const float* __restrict__ us, int side_right, int is_channel,
+                                              int maximize, int native, uint64_t sr_seed, uint64_t sr_step,
+                                              int64_t R, int64_t C) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= R * C) return;
+  const int64_t r = i / C, c = i - r * C;
+  const float sc = is_channel ? gp(fs)[side_right ? r : c] : gp(fs)[0];
+  const float dec = decay ? *decay : 1.0f;
+  const float usv = *us;
+  float g = ld1<GT>(grad, i);
+  if (native) {
+    g = scrub(g);
+    if (maximize) g = -g;
+  }
+  const float p = ld1<T>(param, i);
+  if constexpr (SR) {
+    const float nw = p * dec + (g * sc) * usv;
+    param[i] = sr_round<T>(nw, sr_seed, sr_step, (uint64_t)i);
+  } else {
+    const float dcy = to_f<T>(from_f<T>(p * dec));
+    st1<T>(param, i, dcy + (usv * g) * sc);
+  }
+}
+
+hipError_t prims_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
+
+static int lb_of(int64_t bs, int lo, int hi, int& lb, const char* what) {
+  if (bs < lo || bs > hi || (bs & (bs - 1)) != 0) {
+    static char msg[128];
+    snprintf(msg, sizeof msg, "%s must be a power of two in [%d, %d]", what, lo, hi);
+    return set_error(A8_ERR_BLOCK, msg);
+  }
+  lb = 0;
+  while ((1LL << lb) < bs) ++lb;
+  return 0;
+}
+
+template <typename T>
+static void launch_f2d_t(int op, unsigned nwg, hipStream_t st, const F2& a) {
+  switch (op) {
+    case F_NOCLIP: hipLaunchKernelGGL((k_f2d<T, F_NOCLIP>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_NORM: hipLaunchKernelGGL((k_f2d<T, F_NORM>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_APPLY: hipLaunchKernelGGL((k_f2d<T, F_APPLY>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_LAG: hipLaunchKernelGGL((k_f2d<T, F_LAG>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_SUMS: hipLaunchKernelGGL((k_f2d<T, F_SUMS>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_CAME1: hipLaunchKernelGGL((k_f2d<T, F_CAME1>), dim3(nwg), dim3(256), 0, st, a); break;
+    case F_CAME2N: hipLaunchKernelGGL((k_f2d<T, F_CAME2N>), dim3(nwg), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((k_f2d<T, F_CAME2>), dim3(nwg), dim3(256), 0, st, a); break;
+  }
+}
+
+}  // namespace a8
+
+using namespace a8;
+
+extern "C" {
+
+int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, int x_dtype, float* fp32_out,
+                         double beta, int block_size, int square_input, float eps1, int64_t numel, float log_floor,
+                         int v_bits, void* stream) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (numel == 0) return 0;
+  if (!q || !scale || !min_log || !x) return set_error(A8_ERR_ARG, "null pointer");
+  if (v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
+  if (!aligned16(x) || (fp32_out && !aligned16(fp32_out)))
+    return set_error(A8_ERR_ALIGN, "new_val and fp32_out must be 16-byte aligned");
+  int lbv;
+  int rc = lb_of(block_size, 128, kPElems, lbv, "block_size");
+  if (rc) return rc;
+  const int64_t nblk = (numel + block_size - 1) / block_size;
+  const int64_t nwg = (nblk * block_size + kPElems - 1) / kPElems;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
+  hipStream_t st = (hipStream_t)stream;
+  const float w = (float)beta;
+#define A8_VEMA(VB, T)                                                                                      \
+  hipLaunchKernelGGL((k_vema<VB, T>), dim3((unsigned)nwg), dim3(256), 0, st, q, scale, min_log,             \
+                     reinterpret_cast<const T*>(x), fp32_out, numel, nblk, lbv, w, square_input, eps1, log_floor)
+  switch (x_dtype) {
+    case A8_F32: if (v_bits == 8) A8_VEMA(8, float); else A8_VEMA(16, float); break;
+    case A8_BF16: if (v_bits == 8) A8_VEMA(8, __hip_bfloat16); else A8_VEMA(16, __hip_bfloat16); break;
+    case A8_F16: if (v_bits == 8) A8_VEMA(8, __half); else A8_VEMA(16, __half); break;
+    default: return set_error(A8_ERR_DTYPE, "unsupported new_val dtype");
+  }
+#undef A8_VEMA
+  return check_launch("k_vema");
+}
+
+int a8_factored_prim(int op, int dtype, int stochastic, const a8_factored_prim_args* args, void* stream) {
+  const a8_factored_prim_args& p = *args;
+  if (op < 0 || op > 7) return set_error(A8_ERR_ARG, "op must be 0..7");
+  if (p.numel < 0 || p.rows <= 0 || p.cols <= 0) return set_error(A8_ERR_SIZE, "bad numel/rows/cols");
+  if (p.numel == 0) return 0;
+  if (p.numel % (p.rows * p.cols) != 0) return set_error(A8_ERR_SIZE, "numel must be a multiple of rows*cols");
+  F2 a{};
+  a.param = p.param; a.grad = p.grad; a.m_q = p.m_q; a.m_scale = p.m_scale; a.m = p.m;
+  a.row = p.row; a.col = p.col; a.rmean = p.row_mean; a.crow = p.conf_row; a.ccol = p.conf_col;
+  a.crmean = p.conf_row_mean; a.row_sum = p.row_sum; a.col_sum = p.col_sum; a.norm_buf = p.norm_buf;
+  a.alpha = p.alpha; a.prev_norm = p.prev_norm; a.decay = p.decay; a.clip = p.clip;
+  a.R = p.rows; a.C = p.cols; a.n = p.numel; a.sr_seed = p.sr_seed; a.sr_step = p.sr_step;
+  a.w_m = (float)(1.0 - p.beta1); a.eps_came = p.eps_came; a.d = p.d;
+  a.sqrt_nd = (float)(sqrt((double)p.numel) * (double)p.d);
+  a.sr = stochastic && dtype != A8_F32;
+  a.lbm = 5;
+  const bool writes_p = op == F_NOCLIP || op == F_APPLY || op == F_LAG || op == F_CAME2;
+  const bool uses_g = !((op == F_CAME2N || op == F_CAME2) && p.m && !p.m_q);
+  if (uses_g && !p.grad) return set_error(A8_ERR_ARG, "null grad");
+  if (writes_p && (!p.param || !p.alpha)) return set_error(A8_ERR_ARG, "null param/alpha");
+  if (op != F_SUMS && uses_g && (!p.row || !p.col || !p.row_mean)) return set_error(A8_ERR_ARG, "null row/col/row_mean");
+  if ((op == F_CAME2N || op == F_CAME2) && (!p.conf_row || !p.conf_col || !p.conf_row_mean))
+    return set_error(A8_ERR_ARG, "null confidence vectors");
+  if ((op == F_SUMS || op == F_CAME1) && (!p.row_sum || !p.col_sum)) return set_error(A8_ERR_ARG, "null row/col sums");
+  if ((op == F_NORM || op == F_LAG || op == F_CAME2N || op == F_APPLY) && !p.norm_buf)
+    return set_error(A8_ERR_ARG, "null norm_buf");
+  if (op == F_LAG && !p.prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
+  if (p.m_q && p.m) return set_error(A8_ERR_ARG, "give quantised (m_q) or fp32 (m) momentum, not both");
+  if (op == F_CAME1 || op == F_CAME2N || op == F_CAME2) {
+    if (!p.m_q && !p.m) return set_error(A8_ERR_ARG, "CAME needs momentum");
+  }
+  if (p.m_q) {
+    a.mq = 1;
+    if (!p.m_scale) return set_error(A8_ERR_ARG, "null m_scale");
+    if (p.m_bits == 8) a.mk = p.m_mode ? 3 : 1;
+    else if (p.m_bits == 4) a.mk = p.m_mode ? 4 : 2;
+    else return set_error(A8_ERR_ARG, "m_bits must be 8 or 4");
+    int rc = lb_of(p.m_block_size, 32, kPElems, a.lbm, "m_block_size");
+    if (rc) return rc;
+  } else if (p.m) {
+    a.mq = 2;
+  }
+  if ((uses_g && !aligned16(p.grad)) || (p.param && !aligned16(p.param)) || (p.m && !aligned16(p.m)) ||
+      (p.m_q && !aligned16(p.m_q)))
+    return set_error(A8_ERR_ALIGN, "param, grad and momentum must be 16-byte aligned");
+  const int64_t nwg = (p.numel + kPElems - 1) / kPElems;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case A8_F32: launch_f2d_t<float>(op, (unsigned)nwg, st, a); break;
+    case A8_BF16: launch_f2d_t<__hip_bfloat16>(op, (unsigned)nwg, st, a); break;
+    case A8_F16: launch_f2d_t<__half>(op, (unsigned)nwg, st, a); break;
+    default: return set_error(A8_ERR_DTYPE, "unsupported dtype");
+  }
+  return check_launch("k_f2d");
+}
+
+int a8_apollo_norms(const float* m, const float* v, const float* grad_low, float* norm_update, float* norm_grad,
+                    int64_t n_channels, int64_t d, int64_t stride_n, int64_t stride_d, int64_t numel, float eps,
+                    int came, void* stream) {
+  if (n_channels < 0 || d < 0) return set_error(A8_ERR_SIZE, "bad sizes");
+  if (n_channels == 0) return 0;
+  if (!m || !v || !grad_low || !norm_update || !norm_grad) return set_error(A8_ERR_ARG, "null pointer");
+  if (n_channels > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many channels");
+  hipStream_t st = (hipStream_t)stream;
+  if (came)
+    hipLaunchKernelGGL(k_apnorm<true>, dim3((unsigned)n_channels), dim3(256), 0, st, m, v, grad_low, norm_update,
+                       norm_grad, n_channels, d, stride_n, stride_d, numel, eps);
+  else
+    hipLaunchKernelGGL(k_apnorm<false>, dim3((unsigned)n_channels), dim3(256), 0, st, m, v, grad_low, norm_update,
+                       norm_grad, n_channels, d, stride_n, stride_d, numel, eps);
+  return check_launch("k_apnorm");
+}
+
+int a8_apollo_came_rms(const float* grad_low, const float* v, float* sum_u2, float eps_sq, int64_t numel,
+                       void* stream) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (numel == 0) return 0;
+  if (!grad_low || !v || !sum_u2) return set_error(A8_ERR_ARG, "null pointer");
+  const int64_t nwg = (numel + 255) / 256;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
+  hipLaunchKernelGGL(k_apcrms, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream, grad_low, v, sum_u2, numel,
+                     eps_sq);
+  return check_launch("k_apcrms");
+}
+
+int a8_apollo_came_m_res(const float* grad_low, const float* v, const uint8_t* m_q_old, const float* m_scale_old,
+                         const float* res_old, float* m_out, float* res_out, const float* clip_factor, double beta1,
+                         double beta3, float eps_came, float eps_sq, int m_block_size, int64_t numel, int m_bits,
+                         int m_mode, void* stream) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (numel == 0) return 0;
+  if (!grad_low || !v || !m_q_old || !m_scale_old || !res_old || !m_out || !res_out || !clip_factor)
+    return set_error(A8_ERR_ARG, "null pointer");
+  if (m_block_size <= 0) return set_error(A8_ERR_BLOCK, "m_block_size must be positive");
+  int mk;
+  if (m_bits == 8) mk = m_mode ? 3 : 1;
+  else if (m_bits == 4) mk = m_mode ? 4 : 2;
+  else return set_error(A8_ERR_ARG, "m_bits must be 8 or 4");
+  const int64_t nwg = (numel + 255) / 256;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
+  hipLaunchKernelGGL(k_apres, dim3((unsigned)nwg), dim3(256), 0, (hipStream_t)stream, grad_low, v, m_q_old,
+                     m_scale_old, res_old, m_out, res_out, clip_factor, (float)(1.0 - beta1), (float)(1.0 - beta3),
+                     eps_came, eps_sq, (int64_t)m_block_size, numel, mk);
+  return check_launch("k_apres");
+}
+
+int a8_apollo_writeback(int dtype, int grad_native, int stochastic, void* param, const void* grad,
+                        const float* final_scale, const float* decay, const float* update_scale, int side_right,
+                        int is_channel, int maximize, uint64_t sr_seed, uint64_t sr_step, int64_t rows, int64_t cols,
+                        void* stream) {
+  if (rows < 0 || cols < 0) return set_error(A8_ERR_SIZE, "bad shape");
+  if (rows == 0 || cols == 0) return 0;
+  if (!param || !grad || !final_scale || !update_scale) return set_error(A8_ERR_ARG, "null pointer");
+  const int64_t nwg = (rows * cols + 255) / 256;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "tensor too large");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)nwg), blk(256);
+#define A8_APWB(T, GT, SR)                                                                                  \
+  hipLaunchKernelGGL((k_apwb<T, GT, SR>), grid, blk, 0, st, reinterpret_cast<T*>(param),                    \
+                     reinterpret_cast<const GT*>(grad), final_scale, decay, update_scale, side_right,          \
+                     is_channel, maximize, grad_native, sr_seed, sr_step, rows, cols)
+  if (dtype == A8_BF16) {
+    if (grad_native) { if (stochastic) A8_APWB(__hip_bfloat16, __hip_bfloat16, true); else A8_APWB(__hip_bfloat16, __hip_bfloat16, false); }
+    else { if (stochastic) A8_APWB(__hip_bfloat16, float, true); else A8_APWB(__hip_bfloat16, float, false); }
+  } else if (dtype == A8_F16) {
+    if (grad_native) { if (stochastic) A8_APWB(__half, __half, true); else A8_APWB(__half, __half, false); }
+    else { if (stochastic) A8_APWB(__half, float, true); else A8_APWB(__half, float, false); }
+  } else {
+    return set_error(A8_ERR_DTYPE, "param must be bfloat16 or float16");
+  }
+#undef A8_APWB
+  return check_launch("k_apwb");
+}
+
+}  // extern "C"

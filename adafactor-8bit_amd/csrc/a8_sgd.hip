@@ -91,23 +91,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
   const bool m_ok = MK == 1 && mb < nmb;   // codes are padded to whole blocks
   if constexpr (MK == 1) {
     float mo[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) mo[k] = 0.0f;
-    if (m_ok) {
-      const float ms = gp(D.m_scale)[mb];
-      if (h.mk == 2 || h.mk == 4) {
-        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
-          mo[k] = m_decode(h.mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
-        }
-      } else {
-        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
-#pragma unroll
-        for (int k = 0; k < 8; ++k) mo[k] = m_decode(h.mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
-      }
-    }
+    mq_decode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, mo);
 #pragma unroll
     for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
   } else if constexpr (MK == 2) {
@@ -168,41 +152,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
   if constexpr (MODE == 3) {
     if (D.m_out) store8<float>(D.m_out, e0, n, m);
   }
-  if constexpr (MODE != 1 && MK == 1) {
-    uint32_t ab = 0u;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) ab = max(ab, __float_as_uint(m[k]) & 0x7FFFFFFFu);
-    float bam = grp_max(__uint_as_float(ab), ML < 64 ? ML : 64);
-    if (ML > 64) {
-      if ((lane & 63) == 0) xw[wave] = bam;
-      __syncthreads();
-      const int wpb = ML >> 6, w0 = (wave / wpb) * wpb;
-      bam = xw[w0];
-      for (int ww = 1; ww < wpb; ++ww) bam = fmaxf(bam, xw[w0 + ww]);
-    }
-    if (m_ok) {
-      const float am = fmaxf(bam, 1e-12f);
-      const float ram = fast_rcp(am);
-      if (h.mk == 2 || h.mk == 4) {
-        uint32_t wq = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t hi4 = m_encode(h.mk, m[2 * j], am, ram);
-          const uint32_t lo4 = m_encode(h.mk, m[2 * j + 1], am, ram);
-          wq |= ((hi4 << 4) | lo4) << (8 * j);
-        }
-        *gp(reinterpret_cast<uint32_t*>(D.m_q + (e0 >> 1))) = wq;
-      } else {
-        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) w0 |= m_encode(h.mk, m[k], am, ram) << (8 * k);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) w1 |= m_encode(h.mk, m[k + 4], am, ram) << (8 * k);
-        *gp(reinterpret_cast<u32x2*>(D.m_q + e0)) = u32x2{w0, w1};
-      }
-      if ((lane & (ML - 1)) == 0) gp(D.m_scale)[mb] = am;
-    }
-  }
+  if constexpr (MODE != 1 && MK == 1) mq_encode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, m, ML, xw);
 }
 
 template <typename T, int MK, bool SR>

@@ -870,7 +870,8 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host) {
       a8::factored_upload_qmap(qmap8_host, qmap4_host) != hipSuccess ||
       a8::apollo_upload_qmap(qmap8_host, qmap4_host) != hipSuccess ||
       a8::decode_upload_qmap(qmap8_host, qmap4_host) != hipSuccess ||
-      a8::sgd_upload_qmap(qmap8_host, qmap4_host) != hipSuccess)
+      a8::sgd_upload_qmap(qmap8_host, qmap4_host) != hipSuccess ||
+      a8::prims_upload_qmap(qmap8_host, qmap4_host) != hipSuccess)
     return set_error(A8_ERR_HIP, "codebook upload failed");
   return 0;
 }

@@ -369,6 +369,115 @@ int64_t a8_table_bytes_sgd(int ntensors);
 int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype, float* fp32_out, double beta,
                        int block_size, int64_t numel, int m_bits, int m_mode, void* stream);
 
+/* ---- Stand-alone primitives of the reference's module.  The reference's
+ * optimizer runs its factored, CAME and APOLLO steps as sequences of these; this
+ * library's own optimizer uses the fused entry points above instead.  Each keeps
+ * the arithmetic of the reference's PyTorch twin where one exists. */
+
+/* Replaces fused_log_quantize_lerp (kernels.cu:340-520; called by _fused_v_ema,
+ * optimizer.py:677-685) with the arithmetic of its twin _deq_v -> lerp_ -> _quant_v
+ * (optimizer.py:2232-2238): x = square_input ? x*x + eps1 : x (non-finite read as
+ * 0); v' = lerp(deq(v), x, beta); per block of block_size (a power of two in
+ * [128, 2048]) the AL range is refit from the non-zero v' with floor log_floor;
+ * fp32_out (optional) receives v'.  Codes past numel in the last block become 0.
+ * q: uint8 (v_bits 8) or int16 (v_bits 16) codes padded to whole blocks. */
+int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, int x_dtype, float* fp32_out,
+                         double beta, int block_size, int square_input, float eps1, int64_t numel, float log_floor,
+                         int v_bits, void* stream);
+
+/* Arguments of a8_factored_prim; a pointer an op does not use may be null.
+ * row, col: the row and column second moments (index b*rows + r, b*cols + c);
+ * row_mean: their per-matrix row mean (index b); conf_*: CAME confidence
+ * statistics in the same layout. */
+typedef struct a8_factored_prim_args {
+  void* param;
+  const void* grad;
+  uint8_t* m_q;
+  float* m_scale;
+  float* m;
+  const float* row;
+  const float* col;
+  const float* row_mean;
+  const float* conf_row;
+  const float* conf_col;
+  const float* conf_row_mean;
+  float* row_sum;
+  float* col_sum;
+  float* norm_buf;
+  const float* alpha;
+  const float* prev_norm;
+  const float* decay;
+  const float* clip;
+  int64_t rows;
+  int64_t cols;
+  int64_t numel;
+  double beta1;
+  float eps_came;
+  float d;
+  int m_bits;
+  int m_mode;
+  int m_block_size;
+  uint64_t sr_seed;
+  uint64_t sr_step;
+} a8_factored_prim_args;
+
+/* Factored element primitives over a (batch of) rows x cols matrices, with
+ * inv_row = 1/sqrt(row/row_mean), inv_col = 1/sqrt(col) per element:
+ *   op 0-3  fused_update_2d[_full]_{noclip,norm,apply,lag}[_sr] (kernels.cu:1523-1920;
+ *           twin optimizer.py:958-970): x = lerp(m, g, 1-beta1) (m: m_q codes or fp32
+ *           m, updated in place except by norm) or g; u = (x*inv_row)*inv_col;
+ *           norm and lag add sum(u^2) to *norm_buf; apply divides the step by
+ *           max(1, sqrt(*norm_buf)/(sqrt(numel) d)) and lag by
+ *           max(1, *prev_norm/(sqrt(numel) d)) when d > 0; p = fma(-step, u, p)
+ *           (stochastic: SR of fma(-step, u, p*decay)).  op 1 without momentum is
+ *           compute_ut_rms (kernels.cu:1962-1999).
+ *   op 4    compute_factored_sums (kernels.cu:1925-1956): row_sum[b*rows+r] and
+ *           col_sum[b*cols+c] += g^2 (accumulated with atomics, as the reference).
+ *   op 5    fused_came_pass1 / fused_came_full_pass1 (kernels.cu:2003-2094; twin
+ *           optimizer.py:929-934): U = ((g*inv_row)*inv_col)/ *clip,
+ *           M' = lerp(M, U, 1-beta1), res = (U-M')^2 + eps_came added to
+ *           row_sum/col_sum; fp32 m is updated, codes are not.
+ *   op 6, 7 fused_came_pass2_norm / fused_came_pass2[_sr] and fused_came_full_pass2
+ *           (kernels.cu:2097-2221; twin optimizer.py:950-956): M' recomputed from
+ *           the codes and U (or the fp32 m as pass 1 left it); u = (M'*inv_crow)*inv_ccol
+ *           with the confidence factors; op 6 adds sum(u^2) to *norm_buf, op 7
+ *           writes p = fma(-alpha, u, p) and the codes.
+ * Non-finite gradients are read as 0. */
+int a8_factored_prim(int op, int dtype, int stochastic, const a8_factored_prim_args* args, void* stream);
+
+/* Replaces compute_apollo_norms (kernels.cu:2410-2455; came = 0:
+ * u = m/(sqrt(v)+eps)) and apollo_came_compute_update_norms (kernels.cu:2520-2560;
+ * came = 1: u = m/sqrt(max(v, eps)), elements at index >= numel skipped, gradient
+ * non-finite read as 0): norm_update[c] = ||u||, norm_grad[c] = ||grad_low|| over
+ * element c*stride_n + i*stride_d, i < d (sums in double). */
+int a8_apollo_norms(const float* m, const float* v, const float* grad_low, float* norm_update, float* norm_grad,
+                    int64_t n_channels, int64_t d, int64_t stride_n, int64_t stride_d, int64_t numel, float eps,
+                    int came, void* stream);
+
+/* Replaces compute_apollo_came_rms (kernels.cu:2457-2478): *sum_u2 +=
+ * sum((g / sqrt(max(v, eps_sq)))^2), non-finite g read as 0. */
+int a8_apollo_came_rms(const float* grad_low, const float* v, float* sum_u2, float eps_sq, int64_t numel,
+                       void* stream);
+
+/* Replaces apollo_came_compute_m_res (kernels.cu:2480-2518):
+ * U = (g / sqrt(max(v, eps_sq))) / *clip_factor; m_out = lerp(deq(m_q_old), U, 1-beta1);
+ * res_out = max(lerp(res_old, (U - m_out)^2 + eps_came, 1-beta3), FLT_MIN). */
+int a8_apollo_came_m_res(const float* grad_low, const float* v, const uint8_t* m_q_old, const float* m_scale_old,
+                         const float* res_old, float* m_out, float* res_out, const float* clip_factor, double beta1,
+                         double beta3, float eps_came, float eps_sq, int m_block_size, int64_t numel, int m_bits,
+                         int m_mode, void* stream);
+
+/* Replaces apollo_apply_{bf16_det,bf16_sr,fp16_sr} (grad fp32, grad_native = 0) and
+ * apollo_apply_{bf16,fp16}_{det,sr}_native (grad of the param's type, scrubbed and
+ * negated when maximize; grad_native = 1) (kernels.cu:2638-3000) on a rows x cols
+ * bf16/fp16 param: s = final_scale[row] (side_right), [col], or [0] (tensor scale);
+ * deterministic: p = rn(rn(p*decay) + (update_scale*g)*s); stochastic: the
+ * kernels.cu:48-87 rounding of p*decay + (g*s)*update_scale.  decay may be null. */
+int a8_apollo_writeback(int dtype, int grad_native, int stochastic, void* param, const void* grad,
+                        const float* final_scale, const float* decay, const float* update_scale, int side_right,
+                        int is_channel, int maximize, uint64_t sr_seed, uint64_t sr_step, int64_t rows, int64_t cols,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,3 +64,4 @@ def test_module_signatures_match_reference():
     for name in K.__all__:
         assert name in ref, name
         assert list(inspect.signature(getattr(K, name)).parameters) == ref[name], name
+    assert sorted(set(ref) - {"qmaps"}) == sorted(set(K.__all__)), sorted(set(ref) ^ set(K.__all__))

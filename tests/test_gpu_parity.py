@@ -169,3 +169,40 @@ def test_multi_tensor_equals_single():
         for k, v in oa.state[x].items():
             if torch.is_tensor(v):
                 assert torch.equal(v, ob.state[y][k]), k
+
+
+FP16_PATHS = [
+    ("adamw_q1d", dict(ADAMW, lr=1e-3), [(33, 517)]),
+    ("adamw_fp32_state", dict(ADAMW, lr=1e-3), [(300,)]),
+    ("adafactor_factored", dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=True, relative_step=False,
+                                lr=1e-3, scale_parameter=False), [(64, 300)]),
+    ("sgd_uf8", dict(beta1=0.9, beta2=None, beta2_decay=None, factored=False, relative_step=False,
+                     scale_parameter=False, d=0.0, lr=1e-2), [(33, 517)]),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw,shapes", FP16_PATHS, ids=[c[0] for c in FP16_PATHS])
+def test_fp16_deterministic_writeback_rounds_the_fp32_value(name, kw, shapes):
+    """A deterministic fp16 write is the fp16 rounding of the fp32 value the
+    update computes (fp32 first, then fp16, as the reference's kernels and its
+    PyTorch path round).  A float32 twin stepped from the same values gives
+    that fp32 value; both must agree bit for bit."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[fp16 writeback] {name}", flush=True)
+    ph = [torch.nn.Parameter(make_param(s, i, 2).to(torch.float16).cuda()) for i, s in enumerate(shapes)]
+    pf = [torch.nn.Parameter(p.detach().float()) for p in ph]
+    oh, of = Adafactor8Bit(ph, **kw), Adafactor8Bit(pf, **kw)
+    for t in range(1, 4):
+        with torch.no_grad():
+            for a, b in zip(pf, ph):
+                a.copy_(b.float())
+        for i, (a, b) in enumerate(zip(pf, ph)):
+            g = make_grad(tuple(a.shape), i, t, 2).to(torch.float16)
+            b.grad, a.grad = g.cuda(), g.float().cuda()
+        oh.step()
+        of.step()
+        torch.cuda.synchronize()
+        for a, b in zip(pf, ph):
+            want = a.detach().to(torch.float16)
+            assert torch.equal(b.detach(), want), f"step {t}: {int((b.detach() != want).sum())} differ"

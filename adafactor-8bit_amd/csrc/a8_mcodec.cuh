@@ -93,7 +93,7 @@ __device__ __forceinline__ uint16_t sr_fp16(float x, float u) {
   uint16_t sign = (b & 0x80000000u) ? 0x8000u : 0u;
   if ((b & 0x7F800000u) == 0x7F800000u) return (b & 0x007FFFFFu) ? (sign | 0x7E00u) : (sign | 0x7C00u);
   if (fabsf(x) > 65504.0f) return sign | 0x7BFFu;
-  __half nh = __float2half_rn(x);
+  __half nh = __float2half_rn(f32_value(x));
   uint16_t qb = __half_as_ushort(nh);
   float q = __half2float(nh);
   if (q == x) return qb;

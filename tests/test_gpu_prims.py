@@ -10,7 +10,9 @@ momentum EMA and its codes, and the parameter fma are the same fp32 operations
 on both sides: parameters and momentum are bit-exact.  With d > 0 the step
 depends on a norm reduced in a different order: rtol 1e-6.  CAME's confidence
 statistics are row/column means of the residual, reduced with atomics here and by
-torch.mean there (an ulp apart), so its parameters are held to rtol 1e-5.
+torch.mean there (an ulp apart), so its parameters are held to rtol 1e-5 plus
+1e-5 of the largest displacement (an element near zero keeps the absolute error
+of its update).
 
 The V EMA is compared with the oracle's _deq_v -> lerp -> _quant_v; the oracle
 decodes with torch.pow (not correctly rounded) where the kernel decodes exactly,
@@ -205,6 +207,7 @@ def test_came_chain_matches_fallback(mom, d):
     init_m(st, n, (B, R, C), mbs, mom, True)
     st["conf_row"] = torch.zeros(B, R, 1)
     st["conf_col"] = torch.zeros(B, 1, C)
+    p_init = p.clone()
     pg = p.clone().cuda()
     mq = st.get("m_q")
     stg = {k: v.clone().cuda() for k, v in st.items() if torch.is_tensor(v)}
@@ -238,7 +241,9 @@ def test_came_chain_matches_fallback(mom, d):
         else:
             K.fused_came_full_pass2(pg.view(-1), stg["m"].view(-1), cr, cc, crm, None, a_t, R, C, n, mbs, False)
     torch.cuda.synchronize()
-    np.testing.assert_allclose(pg.cpu().numpy(), p.numpy(), rtol=1e-5, atol=1e-9)
+    # an ulp of a confidence statistic moves an element's update by ~1e-7 of itself
+    disp = float((p - p_init).abs().max())
+    np.testing.assert_allclose(pg.cpu().numpy(), p.numpy(), rtol=1e-5, atol=1e-5 * disp)
     for k in ("conf_row", "conf_col"):
         np.testing.assert_allclose(stg[k].cpu().numpy(), st[k].numpy(), rtol=1e-5, atol=1e-30)
     if d == 0.0:   # the momentum depends on U only: exact without a clip
@@ -324,7 +329,8 @@ def test_apollo_came_rms_and_m_res(mqt):
                                 0.999, 1e-16, 1e-30, bs, n, m_bits_of(mqt), int(mqt.startswith("d")))
     torch.cuda.synchronize()
     gs = torch.nan_to_num(g, nan=0.0)
-    inv = 1.0 / v.clamp(min=1e-30).sqrt()
+    # correctly rounded 1/sqrt (torch's CPU reciprocal is not correctly rounded)
+    inv = torch.from_numpy(np.float32(1.0) / np.sqrt(np.maximum(v.numpy(), np.float32(1e-30))))
     np.testing.assert_allclose(acc.item(), float((gs * inv).double().square().sum()), rtol=1e-5)
     ut = (gs * inv) / clip
     mo = m_dequantize(q, s, n, bs, mqt)
@@ -385,4 +391,6 @@ def test_apollo_writeback(dt, native, sr, scale_kind):
             assert bool(((got == lo) | (got == other)).all())
     else:
         want = ((pf * dec).to(dt).float() + (us * gf) * sc).to(dt)
-        assert torch.equal(pg.cpu(), want), int((pg.cpu() != want).sum())
+        bad = (pg.cpu() != want).reshape(-1).nonzero().reshape(-1)[:6]
+        assert bad.numel() == 0, [(float(p.reshape(-1)[i]), float(gf.reshape(-1)[i]), float(pg.cpu().reshape(-1)[i]),
+                                   float(want.reshape(-1)[i])) for i in bad]

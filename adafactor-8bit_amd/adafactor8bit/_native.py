@@ -36,7 +36,7 @@ class TensorFull(ctypes.Structure):
     """Mirror of ``a8_tensor_full``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("variance", _c_vp), ("m", _c_vp),
                 ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("psq", _c_vp), ("fira_scale", _c_vp)]
 
 
 class TensorSgd(ctypes.Structure):
@@ -97,7 +97,8 @@ _SIGS = {
                                        _c_f, _c_f, _c_i, _c_i, _c_u64, _c_u64, _c_vp]),
     "a8_fused_update_1d_full_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(TensorFull), _c_i, _c_vp,
                                              _c_i64, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_f, _c_i,
-                                             _c_f, _c_f, _c_i, _c_i, _c_u64, _c_i, _c_vp]),
+                                             _c_f, _c_f, _c_i, _c_i, _c_u64, _c_i, _c_f, _c_i, _c_f,
+                                             _c_i, _c_vp]),
     "a8_table_bytes_full": (_c_i64, [_c_i]),
     "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_factored_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(Tensor2D), _c_i, _c_vp, _c_i64, _c_i, _c_d,

@@ -14,6 +14,7 @@ Parameters that share a step counter and hyper-parameters are updated by one
 multi-tensor launch per group instead of one launch per parameter.
 """
 import ctypes
+import gc
 import logging
 import math
 from typing import Any, Dict, Iterable, Optional, Tuple, Union
@@ -282,6 +283,22 @@ class Adafactor8Bit(Optimizer):
         if not hasattr(self, "_allocator_warmed_up"):
             self._warmup_allocator()
             self._allocator_warmed_up = True
+        # A step plans every parameter on the host and holds those temporaries until
+        # its launches are queued.  A cyclic collection running meanwhile would move
+        # them to the oldest generation, whose full pass (tens of ms with torch
+        # loaded) then stalls the launch stream; with automatic collection held off
+        # for the step they are freed by reference counting first.
+        gc_on = gc.isenabled()
+        if gc_on:
+            gc.disable()
+        try:
+            self._step_groups()
+        finally:
+            if gc_on:
+                gc.enable()
+        return loss
+
+    def _step_groups(self):
         for group in self.param_groups:
             params, grads, states = [], [], []
             self._init_group(group, params, grads, states)
@@ -298,7 +315,6 @@ class Adafactor8Bit(Optimizer):
                     st["sr_seed"] = self._sr_seed_counter
                     self._sr_seed_counter += 1
             self._step_group(group, params, grads, states)
-        return loss
 
     # ------------------------------------------------------------------ dispatch
     def _step_group(self, group, params, grads, states):
@@ -329,7 +345,7 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd")
 
     def batch_key(self):
         if self.path == "factored":
@@ -339,9 +355,16 @@ class _Plan:
             return None
         if self.alpha_t is not None or self.decay_t is not None:
             return None
-        if self.d > 0 or self.fira or self.maximize:
+        if self.maximize or self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
-        if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
+        if self.path == "f1d" and (self.d > 0 or self.fira or self.rms_kernel):
+            if self.lag:
+                return None
+            return ("f1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m,
+                    self.beta1, self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
+                    self.alpha_val, self.decay_val, self.kwd, self.group["weight_decay"], self.d, self.fira,
+                    self.margin, self.rms_kernel, self.eps2)
+        if self.d > 0 or self.fira:
             return None
         if self.path == "sgd":
             mq = self.has_m and self.quant and self.mqt != "fp32" and "m_q" in self.st
@@ -425,7 +448,16 @@ def _plan_param(p, grad, st, group) -> _Plan:
         P.rho_t, P.rho_val = rho_t, None
     else:
         P.rho_val = _f32(min(lr, 1.0 / math.sqrt(step)) if relative_step else lr)
-    if scale_parameter:
+    bc_applies = beta1 is not None and not relative_step and not sgd and bool(
+        P.adam_denom if group.get("bias_correction") is None else group.get("bias_correction"))
+    # fp32-state vectors can take alpha = max(rms(p), eps2) * rho inside the batched
+    # kernels (one pass computes sum(p^2)); _materialize_alpha computes it here when
+    # the plan runs on its own.
+    P.rms_kernel = bool(scale_parameter and P.path == "f1d" and P.rho_t is None and not bc_applies)
+    P.kwd = 0
+    if P.rms_kernel:
+        P.alpha_t, P.alpha_val = None, P.rho_val
+    elif scale_parameter:
         rms = torch.linalg.vector_norm(p, ord=2, dtype=torch.float32) / math.sqrt(p.numel())
         rho = P.rho_t if P.rho_t is not None else P.rho_val
         P.alpha_t = torch.clamp(rms, min=eps2) * rho
@@ -458,7 +490,9 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P.decay_val, P.decay_t = None, None
     if wd != 0:
         use_alpha = group.get("scale_weight_decay", True)
-        if use_alpha:
+        if use_alpha and P.rms_kernel:
+            P.kwd = 1   # 1 - alpha*wd with the kernel's alpha
+        elif use_alpha:
             if P.alpha_t is not None:
                 P.decay_t = 1.0 - (P.alpha_t * wd)
             else:
@@ -678,7 +712,21 @@ def _run_sgd(opt, P):
     launch(nat.MODE_APPLY, norm_buf=nb, fira=fira)
 
 
+def _materialize_alpha(P):
+    """alpha (and its weight decay) of a plan that deferred them to the batched
+    kernels, computed as _compute_alpha does (optimizer.py:851-855, 2032-2039)."""
+    if not P.rms_kernel:
+        return
+    rms = torch.linalg.vector_norm(P.p, ord=2, dtype=torch.float32) / math.sqrt(P.p.numel())
+    P.alpha_t = torch.clamp(rms, min=P.eps2) * P.rho_val
+    P.alpha_val = None
+    if P.kwd:
+        P.decay_t = 1.0 - (P.alpha_t * P.group["weight_decay"])
+    P.rms_kernel, P.kwd = False, 0
+
+
 def _run_single(opt, P):
+    _materialize_alpha(P)
     if P.path == "factored":
         _run_factored(opt, [P])
         return
@@ -722,6 +770,99 @@ def _run_single(opt, P):
     _launch_1d(opt, P, nat.MODE_APPLY, alpha_t, alpha_val, norm_buf=nb, v_buf=vb)
 
 
+def _run_batch_f1dc(opt, key, plans):
+    """fp32-state vectors with an RMS clip, Fira or scale_parameter as one group:
+    NORM (sum u^2, and sum p^2 for scale_parameter) -> MNORM (momentum-only Fira)
+    -> Fira scalar over all tensors -> APPLY, each one launch (the per-tensor
+    sequence of _run_single, optimizer.py:1048-1077, 785-793)."""
+    P0 = plans[0]
+    dev = P0.p.device
+    L = nat.lib()
+    n = len(plans)
+    fira = bool(P0.fira)
+    mnorm = fira and P0.has_m and P0.mom_only
+    for pl in plans:
+        if pl.has_m and not pl.st["m"].is_contiguous():
+            pl.st["m"] = pl.st["m"].contiguous()
+        if not pl.st["variance"].is_contiguous():
+            pl.st["variance"] = pl.st["variance"].contiguous()
+    ws = opt._ws.setdefault((dev, "f1dc"), {})
+    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr()) for pl in plans), P0.sr, P0.has_m, fira, mnorm,
+          P0.rms_kernel)
+    refs = [tuple(v.data_ptr() for k, v in pl.st.items() if torch.is_tensor(v) and k != "fira_prev_norm")
+            for pl in plans]
+    ent = ws.get(ck)
+    if ent is None or ent["refs"] != refs:
+        acc = torch.zeros(3 * n, dtype=torch.float32, device=dev)    # sum u^2 | sum M'^2 | sum p^2
+        fout = torch.zeros(3 * n, dtype=torch.float32, device=dev)   # Fira: scale | prev norm | clean sum
+        a0, f0 = acc.data_ptr(), fout.data_ptr()
+        arrs = {}
+        for mode in (nat.MODE_NORM, nat.MODE_MNORM, nat.MODE_APPLY):
+            if mode == nat.MODE_MNORM and not mnorm:
+                continue
+            arr = (nat.TensorFull * n)()
+            for i, pl in enumerate(plans):
+                st = pl.st
+                nb = a0 + 4 * i
+                psq = a0 + 4 * (2 * n + i) if pl.rms_kernel else None
+                prev = None
+                if mode == nat.MODE_MNORM:
+                    nb, prev = a0 + 4 * (n + i), a0 + 4 * i
+                elif mode == nat.MODE_APPLY and fira and not mnorm:
+                    nb = f0 + 4 * (2 * n + i)
+                fs = f0 + 4 * i if (mode == nat.MODE_APPLY and fira) else None
+                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), st["variance"].data_ptr(),
+                                        nat.ptr(st.get("m") if pl.has_m else None), nb, None, prev, None,
+                                        pl.p.numel(), int(st.get("sr_seed", 0)), psq, fs)
+            arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_full(n)), dtype=torch.uint8, device=dev), 1]
+        ent = {"refs": refs, "acc": acc, "fout": fout, "arrs": arrs}
+        if len(ws) > 16:
+            ws.clear()
+        ws[ck] = ent
+    acc, fout = ent["acc"], ent["fout"]
+    strm = nat.stream_of(dev)
+    has_dec = int(P0.decay_val is not None)
+    dec_val = P0.decay_val if has_dec else 1.0
+
+    def launch(mode):
+        arr, table, up = ent["arrs"][mode]
+        rc = L.a8_fused_update_1d_full_multi(
+            mode, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), table.numel(),
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom), P0.eps_g, P0.d,
+            int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr), int(P0.step),
+            int(P0.rms_kernel), _f32(P0.eps2), int(P0.kwd), _f32(P0.group["weight_decay"]), up, strm)
+        nat.check(rc, "a8_fused_update_1d_full_multi")
+        ent["arrs"][mode][2] = 0
+
+    acc.zero_()
+    launch(nat.MODE_NORM)
+    if mnorm:
+        launch(nat.MODE_MNORM)
+    if fira:
+        # A tensor without a previous norm behaves as one whose previous norm is
+        # below 1e-6 (scale 1, next = current), so every slot takes has_prev = 1.
+        prev_ok = True
+        for i, pl in enumerate(plans):
+            pv = pl.st.get("fira_prev_norm")
+            if not (torch.is_tensor(pv) and pv.data_ptr() == fout.data_ptr() + 4 * (n + i)):
+                prev_ok = False
+        if not prev_ok:
+            vals = []
+            for pl in plans:
+                pv = pl.st.get("fira_prev_norm")
+                vals.append(torch.zeros((), dtype=torch.float32, device=dev) if pv is None else
+                            torch.as_tensor(pv, dtype=torch.float32).to(dev).reshape(()))
+            fout[n:2 * n].copy_(torch.stack(vals))
+        x = acc[n:2 * n] if mnorm else acc[0:n]
+        rc = L.a8_fira_scalar(x.data_ptr(), fout.data_ptr() + 4 * n, None, fout.data_ptr(), n, 1, 2,
+                              _f32(1.0 + P0.margin), strm)
+        nat.check(rc, "a8_fira_scalar")
+        if not prev_ok:
+            for i, pl in enumerate(plans):
+                pl.st["fira_prev_norm"] = fout[n + i].view(())
+    launch(nat.MODE_APPLY)
+
+
 def _run_batch(opt, key, plans):
     path = key[0]
     if path == "factored":
@@ -730,12 +871,17 @@ def _run_batch(opt, key, plans):
     if len(plans) == 1:
         _run_single(opt, plans[0])
         return
+    if path == "f1dc":
+        _run_batch_f1dc(opt, key, plans)
+        return
     P0 = plans[0]
     dev = P0.p.device
     L = nat.lib()
     n = len(plans)
     ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr()) for pl in plans)
-    cache_key = (key, ptrs)
+    # The table holds only pointers, sizes and seeds; step-dependent scalars go
+    # to the launch, so one upload serves every later step.
+    cache_key = (path, dev, key[5], ptrs)   # key[5]: stochastic rounding (seeds in the table)
     ws = opt._ws.setdefault((dev, "tables"), {})
     ent = ws.get(cache_key)
     upload = 0
@@ -791,7 +937,8 @@ def _run_batch(opt, key, plans):
             S.m_mode(P0.mqt) if kind == 1 else 0, P0.mbs if kind == 1 else 32, P0.d, float(P0.alpha_val),
             float(dec_val), has_dec, int(P0.step), upload, strm)
         nat.check(rc, "a8_sgd_step_multi")
-        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+        if upload:
+            ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
     elif path == "q1d":
         rc = L.a8_fused_update_1d_multi(
             nat.MODE_NOCLIP, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
@@ -803,15 +950,17 @@ def _run_batch(opt, key, plans):
         nat.check(rc, "a8_fused_update_1d_multi")
         for pl in plans:
             _block_view(pl.st, "variance", pl.bs)
-        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+        if upload:
+            ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
     else:
         rc = L.a8_fused_update_1d_full_multi(
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom),
             P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr),
-            int(P0.step), upload, strm)
+            int(P0.step), 0, 0.0, 0, 0.0, upload, strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
-        ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
+        if upload:
+            ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
 
 
 def _apollo_proj(st, shape, step, device, cache):

@@ -31,6 +31,10 @@ inline int check_launch(const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Host-to-device copy of a descriptor table on stream st that does not wait for
+// earlier work on the stream (staged through pinned host memory).
+hipError_t upload_table(void* dst, const void* src, size_t bytes, hipStream_t st);
+
 }  // namespace a8
 
 namespace a8 {

@@ -1298,7 +1298,7 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
     std::vector<char> blob((size_t)table_bytes(n));
     std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
     std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 5 * (size_t)n);
-    if (hipMemcpyAsync(table_dev, blob.data(), blob.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+    if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
     dtab = reinterpret_cast<const ApDesc*>(table_dev);
   }

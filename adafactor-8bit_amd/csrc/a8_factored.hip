@@ -1189,8 +1189,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (tiles > 0x7FFFFFFF || units > 0x7FFFFFFF || fblks > 0x7FFFFFFF)
     return set_error(A8_ERR_SIZE, "too many workgroups");
   hipStream_t st = (hipStream_t)stream;
-  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(DescF) * (size_t)ntensors,
-                               hipMemcpyHostToDevice, st) != hipSuccess)
+  if (upload && upload_table(table_dev, tab.data(), sizeof(DescF) * (size_t)ntensors, st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   HyperF h{};
   h.bv = (float)beta_val;

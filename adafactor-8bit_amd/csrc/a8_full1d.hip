@@ -26,6 +26,8 @@ struct DescFull {
   int64_t numel;
   int64_t wg_begin;
   uint64_t sr_seed;
+  float* psq;               // sum of p^2 (NORM pass with scale_param), read by the update passes
+  const float* fira_scale;  // Fira limiter scale multiplied into the step, or null
 };
 
 struct HyperFull {
@@ -43,6 +45,10 @@ struct HyperFull {
   float decay_val;
   int has_decay;
   uint64_t sr_step;
+  int scale_param;  // alpha = max(rms(p), eps2) * rho with rms from *psq (optimizer.py:851-855)
+  float eps2;
+  int wd_mode;      // 0: none here, 1: p *= 1 - alpha*wd, 2: p *= 1 - rho*wd (optimizer.py:2032-2039)
+  float wd;
 };
 
 constexpr int kFLanes = 256;
@@ -71,10 +77,15 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
   const int lane = threadIdx.x;
   const int64_t n = D.numel;
   const int64_t e0 = wl * kFElems + (int64_t)lane * 8;
-  float sq = 0.0f;
-  float step = 0.0f, ut_clip = 1.0f;
+  float sq = 0.0f, psum = 0.0f;
+  float step = 0.0f, ut_clip = 1.0f, wdec = 1.0f;
   if constexpr (MODE != 1) {
-    const float a = D.alpha ? *D.alpha : h.alpha_val;
+    float a = D.alpha ? *D.alpha : h.alpha_val;   // rho when scale_param
+    const float rho = a;
+    if (h.scale_param) a = fmaxf(sqrtf(*D.psq) / (float)sqrt((double)n), h.eps2) * a;
+    if (h.wd_mode == 1) wdec = 1.0f - a * h.wd;
+    else if (h.wd_mode == 2) wdec = 1.0f - rho * h.wd;
+    if (D.fira_scale) a = a * *D.fira_scale;
     if constexpr (MODE == 0) {
       step = a;
     } else {
@@ -100,6 +111,10 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
     for (int k = 0; k < cnt; ++k) {
       const int64_t i = e0 + k;
       const float g = scrub(to_f<T>(G[i]));
+      if (MODE == 1 && h.scale_param) {
+        const float pv = to_f<T>(P[i]);
+        psum += pv * pv;
+      }
       float v;
       if (MODE == 2 || MODE == 4) {
         v = D.v[i];
@@ -141,11 +156,12 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       if (MODE != 1 && MODE != 4) {
         float p = to_f<T>(P[i]);
         if constexpr (SR) {
-          const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
+          const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : (h.wd_mode ? wdec : 1.0f));
           P[i] = sr_round<T>(p * dec - step * u, D.sr_seed, h.sr_step, (uint64_t)i);
         } else {
           if (D.decay) p = p * *D.decay;
           else if (h.has_decay) p = p * h.decay_val;
+          else if (h.wd_mode) p = p * wdec;
           P[i] = from_f<T>(__builtin_fmaf(-step, u, p));
         }
       }
@@ -154,6 +170,12 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
   if constexpr (MODE == 1 || MODE == 3 || MODE == 4) {
     float t = grp_sum(sq, 64);
     if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+  }
+  if constexpr (MODE == 1) {
+    if (h.scale_param) {
+      const float t = grp_sum(psum, 64);
+      if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.psq, t);
+    }
   }
 }
 
@@ -201,7 +223,8 @@ static HyperFull make_hf(double beta1, double beta_val, float eps_sq, float eps_
 }
 
 // ------------------------------------------------------------ Fira scalar
-// out[i] = scale (or alpha*scale), out[n+i] = next prev-norm, out[2n+i] = finite(x) ? x : 0
+// out[i] = scale (apply 0: x is the norm; 2: x is its square) or alpha*scale
+// (apply 1: x is the square), out[n+i] = next prev-norm, out[2n+i] = finite(x) ? x : 0
 __global__ void k_fira(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
                        float margin, int apply, int has_prev) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -219,7 +242,7 @@ __global__ void k_fira(const float* x, const float* prev, const float* alpha, fl
     scale = reset ? 1.0f : 1.0f / lim;
     next = reset ? curr : curr * scale;
   }
-  out[i] = apply ? alpha[i] * scale : scale;
+  out[i] = apply == 1 ? alpha[i] * scale : scale;
   out[n + i] = next;
   out[2 * n + i] = fin ? in : 0.0f;
 }
@@ -258,8 +281,11 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   float eps_sq, float eps_for_denom, int use_adam_denom,
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
-                                  uint64_t sr_step, int upload, void* stream) {
+                                  uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
+                                  int upload, void* stream) {
   if (ntensors <= 0) return 0;
+  if (scale_param && mode != 2 && mode != 1) return set_error(A8_ERR_ARG, "scale_param needs the NORM/APPLY passes");
+  if (wd_mode && has_decay) return set_error(A8_ERR_ARG, "give has_decay or wd_mode, not both");
   if ((int64_t)sizeof(DescFull) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_full(ntensors)");
   if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
@@ -279,15 +305,17 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
     D.param = t.param; D.grad = t.grad; D.v = t.variance; D.m = t.m; D.norm_buf = t.norm_buf;
     D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay; D.numel = t.numel;
     D.sr_seed = t.sr_seed;
+    D.psq = t.psq; D.fira_scale = t.fira_scale;
+    if (scale_param && (!t.psq || !t.param)) return set_error(A8_ERR_ARG, "scale_param needs psq and param");
     D.wg_begin = wg;
     wg += (t.numel + kFElems - 1) / kFElems;
   }
   hipStream_t st = (hipStream_t)stream;
-  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(DescFull) * (size_t)ntensors,
-                               hipMemcpyHostToDevice, st) != hipSuccess)
+  if (upload && upload_table(table_dev, tab.data(), sizeof(DescFull) * (size_t)ntensors, st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
                         momentum_only, sr_step, alpha_val, decay_val, has_decay);
+  h.scale_param = scale_param; h.eps2 = eps2; h.wd_mode = wd_mode; h.wd = wd;
   DescFull none{};
   return launch_full_any(dtype, stochastic, mode, none, reinterpret_cast<const DescFull*>(table_dev),
                          ntensors, wg, h, st);
@@ -299,7 +327,8 @@ int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float*
                    int has_prev, int apply, float margin, void* stream) {
   if (n < 0) return set_error(A8_ERR_SIZE, "n < 0");
   if (n == 0) return 0;
-  if (!x || !out || (has_prev && !prev) || (apply && !alpha)) return set_error(A8_ERR_ARG, "null pointer");
+  if (apply < 0 || apply > 2) return set_error(A8_ERR_ARG, "apply must be 0, 1 or 2");
+  if (!x || !out || (has_prev && !prev) || (apply == 1 && !alpha)) return set_error(A8_ERR_ARG, "null pointer");
   const int threads = 128;
   const int64_t blocks = (n + threads - 1) / threads;
   hipLaunchKernelGGL(k_fira, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, x, prev, alpha,

@@ -293,8 +293,7 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
     wg += (t.numel + kSElems - 1) / kSElems;
   }
   hipStream_t st = (hipStream_t)stream;
-  if (upload && hipMemcpyAsync(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)ntensors,
-                               hipMemcpyHostToDevice, st) != hipSuccess)
+  if (upload && upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)ntensors, st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   SgdDesc none{};
   return launch_sgd(dtype, stochastic, mode, m_kind, wg, st, none, reinterpret_cast<const SgdDesc*>(table_dev),

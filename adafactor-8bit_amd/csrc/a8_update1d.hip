@@ -840,7 +840,7 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
     std::vector<char> blob((size_t)a8_table_bytes_1d(ntensors));
     std::memcpy(blob.data(), tab.data(), sizeof(Desc1D) * (size_t)ntensors);
     std::memcpy(blob.data() + sizeof(Desc1D) * (size_t)ntensors, first.data(), sizeof(int32_t) * (size_t)ntensors);
-    if (hipMemcpyAsync(table_dev, blob.data(), blob.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+    if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
   }
   Hyper1D h{};

@@ -240,7 +240,7 @@ def main():
     stream = torch.cuda.current_stream(dev)
     big = [p for p in params if p.numel() >= 4096]
     ws = opt._ws[(dev, "tables")]
-    ents = [v for k, v in ws.items() if k[0][0] == "q1d"]
+    ents = [v for k, v in ws.items() if k[0] == "q1d"]
     ent = ents[-1]
     arr, table, nbytes, _ = ent
     L = nat.lib()

@@ -145,22 +145,32 @@ typedef struct a8_tensor_full {
   const float* decay;
   int64_t numel;
   uint64_t sr_seed;        /* stochastic rounding seed (16-bit params) */
+  float* psq;              /* sum of p^2 slot (zeroed by the caller) when scale_param, else null */
+  const float* fira_scale; /* Fira scale multiplied into alpha by the update passes, or null */
 } a8_tensor_full;
 
-/* Multi-tensor form of a8_fused_update_1d_full (one launch per group). */
+/* Multi-tensor form of a8_fused_update_1d_full (one launch per group).  Beyond the
+ * single-tensor call: scale_param makes the NORM pass add sum(p^2) to each tensor's
+ * psq slot and the APPLY pass take alpha = max(sqrt(psq)/sqrt(numel), eps2) * rho
+ * (rho = alpha_val, or *alpha) (optimizer.py:851-855); wd_mode 1 / 2 multiplies p by
+ * 1 - alpha*wd / 1 - rho*wd before the update (optimizer.py:2032-2039, instead of
+ * has_decay); a tensor's fira_scale, when given, multiplies alpha after both
+ * (_apply_fira_cuda, optimizer.py:785-793). */
 int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* tensors, int ntensors,
                                   void* table_dev, int64_t table_bytes, double beta1, double beta_val,
                                   float eps_sq, float eps_for_denom, int use_adam_denom,
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
-                                  uint64_t sr_step, int upload, void* stream);
+                                  uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
+                                  int upload, void* stream);
 int64_t a8_table_bytes_full(int ntensors);
 
 /* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,
- * optimizer.py:735-757).  For i < n: norm = apply ? sqrt(x[i]) : x[i], zeroed when
+ * optimizer.py:735-757).  For i < n: norm = apply ? sqrt(x[i]) : x[i] (apply 0, 1, 2), zeroed when
  * non-finite; with a previous norm p: ratio = norm/(p+1e-8),
  * limiter = max(ratio, margin)/margin, scale = p < 1e-6 ? 1 : 1/limiter.
- * out[i] = apply ? alpha[i]*scale : scale; out[n+i] = next previous norm;
+ * out[i] = apply == 1 ? alpha[i]*scale : scale (apply 2: x holds squared norms, the
+ * scale alone is written); out[n+i] = next previous norm;
  * out[2n+i] = x[i] if finite else 0.  margin = 1 + fira_margin. */
 int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
                    int has_prev, int apply, float margin, void* stream);

@@ -206,3 +206,50 @@ def test_fp16_deterministic_writeback_rounds_the_fp32_value(name, kw, shapes):
         for a, b in zip(pf, ph):
             want = a.detach().to(torch.float16)
             assert torch.equal(b.detach(), want), f"step {t}: {int((b.detach() != want).sum())} differ"
+
+
+VEC_GROUPS = [
+    # C2's vectors: factored preset, scale_parameter, RMS clip d=1, no momentum
+    ("adafactor_rms_clip", dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=True, relative_step=False,
+                                lr=1e-3)),
+    # C3's vectors: CAME preset (momentum-only 1-D update) with Fira and d=1
+    ("came_fira", dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True,
+                       relative_step=False, scale_parameter=False, scale_weight_decay=False, d=1.0, lr=1e-4,
+                       enable_fira_for_adafactor=True, fira_margin=0.01)),
+    # Adam denominator with momentum, clip, Fira, scaled weight decay and scale_parameter
+    ("adamw_clip_fira_wd_rms", dict(ADAMW, lr=1e-3, d=1.0, weight_decay=0.1, scale_weight_decay=True,
+                                    scale_parameter=True, enable_fira_for_adafactor=True)),
+    # unscaled weight decay (1 - rho*wd) with Fira, no momentum
+    ("rmsprop_fira_wd", dict(beta1=None, beta2=0.99, beta2_decay=None, factored=False, relative_step=False,
+                             scale_parameter=True, scale_weight_decay=False, weight_decay=0.05, d=0.5,
+                             eps=(1e-8, 1e-3), lr=1e-3, enable_fira_for_adafactor=True)),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", VEC_GROUPS, ids=[v[0] for v in VEC_GROUPS])
+def test_fp32_state_vector_group_matches_oracle(name, kw):
+    """A group of fp32-state vectors (below min_8bit_size) runs as one batched
+    NORM -> (MNORM) -> Fira -> APPLY sequence, with alpha = max(rms(p), eps2) * rho
+    and the weight decay computed in the kernels.  Against the oracle over 4 steps:
+    V is bit-exact (it does not depend on any norm); parameters and M within rtol
+    1e-5 (norms and sum(p^2) are reductions in another order); Fira's prev norm
+    within rtol 3e-5."""
+    print(f"[vector group] {name}", flush=True)
+    shapes = [(300,), (2048,), (64,), (1000,), (7,)]
+    pc, pg, oc, og = _run_pair(shapes, kw, 4)
+    for i, (a, b) in enumerate(zip(pc, pg)):
+        ra, rb = a.detach().numpy(), b.detach().cpu().numpy()
+        np.testing.assert_allclose(rb, ra, rtol=1e-5, atol=1e-9, err_msg=f"{name} p{i}")
+        sc, sg = oc.state[id(a)], og.state[b]
+        np.testing.assert_array_equal(sg["variance"].cpu().numpy(), sc["variance"].numpy(),
+                                      err_msg=f"{name} p{i} variance")
+        if "m" in sc:
+            # momentum-only: M averages U / clip, and the clip is a norm reduced in
+            # another order, so an element near zero keeps an error ~1e-7 of max|M|
+            floor = 1e-6 * float(np.abs(sc["m"].numpy()).max())
+            np.testing.assert_allclose(sg["m"].cpu().numpy(), sc["m"].numpy(), rtol=1e-5, atol=floor,
+                                       err_msg=f"{name} p{i} m")
+        if "fira_prev_norm" in sc:
+            np.testing.assert_allclose(float(sg["fira_prev_norm"]), float(sc["fira_prev_norm"]), rtol=3e-5,
+                                       err_msg=f"{name} p{i} fira_prev_norm")

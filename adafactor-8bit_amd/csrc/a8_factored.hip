@@ -809,42 +809,60 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     const int64_t rowbase = (b * R + r) * C;
     const float ir = cp(ws)[W.invr + b * R + r];
     const float icrr = CM ? cp(ws)[W.icr + b * R + r] : 0.0f;
+    // all loads of the row's four chunks first (up to 128 B per lane in flight),
+    // then the arithmetic and stores chunk by chunk
+    float gj[4][4], pj[4][4], msj[4];
+    uint32_t qj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c0 = c_base + 256 * j + 4 * wl;
+      const int64_t e = rowbase + c0;
+      msj[j] = 0.0f;
+      qj[j] = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { gj[j][i] = 0.0f; pj[j][i] = 0.0f; }
+      if (c0 < C) {                       // C % 4 == 0: all four columns or none
+        load4v<T>(G0, e, gj[j]);
+        if constexpr (kHasM) {
+          msj[j] = gp(D.m_scale)[e >> lbm];
+          if (MK == 1 || !(mk == 2 || mk == 4)) qj[j] = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
+          else qj[j] = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
+        }
+        if constexpr (MODE != 1 && !SR) load4v<T>(P0, e, pj[j]);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (c_base + 256 * j >= C) break;     // uniform: chunk beyond the matrix
       const int q0 = 256 * j + 4 * wl;
       const int64_t c0 = c_base + q0;
-      const bool act = c0 < C;            // C % 4 == 0: all four columns or none
+      const bool act = c0 < C;
       const int64_t e = rowbase + c0;
-      float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      float pv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float* pv = pj[j];
       if (act) {
-        load4v<T>(G0, e, g);
         if constexpr (kHasM) {
-          const float ms = gp(D.m_scale)[e >> lbm];
+          const float ms = msj[j];
+          const uint32_t qv = qj[j];
           if (MK == 1) {
-            const uint32_t qv = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
             const float s128 = ms / 128.0f, b128 = -128.0f * s128;
 #pragma unroll
             for (int i = 0; i < 4; ++i) mo[i] = __builtin_fmaf((float)((qv >> (8 * i)) & 0xFFu), s128, b128);
           } else if (mk == 2 || mk == 4) {
-            const uint32_t qv = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const uint32_t byte = (qv >> (8 * (i >> 1))) & 0xFFu;
               mo[i] = m_decode(mk, (i & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
             }
           } else {
-            const uint32_t qv = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
 #pragma unroll
             for (int i = 0; i < 4; ++i) mo[i] = m_decode(mk, (qv >> (8 * i)) & 0xFFu, ms);
           }
         }
-        if constexpr (MODE != 1 && !SR) load4v<T>(P0, e, pv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float gi = scrub(g[i]);
+          const float gi = scrub(gj[j][i]);
           const float ic = s_ic[q0 + i];
           if constexpr (CM) {
             const float ug = ((gi * ir) * ic) / clip;

@@ -66,7 +66,7 @@ class Tensor2D(ctypes.Structure):
                 ("conf_row", _c_vp), ("conf_col_q", _c_vp), ("conf_col_scale", _c_vp),
                 ("conf_col_min_log", _c_vp), ("conf_col", _c_vp), ("workspace", _c_vp),
                 ("lr", _c_vp), ("fira_prev_norm", _c_vp), ("has_fira_prev", _c_i),
-                ("batch", _c_i64), ("rows", _c_i64), ("cols", _c_i64), ("sr_seed", _c_u64)]
+                ("batch", _c_i64), ("rows", _c_i64), ("cols", _c_i64), ("sr_seed", _c_u64), ("m", _c_vp)]
 
 
 class ApolloTensor(ctypes.Structure):
@@ -94,11 +94,11 @@ _SIGS = {
     "a8_table_bytes_1d": (_c_i64, [_c_i]),
     "a8_fused_update_1d_full": (_c_i, [_c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                        _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,
-                                       _c_f, _c_f, _c_i, _c_i, _c_u64, _c_u64, _c_vp]),
+                                       _c_f, _c_f, _c_i, _c_i, _c_u64, _c_u64, _c_i, _c_vp]),
     "a8_fused_update_1d_full_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(TensorFull), _c_i, _c_vp,
                                              _c_i64, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_f, _c_i,
                                              _c_f, _c_f, _c_i, _c_i, _c_u64, _c_i, _c_f, _c_i, _c_f,
-                                             _c_i, _c_vp]),
+                                             _c_i, _c_i, _c_vp]),
     "a8_table_bytes_full": (_c_i64, [_c_i]),
     "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_factored_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(Tensor2D), _c_i, _c_vp, _c_i64, _c_i, _c_d,

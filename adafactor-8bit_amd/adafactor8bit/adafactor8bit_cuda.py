@@ -217,7 +217,7 @@ def _full(mode, param, grad, variance, m, norm_buf, alpha, prev_norm, beta1, bet
         mode, nat.dtype_code(grad.dtype), nat.ptr(param), nat.ptr(grad), nat.ptr(variance), nat.ptr(m),
         nat.ptr(norm_buf), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(decay), float(beta1), float(beta_val),
         float(eps_sq), float(eps_for_denom), int(bool(use_adam_denom)), float(eps_for_grad_sq),
-        int(numel), float(d), int(bool(momentum_only)), 0.0, 1.0, 0, int(sr), int(sr_seed or 0), int(sr_step),
+        int(numel), float(d), int(bool(momentum_only)), 0.0, 1.0, 0, int(sr), int(sr_seed or 0), int(sr_step), 0,
         _stream(grad))
     nat.check(rc, "fused_update_1d_full")
 

@@ -327,6 +327,8 @@ class Adafactor8Bit(Optimizer):
                 ap_batches.setdefault(bkey, []).append((rec, fin))
                 continue
             plan = _plan_param(p, g, st, group)
+            if plan.path == "q1d_fp32m":
+                _prep_q1d_fp32m(self, plan)
             key = plan.batch_key()
             if key is None:
                 _run_single(self, plan)
@@ -345,7 +347,7 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf")
 
     def batch_key(self):
         if self.path == "factored":
@@ -361,6 +363,7 @@ class _Plan:
             if self.lag:
                 return None
             return ("f1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m,
+                    self.vbuf is not None,
                     self.beta1, self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.kwd, self.group["weight_decay"], self.d, self.fira,
                     self.margin, self.rms_kernel, self.eps2)
@@ -371,6 +374,7 @@ class _Plan:
             return ("sgd", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m, mq,
                     self.mqt if mq else None, self.mbs if mq else 0, self.beta1, self.alpha_val, self.decay_val)
         return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
+                self.vbuf is not None,
                 self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                 self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                 self.alpha_val, self.decay_val)
@@ -379,6 +383,7 @@ class _Plan:
 def _plan_param(p, grad, st, group) -> _Plan:
     P = _Plan()
     P.p, P.st, P.group = p, st, group
+    P.vbuf = None
     beta1, beta2, beta2_decay, beta3 = group.get("beta1"), group["beta2"], group["beta2_decay"], group.get("beta3")
     eps1, eps2 = group["eps"]
     eps1 = 1e-30 if eps1 is None else eps1
@@ -609,16 +614,13 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
         if m is not None and not m.is_contiguous():
             m = m.contiguous()
             st["m"] = m
-        var = st["variance"]
-        if not var.is_contiguous():
-            var = var.contiguous()
-            st["variance"] = var
+        var = _variance_of(P)
         rc = L.a8_fused_update_1d_full(
             mode, nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(var), nat.ptr(m),
             nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
             P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
             p.numel(), P.d, int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
-            int(P.sr), int(st.get("sr_seed", 0)), int(P.step), nat.stream_of(p.device))
+            int(P.sr), int(st.get("sr_seed", 0)), int(P.step), int(P.vbuf is not None), nat.stream_of(p.device))
         nat.check(rc, "a8_fused_update_1d_full")
 
 
@@ -712,6 +714,46 @@ def _run_sgd(opt, P):
     launch(nat.MODE_APPLY, norm_buf=nb, fira=fira)
 
 
+def _variance_of(P):
+    """The fp32 second moment an fp32-state launch reads: this step's V' from the
+    quantised-V pre-pass (v_ready), or the fp32 state itself."""
+    if P.vbuf is not None:
+        return P.vbuf
+    var = P.st["variance"]
+    if not var.is_contiguous():
+        var = var.contiguous()
+        P.st["variance"] = var
+    return var
+
+
+def _prep_q1d_fp32m(opt, P):
+    """Quantised V with fp32 momentum (optimizer.py:2078-2087): the V EMA and its AL
+    re-encode run first (a8_log_quantize_lerp, x = g^2 + eps_g), writing this step's
+    fp32 V' to a per-parameter buffer; the update then takes the fp32-state route
+    with that V' (v_ready), as the reference feeds _v_fp32 to _fallback_1d_update."""
+    st, p, g = P.st, P.p, P.g
+    dev = p.device
+    if "m" not in st:
+        st["m"] = torch.zeros_like(g, dtype=torch.float32)
+    if not st["m"].is_contiguous():
+        st["m"] = st["m"].contiguous()
+    key = (dev, "vready", id(p))
+    buf = opt._ws.get(key)
+    if buf is None or buf.numel() != p.numel():
+        buf = torch.empty(p.numel(), dtype=torch.float32, device=dev)
+        opt._ws[key] = buf
+    if g.dtype != p.dtype:
+        raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    rc = nat.lib().a8_log_quantize_lerp(
+        st["variance_q"].data_ptr(), st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(),
+        g.data_ptr(), nat.dtype_code(g.dtype), buf.data_ptr(), float(P.beta_val), int(P.bs), 1, _f32(P.eps_g),
+        p.numel(), _AL_FLOOR, 16 if P.vqt == "al16" else 8, nat.stream_of(dev))
+    nat.check(rc, "a8_log_quantize_lerp")
+    _block_view(st, "variance", P.bs)
+    P.vbuf = buf
+    P.path = "f1d"
+
+
 def _materialize_alpha(P):
     """alpha (and its weight decay) of a plan that deferred them to the batched
     kernels, computed as _compute_alpha does (optimizer.py:851-855, 2032-2039)."""
@@ -784,11 +826,9 @@ def _run_batch_f1dc(opt, key, plans):
     for pl in plans:
         if pl.has_m and not pl.st["m"].is_contiguous():
             pl.st["m"] = pl.st["m"].contiguous()
-        if not pl.st["variance"].is_contiguous():
-            pl.st["variance"] = pl.st["variance"].contiguous()
     ws = opt._ws.setdefault((dev, "f1dc"), {})
-    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr()) for pl in plans), P0.sr, P0.has_m, fira, mnorm,
-          P0.rms_kernel)
+    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr(), _variance_of(pl).data_ptr()) for pl in plans), P0.sr,
+          P0.has_m, fira, mnorm, P0.rms_kernel)
     refs = [tuple(v.data_ptr() for k, v in pl.st.items() if torch.is_tensor(v) and k != "fira_prev_norm")
             for pl in plans]
     ent = ws.get(ck)
@@ -811,7 +851,7 @@ def _run_batch_f1dc(opt, key, plans):
                 elif mode == nat.MODE_APPLY and fira and not mnorm:
                     nb = f0 + 4 * (2 * n + i)
                 fs = f0 + 4 * i if (mode == nat.MODE_APPLY and fira) else None
-                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), st["variance"].data_ptr(),
+                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), _variance_of(pl).data_ptr(),
                                         nat.ptr(st.get("m") if pl.has_m else None), nb, None, prev, None,
                                         pl.p.numel(), int(st.get("sr_seed", 0)), psq, fs)
             arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_full(n)), dtype=torch.uint8, device=dev), 1]
@@ -830,7 +870,8 @@ def _run_batch_f1dc(opt, key, plans):
             mode, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), table.numel(),
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom), P0.eps_g, P0.d,
             int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr), int(P0.step),
-            int(P0.rms_kernel), _f32(P0.eps2), int(P0.kwd), _f32(P0.group["weight_decay"]), up, strm)
+            int(P0.rms_kernel), _f32(P0.eps2), int(P0.kwd), _f32(P0.group["weight_decay"]),
+            int(P0.vbuf is not None), up, strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         ent["arrs"][mode][2] = 0
 
@@ -878,7 +919,7 @@ def _run_batch(opt, key, plans):
     dev = P0.p.device
     L = nat.lib()
     n = len(plans)
-    ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr()) for pl in plans)
+    ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(pl.vbuf)) for pl in plans)
     # The table holds only pointers, sizes and seeds; step-dependent scalars go
     # to the launch, so one upload serves every later step.
     cache_key = (path, dev, key[5], ptrs)   # key[5]: stochastic rounding (seeds in the table)
@@ -908,7 +949,7 @@ def _run_batch(opt, key, plans):
             arr = (nat.TensorFull * n)()
             for i, pl in enumerate(plans):
                 st = pl.st
-                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), st["variance"].data_ptr(),
+                arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), _variance_of(pl).data_ptr(),
                                         nat.ptr(st.get("m") if pl.has_m else None), None, None, None,
                                         None, pl.p.numel(), int(st.get("sr_seed", 0)))
             nbytes = L.a8_table_bytes_full(n)
@@ -957,7 +998,7 @@ def _run_batch(opt, key, plans):
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom),
             P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr),
-            int(P0.step), 0, 0.0, 0, 0.0, upload, strm)
+            int(P0.step), 0, 0.0, 0, 0.0, int(P0.vbuf is not None), upload, strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         if upload:
             ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
@@ -1137,10 +1178,14 @@ def _run_factored(opt, plans):
     if came:
         cqt = P0.st.get("c_quant_type") or P0.vqt
         cbits = 0 if (not P0.quant or cqt == "fp32") else (16 if cqt == "al16" else 8)
+    m32 = P0.has_m and (not P0.quant or P0.mqt == "fp32" or "m_q" not in P0.st)
     for pl in plans:
-        if pl.has_m and (not pl.quant or pl.mqt == "fp32"):
-            raise NotImplementedError("adafactor8bit: factored path with fp32 momentum is not available "
-                                      "in this build yet")
+        if pl.has_m and m32:
+            st = pl.st
+            if "m" not in st:
+                st["m"] = torch.zeros_like(pl.g, dtype=torch.float32)
+            if not st["m"].is_contiguous():
+                st["m"] = st["m"].contiguous()
         if not pl.p.is_contiguous():
             raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
         if pl.g.dtype != pl.p.dtype:
@@ -1217,14 +1262,15 @@ def _run_factored(opt, plans):
                         None if cq else st["conf_col"].data_ptr()]
             arr[i] = nat.Tensor2D(
                 pl.p.data_ptr(), pl.g.data_ptr(),
-                nat.ptr(st.get("m_q") if pl.has_m else None), nat.ptr(st.get("m_scale") if pl.has_m else None),
+                nat.ptr(st.get("m_q") if pl.has_m and not m32 else None),
+                nat.ptr(st.get("m_scale") if pl.has_m and not m32 else None),
                 nat.ptr(st["row_var_q"]) if q else None, nat.ptr(st["row_var_scale"]) if q else None,
                 nat.ptr(st["row_var_min_log"]) if q else None, None if q else st["row_var"].data_ptr(),
                 nat.ptr(st["col_var_q"]) if q else None, nat.ptr(st["col_var_scale"]) if q else None,
                 nat.ptr(st["col_var_min_log"]) if q else None, None if q else st["col_var"].data_ptr(),
                 *conf, base + 4 * offs[i], nat.ptr(pl.rho_t),
                 nat.ptr(st.get("fira_prev_norm")) if fira else None, has_prev[i],
-                B, R, C, int(st.get("sr_seed", 0)))
+                B, R, C, int(st.get("sr_seed", 0)), nat.ptr(st["m"]) if pl.has_m and m32 else None)
         ent = {"sig": sig, "arr": arr, "ws": wbuf, "table": table, "n": n}
         if len(wsd) > 64:
             wsd.clear()

@@ -38,6 +38,7 @@ constexpr int kTR = 32;      // minimum rows per statistics tile
 constexpr int kTC = 1024;    // columns per statistics tile (256 lanes x 4)
 constexpr int kUnit = 2048;  // elements per update workgroup
 constexpr int kScal = 8;     // per-tensor scalars in the workspace
+constexpr int kMkFp32 = 5;   // HyperF::mk of fp32 momentum (codecs are 1-4)
 
 // Per-tensor workspace layout (floats).
 struct FWs {
@@ -108,6 +109,7 @@ struct DescF {
   float* ws;
   const float* lr;
   float* fira_prev;
+  float* m;            // fp32 momentum (MK 3), or null
   int64_t B, R, C, numel;
   int64_t tile_begin;
   int64_t unit_begin;
@@ -370,7 +372,8 @@ __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, 
       if (c0 < C) {
         float g4[4], m4[4];
         load4<T>(G, rowbase, c0, C, vec, g4);
-        m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, m4);
+        if constexpr (MK == 3) load4<float>(D.m, rowbase, c0, C, vec, m4);
+        else m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, m4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (c0 + e < C) {
@@ -575,7 +578,7 @@ __global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, 
 
 // ------------------------------------------------------------ update
 // MODE 0: write with step = alpha; 1: sum(u^2) per unit; 2: write with the
-// step and Fira scale of k_fnorm.  MK: 0 no momentum, 1 UF8, 2 other codecs.
+// step and Fira scale of k_fnorm.  MK: 0 no momentum, 1 UF8, 2 other codecs, 3 fp32 momentum.
 // CM (CAME): the momentum EMA runs on U = ((g * inv_row) * inv_col) / clip and
 // the update is (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
 template <typename T, int MODE, bool SR, int MK, bool CM>
@@ -614,7 +617,9 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
     load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
 #pragma unroll
     for (int k = 0; k < 8; ++k) g[k] = scrub(g[k]);
-    if constexpr (kHasM) {
+    if constexpr (MK == 3) {
+      load8<float>(D.m, e0, n, mo);
+    } else if constexpr (kHasM) {
       const float ms = gp(D.m_scale)[mb];
       if (MK == 1) {
         const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
@@ -634,10 +639,10 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 #pragma unroll
         for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }
-      if constexpr (!CM) {
+    }
+    if constexpr (kHasM && !CM) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) mn[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
-      }
+      for (int k = 0; k < 8; ++k) mn[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
     }
     const float clip = CM ? gp(sl)[4] : 1.0f;
     // element (row, column): row = e / C, column index b*C + c with b = row / R
@@ -708,8 +713,11 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
     if (lane == 0) gp(const_cast<float*>(ws))[W.npart + wl] = tot;
   }
 
+  if constexpr (MODE != 1 && MK == 3) {
+    if (cnt > 0) store8<float>(D.m, e0, n, mn);
+  }
   // momentum re-encode: absmax over B_M elements = ML lanes
-  if constexpr (MODE != 1 && kHasM) {
+  if constexpr (MODE != 1 && kHasM && MK != 3) {
     const int wave = lane >> 6;
     float bam = grp_max(__uint_as_float(amaxb), ML < 64 ? ML : 64);
     if (ML > 64) {
@@ -812,6 +820,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     // all loads of the row's four chunks first (up to 128 B per lane in flight),
     // then the arithmetic and stores chunk by chunk
     float gj[4][4], pj[4][4], msj[4];
+    float mfj[MK == 3 ? 4 : 1][4];
     uint32_t qj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -821,9 +830,15 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
       qj[j] = 0u;
 #pragma unroll
       for (int i = 0; i < 4; ++i) { gj[j][i] = 0.0f; pj[j][i] = 0.0f; }
+      if constexpr (MK == 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mfj[j][i] = 0.0f;
+      }
       if (c0 < C) {                       // C % 4 == 0: all four columns or none
         load4v<T>(G0, e, gj[j]);
-        if constexpr (kHasM) {
+        if constexpr (MK == 3) {
+          load4v<float>(D.m, e, mfj[j]);
+        } else if constexpr (kHasM) {
           msj[j] = gp(D.m_scale)[e >> lbm];
           if (MK == 1 || !(mk == 2 || mk == 4)) qj[j] = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
           else qj[j] = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
@@ -842,7 +857,10 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
       float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       float* pv = pj[j];
       if (act) {
-        if constexpr (kHasM) {
+        if constexpr (MK == 3) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mo[i] = mfj[j][i];
+        } else if constexpr (kHasM) {
           const float ms = msj[j];
           const uint32_t qv = qj[j];
           if (MK == 1) {
@@ -902,7 +920,9 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
             store4n<T>(P0, e, e + 4, pv);
           }
         }
-        if constexpr (kHasM) {
+        if constexpr (MK == 3) {
+          if (act) store4n<float>(D.m, e, e + 4, mn);
+        } else if constexpr (kHasM) {
           // momentum re-encode: absmax over the block's G lanes (inactive lanes hold 0)
           uint32_t ab = 0u;
 #pragma unroll
@@ -1030,11 +1050,13 @@ static int launch_update_m(int mk, const DescF* tab, int ntab, const UpdGrid& ug
     const dim3 g((unsigned)ug.ntiles);
     if constexpr (CM) {
       if (mk == 1) hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
+      else if (mk == kMkFp32) hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 3, true>), g, b, 0, st, tab, ntab, h);
       else hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
     } else {
       switch (mk) {
         case 0: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
         case 1: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
+        case kMkFp32: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 3, false>), g, b, 0, st, tab, ntab, h); break;
         default: hipLaunchKernelGGL((k_fupdt<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
       }
     }
@@ -1045,11 +1067,13 @@ static int launch_update_m(int mk, const DescF* tab, int ntab, const UpdGrid& ug
     const dim3 g((unsigned)ug.nunits);
     if constexpr (CM) {
       if (mk == 1) hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, true>), g, b, 0, st, tab, ntab, h);
+      else if (mk == kMkFp32) hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 3, true>), g, b, 0, st, tab, ntab, h);
       else hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
     } else {
       switch (mk) {
         case 0: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h); break;
         case 1: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 1, false>), g, b, 0, st, tab, ntab, h); break;
+        case kMkFp32: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 3, false>), g, b, 0, st, tab, ntab, h); break;
         default: hipLaunchKernelGGL((k_fupdate<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h); break;
       }
     }
@@ -1100,6 +1124,7 @@ static int run_group(const DescF* tab, int ntab, int64_t ntiles, const UpdGrid& 
       if ((rc = check_launch("k_fclip"))) return rc;
     }
     if (h.mk == 1) hipLaunchKernelGGL((k_came1<T, 1>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
+    else if (h.mk == kMkFp32) hipLaunchKernelGGL((k_came1<T, 3>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     else hipLaunchKernelGGL((k_came1<T, 2>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     if ((rc = check_launch("k_came1"))) return rc;
     if ((rc = launch_finish<true>(cbits, tab, ntab, nfblk, h, st))) return rc;
@@ -1148,9 +1173,10 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (block_size <= 0) return set_error(A8_ERR_BLOCK, "block_size must be positive");
   if ((int64_t)sizeof(DescF) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_2d(ntensors)");
-  const bool has_m = tensors[0].m_q != nullptr;
+  const bool m32 = tensors[0].m != nullptr;
+  const bool has_m = tensors[0].m_q != nullptr || m32;
   int lbm = 0;
-  if (has_m) {
+  if (has_m && !m32) {
     if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
       return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
     if (m_block_size < 32 || m_block_size > kUnit || (m_block_size & (m_block_size - 1)))
@@ -1159,7 +1185,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   } else {
     lbm = 5;
   }
-  if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum codes (m_q)");
+  if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum (m_q or m)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
   int64_t tiles = 0, units = 0, fblks = 0;
@@ -1169,7 +1195,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     const a8_tensor2d& t = tensors[i];
     if (t.batch <= 0 || t.rows <= 0 || t.cols <= 0) return set_error(A8_ERR_SIZE, "empty factored tensor");
     if (!t.param || !t.grad || !t.workspace) return set_error(A8_ERR_ARG, "null param/grad/workspace");
-    if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if ((t.m_q != nullptr) != (has_m && !m32) || (t.m != nullptr) != m32)
+      return set_error(A8_ERR_ARG, "mixed momentum kinds in one launch");
     if (v_bits ? !(t.row_q && t.col_q && t.row_scale && t.col_scale && t.row_min_log && t.col_min_log)
                : !(t.row_var && t.col_var))
       return set_error(A8_ERR_ARG, "row/column state missing");
@@ -1178,12 +1205,12 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                             t.conf_row_min_log && t.conf_col_min_log)
                         : !(t.conf_row && t.conf_col)))
       return set_error(A8_ERR_ARG, "CAME confidence state missing");
-    if (!aligned16(t.param) || !aligned16(t.grad) || (has_m && !aligned16(t.m_q)))
+    if (!aligned16(t.param) || !aligned16(t.grad) || (has_m && !aligned16(m32 ? (const void*)t.m : t.m_q)))
       return set_error(A8_ERR_ALIGN, "param/grad/momentum buffers must be 16-byte aligned");
     const int64_t numel = t.batch * t.rows * t.cols;
     if (numel >= ((int64_t)1 << 40)) return set_error(A8_ERR_SIZE, "tensor too large");
     DescF& D = tab[(size_t)i];
-    D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
+    D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale; D.m = t.m;
     D.row_q = t.row_q; D.row_scale = t.row_scale; D.row_min_log = t.row_min_log; D.row_var = t.row_var;
     D.col_q = t.col_q; D.col_scale = t.col_scale; D.col_min_log = t.col_min_log; D.col_var = t.col_var;
     D.crow_q = t.conf_row_q; D.crow_scale = t.conf_row_scale; D.crow_min_log = t.conf_row_min_log;
@@ -1193,7 +1220,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     D.B = t.batch; D.R = t.rows; D.C = t.cols; D.numel = numel;
     D.sr_seed = t.sr_seed;
     D.vec4 = ((t.cols * esz) % 16 == 0) ? 1 : 0;
-    D.tiled = (t.cols % 4 == 0) && (!has_m || (m_block_size <= 256 && t.cols % m_block_size == 0)) ? 1 : 0;
+    D.tiled = (t.cols % 4 == 0) && (!has_m || m32 || (m_block_size <= 256 && t.cols % m_block_size == 0)) ? 1 : 0;
     (D.tiled ? any_tiled : any_flat) = true;
     const FWs W = fws_layout(t.batch, t.rows, t.cols);
     D.tile_begin = tiles;
@@ -1222,7 +1249,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.w_c = (float)(1.0 - beta3);
   h.eps_came = eps_came;
   h.block_size = block_size;
-  h.mk = has_m ? mk_code(m_bits, m_mode) : 0;
+  h.mk = m32 ? kMkFp32 : (has_m ? mk_code(m_bits, m_mode) : 0);
   h.lbm = lbm;
   h.sr_step = sr_step;
   const bool clip = d > 0.0f || fira;

@@ -49,6 +49,7 @@ struct HyperFull {
   float eps2;
   int wd_mode;      // 0: none here, 1: p *= 1 - alpha*wd, 2: p *= 1 - rho*wd (optimizer.py:2032-2039)
   float wd;
+  int v_ready;      // V holds this step's second moment already (no EMA, not written)
 };
 
 constexpr int kFLanes = 256;
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
         psum += pv * pv;
       }
       float v;
-      if (MODE == 2 || MODE == 4) {
+      if (MODE == 2 || MODE == 4 || h.v_ready) {
         v = D.v[i];
       } else {
         v = __builtin_fmaf(h.bv * g, g, D.v[i] * h.v_keep);
@@ -259,7 +260,7 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
                             float decay_val, int has_decay, int stochastic, uint64_t sr_seed,
-                            uint64_t sr_step, void* stream) {
+                            uint64_t sr_step, int v_ready, void* stream) {
   if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
   if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
   if (!param && mode != 1 && mode != 4) return set_error(A8_ERR_ARG, "null param");
@@ -272,6 +273,7 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
   D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
                         momentum_only, sr_step, alpha_val, decay_val, has_decay);
+  h.v_ready = v_ready;
   return launch_full_any(dtype, stochastic, mode, D, nullptr, 0, (numel + kFElems - 1) / kFElems, h,
                          (hipStream_t)stream);
 }
@@ -282,7 +284,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
-                                  int upload, void* stream) {
+                                  int v_ready, int upload, void* stream) {
   if (ntensors <= 0) return 0;
   if (scale_param && mode != 2 && mode != 1) return set_error(A8_ERR_ARG, "scale_param needs the NORM/APPLY passes");
   if (wd_mode && has_decay) return set_error(A8_ERR_ARG, "give has_decay or wd_mode, not both");
@@ -315,7 +317,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
     return set_error(A8_ERR_HIP, "table upload failed");
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
                         momentum_only, sr_step, alpha_val, decay_val, has_decay);
-  h.scale_param = scale_param; h.eps2 = eps2; h.wd_mode = wd_mode; h.wd = wd;
+  h.scale_param = scale_param; h.eps2 = eps2; h.wd_mode = wd_mode; h.wd = wd; h.v_ready = v_ready;
   DescFull none{};
   return launch_full_any(dtype, stochastic, mode, none, reinterpret_cast<const DescFull*>(table_dev),
                          ntensors, wg, h, st);

@@ -125,14 +125,16 @@ int64_t a8_table_bytes_1d(int ntensors);
  * for tensors below min_8bit_size or with quantize=False.  NORM writes V (and M
  * unless momentum_only) and accumulates sum(u^2) into norm_buf; APPLY reads them.
  * stochastic (16-bit params): p * decay - step * u rounded with the (sr_seed,
- * sr_step, element index) stream of kernels.cu:48-87. */
+ * sr_step, element index) stream of kernels.cu:48-87.  v_ready: variance already
+ * holds this step's second moment (e.g. the fp32 output of a8_log_quantize_lerp for
+ * quantised V with fp32 M, optimizer.py:2078-2087): no EMA, variance not written. */
 int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
                             float* m, float* norm_buf, const float* alpha, const float* prev_norm,
                             const float* decay, double beta1, double beta_val, float eps_sq,
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
                             float decay_val, int has_decay, int stochastic, uint64_t sr_seed,
-                            uint64_t sr_step, void* stream);
+                            uint64_t sr_step, int v_ready, void* stream);
 
 typedef struct a8_tensor_full {
   void* param;
@@ -162,7 +164,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
-                                  int upload, void* stream);
+                                  int v_ready, int upload, void* stream);
 int64_t a8_table_bytes_full(int ntensors);
 
 /* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,
@@ -207,6 +209,7 @@ typedef struct a8_tensor2d {
   int has_fira_prev;       /* 0 on the first Fira step (the state is created) */
   int64_t batch, rows, cols;
   uint64_t sr_seed;
+  float* m;                /* fp32 momentum (m_quant_type 'fp32'), in place of m_q/m_scale, or NULL */
 } a8_tensor2d;
 
 /* Replaces the factored branch of one optimizer step for a group of tensors

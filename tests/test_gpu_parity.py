@@ -253,3 +253,98 @@ def test_fp32_state_vector_group_matches_oracle(name, kw):
         if "fira_prev_norm" in sc:
             np.testing.assert_allclose(float(sg["fira_prev_norm"]), float(sc["fira_prev_norm"]), rtol=3e-5,
                                        err_msg=f"{name} p{i} fira_prev_norm")
+
+
+FP32M = [
+    ("adamw_fp32m", dict(ADAMW, lr=1e-3, m_quant_type="fp32")),
+    ("adamw_fp32m_al16_clip_fira", dict(ADAMW, lr=1e-3, m_quant_type="fp32", v_quant_type="al16", d=1.0,
+                                        enable_fira_for_adafactor=True, weight_decay=0.01)),
+    ("adafactor1d_mom_fp32m", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=False,
+                                   relative_step=False, lr=1e-3, m_quant_type="fp32", block_size=256)),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", FP32M, ids=[c[0] for c in FP32M])
+@pytest.mark.parametrize("multi", [True, False])
+def test_quantized_v_with_fp32_momentum(name, kw, multi):
+    """Quantised V with fp32 momentum (optimizer.py:2078-2087): the V EMA and AL
+    re-encode first, then the fp32-state update from this step's V'.  Against the
+    oracle over 4 steps, with the AL bounds used elsewhere (the oracle decodes V
+    with torch.pow, the kernel exactly): V codes differ on <= 0.1% (one step),
+    block ranges rtol 2e-6; momentum and parameters rtol 1e-5 (plus 1e-6 of the
+    momentum's largest magnitude for elements near zero)."""
+    from adafactor8bit import Adafactor8Bit
+    from oracle.fallback import OracleOptimizer
+    print(f"[fp32 momentum] {name} multi={multi}", flush=True)
+    shapes = [(33, 517), (5000,), (64, 130), (4096,)]
+    pc = [torch.nn.Parameter(make_param(s, i, 6)) for i, s in enumerate(shapes)]
+    pg = [torch.nn.Parameter(p.detach().clone().cuda()) for p in pc]
+    oc = OracleOptimizer(pc, **kw)
+    og = Adafactor8Bit(pg if multi else [{"params": [p]} for p in pg], **kw)
+    for t in range(1, 5):
+        for i, (a, b) in enumerate(zip(pc, pg)):
+            g = make_grad(shapes[i], i, t, 6)
+            a.grad, b.grad = g, g.cuda()
+        oc.step()
+        og.step()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(pc, pg)):
+        sc, sg = oc.state[id(a)], og.state[b]
+        assert "m" in sg and sg["m"].dtype == torch.float32 and "m_q" not in sg
+        frac, mx = _codes(sc["variance_q"], sg["variance_q"])
+        assert mx <= 1 and frac <= 1e-3, (name, i, frac)
+        for k in ("variance_scale", "variance_min_log"):
+            np.testing.assert_allclose(sg[k].cpu().numpy(), sc[k].numpy(), rtol=2e-6, err_msg=f"{name} p{i} {k}")
+        floor = 1e-6 * float(sc["m"].abs().max())
+        np.testing.assert_allclose(sg["m"].cpu().numpy(), sc["m"].numpy(), rtol=1e-5, atol=floor,
+                                   err_msg=f"{name} p{i} m")
+        np.testing.assert_allclose(b.detach().cpu().numpy(), a.detach().numpy(), rtol=1e-5, atol=1e-8,
+                                   err_msg=f"{name} p{i} param")
+
+
+FACT_FP32M = [
+    ("adafactor_mom_fp32m", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=True, relative_step=False,
+                                 lr=1e-3, m_quant_type="fp32", block_size=256)),
+    ("adafactor_mom_fp32m_fira", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=True, relative_step=False,
+                                      lr=1e-3, m_quant_type="fp32", block_size=256,
+                                      enable_fira_for_adafactor=True)),
+    ("came_fp32m", dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True,
+                        relative_step=False, scale_parameter=False, scale_weight_decay=False, d=1.0, lr=1e-4,
+                        m_quant_type="fp32", block_size=256)),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", FACT_FP32M, ids=[c[0] for c in FACT_FP32M])
+def test_factored_with_fp32_momentum(name, kw):
+    """Factored Adafactor and CAME with fp32 momentum against the oracle over 4
+    steps.  Row/column statistics are means reduced in another order (an ulp
+    apart), which every update element depends on, so parameters are held to
+    rtol 1e-5 plus 1e-4 of the largest displacement and the momentum to rtol 1e-5
+    plus 1e-6 of its largest magnitude, as the factored golden tests."""
+    from adafactor8bit import Adafactor8Bit
+    from oracle.fallback import OracleOptimizer
+    print(f"[factored fp32 momentum] {name}", flush=True)
+    shapes = [(64, 300), (300, 64), (2, 40, 130), (64,)]
+    pc = [torch.nn.Parameter(make_param(s, i, 8)) for i, s in enumerate(shapes)]
+    p0 = [p.detach().clone() for p in pc]
+    pg = [torch.nn.Parameter(p.detach().clone().cuda()) for p in pc]
+    oc, og = OracleOptimizer(pc, **kw), Adafactor8Bit(pg, **kw)
+    for t in range(1, 5):
+        for i, (a, b) in enumerate(zip(pc, pg)):
+            g = make_grad(shapes[i], i, t, 8)
+            a.grad, b.grad = g, g.cuda()
+        oc.step()
+        og.step()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(pc, pg)):
+        sc, sg = oc.state[id(a)], og.state[b]
+        disp = float((a.detach() - p0[i]).abs().max())
+        np.testing.assert_allclose(b.detach().cpu().numpy(), a.detach().numpy(), rtol=1e-5, atol=1e-4 * disp,
+                                   err_msg=f"{name} p{i} param")
+        if a.dim() >= 2:
+            assert "m" in sg and "m_q" not in sg and sg["m"].dtype == torch.float32
+        floor = 1e-6 * float(sc["m"].abs().max())
+        np.testing.assert_allclose(sg["m"].cpu().numpy(), sc["m"].numpy(), rtol=1e-5, atol=floor,
+                                   err_msg=f"{name} p{i} m")

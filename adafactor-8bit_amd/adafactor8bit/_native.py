@@ -79,6 +79,21 @@ class ApolloTensor(ctypes.Structure):
                 ("step", _c_u64), ("bias_factor", _c_f)]
 
 
+class ApolloXArgs(ctypes.Structure):
+    """Mirror of ``a8_apollo_x_args``."""
+    _fields_ = [("g_low", _c_vp), ("u", _c_vp), ("xws", _c_vp), ("rows_low", _c_i64), ("cols_low", _c_i64),
+                ("factorize", _c_i), ("came", _c_i), ("has_m", _c_i), ("first_step", _c_i),
+                ("v_q", _c_vp), ("v_scale", _c_vp), ("v_min_log", _c_vp), ("v_fp32", _c_vp), ("v_bits", _c_i),
+                ("block_size", _c_i), ("row_var", _c_vp), ("col_var", _c_vp),
+                ("m_q", _c_vp), ("m_scale", _c_vp), ("m_fp32", _c_vp), ("m_bits", _c_i), ("m_mode", _c_i),
+                ("m_block_size", _c_i),
+                ("res_q", _c_vp), ("res_scale", _c_vp), ("res_min_log", _c_vp), ("res_fp32", _c_vp),
+                ("crow_q", _c_vp), ("crow_scale", _c_vp), ("crow_min_log", _c_vp), ("crow_fp32", _c_vp),
+                ("ccol_q", _c_vp), ("ccol_scale", _c_vp), ("ccol_min_log", _c_vp), ("ccol_fp32", _c_vp),
+                ("c_bits", _c_i), ("beta_v", _c_d), ("beta1", _c_d), ("beta3", _c_d),
+                ("apollo_eps", _c_f), ("eps_sq", _c_f), ("log_floor", _c_f), ("eps_came", _c_f), ("d", _c_f)]
+
+
 _SIGS = {
     "a8_last_error": (ctypes.c_char_p, []),
     "a8_version": (ctypes.c_char_p, []),
@@ -115,6 +130,12 @@ _SIGS = {
                                     _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i,
                                     _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_i, _c_vp]),
     "a8_apollo_table_bytes": (_c_i64, [_c_i]),
+    "a8_apollo_step_multi_phase": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_vp, _c_i64,
+                                          _c_d, _c_d, _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                          _c_i, _c_f, _c_i, _c_i, _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f,
+                                          _c_i, _c_vp]),
+    "a8_apollo_lowrank_x": (_c_i, [ctypes.POINTER(ApolloXArgs), _c_vp]),
+    "a8_apollo_x_workspace_floats": (_c_i64, [_c_i64, _c_i64]),
     "a8_dequantize_log_nonneg": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_dequantize_dynamic": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_sgd_step": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,

@@ -1030,13 +1030,17 @@ def _apollo_proj(st, shape, step, device, cache):
 
 
 def _apollo_prep(opt, p, grad, st, group):
-    """Host side of one APOLLO parameter's step (optimizer.py:2587-3084,
-    non-factorised, beta3 = None): step counter, projection refresh, lazy
-    low-rank state, per-step scalars.  Returns (batch key, tensor record, finish)
-    for the grouped launch."""
+    """Host side of one APOLLO parameter's step (optimizer.py:2587-3084): step
+    counter, projection refresh, lazy low-rank state, per-step scalars.  Returns
+    (batch key, tensor record, finish) for the grouped launch.  The factorised
+    and CAME variants carry an a8_apollo_x_args record for the low-rank stage
+    between the projection and finish phases."""
     beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
-    if group.get("apollo_factorize", False) or group.get("beta3") is not None:
-        raise NotImplementedError("adafactor8bit: factorised / CAME APOLLO is not available in this build yet")
+    factorize = bool(group.get("apollo_factorize", False))
+    came = group.get("beta3") is not None
+    if came and beta1 is None:
+        raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update instability.")
+    xmode = factorize or came
     if p.dtype not in (torch.float32, torch.bfloat16):
         raise NotImplementedError("adafactor8bit: APOLLO needs fp32 or bf16 parameters")
     if not p.is_contiguous():
@@ -1073,9 +1077,17 @@ def _apollo_prep(opt, p, grad, st, group):
     n_low = R * rank if right else rank * C
     quant = st.get("is_quantized", False)
     bs = st.get("block_size", group.get("block_size", 2048))
-    first = st.get("v_low_q") is None and st.get("v_low") is None
+    if factorize:
+        first = st.get("row_var_low") is None
+    else:
+        first = st.get("v_low_q") is None and st.get("v_low") is None
     vbits = 0 if (not quant or vqt == "fp32") else (16 if vqt == "al16" else 8)
-    if first:   # optimizer.py:2770-2779 creates the low-rank V state on the first step
+    low_shape = (R, rank) if right else (rank, C)
+    if factorize:   # optimizer.py:2693-2699 creates the row / column EMAs on the first step
+        if first:
+            st["row_var_low"] = torch.zeros((low_shape[0], 1), dtype=torch.float32, device=dev)
+            st["col_var_low"] = torch.zeros((1, low_shape[1]), dtype=torch.float32, device=dev)
+    elif first:   # optimizer.py:2770-2779 creates the low-rank V state on the first step
         if vbits:
             S.init_v_state(st, "v_low", (n_low,), bs, dev, vqt)
         else:
@@ -1118,6 +1130,17 @@ def _apollo_prep(opt, p, grad, st, group):
         fresh = True
     ent["proj"] = (proj_T.data_ptr(), proj_T._version)
     sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype == torch.bfloat16
+    if xmode:
+        xargs, xkeep = _apollo_x_args(opt, st, group, dev, ent["ws"], low_shape, n_low, factorize, came, first,
+                                      vbits, vqt, bs, has_m, m_fp32, mqt, mbs, quant, beta_val, beta1)
+        t = nat.ApolloTensor(
+            p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank, None, None, None, None, None, None, None,
+            nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
+            nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)),
+            int(first), int(fresh), int(step), float(bias_fac))
+        bkey = (p.dtype, sr, "x", has_m, True, mqt, 0, 0, float(beta_val), float(rho_val), bias_mode)
+        keep = (g, proj_T, rho_t, xkeep)
+        return bkey, t, (st, "x", bs, keep, xargs)
     t = nat.ApolloTensor(
         p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank,
         nat.ptr(st.get("v_low_q")) if vbits else None, nat.ptr(st.get("v_low_scale")) if vbits else None,
@@ -1130,7 +1153,69 @@ def _apollo_prep(opt, p, grad, st, group):
         int(first), int(fresh), int(step), float(bias_fac))
     bkey = (p.dtype, sr, vbits, has_m, m_fp32, mqt, int(mbs), int(bs), float(beta_val), float(rho_val), bias_mode)
     keep = (g, proj_T, rho_t)   # alive until the launch is queued
-    return bkey, t, (st, vbits, bs, keep)
+    return bkey, t, (st, vbits, bs, keep, None)
+
+
+def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, first, vbits, vqt, bs, has_m,
+                   m_fp32, mqt, mbs, quant, beta_val, beta1):
+    """Lazy factorised / CAME low-rank state (optimizer.py:2689-2758, 2800-2815)
+    and the a8_apollo_x_args record of one matrix."""
+    cqt = st.get("c_quant_type") or vqt
+    cbits = 0 if (not quant or cqt == "fp32") else (16 if cqt == "al16" else 8)
+    if came and not factorize and st.get("res_low_q") is None and st.get("res_low") is None:
+        if cbits:
+            S.init_v_state(st, "res_low", low_shape, bs, dev, cqt)
+        else:
+            st["res_low"] = torch.zeros(low_shape, dtype=torch.float32, device=dev)
+    if came and factorize:
+        rs, cs = (low_shape[0], 1), (1, low_shape[1])
+        if cbits:
+            if st.get("conf_row_low_q") is None:
+                S.init_v_state(st, "conf_row_low", rs, bs, dev, cqt)
+                S.init_v_state(st, "conf_col_low", cs, bs, dev, cqt)
+        elif st.get("conf_row_low") is None:
+            st["conf_row_low"] = torch.zeros(rs, dtype=torch.float32, device=dev)
+            st["conf_col_low"] = torch.zeros(cs, dtype=torch.float32, device=dev)
+    for k in ("row_var_low", "col_var_low", "m_low", "res_low", "conf_row_low", "conf_col_low", "v_low"):
+        if torch.is_tensor(st.get(k)) and not st[k].is_contiguous():
+            st[k] = st[k].contiguous()
+    key = (dev, "apollo_x", low_shape)
+    xws = opt._ws.get(key)
+    nx = int(nat.lib().a8_apollo_x_workspace_floats(low_shape[0], low_shape[1]))
+    if xws is None or xws.numel() < nx:
+        xws = torch.empty(nx, dtype=torch.float32, device=dev)
+        opt._ws[key] = xws
+    aeps = group.get("apollo_eps", 1e-6)
+    eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
+    P = nat.ptr
+    a = nat.ApolloXArgs(
+        ws.data_ptr(), ws.data_ptr() + 4 * n_low, xws.data_ptr(), low_shape[0], low_shape[1],
+        int(factorize), int(came), int(has_m), int(first),
+        P(st.get("v_low_q")) if (vbits and not factorize) else None,
+        P(st.get("v_low_scale")) if (vbits and not factorize) else None,
+        P(st.get("v_low_min_log")) if (vbits and not factorize) else None,
+        P(st.get("v_low")) if (not vbits and not factorize) else None, 0 if factorize else vbits, int(bs),
+        P(st.get("row_var_low")) if factorize else None, P(st.get("col_var_low")) if factorize else None,
+        P(st.get("m_low_q")) if (has_m and not m_fp32) else None,
+        P(st.get("m_low_scale")) if (has_m and not m_fp32) else None,
+        P(st.get("m_low")) if (has_m and m_fp32) else None,
+        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(mbs),
+        P(st.get("res_low_q")) if (came and not factorize and cbits) else None,
+        P(st.get("res_low_scale")) if (came and not factorize and cbits) else None,
+        P(st.get("res_low_min_log")) if (came and not factorize and cbits) else None,
+        P(st.get("res_low")) if (came and not factorize and not cbits) else None,
+        P(st.get("conf_row_low_q")) if (came and factorize and cbits) else None,
+        P(st.get("conf_row_low_scale")) if (came and factorize and cbits) else None,
+        P(st.get("conf_row_low_min_log")) if (came and factorize and cbits) else None,
+        P(st.get("conf_row_low")) if (came and factorize and not cbits) else None,
+        P(st.get("conf_col_low_q")) if (came and factorize and cbits) else None,
+        P(st.get("conf_col_low_scale")) if (came and factorize and cbits) else None,
+        P(st.get("conf_col_low_min_log")) if (came and factorize and cbits) else None,
+        P(st.get("conf_col_low")) if (came and factorize and not cbits) else None,
+        cbits if came else 0, float(beta_val), float(beta1) if has_m else 0.0,
+        float(group["beta3"]) if came else 0.0, _f32(aeps), _f32(eps_sq), _f32(math.log2(eps_sq)),
+        _f32(group.get("eps_came", 1e-16)), float(group["d"]))
+    return a, (xws, cbits)
 
 
 def _run_apollo_batch(opt, group, bkey, items):
@@ -1153,17 +1238,36 @@ def _run_apollo_batch(opt, group, bkey, items):
     wd = group["weight_decay"]
     wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
     fira = bool(group.get("enable_fira_for_apollo", True))
+    stream = nat.stream_of(pdev)
+    tail = (int(group.get("apollo_scale_type", "channel") == "channel"), float(group.get("apollo_scale", 1.0)),
+            int(bool(group.get("apollo_scale_front", False))), int(fira), float(group.get("fira_margin", 0.01)),
+            float(group["d"]), float(rho_val), _f32(group["eps"][1]), int(bool(group["scale_parameter"])),
+            bias_mode, _f32(wd), wd_mode, stream)
+    if vbits == "x":
+        # projection, the factorised / CAME low-rank stage per matrix, then scale and writeback
+        head = (nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
+                float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), 0, 2048, 8, 0, 1,
+                256)
+        nat.check(L.a8_apollo_step_multi_phase(1, *head, *tail), "a8_apollo_step_multi_phase(1)")
+        for _, (st, _vb, bsz, _keep, xargs) in items:
+            nat.check(L.a8_apollo_lowrank_x(ctypes.byref(xargs), stream), "a8_apollo_lowrank_x")
+        nat.check(L.a8_apollo_step_multi_phase(2, *head, *tail), "a8_apollo_step_multi_phase(2)")
+        for _, (st, _vb, bsz, keep, xargs) in items:
+            if xargs.v_bits:
+                _block_view(st, "v_low", bsz)
+            if xargs.c_bits and not xargs.factorize:
+                _block_view(st, "res_low", bsz)
+            if xargs.c_bits and xargs.factorize:
+                _block_view(st, "conf_row_low", bsz)
+                _block_view(st, "conf_col_low", bsz)
+        return
     rc = L.a8_apollo_step_multi(
         nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
         float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), vbits, int(bs),
-        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs),
-        int(group.get("apollo_scale_type", "channel") == "channel"), float(group.get("apollo_scale", 1.0)),
-        int(bool(group.get("apollo_scale_front", False))), int(fira), float(group.get("fira_margin", 0.01)),
-        float(group["d"]), float(rho_val), _f32(group["eps"][1]), int(bool(group["scale_parameter"])), bias_mode,
-        _f32(wd), wd_mode, nat.stream_of(pdev))
+        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs), *tail)
     nat.check(rc, "a8_apollo_step_multi")
     if vbits:
-        for _, (st, vb, bsz, _keep) in items:
+        for _, (st, vb, bsz, _keep, _x) in items:
             _block_view(st, "v_low", bsz)
 
 

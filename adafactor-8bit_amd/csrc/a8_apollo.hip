@@ -1238,7 +1238,11 @@ static void launch_low(int mkt, unsigned nb, const ApDesc& one, const ApDesc* ta
 
 static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 5 * sizeof(int32_t)); }
 
-static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int n, void* table_dev,
+// phase 0: the whole step; 1: projection (and the norms of G) only, leaving
+// g_low in workspace[0, n_low); 2: scale, scalars and writeback from the update
+// the caller wrote to workspace[n_low, 2 n_low) (the factorised / CAME low-rank
+// stage of a8_apollo_lowrank_x runs between the two).
+static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tensor* ts, int n, void* table_dev,
                       int64_t tbytes, double beta_val, double beta1, int has_m, float apollo_eps, float log_floor,
                       int v_bits, int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
                       float apollo_scale, int scale_front, int fira, float fira_margin, float d, float lr_val,
@@ -1264,9 +1268,10 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
     if (!t.param || !t.grad || !t.proj_t || !t.workspace) return set_error(A8_ERR_ARG, "null pointer");
     if (t.rows <= 0 || t.cols <= 0 || t.rank <= 0) return set_error(A8_ERR_SIZE, "empty APOLLO tensor");
     if (t.rows * t.cols >= ((int64_t)1 << 31)) return set_error(A8_ERR_SIZE, "APOLLO tensor too large");
-    if (v_bits ? !(t.v_q && t.v_scale && t.v_min_log) : !t.v_fp32)
+    if (phase == 0 && (v_bits ? !(t.v_q && t.v_scale && t.v_min_log) : !t.v_fp32))
       return set_error(A8_ERR_ARG, "APOLLO V state missing");
-    if (has_m && (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale))) return set_error(A8_ERR_ARG, "APOLLO M state missing");
+    if (phase == 0 && has_m && (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale)))
+      return set_error(A8_ERR_ARG, "APOLLO M state missing");
     if (fira && !t.fira_prev) return set_error(A8_ERR_ARG, "APOLLO Fira needs scaled_grad_norm_prev");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.workspace))
       return set_error(A8_ERR_ALIGN, "APOLLO param, grad and workspace must be 16-byte aligned");
@@ -1316,7 +1321,9 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
   h.scale_param = scale_parameter ? 1 : 0; h.bias_mode = bias_mode; h.wd_mode = wd_mode;
   int rc;
   // projection (+ channel norms of G)
-  if (dtype == A8_BF16) {
+  if (phase == 2) {
+    // the projection ran in phase 1
+  } else if (dtype == A8_BF16) {
     for (int i = 0; i < n; ++i) {
       if (!ts[i].proj_fresh) continue;
       const ApDesc& D = tab[(size_t)i];
@@ -1355,11 +1362,14 @@ static int apollo_run(int dtype, int stochastic, const a8_apollo_tensor* ts, int
       if ((rc = check_launch("k_ap_fixlow"))) return rc;
     }
   }
-  const int mkt = !has_m ? 0 : (m_fp32 ? 3 : (h.mk == 1 ? 1 : 2));
-  if (v_bits == 8) launch_low<8>(mkt, (unsigned)nunit, one, dtab, n, h, st);
-  else if (v_bits == 16) launch_low<16>(mkt, (unsigned)nunit, one, dtab, n, h, st);
-  else launch_low<0>(mkt, (unsigned)nunit, one, dtab, n, h, st);
-  if ((rc = check_launch("k_ap_low"))) return rc;
+  if (phase == 1) return 0;
+  if (phase == 0) {
+    const int mkt = !has_m ? 0 : (m_fp32 ? 3 : (h.mk == 1 ? 1 : 2));
+    if (v_bits == 8) launch_low<8>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+    else if (v_bits == 16) launch_low<16>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+    else launch_low<0>(mkt, (unsigned)nunit, one, dtab, n, h, st);
+    if ((rc = check_launch("k_ap_low"))) return rc;
+  }
   hipLaunchKernelGGL(k_ap_scale, dim3((unsigned)nsc), dim3(256), 0, st, one, dtab, n, h);
   if ((rc = check_launch("k_ap_scale"))) return rc;
   hipLaunchKernelGGL(k_ap_scalars, dim3((unsigned)n), dim3(256), 0, st, one, dtab, n, h);
@@ -1399,7 +1409,7 @@ int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int fir
   one.proj_fresh = proj_fresh;
   one.step = sr_step;
   one.bias_factor = bias_factor;
-  return apollo_run(dtype, stochastic, &one, 1, nullptr, 0, beta_val, beta1, has_m, apollo_eps, log_floor, v_bits,
+  return apollo_run(0, dtype, stochastic, &one, 1, nullptr, 0, beta_val, beta1, has_m, apollo_eps, log_floor, v_bits,
                     block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale, scale_front, fira,
                     fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay, wd_mode, stream);
 }
@@ -1410,10 +1420,23 @@ int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* ts, 
                          int m_block_size, int channel, float apollo_scale, int scale_front, int fira,
                          float fira_margin, float d, float lr_val, float eps2, int scale_parameter, int bias_mode,
                          float weight_decay, int wd_mode, void* stream) {
-  return apollo_run(dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m, apollo_eps,
+  return apollo_run(0, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m, apollo_eps,
                     log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale,
                     scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay,
                     wd_mode, stream);
+}
+
+int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_apollo_tensor* ts, int ntensors,
+                               void* table_dev, int64_t table_bytes_, double beta_val, double beta1, int has_m,
+                               float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits, int m_mode,
+                               int m_fp32, int m_block_size, int channel, float apollo_scale, int scale_front,
+                               int fira, float fira_margin, float d, float lr_val, float eps2, int scale_parameter,
+                               int bias_mode, float weight_decay, int wd_mode, void* stream) {
+  if (phase != 1 && phase != 2) return set_error(A8_ERR_ARG, "phase must be 1 (projection) or 2 (finish)");
+  return apollo_run(phase, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m,
+                    apollo_eps, log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel,
+                    apollo_scale, scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode,
+                    weight_decay, wd_mode, stream);
 }
 
 }  // extern "C"

@@ -316,6 +316,74 @@ int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tens
                          float weight_decay, int wd_mode, void* stream);
 int64_t a8_apollo_table_bytes(int ntensors);
 
+/* a8_apollo_step_multi split around the low-rank stage, for the factorised and
+ * CAME variants (optimizer.py:2689-2896) whose stage is a8_apollo_lowrank_x.
+ * phase 1: projection g_low = G P^T / P^T G into workspace[0, n_low) (n_low =
+ * max(rows, cols) * rank; row-major rows x rank on the right side, rank x cols on
+ * the left) plus the norms of G (and of p for scale_parameter); V / M fields of
+ * the records and v_bits, m_* are not used.  phase 2: channel (or tensor) scale
+ * of the update the caller wrote to workspace[n_low, 2 n_low) against g_low,
+ * Fira, alpha, step and writeback, with the same arguments as phase 1. */
+int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_apollo_tensor* tensors,
+                               int ntensors, void* table_dev, int64_t table_bytes, double beta_val, double beta1,
+                               int has_m, float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits,
+                               int m_mode, int m_fp32, int m_block_size, int channel, float apollo_scale,
+                               int scale_front, int fira, float fira_margin, float d, float lr_val, float eps2,
+                               int scale_parameter, int bias_mode, float weight_decay, int wd_mode, void* stream);
+
+/* Low-rank state and hyper-parameters of one matrix for a8_apollo_lowrank_x.
+ * Coded states are AL8 (uint8) / AL16 (int16) codes with per-block scale and
+ * min_log (blocks of block_size), zero codes in a fresh state. */
+typedef struct a8_apollo_x_args {
+  const float* g_low;      /* rows_low x cols_low, row-major (phase-1 workspace) */
+  float* u;                /* out: the low-rank update, same layout */
+  float* xws;              /* a8_apollo_x_workspace_floats(rows_low, cols_low) floats */
+  int64_t rows_low, cols_low;
+  int factorize;           /* apollo_factorize */
+  int came;                /* beta3 set */
+  int has_m;               /* beta1 set */
+  int first_step;          /* no low-rank second moment yet (V or row / column EMA) */
+  /* non-factorised V: codes (v_bits 8 / 16) or fp32 (v_bits 0), n_low values */
+  void* v_q;
+  float* v_scale;
+  float* v_min_log;
+  float* v_fp32;
+  int v_bits;
+  int block_size;          /* AL block of V, residual and confidence codes */
+  /* factorised V: fp32 row (rows_low) and column (cols_low) EMAs */
+  float* row_var;
+  float* col_var;
+  /* momentum: codes (m_q, m_scale) or fp32 m_fp32 (non-null selects it) */
+  uint8_t* m_q;
+  float* m_scale;
+  float* m_fp32;
+  int m_bits, m_mode, m_block_size;
+  /* CAME, non-factorised: residual EMA (n_low values), codes or fp32 */
+  void* res_q;
+  float* res_scale;
+  float* res_min_log;
+  float* res_fp32;
+  /* CAME, factorised: row (rows_low) and column (cols_low) confidence EMAs */
+  void* crow_q;
+  float* crow_scale;
+  float* crow_min_log;
+  float* crow_fp32;
+  void* ccol_q;
+  float* ccol_scale;
+  float* ccol_min_log;
+  float* ccol_fp32;
+  int c_bits;              /* 0: fp32 residual / confidence */
+  double beta_v, beta1, beta3;
+  float apollo_eps, eps_sq, log_floor, eps_came, d;
+} a8_apollo_x_args;
+
+/* Replaces the factorised (apollo_factorize, optimizer.py:2689-2758) and CAME
+ * (beta3, optimizer.py:2800-2896) low-rank stages of _update_param_apollo, in
+ * the arithmetic of its CPU branches: second-moment EMA, RMS clip (d > 0),
+ * momentum EMA, residual / confidence EMAs, and the update u = update_low. */
+int a8_apollo_lowrank_x(const a8_apollo_x_args* args, void* stream);
+int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low);
+
 /* Replaces dequantize_log_nonneg (kernels.cu:2593-2632; called by
  * _log_dequantize_nonneg, optimizer.py:328-338): output[i] = 0 for code 0, else
  * 2^(((q-1) * scale[b]) / (L-2) + min_log[b]) with b = i / block_size, L = 256

@@ -427,6 +427,13 @@ class OracleOptimizer:
             st["m_quant_type"] = mqt
             for k in ("v_low_q", "v_low_scale", "v_low_min_log", "v_low_shape", "v_low_pad", "v_low"):
                 st[k] = None
+            if h["beta3"] is not None:   # optimizer.py:1740-1748
+                names = ("conf_row_low", "conf_col_low") if h["apollo_factorize"] else ("res_low",)
+                for nm in names:
+                    for suf in ("_q", "_scale", "_min_log", "_shape", "_pad"):
+                        st[nm + suf] = None
+                for nm in names:
+                    st[nm] = None
             return
         if p.dim() >= 2 and h["factored"]:
             R, C = p.shape[-2], p.shape[-1]
@@ -657,13 +664,11 @@ def init_m_prefix(st, numel, m_block, mqt, prefix):
 
 @torch.no_grad()
 def apollo_update(opt, p, grad, st):
-    """``_update_param_apollo`` (optimizer.py:2587-3084), CPU branches, for the
-    non-factorised path without CAME (apollo_factorize=False, beta3=None) and
-    deterministic writeback."""
+    """``_update_param_apollo`` (optimizer.py:2587-3084), CPU branches (the
+    reference with no CUDA module), deterministic writeback: plain, factorised
+    (apollo_factorize) and CAME (beta3) low-rank updates."""
     h = opt.hp
     beta1, beta2, beta2_decay = h["beta1"], h["beta2"], h["beta2_decay"]
-    if h["apollo_factorize"] or h["beta3"] is not None:
-        raise NotImplementedError("oracle: factorised / CAME APOLLO")
     if h["stochastic_round_writeback"] and p.dtype in (torch.bfloat16, torch.float16):
         raise NotImplementedError("oracle: SR writeback (its CPU RNG stream is not the GPU's)")
     d, lr = h["d"], h["lr"]
@@ -697,6 +702,18 @@ def apollo_update(opt, p, grad, st):
     aeps = h["apollo_eps"]
     eps_sq = max(aeps * aeps, LOG_QUANT_FLOOR)
     lf = math.log2(eps_sq)
+    if h["apollo_factorize"]:
+        upd = apollo_low_factorised(st, glow, h, bv, beta1, mqt, quant)
+    else:
+        upd = _apollo_low_plain(st, glow, h, bv, beta1, mqt, quant, first, bs, eps_sq, lf)
+    _apollo_finish(opt, st, pw, gw, glow, upd, alpha, rho, step, right, need_norm)
+
+
+def _apollo_low_plain(st, glow, h, bv, beta1, mqt, quant, first, bs, eps_sq, lf):
+    """Non-factorised low-rank V EMA and update (optimizer.py:2759-2951, CPU
+    branches); with beta3 the CAME residual path of optimizer.py:2800-2896."""
+    vqt = st.get("v_quant_type", "al8")
+    aeps = h["apollo_eps"]
     if first:
         vinit = glow.flatten().square() * bv
         if quant and vqt != "fp32":
@@ -713,6 +730,8 @@ def apollo_update(opt, p, grad, st):
         st["v_low"].lerp_(glow.flatten().square(), bv)
         vdeq = st["v_low"]
 
+    if h["beta3"] is not None and beta1 is not None:
+        return _apollo_came_low(st, glow, vdeq, h, beta1, mqt, quant, bs, eps_sq)
     if beta1 is not None:
         if not quant or mqt == "fp32":
             if st.get("m_low") is None:
@@ -724,10 +743,126 @@ def apollo_update(opt, p, grad, st):
             if st.get("m_low_q") is None:
                 init_m_prefix(st, glow.numel(), mbs, mqt, "m_low")
             mdeq = m_ema_prefix(st, glow, beta1, mqt, mbs, "m_low")
-        upd = mdeq / (torch.sqrt(vdeq.view_as(glow)) + aeps)
-    else:
-        upd = glow / (torch.sqrt(vdeq).view_as(glow) + aeps)
+        return mdeq / (torch.sqrt(vdeq.view_as(glow)) + aeps)
+    return glow / (torch.sqrt(vdeq).view_as(glow) + aeps)
 
+
+def apollo_m_ema(st, x, beta1, mqt, mbs, quant, prefix="m_low"):
+    """``_apollo_m_ema`` (optimizer.py:714-729) without the CUDA module: fp32 m
+    through lerp_, codes through ``_m_ema_pytorch``."""
+    if not quant or mqt == "fp32":
+        if st.get(prefix) is None:
+            st[prefix] = torch.zeros_like(x)
+        st[prefix].lerp_(x, 1.0 - beta1)
+        return st[prefix]
+    if st.get(f"{prefix}_q") is None:
+        init_m_prefix(st, x.numel(), mbs, mqt, prefix)
+    return m_ema_prefix(st, x, beta1, mqt, mbs, prefix)
+
+
+def _clip_rms(u, d):
+    """``U.div_(clamp(rms(U) / d, min=1))`` (optimizer.py:2715-2717, 2869-2871)."""
+    if d > 0:
+        rms = torch.linalg.vector_norm(u) / math.sqrt(u.numel())
+        u.div_(torch.clamp(rms / d, min=1.0))
+    return u
+
+
+def _apollo_came_low(st, glow, vdeq, h, beta1, mqt, quant, bs, eps_sq):
+    """CAME on the low-rank gradient, non-factorised (optimizer.py:2800-2896, the
+    branch taken without the CUDA module): U = g / sqrt(max(v, eps^2)) with RMS
+    clipping, m EMA of U, residual EMA (beta3) of (U - m)^2 + eps_came in fp32 or
+    AL codes (read back decoded), u = m / sqrt(max(res, eps^2))."""
+    beta3 = h["beta3"]
+    cqt = st.get("c_quant_type", st.get("v_quant_type", "al8"))
+    mbs = st.get("m_block_size", h["m_block_size"])
+    if st.get("res_low_q") is None and st.get("res_low") is None:
+        if quant and cqt != "fp32":
+            init_v(st, "res_low", tuple(glow.shape), bs, cqt, True)
+        else:
+            st["res_low"] = torch.zeros_like(glow)
+    u = glow * vdeq.view_as(glow).clamp(min=eps_sq).rsqrt()
+    _clip_rms(u, h["d"])
+    m = apollo_m_ema(st, u, beta1, mqt, mbs, quant)
+    res = u.sub(m).square_().add_(h["eps_came"])
+    del u
+    if quant and cqt != "fp32":
+        rd = deq_v(st, "res_low")
+        rd.lerp_(res, 1.0 - beta3)
+        quant_v(st, "res_low", rd, bs, cqt)
+        rd = deq_v(st, "res_low")
+    else:
+        st["res_low"].lerp_(res, 1.0 - beta3)
+        rd = st["res_low"]
+    return m * rd.view_as(glow).clamp(min=eps_sq).rsqrt()
+
+
+def apollo_low_factorised(st, glow, h, bv, beta1, mqt, quant):
+    """Factorised low-rank second moment (optimizer.py:2689-2758): row / column
+    means of g^2 (+ FLT_MIN) into fp32 EMAs, v = r c / max(mean r, eps);
+    u = x / (sqrt(v) + eps) with x = g or its momentum; with beta3 the CAME form
+    with row / column confidence EMAs of the residual."""
+    aeps, beta3 = h["apollo_eps"], h["beta3"]
+    gsq = glow.square()
+    row_mean = gsq.mean(dim=-1, keepdim=True).add_(LOG_QUANT_FLOOR)
+    col_mean = gsq.mean(dim=-2, keepdim=True).add_(LOG_QUANT_FLOOR)
+    del gsq
+    if "row_var_low" not in st:
+        st["row_var_low"] = row_mean * bv
+        st["col_var_low"] = col_mean * bv
+    else:
+        st["row_var_low"].mul_(1.0 - bv).add_(row_mean, alpha=bv)
+        st["col_var_low"].mul_(1.0 - bv).add_(col_mean, alpha=bv)
+    rv, cv = st["row_var_low"], st["col_var_low"]
+    v_est = rv.mul(cv).div_(rv.mean(dim=-2, keepdim=True).clamp_(min=aeps))
+    mbs = st.get("m_block_size", h["m_block_size"])
+    if beta1 is None:
+        return glow / (torch.sqrt(v_est) + aeps)
+    if beta3 is None:
+        m = apollo_m_ema(st, glow, beta1, mqt, mbs, quant)
+        return m / (torch.sqrt(v_est) + aeps)
+    rmv = rv.mean(dim=-2, keepdim=True).clamp(min=LOG_QUANT_FLOOR)
+    inv_row = (rv / rmv).rsqrt_()
+    inv_col = cv.rsqrt()
+    u = glow.mul(inv_row).mul_(inv_col)
+    _clip_rms(u, h["d"])
+    m = apollo_m_ema(st, u, beta1, mqt, mbs, quant)
+    res = u.sub(m).square_().add_(h["eps_came"])
+    del u
+    res_row = res.mean(dim=-1, keepdim=True)
+    res_col = res.mean(dim=-2, keepdim=True)
+    bs = st.get("block_size", h["block_size"])
+    cqt = st.get("c_quant_type", st.get("v_quant_type", "al8"))
+    if quant and cqt != "fp32":
+        if st.get("conf_row_low_q") is None:
+            init_v(st, "conf_row_low", tuple(res_row.shape), bs, cqt, True)
+            init_v(st, "conf_col_low", tuple(res_col.shape), bs, cqt, True)
+        c_row = deq_v(st, "conf_row_low")
+        c_col = deq_v(st, "conf_col_low")
+        c_row.lerp_(res_row, 1.0 - beta3)
+        c_col.lerp_(res_col, 1.0 - beta3)
+        quant_v(st, "conf_row_low", c_row, bs, cqt)
+        quant_v(st, "conf_col_low", c_col, bs, cqt)
+    else:
+        if st.get("conf_row_low") is None:
+            st["conf_row_low"] = torch.zeros_like(res_row)
+            st["conf_col_low"] = torch.zeros_like(res_col)
+        st["conf_row_low"].lerp_(res_row, 1.0 - beta3)
+        st["conf_col_low"].lerp_(res_col, 1.0 - beta3)
+        c_row, c_col = st["conf_row_low"], st["conf_col_low"]
+    crm = c_row.mean(dim=-2, keepdim=True).clamp(min=LOG_QUANT_FLOOR)
+    icr = (c_row / crm).rsqrt_()
+    icc = c_col.rsqrt()
+    return m * icr * icc
+
+
+def _apollo_finish(opt, st, pw, gw, glow, upd, alpha, rho, step, right, need_norm):
+    """Channel / tensor scale, Fira, RMS denominator, bias correction and the
+    deterministic writeback of _update_param_apollo (optimizer.py:2995-3084)."""
+    h = opt.hp
+    beta1, beta2 = h["beta1"], h["beta2"]
+    d = h["d"]
+    fira = h["enable_fira_for_apollo"]
     channel = h["apollo_scale_type"] == "channel"
     nd = -1 if right else -2
     if channel:

@@ -93,6 +93,27 @@ CONFIGS = [
      P_APOLLO, "student_t", 5, (1, 5)),
     ("apollo_fp32_states", dict(APOLLO, lr=1e-3, quantize=False), P_APOLLO, "logscale", 4, (1, 4)),
     ("apollo_bf16_det", dict(APOLLO, lr=1e-3), P_APOLLO, "normal_zeros", 4, (1, 4), "bf16"),
+    # CAME on the low-rank gradient (beta3) and the factorised low-rank second moment
+    ("apollo_came_uf8_al8", dict(APOLLO, lr=1e-3, beta3=0.9999, d=1.0, eps_came=1e-16),
+     P_APOLLO, "normal_zeros", 5, (1, 2, 5)),
+    ("apollo_came_al16_tensor", dict(APOLLO, lr=1e-3, beta3=0.99, d=1.0, eps_came=1e-16,
+                                     v_quant_type="al16", c_quant_type="al16", m_quant_type="uf4",
+                                     apollo_scale_type="tensor", weight_decay=0.1),
+     P_APOLLO, "student_t", 4, (1, 4)),
+    ("apollo_came_fp32", dict(APOLLO, lr=1e-3, beta3=0.9999, d=1.0, eps_came=1e-16, quantize=False),
+     P_APOLLO, "logscale", 4, (1, 4)),
+    ("apollo_fact_uf8", dict(APOLLO, lr=1e-3, apollo_factorize=True), P_APOLLO, "student_t", 5,
+     (1, 2, 5)),
+    ("apollo_fact_nomom", dict(APOLLO, lr=1e-3, apollo_factorize=True, beta1=None, beta2=None,
+                               beta2_decay=-0.8, relative_step=False, d=1.0,
+                               apollo_scale_type="tensor"), P_APOLLO, "logscale", 4, (1, 4)),
+    ("apollo_fact_came", dict(APOLLO, lr=1e-3, apollo_factorize=True, beta3=0.9999, d=1.0,
+                              eps_came=1e-16), P_APOLLO, "normal_zeros", 5, (1, 2, 5)),
+    ("apollo_fact_came_fp32", dict(APOLLO, lr=1e-3, apollo_factorize=True, beta3=0.999, d=1.0,
+                                   eps_came=1e-16, quantize=False, weight_decay=0.05,
+                                   scale_weight_decay=True), P_APOLLO, "student_t", 4, (1, 4)),
+    ("apollo_came_bf16", dict(APOLLO, lr=1e-3, beta3=0.9999, d=1.0, eps_came=1e-16), P_APOLLO,
+     "normal_zeros", 4, (1, 4), "bf16"),
 ]
 
 

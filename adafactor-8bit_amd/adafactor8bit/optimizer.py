@@ -1041,12 +1041,15 @@ def _apollo_prep(opt, p, grad, st, group):
     if came and beta1 is None:
         raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update instability.")
     xmode = factorize or came
-    if p.dtype not in (torch.float32, torch.bfloat16):
-        raise NotImplementedError("adafactor8bit: APOLLO needs fp32 or bf16 parameters")
+    if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise NotImplementedError("adafactor8bit: APOLLO needs fp32, bf16 or fp16 parameters")
     if not p.is_contiguous():
         raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
     g = grad if grad.is_contiguous() else grad.contiguous()
-    if g.dtype != p.dtype:
+    if p.dtype == torch.float16:
+        # the projection runs on fp32 G, as the reference's grad.float() (optimizer.py:2601)
+        g = g.float()
+    elif g.dtype != p.dtype:
         if p.dtype == torch.float32:
             g = g.float()
         else:
@@ -1129,7 +1132,7 @@ def _apollo_prep(opt, p, grad, st, group):
     if ent["proj"] is None or ent["proj"] != (proj_T.data_ptr(), proj_T._version):
         fresh = True
     ent["proj"] = (proj_T.data_ptr(), proj_T._version)
-    sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype == torch.bfloat16
+    sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype in (torch.bfloat16, torch.float16)
     if xmode:
         xargs, xkeep = _apollo_x_args(opt, st, group, dev, ent["ws"], low_shape, n_low, factorize, came, first,
                                       vbits, vqt, bs, has_m, m_fp32, mqt, mbs, quant, beta_val, beta1)

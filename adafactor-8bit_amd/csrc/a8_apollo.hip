@@ -1117,7 +1117,9 @@ __device__ __forceinline__ float ap_fch(const float* fin, int64_t ch, float fs, 
   return f;
 }
 
-template <typename T, bool SR>
+// GT: the gradient's element type (the parameter's, or fp32 for fp16 params,
+// whose projection runs on an fp32 copy of G).
+template <typename T, bool SR, typename GT = T>
 __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   int unit;
   const ApDesc D = ap_pick(one, tab, ntab, 4, (int)blockIdx.x, unit);
@@ -1130,11 +1132,11 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
   const float step = gp(sl)[0], dec = gp(sl)[1], fin_t = gp(sl)[3], fs = gp(sl)[6];
   const bool has_dec = h.wd_mode != 0;
   T* P = reinterpret_cast<T*>(D.param);
-  const T* G = reinterpret_cast<const T*>(D.grad);
+  const GT* G = reinterpret_cast<const GT*>(D.grad);
   const uint32_t e0 = (uint32_t)unit * kApApp + threadIdx.x * 8u;
   if (e0 >= n) return;
   float g[8], p[8], f[8];
-  load8<T>(G, e0, n, g);
+  load8<GT>(G, e0, n, g);
   load8<T>(P, e0, n, p);
   const uint32_t row = e0 / C, col = e0 - row * C;
   if (!h.channel) {
@@ -1166,7 +1168,11 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
       float x = p[k];
       if (has_dec) x = x * dec;
       x = x + (scrub(g[k]) * f[k]) * step;
-      w[k >> 1] |= (uint32_t)sr_bf16_bits(x, sr_bits_at(base, (uint64_t)(e0 + k))) << (16 * (k & 1));
+      const uint32_t bits = sr_bits_at(base, (uint64_t)(e0 + k));
+      uint16_t hb;
+      if constexpr (std::is_same<T, __half>::value) hb = sr_fp16(x, (float)(bits >> 8) * (1.0f / 16777216.0f));
+      else hb = sr_bf16_bits(x, bits);
+      w[k >> 1] |= (uint32_t)hb << (16 * (k & 1));
     }
     if (e0 + 8 <= n) {
       *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P) + e0)) = u32x4{w[0], w[1], w[2], w[3]};
@@ -1250,7 +1256,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
                       void* stream) {
   if (n <= 0) return 0;
   if (!ts) return set_error(A8_ERR_ARG, "null tensor list");
-  if (dtype != A8_F32 && dtype != A8_BF16) return set_error(A8_ERR_DTYPE, "APOLLO supports fp32 and bf16 params");
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16)
+    return set_error(A8_ERR_DTYPE, "APOLLO supports fp32, bf16 and fp16 params");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
   auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
   if (v_bits && !(pow2(block_size) && block_size >= 128 && block_size <= 2048))
@@ -1284,7 +1291,7 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     D.R = t.rows; D.C = t.cols; D.r = t.rank;
     D.sr_seed = t.sr_seed; D.step = t.step; D.bias_factor = t.bias_factor;
     D.first = t.first_step ? 1 : 0; D.has_prev = t.has_fira_prev ? 1 : 0;
-    D.valign = (t.cols % (dtype == A8_F32 ? 4 : 8)) == 0 ? 1 : 0;
+    D.valign = (t.cols % 8) == 0 ? 1 : 0;   // a k_ap_apply unit (8 elements) stays in one row
     D.rtile_begin = (int32_t)nrt; D.ltile_begin = (int32_t)nlt; D.unit_begin = (int32_t)nunit;
     D.sc_begin = (int32_t)nsc; D.app_begin = (int32_t)napp; D.pad_ = 0;
     first[(size_t)i] = D.rtile_begin;
@@ -1355,8 +1362,13 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       const ApDesc& D = tab[(size_t)i];
       const ApL L = ap_layout(D.R, D.C, D.r);
       if ((rc = ap_sgemm(hb, D, L, st))) return rc;
-      hipLaunchKernelGGL(k_ap_norm32, dim3((unsigned)L.ntr), dim3(256), 0, st, D, h.scale_param);
+      hipLaunchKernelGGL(k_ap_norm32, dim3((unsigned)L.ntr), dim3(256), 0, st, D,
+                         dtype == A8_F32 ? h.scale_param : 0);
       if ((rc = check_launch("k_ap_norm32"))) return rc;
+      if (dtype == A8_F16 && h.scale_param) {   // ||p||^2 of the fp16 parameter (after k_ap_norm32's zeros)
+        hipLaunchKernelGGL(k_ap_psq<__half>, dim3((unsigned)L.ntr), dim3(256), 0, st, D);
+        if ((rc = check_launch("k_ap_psq"))) return rc;
+      }
       const int64_t nf = (L.n_low + 255) / 256;
       hipLaunchKernelGGL(k_ap_fixlow, dim3((unsigned)(nf < 1024 ? nf : 1024)), dim3(256), 0, st, D);
       if ((rc = check_launch("k_ap_fixlow"))) return rc;
@@ -1376,6 +1388,10 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   if ((rc = check_launch("k_ap_scalars"))) return rc;
   if (dtype == A8_F32)
     hipLaunchKernelGGL((k_ap_apply<float, false>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  else if (dtype == A8_F16 && stochastic)
+    hipLaunchKernelGGL((k_ap_apply<__half, true, float>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  else if (dtype == A8_F16)
+    hipLaunchKernelGGL((k_ap_apply<__half, false, float>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
   else if (stochastic)
     hipLaunchKernelGGL((k_ap_apply<__hip_bfloat16, true>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
   else

@@ -255,8 +255,9 @@ int64_t a8_table_bytes_2d(int ntensors);
  * One full-rank matrix (a 2-D view: rows x cols; higher-rank parameters are
  * viewed as [shape[0], -1]) per call. */
 typedef struct a8_apollo_tensor {
-  void* param;             /* fp32 or bf16, rows x cols */
-  const void* grad;        /* same dtype as param */
+  void* param;             /* fp32, bf16 or fp16, rows x cols */
+  const void* grad;        /* same dtype as param; fp32 for fp16 params (the reference
+                              projects grad.float(), optimizer.py:2601) */
   int64_t rows, cols;
   const float* proj_t;     /* projection P^T, fp32: right side (rows >= cols) [cols x rank],
                               left side [rank x rows] (P = stable_randn / sqrt(rank)) */

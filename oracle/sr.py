@@ -66,3 +66,57 @@ def sr_round_bf16(x: np.ndarray, seed: int, step: int, idx=None) -> np.ndarray:
     if idx is None:
         idx = np.arange(x.size, dtype=np.uint64)
     return sr_fp32_to_bf16_bits(x, sr_uniform(seed, step, idx))
+
+
+def _fp16_next_up(h):
+    """kernels.cu:88-92 on fp16 bit patterns (uint16 arrays)."""
+    h = np.asarray(h, dtype=np.uint16)
+    up = np.where(h & np.uint16(0x8000), h - np.uint16(1), h + np.uint16(1)).astype(np.uint16)
+    up = np.where(h == 0x8000, np.uint16(0x0001), up)
+    return np.where(h == 0x7C00, h, up).astype(np.uint16)
+
+
+def _fp16_next_down(h):
+    """kernels.cu:94-98 on fp16 bit patterns."""
+    h = np.asarray(h, dtype=np.uint16)
+    dn = np.where(h & np.uint16(0x8000), h + np.uint16(1), h - np.uint16(1)).astype(np.uint16)
+    dn = np.where(h == 0x0000, np.uint16(0x8001), dn)
+    return np.where(h == 0xFC00, h, dn).astype(np.uint16)
+
+
+def sr_fp32_to_fp16_bits(x: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """kernels.cu:100-131: the fp16 bit pattern of x rounded stochastically with u.
+    Inf / NaN keep their class (quiet NaN 0x7E00 with x's sign); |x| > 65504
+    saturates to the largest finite fp16; a value fp16 holds exactly is kept;
+    otherwise the round-to-nearest result q and its neighbour on x's other side
+    bracket x as lo < x < hi and x goes up with probability (x - lo) / (hi - lo),
+    computed in fp32."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    u = np.asarray(u, dtype=np.float32).reshape(-1)
+    b = x.view(np.uint32)
+    sign = np.where(b & np.uint32(0x80000000), np.uint16(0x8000), np.uint16(0)).astype(np.uint16)
+    special = (b & np.uint32(0x7F800000)) == 0x7F800000
+    is_nan = special & ((b & np.uint32(0x007FFFFF)) != 0)
+    with np.errstate(over="ignore", invalid="ignore"):
+        q = x.astype(np.float16)                    # round to nearest, ties to even
+        qb = q.view(np.uint16)
+        qf = q.astype(np.float32)
+        below = qf < x
+        lo_b = np.where(below, qb, _fp16_next_down(qb)).astype(np.uint16)
+        hi_b = np.where(below, _fp16_next_up(qb), qb).astype(np.uint16)
+        lo = lo_b.view(np.float16).astype(np.float32)
+        hi = hi_b.view(np.float16).astype(np.float32)
+        prob = (x - lo) / (hi - lo)
+        out = np.where(u < prob, hi_b, lo_b).astype(np.uint16)
+    out = np.where(qf == x, qb, out)
+    out = np.where(np.abs(x) > np.float32(65504.0), sign | np.uint16(0x7BFF), out)
+    out = np.where(special, np.where(is_nan, sign | np.uint16(0x7E00), sign | np.uint16(0x7C00)), out)
+    return out.astype(np.uint16)
+
+
+def sr_round_fp16(x: np.ndarray, seed: int, step: int, idx=None) -> np.ndarray:
+    """fp16 bits of x (flat, float32) rounded with the stream of (seed, step)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if idx is None:
+        idx = np.arange(x.size, dtype=np.uint64)
+    return sr_fp32_to_fp16_bits(x, sr_uniform(seed, step, idx))

@@ -114,6 +114,11 @@ CONFIGS = [
                                    scale_weight_decay=True), P_APOLLO, "student_t", 4, (1, 4)),
     ("apollo_came_bf16", dict(APOLLO, lr=1e-3, beta3=0.9999, d=1.0, eps_came=1e-16), P_APOLLO,
      "normal_zeros", 4, (1, 4), "bf16"),
+    # fp16 parameters: projection of grad.float(), fp16 rounding of the decayed and updated values
+    ("apollo_fp16_det", dict(APOLLO, lr=1e-3, weight_decay=0.1, scale_weight_decay=True), P_APOLLO,
+     "normal_zeros", 4, (1, 4), "fp16"),
+    ("apollo_fp16_tensor", dict(APOLLO, lr=1e-3, apollo_scale_type="tensor", scale_parameter=True,
+                                relative_step=True, d=1.0), P_APOLLO, "student_t", 4, (1, 4), "fp16"),
 ]
 
 
@@ -125,7 +130,7 @@ def _to_np(v):
 
 
 def run_config(mod, name, kwargs, pspecs, gkind, steps, save_steps, pdtype="f32", outdir=".", seed=0):
-    dt = torch.bfloat16 if pdtype == "bf16" else torch.float32
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16}.get(pdtype, torch.float32)
     params = []
     for i, (shape, init) in enumerate(pspecs):
         params.append(torch.nn.Parameter(make_param(shape, i, seed, kind=init).to(dt)))

@@ -26,7 +26,7 @@ def load(name):
 
 
 def param_dtype(meta):
-    return torch.bfloat16 if meta.get("dtype", "f32") == "bf16" else torch.float32
+    return {"bf16": torch.bfloat16, "fp16": torch.float16}.get(meta.get("dtype", "f32"), torch.float32)
 
 
 def init_params(meta, device="cpu", dtype=None):

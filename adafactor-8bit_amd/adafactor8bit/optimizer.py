@@ -329,6 +329,8 @@ class Adafactor8Bit(Optimizer):
             plan = _plan_param(p, g, st, group)
             if plan.path == "q1d_fp32m":
                 _prep_q1d_fp32m(self, plan)
+            elif plan.path == "f1d_qm":
+                _prep_f1d_qm(self, plan)
             key = plan.batch_key()
             if key is None:
                 _run_single(self, plan)
@@ -347,13 +349,13 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf")
 
     def batch_key(self):
         if self.path == "factored":
             return ("factored", self.p.device, self.p.dtype, self.g.dtype, self.step, self.quant,
                     self.vqt, self.bs, self.has_m, self.mqt, self.mbs, self.sr, self.beta3)
-        if self.path not in ("q1d", "f1d", "sgd"):
+        if self.path not in ("q1d", "f1d", "sgd") or self.mbuf is not None:
             return None
         if self.alpha_t is not None or self.decay_t is not None:
             return None
@@ -384,6 +386,7 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P = _Plan()
     P.p, P.st, P.group = p, st, group
     P.vbuf = None
+    P.mbuf = None
     beta1, beta2, beta2_decay, beta3 = group.get("beta1"), group["beta2"], group["beta2_decay"], group.get("beta3")
     eps1, eps2 = group["eps"]
     eps1 = 1e-30 if eps1 is None else eps1
@@ -614,11 +617,14 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
         if m is not None and not m.is_contiguous():
             m = m.contiguous()
             st["m"] = m
+        beta1 = P.beta1 if P.has_m else 0.0
+        if P.mbuf is not None:   # this step's m' is ready: lerp weight 1 - beta1 = 0 keeps it
+            m, beta1 = P.mbuf, 1.0
         var = _variance_of(P)
         rc = L.a8_fused_update_1d_full(
             mode, nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(var), nat.ptr(m),
             nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
-            P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
+            beta1, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
             p.numel(), P.d, int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
             int(P.sr), int(st.get("sr_seed", 0)), int(P.step), int(P.vbuf is not None), nat.stream_of(p.device))
         nat.check(rc, "a8_fused_update_1d_full")
@@ -751,6 +757,40 @@ def _prep_q1d_fp32m(opt, P):
     nat.check(rc, "a8_log_quantize_lerp")
     _block_view(st, "variance", P.bs)
     P.vbuf = buf
+    P.path = "f1d"
+
+
+def _prep_f1d_qm(opt, P):
+    """fp32 V with quantised momentum.  The reference runs its PyTorch branch here
+    with or without its CUDA module (optimizer.py:2185-2191 into
+    _fallback_1d_update 886-910).  V takes the branch's mul_ / addcmul_ EMA
+    (a8_vema_fp32); the momentum EMA and its re-encode run in a8_m_quantize_lerp,
+    whose fp32 output is this step's m'.  The update then takes the fp32-state
+    route with V and m' as given."""
+    if P.mom_only:
+        raise NotImplementedError("adafactor8bit: the momentum-only 1-D update with quantised momentum and fp32 V "
+                                  "is not available in this build")
+    st, p, g = P.st, P.p, P.g
+    if g.dtype != p.dtype:
+        raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    dev = p.device
+    if not st["variance"].is_contiguous():
+        st["variance"] = st["variance"].contiguous()
+    var = st["variance"]
+    L = nat.lib()
+    strm = nat.stream_of(dev)
+    nat.check(L.a8_vema_fp32(var.data_ptr(), g.data_ptr(), nat.dtype_code(g.dtype), float(P.beta_val),
+                             _f32(P.eps_g), p.numel(), strm), "a8_vema_fp32")
+    key = (dev, "mready", id(p))
+    buf = opt._ws.get(key)
+    if buf is None or buf.numel() != p.numel():
+        buf = torch.empty(p.numel(), dtype=torch.float32, device=dev)
+        opt._ws[key] = buf
+    nat.check(L.a8_m_quantize_lerp(st["m_q"].data_ptr(), st["m_scale"].data_ptr(), g.data_ptr(),
+                                   nat.dtype_code(g.dtype), buf.data_ptr(), float(P.beta1), int(P.mbs), p.numel(),
+                                   S.m_bits(P.mqt), S.m_mode(P.mqt), strm), "a8_m_quantize_lerp")
+    P.vbuf = var
+    P.mbuf = buf
     P.path = "f1d"
 
 

@@ -397,6 +397,20 @@ __global__ __launch_bounds__(256) void k_apwb(T* __restrict__ param, const GT* _
   }
 }
 
+// fp32 second moment of the reference's PyTorch branch (optimizer.py:2185-2188):
+// v = v * (1 - bv) + (bv * g) * g, then + bv * eps_g when eps_g > 0; g scrubbed.
+template <typename GT>
+__global__ __launch_bounds__(256) void k_vema32(float* __restrict__ v, const GT* __restrict__ g, float omb, float bv,
+                                                float add, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float gi = scrub(ld1<GT>(g, i));
+  float x = gp(v)[i] * omb;
+  x = x + (bv * gi) * gi;
+  if (add > 0.0f) x = x + add;
+  gp(v)[i] = x;
+}
+
 hipError_t prims_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
 
 static int lb_of(int64_t bs, int lo, int hi, int& lb, const char* what) {
@@ -565,6 +579,30 @@ int a8_apollo_came_m_res(const float* grad_low, const float* v, const uint8_t* m
                      m_scale_old, res_old, m_out, res_out, clip_factor, (float)(1.0 - beta1), (float)(1.0 - beta3),
                      eps_came, eps_sq, (int64_t)m_block_size, numel, mk);
   return check_launch("k_apres");
+}
+
+int a8_vema_fp32(float* v, const void* grad, int grad_dtype, double beta_val, float eps_g, int64_t numel,
+                 void* stream) {
+  if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+  if (numel == 0) return 0;
+  if (!v || !grad) return set_error(A8_ERR_ARG, "null pointer");
+  const int64_t nwg = (numel + 255) / 256;
+  if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
+  const float omb = (float)(1.0 - beta_val), bv = (float)beta_val;
+  const float add = eps_g > 0.0f ? (float)(beta_val * (double)eps_g) : 0.0f;
+  hipStream_t st = (hipStream_t)stream;
+  if (grad_dtype == A8_F32)
+    hipLaunchKernelGGL(k_vema32<float>, dim3((unsigned)nwg), dim3(256), 0, st, v, (const float*)grad, omb, bv, add,
+                       numel);
+  else if (grad_dtype == A8_BF16)
+    hipLaunchKernelGGL(k_vema32<__hip_bfloat16>, dim3((unsigned)nwg), dim3(256), 0, st, v,
+                       (const __hip_bfloat16*)grad, omb, bv, add, numel);
+  else if (grad_dtype == A8_F16)
+    hipLaunchKernelGGL(k_vema32<__half>, dim3((unsigned)nwg), dim3(256), 0, st, v, (const __half*)grad, omb, bv, add,
+                       numel);
+  else
+    return set_error(A8_ERR_DTYPE, "grad_dtype must be A8_F32, A8_BF16 or A8_F16");
+  return check_launch("k_vema32");
 }
 
 int a8_apollo_writeback(int dtype, int grad_native, int stochastic, void* param, const void* grad,

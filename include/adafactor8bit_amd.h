@@ -549,6 +549,13 @@ int a8_apollo_came_m_res(const float* grad_low, const float* v, const uint8_t* m
                          double beta3, float eps_came, float eps_sq, int m_block_size, int64_t numel, int m_bits,
                          int m_mode, void* stream);
 
+/* fp32 second-moment EMA of the reference's PyTorch branch for fp32 V
+ * (optimizer.py:2185-2188, taken when V is fp32 and M quantised):
+ * v = v * (1 - beta_val) + (beta_val * g) * g, then + beta_val * eps_g when
+ * eps_g > 0; non-finite g read as 0.  grad: grad_dtype (A8_F32/BF16/F16). */
+int a8_vema_fp32(float* v, const void* grad, int grad_dtype, double beta_val, float eps_g, int64_t numel,
+                 void* stream);
+
 /* Replaces apollo_apply_{bf16_det,bf16_sr,fp16_sr} (grad fp32, grad_native = 0) and
  * apollo_apply_{bf16,fp16}_{det,sr}_native (grad of the param's type, scrubbed and
  * negated when maximize; grad_native = 1) (kernels.cu:2638-3000) on a rows x cols

@@ -68,6 +68,9 @@ CONFIGS = [
     ("adamw_clip_fira_wd", dict(ADAMW, lr=1e-3, d=1.0, weight_decay=0.1, scale_weight_decay=True,
                                 enable_fira_for_adafactor=True), P_SMALL, "logscale", 5, (1, 5)),
     ("adamw_fp32_state", dict(ADAMW, lr=1e-4, quantize=False), P_SMALL, "normal_zeros", 4, (1, 4)),
+    # fp32 V with quantised momentum (the reference's PyTorch branch, optimizer.py:2185-2191)
+    ("adamw_fp32v_uf8m", dict(ADAMW, lr=1e-4, v_quant_type="fp32", d=1.0, weight_decay=0.1,
+                              scale_weight_decay=True), P_ADAMW, "student_t", 4, (1, 4)),
     ("rmsprop_al8", dict(RMSPROP, lr=1e-4), P_SMALL, "normal_zeros", 4, (1, 4)),
     ("adafactor_mom1d", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False), P_SMALL,
      "student_t", 4, (1, 4)),

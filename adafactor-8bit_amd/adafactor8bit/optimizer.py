@@ -349,7 +349,7 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep")
 
     def batch_key(self):
         if self.path == "factored":
@@ -766,10 +766,11 @@ def _prep_f1d_qm(opt, P):
     _fallback_1d_update 886-910).  V takes the branch's mul_ / addcmul_ EMA
     (a8_vema_fp32); the momentum EMA and its re-encode run in a8_m_quantize_lerp,
     whose fp32 output is this step's m'.  The update then takes the fp32-state
-    route with V and m' as given."""
-    if P.mom_only:
-        raise NotImplementedError("adafactor8bit: the momentum-only 1-D update with quantised momentum and fp32 V "
-                                  "is not available in this build")
+    route with V and m' as given.  Momentum-only (optimizer.py:894-901): U =
+    g / sqrt(max(v, eps^2)) with the RMS clip, m' = lerp(m, U / clip, 1 - beta1)
+    (a8_apollo_came_rms and a8_apollo_came_m_res compute exactly these), then the
+    re-encode of m' and the update with m' as the step (no clip), as the
+    fp32-momentum route runs it."""
     st, p, g = P.st, P.p, P.g
     if g.dtype != p.dtype:
         raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
@@ -786,9 +787,36 @@ def _prep_f1d_qm(opt, P):
     if buf is None or buf.numel() != p.numel():
         buf = torch.empty(p.numel(), dtype=torch.float32, device=dev)
         opt._ws[key] = buf
-    nat.check(L.a8_m_quantize_lerp(st["m_q"].data_ptr(), st["m_scale"].data_ptr(), g.data_ptr(),
-                                   nat.dtype_code(g.dtype), buf.data_ptr(), float(P.beta1), int(P.mbs), p.numel(),
-                                   S.m_bits(P.mqt), S.m_mode(P.mqt), strm), "a8_m_quantize_lerp")
+    if P.mom_only:
+        n = p.numel()
+        g32 = g if g.dtype == torch.float32 else g.float()
+        aux = opt._ws.get((dev, "mready_aux", id(p)))
+        if aux is None or aux.numel() != 2 * n + 1:
+            aux = torch.zeros(2 * n + 1, dtype=torch.float32, device=dev)
+            opt._ws[(dev, "mready_aux", id(p))] = aux
+        clip = aux[2 * n:]
+        if P.d > 0.0:   # clamp((||U|| / sqrt(n)) / d, min=1) (optimizer.py:897-899)
+            clip.zero_()
+            nat.check(L.a8_apollo_came_rms(g32.data_ptr(), var.data_ptr(), clip.data_ptr(), _f32(P.eps_sq), n,
+                                           strm), "a8_apollo_came_rms")
+            clip.copy_(torch.clamp((torch.sqrt(clip) / math.sqrt(n)) / P.d, min=1.0))
+        else:
+            clip.fill_(1.0)
+        # the residual outputs of the CAME form are not used here
+        nat.check(L.a8_apollo_came_m_res(g32.data_ptr(), var.data_ptr(), st["m_q"].data_ptr(),
+                                         st["m_scale"].data_ptr(), aux.data_ptr(), buf.data_ptr(),
+                                         aux[n:].data_ptr(), clip.data_ptr(), float(P.beta1), 0.0, 0.0,
+                                         _f32(P.eps_sq), int(P.mbs), n, S.m_bits(P.mqt), S.m_mode(P.mqt), strm),
+                  "a8_apollo_came_m_res")
+        # re-encode m' (lerp weight 1 keeps it exactly)
+        nat.check(L.a8_m_quantize_lerp(st["m_q"].data_ptr(), st["m_scale"].data_ptr(), buf.data_ptr(), nat.F32,
+                                       None, 0.0, int(P.mbs), n, S.m_bits(P.mqt), S.m_mode(P.mqt), strm),
+                  "a8_m_quantize_lerp")
+        P._keep = (g32, aux)
+    else:
+        nat.check(L.a8_m_quantize_lerp(st["m_q"].data_ptr(), st["m_scale"].data_ptr(), g.data_ptr(),
+                                       nat.dtype_code(g.dtype), buf.data_ptr(), float(P.beta1), int(P.mbs),
+                                       p.numel(), S.m_bits(P.mqt), S.m_mode(P.mqt), strm), "a8_m_quantize_lerp")
     P.vbuf = var
     P.mbuf = buf
     P.path = "f1d"

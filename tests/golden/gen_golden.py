@@ -74,6 +74,8 @@ CONFIGS = [
     ("rmsprop_al8", dict(RMSPROP, lr=1e-4), P_SMALL, "normal_zeros", 4, (1, 4)),
     ("adafactor_mom1d", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False), P_SMALL,
      "student_t", 4, (1, 4)),
+    ("adafactor_mom1d_fp32v_uf8m", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False, v_quant_type="fp32",
+                                        enable_fira_for_adafactor=True), P_ADAMW, "logscale", 4, (1, 4)),
     ("adafactor_mom1d_fira", dict(ADAFACTOR, lr=1e-3, beta1=0.9, factored=False,
                                   enable_fira_for_adafactor=True, fira_margin=0.01), P_SMALL,
      "logscale", 5, (1, 5)),

@@ -37,7 +37,7 @@ SUPPORTED = ["adamw_uf8_al8", "adamw_uf8_al16", "adamw_uf4_al8", "adamw_d8_al8",
              "adamw_bv256_mb128", "adamw_clip_fira_wd", "adamw_fp32_state", "rmsprop_al8",
              "adafactor_mom1d", "adafactor_mom1d_fira", "adafactor_factored_al8", "adafactor_factored_emb",
              "adafactor_factored_m_uf8", "came_uf8_al8", "came_uf8_al16_fira", "sgd_momentum_uf8",
-             "adamw_fp32v_uf8m"]
+             "adamw_fp32v_uf8m", "adafactor_mom1d_fp32v_uf8m"]
 
 # Row/column statistics are sums over a matrix: the HIP path reduces them in a
 # fixed order of its own (fp32 tiles, double across tiles), the reference in

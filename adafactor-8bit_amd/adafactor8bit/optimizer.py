@@ -321,7 +321,19 @@ class Adafactor8Bit(Optimizer):
         apollo_rank = group.get("apollo_rank", 0)
         batches: Dict[tuple, list] = {}
         ap_batches: Dict[tuple, list] = {}
+        copy_back = []
         for p, g, st in zip(params, grads, states):
+            if not p.is_contiguous():
+                # the reference steps a contiguous copy and writes it back (optimizer.py:2002-2007,
+                # 2608-2614); the copy is kept so workspaces keyed by the tensor stay valid
+                key = (p.device, "contig", id(p))
+                work = self._ws.get(key)
+                if work is None or work.shape != p.shape or work.dtype != p.dtype:
+                    work = torch.empty(p.shape, dtype=p.dtype, device=p.device)
+                    self._ws[key] = work
+                work.copy_(p)
+                copy_back.append((p, work))
+                p = work
             if apollo_rank > 0 and "apollo_seed" in st:
                 bkey, rec, fin = _apollo_prep(self, p, g, st, group)
                 ap_batches.setdefault(bkey, []).append((rec, fin))
@@ -340,6 +352,8 @@ class Adafactor8Bit(Optimizer):
             _run_batch(self, key, plans)
         for bkey, items in ap_batches.items():
             _run_apollo_batch(self, group, bkey, items)
+        for p, work in copy_back:
+            p.copy_(work)
 
 
 # ====================================================================== planning

@@ -348,3 +348,38 @@ def test_factored_with_fp32_momentum(name, kw):
         floor = 1e-6 * float(sc["m"].abs().max())
         np.testing.assert_allclose(sg["m"].cpu().numpy(), sc["m"].numpy(), rtol=1e-5, atol=floor,
                                    err_msg=f"{name} p{i} m")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["adamw_1d", "adafactor_factored", "apollo"])
+def test_noncontiguous_param_matches_contiguous(kind):
+    """A non-contiguous parameter (a transposed view) is stepped through a
+    contiguous copy and written back, as the reference does (optimizer.py:2002-2007,
+    2608-2614): parameters and state equal those of a contiguous parameter with
+    the same values, bit for bit (d = 0: no RMS-clip norm, whose float atomics
+    sum in no fixed order)."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[noncontig] {kind}", flush=True)
+    kw = {"adamw_1d": dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=False,
+                           scale_parameter=False, d=0.0, weight_decay=0.1),
+          "adafactor_factored": dict(lr=1e-3, relative_step=False, block_size=256, d=0.0),
+          "apollo": dict(lr=1e-3, beta1=0.9, beta2=0.999, relative_step=False, scale_parameter=False,
+                         apollo_rank=16, apollo_cache_proj=True, block_size=128, m_block_size=32,
+                         d=0.0)}[kind]
+    shape = (96, 130)
+    base = make_param(shape, 0, 8)
+    pc = torch.nn.Parameter(base.clone().cuda())
+    pn = torch.nn.Parameter(base.clone().t().contiguous().cuda().t())   # same values, transposed strides
+    assert not pn.is_contiguous() and torch.equal(pc, pn)
+    oc, on = Adafactor8Bit([pc], **kw), Adafactor8Bit([pn], **kw)
+    for t in range(1, 4):
+        g = make_grad(shape, 0, t, 8).cuda()
+        pc.grad, pn.grad = g.clone(), g.clone()
+        oc.step()
+        on.step()
+    torch.cuda.synchronize()
+    assert not pn.is_contiguous()
+    assert torch.equal(pc.detach(), pn.detach())
+    for k, v in oc.state[pc].items():
+        if torch.is_tensor(v):
+            assert torch.equal(v, on.state[pn][k]), k

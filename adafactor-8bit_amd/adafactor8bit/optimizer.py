@@ -1272,6 +1272,16 @@ def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, f
         opt._ws[key] = xws
     aeps = group.get("apollo_eps", 1e-6)
     eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
+    # the record is rebuilt only when a state tensor, a workspace or a hyper-parameter changed
+    sig = (ws.data_ptr(), xws.data_ptr(), low_shape, factorize, came, has_m, m_fp32, vbits, cbits, mqt, int(bs),
+           int(mbs), beta1, group.get("beta3"), aeps, group.get("eps_came", 1e-16), group["d"],
+           tuple(v.data_ptr() for v in st.values() if torch.is_tensor(v)))
+    cached = opt._ws.get((dev, "apollo_xargs", id(st)))
+    if cached is not None and cached[0] == sig:
+        a = cached[1]
+        a.first_step = int(first)
+        a.beta_v = float(beta_val)
+        return a, (xws, cbits)
     P = nat.ptr
     a = nat.ApolloXArgs(
         ws.data_ptr(), ws.data_ptr() + 4 * n_low, xws.data_ptr(), low_shape[0], low_shape[1],
@@ -1300,6 +1310,7 @@ def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, f
         cbits if came else 0, float(beta_val), float(beta1) if has_m else 0.0,
         float(group["beta3"]) if came else 0.0, _f32(aeps), _f32(eps_sq), _f32(math.log2(eps_sq)),
         _f32(group.get("eps_came", 1e-16)), float(group["d"]))
+    opt._ws[(dev, "apollo_xargs", id(st))] = (sig, a)
     return a, (xws, cbits)
 
 

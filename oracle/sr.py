@@ -9,12 +9,15 @@ with a counter-based generator (kernels.cu:48-87):
   u       = (bits >> 8) * 2^-24                     (uniform in [0, 1), 24 bits)
   bf16    = truncate(x) + 1 ulp  if u < (low 16 bits of x) / 65536
             (no round-up from or to infinity; NaN becomes the canonical quiet NaN)
+  fp16    = the fp16 neighbours lo < x < hi around round-to-nearest(x); hi if
+            u < (x - lo) / (hi - lo) in fp32 (kernels.cu:100-131; |x| > 65504
+            saturates to +-65504, Inf / NaN keep their class, exact values stay)
 
 ``seed`` is the parameter's ``sr_seed`` (a per-parameter counter from 1,
 optimizer.py:1886-1892), ``step`` the optimizer step and ``idx`` the element's
 index in the flattened parameter.  Pinned by the SplitMix64 published first
-output (state 0 -> 0xE220A8397B1DCDAF) and by the rounding's defining properties
-in tests/test_oracle_sr.py.
+output (state 0 -> 0xE220A8397B1DCDAF) and by each rounding's defining
+properties in tests/test_oracle_sr.py.
 """
 import numpy as np
 

@@ -65,3 +65,31 @@ def test_module_signatures_match_reference():
         assert name in ref, name
         assert list(inspect.signature(getattr(K, name)).parameters) == ref[name], name
     assert sorted(set(ref) - {"qmaps"}) == sorted(set(K.__all__)), sorted(set(ref) ^ set(K.__all__))
+
+
+def test_apollo_lowrank_and_phase_argument_errors_without_gpu():
+    """The factorised / CAME APOLLO stage and the phased group call check their
+    records on the host before any launch."""
+    import ctypes
+    from adafactor8bit import _native as nat
+    L = nat.lib()
+    a = nat.ApolloXArgs()
+    a.rows_low, a.cols_low = 16, 8
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # null g_low / u / workspace
+    a.g_low = a.u = a.xws = 256
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # neither factorised nor CAME
+    assert b"plain APOLLO" in L.a8_last_error()
+    a.came, a.has_m = 1, 0
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # CAME without momentum
+    assert b"beta1" in L.a8_last_error()
+    a.has_m, a.m_fp32, a.v_bits, a.block_size, a.c_bits = 1, 256, 8, 100, 8
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -3            # AL block 100
+    a.rows_low = 0
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -4            # empty matrix
+    assert L.a8_apollo_x_workspace_floats(0, 8) == 0
+    assert L.a8_apollo_x_workspace_floats(5632, 256) > 4 * 5632 * 256
+    rc = L.a8_apollo_step_multi_phase(3, 0, 0, None, 1, None, 0, 0.001, 0.9, 1, 1e-6, -39.9, 0, 2048, 8, 0, 1,
+                                      256, 1, 1.0, 0, 1, 0.01, 0.0, 1e-3, 1e-3, 0, 0, 0.0, 0, None)
+    assert rc == -1 and b"phase" in L.a8_last_error()
+    assert L.a8_vema_fp32(None, None, 0, 0.001, 0.0, 4, None) == -1
+    assert L.a8_vema_fp32(256, 256, 9, 0.001, 0.0, 4, None) == -2

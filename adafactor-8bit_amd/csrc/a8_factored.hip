@@ -56,13 +56,14 @@ struct FWs {
   int64_t tr;        // rows per statistics tile
 };
 
-// Rows per statistics tile: 32, taller for tall matrices so that a column has at
-// most ~64 strip partials to reduce (the tile kernels carry column partials in
-// registers across rows, so a taller tile costs nothing there).
+// Rows per statistics tile: 32, or 64 for matrices of more than 2048 rows.  A
+// workgroup streams tr x 1024 elements, so taller tiles leave the tall matrices
+// (32000 x 2048 embeddings) to a few long-running workgroups that finish last at
+// low occupancy; the column reduction reads one partial per strip in any case.
 __host__ __device__ inline int64_t fws_tile_rows(int64_t R) {
   int64_t tr = (R + 63) / 64;
   tr = (tr + kTR - 1) / kTR * kTR;
-  return tr < kTR ? kTR : (tr > 1024 ? 1024 : tr);
+  return tr < kTR ? kTR : (tr > 64 ? 64 : tr);
 }
 
 __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {

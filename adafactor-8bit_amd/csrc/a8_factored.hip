@@ -1,8 +1,8 @@
 // Factored (Adafactor row/column) optimizer step for MI355X (gfx950).
 //
 // One group step is a few launches over every tensor of the group:
-//   k_fstats   2-D tiles of tr rows x 1024 columns (tr = 32, taller for tall
-//              matrices): row sums and column sums of g^2 (and sum p^2 for the
+//   k_fstats   2-D tiles of tr rows x 1024 columns (tr = 32, or 64 above 2048
+//              rows): row sums and column sums of g^2 (and sum p^2 for the
 //              relative step size), written as per-tile partials -- no atomics,
 //              so the result is deterministic;
 //   k_fblock   one workgroup per AL block of each row/column vector: reduce the

@@ -40,16 +40,21 @@ constexpr int kUnit = 2048;  // elements per update workgroup
 constexpr int kScal = 8;     // per-tensor scalars in the workspace
 constexpr int kMkFp32 = 5;   // HyperF::mk of fp32 momentum (codecs are 1-4)
 
-// Per-tensor workspace layout (floats).
+// Per-tensor workspace layout (offsets in floats).  The partial sums are doubles:
+// every statistic (row / column means, sum p^2, ||u||^2) is accumulated in double
+// from its first term and rounded to float once, so it is the correctly rounded
+// sum in all but vanishingly rare cases, whatever the tiling.  The double regions
+// come first and have even sizes, so each starts 8-byte aligned (the workspace
+// itself is 256-byte aligned).
 struct FWs {
-  int64_t rowpart;   // [nchunk][B*R]      row partial sums
-  int64_t colpart;   // [B][nstrip][C]     column partial sums
-  int64_t p2;        // [ntile]            partial sum p^2
+  int64_t rowpart;   // double [nchunk][B*R]       row partial sums
+  int64_t colpart;   // double [B][nstrip][C]      column partial sums
+  int64_t p2;        // double [ntile]             partial sum p^2
+  int64_t npart;     // double [max(nunit, ntile)] partial sums u^2 (per unit or per tile)
   int64_t invr;      // [B*R]              new row V, then inv_row
   int64_t invc;      // [B*C]              new column V, then inv_col
   int64_t icr;       // [B*R]              CAME: new row confidence, then its inverse root
   int64_t icc;       // [B*C]              CAME: new column confidence, then its inverse root
-  int64_t npart;     // [max(nunit, ntile)] partial sums u^2 (per unit or per tile)
   int64_t scal;      // [8]: alpha, step, fira scale, decay, CAME clip factor
   int64_t total;
   int64_t nchunk, nstrip, ntile, nunit;
@@ -74,16 +79,21 @@ __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
   w.ntile = B * w.nstrip * w.nchunk;
   w.nunit = (B * R * C + kUnit - 1) / kUnit;
   w.rowpart = 0;
-  w.colpart = w.rowpart + w.nchunk * B * R;
-  w.p2 = w.colpart + B * w.nstrip * C;
-  w.invr = w.p2 + w.ntile;
+  w.colpart = w.rowpart + 2 * w.nchunk * B * R;
+  w.p2 = w.colpart + 2 * B * w.nstrip * C;
+  w.npart = w.p2 + 2 * w.ntile;
+  w.invr = w.npart + 2 * (w.nunit > w.ntile ? w.nunit : w.ntile);
   w.invc = w.invr + B * R;
   w.icr = w.invc + B * C;
   w.icc = w.icr + B * R;
-  w.npart = w.icc + B * C;
-  w.scal = w.npart + (w.nunit > w.ntile ? w.nunit : w.ntile);
+  w.scal = w.icc + B * C;
   w.total = w.scal + kScal;
   return w;
+}
+
+__device__ __forceinline__ double* ws_dp(float* ws, int64_t off) { return reinterpret_cast<double*>(ws + off); }
+__device__ __forceinline__ const double* ws_dp(const float* ws, int64_t off) {
+  return reinterpret_cast<const double*>(ws + off);
 }
 
 struct DescF {
@@ -175,15 +185,6 @@ __device__ __forceinline__ double wg_sum_d(double x, double* s4) {
   return ((s4[0] + s4[1]) + s4[2]) + s4[3];
 }
 
-__device__ __forceinline__ float wg_sum_f(float x, float* s4) {
-  x = grp_sum(x, 64);
-  const int lane = threadIdx.x;
-  __syncthreads();
-  if ((lane & 63) == 0) s4[lane >> 6] = x;
-  __syncthreads();
-  return ((s4[0] + s4[1]) + s4[2]) + s4[3];
-}
-
 __device__ __forceinline__ uint32_t nz_key_f(float v) { return __float_as_uint(v) - 1u; }
 
 __device__ __forceinline__ void wg_maxkey(float& mx, uint32_t& key, float* s8) {
@@ -224,8 +225,8 @@ __device__ __forceinline__ void load4(const T* base, int64_t rowbase, int64_t c0
 // ------------------------------------------------------------ statistics
 template <typename T, bool PSQ>
 __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table, int ntab) {
-  __shared__ float s_col[4 * kTC];
-  __shared__ float s4[4];
+  __shared__ double s_col[4 * kTC];
+  __shared__ double s4[4];
   const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
   const FWs W = fws_layout(D.B, D.R, D.C);
   const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
@@ -242,13 +243,15 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
   const T* P = reinterpret_cast<const T*>(D.param);
   float* ws = D.ws;
   const bool vec = D.vec4 != 0;
-  float acc[16];
+  // The float square g*g is the reference's term (g32.square(), optimizer.py:2213);
+  // its sums accumulate in double.
+  double acc[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
-  float psq = 0.0f;
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0;
+  double psq = 0.0;
   for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
     const int64_t rowbase = (b * R + r) * C;
-    float rs = 0.0f;
+    double rs = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t c0 = c_base + 4 * wl + 256 * j;
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float gg = scrub(g4[e]);
-        const float sq = gg * gg;
+        const double sq = (double)(gg * gg);
         rs += sq;
         acc[j * 4 + e] += sq;
       }
@@ -265,11 +268,11 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
         float p4[4];
         load4<T>(P, rowbase, c0, C, vec, p4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) psq = __builtin_fmaf(p4[e], p4[e], psq);
+        for (int e = 0; e < 4; ++e) psq = __builtin_fma((double)p4[e], (double)p4[e], psq);
       }
     }
-    rs = grp_sum(rs, 64);
-    if (wl == 0) gp(ws)[W.rowpart + ch * (D.B * R) + b * R + r] = rs;
+    rs = grp_sum_d(rs, 64);
+    if (wl == 0) gp(ws_dp(ws, W.rowpart))[ch * (D.B * R) + b * R + r] = rs;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -279,13 +282,13 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
   for (int q = lane; q < kTC; q += 256) {
     const int64_t c = c_base + q;
     if (c < C) {
-      const float v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
-      gp(ws)[W.colpart + (b * W.nstrip + s) * C + c] = v;
+      const double v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
+      gp(ws_dp(ws, W.colpart))[(b * W.nstrip + s) * C + c] = v;
     }
   }
   if constexpr (PSQ) {
-    const float tot = wg_sum_f(psq, s4);
-    if (lane == 0) gp(ws)[W.p2 + t] = tot;
+    const double tot = wg_sum_d(psq, s4);
+    if (lane == 0) gp(ws_dp(ws, W.p2))[t] = tot;
   }
 }
 
@@ -335,7 +338,7 @@ __device__ __forceinline__ void m_old4(int mkr, const uint8_t* mq, const float* 
 // of res as per-tile partials in the g^2 partial arrays (consumed by then).
 template <typename T, int MK>
 __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, int ntab, HyperF h) {
-  __shared__ float s_col[4 * kTC];
+  __shared__ double s_col[4 * kTC];
   const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
   const FWs W = fws_layout(D.B, D.R, D.C);
   const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
@@ -360,13 +363,13 @@ __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, 
       const int64_t c = c_base + 4 * wl + 256 * j + e;
       icol[j * 4 + e] = (c < C) ? gp(ws)[W.invc + b * C + c] : 0.0f;
     }
-  float acc[16];
+  double acc[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0;
   for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
     const int64_t rowbase = (b * R + r) * C;
     const float ir = gp(ws)[W.invr + b * R + r];
-    float rs = 0.0f;
+    double rs = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t c0 = c_base + 4 * wl + 256 * j;
@@ -381,15 +384,15 @@ __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, 
             const float ug = ((scrub(g4[e]) * ir) * icol[j * 4 + e]) / clip;
             const float mn = lerp_ref(m4[e], ug, h.w_m);
             const float dd = ug - mn;
-            const float res = dd * dd + h.eps_came;
+            const double res = (double)(dd * dd + h.eps_came);
             rs += res;
             acc[j * 4 + e] += res;
           }
         }
       }
     }
-    rs = grp_sum(rs, 64);
-    if (wl == 0) gp(ws)[W.rowpart + ch * (D.B * R) + b * R + r] = rs;
+    rs = grp_sum_d(rs, 64);
+    if (wl == 0) gp(ws_dp(ws, W.rowpart))[ch * (D.B * R) + b * R + r] = rs;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -399,8 +402,8 @@ __global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, 
   for (int q = lane; q < kTC; q += 256) {
     const int64_t c = c_base + q;
     if (c < C) {
-      const float v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
-      gp(ws)[W.colpart + (b * W.nstrip + s) * C + c] = v;
+      const double v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
+      gp(ws_dp(ws, W.colpart))[(b * W.nstrip + s) * C + c] = v;
     }
   }
 }
@@ -480,19 +483,19 @@ __global__ __launch_bounds__(256) void k_fblock(const DescF* __restrict__ table,
   for (int64_t i = i0 + lane; i < i1; i += 256) {
     double sum = 0.0;
     if (is_row) {
-      for (int64_t k = 0; k < W.nchunk; ++k) sum += (double)gp(ws)[W.rowpart + k * n + i];
+      for (int64_t k = 0; k < W.nchunk; ++k) sum += gp(ws_dp(ws, W.rowpart))[k * n + i];
     } else {
       const int64_t b = i / C, c = i - b * C;
-      const float* cp0 = ws + W.colpart + b * W.nstrip * C + c;
+      const double* cp0 = ws_dp(ws, W.colpart) + b * W.nstrip * C + c;
       int64_t k = 0;
       for (; k + 8 <= W.nstrip; k += 8) {   // eight loads in flight, summed in order
-        float t[8];
+        double t[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) t[u] = gp(cp0)[(k + u) * C];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sum += (double)t[u];
+        for (int u = 0; u < 8; ++u) sum += t[u];
       }
-      for (; k < W.nstrip; ++k) sum += (double)gp(cp0)[k * C];
+      for (; k < W.nstrip; ++k) sum += gp(cp0)[k * C];
     }
     float mean = (float)sum / cnt;
     if constexpr (!CONF) mean = mean + h.eps1;
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, 
     float alpha = rho;
     if (h.scale_param) {
       double s = 0.0;
-      for (int64_t k = lane; k < W.ntile; k += 256) s += (double)gp(ws)[W.p2 + k];
+      for (int64_t k = lane; k < W.ntile; k += 256) s += gp(ws_dp(ws, W.p2))[k];
       s = wg_sum_d(s, sd);
       const float nrm = sqrtf((float)s);
       const float rms = nrm / (float)sqrt((double)D.numel);
@@ -586,6 +589,7 @@ template <typename T, int MODE, bool SR, int MK, bool CM>
 __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table, int ntab, HyperF h) {
   static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s4[8];
+  __shared__ double s4d[4];
   constexpr bool kHasM = MK != 0;
   const DescF D = *find_unit(table, ntab, (int64_t)blockIdx.x);
   if (D.tiled) return;   // updated by k_fupdt
@@ -612,7 +616,7 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   float g[8], mn[8], u[8], mo[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) { g[k] = 0.0f; mn[k] = 0.0f; u[k] = 0.0f; mo[k] = 0.0f; }
-  float sq = 0.0f;
+  double sq = 0.0;   // sum u^2 (MODE 1), accumulated in double
   uint32_t amaxb = 0u;
   if (cnt > 0) {
     load8<T>(reinterpret_cast<const T*>(D.grad), e0, n, g);
@@ -662,7 +666,7 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
           const float x = kHasM ? mn[k] : g[k];
           u[k] = (x * gp(invr)[row]) * gp(invc)[b * C + c];
         }
-        if (MODE == 1) sq = __builtin_fmaf(u[k], u[k], sq);
+        if (MODE == 1) sq = __builtin_fma((double)u[k], (double)u[k], sq);
       }
       if (++c == C) {
         c = 0;
@@ -710,8 +714,8 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   }
 
   if constexpr (MODE == 1) {
-    const float tot = wg_sum_f(sq, s4);
-    if (lane == 0) gp(const_cast<float*>(ws))[W.npart + wl] = tot;
+    const double tot = wg_sum_d(sq, s4d);
+    if (lane == 0) gp(ws_dp(const_cast<float*>(ws), W.npart))[wl] = tot;
   }
 
   if constexpr (MODE != 1 && MK == 3) {
@@ -778,6 +782,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
   static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s_ic[2 * kTC];
   __shared__ float s4[8];
+  __shared__ double s4d[4];
   constexpr bool kHasM = MK != 0;
   const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
   if (!D.tiled) return;   // updated by k_fupdate
@@ -813,7 +818,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
   const bool has_dec = h.wd_mode != 0;
   const T* G0 = reinterpret_cast<const T*>(D.grad);
   T* P0 = reinterpret_cast<T*>(D.param);
-  float sq = 0.0f;
+  double sq = 0.0;   // sum u^2 (MODE 1), accumulated in double
   for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
     const int64_t rowbase = (b * R + r) * C;
     const float ir = cp(ws)[W.invr + b * R + r];
@@ -892,7 +897,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
             if constexpr (kHasM) { mn[i] = lerp_ref(mo[i], gi, h.w_m); x = mn[i]; }
             u[i] = (x * ir) * ic;
           }
-          if (MODE == 1) sq = __builtin_fmaf(u[i], u[i], sq);
+          if (MODE == 1) sq = __builtin_fma((double)u[i], (double)u[i], sq);
         }
       }
       if constexpr (MODE != 1) {
@@ -966,8 +971,8 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     }
   }
   if constexpr (MODE == 1) {
-    const float tot = wg_sum_f(sq, s4);
-    if (lane == 0) gp(ws)[W.npart + t] = tot;
+    const double tot = wg_sum_d(sq, s4d);
+    if (lane == 0) gp(ws_dp(ws, W.npart))[t] = tot;
   }
 }
 
@@ -980,7 +985,7 @@ __global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, 
   float* ws = D.ws;
   double s = 0.0;
   const int64_t np = D.tiled ? W.ntile : W.nunit;
-  for (int64_t k = threadIdx.x; k < np; k += 256) s += (double)gp(ws)[W.npart + k];
+  for (int64_t k = threadIdx.x; k < np; k += 256) s += gp(ws_dp(ws, W.npart))[k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
     float* sl = ws + W.scal;
@@ -1018,7 +1023,7 @@ __global__ __launch_bounds__(256) void k_fclip(const DescF* __restrict__ table, 
   float* ws = D.ws;
   double s = 0.0;
   const int64_t np = D.tiled ? W.ntile : W.nunit;
-  for (int64_t k = threadIdx.x; k < np; k += 256) s += (double)gp(ws)[W.npart + k];
+  for (int64_t k = threadIdx.x; k < np; k += 256) s += gp(ws_dp(ws, W.npart))[k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
     const float rms = sqrtf((float)s) / (float)sqrt((double)D.numel);

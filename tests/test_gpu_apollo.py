@@ -400,3 +400,186 @@ def test_apollo_fp32_width_4_mod_8_matches_oracle(shape, rank, det_proj, monkeyp
         ref.step()
     torch.cuda.synchronize()
     _cmp_params("width", "s3", p.detach().cpu().numpy(), q.detach().numpy(), init.numpy())
+
+
+# C4's configuration: the reference's apollo preset (presets.py:106-125) at rank
+# 256 with 2048-element V blocks and 256-element M blocks.  At rank >= 64 the
+# projection tiles run their second accumulator pair, and AL8 V blocks of 2048
+# elements take the low-rank stage's LDS decode table.
+C4_KW = dict(lr=1e-3, beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=False,
+             relative_step=False, scale_parameter=False, scale_weight_decay=False, d=0.0, eps=(1e-6, 1e-3),
+             apollo_eps=1e-6, apollo_factorize=False, apollo_update_proj_gap=200,
+             apollo_scale_type="channel", apollo_scale=1.0, apollo_scale_front=False, apollo_cache_proj=True,
+             enable_fira_for_apollo=True, apollo_rank=256, block_size=2048, m_block_size=256,
+             m_quant_type="uf8", v_quant_type="al8")
+
+# (shape, rank): right side (R >= C, K = C) and left side (K = R).  Rank 320 takes
+# two 256-wide output passes.
+GEMM_RANKS = [((1024, 512), 64), ((700, 384), 96), ((1024, 512), 256), ((700, 384), 320),
+              ((512, 1536), 256), ((384, 900), 320), ((300, 700), 64), ((200, 900), 96)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,rank", GEMM_RANKS, ids=[f"{s[0]}x{s[1]}_r{r}" for s, r in GEMM_RANKS])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_apollo_projection_error_bound_large_rank(shape, rank, dtype, det_proj):
+    """g_low at ranks 64-320 on both sides against an fp64 product of the same G
+    and P^T, to the K-term fp32 dot-product bound (three times it for bf16 G,
+    whose P^T is split into three bf16 terms)."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[apollo gemm large rank] {shape} r={rank} {dtype}", flush=True)
+    R, C = shape
+    p = torch.nn.Parameter(inputs.make_param(shape, 0, 12).to("cuda", dtype))
+    g = inputs.make_grad(shape, 0, 1, 12, kind="student_t").to(dtype)
+    opt = Adafactor8Bit([p], **dict(C4_KW, apollo_rank=rank))
+    p.grad = g.cuda()
+    opt.step()
+    torch.cuda.synchronize()
+    pt = opt.state[p]["apollo_proj_matrix_T"].double().cpu().numpy()
+    G = g.double().numpy()
+    right = R >= C
+    exact = G @ pt if right else pt @ G
+    assert exact.shape == ((R, rank) if right else (rank, C))
+    absb = np.abs(G) @ np.abs(pt) if right else np.abs(pt) @ np.abs(G)
+    K = C if right else R
+    glow = _ws(opt, p)[:exact.size].reshape(exact.shape).astype(np.float64)
+    terms = 1 if dtype == torch.float32 else 3
+    bound = terms * (K + 2) * 2.0 ** -24 * absb
+    err = np.abs(glow - exact)
+    assert np.all(err <= bound + 1e-30), float(np.max(err / (absb + 1e-30)))
+
+
+def _oracle_state_view(st):
+    """The oracle's per-parameter state as a flat mapping of numpy arrays (and the
+    step), for the golden comparison helpers."""
+    out = {}
+    for k, v in st.items():
+        if torch.is_tensor(v):
+            out[k] = (v.view(torch.int16) if v.dtype == torch.bfloat16 else v).numpy()
+        elif k == "step":
+            out[k] = np.asarray(v)
+    return out
+
+
+C4_SHAPES = [(1024, 512), (512, 1536)]
+
+
+def _c4_codes(name, mine, ref, step):
+    frac, mx = gu.code_mismatch(mine.reshape(-1), ref.reshape(-1))
+    print(f"  {name}: {frac:.2e} of codes differ, max {mx}", flush=True)
+    if step == 1:
+        assert frac <= 1e-5 and mx <= 1, (name, frac, mx)
+    assert frac <= 1e-4 and mx <= 1, (name, frac, mx)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", C4_SHAPES, ids=["right_1024x512", "left_512x1536"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_apollo_c4_rank256_matches_oracle(shape, dtype, det_proj, monkeypatch):
+    """Four APOLLO steps at C4's configuration (rank 256, B_V 2048, B_M 256,
+    UF8 M / AL8 V, channel scale, Fira), deterministic writeback, against the CPU
+    oracle given this library's projection output.
+
+    The projection itself is held to its error bound above.  Here g_low is read
+    from the library's workspace after each step and handed to the oracle
+    (OracleOptimizer.glow_hook): at K = 512 a block's smallest g_low can be a
+    cancelling sum whose last bits depend on the GEMM's summation order, and the
+    AL8 block range follows that smallest value.  With the same g_low, and the
+    oracle's reductions (channel norms, ||G_ch||, the Fira norm) accumulated
+    exactly, the rest of the step is held to the north star's bar: low-rank V
+    and M codes equal except <= 0.01% (by one code; step 1: <= 1e-5, where the
+    CPU log2 is not correctly rounded), block metadata rtol 1e-5, the Fira norm
+    rtol 1e-5, fp32 parameters rtol 1e-5 plus 2e-4 of the largest displacement
+    (a flipped V code moves one element of a 256-element channel norm), bf16
+    parameters within two ulps (of the largest magnitude the element has had) plus
+    1e-5 of the largest displacement, <= 0.1% of them not bit-equal."""
+    import oracle.fallback as F
+    from adafactor8bit import Adafactor8Bit
+    monkeypatch.setattr(F, "stable_randn", inputs.make_proj)
+    old = F.set_exact_reductions(True)
+    try:
+        print(f"[apollo c4] {shape} {dtype}", flush=True)
+        R, C = shape
+        low = (R, 256) if R >= C else (256, C)
+        init = inputs.make_param(shape, 0, 21).to(dtype)
+        p = torch.nn.Parameter(init.clone().cuda())
+        q = torch.nn.Parameter(init.clone())
+        opt = Adafactor8Bit([p], **C4_KW)
+        ref = F.OracleOptimizer([q], **C4_KW)
+        mag = np.abs(_f32(_t2np(init)).astype(np.float64))
+        for t in range(1, 5):
+            g = inputs.make_grad(shape, 0, t, 21, zero_frac=0.0).to(dtype)
+            p.grad, q.grad = g.cuda(), g.clone()
+            opt.step()
+            torch.cuda.synchronize()
+            glow = torch.from_numpy(_ws(opt, p)[:low[0] * low[1]].reshape(low).copy())
+            ref.glow_hook = lambda _p, _g, _pt, x=glow: x
+            ref.step()
+            st, sr = opt.state[p], ref.state[id(q)]
+            print(f"[apollo c4] step {t}", flush=True)
+            _c4_codes("v_low_q", st["v_low_q"].cpu().numpy(), sr["v_low_q"].numpy(), t)
+            _c4_codes("m_low_q", st["m_low_q"].cpu().numpy(), sr["m_low_q"].numpy(), t)
+            for k in ("v_low_scale", "v_low_min_log", "m_low_scale"):
+                np.testing.assert_allclose(st[k].cpu().numpy(), sr[k].numpy(), rtol=3e-7 if t == 1 else 1e-5,
+                                           err_msg=f"step {t} {k}")
+            np.testing.assert_allclose(float(st["scaled_grad_norm_prev"]), float(sr["scaled_grad_norm_prev"]),
+                                       rtol=1e-5, err_msg=f"step {t} scaled_grad_norm_prev")
+            assert np.array_equal(st["apollo_proj_matrix_T"].cpu().numpy(), sr["apollo_proj_matrix_T"].numpy())
+            mine, want = _t2np(p), _t2np(q)
+            disp = float(np.abs(_f32(want).astype(np.float64) - _f32(_t2np(init))).max())
+            if dtype == torch.bfloat16:
+                m64, r64 = _f32(mine).astype(np.float64), _f32(want).astype(np.float64)
+                # largest magnitude each element has had: a one-ulp flip made there keeps its size
+                # in absolute terms when the value later shrinks into a finer binade
+                mag = np.maximum(mag, np.maximum(np.abs(m64), np.abs(r64)))
+                ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 1e-38))) - 7)
+                diff = mine != want
+                print(f"  bf16 params not bit-equal: {diff.mean():.2e}", flush=True)
+                # an element whose fp32 value sat on a bf16 midpoint keeps the one-ulp flip, and a
+                # later step may flip it once more; next to zero the fp32 bound of the update applies
+                err = np.abs(m64 - r64) - (2 * ulp + 1e-5 * disp)
+                k = int(np.argmax(err))
+                assert err.flat[k] <= 0, (f"step {t}: bf16 param beyond two ulps: {m64.flat[k]:.6e} vs "
+                                          f"{r64.flat[k]:.6e} (displacement {disp:.3e})")
+                assert diff.mean() <= 1e-3, f"step {t}: {diff.mean():.2e} bf16 params differ"
+            else:
+                np.testing.assert_allclose(mine, want, rtol=1e-5, atol=1e-8 + 2e-4 * disp, err_msg=f"step {t} param")
+        assert st["v_low_q"].numel() == low[0] * low[1] and st["v_low_scale"].numel() == low[0] * low[1] // 2048
+    finally:
+        F.set_exact_reductions(old)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", C4_SHAPES, ids=["right_1024x512", "left_512x1536"])
+def test_apollo_c4_rank256_sr_writeback_bits(shape, det_proj):
+    """C4's SR writeback at rank 256: x = (p * decay) + (G * f) * step in fp32,
+    rounded with the reference's stream (kernels.cu:48-87), bit for bit against
+    the CPU restatement given the step's scalars from the library's workspace."""
+    from adafactor8bit import Adafactor8Bit
+    from oracle import sr
+    print(f"[apollo c4 sr] {shape}", flush=True)
+    R, C = shape
+    rank = 256
+    p = torch.nn.Parameter(inputs.make_param(shape, 0, 22).to("cuda", torch.bfloat16))
+    opt = Adafactor8Bit([p], **dict(C4_KW, weight_decay=0.1, stochastic_round_writeback=True))
+    right = R >= C
+    n_low = R * rank if right else rank * C
+    nch = R if right else C
+    fin = 2 * n_low + nch
+    scal = fin + nch
+    for t in range(1, 4):
+        p_old = _f32(_t2np(p)).reshape(-1).astype(np.float32)
+        g = inputs.make_grad(shape, 0, t, 22, zero_frac=0.0).to(torch.bfloat16)
+        p.grad = g.cuda()
+        opt.step()
+        torch.cuda.synchronize()
+        st = opt.state[p]
+        ws = _ws(opt, p)
+        step_s, dec, fs = np.float32(ws[scal]), np.float32(ws[scal + 1]), np.float32(ws[scal + 6])
+        gf = _f32(_t2np(g)).reshape(R, C).astype(np.float32)
+        f = ws[fin:fin + nch].astype(np.float32) * fs
+        fm = np.broadcast_to(f[:, None] if right else f[None, :], (R, C))
+        x = (p_old * dec) + ((gf * fm) * step_s).reshape(-1)
+        want = sr.sr_round_bf16(x.astype(np.float32), seed=int(st["sr_seed"]), step=int(st["step"]))
+        got = _t2np(p).reshape(-1).view(np.uint16)
+        assert np.array_equal(got, want), f"step {t}: {(got != want).mean():.2e} differ"

@@ -198,6 +198,17 @@ class Adafactor8Bit(Optimizer):
         self._sr_seed_counter = 1
         self._ws = {}   # device workspaces (tensor tables, norm buffers, v_buf)
 
+    def add_param_group(self, param_group):
+        """``Optimizer.add_param_group`` plus a check that every parameter's route
+        can run with the group's block sizes, so an unsupported size fails here
+        and not halfway through a step."""
+        super().add_param_group(param_group)
+        try:
+            _check_block_sizes(self.param_groups[-1])
+        except ValueError:
+            self.param_groups.pop()
+            raise
+
     # ------------------------------------------------------------------ checkpoint
     def state_dict(self):
         sd = super().state_dict()
@@ -318,6 +329,18 @@ class Adafactor8Bit(Optimizer):
 
     # ------------------------------------------------------------------ dispatch
     def _step_group(self, group, params, grads, states):
+        """Plan and launch one group.  The plans advance each parameter's step
+        counter; if a launch raises, the counters go back, so a step that did not
+        run is not counted."""
+        before = [st.get("step", 0) for st in states]
+        try:
+            self._launch_group(group, params, grads, states)
+        except Exception:
+            for st, s0 in zip(states, before):
+                st["step"] = s0
+            raise
+
+    def _launch_group(self, group, params, grads, states):
         apollo_rank = group.get("apollo_rank", 0)
         batches: Dict[tuple, list] = {}
         ap_batches: Dict[tuple, list] = {}
@@ -354,6 +377,59 @@ class Adafactor8Bit(Optimizer):
             _run_apollo_batch(self, group, bkey, items)
         for p, work in copy_back:
             p.copy_(work)
+
+
+# ====================================================================== block sizes
+def _pow2_in(x, lo, hi):
+    return isinstance(x, int) and lo <= x <= hi and (x & (x - 1)) == 0
+
+
+def _check_block_sizes(group):
+    """Raise ValueError if a parameter of ``group`` would reach a kernel that cannot
+    run its block sizes.  The constructor already enforces the reference's own
+    rules (optimizer.py:1395-1416: B_V a multiple of 128, B_M a multiple of 4 and
+    at least 32, B_V % B_M == 0).  On top of those, the kernels here take:
+      * quantised 1-D V (AL8/AL16): B_V a power of two in [128, 2048], and coded
+        momentum with it a power of two in [32, B_V];
+      * coded momentum elsewhere (SGD, factored, fp32-V 1-D, APOLLO): B_M a power
+        of two in [32, 2048];
+      * APOLLO's coded low-rank V and CAME residual / confidence: B_V a power of
+        two in [128, 2048].
+    The factored row / column statistics take any B_V."""
+    if not group.get("quantize", True):
+        return
+    bs, mbs = group.get("block_size", 2048), group.get("m_block_size", 256)
+    vqt, mqt = group.get("v_quant_type", "al8"), group.get("m_quant_type", "uf8")
+    cqt = group.get("c_quant_type") or vqt
+    beta1, beta3 = group.get("beta1"), group.get("beta3")
+    sgd = group.get("beta2") is None and group.get("beta2_decay") is None
+    min8 = group.get("min_8bit_size", 4096)
+    coded_m = beta1 is not None and mqt != "fp32"
+    for p in group["params"]:
+        if p.numel() < min8:
+            continue
+        if sgd:
+            route, need_v, need_m = "SGD", False, coded_m
+        elif group.get("apollo_rank", 0) > 0 and p.dim() >= 2:
+            route = "APOLLO"
+            need_v = vqt != "fp32" or (beta3 is not None and cqt != "fp32")
+            need_m = coded_m
+        elif p.dim() >= 2 and group.get("factored", True):
+            route, need_v, need_m = "factored", False, coded_m
+        else:
+            route, need_v, need_m = "full-rank", vqt != "fp32", coded_m
+            if need_v and need_m and not _pow2_in(mbs, 32, bs):
+                raise ValueError(
+                    f"m_block_size={mbs} with block_size={bs}: the fused {route} kernel of this build needs "
+                    f"m_block_size to be a power of two in [32, block_size].")
+        if need_v and not _pow2_in(bs, 128, 2048):
+            raise ValueError(
+                f"block_size={bs}: the {route} kernels of this build need a power of two in [128, 2048] "
+                f"(parameter of shape {tuple(p.shape)}).")
+        if need_m and not _pow2_in(mbs, 32, 2048):
+            raise ValueError(
+                f"m_block_size={mbs}: the {route} kernels of this build need a power of two in [32, 2048] "
+                f"(parameter of shape {tuple(p.shape)}).")
 
 
 # ====================================================================== planning

@@ -118,8 +118,8 @@ def test_c1_adamw_4096x4096(steps):
     decode), so a few blocks' l_max/l_min drift by an ulp and near-tie codes
     there may flip.  The bound is the north star's (_check_trajectory)."""
     print(f"[parity] C1 4096x4096 x{steps}", flush=True)
-    res = _trajectory_vs_oracle([(4096, 4096)], steps, "normal_zeros", 0.05, 0)
-    _check_trajectory(*res, steps)
+    pc, pg, oc, og, touched, p0 = _trajectory_vs_oracle([(4096, 4096)], steps, "normal_zeros", 0.05, 0)
+    _check_trajectory(pc, pg, oc, og, touched, steps, p0)
 
 
 @pytest.mark.gpu

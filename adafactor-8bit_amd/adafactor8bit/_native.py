@@ -106,6 +106,10 @@ _SIGS = {
                                         _c_i64, _c_d, _c_d, _c_f, _c_i, _c_f, _c_f, _c_f, _c_i, _c_i,
                                         _c_i, _c_i, _c_f, _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i,
                                         _c_vp]),
+    "a8_fused_update_1d_multi_noalloc": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(Tensor1D), _c_i, _c_d, _c_d,
+                                                _c_f, _c_i, _c_f, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_f,
+                                                _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i, _c_vp]),
+    "a8_noalloc_max_tensors_1d": (_c_i, []),
     "a8_table_bytes_1d": (_c_i64, [_c_i]),
     "a8_fused_update_1d_full": (_c_i, [_c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                        _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,

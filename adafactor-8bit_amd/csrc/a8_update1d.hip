@@ -20,6 +20,8 @@
 #include "a8_mcodec.cuh"
 #include "a8_abi_impl.h"
 
+#include <mutex>
+
 namespace a8 {
 
 struct Desc1D {
@@ -775,6 +777,107 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   return launch_any(dtype, sr, v_bits, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
 }
 
+// Validate a multi-tensor launch and, if `image` is non-null, write its device table
+// image there (a8_table_bytes_1d(ntensors) bytes: the descriptors, then one int32
+// first workgroup per tensor).  The workgroup count goes to *nwg_out.
+static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int ntensors, int block_size,
+                          int m_block_size, int m_bits, int m_mode, int v_bits, int momentum_only, char* image,
+                          int64_t* nwg_out) {
+  if (!tensors) return set_error(A8_ERR_ARG, "null tensor list");
+  const bool has_m = tensors[0].m_q != nullptr;
+  int rc = check_common(dtype, 0, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
+  if (rc) return rc;
+  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
+  if (mode == 4 && !momentum_only) return set_error(A8_ERR_ARG, "MNORM needs momentum_only");
+  Desc1D* tab = reinterpret_cast<Desc1D*>(image);
+  int32_t* first = image ? reinterpret_cast<int32_t*>(image + sizeof(Desc1D) * (size_t)ntensors) : nullptr;
+  int64_t wg = 0;
+  for (int i = 0; i < ntensors; ++i) {
+    const a8_tensor1d& t = tensors[i];
+    if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
+    if (!t.grad || !t.v_q || !t.v_scale || !t.v_min_log || (has_m && !t.m_scale))
+      return set_error(A8_ERR_ARG, "null state pointer");
+    if (mode != 1 && mode != 4 && !t.param) return set_error(A8_ERR_ARG, "null param");
+    if ((mode == 1 || mode == 2 || mode == 4) && !t.v_buf)
+      return set_error(A8_ERR_ARG, "NORM/APPLY/MNORM need v_buf");
+    if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "NORM/APPLY/LAG/MNORM need norm_buf");
+    if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "LAG/MNORM need prev_norm");
+    if (mode == 4 && !has_m) return set_error(A8_ERR_ARG, "MNORM needs momentum codes");
+    if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.v_q) || (has_m && !aligned16(t.m_q)))
+      return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
+    if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
+    if (image) {
+      Desc1D D{};
+      D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
+      D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
+      D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
+      D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed;
+      std::memcpy(&tab[i], &D, sizeof(Desc1D));
+      const int32_t f = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
+      std::memcpy(&first[i], &f, sizeof(int32_t));
+    }
+    wg += (t.numel + kWGElems - 1) / kWGElems;
+  }
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  *nwg_out = wg;
+  return 0;
+}
+
+static int launch_multi_1d(int mode, int stochastic, int dtype, bool has_m, int ntensors, const void* table_dev,
+                           int64_t nwg, double beta1, double beta_val, float eps_for_denom, int use_adam_denom,
+                           float log_floor, float eps_for_grad_sq, float eps_sq, int block_size, int m_block_size,
+                           int m_bits, int m_mode, float d, int v_bits, int momentum_only, uint64_t sr_step,
+                           float alpha_val, float decay_val, int has_decay, hipStream_t st) {
+  Hyper1D h{};
+  h.beta1 = (float)beta1;
+  h.w_m = (float)(1.0 - beta1);
+  h.bv = (float)beta_val;
+  h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
+  h.floor_ = log_floor; h.d = d;
+  h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
+  h.lbv = ilog2(h.block_size); h.lbm = ilog2(h.m_block_size);
+  h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
+  h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
+  h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
+  h.sr_step = sr_step;
+  Desc1D none{};
+  return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev), ntensors,
+                    nwg, h, st);
+}
+
+// ------------------------------------------------------------ no-allocation table
+// a8_fused_update_1d_multi_noalloc keeps its tensor table in this file-scope
+// device array instead of a caller buffer.  In host code `scratch` names a host
+// stand-in, not device memory: its device address is taken once per device with
+// hipGetSymbolAddress (that device current) and only that address is used.  Every
+// GPU holds its own copy until the process ends.
+constexpr int kScratchBytes = 64 * 1024;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) char scratch[kScratchBytes];
+static void* g_scratch_ptr[kScratchDevices];
+static std::mutex g_scratch_mu;
+alignas(16) static char g_stage[kScratchBytes];   // host image of the table (a8_fused_update_1d_multi_noalloc)
+static std::mutex g_stage_mu;
+
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return set_error(A8_ERR_HIP, "no usable current device for the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      char msg[160];
+      snprintf(msg, sizeof msg, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return set_error(A8_ERR_HIP, msg);
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 extern "C" {
 
 int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
@@ -801,64 +904,65 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                              int momentum_only, uint64_t sr_step, float alpha_val,
                              float decay_val, int has_decay, int upload, void* stream) {
   if (ntensors <= 0) return 0;
-  const bool has_m = tensors[0].m_q != nullptr;
-  int rc = check_common(dtype, 0, block_size, m_block_size, m_bits, m_mode, v_bits, has_m);
-  if (rc) return rc;
   if (a8_table_bytes_1d(ntensors) > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_1d(ntensors)");
-  if (mode < 0 || mode > 4) return set_error(A8_ERR_ARG, "mode must be 0..4");
-  if (mode == 4 && !momentum_only) return set_error(A8_ERR_ARG, "MNORM needs momentum_only");
-  std::vector<Desc1D> tab((size_t)ntensors);
-  std::vector<int32_t> first((size_t)ntensors);
-  int64_t wg = 0;
-  for (int i = 0; i < ntensors; ++i) {
-    const a8_tensor1d& t = tensors[i];
-    if ((t.m_q != nullptr) != has_m) return set_error(A8_ERR_ARG, "mixed M / no-M tensors in one launch");
-    if (!t.grad || !t.v_q || !t.v_scale || !t.v_min_log || (has_m && !t.m_scale))
-      return set_error(A8_ERR_ARG, "null state pointer");
-    if (mode != 1 && mode != 4 && !t.param) return set_error(A8_ERR_ARG, "null param");
-    if ((mode == 1 || mode == 2 || mode == 4) && !t.v_buf)
-      return set_error(A8_ERR_ARG, "NORM/APPLY/MNORM need v_buf");
-    if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "NORM/APPLY/LAG/MNORM need norm_buf");
-    if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "LAG/MNORM need prev_norm");
-    if (mode == 4 && !has_m) return set_error(A8_ERR_ARG, "MNORM needs momentum codes");
-    if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.v_q) || (has_m && !aligned16(t.m_q)))
-      return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
-    if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
-    Desc1D& D = tab[(size_t)i];
-    D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
-    D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
-    D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
-    D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed;
-    first[(size_t)i] = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
-    wg += (t.numel + kWGElems - 1) / kWGElems;
-  }
-  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  std::vector<char> image;
+  if (upload) image.resize((size_t)a8_table_bytes_1d(ntensors));
+  int64_t nwg = 0;
+  int rc = table_image_1d(mode, dtype, tensors, ntensors, block_size, m_block_size, m_bits, m_mode, v_bits,
+                          momentum_only, upload ? image.data() : nullptr, &nwg);
+  if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  if (upload) {
-    // one staging copy: descriptors followed by the first-workgroup array
-    std::vector<char> blob((size_t)a8_table_bytes_1d(ntensors));
-    std::memcpy(blob.data(), tab.data(), sizeof(Desc1D) * (size_t)ntensors);
-    std::memcpy(blob.data() + sizeof(Desc1D) * (size_t)ntensors, first.data(), sizeof(int32_t) * (size_t)ntensors);
-    if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
-      return set_error(A8_ERR_HIP, "table upload failed");
-  }
-  Hyper1D h{};
-  h.beta1 = (float)beta1;
-  h.w_m = (float)(1.0 - beta1);
-  h.bv = (float)beta_val;
-  h.eps_d = eps_for_denom; h.eps_g = eps_for_grad_sq; h.eps_sq = eps_sq;
-  h.floor_ = log_floor; h.d = d;
-  h.block_size = block_size; h.m_block_size = has_m ? m_block_size : block_size;
-  h.lbv = ilog2(h.block_size); h.lbm = ilog2(h.m_block_size);
-  h.mk = has_m ? mk_of(m_bits, m_mode) : 0;
-  h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
-  h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
-  h.sr_step = sr_step;
-  Desc1D none{};
-  return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev),
-                    ntensors, wg, h, st);
+  if (upload && upload_table(table_dev, image.data(), image.size(), st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  return launch_multi_1d(mode, stochastic, dtype, tensors[0].m_q != nullptr, ntensors, table_dev, nwg, beta1,
+                         beta_val, eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, block_size,
+                         m_block_size, m_bits, m_mode, d, v_bits, momentum_only, sr_step, alpha_val, decay_val,
+                         has_decay, st);
 }
+
+int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
+                                     int ntensors, double beta1, double beta_val, float eps_for_denom,
+                                     int use_adam_denom, float log_floor, float eps_for_grad_sq, float eps_sq,
+                                     int block_size, int m_block_size, int m_bits, int m_mode, float d,
+                                     int v_bits, int momentum_only, uint64_t sr_step, float alpha_val,
+                                     float decay_val, int has_decay, int upload, void* stream) {
+  if (ntensors <= 0) return 0;
+  if (a8_table_bytes_1d(ntensors) > (int64_t)kScratchBytes) {
+    char msg[160];
+    snprintf(msg, sizeof msg, "a8_fused_update_1d_multi_noalloc: %d tensors need %lld table bytes, above the %d-byte "
+             "scratch (at most %d tensors)", ntensors, (long long)a8_table_bytes_1d(ntensors), kScratchBytes,
+             a8_noalloc_max_tensors_1d());
+    return set_error(A8_ERR_SIZE, msg);
+  }
+  void* table_dev = nullptr;
+  int rc = scratch_of_current_device(&table_dev);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  int64_t nwg = 0;
+  if (upload) {
+    // The image is built in a host buffer of the library's own (no allocation) and
+    // copied from there; the copy from pageable memory has consumed the buffer when
+    // hipMemcpyAsync returns, so the next call may reuse it.
+    std::lock_guard<std::mutex> lock(g_stage_mu);
+    rc = table_image_1d(mode, dtype, tensors, ntensors, block_size, m_block_size, m_bits, m_mode, v_bits,
+                        momentum_only, g_stage, &nwg);
+    if (rc) return rc;
+    if (hipMemcpyAsync(table_dev, g_stage, (size_t)a8_table_bytes_1d(ntensors), hipMemcpyHostToDevice, st) !=
+        hipSuccess)
+      return set_error(A8_ERR_HIP, "scratch table upload failed");
+  } else {
+    rc = table_image_1d(mode, dtype, tensors, ntensors, block_size, m_block_size, m_bits, m_mode, v_bits,
+                        momentum_only, nullptr, &nwg);
+    if (rc) return rc;
+  }
+  return launch_multi_1d(mode, stochastic, dtype, tensors[0].m_q != nullptr, ntensors, table_dev, nwg, beta1,
+                         beta_val, eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, block_size,
+                         m_block_size, m_bits, m_mode, d, v_bits, momentum_only, sr_step, alpha_val, decay_val,
+                         has_decay, st);
+}
+
+int a8_noalloc_max_tensors_1d(void) { return (int)(kScratchBytes / (sizeof(Desc1D) + sizeof(int32_t))); }
 
 int64_t a8_table_bytes_1d(int ntensors) {
   return ((int64_t)sizeof(Desc1D) + (int64_t)sizeof(int32_t)) * (int64_t)ntensors;

@@ -120,6 +120,26 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                              float decay_val, int has_decay, int upload, void* stream);
 int64_t a8_table_bytes_1d(int ntensors);
 
+/* a8_fused_update_1d_multi without any allocation.  It has no counterpart in the
+ * reference; it is for callers that cannot allocate device or pinned host memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * Arguments are those of a8_fused_update_1d_multi minus table_dev / table_bytes:
+ * the tensor table lives in a 64 KiB device array of the library, one per GPU,
+ * held until the process ends, so at most a8_noalloc_max_tensors_1d() tensors
+ * (528) fit; more returns A8_ERR_SIZE.  With `upload` non-zero the table is
+ * written there (a stream-ordered copy from a host buffer of the library); with
+ * upload == 0 the table of the previous call on this GPU is reused, so the
+ * previous call must have had the same tensors.  Every call on a GPU shares that
+ * GPU's array, which keeps the last call's table: calls that overlap on one GPU
+ * (two streams, or two host threads) race. */
+int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
+                                     int ntensors, double beta1, double beta_val, float eps_for_denom,
+                                     int use_adam_denom, float log_floor, float eps_for_grad_sq, float eps_sq,
+                                     int block_size, int m_block_size, int m_bits, int m_mode, float d,
+                                     int v_bits, int momentum_only, uint64_t sr_step, float alpha_val,
+                                     float decay_val, int has_decay, int upload, void* stream);
+int a8_noalloc_max_tensors_1d(void);
+
 /* Replaces fused_update_1d_full_{noclip,norm,apply,lag}[_sr] (kernels.cu:1374-1515;
  * called at optimizer.py:2147-2183): fp32 V (and optional fp32 M, NULL for none)
  * for tensors below min_8bit_size or with quantize=False.  NORM writes V (and M

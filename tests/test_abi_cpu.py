@@ -93,3 +93,20 @@ def test_apollo_lowrank_and_phase_argument_errors_without_gpu():
     assert rc == -1 and b"phase" in L.a8_last_error()
     assert L.a8_vema_fp32(None, None, 0, 0.001, 0.0, 4, None) == -1
     assert L.a8_vema_fp32(256, 256, 9, 0.001, 0.0, 4, None) == -2
+
+
+def test_noalloc_rejects_more_tensors_than_its_scratch_holds():
+    """The no-allocation multi-tensor step holds its table in a fixed 64 KiB device
+    array: a launch over more tensors fails on the host with A8_ERR_SIZE."""
+    from adafactor8bit import _native as nat
+    L = nat.lib()
+    cap = L.a8_noalloc_max_tensors_1d()
+    assert cap * int(L.a8_table_bytes_1d(1)) <= 64 * 1024 < (cap + 1) * int(L.a8_table_bytes_1d(1))
+    n = cap + 1
+    arr = (nat.Tensor1D * n)()
+    rc = L.a8_fused_update_1d_multi_noalloc(0, 0, 0, arr, n, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 2048, 256, 8,
+                                            0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None)
+    assert rc == -4, rc
+    assert b"scratch" in L.a8_last_error()
+    assert L.a8_fused_update_1d_multi_noalloc(0, 0, 0, arr, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 2048, 256,
+                                              8, 0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None) == 0

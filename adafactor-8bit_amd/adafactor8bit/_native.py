@@ -143,6 +143,8 @@ _SIGS = {
     "a8_apollo_x_workspace_floats": (_c_i64, [_c_i64, _c_i64]),
     "a8_dequantize_log_nonneg": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_dequantize_dynamic": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
+    "a8_dequantize_momentum": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_i, _c_vp]),
+    "a8_al_encode": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_sgd_step": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                            _c_i64, _c_d, _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_u64, _c_vp]),
     "a8_sgd_step_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(TensorSgd), _c_i, _c_vp, _c_i64, _c_d, _c_i,

@@ -217,53 +217,14 @@ class Adafactor8Bit(Optimizer):
         return sd
 
     def load_state_dict(self, state_dict):
-        """optimizer.py:1467-1553: keep quantised/fp32 state dtypes, restore type tags."""
-        state_dict = state_dict.copy()
-        state_dict["state"] = {
-            idx: ({k: v for k, v in st.items() if k not in ("m", "m_q", "m_scale")}
-                  if isinstance(st, dict) and "apollo_seed" in st else st)
-            for idx, st in state_dict.get("state", {}).items()
-        }
-        old_vqt, old_mqt, old_cqt, saved_tensors = {}, {}, {}, {}
-        for idx, st in state_dict.get("state", {}).items():
-            if isinstance(st, dict):
-                old_vqt[idx] = st.get("v_quant_type", "al8")
-                old_mqt[idx] = st.get("m_quant_type", "uf8")
-                old_cqt[idx] = st.get("c_quant_type", old_vqt[idx])
-                saved_tensors[idx] = {k: v for k, v in st.items() if torch.is_tensor(v) and k != "step"}
-        saved_ids = [i for g in state_dict.get("param_groups", []) for i in g.get("params", [])]
-        self._apollo_seed_counter = state_dict.get("_apollo_seed_counter", 0)
-        self._sr_seed_counter = state_dict.get("_sr_seed_counter", 0)
-        sr_policy = [g.get("stochastic_round_writeback", False) for g in self.param_groups]
-        sr_missing = [("stochastic_round_writeback" not in sg) if isinstance(sg, dict) else True
-                      for sg in state_dict.get("param_groups", [])]
-        super().load_state_dict(state_dict)
-        if len(self.param_groups) == len(sr_missing):
-            for g, miss, pol in zip(self.param_groups, sr_missing, sr_policy):
-                if miss:
-                    g["stochastic_round_writeback"] = pol
-        cur = [p for g in self.param_groups for p in g["params"]]
-        if len(saved_ids) == len(cur):
-            id_map = dict(zip(saved_ids, cur))
-            for sid, tensors in saved_tensors.items():
-                p = id_map.get(sid)
-                if p is None or p not in self.state:
-                    continue
-                st = self.state[p]
-                for k, v in tensors.items():
-                    st[k] = v.detach().to(device=p.device, dtype=v.dtype, copy=True).contiguous()
-        i = 0
-        for g in self.param_groups:
-            for p in g["params"]:
-                if p in self.state:
-                    st = self.state[p]
-                    st["v_quant_type"] = old_vqt.get(i, "al8")
-                    st["m_quant_type"] = old_mqt.get(i, "uf8")
-                    st["c_quant_type"] = old_cqt.get(i, st["v_quant_type"])
-                    s = st.get("step")
-                    if torch.is_tensor(s):
-                        st["step"] = int(s)
-                i += 1
+        """optimizer.py:1467-1553: the base loader maps saved parameters to these
+        ones; state tensors keep their stored dtype (fp32 or codes, whatever the
+        parameter's dtype), the codec tags, seed counters and SR policy come from
+        the checkpoint, and the loaded state is then compacted (optimizer.py:1555-1590)."""
+        ckpt = S.Checkpoint(state_dict, self.param_groups)
+        super().load_state_dict(ckpt.skeleton)
+        ckpt.restore(self)
+        S.compact(self)
         self._ws.clear()
 
     def _warmup_allocator(self):
@@ -1250,7 +1211,7 @@ def _apollo_prep(opt, p, grad, st, group):
             st["col_var_low"] = torch.zeros((1, low_shape[1]), dtype=torch.float32, device=dev)
     elif first:   # optimizer.py:2770-2779 creates the low-rank V state on the first step
         if vbits:
-            S.init_v_state(st, "v_low", (n_low,), bs, dev, vqt)
+            S.new_al_slot(st, "v_low", (n_low,), bs, vqt, dev)
         else:
             st["v_low"] = torch.zeros(n_low, dtype=torch.float32, device=dev)
     has_m = beta1 is not None
@@ -1261,7 +1222,7 @@ def _apollo_prep(opt, p, grad, st, group):
             if st.get("m_low") is None:
                 st["m_low"] = torch.zeros((R, rank) if right else (rank, C), dtype=torch.float32, device=dev)
         elif st.get("m_low_q") is None:
-            S.m_init_state(st, n_low, mbs, mqt, dev, prefix="m_low")
+            S.new_momentum_codes(st, "m_low", n_low, mbs, mqt, dev)
     fira = bool(group.get("enable_fira_for_apollo", True))
     has_prev = 0
     if fira:
@@ -1325,15 +1286,15 @@ def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, f
     cbits = 0 if (not quant or cqt == "fp32") else (16 if cqt == "al16" else 8)
     if came and not factorize and st.get("res_low_q") is None and st.get("res_low") is None:
         if cbits:
-            S.init_v_state(st, "res_low", low_shape, bs, dev, cqt)
+            S.new_al_slot(st, "res_low", low_shape, bs, cqt, dev)
         else:
             st["res_low"] = torch.zeros(low_shape, dtype=torch.float32, device=dev)
     if came and factorize:
         rs, cs = (low_shape[0], 1), (1, low_shape[1])
         if cbits:
             if st.get("conf_row_low_q") is None:
-                S.init_v_state(st, "conf_row_low", rs, bs, dev, cqt)
-                S.init_v_state(st, "conf_col_low", cs, bs, dev, cqt)
+                S.new_al_slot(st, "conf_row_low", rs, bs, cqt, dev)
+                S.new_al_slot(st, "conf_col_low", cs, bs, cqt, dev)
         elif st.get("conf_row_low") is None:
             st["conf_row_low"] = torch.zeros(rs, dtype=torch.float32, device=dev)
             st["conf_col_low"] = torch.zeros(cs, dtype=torch.float32, device=dev)

@@ -421,6 +421,26 @@ int a8_dequantize_log_nonneg(float* output, const void* q, const float* scale, c
 int a8_dequantize_dynamic(float* output, const uint8_t* q, const float* scale, int64_t numel, int block_size,
                           int m_bits, void* stream);
 
+/* Replaces _m_dequantize (optimizer.py:535-541) for every momentum codec, where
+ * the reference decodes uniform codes with PyTorch ops (_dequantize_uniform_pytorch,
+ * optimizer.py:522-532: (q - 128) * (s / 128), or (q - 8) * (s / 8) for 4 bits)
+ * and dynamic codes as a8_dequantize_dynamic.  m_mode 0 uniform, 1 dynamic;
+ * m_bits 8 or 4 (even element in the high nibble).  Used when a checkpoint's
+ * momentum changes from codes to fp32 (_migrate_quantize_flag, optimizer.py:1032-1042). */
+int a8_dequantize_momentum(float* output, const uint8_t* q, const float* scale, int64_t numel, int block_size,
+                           int m_bits, int m_mode, void* stream);
+
+/* Replaces _quant_v (optimizer.py:379-383, _log_quantize_nonneg 299-325) on a whole
+ * fp32 tensor of non-negative values: per block of any size, l_max = log2 of the
+ * largest value, l_min = log2 of the smallest non-zero one floored at log_floor
+ * (the reference's default -126), l_min := l_max - 1 for a flat block, codes
+ * round((log2 v - l_min) / s * (L - 2)) + 1 and 0 for zeros.  q holds
+ * ceil(numel / block_size) * block_size codes (uint8, or int16 for v_bits 16) and
+ * receives 0 for the padding.  Used when a checkpoint's second-moment state changes
+ * from fp32 to codes (_migrate_quantize_flag, optimizer.py:976-1012). */
+int a8_al_encode(void* q, float* scale, float* min_log, const float* x, int64_t numel, int block_size, int v_bits,
+                 float log_floor, void* stream);
+
 /* Replaces the SGD branch of _update_param_8bit (optimizer.py:2045-2077; beta2 and
  * beta2_decay both None), whose CUDA path calls fused_m_quantize_lerp
  * (kernels.cu:523-588) and then _apply_update_pytorch (optimizer.py:866-881).

@@ -56,8 +56,8 @@ def test_module_noclip_step_matches_oracle(mqt, vbits):
 
     K.set_qmap(*[q.cuda() for q in K.qmaps()])
     st = {}
-    S.init_v_state(st, "variance", shape, bs, "cuda", vqt)
-    S.m_init_state(st, pg.numel(), mbs, mqt, "cuda", shape=shape)
+    S.new_al_slot(st, "variance", shape, bs, vqt, "cuda")
+    S.new_momentum_codes(st, "m", pg.numel(), mbs, mqt, "cuda")
     bc1, bc2 = 1.0 - 0.9, 1.0 - 0.999
     alpha = (torch.tensor(1e-4, dtype=torch.float32) * (math.sqrt(bc2) / bc1)).reshape(1).cuda()
     eps1 = 1e-8

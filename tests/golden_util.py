@@ -12,8 +12,9 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
 def names():
+    """Step-trajectory fixtures (the checkpoint fixtures, ckpt_*.npz, have a format of their own)."""
     return sorted(os.path.splitext(os.path.basename(f))[0]
-                  for f in glob.glob(os.path.join(GOLDEN, "*.npz")))
+                  for f in glob.glob(os.path.join(GOLDEN, "*.npz")) if not os.path.basename(f).startswith("ckpt_"))
 
 
 def load(name):

@@ -60,6 +60,18 @@ def tinyllama_shapes():
     return shapes
 
 
+def llama3_8b_shapes():
+    """Llama-3-8B: 32 layers, hidden 4096, FFN 14336, 8 kv heads of 128 (k/v 1024x4096),
+    vocab 128256, untied embedding and head: 291 tensors, 8,030,261,248 params.  Its
+    4096-element RMSNorm vectors reach min_8bit_size, so every tensor is quantised."""
+    H, F, KV, V, L = 4096, 14336, 1024, 128256, 32
+    shapes = [(V, H)]
+    for _ in range(L):
+        shapes += [(H, H), (KV, H), (KV, H), (H, H), (F, H), (F, H), (H, F), (H,), (H,)]
+    shapes += [(H,), (V, H)]
+    return shapes
+
+
 def step_bytes(shapes, bv=2048, bm=256, min8=4096):
     """Algorithmic HBM bytes of one step: p r+w, g r, codes r+w, block metadata r+w;
     fp32-state tensors: p r+w, g r, v r+w, m r+w."""
@@ -127,6 +139,11 @@ def make_grad(kind, shape, gen, dev, i, embed):
     if kind == "adamw":
         g = torch.randn(shape, device=dev, generator=gen) * 1e-3
         return g * (torch.rand(shape, device=dev, generator=gen) >= 0.05)
+    if kind == "adamw_llama3_8b":   # Student-t df=3 scaled 1e-3 with 2% exact zeros
+        z = torch.randn(shape, device=dev, generator=gen)
+        chi = sum(torch.randn(shape, device=dev, generator=gen) ** 2 for _ in range(3))
+        g = 1e-3 * z * torch.sqrt(3.0 / chi)
+        return g * (torch.rand(shape, device=dev, generator=gen) >= 0.02)
     if kind == "adafactor":  # Student-t df=3 scaled 1e-3; embedding rows 90% zero
         z = torch.randn(shape, device=dev, generator=gen)
         chi = sum(torch.randn(shape, device=dev, generator=gen) ** 2 for _ in range(3))
@@ -153,7 +170,9 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
     torch.set_num_threads(threads)
     shape, pdt, gk = (4096, 4096), torch.float32, "normal_zeros"
     kw = dict(ADAMW)
-    if workload == "adafactor":
+    if workload == "adamw_llama3_8b":
+        shape, gk = (4096, 14336), "student_t"
+    elif workload == "adafactor":
         shape, gk, kw = (2048, 2048), "student_t", dict(ADAFACTOR)
     elif workload == "came":
         shape, gk, kw = (2048, 2048), "logscale", dict(CAME)
@@ -161,7 +180,8 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
         shape, pdt, kw = (2048, 2048), torch.bfloat16, dict(APOLLO, stochastic_round_writeback=False)
     p = torch.nn.Parameter(make_param(shape, 0, 0).to(pdt))
     opt = F.OracleOptimizer([p], **kw)
-    grads = [make_grad(shape, 0, t, 0, kind=gk).to(pdt) for t in (1, 2)]
+    zf = 0.02 if workload == "adamw_llama3_8b" else 0.05
+    grads = [make_grad(shape, 0, t, 0, kind=gk, zero_frac=zf).to(pdt) for t in (1, 2)]
     p.grad = grads[0]
     opt.step()
     times = []
@@ -179,6 +199,7 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
     med = times[len(times) // 2]
     n = shape[0] * shape[1]
     what = {"adamw": "C1: one 4096x4096 fp32 AdamW UF8/AL8 step",
+            "adamw_llama3_8b": "C5: one 4096x14336 fp32 AdamW UF8/AL8 step (Student-t grads)",
             "adafactor": "C2: one 2048x2048 fp32 factored Adafactor AL8 step",
             "came": "C3: one 2048x2048 fp32 CAME UF8/AL16/AL16+Fira step",
             "apollo": "C4: one 2048x2048 bf16 APOLLO r=256 UF8/AL8 step (deterministic writeback)"}[workload]
@@ -194,8 +215,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="after timing, run a plain 256 MiB fp32 copy (for counter calibration)")
-    ap.add_argument("--workload", default="adamw", choices=["adamw", "adafactor", "came", "apollo"],
-                    help="adamw (default, the headline metric), adafactor (C2), came (C3) or apollo (C4)")
+    ap.add_argument("--workload", default="adamw",
+                    choices=["adamw", "adafactor", "came", "apollo", "adamw_llama3_8b"],
+                    help="adamw (default, the headline metric), adafactor (C2), came (C3), apollo (C4) or "
+                         "adamw_llama3_8b (C5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (single-GPU boxes; no collectives); "
@@ -206,7 +229,8 @@ def main():
     from adafactor8bit import _native as nat
     dev = torch.device("cuda", 0)
     torch.manual_seed(0)
-    shapes = tinyllama_shapes()
+    c5 = args.workload == "adamw_llama3_8b"
+    shapes = llama3_8b_shapes() if c5 else tinyllama_shapes()
     params = []
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
@@ -221,7 +245,7 @@ def main():
         p.grad = g
         params.append(p)
     nparams = sum(p.numel() for p in params)
-    if args.workload != "adamw":
+    if args.workload not in ("adamw", "adamw_llama3_8b"):
         return bench_factored(args, params, nparams, shapes, Adafactor8Bit)
     opt = Adafactor8Bit(params, **ADAMW)
     for _ in range(args.warmup):
@@ -265,9 +289,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
 
-    traffic = None
+    traffic = None   # counter-measured bytes exist for the TinyLlama launch only
     tpath = os.path.join(ROOT, "profiles", "traffic_adamw_uf8_al8_tinyllama.json")
-    if os.path.exists(tpath):
+    if not c5 and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
@@ -284,16 +308,19 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "adamw_uf8_al8_tinyllama_1.1b_fp32", "params": nparams,
+        "config": {"workload": "adamw_uf8_al8_llama3_8b_fp32" if c5 else "adamw_uf8_al8_tinyllama_1.1b_fp32",
+                   "params": nparams,
                    "tensors": len(params), "block_size": 2048, "m_block_size": 256,
                    "step_bytes": qbytes + fbytes},
         "step_GBps": (qbytes + fbytes) / (ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": "k_update1d<float,8,0,false> (multi-tensor, 156 tensors)",
+                     "kernel": f"k_update1d<float,8,0,false> (multi-tensor, {len(big)} tensors)",
                      "kernel_ms_avg": k_avg, "kernel_ms_min": kms[0], "bytes_per_launch": qbytes},
-        "cpu_baseline": None if args.no_cpu else cpu_baseline("adamw"),
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.workload),
     }
+    if c5:
+        out["metric"] = "fused step params/sec + achieved HBM GB/s (% of peak), AL8 AdamW @8.03B params"
     print(json.dumps(out), flush=True)
 
 

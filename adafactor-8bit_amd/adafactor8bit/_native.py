@@ -24,6 +24,16 @@ _c_f = ctypes.c_float
 _c_d = ctypes.c_double
 
 
+class StepSpec(ctypes.Structure):
+    """Mirror of ``a8_step_spec``."""
+    _fields_ = [("beta1", _c_d), ("beta2", _c_d), ("beta2_decay", _c_d), ("eps1", _c_d), ("lr", _c_d),
+                ("wd", _c_f), ("v_mode", _c_i), ("relative_step", _c_i), ("bias_mode", _c_i), ("adam_denom", _c_i),
+                ("wd_mode", _c_i), ("fact_bias_mode", _c_i)]
+
+
+STEP_SCALARS_BYTES = 40   # sizeof(a8_step_scalars)
+
+
 class Tensor1D(ctypes.Structure):
     """Mirror of ``a8_tensor1d``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
@@ -105,11 +115,12 @@ _SIGS = {
     "a8_fused_update_1d_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(Tensor1D), _c_i, _c_vp,
                                         _c_i64, _c_d, _c_d, _c_f, _c_i, _c_f, _c_f, _c_f, _c_i, _c_i,
                                         _c_i, _c_i, _c_f, _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i,
-                                        _c_vp]),
+                                        _c_vp, _c_vp]),
     "a8_fused_update_1d_multi_noalloc": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(Tensor1D), _c_i, _c_d, _c_d,
                                                 _c_f, _c_i, _c_f, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_f,
-                                                _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i, _c_vp]),
+                                                _c_i, _c_i, _c_u64, _c_f, _c_f, _c_i, _c_i, _c_vp, _c_vp]),
     "a8_noalloc_max_tensors_1d": (_c_i, []),
+    "a8_step_advance": (_c_i, [ctypes.POINTER(StepSpec), _c_vp, _c_vp, _c_vp]),
     "a8_table_bytes_1d": (_c_i64, [_c_i]),
     "a8_fused_update_1d_full": (_c_i, [_c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                        _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,
@@ -117,13 +128,13 @@ _SIGS = {
     "a8_fused_update_1d_full_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(TensorFull), _c_i, _c_vp,
                                              _c_i64, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_f, _c_i,
                                              _c_f, _c_f, _c_i, _c_i, _c_u64, _c_i, _c_f, _c_i, _c_f,
-                                             _c_i, _c_i, _c_vp]),
+                                             _c_i, _c_i, _c_vp, _c_vp]),
     "a8_table_bytes_full": (_c_i64, [_c_i]),
     "a8_fira_scalar": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_factored_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(Tensor2D), _c_i, _c_vp, _c_i64, _c_i, _c_d,
                                 _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_f, _c_i, _c_f, _c_f,
                                 _c_i, _c_i, _c_d, _c_i, _c_i, _c_i, _c_u64, _c_i, _c_d, _c_f, _c_i,
-                                _c_vp]),
+                                _c_vp, _c_vp]),
     "a8_factored_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "a8_table_bytes_2d": (_c_i64, [_c_i]),
     "a8_apollo_step": (_c_i, [_c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_i, _c_d, _c_d, _c_i, _c_f,

@@ -68,6 +68,15 @@ class Adafactor8Bit(Optimizer):
     ``Adafactor8Bit`` (adafactor8bit/optimizer.py:1176-1360).  ``use_cuda_kernel``
     is accepted for compatibility; the step always runs on the HIP library and
     parameters must live on a ROCm device.
+
+    ``capturable`` (not in the reference; default False) keeps each group's step
+    count on the device.  A step then derives its scalars there (a8_step_advance)
+    and launches only multi-tensor kernels that read them, so ``step()`` can be
+    captured in a CUDA/HIP graph after one eager step and replayed; eager and
+    replayed steps run the same kernels on the same inputs, so they give the same
+    bits.  Paths that need host-side scalars (APOLLO, LAG, per-tensor launches,
+    tensor learning rates) raise in this mode.  ``state_dict()`` reads the device
+    counts back.
     """
 
     def __init__(
@@ -111,6 +120,7 @@ class Adafactor8Bit(Optimizer):
         momentum_only_1d: Optional[bool] = None,
         bias_correction: Optional[bool] = None,
         warmup_multiplier: float = 0.0,
+        capturable: bool = False,
     ):
         # argument validation: optimizer.py:1362-1432 (same conditions and messages)
         if lr < 0.0:
@@ -191,7 +201,7 @@ class Adafactor8Bit(Optimizer):
             scale_weight_decay=scale_weight_decay,
             enable_fira_for_adafactor=enable_fira_for_adafactor, fira_margin=fira_margin,
             lag_norm=lag_norm, momentum_only_1d=momentum_only_1d, bias_correction=bias_correction,
-            warmup_multiplier=warmup_multiplier,
+            warmup_multiplier=warmup_multiplier, capturable=capturable,
         )
         super().__init__(params, defaults)
         self._apollo_seed_counter = 1
@@ -211,6 +221,12 @@ class Adafactor8Bit(Optimizer):
 
     # ------------------------------------------------------------------ checkpoint
     def state_dict(self):
+        for key, ent in list(self._ws.items()):
+            if isinstance(key, tuple) and len(key) == 3 and key[1] == "devstep":
+                t = int(ent["ctr"].item())   # graph replays advance only the device count
+                for p in ent["group"]["params"]:
+                    if p in self.state and "step" in self.state[p]:
+                        self.state[p]["step"] = t
         sd = super().state_dict()
         sd["_apollo_seed_counter"] = self._apollo_seed_counter
         sd["_sr_seed_counter"] = self._sr_seed_counter
@@ -286,22 +302,29 @@ class Adafactor8Bit(Optimizer):
                 if sr_on and p.dtype in (torch.bfloat16, torch.float16) and "sr_seed" not in st:
                     st["sr_seed"] = self._sr_seed_counter
                     self._sr_seed_counter += 1
-            self._step_group(group, params, grads, states)
+            dsc = _advance_device_step(self, group, params, states) if group.get("capturable") else None
+            try:
+                self._step_group(group, params, grads, states, dsc)
+            except Exception:
+                if dsc is not None:   # the device count moved on; rebuild it from the restored host counts
+                    self._ws.pop((params[0].device, "devstep", id(group)), None)
+                raise
 
     # ------------------------------------------------------------------ dispatch
-    def _step_group(self, group, params, grads, states):
+    def _step_group(self, group, params, grads, states, dsc=None):
         """Plan and launch one group.  The plans advance each parameter's step
         counter; if a launch raises, the counters go back, so a step that did not
-        run is not counted."""
+        run is not counted.  ``dsc``: the device block of this step's scalars
+        (capturable groups)."""
         before = [st.get("step", 0) for st in states]
         try:
-            self._launch_group(group, params, grads, states)
+            self._launch_group(group, params, grads, states, dsc)
         except Exception:
             for st, s0 in zip(states, before):
                 st["step"] = s0
             raise
 
-    def _launch_group(self, group, params, grads, states):
+    def _launch_group(self, group, params, grads, states, dsc=None):
         apollo_rank = group.get("apollo_rank", 0)
         batches: Dict[tuple, list] = {}
         ap_batches: Dict[tuple, list] = {}
@@ -319,16 +342,23 @@ class Adafactor8Bit(Optimizer):
                 copy_back.append((p, work))
                 p = work
             if apollo_rank > 0 and "apollo_seed" in st:
+                if dsc is not None:
+                    raise NotImplementedError("adafactor8bit: capturable=True does not cover APOLLO parameters")
                 bkey, rec, fin = _apollo_prep(self, p, g, st, group)
                 ap_batches.setdefault(bkey, []).append((rec, fin))
                 continue
             plan = _plan_param(p, g, st, group)
+            plan.dsc = dsc
             if plan.path == "q1d_fp32m":
                 _prep_q1d_fp32m(self, plan)
             elif plan.path == "f1d_qm":
                 _prep_f1d_qm(self, plan)
             key = plan.batch_key()
             if key is None:
+                if dsc is not None:
+                    raise NotImplementedError(
+                        f"adafactor8bit: capturable=True covers the multi-tensor paths only; a '{plan.path}' "
+                        f"parameter of shape {tuple(p.shape)} needs a per-tensor launch")
                 _run_single(self, plan)
             else:
                 batches.setdefault(key, []).append(plan)
@@ -338,6 +368,61 @@ class Adafactor8Bit(Optimizer):
             _run_apollo_batch(self, group, bkey, items)
         for p, work in copy_back:
             p.copy_(work)
+
+
+# ====================================================================== device step (capturable)
+def _no_upload_in_capture(upload):
+    """A tensor table is uploaded from host memory, which a captured graph would
+    replay from whatever that memory holds later: tables must exist before capture."""
+    if upload and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("adafactor8bit: a step being captured would upload a tensor table; run one eager "
+                           "step with the same parameters, gradients and state first")
+
+
+def _step_spec(group):
+    """The group's a8_step_spec: the host planner's scalar rules (_plan_param,
+    _plan_factored; optimizer.py:2012-2039, 832-856) as data."""
+    beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
+    if isinstance(group["lr"], Tensor):
+        raise NotImplementedError("adafactor8bit: capturable=True needs a float learning rate")
+    sgd = beta2 is None and beta2_decay is None
+    eps1 = group["eps"][0]
+    eps1 = 1e-30 if eps1 is None else eps1
+    adam_denom = (not group.get("factored", True)) and beta2 is not None and group.get("beta3") is None
+    bias_mode = 0
+    if beta1 is not None and not group["relative_step"] and not sgd:
+        bc = group.get("bias_correction")
+        if (adam_denom if bc is None else bool(bc)):
+            bias_mode = 1 if beta2 is not None else 2
+    wd = group["weight_decay"]
+    wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
+    return nat.StepSpec(beta1 if beta1 is not None else 0.0, beta2 if beta2 is not None else 0.0,
+                        beta2_decay if beta2_decay is not None else 0.0, eps1, float(group["lr"]), _f32(wd),
+                        0 if sgd else (1 if beta2 is not None else 2), int(bool(group["relative_step"])), bias_mode,
+                        int(adam_denom), wd_mode, bias_mode)
+
+
+def _advance_device_step(opt, group, params, states):
+    """Advance the group's device step count and write this step's scalars
+    (a8_step_advance); returns the scalar block.  The count starts from the
+    parameters' host count, which must be the same for the whole group."""
+    dev = params[0].device
+    key = (dev, "devstep", id(group))
+    ent = opt._ws.get(key)
+    if ent is None:
+        steps = {int(st.get("step", 0)) for st in states}
+        if len(steps) != 1:
+            raise RuntimeError(f"adafactor8bit: capturable=True needs one step count per group, found {sorted(steps)}")
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("adafactor8bit: run one eager step before capturing a capturable optimizer's step")
+        ent = {"ctr": torch.tensor([steps.pop()], dtype=torch.int64, device=dev),
+               "scal": torch.zeros(nat.STEP_SCALARS_BYTES // 4, dtype=torch.float32, device=dev),
+               "group": group}
+        opt._ws[key] = ent
+    ent["spec"] = _step_spec(group)
+    nat.check(nat.lib().a8_step_advance(ctypes.byref(ent["spec"]), ent["ctr"].data_ptr(), ent["scal"].data_ptr(),
+                                        nat.stream_of(dev)), "a8_step_advance")
+    return ent["scal"]
 
 
 # ====================================================================== block sizes
@@ -400,7 +485,7 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep", "dsc")
 
     def batch_key(self):
         if self.path == "factored":
@@ -985,12 +1070,13 @@ def _run_batch_f1dc(opt, key, plans):
 
     def launch(mode):
         arr, table, up = ent["arrs"][mode]
+        _no_upload_in_capture(up)
         rc = L.a8_fused_update_1d_full_multi(
             mode, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), table.numel(),
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom), P0.eps_g, P0.d,
             int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr), int(P0.step),
             int(P0.rms_kernel), _f32(P0.eps2), int(P0.kwd), _f32(P0.group["weight_decay"]),
-            int(P0.vbuf is not None), up, strm)
+            int(P0.vbuf is not None), up, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         ent["arrs"][mode][2] = 0
 
@@ -1028,7 +1114,7 @@ def _run_batch(opt, key, plans):
     if path == "factored":
         _run_factored(opt, plans)
         return
-    if len(plans) == 1:
+    if len(plans) == 1 and plans[0].dsc is None:
         _run_single(opt, plans[0])
         return
     if path == "f1dc":
@@ -1089,7 +1175,10 @@ def _run_batch(opt, key, plans):
     has_dec = int(P0.decay_val is not None)
     dec_val = P0.decay_val if has_dec else 1.0
     strm = nat.stream_of(dev)
+    _no_upload_in_capture(upload)
     if path == "sgd":
+        if P0.dsc is not None:
+            raise NotImplementedError("adafactor8bit: capturable=True does not cover the SGD path")
         kind = 0 if not P0.has_m else (1 if key[7] else 2)
         rc = L.a8_sgd_step_multi(
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), nbytes,
@@ -1106,7 +1195,7 @@ def _run_batch(opt, key, plans):
             P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
             S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
             16 if P0.vqt == "al16" else 8, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
-            float(dec_val), has_dec, upload, strm)
+            float(dec_val), has_dec, upload, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_fused_update_1d_multi")
         for pl in plans:
             _block_view(pl.st, "variance", pl.bs)
@@ -1117,7 +1206,7 @@ def _run_batch(opt, key, plans):
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_sq, P0.eps_d, int(P0.adam_denom),
             P0.eps_g, P0.d, int(P0.mom_only), float(P0.alpha_val), float(dec_val), has_dec, int(P0.sr),
-            int(P0.step), 0, 0.0, 0, 0.0, int(P0.vbuf is not None), upload, strm)
+            int(P0.step), 0, 0.0, 0, 0.0, int(P0.vbuf is not None), upload, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_fused_update_1d_full_multi")
         if upload:
             ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
@@ -1440,8 +1529,11 @@ def _run_factored(opt, plans):
         if fira:
             prev = st.get("fira_prev_norm")
             if prev is None:
+                # a zero previous norm takes the limiter's reset branch (scale 1, next =
+                # this norm), which is what the first step does without one; one table
+                # then serves every step
                 st["fira_prev_norm"] = torch.zeros((), dtype=torch.float32, device=dev)
-                has_prev.append(0)
+                has_prev.append(1)
             else:
                 if not torch.is_tensor(prev) or prev.device != dev or prev.dtype != torch.float32:
                     prev = torch.as_tensor(prev, dtype=torch.float32).to(dev).reshape(())
@@ -1514,6 +1606,7 @@ def _run_factored(opt, plans):
         wsd[shapes] = ent
         upload = 1
     arr, table = ent["arr"], ent["table"]
+    _no_upload_in_capture(upload)
     rc = L.a8_factored_step(
         nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), table.numel(), upload,
         P0.beta_val, _f32(P0.eps1), _f32(P0.eps2), float(P0.rho_val), int(P0.scale_param),
@@ -1521,7 +1614,7 @@ def _run_factored(opt, plans):
         float(P0.margin), _AL_FLOOR, vbits, int(P0.bs), P0.beta1 if P0.has_m else 0.0,
         int(P0.mbs) if P0.has_m else 32, S.m_bits(P0.mqt) if P0.has_m else 8,
         S.m_mode(P0.mqt) if P0.has_m else 0, int(P0.step), int(came),
-        float(P0.beta3) if came else 0.0, _f32(P0.group.get("eps_came", 1e-16)), cbits,
+        float(P0.beta3) if came else 0.0, _f32(P0.group.get("eps_came", 1e-16)), cbits, nat.ptr(P0.dsc),
         nat.stream_of(dev))
     nat.check(rc, "a8_factored_step")
     if vbits:

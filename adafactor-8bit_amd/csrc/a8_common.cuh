@@ -18,6 +18,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include "../../include/adafactor8bit_amd.h"
+
 namespace a8 {
 
 // Global-memory (address space 1) view of a pointer: descriptor-table pointers
@@ -35,6 +37,18 @@ __device__ __forceinline__ const A8_G T* gp(const T* p) { return (const A8_G T*)
 #define A8_C __attribute__((address_space(4)))
 template <typename T>
 __device__ __forceinline__ const A8_C T* cp(const T* p) { return (const A8_C T*)p; }
+
+// This step's scalars from the block a8_step_advance wrote (uniform, written
+// before the launch): read through the scalar cache as 64-bit words.
+__device__ __forceinline__ a8_step_scalars load_step_scalars(const a8_step_scalars* p) {
+  const A8_C uint64_t* w = (const A8_C uint64_t*)cp(p);
+  uint64_t buf[sizeof(a8_step_scalars) / 8];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(a8_step_scalars) / 8); ++i) buf[i] = w[i];
+  a8_step_scalars s;
+  __builtin_memcpy(&s, buf, sizeof(s));
+  return s;
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

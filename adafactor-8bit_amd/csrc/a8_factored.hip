@@ -154,7 +154,18 @@ struct HyperF {
   int mk;              // momentum codec (0 none, 1 UF8, 2 UF4, 3 D8, 4 D4)
   int lbm;             // log2(m_block_size)
   uint64_t sr_step;
+  const a8_step_scalars* dsc;   // if set: this step's V lerp weight, lr, bias factor and SR step
 };
+
+// The per-step fields from the device block of a8_step_advance, when given.
+__device__ __forceinline__ void hf_step(HyperF& h) {
+  if (!h.dsc) return;
+  const a8_step_scalars sc = load_step_scalars(h.dsc);
+  h.bv = (float)sc.beta_val;
+  h.lr_val = sc.rho;
+  h.bias_factor = sc.bias_factor;
+  h.sr_step = sc.step;
+}
 
 __device__ __forceinline__ const DescF* find_tile(const DescF* tab, int n, int64_t wg) {
   int lo = 0, hi = n - 1;
@@ -445,6 +456,7 @@ __device__ __forceinline__ const DescF* find_fblk(const DescF* tab, int n, int64
 // same size only partition the work).
 template <int VB, bool CONF>
 __global__ __launch_bounds__(256) void k_fblock(const DescF* __restrict__ table, int ntab, HyperF h) {
+  hf_step(h);
   __shared__ float sf[8];
   const DescF D = *find_fblk(table, ntab, (int64_t)blockIdx.x);
   const FWs W = fws_layout(D.B, D.R, D.C);
@@ -536,6 +548,7 @@ __global__ __launch_bounds__(256) void k_fblock(const DescF* __restrict__ table,
 // (optimizer.py:832-856, 2020-2039).
 template <bool CONF>
 __global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, HyperF h) {
+  hf_step(h);
   __shared__ double sd[4];
   const DescF D = table[blockIdx.x];
   const FWs W = fws_layout(D.B, D.R, D.C);
@@ -587,6 +600,7 @@ __global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, 
 // the update is (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
 template <typename T, int MODE, bool SR, int MK, bool CM>
 __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table, int ntab, HyperF h) {
+  if constexpr (SR) hf_step(h);
   static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s4[8];
   __shared__ double s4d[4];
@@ -779,6 +793,7 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 // and operation order as k_fupdate; MODE 1 writes one partial per tile.
 template <typename T, int MODE, bool SR, int MK, bool CM>
 __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, int ntab, HyperF h) {
+  if constexpr (SR) hf_step(h);
   static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s_ic[2 * kTC];
   __shared__ float s4[8];
@@ -1171,7 +1186,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                      float weight_decay, int wd_mode, float d, int fira, float fira_margin,
                      float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
                      int m_bits, int m_mode, uint64_t sr_step, int came, double beta3, float eps_came,
-                     int c_bits, void* stream) {
+                     int c_bits, const void* step_scalars, void* stream) {
   if (ntensors <= 0) return 0;
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
@@ -1258,6 +1273,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.mk = m32 ? kMkFp32 : (has_m ? mk_code(m_bits, m_mode) : 0);
   h.lbm = lbm;
   h.sr_step = sr_step;
+  h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   const bool clip = d > 0.0f || fira;
   const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
   const UpdGrid ug{tiles, units, any_tiled, any_flat};

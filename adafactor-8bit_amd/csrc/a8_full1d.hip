@@ -50,6 +50,8 @@ struct HyperFull {
   int wd_mode;      // 0: none here, 1: p *= 1 - alpha*wd, 2: p *= 1 - rho*wd (optimizer.py:2032-2039)
   float wd;
   int v_ready;      // V holds this step's second moment already (no EMA, not written)
+  float eps_g;      // added to g^2 (times beta_val)
+  const a8_step_scalars* dsc;   // if set: this step's beta_val, eps_d, alpha, decay and SR step
 };
 
 constexpr int kFLanes = 256;
@@ -73,6 +75,16 @@ __device__ __forceinline__ const DescFull* find_full(const DescFull* tab, int n,
 template <typename T, int MODE, bool SR>
 __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const DescFull* __restrict__ table,
                                                          int ntab, HyperFull h) {
+  if (h.dsc) {   // the derived fields as make_hf forms them from beta_val
+    const a8_step_scalars sc = load_step_scalars(h.dsc);
+    h.bv = (float)sc.beta_val;
+    h.v_keep = (float)(1.0 - sc.beta_val);
+    h.eps_add = (float)(sc.beta_val * (double)h.eps_g);
+    h.eps_d = sc.eps_d;
+    h.alpha_val = sc.alpha;
+    h.decay_val = sc.decay;
+    h.sr_step = sc.step;
+  }
   const DescFull D = table ? *find_full(table, ntab, (int64_t)blockIdx.x) : one;
   const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
@@ -168,14 +180,27 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       }
     }
   }
+  // Sums: the workgroup reduces in a fixed order (waves, then the four wave sums
+  // through LDS) and adds once to the tensor's accumulator.  A tensor with fp32
+  // state has fewer than min_8bit_size (4096) elements, at most two workgroups,
+  // and a float sum of two terms does not depend on their order: run to run the
+  // result is the same bits.
   if constexpr (MODE == 1 || MODE == 3 || MODE == 4) {
-    float t = grp_sum(sq, 64);
-    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
-  }
-  if constexpr (MODE == 1) {
-    if (h.scale_param) {
-      const float t = grp_sum(psum, 64);
-      if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.psq, t);
+    __shared__ float s4[8];
+    const float t = grp_sum(sq, 64);
+    const float tp = (MODE == 1 && h.scale_param) ? grp_sum(psum, 64) : 0.0f;
+    if ((lane & 63) == 0) {
+      s4[lane >> 6] = t;
+      s4[4 + (lane >> 6)] = tp;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      const float tot = ((s4[0] + s4[1]) + s4[2]) + s4[3];
+      if (tot != 0.0f) atomicAdd(D.norm_buf, tot);
+      if (MODE == 1 && h.scale_param) {
+        const float ptot = ((s4[4] + s4[5]) + s4[6]) + s4[7];
+        if (ptot != 0.0f) atomicAdd(D.psq, ptot);
+      }
     }
   }
 }
@@ -218,6 +243,7 @@ static HyperFull make_hf(double beta1, double beta_val, float eps_sq, float eps_
   h.v_keep = (float)(1.0 - beta_val);
   h.eps_add = (float)(beta_val * (double)eps_g);
   h.has_eps_add = eps_g > 0.0f;
+  h.eps_g = eps_g;
   h.eps_d = eps_d; h.eps_sq = eps_sq; h.d = d;
   h.adam_denom = adam; h.momentum_only = mom_only; h.sr_step = sr_step;
   return h;
@@ -284,7 +310,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
-                                  int v_ready, int upload, void* stream) {
+                                  int v_ready, int upload, const void* step_scalars, void* stream) {
   if (ntensors <= 0) return 0;
   if (scale_param && mode != 2 && mode != 1) return set_error(A8_ERR_ARG, "scale_param needs the NORM/APPLY passes");
   if (wd_mode && has_decay) return set_error(A8_ERR_ARG, "give has_decay or wd_mode, not both");
@@ -318,6 +344,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
                         momentum_only, sr_step, alpha_val, decay_val, has_decay);
   h.scale_param = scale_param; h.eps2 = eps2; h.wd_mode = wd_mode; h.wd = wd; h.v_ready = v_ready;
+  h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   DescFull none{};
   return launch_full_any(dtype, stochastic, mode, none, reinterpret_cast<const DescFull*>(table_dev),
                          ntensors, wg, h, st);

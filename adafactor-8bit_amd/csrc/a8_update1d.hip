@@ -62,6 +62,7 @@ struct Hyper1D {
   float decay_val;  // used when a tensor's decay pointer is NULL and has_decay
   int has_decay;
   uint64_t sr_step;
+  const a8_step_scalars* dsc;   // if set: bv, eps_d, alpha_val, decay_val and sr_step come from here
 };
 
 // ------------------------------------------------------------ main kernel
@@ -630,6 +631,14 @@ template <typename T, int VB, int MODE, bool SR, int MK>
 __global__ __launch_bounds__(kLanes) __attribute__((amdgpu_waves_per_eu(7)))
 void k_update1d(Desc1D one, const Desc1D* __restrict__ table, int ntab, Hyper1D h) {
   extern __shared__ float s_lds[];  // [nv_wg * 256] AL8 tables | cross-wave partials and fits
+  if (h.dsc) {
+    const a8_step_scalars sc = load_step_scalars(h.dsc);
+    h.bv = (float)sc.beta_val;
+    h.eps_d = sc.eps_d;
+    h.alpha_val = sc.alpha;
+    h.decay_val = sc.decay;
+    h.sr_step = sc.step;
+  }
   Desc1D D;
   if (table != nullptr) D = load_desc(table, ntab, (int)blockIdx.x);
   else D = one;
@@ -827,7 +836,7 @@ static int launch_multi_1d(int mode, int stochastic, int dtype, bool has_m, int 
                            int64_t nwg, double beta1, double beta_val, float eps_for_denom, int use_adam_denom,
                            float log_floor, float eps_for_grad_sq, float eps_sq, int block_size, int m_block_size,
                            int m_bits, int m_mode, float d, int v_bits, int momentum_only, uint64_t sr_step,
-                           float alpha_val, float decay_val, int has_decay, hipStream_t st) {
+                           float alpha_val, float decay_val, int has_decay, const void* dsc, hipStream_t st) {
   Hyper1D h{};
   h.beta1 = (float)beta1;
   h.w_m = (float)(1.0 - beta1);
@@ -840,6 +849,7 @@ static int launch_multi_1d(int mode, int stochastic, int dtype, bool has_m, int 
   h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
   h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
   h.sr_step = sr_step;
+  h.dsc = reinterpret_cast<const a8_step_scalars*>(dsc);
   Desc1D none{};
   return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev), ntensors,
                     nwg, h, st);
@@ -902,7 +912,8 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                              float log_floor, float eps_for_grad_sq, float eps_sq, int block_size,
                              int m_block_size, int m_bits, int m_mode, float d, int v_bits,
                              int momentum_only, uint64_t sr_step, float alpha_val,
-                             float decay_val, int has_decay, int upload, void* stream) {
+                             float decay_val, int has_decay, int upload, const void* step_scalars,
+                             void* stream) {
   if (ntensors <= 0) return 0;
   if (a8_table_bytes_1d(ntensors) > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_1d(ntensors)");
@@ -918,7 +929,7 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
   return launch_multi_1d(mode, stochastic, dtype, tensors[0].m_q != nullptr, ntensors, table_dev, nwg, beta1,
                          beta_val, eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, block_size,
                          m_block_size, m_bits, m_mode, d, v_bits, momentum_only, sr_step, alpha_val, decay_val,
-                         has_decay, st);
+                         has_decay, step_scalars, st);
 }
 
 int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
@@ -926,7 +937,8 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
                                      int use_adam_denom, float log_floor, float eps_for_grad_sq, float eps_sq,
                                      int block_size, int m_block_size, int m_bits, int m_mode, float d,
                                      int v_bits, int momentum_only, uint64_t sr_step, float alpha_val,
-                                     float decay_val, int has_decay, int upload, void* stream) {
+                                     float decay_val, int has_decay, int upload, const void* step_scalars,
+                                     void* stream) {
   if (ntensors <= 0) return 0;
   if (a8_table_bytes_1d(ntensors) > (int64_t)kScratchBytes) {
     char msg[160];
@@ -959,7 +971,7 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
   return launch_multi_1d(mode, stochastic, dtype, tensors[0].m_q != nullptr, ntensors, table_dev, nwg, beta1,
                          beta_val, eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, block_size,
                          m_block_size, m_bits, m_mode, d, v_bits, momentum_only, sr_step, alpha_val, decay_val,
-                         has_decay, st);
+                         has_decay, step_scalars, st);
 }
 
 int a8_noalloc_max_tensors_1d(void) { return (int)(kScratchBytes / (sizeof(Desc1D) + sizeof(int32_t))); }

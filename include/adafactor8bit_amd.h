@@ -87,6 +87,44 @@ int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const v
                        int momentum_only, float alpha_val, float decay_val, int has_decay,
                        void* stream);
 
+/* ---- Per-step scalars on the device (graph-capturable steps) ---------------
+ * No counterpart in the reference, which forms these on the host per parameter
+ * (optimizer.py:2012-2039, 832-856).  a8_step_advance adds one to a device step
+ * counter and writes this step's scalars, derived from the counter as the host
+ * derives them from its step: the V lerp weight 1 - beta2 or t^beta2_decay, the
+ * step size rho (lr, or min(lr, 1/sqrt(t)) for the relative step) with its bias
+ * correction, the Adam epsilon eps1 * sqrt(1 - beta2^t), the weight-decay factor
+ * and the factored path's bias factor.  The multi-tensor entry points take
+ * `step_scalars` (NULL: use their scalar arguments): with it, beta_val,
+ * eps_for_denom, alpha_val, decay_val (when has_decay), the factored path's
+ * lr_val and bias_factor, and sr_step are read from the device block instead, so
+ * the launch sequence of a step can be captured once in a HIP graph and replayed. */
+typedef struct a8_step_spec {
+  double beta1, beta2, beta2_decay, eps1;
+  double lr;
+  float wd;
+  int v_mode;          /* V lerp weight: 0 none (SGD), 1 1 - beta2, 2 t^beta2_decay */
+  int relative_step;   /* rho = min(lr, 1/sqrt(t)) */
+  int bias_mode;       /* 0 none; 1 alpha *= sqrt(bc2)/bc1 (and eps1 *= sqrt(bc2) when adam_denom);
+                          2 alpha /= bc1 (beta2 = None) */
+  int adam_denom;
+  int wd_mode;         /* 0 none; 1 decay = 1 - alpha*wd; 2 decay = 1 - rho*wd */
+  int fact_bias_mode;  /* factored path: 0 none; 1 sqrt(1 - beta2^t)/bc1; 2 bc1 */
+} a8_step_spec;
+
+typedef struct a8_step_scalars {
+  double beta_val;     /* V lerp weight (double: the kernels derive 1 - beta_val from it as the host does) */
+  float eps_d;         /* Adam denominator epsilon */
+  float alpha;         /* step size, bias corrected (1-D paths) */
+  float decay;         /* weight-decay factor (1 without decay) */
+  float bias_factor;   /* factored path */
+  float rho;           /* step size before the RMS scaling and bias correction */
+  float pad_;
+  uint64_t step;       /* this step's number (the SR stream's step) */
+} a8_step_scalars;
+
+int a8_step_advance(const a8_step_spec* spec, int64_t* counter, a8_step_scalars* out, void* stream);
+
 /* One tensor of a multi-tensor launch. */
 typedef struct a8_tensor1d {
   void* param;
@@ -117,7 +155,8 @@ int a8_fused_update_1d_multi(int mode, int stochastic, int dtype, const a8_tenso
                              float log_floor, float eps_for_grad_sq, float eps_sq, int block_size,
                              int m_block_size, int m_bits, int m_mode, float d, int v_bits,
                              int momentum_only, uint64_t sr_step, float alpha_val,
-                             float decay_val, int has_decay, int upload, void* stream);
+                             float decay_val, int has_decay, int upload, const void* step_scalars,
+                             void* stream);
 int64_t a8_table_bytes_1d(int ntensors);
 
 /* a8_fused_update_1d_multi without any allocation.  It has no counterpart in the
@@ -137,7 +176,8 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
                                      int use_adam_denom, float log_floor, float eps_for_grad_sq, float eps_sq,
                                      int block_size, int m_block_size, int m_bits, int m_mode, float d,
                                      int v_bits, int momentum_only, uint64_t sr_step, float alpha_val,
-                                     float decay_val, int has_decay, int upload, void* stream);
+                                     float decay_val, int has_decay, int upload, const void* step_scalars,
+                                     void* stream);
 int a8_noalloc_max_tensors_1d(void);
 
 /* Replaces fused_update_1d_full_{noclip,norm,apply,lag}[_sr] (kernels.cu:1374-1515;
@@ -184,7 +224,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   float eps_for_grad_sq, float d, int momentum_only,
                                   float alpha_val, float decay_val, int has_decay, int stochastic,
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
-                                  int v_ready, int upload, void* stream);
+                                  int v_ready, int upload, const void* step_scalars, void* stream);
 int64_t a8_table_bytes_full(int ntensors);
 
 /* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,
@@ -267,7 +307,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                      float weight_decay, int wd_mode, float d, int fira, float fira_margin,
                      float log_floor, int v_bits, int block_size, double beta1, int m_block_size,
                      int m_bits, int m_mode, uint64_t sr_step, int came, double beta3, float eps_came,
-                     int c_bits, void* stream);
+                     int c_bits, const void* step_scalars, void* stream);
 int64_t a8_factored_workspace_floats(int64_t batch, int64_t rows, int64_t cols);
 int64_t a8_table_bytes_2d(int ntensors);
 

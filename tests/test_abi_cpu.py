@@ -105,8 +105,8 @@ def test_noalloc_rejects_more_tensors_than_its_scratch_holds():
     n = cap + 1
     arr = (nat.Tensor1D * n)()
     rc = L.a8_fused_update_1d_multi_noalloc(0, 0, 0, arr, n, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 2048, 256, 8,
-                                            0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None)
+                                            0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None, None)
     assert rc == -4, rc
     assert b"scratch" in L.a8_last_error()
     assert L.a8_fused_update_1d_multi_noalloc(0, 0, 0, arr, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 2048, 256,
-                                              8, 0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None) == 0
+                                              8, 0, 0.0, 8, 0, 1, 1e-4, 1.0, 0, 1, None, None) == 0

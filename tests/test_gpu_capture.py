@@ -1,0 +1,122 @@
+"""Graph-captured optimizer steps (capturable=True) on the GPU.
+
+With ``capturable=True`` a group's step count lives on the device: each step
+starts with a8_step_advance (count + 1, this step's scalars) and runs only
+multi-tensor kernels that read those scalars, so ``step()`` captured once in a
+graph replays as a real next step every time.  For the benchmark configurations
+(C1 AdamW UF8/AL8, C2 factored Adafactor with its fp32-state vectors, C3 CAME with
+Fira) and two more (weight decay with bias correction; bf16 with stochastic
+rounding):
+
+* N graph replays leave parameters and every state tensor bit-identical to N
+  eager steps of a second capturable optimizer on the same gradients, with eager
+  work and synchronisations between the replays; ``state_dict()`` reports the
+  replayed step count;
+* eager capturable steps equal the default (host-scalar) path bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from inputs import make_grad, make_param
+
+ADAMW = dict(beta1=0.9, beta2=0.999, beta2_decay=None, factored=False, relative_step=False, scale_parameter=False,
+             scale_weight_decay=False, d=0.0, eps=(1e-8, 1e-3), lr=1e-4, block_size=2048, m_block_size=256)
+C2 = dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=True, relative_step=False, lr=1e-3, block_size=256)
+C3 = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True, relative_step=False,
+          scale_parameter=False, scale_weight_decay=False, d=1.0, eps_came=1e-16, lr=1e-4, block_size=2048,
+          m_block_size=256, m_quant_type="uf8", v_quant_type="al16", c_quant_type="al16",
+          enable_fira_for_adafactor=True, fira_margin=0.01)
+
+CASES = [
+    ("c1_adamw", ADAMW, [(300, 260), (2048,), (5000,), (64, 64)], torch.float32, "normal_zeros"),
+    ("c2_adafactor", C2, [(300, 260), (130, 70), (2048,), (64,)], torch.float32, "student_t"),
+    ("c3_came_fira", C3, [(256, 300), (300, 64), (2048,), (64,)], torch.float32, "logscale"),
+    ("adamw_wd_bias", dict(ADAMW, weight_decay=0.1, scale_weight_decay=True, lr=1e-3), [(300, 260), (1000,)],
+     torch.float32, "student_t"),
+    ("adamw_bf16_sr", dict(ADAMW, stochastic_round_writeback=True, lr=1e-3), [(300, 260), (1000,)], torch.bfloat16,
+     "normal_zeros"),
+]
+
+
+def _setup(kw, shapes, dtype, **extra):
+    from adafactor8bit import Adafactor8Bit
+    ps = [torch.nn.Parameter(make_param(s, i, 17).to("cuda", dtype)) for i, s in enumerate(shapes)]
+    for p in ps:
+        p.grad = torch.zeros_like(p)   # static gradient buffers: the graph reads these addresses
+    return ps, Adafactor8Bit(ps, **dict(kw, **extra))
+
+
+def _load_grads(ps, t, gkind, dtype):
+    for i, p in enumerate(ps):
+        p.grad.copy_(make_grad(tuple(p.shape), i, t, 17, kind=gkind).to(dtype))
+
+
+def _same_state(oa, ob, pa, pb, what):
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert torch.equal(a, b), f"{what}: param {i}"
+        sa, sb = oa.state[a], ob.state[b]
+        assert sorted(sa) == sorted(sb), (what, i)
+        for k, v in sa.items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, sb[k]), f"{what}: param {i} {k}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw,shapes,dtype,gkind", CASES, ids=[c[0] for c in CASES])
+def test_graph_replays_equal_eager_steps(name, kw, shapes, dtype, gkind):
+    print(f"[capture] {name}", flush=True)
+    pa, oa = _setup(kw, shapes, dtype, capturable=True)   # replayed
+    pb, ob = _setup(kw, shapes, dtype, capturable=True)   # eager
+    for t in (1, 2):   # eager warm-up: state, tables and device step counts exist before capture
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load_grads(ps, t, gkind, dtype)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load_grads(pa, 3, gkind, dtype)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    _same_state(oa, ob, pa, pb, "after capture (nothing ran)")   # capture launches no kernel
+    steps = 5
+    for t in range(3, 3 + steps):
+        _load_grads(pa, t, gkind, dtype)
+        graph.replay()
+        _load_grads(pb, t, gkind, dtype)
+        ob.step()
+        junk = torch.randn(1024, device="cuda").sum()   # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        _same_state(oa, ob, pa, pb, f"step {t}")
+    sa = oa.state_dict()
+    assert {st["step"] for st in sa["state"].values()} == {2 + steps}
+    assert {st["step"] for st in ob.state_dict()["state"].values()} == {2 + steps}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw,shapes,dtype,gkind", CASES, ids=[c[0] for c in CASES])
+def test_capturable_eager_equals_default_path(name, kw, shapes, dtype, gkind):
+    print(f"[capturable eager] {name}", flush=True)
+    pa, oa = _setup(kw, shapes, dtype, capturable=True)
+    pb, ob = _setup(kw, shapes, dtype)
+    for t in range(1, 6):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load_grads(ps, t, gkind, dtype)
+            o.step()
+    torch.cuda.synchronize()
+    _same_state(oa, ob, pa, pb, "after 5 steps")
+
+
+@pytest.mark.gpu
+def test_capturable_rejects_paths_with_host_scalars():
+    print("[capturable] APOLLO rejected", flush=True)
+    ps, o = _setup(dict(ADAMW, apollo_rank=8, block_size=128, m_block_size=32), [(64, 96)], torch.float32,
+                   capturable=True)
+    ps[0].grad.copy_(make_grad((64, 96), 0, 1, 17))
+    with pytest.raises(NotImplementedError, match="APOLLO"):
+        o.step()
+    assert o.state[ps[0]]["step"] == 0

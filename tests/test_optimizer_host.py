@@ -53,7 +53,7 @@ def test_step_counter_restored_when_launch_fails(monkeypatch):
     for st in states:
         st["step"] = 7
 
-    def boom(self, group, params, grads, sts):
+    def boom(self, group, params, grads, sts, dsc=None):
         for st in sts:
             st["step"] += 1
         raise RuntimeError("launch failed")

@@ -65,9 +65,9 @@ def test_noalloc_matches_multi_over_calls():
         rb = _records(nat, [pb[i] for i in idx], grads, [sb[i] for i in idx])
         upload = 0 if t == 3 else 1   # the third call reuses the second call's table
         rc = L.a8_fused_update_1d_multi(0, 0, nat.F32, ra, len(idx), table.data_ptr(), table.numel(), *_hyper(t),
-                                        1, strm)
+                                        1, None, strm)
         nat.check(rc, "a8_fused_update_1d_multi")
-        rc = L.a8_fused_update_1d_multi_noalloc(0, 0, nat.F32, rb, len(idx), *_hyper(t), upload, strm)
+        rc = L.a8_fused_update_1d_multi_noalloc(0, 0, nat.F32, rb, len(idx), *_hyper(t), upload, None, strm)
         nat.check(rc, "a8_fused_update_1d_multi_noalloc")
         torch.cuda.synchronize()
         for i in range(len(shapes)):

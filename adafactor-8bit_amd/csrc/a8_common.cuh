@@ -63,6 +63,53 @@ __device__ __forceinline__ float lerp_ref(float s, float e, float w) {
   return (fabsf(w) < 0.5f) ? __builtin_fmaf(w, e - s, s) : __builtin_fmaf(w - 1.0f, e - s, e);
 }
 
+// lerp_ref with a weight shared by every lane: the weight's branch is settled
+// once (lerp_weight), so each element costs one subtraction, one select and one
+// fma.  lerp_u(s, e, lerp_weight(w)) == lerp_ref(s, e, w) bit for bit.
+struct LerpW {
+  float wc;     // w, or w - 1 for |w| >= 0.5
+  bool small;   // |w| < 0.5: base s, else base e
+};
+
+__device__ __forceinline__ LerpW lerp_weight(float w) {
+  const bool small = fabsf(w) < 0.5f;
+  return LerpW{small ? w : w - 1.0f, small};
+}
+
+__device__ __forceinline__ float lerp_u(float s, float e, LerpW L) {
+  return __builtin_fmaf(L.wc, e - s, L.small ? s : e);
+}
+
+// q[i] = x[i] / d, correctly rounded, for a divisor d >= 1 shared by every lane
+// and its IEEE reciprocal rd = 1.0f / d: one Markstein correction of x * rd (rd
+// the correctly rounded reciprocal and q0 within an ulp of x / d, so the
+// remainder x - q0 d is exact in one fma and q0 + r rd rounds to the correctly
+// rounded quotient).  The theorem needs quotient and remainder in the normal
+// range: when any lane holds a value with |q0| < 2^-100, zero or non-finite, the
+// wave redoes those elements with the IEEE division (a uniform branch, so the
+// division is not executed otherwise).  Three operations in place of ten.
+__device__ __forceinline__ bool div_fast_ok(float q0) {
+  const float a = fabsf(q0);
+  return a >= 0x1p-100f && a <= 0x1.fffffep127f;   // false for NaN
+}
+
+template <int N>
+__device__ __forceinline__ void div_by(float* q, const float* x, float d, float rd) {
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float q0 = x[i] * rd;
+    const float r = __builtin_fmaf(-q0, d, x[i]);
+    q[i] = __builtin_fmaf(r, rd, q0);
+    bad = bad || !div_fast_ok(q0);
+  }
+  if (__builtin_amdgcn_ballot_w64(bad)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (!div_fast_ok(x[i] * rd)) q[i] = x[i] / d;
+  }
+}
+
 __device__ __forceinline__ float log2_exact(float x) {   // x > 0, correctly rounded to fp32
   return (float)::log2((double)x);
 }

@@ -1,28 +1,30 @@
 // Factored (Adafactor row/column) optimizer step for MI355X (gfx950).
 //
 // One group step is a few launches over every tensor of the group:
-//   k_fstats   2-D tiles of tr rows x 1024 columns (tr = 32, or 64 above 2048
-//              rows): row sums and column sums of g^2 (and sum p^2 for the
-//              relative step size), written as per-tile partials -- no atomics,
-//              so the result is deterministic;
+//   k_fstats   2-D tiles of up to kTRS rows x 1024 columns: row sums and column
+//              sums of g^2 (and sum p^2 for the relative step size), written as
+//              per-tile partials -- no atomics, so the result is deterministic;
+//   k_fcolsum  (tensors of more than kSplit row strips) the column partials
+//              summed over groups of kSplit strips, in parallel;
 //   k_fblock   one workgroup per AL block of each row/column vector: reduce the
 //              partials in a fixed order, EMA the second moment, refit and
 //              re-encode the block (columns: inv_col in place);
 //   k_frows    one workgroup per tensor: the row mean, inv_row, the step size
 //              and the weight-decay factor;
-//   k_fupdate  flat 2048-element units (8 per lane, as the 1-D step): the
-//              update u = (x * inv_row) * inv_col with x = g or the momentum
-//              EMA, the parameter write and the momentum re-encode.  With RMS
-//              clipping or Fira it runs twice: first for sum(u^2) per unit,
-//              then (after k_fnorm) to apply;
+//   k_fupdt    on tiles of 32 rows x 1024 columns (k_fupdate, flat 2048-element units, for
+//              the few tensors whose column count rules tiles out): the update
+//              u = (x * inv_row) * inv_col with x = g or the momentum EMA, the
+//              parameter write and the momentum re-encode.  With RMS clipping
+//              or Fira it runs twice: first for sum(u^2) per tile, then (after
+//              k_fnorm) to apply;
 //   k_fnorm    one workgroup per tensor: ||u||, the Fira limiter and the step.
 // CAME (beta3) adds, between k_frows and the update:
 //   k_fclip    the RMS clip factor of U = (g * inv_row) * inv_col (after a
-//              k_fupdate norm pass over U, only when d > 0);
+//              norm pass over U, only when d > 0);
 //   k_came1    the same 2-D tiles as k_fstats: U / clip, the momentum EMA M',
 //              and row/column sums of the residual (U - M')^2 + eps_came;
-//   k_fblock / k_frows again, on the residual sums: the confidence EMA, its AL
-//              re-encode and inv_conf_row / inv_conf_col;
+//   k_fcolsum, k_fblock, k_frows again, on the residual sums: the confidence
+//              EMA, its AL re-encode and inv_conf_row / inv_conf_col;
 // and the update becomes (M' * inv_conf_row) * inv_conf_col (optimizer.py:929-956).
 // Numbers follow the reference's PyTorch path (optimizer.py:2198-2252 and
 // _fallback_2d_update 920-970): means are sum/count of the fp32 squares,
@@ -49,8 +51,9 @@ constexpr int kMkFp32 = 5;   // HyperF::mk of fp32 momentum (codecs are 1-4)
 struct FWs {
   int64_t rowpart;   // double [nchunk][B*R]       row partial sums
   int64_t colpart;   // double [B][nstrip][C]      column partial sums
+  int64_t colsum;    // double [B][nsplit][C]      column sums over groups of kSplit strips
   int64_t p2;        // double [ntile]             partial sum p^2
-  int64_t npart;     // double [max(nunit, ntile)] partial sums u^2 (per unit or per tile)
+  int64_t npart;     // double [max(nunit, nutile)] partial sums u^2 (per unit or per update tile)
   int64_t invr;      // [B*R]              new row V, then inv_row
   int64_t invc;      // [B*C]              new column V, then inv_col
   int64_t icr;       // [B*R]              CAME: new row confidence, then its inverse root
@@ -58,17 +61,27 @@ struct FWs {
   int64_t scal;      // [8]: alpha, step, fira scale, decay, CAME clip factor
   int64_t total;
   int64_t nchunk, nstrip, ntile, nunit;
+  int64_t nsplit;    // strip groups of the column reduction (1: k_fblock reads colpart)
   int64_t tr;        // rows per statistics tile
+  int64_t nustrip, nutile;   // update tiles: kTR rows x 1024 columns
 };
 
-// Rows per statistics tile: 32, or 64 for matrices of more than 2048 rows.  A
-// workgroup streams tr x 1024 elements, so taller tiles leave the tall matrices
-// (32000 x 2048 embeddings) to a few long-running workgroups that finish last at
-// low occupancy; the column reduction reads one partial per strip in any case.
+// Tile geometry.  The update passes (k_fupdt) run on tiles of kTR = 32 rows x
+// 1024 columns, which stream best for them.  The statistics passes (k_fstats,
+// k_came1) take up to kTRS rows per tile: each tile ends with a write of its row
+// and column partials, and such writes spread through the read stream cost far
+// more bandwidth than their bytes, so fewer, taller tiles write less often.  The
+// column partials of tall matrices are reduced in parallel by k_fcolsum, kSplit
+// strips per workgroup, before k_fblock.
+#ifndef A8_TRS
+#define A8_TRS 256
+#endif
+constexpr int kTRS = A8_TRS;
+constexpr int kSplit = 32;
+
 __host__ __device__ inline int64_t fws_tile_rows(int64_t R) {
-  int64_t tr = (R + 63) / 64;
-  tr = (tr + kTR - 1) / kTR * kTR;
-  return tr < kTR ? kTR : (tr > 64 ? 64 : tr);
+  const int64_t r = (R + kTR - 1) / kTR * kTR;
+  return r < kTRS ? r : kTRS;
 }
 
 __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
@@ -77,12 +90,16 @@ __host__ __device__ inline FWs fws_layout(int64_t B, int64_t R, int64_t C) {
   w.tr = fws_tile_rows(R);
   w.nstrip = (R + w.tr - 1) / w.tr;
   w.ntile = B * w.nstrip * w.nchunk;
+  w.nustrip = (R + kTR - 1) / kTR;
+  w.nutile = B * w.nustrip * w.nchunk;
   w.nunit = (B * R * C + kUnit - 1) / kUnit;
+  w.nsplit = (w.nstrip > kSplit) ? (w.nstrip + kSplit - 1) / kSplit : 1;
   w.rowpart = 0;
   w.colpart = w.rowpart + 2 * w.nchunk * B * R;
-  w.p2 = w.colpart + 2 * B * w.nstrip * C;
+  w.colsum = w.colpart + 2 * B * w.nstrip * C;
+  w.p2 = w.colsum + (w.nsplit > 1 ? 2 * B * w.nsplit * C : 0);
   w.npart = w.p2 + 2 * w.ntile;
-  w.invr = w.npart + 2 * (w.nunit > w.ntile ? w.nunit : w.ntile);
+  w.invr = w.npart + 2 * (w.nunit > w.nutile ? w.nunit : w.nutile);
   w.invc = w.invr + B * R;
   w.icr = w.invc + B * C;
   w.icc = w.icr + B * R;
@@ -122,9 +139,11 @@ struct DescF {
   float* fira_prev;
   float* m;            // fp32 momentum (MK 3), or null
   int64_t B, R, C, numel;
-  int64_t tile_begin;
+  int64_t tile_begin;  // first statistics tile of this tensor
+  int64_t utile_begin; // first update tile
   int64_t unit_begin;
   int64_t fblk_begin;  // first k_fblock workgroup of this tensor
+  int64_t cs_begin;    // first k_fcolsum workgroup of this tensor
   int64_t nbr;         // AL blocks of the row vector (the column vector follows)
   uint64_t sr_seed;
   int has_fira_prev;
@@ -172,6 +191,15 @@ __device__ __forceinline__ const DescF* find_tile(const DescF* tab, int n, int64
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
     if (tab[mid].tile_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+__device__ __forceinline__ const DescF* find_utile(const DescF* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].utile_begin <= wg) lo = mid; else hi = mid - 1;
   }
   return tab + lo;
 }
@@ -234,72 +262,198 @@ __device__ __forceinline__ void load4(const T* base, int64_t rowbase, int64_t c0
 }
 
 // ------------------------------------------------------------ statistics
+// Tile layout of the two statistics kernels (k_fstats, k_came1): wave w of the
+// workgroup owns columns c_base + 256 w .. + 255 of every row of the tile, a lane
+// one 4-column window.  A lane's column sums therefore cover the whole tile in
+// four registers (double), written straight to the column partials; the row sums
+// are kept per lane for kRB rows at a time and then reduce-scattered across the
+// wave (one 6-step butterfly for all kRB rows), the four waves' row partials
+// meeting in LDS at the end of the tile.  Every load of a batch of rows is issued
+// before its arithmetic: rows beyond the tile and windows beyond C read a valid
+// address (the tile's first row, column 0) and count zero.
+constexpr int kRB = 4;   // rows per row-sum batch
+
+// Sum of v[0..3] over the 64 lanes of the wave for each k, scattered: on return
+// every lane holds the total of v[k] for k = row_of_lane(lane).
+__device__ __forceinline__ double reduce_scatter4(const double* v, int wl) {
+  const bool b5 = (wl & 32) != 0, b4 = (wl & 16) != 0;
+  double a[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const double mine = b5 ? v[k + 2] : v[k];
+    const double other = b5 ? v[k] : v[k + 2];
+    a[k] = mine + __shfl_xor(other, 32, 64);
+  }
+  double x = (b4 ? a[1] : a[0]) + __shfl_xor(b4 ? a[0] : a[1], 16, 64);
+  x += __shfl_xor(x, 8, 64);
+  x += __shfl_xor(x, 4, 64);
+  x += __shfl_xor(x, 2, 64);
+  x += __shfl_xor(x, 1, 64);
+  return x;
+}
+
+__device__ __forceinline__ int row_of_lane(int wl) { return ((wl >> 5) & 1) * 2 + ((wl >> 4) & 1); }
+
+// Four consecutive elements at a per-lane 32-bit element offset from a
+// workgroup-uniform row pointer.  The offset is scaled to bytes in 32 bits (rows
+// of a tensor are far below 4 GiB apart... the offset is below C * sizeof(T)), so
+// the address is a scalar base plus a zero-extended vector offset: the saddr form
+// of the global load, with no 64-bit address per lane.
+// (The row pointer passes through readfirstlane: it is uniform anyway, and the
+// opaque step keeps loop strength reduction from turning base + offset back into
+// one 64-bit induction pointer per load.)
+template <typename T>
+__device__ __forceinline__ const char* at_off(const T* row, uint32_t off) {
+  const uint64_t v = reinterpret_cast<uint64_t>(row);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo) + (off * (uint32_t)sizeof(T));
+}
+
+template <typename T>
+__device__ __forceinline__ void load4o(const T* row, uint32_t off, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(at_off(row, off))));
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  } else {
+    const u32x2 a = __builtin_nontemporal_load(gp(reinterpret_cast<const u32x2*>(at_off(row, off))));
+    const T* h = reinterpret_cast<const T*>(&a);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[k] = to_f<T>(h[k]);
+  }
+}
+
+// Where a statistics workgroup sits: tensor-local tile t, chunk, strip, batch.
+struct TilePos {
+  int64_t t, ch, s, b, r_lo, r_hi, c_base;
+};
+
+// (UPD: an update tile of kTR rows, else a statistics tile of W.tr rows.)
+template <bool UPD>
+__device__ __forceinline__ TilePos tile_pos(const DescF& D, const FWs& W) {
+  TilePos q;
+  q.t = (int64_t)blockIdx.x - (UPD ? D.utile_begin : D.tile_begin);
+  const int64_t tr = UPD ? kTR : W.tr;
+  const uint32_t t32 = (uint32_t)q.t, nch = (uint32_t)W.nchunk, nst = (uint32_t)(UPD ? W.nustrip : W.nstrip);
+  const uint32_t bs = t32 / nch;
+  q.ch = (int64_t)(t32 - bs * nch);
+  q.b = (int64_t)(bs / nst);
+  q.s = (int64_t)(bs - (uint32_t)q.b * nst);
+  q.r_lo = q.s * tr;
+  q.r_hi = (q.r_lo + tr < D.R) ? q.r_lo + tr : D.R;
+  q.c_base = q.ch * kTC;
+  return q;
+}
+
+// The four waves' row partials of the tile (LDS, [4][kTRS]) summed in a fixed
+// order into the chunk's row partials.
+__device__ __forceinline__ void tile_rows_out(const double* s_row, double* rowpart, int64_t r_lo, int64_t r_hi) {
+  __syncthreads();
+  for (int i = threadIdx.x; i < r_hi - r_lo; i += 256) {
+    const double v = ((s_row[i] + s_row[kTRS + i]) + s_row[2 * kTRS + i]) + s_row[3 * kTRS + i];
+    gp(rowpart)[r_lo + i] = v;
+  }
+}
+
+template <typename T, bool PSQ, bool RAGGED>
+__device__ __forceinline__ void fstats_tile(const DescF& D, const TilePos& q, int64_t c0, bool act, double* acc,
+                                            double& psq, double* s_row) {
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  const T* P = reinterpret_cast<const T*>(D.param);
+  const int64_t R = D.R, C = D.C;
+  const int wl = threadIdx.x & 63;
+  const uint32_t cl = act ? (uint32_t)c0 : 0u;
+  const bool vec = D.vec4 != 0;
+  float g[kRB][4], pv[kRB][PSQ ? 4 : 1];
+  bool rv[kRB];
+  auto issue = [&](int64_t r0) {
+#pragma unroll
+    for (int k = 0; k < kRB; ++k) {
+      const int64_t r = r0 + k;
+      rv[k] = r < q.r_hi;
+      const int64_t rowbase = (q.b * R + (rv[k] ? r : q.r_lo)) * C;
+      if constexpr (RAGGED) {
+        load4<T>(G, rowbase, c0, C, vec, g[k]);
+        if constexpr (PSQ) load4<T>(P, rowbase, c0, C, vec, pv[k]);
+      } else {
+        load4o<T>(G + rowbase, cl, g[k]);
+        if constexpr (PSQ) load4o<T>(P + rowbase, cl, pv[k]);
+      }
+    }
+  };
+  double rp[kRB];
+  auto consume = [&]() {
+#pragma unroll
+    for (int k = 0; k < kRB; ++k) {
+      const bool ok = rv[k] && act;
+      double rk = 0.0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // the float square g*g is the reference's term (g32.square(), optimizer.py:2213)
+        const float gg = ok ? scrub(g[k][e]) : 0.0f;
+        const double sq = (double)(gg * gg);
+        acc[e] += sq;
+        rk += sq;
+        if constexpr (PSQ) {
+          const double pd = ok ? (double)pv[k][e] : 0.0;
+          psq = __builtin_fma(pd, pd, psq);
+        }
+      }
+      rp[k] = rk;
+    }
+  };
+  auto reduce = [&](int64_t r0) {
+    const double tot = reduce_scatter4(rp, wl);
+    if ((wl & 15) == 0) s_row[(r0 - q.r_lo) + row_of_lane(wl)] = tot;
+  };
+  // Each batch's row-sum reduction runs while the next batch's loads are in
+  // flight (issued just before it).
+  issue(q.r_lo);
+  __builtin_amdgcn_sched_barrier(0);
+  consume();
+  int64_t r0 = q.r_lo + kRB;
+  for (; r0 < q.r_hi; r0 += kRB) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(r0);
+    __builtin_amdgcn_sched_barrier(0);
+    reduce(r0 - kRB);
+    __builtin_amdgcn_sched_barrier(0);
+    consume();
+  }
+  reduce(r0 - kRB);
+}
+
+// Row sums and column sums of g^2 (and sum p^2) as per-tile partials, accumulated
+// in double (optimizer.py:2211-2219).
 template <typename T, bool PSQ>
 __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table, int ntab) {
-  __shared__ double s_col[4 * kTC];
+  __shared__ double s_row[4 * kTRS];
   __shared__ double s4[4];
   const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
   const FWs W = fws_layout(D.B, D.R, D.C);
-  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
-  const int64_t R = D.R, C = D.C;
-  const int64_t ch = t % W.nchunk;
-  const int64_t bs = t / W.nchunk;
-  const int64_t s = bs % W.nstrip;
-  const int64_t b = bs / W.nstrip;
-  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  const int64_t r_lo = s * W.tr;
-  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
-  const int64_t c_base = ch * kTC;
-  const T* G = reinterpret_cast<const T*>(D.grad);
-  const T* P = reinterpret_cast<const T*>(D.param);
-  float* ws = D.ws;
-  const bool vec = D.vec4 != 0;
-  // The float square g*g is the reference's term (g32.square(), optimizer.py:2213);
-  // its sums accumulate in double.
-  double acc[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) acc[k] = 0.0;
+  const TilePos q = tile_pos<false>(D, W);
+  const int lane = threadIdx.x, wl = lane & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(lane >> 6);
+  const int64_t C = D.C;
+  const int64_t c0 = q.c_base + 256 * wave + 4 * wl;
+  const bool act = c0 < C;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
   double psq = 0.0;
-  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
-    const int64_t rowbase = (b * R + r) * C;
-    double rs = 0.0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c0 = c_base + 4 * wl + 256 * j;
-      float g4[4];
-      load4<T>(G, rowbase, c0, C, vec, g4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float gg = scrub(g4[e]);
-        const double sq = (double)(gg * gg);
-        rs += sq;
-        acc[j * 4 + e] += sq;
-      }
-      if constexpr (PSQ) {
-        float p4[4];
-        load4<T>(P, rowbase, c0, C, vec, p4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) psq = __builtin_fma((double)p4[e], (double)p4[e], psq);
-      }
-    }
-    rs = grp_sum_d(rs, 64);
-    if (wl == 0) gp(ws_dp(ws, W.rowpart))[ch * (D.B * R) + b * R + r] = rs;
+  double* srow = s_row + kTRS * wave;
+  if (q.c_base + 256 * wave >= C) {   // the wave's columns lie beyond C
+    for (int i = wl; i < kTRS; i += 64) srow[i] = 0.0;
   }
+  else if ((C & 3) == 0) fstats_tile<T, PSQ, false>(D, q, c0, act, acc, psq, srow);
+  else fstats_tile<T, PSQ, true>(D, q, c0, act, acc, psq, srow);
+  float* ws = D.ws;
+  double* colp = ws_dp(ws, W.colpart) + (q.b * W.nstrip + q.s) * C;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s_col[wave * kTC + 4 * wl + 256 * j + e] = acc[j * 4 + e];
-  __syncthreads();
-  for (int q = lane; q < kTC; q += 256) {
-    const int64_t c = c_base + q;
-    if (c < C) {
-      const double v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
-      gp(ws_dp(ws, W.colpart))[(b * W.nstrip + s) * C + c] = v;
-    }
-  }
+  for (int e = 0; e < 4; ++e)
+    if (c0 + e < C) gp(colp)[c0 + e] = acc[e];
+  tile_rows_out(s_row, ws_dp(ws, W.rowpart) + q.ch * (D.B * D.R) + q.b * D.R, q.r_lo, q.r_hi);
   if constexpr (PSQ) {
     const double tot = wg_sum_d(psq, s4);
-    if (lane == 0) gp(ws_dp(ws, W.p2))[t] = tot;
+    if (lane == 0) gp(ws_dp(ws, W.p2))[q.t] = tot;
   }
 }
 
@@ -344,79 +498,142 @@ __device__ __forceinline__ void m_old4(int mkr, const uint8_t* mq, const float* 
   }
 }
 
-// CAME pass 1 (optimizer.py:929-937): U = ((g * inv_row) * inv_col) / clip,
-// M' = lerp(M, U, 1 - beta1), res = (U - M')^2 + eps_came; row and column sums
-// of res as per-tile partials in the g^2 partial arrays (consumed by then).
-template <typename T, int MK>
-__global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, int ntab, HyperF h) {
-  __shared__ double s_col[4 * kTC];
-  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
-  const FWs W = fws_layout(D.B, D.R, D.C);
-  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
-  const int64_t R = D.R, C = D.C;
-  const int64_t ch = t % W.nchunk;
-  const int64_t bs = t / W.nchunk;
-  const int64_t s = bs % W.nstrip;
-  const int64_t b = bs / W.nstrip;
-  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  const int64_t r_lo = s * W.tr;
-  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
-  const int64_t c_base = ch * kTC;
+// CAME pass 1 over the statistics tiles of one workgroup (layout of fstats_tile):
+// U = ((g * inv_row) * inv_col) / clip, M' = lerp(M, U, 1 - beta1),
+// res = (U - M')^2 + eps_came, row and column sums of res (optimizer.py:929-937).
+template <typename T, int MK, bool RAGGED>
+__device__ __forceinline__ void came1_tile(const DescF& D, const FWs& W, const TilePos& q, const HyperF& h,
+                                           int64_t c0, bool act, const float* icol, float clip, double* acc,
+                                           double* s_row) {
   const T* G = reinterpret_cast<const T*>(D.grad);
-  float* ws = D.ws;
+  const int64_t R = D.R, C = D.C;
+  const int wl = threadIdx.x & 63;
+  const uint32_t cl = act ? (uint32_t)c0 : 0u;
   const bool vec = D.vec4 != 0;
-  const float clip = gp(ws)[W.scal + 4];
-  float icol[16];
+  const float* ws = D.ws;
+  const int mk = MK == 1 ? 1 : h.mk;
+  const bool nib = (mk == 2 || mk == 4);
+  const LerpW lw = lerp_weight(h.w_m);
+  const float rclip = 1.0f / clip;
+  float g[kRB][4], mo[kRB][4], ir[kRB];
+  uint32_t qv[kRB];
+  float ms[kRB];
+  bool rv[kRB];
+  auto issue = [&](int64_t r0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t c = c_base + 4 * wl + 256 * j + e;
-      icol[j * 4 + e] = (c < C) ? gp(ws)[W.invc + b * C + c] : 0.0f;
-    }
-  double acc[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) acc[k] = 0.0;
-  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
-    const int64_t rowbase = (b * R + r) * C;
-    const float ir = gp(ws)[W.invr + b * R + r];
-    double rs = 0.0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c0 = c_base + 4 * wl + 256 * j;
-      if (c0 < C) {
-        float g4[4], m4[4];
-        load4<T>(G, rowbase, c0, C, vec, g4);
-        if constexpr (MK == 3) load4<float>(D.m, rowbase, c0, C, vec, m4);
-        else m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, m4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (c0 + e < C) {
-            const float ug = ((scrub(g4[e]) * ir) * icol[j * 4 + e]) / clip;
-            const float mn = lerp_ref(m4[e], ug, h.w_m);
-            const float dd = ug - mn;
-            const double res = (double)(dd * dd + h.eps_came);
-            rs += res;
-            acc[j * 4 + e] += res;
-          }
+    for (int k = 0; k < kRB; ++k) {
+      const int64_t r = r0 + k;
+      rv[k] = r < q.r_hi;
+      const int64_t rr = rv[k] ? r : q.r_lo;
+      const int64_t rowbase = (q.b * R + rr) * C;
+      ir[k] = cp(ws)[W.invr + q.b * R + rr];
+      if constexpr (RAGGED) {
+        load4<T>(G, rowbase, c0, C, vec, g[k]);
+        if constexpr (MK == 3) load4<float>(D.m, rowbase, c0, C, vec, mo[k]);
+        else m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, mo[k]);
+      } else {
+        load4o<T>(G + rowbase, cl, g[k]);
+        if constexpr (MK == 3) {
+          load4o<float>(D.m + rowbase, cl, mo[k]);
+        } else {
+          const int64_t e = rowbase + cl;
+          ms[k] = gp(D.m_scale)[e >> h.lbm];
+          if (MK == 1 || !nib) qv[k] = __builtin_nontemporal_load(gp(reinterpret_cast<const uint32_t*>(D.m_q + e)));
+          else qv[k] = __builtin_nontemporal_load(gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1))));
         }
       }
     }
-    rs = grp_sum_d(rs, 64);
-    if (wl == 0) gp(ws_dp(ws, W.rowpart))[ch * (D.B * R) + b * R + r] = rs;
-  }
+  };
+  double rp[kRB];
+  auto consume = [&]() {
+    float mk4[kRB][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+    for (int k = 0; k < kRB; ++k) {
+      if constexpr (!RAGGED && MK != 3) {
+        if (MK == 1 || !nib) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s_col[wave * kTC + 4 * wl + 256 * j + e] = acc[j * 4 + e];
-  __syncthreads();
-  for (int q = lane; q < kTC; q += 256) {
-    const int64_t c = c_base + q;
-    if (c < C) {
-      const double v = ((s_col[q] + s_col[kTC + q]) + s_col[2 * kTC + q]) + s_col[3 * kTC + q];
-      gp(ws_dp(ws, W.colpart))[(b * W.nstrip + s) * C + c] = v;
+          for (int e = 0; e < 4; ++e) mk4[k][e] = m_decode(mk, (qv[k] >> (8 * e)) & 0xFFu, ms[k]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t byte = (qv[k] >> (8 * (e >> 1))) & 0xFFu;
+            mk4[k][e] = m_decode(mk, (e & 1) ? (byte & 0x0Fu) : (byte >> 4), ms[k]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mk4[k][e] = mo[k][e];
+      }
     }
+#pragma unroll
+    for (int k = 0; k < kRB; ++k) {
+      float xs[4], ug[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xs[e] = (scrub(g[k][e]) * ir[k]) * icol[e];
+      div_by<4>(ug, xs, clip, rclip);
+      double rk = 0.0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = rv[k] && (RAGGED ? c0 + e < C : act);
+        const float mn = lerp_u(mk4[k][e], ug[e], lw);
+        const float dd = ug[e] - mn;
+        const double res = ok ? (double)(dd * dd + h.eps_came) : 0.0;
+        acc[e] += res;
+        rk += res;
+      }
+      rp[k] = rk;
+    }
+  };
+  auto reduce = [&](int64_t r0) {
+    const double tot = reduce_scatter4(rp, wl);
+    if ((wl & 15) == 0) s_row[(r0 - q.r_lo) + row_of_lane(wl)] = tot;
+  };
+  // next batch's loads in flight during the row-sum reduction, as in fstats_tile
+  issue(q.r_lo);
+  __builtin_amdgcn_sched_barrier(0);
+  consume();
+  int64_t r0 = q.r_lo + kRB;
+  for (; r0 < q.r_hi; r0 += kRB) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(r0);
+    __builtin_amdgcn_sched_barrier(0);
+    reduce(r0 - kRB);
+    __builtin_amdgcn_sched_barrier(0);
+    consume();
   }
+  reduce(r0 - kRB);
+}
+
+// CAME pass 1: the residual's row and column sums as per-tile partials in the
+// g^2 partial arrays (consumed by then).
+template <typename T, int MK>
+__global__ __launch_bounds__(256) void k_came1(const DescF* __restrict__ table, int ntab, HyperF h) {
+  __shared__ double s_row[4 * kTRS];
+  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const TilePos q = tile_pos<false>(D, W);
+  const int lane = threadIdx.x, wl = lane & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(lane >> 6);
+  const int64_t C = D.C;
+  const int64_t c0 = q.c_base + 256 * wave + 4 * wl;
+  const bool act = c0 < C;
+  float* ws = D.ws;
+  const float clip = cp(ws)[W.scal + 4];
+  float icol[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) icol[e] = (c0 + e < C) ? gp(ws)[W.invc + q.b * C + c0 + e] : 0.0f;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  double* srow = s_row + kTRS * wave;
+  if (q.c_base + 256 * wave >= C) {   // the wave's columns lie beyond C
+    for (int i = wl; i < kTRS; i += 64) srow[i] = 0.0;
+  }
+  else if ((C & 3) == 0) came1_tile<T, MK, false>(D, W, q, h, c0, act, icol, clip, acc, srow);
+  else came1_tile<T, MK, true>(D, W, q, h, c0, act, icol, clip, acc, srow);
+  double* colp = ws_dp(ws, W.colpart) + (q.b * W.nstrip + q.s) * C;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c0 + e < C) gp(colp)[c0 + e] = acc[e];
+  tile_rows_out(s_row, ws_dp(ws, W.rowpart) + q.ch * (D.B * D.R) + q.b * D.R, q.r_lo, q.r_hi);
 }
 
 // ------------------------------------------------------------ row/column V EMA
@@ -434,6 +651,47 @@ __device__ __forceinline__ float fv_decode(const void* q, const float* sc, const
     const int64_t bi = i / bsz;
     return exp2_exact(((float)(c - 1) * gp(sc)[bi]) / 65534.0f + gp(ml)[bi]);
   }
+}
+
+__device__ __forceinline__ const DescF* find_cs(const DescF* tab, int n, int64_t wg) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (tab[mid].cs_begin <= wg) lo = mid; else hi = mid - 1;
+  }
+  return tab + lo;
+}
+
+// First level of the column reduction for tensors of more than kSplit strips:
+// one workgroup per (batch, 256 columns, group of kSplit strips) sums its strips'
+// partials in strip order (double) into colsum.  k_fblock then adds the nsplit
+// group sums in order.
+__global__ __launch_bounds__(256) void k_fcolsum(const DescF* __restrict__ table, int ntab) {
+  const DescF D = *find_cs(table, ntab, (int64_t)blockIdx.x);
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  if (W.nsplit <= 1) return;
+  const int64_t C = D.C;
+  const int64_t ncg = (C + 255) / 256;
+  const int64_t w = (int64_t)blockIdx.x - D.cs_begin;
+  const int64_t sg = w % W.nsplit;
+  const int64_t cg = (w / W.nsplit) % ncg;
+  const int64_t b = w / (W.nsplit * ncg);
+  const int64_t c = cg * 256 + threadIdx.x;
+  if (c >= C) return;
+  const int64_t k0 = sg * kSplit;
+  const int64_t k1 = (k0 + kSplit < W.nstrip) ? k0 + kSplit : W.nstrip;
+  const double* src = ws_dp(D.ws, W.colpart) + b * W.nstrip * C + c;
+  double sum = 0.0;
+  int64_t k = k0;
+  for (; k + 8 <= k1; k += 8) {   // eight loads in flight, summed in order
+    double t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = gp(src)[(k + u) * C];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += t[u];
+  }
+  for (; k < k1; ++k) sum += gp(src)[k * C];
+  gp(ws_dp(D.ws, W.colsum))[(b * W.nsplit + sg) * C + c] = sum;
 }
 
 __device__ __forceinline__ const DescF* find_fblk(const DescF* tab, int n, int64_t wg) {
@@ -497,17 +755,19 @@ __global__ __launch_bounds__(256) void k_fblock(const DescF* __restrict__ table,
     if (is_row) {
       for (int64_t k = 0; k < W.nchunk; ++k) sum += gp(ws_dp(ws, W.rowpart))[k * n + i];
     } else {
+      // the column's strip partials, or k_fcolsum's sums of kSplit strips each
       const int64_t b = i / C, c = i - b * C;
-      const double* cp0 = ws_dp(ws, W.colpart) + b * W.nstrip * C + c;
+      const int64_t np = W.nsplit > 1 ? W.nsplit : W.nstrip;
+      const double* cp0 = ws_dp(ws, W.nsplit > 1 ? W.colsum : W.colpart) + b * np * C + c;
       int64_t k = 0;
-      for (; k + 8 <= W.nstrip; k += 8) {   // eight loads in flight, summed in order
+      for (; k + 8 <= np; k += 8) {   // eight loads in flight, summed in order
         double t[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) t[u] = gp(cp0)[(k + u) * C];
 #pragma unroll
         for (int u = 0; u < 8; ++u) sum += t[u];
       }
-      for (; k < W.nstrip; ++k) sum += gp(cp0)[k * C];
+      for (; k < np; ++k) sum += gp(cp0)[k * C];
     }
     float mean = (float)sum / cnt;
     if constexpr (!CONF) mean = mean + h.eps1;
@@ -791,32 +1051,33 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 // inv_conf_col) are staged in LDS once, a row's inv_row arrives through a scalar
 // load, and an M block is B_M/4 lanes of one chunk of one row.  Same arithmetic
 // and operation order as k_fupdate; MODE 1 writes one partial per tile.
+// Pins four values in VGPRs at this point, so the arithmetic that forms them (and
+// the waits for its loads) stays ahead of a following lane-conditional store
+// instead of being sunk into it; a load left unconsumed on the store-skipping path
+// would make the next row's loads wait for every outstanding store.
+__device__ __forceinline__ void keep4(const float* v) {
+  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
+}
+
 template <typename T, int MODE, bool SR, int MK, bool CM>
 __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, int ntab, HyperF h) {
   if constexpr (SR) hf_step(h);
   static_assert(!CM || MK != 0, "CAME needs momentum");
   __shared__ float s_ic[2 * kTC];
-  __shared__ float s4[8];
   __shared__ double s4d[4];
   constexpr bool kHasM = MK != 0;
-  const DescF D = *find_tile(table, ntab, (int64_t)blockIdx.x);
+  const DescF D = *find_utile(table, ntab, (int64_t)blockIdx.x);
   if (!D.tiled) return;   // updated by k_fupdate
   const FWs W = fws_layout(D.B, D.R, D.C);
-  const int64_t t = (int64_t)blockIdx.x - D.tile_begin;
-  const int64_t R = D.R, C = D.C;
-  const int64_t ch = t % W.nchunk;
-  const int64_t bs = t / W.nchunk;
-  const int64_t s = bs % W.nstrip;
-  const int64_t b = bs / W.nstrip;
-  const int lane = threadIdx.x, wave = lane >> 6, wl = lane & 63;
-  const int64_t r_lo = s * W.tr;
-  const int64_t r_hi = (r_lo + W.tr < R) ? r_lo + W.tr : R;
-  const int64_t c_base = ch * kTC;
+  const TilePos q = tile_pos<true>(D, W);
+  const int64_t R = D.R, C = D.C, b = q.b, c_base = q.c_base;
+  const int lane = threadIdx.x, wl = lane & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(lane >> 6);
   float* ws = D.ws;
-  for (int q = lane; q < kTC; q += 256) {
-    const int64_t c = c_base + q;
-    s_ic[q] = c < C ? gp(ws)[W.invc + b * C + c] : 0.0f;
-    if constexpr (CM) s_ic[kTC + q] = c < C ? gp(ws)[W.icc + b * C + c] : 0.0f;
+  for (int k = lane; k < kTC; k += 256) {
+    const int64_t c = c_base + k;
+    s_ic[k] = c < C ? gp(ws)[W.invc + b * C + c] : 0.0f;
+    if constexpr (CM) s_ic[kTC + k] = c < C ? gp(ws)[W.icc + b * C + c] : 0.0f;
   }
   __syncthreads();
   const float* sl = ws + W.scal;
@@ -824,6 +1085,8 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
   const int G = (1 << lbm) >> 2;          // lanes per M block
   const int mk = (MK == 1) ? 1 : h.mk;
   const float clip = CM ? cp(sl)[4] : 1.0f;
+  const float rclip = 1.0f / clip;
+  const LerpW lw = lerp_weight(h.w_m);
   float step = 0.0f, fs = 1.0f, dec = 1.0f;
   if constexpr (MODE != 1) {
     step = (MODE == 0) ? cp(sl)[0] : cp(sl)[1];
@@ -833,95 +1096,117 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
   const bool has_dec = h.wd_mode != 0;
   const T* G0 = reinterpret_cast<const T*>(D.grad);
   T* P0 = reinterpret_cast<T*>(D.param);
+  // A lane's four 4-column windows.  C % 4 == 0, so a window holds all four
+  // columns or none; one beyond C is pointed at the tile's first window (a valid
+  // address), computed on like the others and never stored.  Loads and their
+  // arithmetic are unconditional, so nothing is left in flight across rows.
+  uint32_t cl[4];
+  bool act[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t c0 = c_base + 256 * j + 4 * wl;
+    act[j] = c0 < C;
+    cl[j] = act[j] ? (uint32_t)c0 : (uint32_t)c_base;
+  }
+  // Rows r and r + 4 in one pass for the plain update (the loads of both in
+  // flight together); one row per pass with momentum and in the read-only norm
+  // pass, where registers are better spent on occupancy.  A second row beyond
+  // the tile reads the first one again and stores nothing.
+  constexpr int NRW = (kHasM || MODE == 1) ? 1 : 2;
   double sq = 0.0;   // sum u^2 (MODE 1), accumulated in double
-  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
-    const int64_t rowbase = (b * R + r) * C;
-    const float ir = cp(ws)[W.invr + b * R + r];
-    const float icrr = CM ? cp(ws)[W.icr + b * R + r] : 0.0f;
-    // all loads of the row's four chunks first (up to 128 B per lane in flight),
-    // then the arithmetic and stores chunk by chunk
-    float gj[4][4], pj[4][4], msj[4];
+  for (int64_t r0 = q.r_lo + wave; r0 < q.r_hi; r0 += 4 * NRW) {
+    int64_t rowb[NRW];
+    bool rv[NRW];
+    float irw[NRW], icrw[NRW];
+    float gj[NRW][4][4], pj[NRW][4][4], msj[4];
     float mfj[MK == 3 ? 4 : 1][4];
     uint32_t qj[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c0 = c_base + 256 * j + 4 * wl;
-      const int64_t e = rowbase + c0;
-      msj[j] = 0.0f;
-      qj[j] = 0u;
+    for (int rr = 0; rr < NRW; ++rr) {
+      rv[rr] = r0 + 4 * rr < q.r_hi;
+      const int64_t r = rv[rr] ? r0 + 4 * rr : r0;
+      rowb[rr] = (b * R + r) * C;
+      irw[rr] = cp(ws)[W.invr + b * R + r];
+      icrw[rr] = CM ? cp(ws)[W.icr + b * R + r] : 0.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { gj[j][i] = 0.0f; pj[j][i] = 0.0f; }
-      if constexpr (MK == 3) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mfj[j][i] = 0.0f;
-      }
-      if (c0 < C) {                       // C % 4 == 0: all four columns or none
-        load4v<T>(G0, e, gj[j]);
+      for (int j = 0; j < 4; ++j) {
+        const int64_t e = rowb[rr] + cl[j];
+        load4o<T>(G0 + rowb[rr], cl[j], gj[rr][j]);
         if constexpr (MK == 3) {
-          load4v<float>(D.m, e, mfj[j]);
+          load4o<float>(D.m + rowb[rr], cl[j], mfj[j]);
         } else if constexpr (kHasM) {
           msj[j] = gp(D.m_scale)[e >> lbm];
           if (MK == 1 || !(mk == 2 || mk == 4)) qj[j] = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
           else qj[j] = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
         }
-        if constexpr (MODE != 1 && !SR) load4v<T>(P0, e, pj[j]);
+        if constexpr (MODE != 1 && !SR) load4o<T>(P0 + rowb[rr], cl[j], pj[rr][j]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);   // every load of the pass is issued before its arithmetic
+#pragma unroll
+    for (int rr = 0; rr < NRW; ++rr)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (c_base + 256 * j >= C) break;     // uniform: chunk beyond the matrix
       const int q0 = 256 * j + 4 * wl;
-      const int64_t c0 = c_base + q0;
-      const bool act = c0 < C;
-      const int64_t e = rowbase + c0;
+      const int64_t e = rowb[rr] + cl[j];
+      const float ir = irw[rr], icrr = icrw[rr];
+      const bool st = rv[rr] && act[j];   // this window of this row is stored
       float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      float* pv = pj[j];
-      if (act) {
-        if constexpr (MK == 3) {
+      float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4];
+      float* pv = pj[rr][j];
+      if constexpr (MK == 3) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) mo[i] = mfj[j][i];
-        } else if constexpr (kHasM) {
-          const float ms = msj[j];
-          const uint32_t qv = qj[j];
-          if (MK == 1) {
-            const float s128 = ms / 128.0f, b128 = -128.0f * s128;
+        for (int i = 0; i < 4; ++i) mo[i] = mfj[j][i];
+      } else if constexpr (kHasM) {
+        const float ms = msj[j];
+        const uint32_t qv = qj[j];
+        if (MK == 1) {
+          const float s128 = ms / 128.0f, b128 = -128.0f * s128;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mo[i] = __builtin_fmaf((float)((qv >> (8 * i)) & 0xFFu), s128, b128);
-          } else if (mk == 2 || mk == 4) {
+          for (int i = 0; i < 4; ++i) mo[i] = __builtin_fmaf((float)((qv >> (8 * i)) & 0xFFu), s128, b128);
+        } else if (mk == 2 || mk == 4) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const uint32_t byte = (qv >> (8 * (i >> 1))) & 0xFFu;
-              mo[i] = m_decode(mk, (i & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
-            }
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mo[i] = m_decode(mk, (qv >> (8 * i)) & 0xFFu, ms);
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t byte = (qv >> (8 * (i >> 1))) & 0xFFu;
+            mo[i] = m_decode(mk, (i & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
           }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mo[i] = m_decode(mk, (qv >> (8 * i)) & 0xFFu, ms);
         }
+      }
+      float ugj[4];
+      if constexpr (CM) {
+        float xs[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gi = scrub(gj[j][i]);
-          const float ic = s_ic[q0 + i];
-          if constexpr (CM) {
-            const float ug = ((gi * ir) * ic) / clip;
-            mn[i] = lerp_ref(mo[i], ug, h.w_m);
-            u[i] = (mn[i] * icrr) * s_ic[kTC + q0 + i];
-          } else {
-            float x = gi;
-            if constexpr (kHasM) { mn[i] = lerp_ref(mo[i], gi, h.w_m); x = mn[i]; }
-            u[i] = (x * ir) * ic;
-          }
-          if (MODE == 1) sq = __builtin_fma((double)u[i], (double)u[i], sq);
+        for (int i = 0; i < 4; ++i) xs[i] = (scrub(gj[rr][j][i]) * ir) * s_ic[q0 + i];
+        div_by<4>(ugj, xs, clip, rclip);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gi = scrub(gj[rr][j][i]);
+        const float ic = s_ic[q0 + i];
+        if constexpr (CM) {
+          mn[i] = lerp_u(mo[i], ugj[i], lw);
+          u[i] = (mn[i] * icrr) * s_ic[kTC + q0 + i];
+        } else {
+          float x = gi;
+          if constexpr (kHasM) { mn[i] = lerp_u(mo[i], gi, lw); x = mn[i]; }
+          u[i] = (x * ir) * ic;
+        }
+        if (MODE == 1) {
+          const double ud = st ? (double)u[i] : 0.0;
+          sq = __builtin_fma(ud, ud, sq);
         }
       }
       if constexpr (MODE != 1) {
-        if (act) {
-          if (MODE == 2) {
+        if (MODE == 2) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) u[i] = u[i] * fs;
-          }
-          if constexpr (SR) {
+          for (int i = 0; i < 4; ++i) u[i] = u[i] * fs;
+        }
+        if constexpr (SR) {
+          keep4(u);
+          if (st) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const float p = ld1<T>(P0, e + i);
@@ -931,25 +1216,28 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
               __builtin_memcpy(&bits, &rr, 2);
               gp(reinterpret_cast<uint16_t*>(P0))[e + i] = bits;
             }
-          } else {
-            if (has_dec) {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) pv[i] = pv[i] * dec;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = __builtin_fmaf(-step, u[i], pv[i]);
-            store4n<T>(P0, e, e + 4, pv);
           }
+        } else {
+          if (has_dec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[i] = pv[i] * dec;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pv[i] = __builtin_fmaf(-step, u[i], pv[i]);
+          keep4(pv);
+          if (st) store4n<T>(P0, e, e + 4, pv);
         }
         if constexpr (MK == 3) {
-          if (act) store4n<float>(D.m, e, e + 4, mn);
+          keep4(mn);
+          if (st) store4n<float>(D.m, e, e + 4, mn);
         } else if constexpr (kHasM) {
-          // momentum re-encode: absmax over the block's G lanes (inactive lanes hold 0)
+          // momentum re-encode: absmax over the block's G lanes.  C is a multiple
+          // of the M block, so a block is wholly inside or wholly beyond C.
           uint32_t ab = 0u;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ab = max(ab, __float_as_uint(mn[i]) & 0x7FFFFFFFu);
+          for (int i = 0; i < 4; ++i) ab = max(ab, st ? (__float_as_uint(mn[i]) & 0x7FFFFFFFu) : 0u);
           const float bam = grp_max(__uint_as_float(ab), G);
-          if (act) {
+          if (st) {
             const float am = fmaxf(bam, 1e-12f);
             const float ram = fast_rcp(am);
             if (MK == 1) {
@@ -967,10 +1255,10 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
             } else if (mk == 2 || mk == 4) {
               uint32_t w = 0;
 #pragma unroll
-              for (int q = 0; q < 2; ++q) {
-                const uint32_t hi = m_encode(mk, mn[2 * q], am, ram);
-                const uint32_t lo = m_encode(mk, mn[2 * q + 1], am, ram);
-                w |= ((hi << 4) | lo) << (8 * q);
+              for (int k = 0; k < 2; ++k) {
+                const uint32_t hi = m_encode(mk, mn[2 * k], am, ram);
+                const uint32_t lo = m_encode(mk, mn[2 * k + 1], am, ram);
+                w |= ((hi << 4) | lo) << (8 * k);
               }
               *gp(reinterpret_cast<uint16_t*>(D.m_q + (e >> 1))) = (uint16_t)w;
             } else {
@@ -987,7 +1275,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
   }
   if constexpr (MODE == 1) {
     const double tot = wg_sum_d(sq, s4d);
-    if (lane == 0) gp(ws_dp(ws, W.npart))[t] = tot;
+    if (lane == 0) gp(ws_dp(ws, W.npart))[q.t] = tot;
   }
 }
 
@@ -999,7 +1287,7 @@ __global__ __launch_bounds__(256) void k_fnorm(const DescF* __restrict__ table, 
   const FWs W = fws_layout(D.B, D.R, D.C);
   float* ws = D.ws;
   double s = 0.0;
-  const int64_t np = D.tiled ? W.ntile : W.nunit;
+  const int64_t np = D.tiled ? W.nutile : W.nunit;
   for (int64_t k = threadIdx.x; k < np; k += 256) s += gp(ws_dp(ws, W.npart))[k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
@@ -1037,7 +1325,7 @@ __global__ __launch_bounds__(256) void k_fclip(const DescF* __restrict__ table, 
   const FWs W = fws_layout(D.B, D.R, D.C);
   float* ws = D.ws;
   double s = 0.0;
-  const int64_t np = D.tiled ? W.ntile : W.nunit;
+  const int64_t np = D.tiled ? W.nutile : W.nunit;
   for (int64_t k = threadIdx.x; k < np; k += 256) s += gp(ws_dp(ws, W.npart))[k];
   s = wg_sum_d(s, sd);
   if (threadIdx.x == 0) {
@@ -1113,6 +1401,12 @@ static int launch_update(int mode, int mk, const DescF* tab, int ntab, const Upd
   }
 }
 
+static int launch_colsum(const DescF* tab, int ntab, int64_t ncs, hipStream_t st) {
+  if (ncs <= 0) return 0;
+  hipLaunchKernelGGL(k_fcolsum, dim3((unsigned)ncs), dim3(256), 0, st, tab, ntab);
+  return check_launch("k_fcolsum");
+}
+
 template <bool CONF>
 static int launch_finish(int bits, const DescF* tab, int ntab, int64_t nfblk, const HyperF& h,
                          hipStream_t st) {
@@ -1133,10 +1427,11 @@ static int launch_finish(int bits, const DescF* tab, int ntab, int64_t nfblk, co
 // stats, finish, [U norm + k_fclip when d > 0], k_came1, confidence finish,
 // [update norm + k_fnorm with Fira], update.
 template <typename T, bool SR>
-static int run_group(const DescF* tab, int ntab, int64_t ntiles, const UpdGrid& ug, int64_t nfblk, int vbits,
-                     int cbits, bool clip, const HyperF& h, hipStream_t st) {
+static int run_group(const DescF* tab, int ntab, int64_t ntiles, const UpdGrid& ug, int64_t nfblk, int64_t ncs,
+                     int vbits, int cbits, bool clip, const HyperF& h, hipStream_t st) {
   int rc = launch_stats<T>(h.scale_param != 0, tab, ntab, ntiles, st);
   if (rc) return rc;
+  if ((rc = launch_colsum(tab, ntab, ncs, st))) return rc;
   if ((rc = launch_finish<false>(vbits, tab, ntab, nfblk, h, st))) return rc;
   if (h.came) {
     if (h.d > 0.0f) {
@@ -1148,6 +1443,7 @@ static int run_group(const DescF* tab, int ntab, int64_t ntiles, const UpdGrid& 
     else if (h.mk == kMkFp32) hipLaunchKernelGGL((k_came1<T, 3>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     else hipLaunchKernelGGL((k_came1<T, 2>), dim3((unsigned)ntiles), dim3(256), 0, st, tab, ntab, h);
     if ((rc = check_launch("k_came1"))) return rc;
+    if ((rc = launch_colsum(tab, ntab, ncs, st))) return rc;
     if ((rc = launch_finish<true>(cbits, tab, ntab, nfblk, h, st))) return rc;
     if (!h.fira) return launch_update<T, SR, true>(0, h.mk, tab, ntab, ug, h, st);
     if ((rc = launch_update<T, false, true>(1, h.mk, tab, ntab, ug, h, st))) return rc;
@@ -1209,7 +1505,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum (m_q or m)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
-  int64_t tiles = 0, units = 0, fblks = 0;
+  int64_t tiles = 0, utiles = 0, units = 0, fblks = 0, csw = 0;
   bool any_tiled = false, any_flat = false;
   const size_t esz = dtype == A8_F32 ? 4 : 2;
   for (int i = 0; i < ntensors; ++i) {
@@ -1245,14 +1541,18 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     (D.tiled ? any_tiled : any_flat) = true;
     const FWs W = fws_layout(t.batch, t.rows, t.cols);
     D.tile_begin = tiles;
+    D.utile_begin = utiles;
     D.unit_begin = units;
     D.fblk_begin = fblks;
+    D.cs_begin = csw;
     D.nbr = (t.batch * t.rows + block_size - 1) / block_size;
     tiles += W.ntile;
+    utiles += W.nutile;
     units += W.nunit;
     fblks += D.nbr + (t.batch * t.cols + block_size - 1) / block_size;
+    if (W.nsplit > 1) csw += t.batch * ((t.cols + 255) / 256) * W.nsplit;
   }
-  if (tiles > 0x7FFFFFFF || units > 0x7FFFFFFF || fblks > 0x7FFFFFFF)
+  if (tiles > 0x7FFFFFFF || utiles > 0x7FFFFFFF || units > 0x7FFFFFFF || fblks > 0x7FFFFFFF || csw > 0x7FFFFFFF)
     return set_error(A8_ERR_SIZE, "too many workgroups");
   hipStream_t st = (hipStream_t)stream;
   if (upload && upload_table(table_dev, tab.data(), sizeof(DescF) * (size_t)ntensors, st) != hipSuccess)
@@ -1276,15 +1576,15 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   const bool clip = d > 0.0f || fira;
   const DescF* dt = reinterpret_cast<const DescF*>(table_dev);
-  const UpdGrid ug{tiles, units, any_tiled, any_flat};
+  const UpdGrid ug{utiles, units, any_tiled, any_flat};
   switch (dtype) {
-    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
+    case A8_F32: return run_group<float, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);
     case A8_BF16:
-      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st)
-                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st)
+                        : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);
     default:
-      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st)
-                        : run_group<__half, false>(dt, ntensors, tiles, ug, fblks, v_bits, c_bits, clip, h, st);
+      return stochastic ? run_group<__half, true>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st)
+                        : run_group<__half, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);
   }
 }
 

@@ -414,6 +414,27 @@ __device__ __forceinline__ float grp_max(float x, int G) {
   for (int o = 1; o < G; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
   return x;
 }
+// grp_max over aligned groups of G lanes (a power of two, uniform), with DPP lane
+// moves inside 16-lane rows (quad_perm 1032 / 2301, row_half_mirror, row_mirror:
+// each pairs every lane with one of the same group) and lane shuffles beyond.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float grp_max_dpp(float x, int G) {
+  x = fmaxf(x, dpp_f<0xB1>(x));                // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp_f<0x4E>(x));                // quad_perm [2,3,0,1]
+  if (G <= 4) return x;
+  x = fmaxf(x, dpp_f<0x141>(x));               // row_half_mirror
+  if (G <= 8) return x;
+  x = fmaxf(x, dpp_f<0x140>(x));               // row_mirror
+  if (G <= 16) return x;
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  if (G <= 32) return x;
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+
 __device__ __forceinline__ float grp_min(float x, int G) {
   for (int o = 1; o < G; o <<= 1) x = fminf(x, __shfl_xor(x, o, 64));
   return x;

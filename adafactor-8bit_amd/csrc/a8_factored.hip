@@ -817,14 +817,28 @@ __global__ __launch_bounds__(256) void k_frows(const DescF* __restrict__ table, 
   float* ws = D.ws;
   float* vec = ws + (CONF ? W.icr : W.invr);
   for (int64_t b = 0; b < B; ++b) {
+    float* v = vec + b * R;
     double s = 0.0;
-    for (int64_t r = lane; r < R; r += 256) s += (double)gp(vec)[b * R + r];
+    int64_t r = lane;
+    for (; r + 7 * 256 < R; r += 8 * 256) {   // eight loads in flight, summed in order
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = gp(v)[r + 256 * u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += (double)t[u];
+    }
+    for (; r < R; r += 256) s += (double)gp(v)[r];
     s = wg_sum_d(s, sd);
     const float rmv = fmaxf((float)s / (float)R, h.eps1);
-    for (int64_t r = lane; r < R; r += 256) {
-      const int64_t i = b * R + r;
-      gp(vec)[i] = 1.0f / sqrtf(gp(vec)[i] / rmv);
+    r = lane;
+    for (; r + 3 * 256 < R; r += 4 * 256) {
+      float t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t[u] = gp(v)[r + 256 * u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) gp(v)[r + 256 * u] = 1.0f / sqrtf(t[u] / rmv);
     }
+    for (; r < R; r += 256) gp(v)[r] = 1.0f / sqrtf(gp(v)[r] / rmv);
   }
   if constexpr (!CONF) {
     const float rho = D.lr ? *gp(D.lr) : h.lr_val;
@@ -1118,9 +1132,9 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     int64_t rowb[NRW];
     bool rv[NRW];
     float irw[NRW], icrw[NRW];
-    float gj[NRW][4][4], pj[NRW][4][4], msj[4];
-    float mfj[MK == 3 ? 4 : 1][4];
-    uint32_t qj[4];
+    float gj[NRW][4][4], pj[NRW][4][4], msj[NRW][4];
+    float mfj[NRW][MK == 3 ? 4 : 1][4];
+    uint32_t qj[NRW][4];
 #pragma unroll
     for (int rr = 0; rr < NRW; ++rr) {
       rv[rr] = r0 + 4 * rr < q.r_hi;
@@ -1133,11 +1147,11 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
         const int64_t e = rowb[rr] + cl[j];
         load4o<T>(G0 + rowb[rr], cl[j], gj[rr][j]);
         if constexpr (MK == 3) {
-          load4o<float>(D.m + rowb[rr], cl[j], mfj[j]);
+          load4o<float>(D.m + rowb[rr], cl[j], mfj[rr][j]);
         } else if constexpr (kHasM) {
-          msj[j] = gp(D.m_scale)[e >> lbm];
-          if (MK == 1 || !(mk == 2 || mk == 4)) qj[j] = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
-          else qj[j] = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
+          msj[rr][j] = gp(D.m_scale)[e >> lbm];
+          if (MK == 1 || !(mk == 2 || mk == 4)) qj[rr][j] = *gp(reinterpret_cast<const uint32_t*>(D.m_q + e));
+          else qj[rr][j] = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1)));
         }
         if constexpr (MODE != 1 && !SR) load4o<T>(P0 + rowb[rr], cl[j], pj[rr][j]);
       }
@@ -1156,10 +1170,10 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
       float* pv = pj[rr][j];
       if constexpr (MK == 3) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mo[i] = mfj[j][i];
+        for (int i = 0; i < 4; ++i) mo[i] = mfj[rr][j][i];
       } else if constexpr (kHasM) {
-        const float ms = msj[j];
-        const uint32_t qv = qj[j];
+        const float ms = msj[rr][j];
+        const uint32_t qv = qj[rr][j];
         if (MK == 1) {
           const float s128 = ms / 128.0f, b128 = -128.0f * s128;
 #pragma unroll
@@ -1236,7 +1250,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
           uint32_t ab = 0u;
 #pragma unroll
           for (int i = 0; i < 4; ++i) ab = max(ab, st ? (__float_as_uint(mn[i]) & 0x7FFFFFFFu) : 0u);
-          const float bam = grp_max(__uint_as_float(ab), G);
+          const float bam = grp_max_dpp(__uint_as_float(ab), G);
           if (st) {
             const float am = fmaxf(bam, 1e-12f);
             const float ram = fast_rcp(am);

@@ -26,7 +26,9 @@ kernels): ``adafactor`` (C2: factored AL8, B_V 256, no beta1, Student-t grads,
 bf16 params and grads 1e-3*N(0,1), the reference's apollo preset at rank 256,
 gap 200, channel scale, Fira, UF8 M / AL8 V low-rank states, SR writeback).
 For those the roofline is the whole step's algorithmic bytes over its GPU time
-(HIP events around ``step()``); apollo also reports the projection's flops.
+(HIP events around each step); adafactor and came are timed, like the headline,
+eagerly and then as graph replays of one captured ``step()`` (``value`` from the
+replays), apollo eagerly; apollo also reports the projection's flops.
 """
 import argparse
 import json
@@ -349,22 +351,42 @@ def main():
 
 def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
     kw = {"adafactor": ADAFACTOR, "came": CAME, "apollo": APOLLO}[args.workload]
-    opt = Adafactor8Bit(params, **kw)
+    # adafactor / came run capturable (device step count): timed eagerly, then as
+    # replays of one captured step; APOLLO forms per-step scalars on the host and
+    # runs eagerly only
+    graphable = args.workload != "apollo"
+    opt = Adafactor8Bit(params, **(dict(kw, capturable=True) if graphable else kw))
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        evs[i][0].record(stream)
-        opt.step()
-        evs[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = wall / args.steps * 1e3
-    gms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+
+    def timed(fn):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            evs[i][0].record(stream)
+            fn()
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return wall / args.steps * 1e3, sum(a.elapsed_time(b) for a, b in evs) / args.steps
+
+    eager_ms, eager_gms = timed(opt.step)
+    ms, gms, mode = eager_ms, eager_gms, "eager step()"
+    if graphable:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph):
+                opt.step()
+        stream.wait_stream(side)
+        graph.replay()   # warm-up replay
+        torch.cuda.synchronize()
+        ms, gms = timed(graph.replay)
+        mode = "graph replay of one captured step() (capturable=True)"
     flops = None
     if args.workload == "apollo":
         nbytes, flops = apollo_step_bytes_flops(shapes)
@@ -381,9 +403,10 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": name + "_tinyllama_1.1b_" + dt, "params": nparams, "tensors": len(params),
                    "step_bytes": nbytes},
+        "step_mode": mode, "eager_ms_per_step": eager_ms, "eager_gpu_ms_per_step": eager_gms,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
-                     "kernel": "whole step (all launches of one step, HIP events around step())",
+                     "kernel": "whole step (all launches of one step, HIP events around each step)",
                      "gpu_ms_per_step": gms, "bytes_per_step": nbytes},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(args.workload),
     }

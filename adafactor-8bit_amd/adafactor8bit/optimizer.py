@@ -1390,7 +1390,7 @@ def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, f
     for k in ("row_var_low", "col_var_low", "m_low", "res_low", "conf_row_low", "conf_col_low", "v_low"):
         if torch.is_tensor(st.get(k)) and not st[k].is_contiguous():
             st[k] = st[k].contiguous()
-    key = (dev, "apollo_x", low_shape)
+    key = (dev, "apollo_x", id(st))   # one per matrix: the batched stage runs them together
     xws = opt._ws.get(key)
     nx = int(nat.lib().a8_apollo_x_workspace_floats(low_shape[0], low_shape[1]))
     if xws is None or xws.numel() < nx:
@@ -1471,8 +1471,14 @@ def _run_apollo_batch(opt, group, bkey, items):
                 float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), 0, 2048, 8, 0, 1,
                 256)
         nat.check(L.a8_apollo_step_multi_phase(1, *head, *tail), "a8_apollo_step_multi_phase(1)")
-        for _, (st, _vb, bsz, _keep, xargs) in items:
-            nat.check(L.a8_apollo_lowrank_x(ctypes.byref(xargs), stream), "a8_apollo_lowrank_x")
+        xarr = (nat.ApolloXArgs * n)(*[it[1][4] for it in items])
+        xneed = int(L.a8_apollo_x_table_bytes(n))
+        xtab = opt._ws.get((pdev, "apx_table"))
+        if xtab is None or xtab.numel() < xneed:
+            xtab = torch.empty(max(xneed, 4096), dtype=torch.uint8, device=pdev)
+            opt._ws[(pdev, "apx_table")] = xtab
+        nat.check(L.a8_apollo_lowrank_x_multi(xarr, n, xtab.data_ptr(), xtab.numel(), stream),
+                  "a8_apollo_lowrank_x_multi")
         nat.check(L.a8_apollo_step_multi_phase(2, *head, *tail), "a8_apollo_step_multi_phase(2)")
         for _, (st, _vb, bsz, keep, xargs) in items:
             if xargs.v_bits:

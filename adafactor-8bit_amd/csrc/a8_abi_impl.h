@@ -38,6 +38,32 @@ hipError_t upload_table(void* dst, const void* src, size_t bytes, hipStream_t st
 }  // namespace a8
 
 namespace a8 {
+// Table forms of the standalone EMAs, for callers that run one stage over many
+// tensors (a8_apollo_x.hip).  x, out and dec are fp32.
+struct MEmaItem {   // momentum: m' = lerp(deq(m), x, 1 - beta), re-encoded; out = m' (optional)
+  uint8_t* m_q;
+  float* m_scale;
+  const float* x;
+  float* out;
+  int64_t n;
+};
+int64_t m_ema_table_bytes(int n);
+int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int block_size, int m_bits, int m_mode,
+                hipStream_t st);
+
+struct VEmaItem {   // AL state: v' = lerp(deq(v), x (or x^2 + eps1), w), re-encoded with a block refit
+  void* q;
+  float* scale;
+  float* min_log;
+  const float* x;
+  float* out;       // v' before encoding (optional)
+  float* dec;       // the decoded new codes (optional)
+  int64_t n;
+};
+int64_t v_ema_table_bytes(int n);
+int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_size, int square, float eps1,
+                float log_floor, int v_bits, hipStream_t st);
+
 // Codebook upload of the factored-step translation unit (called by a8_set_qmap).
 hipError_t factored_upload_qmap(const float* q8, const float* q4);
 hipError_t apollo_upload_qmap(const float* q8, const float* q4);

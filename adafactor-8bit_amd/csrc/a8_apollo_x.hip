@@ -42,21 +42,23 @@ __host__ __device__ inline XL x_layout(int64_t R, int64_t C) {
   XL w;
   w.n = R * C;
   w.nch = (R + kXRowChunk - 1) / kXRowChunk;
+  const int64_t n4 = (w.n + 3) / 4 * 4;   // regions start 16-byte aligned
   w.xv = 0;                    // V values of coded V (the lerped values)
-  w.xu = w.xv + w.n;           // U (CAME)
-  w.xm = w.xu + w.n;           // momentum values of coded M
-  w.xr = w.xm + w.n;           // residual, then its decoded EMA
-  w.rowm = w.xr + w.n;         // row means
-  w.colm = w.rowm + R;         // column means
-  w.crow = w.colm + C;         // confidence values of coded confidence
-  w.ccol = w.crow + R;
-  w.scal = w.ccol + C;         // [0] clip, [1] row-variance mean (clamped), [2] confidence row mean
+  w.xu = w.xv + n4;            // U (CAME)
+  w.xm = w.xu + n4;            // momentum values of coded M
+  w.xr = w.xm + n4;            // residual, then its decoded EMA
+  w.rowm = w.xr + n4;          // row means
+  w.colm = w.rowm + (R + 3) / 4 * 4;   // column means
+  w.crow = w.colm + (C + 3) / 4 * 4;   // confidence values of coded confidence
+  w.ccol = w.crow + (R + 3) / 4 * 4;
+  w.scal = w.ccol + (C + 3) / 4 * 4;   // [0] clip, [1] row-variance mean (clamped), [2] confidence row mean
   w.part = (w.scal + 16 + 1) / 2 * 2;
   w.cpart = w.part + 2 * kXParts;
   w.total = w.cpart + 2 * w.nch * C;
   return w;
 }
 
+// One matrix of a launch.
 struct XK {
   const float* g;      // g_low, R x C row-major
   const float* src;    // input of the fp32 momentum EMA (g_low or U)
@@ -73,7 +75,42 @@ struct XK {
   int64_t R, C, n;
   float bv, omb, w1, w3, aeps, eps_sq, eps_came, d, sqn;
   int first, np;
+  int v4;              // every stream of this matrix is 16-byte aligned and n % 4 == 0
 };
+
+// Launch kinds: each has its own grid over the batch, and a matrix owns the
+// workgroups [wb[kind], wb[kind] + count) of it.
+enum { XW_EL = 0, XW_ROWS, XW_CPART, XW_CFIN, XW_VEC, XW_ONE, XW_N };
+
+struct XD {
+  XK k;
+  int64_t wb[XW_N];
+};
+
+// Where a launch finds its matrices: a device table, or one matrix by value.
+struct XT {
+  XD one;
+  const XD* tab;
+  int ntab;
+};
+
+// The matrix that owns workgroup blockIdx.x of a launch of kind KIND, and the
+// workgroup's index within that matrix.
+template <int KIND>
+__device__ __forceinline__ XK x_find(const XT& t, int64_t& local) {
+  const int64_t wg = blockIdx.x;
+  if (!t.tab) {
+    local = wg;
+    return t.one.k;
+  }
+  int lo = 0, hi = t.ntab - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t.tab[mid].wb[KIND] <= wg) lo = mid; else hi = mid - 1;
+  }
+  local = wg - t.tab[lo].wb[KIND];
+  return t.tab[lo].k;
+}
 
 enum {
   XE_SQB = 0,   // xv = (g^2) * bv
@@ -99,134 +136,228 @@ __device__ __forceinline__ double x_wg_sum(double v, double* sd) {
   return ((sd[0] + sd[1]) + sd[2]) + sd[3];
 }
 
-template <int OP>
-__global__ __launch_bounds__(256) void k_ax_el(XK k) {
-  __shared__ double sd[4];
-  float* ws = k.ws;
-  const XL L = x_layout(k.R, k.C);
-  const float clip = (OP == XE_DIV) ? gp(ws)[L.scal] : 1.0f;
-  double acc = 0.0;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < k.n; i += stride) {
-    if constexpr (OP == XE_SQB) {
-      const float g = gp(k.g)[i];
-      gp(ws)[L.xv + i] = (g * g) * k.bv;
-    } else if constexpr (OP == XE_V32) {
-      const float g = gp(k.g)[i];
-      const float g2 = g * g;
-      gp(k.v)[i] = k.first ? g2 * k.bv : lerp_ref(gp(k.v)[i], g2, k.bv);
-    } else if constexpr (OP == XE_U) {
-      const float x = gp(k.g)[i] * rsqrt_ref(fmaxf(gp(k.v)[i], k.eps_sq));
-      gp(k.dst)[i] = x;
-      acc += (double)(x * x);
-    } else if constexpr (OP == XE_FCU) {
-      const int64_t r = i / k.C, c = i - r * k.C;
-      const float ir = rsqrt_ref(gp(k.rv)[r] / gp(ws)[L.scal + 1]);
-      const float ic = rsqrt_ref(gp(k.cv)[c]);
-      const float x = (gp(k.g)[i] * ir) * ic;
-      gp(k.dst)[i] = x;
-      acc += (double)(x * x);
-    } else if constexpr (OP == XE_DIV) {
-      gp(k.dst)[i] = gp(k.dst)[i] / clip;
-    } else if constexpr (OP == XE_M32) {
-      gp(k.m)[i] = lerp_ref(gp(k.m)[i], gp(k.src)[i], k.w1);
-    } else if constexpr (OP == XE_RES) {
-      float r = gp(ws)[L.xu + i] - gp(k.m)[i];
-      r = r * r;
-      r = r + k.eps_came;
-      gp(ws)[L.xr + i] = r;
-      if (k.res) gp(k.res)[i] = lerp_ref(gp(k.res)[i], r, k.w3);
-    } else if constexpr (OP == XE_UCAME) {
-      const float rd = k.res ? gp(k.res)[i] : gp(ws)[L.xr + i];
-      gp(k.u)[i] = gp(k.m)[i] * rsqrt_ref(fmaxf(rd, k.eps_sq));
-    } else if constexpr (OP == XE_FU) {
-      const int64_t r = i / k.C, c = i - r * k.C;
-      const float ve = (gp(k.rv)[r] * gp(k.cv)[c]) / gp(ws)[L.scal + 1];
-      gp(k.u)[i] = gp(k.src)[i] / (sqrtf(ve) + k.aeps);
-    } else {   // XE_FUC
-      const int64_t r = i / k.C, c = i - r * k.C;
-      const float icr = rsqrt_ref(gp(k.cr)[r] / gp(ws)[L.scal + 2]);
-      const float icc = rsqrt_ref(gp(k.cc)[c]);
-      gp(k.u)[i] = (gp(k.m)[i] * icr) * icc;
-    }
+// Four consecutive elements of a stream: one 16-byte access when the matrix's
+// streams are aligned (v4), else element by element inside n.
+__device__ __forceinline__ void x_ld4(const float* p, int64_t i, int64_t n, int v4, float* o) {
+  if (v4) {
+    load4v<float>(p, i, o);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (i + e < n) ? gp(p)[i + e] : 0.0f;
   }
-  if constexpr (OP == XE_U || OP == XE_FCU) {
-    const double t = x_wg_sum(acc, sd);
-    if (threadIdx.x == 0) reinterpret_cast<A8_G double*>(gp(ws) + L.part)[blockIdx.x] = t;
+}
+__device__ __forceinline__ void x_st4(float* p, int64_t i, int64_t n, int v4, const float* o) {
+  if (v4) {
+    store4n<float>(p, i, i + 4, o);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (i + e < n) gp(p)[i + e] = o[e];
   }
 }
 
-// Row means of x (or x^2): one wave per row, 4 rows per workgroup.
-__global__ __launch_bounds__(256) void k_ax_rows(const float* __restrict__ x, int sq, int64_t R, int64_t C,
-                                                 float* __restrict__ out, float add) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Element passes: lane t of local workgroup b handles elements 4(b*256 + t) ..
+// +3, striding by the matrix's np workgroups.
+template <int OP>
+__global__ __launch_bounds__(256) void k_ax_el(XT t) {
+  __shared__ double sd[4];
+  int64_t lb;
+  const XK k = x_find<XW_EL>(t, lb);
+  float* ws = k.ws;
+  const XL L = x_layout(k.R, k.C);
+  const float clip = (OP == XE_DIV) ? gp(ws)[L.scal] : 1.0f;
+  const float rmean = (OP == XE_FCU || OP == XE_FU) ? gp(ws)[L.scal + 1] : 1.0f;
+  const float cmean = (OP == XE_FUC) ? gp(ws)[L.scal + 2] : 1.0f;
+  double acc = 0.0;
+  const int64_t stride = (int64_t)k.np * 1024;
+  for (int64_t i = (lb * 256 + threadIdx.x) * 4; i < k.n; i += stride) {
+    float a[4], b[4], o[4];
+    if constexpr (OP == XE_SQB) {
+      x_ld4(k.g, i, k.n, k.v4, a);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (a[e] * a[e]) * k.bv;
+      x_st4(ws + L.xv, i, k.n, k.v4, o);
+    } else if constexpr (OP == XE_V32) {
+      x_ld4(k.g, i, k.n, k.v4, a);
+      if (!k.first) x_ld4(k.v, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float g2 = a[e] * a[e];
+        o[e] = k.first ? g2 * k.bv : lerp_ref(b[e], g2, k.bv);
+      }
+      x_st4(k.v, i, k.n, k.v4, o);
+    } else if constexpr (OP == XE_U) {
+      x_ld4(k.g, i, k.n, k.v4, a);
+      x_ld4(k.v, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = a[e] * rsqrt_ref(fmaxf(b[e], k.eps_sq));
+        if (i + e < k.n) acc += (double)(o[e] * o[e]);
+      }
+      x_st4(k.dst, i, k.n, k.v4, o);
+    } else if constexpr (OP == XE_DIV) {
+      x_ld4(k.dst, i, k.n, k.v4, a);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = a[e] / clip;
+      x_st4(k.dst, i, k.n, k.v4, o);
+    } else if constexpr (OP == XE_M32) {
+      x_ld4(k.m, i, k.n, k.v4, a);
+      x_ld4(k.src, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = lerp_ref(a[e], b[e], k.w1);
+      x_st4(k.m, i, k.n, k.v4, o);
+    } else if constexpr (OP == XE_RES) {
+      x_ld4(ws + L.xu, i, k.n, k.v4, a);
+      x_ld4(k.m, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float r = a[e] - b[e];
+        r = r * r;
+        o[e] = r + k.eps_came;
+      }
+      x_st4(ws + L.xr, i, k.n, k.v4, o);
+      if (k.res) {
+        x_ld4(k.res, i, k.n, k.v4, a);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = lerp_ref(a[e], o[e], k.w3);
+        x_st4(k.res, i, k.n, k.v4, a);
+      }
+    } else if constexpr (OP == XE_UCAME) {
+      x_ld4(k.m, i, k.n, k.v4, a);
+      x_ld4(k.res ? k.res : ws + L.xr, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = a[e] * rsqrt_ref(fmaxf(b[e], k.eps_sq));
+      x_st4(k.u, i, k.n, k.v4, o);
+    } else {   // XE_FCU, XE_FU, XE_FUC: row / column factors, (r, c) stepped from the first element
+      x_ld4(OP == XE_FCU ? k.g : (OP == XE_FU ? k.src : k.m), i, k.n, k.v4, a);
+      int64_t r = i / k.C, c = i - r * k.C;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (i + e < k.n) {
+          if constexpr (OP == XE_FCU) {
+            const float ir = rsqrt_ref(gp(k.rv)[r] / rmean);
+            const float ic = rsqrt_ref(gp(k.cv)[c]);
+            o[e] = (a[e] * ir) * ic;
+            acc += (double)(o[e] * o[e]);
+          } else if constexpr (OP == XE_FU) {
+            const float ve = (gp(k.rv)[r] * gp(k.cv)[c]) / rmean;
+            o[e] = a[e] / (sqrtf(ve) + k.aeps);
+          } else {
+            const float icr = rsqrt_ref(gp(k.cr)[r] / cmean);
+            const float icc = rsqrt_ref(gp(k.cc)[c]);
+            o[e] = (a[e] * icr) * icc;
+          }
+        } else {
+          o[e] = 0.0f;
+        }
+        if (++c == k.C) { c = 0; ++r; }
+      }
+      x_st4(OP == XE_FCU ? k.dst : k.u, i, k.n, k.v4, o);
+    }
+  }
+  if constexpr (OP == XE_U || OP == XE_FCU) {
+    const double s = x_wg_sum(acc, sd);
+    if (threadIdx.x == 0) reinterpret_cast<A8_G double*>(gp(ws) + L.part)[lb] = s;
+  }
+}
+
+// Which vector a row / column pass reads: g_low^2, or the residual.
+enum { XR_GSQ = 0, XR_RES };
+
+template <int SRC>
+__device__ __forceinline__ const float* x_src(const XK& k) {
+  return SRC == XR_GSQ ? k.g : k.ws + x_layout(k.R, k.C).xr;
+}
+
+// Row means of x (or x^2) plus add: one wave per row, 4 rows per workgroup.
+template <int SRC>
+__global__ __launch_bounds__(256) void k_ax_rows(XT t, float add) {
+  int64_t lb;
+  const XK k = x_find<XW_ROWS>(t, lb);
+  const float* x = x_src<SRC>(k);
+  const int64_t row = lb * 4 + (threadIdx.x >> 6);
   const int l = threadIdx.x & 63;
-  if (row >= R) return;
+  if (row >= k.R) return;
   double s = 0.0;
-  for (int64_t j = l; j < C; j += 64) {
-    const float v = gp(x)[row * C + j];
-    s += (double)(sq ? v * v : v);
+  for (int64_t j = l; j < k.C; j += 64) {
+    const float v = gp(x)[row * k.C + j];
+    s += (double)(SRC == XR_GSQ ? v * v : v);
   }
   s = grp_sum_d(s, 64);
-  if (l == 0) gp(out)[row] = (float)s / (float)C + add;
+  if (l == 0) gp(k.ws)[x_layout(k.R, k.C).rowm + row] = (float)s / (float)k.C + add;
 }
 
 // Column sums of x (or x^2) over a chunk of kXRowChunk rows: 64 columns per
 // workgroup, the four waves striding the chunk's rows, combined in order.
-__global__ __launch_bounds__(256) void k_ax_colpart(const float* __restrict__ x, int sq, int64_t R, int64_t C,
-                                                    double* __restrict__ part) {
+template <int SRC>
+__global__ __launch_bounds__(256) void k_ax_colpart(XT t) {
   __shared__ double sd[256];
+  int64_t lb;
+  const XK k = x_find<XW_CPART>(t, lb);
+  const float* x = x_src<SRC>(k);
+  const XL L = x_layout(k.R, k.C);
+  const int64_t ncb = (k.C + 63) / 64;
+  const int64_t by = lb / ncb, bx = lb - by * ncb;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int64_t c = (int64_t)blockIdx.x * 64 + l;
-  const int64_t r0 = (int64_t)blockIdx.y * kXRowChunk;
-  const int64_t r1 = r0 + kXRowChunk < R ? r0 + kXRowChunk : R;
+  const int64_t c = bx * 64 + l;
+  const int64_t r0 = by * kXRowChunk;
+  const int64_t r1 = r0 + kXRowChunk < k.R ? r0 + kXRowChunk : k.R;
   double s = 0.0;
-  if (c < C) {
+  if (c < k.C) {
     for (int64_t r = r0 + w; r < r1; r += 4) {
-      const float v = gp(x)[r * C + c];
-      s += (double)(sq ? v * v : v);
+      const float v = gp(x)[r * k.C + c];
+      s += (double)(SRC == XR_GSQ ? v * v : v);
     }
   }
   sd[threadIdx.x] = s;
   __syncthreads();
-  if (w == 0 && c < C) gp(part)[(int64_t)blockIdx.y * C + c] = ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
+  if (w == 0 && c < k.C)
+    reinterpret_cast<A8_G double*>(gp(k.ws) + L.cpart)[by * k.C + c] =
+        ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
 }
 
-__global__ __launch_bounds__(256) void k_ax_colfin(const double* __restrict__ part, int64_t nch, int64_t R,
-                                                   int64_t C, float* __restrict__ out, float add) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
+__global__ __launch_bounds__(256) void k_ax_colfin(XT t, float add) {
+  int64_t lb;
+  const XK k = x_find<XW_CFIN>(t, lb);
+  const XL L = x_layout(k.R, k.C);
+  const int64_t c = lb * 256 + threadIdx.x;
+  if (c >= k.C) return;
+  const A8_G double* part = reinterpret_cast<const A8_G double*>(gp(k.ws) + L.cpart);
   double s = 0.0;
-  for (int64_t h = 0; h < nch; ++h) s += gp(part)[h * C + c];
-  gp(out)[c] = (float)s / (float)R + add;
+  for (int64_t h = 0; h < L.nch; ++h) s += part[h * k.C + c];
+  gp(k.ws)[L.colm + c] = (float)s / (float)k.R + add;
 }
 
 enum { XV_VAR = 0, XV_CONF };
 
 // Row (index < R) and column (index >= R) vectors of the factorised EMAs.
 template <int OP>
-__global__ __launch_bounds__(256) void k_ax_vec(XK k) {
+__global__ __launch_bounds__(256) void k_ax_vec(XT t) {
+  int64_t lb;
+  const XK k = x_find<XW_VEC>(t, lb);
   const XL L = x_layout(k.R, k.C);
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t j = lb * 256 + threadIdx.x;
   if (j >= k.R + k.C) return;
   const bool row = j < k.R;
-  const int64_t t = row ? j : j - k.R;
-  const float mean = gp(k.ws)[(row ? L.rowm : L.colm) + t];
+  const int64_t i = row ? j : j - k.R;
+  const float mean = gp(k.ws)[(row ? L.rowm : L.colm) + i];
   if constexpr (OP == XV_VAR) {
     float* s = row ? k.rv : k.cv;
-    gp(s)[t] = k.first ? mean * k.bv : __builtin_fmaf(k.bv, mean, gp(s)[t] * k.omb);
+    gp(s)[i] = k.first ? mean * k.bv : __builtin_fmaf(k.bv, mean, gp(s)[i] * k.omb);
   } else {
     float* s = row ? k.cr : k.cc;
-    gp(s)[t] = lerp_ref(gp(s)[t], mean, k.w3);
+    gp(s)[i] = lerp_ref(gp(s)[i], mean, k.w3);
   }
 }
 
 enum { XS_CLIP = 0, XS_RMEAN, XS_RMEAN_CAME, XS_CMEAN };
 
-// One workgroup: the scalars between passes.
+// One workgroup per matrix: the scalars between passes.
 template <int OP>
-__global__ __launch_bounds__(256) void k_ax_s(XK k) {
+__global__ __launch_bounds__(256) void k_ax_s(XT t) {
   __shared__ double sd[4];
+  int64_t lb;
+  const XK k = x_find<XW_ONE>(t, lb);
   float* ws = k.ws;
   const XL L = x_layout(k.R, k.C);
   double s = 0.0;
@@ -250,69 +381,201 @@ __global__ __launch_bounds__(256) void k_ax_s(XK k) {
   }
 }
 
-static unsigned x_grid(int64_t n) {
-  const int64_t nb = (n + 255) / 256;
-  return (unsigned)(nb < kXParts ? (nb > 0 ? nb : 1) : kXParts);
+// Workgroups of an element pass over n elements (4 per lane): at most kXParts,
+// which is also the number of partial sums a reduction leaves.
+static int64_t x_grid(int64_t n) {
+  const int64_t nb = (n + 1023) / 1024;
+  return nb < kXParts ? (nb > 0 ? nb : 1) : kXParts;
+}
+
+// Workgroups of each launch kind for one matrix.
+static void x_counts(const XK& k, int64_t* cnt) {
+  const XL L = x_layout(k.R, k.C);
+  cnt[XW_EL] = x_grid(k.n);
+  cnt[XW_ROWS] = (k.R + 3) / 4;
+  cnt[XW_CPART] = ((k.C + 63) / 64) * L.nch;
+  cnt[XW_CFIN] = (k.C + 255) / 256;
+  cnt[XW_VEC] = (k.R + k.C + 255) / 256;
+  cnt[XW_ONE] = 1;
+}
+
+// A batch of matrices that share every flag and hyper-parameter of the stage:
+// their descriptors (wb filled in), the total grid of each launch kind, the
+// device tables (null for a single matrix), and the arguments.
+struct XB {
+  std::vector<XD> d;
+  std::vector<const a8_apollo_x_args*> a;
+  int64_t total[XW_N];
+  XD* tab_dev;          // n descriptors
+  void* mema_dev;       // m_ema_table_bytes(n)
+  void* vema_dev;       // v_ema_table_bytes(2 n)
+  hipStream_t st;
+};
+
+static XT x_tab(const XB& b) {
+  XT t{};
+  if (b.tab_dev) {
+    t.tab = b.tab_dev;
+    t.ntab = (int)b.d.size();
+  } else {
+    t.one = b.d[0];
+  }
+  return t;
 }
 
 template <int OP>
-static int x_el(const XK& k, hipStream_t st) {
-  hipLaunchKernelGGL((k_ax_el<OP>), dim3(x_grid(k.n)), dim3(256), 0, st, k);
+static int x_el(const XB& b) {
+  hipLaunchKernelGGL((k_ax_el<OP>), dim3((unsigned)b.total[XW_EL]), dim3(256), 0, b.st, x_tab(b));
   return check_launch("k_ax_el");
 }
 
-// Row means into ws.rowm and column means into ws.colm of x (or x^2), plus add.
-static int x_rowcol(const XK& k, const float* x, int sq, float add, hipStream_t st) {
-  const XL L = x_layout(k.R, k.C);
-  hipLaunchKernelGGL(k_ax_rows, dim3((unsigned)((k.R + 3) / 4)), dim3(256), 0, st, x, sq, k.R, k.C, k.ws + L.rowm,
-                     add);
+// Row means into ws.rowm and column means into ws.colm of g_low^2 or the residual, plus add.
+template <int SRC>
+static int x_rowcol(const XB& b, float add) {
+  const XT t = x_tab(b);
+  hipLaunchKernelGGL((k_ax_rows<SRC>), dim3((unsigned)b.total[XW_ROWS]), dim3(256), 0, b.st, t, add);
   int rc = check_launch("k_ax_rows");
   if (rc) return rc;
-  double* cpart = reinterpret_cast<double*>(k.ws + L.cpart);
-  hipLaunchKernelGGL(k_ax_colpart, dim3((unsigned)((k.C + 63) / 64), (unsigned)L.nch), dim3(256), 0, st, x, sq, k.R,
-                     k.C, cpart);
+  hipLaunchKernelGGL((k_ax_colpart<SRC>), dim3((unsigned)b.total[XW_CPART]), dim3(256), 0, b.st, t);
   if ((rc = check_launch("k_ax_colpart"))) return rc;
-  hipLaunchKernelGGL(k_ax_colfin, dim3((unsigned)((k.C + 255) / 256)), dim3(256), 0, st, cpart, L.nch, k.R, k.C,
-                     k.ws + L.colm, add);
+  hipLaunchKernelGGL(k_ax_colfin, dim3((unsigned)b.total[XW_CFIN]), dim3(256), 0, b.st, t, add);
   return check_launch("k_ax_colfin");
 }
 
 template <int OP>
-static int x_vec(const XK& k, hipStream_t st) {
-  hipLaunchKernelGGL((k_ax_vec<OP>), dim3((unsigned)((k.R + k.C + 255) / 256)), dim3(256), 0, st, k);
+static int x_vec(const XB& b) {
+  hipLaunchKernelGGL((k_ax_vec<OP>), dim3((unsigned)b.total[XW_VEC]), dim3(256), 0, b.st, x_tab(b));
   return check_launch("k_ax_vec");
 }
 
 template <int OP>
-static int x_s(const XK& k, hipStream_t st) {
-  hipLaunchKernelGGL((k_ax_s<OP>), dim3(1), dim3(256), 0, st, k);
+static int x_s(const XB& b) {
+  hipLaunchKernelGGL((k_ax_s<OP>), dim3((unsigned)b.total[XW_ONE]), dim3(256), 0, b.st, x_tab(b));
   return check_launch("k_ax_s");
 }
 
 // Clip of U in dst (partials of the preceding U pass) and the division.
-static int x_clip(XK& k, hipStream_t st) {
-  if (!(k.d > 0.0f)) return 0;
-  k.np = (int)x_grid(k.n);
-  int rc = x_s<XS_CLIP>(k, st);
+static int x_clip(const XB& b) {
+  if (!(b.a[0]->d > 0.0f)) return 0;
+  int rc = x_s<XS_CLIP>(b);
   if (rc) return rc;
-  return x_el<XE_DIV>(k, st);
+  return x_el<XE_DIV>(b);
 }
 
-// Momentum EMA of x (n values): fp32 state in place, or codes re-encoded with the
-// lerped values in ws.xm.  Sets k.m.
-static int x_momentum(XK& k, const a8_apollo_x_args* a, const float* x, hipStream_t st) {
-  const XL L = x_layout(k.R, k.C);
-  if (a->m_fp32) {
-    k.m = a->m_fp32;
-    k.src = x;
-    return x_el<XE_M32>(k, st);
+// Re-uploads the descriptors after a change of the per-matrix pointers.
+static int x_sync(XB& b) {
+  if (!b.tab_dev) return 0;
+  if (upload_table(b.tab_dev, b.d.data(), sizeof(XD) * b.d.size(), b.st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  return 0;
+}
+
+// Momentum EMA of x (ws region XU or g_low): fp32 state in place, or codes
+// re-encoded with the lerped values in ws.xm.  Sets each k.m.
+static int x_momentum(XB& b, bool from_u) {
+  const a8_apollo_x_args* a0 = b.a[0];
+  const size_t n = b.d.size();
+  for (size_t i = 0; i < n; ++i) {
+    XK& k = b.d[i].k;
+    k.src = from_u ? k.ws + x_layout(k.R, k.C).xu : k.g;
+    k.m = a0->m_fp32 ? b.a[i]->m_fp32 : k.ws + x_layout(k.R, k.C).xm;
   }
-  k.m = k.ws + L.xm;
-  return a8_m_quantize_lerp(a->m_q, a->m_scale, x, A8_F32, k.m, a->beta1, a->m_block_size, k.n, a->m_bits,
-                            a->m_mode, st);
+  int rc = x_sync(b);
+  if (rc) return rc;
+  if (a0->m_fp32) return x_el<XE_M32>(b);
+  std::vector<MEmaItem> it(n);
+  for (size_t i = 0; i < n; ++i) it[i] = MEmaItem{b.a[i]->m_q, b.a[i]->m_scale, b.d[i].k.src, b.d[i].k.m, b.d[i].k.n};
+  return m_ema_multi(it.data(), (int)n, b.mema_dev, a0->beta1, a0->m_block_size, a0->m_bits, a0->m_mode, b.st);
 }
 
-static int x_run(const a8_apollo_x_args* a, hipStream_t st) {
+static int x_run(XB& b) {
+  const a8_apollo_x_args* a0 = b.a[0];
+  const size_t n = b.d.size();
+  int rc;
+  if (a0->factorize) {
+    if ((rc = x_rowcol<XR_GSQ>(b, 1.17549435e-38f))) return rc;
+    if ((rc = x_vec<XV_VAR>(b))) return rc;
+    if (!a0->came) {
+      if ((rc = x_s<XS_RMEAN>(b))) return rc;
+      if (a0->has_m) {
+        if ((rc = x_momentum(b, false))) return rc;
+        for (auto& e : b.d) e.k.src = e.k.m;
+      } else {
+        for (auto& e : b.d) e.k.src = e.k.g;
+      }
+      if ((rc = x_sync(b))) return rc;
+      return x_el<XE_FU>(b);
+    }
+    if ((rc = x_s<XS_RMEAN_CAME>(b))) return rc;
+    if ((rc = x_el<XE_FCU>(b))) return rc;
+    if ((rc = x_clip(b))) return rc;
+    if ((rc = x_momentum(b, true))) return rc;
+    if ((rc = x_el<XE_RES>(b))) return rc;
+    if ((rc = x_rowcol<XR_RES>(b, 0.0f))) return rc;
+    if (a0->c_bits) {
+      std::vector<VEmaItem> it(2 * n);
+      for (size_t i = 0; i < n; ++i) {
+        const a8_apollo_x_args* a = b.a[i];
+        const XK& k = b.d[i].k;
+        const XL L = x_layout(k.R, k.C);
+        it[2 * i] = VEmaItem{a->crow_q, a->crow_scale, a->crow_min_log, k.ws + L.rowm, k.ws + L.crow, nullptr, k.R};
+        it[2 * i + 1] = VEmaItem{a->ccol_q, a->ccol_scale, a->ccol_min_log, k.ws + L.colm, k.ws + L.ccol, nullptr,
+                                 k.C};
+      }
+      if ((rc = v_ema_multi(it.data(), (int)(2 * n), b.vema_dev, 1.0 - a0->beta3, a0->block_size, 0, 0.0f,
+                            -126.0f, a0->c_bits, b.st)))
+        return rc;
+    } else if ((rc = x_vec<XV_CONF>(b))) {
+      return rc;
+    }
+    if ((rc = x_s<XS_CMEAN>(b))) return rc;
+    return x_el<XE_FUC>(b);
+  }
+  // non-factorised CAME: low-rank V
+  if (a0->v_bits) {
+    std::vector<VEmaItem> it(n);
+    for (size_t i = 0; i < n; ++i) {
+      const a8_apollo_x_args* a = b.a[i];
+      const XK& k = b.d[i].k;
+      it[i] = a0->first_step ? VEmaItem{a->v_q, a->v_scale, a->v_min_log, k.v, nullptr, nullptr, k.n}
+                             : VEmaItem{a->v_q, a->v_scale, a->v_min_log, k.g, k.v, nullptr, k.n};
+    }
+    if (a0->first_step) {
+      if ((rc = x_el<XE_SQB>(b))) return rc;
+      if ((rc = v_ema_multi(it.data(), (int)n, b.vema_dev, 1.0, a0->block_size, 0, 0.0f, -126.0f, a0->v_bits,
+                            b.st)))
+        return rc;
+    } else if ((rc = v_ema_multi(it.data(), (int)n, b.vema_dev, a0->beta_v, a0->block_size, 1, 0.0f, a0->log_floor,
+                                 a0->v_bits, b.st))) {
+      return rc;
+    }
+  } else if ((rc = x_el<XE_V32>(b))) {
+    return rc;
+  }
+  if ((rc = x_el<XE_U>(b))) return rc;
+  if ((rc = x_clip(b))) return rc;
+  if (!a0->has_m) return 0;   // unreachable through the optimizer (beta3 needs beta1): u = clipped U
+  if ((rc = x_momentum(b, true))) return rc;
+  if ((rc = x_el<XE_RES>(b))) return rc;
+  if (a0->c_bits) {
+    // the residual EMA is read back decoded after its re-encode (optimizer.py:2857-2866)
+    std::vector<VEmaItem> it(n);
+    for (size_t i = 0; i < n; ++i) {
+      const a8_apollo_x_args* a = b.a[i];
+      const XK& k = b.d[i].k;
+      float* xr = k.ws + x_layout(k.R, k.C).xr;
+      it[i] = VEmaItem{a->res_q, a->res_scale, a->res_min_log, xr, nullptr, xr, k.n};
+    }
+    char* vt = b.vema_dev ? static_cast<char*>(b.vema_dev) + v_ema_table_bytes((int)n) : nullptr;
+    if ((rc = v_ema_multi(it.data(), (int)n, vt, 1.0 - a0->beta3, a0->block_size, 0, 0.0f, -126.0f, a0->c_bits,
+                          b.st)))
+      return rc;
+  }
+  return x_el<XE_UCAME>(b);
+}
+
+// The stage's descriptor of one matrix.
+static XK x_desc(const a8_apollo_x_args* a) {
   const int64_t R = a->rows_low, C = a->cols_low;
   const XL L = x_layout(R, C);
   XK k{};
@@ -323,93 +586,27 @@ static int x_run(const a8_apollo_x_args* a, hipStream_t st) {
   k.aeps = a->apollo_eps; k.eps_sq = a->eps_sq; k.eps_came = a->eps_came; k.d = a->d;
   k.sqn = (float)sqrt((double)L.n);
   k.first = a->first_step ? 1 : 0;
-  int rc;
+  k.np = (int)x_grid(L.n);
+  k.dst = a->xws + L.xu;
   if (a->factorize) {
     k.rv = a->row_var; k.cv = a->col_var;
-    if ((rc = x_rowcol(k, a->g_low, 1, 1.17549435e-38f, st))) return rc;
-    if ((rc = x_vec<XV_VAR>(k, st))) return rc;
-    if (!a->came) {
-      if ((rc = x_s<XS_RMEAN>(k, st))) return rc;
-      k.src = a->g_low;
-      if (a->has_m) {
-        if ((rc = x_momentum(k, a, a->g_low, st))) return rc;
-        k.src = k.m;
-      }
-      return x_el<XE_FU>(k, st);
-    }
-    if ((rc = x_s<XS_RMEAN_CAME>(k, st))) return rc;
-    k.dst = k.ws + L.xu;
-    if ((rc = x_el<XE_FCU>(k, st))) return rc;
-    if ((rc = x_clip(k, st))) return rc;
-    if ((rc = x_momentum(k, a, k.ws + L.xu, st))) return rc;
-    k.res = nullptr;
-    if ((rc = x_el<XE_RES>(k, st))) return rc;
-    if ((rc = x_rowcol(k, k.ws + L.xr, 0, 0.0f, st))) return rc;
-    if (a->c_bits) {
-      if ((rc = a8_log_quantize_lerp(a->crow_q, a->crow_scale, a->crow_min_log, k.ws + L.rowm, A8_F32, k.ws + L.crow,
-                                     1.0 - a->beta3, a->block_size, 0, 0.0f, R, -126.0f, a->c_bits, st)))
-        return rc;
-      if ((rc = a8_log_quantize_lerp(a->ccol_q, a->ccol_scale, a->ccol_min_log, k.ws + L.colm, A8_F32, k.ws + L.ccol,
-                                     1.0 - a->beta3, a->block_size, 0, 0.0f, C, -126.0f, a->c_bits, st)))
-        return rc;
-      k.cr = k.ws + L.crow; k.cc = k.ws + L.ccol;
-    } else {
-      k.cr = a->crow_fp32; k.cc = a->ccol_fp32;
-      if ((rc = x_vec<XV_CONF>(k, st))) return rc;
-    }
-    if ((rc = x_s<XS_CMEAN>(k, st))) return rc;
-    return x_el<XE_FUC>(k, st);
-  }
-  // non-factorised CAME: low-rank V
-  if (a->v_bits) {
-    k.v = k.ws + L.xv;
-    if (a->first_step) {
-      if ((rc = x_el<XE_SQB>(k, st))) return rc;
-      if ((rc = a8_log_quantize_lerp(a->v_q, a->v_scale, a->v_min_log, k.v, A8_F32, nullptr, 1.0, a->block_size, 0,
-                                     0.0f, L.n, -126.0f, a->v_bits, st)))
-        return rc;
-    } else if ((rc = a8_log_quantize_lerp(a->v_q, a->v_scale, a->v_min_log, a->g_low, A8_F32, k.v, a->beta_v,
-                                          a->block_size, 1, 0.0f, L.n, a->log_floor, a->v_bits, st))) {
-      return rc;
+    if (a->came) {
+      k.cr = a->c_bits ? a->xws + L.crow : a->crow_fp32;
+      k.cc = a->c_bits ? a->xws + L.ccol : a->ccol_fp32;
     }
   } else {
-    k.v = a->v_fp32;
-    if ((rc = x_el<XE_V32>(k, st))) return rc;
+    k.v = a->v_bits ? a->xws + L.xv : a->v_fp32;
+    k.res = a->c_bits ? nullptr : a->res_fp32;
+    if (!a->has_m) k.dst = a->u;
   }
-  if (!a->has_m) {   // unreachable through the optimizer (beta3 needs beta1); u = clipped U
-    k.dst = a->u;
-    if ((rc = x_el<XE_U>(k, st))) return rc;
-    return x_clip(k, st);
-  }
-  k.dst = k.ws + L.xu;
-  if ((rc = x_el<XE_U>(k, st))) return rc;
-  if ((rc = x_clip(k, st))) return rc;
-  if ((rc = x_momentum(k, a, k.ws + L.xu, st))) return rc;
-  k.res = a->c_bits ? nullptr : a->res_fp32;
-  if ((rc = x_el<XE_RES>(k, st))) return rc;
-  if (a->c_bits) {
-    if ((rc = a8_log_quantize_lerp(a->res_q, a->res_scale, a->res_min_log, k.ws + L.xr, A8_F32, nullptr,
-                                   1.0 - a->beta3, a->block_size, 0, 0.0f, L.n, -126.0f, a->c_bits, st)))
-      return rc;
-    if ((rc = a8_dequantize_log_nonneg(k.ws + L.xr, a->res_q, a->res_scale, a->res_min_log, L.n, a->block_size,
-                                       a->c_bits, st)))
-      return rc;
-  }
-  return x_el<XE_UCAME>(k, st);
+  const void* streams[] = {a->g_low, a->u, a->v_fp32, a->m_fp32, a->res_fp32};
+  bool al = (L.n & 3) == 0;
+  for (const void* p : streams) al = al && aligned16(p);   // aligned16(nullptr) holds
+  k.v4 = al ? 1 : 0;
+  return k;
 }
 
-}  // namespace a8
-
-using namespace a8;
-
-extern "C" {
-
-int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low) {
-  if (rows_low <= 0 || cols_low <= 0) return 0;
-  return x_layout(rows_low, cols_low).total;
-}
-
-int a8_apollo_lowrank_x(const a8_apollo_x_args* a, void* stream) {
+static int x_check(const a8_apollo_x_args* a) {
   if (!a) return set_error(A8_ERR_ARG, "null pointer");
   if (a->rows_low <= 0 || a->cols_low <= 0) return set_error(A8_ERR_SIZE, "empty low-rank matrix");
   if (a->rows_low * a->cols_low >= ((int64_t)1 << 31)) return set_error(A8_ERR_SIZE, "low-rank matrix too large");
@@ -444,7 +641,98 @@ int a8_apollo_lowrank_x(const a8_apollo_x_args* a, void* stream) {
     if (a->came && (a->c_bits ? !(a->res_q && a->res_scale && a->res_min_log) : !a->res_fp32))
       return set_error(A8_ERR_ARG, "residual state missing");
   }
-  return x_run(a, (hipStream_t)stream);
+  return 0;
+}
+
+// Two matrices can share the stage's launches when every flag and
+// hyper-parameter agrees.
+static bool x_same(const a8_apollo_x_args* a, const a8_apollo_x_args* b) {
+  return a->factorize == b->factorize && a->came == b->came && a->has_m == b->has_m &&
+         a->first_step == b->first_step && (a->factorize || a->v_bits == b->v_bits) &&
+         a->block_size == b->block_size && (a->m_fp32 == nullptr) == (b->m_fp32 == nullptr) &&
+         a->m_bits == b->m_bits && a->m_mode == b->m_mode && a->m_block_size == b->m_block_size &&
+         a->c_bits == b->c_bits && a->beta_v == b->beta_v && a->beta1 == b->beta1 && a->beta3 == b->beta3 &&
+         a->apollo_eps == b->apollo_eps && a->eps_sq == b->eps_sq && a->log_floor == b->log_floor &&
+         a->eps_came == b->eps_came && a->d == b->d;
+}
+
+// Table bytes of one batch of n matrices: descriptors, momentum and AL tables.
+static int64_t x_round(int64_t b) { return (b + 255) / 256 * 256; }
+static int64_t x_bytes(int n) {
+  return x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) + x_round(v_ema_table_bytes(2 * n));
+}
+
+}  // namespace a8
+
+using namespace a8;
+
+extern "C" {
+
+int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low) {
+  if (rows_low <= 0 || cols_low <= 0) return 0;
+  return x_layout(rows_low, cols_low).total;
+}
+
+int64_t a8_apollo_x_table_bytes(int nmat) { return nmat > 0 ? x_bytes(nmat) : 0; }
+
+int a8_apollo_lowrank_x(const a8_apollo_x_args* a, void* stream) {
+  int rc = x_check(a);
+  if (rc) return rc;
+  XB b{};
+  b.d.resize(1);
+  b.a.push_back(a);
+  b.d[0].k = x_desc(a);
+  x_counts(b.d[0].k, b.total);
+  b.st = (hipStream_t)stream;
+  return x_run(b);
+}
+
+int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* table_dev, int64_t table_bytes,
+                              void* stream) {
+  if (nmat <= 0) return 0;
+  if (!args) return set_error(A8_ERR_ARG, "null pointer");
+  if (!table_dev || table_bytes < x_bytes(nmat))
+    return set_error(A8_ERR_SIZE, "table_dev too small: need a8_apollo_x_table_bytes(nmat)");
+  for (int i = 0; i < nmat; ++i) {
+    const int rc = x_check(args + i);
+    if (rc) return rc;
+  }
+  // batches of matrices that agree on every flag, in order of first appearance;
+  // each takes its own slice of the table
+  std::vector<int> batch_of((size_t)nmat, -1);
+  char* base = static_cast<char*>(table_dev);
+  for (int i = 0; i < nmat; ++i) {
+    if (batch_of[(size_t)i] >= 0) continue;
+    XB b{};
+    b.st = (hipStream_t)stream;
+    for (int j = i; j < nmat; ++j) {
+      if (batch_of[(size_t)j] >= 0 || !x_same(args + i, args + j)) continue;
+      batch_of[(size_t)j] = i;
+      b.a.push_back(args + j);
+    }
+    const int n = (int)b.a.size();
+    b.d.resize((size_t)n);
+    for (int e = 0; e < XW_N; ++e) b.total[e] = 0;
+    for (int j = 0; j < n; ++j) {
+      b.d[(size_t)j].k = x_desc(b.a[(size_t)j]);
+      int64_t cnt[XW_N];
+      x_counts(b.d[(size_t)j].k, cnt);
+      for (int e = 0; e < XW_N; ++e) {
+        b.d[(size_t)j].wb[e] = b.total[e];
+        b.total[e] += cnt[e];
+      }
+    }
+    for (int e = 0; e < XW_N; ++e)
+      if (b.total[e] > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "low-rank batch too large");
+    b.tab_dev = reinterpret_cast<XD*>(base);
+    b.mema_dev = base + x_round((int64_t)sizeof(XD) * n);
+    b.vema_dev = static_cast<char*>(b.mema_dev) + x_round(m_ema_table_bytes(n));
+    base += x_bytes(n);
+    int rc = x_sync(b);
+    if (rc) return rc;
+    if ((rc = x_run(b))) return rc;
+  }
+  return 0;
 }
 
 }  // extern "C"

@@ -30,14 +30,17 @@ namespace a8 {
 constexpr int kPElems = 2048;
 
 // ============================================================ V EMA
+// One 2048-element unit (unit index bid) of the EMA; xw: 8 floats of LDS.  dec,
+// when given, receives the decoded new codes (what dequantize_log_nonneg would
+// read back).
 template <int VB, typename T>
-__global__ __launch_bounds__(256) void k_vema(void* __restrict__ q, float* __restrict__ scale,
-                                              float* __restrict__ min_log, const T* __restrict__ x,
-                                              float* __restrict__ out, int64_t n, int64_t nblk, int lbv, float w,
-                                              int square, float eps1, float floor_) {
-  __shared__ float xw[8];
+__device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restrict__ scale,
+                                          float* __restrict__ min_log, const T* __restrict__ x,
+                                          float* __restrict__ out, float* __restrict__ dec, int64_t n, int64_t nblk,
+                                          int64_t bid, int lbv, float w, int square, float eps1, float floor_,
+                                          float* xw) {
   const int lane = threadIdx.x, wave = lane >> 6;
-  const int64_t e0 = (int64_t)blockIdx.x * kPElems + (int64_t)lane * 8;
+  const int64_t e0 = bid * kPElems + (int64_t)lane * 8;
   const int VL = (1 << lbv) >> 3;
   const int64_t vb = e0 >> lbv;
   const bool v_ok = vb < nblk;
@@ -88,13 +91,55 @@ __global__ __launch_bounds__(256) void k_vema(void* __restrict__ q, float* __res
   const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
   constexpr int L2 = VB == 8 ? 254 : 65534;
   const ALFit f = al_refit(bmax, mnz, floor_, (float)L2);
+  float dv[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const uint32_t code = al_finish<L2>(v[k], al_round_exact<L2>(v[k], f));
     if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[e0 + k] = (uint8_t)code;
     else gp(reinterpret_cast<uint16_t*>(q))[e0 + k] = (uint16_t)code;
+    dv[k] = code ? exp2_exact(((float)(code - 1) * f.s) / LM2 + f.lmin) : 0.0f;
   }
+  if (dec) store8<float>(dec, e0, n, dv);
   if ((lane & (VL - 1)) == 0) { gp(scale)[vb] = f.s; gp(min_log)[vb] = f.lmin; }
+}
+
+template <int VB, typename T>
+__global__ __launch_bounds__(256) void k_vema(void* __restrict__ q, float* __restrict__ scale,
+                                              float* __restrict__ min_log, const T* __restrict__ x,
+                                              float* __restrict__ out, int64_t n, int64_t nblk, int lbv, float w,
+                                              int square, float eps1, float floor_) {
+  __shared__ float xw[8];
+  vema_unit<VB, T>(q, scale, min_log, x, out, nullptr, n, nblk, (int64_t)blockIdx.x, lbv, w, square, eps1, floor_,
+                   xw);
+}
+
+// Table form: one launch over several tensors, each a run of whole units.
+struct VemaDesc {
+  void* q;
+  float* scale;
+  float* min_log;
+  const float* x;
+  float* out;
+  float* dec;
+  int64_t n, nblk, wg_begin;
+};
+
+template <int VB>
+__global__ __launch_bounds__(256) void k_vema_multi(VemaDesc one, const VemaDesc* __restrict__ tab, int ntab,
+                                                    int lbv, float w, int square, float eps1, float floor_) {
+  __shared__ float xw[8];
+  const int64_t wg = blockIdx.x;
+  int lo = 0;
+  if (tab) {
+    int hi = ntab - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    }
+  }
+  const VemaDesc d = tab ? tab[lo] : one;
+  vema_unit<VB, float>(d.q, d.scale, d.min_log, d.x, d.out, d.dec, d.n, d.nblk, wg - d.wg_begin, lbv, w, square,
+                       eps1, floor_, xw);
 }
 
 // ============================================================ factored element kernel
@@ -436,6 +481,53 @@ static void launch_f2d_t(int op, unsigned nwg, hipStream_t st, const F2& a) {
     case F_CAME2N: hipLaunchKernelGGL((k_f2d<T, F_CAME2N>), dim3(nwg), dim3(256), 0, st, a); break;
     default: hipLaunchKernelGGL((k_f2d<T, F_CAME2>), dim3(nwg), dim3(256), 0, st, a); break;
   }
+}
+
+int64_t v_ema_table_bytes(int n) { return (int64_t)sizeof(VemaDesc) * (int64_t)n; }
+
+int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_size, int square, float eps1,
+                float log_floor, int v_bits, hipStream_t st) {
+  if (n <= 0) return 0;
+  if (!table_dev && n > 1) {   // no table: one launch per tensor
+    for (int i = 0; i < n; ++i) {
+      const int rc = v_ema_multi(it + i, 1, nullptr, w, block_size, square, eps1, log_floor, v_bits, st);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  if (v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
+  int lbv;
+  int rc = lb_of(block_size, 128, kPElems, lbv, "block_size");
+  if (rc) return rc;
+  std::vector<VemaDesc> tab((size_t)n);
+  int64_t wg = 0;
+  for (int i = 0; i < n; ++i) {
+    const VEmaItem& t = it[i];
+    if (!t.q || !t.scale || !t.min_log || !t.x) return set_error(A8_ERR_ARG, "null AL state");
+    if (!aligned16(t.x) || (t.out && !aligned16(t.out)) || (t.dec && !aligned16(t.dec)))
+      return set_error(A8_ERR_ALIGN, "AL EMA input and outputs must be 16-byte aligned");
+    VemaDesc& D = tab[(size_t)i];
+    D.q = t.q; D.scale = t.scale; D.min_log = t.min_log; D.x = t.x; D.out = t.out; D.dec = t.dec; D.n = t.n;
+    D.nblk = (t.n + block_size - 1) / block_size;
+    D.wg_begin = wg;
+    wg += (D.nblk * block_size + kPElems - 1) / kPElems;
+  }
+  if (wg == 0) return 0;
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "AL EMA: too many elements");
+  const VemaDesc* dt = nullptr;
+  if (table_dev) {
+    if (upload_table(table_dev, tab.data(), sizeof(VemaDesc) * (size_t)n, st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "table upload failed");
+    dt = reinterpret_cast<const VemaDesc*>(table_dev);
+  }
+  const VemaDesc one = tab[0];
+  if (v_bits == 8)
+    hipLaunchKernelGGL(k_vema_multi<8>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
+                       eps1, log_floor);
+  else
+    hipLaunchKernelGGL(k_vema_multi<16>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
+                       eps1, log_floor);
+  return check_launch("k_vema_multi");
 }
 
 }  // namespace a8

@@ -211,6 +211,44 @@ static int block_log2(int bs, int& lb) {
 
 hipError_t sgd_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
 
+int64_t m_ema_table_bytes(int n) { return (int64_t)sizeof(SgdDesc) * (int64_t)n; }
+
+// The standalone momentum EMA over n tensors in one launch (the table form of
+// a8_m_quantize_lerp).  table_dev: m_ema_table_bytes(n) of device memory, or null
+// for one launch per tensor (the descriptor then travels as a kernel argument).
+int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int block_size, int m_bits, int m_mode,
+                hipStream_t st) {
+  if (n <= 0) return 0;
+  if (!table_dev && n > 1) {   // no table: one launch per tensor
+    for (int i = 0; i < n; ++i) {
+      const int rc = m_ema_multi(it + i, 1, nullptr, beta, block_size, m_bits, m_mode, st);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  SgdHyp h{};
+  int rc = m_codec(m_bits, m_mode, h.mk);
+  if (rc) return rc;
+  if ((rc = block_log2(block_size, h.lbm))) return rc;
+  h.w_m = (float)(1.0 - beta);
+  std::vector<SgdDesc> tab((size_t)n);
+  int64_t wg = 0;
+  for (int i = 0; i < n; ++i) {
+    if (!it[i].m_q || !it[i].m_scale || !it[i].x) return set_error(A8_ERR_ARG, "null momentum state");
+    if (!aligned16(it[i].x) || !aligned16(it[i].m_q) || (it[i].out && !aligned16(it[i].out)))
+      return set_error(A8_ERR_ALIGN, "momentum codes, input and output must be 16-byte aligned");
+    SgdDesc& D = tab[(size_t)i];
+    D.grad = it[i].x; D.m_q = it[i].m_q; D.m_scale = it[i].m_scale; D.m_out = it[i].out; D.numel = it[i].n;
+    D.wg_begin = wg;
+    wg += (it[i].n + kSElems - 1) / kSElems;
+  }
+  if (!table_dev) return launch_sgd(A8_F32, 0, 3, 1, wg, st, tab[0], nullptr, 0, h);
+  if (upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)n, st) != hipSuccess)
+    return set_error(A8_ERR_HIP, "table upload failed");
+  SgdDesc none{};
+  return launch_sgd(A8_F32, 0, 3, 1, wg, st, none, reinterpret_cast<const SgdDesc*>(table_dev), n, h);
+}
+
 }  // namespace a8
 
 using namespace a8;

@@ -29,6 +29,9 @@ For those the roofline is the whole step's algorithmic bytes over its GPU time
 (HIP events around each step); adafactor and came are timed, like the headline,
 eagerly and then as graph replays of one captured ``step()`` (``value`` from the
 replays), apollo eagerly; apollo also reports the projection's flops.
+``apollo_factorize`` and ``apollo_came`` time C4 with the factorised (row /
+column low-rank second moment) and CAME (beta3 0.9999, RMS clip d=1) low-rank
+stages; their roofline counts C4's bytes only (a lower bound).
 """
 import argparse
 import json
@@ -102,6 +105,10 @@ APOLLO = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=Fal
               stochastic_round_writeback=True)
 
 
+APOLLO_VARIANTS = {"apollo": APOLLO, "apollo_factorize": dict(APOLLO, apollo_factorize=True),
+                   "apollo_came": dict(APOLLO, beta3=0.9999, d=1.0, eps_came=1e-16)}
+
+
 def apollo_step_bytes_flops(shapes, rank=256, bs=2048, mbs=256):
     """Algorithmic bytes and projection flops of one APOLLO step (C4, bf16).
     Per matrix element: g read by the projection and by the writeback, p read
@@ -141,7 +148,7 @@ def factored_step_bytes(shapes, workload):
 
 
 def make_grad(kind, shape, gen, dev, i, embed):
-    if kind == "apollo":
+    if kind.startswith("apollo"):
         return torch.randn(shape, device=dev, generator=gen) * 1e-3
     if kind == "adamw":
         g = torch.randn(shape, device=dev, generator=gen) * 1e-3
@@ -183,8 +190,9 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
         shape, gk, kw = (2048, 2048), "student_t", dict(ADAFACTOR)
     elif workload == "came":
         shape, gk, kw = (2048, 2048), "logscale", dict(CAME)
-    elif workload == "apollo":
-        shape, pdt, kw = (2048, 2048), torch.bfloat16, dict(APOLLO, stochastic_round_writeback=False)
+    elif workload.startswith("apollo"):
+        shape, pdt = (2048, 2048), torch.bfloat16
+        kw = dict(APOLLO_VARIANTS[workload], stochastic_round_writeback=False)
     p = torch.nn.Parameter(make_param(shape, 0, 0).to(pdt))
     opt = F.OracleOptimizer([p], **kw)
     zf = 0.02 if workload == "adamw_llama3_8b" else 0.05
@@ -209,7 +217,9 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
             "adamw_llama3_8b": "C5: one 4096x14336 fp32 AdamW UF8/AL8 step (Student-t grads)",
             "adafactor": "C2: one 2048x2048 fp32 factored Adafactor AL8 step",
             "came": "C3: one 2048x2048 fp32 CAME UF8/AL16/AL16+Fira step",
-            "apollo": "C4: one 2048x2048 bf16 APOLLO r=256 UF8/AL8 step (deterministic writeback)"}[workload]
+            "apollo": "C4: one 2048x2048 bf16 APOLLO r=256 UF8/AL8 step (deterministic writeback)",
+            "apollo_factorize": "one 2048x2048 bf16 factorised APOLLO r=256 step (deterministic writeback)",
+            "apollo_came": "one 2048x2048 bf16 CAME APOLLO r=256 step (deterministic writeback)"}[workload]
     return {"value": n / med, "unit": "params/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{what}, median of {len(times)} after 1 warm-up", "ms_per_step": med * 1e3}
 
@@ -223,7 +233,8 @@ def main():
     ap.add_argument("--calib", action="store_true",
                     help="after timing, run a plain 256 MiB fp32 copy (for counter calibration)")
     ap.add_argument("--workload", default="adamw",
-                    choices=["adamw", "adafactor", "came", "apollo", "adamw_llama3_8b"],
+                    choices=["adamw", "adafactor", "came", "apollo", "adamw_llama3_8b", "apollo_factorize",
+                             "apollo_came"],
                     help="adamw (default, the headline metric), adafactor (C2), came (C3), apollo (C4) or "
                          "adamw_llama3_8b (C5)")
     args = ap.parse_args()
@@ -241,7 +252,7 @@ def main():
     params = []
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    pdt = torch.bfloat16 if args.workload == "apollo" else torch.float32
+    pdt = torch.bfloat16 if args.workload.startswith("apollo") else torch.float32
     for i, s in enumerate(shapes):
         if len(s) == 1:
             p = torch.ones(s, device=dev)
@@ -350,11 +361,12 @@ def main():
 
 
 def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
-    kw = {"adafactor": ADAFACTOR, "came": CAME, "apollo": APOLLO}[args.workload]
+    apollo = args.workload.startswith("apollo")
+    kw = APOLLO_VARIANTS[args.workload] if apollo else {"adafactor": ADAFACTOR, "came": CAME}[args.workload]
     # adafactor / came run capturable (device step count): timed eagerly, then as
     # replays of one captured step; APOLLO forms per-step scalars on the host and
     # runs eagerly only
-    graphable = args.workload != "apollo"
+    graphable = not apollo
     opt = Adafactor8Bit(params, **(dict(kw, capturable=True) if graphable else kw))
     for _ in range(args.warmup):
         opt.step()
@@ -388,14 +400,15 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
         ms, gms = timed(graph.replay)
         mode = "graph replay of one captured step() (capturable=True)"
     flops = None
-    if args.workload == "apollo":
+    if apollo:
         nbytes, flops = apollo_step_bytes_flops(shapes)
     else:
         nbytes = factored_step_bytes(shapes, args.workload)
     achieved = nbytes / (gms * 1e-3) / 1e9
     name = {"adafactor": "adafactor_factored_al8_bv256", "came": "came_uf8_al16_al16_fira_bv2048",
-            "apollo": "apollo_r256_uf8_al8_sr"}[args.workload]
-    dt = "bf16" if args.workload == "apollo" else "fp32"
+            "apollo": "apollo_r256_uf8_al8_sr", "apollo_factorize": "apollo_factorize_r256_uf8_sr",
+            "apollo_came": "apollo_came_r256_uf8_al8_sr"}[args.workload]
+    dt = "bf16" if apollo else "fp32"
     out = {
         "metric": "fused step params/sec + achieved HBM GB/s (% of peak), " + args.workload + " @1.1B params",
         "value": nparams / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,

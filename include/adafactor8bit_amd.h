@@ -445,6 +445,15 @@ typedef struct a8_apollo_x_args {
 int a8_apollo_lowrank_x(const a8_apollo_x_args* args, void* stream);
 int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low);
 
+/* The same stage for nmat matrices at once (the reference steps them one by one
+ * in _update_param_apollo, optimizer.py:2587-3084): matrices that agree on every
+ * flag and hyper-parameter of their records share one launch per pass, over a
+ * descriptor table in table_dev (a8_apollo_x_table_bytes(nmat) bytes of device
+ * memory, written on the stream).  Each record needs its own xws. */
+int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* table_dev, int64_t table_bytes,
+                              void* stream);
+int64_t a8_apollo_x_table_bytes(int nmat);
+
 /* Replaces dequantize_log_nonneg (kernels.cu:2593-2632; called by
  * _log_dequantize_nonneg, optimizer.py:328-338): output[i] = 0 for code 0, else
  * 2^(((q-1) * scale[b]) / (L-2) + min_log[b]) with b = i / block_size, L = 256

@@ -585,3 +585,67 @@ def test_apollo_c4_rank256_sr_writeback_bits(shape, det_proj):
         want = sr.sr_round_bf16(x.astype(np.float32), seed=int(st["sr_seed"]), step=int(st["step"]))
         got = _t2np(p).reshape(-1).view(np.uint16)
         assert np.array_equal(got, want), f"step {t}: {(got != want).mean():.2e} differ"
+
+
+# Factorised and CAME APOLLO over a group of matrices of several shapes (right
+# and left side, ragged widths).  The optimizer runs the low-rank stage of the
+# whole group as one launch per pass (a8_apollo_lowrank_x_multi); the same steps
+# through the one-matrix entry point (a8_apollo_lowrank_x, per matrix, in
+# order) must give the same bits, since every reduction stays inside its matrix.
+X_SHAPES = [(300, 200), (96, 260), (513, 40), (64, 1030), (200, 300), (700, 129)]
+X_VARIANTS = {
+    "fact_uf8": dict(apollo_factorize=True),
+    "fact_nomom": dict(apollo_factorize=True, beta1=None, beta2=None, beta2_decay=-0.8, d=1.0),
+    "came_al8_clip": dict(beta3=0.9999, d=1.0, eps_came=1e-16),
+    "came_al16_uf4": dict(beta3=0.99, d=1.0, eps_came=1e-16, v_quant_type="al16", c_quant_type="al16",
+                          m_quant_type="uf4"),
+    "came_fp32": dict(beta3=0.9999, d=1.0, eps_came=1e-16, quantize=False),
+    "fact_came_al8": dict(apollo_factorize=True, beta3=0.9999, d=1.0, eps_came=1e-16),
+    "fact_came_fp32": dict(apollo_factorize=True, beta3=0.999, d=1.0, eps_came=1e-16, quantize=False),
+}
+
+
+def _per_matrix_stage(L):
+    import ctypes
+    from adafactor8bit import _native as nat
+
+    def run(xarr, n, tab, nbytes, stream):
+        recs = ctypes.cast(xarr, ctypes.POINTER(nat.ApolloXArgs))
+        for i in range(n):
+            rc = L.a8_apollo_lowrank_x(ctypes.byref(recs[i]), stream)
+            if rc:
+                return rc
+        return 0
+    return run
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", sorted(X_VARIANTS))
+@pytest.mark.parametrize("rank", [32, 5])
+def test_apollo_x_batched_equals_per_matrix(variant, rank, det_proj):
+    from adafactor8bit import Adafactor8Bit
+    from adafactor8bit import _native as nat
+    print(f"[apollo x batched] {variant} rank={rank}", flush=True)
+    kw = dict(_apollo_kw(apollo_rank=rank, apollo_scale_type="channel"), **X_VARIANTS[variant])
+    init = [inputs.make_param(s, i, 31) for i, s in enumerate(X_SHAPES)]
+    runs = []
+    for batched in (True, False):
+        with pytest.MonkeyPatch.context() as mp:
+            L = nat.lib()
+            if not batched:
+                mp.setattr(L, "a8_apollo_lowrank_x_multi", _per_matrix_stage(L))
+            params = [torch.nn.Parameter(x.clone().cuda()) for x in init]
+            opt = Adafactor8Bit(params, **kw)
+            for t in range(1, 4):
+                for i, p in enumerate(params):
+                    p.grad = inputs.make_grad(X_SHAPES[i], i, t, 31, kind="student_t").cuda()
+                opt.step()
+            torch.cuda.synchronize()
+        runs.append((params, opt))
+    (pa, oa), (pb, ob) = runs
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert torch.equal(a.detach(), b.detach()), f"{variant} p{i}: parameters differ"
+        sa, sb = oa.state[a], ob.state[b]
+        for k, v in sa.items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, sb[k]), f"{variant} p{i}: state {k} differs"

@@ -867,17 +867,18 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
     constexpr int LM2 = VB == 8 ? 254 : 65534;
     const ALFit f = al_refit(bmax, mnz, floor_, (float)LM2);
     if (v_ok) {
+      uint32_t code[8];
+      al_codes<LM2, 8>(v, f, code);
       if constexpr (FULL && VB == 8) {
         uint32_t cw[2] = {0u, 0u};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) cw[k >> 2] |= al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f)) << (8 * (k & 3));
+        for (int k = 0; k < 8; ++k) cw[k >> 2] |= code[k] << (8 * (k & 3));
         *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(D.v_q) + e0)) = u32x2{cw[0], cw[1]};
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const uint32_t code = al_finish<LM2>(v[k], al_round_exact<LM2>(v[k], f));
-          if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(D.v_q))[e0 + k] = (uint8_t)code;
-          else gp(reinterpret_cast<uint16_t*>(D.v_q))[e0 + k] = (uint16_t)code;
+          if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(D.v_q))[e0 + k] = (uint8_t)code[k];
+          else gp(reinterpret_cast<uint16_t*>(D.v_q))[e0 + k] = (uint16_t)code[k];
         }
       }
       if ((lane & (VL - 1)) == 0) { gp(D.v_scale)[vb] = f.s; gp(D.v_min_log)[vb] = f.lmin; }

@@ -218,6 +218,27 @@ __device__ __forceinline__ uint32_t al_finish(float v, float r1) {
   return (uint32_t)al_clamp<LM2>(v, r1);
 }
 
+// AL codes of N values under one block fit, equal to al_round_exact's: AL8 takes
+// the fast argument and re-decides only the values inside its margin; AL16,
+// whose margin would cover most values, always rounds exactly.
+template <int LM2, int N>
+__device__ __forceinline__ void al_codes(const float* v, const ALFit& f, uint32_t* q) {
+  float r[N];
+  if constexpr (LM2 == 254) {
+    bool bad[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = al8_round_fast(v[i], f, bad[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (bad[i]) r[i] = al_round_exact<254>(v[i], f);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = al_round_exact<LM2>(v[i], f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) q[i] = al_finish<LM2>(v[i], r[i]);
+}
+
 // Fast UF code argument: t' = fma(m, H/absmax, H) ~ (m/absmax)*H + H with a
 // faithful reciprocal; against the exact argument the error is at most
 // H*3*2^-24 + ulp(2H)/2 (< 4e-5 for H = 128), margin 1e-4.

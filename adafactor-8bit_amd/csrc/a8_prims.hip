@@ -30,15 +30,18 @@ namespace a8 {
 constexpr int kPElems = 2048;
 
 // ============================================================ V EMA
-// One 2048-element unit (unit index bid) of the EMA; xw: 8 floats of LDS.  dec,
-// when given, receives the decoded new codes (what dequantize_log_nonneg would
-// read back).
+// One 2048-element unit (unit index bid) of the EMA; xw: 8 floats and dtab:
+// 4 * 256 floats of LDS.  dec, when given, receives the decoded new codes (what
+// dequantize_log_nonneg would read back).  AL8 blocks of >= 512 elements decode
+// through a table of their 255 values (one correctly rounded exp2 per lane and
+// block instead of one per element); the new codes take the fast AL8 argument
+// with exact re-decision near rounding boundaries.
 template <int VB, typename T>
 __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restrict__ scale,
                                           float* __restrict__ min_log, const T* __restrict__ x,
                                           float* __restrict__ out, float* __restrict__ dec, int64_t n, int64_t nblk,
                                           int64_t bid, int lbv, float w, int square, float eps1, float floor_,
-                                          float* xw) {
+                                          float* xw, float* dtab) {
   const int lane = threadIdx.x, wave = lane >> 6;
   const int64_t e0 = bid * kPElems + (int64_t)lane * 8;
   const int VL = (1 << lbv) >> 3;
@@ -51,6 +54,13 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   load8<T>(x, e0, n, xv);
   float v[8];
   const float s_old = v_ok ? gp(scale)[vb] : 0.0f, lm_old = v_ok ? gp(min_log)[vb] : 0.0f;
+  const bool tab8 = VB == 8 && VL >= 64;   // uniform
+  const int bw = tab8 ? lane / VL : 0;     // block slot of this lane in the unit
+  if (tab8) {
+    for (int c = lane % VL; c < 256; c += VL)
+      dtab[bw * 256 + c] = c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f;
+    __syncthreads();
+  }
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     float xi = xv[k];
@@ -61,7 +71,7 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
       uint32_t c;
       if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(q))[e0 + k];
       else c = gp(reinterpret_cast<const uint16_t*>(q))[e0 + k];
-      vo = c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f;
+      vo = tab8 ? dtab[bw * 256 + c] : (c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f);
     }
     v[k] = (k < cnt) ? lerp_ref(vo, xi, w) : 0.0f;   // padding quantises as zero
   }
@@ -87,20 +97,37 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
       bkey = min(bkey, __float_as_uint(xw[(w0 + ww) * 2 + 1]));
     }
   }
-  if (!v_ok) return;
+  // every lane stays to the end (the read-back table below has barriers); lanes
+  // past the last block store nothing
   const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
   constexpr int L2 = VB == 8 ? 254 : 65534;
   const ALFit f = al_refit(bmax, mnz, floor_, (float)L2);
-  float dv[8];
+  uint32_t code[8];
+  al_codes<L2, 8>(v, f, code);
+  if (v_ok) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const uint32_t code = al_finish<L2>(v[k], al_round_exact<L2>(v[k], f));
-    if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[e0 + k] = (uint8_t)code;
-    else gp(reinterpret_cast<uint16_t*>(q))[e0 + k] = (uint16_t)code;
-    dv[k] = code ? exp2_exact(((float)(code - 1) * f.s) / LM2 + f.lmin) : 0.0f;
+    for (int k = 0; k < 8; ++k) {
+      if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[e0 + k] = (uint8_t)code[k];
+      else gp(reinterpret_cast<uint16_t*>(q))[e0 + k] = (uint16_t)code[k];
+    }
   }
-  if (dec) store8<float>(dec, e0, n, dv);
-  if ((lane & (VL - 1)) == 0) { gp(scale)[vb] = f.s; gp(min_log)[vb] = f.lmin; }
+  if (dec) {   // uniform
+    float dv[8];
+    if (tab8) {   // the new fit's table, after every lane has read the old one
+      __syncthreads();
+      for (int c = lane % VL; c < 256; c += VL)
+        dtab[bw * 256 + c] = c ? exp2_exact(((float)(c - 1) * f.s) / LM2 + f.lmin) : 0.0f;
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dv[k] = dtab[bw * 256 + code[k]];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        dv[k] = code[k] ? exp2_exact(((float)(code[k] - 1) * f.s) / LM2 + f.lmin) : 0.0f;
+    }
+    if (v_ok) store8<float>(dec, e0, n, dv);
+  }
+  if (v_ok && (lane & (VL - 1)) == 0) { gp(scale)[vb] = f.s; gp(min_log)[vb] = f.lmin; }
 }
 
 template <int VB, typename T>
@@ -109,8 +136,9 @@ __global__ __launch_bounds__(256) void k_vema(void* __restrict__ q, float* __res
                                               float* __restrict__ out, int64_t n, int64_t nblk, int lbv, float w,
                                               int square, float eps1, float floor_) {
   __shared__ float xw[8];
+  __shared__ float dtab[4 * 256];
   vema_unit<VB, T>(q, scale, min_log, x, out, nullptr, n, nblk, (int64_t)blockIdx.x, lbv, w, square, eps1, floor_,
-                   xw);
+                   xw, dtab);
 }
 
 // Table form: one launch over several tensors, each a run of whole units.
@@ -128,6 +156,7 @@ template <int VB>
 __global__ __launch_bounds__(256) void k_vema_multi(VemaDesc one, const VemaDesc* __restrict__ tab, int ntab,
                                                     int lbv, float w, int square, float eps1, float floor_) {
   __shared__ float xw[8];
+  __shared__ float dtab[4 * 256];
   const int64_t wg = blockIdx.x;
   int lo = 0;
   if (tab) {
@@ -139,7 +168,7 @@ __global__ __launch_bounds__(256) void k_vema_multi(VemaDesc one, const VemaDesc
   }
   const VemaDesc d = tab ? tab[lo] : one;
   vema_unit<VB, float>(d.q, d.scale, d.min_log, d.x, d.out, d.dec, d.n, d.nblk, wg - d.wg_begin, lbv, w, square,
-                       eps1, floor_, xw);
+                       eps1, floor_, xw, dtab);
 }
 
 // ============================================================ factored element kernel

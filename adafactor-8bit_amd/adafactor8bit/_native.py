@@ -39,7 +39,7 @@ class Tensor1D(ctypes.Structure):
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
                 ("v_q", _c_vp), ("v_scale", _c_vp), ("v_min_log", _c_vp), ("v_buf", _c_vp),
                 ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("fira_scale", _c_vp)]
 
 
 class TensorFull(ctypes.Structure):

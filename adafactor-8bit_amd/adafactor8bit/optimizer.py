@@ -505,6 +505,13 @@ class _Plan:
                     self.beta1, self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.kwd, self.group["weight_decay"], self.d, self.fira,
                     self.margin, self.rms_kernel, self.eps2)
+        if self.path == "q1d" and (self.d > 0 or self.fira):
+            if self.lag:
+                return None
+            return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
+                    self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
+                    self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
+                    self.alpha_val, self.decay_val, self.d, self.fira, self.margin)
         if self.d > 0 or self.fira:
             return None
         if self.path == "sgd":
@@ -1109,6 +1116,106 @@ def _run_batch_f1dc(opt, key, plans):
     launch(nat.MODE_APPLY)
 
 
+def _run_batch_q1dc(opt, key, plans):
+    """Quantised 1-D tensors with an RMS clip or Fira as one group: NORM (V' to
+    each tensor's slice of one v_buf, sum u^2) -> MNORM (momentum-only Fira) ->
+    one Fira launch over all tensors -> APPLY, each one multi-tensor launch (the
+    per-tensor sequence of _run_single / _dispatch_1d_cuda, optimizer.py:1080-1170,
+    785-793).  Fira's scale reaches APPLY as each tensor's fira_scale."""
+    P0 = plans[0]
+    dev = P0.p.device
+    L = nat.lib()
+    n = len(plans)
+    fira = bool(P0.fira)
+    mnorm = fira and P0.has_m and P0.mom_only
+    ws = opt._ws.setdefault((dev, "q1dc"), {})
+    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr(), pl.st["variance_q"].data_ptr()) for pl in plans), P0.sr,
+          P0.has_m, fira, mnorm)
+    refs = [tuple(v.data_ptr() for k, v in pl.st.items() if torch.is_tensor(v) and k != "fira_prev_norm")
+            for pl in plans]
+    ent = ws.get(ck)
+    if ent is None or ent["refs"] != refs:
+        offs, tot = [], 0
+        for pl in plans:   # v_buf slices start 16-byte aligned
+            offs.append(tot)
+            tot += (pl.p.numel() + 3) // 4 * 4
+        vbuf = torch.empty(max(tot, 4), dtype=torch.float32, device=dev)
+        acc = torch.zeros(2 * n, dtype=torch.float32, device=dev)    # sum u^2 | sum M'^2
+        fout = torch.zeros(3 * n, dtype=torch.float32, device=dev)   # Fira: scale | prev norm | clean sum
+        a0, f0, v0 = acc.data_ptr(), fout.data_ptr(), vbuf.data_ptr()
+        arrs = {}
+        for mode in (nat.MODE_NORM, nat.MODE_MNORM, nat.MODE_APPLY):
+            if mode == nat.MODE_MNORM and not mnorm:
+                continue
+            arr = (nat.Tensor1D * n)()
+            for i, pl in enumerate(plans):
+                st = pl.st
+                nb, prev, fs = a0 + 4 * i, None, None
+                if mode == nat.MODE_MNORM:
+                    nb, prev = a0 + 4 * (n + i), a0 + 4 * i
+                elif mode == nat.MODE_APPLY and fira:
+                    fs = f0 + 4 * i
+                    if not mnorm:   # the update clip reads the Fira launch's finite sum
+                        nb = f0 + 4 * (2 * n + i)
+                arr[i] = nat.Tensor1D(
+                    pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(st.get("m_q") if pl.has_m else None),
+                    nat.ptr(st.get("m_scale") if pl.has_m else None), st["variance_q"].data_ptr(),
+                    st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), v0 + 4 * offs[i], nb,
+                    None, prev, None, pl.p.numel(), int(st.get("sr_seed", 0)), fs)
+            arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_1d(n)), dtype=torch.uint8, device=dev), 1]
+        ent = {"refs": refs, "acc": acc, "fout": fout, "vbuf": vbuf, "arrs": arrs}
+        if len(ws) > 16:
+            ws.clear()
+        ws[ck] = ent
+    acc, fout = ent["acc"], ent["fout"]
+    strm = nat.stream_of(dev)
+    has_dec = int(P0.decay_val is not None)
+    dec_val = P0.decay_val if has_dec else 1.0
+
+    def launch(mode):
+        arr, table, up = ent["arrs"][mode]
+        _no_upload_in_capture(up)
+        rc = L.a8_fused_update_1d_multi(
+            mode, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), table.numel(),
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,
+            P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
+            S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
+            16 if P0.vqt == "al16" else 8, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
+            float(dec_val), has_dec, up, nat.ptr(P0.dsc), strm)
+        nat.check(rc, "a8_fused_update_1d_multi")
+        ent["arrs"][mode][2] = 0
+
+    acc.zero_()
+    launch(nat.MODE_NORM)
+    for pl in plans:
+        _block_view(pl.st, "variance", pl.bs)
+    if mnorm:
+        launch(nat.MODE_MNORM)
+    if fira:
+        # A tensor without a previous norm behaves as one whose previous norm is
+        # below 1e-6 (scale 1, next = current), so every slot takes has_prev = 1.
+        prev_ok = True
+        for i, pl in enumerate(plans):
+            pv = pl.st.get("fira_prev_norm")
+            if not (torch.is_tensor(pv) and pv.data_ptr() == fout.data_ptr() + 4 * (n + i)):
+                prev_ok = False
+        if not prev_ok:
+            vals = []
+            for pl in plans:
+                pv = pl.st.get("fira_prev_norm")
+                vals.append(torch.zeros((), dtype=torch.float32, device=dev) if pv is None else
+                            torch.as_tensor(pv, dtype=torch.float32).to(dev).reshape(()))
+            fout[n:2 * n].copy_(torch.stack(vals))
+        x = acc[n:2 * n] if mnorm else acc[0:n]
+        rc = L.a8_fira_scalar(x.data_ptr(), fout.data_ptr() + 4 * n, None, fout.data_ptr(), n, 1, 2,
+                              _f32(1.0 + P0.margin), strm)
+        nat.check(rc, "a8_fira_scalar")
+        if not prev_ok:
+            for i, pl in enumerate(plans):
+                pl.st["fira_prev_norm"] = fout[n + i].view(())
+    launch(nat.MODE_APPLY)
+
+
 def _run_batch(opt, key, plans):
     path = key[0]
     if path == "factored":
@@ -1119,6 +1226,9 @@ def _run_batch(opt, key, plans):
         return
     if path == "f1dc":
         _run_batch_f1dc(opt, key, plans)
+        return
+    if path == "q1dc":
+        _run_batch_q1dc(opt, key, plans)
         return
     P0 = plans[0]
     dev = P0.p.device

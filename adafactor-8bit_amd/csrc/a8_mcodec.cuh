@@ -45,17 +45,17 @@ __device__ __forceinline__ uint64_t sr_base(uint64_t seed, uint64_t step) {
 
 // bf16 stochastic rounding decided in integers: u < rem / 2^16 with
 // u = (bits >> 8) / 2^24 is (bits >> 8) < rem * 2^8 exactly (both sides are
-// exact in fp32), so the result equals sr_bf16(x, u).
+// exact in fp32), so the result equals sr_bf16(x, u).  sr_bf16's three guards
+// fold into one magnitude compare: rem == 0 never rounds up (the compare is
+// false), and |x| >= 0x7F7F0000 (inf, NaN, or a truncation whose upper
+// neighbour is inf) never rounds up either; NaN becomes the quiet NaN.
 __device__ __forceinline__ uint16_t sr_bf16_bits(float x, uint32_t bits) {
   const uint32_t b = __float_as_uint(x);
-  const bool nan = ((b & 0x7F800000u) == 0x7F800000u) && (b & 0x007FFFFFu);
-  const uint32_t lo = b & 0xFFFF0000u;
+  const uint32_t a = b & 0x7FFFFFFFu;
   const uint32_t rem = b & 0x0000FFFFu;
-  const uint32_t hi = lo + 0x00010000u;
-  const bool lo_inf = (lo & 0x7F800000u) == 0x7F800000u;
-  const bool hi_inf = ((hi & 0x7F800000u) == 0x7F800000u) && !(hi & 0x007FFFFFu);
-  const bool up = rem && !lo_inf && !hi_inf && ((bits >> 8) < (rem << 8));
-  const uint32_t r = nan ? ((b & 0x80000000u) | 0x7FC00000u) : (up ? hi : lo);
+  const bool up = ((bits >> 8) < (rem << 8)) && a < 0x7F7F0000u;
+  const uint32_t r = (a > 0x7F800000u) ? ((b & 0x80000000u) | 0x7FC00000u)
+                                       : (b & 0xFFFF0000u) + (up ? 0x00010000u : 0u);
   return (uint16_t)(r >> 16);
 }
 

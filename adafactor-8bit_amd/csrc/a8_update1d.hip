@@ -40,6 +40,7 @@ struct Desc1D {
   int64_t numel;
   int64_t wg_begin;
   uint64_t sr_seed;
+  const float* fira_scale;   // APPLY: Fira limiter scale multiplied into the step, or null
 };
 
 struct Hyper1D {
@@ -235,7 +236,8 @@ __device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int
   // ---- step scale
   float step = 0.0f, ut_clip = 1.0f;
   if constexpr (MODE != 1) {
-    const float a = D.alpha ? *gp(D.alpha) : h.alpha_val;
+    float a = D.alpha ? *gp(D.alpha) : h.alpha_val;
+    if (MODE == 2 && D.fira_scale) a = a * *gp(D.fira_scale);
     if constexpr (MODE == 0) {
       step = a;
     } else {
@@ -820,7 +822,7 @@ static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int n
       D.param = t.param; D.grad = t.grad; D.m_q = t.m_q; D.m_scale = t.m_scale;
       D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
       D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
-      D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed;
+      D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed; D.fira_scale = t.fira_scale;
       std::memcpy(&tab[i], &D, sizeof(Desc1D));
       const int32_t f = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
       std::memcpy(&first[i], &f, sizeof(int32_t));

@@ -141,6 +141,7 @@ typedef struct a8_tensor1d {
   const float* decay;
   int64_t numel;
   uint64_t sr_seed;
+  const float* fira_scale; /* APPLY: the step is multiplied by this Fira limiter scale (NULL: none) */
 } a8_tensor1d;
 
 /* Multi-tensor form of a8_fused_update_1d: one launch over `ntensors` tensors

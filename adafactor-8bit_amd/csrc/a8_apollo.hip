@@ -865,7 +865,23 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
     }
     const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
     constexpr int LM2 = VB == 8 ? 254 : 65534;
-    const ALFit f = al_refit(bmax, mnz, floor_, (float)LM2);
+    // the two correctly rounded logarithms of a block: one lane pair per wave
+    // (al_refit_pair); a block spanning several waves is fitted by its first wave
+    // only and shared through LDS, so the others skip the double-precision work
+    ALFit f;
+    if (VL > 64) {   // uniform
+      const int wpb = VL >> 6, bw = wave / wpb;
+      if (wave % wpb == 0) {
+        f = al_refit_pair(bmax, mnz, floor_, (float)LM2, lane);
+        if ((lane & 63) == 0) { xw[12 + 2 * bw] = f.lmin; xw[13 + 2 * bw] = f.s; }
+      }
+      __syncthreads();
+      f.lmin = xw[12 + 2 * bw];
+      f.s = xw[13 + 2 * bw];
+      al_fit_consts(f, (float)LM2);
+    } else {
+      f = al_refit_pair(bmax, mnz, floor_, (float)LM2, lane);
+    }
     if (v_ok) {
       uint32_t code[8];
       al_codes<LM2, 8>(v, f, code);

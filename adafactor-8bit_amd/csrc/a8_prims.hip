@@ -101,7 +101,7 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   // past the last block store nothing
   const float mnz = (bkey == 0xFFFFFFFFu) ? __builtin_inff() : __uint_as_float(bkey + 1u);
   constexpr int L2 = VB == 8 ? 254 : 65534;
-  const ALFit f = al_refit(bmax, mnz, floor_, (float)L2);
+  const ALFit f = al_refit_pair(bmax, mnz, floor_, (float)L2, lane);   // a block spans >= 16 lanes
   uint32_t code[8];
   al_codes<L2, 8>(v, f, code);
   if (v_ok) {

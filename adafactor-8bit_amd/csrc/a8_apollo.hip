@@ -851,7 +851,7 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
     }
     float bmax = grp_max(__uint_as_float(vmaxb), VL < 64 ? VL : 64);
     uint32_t bkey = vkey;
-    for (int o = 1; o < (VL < 64 ? VL : 64); o <<= 1) bkey = min(bkey, (uint32_t)__shfl_xor((int)bkey, o, 64));
+    bkey = grp_umin(bkey, VL < 64 ? VL : 64);
     if (VL > 64) {
       if ((lane & 63) == 0) { xw[wave * 2] = bmax; xw[wave * 2 + 1] = __uint_as_float(bkey); }
       __syncthreads();

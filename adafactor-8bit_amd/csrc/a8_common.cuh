@@ -430,42 +430,83 @@ __device__ __forceinline__ void store4n(T* base, int64_t i0, int64_t n, const fl
 }
 
 // ---------------------------------------------------------------- reductions
-// Butterfly reductions over aligned groups of G lanes (G power of two <= 64).
-__device__ __forceinline__ float grp_max(float x, int G) {
-  for (int o = 1; o < G; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-  return x;
+// Max / min over aligned groups of G lanes (G a power of two <= 64, uniform),
+// with no LDS traffic: DPP moves inside 16-lane rows (quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror, row_mirror -- each pairs every lane with one of
+// its own group, so after them every lane of a row holds the row's result),
+// ds_swizzle in bit mode (xor 16) across the two rows of a 32-lane half, and
+// v_readlane of lanes 0 and 32 across the halves (the result is then uniform).
+// Max and min are exact, so the order of the steps does not matter.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, true);
 }
-// grp_max over aligned groups of G lanes (a power of two, uniform), with DPP lane
-// moves inside 16-lane rows (quad_perm 1032 / 2301, row_half_mirror, row_mirror:
-// each pairs every lane with one of the same group) and lane shuffles beyond.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+  return __uint_as_float(dpp_u<CTRL>(__float_as_uint(x)));
 }
 
-__device__ __forceinline__ float grp_max_dpp(float x, int G) {
-  x = fmaxf(x, dpp_f<0xB1>(x));                // quad_perm [1,0,3,2]
-  x = fmaxf(x, dpp_f<0x4E>(x));                // quad_perm [2,3,0,1]
-  if (G <= 4) return x;
-  x = fmaxf(x, dpp_f<0x141>(x));               // row_half_mirror
-  if (G <= 8) return x;
-  x = fmaxf(x, dpp_f<0x140>(x));               // row_mirror
-  if (G <= 16) return x;
-  x = fmaxf(x, __shfl_xor(x, 16, 64));
-  if (G <= 32) return x;
-  return fmaxf(x, __shfl_xor(x, 32, 64));
+template <typename Op>
+__device__ __forceinline__ uint32_t grp_red_u(uint32_t x, int G, Op op) {
+  if (G >= 2) x = op(x, dpp_u<0xB1>(x));    // quad_perm [1,0,3,2]
+  if (G >= 4) x = op(x, dpp_u<0x4E>(x));    // quad_perm [2,3,0,1]
+  if (G >= 8) x = op(x, dpp_u<0x141>(x));   // row_half_mirror
+  if (G >= 16) x = op(x, dpp_u<0x140>(x));  // row_mirror
+  if (G >= 32) x = op(x, (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F));   // xor 16 within 32
+  if (G >= 64) x = op((uint32_t)__builtin_amdgcn_readlane((int)x, 0), (uint32_t)__builtin_amdgcn_readlane((int)x, 32));
+  return x;
 }
 
+__device__ __forceinline__ float grp_max(float x, int G) {
+  return __uint_as_float(grp_red_u(__float_as_uint(x), G, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
 __device__ __forceinline__ float grp_min(float x, int G) {
-  for (int o = 1; o < G; o <<= 1) x = fminf(x, __shfl_xor(x, o, 64));
-  return x;
+  return __uint_as_float(grp_red_u(__float_as_uint(x), G, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b)));
+  }));
 }
+__device__ __forceinline__ uint32_t grp_umin(uint32_t x, int G) {
+  return grp_red_u(x, G, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ float grp_max_dpp(float x, int G) { return grp_max(x, G); }
+
+// Sums over the same groups: every step adds two equal-ordered partial sums
+// (within a quad the xor-1 / xor-2 partners, then whole quads, rows and halves
+// whose lanes already agree), so each lane's result is the butterfly's, bit for
+// bit, whatever the pairing inside a step.
 __device__ __forceinline__ float grp_sum(float x, int G) {
-  for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
-  return x;
+  return __uint_as_float(grp_red_u(__float_as_uint(x), G, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = dpp_u<CTRL>((uint32_t)u), hi = dpp_u<CTRL>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double swz16_d(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, 0x401F);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), 0x401F);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double lane_d(double x, int l) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 __device__ __forceinline__ double grp_sum_d(double x, int G) {
-  for (int o = 1; o < G; o <<= 1) x += __shfl_xor(x, o, 64);
+  if (G >= 2) x += dpp_d<0xB1>(x);
+  if (G >= 4) x += dpp_d<0x4E>(x);
+  if (G >= 8) x += dpp_d<0x141>(x);
+  if (G >= 16) x += dpp_d<0x140>(x);
+  if (G >= 32) x += swz16_d(x);
+  if (G >= 64) x = lane_d(x, 0) + lane_d(x, 32);
   return x;
 }
 

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void k_al_enc(void* __restrict__ q, float* __r
     key = min(key, __float_as_uint(v) - 1u);
   }
   mx = grp_max(mx, 64);
-  for (int o = 1; o < 64; o <<= 1) key = min(key, (uint32_t)__shfl_xor((int)key, o, 64));
+  key = grp_umin(key, 64);
   if ((lane & 63) == 0) {
     s8[lane >> 6] = mx;
     s8[4 + (lane >> 6)] = __uint_as_float(key);

@@ -228,7 +228,7 @@ __device__ __forceinline__ uint32_t nz_key_f(float v) { return __float_as_uint(v
 
 __device__ __forceinline__ void wg_maxkey(float& mx, uint32_t& key, float* s8) {
   mx = grp_max(mx, 64);
-  for (int o = 1; o < 64; o <<= 1) key = min(key, (uint32_t)__shfl_xor((int)key, o, 64));
+  key = grp_umin(key, 64);
   const int lane = threadIdx.x;
   __syncthreads();
   if ((lane & 63) == 0) {

@@ -85,7 +85,7 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   const int G = VL < 64 ? VL : 64;
   float bmax = grp_max(__uint_as_float(vmaxb), G);
   uint32_t bkey = vkey;
-  for (int o = 1; o < G; o <<= 1) bkey = min(bkey, (uint32_t)__shfl_xor((int)bkey, o, 64));
+  bkey = grp_umin(bkey, G);
   if (VL > 64) {
     if ((lane & 63) == 0) { xw[wave * 2] = bmax; xw[wave * 2 + 1] = __uint_as_float(bkey); }
     __syncthreads();

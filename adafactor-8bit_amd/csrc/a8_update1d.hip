@@ -98,10 +98,6 @@ __device__ __forceinline__ Desc1D load_desc(const Desc1D* tab, int n, int wg) {
 // order of these keys is the float order, and v == 0 maps to 0xFFFFFFFF, so an
 // unsigned min over keys is the minimum over the non-zero entries.
 __device__ __forceinline__ uint32_t nz_key(float v) { return __float_as_uint(v) - 1u; }
-__device__ __forceinline__ uint32_t grp_umin(uint32_t x, int G) {
-  for (int o = 1; o < G; o <<= 1) x = min(x, (uint32_t)__shfl_xor((int)x, o, 64));
-  return x;
-}
 
 // MK: 0 no momentum, 1 UF8 (specialised), 2 UF4/D8/D4 (codec chosen by h.mk).
 // MODE: 0 single pass, 1 NORM (V codes + v_buf, sum of squares), 2 APPLY (reads

@@ -13,7 +13,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libadafactor8bit_amd.so")
 
-F32, BF16, F16 = 0, 1, 2
+F32, BF16, F16, F64 = 0, 1, 2, 3
 MODE_NOCLIP, MODE_NORM, MODE_APPLY, MODE_LAG, MODE_MNORM = 0, 1, 2, 3, 4
 
 _c_vp = ctypes.c_void_p
@@ -220,6 +220,8 @@ def dtype_code(dt) -> int:
         return BF16
     if dt == torch.float16:
         return F16
+    if dt == torch.float64:
+        return F64
     raise TypeError(f"adafactor8bit: unsupported parameter dtype {dt}")
 
 

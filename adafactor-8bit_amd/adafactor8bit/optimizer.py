@@ -592,6 +592,10 @@ def _plan_param(p, grad, st, group) -> _Plan:
     lr = group["lr"]
     P.alpha_t = P.rho_t = None
     relative_step, scale_parameter = group["relative_step"], group["scale_parameter"]
+    if scale_parameter and p.dtype == torch.float64:
+        # the reference's _compute_alpha (optimizer.py:850-852) takes the norm with
+        # dtype=float32, which torch refuses for a float64 tensor: the same error here
+        torch.linalg.vector_norm(p, ord=2, dtype=torch.float32)
     if isinstance(lr, Tensor):
         rho_t = lr.to(device=p.device, dtype=torch.float32)
         if relative_step:
@@ -893,10 +897,12 @@ def _prep_q1d_fp32m(opt, P):
         opt._ws[key] = buf
     if g.dtype != p.dtype:
         raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    gx = g.float() if g.dtype == torch.float64 else g   # fp64: the gradient is read as fp32
     rc = nat.lib().a8_log_quantize_lerp(
         st["variance_q"].data_ptr(), st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(),
-        g.data_ptr(), nat.dtype_code(g.dtype), buf.data_ptr(), float(P.beta_val), int(P.bs), 1, _f32(P.eps_g),
+        gx.data_ptr(), nat.dtype_code(gx.dtype), buf.data_ptr(), float(P.beta_val), int(P.bs), 1, _f32(P.eps_g),
         p.numel(), _AL_FLOOR, 16 if P.vqt == "al16" else 8, nat.stream_of(dev))
+    P._keep = gx
     nat.check(rc, "a8_log_quantize_lerp")
     _block_view(st, "variance", P.bs)
     P.vbuf = buf
@@ -917,6 +923,8 @@ def _prep_f1d_qm(opt, P):
     st, p, g = P.st, P.p, P.g
     if g.dtype != p.dtype:
         raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
+    if g.dtype == torch.float64:   # the gradient is read as fp32 (the update kernel reads P.g itself)
+        g = g.float()
     dev = p.device
     if not st["variance"].is_contiguous():
         st["variance"] = st["variance"].contiguous()

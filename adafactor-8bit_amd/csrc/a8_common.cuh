@@ -305,11 +305,46 @@ __device__ __forceinline__ float f32_value(float x) {
 }
 template <> __device__ __forceinline__ __half from_f<__half>(float x) { return __float2half(f32_value(x)); }
 
+// fp64 parameters: gradients are read as fp32 (torch's grad.float(), round to
+// nearest), parameters stay double and take their update in double -- what
+// p.mul_(decay) and p.add_(u, alpha=-step) do on a float64 tensor.  pval_t<T> is
+// the register type of a parameter value: double for fp64, fp32 otherwise.
+template <> __device__ __forceinline__ float to_f<double>(double x) { return (float)x; }
+template <> __device__ __forceinline__ double from_f<double>(float x) { return (double)x; }
+template <typename T> struct PVal { using type = float; };
+template <> struct PVal<double> { using type = double; };
+template <typename T> using pval_t = typename PVal<T>::type;
+
+// p * decay and fma(-step, u, p) in the parameter's register type.  With fp64
+// the product step * u of two floats is exact in double, so the fma rounds once,
+// as the double add of torch does.
+__device__ __forceinline__ float pdec(float p, float d) { return p * d; }
+__device__ __forceinline__ double pdec(double p, float d) { return p * (double)d; }
+__device__ __forceinline__ float pupd(float step, float u, float p) { return __builtin_fmaf(-step, u, p); }
+__device__ __forceinline__ double pupd(float step, float u, double p) {
+  return __builtin_fma(-(double)step, (double)u, p);
+}
+
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+
+// A parameter element to / from its register type.
+template <typename T>
+__device__ __forceinline__ pval_t<T> pv_of(T x) {
+  if constexpr (sizeof(T) == 8) return x; else return to_f<T>(x);
+}
+template <typename T>
+__device__ __forceinline__ T pv_to(pval_t<T> x) {
+  if constexpr (sizeof(T) == 8) return x; else return from_f<T>(x);
+}
+
 // Single-element global load / store of a param-typed value (16-bit types go
 // through their bit pattern: class types cannot be bound in address space 1).
-template <typename T>
-__device__ __forceinline__ float ld1(const T* p, int64_t i) {
-  if constexpr (sizeof(T) == 4) {
+// V: the register type (fp32, or double for fp64 parameters).
+template <typename T, typename V = float>
+__device__ __forceinline__ V ld1(const T* p, int64_t i) {
+  if constexpr (sizeof(T) == 8) {
+    return (V)gp(reinterpret_cast<const double*>(p))[i];
+  } else if constexpr (sizeof(T) == 4) {
     return gp(reinterpret_cast<const float*>(p))[i];
   } else {
     const uint16_t b = gp(reinterpret_cast<const uint16_t*>(p))[i];
@@ -318,9 +353,11 @@ __device__ __forceinline__ float ld1(const T* p, int64_t i) {
     return to_f<T>(t);
   }
 }
-template <typename T>
-__device__ __forceinline__ void st1(T* p, int64_t i, float v) {
-  if constexpr (sizeof(T) == 4) {
+template <typename T, typename V>
+__device__ __forceinline__ void st1(T* p, int64_t i, V v) {
+  if constexpr (sizeof(T) == 8) {
+    gp(reinterpret_cast<double*>(p))[i] = (double)v;
+  } else if constexpr (sizeof(T) == 4) {
     gp(reinterpret_cast<float*>(p))[i] = v;
   } else {
     const T t = from_f<T>(v);
@@ -330,11 +367,29 @@ __device__ __forceinline__ void st1(T* p, int64_t i, float v) {
   }
 }
 
+// Four fp64 values from 32 aligned bytes.
+template <typename V>
+__device__ __forceinline__ void ld4d(const double* p, V* out) {
+  const f64x2 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f64x2*>(p)));
+  const f64x2 b = __builtin_nontemporal_load(gp(reinterpret_cast<const f64x2*>(p)) + 1);
+  out[0] = (V)a.x; out[1] = (V)a.y; out[2] = (V)b.x; out[3] = (V)b.y;
+}
+template <typename V>
+__device__ __forceinline__ void st4d(double* p, const V* v) {
+  const f64x2 a = {(double)v[0], (double)v[1]};
+  const f64x2 b = {(double)v[2], (double)v[3]};
+  __builtin_nontemporal_store(a, gp(reinterpret_cast<f64x2*>(p)));
+  __builtin_nontemporal_store(b, gp(reinterpret_cast<f64x2*>(p)) + 1);
+}
+
 // Load / store 8 consecutive elements (aligned fast path when fully in range).
-template <typename T>
-__device__ __forceinline__ void load8(const T* base, int64_t i0, int64_t n, float* out) {
+template <typename T, typename V>
+__device__ __forceinline__ void load8(const T* base, int64_t i0, int64_t n, V* out) {
   if (i0 + 8 <= n) {
-    if constexpr (sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8) {
+      ld4d<V>(reinterpret_cast<const double*>(base) + i0, out);
+      ld4d<V>(reinterpret_cast<const double*>(base) + i0 + 4, out + 4);
+    } else if constexpr (sizeof(T) == 4) {
       const A8_G f32x4* p = gp(reinterpret_cast<const f32x4*>(base + i0));
       f32x4 a = __builtin_nontemporal_load(p);
       f32x4 b = __builtin_nontemporal_load(p + 1);
@@ -348,14 +403,17 @@ __device__ __forceinline__ void load8(const T* base, int64_t i0, int64_t n, floa
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) out[k] = (i0 + k < n) ? ld1<T>(base, i0 + k) : 0.0f;
+    for (int k = 0; k < 8; ++k) out[k] = (i0 + k < n) ? ld1<T, V>(base, i0 + k) : (V)0;
   }
 }
 
-template <typename T>
-__device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const float* v) {
+template <typename T, typename V>
+__device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const V* v) {
   if (i0 + 8 <= n) {
-    if constexpr (sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8) {
+      st4d<V>(reinterpret_cast<double*>(base) + i0, v);
+      st4d<V>(reinterpret_cast<double*>(base) + i0 + 4, v + 4);
+    } else if constexpr (sizeof(T) == 4) {
       A8_G f32x4* p = gp(reinterpret_cast<f32x4*>(base + i0));
       f32x4 a = {v[0], v[1], v[2], v[3]};
       f32x4 b = {v[4], v[5], v[6], v[7]};
@@ -371,16 +429,18 @@ __device__ __forceinline__ void store8(T* base, int64_t i0, int64_t n, const flo
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (i0 + k < n) st1<T>(base, i0 + k, v[k]);
+      if (i0 + k < n) st1<T, V>(base, i0 + k, v[k]);
   }
 }
 
 // Load / store 4 consecutive elements (one 16-byte fp32 or 8-byte 16-bit
-// access per lane when fully in range).
-template <typename T>
-__device__ __forceinline__ void load4n(const T* base, int64_t i0, int64_t n, float* out) {
+// access per lane when fully in range; two 16-byte accesses for fp64).
+template <typename T, typename V>
+__device__ __forceinline__ void load4n(const T* base, int64_t i0, int64_t n, V* out) {
   if (i0 + 4 <= n) {
-    if constexpr (sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8) {
+      ld4d<V>(reinterpret_cast<const double*>(base) + i0, out);
+    } else if constexpr (sizeof(T) == 4) {
       const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(base + i0)));
       out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
     } else {
@@ -391,14 +451,16 @@ __device__ __forceinline__ void load4n(const T* base, int64_t i0, int64_t n, flo
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) out[k] = (i0 + k < n) ? ld1<T>(base, i0 + k) : 0.0f;
+    for (int k = 0; k < 4; ++k) out[k] = (i0 + k < n) ? ld1<T, V>(base, i0 + k) : (V)0;
   }
 }
 
 // Unchecked form of load4n for a window known to lie inside the tensor.
-template <typename T>
-__device__ __forceinline__ void load4v(const T* base, int64_t i0, float* out) {
-  if constexpr (sizeof(T) == 4) {
+template <typename T, typename V>
+__device__ __forceinline__ void load4v(const T* base, int64_t i0, V* out) {
+  if constexpr (sizeof(T) == 8) {
+    ld4d<V>(reinterpret_cast<const double*>(base) + i0, out);
+  } else if constexpr (sizeof(T) == 4) {
     const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(base + i0)));
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
   } else {
@@ -409,10 +471,12 @@ __device__ __forceinline__ void load4v(const T* base, int64_t i0, float* out) {
   }
 }
 
-template <typename T>
-__device__ __forceinline__ void store4n(T* base, int64_t i0, int64_t n, const float* v) {
+template <typename T, typename V>
+__device__ __forceinline__ void store4n(T* base, int64_t i0, int64_t n, const V* v) {
   if (i0 + 4 <= n) {
-    if constexpr (sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8) {
+      st4d<V>(reinterpret_cast<double*>(base) + i0, v);
+    } else if constexpr (sizeof(T) == 4) {
       const f32x4 a = {v[0], v[1], v[2], v[3]};
       __builtin_nontemporal_store(a, gp(reinterpret_cast<f32x4*>(base + i0)));
     } else {
@@ -425,7 +489,7 @@ __device__ __forceinline__ void store4n(T* base, int64_t i0, int64_t n, const fl
   } else {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if (i0 + k < n) st1<T>(base, i0 + k, v[k]);
+      if (i0 + k < n) st1<T, V>(base, i0 + k, v[k]);
   }
 }
 

@@ -242,11 +242,13 @@ __device__ __forceinline__ void wg_maxkey(float& mx, uint32_t& key, float* s8) {
 }
 
 // Four consecutive row elements starting at column c0 (zero beyond C).
-template <typename T>
+template <typename T, typename V>
 __device__ __forceinline__ void load4(const T* base, int64_t rowbase, int64_t c0, int64_t C, bool vec,
-                                      float* out) {
+                                      V* out) {
   if (vec && c0 + 4 <= C) {
-    if constexpr (sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 8) {
+      ld4d<V>(reinterpret_cast<const double*>(base) + rowbase + c0, out);
+    } else if constexpr (sizeof(T) == 4) {
       const f32x4 a = *gp(reinterpret_cast<const f32x4*>(base + rowbase + c0));
       out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
     } else {
@@ -257,7 +259,7 @@ __device__ __forceinline__ void load4(const T* base, int64_t rowbase, int64_t c0
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) out[k] = (c0 + k < C) ? ld1<T>(base, rowbase + c0 + k) : 0.0f;
+    for (int k = 0; k < 4; ++k) out[k] = (c0 + k < C) ? ld1<T, V>(base, rowbase + c0 + k) : (V)0;
   }
 }
 
@@ -310,9 +312,11 @@ __device__ __forceinline__ const char* at_off(const T* row, uint32_t off) {
   return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo) + (off * (uint32_t)sizeof(T));
 }
 
-template <typename T>
-__device__ __forceinline__ void load4o(const T* row, uint32_t off, float* out) {
-  if constexpr (sizeof(T) == 4) {
+template <typename T, typename V>
+__device__ __forceinline__ void load4o(const T* row, uint32_t off, V* out) {
+  if constexpr (sizeof(T) == 8) {
+    ld4d<V>(reinterpret_cast<const double*>(at_off(row, off)), out);
+  } else if constexpr (sizeof(T) == 4) {
     const f32x4 a = __builtin_nontemporal_load(gp(reinterpret_cast<const f32x4*>(at_off(row, off))));
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
   } else {
@@ -988,14 +992,14 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
           }
         }
       } else {
-        float p[8];
+        pval_t<T> p[8];
         load8<T>(P, e0, n, p);
         if (has_dec) {
 #pragma unroll
-          for (int k = 0; k < 8; ++k) p[k] = p[k] * dec;
+          for (int k = 0; k < 8; ++k) p[k] = pdec(p[k], dec);
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) p[k] = __builtin_fmaf(-step, u[k], p[k]);
+        for (int k = 0; k < 8; ++k) p[k] = pupd(step, u[k], p[k]);
         store8<T>(P, e0, n, p);
       }
     }
@@ -1069,7 +1073,8 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 // the waits for its loads) stays ahead of a following lane-conditional store
 // instead of being sunk into it; a load left unconsumed on the store-skipping path
 // would make the next row's loads wait for every outstanding store.
-__device__ __forceinline__ void keep4(const float* v) {
+template <typename V>
+__device__ __forceinline__ void keep4(const V* v) {
   asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
 }
 
@@ -1132,7 +1137,8 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     int64_t rowb[NRW];
     bool rv[NRW];
     float irw[NRW], icrw[NRW];
-    float gj[NRW][4][4], pj[NRW][4][4], msj[NRW][4];
+    float gj[NRW][4][4], msj[NRW][4];
+    pval_t<T> pj[NRW][4][4];   // double for fp64 parameters
     float mfj[NRW][MK == 3 ? 4 : 1][4];
     uint32_t qj[NRW][4];
 #pragma unroll
@@ -1167,7 +1173,7 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
       const bool st = rv[rr] && act[j];   // this window of this row is stored
       float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       float mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4];
-      float* pv = pj[rr][j];
+      pval_t<T>* pv = pj[rr][j];
       if constexpr (MK == 3) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) mo[i] = mfj[rr][j][i];
@@ -1234,10 +1240,10 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
         } else {
           if (has_dec) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = pv[i] * dec;
+            for (int i = 0; i < 4; ++i) pv[i] = pdec(pv[i], dec);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pv[i] = __builtin_fmaf(-step, u[i], pv[i]);
+          for (int i = 0; i < 4; ++i) pv[i] = pupd(step, u[i], pv[i]);
           keep4(pv);
           if (st) store4n<T>(P0, e, e + 4, pv);
         }
@@ -1498,7 +1504,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
                      int m_bits, int m_mode, uint64_t sr_step, int came, double beta3, float eps_came,
                      int c_bits, const void* step_scalars, void* stream) {
   if (ntensors <= 0) return 0;
-  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
+    return set_error(A8_ERR_DTYPE, "dtype");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
   if (came && c_bits != 0 && c_bits != 8 && c_bits != 16) return set_error(A8_ERR_ARG, "c_bits must be 0, 8 or 16");
   if (block_size <= 0) return set_error(A8_ERR_BLOCK, "block_size must be positive");
@@ -1596,6 +1603,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     case A8_BF16:
       return stochastic ? run_group<__hip_bfloat16, true>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st)
                         : run_group<__hip_bfloat16, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);
+    case A8_F64: return run_group<double, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);
     default:
       return stochastic ? run_group<__half, true>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st)
                         : run_group<__half, false>(dt, ntensors, tiles, ug, fblks, csw, v_bits, c_bits, clip, h, st);

@@ -167,15 +167,15 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
         if (MODE == 1 || MODE == 3) sq += u * u;
       }
       if (MODE != 1 && MODE != 4) {
-        float p = to_f<T>(P[i]);
+        pval_t<T> p = pv_of<T>(P[i]);
         if constexpr (SR) {
           const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : (h.wd_mode ? wdec : 1.0f));
           P[i] = sr_round<T>(p * dec - step * u, D.sr_seed, h.sr_step, (uint64_t)i);
         } else {
-          if (D.decay) p = p * *D.decay;
-          else if (h.has_decay) p = p * h.decay_val;
-          else if (h.wd_mode) p = p * wdec;
-          P[i] = from_f<T>(__builtin_fmaf(-step, u, p));
+          if (D.decay) p = pdec(p, *D.decay);
+          else if (h.has_decay) p = pdec(p, h.decay_val);
+          else if (h.wd_mode) p = pdec(p, wdec);
+          P[i] = pv_to<T>(pupd(step, u, p));
         }
       }
     }
@@ -229,6 +229,7 @@ static int launch_full_any(int dtype, int stochastic, int mode, const DescFull& 
     case A8_F16:
       return stochastic ? launch_full<__half, true>(mode, one, tab, ntab, nwg, h, st)
                         : launch_full<__half, false>(mode, one, tab, ntab, nwg, h, st);
+    case A8_F64: return launch_full<double, false>(mode, one, tab, ntab, nwg, h, st);
     default: return set_error(A8_ERR_DTYPE, "unsupported param dtype");
   }
 }

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
       }
       const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
       const bool use_dec = D.decay != nullptr || h.has_decay;
-      float p[8];
+      pval_t<T> p[8];   // double for fp64 parameters
       load8<T>(reinterpret_cast<const T*>(D.param), e0, n, p);
       if constexpr (SR) {
         T* P = reinterpret_cast<T*>(D.param);
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
                                                (uint64_t)(e0 + k));
       } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) p[k] = __builtin_fmaf(-step, u[k], use_dec ? p[k] * dec : p[k]);
+        for (int k = 0; k < 8; ++k) p[k] = pupd(step, u[k], use_dec ? pdec(p[k], dec) : p[k]);
         store8<T>(reinterpret_cast<T*>(D.param), e0, n, p);
       }
     }
@@ -190,6 +190,9 @@ static int launch_sgd(int dtype, int stochastic, int mode, int kind, int64_t nwg
     case A8_F16:
       return stochastic ? launch_t<__half, true>(mode, kind, nwg, st, one, tab, ntab, h)
                         : launch_t<__half, false>(mode, kind, nwg, st, one, tab, ntab, h);
+    case A8_F64:
+      if (mode == 3) return set_error(A8_ERR_DTYPE, "the momentum EMA input must be fp32, bf16 or fp16");
+      return launch_t<double, false>(mode, kind, nwg, st, one, tab, ntab, h);
     default: return set_error(A8_ERR_DTYPE, "unsupported dtype");
   }
 }

@@ -171,12 +171,13 @@ __device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int
 
   // ---- stream loads, issued before the decode table and its barrier so that
   // their latency overlaps the table build
-  float g[kEPT], pin[kEPT];
+  float g[kEPT];
+  pval_t<T> pin[kEPT];   // parameter values (double for fp64 parameters)
   uint32_t vq8[2] = {0u, 0u}, mq8[2] = {0u, 0u}, mq4[2] = {0u, 0u};
   u32x2 vq16[2] = {{0u, 0u}, {0u, 0u}};
   float ms[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int k = 0; k < kEPT; ++k) { g[k] = 0.0f; pin[k] = 0.0f; }
+  for (int k = 0; k < kEPT; ++k) { g[k] = 0.0f; pin[k] = 0; }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     if (vok[j]) {
@@ -433,15 +434,15 @@ __device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int
             }
           }
         } else {
-          float p[4];
+          pval_t<T> p[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) p[i] = pin[4 * j + i];
           if (has_dec) {  // decoupled weight decay: p*decay rounded, then the update (optimizer.py:2039)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = p[i] * dec;
+            for (int i = 0; i < 4; ++i) p[i] = pdec(p[i], dec);
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) p[i] = __builtin_fmaf(-step, uu[4 * j + i], p[i]);
+          for (int i = 0; i < 4; ++i) p[i] = pupd(step, uu[4 * j + i], p[i]);
           store4n<T>(Pu, lo[j], nrem, p);
         }
       }
@@ -705,6 +706,7 @@ static int launch_any(int dtype, int sr, int vbits, int mode, const Desc1D& one,
     case A8_F16:
       return sr ? launch_dispatch<__half, true>(vbits, mode, one, table, ntab, nwg, h, st)
                 : launch_dispatch<__half, false>(vbits, mode, one, table, ntab, nwg, h, st);
+    case A8_F64: return launch_dispatch<double, false>(vbits, mode, one, table, ntab, nwg, h, st);
     default: return set_error(A8_ERR_DTYPE, "unsupported param dtype");
   }
 }
@@ -719,7 +721,8 @@ static int check_common(int dtype, int64_t numel, int bv, int bm, int mbits, int
                                    "m_block_size a power of two in [32, block_size]");
   if (has_m && !((mbits == 8 || mbits == 4) && (mmode == 0 || mmode == 1)))
     return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
-  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16) return set_error(A8_ERR_DTYPE, "dtype");
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
+    return set_error(A8_ERR_DTYPE, "dtype");
   return 0;
 }
 

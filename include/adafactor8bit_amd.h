@@ -37,6 +37,12 @@ extern "C" {
 #define A8_F32 0
 #define A8_BF16 1
 #define A8_F16 2
+/* fp64 parameters (the reference's kernels dispatch double too,
+ * AT_DISPATCH_FLOATING_TYPES_AND2, kernels.cu:840): the gradient is read as fp32
+ * and the parameter takes its update in double, as the reference's PyTorch path
+ * does on a float64 tensor.  Accepted by the 1-D (quantised and fp32-state), SGD
+ * and factored steps; no stochastic rounding. */
+#define A8_F64 3
 
 /* kernel modes (kernels.cu:19-24): single pass, norm pass, apply pass, lagged norm */
 #define A8_MODE_NOCLIP 0

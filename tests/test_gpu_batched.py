@@ -8,8 +8,8 @@ _dispatch_1d_cuda per parameter, optimizer.py:1080-1170, with _apply_fira_cuda,
 agree.  They are not bit-identical: the NORM pass adds each wave's sum of u^2
 into the tensor's norm buffer with a float atomic add (as the reference's
 kernels do), so the last bit of the clip norm depends on the order the waves
-finish, in either form.  Parameters therefore agree to rtol 1e-6 and codes to
-the parity bar (at most 1e-4 of codes, by one).  The reference-written fixtures
+finish, in either form.  Parameters therefore agree to rtol 1e-6 plus 1e-5 of
+the tensor's largest displacement, and codes to the parity bar (at most 1e-4 of codes, by one).  The reference-written fixtures
 adamw_clip_fira_wd and adafactor_mom1d_fira pin the arithmetic itself
 (tests/test_gpu_golden.py), through this batched path.
 """
@@ -58,7 +58,8 @@ def test_q1d_clip_batched_equals_per_tensor(case):
         runs.append((params, opt))
     (pa, oa), (pb, ob) = runs
     for i, (a, b) in enumerate(zip(pa, pb)):
-        torch.testing.assert_close(a.detach().float(), b.detach().float(), rtol=1e-6, atol=1e-9,
+        disp = float((a.detach().float().cpu() - init[i].float()).abs().max())
+        torch.testing.assert_close(a.detach().float(), b.detach().float(), rtol=1e-6, atol=1e-5 * disp,
                                    msg=lambda m: f"{case} p{i}: {m}")
         sa, sb = oa.state[a], ob.state[b]
         assert "variance_q" in sa, f"{case} p{i}: expected quantised state"

@@ -434,9 +434,11 @@ def _check_block_sizes(group):
     """Raise ValueError if a parameter of ``group`` would reach a kernel that cannot
     run its block sizes.  The constructor already enforces the reference's own
     rules (optimizer.py:1395-1416: B_V a multiple of 128, B_M a multiple of 4 and
-    at least 32, B_V % B_M == 0).  On top of those, the kernels here take:
-      * quantised 1-D V (AL8/AL16): B_V a power of two in [128, 2048], and coded
-        momentum with it a power of two in [32, B_V];
+    at least 32, B_V % B_M == 0).  The kernels here take:
+      * quantised 1-D V (AL8/AL16) with coded momentum or none: every size those
+        rules allow, up to B_V = 65536 (powers of two in [128, 2048] take the unit
+        layout, the others one workgroup per V block);
+      * quantised 1-D V with fp32 momentum: B_V a power of two in [128, 2048];
       * coded momentum elsewhere (SGD, factored, fp32-V 1-D, APOLLO): B_M a power
         of two in [32, 2048];
       * APOLLO's coded low-rank V and CAME residual / confidence: B_V a power of
@@ -464,10 +466,13 @@ def _check_block_sizes(group):
             route, need_v, need_m = "factored", False, coded_m
         else:
             route, need_v, need_m = "full-rank", vqt != "fp32", coded_m
-            if need_v and need_m and not _pow2_in(mbs, 32, bs):
-                raise ValueError(
-                    f"m_block_size={mbs} with block_size={bs}: the fused {route} kernel of this build needs "
-                    f"m_block_size to be a power of two in [32, block_size].")
+            if need_v and (need_m or beta1 is None):
+                # the fused 1-D kernels: any size the reference accepts, up to 65536
+                if bs > 65536:
+                    raise ValueError(
+                        f"block_size={bs}: the fused {route} kernels of this build take at most 65536 "
+                        f"(parameter of shape {tuple(p.shape)}).")
+                continue
         if need_v and not _pow2_in(bs, 128, 2048):
             raise ValueError(
                 f"block_size={bs}: the {route} kernels of this build need a power of two in [128, 2048] "

@@ -64,6 +64,7 @@ struct Hyper1D {
   int has_decay;
   uint64_t sr_step;
   const a8_step_scalars* dsc;   // if set: bv, eps_d, alpha_val, decay_val and sr_step come from here
+  int gen;          // block sizes the unit layout cannot take: k_update1d_gen, one V block per workgroup
 };
 
 // ------------------------------------------------------------ main kernel
@@ -646,20 +647,292 @@ void k_update1d(Desc1D one, const Desc1D* __restrict__ table, int ntab, Hyper1D 
   else unit_step<T, VB, MODE, SR, MK, false>(D, h, wl, s_lds);
 }
 
+// ------------------------------------------------------------ any block size
+// The reference accepts any B_V that is a multiple of 128 and any B_M that is a
+// multiple of 4, at least 32 and a divisor of B_V (optimizer.py:1395-1416).  The
+// unit layout above needs powers of two; every other size takes this kernel: one
+// workgroup per V block, lanes over its quads (four consecutive elements: a quad
+// never straddles an M block, since B_M % 4 == 0), block statistics through LDS
+// (the V max and non-zero minimum, one M absmax per M block of the V block, all
+// exact max/min).  Pass 1 forms v', m', u, writes p (and v_buf in NORM) and the
+// statistics; pass 2, after the block fit, forms v' and m' again from the same
+// inputs (the same bits) and writes the codes.  The element arithmetic is
+// unit_step's, element for element.
+constexpr int kGenMaxBV = 65536;
+constexpr int kGenMaxMB = kGenMaxBV / 32;
+
+template <typename T, int VB, int MODE, bool SR, int MK>
+__global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1D* __restrict__ table, int ntab,
+                                                         Hyper1D h) {
+  constexpr bool kHasM = MK != 0;
+  constexpr bool kVbuf = MODE == 2 || MODE == 4;
+  constexpr bool kSq = MODE == 1 || MODE == 3 || MODE == 4;
+  constexpr bool kWrite = MODE == 0 || MODE == 2 || MODE == 3;
+  constexpr float LM2 = VB == 8 ? 254.0f : 65534.0f;
+  __shared__ float s_tab[256];
+  __shared__ uint32_t s_st[2];           // V max bits, V non-zero minimum key
+  __shared__ float s_fit[2];             // new l_min, scale
+  __shared__ uint32_t s_mab[kGenMaxMB];  // |m'| max bits per M block of this V block
+  if (h.dsc) {
+    const a8_step_scalars sc = load_step_scalars(h.dsc);
+    h.bv = (float)sc.beta_val;
+    h.eps_d = sc.eps_d;
+    h.alpha_val = sc.alpha;
+    h.decay_val = sc.decay;
+    h.sr_step = sc.step;
+  }
+  const Desc1D D = table != nullptr ? load_desc(table, ntab, (int)blockIdx.x) : one;
+  const int lane = threadIdx.x;
+  const int BV = h.block_size, BM = h.m_block_size;
+  const int64_t blk = (int64_t)blockIdx.x - D.wg_begin;
+  const int64_t n = D.numel, base = blk * BV;
+  const int nq = BV >> 2;
+  const int mpb = kHasM ? BV / BM : 0;                        // M blocks per V block
+  const int64_t nmb = kHasM ? (n + BM - 1) / BM : 0;          // M blocks of the tensor
+  const int mk = (MK == 1) ? 1 : h.mk;
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  T* P = reinterpret_cast<T*>(D.param);
+  const float s_old = kVbuf ? 0.0f : gp(D.v_scale)[blk], lm_old = kVbuf ? 0.0f : gp(D.v_min_log)[blk];
+  if (lane == 0) { s_st[0] = 0u; s_st[1] = 0xFFFFFFFFu; }
+  for (int i = lane; i < mpb; i += kLanes) s_mab[i] = 0u;
+  if (VB == 8 && !kVbuf) s_tab[lane] = lane ? exp2_exact(((float)(lane - 1) * s_old) / 254.0f + lm_old) : 0.0f;
+  __syncthreads();
+
+  // step scale (unit_step's)
+  float step = 0.0f, ut_clip = 1.0f;
+  if constexpr (MODE != 1) {
+    float a = D.alpha ? *gp(D.alpha) : h.alpha_val;
+    if (MODE == 2 && D.fira_scale) a = a * *gp(D.fira_scale);
+    if constexpr (MODE == 0) {
+      step = a;
+    } else {
+      float denom = 1.0f;
+      if (h.d > 0.0f) {
+        const float nrm = (MODE == 2) ? sqrtf(*gp(D.norm_buf))
+                          : (MODE == 4 ? sqrtf(*gp(D.prev_norm)) : *gp(D.prev_norm));
+        if (h.momentum_only && kHasM)
+          denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
+        else
+          denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));
+      }
+      if (h.momentum_only && kHasM) { step = a; ut_clip = denom; }
+      else { step = a / denom; }
+    }
+  }
+  const bool mom = kHasM && h.momentum_only;
+
+  // v' and m' of quad q (elements beyond the tensor: zero), and the quad's M block
+  auto quad_state = [&](int q, float* g, float* vn, float* mn, float* inv, int& cnt, int& mb, bool& m_ok) {
+    const int64_t i0 = base + 4 * q;
+    cnt = i0 >= n ? 0 : (n - i0 >= 4 ? 4 : (int)(n - i0));
+    load4n<T>(G, i0, n, g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g[k] = scrub(g[k]);
+    if constexpr (kVbuf) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) vn[k] = k < cnt ? gp(D.v_buf)[i0 + k] : 0.0f;
+    } else {
+      float vo[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t c;
+        if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(D.v_q))[i0 + k];
+        else c = gp(reinterpret_cast<const uint16_t*>(D.v_q))[i0 + k];
+        vo[k] = (VB == 8) ? s_tab[c] : (c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f);
+        float gsq = g[k] * g[k];
+        if (h.eps_g != 0.0f) gsq = gsq + h.eps_g;
+        vn[k] = fabsf(h.bv) < 0.5f ? __builtin_fmaf(h.bv, gsq - vo[k], vo[k])
+                                   : __builtin_fmaf(h.bv - 1.0f, gsq - vo[k], gsq);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (mom) inv[k] = 1.0f / sqrtf(fmaxf(vn[k], h.eps_sq));
+      else if (h.adam_denom) inv[k] = fast_rcp(fast_sqrt(vn[k]) + h.eps_d);
+      else inv[k] = __builtin_amdgcn_rsqf(fmaxf(vn[k], h.eps_sq));
+    }
+    mb = kHasM ? (4 * q) / BM : 0;
+    m_ok = kHasM && blk * mpb + mb < nmb;
+    if constexpr (kHasM) {
+      float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (m_ok) {
+        const float ms = gp(D.m_scale)[blk * mpb + mb];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t e = i0 + k;
+          uint32_t c;
+          if (mk == 2 || mk == 4) {
+            const uint32_t byte = gp(D.m_q)[e >> 1];
+            c = (e & 1) ? (byte & 0x0Fu) : (byte >> 4);
+          } else {
+            c = gp(D.m_q)[e];
+          }
+          mo[k] = m_decode(mk, c, ms);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float x = g[k];
+        if (mom) {
+          x = g[k] * inv[k];
+          if (ut_clip != 1.0f) x = x / ut_clip;
+        }
+        mn[k] = fabsf(h.w_m) < 0.5f ? __builtin_fmaf(h.w_m, x - mo[k], mo[k])
+                                    : __builtin_fmaf(h.w_m - 1.0f, x - mo[k], x);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; }
+  };
+
+  // ---- pass 1: update, parameter, statistics
+  float sq = 0.0f;
+  uint32_t vmax = 0u, vkey = 0xFFFFFFFFu;
+  for (int q = lane; q < nq; q += kLanes) {
+    float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4], uu[4];
+    int cnt, mb;
+    bool m_ok;
+    quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
+    const int64_t i0 = base + 4 * q;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uu[k] = kHasM ? (mom ? mn[k] : mn[k] * inv[k]) : g[k] * inv[k];
+      if (k >= cnt) uu[k] = 0.0f;
+      if constexpr (kSq) {
+        const float t = (MODE == 4) ? mn[k] : ((mom && k < cnt) ? g[k] * inv[k] : uu[k]);
+        sq = __builtin_fmaf(t, t, sq);
+      }
+      vmax = max(vmax, __float_as_uint(vn[k]));
+      vkey = min(vkey, __float_as_uint(vn[k]) - 1u);
+    }
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < cnt) gp(D.v_buf)[i0 + k] = vn[k];
+    }
+    if constexpr (kWrite && kHasM) {
+      uint32_t ab = 0u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ab = max(ab, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
+      if (m_ok) atomicMax(&s_mab[mb], ab);
+    }
+    if constexpr (kWrite) {
+      const bool has_dec = D.decay || h.has_decay;
+      const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k >= cnt) continue;
+        if constexpr (SR) {
+          const float pv = ld1<T>(P, i0 + k);
+          const T r = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(i0 + k));
+          uint16_t bits;
+          __builtin_memcpy(&bits, &r, 2);
+          gp(reinterpret_cast<uint16_t*>(P))[i0 + k] = bits;
+        } else {
+          pval_t<T> pv = ld1<T, pval_t<T>>(P, i0 + k);
+          if (has_dec) pv = pdec(pv, dec);
+          st1<T>(P, i0 + k, pupd(step, uu[k], pv));
+        }
+      }
+    }
+  }
+  if constexpr (!kVbuf) {
+    vmax = grp_red_u(vmax, 64, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+    vkey = grp_umin(vkey, 64);
+    if ((lane & 63) == 0) {
+      atomicMax(&s_st[0], vmax);
+      atomicMin(&s_st[1], vkey);
+    }
+  }
+  if constexpr (kSq) {
+    const float t = grp_sum(sq, 64);
+    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+  }
+  __syncthreads();
+  if constexpr (kVbuf && !(kWrite && kHasM)) return;   // MNORM: no state written
+
+  // ---- block fit (one lane pair) and pass 2: codes
+  ALFit f{};
+  if constexpr (!kVbuf) {
+    if (lane < 64) {
+      const uint32_t key = s_st[1];
+      const float mnz = key == 0xFFFFFFFFu ? __builtin_inff() : __uint_as_float(key + 1u);
+      const ALFit ft = al_refit_pair(__uint_as_float(s_st[0]), mnz, h.floor_, LM2, lane);
+      if (lane == 0) { s_fit[0] = ft.lmin; s_fit[1] = ft.s; }
+    }
+    __syncthreads();
+    f.lmin = s_fit[0];
+    f.s = s_fit[1];
+    al_fit_consts(f, LM2);
+  }
+  for (int q = lane; q < nq; q += kLanes) {
+    float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4];
+    int cnt, mb;
+    bool m_ok;
+    quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
+    const int64_t i0 = base + 4 * q;
+    if constexpr (!kVbuf) {
+      uint32_t code[4];
+      al_codes<(int)LM2, 4>(vn, f, code);
+      if constexpr (VB == 8) {
+        *gp(reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(D.v_q) + i0)) =
+            code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+      } else {
+        *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(D.v_q) + i0)) =
+            u32x2{code[0] | (code[1] << 16), code[2] | (code[3] << 16)};
+      }
+    }
+    if constexpr (kWrite && kHasM) {
+      if (m_ok) {
+        const float am = fmaxf(__uint_as_float(s_mab[mb]), 1e-12f);
+        const float ram = fast_rcp(am);
+        if (mk == 2 || mk == 4) {
+          const uint32_t w = ((m_encode(mk, mn[0], am, ram) << 4) | m_encode(mk, mn[1], am, ram)) |
+                             (((m_encode(mk, mn[2], am, ram) << 4) | m_encode(mk, mn[3], am, ram)) << 8);
+          *gp(reinterpret_cast<uint16_t*>(D.m_q + (i0 >> 1))) = (uint16_t)w;
+        } else {
+          uint32_t w = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) w |= m_encode(mk, mn[k], am, ram) << (8 * k);
+          *gp(reinterpret_cast<uint32_t*>(D.m_q + i0)) = w;
+        }
+      }
+    }
+  }
+  __syncthreads();   // every lane has read the old block metadata
+  if (!kVbuf && lane == 0) { gp(D.v_scale)[blk] = f.s; gp(D.v_min_log)[blk] = f.lmin; }
+  if constexpr (kWrite && kHasM) {
+    for (int i = lane; i < mpb; i += kLanes)
+      if (blk * mpb + i < nmb) gp(D.m_scale)[blk * mpb + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+  }
+}
+
 // ------------------------------------------------------------ launch glue
 static bool fast_shape_ok(int bv, int bm) {
   auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
   return pow2(bv) && bv >= 128 && bv <= 2048 && pow2(bm) && bm >= 32 && bm <= bv;
 }
+// The reference's rules (optimizer.py:1395-1416), up to kGenMaxBV.
+static bool gen_shape_ok(int bv, int bm) {
+  return bv >= 128 && bv % 128 == 0 && bv <= kGenMaxBV && bm >= 32 && bm % 4 == 0 && bv % bm == 0;
+}
+// Elements per workgroup of the chosen kernel.
+static int64_t unit_of(int bv, int bm) { return fast_shape_ok(bv, bm) ? kWGElems : bv; }
 
 template <typename T, int VB, int MODE, bool SR, int MK>
 static int launch_t(const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg, const Hyper1D& h,
                     hipStream_t st) {
-  const int nv_wg = kWGElems / h.block_size;
+  const int nv_wg = h.gen ? 1 : kWGElems / h.block_size;
   size_t lds = ((VB == 8 && MODE != 2 && MODE != 4) ? (size_t)nv_wg * 256 : 0) * sizeof(float) +
                48 * sizeof(float);
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
+  if (h.gen) {
+    hipLaunchKernelGGL((k_update1d_gen<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), 0, st, one,
+                       table, ntab, h);
+    return check_launch("k_update1d_gen");
+  }
   hipLaunchKernelGGL((k_update1d<T, VB, MODE, SR, MK>), dim3((unsigned)nwg), dim3(kLanes), lds, st, one,
                      table, ntab, h);
   return check_launch("k_update1d");
@@ -716,9 +989,9 @@ static int check_common(int dtype, int64_t numel, int bv, int bm, int mbits, int
   if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
   if (vbits != 8 && vbits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
   if (!has_m) bm = bv;
-  if (!fast_shape_ok(bv, bm))
-    return set_error(A8_ERR_BLOCK, "block_size must be a power of two in [128, 2048] and "
-                                   "m_block_size a power of two in [32, block_size]");
+  if (!fast_shape_ok(bv, bm) && !gen_shape_ok(bv, bm))
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 (at most 65536) and m_block_size a "
+                                   "multiple of 4, at least 32, that divides block_size");
   if (has_m && !((mbits == 8 || mbits == 4) && (mmode == 0 || mmode == 1)))
     return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
@@ -783,7 +1056,9 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   h.adam_denom = use_adam_denom; h.momentum_only = momentum_only;
   h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
   h.sr_step = sr_step;
-  const int64_t nwg = (numel + kWGElems - 1) / kWGElems;
+  h.gen = fast_shape_ok(h.block_size, h.m_block_size) ? 0 : 1;
+  const int64_t unit = unit_of(h.block_size, h.m_block_size);
+  const int64_t nwg = (numel + unit - 1) / unit;
   return launch_any(dtype, sr, v_bits, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
 }
 
@@ -801,6 +1076,7 @@ static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int n
   if (mode == 4 && !momentum_only) return set_error(A8_ERR_ARG, "MNORM needs momentum_only");
   Desc1D* tab = reinterpret_cast<Desc1D*>(image);
   int32_t* first = image ? reinterpret_cast<int32_t*>(image + sizeof(Desc1D) * (size_t)ntensors) : nullptr;
+  const int64_t unit = unit_of(block_size, has_m ? m_block_size : block_size);
   int64_t wg = 0;
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor1d& t = tensors[i];
@@ -826,7 +1102,7 @@ static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int n
       const int32_t f = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
       std::memcpy(&first[i], &f, sizeof(int32_t));
     }
-    wg += (t.numel + kWGElems - 1) / kWGElems;
+    wg += (t.numel + unit - 1) / unit;
   }
   if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "too many workgroups");
   *nwg_out = wg;
@@ -851,6 +1127,7 @@ static int launch_multi_1d(int mode, int stochastic, int dtype, bool has_m, int 
   h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay;
   h.sr_step = sr_step;
   h.dsc = reinterpret_cast<const a8_step_scalars*>(dsc);
+  h.gen = fast_shape_ok(h.block_size, h.m_block_size) ? 0 : 1;
   Desc1D none{};
   return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev), ntensors,
                     nwg, h, st);

@@ -15,16 +15,20 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
 
 @pytest.mark.parametrize("kw,shapes,ok", [
     (dict(ADAMW, block_size=2048, m_block_size=256), [(64, 64)], True),
-    (dict(ADAMW, block_size=384, m_block_size=128), [(64, 64)], False),     # quantised 1-D V
+    (dict(ADAMW, block_size=384, m_block_size=128), [(64, 64)], True),      # quantised 1-D V: any size
+    (dict(ADAMW, block_size=1152, m_block_size=36), [(64, 64)], True),
+    (dict(ADAMW, block_size=6400, m_block_size=100, m_quant_type="uf4"), [(64, 64)], True),
+    (dict(ADAMW, block_size=131072, m_block_size=256), [(64, 64)], False),   # beyond 65536
+    (dict(ADAMW, block_size=384, m_block_size=128, m_quant_type="fp32"), [(64, 64)], False),  # fp32 M: AL EMA
     (dict(ADAMW, block_size=384, m_block_size=128), [(63, 64)], True),      # below min_8bit_size
     (dict(ADAMW, block_size=384, m_block_size=128, quantize=False), [(64, 64)], True),
     (dict(ADAMW, block_size=384, m_block_size=128, v_quant_type="fp32", m_quant_type="fp32"), [(64, 64)], True),
-    (dict(ADAMW, block_size=2048, m_block_size=36), [(64, 64)], False),      # momentum block
-    (dict(ADAMW, block_size=4096, m_block_size=256), [(64, 64)], False),
+    (dict(ADAMW, block_size=2048, m_block_size=36), [(64, 64)], False),      # 36 does not divide 2048
+    (dict(ADAMW, block_size=4096, m_block_size=256), [(64, 64)], True),
     (dict(lr=1e-3, relative_step=False, block_size=384), [(64, 64)], True),  # factored, no momentum
     (dict(lr=1e-3, relative_step=False, beta1=0.9, block_size=384, m_block_size=128), [(64, 64)], True),
     (dict(lr=1e-3, relative_step=False, beta1=0.9, block_size=1024, m_block_size=100), [(64, 64)], False),
-    (dict(lr=1e-3, relative_step=False, block_size=384), [(4096,)], False),  # 1-D vector of a factored group
+    (dict(lr=1e-3, relative_step=False, block_size=384), [(4096,)], True),   # 1-D vector of a factored group
     (dict(ADAMW, apollo_rank=8, block_size=640, m_block_size=128), [(64, 64)], False),
     (dict(ADAMW, apollo_rank=8, block_size=2048, m_block_size=256), [(64, 64)], True),
     (dict(lr=1e-2, beta1=0.9, beta2=None, beta2_decay=None, relative_step=False, m_block_size=36), [(64, 64)],
@@ -40,7 +44,8 @@ def test_block_sizes_checked_at_construction(kw, shapes, ok):
 
 def test_add_param_group_rejects_and_leaves_groups_unchanged():
     opt, _ = _opt([(64, 64)], **dict(ADAMW))
-    bad = {"params": [torch.nn.Parameter(torch.zeros(5000))], "block_size": 384, "m_block_size": 128}
+    bad = {"params": [torch.nn.Parameter(torch.zeros(5000))], "block_size": 384, "m_block_size": 128,
+           "m_quant_type": "fp32"}
     with pytest.raises(ValueError):
         opt.add_param_group(bad)
     assert len(opt.param_groups) == 1

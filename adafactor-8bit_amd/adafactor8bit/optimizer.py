@@ -438,9 +438,11 @@ def _check_block_sizes(group):
       * quantised 1-D V (AL8/AL16) with coded momentum or none: every size those
         rules allow, up to B_V = 65536 (powers of two in [128, 2048] take the unit
         layout, the others one workgroup per V block);
+      * coded momentum on the SGD route and with fp32 V on the 1-D route: any
+        multiple of 4 from 32 to 65536;
       * quantised 1-D V with fp32 momentum: B_V a power of two in [128, 2048];
-      * coded momentum elsewhere (SGD, factored, fp32-V 1-D, APOLLO): B_M a power
-        of two in [32, 2048];
+      * coded momentum on the factored and APOLLO routes: B_M a power of two in
+        [32, 2048];
       * APOLLO's coded low-rank V and CAME residual / confidence: B_V a power of
         two in [128, 2048].
     The factored row / column statistics take any B_V."""
@@ -453,34 +455,38 @@ def _check_block_sizes(group):
     sgd = group.get("beta2") is None and group.get("beta2_decay") is None
     min8 = group.get("min_8bit_size", 4096)
     coded_m = beta1 is not None and mqt != "fp32"
+
+    def need(ok, what, size, rule):
+        if not ok:
+            raise ValueError(f"{what}={size}: the {route} kernels of this build need {rule} "
+                             f"(parameter of shape {tuple(p.shape)}).")
+
     for p in group["params"]:
         if p.numel() < min8:
             continue
+        any_m = 32 <= mbs <= 65536 and mbs % 4 == 0
         if sgd:
-            route, need_v, need_m = "SGD", False, coded_m
+            route = "SGD"
+            if coded_m:
+                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
         elif group.get("apollo_rank", 0) > 0 and p.dim() >= 2:
             route = "APOLLO"
-            need_v = vqt != "fp32" or (beta3 is not None and cqt != "fp32")
-            need_m = coded_m
+            if vqt != "fp32" or (beta3 is not None and cqt != "fp32"):
+                need(_pow2_in(bs, 128, 2048), "block_size", bs, "a power of two in [128, 2048]")
+            if coded_m:
+                need(_pow2_in(mbs, 32, 2048), "m_block_size", mbs, "a power of two in [32, 2048]")
         elif p.dim() >= 2 and group.get("factored", True):
-            route, need_v, need_m = "factored", False, coded_m
+            route = "factored"
+            if coded_m:
+                need(_pow2_in(mbs, 32, 2048), "m_block_size", mbs, "a power of two in [32, 2048]")
         else:
-            route, need_v, need_m = "full-rank", vqt != "fp32", coded_m
-            if need_v and (need_m or beta1 is None):
-                # the fused 1-D kernels: any size the reference accepts, up to 65536
-                if bs > 65536:
-                    raise ValueError(
-                        f"block_size={bs}: the fused {route} kernels of this build take at most 65536 "
-                        f"(parameter of shape {tuple(p.shape)}).")
-                continue
-        if need_v and not _pow2_in(bs, 128, 2048):
-            raise ValueError(
-                f"block_size={bs}: the {route} kernels of this build need a power of two in [128, 2048] "
-                f"(parameter of shape {tuple(p.shape)}).")
-        if need_m and not _pow2_in(mbs, 32, 2048):
-            raise ValueError(
-                f"m_block_size={mbs}: the {route} kernels of this build need a power of two in [32, 2048] "
-                f"(parameter of shape {tuple(p.shape)}).")
+            route = "full-rank"
+            if vqt != "fp32" and (coded_m or beta1 is None):
+                need(bs <= 65536, "block_size", bs, "at most 65536")
+            elif vqt != "fp32":   # fp32 momentum: the stand-alone AL EMA
+                need(_pow2_in(bs, 128, 2048), "block_size", bs, "a power of two in [128, 2048]")
+            elif coded_m:         # fp32 V: the stand-alone momentum EMA
+                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
 
 
 # ====================================================================== planning

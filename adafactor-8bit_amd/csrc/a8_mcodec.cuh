@@ -193,8 +193,7 @@ __device__ __forceinline__ void mq_encode8(int mk, uint8_t* m_q, float* m_scale,
   uint32_t ab = 0u;
 #pragma unroll
   for (int k = 0; k < 8; ++k) ab = max(ab, __float_as_uint(m[k]) & 0x7FFFFFFFu);
-  float bam = __uint_as_float(ab);
-  for (int o = 1; o < (ML < 64 ? ML : 64); o <<= 1) bam = fmaxf(bam, __shfl_xor(bam, o, 64));
+  float bam = grp_max(__uint_as_float(ab), ML < 64 ? ML : 64);
   if (ML > 64) {
     if ((lane & 63) == 0) xw[wave] = bam;
     __syncthreads();

@@ -50,6 +50,9 @@ struct SgdHyp {
   int lbm;          // log2(B_M)
   int mk;           // 1 UF8, 2 UF4, 3 D8, 4 D4
   uint64_t sr_step;
+  int gen;          // B_M not a power of two in [32, 2048]: k_sgd_gen over units of `unit` elements
+  int bm;           // B_M (gen)
+  int unit;         // elements per workgroup (gen): a whole number of M blocks
 };
 
 __device__ __forceinline__ const SgdDesc* find_sgd(const SgdDesc* tab, int n, int64_t wg) {
@@ -155,9 +158,169 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
   if constexpr (MODE != 1 && MK == 1) mq_encode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, m, ML, xw);
 }
 
+// Coded momentum with a block size the reference accepts but the unit layout
+// cannot take (B_M a multiple of 4, at least 32, not a power of two in
+// [32, 2048]; up to 65536).  One workgroup covers `unit` elements: floor(2048 /
+// B_M) whole M blocks (one block when B_M > 2048).  Lanes take quads (a quad never
+// straddles a block, B_M % 4 == 0); each block's absmax meets in LDS (an exact
+// max).  Pass 1 forms m' and u and writes p (or m_out); pass 2, after the
+// absmaxes, forms m' again from the same inputs and writes the codes.  The
+// arithmetic is k_sgd's, element for element.
+constexpr int kSGenMaxMB = 64;
+
+template <typename T, int MODE, bool SR>
+__global__ __launch_bounds__(kSLanes) void k_sgd_gen(SgdDesc one, const SgdDesc* __restrict__ table, int ntab,
+                                                     SgdHyp h) {
+  __shared__ uint32_t s_mab[kSGenMaxMB];
+  const SgdDesc D = table ? *find_sgd(table, ntab, (int64_t)blockIdx.x) : one;
+  const int lane = threadIdx.x;
+  const int BM = h.bm, U = h.unit, mpu = U / BM;
+  const int64_t n = D.numel;
+  const int64_t base = ((int64_t)blockIdx.x - D.wg_begin) * U;
+  const int64_t mb0 = base / BM, nmb = (n + BM - 1) / BM;
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  T* P = reinterpret_cast<T*>(D.param);
+  for (int i = lane; i < mpu; i += kSLanes) s_mab[i] = 0u;
+  __syncthreads();
+
+  auto quad = [&](int q, float* g, float* m, int& cnt, int& mb, bool& m_ok) {
+    const int64_t i0 = base + 4 * q;
+    cnt = i0 >= n ? 0 : (n - i0 >= 4 ? 4 : (int)(n - i0));
+    load4n<T>(G, i0, n, g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g[k] = scrub(g[k]);
+    mb = (4 * q) / BM;
+    m_ok = mb0 + mb < nmb;
+    float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (m_ok) {
+      const float ms = gp(D.m_scale)[mb0 + mb];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int64_t e = i0 + k;
+        uint32_t c;
+        if (h.mk == 2 || h.mk == 4) {
+          const uint32_t byte = gp(D.m_q)[e >> 1];
+          c = (e & 1) ? (byte & 0x0Fu) : (byte >> 4);
+        } else {
+          c = gp(D.m_q)[e];
+        }
+        mo[k] = m_decode(h.mk, c, ms);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
+  };
+
+  float step = 0.0f, dec = 1.0f, fsc = 1.0f;   // fsc: the Fira scale of APPLY
+  bool use_dec = false;
+  if constexpr (MODE == 0 || MODE == 2) {
+    const float a = D.alpha ? *D.alpha : h.alpha_val;
+    step = a;
+    if constexpr (MODE == 2) {
+      float sum = *D.norm_buf;
+      if (D.fira) {
+        const bool fin = __builtin_isfinite(sqrtf(sum));   // a non-finite norm zeroes the update
+        fsc = fin ? D.fira[0] : 0.0f;
+        sum = D.fira[2];
+      }
+      if (h.d > 0.0f) step = a / fmaxf(1.0f, sqrtf(sum) / (float)(sqrt((double)n) * (double)h.d));
+    }
+    dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : 1.0f);
+    use_dec = D.decay != nullptr || h.has_decay;
+  }
+
+  // ---- pass 1
+  float sq = 0.0f;
+  for (int q = lane; q < (U >> 2); q += kSLanes) {
+    float g[4], m[4];
+    int cnt, mb;
+    bool m_ok;
+    quad(q, g, m, cnt, mb, m_ok);
+    const int64_t i0 = base + 4 * q;
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float u = m[k] / h.mdiv;
+        sq += u * u;
+      }
+    } else if constexpr (MODE == 3) {
+      if (D.m_out) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (k < cnt) gp(D.m_out)[i0 + k] = m[k];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k >= cnt) continue;
+        float u = m[k] / h.mdiv;
+        if constexpr (MODE == 2) {
+          if (D.fira) u = u * fsc;
+        }
+        if constexpr (SR) {
+          const float pv = ld1<T>(P, i0 + k);
+          const T r = sr_round<T>(__builtin_fmaf(-step, u, pv * dec), D.sr_seed, h.sr_step, (uint64_t)(i0 + k));
+          uint16_t bits;
+          __builtin_memcpy(&bits, &r, 2);
+          gp(reinterpret_cast<uint16_t*>(P))[i0 + k] = bits;
+        } else {
+          const pval_t<T> pv = ld1<T, pval_t<T>>(P, i0 + k);
+          st1<T>(P, i0 + k, pupd(step, u, use_dec ? pdec(pv, dec) : pv));
+        }
+      }
+    }
+    if constexpr (MODE != 1) {
+      uint32_t ab = 0u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ab = max(ab, __float_as_uint(m[k]) & 0x7FFFFFFFu);
+      if (m_ok) atomicMax(&s_mab[mb], ab);
+    }
+  }
+  if constexpr (MODE == 1) {
+    const float t = grp_sum(sq, 64);
+    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+    return;
+  }
+  __syncthreads();
+
+  // ---- pass 2: codes
+  for (int q = lane; q < (U >> 2); q += kSLanes) {
+    float g[4], m[4];
+    int cnt, mb;
+    bool m_ok;
+    quad(q, g, m, cnt, mb, m_ok);
+    if (!m_ok) continue;
+    const int64_t i0 = base + 4 * q;
+    const float am = fmaxf(__uint_as_float(s_mab[mb]), 1e-12f);
+    const float ram = __builtin_amdgcn_rcpf(am);
+    if (h.mk == 2 || h.mk == 4) {
+      const uint32_t w = ((m_encode(h.mk, m[0], am, ram) << 4) | m_encode(h.mk, m[1], am, ram)) |
+                         (((m_encode(h.mk, m[2], am, ram) << 4) | m_encode(h.mk, m[3], am, ram)) << 8);
+      *gp(reinterpret_cast<uint16_t*>(D.m_q + (i0 >> 1))) = (uint16_t)w;
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w |= m_encode(h.mk, m[k], am, ram) << (8 * k);
+      *gp(reinterpret_cast<uint32_t*>(D.m_q + i0)) = w;
+    }
+  }
+  __syncthreads();   // every lane has read the old scales
+  for (int i = lane; i < mpu; i += kSLanes)
+    if (mb0 + i < nmb) gp(D.m_scale)[mb0 + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+}
+
 template <typename T, int MK, bool SR>
 static void launch_mode(int mode, dim3 grid, hipStream_t st, const SgdDesc& one, const SgdDesc* tab, int ntab,
                         const SgdHyp& h) {
+  if (MK == 1 && h.gen) {
+    switch (mode) {
+      case 0: hipLaunchKernelGGL((k_sgd_gen<T, 0, SR>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
+      case 1: hipLaunchKernelGGL((k_sgd_gen<T, 1, SR>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
+      case 2: hipLaunchKernelGGL((k_sgd_gen<T, 2, SR>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
+      default: hipLaunchKernelGGL((k_sgd_gen<T, 3, false>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
+    }
+    return;
+  }
   switch (mode) {
     case 0: hipLaunchKernelGGL((k_sgd<T, MK, 0, SR>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
     case 1: hipLaunchKernelGGL((k_sgd<T, MK, 1, SR>), grid, dim3(kSLanes), 0, st, one, tab, ntab, h); break;
@@ -204,12 +367,22 @@ static int m_codec(int m_bits, int m_mode, int& mk) {
   return 0;
 }
 
-static int block_log2(int bs, int& lb) {
-  if (bs < 32 || bs > kSElems || (bs & (bs - 1)) != 0)
-    return set_error(A8_ERR_BLOCK, "m_block_size must be a power of two in [32, 2048]");
-  lb = 0;
-  while ((1 << lb) < bs) ++lb;
+// The momentum block: a power of two in [32, 2048] takes the unit layout (lbm);
+// any other multiple of 4 from 32 to 65536 takes k_sgd_gen (gen, bm, unit).
+static int block_log2(int bs, SgdHyp& h) {
+  const bool pow2 = bs >= 32 && bs <= kSElems && (bs & (bs - 1)) == 0;
+  if (!pow2 && !(bs >= 32 && bs % 4 == 0 && bs <= 65536))
+    return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
+  h.gen = pow2 ? 0 : 1;
+  h.bm = bs;
+  h.unit = pow2 ? kSElems : bs * (bs < kSElems ? kSElems / bs : 1);
+  h.lbm = 0;
+  while (pow2 && (1 << h.lbm) < bs) ++h.lbm;
   return 0;
+}
+static int64_t units_of(int64_t numel, const SgdHyp& h) {
+  const int64_t u = h.gen ? h.unit : kSElems;
+  return (numel + u - 1) / u;
 }
 
 hipError_t sgd_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
@@ -232,7 +405,7 @@ int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int blo
   SgdHyp h{};
   int rc = m_codec(m_bits, m_mode, h.mk);
   if (rc) return rc;
-  if ((rc = block_log2(block_size, h.lbm))) return rc;
+  if ((rc = block_log2(block_size, h))) return rc;
   h.w_m = (float)(1.0 - beta);
   std::vector<SgdDesc> tab((size_t)n);
   int64_t wg = 0;
@@ -243,7 +416,7 @@ int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int blo
     SgdDesc& D = tab[(size_t)i];
     D.grad = it[i].x; D.m_q = it[i].m_q; D.m_scale = it[i].m_scale; D.m_out = it[i].out; D.numel = it[i].n;
     D.wg_begin = wg;
-    wg += (it[i].n + kSElems - 1) / kSElems;
+    wg += units_of(it[i].n, h);
   }
   if (!table_dev) return launch_sgd(A8_F32, 0, 3, 1, wg, st, tab[0], nullptr, 0, h);
   if (upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)n, st) != hipSuccess)
@@ -280,7 +453,7 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
     kind = 1;
     int rc = m_codec(m_bits, m_mode, h.mk);
     if (rc) return rc;
-    if ((rc = block_log2(m_block_size, h.lbm))) return rc;
+    if ((rc = block_log2(m_block_size, h))) return rc;
   } else if (m) {
     kind = 2;
     h.lbm = 5;
@@ -290,7 +463,7 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
   SgdDesc D{};
   D.param = param; D.grad = grad; D.m_q = m_q; D.m_scale = m_scale; D.m = m; D.norm_buf = norm_buf;
   D.fira = fira; D.alpha = alpha; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
-  return launch_sgd(dtype, stochastic, mode, kind, (numel + kSElems - 1) / kSElems, (hipStream_t)stream, D,
+  return launch_sgd(dtype, stochastic, mode, kind, units_of(numel, h), (hipStream_t)stream, D,
                     nullptr, 0, h);
 }
 
@@ -311,7 +484,7 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
   if (m_kind == 1) {
     int rc = m_codec(m_bits, m_mode, h.mk);
     if (rc) return rc;
-    if ((rc = block_log2(m_block_size, h.lbm))) return rc;
+    if ((rc = block_log2(m_block_size, h))) return rc;
   }
   std::vector<SgdDesc> tab((size_t)ntensors);
   int64_t wg = 0;
@@ -331,7 +504,7 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
     if (m_kind == 1) { D.m_q = t.m_q; D.m_scale = t.m_scale; }
     if (m_kind == 2) D.m = t.m;
     D.wg_begin = wg;
-    wg += (t.numel + kSElems - 1) / kSElems;
+    wg += units_of(t.numel, h);
   }
   hipStream_t st = (hipStream_t)stream;
   if (upload && upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)ntensors, st) != hipSuccess)
@@ -353,11 +526,11 @@ int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype,
   SgdHyp h{};
   int rc = m_codec(m_bits, m_mode, h.mk);
   if (rc) return rc;
-  if ((rc = block_log2(block_size, h.lbm))) return rc;
+  if ((rc = block_log2(block_size, h))) return rc;
   h.w_m = (float)(1.0 - beta);   // lerp weight of _m_ema_pytorch (optimizer.py:699)
   SgdDesc D{};
   D.grad = x; D.m_q = m_q; D.m_scale = m_scale; D.m_out = fp32_out; D.numel = numel;
-  return launch_sgd(x_dtype, 0, 3, 1, (numel + kSElems - 1) / kSElems, (hipStream_t)stream, D, nullptr, 0, h);
+  return launch_sgd(x_dtype, 0, 3, 1, units_of(numel, h), (hipStream_t)stream, D, nullptr, 0, h);
 }
 
 }  // extern "C"

@@ -10,7 +10,8 @@ codes (+1 per tensor) differ, by at most 2; block metadata within rtol 1e-5;
 parameters within rtol 1e-5 except the elements whose codes differed at some
 step, which stay within rtol 2e-3 plus 1% of the largest displacement.  The
 modes: NOCLIP (AdamW, V-only), NORM/APPLY (RMS clip and Fira, batched) and
-MNORM (momentum-only Fira).
+MNORM (momentum-only Fira).  Coded momentum on the SGD route and with fp32 V
+takes k_sgd_gen at such blocks (one workgroup per whole number of M blocks).
 """
 import numpy as np
 import pytest
@@ -36,6 +37,19 @@ CASES = [
     ("mom1d_bv640_bm160_fira", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=False, relative_step=False,
                                     scale_parameter=False, lr=1e-3, block_size=640, m_block_size=160,
                                     enable_fira_for_adafactor=True)),
+]
+SGD = dict(ADAMW, beta2=None, beta2_decay=None, lr=1e-2)
+CASES += [
+    # coded momentum outside the fused 1-D kernel: SGD (k_sgd) and fp32 V with the
+    # stand-alone momentum EMA (a8_m_quantize_lerp), at blocks the unit layout cannot take
+    ("sgd_bv1152_bm36", dict(SGD, block_size=1152, m_block_size=36, weight_decay=0.01)),
+    ("sgd_bv6400_bm100_uf4_clip_fira", dict(SGD, block_size=6400, m_block_size=100, m_quant_type="uf4", d=1.0,
+                                            enable_fira_for_adafactor=True)),
+    ("sgd_bv4608_bm4608_d8", dict(SGD, block_size=4608, m_block_size=4608, m_quant_type="d8")),
+    ("adamw_fp32v_bv6400_bm100", dict(ADAMW, v_quant_type="fp32", block_size=6400, m_block_size=100)),
+    ("mom1d_fp32v_bv1152_bm36_fira", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=False,
+                                          relative_step=False, scale_parameter=False, lr=1e-3, v_quant_type="fp32",
+                                          block_size=1152, m_block_size=36, enable_fira_for_adafactor=True)),
 ]
 SHAPES = [(300, 77), (5000,), (4096,), (9000,)]
 

@@ -31,8 +31,10 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
     (dict(lr=1e-3, relative_step=False, block_size=384), [(4096,)], True),   # 1-D vector of a factored group
     (dict(ADAMW, apollo_rank=8, block_size=640, m_block_size=128), [(64, 64)], False),
     (dict(ADAMW, apollo_rank=8, block_size=2048, m_block_size=256), [(64, 64)], True),
-    (dict(lr=1e-2, beta1=0.9, beta2=None, beta2_decay=None, relative_step=False, m_block_size=36), [(64, 64)],
-     False),                                                                  # SGD with coded momentum
+    (dict(lr=1e-2, beta1=0.9, beta2=None, beta2_decay=None, relative_step=False, block_size=1152,
+          m_block_size=36), [(64, 64)], True),                                # SGD with coded momentum
+    (dict(ADAMW, v_quant_type="fp32", block_size=6400, m_block_size=100), [(64, 64)], True),  # fp32 V, coded M
+    (dict(ADAMW, v_quant_type="fp32", block_size=131072, m_block_size=131072), [(64, 64)], False)
 ])
 def test_block_sizes_checked_at_construction(kw, shapes, ok):
     if ok:

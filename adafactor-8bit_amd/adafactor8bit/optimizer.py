@@ -440,7 +440,8 @@ def _check_block_sizes(group):
         layout, the others one workgroup per V block);
       * coded momentum on the SGD route and with fp32 V on the 1-D route: any
         multiple of 4 from 32 to 65536;
-      * quantised 1-D V with fp32 momentum: B_V a power of two in [128, 2048];
+      * quantised 1-D V with fp32 momentum (the stand-alone AL EMA): any multiple
+        of 128 up to 65536;
       * coded momentum on the factored and APOLLO routes: B_M a power of two in
         [32, 2048];
       * APOLLO's coded low-rank V and CAME residual / confidence: B_V a power of
@@ -484,7 +485,7 @@ def _check_block_sizes(group):
             if vqt != "fp32" and (coded_m or beta1 is None):
                 need(bs <= 65536, "block_size", bs, "at most 65536")
             elif vqt != "fp32":   # fp32 momentum: the stand-alone AL EMA
-                need(_pow2_in(bs, 128, 2048), "block_size", bs, "a power of two in [128, 2048]")
+                need(bs <= 65536, "block_size", bs, "at most 65536")
             elif coded_m:         # fp32 V: the stand-alone momentum EMA
                 need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
 

@@ -487,6 +487,116 @@ __global__ __launch_bounds__(256) void k_vema32(float* __restrict__ v, const GT*
 
 hipError_t prims_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
 
+// AL EMA at a block size the unit layout cannot take (a multiple of 128 that is
+// not a power of two in [128, 2048], up to 65536): one workgroup per block,
+// lanes over its quads.  Pass 1 forms v' (and out), the block max and non-zero
+// minimum meet in LDS (exact); pass 2 forms v' again from the same inputs and
+// writes the codes (and dec).  vema_unit's arithmetic, element for element.
+template <int VB, typename T>
+__global__ __launch_bounds__(256) void k_vema_gen(VemaDesc one, const VemaDesc* __restrict__ tab, int ntab, int bs,
+                                                  float w, int square, float eps1, float floor_) {
+  __shared__ float s_tab[256];   // decode table of the old fit (both passes read it)
+  __shared__ float s_new[256];   // decode table of the new fit (dec)
+  __shared__ uint32_t s_st[2];
+  __shared__ float s_fit[2];
+  const int64_t wg = blockIdx.x;
+  int lo = 0;
+  if (tab) {
+    int hi = ntab - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    }
+  }
+  const VemaDesc d = tab ? tab[lo] : one;
+  const int lane = threadIdx.x;
+  const int64_t blk = wg - d.wg_begin, base = blk * bs, n = d.n;
+  constexpr float LM2 = VB == 8 ? 254.0f : 65534.0f;
+  const T* X = reinterpret_cast<const T*>(d.x);
+  const float s_old = gp(d.scale)[blk], lm_old = gp(d.min_log)[blk];
+  if (lane == 0) { s_st[0] = 0u; s_st[1] = 0xFFFFFFFFu; }
+  if (VB == 8) s_tab[lane] = lane ? exp2_exact(((float)(lane - 1) * s_old) / 254.0f + lm_old) : 0.0f;
+  __syncthreads();
+  auto quad = [&](int q, float* v) {
+    const int64_t i0 = base + 4 * q;
+    float xv[4];
+    load4n<T>(X, i0, n, xv);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float xi = xv[k];
+      if (square) xi = xi * xi + eps1;
+      xi = scrub(xi);
+      float vo = 0.0f;
+      if (i0 + k < n) {
+        uint32_t c;
+        if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(d.q))[i0 + k];
+        else c = gp(reinterpret_cast<const uint16_t*>(d.q))[i0 + k];
+        vo = VB == 8 ? s_tab[c] : (c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f);
+      }
+      v[k] = (i0 + k < n) ? lerp_ref(vo, xi, w) : 0.0f;   // padding quantises as zero
+    }
+  };
+  uint32_t vmax = 0u, vkey = 0xFFFFFFFFu;
+  for (int q = lane; q < (bs >> 2); q += 256) {
+    float v[4];
+    quad(q, v);
+    if (d.out) store4n<float>(d.out, base + 4 * q, n, v);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      vmax = max(vmax, __float_as_uint(v[k]));
+      vkey = min(vkey, __float_as_uint(v[k]) - 1u);
+    }
+  }
+  vmax = grp_red_u(vmax, 64, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+  vkey = grp_umin(vkey, 64);
+  if ((lane & 63) == 0) {
+    atomicMax(&s_st[0], vmax);
+    atomicMin(&s_st[1], vkey);
+  }
+  __syncthreads();
+  if (lane < 64) {
+    const uint32_t key = s_st[1];
+    const float mnz = key == 0xFFFFFFFFu ? __builtin_inff() : __uint_as_float(key + 1u);
+    const ALFit ft = al_refit_pair(__uint_as_float(s_st[0]), mnz, floor_, LM2, lane);
+    if (lane == 0) { s_fit[0] = ft.lmin; s_fit[1] = ft.s; }
+  }
+  __syncthreads();
+  ALFit f{};
+  f.lmin = s_fit[0];
+  f.s = s_fit[1];
+  al_fit_consts(f, LM2);
+  if (d.dec && VB == 8) s_new[lane] = lane ? exp2_exact(((float)(lane - 1) * f.s) / 254.0f + f.lmin) : 0.0f;
+  __syncthreads();
+  for (int q = lane; q < (bs >> 2); q += 256) {
+    float v[4];
+    quad(q, v);
+    uint32_t code[4];
+    al_codes<(int)LM2, 4>(v, f, code);
+    const int64_t i0 = base + 4 * q;
+    if constexpr (VB == 8) {
+      *gp(reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(d.q) + i0)) =
+          code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+    } else {
+      *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(d.q) + i0)) =
+          u32x2{code[0] | (code[1] << 16), code[2] | (code[3] << 16)};
+    }
+    if (d.dec) {
+      float dv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        dv[k] = VB == 8 ? s_new[code[k]]
+                        : (code[k] ? exp2_exact(((float)(code[k] - 1) * f.s) / LM2 + f.lmin) : 0.0f);
+      store4n<float>(d.dec, i0, n, dv);
+    }
+  }
+  __syncthreads();   // every lane has read the old metadata
+  if (lane == 0) { gp(d.scale)[blk] = f.s; gp(d.min_log)[blk] = f.lmin; }
+}
+
+// AL block sizes: powers of two in [128, 2048] take the unit layout; other
+// multiples of 128 up to 65536 take k_vema_gen.
+static bool al_gen_ok(int64_t bs) { return bs >= 128 && bs % 128 == 0 && bs <= 65536; }
+
 static int lb_of(int64_t bs, int lo, int hi, int& lb, const char* what) {
   if (bs < lo || bs > hi || (bs & (bs - 1)) != 0) {
     static char msg[128];
@@ -525,9 +635,10 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
     return 0;
   }
   if (v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
-  int lbv;
-  int rc = lb_of(block_size, 128, kPElems, lbv, "block_size");
-  if (rc) return rc;
+  int lbv = 0;
+  const bool gen = lb_of(block_size, 128, kPElems, lbv, "block_size") != 0;
+  if (gen && !al_gen_ok(block_size))
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
   std::vector<VemaDesc> tab((size_t)n);
   int64_t wg = 0;
   for (int i = 0; i < n; ++i) {
@@ -539,7 +650,7 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
     D.q = t.q; D.scale = t.scale; D.min_log = t.min_log; D.x = t.x; D.out = t.out; D.dec = t.dec; D.n = t.n;
     D.nblk = (t.n + block_size - 1) / block_size;
     D.wg_begin = wg;
-    wg += (D.nblk * block_size + kPElems - 1) / kPElems;
+    wg += gen ? D.nblk : (D.nblk * block_size + kPElems - 1) / kPElems;
   }
   if (wg == 0) return 0;
   if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "AL EMA: too many elements");
@@ -550,6 +661,15 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
     dt = reinterpret_cast<const VemaDesc*>(table_dev);
   }
   const VemaDesc one = tab[0];
+  if (gen) {
+    if (v_bits == 8)
+      hipLaunchKernelGGL((k_vema_gen<8, float>), dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, block_size,
+                         (float)w, square, eps1, log_floor);
+    else
+      hipLaunchKernelGGL((k_vema_gen<16, float>), dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, block_size,
+                         (float)w, square, eps1, log_floor);
+    return check_launch("k_vema_gen");
+  }
   if (v_bits == 8)
     hipLaunchKernelGGL(k_vema_multi<8>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
                        eps1, log_floor);
@@ -574,14 +694,31 @@ int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, i
   if (v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
   if (!aligned16(x) || (fp32_out && !aligned16(fp32_out)))
     return set_error(A8_ERR_ALIGN, "new_val and fp32_out must be 16-byte aligned");
-  int lbv;
-  int rc = lb_of(block_size, 128, kPElems, lbv, "block_size");
-  if (rc) return rc;
+  int lbv = 0;
+  const bool gen = lb_of(block_size, 128, kPElems, lbv, "block_size") != 0;
+  if (gen && !al_gen_ok(block_size))
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
   const int64_t nblk = (numel + block_size - 1) / block_size;
-  const int64_t nwg = (nblk * block_size + kPElems - 1) / kPElems;
+  const int64_t nwg = gen ? nblk : (nblk * block_size + kPElems - 1) / kPElems;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");
   hipStream_t st = (hipStream_t)stream;
   const float w = (float)beta;
+  if (gen) {
+    VemaDesc one{};
+    one.q = q; one.scale = scale; one.min_log = min_log; one.x = reinterpret_cast<const float*>(x);
+    one.out = fp32_out; one.n = numel; one.nblk = nblk;
+#define A8_VEMAG(VB, T)                                                                                        \
+  hipLaunchKernelGGL((k_vema_gen<VB, T>), dim3((unsigned)nwg), dim3(256), 0, st, one, nullptr, 1, block_size, w, \
+                     square_input, eps1, log_floor)
+    switch (x_dtype) {
+      case A8_F32: if (v_bits == 8) A8_VEMAG(8, float); else A8_VEMAG(16, float); break;
+      case A8_BF16: if (v_bits == 8) A8_VEMAG(8, __hip_bfloat16); else A8_VEMAG(16, __hip_bfloat16); break;
+      case A8_F16: if (v_bits == 8) A8_VEMAG(8, __half); else A8_VEMAG(16, __half); break;
+      default: return set_error(A8_ERR_DTYPE, "unsupported new_val dtype");
+    }
+#undef A8_VEMAG
+    return check_launch("k_vema_gen");
+  }
 #define A8_VEMA(VB, T)                                                                                      \
   hipLaunchKernelGGL((k_vema<VB, T>), dim3((unsigned)nwg), dim3(256), 0, st, q, scale, min_log,             \
                      reinterpret_cast<const T*>(x), fp32_out, numel, nblk, lbv, w, square_input, eps1, log_floor)

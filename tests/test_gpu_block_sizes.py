@@ -47,6 +47,9 @@ CASES += [
                                             enable_fira_for_adafactor=True)),
     ("sgd_bv4608_bm4608_d8", dict(SGD, block_size=4608, m_block_size=4608, m_quant_type="d8")),
     ("adamw_fp32v_bv6400_bm100", dict(ADAMW, v_quant_type="fp32", block_size=6400, m_block_size=100)),
+    # quantised V with fp32 momentum: the stand-alone AL EMA (k_vema_gen) at such blocks
+    ("adamw_fp32m_bv640_al8", dict(ADAMW, m_quant_type="fp32", block_size=640)),
+    ("adamw_fp32m_bv3200_al16_clip", dict(ADAMW, m_quant_type="fp32", v_quant_type="al16", block_size=3200, d=1.0)),
     ("mom1d_fp32v_bv1152_bm36_fira", dict(beta1=0.9, beta2=None, beta2_decay=-0.8, factored=False,
                                           relative_step=False, scale_parameter=False, lr=1e-3, v_quant_type="fp32",
                                           block_size=1152, m_block_size=36, enable_fira_for_adafactor=True)),

@@ -81,8 +81,10 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
  *   beta1, beta_val  EMA coefficients as the host's doubles: the lerp weights are
  *               (float)(1 - beta1) and (float)beta_val, as torch.lerp_ receives them
  *   log_floor   lower bound of a block's l_min (-126 for the reference numerics)
- * block_size must be a power of two in [128, 2048], m_block_size a power of two
- * in [32, block_size]. */
+ * block_size: a multiple of 128 up to 65536; m_block_size: a multiple of 4, at least
+ * 32, dividing block_size (the reference's rules, optimizer.py:1395-1416).  Powers of
+ * two (block_size <= 2048) run the 2048-element unit layout, other sizes one
+ * workgroup per V block. */
 int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
                        uint8_t* m_q, float* m_scale, void* v_q, float* v_scale, float* v_min_log,
                        float* v_buf, float* norm_buf, const float* alpha, const float* prev_norm,
@@ -509,8 +511,9 @@ int a8_al_encode(void* q, float* scale, float* min_log, const float* x, int64_t 
  * *norm_buf, and fira = the 3-float output of a8_fira_scalar(norm_buf, prev, one,
  * apply=1) when Fira is on (else null); a non-finite norm then zeroes the update
  * (optimizer.py:797-800).  Momentum: m_q/m_scale (codes padded to whole
- * m_block_size blocks, m_bits/m_mode as in a8_fused_update_1d), or fp32 m, or
- * neither.  stochastic: 16-bit params written with the kernels.cu:48-87 stream. */
+ * m_block_size blocks, m_bits/m_mode as in a8_fused_update_1d; m_block_size a
+ * multiple of 4 in [32, 65536]), or fp32 m, or neither.  stochastic: 16-bit params
+ * written with the kernels.cu:48-87 stream. */
 int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* grad, uint8_t* m_q, float* m_scale,
                 float* m, float* norm_buf, const float* fira, const float* alpha, const float* decay, int64_t numel,
                 double beta1, int m_bits, int m_mode, int m_block_size, float d, float alpha_val, float decay_val,
@@ -543,7 +546,7 @@ int64_t a8_table_bytes_sgd(int ntensors);
  * _m_ema_pytorch (optimizer.py:690-701): m' = lerp(deq(m), x, 1 - beta) per
  * element (non-finite x read as 0), then one absmax per block and requantised
  * codes; fp32_out (optional) receives m'.  x: x_dtype (A8_F32/BF16/F16).
- * block_size: a power of two in [32, 2048]. */
+ * block_size: a multiple of 4 in [32, 65536]. */
 int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype, float* fp32_out, double beta,
                        int block_size, int64_t numel, int m_bits, int m_mode, void* stream);
 
@@ -555,8 +558,8 @@ int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype,
 /* Replaces fused_log_quantize_lerp (kernels.cu:340-520; called by _fused_v_ema,
  * optimizer.py:677-685) with the arithmetic of its twin _deq_v -> lerp_ -> _quant_v
  * (optimizer.py:2232-2238): x = square_input ? x*x + eps1 : x (non-finite read as
- * 0); v' = lerp(deq(v), x, beta); per block of block_size (a power of two in
- * [128, 2048]) the AL range is refit from the non-zero v' with floor log_floor;
+ * 0); v' = lerp(deq(v), x, beta); per block of block_size (a multiple of 128 up to
+ * 65536) the AL range is refit from the non-zero v' with floor log_floor;
  * fp32_out (optional) receives v'.  Codes past numel in the last block become 0.
  * q: uint8 (v_bits 8) or int16 (v_bits 16) codes padded to whole blocks. */
 int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, int x_dtype, float* fp32_out,

@@ -108,7 +108,17 @@ static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
 struct ApHyp {
   float bv, w_m, aeps, log_floor, lr_val, eps2, wd, d, margin, sv;
   int lbv, lbm, mk, channel, front, fira, scale_param, bias_mode, wd_mode;
+  int rowsum;   // k_ap_low leaves row sums for k_ap_scale where ap_rowsum holds (the plain step)
 };
+
+// A right-side matrix whose low-rank rows (r elements, a power of two in [8, 512])
+// lie whole inside k_ap_low's units and within one wave: k_ap_low sums each row's
+// u^2 and g_low^2 (double) and stores the two sums where u would go, and
+// k_ap_scale reads them instead of u and g_low.  u itself is read by nothing else
+// on this path, so it is not written.
+__device__ __forceinline__ bool ap_rowsum(const ApDesc& D, const ApHyp& h) {
+  return h.rowsum && D.R >= D.C && D.r >= 8 && D.r <= 512 && (D.r & (D.r - 1)) == 0;
+}
 
 // Table: ntab descriptors, then five int32 first-workgroup arrays (right-side
 // projection tiles, left-side projection tiles, low units, scale workgroups,
@@ -709,7 +719,9 @@ __global__ __launch_bounds__(256) void k_ap_fixlow(ApDesc D) {
 // block is B/8 consecutive lanes.  Arithmetic as optimizer.py:2765-2790, 2911-2951
 // (quantised states through _quant_v / _m_ema_pytorch, fp32 states through
 // lerp_): v = first ? g^2 * bv : lerp(v, g^2, bv); m = lerp(m, g, 1 - beta1);
-// u = m / (sqrt(v) + eps) with IEEE sqrt and division.  FULL: the unit lies
+// u = m / (sqrt(v) + eps).  u enters the step only through the norms ||u_ch||
+// (the channel or tensor scale, optimizer.py:2997-3001), so it takes the hardware
+// square root and reciprocal (<= 2 ulp), as the 1-D step's Adam denominator does.  FULL: the unit lies
 // inside g_low and u is 16-byte aligned, so every access is a vector access.
 // AL8 blocks of >= 512 elements decode through an LDS table of the block's
 // 255 code values (one correctly rounded exp2 per lane per block).
@@ -821,11 +833,29 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
 #pragma unroll
     for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], g[k], h.w_m) : 0.0f;
   }
-  // ---- u
-  if constexpr (FULL) {
+  // ---- u, or the row sums of u^2 and g_low^2 (ap_rowsum)
+  if (ap_rowsum(D, h)) {
+    double su = 0.0, sg = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < cnt) {
+        const float uk = (MK != 0 ? m[k] : g[k]) * fast_rcp(fast_sqrt(v[k]) + h.aeps);
+        su += (double)(uk * uk);
+        sg += (double)(g[k] * g[k]);
+      }
+    }
+    const int G = (int)(D.r >> 3);   // lanes of a row, <= 64
+    su = grp_sum_d(su, G);
+    sg = grp_sum_d(sg, G);
+    const int64_t row = e0 / D.r;
+    if ((lane & (G - 1)) == 0 && row < D.R) {
+      ws_d_set(ws, L.u, 2 * row, su);
+      ws_d_set(ws, L.u, 2 * row + 1, sg);
+    }
+  } else if constexpr (FULL) {
     float uu[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) uu[k] = (MK != 0 ? m[k] : g[k]) / (sqrtf(v[k]) + h.aeps);
+    for (int k = 0; k < 8; ++k) uu[k] = (MK != 0 ? m[k] : g[k]) * fast_rcp(fast_sqrt(v[k]) + h.aeps);
     *gp(reinterpret_cast<f32x4*>(ws + L.u + e0)) = f32x4{uu[0], uu[1], uu[2], uu[3]};
     *gp(reinterpret_cast<f32x4*>(ws + L.u + e0 + 4)) = f32x4{uu[4], uu[5], uu[6], uu[7]};
   } else {
@@ -833,7 +863,7 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
     for (int k = 0; k < 8; ++k) {
       if (k < cnt) {
         const float x = MK != 0 ? m[k] : g[k];
-        gp(ws)[L.u + e0 + k] = x / (sqrtf(v[k]) + h.aeps);
+        gp(ws)[L.u + e0 + k] = x * fast_rcp(fast_sqrt(v[k]) + h.aeps);
       }
     }
   }
@@ -970,6 +1000,7 @@ __global__ __launch_bounds__(256) void k_ap_scale(ApDesc one, const ApDesc* tab,
   const float* U = D.ws + L.u;
   const float* GL = D.ws + L.glow;
   const int lane = threadIdx.x, w = lane >> 6, l = lane & 63;
+  const bool rs = ap_rowsum(D, h);
   double a0 = 0.0, a1 = 0.0, a2 = 0.0;
   if (R >= C) {
 #pragma unroll 1
@@ -977,13 +1008,20 @@ __global__ __launch_bounds__(256) void k_ap_scale(ApDesc one, const ApDesc* tab,
       const int64_t row = (int64_t)wg * kApScR + w * (kApScR / 4) + i;
       if (row >= R) break;
       double su = 0.0, sg = 0.0;
-      for (int64_t k = l; k < r; k += 64) {
-        const float u = gp(U)[row * r + k], g = gp(GL)[row * r + k];
-        su += (double)(u * u);
-        sg += (double)(g * g);
+      if (rs) {   // k_ap_low's row sums
+        if (l == 0) {
+          su = ws_d(D.ws, L.u, 2 * row);
+          sg = ws_d(D.ws, L.u, 2 * row + 1);
+        }
+      } else {
+        for (int64_t k = l; k < r; k += 64) {
+          const float u = gp(U)[row * r + k], g = gp(GL)[row * r + k];
+          su += (double)(u * u);
+          sg += (double)(g * g);
+        }
+        su = grp_sum_d(su, 64);
+        sg = grp_sum_d(sg, 64);
       }
-      su = grp_sum_d(su, 64);
-      sg = grp_sum_d(sg, 64);
       if (l == 0) {
         if (h.channel) {
           float s = sqrtf((float)su) / (sqrtf((float)sg) + 1e-8f);
@@ -1343,6 +1381,7 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   h.mk = has_m && !m_fp32 ? (m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4)) : 0;
   h.channel = channel ? 1 : 0; h.front = scale_front ? 1 : 0; h.fira = fira ? 1 : 0;
   h.scale_param = scale_parameter ? 1 : 0; h.bias_mode = bias_mode; h.wd_mode = wd_mode;
+  h.rowsum = phase == 0 ? 1 : 0;   // phase 2 finishes a low-rank stage that wrote u itself
   int rc;
   // projection (+ channel norms of G)
   if (phase == 2) {

@@ -442,10 +442,12 @@ def _check_block_sizes(group):
         multiple of 4 from 32 to 65536;
       * quantised 1-D V with fp32 momentum (the stand-alone AL EMA): any multiple
         of 128 up to 65536;
-      * coded momentum on the factored and APOLLO routes: B_M a power of two in
-        [32, 2048];
-      * APOLLO's coded low-rank V and CAME residual / confidence: B_V a power of
-        two in [128, 2048].
+      * coded momentum on the factored route: any multiple of 4 from 32 to 65536
+        (powers of two up to 2048 take the tiled / unit layouts, the others whole
+        M blocks per workgroup);
+      * the APOLLO route: every size those rules allow, up to 65536 (powers of
+        two, B_V in [128, 2048] and B_M in [32, 2048], take the fused low-rank
+        stage, the others the stage of a8_apollo_lowrank_x).
     The factored row / column statistics take any B_V."""
     if not group.get("quantize", True):
         return
@@ -473,13 +475,13 @@ def _check_block_sizes(group):
         elif group.get("apollo_rank", 0) > 0 and p.dim() >= 2:
             route = "APOLLO"
             if vqt != "fp32" or (beta3 is not None and cqt != "fp32"):
-                need(_pow2_in(bs, 128, 2048), "block_size", bs, "a power of two in [128, 2048]")
+                need(bs <= 65536, "block_size", bs, "at most 65536")
             if coded_m:
-                need(_pow2_in(mbs, 32, 2048), "m_block_size", mbs, "a power of two in [32, 2048]")
+                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
         elif p.dim() >= 2 and group.get("factored", True):
             route = "factored"
             if coded_m:
-                need(_pow2_in(mbs, 32, 2048), "m_block_size", mbs, "a power of two in [32, 2048]")
+                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
         else:
             route = "full-rank"
             if vqt != "fp32" and (coded_m or beta1 is None):
@@ -1378,7 +1380,6 @@ def _apollo_prep(opt, p, grad, st, group):
     came = group.get("beta3") is not None
     if came and beta1 is None:
         raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update instability.")
-    xmode = factorize or came
     if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         raise NotImplementedError("adafactor8bit: APOLLO needs fp32, bf16 or fp16 parameters")
     if not p.is_contiguous():
@@ -1423,6 +1424,13 @@ def _apollo_prep(opt, p, grad, st, group):
     else:
         first = st.get("v_low_q") is None and st.get("v_low") is None
     vbits = 0 if (not quant or vqt == "fp32") else (16 if vqt == "al16" else 8)
+    has_m = beta1 is not None
+    m_fp32 = has_m and (not quant or mqt == "fp32")
+    mbs = st.get("m_block_size", group.get("m_block_size", 256))
+    # the fused low-rank stage (k_ap_low) takes power-of-two blocks; other sizes
+    # run the plain stage of a8_apollo_lowrank_x
+    xmode = bool(factorize or came or (vbits and not _pow2_in(bs, 128, 2048))) or \
+        (has_m and not m_fp32 and not _pow2_in(mbs, 32, 2048))
     low_shape = (R, rank) if right else (rank, C)
     if factorize:   # optimizer.py:2693-2699 creates the row / column EMAs on the first step
         if first:
@@ -1433,9 +1441,6 @@ def _apollo_prep(opt, p, grad, st, group):
             S.new_al_slot(st, "v_low", (n_low,), bs, vqt, dev)
         else:
             st["v_low"] = torch.zeros(n_low, dtype=torch.float32, device=dev)
-    has_m = beta1 is not None
-    m_fp32 = has_m and (not quant or mqt == "fp32")
-    mbs = st.get("m_block_size", group.get("m_block_size", 256))
     if has_m:
         if m_fp32:
             if st.get("m_low") is None:

@@ -1,4 +1,5 @@
-// APOLLO low-rank stage of the factorised and CAME variants, one matrix per call.
+// APOLLO low-rank stage of the factorised and CAME variants, and of the plain
+// variant at block sizes the fused k_ap_low does not take.
 //
 // Follows _update_param_apollo (optimizer.py:2587-3084) on the branches its
 // CPU fallback takes (no CUDA module) for what a8_apollo_step's fused k_ap_low
@@ -17,6 +18,11 @@
 //     log2(eps^2)); U = g / sqrt(max(v, eps^2)), RMS clip, m EMA of U, residual
 //     EMA (beta3) of (U - m)^2 + eps_came in fp32 or AL codes (read back decoded
 //     after the re-encode), u = m / sqrt(max(res, eps^2)).
+//   plain (optimizer.py:2759-2799), for a coded low-rank V block that is not a
+//     power of two in [128, 2048] or such a momentum block outside [32, 2048]:
+//     the low-rank V EMA above, the momentum EMA of g_low (its lerped values),
+//     u = x / (sqrt(v) + eps) with x = m or g_low and v the lerped V values.
+//     The EMAs run in the general-block kernels of a8_prims / a8_sgd.
 // RMS clip (optimizer.py:2715-2717, 2869-2871): U /= max((||U|| / sqrt(n)) / d, 1)
 // for d > 0, ||U|| summed in double.  Row / column means are sums in double
 // rounded to fp32 and divided by the count in fp32.  rsqrt is 1 / sqrt, both
@@ -122,7 +128,8 @@ enum {
   XE_RES,       // xr = (U - m)^2 + eps_came; fp32 res state lerped toward it
   XE_UCAME,     // u = m / sqrt(max(res, eps^2))
   XE_FU,        // u = src / (sqrt((r_i c_j) / max(mean r, eps)) + eps)
-  XE_FUC        // u = (m / sqrt(cr_i / cmean)) / sqrt(cc_j)
+  XE_FUC,       // u = (m / sqrt(cr_i / cmean)) / sqrt(cc_j)
+  XE_AU         // u = x / (sqrt(v) + eps), x = m (momentum) or g
 };
 
 __device__ __forceinline__ float rsqrt_ref(float x) { return 1.0f / sqrtf(x); }
@@ -222,6 +229,12 @@ __global__ __launch_bounds__(256) void k_ax_el(XT t) {
         for (int e = 0; e < 4; ++e) a[e] = lerp_ref(a[e], o[e], k.w3);
         x_st4(k.res, i, k.n, k.v4, a);
       }
+    } else if constexpr (OP == XE_AU) {
+      x_ld4(k.m ? k.m : k.g, i, k.n, k.v4, a);
+      x_ld4(k.v, i, k.n, k.v4, b);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = a[e] / (sqrtf(b[e]) + k.aeps);
+      x_st4(k.u, i, k.n, k.v4, o);
     } else if constexpr (OP == XE_UCAME) {
       x_ld4(k.m, i, k.n, k.v4, a);
       x_ld4(k.res ? k.res : ws + L.xr, i, k.n, k.v4, b);
@@ -552,6 +565,10 @@ static int x_run(XB& b) {
   } else if ((rc = x_el<XE_V32>(b))) {
     return rc;
   }
+  if (!a0->came) {   // plain: u from the momentum values (x_momentum sets k.m) or g_low
+    if (a0->has_m && (rc = x_momentum(b, false))) return rc;
+    return x_el<XE_AU>(b);
+  }
   if ((rc = x_el<XE_U>(b))) return rc;
   if ((rc = x_clip(b))) return rc;
   if (!a0->has_m) return 0;   // unreachable through the optimizer (beta3 needs beta1): u = clipped U
@@ -612,21 +629,18 @@ static int x_check(const a8_apollo_x_args* a) {
   if (a->rows_low * a->cols_low >= ((int64_t)1 << 31)) return set_error(A8_ERR_SIZE, "low-rank matrix too large");
   if (!a->g_low || !a->u || !a->xws) return set_error(A8_ERR_ARG, "null g_low, u or workspace");
   if (!aligned16(a->xws)) return set_error(A8_ERR_ALIGN, "workspace must be 16-byte aligned");
-  if (!a->factorize && !a->came)
-    return set_error(A8_ERR_ARG, "plain APOLLO runs in a8_apollo_step; this entry is factorised or CAME");
   if (a->came && !a->has_m) return set_error(A8_ERR_ARG, "CAME (beta3) requires momentum (beta1)");
-  auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
   const bool v_coded = !a->factorize && a->v_bits;
   const bool c_coded = a->came && a->c_bits;
-  if ((v_coded || c_coded) && !(pow2(a->block_size) && a->block_size >= 128 && a->block_size <= 2048))
-    return set_error(A8_ERR_BLOCK, "block_size must be a power of two in [128, 2048]");
+  if ((v_coded || c_coded) && !(a->block_size >= 128 && a->block_size <= 65536 && a->block_size % 128 == 0))
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
   if ((v_coded && a->v_bits != 8 && a->v_bits != 16) || (c_coded && a->c_bits != 8 && a->c_bits != 16))
     return set_error(A8_ERR_ARG, "v_bits / c_bits must be 0, 8 or 16");
   if (a->has_m) {
     if (a->m_fp32 == nullptr) {
       if (!a->m_q || !a->m_scale) return set_error(A8_ERR_ARG, "momentum state missing");
-      if (!(pow2(a->m_block_size) && a->m_block_size >= 32 && a->m_block_size <= 2048))
-        return set_error(A8_ERR_BLOCK, "m_block_size must be a power of two in [32, 2048]");
+      if (!(a->m_block_size >= 32 && a->m_block_size <= 65536 && a->m_block_size % 4 == 0))
+        return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
     }
   }
   if (a->factorize) {

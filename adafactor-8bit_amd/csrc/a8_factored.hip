@@ -147,7 +147,7 @@ struct DescF {
   int64_t nbr;         // AL blocks of the row vector (the column vector follows)
   uint64_t sr_seed;
   int has_fira_prev;
-  int vec4;            // rows start 16-byte aligned for fp32 (8-byte for 16-bit types)
+  int vec4;            // every row starts 16-byte aligned
   int tiled;           // update runs on the statistics tiles (k_fupdt), else flat units
 };
 
@@ -171,7 +171,9 @@ struct HyperF {
   int fira;
   int block_size;      // V block size
   int mk;              // momentum codec (0 none, 1 UF8, 2 UF4, 3 D8, 4 D4)
-  int lbm;             // log2(m_block_size)
+  int lbm;             // log2(m_block_size); -1: B_M not a power of two in [32, 2048]
+  int bm;              // B_M when lbm < 0 (k_fupdate_gen), else 0
+  int unit;            // elements per k_fupdate_gen workgroup (a whole number of M blocks)
   uint64_t sr_step;
   const a8_step_scalars* dsc;   // if set: this step's V lerp weight, lr, bias factor and SR step
 };
@@ -464,8 +466,12 @@ __global__ __launch_bounds__(256) void k_fstats(const DescF* __restrict__ table,
 // ------------------------------------------------------------ CAME residual statistics
 // Old momentum of the element at flat index e (codec mk: 1 UF8, 2 UF4, 3 D8,
 // 4 D4; UF4/D4 keep the even element in the high nibble).
-__device__ __forceinline__ float m_old_at(int mk, const uint8_t* mq, const float* msc, int64_t e, int lbm) {
-  const float ms = gp(msc)[e >> lbm];
+// M block of flat index e: a shift for the power-of-two sizes (lbm >= 0), else a
+// division by B_M.
+__device__ __forceinline__ int64_t m_blk(int64_t e, int lbm, int bm) { return lbm >= 0 ? e >> lbm : e / bm; }
+
+__device__ __forceinline__ float m_old_at(int mk, const uint8_t* mq, const float* msc, int64_t e, int lbm, int bm) {
+  const float ms = gp(msc)[m_blk(e, lbm, bm)];
   uint32_t q;
   if (mk == 2 || mk == 4) {
     const uint32_t byte = gp(mq)[e >> 1];
@@ -480,10 +486,10 @@ __device__ __forceinline__ float m_old_at(int mk, const uint8_t* mq, const float
 // `avail`).  The vector form needs e % 4 == 0 (the four share an M block).
 template <int MK>
 __device__ __forceinline__ void m_old4(int mkr, const uint8_t* mq, const float* msc, int64_t e, int64_t avail,
-                                       bool vec, int lbm, float* out) {
+                                       bool vec, int lbm, int bm, float* out) {
   const int mk = MK == 1 ? 1 : mkr;
   if (vec && avail >= 4) {
-    const float ms = gp(msc)[e >> lbm];
+    const float ms = gp(msc)[m_blk(e, lbm, bm)];
     if (mk == 2 || mk == 4) {
       const uint32_t w = *gp(reinterpret_cast<const uint16_t*>(mq + (e >> 1)));
 #pragma unroll
@@ -498,7 +504,7 @@ __device__ __forceinline__ void m_old4(int mkr, const uint8_t* mq, const float* 
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) out[k] = (k < avail) ? m_old_at(mk, mq, msc, e + k, lbm) : 0.0f;
+    for (int k = 0; k < 4; ++k) out[k] = (k < avail) ? m_old_at(mk, mq, msc, e + k, lbm, bm) : 0.0f;
   }
 }
 
@@ -534,14 +540,14 @@ __device__ __forceinline__ void came1_tile(const DescF& D, const FWs& W, const T
       if constexpr (RAGGED) {
         load4<T>(G, rowbase, c0, C, vec, g[k]);
         if constexpr (MK == 3) load4<float>(D.m, rowbase, c0, C, vec, mo[k]);
-        else m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, mo[k]);
+        else m_old4<MK>(h.mk, D.m_q, D.m_scale, rowbase + c0, C - c0, vec, h.lbm, h.bm, mo[k]);
       } else {
         load4o<T>(G + rowbase, cl, g[k]);
         if constexpr (MK == 3) {
           load4o<float>(D.m + rowbase, cl, mo[k]);
         } else {
           const int64_t e = rowbase + cl;
-          ms[k] = gp(D.m_scale)[e >> h.lbm];
+          ms[k] = gp(D.m_scale)[m_blk(e, h.lbm, h.bm)];
           if (MK == 1 || !nib) qv[k] = __builtin_nontemporal_load(gp(reinterpret_cast<const uint32_t*>(D.m_q + e)));
           else qv[k] = __builtin_nontemporal_load(gp(reinterpret_cast<const uint16_t*>(D.m_q + (e >> 1))));
         }
@@ -1062,6 +1068,189 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
   }
 }
 
+// k_fupdate for coded momentum whose block size the unit layout cannot take
+// (B_M a multiple of 4 in [32, 65536], not a power of two up to 2048).  One
+// workgroup covers h.unit = B_M * ceil(2048 / B_M) elements, a whole number of M
+// blocks and at least kUnit, so a tensor takes no more workgroups than its
+// W.nunit norm-partial slots; its last workgroup zeroes the slots it does not
+// use.  Lanes take quads (a quad never straddles an M block, B_M % 4 == 0); each
+// block's absmax meets in LDS (an exact max).  Pass 1 forms M' and u and writes
+// the parameter (MODE 1: the partial sum of u^2); pass 2, after the absmaxes,
+// forms M' again from the same inputs and writes the codes; the scales follow
+// once every lane has read the old ones.  Element for element the arithmetic is
+// k_fupdate's.  MK: 0 no momentum (the CAME clip pass), 2 any codec (h.mk).
+constexpr int kFGenMaxMB = 64;
+
+template <typename T, int MODE, bool SR, int MK, bool CM>
+__global__ __launch_bounds__(256) void k_fupdate_gen(const DescF* __restrict__ table, int ntab, HyperF h) {
+  if constexpr (SR) hf_step(h);
+  static_assert(MK == 0 || MK == 2, "codes through m_decode / m_encode");
+  static_assert(!CM || MK != 0, "CAME needs momentum");
+  __shared__ uint32_t s_mab[kFGenMaxMB];
+  __shared__ double s4d[4];
+  const DescF D = *find_unit(table, ntab, (int64_t)blockIdx.x);
+  if (D.tiled) return;
+  const FWs W = fws_layout(D.B, D.R, D.C);
+  const int lane = threadIdx.x;
+  const int BM = h.bm, U = h.unit, mpu = U / BM;
+  const int64_t wl = (int64_t)blockIdx.x - D.unit_begin;
+  const int64_t n = D.numel;
+  const int64_t base = wl * U;
+  const int64_t mb0 = base / BM, nmb = (n + BM - 1) / BM;
+  const int64_t R = D.R, C = D.C;
+  float* ws = D.ws;
+  const float* invr = ws + W.invr;
+  const float* invc = ws + W.invc;
+  const float* icr = ws + W.icr;
+  const float* icc = ws + W.icc;
+  const float* sl = ws + W.scal;
+  const T* G = reinterpret_cast<const T*>(D.grad);
+  T* P = reinterpret_cast<T*>(D.param);
+  const int mk = h.mk;
+  const bool nib = mk == 2 || mk == 4;
+  const float clip = CM ? gp(sl)[4] : 1.0f;
+  if constexpr (MK != 0 && MODE != 1) {
+    for (int i = lane; i < mpu; i += 256) s_mab[i] = 0u;
+    __syncthreads();
+  }
+
+  // M' and u of the quad at unit offset 4q (zero past the tensor)
+  auto quad = [&](int q, float* g, float* mn, float* u, int& cnt, int& mb, bool& m_ok) {
+    const int64_t i0 = base + 4 * q;
+    cnt = i0 >= n ? 0 : (n - i0 >= 4 ? 4 : (int)(n - i0));
+    load4n<T>(G, i0, n, g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g[k] = scrub(g[k]);
+    mb = (4 * q) / BM;
+    m_ok = MK != 0 && mb0 + mb < nmb;   // codes are padded to whole blocks
+    float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (m_ok) {
+      const float ms = gp(D.m_scale)[mb0 + mb];
+      if (nib) {
+        const uint32_t w = *gp(reinterpret_cast<const uint16_t*>(D.m_q + (i0 >> 1)));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t byte = (w >> (8 * (k >> 1))) & 0xFFu;
+          mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
+        }
+      } else {
+        const uint32_t w = *gp(reinterpret_cast<const uint32_t*>(D.m_q + i0));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mo[k] = m_decode(mk, (w >> (8 * k)) & 0xFFu, ms);
+      }
+    }
+    int64_t row = i0 / C;
+    int64_t c = i0 - row * C;
+    int64_t b = row / R;
+    int64_t rr = row - b * R;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      mn[k] = 0.0f;
+      u[k] = 0.0f;
+      if (k < cnt) {
+        if constexpr (CM) {
+          const float ug = ((g[k] * gp(invr)[row]) * gp(invc)[b * C + c]) / clip;
+          mn[k] = lerp_ref(mo[k], ug, h.w_m);
+          u[k] = (mn[k] * gp(icr)[row]) * gp(icc)[b * C + c];
+        } else {
+          if constexpr (MK != 0) mn[k] = lerp_ref(mo[k], g[k], h.w_m);
+          const float x = MK != 0 ? mn[k] : g[k];
+          u[k] = (x * gp(invr)[row]) * gp(invc)[b * C + c];
+        }
+      }
+      if (++c == C) {
+        c = 0;
+        ++row;
+        if (++rr == R) { rr = 0; ++b; }
+      }
+    }
+  };
+
+  float step = 0.0f, fs = 1.0f, dec = 1.0f;
+  if constexpr (MODE != 1) {
+    step = (MODE == 0) ? gp(sl)[0] : gp(sl)[1];
+    fs = (MODE == 2) ? gp(sl)[2] : 1.0f;
+    dec = gp(sl)[3];
+  }
+  const bool has_dec = h.wd_mode != 0;
+
+  // ---- pass 1
+  double sq = 0.0;
+  for (int q = lane; q < (U >> 2); q += 256) {
+    float g[4], mn[4], u[4];
+    int cnt, mb;
+    bool m_ok;
+    quad(q, g, mn, u, cnt, mb, m_ok);
+    const int64_t i0 = base + 4 * q;
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < cnt) sq = __builtin_fma((double)u[k], (double)u[k], sq);
+    } else {
+      if (MODE == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) u[k] = u[k] * fs;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k >= cnt) continue;
+        if constexpr (SR) {
+          const float pv = ld1<T>(P, i0 + k);
+          const T r = sr_round<T>((has_dec ? pv * dec : pv) - step * u[k], D.sr_seed, h.sr_step,
+                                  (uint64_t)(i0 + k));
+          uint16_t bits;
+          __builtin_memcpy(&bits, &r, 2);
+          gp(reinterpret_cast<uint16_t*>(P))[i0 + k] = bits;
+        } else {
+          const pval_t<T> pv = ld1<T, pval_t<T>>(P, i0 + k);
+          st1<T>(P, i0 + k, pupd(step, u[k], has_dec ? pdec(pv, dec) : pv));
+        }
+      }
+      if constexpr (MK != 0) {
+        uint32_t ab = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ab = max(ab, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
+        if (m_ok) atomicMax(&s_mab[mb], ab);
+      }
+    }
+  }
+  if constexpr (MODE == 1) {
+    const double tot = wg_sum_d(sq, s4d);
+    const int64_t nu = (n + U - 1) / U;
+    if (lane == 0) gp(ws_dp(ws, W.npart))[wl] = tot;
+    if (wl == nu - 1)
+      for (int64_t k = nu + lane; k < W.nunit; k += 256) gp(ws_dp(ws, W.npart))[k] = 0.0;
+    return;
+  }
+  if constexpr (MK != 0) {
+    __syncthreads();
+    // ---- pass 2: codes
+    for (int q = lane; q < (U >> 2); q += 256) {
+      float g[4], mn[4], u[4];
+      int cnt, mb;
+      bool m_ok;
+      quad(q, g, mn, u, cnt, mb, m_ok);
+      if (!m_ok) continue;
+      const int64_t i0 = base + 4 * q;
+      const float am = fmaxf(__uint_as_float(s_mab[mb]), 1e-12f);
+      const float ram = fast_rcp(am);
+      if (nib) {
+        const uint32_t w = ((m_encode(mk, mn[0], am, ram) << 4) | m_encode(mk, mn[1], am, ram)) |
+                           (((m_encode(mk, mn[2], am, ram) << 4) | m_encode(mk, mn[3], am, ram)) << 8);
+        *gp(reinterpret_cast<uint16_t*>(D.m_q + (i0 >> 1))) = (uint16_t)w;
+      } else {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w |= m_encode(mk, mn[k], am, ram) << (8 * k);
+        *gp(reinterpret_cast<uint32_t*>(D.m_q + i0)) = w;
+      }
+    }
+    __syncthreads();   // every lane has read the old scales
+    for (int i = lane; i < mpu; i += 256)
+      if (mb0 + i < nmb) gp(D.m_scale)[mb0 + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+  }
+}
+
 // Tiled form of k_fupdate for tensors whose columns allow it (C % 4 == 0 and,
 // with momentum, B_M <= 256 dividing C): the statistics tiles (tr rows x 1024
 // columns), each wave walking rows, lanes holding 4 consecutive columns of each
@@ -1392,6 +1581,13 @@ static int launch_update_m(int mk, const DescF* tab, int ntab, const UpdGrid& ug
     int rc = check_launch("k_fupdt");
     if (rc) return rc;
   }
+  if (ug.any_flat && h.lbm < 0) {   // general B_M: every tensor is flat, units of h.unit
+    const dim3 g((unsigned)ug.nunits);
+    if constexpr (CM) hipLaunchKernelGGL((k_fupdate_gen<T, MODE, SR, 2, true>), g, b, 0, st, tab, ntab, h);
+    else if (mk == 0) hipLaunchKernelGGL((k_fupdate_gen<T, MODE, SR, 0, false>), g, b, 0, st, tab, ntab, h);
+    else hipLaunchKernelGGL((k_fupdate_gen<T, MODE, SR, 2, false>), g, b, 0, st, tab, ntab, h);
+    return check_launch("k_fupdate_gen");
+  }
   if (ug.any_flat) {
     const dim3 g((unsigned)ug.nunits);
     if constexpr (CM) {
@@ -1513,22 +1709,27 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_2d(ntensors)");
   const bool m32 = tensors[0].m != nullptr;
   const bool has_m = tensors[0].m_q != nullptr || m32;
-  int lbm = 0;
+  int lbm = 5, gbm = 0, gunit = 0;
   if (has_m && !m32) {
     if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
       return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
-    if (m_block_size < 32 || m_block_size > kUnit || (m_block_size & (m_block_size - 1)))
-      return set_error(A8_ERR_BLOCK, "m_block_size must be a power of two in [32, 2048]");
-    while ((1 << lbm) < m_block_size) ++lbm;
-  } else {
-    lbm = 5;
+    if (m_block_size < 32 || m_block_size > 65536 || (m_block_size & 3))
+      return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
+    if (m_block_size <= kUnit && !(m_block_size & (m_block_size - 1))) {
+      lbm = 0;
+      while ((1 << lbm) < m_block_size) ++lbm;
+    } else {   // k_fupdate_gen: whole M blocks per workgroup, at least kUnit elements
+      lbm = -1;
+      gbm = m_block_size;
+      gunit = m_block_size * ((kUnit + m_block_size - 1) / m_block_size);
+    }
   }
   if (came && !has_m) return set_error(A8_ERR_ARG, "CAME needs momentum (m_q or m)");
   if (stochastic && dtype == A8_F32) stochastic = 0;
   std::vector<DescF> tab((size_t)ntensors);
   int64_t tiles = 0, utiles = 0, units = 0, fblks = 0, csw = 0;
   bool any_tiled = false, any_flat = false;
-  const size_t esz = dtype == A8_F32 ? 4 : 2;
+  const size_t esz = dtype == A8_F32 ? 4 : (dtype == A8_F64 ? 8 : 2);
   for (int i = 0; i < ntensors; ++i) {
     const a8_tensor2d& t = tensors[i];
     if (t.batch <= 0 || t.rows <= 0 || t.cols <= 0) return set_error(A8_ERR_SIZE, "empty factored tensor");
@@ -1558,7 +1759,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     D.B = t.batch; D.R = t.rows; D.C = t.cols; D.numel = numel;
     D.sr_seed = t.sr_seed;
     D.vec4 = ((t.cols * esz) % 16 == 0) ? 1 : 0;
-    D.tiled = (t.cols % 4 == 0) && (!has_m || m32 || (m_block_size <= 256 && t.cols % m_block_size == 0)) ? 1 : 0;
+    D.tiled = (t.cols % 4 == 0) &&
+              (!has_m || m32 || (lbm >= 0 && m_block_size <= 256 && t.cols % m_block_size == 0)) ? 1 : 0;
     (D.tiled ? any_tiled : any_flat) = true;
     const FWs W = fws_layout(t.batch, t.rows, t.cols);
     D.tile_begin = tiles;
@@ -1569,7 +1771,7 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
     D.nbr = (t.batch * t.rows + block_size - 1) / block_size;
     tiles += W.ntile;
     utiles += W.nutile;
-    units += W.nunit;
+    units += lbm >= 0 ? W.nunit : (numel + gunit - 1) / gunit;   // gunit >= kUnit: within W.nunit slots
     fblks += D.nbr + (t.batch * t.cols + block_size - 1) / block_size;
     if (W.nsplit > 1) csw += t.batch * ((t.cols + 255) / 256) * W.nsplit;
   }
@@ -1593,6 +1795,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   h.block_size = block_size;
   h.mk = m32 ? kMkFp32 : (has_m ? mk_code(m_bits, m_mode) : 0);
   h.lbm = lbm;
+  h.bm = gbm;
+  h.unit = gunit;
   h.sr_step = sr_step;
   h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   const bool clip = d > 0.0f || fira;

@@ -296,7 +296,9 @@ typedef struct a8_tensor2d {
  * bias_mode: 0 none, 1 alpha *= bias_factor, 2 alpha /= bias_factor.
  * wd_mode: 0 none, 1 decay uses alpha, 2 decay uses lr.
  * v_bits: 8 / 16 (codes) or 0 (fp32 row_var/col_var).  block_size: V block
- * (any positive size).  m_block_size: power of two in [32, 2048].
+ * (any positive size).  m_block_size: a multiple of 4 in [32, 65536] (powers of
+ * two up to 2048 take the tiled / unit layouts, other sizes whole M blocks per
+ * workgroup).
  * table_dev: device buffer of a8_table_bytes_2d(ntensors) bytes (uploaded when upload != 0).
  *
  * came != 0 selects CAME (beta3; _fallback_2d_update optimizer.py:929-956, kernels
@@ -362,7 +364,9 @@ typedef struct a8_apollo_tensor {
  * m_fp32 selects fp32 m_low.  channel: apollo_scale_type "channel" (else
  * "tensor").  bias_mode 0/1/2: none / step *= bias_factor / step /= bias_factor.
  * wd_mode 0/1/2: none / decay uses alpha / decay uses lr.  V block_size and
- * m_block_size are powers of two (V: 128..2048, M: 32..2048). */
+ * m_block_size are powers of two (V: 128..2048, M: 32..2048); other sizes run
+ * the low-rank stage of a8_apollo_lowrank_x between the phases of
+ * a8_apollo_step_multi_phase. */
 int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int first_step, int proj_fresh,
                    double beta_val, double beta1, int has_m, float apollo_eps, float log_floor, int v_bits,
                    int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
@@ -387,7 +391,8 @@ int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tens
 int64_t a8_apollo_table_bytes(int ntensors);
 
 /* a8_apollo_step_multi split around the low-rank stage, for the factorised and
- * CAME variants (optimizer.py:2689-2896) whose stage is a8_apollo_lowrank_x.
+ * CAME variants (optimizer.py:2689-2896), and the plain variant at block sizes
+ * the fused stage does not take, whose stage is a8_apollo_lowrank_x.
  * phase 1: projection g_low = G P^T / P^T G into workspace[0, n_low) (n_low =
  * max(rows, cols) * rank; row-major rows x rank on the right side, rank x cols on
  * the left) plus the norms of G (and of p for scale_parameter); V / M fields of
@@ -450,7 +455,11 @@ typedef struct a8_apollo_x_args {
 /* Replaces the factorised (apollo_factorize, optimizer.py:2689-2758) and CAME
  * (beta3, optimizer.py:2800-2896) low-rank stages of _update_param_apollo, in
  * the arithmetic of its CPU branches: second-moment EMA, RMS clip (d > 0),
- * momentum EMA, residual / confidence EMAs, and the update u = update_low. */
+ * momentum EMA, residual / confidence EMAs, and the update u = update_low.
+ * With neither flag, the plain stage (optimizer.py:2759-2799): V EMA, momentum
+ * EMA, u = x / (sqrt(v) + apollo_eps).  block_size (coded V, residual or
+ * confidence): a multiple of 128 up to 65536; m_block_size (coded momentum): a
+ * multiple of 4 in [32, 65536]. */
 int a8_apollo_lowrank_x(const a8_apollo_x_args* args, void* stream);
 int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low);
 

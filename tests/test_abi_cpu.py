@@ -68,8 +68,8 @@ def test_module_signatures_match_reference():
 
 
 def test_apollo_lowrank_and_phase_argument_errors_without_gpu():
-    """The factorised / CAME APOLLO stage and the phased group call check their
-    records on the host before any launch."""
+    """The APOLLO low-rank stage and the phased group call check their records on
+    the host before any launch."""
     import ctypes
     from adafactor8bit import _native as nat
     L = nat.lib()
@@ -77,8 +77,8 @@ def test_apollo_lowrank_and_phase_argument_errors_without_gpu():
     a.rows_low, a.cols_low = 16, 8
     assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # null g_low / u / workspace
     a.g_low = a.u = a.xws = 256
-    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # neither factorised nor CAME
-    assert b"plain APOLLO" in L.a8_last_error()
+    assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # plain stage without its V state
+    assert b"low-rank V state" in L.a8_last_error()
     a.came, a.has_m = 1, 0
     assert L.a8_apollo_lowrank_x(ctypes.byref(a), None) == -1            # CAME without momentum
     assert b"beta1" in L.a8_last_error()

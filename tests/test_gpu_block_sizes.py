@@ -11,7 +11,9 @@ parameters within rtol 1e-5 except the elements whose codes differed at some
 step, which stay within rtol 2e-3 plus 1% of the largest displacement.  The
 modes: NOCLIP (AdamW, V-only), NORM/APPLY (RMS clip and Fira, batched) and
 MNORM (momentum-only Fira).  Coded momentum on the SGD route and with fp32 V
-takes k_sgd_gen at such blocks (one workgroup per whole number of M blocks).
+takes k_sgd_gen at such blocks (one workgroup per whole number of M blocks), and
+the factored route's coded momentum k_fupdate_gen (compared as the factored
+goldens are, against an exact-reduction oracle).
 """
 import numpy as np
 import pytest
@@ -106,3 +108,166 @@ def test_general_block_sizes_match_oracle(name, kw):
         np.testing.assert_allclose(P[~tm], Q[~tm], rtol=1e-5, atol=1e-8, err_msg=f"{name} p{i} param")
         disp = float(np.abs(Q - p0[i].reshape(-1).numpy()).max())
         np.testing.assert_allclose(P[tm], Q[tm], rtol=2e-3, atol=1e-8 + 1e-2 * disp, err_msg=f"{name} p{i}")
+
+
+# Factored route (row / column statistics, coded momentum): B_M outside the powers
+# of two in [32, 2048] takes k_fupdate_gen, whole M blocks per workgroup, with the
+# flat element walk of k_fupdate; CAME pass 1 decodes the old momentum by division.
+# Shapes: ragged width (77), a width the tiles take at power-of-two blocks (384)
+# and a batched 3-D tensor.  The oracle runs with exact reductions; the comparison
+# is the factored golden one (tests/test_gpu_golden.py, _cmp_state) with the
+# momentum-scale and parameter bounds of tests/test_gpu_factored_shapes.py.
+FSHAPES = [(300, 77), (256, 384), (3, 100, 96)]
+FACT = dict(beta1=0.9, beta2=None, beta2_decay=-0.8, beta3=None, factored=True, relative_step=False, lr=1e-3,
+            scale_parameter=False)
+CAME = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True, relative_step=False,
+            scale_parameter=False, scale_weight_decay=False, eps_came=1e-16, lr=1e-4, v_quant_type="al8",
+            c_quant_type="al8")
+FCASES = [
+    ("adafactor_factored_bm36", dict(FACT, block_size=1152, m_block_size=36, d=0.0)),
+    ("adafactor_factored_bm100_uf4_clip_fira", dict(FACT, block_size=6400, m_block_size=100, m_quant_type="uf4",
+                                                    d=1.0, enable_fira_for_adafactor=True)),
+    ("adafactor_factored_bm4096_d4", dict(FACT, block_size=4096, m_block_size=4096, m_quant_type="d4", d=1.0,
+                                          weight_decay=0.01)),
+    ("came_bm96_d8_clip", dict(CAME, block_size=384, m_block_size=96, m_quant_type="d8", d=1.0)),
+    ("came_bm160_uf8_fira", dict(CAME, block_size=640, m_block_size=160, d=1.0, enable_fira_for_adafactor=True,
+                                 fira_margin=0.01)),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", FCASES, ids=[c[0] for c in FCASES])
+def test_factored_general_m_block_matches_oracle(name, kw):
+    import oracle.fallback as F
+    from adafactor8bit import Adafactor8Bit
+    from test_gpu_factored_shapes import _cmp_m_scale, _state_np
+    from test_gpu_golden import _cmp_state
+    print(f"[block sizes] {name}", flush=True)
+    pc = [torch.nn.Parameter(make_param(s, i, 13)) for i, s in enumerate(FSHAPES)]
+    p0 = [p.detach().clone() for p in pc]
+    pg = [torch.nn.Parameter(p.detach().clone().cuda()) for p in pc]
+    oc, og = F.OracleOptimizer(pc, **kw), Adafactor8Bit(pg, **kw)
+    for t in range(1, 6):
+        for i, (a, b) in enumerate(zip(pc, pg)):
+            g = make_grad(tuple(a.shape), i, t, 13, kind="student_t")
+            a.grad, b.grad = g, g.cuda()
+        old = F.set_exact_reductions(True)
+        try:
+            oc.step()
+        finally:
+            F.set_exact_reductions(old)
+        og.step()
+        torch.cuda.synchronize()
+        report = []
+        for i, (a, b) in enumerate(zip(pc, pg)):
+            key = f"s{t}/p{i}"
+            assert og.state[b]["is_quantized"]
+            ref_p, mine_p = a.detach().numpy(), b.detach().cpu().numpy()
+            disp = float(np.abs(ref_p - p0[i].numpy()).max())
+            close = np.abs(mine_p - ref_p) <= 1e-5 * np.abs(ref_p) + 1e-8 + 1e-4 * disp
+            assert (~close).mean() <= 1e-4 + 1.0 / close.size, f"{name} {key} param: {(~close).mean():.2e}"
+            np.testing.assert_allclose(mine_p, ref_p, rtol=2e-3, atol=1e-8 + 1e-2 * disp,
+                                       err_msg=f"{name} {key} param")
+            ref_st = _state_np(oc.state[id(a)])
+            assert "m_q" in ref_st, f"{name}: the oracle keeps no coded momentum"
+            _cmp_m_scale(name, key, og.state[b]["m_scale"].cpu().numpy(), ref_st.pop("m_scale"))
+            z = {f"{key}/{k}": v for k, v in ref_st.items()}
+            _cmp_state(name, key, og.state[b], z, list(ref_st), report)
+        print(report, flush=True)
+
+
+# APOLLO route: a coded low-rank V block that is not a power of two in [128, 2048],
+# or such a momentum block outside [32, 2048], takes the low-rank stage of
+# a8_apollo_lowrank_x (the plain stage, or the factorised / CAME ones) with the
+# general-block EMA kernels.  The oracle gets this library's projection output
+# (glow_hook, as in the rank-256 test of tests/test_gpu_apollo.py) and reduces
+# exactly.  Plain: V and M codes equal but for <= 0.01% (+1 per tensor), by one
+# code; block metadata rtol 1e-5; the Fira norm rtol 1e-5; fp32 parameters rtol
+# 1e-5 plus 2e-4 of the largest displacement.  Factorised / CAME: the bounds of
+# the APOLLO golden comparison (tests/test_gpu_apollo.py, _cmp_state).
+APOLLO_BASE = dict(lr=1e-3, beta1=0.9, beta2=0.999, relative_step=False, scale_parameter=False, apollo_rank=32,
+                   apollo_update_proj_gap=200, apollo_cache_proj=True, enable_fira_for_apollo=True, d=0.0)
+ACASES = [
+    ("apollo_plain_bv384_bm96", dict(APOLLO_BASE, block_size=384, m_block_size=96)),
+    ("apollo_plain_bv1152_bm36_uf4_al16_clip", dict(APOLLO_BASE, block_size=1152, m_block_size=36,
+                                                    m_quant_type="uf4", v_quant_type="al16", d=1.0)),
+    ("apollo_plain_bv4096_bm4096_d8_tensor", dict(APOLLO_BASE, block_size=4096, m_block_size=4096,
+                                                  m_quant_type="d8", apollo_scale_type="tensor")),
+    ("apollo_plain_bv6400_bm100_nofira", dict(APOLLO_BASE, block_size=6400, m_block_size=100,
+                                              enable_fira_for_apollo=False, weight_decay=0.01)),
+    ("apollo_plain_bv384_bm128", dict(APOLLO_BASE, block_size=384, m_block_size=128)),
+    ("apollo_plain_bv640_nomom", dict(APOLLO_BASE, beta1=None, block_size=640)),
+    ("apollo_came_bv640_bm160", dict(APOLLO_BASE, beta3=0.9999, d=1.0, eps_came=1e-16, block_size=640,
+                                     m_block_size=160)),
+    ("apollo_fact_bm36", dict(APOLLO_BASE, apollo_factorize=True, block_size=1152, m_block_size=36)),
+]
+ASHAPES = [(300, 200), (160, 420)]
+
+
+class _Z(dict):
+    """The oracle's state in the form the APOLLO golden comparison reads."""
+    @property
+    def files(self):
+        return list(self.keys())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", ACASES, ids=[c[0] for c in ACASES])
+def test_apollo_general_blocks_match_oracle(name, kw, monkeypatch):
+    import adafactor8bit.optimizer as O
+    import inputs
+    import oracle.fallback as F
+    from adafactor8bit import Adafactor8Bit
+    from test_gpu_apollo import _cmp_params, _t2np
+    from test_gpu_apollo import _cmp_state as ap_cmp_state
+    monkeypatch.setattr(O, "stable_randn", inputs.make_proj)
+    monkeypatch.setattr(F, "stable_randn", inputs.make_proj)
+    old = F.set_exact_reductions(True)
+    plain = name.startswith("apollo_plain")
+    try:
+        print(f"[block sizes] {name}", flush=True)
+        init = [inputs.make_param(s, i, 17) for i, s in enumerate(ASHAPES)]
+        pg = [torch.nn.Parameter(x.clone().cuda()) for x in init]
+        pc = [torch.nn.Parameter(x.clone()) for x in init]
+        og, oc = Adafactor8Bit(pg, **kw), F.OracleOptimizer(pc, **kw)
+        lows = [(R, 32) if R >= C else (32, C) for R, C in ASHAPES]
+        glows = {}
+        oc.glow_hook = lambda p, _g, _pt: glows[id(p)]
+        for t in range(1, 6):
+            for i, (a, b) in enumerate(zip(pc, pg)):
+                g = inputs.make_grad(ASHAPES[i], i, t, 17, zero_frac=0.0)
+                a.grad, b.grad = g.clone(), g.cuda()
+            og.step()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(pc, pg)):
+                ws = og._ws[(b.device, "apollo", id(b))]["ws"].cpu().numpy()
+                glows[id(a)] = torch.from_numpy(ws[:lows[i][0] * lows[i][1]].reshape(lows[i]).copy())
+            oc.step()
+            for i, (a, b) in enumerate(zip(pc, pg)):
+                key = f"s{t}/p{i}"
+                st, sr = og.state[b], oc.state[id(a)]
+                if plain:
+                    for k in ("v_low_q", "m_low_q"):
+                        if k not in sr:
+                            continue
+                        x, y = st[k].cpu().numpy().reshape(-1), sr[k].numpy().reshape(-1)
+                        frac, mx = gu.code_mismatch(x, y)
+                        print(f"  {key} {k}: {frac:.2e} of codes differ, max {mx}", flush=True)
+                        assert frac <= 1e-4 + 1.0 / x.size and mx <= 1, f"{name} {key} {k}: {frac:.2e}, max {mx}"
+                    for k in ("v_low_scale", "v_low_min_log", "m_low_scale", "scaled_grad_norm_prev"):
+                        if k in sr:
+                            np.testing.assert_allclose(np.asarray(st[k].cpu()).reshape(-1),
+                                                       np.asarray(sr[k]).reshape(-1), rtol=1e-5,
+                                                       err_msg=f"{name} {key} {k}")
+                    mine, want = b.detach().cpu().numpy(), a.detach().numpy()
+                    disp = float(np.abs(want - init[i].numpy()).max())
+                    np.testing.assert_allclose(mine, want, rtol=1e-5, atol=1e-8 + 2e-4 * disp,
+                                               err_msg=f"{name} {key} param")
+                else:
+                    z = _Z({f"{key}/{k}": v.numpy() for k, v in sr.items() if torch.is_tensor(v)})
+                    keys = [k[len(key) + 1:] for k in z.files]
+                    _cmp_params(name, key, _t2np(b), a.detach().numpy(), init[i].numpy())
+                    ap_cmp_state(name, key, st, z, keys)
+            assert "m_low_q" in og.state[pg[0]] or kw.get("beta1") is None
+    finally:
+        F.set_exact_reductions(old)

@@ -20,7 +20,8 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
     (dict(ADAMW, block_size=6400, m_block_size=100, m_quant_type="uf4"), [(64, 64)], True),
     (dict(ADAMW, block_size=131072, m_block_size=256), [(64, 64)], False),   # beyond 65536
     (dict(ADAMW, block_size=384, m_block_size=128, m_quant_type="fp32"), [(64, 64)], True),   # fp32 M: AL EMA
-    (dict(ADAMW, apollo_rank=4, block_size=384, m_block_size=128), [(64, 64)], False),        # APOLLO low-rank V
+    (dict(ADAMW, apollo_rank=4, block_size=384, m_block_size=128), [(64, 64)], True),         # APOLLO low-rank V
+    (dict(ADAMW, apollo_rank=4, block_size=131072, m_block_size=128), [(64, 64)], False),     # beyond 65536
     (dict(ADAMW, block_size=384, m_block_size=128), [(63, 64)], True),      # below min_8bit_size
     (dict(ADAMW, block_size=384, m_block_size=128, quantize=False), [(64, 64)], True),
     (dict(ADAMW, block_size=384, m_block_size=128, v_quant_type="fp32", m_quant_type="fp32"), [(64, 64)], True),
@@ -30,7 +31,8 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
     (dict(lr=1e-3, relative_step=False, beta1=0.9, block_size=384, m_block_size=128), [(64, 64)], True),
     (dict(lr=1e-3, relative_step=False, beta1=0.9, block_size=1024, m_block_size=100), [(64, 64)], False),
     (dict(lr=1e-3, relative_step=False, block_size=384), [(4096,)], True),   # 1-D vector of a factored group
-    (dict(ADAMW, apollo_rank=8, block_size=640, m_block_size=128), [(64, 64)], False),
+    (dict(ADAMW, apollo_rank=8, block_size=640, m_block_size=160), [(64, 64)], True),
+    (dict(lr=1e-3, relative_step=False, beta1=0.9, block_size=1152, m_block_size=36), [(64, 64)], True),
     (dict(ADAMW, apollo_rank=8, block_size=2048, m_block_size=256), [(64, 64)], True),
     (dict(lr=1e-2, beta1=0.9, beta2=None, beta2_decay=None, relative_step=False, block_size=1152,
           m_block_size=36), [(64, 64)], True),                                # SGD with coded momentum

@@ -1380,12 +1380,16 @@ def _apollo_prep(opt, p, grad, st, group):
     came = group.get("beta3") is not None
     if came and beta1 is None:
         raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update instability.")
-    if p.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-        raise NotImplementedError("adafactor8bit: APOLLO needs fp32, bf16 or fp16 parameters")
+    if p.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
+        raise NotImplementedError("adafactor8bit: APOLLO needs fp32, bf16, fp16 or fp64 parameters")
+    if p.dtype == torch.float64 and group["scale_parameter"]:
+        # the reference's alpha (optimizer.py:850-852) takes the norm with dtype=float32,
+        # which torch refuses for a float64 tensor: the same error here
+        torch.linalg.vector_norm(p, ord=2, dtype=torch.float32)
     if not p.is_contiguous():
         raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
     g = grad if grad.is_contiguous() else grad.contiguous()
-    if p.dtype == torch.float16:
+    if p.dtype in (torch.float16, torch.float64):
         # the projection runs on fp32 G, as the reference's grad.float() (optimizer.py:2601)
         g = g.float()
     elif g.dtype != p.dtype:

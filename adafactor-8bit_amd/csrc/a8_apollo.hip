@@ -1190,7 +1190,8 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
   const GT* G = reinterpret_cast<const GT*>(D.grad);
   const uint32_t e0 = (uint32_t)unit * kApApp + threadIdx.x * 8u;
   if (e0 >= n) return;
-  float g[8], p[8], f[8];
+  float g[8], f[8];
+  pval_t<T> p[8];   // double for fp64 parameters
   load8<GT>(G, e0, n, g);
   load8<T>(P, e0, n, p);
   const uint32_t row = e0 / C, col = e0 - row * C;
@@ -1236,6 +1237,19 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
       for (int k = 0; k < 8; ++k)
         if (e0 + k < n) gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
     }
+  } else if constexpr (sizeof(T) == 8) {
+    // fp64 parameter (G read as fp32): p.mul_(decay), then addcmul_ / add_ in
+    // double, as torch computes them on a float64 tensor with fp32 operands
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const double gk = (double)scrub(g[k]);
+      double x = p[k];
+      if (has_dec) x = pdec(x, dec);
+      if (h.channel) x = x + ((double)step * gk) * (double)f[k];
+      else x = __builtin_fma((double)ts, gk, x);
+      p[k] = x;
+    }
+    store8<T>(P, e0, n, p);
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -1311,8 +1325,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
                       void* stream) {
   if (n <= 0) return 0;
   if (!ts) return set_error(A8_ERR_ARG, "null tensor list");
-  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16)
-    return set_error(A8_ERR_DTYPE, "APOLLO supports fp32, bf16 and fp16 params");
+  if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
+    return set_error(A8_ERR_DTYPE, "APOLLO supports fp32, bf16, fp16 and fp64 params");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
   auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
   if (v_bits && !(pow2(block_size) && block_size >= 128 && block_size <= 2048))
@@ -1321,7 +1335,9 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     return set_error(A8_ERR_BLOCK, "APOLLO m_block_size must be a power of two in [32, 2048]");
   if (n > 1 && (!table_dev || tbytes < table_bytes(n)))
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_apollo_table_bytes(n)");
-  if (stochastic && dtype == A8_F32) stochastic = 0;
+  if (dtype == A8_F64 && scale_parameter)   // the reference takes an fp32 norm of the fp64 tensor, which torch refuses
+    return set_error(A8_ERR_ARG, "scale_parameter is not available for fp64 APOLLO parameters");
+  if (stochastic && (dtype == A8_F32 || dtype == A8_F64)) stochastic = 0;
   std::vector<ApDesc> tab((size_t)n);
   std::vector<int32_t> first((size_t)5 * n);
   int64_t nrt = 0, nlt = 0, nunit = 0, nsc = 0, napp = 0;
@@ -1444,6 +1460,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   if ((rc = check_launch("k_ap_scalars"))) return rc;
   if (dtype == A8_F32)
     hipLaunchKernelGGL((k_ap_apply<float, false>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
+  else if (dtype == A8_F64)
+    hipLaunchKernelGGL((k_ap_apply<double, false, float>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
   else if (dtype == A8_F16 && stochastic)
     hipLaunchKernelGGL((k_ap_apply<__half, true, float>), dim3((unsigned)napp), dim3(256), 0, st, one, dtab, n, h);
   else if (dtype == A8_F16)

@@ -40,8 +40,10 @@ extern "C" {
 /* fp64 parameters (the reference's kernels dispatch double too,
  * AT_DISPATCH_FLOATING_TYPES_AND2, kernels.cu:840): the gradient is read as fp32
  * and the parameter takes its update in double, as the reference's PyTorch path
- * does on a float64 tensor.  Accepted by the 1-D (quantised and fp32-state), SGD
- * and factored steps; no stochastic rounding. */
+ * does on a float64 tensor.  Accepted by the 1-D (quantised and fp32-state), SGD,
+ * factored and APOLLO steps (APOLLO: grad is an fp32 copy, projected with the
+ * fp32 GEMM; scale_parameter is refused, as torch refuses the reference's fp32
+ * norm of a float64 tensor); no stochastic rounding. */
 #define A8_F64 3
 
 /* kernel modes (kernels.cu:19-24): single pass, norm pass, apply pass, lagged norm */
@@ -326,9 +328,9 @@ int64_t a8_table_bytes_2d(int ntensors);
  * One full-rank matrix (a 2-D view: rows x cols; higher-rank parameters are
  * viewed as [shape[0], -1]) per call. */
 typedef struct a8_apollo_tensor {
-  void* param;             /* fp32, bf16 or fp16, rows x cols */
-  const void* grad;        /* same dtype as param; fp32 for fp16 params (the reference
-                              projects grad.float(), optimizer.py:2601) */
+  void* param;             /* fp32, bf16, fp16 or fp64, rows x cols */
+  const void* grad;        /* same dtype as param; fp32 for fp16 and fp64 params (the
+                              reference projects grad.float(), optimizer.py:2601) */
   int64_t rows, cols;
   const float* proj_t;     /* projection P^T, fp32: right side (rows >= cols) [cols x rank],
                               left side [rank x rows] (P = stable_randn / sqrt(rank)) */

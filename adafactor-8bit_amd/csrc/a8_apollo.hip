@@ -43,7 +43,8 @@ constexpr int kApPass = 256;    // low-rank outputs per projection pass (4 waves
 constexpr int kApUnit = 2048;   // low-rank elements per k_ap_low workgroup (8 per lane)
 constexpr int kApScR = 16;      // right side: g_low rows per k_ap_scale workgroup
 constexpr int kApScL = 64;      // left side: g_low columns per k_ap_scale workgroup
-constexpr int kApApp = 2048;    // matrix elements per k_ap_apply workgroup (8 per lane)
+constexpr int kApRuns = 2;      // runs of eight elements per k_ap_apply lane (4 measured slower)
+constexpr int kApApp = 2048 * kApRuns;   // matrix elements per k_ap_apply workgroup
 
 // Workspace of one matrix (offsets in floats; partial arrays hold doubles).
 struct ApL {
@@ -1188,80 +1189,107 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
   const bool has_dec = h.wd_mode != 0;
   T* P = reinterpret_cast<T*>(D.param);
   const GT* G = reinterpret_cast<const GT*>(D.grad);
-  const uint32_t e0 = (uint32_t)unit * kApApp + threadIdx.x * 8u;
-  if (e0 >= n) return;
-  float g[8], f[8];
-  pval_t<T> p[8];   // double for fp64 parameters
-  load8<GT>(G, e0, n, g);
-  load8<T>(P, e0, n, p);
-  const uint32_t row = e0 / C, col = e0 - row * C;
-  if (!h.channel) {
+  // kApRuns runs of eight per lane, 2048 elements apart; every run's loads are
+  // issued before the first is computed (a wave keeps several kilobytes in flight)
+  const uint32_t ea = (uint32_t)unit * kApApp + threadIdx.x * 8u;
+  if (ea >= n) return;
+  float gr[kApRuns][8];
+  pval_t<T> pr[kApRuns][8];   // double for fp64 parameters
 #pragma unroll
-    for (int k = 0; k < 8; ++k) f[k] = fin_t;
-  } else if (D.valign && e0 + 8 <= n) {   // all eight in one row
-    if (right) {
-      const float fr = ap_fch<T>(fin, row, fs, h);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) f[k] = fr;
-    } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) f[k] = ap_fch<T>(fin, col + k, fs, h);
-    }
-  } else {
-    uint32_t rr = row, cc = col;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      f[k] = (e0 + k < n) ? ap_fch<T>(fin, right ? rr : cc, fs, h) : 0.0f;
-      if (++cc == C) { cc = 0; ++rr; }
+  for (int q = 0; q < kApRuns; ++q) {
+    const uint32_t e = ea + 2048u * q;
+    if (q == 0 || e < n) {
+      load8<GT>(G, e, n, gr[q]);
+      load8<T>(P, e, n, pr[q]);
     }
   }
-  const float ts = step * fin_t;   // tensor: alpha = step * final_scale
-  if constexpr (SR) {
-    const uint64_t base = sr_base(D.sr_seed, D.step);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+  auto run8 = [&](const uint32_t e0, float* g, pval_t<T>* p) {
+    float f[8];
+    const uint32_t row = e0 / C, col = e0 - row * C;
+    if (!h.channel) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float x = p[k];
-      if (has_dec) x = x * dec;
-      x = x + (scrub(g[k]) * f[k]) * step;
-      const uint32_t bits = sr_bits_at(base, (uint64_t)(e0 + k));
-      uint16_t hb;
-      if constexpr (std::is_same<T, __half>::value) hb = sr_fp16(x, (float)(bits >> 8) * (1.0f / 16777216.0f));
-      else hb = sr_bf16_bits(x, bits);
-      w[k >> 1] |= (uint32_t)hb << (16 * (k & 1));
+      for (int k = 0; k < 8; ++k) f[k] = fin_t;
+    } else if (D.valign && e0 + 8 <= n) {   // all eight in one row
+      if (right) {
+        const float fr = ap_fch<T>(fin, row, fs, h);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] = fr;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[k] = ap_fch<T>(fin, col + k, fs, h);
+      }
+    } else {
+      uint32_t rr = row, cc = col;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        f[k] = (e0 + k < n) ? ap_fch<T>(fin, right ? rr : cc, fs, h) : 0.0f;
+        if (++cc == C) { cc = 0; ++rr; }
+      }
     }
-    if (e0 + 8 <= n) {
-      *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P) + e0)) = u32x4{w[0], w[1], w[2], w[3]};
+    const float ts = step * fin_t;   // tensor: alpha = step * final_scale
+    if constexpr (SR) {
+      // The lane's first counter; element k's is zb + k.  The random words come
+      // first: unless the low word wraps within the eight (a lane in 6e8), the
+      // counters share their high word and so its share of the first product.
+      const uint64_t zb = sr_base(D.sr_seed, D.step) + 0x9E3779B97F4A7C15ULL + (uint64_t)e0;
+      const uint32_t zl = (uint32_t)zb, zh = (uint32_t)(zb >> 32);
+      uint32_t hv[8];
+      if (zl <= 0xFFFFFFF8u) {
+        const uint32_t yhc = sm_yhc(zh);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) hv[k] = sm_hi_yh(zl + (uint32_t)k, zh, yhc);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) hv[k] = sm_hi(zb + (uint64_t)k);
+      }
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float x = p[k];
+        if (has_dec) x = x * dec;
+        x = x + (scrub(g[k]) * f[k]) * step;
+        const uint32_t hi = hv[k];
+        uint16_t hb;
+        if constexpr (std::is_same<T, __half>::value) hb = sr_fp16(x, (float)(hi >> 8) * (1.0f / 16777216.0f));
+        else hb = sr_bf16_hi(x, hi);
+        w[k >> 1] |= (uint32_t)hb << (16 * (k & 1));
+      }
+      if (e0 + 8 <= n) {
+        *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P) + e0)) = u32x4{w[0], w[1], w[2], w[3]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (e0 + k < n) gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+      }
+    } else if constexpr (sizeof(T) == 8) {
+      // fp64 parameter (G read as fp32): p.mul_(decay), then addcmul_ / add_ in
+      // double, as torch computes them on a float64 tensor with fp32 operands
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double gk = (double)scrub(g[k]);
+        double x = p[k];
+        if (has_dec) x = pdec(x, dec);
+        if (h.channel) x = x + ((double)step * gk) * (double)f[k];
+        else x = __builtin_fma((double)ts, gk, x);
+        p[k] = x;
+      }
+      store8<T>(P, e0, n, p);
     } else {
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (e0 + k < n) gp(reinterpret_cast<uint16_t*>(P))[e0 + k] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+      for (int k = 0; k < 8; ++k) {
+        const float gk = scrub(g[k]);
+        float x = p[k];
+        if (has_dec) x = to_f<T>(from_f<T>(x * dec));
+        if (h.channel) x = x + (step * gk) * f[k];
+        else x = __builtin_fmaf(ts, gk, x);
+        p[k] = x;
+      }
+      store8<T>(P, e0, n, p);
     }
-  } else if constexpr (sizeof(T) == 8) {
-    // fp64 parameter (G read as fp32): p.mul_(decay), then addcmul_ / add_ in
-    // double, as torch computes them on a float64 tensor with fp32 operands
+  };
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const double gk = (double)scrub(g[k]);
-      double x = p[k];
-      if (has_dec) x = pdec(x, dec);
-      if (h.channel) x = x + ((double)step * gk) * (double)f[k];
-      else x = __builtin_fma((double)ts, gk, x);
-      p[k] = x;
-    }
-    store8<T>(P, e0, n, p);
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float gk = scrub(g[k]);
-      float x = p[k];
-      if (has_dec) x = to_f<T>(from_f<T>(x * dec));
-      if (h.channel) x = x + (step * gk) * f[k];
-      else x = __builtin_fmaf(ts, gk, x);
-      p[k] = x;
-    }
-    store8<T>(P, e0, n, p);
-  }
+  for (int q = 0; q < kApRuns; ++q)
+    if (q == 0 || ea + 2048u * q < n) run8(ea + 2048u * q, gr[q], pr[q]);
 }
 
 hipError_t apollo_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }

@@ -21,46 +21,65 @@ static inline hipError_t upload_qmap_tu(const float* q8, const float* q4) {
 // ------------------------------------------------------------ SR writeback
 // SplitMix64 counter stream keyed by (seed, step, element) and the bf16/fp16
 // stochastic rounding rules of the reference (kernels.cu:48-161).
-__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64_t idx) {
-  uint64_t z = seed * 0x9E3779B97F4A7C15ULL + step * 0xD1B54A32D192ED03ULL + idx;
-  z += 0x9E3779B97F4A7C15ULL;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-  z ^= z >> 31;
-  return (uint32_t)(z >> 32);
+//
+// sm_hi(z): the high 32 bits of the mix of counter z before its last xorshift,
+// in 32-bit halves: z ^ (z >> k) takes one funnel shift (v_alignbit) for the low
+// word, a 64 x 64 product keeps only what its low 64 bits need (the second one
+// only its high word).  The stream's 32 random bits are hi ^ (hi >> 31) (the high
+// word of z ^ (z >> 31)); every consumer here reads bits >> 8 or less, to which
+// that xor is invisible, so the decisions take hi itself.  sm_hi_yh takes
+// yhc = (zh ^ (zh >> 30)) * 0x1CE4E5B9, the high word's share of the first
+// product, which counters that differ only in their low word share.
+__device__ __forceinline__ uint32_t sm_hi_yh(uint32_t zl, uint32_t zh, uint32_t yhc) {
+  const uint32_t yl = zl ^ __builtin_amdgcn_alignbit(zh, zl, 30);
+  const uint64_t p = (uint64_t)yl * 0x1CE4E5B9u;   // * 0xBF58476D1CE4E5B9
+  const uint32_t z1l = (uint32_t)p;
+  const uint32_t z1h = (uint32_t)(p >> 32) + yl * 0xBF58476Du + yhc;
+  const uint32_t y2l = z1l ^ __builtin_amdgcn_alignbit(z1h, z1l, 27), y2h = z1h ^ (z1h >> 27);
+  return __umulhi(y2l, 0x133111EBu) + y2l * 0x94D049BBu + y2h * 0x133111EBu;   // * 0x94D049BB133111EB
+}
+__device__ __forceinline__ uint32_t sm_yhc(uint32_t zh) { return (zh ^ (zh >> 30)) * 0x1CE4E5B9u; }
+
+__device__ __forceinline__ uint32_t sm_hi(uint64_t z) {
+  return sm_hi_yh((uint32_t)z, (uint32_t)(z >> 32), sm_yhc((uint32_t)(z >> 32)));
 }
 
-// The same stream from a precomputed counter base (seed * gamma + step * K): the
-// element's 32 random bits.
-__device__ __forceinline__ uint32_t sr_bits_at(uint64_t base, uint64_t idx) {
-  uint64_t z = base + idx + 0x9E3779B97F4A7C15ULL;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-  z ^= z >> 31;
-  return (uint32_t)(z >> 32);
-}
 __device__ __forceinline__ uint64_t sr_base(uint64_t seed, uint64_t step) {
   return seed * 0x9E3779B97F4A7C15ULL + step * 0xD1B54A32D192ED03ULL;
 }
 
-// bf16 stochastic rounding decided in integers: u < rem / 2^16 with
-// u = (bits >> 8) / 2^24 is (bits >> 8) < rem * 2^8 exactly (both sides are
-// exact in fp32), so the result equals sr_bf16(x, u).  sr_bf16's three guards
-// fold into one magnitude compare: rem == 0 never rounds up (the compare is
-// false), and |x| >= 0x7F7F0000 (inf, NaN, or a truncation whose upper
-// neighbour is inf) never rounds up either; NaN becomes the quiet NaN.
-__device__ __forceinline__ uint16_t sr_bf16_bits(float x, uint32_t bits) {
-  const uint32_t b = __float_as_uint(x);
-  const uint32_t a = b & 0x7FFFFFFFu;
-  const uint32_t rem = b & 0x0000FFFFu;
-  const bool up = ((bits >> 8) < (rem << 8)) && a < 0x7F7F0000u;
-  const uint32_t r = (a > 0x7F800000u) ? ((b & 0x80000000u) | 0x7FC00000u)
-                                       : (b & 0xFFFF0000u) + (up ? 0x00010000u : 0u);
-  return (uint16_t)(r >> 16);
+// sm_hi of the element's counter (seed * gamma + step * K + idx + gamma).
+__device__ __forceinline__ uint32_t sr_hi_at(uint64_t base, uint64_t idx) {
+  return sm_hi(base + idx + 0x9E3779B97F4A7C15ULL);
 }
 
+// The element's 32 random bits.
+__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64_t idx) {
+  const uint32_t hi = sr_hi_at(sr_base(seed, step), idx);
+  return hi ^ (hi >> 31);
+}
+__device__ __forceinline__ uint32_t sr_bits_at(uint64_t base, uint64_t idx) {
+  const uint32_t hi = sr_hi_at(base, idx);
+  return hi ^ (hi >> 31);
+}
+
+// bf16 stochastic rounding decided in integers: u < rem / 2^16 with
+// u = (bits >> 8) / 2^24 is (bits >> 8) < rem * 2^8 exactly (both sides are
+// exact in fp32), that is (bits >> 16) < rem, that is hi < rem * 2^16 = x's bits
+// << 16 (bits and hi differ in bit 0 only), so the result equals sr_bf16(x, u).
+// sr_bf16's three guards fold into one magnitude compare: rem == 0 never rounds
+// up (the compare is false), and |x| >= 0x7F7F0000 (inf, NaN, or a truncation
+// whose upper neighbour is inf) never rounds up either; NaN becomes the quiet NaN.
+__device__ __forceinline__ uint16_t sr_bf16_hi(float x, uint32_t hi) {
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t a = b & 0x7FFFFFFFu;
+  const uint32_t up = (uint32_t)(hi < (b << 16)) & (uint32_t)(a < 0x7F7F0000u);
+  const uint32_t rn = (b >> 16) + up;
+  const uint32_t rq = ((b >> 16) & 0x8000u) | 0x7FC0u;
+  return (uint16_t)(a > 0x7F800000u ? rq : rn);
+}
 __device__ __forceinline__ float sr_uniform(uint64_t seed, uint64_t step, uint64_t idx) {
-  return (float)(sr_bits(seed, step, idx) >> 8) * (1.0f / 16777216.0f);
+  return (float)(sr_hi_at(sr_base(seed, step), idx) >> 8) * (1.0f / 16777216.0f);
 }
 
 __device__ __forceinline__ uint16_t sr_bf16(float x, float u) {
@@ -107,11 +126,10 @@ __device__ __forceinline__ uint16_t sr_fp16(float x, float u) {
 
 template <typename T>
 __device__ __forceinline__ T sr_round(float x, uint64_t seed, uint64_t step, uint64_t idx) {
-  float u = sr_uniform(seed, step, idx);
-  if constexpr (sizeof(T) == 2 && std::is_same<T, __hip_bfloat16>::value) {
-    return __ushort_as_bfloat16(sr_bf16(x, u));
+  if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+    return __ushort_as_bfloat16(sr_bf16_hi(x, sr_hi_at(sr_base(seed, step), idx)));
   } else if constexpr (sizeof(T) == 2) {
-    return __ushort_as_half(sr_fp16(x, u));
+    return __ushort_as_half(sr_fp16(x, sr_uniform(seed, step, idx)));
   } else {
     return x;
   }

@@ -271,3 +271,56 @@ def test_apollo_general_blocks_match_oracle(name, kw, monkeypatch):
             assert "m_low_q" in og.state[pg[0]] or kw.get("beta1") is None
     finally:
         F.set_exact_reductions(old)
+
+
+# SR writeback in the general-block kernels (k_update1d_gen, k_sgd_gen,
+# k_fupdate_gen): the 16-bit result is the stochastic rounding, under the
+# reference's stream (kernels.cu:48-131, oracle/sr.py), of the same step run on
+# fp32 parameters; the two runs round (p - step * u) once apart, so at most 0.1% of
+# the elements may land on the other neighbour (as in the unit-layout SR test,
+# tests/test_gpu_apollo.py::test_1d_sr_writeback_stream).
+SR_CASES = [
+    ("adamw_bv384_bm96", dict(ADAMW, block_size=384, m_block_size=96), [(700, 300), (5000,)]),
+    ("sgd_bm36_wd", dict(SGD, block_size=1152, m_block_size=36, weight_decay=0.01), [(700, 300), (5000,)]),
+    ("factored_bm36", dict(FACT, block_size=1152, m_block_size=36, d=1.0), [(300, 77), (256, 384)]),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("name,kw,shapes", SR_CASES, ids=[c[0] for c in SR_CASES])
+def test_general_block_sr_writeback_stream(name, kw, shapes, dtype):
+    from adafactor8bit import Adafactor8Bit
+    from inputs import make_grad, make_param
+    from oracle import sr
+    print(f"[block sizes sr] {name} {dtype}", flush=True)
+    p16 = [torch.nn.Parameter(make_param(s, i, 3).to("cuda", dtype)) for i, s in enumerate(shapes)]
+    p32 = [torch.nn.Parameter(p.detach().float()) for p in p16]
+    o16 = Adafactor8Bit(p16, **dict(kw, stochastic_round_writeback=True))
+    o32 = Adafactor8Bit(p32, **kw)
+    for i, s in enumerate(shapes):
+        g = make_grad(s, i, 1, 3).to(dtype).cuda()
+        p16[i].grad = g
+        p32[i].grad = g.float()
+    o16.step()
+    o32.step()
+    torch.cuda.synchronize()
+    rnd = sr.sr_round_bf16 if dtype == torch.bfloat16 else sr.sr_round_fp16
+    for p, q in zip(p16, p32):
+        assert o16.state[p]["is_quantized"]
+        x = q.detach().cpu().numpy().reshape(-1)
+        want = rnd(x, seed=int(o16.state[p]["sr_seed"]), step=int(o16.state[p]["step"]))
+        got = p.detach().cpu().view(torch.int16).numpy().reshape(-1).view(np.uint16)
+        diff = got != want
+        print(f"  {tuple(p.shape)}: {diff.mean():.2e} on the other neighbour", flush=True)
+        assert diff.sum() <= max(1, 1e-3 * diff.size), diff.mean()
+        x16 = x.astype(np.float16) if dtype == torch.float16 else None
+        if dtype == torch.bfloat16:
+            lo = (x.view(np.uint32) & np.uint32(0xFFFF0000)) >> np.uint32(16)
+            assert np.all(np.isin(got[diff].astype(np.int64) - lo[diff].astype(np.int64), [0, 1]))
+        else:
+            xd, q16 = x[diff], x16[diff]
+            other = np.nextafter(q16, np.where(q16.astype(np.float32) < xd, np.float16(np.inf),
+                                               np.float16(-np.inf)).astype(np.float16))
+            gv = got[diff].view(np.float16)
+            assert np.all((gv == q16) | (gv == other))

@@ -757,6 +757,30 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
     for (int k = 0; k < 8; ++k)
       if (k < cnt) g[k] = gp(ws)[L.glow + e0 + k];
   }
+  // The code streams are loaded here, before the AL8 decode table and its
+  // barrier, so that their latency overlaps the table build.
+  uint32_t cw[2] = {0u, 0u};   // AL8 codes (table path)
+  if constexpr (VB == 8) {
+    if (!first && VL >= 64) {
+      if constexpr (FULL) {
+        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
+        cw[0] = q.x; cw[1] = q.y;
+      } else if (v_ok) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          cw[k >> 2] |= (uint32_t)gp(reinterpret_cast<const uint8_t*>(D.v_q))[e0 + k] << (8 * (k & 3));
+      }
+    }
+  }
+  float ms_old = 0.0f;   // M block scale and codes
+  u32x2 mqv = {0u, 0u};
+  if constexpr (MK == 1 || MK == 2) {
+    if (m_ok) {
+      ms_old = gp(D.m_scale)[mb];
+      if (mk == 2 || mk == 4) mqv.x = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
+      else mqv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+    }
+  }
   // ---- V
   float vo[8];
 #pragma unroll
@@ -775,18 +799,6 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
       for (int c = lane % VL; c < 256; c += VL)
         dtab[bw * 256 + c] = c ? exp2_exact(((float)(c - 1) * s_old) / 254.0f + lm_old) : 0.0f;
       __syncthreads();
-      uint32_t cw[2];
-      if constexpr (FULL) {
-        const u32x2 q = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(D.v_q) + e0));
-        cw[0] = q.x; cw[1] = q.y;
-      } else {
-        cw[0] = cw[1] = 0u;
-        if (v_ok) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            cw[k >> 2] |= (uint32_t)gp(reinterpret_cast<const uint8_t*>(D.v_q))[e0 + k] << (8 * (k & 3));
-        }
-      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) vo[k] = dtab[bw * 256 + ((cw[k >> 2] >> (8 * (k & 3))) & 0xFFu)];
     } else if (v_ok) {
@@ -817,16 +829,16 @@ __device__ __forceinline__ void ap_low_unit(const ApDesc& D, const ApL& L, int u
       for (int k = 0; k < 8; ++k)
         if (k < cnt) mo[k] = gp(D.m_fp32)[e0 + k];
     } else if (m_ok) {
-      const float ms = gp(D.m_scale)[mb];
+      const float ms = ms_old;
       if (mk == 2 || mk == 4) {
-        const uint32_t qw = *gp(reinterpret_cast<const uint32_t*>(D.m_q + (e0 >> 1)));
+        const uint32_t qw = mqv.x;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t byte = (qw >> (8 * (k >> 1))) & 0xFFu;
           mo[k] = m_decode(mk, (k & 1) ? (byte & 0x0Fu) : (byte >> 4), ms);
         }
       } else {
-        const u32x2 qv = *gp(reinterpret_cast<const u32x2*>(D.m_q + e0));
+        const u32x2 qv = mqv;
 #pragma unroll
         for (int k = 0; k < 8; ++k) mo[k] = m_decode(mk, ((k < 4 ? qv.x : qv.y) >> (8 * (k & 3))) & 0xFFu, ms);
       }

@@ -54,6 +54,22 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   load8<T>(x, e0, n, xv);
   float v[8];
   const float s_old = v_ok ? gp(scale)[vb] : 0.0f, lm_old = v_ok ? gp(min_log)[vb] : 0.0f;
+  // The lane's eight codes in one 8- or 16-byte access, issued with the loads
+  // above (before the decode table's barrier).  Codes are padded to whole blocks,
+  // so a lane of an existing block reads all eight.
+  const bool cvec = v_ok && ((reinterpret_cast<uintptr_t>(q) & 15) == 0);
+  uint32_t cq[VB == 8 ? 2 : 4];
+#pragma unroll
+  for (int i = 0; i < (VB == 8 ? 2 : 4); ++i) cq[i] = 0u;
+  if (cvec) {
+    if constexpr (VB == 8) {
+      const u32x2 t = *gp(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(q) + e0));
+      cq[0] = t.x; cq[1] = t.y;
+    } else {
+      const u32x4 t = *gp(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(q) + e0));
+      cq[0] = t.x; cq[1] = t.y; cq[2] = t.z; cq[3] = t.w;
+    }
+  }
   const bool tab8 = VB == 8 && VL >= 64;   // uniform
   const int bw = tab8 ? lane / VL : 0;     // block slot of this lane in the unit
   if (tab8) {
@@ -69,7 +85,8 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
     float vo = 0.0f;
     if (k < cnt) {
       uint32_t c;
-      if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(q))[e0 + k];
+      if (cvec) c = VB == 8 ? (cq[k >> 2] >> (8 * (k & 3))) & 0xFFu : (cq[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      else if constexpr (VB == 8) c = gp(reinterpret_cast<const uint8_t*>(q))[e0 + k];
       else c = gp(reinterpret_cast<const uint16_t*>(q))[e0 + k];
       vo = tab8 ? dtab[bw * 256 + c] : (c ? exp2_exact(((float)(c - 1) * s_old) / LM2 + lm_old) : 0.0f);
     }
@@ -104,7 +121,17 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   const ALFit f = al_refit_pair(bmax, mnz, floor_, (float)L2, lane);   // a block spans >= 16 lanes
   uint32_t code[8];
   al_codes<L2, 8>(v, f, code);
-  if (v_ok) {
+  if (cvec) {
+    if constexpr (VB == 8) {
+      *gp(reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(q) + e0)) =
+          u32x2{code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24),
+                code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24)};
+    } else {
+      *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(q) + e0)) =
+          u32x4{code[0] | (code[1] << 16), code[2] | (code[3] << 16), code[4] | (code[5] << 16),
+                code[6] | (code[7] << 16)};
+    }
+  } else if (v_ok) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       if constexpr (VB == 8) gp(reinterpret_cast<uint8_t*>(q))[e0 + k] = (uint8_t)code[k];

@@ -51,6 +51,25 @@ int64_t m_ema_table_bytes(int n);
 int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int block_size, int m_bits, int m_mode,
                 hipStream_t st);
 
+struct CameTailItem {   // non-factorised CAME APOLLO after the RMS clip (k_came_tail)
+  const float* U;         // U before the clip division
+  const float* clip;      // device clip factor, or null (d = 0)
+  uint8_t* m_q;           // coded momentum, or
+  float* m_scale;
+  float* m_fp32;          // fp32 momentum
+  void* r_q;              // coded residual EMA, or
+  float* r_scale;
+  float* r_min_log;
+  float* r_fp32;          // fp32 residual EMA
+  float* u;               // out: the low-rank update
+  int64_t n;
+};
+bool came_tail_ok(int m_fp32, int m_block_size, int c_bits, int block_size);
+int64_t came_tail_table_bytes(int n);
+int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1, double beta3, float eps_came,
+                    float eps_sq, int m_fp32, int m_bits, int m_mode, int m_block_size, int c_bits, int block_size,
+                    hipStream_t st);
+
 struct VEmaItem {   // AL state: v' = lerp(deq(v), x (or x^2 + eps1), w), re-encoded with a block refit
   void* q;
   float* scale;

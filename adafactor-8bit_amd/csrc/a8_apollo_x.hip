@@ -422,6 +422,7 @@ struct XB {
   XD* tab_dev;          // n descriptors
   void* mema_dev;       // m_ema_table_bytes(n)
   void* vema_dev;       // v_ema_table_bytes(2 n)
+  void* tail_dev;       // came_tail_table_bytes(n)
   hipStream_t st;
 };
 
@@ -570,6 +571,29 @@ static int x_run(XB& b) {
     return x_el<XE_AU>(b);
   }
   if ((rc = x_el<XE_U>(b))) return rc;
+  // the fused tail takes power-of-two blocks and 16-byte aligned streams (its lanes
+  // read eight elements at a time); other batches run the passes one by one
+  bool tail = a0->has_m && came_tail_ok(a0->m_fp32 != nullptr, a0->m_block_size, a0->c_bits, a0->block_size);
+  for (size_t i = 0; tail && i < n; ++i) {
+    const a8_apollo_x_args* a = b.a[i];
+    const XK& k = b.d[i].k;
+    tail = aligned16(k.dst) && aligned16(k.u) && (a->m_fp32 ? aligned16(a->m_fp32) : aligned16(a->m_q)) &&
+           (a->c_bits || aligned16(a->res_fp32));
+  }
+  if (tail) {
+    // the clip factor, then one kernel for division, momentum, residual, its EMA and u
+    if (a0->d > 0.0f && (rc = x_s<XS_CLIP>(b))) return rc;
+    std::vector<CameTailItem> it(n);
+    for (size_t i = 0; i < n; ++i) {
+      const a8_apollo_x_args* a = b.a[i];
+      const XK& k = b.d[i].k;
+      it[i] = CameTailItem{k.dst, a->d > 0.0f ? k.ws + x_layout(k.R, k.C).scal : nullptr, a->m_q, a->m_scale,
+                           a->m_fp32, a->res_q, a->res_scale, a->res_min_log, a->res_fp32, k.u, k.n};
+    }
+    return came_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->beta3, a0->eps_came, a0->eps_sq,
+                           a0->m_fp32 != nullptr, a0->m_bits, a0->m_mode, a0->m_block_size, a0->c_bits,
+                           a0->block_size, b.st);
+  }
   if ((rc = x_clip(b))) return rc;
   if (!a0->has_m) return 0;   // unreachable through the optimizer (beta3 needs beta1): u = clipped U
   if ((rc = x_momentum(b, true))) return rc;
@@ -673,7 +697,8 @@ static bool x_same(const a8_apollo_x_args* a, const a8_apollo_x_args* b) {
 // Table bytes of one batch of n matrices: descriptors, momentum and AL tables.
 static int64_t x_round(int64_t b) { return (b + 255) / 256 * 256; }
 static int64_t x_bytes(int n) {
-  return x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) + x_round(v_ema_table_bytes(2 * n));
+  return x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) + x_round(v_ema_table_bytes(2 * n)) +
+         x_round(came_tail_table_bytes(n));
 }
 
 }  // namespace a8
@@ -741,6 +766,7 @@ int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* tabl
     b.tab_dev = reinterpret_cast<XD*>(base);
     b.mema_dev = base + x_round((int64_t)sizeof(XD) * n);
     b.vema_dev = static_cast<char*>(b.mema_dev) + x_round(m_ema_table_bytes(n));
+    b.tail_dev = static_cast<char*>(b.vema_dev) + x_round(v_ema_table_bytes(2 * n));
     base += x_bytes(n);
     int rc = x_sync(b);
     if (rc) return rc;

@@ -36,12 +36,15 @@ constexpr int kPElems = 2048;
 // through a table of their 255 values (one correctly rounded exp2 per lane and
 // block instead of one per element); the new codes take the fast AL8 argument
 // with exact re-decision near rounding boundaries.
-template <int VB, typename T>
+// XREG: the lane's eight inputs come in registers (xreg) instead of from x, and
+// the decoded new codes are returned in dvr (every lane reaches the barriers).
+template <int VB, typename T, bool XREG = false>
 __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restrict__ scale,
                                           float* __restrict__ min_log, const T* __restrict__ x,
                                           float* __restrict__ out, float* __restrict__ dec, int64_t n, int64_t nblk,
                                           int64_t bid, int lbv, float w, int square, float eps1, float floor_,
-                                          float* xw, float* dtab) {
+                                          float* xw, float* dtab, const float* xreg = nullptr,
+                                          float* dvr = nullptr) {
   const int lane = threadIdx.x, wave = lane >> 6;
   const int64_t e0 = bid * kPElems + (int64_t)lane * 8;
   const int VL = (1 << lbv) >> 3;
@@ -51,7 +54,12 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
   const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
   constexpr float LM2 = VB == 8 ? 254.0f : 65534.0f;
   float xv[8];
-  load8<T>(x, e0, n, xv);
+  if constexpr (XREG) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xv[k] = xreg[k];
+  } else {
+    load8<T>(x, e0, n, xv);
+  }
   float v[8];
   const float s_old = v_ok ? gp(scale)[vb] : 0.0f, lm_old = v_ok ? gp(min_log)[vb] : 0.0f;
   // The lane's eight codes in one 8- or 16-byte access, issued with the loads
@@ -138,7 +146,7 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
       else gp(reinterpret_cast<uint16_t*>(q))[e0 + k] = (uint16_t)code[k];
     }
   }
-  if (dec) {   // uniform
+  if (dec || XREG) {   // uniform
     float dv[8];
     if (tab8) {   // the new fit's table, after every lane has read the old one
       __syncthreads();
@@ -152,7 +160,11 @@ __device__ __forceinline__ void vema_unit(void* __restrict__ q, float* __restric
       for (int k = 0; k < 8; ++k)
         dv[k] = code[k] ? exp2_exact(((float)(code[k] - 1) * f.s) / LM2 + f.lmin) : 0.0f;
     }
-    if (v_ok) store8<float>(dec, e0, n, dv);
+    if (dec && v_ok) store8<float>(dec, e0, n, dv);
+    if constexpr (XREG) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dvr[k] = dv[k];
+    }
   }
   if (v_ok && (lane & (VL - 1)) == 0) { gp(scale)[vb] = f.s; gp(min_log)[vb] = f.lmin; }
 }
@@ -704,6 +716,174 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
     hipLaunchKernelGGL(k_vema_multi<16>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
                        eps1, log_floor);
   return check_launch("k_vema_multi");
+}
+
+// ------------------------------------------------------------ CAME APOLLO tail
+// The low-rank passes of non-factorised CAME APOLLO after the RMS clip, in one
+// kernel (optimizer.py:2846-2896): U /= clip; m' = lerp(m, U, 1 - beta1)
+// re-encoded per M block (or fp32 m); res = (U - m')^2 + eps_came; its EMA with
+// beta3 (AL codes re-fitted per block and read back decoded, or fp32);
+// u = m' / sqrt(max(res, eps^2)).  One workgroup per 2048-element unit, eight
+// consecutive elements per lane (the units of k_sgd and k_vema), element for
+// element the arithmetic of the passes it replaces: the division of the clip
+// pass, k_sgd's momentum EMA (U scrubbed, as k_sgd scrubs its input) or the
+// fp32 lerp, the residual of the element pass, vema_unit for the residual EMA,
+// and the update's 1 / sqrt.  MK: 1 coded M, 3 fp32 M; VB: 8 / 16 coded
+// residual, 0 fp32.
+struct CameTailDesc {
+  const float* U;
+  const float* clip;
+  uint8_t* m_q;
+  float* m_scale;
+  float* m_fp32;
+  void* r_q;
+  float* r_scale;
+  float* r_min_log;
+  float* r_fp32;
+  float* u;
+  int64_t n, nmb, nvb, wg_begin;
+};
+
+struct CameTailHyp {
+  float w1, w3, eps_came, eps_sq;
+  int mk, lbm, lbv;
+};
+
+template <int VB, int MK>
+__global__ __launch_bounds__(256) void k_came_tail(CameTailDesc one, const CameTailDesc* __restrict__ tab, int ntab,
+                                                   CameTailHyp h) {
+  __shared__ float xw[8];
+  __shared__ float xm[4];
+  __shared__ float dtab[4 * 256];
+  const int64_t wg = blockIdx.x;
+  CameTailDesc D = one;
+  if (tab) {
+    int lo = 0, hi = ntab - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    }
+    D = tab[lo];
+  }
+  const int64_t bid = wg - D.wg_begin;
+  const int64_t n = D.n;
+  const int64_t e0 = bid * kPElems + (int64_t)threadIdx.x * 8;
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
+  float U[8];
+  load8<float>(D.U, e0, n, U);
+  if (D.clip) {   // uniform
+    const float clip = *gp(D.clip);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) U[k] = U[k] / clip;
+  }
+  // ---- momentum
+  float m[8];
+  if constexpr (MK == 3) {
+    float mo[8];
+    load8<float>(D.m_fp32, e0, n, mo);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = lerp_ref(mo[k], U[k], h.w1);
+    store8<float>(D.m_fp32, e0, n, m);
+  } else {
+    const int64_t mb = e0 >> h.lbm;
+    const bool m_ok = mb < D.nmb;   // codes are padded to whole blocks
+    float mo[8];
+    mq_decode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, mo);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], scrub(U[k]), h.w1) : 0.0f;
+    mq_encode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, m, (1 << h.lbm) >> 3, xm);
+  }
+  // ---- residual and its EMA
+  float rin[8], res[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float r = U[k] - m[k];
+    r = r * r;
+    rin[k] = r + h.eps_came;
+  }
+  if constexpr (VB == 0) {
+    float ro[8];
+    load8<float>(D.r_fp32, e0, n, ro);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) res[k] = lerp_ref(ro[k], rin[k], h.w3);
+    store8<float>(D.r_fp32, e0, n, res);
+  } else {
+    vema_unit<VB, float, true>(D.r_q, D.r_scale, D.r_min_log, nullptr, nullptr, nullptr, n, D.nvb, bid, h.lbv, h.w3,
+                               0, 0.0f, -126.0f, xw, dtab, rin, res);
+  }
+  // ---- update
+  float uo[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) uo[k] = m[k] * (1.0f / sqrtf(fmaxf(res[k], h.eps_sq)));
+  store8<float>(D.u, e0, n, uo);
+}
+
+static bool pow2_in(int x, int lo, int hi) { return x >= lo && x <= hi && (x & (x - 1)) == 0; }
+
+bool came_tail_ok(int m_fp32, int m_block_size, int c_bits, int block_size) {
+  return (m_fp32 || pow2_in(m_block_size, 32, 2048)) && (c_bits == 0 || pow2_in(block_size, 128, 2048));
+}
+
+int64_t came_tail_table_bytes(int n) { return (int64_t)sizeof(CameTailDesc) * (int64_t)n; }
+
+int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1, double beta3, float eps_came,
+                    float eps_sq, int m_fp32, int m_bits, int m_mode, int m_block_size, int c_bits, int block_size,
+                    hipStream_t st) {
+  if (n <= 0) return 0;
+  if (!came_tail_ok(m_fp32, m_block_size, c_bits, block_size))
+    return set_error(A8_ERR_BLOCK, "CAME tail: block sizes must be powers of two");
+  CameTailHyp h{};
+  h.w1 = (float)(1.0 - beta1);
+  h.w3 = (float)(1.0 - beta3);
+  h.eps_came = eps_came;
+  h.eps_sq = eps_sq;
+  if (!m_fp32) {
+    if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
+      return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
+    h.mk = m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4);
+  }
+  while ((1 << h.lbm) < (m_fp32 ? 32 : m_block_size)) ++h.lbm;
+  while ((1 << h.lbv) < (c_bits ? block_size : 128)) ++h.lbv;
+  std::vector<CameTailDesc> tab((size_t)n);
+  int64_t wg = 0;
+  for (int i = 0; i < n; ++i) {
+    const CameTailItem& t = it[i];
+    if (!t.U || !t.u || (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale)) ||
+        (c_bits ? !(t.r_q && t.r_scale && t.r_min_log) : !t.r_fp32))
+      return set_error(A8_ERR_ARG, "CAME tail: state missing");
+    if (!aligned16(t.U) || !aligned16(t.u) || (m_fp32 ? !aligned16(t.m_fp32) : !aligned16(t.m_q)) ||
+        (!c_bits && !aligned16(t.r_fp32)))
+      return set_error(A8_ERR_ALIGN, "CAME tail: streams must be 16-byte aligned");
+    CameTailDesc& D = tab[(size_t)i];
+    D.U = t.U; D.clip = t.clip; D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
+    D.r_q = t.r_q; D.r_scale = t.r_scale; D.r_min_log = t.r_min_log; D.r_fp32 = t.r_fp32; D.u = t.u;
+    D.n = t.n;
+    D.nmb = (t.n + (1 << h.lbm) - 1) >> h.lbm;
+    D.nvb = (t.n + (1 << h.lbv) - 1) >> h.lbv;
+    D.wg_begin = wg;
+    wg += (t.n + kPElems - 1) / kPElems;   // blocks are powers of two up to a unit: padding stays inside
+  }
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "CAME tail: too many elements");
+  const CameTailDesc* dt = nullptr;
+  if (n > 1) {
+    if (!table_dev) return set_error(A8_ERR_ARG, "CAME tail: a table is needed for several matrices");
+    if (upload_table(table_dev, tab.data(), sizeof(CameTailDesc) * (size_t)n, st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "table upload failed");
+    dt = reinterpret_cast<const CameTailDesc*>(table_dev);
+  }
+  const dim3 g((unsigned)wg), b(256);
+  const CameTailDesc& one = tab[0];
+  if (m_fp32) {
+    if (c_bits == 8) hipLaunchKernelGGL((k_came_tail<8, 3>), g, b, 0, st, one, dt, n, h);
+    else if (c_bits == 16) hipLaunchKernelGGL((k_came_tail<16, 3>), g, b, 0, st, one, dt, n, h);
+    else hipLaunchKernelGGL((k_came_tail<0, 3>), g, b, 0, st, one, dt, n, h);
+  } else {
+    if (c_bits == 8) hipLaunchKernelGGL((k_came_tail<8, 1>), g, b, 0, st, one, dt, n, h);
+    else if (c_bits == 16) hipLaunchKernelGGL((k_came_tail<16, 1>), g, b, 0, st, one, dt, n, h);
+    else hipLaunchKernelGGL((k_came_tail<0, 1>), g, b, 0, st, one, dt, n, h);
+  }
+  return check_launch("k_came_tail");
 }
 
 }  // namespace a8

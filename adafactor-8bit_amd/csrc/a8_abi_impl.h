@@ -70,6 +70,21 @@ int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1
                     float eps_sq, int m_fp32, int m_bits, int m_mode, int m_block_size, int c_bits, int block_size,
                     hipStream_t st);
 
+struct FactTailItem {   // factorised APOLLO momentum EMA and update (k_fact_tail)
+  const float* g;         // g_low
+  uint8_t* m_q;           // coded momentum, or
+  float* m_scale;
+  float* m_fp32;          // fp32 momentum
+  const float* rv;        // row / column EMAs (R, C)
+  const float* cv;
+  const float* rmean;     // device clamped row mean
+  float* u;               // out: the low-rank update
+  int64_t n, C;
+};
+int64_t fact_tail_table_bytes(int n);
+int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1, float apollo_eps, int m_fp32,
+                    int m_bits, int m_mode, int m_block_size, hipStream_t st);
+
 struct VEmaItem {   // AL state: v' = lerp(deq(v), x (or x^2 + eps1), w), re-encoded with a block refit
   void* q;
   float* scale;

@@ -422,7 +422,7 @@ struct XB {
   XD* tab_dev;          // n descriptors
   void* mema_dev;       // m_ema_table_bytes(n)
   void* vema_dev;       // v_ema_table_bytes(2 n)
-  void* tail_dev;       // came_tail_table_bytes(n)
+  void* tail_dev;       // the larger of came_tail_table_bytes(n) and fact_tail_table_bytes(n)
   hipStream_t st;
 };
 
@@ -512,6 +512,24 @@ static int x_run(XB& b) {
     if (!a0->came) {
       if ((rc = x_s<XS_RMEAN>(b))) return rc;
       if (a0->has_m) {
+        // momentum EMA and update in one pass (power-of-two M blocks, aligned streams)
+        bool tail = a0->m_fp32 || (a0->m_block_size >= 32 && a0->m_block_size <= 2048 &&
+                                   (a0->m_block_size & (a0->m_block_size - 1)) == 0);
+        for (size_t i = 0; tail && i < n; ++i) {
+          const a8_apollo_x_args* a = b.a[i];
+          tail = aligned16(b.d[i].k.g) && aligned16(b.d[i].k.u) && (a->m_fp32 ? aligned16(a->m_fp32) : aligned16(a->m_q));
+        }
+        if (tail) {
+          std::vector<FactTailItem> it(n);
+          for (size_t i = 0; i < n; ++i) {
+            const a8_apollo_x_args* a = b.a[i];
+            const XK& k = b.d[i].k;
+            it[i] = FactTailItem{k.g, a->m_q, a->m_scale, a->m_fp32, k.rv, k.cv, k.ws + x_layout(k.R, k.C).scal + 1,
+                                 k.u, k.n, k.C};
+          }
+          return fact_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->apollo_eps, a0->m_fp32 != nullptr,
+                                 a0->m_bits, a0->m_mode, a0->m_block_size, b.st);
+        }
         if ((rc = x_momentum(b, false))) return rc;
         for (auto& e : b.d) e.k.src = e.k.m;
       } else {
@@ -697,8 +715,10 @@ static bool x_same(const a8_apollo_x_args* a, const a8_apollo_x_args* b) {
 // Table bytes of one batch of n matrices: descriptors, momentum and AL tables.
 static int64_t x_round(int64_t b) { return (b + 255) / 256 * 256; }
 static int64_t x_bytes(int n) {
+  const int64_t tail = came_tail_table_bytes(n) > fact_tail_table_bytes(n) ? came_tail_table_bytes(n)
+                                                                           : fact_tail_table_bytes(n);
   return x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) + x_round(v_ema_table_bytes(2 * n)) +
-         x_round(came_tail_table_bytes(n));
+         x_round(tail);
 }
 
 }  // namespace a8

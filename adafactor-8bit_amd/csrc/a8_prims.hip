@@ -819,6 +819,124 @@ __global__ __launch_bounds__(256) void k_came_tail(CameTailDesc one, const CameT
   store8<float>(D.u, e0, n, uo);
 }
 
+// Factorised APOLLO with momentum, after the row / column EMAs and their clamped
+// row mean (optimizer.py:2689-2758): m' = lerp(m, g_low, 1 - beta1) re-encoded
+// per M block (or fp32 m), u = m' / (sqrt((r_i c_j) / rmean) + eps), in one pass
+// (k_sgd's momentum EMA, g scrubbed as k_sgd scrubs it, then the update pass's
+// arithmetic), for the same units as k_came_tail.
+struct FactTailDesc {
+  const float* g;
+  uint8_t* m_q;
+  float* m_scale;
+  float* m_fp32;
+  const float* rv;
+  const float* cv;
+  const float* rmean;
+  float* u;
+  int64_t n, C, nmb, wg_begin;
+};
+
+struct FactTailHyp {
+  float w1, aeps;
+  int mk, lbm;
+};
+
+template <int MK>
+__global__ __launch_bounds__(256) void k_fact_tail(FactTailDesc one, const FactTailDesc* __restrict__ tab, int ntab,
+                                                   FactTailHyp h) {
+  __shared__ float xm[4];
+  const int64_t wg = blockIdx.x;
+  FactTailDesc D = one;
+  if (tab) {
+    int lo = 0, hi = ntab - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    }
+    D = tab[lo];
+  }
+  const int64_t n = D.n;
+  const int64_t e0 = (wg - D.wg_begin) * kPElems + (int64_t)threadIdx.x * 8;
+  const int64_t rem = n - e0;
+  const int cnt = rem <= 0 ? 0 : (rem >= 8 ? 8 : (int)rem);
+  float g[8], m[8];
+  load8<float>(D.g, e0, n, g);
+  if constexpr (MK == 3) {
+    float mo[8];
+    load8<float>(D.m_fp32, e0, n, mo);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = lerp_ref(mo[k], g[k], h.w1);
+    store8<float>(D.m_fp32, e0, n, m);
+  } else {
+    const int64_t mb = e0 >> h.lbm;
+    const bool m_ok = mb < D.nmb;   // codes are padded to whole blocks
+    float mo[8];
+    mq_decode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, mo);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m[k] = (k < cnt) ? lerp_ref(mo[k], scrub(g[k]), h.w1) : 0.0f;
+    mq_encode8(h.mk, D.m_q, D.m_scale, e0, mb, m_ok, m, (1 << h.lbm) >> 3, xm);
+  }
+  const float rmean = *gp(D.rmean);
+  float uo[8];
+  int64_t r = e0 / D.C, c = e0 - r * D.C;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uo[k] = 0.0f;
+    if (k < cnt) {
+      const float ve = (gp(D.rv)[r] * gp(D.cv)[c]) / rmean;
+      uo[k] = m[k] / (sqrtf(ve) + h.aeps);
+    }
+    if (++c == D.C) { c = 0; ++r; }
+  }
+  store8<float>(D.u, e0, n, uo);
+}
+
+int64_t fact_tail_table_bytes(int n) { return (int64_t)sizeof(FactTailDesc) * (int64_t)n; }
+
+int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1, float apollo_eps, int m_fp32,
+                    int m_bits, int m_mode, int m_block_size, hipStream_t st) {
+  if (n <= 0) return 0;
+  if (!m_fp32 && !(m_block_size >= 32 && m_block_size <= 2048 && (m_block_size & (m_block_size - 1)) == 0))
+    return set_error(A8_ERR_BLOCK, "factorised tail: m_block_size must be a power of two in [32, 2048]");
+  FactTailHyp h{};
+  h.w1 = (float)(1.0 - beta1);
+  h.aeps = apollo_eps;
+  if (!m_fp32) {
+    if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
+      return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
+    h.mk = m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4);
+  }
+  while ((1 << h.lbm) < (m_fp32 ? 32 : m_block_size)) ++h.lbm;
+  std::vector<FactTailDesc> tab((size_t)n);
+  int64_t wg = 0;
+  for (int i = 0; i < n; ++i) {
+    const FactTailItem& t = it[i];
+    if (!t.g || !t.u || !t.rv || !t.cv || !t.rmean || t.C <= 0 || (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale)))
+      return set_error(A8_ERR_ARG, "factorised tail: state missing");
+    if (!aligned16(t.g) || !aligned16(t.u) || (m_fp32 ? !aligned16(t.m_fp32) : !aligned16(t.m_q)))
+      return set_error(A8_ERR_ALIGN, "factorised tail: streams must be 16-byte aligned");
+    FactTailDesc& D = tab[(size_t)i];
+    D.g = t.g; D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
+    D.rv = t.rv; D.cv = t.cv; D.rmean = t.rmean; D.u = t.u;
+    D.n = t.n; D.C = t.C;
+    D.nmb = (t.n + (1 << h.lbm) - 1) >> h.lbm;
+    D.wg_begin = wg;
+    wg += (t.n + kPElems - 1) / kPElems;   // M blocks are powers of two up to a unit
+  }
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "factorised tail: too many elements");
+  const FactTailDesc* dt = nullptr;
+  if (n > 1) {
+    if (!table_dev) return set_error(A8_ERR_ARG, "factorised tail: a table is needed for several matrices");
+    if (upload_table(table_dev, tab.data(), sizeof(FactTailDesc) * (size_t)n, st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "table upload failed");
+    dt = reinterpret_cast<const FactTailDesc*>(table_dev);
+  }
+  const dim3 g((unsigned)wg), b(256);
+  if (m_fp32) hipLaunchKernelGGL((k_fact_tail<3>), g, b, 0, st, tab[0], dt, n, h);
+  else hipLaunchKernelGGL((k_fact_tail<1>), g, b, 0, st, tab[0], dt, n, h);
+  return check_launch("k_fact_tail");
+}
+
 static bool pow2_in(int x, int lo, int hi) { return x >= lo && x <= hi && (x & (x - 1)) == 0; }
 
 bool came_tail_ok(int m_fp32, int m_block_size, int c_bits, int block_size) {

@@ -179,7 +179,10 @@ def test_factored_general_m_block_matches_oracle(name, kw):
 # APOLLO route: a coded low-rank V block that is not a power of two in [128, 2048],
 # or such a momentum block outside [32, 2048], takes the low-rank stage of
 # a8_apollo_lowrank_x (the plain stage, or the factorised / CAME ones) with the
-# general-block EMA kernels.  The oracle gets this library's projection output
+# general-block EMA kernels.  The last five cases keep power-of-two blocks: the
+# factorised and CAME stages then end in the fused tails (k_fact_tail,
+# k_came_tail), here in each state form (fp32 or coded momentum and residual,
+# UF4 / D8 momentum, AL16 residual, with and without the RMS clip).  The oracle gets this library's projection output
 # (glow_hook, as in the rank-256 test of tests/test_gpu_apollo.py) and reduces
 # exactly.  Plain: V and M codes equal but for <= 0.01% (+1 per tensor), by one
 # code; block metadata rtol 1e-5; the Fira norm rtol 1e-5; fp32 parameters rtol
@@ -200,6 +203,13 @@ ACASES = [
     ("apollo_came_bv640_bm160", dict(APOLLO_BASE, beta3=0.9999, d=1.0, eps_came=1e-16, block_size=640,
                                      m_block_size=160)),
     ("apollo_fact_bm36", dict(APOLLO_BASE, apollo_factorize=True, block_size=1152, m_block_size=36)),
+    # power-of-two blocks: the fused low-rank tails (k_fact_tail, k_came_tail) in each state form
+    ("apollo_fact_fp32m", dict(APOLLO_BASE, apollo_factorize=True, m_quant_type="fp32")),
+    ("apollo_fact_uf4", dict(APOLLO_BASE, apollo_factorize=True, m_quant_type="uf4", m_block_size=64)),
+    ("apollo_came_res_fp32", dict(APOLLO_BASE, beta3=0.9999, d=1.0, eps_came=1e-16, c_quant_type="fp32")),
+    ("apollo_came_d8_al16", dict(APOLLO_BASE, beta3=0.999, d=1.0, eps_came=1e-16, m_quant_type="d8",
+                                 v_quant_type="al16", c_quant_type="al16", block_size=512, m_block_size=128)),
+    ("apollo_came_fp32m_d0", dict(APOLLO_BASE, beta3=0.9999, d=0.0, eps_came=1e-16, m_quant_type="fp32")),
 ]
 ASHAPES = [(300, 200), (160, 420)]
 
@@ -268,7 +278,7 @@ def test_apollo_general_blocks_match_oracle(name, kw, monkeypatch):
                     keys = [k[len(key) + 1:] for k in z.files]
                     _cmp_params(name, key, _t2np(b), a.detach().numpy(), init[i].numpy())
                     ap_cmp_state(name, key, st, z, keys)
-            assert "m_low_q" in og.state[pg[0]] or kw.get("beta1") is None
+            assert "m_low_q" in og.state[pg[0]] or "m_low" in og.state[pg[0]] or kw.get("beta1") is None
     finally:
         F.set_exact_reductions(old)
 

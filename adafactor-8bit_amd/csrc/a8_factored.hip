@@ -1316,11 +1316,12 @@ __global__ __launch_bounds__(256) void k_fupdt(const DescF* __restrict__ table, 
     act[j] = c0 < C;
     cl[j] = act[j] ? (uint32_t)c0 : (uint32_t)c_base;
   }
-  // Rows r and r + 4 in one pass for the plain update (the loads of both in
-  // flight together); one row per pass with momentum and in the read-only norm
-  // pass, where registers are better spent on occupancy.  A second row beyond
-  // the tile reads the first one again and stores nothing.
-  constexpr int NRW = (kHasM || MODE == 1) ? 1 : 2;
+  // Rows r, r + 4, r + 8 and r + 12 in one pass for the plain update (the loads
+  // of all four in flight together: 2.40 -> 2.33 ms at C2 against two rows); one
+  // row per pass with momentum (two rows measured slower there: 172 registers)
+  // and in the read-only norm pass, where registers are better spent on
+  // occupancy.  A row beyond the tile reads the first one again and stores nothing.
+  constexpr int NRW = (kHasM || MODE == 1) ? 1 : 4;
   double sq = 0.0;   // sum u^2 (MODE 1), accumulated in double
   for (int64_t r0 = q.r_lo + wave; r0 < q.r_hi; r0 += 4 * NRW) {
     int64_t rowb[NRW];

@@ -53,23 +53,14 @@ __device__ __forceinline__ uint32_t sr_hi_at(uint64_t base, uint64_t idx) {
   return sm_hi(base + idx + 0x9E3779B97F4A7C15ULL);
 }
 
-// The element's 32 random bits.
-__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t step, uint64_t idx) {
-  const uint32_t hi = sr_hi_at(sr_base(seed, step), idx);
-  return hi ^ (hi >> 31);
-}
-__device__ __forceinline__ uint32_t sr_bits_at(uint64_t base, uint64_t idx) {
-  const uint32_t hi = sr_hi_at(base, idx);
-  return hi ^ (hi >> 31);
-}
-
-// bf16 stochastic rounding decided in integers: u < rem / 2^16 with
-// u = (bits >> 8) / 2^24 is (bits >> 8) < rem * 2^8 exactly (both sides are
+// bf16 stochastic rounding (kernels.cu:67-87) decided in integers: the reference
+// takes x's upper bf16 neighbour when u < rem / 2^16 (rem: x's low 16 bits), with
+// u = (bits >> 8) / 2^24; that is (bits >> 8) < rem * 2^8 exactly (both sides are
 // exact in fp32), that is (bits >> 16) < rem, that is hi < rem * 2^16 = x's bits
-// << 16 (bits and hi differ in bit 0 only), so the result equals sr_bf16(x, u).
-// sr_bf16's three guards fold into one magnitude compare: rem == 0 never rounds
-// up (the compare is false), and |x| >= 0x7F7F0000 (inf, NaN, or a truncation
-// whose upper neighbour is inf) never rounds up either; NaN becomes the quiet NaN.
+// << 16 (bits and hi differ in bit 0 only).  Its three guards fold into one
+// magnitude compare: rem == 0 never rounds up (the compare is false), and
+// |x| >= 0x7F7F0000 (inf, NaN, or a truncation whose upper neighbour is inf) never
+// rounds up either; NaN becomes the quiet NaN.
 __device__ __forceinline__ uint16_t sr_bf16_hi(float x, uint32_t hi) {
   const uint32_t b = __float_as_uint(x);
   const uint32_t a = b & 0x7FFFFFFFu;
@@ -78,22 +69,9 @@ __device__ __forceinline__ uint16_t sr_bf16_hi(float x, uint32_t hi) {
   const uint32_t rq = ((b >> 16) & 0x8000u) | 0x7FC0u;
   return (uint16_t)(a > 0x7F800000u ? rq : rn);
 }
+
 __device__ __forceinline__ float sr_uniform(uint64_t seed, uint64_t step, uint64_t idx) {
   return (float)(sr_hi_at(sr_base(seed, step), idx) >> 8) * (1.0f / 16777216.0f);
-}
-
-__device__ __forceinline__ uint16_t sr_bf16(float x, float u) {
-  uint32_t b = __float_as_uint(x);
-  const bool nan = ((b & 0x7F800000u) == 0x7F800000u) && (b & 0x007FFFFFu);
-  if (nan) return (uint16_t)(((b & 0x80000000u) | 0x7FC00000u) >> 16);
-  uint32_t lo = b & 0xFFFF0000u;
-  uint32_t rem = b & 0x0000FFFFu;
-  uint32_t hi = lo + 0x00010000u;
-  bool lo_inf = (lo & 0x7F800000u) == 0x7F800000u;
-  bool hi_inf = ((hi & 0x7F800000u) == 0x7F800000u) && !(hi & 0x007FFFFFu);
-  bool up_ok = rem && !lo_inf && !hi_inf;
-  float prob = up_ok ? (float)rem * (1.0f / 65536.0f) : 0.0f;
-  return (uint16_t)(((up_ok && u < prob) ? hi : lo) >> 16);
 }
 
 __device__ __forceinline__ uint16_t h_next_up(uint16_t h) {

@@ -1254,17 +1254,35 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
 #pragma unroll
         for (int k = 0; k < 8; ++k) hv[k] = sm_hi(zb + (uint64_t)k);
       }
-      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      float xv[8];   // (p * decay) + (g * f) * step; the decay branch is uniform
+      if (has_dec) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        float x = p[k];
-        if (has_dec) x = x * dec;
-        x = x + (scrub(g[k]) * f[k]) * step;
-        const uint32_t hi = hv[k];
-        uint16_t hb;
-        if constexpr (std::is_same<T, __half>::value) hb = sr_fp16(x, (float)(hi >> 8) * (1.0f / 16777216.0f));
-        else hb = sr_bf16_hi(x, hi);
-        w[k >> 1] |= (uint32_t)hb << (16 * (k & 1));
+        for (int k = 0; k < 8; ++k) xv[k] = (p[k] * dec) + (scrub(g[k]) * f[k]) * step;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xv[k] = p[k] + (scrub(g[k]) * f[k]) * step;
+      }
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if constexpr (std::is_same<T, __half>::value) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          w[k >> 1] |= (uint32_t)sr_fp16(xv[k], (float)(hv[k] >> 8) * (1.0f / 16777216.0f)) << (16 * (k & 1));
+      } else {
+        uint32_t amax = 0u;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) amax = max(amax, __float_as_uint(xv[k]) & 0x7FFFFFFFu);
+        if (amax < 0x7F7F0000u) {
+          // all eight finite and below the largest value that can round up:
+          // sr_bf16_hi without its guards
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t b = __float_as_uint(xv[k]);
+            w[k >> 1] |= ((b >> 16) + (uint32_t)(hv[k] < (b << 16))) << (16 * (k & 1));
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) w[k >> 1] |= (uint32_t)sr_bf16_hi(xv[k], hv[k]) << (16 * (k & 1));
+        }
       }
       if (e0 + 8 <= n) {
         *gp(reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(P) + e0)) = u32x4{w[0], w[1], w[2], w[3]};

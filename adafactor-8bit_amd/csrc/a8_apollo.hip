@@ -1241,15 +1241,16 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
     const float ts = step * fin_t;   // tensor: alpha = step * final_scale
     if constexpr (SR) {
       // The lane's first counter; element k's is zb + k.  The random words come
-      // first: unless the low word wraps within the eight (a lane in 6e8), the
-      // counters share their high word and so its share of the first product.
+      // first: unless the eight counters cross a multiple of 2^30 (a lane in 1.5e8),
+      // they share their bits from 30 up, hence the high word's share of the first
+      // product and the low word of z >> 30.
       const uint64_t zb = sr_base(D.sr_seed, D.step) + 0x9E3779B97F4A7C15ULL + (uint64_t)e0;
       const uint32_t zl = (uint32_t)zb, zh = (uint32_t)(zb >> 32);
       uint32_t hv[8];
-      if (zl <= 0xFFFFFFF8u) {
-        const uint32_t yhc = sm_yhc(zh);
+      if ((zl & 0x3FFFFFFFu) <= 0x3FFFFFF8u) {   // the eight agree from bit 30 up
+        const uint32_t yhc = sm_yhc(zh), sh30 = __builtin_amdgcn_alignbit(zh, zl, 30);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) hv[k] = sm_hi_yh(zl + (uint32_t)k, zh, yhc);
+        for (int k = 0; k < 8; ++k) hv[k] = sm_hi_ys(zl + (uint32_t)k, sh30, yhc);
       } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) hv[k] = sm_hi(zb + (uint64_t)k);

@@ -30,6 +30,16 @@ static inline hipError_t upload_qmap_tu(const float* q8, const float* q4) {
 // that xor is invisible, so the decisions take hi itself.  sm_hi_yh takes
 // yhc = (zh ^ (zh >> 30)) * 0x1CE4E5B9, the high word's share of the first
 // product, which counters that differ only in their low word share.
+// sm_hi_ys: the same given the low word of z >> 30 (sh30), which counters that
+// agree in their bits from 30 up share.
+__device__ __forceinline__ uint32_t sm_hi_ys(uint32_t zl, uint32_t sh30, uint32_t yhc) {
+  const uint32_t yl = zl ^ sh30;
+  const uint64_t p = (uint64_t)yl * 0x1CE4E5B9u;   // * 0xBF58476D1CE4E5B9
+  const uint32_t z1l = (uint32_t)p;
+  const uint32_t z1h = (uint32_t)(p >> 32) + yl * 0xBF58476Du + yhc;
+  const uint32_t y2l = z1l ^ __builtin_amdgcn_alignbit(z1h, z1l, 27), y2h = z1h ^ (z1h >> 27);
+  return __umulhi(y2l, 0x133111EBu) + y2l * 0x94D049BBu + y2h * 0x133111EBu;   // * 0x94D049BB133111EB
+}
 __device__ __forceinline__ uint32_t sm_hi_yh(uint32_t zl, uint32_t zh, uint32_t yhc) {
   const uint32_t yl = zl ^ __builtin_amdgcn_alignbit(zh, zl, 30);
   const uint64_t p = (uint64_t)yl * 0x1CE4E5B9u;   // * 0xBF58476D1CE4E5B9

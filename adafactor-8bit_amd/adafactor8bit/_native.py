@@ -101,7 +101,8 @@ class ApolloXArgs(ctypes.Structure):
                 ("crow_q", _c_vp), ("crow_scale", _c_vp), ("crow_min_log", _c_vp), ("crow_fp32", _c_vp),
                 ("ccol_q", _c_vp), ("ccol_scale", _c_vp), ("ccol_min_log", _c_vp), ("ccol_fp32", _c_vp),
                 ("c_bits", _c_i), ("beta_v", _c_d), ("beta1", _c_d), ("beta3", _c_d),
-                ("apollo_eps", _c_f), ("eps_sq", _c_f), ("log_floor", _c_f), ("eps_came", _c_f), ("d", _c_f)]
+                ("apollo_eps", _c_f), ("eps_sq", _c_f), ("log_floor", _c_f), ("eps_came", _c_f), ("d", _c_f),
+                ("u_rowsums", _c_i)]
 
 
 _SIGS = {

@@ -1483,6 +1483,9 @@ def _apollo_prep(opt, p, grad, st, group):
     if xmode:
         xargs, xkeep = _apollo_x_args(opt, st, group, dev, ent["ws"], low_shape, n_low, factorize, came, first,
                                       vbits, vqt, bs, has_m, m_fp32, mqt, mbs, quant, beta_val, beta1)
+        # the stage leaves the per-row sums of u^2 and g_low^2 where the finish phase
+        # reads them (right side, rank a power of two in [8, 512]: phase 3)
+        xargs.u_rowsums = int(right and _pow2_in(rank, 8, 512))
         t = nat.ApolloTensor(
             p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank, None, None, None, None, None, None, None,
             nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
@@ -1618,7 +1621,7 @@ def _run_apollo_batch(opt, group, bkey, items):
             opt._ws[(pdev, "apx_table")] = xtab
         nat.check(L.a8_apollo_lowrank_x_multi(xarr, n, xtab.data_ptr(), xtab.numel(), stream),
                   "a8_apollo_lowrank_x_multi")
-        nat.check(L.a8_apollo_step_multi_phase(2, *head, *tail), "a8_apollo_step_multi_phase(2)")
+        nat.check(L.a8_apollo_step_multi_phase(3, *head, *tail), "a8_apollo_step_multi_phase(3)")
         for _, (st, _vb, bsz, keep, xargs) in items:
             if xargs.v_bits:
                 _block_view(st, "v_low", bsz)

@@ -61,8 +61,10 @@ struct CameTailItem {   // non-factorised CAME APOLLO after the RMS clip (k_came
   float* r_scale;
   float* r_min_log;
   float* r_fp32;          // fp32 residual EMA
-  float* u;               // out: the low-rank update
+  float* u;               // out: the low-rank update, or its row sums (rs_C)
   int64_t n;
+  const float* g;         // g_low, read for the row sums
+  int64_t rs_C;           // row length C (> 0): row sums of u^2 and g_low^2 in u's place
 };
 bool came_tail_ok(int m_fp32, int m_block_size, int c_bits, int block_size);
 int64_t came_tail_table_bytes(int n);
@@ -78,12 +80,19 @@ struct FactTailItem {   // factorised APOLLO momentum EMA and update (k_fact_tai
   const float* rv;        // row / column EMAs (R, C)
   const float* cv;
   const float* rmean;     // device clamped row mean
-  float* u;               // out: the low-rank update
+  float* u;               // out: the low-rank update, or its row sums (rs)
   int64_t n, C;
+  int rs;                 // row sums of u^2 and g_low^2 in u's place
 };
 int64_t fact_tail_table_bytes(int n);
 int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1, float apollo_eps, int m_fp32,
                     int m_bits, int m_mode, int m_block_size, hipStream_t st);
+
+// Row sums of u^2 and g^2 (double, summed from fp32 squares) over the rows of C
+// elements of an n-element row-major matrix (C a power of two in [8, 512]), two
+// per row at out[2 i], out[2 i + 1]; out must not overlap u or g.
+int rowsum_sq(const float* u, const float* g, int64_t n, int64_t C, double* out, hipStream_t st);
+bool rowsum_len_ok(int64_t C);
 
 struct VEmaItem {   // AL state: v' = lerp(deq(v), x (or x^2 + eps1), w), re-encoded with a block refit
   void* q;

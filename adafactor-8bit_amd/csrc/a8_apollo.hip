@@ -1375,7 +1375,8 @@ static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc)
 // phase 0: the whole step; 1: projection (and the norms of G) only, leaving
 // g_low in workspace[0, n_low); 2: scale, scalars and writeback from the update
 // the caller wrote to workspace[n_low, 2 n_low) (the factorised / CAME low-rank
-// stage of a8_apollo_lowrank_x runs between the two).
+// stage of a8_apollo_lowrank_x runs between the two); 3: as 2, reading the row
+// sums that stage left in place of u for the matrices where ap_rowsum holds.
 static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tensor* ts, int n, void* table_dev,
                       int64_t tbytes, double beta_val, double beta1, int has_m, float apollo_eps, float log_floor,
                       int v_bits, int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
@@ -1456,10 +1457,12 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   h.mk = has_m && !m_fp32 ? (m_mode == 0 ? (m_bits == 8 ? 1 : 2) : (m_bits == 8 ? 3 : 4)) : 0;
   h.channel = channel ? 1 : 0; h.front = scale_front ? 1 : 0; h.fira = fira ? 1 : 0;
   h.scale_param = scale_parameter ? 1 : 0; h.bias_mode = bias_mode; h.wd_mode = wd_mode;
-  h.rowsum = phase == 0 ? 1 : 0;   // phase 2 finishes a low-rank stage that wrote u itself
+  // phase 2 finishes a low-rank stage that wrote u itself, phase 3 one that left
+  // the row sums (a8_apollo_x_args.u_rowsums) where ap_rowsum holds
+  h.rowsum = (phase == 0 || phase == 3) ? 1 : 0;
   int rc;
   // projection (+ channel norms of G)
-  if (phase == 2) {
+  if (phase >= 2) {
     // the projection ran in phase 1
   } else if (dtype == A8_BF16) {
     for (int i = 0; i < n; ++i) {
@@ -1581,7 +1584,8 @@ int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_ap
                                int m_fp32, int m_block_size, int channel, float apollo_scale, int scale_front,
                                int fira, float fira_margin, float d, float lr_val, float eps2, int scale_parameter,
                                int bias_mode, float weight_decay, int wd_mode, void* stream) {
-  if (phase != 1 && phase != 2) return set_error(A8_ERR_ARG, "phase must be 1 (projection) or 2 (finish)");
+  if (phase < 1 || phase > 3)
+    return set_error(A8_ERR_ARG, "phase must be 1 (projection), 2 or 3 (finish)");
   return apollo_run(phase, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m,
                     apollo_eps, log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel,
                     apollo_scale, scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode,

@@ -424,6 +424,7 @@ struct XB {
   void* vema_dev;       // v_ema_table_bytes(2 n)
   void* tail_dev;       // the larger of came_tail_table_bytes(n) and fact_tail_table_bytes(n)
   hipStream_t st;
+  int tail_rs;          // a fused tail wrote the row sums of u_rowsums matrices
 };
 
 static XT x_tab(const XB& b) {
@@ -502,7 +503,7 @@ static int x_momentum(XB& b, bool from_u) {
   return m_ema_multi(it.data(), (int)n, b.mema_dev, a0->beta1, a0->m_block_size, a0->m_bits, a0->m_mode, b.st);
 }
 
-static int x_run(XB& b) {
+static int x_stage(XB& b) {
   const a8_apollo_x_args* a0 = b.a[0];
   const size_t n = b.d.size();
   int rc;
@@ -525,8 +526,9 @@ static int x_run(XB& b) {
             const a8_apollo_x_args* a = b.a[i];
             const XK& k = b.d[i].k;
             it[i] = FactTailItem{k.g, a->m_q, a->m_scale, a->m_fp32, k.rv, k.cv, k.ws + x_layout(k.R, k.C).scal + 1,
-                                 k.u, k.n, k.C};
+                                 k.u, k.n, k.C, a->u_rowsums ? 1 : 0};
           }
+          b.tail_rs = 1;
           return fact_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->apollo_eps, a0->m_fp32 != nullptr,
                                  a0->m_bits, a0->m_mode, a0->m_block_size, b.st);
         }
@@ -606,8 +608,10 @@ static int x_run(XB& b) {
       const a8_apollo_x_args* a = b.a[i];
       const XK& k = b.d[i].k;
       it[i] = CameTailItem{k.dst, a->d > 0.0f ? k.ws + x_layout(k.R, k.C).scal : nullptr, a->m_q, a->m_scale,
-                           a->m_fp32, a->res_q, a->res_scale, a->res_min_log, a->res_fp32, k.u, k.n};
+                           a->m_fp32, a->res_q, a->res_scale, a->res_min_log, a->res_fp32, k.u, k.n, k.g,
+                           a->u_rowsums ? k.C : 0};
     }
+    b.tail_rs = 1;
     return came_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->beta3, a0->eps_came, a0->eps_sq,
                            a0->m_fp32 != nullptr, a0->m_bits, a0->m_mode, a0->m_block_size, a0->c_bits,
                            a0->block_size, b.st);
@@ -672,6 +676,8 @@ static int x_check(const a8_apollo_x_args* a) {
   if (!a->g_low || !a->u || !a->xws) return set_error(A8_ERR_ARG, "null g_low, u or workspace");
   if (!aligned16(a->xws)) return set_error(A8_ERR_ALIGN, "workspace must be 16-byte aligned");
   if (a->came && !a->has_m) return set_error(A8_ERR_ARG, "CAME (beta3) requires momentum (beta1)");
+  if (a->u_rowsums && !rowsum_len_ok(a->cols_low))
+    return set_error(A8_ERR_SIZE, "u_rowsums: cols_low must be a power of two in [8, 512]");
   const bool v_coded = !a->factorize && a->v_bits;
   const bool c_coded = a->came && a->c_bits;
   if ((v_coded || c_coded) && !(a->block_size >= 128 && a->block_size <= 65536 && a->block_size % 128 == 0))
@@ -696,6 +702,25 @@ static int x_check(const a8_apollo_x_args* a) {
       return set_error(A8_ERR_ARG, "low-rank V state missing");
     if (a->came && (a->c_bits ? !(a->res_q && a->res_scale && a->res_min_log) : !a->res_fp32))
       return set_error(A8_ERR_ARG, "residual state missing");
+  }
+  return 0;
+}
+
+// The stage, then the row sums of u^2 and g_low^2 of the u_rowsums matrices
+// where no fused tail left them: summed from u into the workspace's V region
+// (free once the stage is done) and copied over u.
+static int x_run(XB& b) {
+  b.tail_rs = 0;
+  int rc = x_stage(b);
+  if (rc || b.tail_rs) return rc;
+  for (size_t i = 0; i < b.a.size(); ++i) {
+    const a8_apollo_x_args* a = b.a[i];
+    if (!a->u_rowsums) continue;
+    const XK& k = b.d[i].k;
+    double* tmp = reinterpret_cast<double*>(k.ws + x_layout(k.R, k.C).xv);
+    if ((rc = rowsum_sq(a->u, a->g_low, k.n, k.C, tmp, b.st))) return rc;
+    if (hipMemcpyAsync(a->u, tmp, sizeof(double) * 2 * (size_t)k.R, hipMemcpyDeviceToDevice, b.st) != hipSuccess)
+      return set_error(A8_ERR_HIP, "row sums: copy failed");
   }
   return 0;
 }

@@ -718,6 +718,56 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
   return check_launch("k_vema_multi");
 }
 
+// Row sums for the finish phase of APOLLO: the squares of a lane's eight
+// elements summed in double, then over the C / 8 lanes of its row (C a power
+// of two in [8, 512], so a row lies inside one wave and starts on a lane that
+// is a multiple of C / 8), stored as two doubles per row.  Every lane of the
+// wave must take part.
+__device__ __forceinline__ void rowsum_store(const float* u, const float* g, int cnt, int64_t e0, int64_t n,
+                                             int64_t C, double* out) {
+  double su = 0.0, sg = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < cnt) {
+      su += (double)(u[k] * u[k]);
+      sg += (double)(g[k] * g[k]);
+    }
+  }
+  const int G = (int)(C >> 3);
+  su = grp_sum_d(su, G);
+  sg = grp_sum_d(sg, G);
+  if ((threadIdx.x & (G - 1)) == 0 && e0 < n) {
+    const int64_t row = e0 / C;
+    gp(out)[2 * row] = su;
+    gp(out)[2 * row + 1] = sg;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_rowsum_sq(const float* u, const float* g, int64_t n, int64_t C,
+                                                   double* out) {
+  const int64_t e0 = (int64_t)blockIdx.x * kPElems + (int64_t)threadIdx.x * 8;
+  const int cnt = e0 >= n ? 0 : 8;   // n is a multiple of C >= 8
+  float uv[8], gv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uv[k] = k < cnt ? gp(u)[e0 + k] : 0.0f;
+    gv[k] = k < cnt ? gp(g)[e0 + k] : 0.0f;
+  }
+  rowsum_store(uv, gv, cnt, e0, n, C, out);
+}
+
+bool rowsum_len_ok(int64_t C) { return C >= 8 && C <= 512 && (C & (C - 1)) == 0; }
+
+int rowsum_sq(const float* u, const float* g, int64_t n, int64_t C, double* out, hipStream_t st) {
+  if (!u || !g || !out) return set_error(A8_ERR_ARG, "row sums: null pointer");
+  if (!rowsum_len_ok(C) || n <= 0 || n % C) return set_error(A8_ERR_SIZE, "row sums: rows must be 8..512 (2^k)");
+  if (reinterpret_cast<uintptr_t>(out) & 7) return set_error(A8_ERR_ALIGN, "row sums: output must be 8-byte aligned");
+  const int64_t wg = (n + kPElems - 1) / kPElems;
+  if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "row sums: too many elements");
+  hipLaunchKernelGGL(k_rowsum_sq, dim3((unsigned)wg), dim3(256), 0, st, u, g, n, C, out);
+  return check_launch("k_rowsum_sq");
+}
+
 // ------------------------------------------------------------ CAME APOLLO tail
 // The low-rank passes of non-factorised CAME APOLLO after the RMS clip, in one
 // kernel (optimizer.py:2846-2896): U /= clip; m' = lerp(m, U, 1 - beta1)
@@ -741,7 +791,8 @@ struct CameTailDesc {
   float* r_min_log;
   float* r_fp32;
   float* u;
-  int64_t n, nmb, nvb, wg_begin;
+  const float* g;
+  int64_t n, nmb, nvb, wg_begin, rs_C;
 };
 
 struct CameTailHyp {
@@ -816,7 +867,13 @@ __global__ __launch_bounds__(256) void k_came_tail(CameTailDesc one, const CameT
   float uo[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) uo[k] = m[k] * (1.0f / sqrtf(fmaxf(res[k], h.eps_sq)));
-  store8<float>(D.u, e0, n, uo);
+  if (D.rs_C) {   // uniform
+    float g[8];
+    load8<float>(D.g, e0, n, g);
+    rowsum_store(uo, g, cnt, e0, n, D.rs_C, reinterpret_cast<double*>(D.u));
+  } else {
+    store8<float>(D.u, e0, n, uo);
+  }
 }
 
 // Factorised APOLLO with momentum, after the row / column EMAs and their clamped
@@ -833,7 +890,7 @@ struct FactTailDesc {
   const float* cv;
   const float* rmean;
   float* u;
-  int64_t n, C, nmb, wg_begin;
+  int64_t n, C, nmb, wg_begin, rs;
 };
 
 struct FactTailHyp {
@@ -888,7 +945,8 @@ __global__ __launch_bounds__(256) void k_fact_tail(FactTailDesc one, const FactT
     }
     if (++c == D.C) { c = 0; ++r; }
   }
-  store8<float>(D.u, e0, n, uo);
+  if (D.rs) rowsum_store(uo, g, cnt, e0, n, D.C, reinterpret_cast<double*>(D.u));   // uniform
+  else store8<float>(D.u, e0, n, uo);
 }
 
 int64_t fact_tail_table_bytes(int n) { return (int64_t)sizeof(FactTailDesc) * (int64_t)n; }
@@ -919,6 +977,9 @@ int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1
     D.g = t.g; D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
     D.rv = t.rv; D.cv = t.cv; D.rmean = t.rmean; D.u = t.u;
     D.n = t.n; D.C = t.C;
+    if (t.rs && !(rowsum_len_ok(t.C) && t.n % t.C == 0))
+      return set_error(A8_ERR_SIZE, "factorised tail: row sums need rows of 8..512 (2^k) elements");
+    D.rs = t.rs ? 1 : 0;
     D.nmb = (t.n + (1 << h.lbm) - 1) >> h.lbm;
     D.wg_begin = wg;
     wg += (t.n + kPElems - 1) / kPElems;   // M blocks are powers of two up to a unit
@@ -977,6 +1038,10 @@ int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1
     D.U = t.U; D.clip = t.clip; D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
     D.r_q = t.r_q; D.r_scale = t.r_scale; D.r_min_log = t.r_min_log; D.r_fp32 = t.r_fp32; D.u = t.u;
     D.n = t.n;
+    if (t.rs_C && !(t.g && aligned16(t.g) && rowsum_len_ok(t.rs_C) && t.n % t.rs_C == 0))
+      return set_error(A8_ERR_SIZE, "CAME tail: row sums need an aligned g_low and rows of 8..512 (2^k) elements");
+    D.g = t.g;
+    D.rs_C = t.rs_C;
     D.nmb = (t.n + (1 << h.lbm) - 1) >> h.lbm;
     D.nvb = (t.n + (1 << h.lbv) - 1) >> h.lbv;
     D.wg_begin = wg;

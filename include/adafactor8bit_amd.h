@@ -400,7 +400,12 @@ int64_t a8_apollo_table_bytes(int ntensors);
  * the left) plus the norms of G (and of p for scale_parameter); V / M fields of
  * the records and v_bits, m_* are not used.  phase 2: channel (or tensor) scale
  * of the update the caller wrote to workspace[n_low, 2 n_low) against g_low,
- * Fira, alpha, step and writeback, with the same arguments as phase 1. */
+ * Fira, alpha, step and writeback, with the same arguments as phase 1.  phase 3:
+ * as phase 2, for a low-rank stage run with u_rowsums set on exactly the
+ * matrices with rows >= cols and rank a power of two in [8, 512]: their row
+ * sums of u^2 and g_low^2 are read in place of u and g_low (the two norms of
+ * compute_apollo_norms, kernels.cu:2410-2453, per channel); u_rowsums on any
+ * other matrix, or phase 3 without it, reads the wrong values. */
 int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_apollo_tensor* tensors,
                                int ntensors, void* table_dev, int64_t table_bytes, double beta_val, double beta1,
                                int has_m, float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits,
@@ -452,6 +457,11 @@ typedef struct a8_apollo_x_args {
   int c_bits;              /* 0: fp32 residual / confidence */
   double beta_v, beta1, beta3;
   float apollo_eps, eps_sq, log_floor, eps_came, d;
+  /* 1: in place of u, leave for each row i the sums of u^2 and g_low^2 (double,
+   * from fp32 squares) at ((double*)u)[2 i] and [2 i + 1], for phase 3 of
+   * a8_apollo_step_multi_phase; cols_low must be a power of two in [8, 512].
+   * 0: write u. */
+  int u_rowsums;
 } a8_apollo_x_args;
 
 /* Replaces the factorised (apollo_factorize, optimizer.py:2689-2758) and CAME

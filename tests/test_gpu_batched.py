@@ -9,7 +9,9 @@ agree.  They are not bit-identical: the NORM pass adds each wave's sum of u^2
 into the tensor's norm buffer with a float atomic add (as the reference's
 kernels do), so the last bit of the clip norm depends on the order the waves
 finish, in either form.  Parameters therefore agree to rtol 1e-6 plus 1e-5 of
-the tensor's largest displacement, and codes to the parity bar (at most 1e-4 of codes, by one).  The reference-written fixtures
+the tensor's largest displacement (bf16 parameters, where that last bit can move
+a rounding decision: all but at most 1e-4 of them, the rest by one bf16 step),
+and codes to the parity bar (at most 1e-4 of codes, by one).  The reference-written fixtures
 adamw_clip_fira_wd and adafactor_mom1d_fira pin the arithmetic itself
 (tests/test_gpu_golden.py), through this batched path.
 """
@@ -59,8 +61,14 @@ def test_q1d_clip_batched_equals_per_tensor(case):
     (pa, oa), (pb, ob) = runs
     for i, (a, b) in enumerate(zip(pa, pb)):
         disp = float((a.detach().float().cpu() - init[i].float()).abs().max())
-        torch.testing.assert_close(a.detach().float(), b.detach().float(), rtol=1e-6, atol=1e-5 * disp,
-                                   msg=lambda m: f"{case} p{i}: {m}")
+        if dtype == torch.bfloat16:
+            xa, xb = a.detach().cpu().view(torch.int16).reshape(-1), b.detach().cpu().view(torch.int16).reshape(-1)
+            off = (xa.int() - xb.int()).abs()
+            assert int(off.max()) <= 1 and int((off > 0).sum()) <= max(1, int(1e-4 * xa.numel())), \
+                f"{case} p{i}: {int((off > 0).sum())} of {xa.numel()} bf16 values differ, by up to {int(off.max())} steps"
+        else:
+            torch.testing.assert_close(a.detach().float(), b.detach().float(), rtol=1e-6, atol=1e-5 * disp,
+                                       msg=lambda m: f"{case} p{i}: {m}")
         sa, sb = oa.state[a], ob.state[b]
         assert "variance_q" in sa, f"{case} p{i}: expected quantised state"
         for k, v in sa.items():

@@ -38,16 +38,18 @@ namespace a8 {
 
 constexpr int kXParts = 1024;     // max workgroups of an element pass (= partial sums of a reduction)
 constexpr int kXRowChunk = 256;   // rows per column-sum partial
+constexpr int kXColBlk = 256;     // columns per row-sum partial (four per lane)
 
 // Extended workspace of one matrix (offsets in floats; part / cpart hold doubles).
 struct XL {
-  int64_t n, nch, xv, xu, xm, xr, rowm, colm, crow, ccol, scal, part, cpart, total;
+  int64_t n, nch, ncb, xv, xu, xm, xr, rowm, colm, crow, ccol, scal, part, cpart, rpart, total;
 };
 
 __host__ __device__ inline XL x_layout(int64_t R, int64_t C) {
   XL w;
   w.n = R * C;
   w.nch = (R + kXRowChunk - 1) / kXRowChunk;
+  w.ncb = (C + kXColBlk - 1) / kXColBlk;
   const int64_t n4 = (w.n + 3) / 4 * 4;   // regions start 16-byte aligned
   w.xv = 0;                    // V values of coded V (the lerped values)
   w.xu = w.xv + n4;            // U (CAME)
@@ -60,7 +62,8 @@ __host__ __device__ inline XL x_layout(int64_t R, int64_t C) {
   w.scal = w.ccol + (C + 3) / 4 * 4;   // [0] clip, [1] row-variance mean (clamped), [2] confidence row mean
   w.part = (w.scal + 16 + 1) / 2 * 2;
   w.cpart = w.part + 2 * kXParts;
-  w.total = w.cpart + 2 * w.nch * C;
+  w.rpart = w.cpart + 2 * w.nch * C;
+  w.total = w.rpart + 2 * w.ncb * R;
   return w;
 }
 
@@ -282,51 +285,78 @@ __device__ __forceinline__ const float* x_src(const XK& k) {
   return SRC == XR_GSQ ? k.g : k.ws + x_layout(k.R, k.C).xr;
 }
 
-// Row means of x (or x^2) plus add: one wave per row, 4 rows per workgroup.
+// Row and column sums of x (or x^2) in one read, over a tile of kXRowChunk rows
+// and kXColBlk columns: each wave walks every fourth row of the tile, a lane
+// holding four consecutive columns.  A row's sum over the tile's columns (lane
+// sums, then the wave's fixed tree) is its mean when the matrix has one column
+// block, else a partial in rpart; a lane's columns accumulate down its rows and
+// the four waves combine in order into the chunk's column partial.
 template <int SRC>
-__global__ __launch_bounds__(256) void k_ax_rows(XT t, float add) {
-  int64_t lb;
-  const XK k = x_find<XW_ROWS>(t, lb);
-  const float* x = x_src<SRC>(k);
-  const int64_t row = lb * 4 + (threadIdx.x >> 6);
-  const int l = threadIdx.x & 63;
-  if (row >= k.R) return;
-  double s = 0.0;
-  for (int64_t j = l; j < k.C; j += 64) {
-    const float v = gp(x)[row * k.C + j];
-    s += (double)(SRC == XR_GSQ ? v * v : v);
-  }
-  s = grp_sum_d(s, 64);
-  if (l == 0) gp(k.ws)[x_layout(k.R, k.C).rowm + row] = (float)s / (float)k.C + add;
-}
-
-// Column sums of x (or x^2) over a chunk of kXRowChunk rows: 64 columns per
-// workgroup, the four waves striding the chunk's rows, combined in order.
-template <int SRC>
-__global__ __launch_bounds__(256) void k_ax_colpart(XT t) {
-  __shared__ double sd[256];
+__global__ __launch_bounds__(256) void k_ax_rcpart(XT t, float add) {
+  __shared__ double sd[4 * kXColBlk];
   int64_t lb;
   const XK k = x_find<XW_CPART>(t, lb);
   const float* x = x_src<SRC>(k);
   const XL L = x_layout(k.R, k.C);
-  const int64_t ncb = (k.C + 63) / 64;
-  const int64_t by = lb / ncb, bx = lb - by * ncb;
+  const int64_t by = lb / L.ncb, bx = lb - by * L.ncb;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int64_t c = bx * 64 + l;
+  const int64_t c0 = bx * kXColBlk + 4 * l;
   const int64_t r0 = by * kXRowChunk;
   const int64_t r1 = r0 + kXRowChunk < k.R ? r0 + kXRowChunk : k.R;
-  double s = 0.0;
-  if (c < k.C) {
-    for (int64_t r = r0 + w; r < r1; r += 4) {
-      const float v = gp(x)[r * k.C + c];
-      s += (double)(SRC == XR_GSQ ? v * v : v);
+  const bool vec = k.v4 && (k.C & 3) == 0 && (SRC == XR_RES || (reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  double cs[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int64_t r = r0 + w; r < r1; r += 4) {   // uniform per wave
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* xr = x + r * k.C;
+    if (vec) {
+      if (c0 < k.C) {
+        const f32x4 q = *gp(reinterpret_cast<const f32x4*>(xr + c0));
+        a[0] = q.x; a[1] = q.y; a[2] = q.z; a[3] = q.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < k.C) a[e] = gp(xr)[c0 + e];
+    }
+    double rs = 0.0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const double q = (double)(SRC == XR_GSQ ? a[e] * a[e] : a[e]);
+      cs[e] += q;
+      rs += q;
+    }
+    rs = grp_sum_d(rs, 64);
+    if (l == 0) {
+      if (L.ncb == 1) gp(k.ws)[L.rowm + r] = (float)rs / (float)k.C + add;
+      else reinterpret_cast<A8_G double*>(gp(k.ws) + L.rpart)[bx * k.R + r] = rs;
     }
   }
-  sd[threadIdx.x] = s;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) sd[w * kXColBlk + 4 * l + e] = cs[e];
   __syncthreads();
-  if (w == 0 && c < k.C)
-    reinterpret_cast<A8_G double*>(gp(k.ws) + L.cpart)[by * k.C + c] =
-        ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
+  if (w == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 4 * l + e;
+      if (c0 + e < k.C)
+        reinterpret_cast<A8_G double*>(gp(k.ws) + L.cpart)[by * k.C + c0 + e] =
+            ((sd[j] + sd[kXColBlk + j]) + sd[2 * kXColBlk + j]) + sd[3 * kXColBlk + j];
+    }
+  }
+}
+
+// Row means from the column blocks' partials, in block order (matrices with
+// more than one column block).
+__global__ __launch_bounds__(256) void k_ax_rowfin(XT t, float add) {
+  int64_t lb;
+  const XK k = x_find<XW_ROWS>(t, lb);
+  const XL L = x_layout(k.R, k.C);
+  const int64_t r = lb * 256 + threadIdx.x;
+  if (r >= k.R || L.ncb == 1) return;
+  const A8_G double* part = reinterpret_cast<const A8_G double*>(gp(k.ws) + L.rpart);
+  double s = 0.0;
+  for (int64_t h = 0; h < L.ncb; ++h) s += part[h * k.R + r];
+  gp(k.ws)[L.rowm + r] = (float)s / (float)k.C + add;
 }
 
 __global__ __launch_bounds__(256) void k_ax_colfin(XT t, float add) {
@@ -405,8 +435,8 @@ static int64_t x_grid(int64_t n) {
 static void x_counts(const XK& k, int64_t* cnt) {
   const XL L = x_layout(k.R, k.C);
   cnt[XW_EL] = x_grid(k.n);
-  cnt[XW_ROWS] = (k.R + 3) / 4;
-  cnt[XW_CPART] = ((k.C + 63) / 64) * L.nch;
+  cnt[XW_ROWS] = L.ncb > 1 ? (k.R + 255) / 256 : 0;
+  cnt[XW_CPART] = L.ncb * L.nch;
   cnt[XW_CFIN] = (k.C + 255) / 256;
   cnt[XW_VEC] = (k.R + k.C + 255) / 256;
   cnt[XW_ONE] = 1;
@@ -448,11 +478,13 @@ static int x_el(const XB& b) {
 template <int SRC>
 static int x_rowcol(const XB& b, float add) {
   const XT t = x_tab(b);
-  hipLaunchKernelGGL((k_ax_rows<SRC>), dim3((unsigned)b.total[XW_ROWS]), dim3(256), 0, b.st, t, add);
-  int rc = check_launch("k_ax_rows");
+  hipLaunchKernelGGL((k_ax_rcpart<SRC>), dim3((unsigned)b.total[XW_CPART]), dim3(256), 0, b.st, t, add);
+  int rc = check_launch("k_ax_rcpart");
   if (rc) return rc;
-  hipLaunchKernelGGL((k_ax_colpart<SRC>), dim3((unsigned)b.total[XW_CPART]), dim3(256), 0, b.st, t);
-  if ((rc = check_launch("k_ax_colpart"))) return rc;
+  if (b.total[XW_ROWS] > 0) {
+    hipLaunchKernelGGL(k_ax_rowfin, dim3((unsigned)b.total[XW_ROWS]), dim3(256), 0, b.st, t, add);
+    if ((rc = check_launch("k_ax_rowfin"))) return rc;
+  }
   hipLaunchKernelGGL(k_ax_colfin, dim3((unsigned)b.total[XW_CFIN]), dim3(256), 0, b.st, t, add);
   return check_launch("k_ax_colfin");
 }

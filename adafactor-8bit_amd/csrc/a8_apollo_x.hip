@@ -305,30 +305,43 @@ __global__ __launch_bounds__(256) void k_ax_rcpart(XT t, float add) {
   const int64_t r1 = r0 + kXRowChunk < k.R ? r0 + kXRowChunk : k.R;
   const bool vec = k.v4 && (k.C & 3) == 0 && (SRC == XR_RES || (reinterpret_cast<uintptr_t>(x) & 15) == 0);
   double cs[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int64_t r = r0 + w; r < r1; r += 4) {   // uniform per wave
-    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* xr = x + r * k.C;
-    if (vec) {
-      if (c0 < k.C) {
-        const f32x4 q = *gp(reinterpret_cast<const f32x4*>(xr + c0));
-        a[0] = q.x; a[1] = q.y; a[2] = q.z; a[3] = q.w;
+  // four of the wave's rows per round, all loaded before any is summed
+  for (int64_t rb = r0 + w; rb < r1; rb += 16) {   // uniform per wave
+    float a[4][4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t r = rb + 4 * h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[h][e] = 0.0f;
+      if (r >= r1) continue;
+      const float* xr = x + r * k.C;
+      if (vec) {
+        if (c0 < k.C) {
+          const f32x4 q = *gp(reinterpret_cast<const f32x4*>(xr + c0));
+          a[h][0] = q.x; a[h][1] = q.y; a[h][2] = q.z; a[h][3] = q.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c0 + e < k.C) a[h][e] = gp(xr)[c0 + e];
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (c0 + e < k.C) a[e] = gp(xr)[c0 + e];
     }
-    double rs = 0.0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const double q = (double)(SRC == XR_GSQ ? a[e] * a[e] : a[e]);
-      cs[e] += q;
-      rs += q;
-    }
-    rs = grp_sum_d(rs, 64);
-    if (l == 0) {
-      if (L.ncb == 1) gp(k.ws)[L.rowm + r] = (float)rs / (float)k.C + add;
-      else reinterpret_cast<A8_G double*>(gp(k.ws) + L.rpart)[bx * k.R + r] = rs;
+    for (int h = 0; h < 4; ++h) {
+      const int64_t r = rb + 4 * h;
+      if (r >= r1) break;   // uniform per wave
+      double rs = 0.0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const double q = (double)(SRC == XR_GSQ ? a[h][e] * a[h][e] : a[h][e]);
+        cs[e] += q;
+        rs += q;
+      }
+      rs = grp_sum_d(rs, 64);
+      if (l == 0) {
+        if (L.ncb == 1) gp(k.ws)[L.rowm + r] = (float)rs / (float)k.C + add;
+        else reinterpret_cast<A8_G double*>(gp(k.ws) + L.rpart)[bx * k.R + r] = rs;
+      }
     }
   }
 #pragma unroll

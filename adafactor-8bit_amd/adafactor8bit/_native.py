@@ -39,21 +39,22 @@ class Tensor1D(ctypes.Structure):
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
                 ("v_q", _c_vp), ("v_scale", _c_vp), ("v_min_log", _c_vp), ("v_buf", _c_vp),
                 ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64), ("fira_scale", _c_vp)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("fira_scale", _c_vp), ("norm_parts", _c_vp)]
 
 
 class TensorFull(ctypes.Structure):
     """Mirror of ``a8_tensor_full``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("variance", _c_vp), ("m", _c_vp),
                 ("norm_buf", _c_vp), ("alpha", _c_vp), ("prev_norm", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64), ("psq", _c_vp), ("fira_scale", _c_vp)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("psq", _c_vp), ("fira_scale", _c_vp),
+                ("norm_parts", _c_vp)]
 
 
 class TensorSgd(ctypes.Structure):
     """Mirror of ``a8_tensor_sgd``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp), ("m", _c_vp),
                 ("norm_buf", _c_vp), ("fira", _c_vp), ("alpha", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("norm_parts", _c_vp)]
 
 
 class FactoredPrimArgs(ctypes.Structure):
@@ -110,7 +111,7 @@ _SIGS = {
     "a8_version": (ctypes.c_char_p, []),
     "a8_set_qmap": (_c_i, [_c_vp, _c_vp]),
     "a8_fused_update_1d": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_u64, _c_u64, _c_d, _c_d,
+                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_u64, _c_u64, _c_d, _c_d,
                                   _c_f, _c_i, _c_f, _c_f, _c_f, _c_i64, _c_i, _c_i, _c_i, _c_i,
                                   _c_f, _c_i, _c_i, _c_f, _c_f, _c_i, _c_vp]),
     "a8_fused_update_1d_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(Tensor1D), _c_i, _c_vp,
@@ -123,8 +124,11 @@ _SIGS = {
     "a8_noalloc_max_tensors_1d": (_c_i, []),
     "a8_step_advance": (_c_i, [ctypes.POINTER(StepSpec), _c_vp, _c_vp, _c_vp]),
     "a8_table_bytes_1d": (_c_i64, [_c_i]),
+    "a8_norm_parts_1d": (_c_i64, [_c_i64, _c_i, _c_i]),
+    "a8_norm_parts_full": (_c_i64, [_c_i64]),
+    "a8_norm_parts_sgd": (_c_i64, [_c_i64, _c_i]),
     "a8_fused_update_1d_full": (_c_i, [_c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                       _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,
+                                       _c_vp, _c_vp, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_i64, _c_f, _c_i,
                                        _c_f, _c_f, _c_i, _c_i, _c_u64, _c_u64, _c_i, _c_vp]),
     "a8_fused_update_1d_full_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(TensorFull), _c_i, _c_vp,
                                              _c_i64, _c_d, _c_d, _c_f, _c_f, _c_i, _c_f, _c_f, _c_i,
@@ -160,7 +164,7 @@ _SIGS = {
     "a8_dequantize_momentum": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_i, _c_vp]),
     "a8_al_encode": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_f, _c_vp]),
     "a8_sgd_step": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                           _c_i64, _c_d, _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_u64, _c_vp]),
+                           _c_vp, _c_i64, _c_d, _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_u64, _c_vp]),
     "a8_sgd_step_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(TensorSgd), _c_i, _c_vp, _c_i64, _c_d, _c_i,
                                  _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_i, _c_vp]),
     "a8_table_bytes_sgd": (_c_i64, [_c_i]),

@@ -66,6 +66,12 @@ def set_qmap(qmap_8, qmap_4):
         nat.check(nat.lib().a8_set_qmap(q8.data_ptr(), q4.data_ptr()), "set_qmap")
 
 
+def _parts(device, n):
+    """Workspace for a norm pass's per-workgroup partial sums (the library adds them
+    in a fixed order, where the reference adds into norm_buf with float atomics)."""
+    return torch.empty(max(int(n), 1), dtype=torch.float64, device=device)
+
+
 def _u1d(mode, sr, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, norm_buf, alpha,
          prev_norm, decay, sr_seed, sr_step, beta1, beta_val, eps_for_denom, use_adam_denom,
          log_eps_sq, eps_for_grad_sq, numel, block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only):
@@ -82,10 +88,13 @@ def _u1d(mode, sr, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, no
         eps_sq = max(2.0 ** float(log_eps_sq), _EPS_FLOOR)
     else:
         eps_sq = max(float(eps_for_grad_sq) ** 2, _EPS_FLOOR)
+    parts = None
+    if mode in (1, 3):
+        parts = _parts(ref.device, nat.lib().a8_norm_parts_1d(int(numel), int(block_size), int(m_block_size)))
     rc = nat.lib().a8_fused_update_1d(
         mode, int(sr), nat.dtype_code(ref.dtype), nat.ptr(param), nat.ptr(grad), nat.ptr(m_q),
         nat.ptr(m_scale), nat.ptr(v_q), nat.ptr(v_scale), nat.ptr(v_min_log), nat.ptr(v_buf),
-        nat.ptr(norm_buf), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(dec), int(sr_seed), int(sr_step),
+        nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(dec), int(sr_seed), int(sr_step),
         float(beta1), float(beta_val), float(eps_for_denom), int(bool(use_adam_denom)), _AL_FLOOR,
         float(eps_for_grad_sq), eps_sq, int(numel),
         int(block_size), int(m_block_size), int(m_bits), int(m_mode), float(d), int(v_bits),
@@ -213,9 +222,10 @@ def _full(mode, param, grad, variance, m, norm_buf, alpha, prev_norm, beta1, bet
           eps_for_denom, use_adam_denom, eps_for_grad_sq, numel, d, momentum_only, decay=None, sr_seed=None,
           sr_step=0):
     sr = sr_seed is not None and param is not None and param.dtype in (torch.bfloat16, torch.float16)
+    parts = _parts(grad.device, nat.lib().a8_norm_parts_full(int(numel))) if mode in (1, 3) else None
     rc = nat.lib().a8_fused_update_1d_full(
         mode, nat.dtype_code(grad.dtype), nat.ptr(param), nat.ptr(grad), nat.ptr(variance), nat.ptr(m),
-        nat.ptr(norm_buf), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(decay), float(beta1), float(beta_val),
+        nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(decay), float(beta1), float(beta_val),
         float(eps_sq), float(eps_for_denom), int(bool(use_adam_denom)), float(eps_for_grad_sq),
         int(numel), float(d), int(bool(momentum_only)), 0.0, 1.0, 0, int(sr), int(sr_seed or 0), int(sr_step), 0,
         _stream(grad))

@@ -736,6 +736,31 @@ def _norm_buf(opt, device, which="norm_buf"):
     return b
 
 
+def _norm_parts(opt, device, n):
+    """Workspace of a norm pass's per-workgroup partial sums (float64): the library
+    adds a tensor's partials in index order, so the sum has the same bits run to
+    run.  Shared by the passes of a step, which run one after another on the stream."""
+    key = (device, "norm_parts")
+    b = opt._ws.get(key)
+    n = max(int(n), 1)
+    if b is None or b.numel() < n:
+        b = torch.empty(n, dtype=torch.float64, device=device)
+        opt._ws[key] = b
+    return b
+
+
+def _parts_of(P):
+    """Doubles of norm-pass workspace one tensor of plan P needs."""
+    L = nat.lib()
+    n = P.p.numel()
+    if P.path == "q1d":
+        return int(L.a8_norm_parts_1d(n, P.bs, P.mbs if P.has_m else P.bs))
+    if P.path == "sgd":
+        _, _, _, kind = _sgd_momentum(P)
+        return int(L.a8_norm_parts_sgd(n, P.mbs if kind == 1 else 0))
+    return int(L.a8_norm_parts_full(n))
+
+
 def _alpha_args(P):
     if P.alpha_t is not None:
         a = P.alpha_t.reshape(()).to(torch.float32)
@@ -755,6 +780,7 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
     L = nat.lib()
     st, p, g = P.st, P.p, P.g
     dec_t, dec_val, has_dec = _decay_args(P)
+    parts = _norm_parts(opt, p.device, _parts_of(P)) if norm_buf is not None else None
     if P.path == "q1d":
         vq = st["variance_q"]
         m_q = st["m_q"] if P.has_m else None
@@ -764,8 +790,8 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
         rc = L.a8_fused_update_1d(
             mode, int(P.sr), nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(m_q),
             nat.ptr(m_scale), nat.ptr(vq), nat.ptr(st["variance_scale"]), nat.ptr(st["variance_min_log"]),
-            nat.ptr(v_buf), nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
-            int(st.get("sr_seed", 0)), int(P.step), P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_d,
+            nat.ptr(v_buf), nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha_t), nat.ptr(prev_norm),
+            nat.ptr(dec_t), int(st.get("sr_seed", 0)), int(P.step), P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_d,
             int(P.adam_denom), _AL_FLOOR, P.eps_g, P.eps_sq, p.numel(), P.bs,
             P.mbs if P.has_m else P.bs, m_bits, m_mode, P.d, 16 if P.vqt == "al16" else 8,
             int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
@@ -784,7 +810,7 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
         var = _variance_of(P)
         rc = L.a8_fused_update_1d_full(
             mode, nat.dtype_code(p.dtype), nat.ptr(p), nat.ptr(g), nat.ptr(var), nat.ptr(m),
-            nat.ptr(norm_buf), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
+            nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha_t), nat.ptr(prev_norm), nat.ptr(dec_t),
             beta1, P.beta_val, P.eps_sq, P.eps_d, int(P.adam_denom), P.eps_g,
             p.numel(), P.d, int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
             int(P.sr), int(st.get("sr_seed", 0)), int(P.step), int(P.vbuf is not None), nat.stream_of(p.device))
@@ -855,8 +881,10 @@ def _run_sgd(opt, P):
     strm = nat.stream_of(dev)
 
     def launch(mode, norm_buf=None, fira=None):
+        parts = _norm_parts(opt, dev, _parts_of(P)) if mode == nat.MODE_NORM else None
         rc = L.a8_sgd_step(mode, nat.dtype_code(P.p.dtype), int(P.sr), nat.ptr(P.p), nat.ptr(P.g), nat.ptr(m_q),
-                           nat.ptr(m_scale), nat.ptr(m), nat.ptr(norm_buf), nat.ptr(fira), nat.ptr(alpha_t),
+                           nat.ptr(m_scale), nat.ptr(m), nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(fira),
+                           nat.ptr(alpha_t),
                            nat.ptr(dec_t), P.p.numel(), P.beta1 if P.has_m else 0.0, m_bits, m_mode,
                            P.mbs if kind == 1 else 32, P.d, float(alpha_val), float(dec_val), has_dec,
                            int(st.get("sr_seed", 0)), int(P.step), strm)
@@ -1069,6 +1097,11 @@ def _run_batch_f1dc(opt, key, plans):
         acc = torch.zeros(3 * n, dtype=torch.float32, device=dev)    # sum u^2 | sum M'^2 | sum p^2
         fout = torch.zeros(3 * n, dtype=torch.float32, device=dev)   # Fira: scale | prev norm | clean sum
         a0, f0 = acc.data_ptr(), fout.data_ptr()
+        poffs, ptot = [], 0
+        for pl in plans:   # per-tensor slices of the passes' partial-sum workspace
+            poffs.append(ptot)
+            ptot += _parts_of(pl)
+        parts = torch.empty(max(ptot, 1), dtype=torch.float64, device=dev)
         arrs = {}
         for mode in (nat.MODE_NORM, nat.MODE_MNORM, nat.MODE_APPLY):
             if mode == nat.MODE_MNORM and not mnorm:
@@ -1086,9 +1119,10 @@ def _run_batch_f1dc(opt, key, plans):
                 fs = f0 + 4 * i if (mode == nat.MODE_APPLY and fira) else None
                 arr[i] = nat.TensorFull(pl.p.data_ptr(), pl.g.data_ptr(), _variance_of(pl).data_ptr(),
                                         nat.ptr(st.get("m") if pl.has_m else None), nb, None, prev, None,
-                                        pl.p.numel(), int(st.get("sr_seed", 0)), psq, fs)
+                                        pl.p.numel(), int(st.get("sr_seed", 0)), psq, fs,
+                                        parts.data_ptr() + 8 * poffs[i])
             arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_full(n)), dtype=torch.uint8, device=dev), 1]
-        ent = {"refs": refs, "acc": acc, "fout": fout, "arrs": arrs}
+        ent = {"refs": refs, "acc": acc, "fout": fout, "parts": parts, "arrs": arrs}
         if len(ws) > 16:
             ws.clear()
         ws[ck] = ent
@@ -1162,6 +1196,11 @@ def _run_batch_q1dc(opt, key, plans):
             offs.append(tot)
             tot += (pl.p.numel() + 3) // 4 * 4
         vbuf = torch.empty(max(tot, 4), dtype=torch.float32, device=dev)
+        poffs, ptot = [], 0
+        for pl in plans:   # per-tensor slices of the passes' partial-sum workspace
+            poffs.append(ptot)
+            ptot += _parts_of(pl)
+        parts = torch.empty(max(ptot, 1), dtype=torch.float64, device=dev)
         acc = torch.zeros(2 * n, dtype=torch.float32, device=dev)    # sum u^2 | sum M'^2
         fout = torch.zeros(3 * n, dtype=torch.float32, device=dev)   # Fira: scale | prev norm | clean sum
         a0, f0, v0 = acc.data_ptr(), fout.data_ptr(), vbuf.data_ptr()
@@ -1183,9 +1222,10 @@ def _run_batch_q1dc(opt, key, plans):
                     pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(st.get("m_q") if pl.has_m else None),
                     nat.ptr(st.get("m_scale") if pl.has_m else None), st["variance_q"].data_ptr(),
                     st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), v0 + 4 * offs[i], nb,
-                    None, prev, None, pl.p.numel(), int(st.get("sr_seed", 0)), fs)
+                    None, prev, None, pl.p.numel(), int(st.get("sr_seed", 0)), fs,
+                    parts.data_ptr() + 8 * poffs[i])
             arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_1d(n)), dtype=torch.uint8, device=dev), 1]
-        ent = {"refs": refs, "acc": acc, "fout": fout, "vbuf": vbuf, "arrs": arrs}
+        ent = {"refs": refs, "acc": acc, "fout": fout, "vbuf": vbuf, "parts": parts, "arrs": arrs}
         if len(ws) > 16:
             ws.clear()
         ws[ck] = ent
@@ -1243,11 +1283,11 @@ def _run_batch(opt, key, plans):
     if path == "factored":
         _run_factored(opt, plans)
         return
+    if path == "f1dc":   # also for one tensor: scale_parameter's sum of p^2 is the kernel's fixed-order sum
+        _run_batch_f1dc(opt, key, plans)
+        return
     if len(plans) == 1 and plans[0].dsc is None:
         _run_single(opt, plans[0])
-        return
-    if path == "f1dc":
-        _run_batch_f1dc(opt, key, plans)
         return
     if path == "q1dc":
         _run_batch_q1dc(opt, key, plans)

@@ -574,4 +574,42 @@ __device__ __forceinline__ double grp_sum_d(double x, int G) {
   return x;
 }
 
+// ---------------------------------------------------------------- fixed-order sums
+// A norm pass writes one partial sum per workgroup, and a finishing launch adds
+// a tensor's partials in index order, so a sum of squares has the same bits
+// whatever order the workgroups ran in (float atomics would not), and a tensor
+// gives the same sum in a batched launch as on its own.
+//
+// wg_partial: the workgroup's sum of one float per lane -- each wave's butterfly
+// sum (grp_sum), then the NW wave sums added in wave order in double.  Every lane
+// calls it (one barrier); lane 0 receives the sum.  s_w: NW floats of LDS that
+// nothing else uses.
+template <int NW>
+__device__ __forceinline__ double wg_partial(float v, float* s_w) {
+  const float t = grp_sum(v, 64);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = t;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += (double)s_w[w];
+  }
+  return s;
+}
+
+// sum_parts: the sum of p[0..n) by one 256-lane workgroup in a fixed order --
+// lane l adds p[l], p[l + 256], ... in turn, then each wave's butterfly and the
+// four wave sums in wave order.  Every lane calls it; lane 0 receives the sum.
+// s_w: 4 doubles of LDS.
+__device__ __forceinline__ double sum_parts(const double* p, int64_t n, double* s_w) {
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) s += p[i];
+  s = grp_sum_d(s, 64);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = s;
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x == 0) t = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
+  return t;
+}
+
 }  // namespace a8

@@ -28,6 +28,7 @@ struct DescFull {
   uint64_t sr_seed;
   float* psq;               // sum of p^2 (NORM pass with scale_param), read by the update passes
   const float* fira_scale;  // Fira limiter scale multiplied into the step, or null
+  double* norm_part;        // NORM / LAG / MNORM: partial sums of u^2 (then of p^2), one per workgroup
 };
 
 struct HyperFull {
@@ -180,29 +181,45 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
       }
     }
   }
-  // Sums: the workgroup reduces in a fixed order (waves, then the four wave sums
-  // through LDS) and adds once to the tensor's accumulator.  A tensor with fp32
-  // state has fewer than min_8bit_size (4096) elements, at most two workgroups,
-  // and a float sum of two terms does not depend on their order: run to run the
-  // result is the same bits.
+  // Sums: this workgroup's partials (wg_partial: a fixed order), u^2 at
+  // norm_part[wl] and p^2 at norm_part[np + wl] (np workgroups of the tensor);
+  // k_full_fin adds them in index order.
   if constexpr (MODE == 1 || MODE == 3 || MODE == 4) {
-    __shared__ float s4[8];
-    const float t = grp_sum(sq, 64);
-    const float tp = (MODE == 1 && h.scale_param) ? grp_sum(psum, 64) : 0.0f;
-    if ((lane & 63) == 0) {
-      s4[lane >> 6] = t;
-      s4[4 + (lane >> 6)] = tp;
-    }
-    __syncthreads();
-    if (lane == 0) {
-      const float tot = ((s4[0] + s4[1]) + s4[2]) + s4[3];
-      if (tot != 0.0f) atomicAdd(D.norm_buf, tot);
-      if (MODE == 1 && h.scale_param) {
-        const float ptot = ((s4[4] + s4[5]) + s4[6]) + s4[7];
-        if (ptot != 0.0f) atomicAdd(D.psq, ptot);
-      }
+    __shared__ float s4[4], s4p[4];
+    const double t = wg_partial<4>(sq, s4);
+    if (lane == 0) gp(D.norm_part)[wl] = t;
+    if (MODE == 1 && h.scale_param) {
+      const int64_t np = (n + kFElems - 1) / kFElems;
+      const double tp = wg_partial<4>(psum, s4p);
+      if (lane == 0) gp(D.norm_part)[np + wl] = tp;
     }
   }
+}
+
+// Second launch of a NORM / LAG / MNORM pass: one workgroup per tensor adds the
+// tensor's partials in index order to norm_buf (and, with scale_param, the p^2
+// partials to psq), both zeroed by the caller.
+__global__ __launch_bounds__(kFLanes) void k_full_fin(DescFull one, const DescFull* __restrict__ table, int ntab,
+                                                     int64_t nwg, int psq) {
+  __shared__ double s_w[4];
+  const int i = (int)blockIdx.x;
+  const DescFull D = table ? table[i] : one;
+  const int64_t np = (table ? (i + 1 < ntab ? table[i + 1].wg_begin : nwg) : nwg) - D.wg_begin;
+  const double s = sum_parts(D.norm_part, np, s_w);
+  if (threadIdx.x == 0) *gp(D.norm_buf) += (float)s;
+  if (psq) {
+    __syncthreads();   // lane 0 has read s_w
+    const double t = sum_parts(D.norm_part + np, np, s_w);
+    if (threadIdx.x == 0) *gp(D.psq) += (float)t;
+  }
+}
+
+static int finish_full(int mode, const DescFull& one, const DescFull* tab, int ntab, int64_t nwg, int psq,
+                       hipStream_t st) {
+  if (mode != 1 && mode != 3 && mode != 4) return 0;
+  hipLaunchKernelGGL(k_full_fin, dim3(tab ? (unsigned)ntab : 1u), dim3(kFLanes), 0, st, one, tab, ntab, nwg,
+                     mode == 1 ? psq : 0);
+  return check_launch("k_full_fin");
 }
 
 template <typename T, bool SR>
@@ -282,7 +299,7 @@ using namespace a8;
 extern "C" {
 
 int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
-                            float* m, float* norm_buf, const float* alpha, const float* prev_norm,
+                            float* m, float* norm_buf, double* norm_parts, const float* alpha, const float* prev_norm,
                             const float* decay, double beta1, double beta_val, float eps_sq,
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
@@ -295,14 +312,18 @@ int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, 
   if (mode != 0 && !norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
   if ((mode == 3 || mode == 4) && !prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
   if (mode == 4 && !(m && momentum_only)) return set_error(A8_ERR_ARG, "MNORM needs momentum and momentum_only");
+  if ((mode == 1 || mode == 3 || mode == 4) && !norm_parts)
+    return set_error(A8_ERR_ARG, "NORM/LAG/MNORM need norm_parts (a8_norm_parts_full doubles)");
   DescFull D{};
-  D.param = param; D.grad = grad; D.v = variance; D.m = m; D.norm_buf = norm_buf;
+  D.param = param; D.grad = grad; D.v = variance; D.m = m; D.norm_buf = norm_buf; D.norm_part = norm_parts;
   D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
   HyperFull h = make_hf(beta1, beta_val, eps_sq, eps_for_denom, use_adam_denom, eps_for_grad_sq, d,
                         momentum_only, sr_step, alpha_val, decay_val, has_decay);
   h.v_ready = v_ready;
-  return launch_full_any(dtype, stochastic, mode, D, nullptr, 0, (numel + kFElems - 1) / kFElems, h,
-                         (hipStream_t)stream);
+  const int64_t nwg = (numel + kFElems - 1) / kFElems;
+  const int rc = launch_full_any(dtype, stochastic, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
+  if (rc) return rc;
+  return finish_full(mode, D, nullptr, 0, nwg, 0, (hipStream_t)stream);
 }
 
 int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* tensors, int ntensors,
@@ -313,7 +334,8 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
                                   int v_ready, int upload, const void* step_scalars, void* stream) {
   if (ntensors <= 0) return 0;
-  if (scale_param && mode != 2 && mode != 1) return set_error(A8_ERR_ARG, "scale_param needs the NORM/APPLY passes");
+  if (scale_param && mode != 1 && mode != 2 && mode != 4)
+    return set_error(A8_ERR_ARG, "scale_param needs the NORM / MNORM / APPLY passes");
   if (wd_mode && has_decay) return set_error(A8_ERR_ARG, "give has_decay or wd_mode, not both");
   if ((int64_t)sizeof(DescFull) * ntensors > table_bytes)
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_table_bytes_full(ntensors)");
@@ -330,11 +352,13 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
     if (!t.param && mode != 1 && mode != 4) return set_error(A8_ERR_ARG, "null param");
     if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
     if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "null prev_norm");
+    if ((mode == 1 || mode == 3 || mode == 4) && !t.norm_parts)
+      return set_error(A8_ERR_ARG, "NORM/LAG/MNORM need norm_parts (a8_norm_parts_full doubles per tensor)");
     DescFull& D = tab[(size_t)i];
     D.param = t.param; D.grad = t.grad; D.v = t.variance; D.m = t.m; D.norm_buf = t.norm_buf;
     D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay; D.numel = t.numel;
     D.sr_seed = t.sr_seed;
-    D.psq = t.psq; D.fira_scale = t.fira_scale;
+    D.psq = t.psq; D.fira_scale = t.fira_scale; D.norm_part = t.norm_parts;
     if (scale_param && (!t.psq || !t.param)) return set_error(A8_ERR_ARG, "scale_param needs psq and param");
     D.wg_begin = wg;
     wg += (t.numel + kFElems - 1) / kFElems;
@@ -347,11 +371,18 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
   h.scale_param = scale_param; h.eps2 = eps2; h.wd_mode = wd_mode; h.wd = wd; h.v_ready = v_ready;
   h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   DescFull none{};
-  return launch_full_any(dtype, stochastic, mode, none, reinterpret_cast<const DescFull*>(table_dev),
-                         ntensors, wg, h, st);
+  const DescFull* tabd = reinterpret_cast<const DescFull*>(table_dev);
+  const int rc = launch_full_any(dtype, stochastic, mode, none, tabd, ntensors, wg, h, st);
+  if (rc) return rc;
+  return finish_full(mode, none, tabd, ntensors, wg, scale_param, st);
 }
 
 int64_t a8_table_bytes_full(int ntensors) { return (int64_t)sizeof(DescFull) * (int64_t)ntensors; }
+
+int64_t a8_norm_parts_full(int64_t numel) {
+  if (numel <= 0) return 0;
+  return 2 * ((numel + kFElems - 1) / kFElems);
+}
 
 int a8_fira_scalar(const float* x, const float* prev, const float* alpha, float* out, int64_t n,
                    int has_prev, int apply, float margin, void* stream) {

@@ -38,6 +38,7 @@ struct SgdDesc {
   int64_t numel;
   int64_t wg_begin;
   uint64_t sr_seed;
+  double* norm_part;    // NORM: one partial sum of u^2 per workgroup (added in order by k_sgd_fin)
 };
 
 struct SgdHyp {
@@ -113,8 +114,9 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
       float sq = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k) sq += u[k] * u[k];
-      const float t = grp_sum(sq, 64);
-      if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+      __shared__ float s_nw[4];
+      const double t = wg_partial<4>(sq, s_nw);
+      if (lane == 0) gp(D.norm_part)[(int64_t)blockIdx.x - D.wg_begin] = t;
     } else {
       const float a = D.alpha ? *D.alpha : h.alpha_val;
       float step = a;
@@ -277,8 +279,9 @@ __global__ __launch_bounds__(kSLanes) void k_sgd_gen(SgdDesc one, const SgdDesc*
     }
   }
   if constexpr (MODE == 1) {
-    const float t = grp_sum(sq, 64);
-    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+    __shared__ float s_nw[4];
+    const double t = wg_partial<4>(sq, s_nw);
+    if (lane == 0) gp(D.norm_part)[(int64_t)blockIdx.x - D.wg_begin] = t;
     return;
   }
   __syncthreads();
@@ -339,8 +342,31 @@ static int launch_t(int mode, int mk, int64_t nwg, hipStream_t st, const SgdDesc
   return check_launch("k_sgd");
 }
 
-// kind: 0 no momentum, 1 quantised, 2 fp32 momentum.
+// Second launch of a NORM pass: one workgroup per tensor adds the tensor's
+// partials in index order (sum_parts) to its norm_buf, which the caller zeroed.
+__global__ __launch_bounds__(kSLanes) void k_sgd_fin(SgdDesc one, const SgdDesc* __restrict__ table, int ntab,
+                                                    int64_t nwg) {
+  __shared__ double s_w[4];
+  const int i = (int)blockIdx.x;
+  const SgdDesc D = table ? table[i] : one;
+  const int64_t end = table ? (i + 1 < ntab ? table[i + 1].wg_begin : nwg) : nwg;
+  const double s = sum_parts(D.norm_part, end - D.wg_begin, s_w);
+  if (threadIdx.x == 0) *gp(D.norm_buf) += (float)s;
+}
+
+static int launch_sgd_body(int dtype, int stochastic, int mode, int kind, int64_t nwg, hipStream_t st,
+                           const SgdDesc& one, const SgdDesc* tab, int ntab, const SgdHyp& h);
+
+// kind: 0 no momentum, 1 quantised, 2 fp32 momentum.  NORM adds its finishing launch.
 static int launch_sgd(int dtype, int stochastic, int mode, int kind, int64_t nwg, hipStream_t st,
+                      const SgdDesc& one, const SgdDesc* tab, int ntab, const SgdHyp& h) {
+  const int rc = launch_sgd_body(dtype, stochastic, mode, kind, nwg, st, one, tab, ntab, h);
+  if (rc || mode != 1 || nwg <= 0) return rc;
+  hipLaunchKernelGGL(k_sgd_fin, dim3(tab ? (unsigned)ntab : 1u), dim3(kSLanes), 0, st, one, tab, ntab, nwg);
+  return check_launch("k_sgd_fin");
+}
+
+static int launch_sgd_body(int dtype, int stochastic, int mode, int kind, int64_t nwg, hipStream_t st,
                       const SgdDesc& one, const SgdDesc* tab, int ntab, const SgdHyp& h) {
   if (nwg <= 0) return 0;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "tensor too large");
@@ -432,7 +458,7 @@ using namespace a8;
 extern "C" {
 
 int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* grad, uint8_t* m_q, float* m_scale,
-                float* m, float* norm_buf, const float* fira, const float* alpha, const float* decay, int64_t numel,
+                float* m, float* norm_buf, double* norm_parts, const float* fira, const float* alpha, const float* decay, int64_t numel,
                 double beta1, int m_bits, int m_mode, int m_block_size, float d, float alpha_val, float decay_val,
                 int has_decay, uint64_t sr_seed, uint64_t sr_step, void* stream) {
   if (numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
@@ -440,6 +466,7 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
   if (numel == 0) return 0;
   if (!grad || (mode != 1 && !param)) return set_error(A8_ERR_ARG, "null param/grad");
   if (mode != 0 && !norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
+  if (mode == 1 && !norm_parts) return set_error(A8_ERR_ARG, "NORM needs norm_parts (a8_norm_parts_sgd doubles)");
   if (m_q && m) return set_error(A8_ERR_ARG, "give quantised (m_q) or fp32 (m) momentum, not both");
   if (m_q && !m_scale) return set_error(A8_ERR_ARG, "null m_scale");
   if (!aligned16(grad) || (param && !aligned16(param)) || (m && !aligned16(m)) || (m_q && !aligned16(m_q)))
@@ -463,6 +490,7 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
   SgdDesc D{};
   D.param = param; D.grad = grad; D.m_q = m_q; D.m_scale = m_scale; D.m = m; D.norm_buf = norm_buf;
   D.fira = fira; D.alpha = alpha; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
+  D.norm_part = norm_parts;
   return launch_sgd(dtype, stochastic, mode, kind, units_of(numel, h), (hipStream_t)stream, D,
                     nullptr, 0, h);
 }
@@ -493,13 +521,14 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
     if (t.numel < 0) return set_error(A8_ERR_SIZE, "numel < 0");
     if (!t.grad || (mode != 1 && !t.param)) return set_error(A8_ERR_ARG, "null param/grad");
     if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "null norm_buf");
+    if (mode == 1 && !t.norm_parts) return set_error(A8_ERR_ARG, "NORM needs norm_parts (a8_norm_parts_sgd doubles)");
     if (m_kind == 1 && (!t.m_q || !t.m_scale)) return set_error(A8_ERR_ARG, "null m_q/m_scale");
     if (m_kind == 2 && !t.m) return set_error(A8_ERR_ARG, "null m");
     if (!aligned16(t.grad) || (t.param && !aligned16(t.param)) || (m_kind == 2 && !aligned16(t.m)) ||
         (m_kind == 1 && !aligned16(t.m_q)))
       return set_error(A8_ERR_ALIGN, "param, grad and momentum must be 16-byte aligned");
     SgdDesc& D = tab[(size_t)i];
-    D.param = t.param; D.grad = t.grad; D.norm_buf = t.norm_buf; D.fira = t.fira;
+    D.param = t.param; D.grad = t.grad; D.norm_buf = t.norm_buf; D.fira = t.fira; D.norm_part = t.norm_parts;
     D.alpha = t.alpha; D.decay = t.decay; D.numel = t.numel; D.sr_seed = t.sr_seed;
     if (m_kind == 1) { D.m_q = t.m_q; D.m_scale = t.m_scale; }
     if (m_kind == 2) D.m = t.m;
@@ -515,6 +544,13 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
 }
 
 int64_t a8_table_bytes_sgd(int ntensors) { return (int64_t)sizeof(SgdDesc) * (int64_t)ntensors; }
+
+int64_t a8_norm_parts_sgd(int64_t numel, int m_block_size) {
+  SgdHyp h{};
+  if (m_block_size > 0 && block_log2(m_block_size, h)) return -1;
+  if (numel <= 0) return 0;
+  return units_of(numel, h);
+}
 
 int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype, float* fp32_out, double beta,
                        int block_size, int64_t numel, int m_bits, int m_mode, void* stream) {

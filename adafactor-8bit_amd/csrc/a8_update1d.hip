@@ -41,6 +41,7 @@ struct Desc1D {
   int64_t wg_begin;
   uint64_t sr_seed;
   const float* fira_scale;   // APPLY: Fira limiter scale multiplied into the step, or null
+  double* norm_part;         // NORM / LAG / MNORM: one partial sum of squares per workgroup
 };
 
 struct Hyper1D {
@@ -618,10 +619,11 @@ __device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int
     }
   }
 
-  // ---- sum of squares for NORM / LAG / MNORM
+  // ---- sum of squares for NORM / LAG / MNORM: this workgroup's partial
   if constexpr (kSq) {
-    const float t = grp_sum(sq, 64);
-    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+    __shared__ float s_nw[4];
+    const double t = wg_partial<4>(sq, s_nw);
+    if (lane == 0) gp(D.norm_part)[wl] = t;
   }
 }
 
@@ -845,9 +847,10 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
       atomicMin(&s_st[1], vkey);
     }
   }
-  if constexpr (kSq) {
-    const float t = grp_sum(sq, 64);
-    if ((lane & 63) == 0 && t != 0.0f) atomicAdd(D.norm_buf, t);
+  if constexpr (kSq) {   // this workgroup's partial sum of squares
+    __shared__ float s_nw[4];
+    const double t = wg_partial<4>(sq, s_nw);
+    if (lane == 0) gp(D.norm_part)[blk] = t;
   }
   __syncthreads();
   if constexpr (kVbuf && !(kWrite && kHasM)) return;   // MNORM: no state written
@@ -906,6 +909,29 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
     for (int i = lane; i < mpb; i += kLanes)
       if (blk * mpb + i < nmb) gp(D.m_scale)[blk * mpb + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
   }
+}
+
+// ------------------------------------------------------------ norm finish
+// Second launch of a NORM / LAG / MNORM pass: one workgroup per tensor adds the
+// tensor's workgroup partials in index order (sum_parts) and adds the sum to its
+// norm_buf, which the caller zeroed.  The sum is the same bits whatever order
+// the pass's workgroups ran in, and the same in a batched launch as alone.
+__global__ __launch_bounds__(kLanes) void k_update1d_fin(Desc1D one, const Desc1D* __restrict__ table, int ntab,
+                                                        int64_t nwg) {
+  __shared__ double s_w[4];
+  const int i = (int)blockIdx.x;
+  const Desc1D D = table ? table[i] : one;
+  const int64_t end = table ? (i + 1 < ntab ? table[i + 1].wg_begin : nwg) : nwg;
+  const double s = sum_parts(D.norm_part, end - D.wg_begin, s_w);
+  if (threadIdx.x == 0) *gp(D.norm_buf) += (float)s;
+}
+
+static int finish_norm_1d(int mode, const Desc1D& one, const Desc1D* table, int ntab, int64_t nwg,
+                          hipStream_t st) {
+  if (mode != 1 && mode != 3 && mode != 4) return 0;
+  hipLaunchKernelGGL(k_update1d_fin, dim3(table ? (unsigned)ntab : 1u), dim3(kLanes), 0, st, one, table, ntab,
+                     nwg);
+  return check_launch("k_update1d_fin");
 }
 
 // ------------------------------------------------------------ launch glue
@@ -1017,7 +1043,7 @@ using namespace a8;
 // ============================================================== C-ABI
 static int update1d_entry(int mode, int sr, int dtype, void* param, const void* grad, uint8_t* m_q,
                           float* m_scale, void* v_q, float* v_scale, float* v_min_log, float* v_buf,
-                          float* norm_buf, const float* alpha, const float* prev_norm,
+                          float* norm_buf, double* norm_parts, const float* alpha, const float* prev_norm,
                           const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
                           double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
                           float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
@@ -1037,13 +1063,15 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   if ((mode == 1 || mode == 3) && !norm_buf) return set_error(A8_ERR_ARG, "NORM/LAG need norm_buf");
   if (mode == 2 && !norm_buf) return set_error(A8_ERR_ARG, "APPLY needs norm_buf");
   if (mode == 3 && !prev_norm) return set_error(A8_ERR_ARG, "LAG needs prev_norm");
+  if ((mode == 1 || mode == 3 || mode == 4) && !norm_parts)
+    return set_error(A8_ERR_ARG, "NORM/LAG/MNORM need norm_parts (a8_norm_parts_1d doubles)");
   if (!aligned16(param) || !aligned16(grad) || !aligned16(v_q) || (has_m && !aligned16(m_q)))
     return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
   Desc1D D{};
   D.param = param; D.grad = grad; D.m_q = m_q; D.m_scale = m_scale;
   D.v_q = v_q; D.v_scale = v_scale; D.v_min_log = v_min_log; D.v_buf = v_buf;
   D.norm_buf = norm_buf; D.alpha = alpha; D.prev_norm = prev_norm; D.decay = decay;
-  D.numel = numel; D.wg_begin = 0; D.sr_seed = sr_seed;
+  D.numel = numel; D.wg_begin = 0; D.sr_seed = sr_seed; D.norm_part = norm_parts;
   Hyper1D h{};
   h.beta1 = (float)beta1;
   h.w_m = (float)(1.0 - beta1);
@@ -1059,7 +1087,9 @@ static int update1d_entry(int mode, int sr, int dtype, void* param, const void* 
   h.gen = fast_shape_ok(h.block_size, h.m_block_size) ? 0 : 1;
   const int64_t unit = unit_of(h.block_size, h.m_block_size);
   const int64_t nwg = (numel + unit - 1) / unit;
-  return launch_any(dtype, sr, v_bits, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
+  rc = launch_any(dtype, sr, v_bits, mode, D, nullptr, 0, nwg, h, (hipStream_t)stream);
+  if (rc) return rc;
+  return finish_norm_1d(mode, D, nullptr, 0, nwg, (hipStream_t)stream);
 }
 
 // Validate a multi-tensor launch and, if `image` is non-null, write its device table
@@ -1088,6 +1118,8 @@ static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int n
       return set_error(A8_ERR_ARG, "NORM/APPLY/MNORM need v_buf");
     if (mode != 0 && !t.norm_buf) return set_error(A8_ERR_ARG, "NORM/APPLY/LAG/MNORM need norm_buf");
     if ((mode == 3 || mode == 4) && !t.prev_norm) return set_error(A8_ERR_ARG, "LAG/MNORM need prev_norm");
+    if ((mode == 1 || mode == 3 || mode == 4) && !t.norm_parts)
+      return set_error(A8_ERR_ARG, "NORM/LAG/MNORM need norm_parts (a8_norm_parts_1d doubles per tensor)");
     if (mode == 4 && !has_m) return set_error(A8_ERR_ARG, "MNORM needs momentum codes");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.v_q) || (has_m && !aligned16(t.m_q)))
       return set_error(A8_ERR_ALIGN, "param/grad/code buffers must be 16-byte aligned");
@@ -1098,6 +1130,7 @@ static int table_image_1d(int mode, int dtype, const a8_tensor1d* tensors, int n
       D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_buf = t.v_buf;
       D.norm_buf = t.norm_buf; D.alpha = t.alpha; D.prev_norm = t.prev_norm; D.decay = t.decay;
       D.numel = t.numel; D.wg_begin = wg; D.sr_seed = t.sr_seed; D.fira_scale = t.fira_scale;
+      D.norm_part = t.norm_parts;
       std::memcpy(&tab[i], &D, sizeof(Desc1D));
       const int32_t f = (int32_t)(wg < 0x7FFFFFFF ? wg : 0x7FFFFFFF);
       std::memcpy(&first[i], &f, sizeof(int32_t));
@@ -1129,8 +1162,10 @@ static int launch_multi_1d(int mode, int stochastic, int dtype, bool has_m, int 
   h.dsc = reinterpret_cast<const a8_step_scalars*>(dsc);
   h.gen = fast_shape_ok(h.block_size, h.m_block_size) ? 0 : 1;
   Desc1D none{};
-  return launch_any(dtype, stochastic, v_bits, mode, none, reinterpret_cast<const Desc1D*>(table_dev), ntensors,
-                    nwg, h, st);
+  const Desc1D* tab = reinterpret_cast<const Desc1D*>(table_dev);
+  const int rc = launch_any(dtype, stochastic, v_bits, mode, none, tab, ntensors, nwg, h, st);
+  if (rc) return rc;
+  return finish_norm_1d(mode, none, tab, ntensors, nwg, st);
 }
 
 // ------------------------------------------------------------ no-allocation table
@@ -1146,6 +1181,29 @@ static void* g_scratch_ptr[kScratchDevices];
 static std::mutex g_scratch_mu;
 alignas(16) static char g_stage[kScratchBytes];   // host image of the table (a8_fused_update_1d_multi_noalloc)
 static std::mutex g_stage_mu;
+// Per device: a fingerprint of the tensors whose table the scratch array holds, so
+// that a call with upload == 0 is refused unless it names those same tensors.
+struct ScratchPrint {
+  uint64_t hash;
+  int ntensors;
+  int valid;
+};
+static ScratchPrint g_scratch_print[kScratchDevices];
+
+// FNV-1a over the tensor records and the block sizes (the inputs of the table
+// image; a8_tensor1d has no padding bytes).
+static uint64_t table_print(const a8_tensor1d* t, int n, int block_size, int m_block_size) {
+  uint64_t h = 1469598103934665603ull;
+  auto mix = [&h](const void* p, size_t bytes) {
+    const unsigned char* c = static_cast<const unsigned char*>(p);
+    for (size_t i = 0; i < bytes; ++i) { h ^= c[i]; h *= 1099511628211ull; }
+  };
+  mix(&n, sizeof n);
+  mix(&block_size, sizeof block_size);
+  mix(&m_block_size, sizeof m_block_size);
+  mix(t, sizeof(a8_tensor1d) * (size_t)n);
+  return h;
+}
 
 static int scratch_of_current_device(void** out) {
   int dev = -1;
@@ -1170,15 +1228,15 @@ extern "C" {
 
 int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
                        uint8_t* m_q, float* m_scale, void* v_q, float* v_scale, float* v_min_log,
-                       float* v_buf, float* norm_buf, const float* alpha, const float* prev_norm,
-                       const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
-                       double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
-                       float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
-                       int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                       float* v_buf, float* norm_buf, double* norm_parts, const float* alpha,
+                       const float* prev_norm, const float* decay, uint64_t sr_seed, uint64_t sr_step,
+                       double beta1, double beta_val, float eps_for_denom, int use_adam_denom,
+                       float log_floor, float eps_for_grad_sq, float eps_sq, int64_t numel,
+                       int block_size, int m_block_size, int m_bits, int m_mode, float d, int v_bits,
                        int momentum_only, float alpha_val, float decay_val, int has_decay,
                        void* stream) {
   return update1d_entry(mode, stochastic, dtype, param, grad, m_q, m_scale, v_q, v_scale, v_min_log,
-                        v_buf, norm_buf, alpha, prev_norm, decay, sr_seed, sr_step, beta1, beta_val,
+                        v_buf, norm_buf, norm_parts, alpha, prev_norm, decay, sr_seed, sr_step, beta1, beta_val,
                         eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, numel,
                         block_size, m_block_size, m_bits, m_mode, d, v_bits, momentum_only, alpha_val,
                         decay_val, has_decay, stream);
@@ -1229,8 +1287,20 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
   int rc = scratch_of_current_device(&table_dev);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(A8_ERR_HIP, "hipGetDevice failed");
+  const uint64_t print = table_print(tensors, ntensors, block_size, m_block_size);
   int64_t nwg = 0;
   if (upload) {
+    // A captured graph would replay the copy from the library's host buffer as it is at
+    // replay time, which a later call may have rewritten: the table must be uploaded
+    // eagerly, and a captured call reuses it (upload == 0).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess)
+      return set_error(A8_ERR_HIP, "hipStreamIsCapturing failed");
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(A8_ERR_ARG, "a8_fused_update_1d_multi_noalloc: upload != 0 on a capturing stream; upload "
+                                   "the table in an eager call first and capture with upload == 0");
     // The image is built in a host buffer of the library's own (no allocation) and
     // copied from there; the copy from pageable memory has consumed the buffer when
     // hipMemcpyAsync returns, so the next call may reuse it.
@@ -1241,7 +1311,16 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
     if (hipMemcpyAsync(table_dev, g_stage, (size_t)a8_table_bytes_1d(ntensors), hipMemcpyHostToDevice, st) !=
         hipSuccess)
       return set_error(A8_ERR_HIP, "scratch table upload failed");
+    std::lock_guard<std::mutex> plock(g_scratch_mu);
+    g_scratch_print[dev] = ScratchPrint{print, ntensors, 1};
   } else {
+    {
+      std::lock_guard<std::mutex> plock(g_scratch_mu);
+      const ScratchPrint& sp = g_scratch_print[dev];
+      if (!sp.valid || sp.ntensors != ntensors || sp.hash != print)
+        return set_error(A8_ERR_ARG, "a8_fused_update_1d_multi_noalloc: upload == 0, but the tensors (or block "
+                                     "sizes) differ from those of the table last uploaded on this device");
+    }
     rc = table_image_1d(mode, dtype, tensors, ntensors, block_size, m_block_size, m_bits, m_mode, v_bits,
                         momentum_only, nullptr, &nwg);
     if (rc) return rc;
@@ -1250,6 +1329,13 @@ int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const 
                          beta_val, eps_for_denom, use_adam_denom, log_floor, eps_for_grad_sq, eps_sq, block_size,
                          m_block_size, m_bits, m_mode, d, v_bits, momentum_only, sr_step, alpha_val, decay_val,
                          has_decay, step_scalars, st);
+}
+
+int64_t a8_norm_parts_1d(int64_t numel, int block_size, int m_block_size) {
+  if (block_size <= 0 || m_block_size <= 0) return -1;
+  if (numel <= 0) return 0;
+  const int64_t unit = unit_of(block_size, m_block_size);
+  return (numel + unit - 1) / unit;
 }
 
 int a8_noalloc_max_tensors_1d(void) { return (int)(kScratchBytes / (sizeof(Desc1D) + sizeof(int32_t))); }

@@ -77,6 +77,11 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
  *               v_min_log fp32 per block
  *   v_buf       fp32[numel] exact V written by NORM, read by APPLY
  *   norm_buf    fp32[1] sum of squares accumulated by NORM/LAG, read by APPLY
+ *   norm_parts  NORM/LAG/MNORM: a8_norm_parts_1d(numel, block_size, m_block_size)
+ *               doubles of workspace.  The pass writes one partial sum per workgroup
+ *               there and a second launch adds them in index order to norm_buf, so
+ *               the sum has the same bits run to run (the reference adds with float
+ *               atomics, kernels.cu:297-316); NULL is allowed for modes 0 and 2
  *   alpha, prev_norm, decay: device fp32 scalars; alpha == NULL uses alpha_val,
  *               decay == NULL uses decay_val when has_decay (p := p*decay before
  *               the update, the decoupled weight decay of optimizer.py:2034-2039)
@@ -89,13 +94,16 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
  * workgroup per V block. */
 int a8_fused_update_1d(int mode, int stochastic, int dtype, void* param, const void* grad,
                        uint8_t* m_q, float* m_scale, void* v_q, float* v_scale, float* v_min_log,
-                       float* v_buf, float* norm_buf, const float* alpha, const float* prev_norm,
-                       const float* decay, uint64_t sr_seed, uint64_t sr_step, double beta1,
-                       double beta_val, float eps_for_denom, int use_adam_denom, float log_floor,
-                       float eps_for_grad_sq, float eps_sq, int64_t numel, int block_size,
-                       int m_block_size, int m_bits, int m_mode, float d, int v_bits,
+                       float* v_buf, float* norm_buf, double* norm_parts, const float* alpha,
+                       const float* prev_norm, const float* decay, uint64_t sr_seed, uint64_t sr_step,
+                       double beta1, double beta_val, float eps_for_denom, int use_adam_denom,
+                       float log_floor, float eps_for_grad_sq, float eps_sq, int64_t numel,
+                       int block_size, int m_block_size, int m_bits, int m_mode, float d, int v_bits,
                        int momentum_only, float alpha_val, float decay_val, int has_decay,
                        void* stream);
+/* Doubles of norm_parts workspace a NORM / LAG / MNORM pass of a8_fused_update_1d needs for
+ * one tensor (the workgroups it runs; pass m_block_size = block_size without momentum). */
+int64_t a8_norm_parts_1d(int64_t numel, int block_size, int m_block_size);
 
 /* ---- Per-step scalars on the device (graph-capturable steps) ---------------
  * No counterpart in the reference, which forms these on the host per parameter
@@ -152,6 +160,7 @@ typedef struct a8_tensor1d {
   int64_t numel;
   uint64_t sr_seed;
   const float* fira_scale; /* APPLY: the step is multiplied by this Fira limiter scale (NULL: none) */
+  double* norm_parts;      /* NORM/LAG/MNORM: a8_norm_parts_1d(numel, ...) doubles of workspace */
 } a8_tensor1d;
 
 /* Multi-tensor form of a8_fused_update_1d: one launch over `ntensors` tensors
@@ -176,12 +185,17 @@ int64_t a8_table_bytes_1d(int ntensors);
  * Arguments are those of a8_fused_update_1d_multi minus table_dev / table_bytes:
  * the tensor table lives in a 64 KiB device array of the library, one per GPU,
  * held until the process ends, so at most a8_noalloc_max_tensors_1d() tensors
- * (528) fit; more returns A8_ERR_SIZE.  With `upload` non-zero the table is
- * written there (a stream-ordered copy from a host buffer of the library); with
- * upload == 0 the table of the previous call on this GPU is reused, so the
- * previous call must have had the same tensors.  Every call on a GPU shares that
- * GPU's array, which keeps the last call's table: calls that overlap on one GPU
- * (two streams, or two host threads) race. */
+ * (468) fit; more returns A8_ERR_SIZE.  With `upload` non-zero the table is
+ * written there (a stream-ordered copy from a host buffer of the library); this is
+ * refused (A8_ERR_ARG) on a stream that is being captured, since a replay would
+ * copy from that host buffer as it is at replay time.  With upload == 0 the table
+ * of the last upload on this GPU is reused; the call is refused (A8_ERR_ARG) unless
+ * it names the same tensors (every record field) and block sizes as that upload.
+ * So under capture: one eager call with upload != 0, then capture calls with
+ * upload == 0.  Every call on a GPU shares that GPU's array, which keeps the last
+ * upload's table: calls that overlap on one GPU (two streams, or two host threads)
+ * race.  NORM/LAG/MNORM need each record's norm_parts workspace, as in
+ * a8_fused_update_1d_multi (the caller's memory, like v_buf and norm_buf). */
 int a8_fused_update_1d_multi_noalloc(int mode, int stochastic, int dtype, const a8_tensor1d* tensors,
                                      int ntensors, double beta1, double beta_val, float eps_for_denom,
                                      int use_adam_denom, float log_floor, float eps_for_grad_sq, float eps_sq,
@@ -195,13 +209,15 @@ int a8_noalloc_max_tensors_1d(void);
  * called at optimizer.py:2147-2183): fp32 V (and optional fp32 M, NULL for none)
  * for tensors below min_8bit_size or with quantize=False.  NORM writes V (and M
  * unless momentum_only) and accumulates sum(u^2) into norm_buf; APPLY reads them.
+ * NORM/LAG/MNORM take norm_parts, a8_norm_parts_full(numel) doubles of workspace: one
+ * partial per workgroup, added in index order by a second launch (same bits run to run).
  * stochastic (16-bit params): p * decay - step * u rounded with the (sr_seed,
  * sr_step, element index) stream of kernels.cu:48-87.  v_ready: variance already
  * holds this step's second moment (e.g. the fp32 output of a8_log_quantize_lerp for
  * quantised V with fp32 M, optimizer.py:2078-2087): no EMA, variance not written. */
 int a8_fused_update_1d_full(int mode, int dtype, void* param, const void* grad, float* variance,
-                            float* m, float* norm_buf, const float* alpha, const float* prev_norm,
-                            const float* decay, double beta1, double beta_val, float eps_sq,
+                            float* m, float* norm_buf, double* norm_parts, const float* alpha,
+                            const float* prev_norm, const float* decay, double beta1, double beta_val, float eps_sq,
                             float eps_for_denom, int use_adam_denom, float eps_for_grad_sq,
                             int64_t numel, float d, int momentum_only, float alpha_val,
                             float decay_val, int has_decay, int stochastic, uint64_t sr_seed,
@@ -220,6 +236,7 @@ typedef struct a8_tensor_full {
   uint64_t sr_seed;        /* stochastic rounding seed (16-bit params) */
   float* psq;              /* sum of p^2 slot (zeroed by the caller) when scale_param, else null */
   const float* fira_scale; /* Fira scale multiplied into alpha by the update passes, or null */
+  double* norm_parts;      /* NORM/LAG/MNORM: a8_norm_parts_full(numel) doubles of workspace */
 } a8_tensor_full;
 
 /* Multi-tensor form of a8_fused_update_1d_full (one launch per group).  Beyond the
@@ -237,6 +254,7 @@ int a8_fused_update_1d_full_multi(int mode, int dtype, const a8_tensor_full* ten
                                   uint64_t sr_step, int scale_param, float eps2, int wd_mode, float wd,
                                   int v_ready, int upload, const void* step_scalars, void* stream);
 int64_t a8_table_bytes_full(int ntensors);
+int64_t a8_norm_parts_full(int64_t numel);
 
 /* Replaces fira_scalar (kernels.cu:3030-3084; used by _fira_scalar_cuda,
  * optimizer.py:735-757).  For i < n: norm = apply ? sqrt(x[i]) : x[i] (apply 0, 1, 2), zeroed when
@@ -528,7 +546,9 @@ int a8_al_encode(void* q, float* scale, float* min_log, const float* x, int64_t 
  * denom = max(1, sqrt(sum u^2) / (sqrt(numel) d)) for d > 0 and the Fira scale s
  * (1 without Fira); M is requantised from the fp32 m'.
  * mode 0: one pass, no clip, no Fira.  mode 1 (NORM): accumulates sum(u^2) into
- * *norm_buf (zeroed by the caller), writes nothing.  mode 2 (APPLY): reads
+ * *norm_buf (zeroed by the caller), writes nothing; it needs norm_parts,
+ * a8_norm_parts_sgd doubles of workspace (one partial per workgroup, added in
+ * index order by a second launch, so the sum has the same bits run to run).  mode 2 (APPLY): reads
  * *norm_buf, and fira = the 3-float output of a8_fira_scalar(norm_buf, prev, one,
  * apply=1) when Fira is on (else null); a non-finite norm then zeroes the update
  * (optimizer.py:797-800).  Momentum: m_q/m_scale (codes padded to whole
@@ -536,7 +556,7 @@ int a8_al_encode(void* q, float* scale, float* min_log, const float* x, int64_t 
  * multiple of 4 in [32, 65536]), or fp32 m, or neither.  stochastic: 16-bit params
  * written with the kernels.cu:48-87 stream. */
 int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* grad, uint8_t* m_q, float* m_scale,
-                float* m, float* norm_buf, const float* fira, const float* alpha, const float* decay, int64_t numel,
+                float* m, float* norm_buf, double* norm_parts, const float* fira, const float* alpha, const float* decay, int64_t numel,
                 double beta1, int m_bits, int m_mode, int m_block_size, float d, float alpha_val, float decay_val,
                 int has_decay, uint64_t sr_seed, uint64_t sr_step, void* stream);
 
@@ -552,6 +572,7 @@ typedef struct a8_tensor_sgd {
   const float* decay;
   int64_t numel;
   uint64_t sr_seed;
+  double* norm_parts;      /* NORM: a8_norm_parts_sgd(numel, ...) doubles of workspace */
 } a8_tensor_sgd;
 
 /* Multi-tensor form of a8_sgd_step: one launch per group.  m_kind: 0 none,
@@ -561,6 +582,9 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
                       int m_block_size, float d, float alpha_val, float decay_val, int has_decay, uint64_t sr_step,
                       int upload, void* stream);
 int64_t a8_table_bytes_sgd(int ntensors);
+/* Doubles of norm_parts workspace a NORM pass of the SGD step needs for one tensor
+ * (m_block_size: that of coded momentum, 0 without); -1 for an invalid block size. */
+int64_t a8_norm_parts_sgd(int64_t numel, int m_block_size);
 
 /* Replaces fused_m_quantize_lerp (kernels.cu:523-588; called by
  * _m_fused_quantize_lerp, optimizer.py:563-571) with the arithmetic of its twin

@@ -40,12 +40,12 @@ def test_argument_errors_without_gpu():
     from adafactor8bit import _native as nat
     L = nat.lib()
     rc = L.a8_fused_update_1d(0, 0, 0, None, None, None, None, None, None, None, None, None, None,
-                              None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 100,
+                              None, None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 100,
                               256, 8, 0, 0.0, 8, 0, 1e-4, 1.0, 0, None)
     assert rc == -3, rc  # block_size 100 rejected
     assert b"block_size" in L.a8_last_error()
     rc = L.a8_fused_update_1d(0, 0, 7, None, None, None, None, None, None, None, None, None, None,
-                              None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 2048,
+                              None, None, None, 0, 0, 0.9, 0.001, 1e-8, 1, -126.0, 0.0, 1e-16, 10, 2048,
                               256, 8, 0, 0.0, 8, 0, 1e-4, 1.0, 0, None)
     assert rc == -2, rc
 

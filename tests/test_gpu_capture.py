@@ -5,8 +5,10 @@ starts with a8_step_advance (count + 1, this step's scalars) and runs only
 multi-tensor kernels that read those scalars, so ``step()`` captured once in a
 graph replays as a real next step every time.  For the benchmark configurations
 (C1 AdamW UF8/AL8, C2 factored Adafactor with its fp32-state vectors, C3 CAME with
-Fira) and two more (weight decay with bias correction; bf16 with stochastic
-rounding):
+Fira) and four more (weight decay with bias correction; bf16 with stochastic
+rounding; a clipped, Fira-limited quantised AdamW group and an fp32-state
+Adafactor group with scale_parameter, clip and Fira, on tensors of hundreds of
+workgroups, whose sums of squares are fixed-order sums):
 
 * N graph replays leave parameters and every state tensor bit-identical to N
   eager steps of a second capturable optimizer on the same gradients, with eager
@@ -27,6 +29,8 @@ C3 = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True,
           scale_parameter=False, scale_weight_decay=False, d=1.0, eps_came=1e-16, lr=1e-4, block_size=2048,
           m_block_size=256, m_quant_type="uf8", v_quant_type="al16", c_quant_type="al16",
           enable_fira_for_adafactor=True, fira_margin=0.01)
+FP32S = dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=False, relative_step=False, scale_parameter=True,
+             d=1.0, quantize=False, enable_fira_for_adafactor=True, eps=(1e-30, 1e-3), lr=1e-3)
 
 CASES = [
     ("c1_adamw", ADAMW, [(300, 260), (2048,), (5000,), (64, 64)], torch.float32, "normal_zeros"),
@@ -36,6 +40,11 @@ CASES = [
      torch.float32, "student_t"),
     ("adamw_bf16_sr", dict(ADAMW, stochastic_round_writeback=True, lr=1e-3), [(300, 260), (1000,)], torch.bfloat16,
      "normal_zeros"),
+    # clipped / Fira / scale_parameter 1-D groups on tensors of hundreds of workgroups: their
+    # sums of squares are fixed-order sums, so eager and replayed steps agree bit for bit
+    ("adamw_clip_fira_q1d", dict(ADAMW, d=1.0, enable_fira_for_adafactor=True, lr=1e-3),
+     [(700, 1100), (300, 260), (5000,)], torch.float32, "logscale"),
+    ("adafactor1d_fp32_scale_clip_fira", FP32S, [(700, 1100), (2048,), (5000,)], torch.float32, "student_t"),
 ]
 
 

@@ -28,7 +28,7 @@ class StepSpec(ctypes.Structure):
     """Mirror of ``a8_step_spec``."""
     _fields_ = [("beta1", _c_d), ("beta2", _c_d), ("beta2_decay", _c_d), ("eps1", _c_d), ("lr", _c_d),
                 ("wd", _c_f), ("v_mode", _c_i), ("relative_step", _c_i), ("bias_mode", _c_i), ("adam_denom", _c_i),
-                ("wd_mode", _c_i), ("fact_bias_mode", _c_i)]
+                ("wd_mode", _c_i), ("fact_bias_mode", _c_i), ("apollo_bias_mode", _c_i), ("lr_dev", _c_vp)]
 
 
 STEP_SCALARS_BYTES = 40   # sizeof(a8_step_scalars)
@@ -87,7 +87,7 @@ class ApolloTensor(ctypes.Structure):
                 ("v_min_log", _c_vp), ("v_fp32", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp),
                 ("m_fp32", _c_vp), ("fira_prev", _c_vp), ("has_fira_prev", _c_i), ("lr", _c_vp),
                 ("workspace", _c_vp), ("sr_seed", _c_u64), ("first_step", _c_i), ("proj_fresh", _c_i),
-                ("step", _c_u64), ("bias_factor", _c_f)]
+                ("step", _c_u64), ("bias_factor", _c_f), ("proj_state", _c_vp), ("proj_gap", _c_i)]
 
 
 class ApolloXArgs(ctypes.Structure):
@@ -148,7 +148,9 @@ _SIGS = {
     "a8_apollo_workspace_floats": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i]),
     "a8_apollo_step_multi": (_c_i, [_c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_vp, _c_i64, _c_d, _c_d,
                                     _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_f, _c_i, _c_i,
-                                    _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_i, _c_vp]),
+                                    _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f, _c_i, _c_i, _c_vp, _c_vp]),
+    "a8_apollo_proj_gen": (_c_i, [_c_vp, _c_i64, _c_i64, _c_i64, _c_u64, _c_vp]),
+    "a8_apollo_next_seed": (_c_i, [_c_vp, _c_vp, _c_i64, _c_vp]),
     "a8_apollo_table_bytes": (_c_i64, [_c_i]),
     "a8_apollo_step_multi_phase": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_vp, _c_i64,
                                           _c_d, _c_d, _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
@@ -166,7 +168,7 @@ _SIGS = {
     "a8_sgd_step": (_c_i, [_c_i, _c_i, _c_i, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                            _c_vp, _c_i64, _c_d, _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_u64, _c_vp]),
     "a8_sgd_step_multi": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(TensorSgd), _c_i, _c_vp, _c_i64, _c_d, _c_i,
-                                 _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_i, _c_vp]),
+                                 _c_i, _c_i, _c_i, _c_f, _c_f, _c_f, _c_i, _c_u64, _c_i, _c_vp, _c_vp]),
     "a8_table_bytes_sgd": (_c_i64, [_c_i]),
     "a8_m_quantize_lerp": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i, _c_vp, _c_d, _c_i, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_log_quantize_lerp": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i, _c_vp, _c_d, _c_i, _c_i, _c_f, _c_i64, _c_f,

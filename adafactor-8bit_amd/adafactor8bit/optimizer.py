@@ -227,6 +227,7 @@ class Adafactor8Bit(Optimizer):
                 for p in ent["group"]["params"]:
                     if p in self.state and "step" in self.state[p]:
                         self.state[p]["step"] = t
+        _sync_apollo_schedule(self)
         sd = super().state_dict()
         sd["_apollo_seed_counter"] = self._apollo_seed_counter
         sd["_sr_seed_counter"] = self._sr_seed_counter
@@ -326,6 +327,10 @@ class Adafactor8Bit(Optimizer):
 
     def _launch_group(self, group, params, grads, states, dsc=None):
         apollo_rank = group.get("apollo_rank", 0)
+        if dsc is not None and isinstance(group["lr"], Tensor):
+            # the kernels read this step's lr from the device block: plan with a
+            # placeholder so no host scalar is formed from the tensor
+            group = dict(group, lr=1.0)
         batches: Dict[tuple, list] = {}
         ap_batches: Dict[tuple, list] = {}
         copy_back = []
@@ -342,9 +347,7 @@ class Adafactor8Bit(Optimizer):
                 copy_back.append((p, work))
                 p = work
             if apollo_rank > 0 and "apollo_seed" in st:
-                if dsc is not None:
-                    raise NotImplementedError("adafactor8bit: capturable=True does not cover APOLLO parameters")
-                bkey, rec, fin = _apollo_prep(self, p, g, st, group)
+                bkey, rec, fin = _apollo_prep(self, p, g, st, group, dsc)
                 ap_batches.setdefault(bkey, []).append((rec, fin))
                 continue
             plan = _plan_param(p, g, st, group)
@@ -365,7 +368,7 @@ class Adafactor8Bit(Optimizer):
         for key, plans in batches.items():
             _run_batch(self, key, plans)
         for bkey, items in ap_batches.items():
-            _run_apollo_batch(self, group, bkey, items)
+            _run_apollo_batch(self, group, bkey, items, dsc)
         for p, work in copy_back:
             p.copy_(work)
 
@@ -383,8 +386,10 @@ def _step_spec(group):
     """The group's a8_step_spec: the host planner's scalar rules (_plan_param,
     _plan_factored; optimizer.py:2012-2039, 832-856) as data."""
     beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
-    if isinstance(group["lr"], Tensor):
-        raise NotImplementedError("adafactor8bit: capturable=True needs a float learning rate")
+    lr, lr_dev = group["lr"], None
+    if isinstance(lr, Tensor):
+        lr_dev = _device_lr(lr, group)
+        lr = 0.0
     sgd = beta2 is None and beta2_decay is None
     eps1 = group["eps"][0]
     eps1 = 1e-30 if eps1 is None else eps1
@@ -396,10 +401,28 @@ def _step_spec(group):
             bias_mode = 1 if beta2 is not None else 2
     wd = group["weight_decay"]
     wd_mode = 0 if wd == 0 else (1 if group.get("scale_weight_decay", True) else 2)
+    # APOLLO's bias correction is on unless bias_correction=False (optimizer.py:3015-3023)
+    ap_bias = 0
+    if beta1 is not None and not group["relative_step"]:
+        bc = group.get("bias_correction")
+        if bc is None or bool(bc):
+            ap_bias = 1 if beta2 is not None else 2
     return nat.StepSpec(beta1 if beta1 is not None else 0.0, beta2 if beta2 is not None else 0.0,
-                        beta2_decay if beta2_decay is not None else 0.0, eps1, float(group["lr"]), _f32(wd),
+                        beta2_decay if beta2_decay is not None else 0.0, eps1, float(lr), _f32(wd),
                         0 if sgd else (1 if beta2 is not None else 2), int(bool(group["relative_step"])), bias_mode,
-                        int(adam_denom), wd_mode, bias_mode)
+                        int(adam_denom), wd_mode, bias_mode, ap_bias, lr_dev)
+
+
+def _device_lr(lr, group):
+    """A tensor learning rate of a capturable group: read on the device at every step
+    (a scheduler that fill_()s it changes the lr of graph replays too)."""
+    p0 = group["params"][0]
+    if not (lr.numel() == 1 and lr.dtype == torch.float32 and lr.device == p0.device):
+        raise NotImplementedError("adafactor8bit: capturable=True takes a float learning rate or a one-element "
+                                  "float32 tensor on the parameters' device")
+    if group["relative_step"]:
+        raise NotImplementedError("adafactor8bit: capturable=True with relative_step needs a float learning rate")
+    return lr.data_ptr()
 
 
 def _advance_device_step(opt, group, params, states):
@@ -1349,14 +1372,12 @@ def _run_batch(opt, key, plans):
     strm = nat.stream_of(dev)
     _no_upload_in_capture(upload)
     if path == "sgd":
-        if P0.dsc is not None:
-            raise NotImplementedError("adafactor8bit: capturable=True does not cover the SGD path")
         kind = 0 if not P0.has_m else (1 if key[7] else 2)
         rc = L.a8_sgd_step_multi(
             nat.MODE_NOCLIP, nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), nbytes,
             P0.beta1 if P0.has_m else 0.0, kind, S.m_bits(P0.mqt) if kind == 1 else 0,
             S.m_mode(P0.mqt) if kind == 1 else 0, P0.mbs if kind == 1 else 32, P0.d, float(P0.alpha_val),
-            float(dec_val), has_dec, int(P0.step), upload, strm)
+            float(dec_val), has_dec, int(P0.step), upload, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_sgd_step_multi")
         if upload:
             ent[3] = [tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)) for pl in plans]
@@ -1409,12 +1430,54 @@ def _apollo_proj(st, shape, step, device, cache):
     return proj_T, True
 
 
-def _apollo_prep(opt, p, grad, st, group):
+def _apollo_proj_device(opt, st, shape, step, device, group):
+    """P^T of a capturable step.  It lives in a persistent buffer, and the projection
+    schedule -- the refresh decision, the reference's seed chain (next_seed) and the
+    generation of a new P -- runs on the device (a8_apollo_step_multi with
+    step_scalars), so replayed steps refresh the projection as eager ones do.  The
+    first such step of a matrix (eager) takes P^T from the host schedule
+    (_get_apollo_proj_matrix, optimizer.py:2557-2584) and hands the schedule over:
+    refreshes after that draw P with the device generator (a8_apollo_proj_gen), in
+    place of stable_randn's torch generator, which is seeded on the host."""
+    key = (device, "apollo_pdev", id(st))
+    ent = opt._ws.get(key)
+    if ent is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("adafactor8bit: run one eager step of a capturable APOLLO group before capturing")
+        cache = group.get("apollo_cache_proj", False)
+        proj_T, _ = _apollo_proj(st, shape, step, device, cache)
+        gap = int(st["apollo_update_proj_gap"])
+        if gap <= 0:
+            raise NotImplementedError("adafactor8bit: capturable APOLLO needs apollo_update_proj_gap > 0")
+        pt = proj_T.detach().to(torch.float32).contiguous().clone()
+        seed = int(st["apollo_seed"])
+        # {last_proj_step, apollo_seed, current_proj_seed, fresh = 2: split P^T as given}
+        ps = torch.tensor([int(st.get("last_proj_step", -gap)), seed, int(st.get("current_proj_seed", seed)), 2],
+                          dtype=torch.int64, device=device)
+        ent = {"pt": pt, "ps": ps, "st": st}
+        opt._ws[key] = ent
+        if cache:
+            st["apollo_proj_matrix_T"] = pt
+    return ent["pt"], ent["ps"]
+
+
+def _sync_apollo_schedule(opt):
+    """Copy the device projection schedules of capturable APOLLO matrices back to
+    their state (last_proj_step, apollo_seed, current_proj_seed)."""
+    for key, ent in list(opt._ws.items()):
+        if isinstance(key, tuple) and len(key) == 3 and key[1] == "apollo_pdev":
+            last, seed, cur, _ = (int(x) for x in ent["ps"].tolist())
+            st = ent["st"]
+            st["last_proj_step"], st["apollo_seed"], st["current_proj_seed"] = last, seed, cur
+
+
+def _apollo_prep(opt, p, grad, st, group, dsc=None):
     """Host side of one APOLLO parameter's step (optimizer.py:2587-3084): step
     counter, projection refresh, lazy low-rank state, per-step scalars.  Returns
     (batch key, tensor record, finish) for the grouped launch.  The factorised
     and CAME variants carry an a8_apollo_x_args record for the low-rank stage
-    between the projection and finish phases."""
+    between the projection and finish phases.  With ``dsc`` (capturable groups)
+    the per-step scalars and the projection schedule come from the device."""
     beta1, beta2, beta2_decay = group.get("beta1"), group["beta2"], group["beta2_decay"]
     factorize = bool(group.get("apollo_factorize", False))
     came = group.get("beta3") is not None
@@ -1458,8 +1521,14 @@ def _apollo_prep(opt, p, grad, st, group):
         rho_val = 0.0
     else:
         rho_val = _f32(min(lr, 1.0 / math.sqrt(step)) if group["relative_step"] else lr)
-    proj_T, fresh = _apollo_proj(st, (R, C), step, dev, group.get("apollo_cache_proj", False))
     right = R >= C
+    pstate = None
+    if dsc is not None:
+        _apollo_capturable_check(p, group, factorize, came)
+        proj_T, pstate = _apollo_proj_device(opt, st, (R, C), step, dev, group)
+        fresh = False
+    else:
+        proj_T, fresh = _apollo_proj(st, (R, C), step, dev, group.get("apollo_cache_proj", False))
     n_low = R * rank if right else rank * C
     quant = st.get("is_quantized", False)
     bs = st.get("block_size", group.get("block_size", 2048))
@@ -1475,6 +1544,9 @@ def _apollo_prep(opt, p, grad, st, group):
     # run the plain stage of a8_apollo_lowrank_x
     xmode = bool(factorize or came or (vbits and not _pow2_in(bs, 128, 2048))) or \
         (has_m and not m_fp32 and not _pow2_in(mbs, 32, 2048))
+    if dsc is not None and xmode:
+        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO with power-of-two block sizes "
+                                  "(V 128..2048, momentum 32..2048); this matrix needs the host-scalar low-rank stage")
     low_shape = (R, rank) if right else (rank, C)
     if factorize:   # optimizer.py:2693-2699 creates the row / column EMAs on the first step
         if first:
@@ -1516,7 +1588,7 @@ def _apollo_prep(opt, p, grad, st, group):
     if ent is None or ent["ws"].numel() < nws:
         ent = {"ws": torch.empty(nws, dtype=torch.float32, device=dev), "proj": None}
         opt._ws[key] = ent
-    if ent["proj"] is None or ent["proj"] != (proj_T.data_ptr(), proj_T._version):
+    if dsc is None and (ent["proj"] is None or ent["proj"] != (proj_T.data_ptr(), proj_T._version)):
         fresh = True
     ent["proj"] = (proj_T.data_ptr(), proj_T._version)
     sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype in (torch.bfloat16, torch.float16)
@@ -1534,6 +1606,12 @@ def _apollo_prep(opt, p, grad, st, group):
         bkey = (p.dtype, sr, "x", has_m, True, mqt, 0, 0, float(beta_val), float(rho_val), bias_mode)
         keep = (g, proj_T, rho_t, xkeep)
         return bkey, t, (st, "x", bs, keep, xargs)
+    if dsc is not None:
+        # the device block supplies step, bias factor, V weight and lr: the record
+        # (and so the uploaded table) stays the same from step to step
+        step_rec, bias_rec, beta_key, rho_key = 0, 0.0, 0.0, 0.0
+    else:
+        step_rec, bias_rec, beta_key, rho_key = int(step), float(bias_fac), float(beta_val), float(rho_val)
     t = nat.ApolloTensor(
         p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank,
         nat.ptr(st.get("v_low_q")) if vbits else None, nat.ptr(st.get("v_low_scale")) if vbits else None,
@@ -1543,10 +1621,23 @@ def _apollo_prep(opt, p, grad, st, group):
         st["m_low"].data_ptr() if m_fp32 else None,
         nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
         nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)),
-        int(first), int(fresh), int(step), float(bias_fac))
-    bkey = (p.dtype, sr, vbits, has_m, m_fp32, mqt, int(mbs), int(bs), float(beta_val), float(rho_val), bias_mode)
-    keep = (g, proj_T, rho_t)   # alive until the launch is queued
+        int(first), int(fresh), step_rec, bias_rec, nat.ptr(pstate),
+        int(st["apollo_update_proj_gap"]) if pstate is not None else 0)
+    bkey = (p.dtype, sr, vbits, has_m, m_fp32, mqt, int(mbs), int(bs), beta_key, rho_key, bias_mode)
+    keep = (g, proj_T, rho_t, pstate)   # alive until the launch is queued
     return bkey, t, (st, vbits, bs, keep, None)
+
+
+def _apollo_capturable_check(p, group, factorize, came):
+    """What a capturable APOLLO step covers: bf16 parameters (the projection is the
+    MFMA kernel), the plain low-rank stage, no maximize (a negated gradient copy)."""
+    if p.dtype != torch.bfloat16:
+        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO on bf16 parameters")
+    if factorize or came:
+        raise NotImplementedError("adafactor8bit: capturable=True does not cover the factorised or CAME APOLLO "
+                                  "stages (apollo_factorize, beta3)")
+    if group["maximize"]:
+        raise NotImplementedError("adafactor8bit: capturable=True does not cover APOLLO with maximize=True")
 
 
 def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, first, vbits, vqt, bs, has_m,
@@ -1622,20 +1713,29 @@ def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, f
     return a, (xws, cbits)
 
 
-def _run_apollo_batch(opt, group, bkey, items):
+def _run_apollo_batch(opt, group, bkey, items, dsc=None):
     """One a8_apollo_step_multi launch sequence for the APOLLO matrices of a group
-    that share dtype, state formats and step scalars."""
+    that share dtype, state formats and step scalars.  With ``dsc`` (capturable)
+    the table is uploaded only when its records change, and never under capture."""
     pdt, sr, vbits, has_m, m_fp32, mqt, mbs, bs, beta_val, rho_val, bias_mode = bkey
     n = len(items)
     arr = (nat.ApolloTensor * n)(*[t for t, _ in items])
     L = nat.lib()
     pdev = items[0][1][3][0].device   # the first record's gradient
-    tkey = (pdev, "ap_table")
+    tkey = (pdev, "ap_table", id(group), bkey) if dsc is not None else (pdev, "ap_table")
     need = int(L.a8_apollo_table_bytes(n))
     tab = opt._ws.get(tkey)
     if tab is None or tab.numel() < need:
         tab = torch.empty(max(need, 4096), dtype=torch.uint8, device=pdev)
         opt._ws[tkey] = tab
+    upload = 1
+    if dsc is not None:
+        blob = bytes(arr)
+        bk = (pdev, "ap_table_blob", id(group), bkey)
+        if n > 1 and opt._ws.get(bk) == blob:
+            upload = 0
+        _no_upload_in_capture(upload if n > 1 else 0)
+        opt._ws[bk] = blob
     beta1 = group.get("beta1")
     aeps = group.get("apollo_eps", 1e-6)
     eps_sq = max(aeps * aeps, _LOG_QUANT_FLOOR)
@@ -1671,10 +1771,13 @@ def _run_apollo_batch(opt, group, bkey, items):
                 _block_view(st, "conf_row_low", bsz)
                 _block_view(st, "conf_col_low", bsz)
         return
+    if dsc is not None:
+        beta_val, tail = 0.0, tail[:6] + (0.0,) + tail[7:]   # from the device block
     rc = L.a8_apollo_step_multi(
         nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
         float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), vbits, int(bs),
-        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs), *tail)
+        S.m_bits(mqt) if has_m else 8, S.m_mode(mqt) if has_m else 0, int(m_fp32), int(mbs), *tail[:-1], upload,
+        nat.ptr(dsc), tail[-1])
     nat.check(rc, "a8_apollo_step_multi")
     if vbits:
         for _, (st, vb, bsz, _keep, _x) in items:

@@ -102,7 +102,8 @@ struct ApDesc {
   uint64_t sr_seed, step;
   float bias_factor;
   int32_t first, has_prev, valign;
-  int32_t rtile_begin, ltile_begin, unit_begin, sc_begin, app_begin, pad_;
+  int32_t rtile_begin, ltile_begin, unit_begin, sc_begin, app_begin, gap;
+  int64_t* pstate;   // device projection schedule {last_proj_step, seed, current seed, fresh}, or null
 };
 static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
 
@@ -110,6 +111,7 @@ struct ApHyp {
   float bv, w_m, aeps, log_floor, lr_val, eps2, wd, d, margin, sv;
   int lbv, lbm, mk, channel, front, fira, scale_param, bias_mode, wd_mode;
   int rowsum;   // k_ap_low leaves row sums for k_ap_scale where ap_rowsum holds (the plain step)
+  const a8_step_scalars* dsc;   // if set: the V lerp weight, rho, bias factor and SR step of this step
 };
 
 // A right-side matrix whose low-rank rows (r elements, a power of two in [8, 512])
@@ -230,36 +232,169 @@ __device__ __forceinline__ int64_t psw_unit(int64_t t, int64_t blk, int64_t kc, 
   return (((t * nblk + blk) * nkc + kc) * 2 + j) * 64 + l;
 }
 
+// One 16-byte unit u of the split (three terms), from P^T values pv(row, k).
+template <typename PV>
+__device__ __forceinline__ void split_unit(int64_t u, int64_t nblk, int64_t nkc, int64_t r, int64_t K,
+                                           PV pv, u32x4* __restrict__ out) {
+  const int l = (int)(u & 63), j = (int)((u >> 6) & 1);
+  const int64_t c = u >> 7, kc = c % nkc, blk = c / nkc;
+  const int64_t row = 32 * blk + (l & 31), k0 = 32 * kc + 16 * (l >> 5) + 8 * j;
+  uint32_t w[3][4] = {};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t k = k0 + e;
+    const float x = (row < r && k < K) ? pv(row, k) : 0.0f;
+    const __hip_bfloat16 h = __float2bfloat16(x);
+    const float r1 = x - __bfloat162float(h);
+    const __hip_bfloat16 m = __float2bfloat16(r1);
+    const __hip_bfloat16 lo = __float2bfloat16(r1 - __bfloat162float(m));
+    uint16_t bh, bm, bl;
+    __builtin_memcpy(&bh, &h, 2);
+    __builtin_memcpy(&bm, &m, 2);
+    __builtin_memcpy(&bl, &lo, 2);
+    w[0][e >> 1] |= (uint32_t)bh << (16 * (e & 1));
+    w[1][e >> 1] |= (uint32_t)bm << (16 * (e & 1));
+    w[2][e >> 1] |= (uint32_t)bl << (16 * (e & 1));
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    gp(out)[psw_unit(t, blk, kc, j, l, nblk, nkc)] = u32x4{w[t][0], w[t][1], w[t][2], w[t][3]};
+}
+
 __global__ __launch_bounds__(256) void k_ap_split(const float* __restrict__ pt, int64_t r, int64_t K, int right,
                                                  int64_t rp, int64_t Kp, u32x4* __restrict__ out) {
   const int64_t nblk = rp / 32, nkc = Kp / 32;
   const int64_t nu = nblk * nkc * 128;   // units per term
-  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < nu; u += (int64_t)gridDim.x * 256) {
-    const int l = (int)(u & 63), j = (int)((u >> 6) & 1);
-    const int64_t c = u >> 7, kc = c % nkc, blk = c / nkc;
-    const int64_t row = 32 * blk + (l & 31), k0 = 32 * kc + 16 * (l >> 5) + 8 * j;
-    uint32_t w[3][4] = {};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t k = k0 + e;
-      float x = 0.0f;
-      if (row < r && k < K) x = right ? gp(pt)[k * r + row] : gp(pt)[row * K + k];
-      const __hip_bfloat16 h = __float2bfloat16(x);
-      const float r1 = x - __bfloat162float(h);
-      const __hip_bfloat16 m = __float2bfloat16(r1);
-      const __hip_bfloat16 lo = __float2bfloat16(r1 - __bfloat162float(m));
-      uint16_t bh, bm, bl;
-      __builtin_memcpy(&bh, &h, 2);
-      __builtin_memcpy(&bm, &m, 2);
-      __builtin_memcpy(&bl, &lo, 2);
-      w[0][e >> 1] |= (uint32_t)bh << (16 * (e & 1));
-      w[1][e >> 1] |= (uint32_t)bm << (16 * (e & 1));
-      w[2][e >> 1] |= (uint32_t)bl << (16 * (e & 1));
-    }
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-      gp(out)[psw_unit(t, blk, kc, j, l, nblk, nkc)] = u32x4{w[t][0], w[t][1], w[t][2], w[t][3]};
+  auto pv = [&](int64_t row, int64_t k) { return right ? gp(pt)[k * r + row] : gp(pt)[row * K + k]; };
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < nu; u += (int64_t)gridDim.x * 256)
+    split_unit(u, nblk, nkc, r, K, pv, out);
+}
+
+// ------------------------------------------------------------ device projection schedule
+// Capturable steps decide the projection refresh on the device (the host's
+// _get_apollo_proj_matrix, optimizer.py:2557-2584), so the seed chain and the
+// generator run there too.
+//
+// next_seed (optimizer.py:152-155) is the last of 15 torch.randint(0, 2^63 - 1)
+// draws from a CPU generator seeded with the seed.  That generator is MT19937
+// (Matsumoto and Nishimura, 1998) initialised from the seed's low 32 bits; a 64-bit
+// draw joins two consecutive 32-bit outputs, the first as the high word, and is
+// reduced modulo 2^63 - 1.  The 15th draw is outputs 28 and 29.  Output i (< 227)
+// is the tempered word mt'[i] = mt[i + 397] ^ twist(mt[i], mt[i + 1]) of the first
+// regeneration, which reads initial words only: the initialisation runs to word 426.
+__device__ __forceinline__ uint32_t mt_twist_word(uint32_t a, uint32_t b, uint32_t c) {
+  const uint32_t y = (a & 0x80000000u) | (b & 0x7FFFFFFFu);
+  return c ^ (y >> 1) ^ ((y & 1u) ? 0x9908B0DFu : 0u);
+}
+__device__ __forceinline__ uint32_t mt_temper(uint32_t y) {
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9D2C5680u;
+  y ^= (y << 15) & 0xEFC60000u;
+  y ^= y >> 18;
+  return y;
+}
+__device__ uint64_t mt_next_seed(uint64_t seed) {
+  uint32_t x = (uint32_t)seed;
+  uint32_t w28 = 0, w29 = 0, w30 = 0, w425 = 0, w426 = 0;
+  for (uint32_t j = 1; j <= 426; ++j) {
+    x = 1812433253u * (x ^ (x >> 30)) + j;
+    if (j == 28) w28 = x;
+    else if (j == 29) w29 = x;
+    else if (j == 30) w30 = x;
+    else if (j == 425) w425 = x;
+    else if (j == 426) w426 = x;
   }
+  const uint32_t hi = mt_temper(mt_twist_word(w28, w29, w425));
+  const uint32_t lo = mt_temper(mt_twist_word(w29, w30, w426));
+  return (((uint64_t)hi << 32) | lo) % 0x7FFFFFFFFFFFFFFFull;
+}
+
+// The generator: P's element k (row-major) is z / sqrt(r) with z the Box-Muller
+// transform (Box and Muller, 1958) of two uniforms from SplitMix64 (Steele, Lea
+// and Flood, 2014) seeded with the projection seed, outputs 2k + 1 and 2k + 2.
+__device__ __forceinline__ uint64_t sm64_out(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + i * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ float proj_value(uint64_t seed, uint64_t k, float rsq) {
+  const uint64_t a = sm64_out(seed, 2 * k + 1), b = sm64_out(seed, 2 * k + 2);
+  const double u1 = (double)((a >> 11) + 1) * 0x1.0p-53;
+  const double u2 = (double)(b >> 11) * 0x1.0p-53;
+  const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+  return (float)z / rsq;
+}
+
+// One lane per matrix: t - last_proj_step >= gap starts a new projection.
+__global__ __launch_bounds__(64) void k_ap_decide(ApDesc one, const ApDesc* tab, int ntab,
+                                                  const a8_step_scalars* dsc) {
+  const int i = (int)(blockIdx.x * 64 + threadIdx.x);
+  if (i >= (tab ? ntab : 1)) return;
+  const ApDesc D = tab ? tab[i] : one;
+  if (!D.pstate) return;
+  int64_t* ps = D.pstate;
+  const int64_t t = (int64_t)load_step_scalars(dsc).step;
+  if (t - gp(ps)[0] >= (int64_t)D.gap) {
+    const uint64_t cur = (uint64_t)gp(ps)[1];
+    gp(ps)[2] = (int64_t)cur;
+    gp(ps)[1] = (int64_t)mt_next_seed(cur);
+    gp(ps)[0] = t;
+    gp(ps)[3] = 1;
+  }
+}
+
+// kPGen workgroups per matrix: with fresh == 1 they generate P^T from the current
+// seed (written to proj_t) and its split; with 2, the split of proj_t as given;
+// with 0 (no refresh this step) they exit.  k_ap_scalars clears fresh.
+constexpr int kPGen = 32;
+__global__ __launch_bounds__(256) void k_ap_pgen(ApDesc one, const ApDesc* tab, int ntab) {
+  const int i = (int)blockIdx.x / kPGen, slot = (int)blockIdx.x % kPGen;
+  const ApDesc D = tab ? tab[i] : one;
+  if (!D.pstate) return;
+  const int64_t fresh = gp(D.pstate)[3];
+  if (fresh == 0) return;
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const bool right = D.R >= D.C;
+  const int64_t r = D.r, K = L.K, nblk = L.rp / 32, nkc = L.Kp / 32, nu = nblk * nkc * 128;
+  u32x4* out = reinterpret_cast<u32x4*>(D.ws + L.psplit);
+  float* pt = const_cast<float*>(D.proj_t);
+  const uint64_t seed = (uint64_t)gp(D.pstate)[2];
+  const float rsq = (float)sqrt((double)r);
+  for (int64_t u = (int64_t)slot * 256 + threadIdx.x; u < nu; u += (int64_t)kPGen * 256) {
+    if (fresh == 1) {
+      auto pv = [&](int64_t row, int64_t k) {
+        // right: P is r x C, element (row, k); left: P is R x r, element (k, row)
+        const float v = proj_value(seed, right ? (uint64_t)(row * K + k) : (uint64_t)(k * r + row), rsq);
+        gp(pt)[right ? k * r + row : row * K + k] = v;
+        return v;
+      };
+      split_unit(u, nblk, nkc, r, K, pv, out);
+    } else {
+      auto pv = [&](int64_t row, int64_t k) { return right ? gp(pt)[k * r + row] : gp(pt)[row * K + k]; };
+      split_unit(u, nblk, nkc, r, K, pv, out);
+    }
+  }
+}
+
+// a8_apollo_proj_gen: P^T of one matrix with the generator above.
+__global__ __launch_bounds__(256) void k_proj_gen(float* __restrict__ pt, int64_t R, int64_t C, int64_t r,
+                                                 uint64_t seed) {
+  const bool right = R >= C;
+  const int64_t K = right ? C : R, n = r * K;
+  const float rsq = (float)sqrt((double)r);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    // e runs over P^T row-major: right [K x r] (k, row), left [r x K] (row, k)
+    const int64_t a = e / (right ? r : K), b = e - a * (right ? r : K);
+    const int64_t row = right ? b : a, k = right ? a : b;
+    gp(pt)[e] = proj_value(seed, right ? (uint64_t)(row * K + k) : (uint64_t)(k * r + row), rsq);
+  }
+}
+
+__global__ __launch_bounds__(64) void k_next_seed(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
+                                                  int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (i < n) gp(out)[i] = mt_next_seed(gp(in)[i]);
 }
 
 // ------------------------------------------------------------ MFMA projection (bf16)
@@ -993,8 +1128,10 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
   int unit;
   const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, unit);
   const ApL L = ap_layout(D.R, D.C, D.r);
-  if ((int64_t)(unit + 1) * kApUnit <= L.n_low && (L.u & 3) == 0) ap_low_unit<VB, MK, true>(D, L, unit, h, xw, dtab);
-  else ap_low_unit<VB, MK, false>(D, L, unit, h, xw, dtab);
+  ApHyp hh = h;
+  if (hh.dsc) hh.bv = (float)load_step_scalars(hh.dsc).beta_val;
+  if ((int64_t)(unit + 1) * kApUnit <= L.n_low && (L.u & 3) == 0) ap_low_unit<VB, MK, true>(D, L, unit, hh, xw, dtab);
+  else ap_low_unit<VB, MK, false>(D, L, unit, hh, xw, dtab);
 }
 
 // ------------------------------------------------------------ scale
@@ -1118,8 +1255,15 @@ __global__ __launch_bounds__(256) void k_ap_scalars(ApDesc one, const ApDesc* ta
   s1 = ap_wg_sum(s1, sd);
   s2 = ap_wg_sum(s2, sd);
   if (lane != 0) return;
+  if (D.pstate) gp(D.pstate)[3] = 0;   // this step's projection refresh (if any) is done
+  float lr_val = h.lr_val, bias_factor = D.bias_factor;
+  if (h.dsc) {
+    const a8_step_scalars sc = load_step_scalars(h.dsc);
+    lr_val = sc.rho;
+    bias_factor = sc.apollo_bias;
+  }
   const int64_t numel = D.R * D.C;
-  const float rho = D.lr ? *gp(D.lr) : h.lr_val;
+  const float rho = D.lr ? *gp(D.lr) : lr_val;
   float alpha = rho;
   if (h.scale_param) {
     const float rms = sqrtf((float)pp) / (float)sqrt((double)numel);
@@ -1151,8 +1295,8 @@ __global__ __launch_bounds__(256) void k_ap_scalars(ApDesc one, const ApDesc* ta
   float denom = 1.0f;
   if (h.d > 0.0f) denom = fmaxf(nun / (float)(sqrt((double)numel) * (double)h.d), 1.0f);
   float step = -alpha / denom;
-  if (h.bias_mode == 1) step = step * D.bias_factor;
-  else if (h.bias_mode == 2) step = step / D.bias_factor;
+  if (h.bias_mode == 1) step = step * bias_factor;
+  else if (h.bias_mode == 2) step = step / bias_factor;
   float dec = 1.0f;
   if (h.wd_mode == 1) dec = 1.0f - alpha * h.wd;
   else if (h.wd_mode == 2) dec = 1.0f - rho * h.wd;
@@ -1205,6 +1349,7 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
   // issued before the first is computed (a wave keeps several kilobytes in flight)
   const uint32_t ea = (uint32_t)unit * kApApp + threadIdx.x * 8u;
   if (ea >= n) return;
+  const uint64_t sr_step = SR && h.dsc ? load_step_scalars(h.dsc).step : D.step;
   float gr[kApRuns][8];
   pval_t<T> pr[kApRuns][8];   // double for fp64 parameters
 #pragma unroll
@@ -1244,7 +1389,7 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
       // first: unless the eight counters cross a multiple of 2^30 (a lane in 1.5e8),
       // they share their bits from 30 up, hence the high word's share of the first
       // product and the low word of z >> 30.
-      const uint64_t zb = sr_base(D.sr_seed, D.step) + 0x9E3779B97F4A7C15ULL + (uint64_t)e0;
+      const uint64_t zb = sr_base(D.sr_seed, sr_step) + 0x9E3779B97F4A7C15ULL + (uint64_t)e0;
       const uint32_t zl = (uint32_t)zb, zh = (uint32_t)(zb >> 32);
       uint32_t hv[8];
       if ((zl & 0x3FFFFFFFu) <= 0x3FFFFFF8u) {   // the eight agree from bit 30 up
@@ -1382,9 +1527,11 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
                       int v_bits, int block_size, int m_bits, int m_mode, int m_fp32, int m_block_size, int channel,
                       float apollo_scale, int scale_front, int fira, float fira_margin, float d, float lr_val,
                       float eps2, int scale_parameter, int bias_mode, float weight_decay, int wd_mode,
-                      void* stream) {
+                      int upload, const a8_step_scalars* dsc, void* stream) {
   if (n <= 0) return 0;
   if (!ts) return set_error(A8_ERR_ARG, "null tensor list");
+  if (dsc && dtype != A8_BF16)
+    return set_error(A8_ERR_DTYPE, "APOLLO with step_scalars (device-scheduled projection) needs bf16 params");
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
     return set_error(A8_ERR_DTYPE, "APOLLO supports fp32, bf16, fp16 and fp64 params");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
@@ -1411,6 +1558,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     if (phase == 0 && has_m && (m_fp32 ? !t.m_fp32 : !(t.m_q && t.m_scale)))
       return set_error(A8_ERR_ARG, "APOLLO M state missing");
     if (fira && !t.fira_prev) return set_error(A8_ERR_ARG, "APOLLO Fira needs scaled_grad_norm_prev");
+    if (dsc && (!t.proj_state || t.proj_gap <= 0))
+      return set_error(A8_ERR_ARG, "APOLLO with step_scalars needs each record's proj_state and proj_gap > 0");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.workspace))
       return set_error(A8_ERR_ALIGN, "APOLLO param, grad and workspace must be 16-byte aligned");
     const ApL L = ap_layout(t.rows, t.cols, t.rank);
@@ -1420,11 +1569,12 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
     D.fira_prev = t.fira_prev; D.lr = t.lr;
     D.R = t.rows; D.C = t.cols; D.r = t.rank;
-    D.sr_seed = t.sr_seed; D.step = t.step; D.bias_factor = t.bias_factor;
+    D.sr_seed = t.sr_seed; D.step = dsc ? 0 : t.step; D.bias_factor = dsc ? 0.0f : t.bias_factor;
     D.first = t.first_step ? 1 : 0; D.has_prev = t.has_fira_prev ? 1 : 0;
+    D.pstate = dsc ? t.proj_state : nullptr; D.gap = dsc ? t.proj_gap : 0;
     D.valign = (t.cols % 8) == 0 ? 1 : 0;   // a k_ap_apply unit (8 elements) stays in one row
     D.rtile_begin = (int32_t)nrt; D.ltile_begin = (int32_t)nlt; D.unit_begin = (int32_t)nunit;
-    D.sc_begin = (int32_t)nsc; D.app_begin = (int32_t)napp; D.pad_ = 0;
+    D.sc_begin = (int32_t)nsc; D.app_begin = (int32_t)napp;
     first[(size_t)i] = D.rtile_begin;
     first[(size_t)n + i] = D.ltile_begin;
     first[(size_t)2 * n + i] = D.unit_begin;
@@ -1438,11 +1588,13 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   hipStream_t st = (hipStream_t)stream;
   const ApDesc* dtab = nullptr;
   if (n > 1) {
-    std::vector<char> blob((size_t)table_bytes(n));
-    std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
-    std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 5 * (size_t)n);
-    if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
-      return set_error(A8_ERR_HIP, "table upload failed");
+    if (upload) {
+      std::vector<char> blob((size_t)table_bytes(n));
+      std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
+      std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 5 * (size_t)n);
+      if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
+        return set_error(A8_ERR_HIP, "table upload failed");
+    }
     dtab = reinterpret_cast<const ApDesc*>(table_dev);
   }
   const ApDesc& one = tab[0];
@@ -1460,12 +1612,19 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   // phase 2 finishes a low-rank stage that wrote u itself, phase 3 one that left
   // the row sums (a8_apollo_x_args.u_rowsums) where ap_rowsum holds
   h.rowsum = (phase == 0 || phase == 3) ? 1 : 0;
+  h.dsc = dsc;
   int rc;
   // projection (+ channel norms of G)
   if (phase >= 2) {
     // the projection ran in phase 1
   } else if (dtype == A8_BF16) {
-    for (int i = 0; i < n; ++i) {
+    if (dsc) {   // the projection schedule on the device: refresh decision, then P^T and its split
+      hipLaunchKernelGGL(k_ap_decide, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, st, one, dtab, n, dsc);
+      if ((rc = check_launch("k_ap_decide"))) return rc;
+      hipLaunchKernelGGL(k_ap_pgen, dim3((unsigned)(n * kPGen)), dim3(256), 0, st, one, dtab, n);
+      if ((rc = check_launch("k_ap_pgen"))) return rc;
+    }
+    for (int i = 0; i < n && !dsc; ++i) {
       if (!ts[i].proj_fresh) continue;
       const ApDesc& D = tab[(size_t)i];
       const ApL L = ap_layout(D.R, D.C, D.r);
@@ -1561,9 +1720,11 @@ int a8_apollo_step(int dtype, int stochastic, const a8_apollo_tensor* t, int fir
   one.proj_fresh = proj_fresh;
   one.step = sr_step;
   one.bias_factor = bias_factor;
+  one.proj_state = nullptr;
   return apollo_run(0, dtype, stochastic, &one, 1, nullptr, 0, beta_val, beta1, has_m, apollo_eps, log_floor, v_bits,
                     block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale, scale_front, fira,
-                    fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay, wd_mode, stream);
+                    fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay, wd_mode, 1, nullptr,
+                    stream);
 }
 
 int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* ts, int ntensors, void* table_dev,
@@ -1571,11 +1732,29 @@ int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* ts, 
                          float log_floor, int v_bits, int block_size, int m_bits, int m_mode, int m_fp32,
                          int m_block_size, int channel, float apollo_scale, int scale_front, int fira,
                          float fira_margin, float d, float lr_val, float eps2, int scale_parameter, int bias_mode,
-                         float weight_decay, int wd_mode, void* stream) {
+                         float weight_decay, int wd_mode, int upload, const void* step_scalars, void* stream) {
   return apollo_run(0, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m, apollo_eps,
                     log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel, apollo_scale,
                     scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode, weight_decay,
-                    wd_mode, stream);
+                    wd_mode, upload, reinterpret_cast<const a8_step_scalars*>(step_scalars), stream);
+}
+
+int a8_apollo_proj_gen(float* proj_t, int64_t rows, int64_t cols, int64_t rank, uint64_t seed, void* stream) {
+  if (!proj_t) return set_error(A8_ERR_ARG, "null proj_t");
+  if (rows <= 0 || cols <= 0 || rank <= 0) return set_error(A8_ERR_SIZE, "empty projection");
+  const int64_t n = rank * (rows >= cols ? cols : rows);
+  const int64_t nb = (n + 255) / 256;
+  hipLaunchKernelGGL(k_proj_gen, dim3((unsigned)(nb < 8192 ? nb : 8192)), dim3(256), 0, (hipStream_t)stream,
+                     proj_t, rows, cols, rank, seed);
+  return check_launch("k_proj_gen");
+}
+
+int a8_apollo_next_seed(const uint64_t* seeds, uint64_t* out, int64_t n, void* stream) {
+  if (n < 0) return set_error(A8_ERR_SIZE, "n < 0");
+  if (n == 0) return 0;
+  if (!seeds || !out) return set_error(A8_ERR_ARG, "null pointer");
+  hipLaunchKernelGGL(k_next_seed, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)stream, seeds, out, n);
+  return check_launch("k_next_seed");
 }
 
 int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_apollo_tensor* ts, int ntensors,
@@ -1589,7 +1768,7 @@ int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_ap
   return apollo_run(phase, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m,
                     apollo_eps, log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel,
                     apollo_scale, scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode,
-                    weight_decay, wd_mode, stream);
+                    weight_decay, wd_mode, 1, nullptr, stream);
 }
 
 }  // extern "C"

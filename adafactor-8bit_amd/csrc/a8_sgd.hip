@@ -54,7 +54,17 @@ struct SgdHyp {
   int gen;          // B_M not a power of two in [32, 2048]: k_sgd_gen over units of `unit` elements
   int bm;           // B_M (gen)
   int unit;         // elements per workgroup (gen): a whole number of M blocks
+  const a8_step_scalars* dsc;   // if set: alpha, decay (when has_decay) and the SR step of this step
 };
+
+// A captured step reads its scalars from the device block of a8_step_advance.
+__device__ __forceinline__ void sgd_step_scalars(SgdHyp& h) {
+  if (!h.dsc) return;
+  const a8_step_scalars sc = load_step_scalars(h.dsc);
+  h.alpha_val = sc.alpha;
+  h.decay_val = sc.decay;
+  h.sr_step = sc.step;
+}
 
 __device__ __forceinline__ const SgdDesc* find_sgd(const SgdDesc* tab, int n, int64_t wg) {
   int lo = 0, hi = n - 1;
@@ -75,6 +85,7 @@ template <typename T, int MK, int MODE, bool SR>
 __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __restrict__ table, int ntab,
                                                  SgdHyp h) {
   __shared__ float xw[4];
+  sgd_step_scalars(h);
   const SgdDesc D = table ? *find_sgd(table, ntab, (int64_t)blockIdx.x) : one;
   const int lane = threadIdx.x, wave = lane >> 6;
   const int64_t n = D.numel;
@@ -174,6 +185,7 @@ template <typename T, int MODE, bool SR>
 __global__ __launch_bounds__(kSLanes) void k_sgd_gen(SgdDesc one, const SgdDesc* __restrict__ table, int ntab,
                                                      SgdHyp h) {
   __shared__ uint32_t s_mab[kSGenMaxMB];
+  sgd_step_scalars(h);
   const SgdDesc D = table ? *find_sgd(table, ntab, (int64_t)blockIdx.x) : one;
   const int lane = threadIdx.x;
   const int BM = h.bm, U = h.unit, mpu = U / BM;
@@ -498,7 +510,7 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
 int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* tensors, int ntensors,
                       void* table_dev, int64_t table_bytes, double beta1, int m_kind, int m_bits, int m_mode,
                       int m_block_size, float d, float alpha_val, float decay_val, int has_decay, uint64_t sr_step,
-                      int upload, void* stream) {
+                      int upload, const void* step_scalars, void* stream) {
   if (ntensors <= 0) return 0;
   if (mode < 0 || mode > 2) return set_error(A8_ERR_ARG, "mode must be 0 (single), 1 (NORM) or 2 (APPLY)");
   if ((int64_t)sizeof(SgdDesc) * ntensors > table_bytes)
@@ -508,6 +520,7 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
   h.w_m = (float)(1.0 - beta1);
   h.mdiv = (float)(1.0 - beta1);
   h.d = d; h.alpha_val = alpha_val; h.decay_val = decay_val; h.has_decay = has_decay; h.sr_step = sr_step;
+  h.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
   h.lbm = 5;
   if (m_kind == 1) {
     int rc = m_codec(m_bits, m_mode, h.mk);

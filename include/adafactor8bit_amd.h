@@ -128,6 +128,9 @@ typedef struct a8_step_spec {
   int adam_denom;
   int wd_mode;         /* 0 none; 1 decay = 1 - alpha*wd; 2 decay = 1 - rho*wd */
   int fact_bias_mode;  /* factored path: 0 none; 1 sqrt(1 - beta2^t)/bc1; 2 bc1 */
+  int apollo_bias_mode;   /* APOLLO (optimizer.py:3015-3023): 0 none; 1 sqrt(1 - beta2^t)/bc1; 2 bc1 */
+  const float* lr_dev;    /* device fp32 learning rate read at each step (a scheduler may fill_ it
+                             between graph replays), or NULL for lr */
 } a8_step_spec;
 
 typedef struct a8_step_scalars {
@@ -137,7 +140,7 @@ typedef struct a8_step_scalars {
   float decay;         /* weight-decay factor (1 without decay) */
   float bias_factor;   /* factored path */
   float rho;           /* step size before the RMS scaling and bias correction */
-  float pad_;
+  float apollo_bias;   /* APOLLO bias factor (apollo_bias_mode) */
   uint64_t step;       /* this step's number (the SR stream's step) */
 } a8_step_scalars;
 
@@ -371,6 +374,10 @@ typedef struct a8_apollo_tensor {
   int proj_fresh;          /* P^T changed since the last call for this workspace */
   uint64_t step;           /* optimizer step (stochastic-rounding stream) */
   float bias_factor;       /* see bias_mode */
+  /* device projection schedule (with step_scalars; NULL otherwise): int64[4] =
+     {last_proj_step, apollo_seed, current_proj_seed, fresh}, see a8_apollo_step_multi */
+  int64_t* proj_state;
+  int proj_gap;            /* apollo_update_proj_gap */
 } a8_apollo_tensor;
 
 /* Replaces the APOLLO update of one parameter (_update_param_apollo,
@@ -401,13 +408,43 @@ int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int
  * Same hyper-parameters as a8_apollo_step; per-matrix step, first_step,
  * proj_fresh and bias_factor come from the tensor records.  table_dev: device
  * memory of a8_apollo_table_bytes(ntensors) bytes, written by this call (stream
- * ordered).  Calls that share a table_dev must not overlap. */
+ * ordered) when `upload` is non-zero; with upload == 0 the table already there
+ * (from a call with the same records) is used.  Calls that share a table_dev
+ * must not overlap.
+ *
+ * step_scalars (NULL: host scalars as above): the device block of a8_step_advance.
+ * The V lerp weight, lr (rho), the bias factor (apollo_bias) and the SR step then
+ * come from it, and each record's proj_state schedules the projection on the
+ * device, as _get_apollo_proj_matrix does on the host (optimizer.py:2557-2584):
+ * with t the device step, when t - last_proj_step >= proj_gap the step takes
+ * current_proj_seed = apollo_seed, apollo_seed = next_seed(that seed) (the
+ * reference's seed chain, optimizer.py:152-155, restated on the device) and
+ * last_proj_step = t, and regenerates P^T (proj_t, written in place) and its bf16
+ * split with a8_apollo_proj_gen's generator; fresh = 2 set by the caller rebuilds
+ * only the split from proj_t.  proj_fresh, step and bias_factor of the records are
+ * then not read, so a step so launched can be captured in a HIP graph and
+ * replayed.  bf16 parameters only with step_scalars. */
 int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tensors, int ntensors,
                          void* table_dev, int64_t table_bytes, double beta_val, double beta1, int has_m,
                          float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits, int m_mode,
                          int m_fp32, int m_block_size, int channel, float apollo_scale, int scale_front, int fira,
                          float fira_margin, float d, float lr_val, float eps2, int scale_parameter, int bias_mode,
-                         float weight_decay, int wd_mode, void* stream);
+                         float weight_decay, int wd_mode, int upload, const void* step_scalars, void* stream);
+
+/* The device projection generator of capturable APOLLO steps (no counterpart in
+ * the reference, whose stable_randn draws from a torch generator seeded on the
+ * host, optimizer.py:139-149).  Writes P^T for a rows x cols matrix at rank r
+ * (right side, rows >= cols: [cols x r]; left: [r x rows]) with P[i][j] = z / sqrt(r)
+ * (fp32 IEEE division), z = (float)(sqrt(-2 ln u1) cos(2 pi u2)) (Box-Muller, in
+ * double), u1 = ((a >> 11) + 1) 2^-53, u2 = (b >> 11) 2^-53, where a and b are
+ * outputs 2k + 1 and 2k + 2 of SplitMix64 seeded with `seed` and k = i * (P's
+ * columns) + j is P's row-major index. */
+int a8_apollo_proj_gen(float* proj_t, int64_t rows, int64_t cols, int64_t rank, uint64_t seed, void* stream);
+/* out[i] = next_seed(seeds[i]) (optimizer.py:152-155) on the device: the 15th
+ * torch.randint(0, 2^63 - 1) draw of a CPU generator seeded with the seed (MT19937
+ * from its low 32 bits; a draw is two outputs, first high, modulo 2^63 - 1).  Device
+ * arrays of n uint64. */
+int a8_apollo_next_seed(const uint64_t* seeds, uint64_t* out, int64_t n, void* stream);
 int64_t a8_apollo_table_bytes(int ntensors);
 
 /* a8_apollo_step_multi split around the low-rank stage, for the factorised and
@@ -576,11 +613,13 @@ typedef struct a8_tensor_sgd {
 } a8_tensor_sgd;
 
 /* Multi-tensor form of a8_sgd_step: one launch per group.  m_kind: 0 none,
- * 1 quantised (m_q, m_scale), 2 fp32 (m). */
+ * 1 quantised (m_q, m_scale), 2 fp32 (m).  step_scalars (NULL: the scalar
+ * arguments): the device block of a8_step_advance, whose alpha, decay (when
+ * has_decay) and step replace alpha_val, decay_val and sr_step (graph capture). */
 int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* tensors, int ntensors,
                       void* table_dev, int64_t table_bytes, double beta1, int m_kind, int m_bits, int m_mode,
                       int m_block_size, float d, float alpha_val, float decay_val, int has_decay, uint64_t sr_step,
-                      int upload, void* stream);
+                      int upload, const void* step_scalars, void* stream);
 int64_t a8_table_bytes_sgd(int ntensors);
 /* Doubles of norm_parts workspace a NORM pass of the SGD step needs for one tensor
  * (m_block_size: that of coded momentum, 0 without); -1 for an invalid block size. */

@@ -1,0 +1,165 @@
+"""Capturable APOLLO steps (capturable=True) at C4's settings on the GPU.
+
+A capturable group keeps its step count on the device (a8_step_advance).  For
+APOLLO matrices the per-step scalars (V lerp weight, lr, bias factor, SR step)
+come from that block, and the projection schedule of _get_apollo_proj_matrix
+(optimizer.py:2557-2584) runs on the device: the refresh decision, the
+reference's seed chain next_seed (optimizer.py:152-155, restated on the device)
+and a new P from the device generator.  The first step of a matrix takes P from
+the host schedule (stable_randn); later refreshes use the device generator
+(oracle/apollo_proj.py restates it).
+
+* the device seed chain equals torch's next_seed bit for bit, and the device
+  generator equals the oracle's restatement (all but a few elements bit-exact,
+  those within one fp32 ulp: double log / cos of two libraries);
+* at C4's settings (rank 256, B_V 2048, B_M 256, UF8 / AL8, channel scale, Fira,
+  bf16 parameters with SR, one right-side and one left-side matrix plus an fp32-
+  state vector, apollo_update_proj_gap=3), graph replays across two projection
+  refreshes equal eager capturable steps bit for bit, P^T after a device refresh
+  is the generator's for the new seed, and the schedule's state (apollo_seed,
+  current_proj_seed, last_proj_step) equals the default path's;
+* before the first device refresh, capturable eager steps equal the default
+  path's bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from inputs import make_grad, make_param
+from oracle import apollo_proj as ap
+
+C4_CAP = dict(lr=1e-3, beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=False,
+              relative_step=False, scale_parameter=False, scale_weight_decay=False, d=0.0, eps=(1e-6, 1e-3),
+              apollo_eps=1e-6, apollo_factorize=False, apollo_update_proj_gap=3,
+              apollo_scale_type="channel", apollo_scale=1.0, apollo_scale_front=False, apollo_cache_proj=True,
+              enable_fira_for_apollo=True, apollo_rank=256, block_size=2048, m_block_size=256,
+              m_quant_type="uf8", v_quant_type="al8", stochastic_round_writeback=True)
+SHAPES = [(1024, 512), (512, 1536), (2048,)]
+
+
+def _assert_ulp1(dev, ref, what):
+    a = dev.view(np.int32).astype(np.int64)
+    b = ref.view(np.int32).astype(np.int64)
+    off = np.abs(a - b)
+    nd = int((off > 0).sum())
+    print(f"[apollo proj gen] {what}: {nd} of {a.size} differ (max {int(off.max())} ulp)", flush=True)
+    assert int(off.max()) <= 1 and nd <= max(2, int(1e-5 * a.size)), (what, nd, int(off.max()))
+
+
+@pytest.mark.gpu
+def test_device_next_seed_matches_reference():
+    from adafactor8bit import _native as nat
+    from adafactor8bit.optimizer import next_seed
+    rng = np.random.default_rng(11)
+    seeds = [0, 1, 921, 2 ** 32 + 5, 2 ** 63 - 2] + [int(x) for x in rng.integers(0, 2 ** 63 - 1, 250)]
+    dev = torch.device("cuda", 0)
+    s = torch.tensor(seeds, dtype=torch.int64, device=dev)
+    out = torch.empty_like(s)
+    nat.check(nat.lib().a8_apollo_next_seed(s.data_ptr(), out.data_ptr(), s.numel(), nat.stream_of(dev)),
+              "a8_apollo_next_seed")
+    got = out.cpu().tolist()
+    for x, y in zip(seeds, got):
+        assert y == next_seed(x), x
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols,rank", [(1024, 512, 256), (512, 1536, 256), (700, 384, 96), (300, 700, 64)])
+def test_device_projection_generator_matches_oracle(rows, cols, rank):
+    from adafactor8bit import _native as nat
+    dev = torch.device("cuda", 0)
+    seed = 0x5DEECE66D + rows
+    k = rank * (cols if rows >= cols else rows)
+    pt = torch.empty(k, dtype=torch.float32, device=dev)
+    nat.check(nat.lib().a8_apollo_proj_gen(pt.data_ptr(), rows, cols, rank, seed, nat.stream_of(dev)),
+              "a8_apollo_proj_gen")
+    ref = ap.proj_t(rows, cols, rank, seed).reshape(-1)
+    _assert_ulp1(pt.cpu().numpy(), ref, f"{rows}x{cols} r{rank}")
+
+
+def _setup(capturable):
+    from adafactor8bit import Adafactor8Bit
+    ps = [torch.nn.Parameter(make_param(s, i, 29).to("cuda", torch.bfloat16)) for i, s in enumerate(SHAPES)]
+    for p in ps:
+        p.grad = torch.zeros_like(p)   # static gradient buffers
+    return ps, Adafactor8Bit(ps, **dict(C4_CAP, capturable=capturable))
+
+
+def _load(ps, t):
+    for i, p in enumerate(ps):
+        p.grad.copy_(make_grad(tuple(p.shape), i, t, 29, zero_frac=0.0).to(torch.bfloat16))
+
+
+def _same(oa, ob, pa, pb, what):
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert torch.equal(a, b), f"{what}: param {i}"
+        sa, sb = oa.state[a], ob.state[b]
+        for k, v in sa.items():
+            if torch.is_tensor(v) and k in sb:
+                assert torch.equal(v, sb[k]), f"{what}: param {i} {k}"
+
+
+SCHED = ("apollo_seed", "current_proj_seed", "last_proj_step")
+
+
+def _schedule(opt, ps):
+    sd = opt.state_dict()["state"]
+    return [tuple(sd[i].get(k) for k in SCHED) for i in range(2)]
+
+
+@pytest.mark.gpu
+def test_apollo_graph_replays_equal_eager_steps_across_refreshes():
+    print("[apollo capture] C4 settings, gap 3", flush=True)
+    pa, oa = _setup(True)   # replayed
+    pb, ob = _setup(True)   # eager
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load(ps, t)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load(pa, 3)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    _same(oa, ob, pa, pb, "after capture (nothing ran)")
+    for t in range(3, 10):   # device refreshes at steps 4 and 7
+        _load(pa, t)
+        graph.replay()
+        _load(pb, t)
+        ob.step()
+        junk = torch.randn(4096, device="cuda").sum()
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        _same(oa, ob, pa, pb, f"step {t}")
+        print(f"[apollo capture] step {t} equal", flush=True)
+    assert _schedule(oa, pa) == _schedule(ob, pb)
+    sd = oa.state_dict()["state"]
+    assert {sd[i]["step"] for i in range(3)} == {9}
+    assert all(sd[i]["last_proj_step"] == 7 for i in range(2))
+
+
+@pytest.mark.gpu
+def test_apollo_capturable_schedule_matches_default_path():
+    """Eager capturable steps against the default path: the same seed chain at every
+    step; bit-identical parameters and states until the first device refresh
+    (step 4), whose P is the device generator's for the new seed."""
+    pa, oa = _setup(True)
+    pb, ob = _setup(False)
+    for t in range(1, 8):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load(ps, t)
+            o.step()
+        torch.cuda.synchronize()
+        assert _schedule(oa, pa) == _schedule(ob, pb), t
+        if t <= 3:
+            _same(oa, ob, pa, pb, f"step {t}")
+        if t == 4:
+            for i, p in enumerate(pa[:2]):
+                st = oa.state[p]
+                pt = st["apollo_proj_matrix_T"].cpu().numpy().reshape(-1)
+                ref = ap.proj_t(p.shape[0], p.shape[1], 256, int(st["current_proj_seed"])).reshape(-1)
+                _assert_ulp1(pt, ref, f"step 4 refresh, matrix {i}")
+        print(f"[apollo capturable eager] step {t}", flush=True)

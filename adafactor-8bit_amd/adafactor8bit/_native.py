@@ -232,5 +232,49 @@ def dtype_code(dt) -> int:
     raise TypeError(f"adafactor8bit: unsupported parameter dtype {dt}")
 
 
+_ROCTX = None
+
+
+def roctx():
+    """The ROCm tracing-marker library (rocprofiler-sdk roctx), or False when the
+    runtime has none: optimizer steps push named ranges onto it, which
+    ``rocprofv3 --marker-trace`` records around each step's kernels."""
+    global _ROCTX
+    if _ROCTX is None:
+        _ROCTX = False
+        for name in ("librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so", "/opt/rocm/lib/librocprofiler-sdk-roctx.so"):
+            try:
+                r = ctypes.CDLL(name)
+                r.roctxRangePushA.argtypes = [ctypes.c_char_p]
+                r.roctxRangePushA.restype = ctypes.c_int
+                r.roctxRangePop.argtypes = []
+                r.roctxRangePop.restype = ctypes.c_int
+                _ROCTX = r
+                break
+            except (OSError, AttributeError):
+                continue
+    return _ROCTX
+
+
+class range_marker:
+    """``with range_marker(b"name"):`` -- a roctx range (no-op without roctx)."""
+    __slots__ = ("msg",)
+
+    def __init__(self, msg: bytes):
+        self.msg = msg
+
+    def __enter__(self):
+        r = roctx()
+        if r:
+            r.roctxRangePushA(self.msg)
+        return self
+
+    def __exit__(self, *exc):
+        r = roctx()
+        if r:
+            r.roctxRangePop()
+        return False
+
+
 def exported_symbols():
     return sorted(_SIGS)

@@ -281,7 +281,8 @@ class Adafactor8Bit(Optimizer):
         if gc_on:
             gc.disable()
         try:
-            self._step_groups()
+            with nat.range_marker(b"adafactor8bit.step"):
+                self._step_groups()
         finally:
             if gc_on:
                 gc.enable()
@@ -305,7 +306,8 @@ class Adafactor8Bit(Optimizer):
                     self._sr_seed_counter += 1
             dsc = _advance_device_step(self, group, params, states) if group.get("capturable") else None
             try:
-                self._step_group(group, params, grads, states, dsc)
+                with nat.range_marker(b"adafactor8bit.group"):
+                    self._step_group(group, params, grads, states, dsc)
             except Exception:
                 if dsc is not None:   # the device count moved on; rebuild it from the restored host counts
                     self._ws.pop((params[0].device, "devstep", id(group)), None)

@@ -173,7 +173,7 @@ def make_grad(kind, shape, gen, dev, i, embed):
 
 def cpu_baseline(workload="adamw", seconds_budget=20.0):
     """The CPU oracle (torch CPU restatement of the reference's fallback) on a
-    bounded sample of the workload, 1 warm-up + timed steps within the budget:
+    bounded sample of the workload, 2 warm-up + timed steps within the budget:
     adamw (C1): one 4096x4096 fp32 AdamW UF8/AL8 step; adafactor / came (C2, C3):
     one 2048x2048 fp32 matrix of the config; apollo (C4): one 2048x2048 bf16
     matrix at rank 256 (deterministic writeback: the reference's CPU stochastic
@@ -197,8 +197,9 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
     opt = F.OracleOptimizer([p], **kw)
     zf = 0.02 if workload == "adamw_llama3_8b" else 0.05
     grads = [make_grad(shape, 0, t, 0, kind=gk, zero_frac=zf).to(pdt) for t in (1, 2)]
-    p.grad = grads[0]
-    opt.step()
+    for w in range(2):   # two warm-up steps (the plan for the baseline)
+        p.grad = grads[w]
+        opt.step()
     times = []
     t_end = time.perf_counter() + seconds_budget
     i = 0
@@ -221,7 +222,22 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
             "apollo_factorize": "one 2048x2048 bf16 factorised APOLLO r=256 step (deterministic writeback)",
             "apollo_came": "one 2048x2048 bf16 CAME APOLLO r=256 step (deterministic writeback)"}[workload]
     return {"value": n / med, "unit": "params/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{what}, median of {len(times)} after 1 warm-up", "ms_per_step": med * 1e3}
+            "sample": f"{what}, median of {len(times)} after 2 warm-ups", "ms_per_step": med * 1e3}
+
+
+def copy_ceiling(dev, stream, mib=1024, reps=10):
+    """This box's streaming ceiling: a device-to-device copy of `mib` MiB (read +
+    write counted), average of `reps` launches timed with HIP events."""
+    src = torch.empty(mib << 18, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return 2.0 * (mib << 20) * reps / (a.elapsed_time(b) * 1e-3) / 1e9
 
 
 def main():
@@ -316,7 +332,8 @@ def main():
     k_avg = sum(kms) / len(kms)
     achieved = qbytes / (k_avg * 1e-3) / 1e9
 
-    if args.calib:  # known-size copy: 256 MiB read + 256 MiB written per launch
+    ceiling = copy_ceiling(dev, stream)
+    if args.calib:  # known-size copy for the counters: 256 MiB read + 256 MiB written per launch
         src = torch.empty(64 << 20, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -351,6 +368,7 @@ def main():
         "eager_ms_per_step": eager_ms,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "copy_ceiling_GBps": ceiling, "frac_of_copy": achieved / ceiling,
                      "kernel": f"k_update1d<float,8,0,false> (multi-tensor, {len(big)} tensors)",
                      "kernel_ms_avg": k_avg, "kernel_ms_min": kms[0], "bytes_per_launch": qbytes},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(args.workload),

@@ -29,6 +29,9 @@ C3 = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True,
           scale_parameter=False, scale_weight_decay=False, d=1.0, eps_came=1e-16, lr=1e-4, block_size=2048,
           m_block_size=256, m_quant_type="uf8", v_quant_type="al16", c_quant_type="al16",
           enable_fira_for_adafactor=True, fira_margin=0.01)
+SGD = dict(beta1=0.9, beta2=None, beta2_decay=None, factored=False, relative_step=False, scale_parameter=False,
+           scale_weight_decay=True, weight_decay=0.01, d=0.0, lr=1e-2, block_size=2048, m_block_size=256,
+           m_quant_type="uf8", stochastic_round_writeback=True)
 FP32S = dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=False, relative_step=False, scale_parameter=True,
              d=1.0, quantize=False, enable_fira_for_adafactor=True, eps=(1e-30, 1e-3), lr=1e-3)
 
@@ -45,6 +48,8 @@ CASES = [
     ("adamw_clip_fira_q1d", dict(ADAMW, d=1.0, enable_fira_for_adafactor=True, lr=1e-3),
      [(700, 1100), (300, 260), (5000,)], torch.float32, "logscale"),
     ("adafactor1d_fp32_scale_clip_fira", FP32S, [(700, 1100), (2048,), (5000,)], torch.float32, "student_t"),
+    # SGD (beta2 = beta2_decay = None): coded momentum with weight decay, bf16 with SR
+    ("sgd_uf8_wd_bf16_sr", SGD, [(300, 260), (5000,), (2048,)], torch.bfloat16, "normal_zeros"),
 ]
 
 
@@ -118,6 +123,47 @@ def test_capturable_eager_equals_default_path(name, kw, shapes, dtype, gkind):
             o.step()
     torch.cuda.synchronize()
     _same_state(oa, ob, pa, pb, "after 5 steps")
+
+
+@pytest.mark.gpu
+@pytest.mark.filterwarnings("ignore:Detected call of")
+@pytest.mark.parametrize("name,kw,shapes", [("c1_adamw", ADAMW, [(300, 260), (2048,), (5000,)]),
+                                            ("c2_adafactor", C2, [(300, 260), (2048,), (130, 70)])])
+def test_tensor_lr_scheduled_between_replays(name, kw, shapes):
+    """A one-element fp32 device tensor lr is read by every replay: a scheduler that
+    fill_()s it between replays changes the step of the replayed graph exactly as
+    it changes an eager capturable step."""
+    print(f"[capture tensor lr] {name}", flush=True)
+    lra = torch.tensor(1e-3, dtype=torch.float32, device="cuda")
+    lrb = torch.tensor(1e-3, dtype=torch.float32, device="cuda")
+    pa, oa = _setup(dict(kw, lr=lra), shapes, torch.float32, capturable=True)
+    pb, ob = _setup(dict(kw, lr=lrb), shapes, torch.float32, capturable=True)
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load_grads(ps, t, "student_t", torch.float32)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    sched = torch.optim.lr_scheduler.LambdaLR(oa, lambda e: 0.5 ** e)
+    schedb = torch.optim.lr_scheduler.LambdaLR(ob, lambda e: 0.5 ** e)
+    before = [p.clone() for p in pa]
+    for t in range(3, 7):
+        _load_grads(pa, t, "student_t", torch.float32)
+        graph.replay()
+        _load_grads(pb, t, "student_t", torch.float32)
+        ob.step()
+        torch.cuda.synchronize()
+        _same_state(oa, ob, pa, pb, f"step {t}")
+        sched.step()
+        schedb.step()
+    assert abs(float(lra) - 1e-3 * 0.5 ** 4) < 1e-10 and float(lrb) == float(lra)
+    assert not all(torch.equal(a, b) for a, b in zip(pa, before))
 
 
 @pytest.mark.gpu

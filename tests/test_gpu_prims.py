@@ -341,6 +341,63 @@ def test_apollo_came_rms_and_m_res(mqt):
 
 
 @pytest.mark.gpu
+def test_apollo_came_primitives_within_rsqrtf_bound():
+    """compute_apollo_came_rms, apollo_came_compute_m_res and
+    apollo_came_compute_update_norms (kernels.cu:2455-2566) take x * rsqrtf(max(v,
+    eps_sq)), whose documented error is at most 2 ulp; this library takes the
+    correctly rounded 1/sqrt.  Both lie within a few fp32 ulps of the exact value,
+    so each output is held against a float64 restatement of the kernel formula
+    with the exact reciprocal square root: the per-element factors within 2^-21
+    relative (the reference's 2 ulp plus this build's 1, plus the products'
+    roundings), the sums and norms within 2^-20 relative (the reference sums in
+    fp32 atomics), the momentum EMA within 4 ulps of its terms' magnitudes.  The
+    reference's own outputs satisfy the same bounds by its documented rsqrtf
+    error, so this pins the two to within those bands (not bit for bit)."""
+    from oracle.fallback import m_bits_of, m_dequantize, m_quantize
+    K = _k()
+    print("[apollo came rsqrtf bound]", flush=True)
+    n, bs, eps_sq = 6000, 256, 1e-30
+    gen = torch.Generator().manual_seed(9)
+    g = torch.randn(n, generator=gen) * 1e-2
+    v = torch.rand(n, generator=gen) * 1e-4 + 1e-9
+    m0 = torch.randn(n, generator=gen) * 1e-2
+    q, s = m_quantize(m0, "uf8", bs)
+    res_old = torch.rand(n, generator=gen) * 1e-4
+    clip = torch.tensor([1.25])
+    acc = torch.zeros(1, device="cuda")
+    K.compute_apollo_came_rms(g.cuda(), v.cuda(), acc, eps_sq, n)
+    mt = torch.empty(n, device="cuda")
+    rt = torch.empty(n, device="cuda")
+    K.apollo_came_compute_m_res(g.cuda(), v.cuda(), q.cuda(), s.cuda(), res_old.cuda(), mt, rt, clip.cuda(), 0.9,
+                                0.999, 1e-16, eps_sq, bs, n, m_bits_of("uf8"), 0)
+    torch.cuda.synchronize()
+    g64, v64 = g.double().numpy(), np.maximum(v.double().numpy(), eps_sq)
+    u = g64 / np.sqrt(v64)                       # exact reciprocal square root
+    exact_rms = float((u * u).sum())
+    assert abs(acc.item() - exact_rms) <= 2.0 ** -20 * exact_rms, (acc.item(), exact_rms)
+    ut = u / 1.25
+    mo = m_dequantize(q, s, n, bs, "uf8").double().numpy()
+    m_exact = 0.9 * mo + 0.1 * ut                # kernels.cu: beta1 * m_old + (1 - beta1) * u_t
+    tol = 4 * 2.0 ** -24 * (np.abs(0.9 * mo) + np.abs(0.1 * ut)) + 2.0 ** -21 * np.abs(0.1 * ut)
+    assert np.all(np.abs(mt.cpu().double().numpy() - m_exact) <= tol)
+    d = ut - mt.cpu().double().numpy()
+    r_exact = 0.999 * res_old.double().numpy() + 0.001 * (d * d + 1e-16)
+    assert np.all(np.abs(rt.cpu().double().numpy() - r_exact) <= 2.0 ** -20 * r_exact)
+    # update norms: channel norms of m * rsqrt(max(res, eps_sq)) over rows of a 40 x 150 view
+    N, D = 40, 150
+    mm, rr, gl = mt[:N * D], rt[:N * D], g[:N * D].cuda()
+    nu = torch.empty(N, device="cuda")
+    ng = torch.empty(N, device="cuda")
+    K.apollo_came_compute_update_norms(mm, rr, gl, nu, ng, eps_sq, N, D, D, 1, N * D)
+    torch.cuda.synchronize()
+    um = mm.cpu().double().numpy() / np.sqrt(np.maximum(rr.cpu().double().numpy(), eps_sq))
+    nu_exact = np.sqrt((um.reshape(N, D) ** 2).sum(axis=1))
+    np.testing.assert_allclose(nu.cpu().double().numpy(), nu_exact, rtol=2.0 ** -20)
+    np.testing.assert_allclose(ng.cpu().double().numpy(), np.sqrt((g64[:N * D].reshape(N, D) ** 2).sum(axis=1)),
+                               rtol=2.0 ** -20)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("native", [False, True])
 @pytest.mark.parametrize("sr", [False, True])

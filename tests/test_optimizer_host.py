@@ -71,3 +71,16 @@ def test_step_counter_restored_when_launch_fails(monkeypatch):
     with pytest.raises(RuntimeError, match="launch failed"):
         opt._step_group(opt.param_groups[0], ps, [None, None], states)
     assert [st["step"] for st in states] == [7, 7]
+
+
+def test_roctx_step_ranges_available():
+    """step() pushes roctx ranges (adafactor8bit.step, adafactor8bit.group) that
+    rocprofv3 --marker-trace records; the marker library is part of ROCm."""
+    from adafactor8bit import _native as nat
+    r = nat.roctx()
+    assert r, "librocprofiler-sdk-roctx not loadable"
+    depth = r.roctxRangePushA(b"adafactor8bit.test")
+    assert depth >= 0
+    assert r.roctxRangePop() >= 0
+    with nat.range_marker(b"adafactor8bit.test"):
+        pass

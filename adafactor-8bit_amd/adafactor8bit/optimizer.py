@@ -1631,10 +1631,11 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
 
 
 def _apollo_capturable_check(p, group, factorize, came):
-    """What a capturable APOLLO step covers: bf16 parameters (the projection is the
-    MFMA kernel), the plain low-rank stage, no maximize (a negated gradient copy)."""
-    if p.dtype != torch.bfloat16:
-        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO on bf16 parameters")
+    """What a capturable APOLLO step covers: bf16 and fp32 parameters (fp16 and fp64
+    ones project an fp32 copy of the gradient made each step), the plain low-rank
+    stage, no maximize (a negated gradient copy)."""
+    if p.dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO on bf16 and fp32 parameters")
     if factorize or came:
         raise NotImplementedError("adafactor8bit: capturable=True does not cover the factorised or CAME APOLLO "
                                   "stages (apollo_factorize, beta3)")

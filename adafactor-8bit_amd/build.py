@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "adafactor8bit", "libadafactor8bit_amd.so")
 SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip", "a8_factored.hip", "a8_apollo.hip",
            "a8_decode.hip", "a8_sgd.hip", "a8_prims.hip", "a8_apollo_x.hip", "a8_step.hip"]
-LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+LIBS = ["-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = os.environ.get("A8_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -21,13 +21,12 @@
 //                three bf16 terms (3 x 8 significand bits carry fp32's 24; all
 //                products land in one fp32 accumulator), reading G once: the
 //                same pass scrubs non-finite entries and accumulates the channel
-//                norms of G (and of p for scale_parameter).  fp32 G: rocBLAS
-//                sgemm plus a norm pass per matrix.
+//                norms of G.  fp32 G: the same tiles with G split into three
+//                bf16 terms as well (six products per pair of terms).
 //   k_ap_low     low-rank V/M EMA and re-encode, u
 //   k_ap_scale   channel (or tensor) norms of u and g_low, per-workgroup partials
 //   k_ap_scalars one workgroup per matrix: alpha, Fira, step, decay
 //   k_ap_apply   full-rank writeback (deterministic or stochastic rounding)
-#include <rocblas/rocblas.h>
 #include <vector>
 #include "a8_common.cuh"
 #include "a8_mcodec.cuh"
@@ -49,7 +48,7 @@ constexpr int kApApp = 2048 * kApRuns;   // matrix elements per k_ap_apply workg
 // Workspace of one matrix (offsets in floats; partial arrays hold doubles).
 struct ApL {
   int64_t n_low, nchg, K, Kp, rp, ntr, npass, ntile, nunit, nsc, napp;
-  int64_t glow, u, ngsq, fin, scal, gpart, ppart, spart, nfpart, psplit, total;
+  int64_t glow, u, ngsq, fin, scal, gpart, ppart, spart, psplit, total;
 };
 
 __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
@@ -74,8 +73,7 @@ __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
   w.gpart = (w.scal + 16 + 1) / 2 * 2;     // double[ntr]  ||G||^2 per tile
   w.ppart = w.gpart + 2 * w.ntr;           // double[ntr]  ||p||^2 per tile
   w.spart = w.ppart + 2 * w.ntr;           // double[3 nsc] sum ngsq s^2, sum u^2, sum g_low^2
-  w.nfpart = w.spart + 6 * w.nsc;          // int[ntr]     non-finite G seen (fp32 path)
-  w.psplit = (w.nfpart + w.ntr + 63) / 64 * 64;   // bf16[3][rp][Kp]  P rows, three terms
+  w.psplit = (w.spart + 6 * w.nsc + 63) / 64 * 64;   // bf16[3][rp][Kp]  P rows, three terms
   w.total = w.psplit + (3 * w.rp * w.Kp + 1) / 2;
   return w;
 }
@@ -681,6 +679,307 @@ __device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int til
   if (lane == 0) ws_d_set(D.ws, L.gpart, ct, t);
 }
 
+// ------------------------------------------------------------ MFMA projection (fp32 G)
+// fp32 G (fp32 parameters; fp16 / fp64 ones project grad.float()) takes the same
+// tiles with G split as P is: hi + mid + lo bf16 terms that sum to the fp32 value
+// exactly (24 significand bits in three 8-bit pieces).  The split happens once,
+// when a slab is stored to LDS (three planes); the MFMAs take the six products
+// whose weight is at least 2^-16 of the leading one -- G_hi P_hi, G_hi P_mid,
+// G_mid P_hi, G_hi P_lo, G_mid P_mid, G_lo P_hi -- all exact in the fp32
+// accumulator.  The three dropped ones weigh at most 2^-24 (about one fp32
+// rounding of each product), so g_low keeps an fp32 GEMM's error bound.
+// Non-finite G entries count as zero (optimizer.py:2606); the channel norms take
+// fp32 squares summed in double.
+
+// x (fp32, finite or not) -> three bf16 terms of scrub(x); returns scrub(x).
+__device__ __forceinline__ float split3(float x, uint16_t& h, uint16_t& m, uint16_t& lo) {
+  x = scrub(x);
+  const __hip_bfloat16 bh = __float2bfloat16(x);
+  const float r1 = x - __bfloat162float(bh);
+  const __hip_bfloat16 bm = __float2bfloat16(r1);
+  const __hip_bfloat16 bl = __float2bfloat16(r1 - __bfloat162float(bm));
+  __builtin_memcpy(&h, &bh, 2);
+  __builtin_memcpy(&m, &bm, 2);
+  __builtin_memcpy(&lo, &bl, 2);
+  return x;
+}
+// Eight fp32 values -> three planes of eight bf16 (u32x4 each); adds their squares.
+__device__ __forceinline__ void split8(const float* x, u32x4* pl, double& sq) {
+  uint32_t w[3][4] = {};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint16_t h, m, lo;
+    const float v = split3(x[e], h, m, lo);
+    sq += (double)(v * v);
+    w[0][e >> 1] |= (uint32_t)h << (16 * (e & 1));
+    w[1][e >> 1] |= (uint32_t)m << (16 * (e & 1));
+    w[2][e >> 1] |= (uint32_t)lo << (16 * (e & 1));
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t) pl[t] = u32x4{w[t][0], w[t][1], w[t][2], w[t][3]};
+}
+// Eight fp32 of a row at element offset off: two 16-byte loads when all eight exist
+// and the row is aligned, element loads otherwise (missing ones zero).
+__device__ __forceinline__ void ldf8(const float* base, int64_t off, int cnt, int vec, float* x) {
+  if (vec && cnt == 8) {
+    const f32x4 a = *gp(reinterpret_cast<const f32x4*>(base + off));
+    const f32x4 b = *gp(reinterpret_cast<const f32x4*>(base + off + 4));
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = e < cnt ? gp(base)[off + e] : 0.0f;
+}
+
+constexpr int kApPlaneR = 2 * kApTile * kApGS;   // halves per G plane (two buffers), right side
+constexpr int kApPlaneL = 2 * kApTile * kApTS;   // left side
+
+template <bool FULL, int NB>
+__device__ __forceinline__ void proj_right32(const ApDesc& D, const ApL& L, int tile, uint16_t* lds, double* sred) {
+  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
+  const int pass = (int)(tile / L.ntr);
+  const int64_t rt = tile - (int64_t)pass * L.ntr;
+  const int64_t R = D.R, C = D.C, r = D.r, K = C;
+  const int64_t row0 = rt * kApTile;
+  const int64_t cb0 = (int64_t)pass * kApPass + w * 64;
+  constexpr bool act1 = NB >= 2;
+  const int64_t nblk = L.rp / 32, nkc = L.Kp / 32;
+  const int64_t blk0 = cb0 / 32;
+  const float* G = reinterpret_cast<const float*>(D.grad);
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: rows lr and lr + 32, k chunk lc
+  const int64_t ga = row0 + lr, gb = row0 + lr + 32;
+  const bool pass0 = pass == 0;
+  f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
+  double na = 0.0, nb = 0.0;
+  auto ldG = [&](int64_t k0, float* x, float* y) {
+    const int64_t k = k0 + lc;
+    const int cnt = FULL ? 8 : (K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0));
+    ldf8(G, ga * C + k, (FULL || ga < R) ? cnt : 0, FULL ? 1 : D.valign, x);
+    ldf8(G, gb * C + k, (FULL || gb < R) ? cnt : 0, FULL ? 1 : D.valign, y);
+  };
+  auto ldB = [&](int64_t kc, int t, u32x4* x0, u32x4* x1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      x0[j] = gp(Ps)[psw_unit(t, blk0, kc, j, l, nblk, nkc)];
+      if constexpr (act1) x1[j] = gp(Ps)[psw_unit(t, blk0 + 1, kc, j, l, nblk, nkc)];
+    }
+  };
+  float fx[8], fy[8];   // the next slab's G, prefetched
+  ldG(0, fx, fy);
+  u32x4 b0[2], b1[2], c0[2], c1[2];
+  if constexpr (NB > 0) ldB(0, 0, b0, b1);
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += 64) {
+    u32x4 px[3], py[3];
+    double sa = 0.0, sb = 0.0;
+    split8(fx, px, sa);
+    split8(fy, py, sb);
+    if (pass0) { na += sa; nb += sb; }
+    if (k0 + 64 < K) ldG(k0 + 64, fx, fy);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      uint16_t* sl = lds + t * kApPlaneR + buf * (kApTile * kApGS);
+      *reinterpret_cast<u32x4*>(&sl[lr * kApGS + lc]) = px[t];
+      *reinterpret_cast<u32x4*>(&sl[(lr + 32) * kApGS + lc]) = py[t];
+    }
+    __syncthreads();   // the slab is in LDS; the other buffer's readers finished a barrier ago
+    if constexpr (NB > 0) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int64_t kcg = k0 / 32 + kc;
+        u32x4 ar0[3][2], ar1[3][2];
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          const uint16_t* sl = lds + t * kApPlaneR + buf * (kApTile * kApGS);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            ar0[t][j] = *reinterpret_cast<const u32x4*>(&sl[l32 * kApGS + 32 * kc + 16 * hi + 8 * j]);
+            ar1[t][j] = *reinterpret_cast<const u32x4*>(&sl[(32 + l32) * kApGS + 32 * kc + 16 * hi + 8 * j]);
+          }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 3; ++tb) {   // P term tb meets G planes 0 .. 2 - tb
+          const bool last = kc == 1 && tb == 2;
+          if (tb < 2) ldB(kcg, tb + 1, c0, c1);
+          else if (!last || k0 + 64 < K) ldB(kcg + 1, 0, c0, c1);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int ta = 0; ta < 3 - tb; ++ta) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              a00 = mfma(as_bf8(ar0[ta][j]), as_bf8(b0[j]), a00);
+              a10 = mfma(as_bf8(ar1[ta][j]), as_bf8(b0[j]), a10);
+              if constexpr (act1) {
+                a01 = mfma(as_bf8(ar0[ta][j]), as_bf8(b1[j]), a01);
+                a11 = mfma(as_bf8(ar1[ta][j]), as_bf8(b1[j]), a11);
+              }
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            b0[j] = c0[j];
+            if constexpr (act1) b1[j] = c1[j];
+          }
+        }
+      }
+    }
+    buf ^= 1;
+  }
+  float* glow = D.ws + L.glow;
+  if constexpr (NB > 0) {
+    store_acc(a00, glow, r, row0, cb0 + l32, R, r, hi);
+    store_acc(a10, glow, r, row0 + 32, cb0 + l32, R, r, hi);
+  }
+  if constexpr (act1) {
+    store_acc(a01, glow, r, row0, cb0 + 32 + l32, R, r, hi);
+    store_acc(a11, glow, r, row0 + 32, cb0 + 32 + l32, R, r, hi);
+  }
+  if (!pass0) return;
+  na += __shfl_xor(na, 1, 64);
+  na += __shfl_xor(na, 2, 64);
+  na += __shfl_xor(na, 4, 64);
+  nb += __shfl_xor(nb, 1, 64);
+  nb += __shfl_xor(nb, 2, 64);
+  nb += __shfl_xor(nb, 4, 64);
+  double t = 0.0;
+  if ((lane & 7) == 0) {
+    if (ga < R) { gp(D.ws + L.ngsq)[ga] = norm_sq(na); t += na; }
+    if (gb < R) { gp(D.ws + L.ngsq)[gb] = norm_sq(nb); t += nb; }
+  }
+  t = ap_wg_sum(t, sred);
+  if (lane == 0) ws_d_set(D.ws, L.gpart, rt, t);
+}
+
+template <bool FULL, int NB>
+__device__ __forceinline__ void proj_left32(const ApDesc& D, const ApL& L, int tile, uint16_t* ldsT, double* sred) {
+  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
+  const int pass = (int)(tile / L.ntr);
+  const int64_t ct = tile - (int64_t)pass * L.ntr;
+  const int64_t C = D.C, r = D.r, K = D.R;
+  const int64_t n0 = ct * kApTile;
+  const int64_t mb0 = (int64_t)pass * kApPass + w * 64;
+  constexpr bool act1 = NB >= 2;
+  const int64_t nblk = L.rp / 32, nkc = L.Kp / 32;
+  const int64_t blk0 = mb0 / 32;
+  const float* G = reinterpret_cast<const float*>(D.grad);
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: row lr of the slab, 8 columns
+  const int64_t gc = n0 + lc;
+  const int cc = C - gc >= 8 ? 8 : (C - gc > 0 ? (int)(C - gc) : 0);
+  const bool pass0 = pass == 0;
+  f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
+  double cs[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) cs[j] = 0.0;
+  auto ldG = [&](int64_t row, float* x) {
+    ldf8(G, row * C + gc, (FULL || row < K) ? (FULL ? 8 : cc) : 0, FULL ? 1 : D.valign, x);
+  };
+  auto ldA = [&](int64_t kc, int t, u32x4* x0, u32x4* x1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      x0[j] = gp(Ps)[psw_unit(t, blk0, kc, j, l, nblk, nkc)];
+      if constexpr (act1) x1[j] = gp(Ps)[psw_unit(t, blk0 + 1, kc, j, l, nblk, nkc)];
+    }
+  };
+  float f[8];   // the next slab's row, prefetched
+  ldG(lr, f);
+  u32x4 p0[2], p1[2], q0[2], q1[2];
+  if constexpr (NB > 0) ldA(0, 0, p0, p1);
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += 32) {
+    uint16_t h[3][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = split3(f[j], h[0][j], h[1][j], h[2][j]);
+      if (pass0) cs[j] += (double)(v * v);
+    }
+    if (k0 + 32 < K) ldG(k0 + 32 + lr, f);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      uint16_t* sl = ldsT + t * kApPlaneL + buf * (kApTile * kApTS);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sl[(lc + j) * kApTS + lr] = h[t][j];
+    }
+    __syncthreads();   // the slab is in LDS; the other buffer's readers finished a barrier ago
+    if constexpr (NB > 0) {
+      const int64_t kcg = k0 / 32;
+      u32x4 bc0[3][2], bc1[3][2];
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const uint16_t* sl = ldsT + t * kApPlaneL + buf * (kApTile * kApTS);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          bc0[t][j] = *reinterpret_cast<const u32x4*>(&sl[l32 * kApTS + 16 * hi + 8 * j]);
+          bc1[t][j] = *reinterpret_cast<const u32x4*>(&sl[(32 + l32) * kApTS + 16 * hi + 8 * j]);
+        }
+      }
+#pragma unroll
+      for (int ta = 0; ta < 3; ++ta) {   // P term ta meets G planes 0 .. 2 - ta
+        if (ta < 2) ldA(kcg, ta + 1, q0, q1);
+        else if (k0 + 32 < K) ldA(kcg + 1, 0, q0, q1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int tb = 0; tb < 3 - ta; ++tb) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            a00 = mfma(as_bf8(p0[j]), as_bf8(bc0[tb][j]), a00);
+            a01 = mfma(as_bf8(p0[j]), as_bf8(bc1[tb][j]), a01);
+            if constexpr (act1) {
+              a10 = mfma(as_bf8(p1[j]), as_bf8(bc0[tb][j]), a10);
+              a11 = mfma(as_bf8(p1[j]), as_bf8(bc1[tb][j]), a11);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          p0[j] = q0[j];
+          if constexpr (act1) p1[j] = q1[j];
+        }
+      }
+    }
+    buf ^= 1;
+  }
+  float* glow = D.ws + L.glow;
+  if constexpr (NB > 0) {
+    store_acc(a00, glow, C, mb0, n0 + l32, r, C, hi);
+    store_acc(a01, glow, C, mb0, n0 + 32 + l32, r, C, hi);
+  }
+  if constexpr (act1) {
+    store_acc(a10, glow, C, mb0 + 32, n0 + l32, r, C, hi);
+    store_acc(a11, glow, C, mb0 + 32, n0 + 32 + l32, r, C, hi);
+  }
+  if (!pass0) return;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    double x = cs[j];
+    x += __shfl_xor(x, 8, 64);
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
+    cs[j] = x;
+  }
+  if (l < 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sred[w * 64 + l * 8 + j] = cs[j];
+  }
+  __syncthreads();
+  double t = 0.0;
+  if (w == 0) {
+    const double s = ((sred[l] + sred[64 + l]) + sred[128 + l]) + sred[192 + l];
+    if (n0 + l < C) {
+      gp(D.ws + L.ngsq)[n0 + l] = norm_sq(s);
+      t = s;
+    }
+    t = grp_sum_d(t, 64);
+  }
+  if (lane == 0) ws_d_set(D.ws, L.gpart, ct, t);
+}
+
 // Workgroups are dealt to the 8 XCDs round-robin by index, each XCD with its own
 // L2.  Consecutive projection tiles of a matrix share its P split (3 x 2 r K
 // bytes, ~3 MB at r = 256, K = 2048), so tile order is remapped to give each XCD
@@ -738,6 +1037,50 @@ void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
   }
 }
 
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_ap_proj_r32(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[3 * kApPlaneR];
+  __shared__ double sred[8];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 0, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t row0 = (local % L.ntr) * kApTile;
+  const bool full = D.valign && row0 + kApTile <= D.R && D.C % 64 == 0;
+  const int64_t cb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
+  const int nb = cb0 + 32 < L.rp ? 2 : (cb0 < L.rp ? 1 : 0);   // uniform per wave
+  if (full) {
+    if (nb == 2) proj_right32<true, 2>(D, L, local, lds, sred);
+    else if (nb == 1) proj_right32<true, 1>(D, L, local, lds, sred);
+    else proj_right32<true, 0>(D, L, local, lds, sred);
+  } else {
+    if (nb == 2) proj_right32<false, 2>(D, L, local, lds, sred);
+    else if (nb == 1) proj_right32<false, 1>(D, L, local, lds, sred);
+    else proj_right32<false, 0>(D, L, local, lds, sred);
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_ap_proj_l32(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t ldsT[3 * kApPlaneL];
+  __shared__ double sred[4 * 64 + 4];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 1, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApL L = ap_layout(D.R, D.C, D.r);
+  const int64_t n0 = (local % L.ntr) * kApTile;
+  const bool full = D.valign && n0 + kApTile <= D.C && D.R % 32 == 0;
+  const int64_t mb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
+  const int nb = mb0 + 32 < L.rp ? 2 : (mb0 < L.rp ? 1 : 0);   // uniform per wave
+  if (full) {
+    if (nb == 2) proj_left32<true, 2>(D, L, local, ldsT, sred);
+    else if (nb == 1) proj_left32<true, 1>(D, L, local, ldsT, sred);
+    else proj_left32<true, 0>(D, L, local, ldsT, sred);
+  } else {
+    if (nb == 2) proj_left32<false, 2>(D, L, local, ldsT, sred);
+    else if (nb == 1) proj_left32<false, 1>(D, L, local, ldsT, sred);
+    else proj_left32<false, 0>(D, L, local, ldsT, sred);
+  }
+}
+
 // ------------------------------------------------------------ ||p||^2 (scale_parameter)
 // ntr workgroups per matrix, each summing a contiguous share of p^2 in double;
 // only the total (k_ap_scalars) is used.
@@ -756,97 +1099,6 @@ __global__ __launch_bounds__(256) void k_ap_psq(ApDesc D) {
   }
   s = ap_wg_sum(s, sd);
   if (threadIdx.x == 0) ws_d_set(D.ws, L.ppart, blockIdx.x, s);
-}
-
-// ------------------------------------------------------------ fp32 G: norms and flags
-// One workgroup per 64 rows (right) / 64 columns (left): ||G_ch||^2, ||G||^2 and
-// ||p||^2 partials, and whether a non-finite entry was seen (the library GEMM
-// reads G as given; k_ap_fixlow then recomputes g_low from the scrubbed G).
-__global__ __launch_bounds__(256) void k_ap_norm32(ApDesc D, int scale_param) {
-  __shared__ double sd[4 * 64 + 4];
-  const ApL L = ap_layout(D.R, D.C, D.r);
-  const int64_t R = D.R, C = D.C;
-  const float* G = reinterpret_cast<const float*>(D.grad);
-  const float* P = reinterpret_cast<const float*>(D.param);
-  const int lane = threadIdx.x, w = lane >> 6, l = lane & 63;
-  const int64_t t = blockIdx.x;
-  bool nonfin = false;
-  double tg = 0.0, tp = 0.0;
-  if (R >= C) {
-    for (int i = 0; i < kApTile / 4; ++i) {
-      const int64_t row = t * kApTile + w * (kApTile / 4) + i;
-      if (row >= R) break;
-      double s = 0.0, sp = 0.0;
-      for (int64_t c = l; c < C; c += 64) {
-        const float g = gp(G)[row * C + c];
-        nonfin |= !__builtin_isfinite(g);
-        const float gs = scrub(g);
-        s += (double)(gs * gs);
-        if (scale_param) {
-          const float p = gp(P)[row * C + c];
-          sp += (double)(p * p);
-        }
-      }
-      s = grp_sum_d(s, 64);
-      if (l == 0) gp(D.ws + L.ngsq)[row] = norm_sq(s);
-      tg += (l == 0) ? s : 0.0;
-      tp += sp;
-    }
-  } else {
-    const int64_t c = t * kApTile + l;
-    double s = 0.0;
-    if (c < C) {
-      for (int64_t row = w; row < R; row += 4) {
-        const float g = gp(G)[row * C + c];
-        nonfin |= !__builtin_isfinite(g);
-        const float gs = scrub(g);
-        s += (double)(gs * gs);
-        if (scale_param) {
-          const float p = gp(P)[row * C + c];
-          tp += (double)(p * p);
-        }
-      }
-    }
-    sd[w * 64 + l] = s;
-    __syncthreads();
-    if (w == 0 && c < C) {
-      const double cs = ((sd[l] + sd[64 + l]) + sd[128 + l]) + sd[192 + l];
-      gp(D.ws + L.ngsq)[c] = norm_sq(cs);
-      tg = cs;
-    }
-    __syncthreads();
-  }
-  const double sg = ap_wg_sum(tg, sd + 256);
-  const double sp = ap_wg_sum(tp, sd + 256);
-  const int nf = __syncthreads_or(nonfin ? 1 : 0);
-  if (lane == 0) {
-    ws_d_set(D.ws, L.gpart, t, sg);
-    ws_d_set(D.ws, L.ppart, t, sp);
-    gp(reinterpret_cast<int*>(D.ws + L.nfpart))[t] = nf ? 1 : 0;
-  }
-}
-
-// With a finite G every workgroup returns after reading the flags.
-__global__ __launch_bounds__(256) void k_ap_fixlow(ApDesc D) {
-  const ApL L = ap_layout(D.R, D.C, D.r);
-  const int lane = threadIdx.x;
-  int f = 0;
-  for (int64_t k = lane; k < L.ntr; k += 256) f |= gp(reinterpret_cast<const int*>(D.ws + L.nfpart))[k];
-  if (!__syncthreads_or(f)) return;
-  const int64_t R = D.R, C = D.C, r = D.r;
-  const float* G = reinterpret_cast<const float*>(D.grad);
-  const float* pt = D.proj_t;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + lane; i < L.n_low; i += (int64_t)gridDim.x * 256) {
-    float acc = 0.0f;
-    if (R >= C) {
-      const int64_t row = i / r, k = i - row * r;
-      for (int64_t c = 0; c < C; ++c) acc = __builtin_fmaf(scrub(gp(G)[row * C + c]), gp(pt)[c * r + k], acc);
-    } else {
-      const int64_t k = i / C, j = i - k * C;
-      for (int64_t q = 0; q < R; ++q) acc = __builtin_fmaf(gp(pt)[k * R + q], scrub(gp(G)[q * C + j]), acc);
-    }
-    gp(D.ws + L.glow)[i] = acc;
-  }
 }
 
 // ------------------------------------------------------------ low-rank V / M and u
@@ -1471,38 +1723,6 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
 hipError_t apollo_upload_qmap(const float* q8, const float* q4) { return upload_qmap_tu(q8, q4); }
 
 // ------------------------------------------------------------ rocBLAS (fp32 G)
-static rocblas_handle g_blas[64];
-
-static int blas_handle(rocblas_handle* out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(A8_ERR_HIP, "hipGetDevice");
-  if (!g_blas[dev]) {
-    if (rocblas_create_handle(&g_blas[dev]) != rocblas_status_success)
-      return set_error(A8_ERR_HIP, "rocblas_create_handle failed");
-    rocblas_set_pointer_mode(g_blas[dev], rocblas_pointer_mode_host);
-  }
-  *out = g_blas[dev];
-  return 0;
-}
-
-// g_low = G P^T (right) or P^T G (left), row-major, through column-major GEMMs:
-// right: g_low^T (r x R) = PT^T (r x C) . G^T (C x R); left: g_low^T (C x r) = G^T . PT^T.
-static int ap_sgemm(rocblas_handle hb, const ApDesc& D, const ApL& L, hipStream_t st) {
-  const int64_t R = D.R, C = D.C, r = D.r;
-  const float one = 1.0f, zero = 0.0f;
-  float* glow = D.ws + L.glow;
-  rocblas_set_stream(hb, st);
-  rocblas_status s;
-  if (R >= C)
-    s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)r, (rocblas_int)R,
-                      (rocblas_int)C, &one, D.proj_t, (rocblas_int)r, reinterpret_cast<const float*>(D.grad),
-                      (rocblas_int)C, &zero, glow, (rocblas_int)r);
-  else
-    s = rocblas_sgemm(hb, rocblas_operation_none, rocblas_operation_none, (rocblas_int)C, (rocblas_int)r,
-                      (rocblas_int)R, &one, reinterpret_cast<const float*>(D.grad), (rocblas_int)C, D.proj_t,
-                      (rocblas_int)R, &zero, glow, (rocblas_int)C);
-  return s == rocblas_status_success ? 0 : set_error(A8_ERR_HIP, "rocblas_sgemm failed");
-}
 
 template <int VB>
 static void launch_low(int mkt, unsigned nb, const ApDesc& one, const ApDesc* tab, int ntab, const ApHyp& h,
@@ -1530,8 +1750,6 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
                       int upload, const a8_step_scalars* dsc, void* stream) {
   if (n <= 0) return 0;
   if (!ts) return set_error(A8_ERR_ARG, "null tensor list");
-  if (dsc && dtype != A8_BF16)
-    return set_error(A8_ERR_DTYPE, "APOLLO with step_scalars (device-scheduled projection) needs bf16 params");
   if (dtype != A8_F32 && dtype != A8_BF16 && dtype != A8_F16 && dtype != A8_F64)
     return set_error(A8_ERR_DTYPE, "APOLLO supports fp32, bf16, fp16 and fp64 params");
   if (v_bits != 0 && v_bits != 8 && v_bits != 16) return set_error(A8_ERR_ARG, "v_bits must be 0, 8 or 16");
@@ -1617,8 +1835,9 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
   // projection (+ channel norms of G)
   if (phase >= 2) {
     // the projection ran in phase 1
-  } else if (dtype == A8_BF16) {
-    if (dsc) {   // the projection schedule on the device: refresh decision, then P^T and its split
+  } else {
+    // P^T's split: on the device schedule (capturable steps), or when a record says it changed
+    if (dsc) {
       hipLaunchKernelGGL(k_ap_decide, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, st, one, dtab, n, dsc);
       if ((rc = check_launch("k_ap_decide"))) return rc;
       hipLaunchKernelGGL(k_ap_pgen, dim3((unsigned)(n * kPGen)), dim3(256), 0, st, one, dtab, n);
@@ -1633,38 +1852,27 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
                          (int)(D.R >= D.C), L.rp, L.Kp, reinterpret_cast<u32x4*>(D.ws + L.psplit));
       if ((rc = check_launch("k_ap_split"))) return rc;
     }
+    // g_low = G P^T / P^T G with the channel norms of G: bf16 G as it is, fp32 G in three terms
+    const bool g16 = dtype == A8_BF16;
     if (nrt > 0) {
-      hipLaunchKernelGGL(k_ap_proj_r, dim3((unsigned)nrt), dim3(256), 0, st, one, dtab, n);
+      if (g16) hipLaunchKernelGGL(k_ap_proj_r, dim3((unsigned)nrt), dim3(256), 0, st, one, dtab, n);
+      else hipLaunchKernelGGL(k_ap_proj_r32, dim3((unsigned)nrt), dim3(256), 0, st, one, dtab, n);
       if ((rc = check_launch("k_ap_proj_r"))) return rc;
     }
     if (nlt > 0) {
-      hipLaunchKernelGGL(k_ap_proj_l, dim3((unsigned)nlt), dim3(256), 0, st, one, dtab, n);
+      if (g16) hipLaunchKernelGGL(k_ap_proj_l, dim3((unsigned)nlt), dim3(256), 0, st, one, dtab, n);
+      else hipLaunchKernelGGL(k_ap_proj_l32, dim3((unsigned)nlt), dim3(256), 0, st, one, dtab, n);
       if ((rc = check_launch("k_ap_proj_l"))) return rc;
     }
-    if (h.scale_param) {
+    if (h.scale_param) {   // ||p||^2 of the parameter (fp64 parameters refuse scale_parameter above)
       for (int i = 0; i < n; ++i) {
         const ApDesc& D = tab[(size_t)i];
-        hipLaunchKernelGGL(k_ap_psq<__hip_bfloat16>, dim3((unsigned)ap_layout(D.R, D.C, D.r).ntr), dim3(256), 0, st, D);
+        const dim3 grid((unsigned)ap_layout(D.R, D.C, D.r).ntr);
+        if (dtype == A8_BF16) hipLaunchKernelGGL(k_ap_psq<__hip_bfloat16>, grid, dim3(256), 0, st, D);
+        else if (dtype == A8_F16) hipLaunchKernelGGL(k_ap_psq<__half>, grid, dim3(256), 0, st, D);
+        else hipLaunchKernelGGL(k_ap_psq<float>, grid, dim3(256), 0, st, D);
         if ((rc = check_launch("k_ap_psq"))) return rc;
       }
-    }
-  } else {
-    rocblas_handle hb;
-    if ((rc = blas_handle(&hb))) return rc;
-    for (int i = 0; i < n; ++i) {
-      const ApDesc& D = tab[(size_t)i];
-      const ApL L = ap_layout(D.R, D.C, D.r);
-      if ((rc = ap_sgemm(hb, D, L, st))) return rc;
-      hipLaunchKernelGGL(k_ap_norm32, dim3((unsigned)L.ntr), dim3(256), 0, st, D,
-                         dtype == A8_F32 ? h.scale_param : 0);
-      if ((rc = check_launch("k_ap_norm32"))) return rc;
-      if (dtype == A8_F16 && h.scale_param) {   // ||p||^2 of the fp16 parameter (after k_ap_norm32's zeros)
-        hipLaunchKernelGGL(k_ap_psq<__half>, dim3((unsigned)L.ntr), dim3(256), 0, st, D);
-        if ((rc = check_launch("k_ap_psq"))) return rc;
-      }
-      const int64_t nf = (L.n_low + 255) / 256;
-      hipLaunchKernelGGL(k_ap_fixlow, dim3((unsigned)(nf < 1024 ? nf : 1024)), dim3(256), 0, st, D);
-      if ((rc = check_launch("k_ap_fixlow"))) return rc;
     }
   }
   if (phase == 1) return 0;

@@ -106,24 +106,27 @@ APOLLO = dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, factored=Fal
 
 
 APOLLO_VARIANTS = {"apollo": APOLLO, "apollo_factorize": dict(APOLLO, apollo_factorize=True),
-                   "apollo_came": dict(APOLLO, beta3=0.9999, d=1.0, eps_came=1e-16)}
+                   "apollo_came": dict(APOLLO, beta3=0.9999, d=1.0, eps_came=1e-16),
+                   "apollo_fp32": APOLLO}   # fp32 parameters (the reference's published APOLLO setting)
 
 
-def apollo_step_bytes_flops(shapes, rank=256, bs=2048, mbs=256):
-    """Algorithmic bytes and projection flops of one APOLLO step (C4, bf16).
-    Per matrix element: g read by the projection and by the writeback, p read
-    and written = 8 B.  Per low-rank element (R*r or r*C): V code r+w and M code
-    r+w = 4 B, plus their block scales; per matrix the fp32 P^T (4 r K B).  The
-    projection is 2 R C r flops.  The 1-D vectors (bf16 p, fp32 V and M): 22 B."""
+def apollo_step_bytes_flops(shapes, rank=256, bs=2048, mbs=256, pbytes=2):
+    """Algorithmic bytes and projection flops of one APOLLO step (C4; pbytes 2 for
+    bf16, 4 for fp32 parameters).  Per matrix element: g read by the projection
+    and by the writeback, p read and written = 4 pbytes.  Per low-rank element
+    (R*r or r*C): V code r+w and M code r+w = 4 B, plus their block scales; per
+    matrix the fp32 P^T (4 r K B).  The projection is 2 R C r flops (three bf16
+    terms of P, six products for fp32 G, on MFMA).  The 1-D vectors (p and g,
+    fp32 V and M): 3 pbytes + 16 B."""
     nbytes = flops = 0.0
     for s in shapes:
         if len(s) < 2:
-            nbytes += 22.0 * s[0]
+            nbytes += (3.0 * pbytes + 16.0) * s[0]
             continue
         R, C = s
         right = R >= C
         n_low = (R if right else C) * rank
-        nbytes += 8.0 * R * C + 4.0 * n_low + n_low * (8.0 / bs + 8.0 / mbs) + 4.0 * rank * (C if right else R)
+        nbytes += 4.0 * pbytes * R * C + 4.0 * n_low + n_low * (8.0 / bs + 8.0 / mbs) + 4.0 * rank * (C if right else R)
         flops += 2.0 * R * C * rank
     return nbytes, flops
 
@@ -191,7 +194,7 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
     elif workload == "came":
         shape, gk, kw = (2048, 2048), "logscale", dict(CAME)
     elif workload.startswith("apollo"):
-        shape, pdt = (2048, 2048), torch.bfloat16
+        shape, pdt = (2048, 2048), (torch.float32 if workload == "apollo_fp32" else torch.bfloat16)
         kw = dict(APOLLO_VARIANTS[workload], stochastic_round_writeback=False)
     p = torch.nn.Parameter(make_param(shape, 0, 0).to(pdt))
     opt = F.OracleOptimizer([p], **kw)
@@ -220,7 +223,8 @@ def cpu_baseline(workload="adamw", seconds_budget=20.0):
             "came": "C3: one 2048x2048 fp32 CAME UF8/AL16/AL16+Fira step",
             "apollo": "C4: one 2048x2048 bf16 APOLLO r=256 UF8/AL8 step (deterministic writeback)",
             "apollo_factorize": "one 2048x2048 bf16 factorised APOLLO r=256 step (deterministic writeback)",
-            "apollo_came": "one 2048x2048 bf16 CAME APOLLO r=256 step (deterministic writeback)"}[workload]
+            "apollo_came": "one 2048x2048 bf16 CAME APOLLO r=256 step (deterministic writeback)",
+            "apollo_fp32": "one 2048x2048 fp32 APOLLO r=256 UF8/AL8 step"}[workload]
     return {"value": n / med, "unit": "params/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{what}, median of {len(times)} after 2 warm-ups", "ms_per_step": med * 1e3}
 
@@ -250,7 +254,7 @@ def main():
                     help="after timing, run a plain 256 MiB fp32 copy (for counter calibration)")
     ap.add_argument("--workload", default="adamw",
                     choices=["adamw", "adafactor", "came", "apollo", "adamw_llama3_8b", "apollo_factorize",
-                             "apollo_came"],
+                             "apollo_came", "apollo_fp32"],
                     help="adamw (default, the headline metric), adafactor (C2), came (C3), apollo (C4) or "
                          "adamw_llama3_8b (C5)")
     args = ap.parse_args()
@@ -268,7 +272,7 @@ def main():
     params = []
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    pdt = torch.bfloat16 if args.workload.startswith("apollo") else torch.float32
+    pdt = torch.bfloat16 if (args.workload.startswith("apollo") and args.workload != "apollo_fp32") else torch.float32
     for i, s in enumerate(shapes):
         if len(s) == 1:
             p = torch.ones(s, device=dev)
@@ -385,7 +389,7 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
     # APOLLO, the device projection schedule): timed eagerly, then as replays of one
     # captured step; the factorised and CAME APOLLO stages take host scalars and
     # run eagerly only
-    graphable = args.workload in ("adafactor", "came", "apollo")
+    graphable = args.workload in ("adafactor", "came", "apollo", "apollo_fp32")
     opt = Adafactor8Bit(params, **(dict(kw, capturable=True) if graphable else kw))
     for _ in range(args.warmup):
         opt.step()
@@ -420,14 +424,14 @@ def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
         mode = "graph replay of one captured step() (capturable=True)"
     flops = None
     if apollo:
-        nbytes, flops = apollo_step_bytes_flops(shapes)
+        nbytes, flops = apollo_step_bytes_flops(shapes, pbytes=4 if args.workload == "apollo_fp32" else 2)
     else:
         nbytes = factored_step_bytes(shapes, args.workload)
     achieved = nbytes / (gms * 1e-3) / 1e9
     name = {"adafactor": "adafactor_factored_al8_bv256", "came": "came_uf8_al16_al16_fira_bv2048",
             "apollo": "apollo_r256_uf8_al8_sr", "apollo_factorize": "apollo_factorize_r256_uf8_sr",
-            "apollo_came": "apollo_came_r256_uf8_al8_sr"}[args.workload]
-    dt = "bf16" if apollo else "fp32"
+            "apollo_came": "apollo_came_r256_uf8_al8_sr", "apollo_fp32": "apollo_r256_uf8_al8"}[args.workload]
+    dt = "bf16" if (apollo and args.workload != "apollo_fp32") else "fp32"
     out = {
         "metric": "fused step params/sec + achieved HBM GB/s (% of peak), " + args.workload + " @1.1B params",
         "value": nparams / (ms * 1e-3), "unit": "params/s", "n_gpus": 1, "steps": args.steps,

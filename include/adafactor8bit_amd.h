@@ -351,7 +351,8 @@ int64_t a8_table_bytes_2d(int ntensors);
 typedef struct a8_apollo_tensor {
   void* param;             /* fp32, bf16, fp16 or fp64, rows x cols */
   const void* grad;        /* same dtype as param; fp32 for fp16 and fp64 params (the
-                              reference projects grad.float(), optimizer.py:2601) */
+                              reference projects grad.float(), optimizer.py:2601).  The
+                              projection runs on MFMA for bf16 and fp32 G alike */
   int64_t rows, cols;
   const float* proj_t;     /* projection P^T, fp32: right side (rows >= cols) [cols x rank],
                               left side [rank x rows] (P = stable_randn / sqrt(rank)) */
@@ -423,7 +424,7 @@ int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int
  * split with a8_apollo_proj_gen's generator; fresh = 2 set by the caller rebuilds
  * only the split from proj_t.  proj_fresh, step and bias_factor of the records are
  * then not read, so a step so launched can be captured in a HIP graph and
- * replayed.  bf16 parameters only with step_scalars. */
+ * replayed. */
 int a8_apollo_step_multi(int dtype, int stochastic, const a8_apollo_tensor* tensors, int ntensors,
                          void* table_dev, int64_t table_bytes, double beta_val, double beta1, int has_m,
                          float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits, int m_mode,

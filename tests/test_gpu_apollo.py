@@ -5,16 +5,25 @@ Golden trajectories (apollo_* fixtures, made by the reference's own
 ``inputs.make_proj``, which the test installs in the same place).
 
 The projection g_low = G P^T (right side, R >= C) or P^T G (left side) is a
-GEMM: the HIP path sums its K products in rocBLAS's order, the reference in
-its CPU BLAS's order.  On the right-side matrices of these fixtures the two
-orders agree bit for bit.  On the left side the two results differ at the
-ulp level.  That is why the tolerances below are looser than the 1-D path's:
+GEMM: the HIP path sums its K products on MFMA (P^T, and fp32 G, split into
+bf16 terms whose products are exact in the fp32 accumulator), the reference in
+its CPU BLAS's order, so the two results differ at the ulp level.  That is why
+the tolerances below are looser than the 1-D path's.  Where an element of g_low
+is a cancelling sum, its relative error -- bounded by b / |g_low| with
+b = 2 (3K + 2) u sum |g||p| for the two GEMMs -- passes into the states built on
+it; those elements (and, at step 1, the V block ranges set by them) are held to
+that bound (_GemmCond), everything else to the fixed tolerances:
 
 * V codes (AL8, low rank): every decoded value within two code steps
-  (2^(2 s / 254) - 1, relative) of the reference's decoded value.  At most 2%
-  of codes may differ, by at most 2.  The block's range is set by its smallest
-  nonzero g_low^2, which can be a cancelling sum with a large relative error.
-  So block scale / min_log are held to 2e-2 absolute (log2 units).
+  (2^(2 s / 254) - 1, relative) of the reference's decoded value, widened by
+  the difference of the two block ranges (|dl_min| + |ds| in log2 units), and by
+  4 rel for elements of an ill-conditioned g_low.  Codes differ by at most 2,
+  and on at most 2% of the elements of blocks whose ranges agree to half a code
+  step (a moved range shifts its block's codes together).  The block's range is
+  set by its smallest nonzero g_low^2, which can be a cancelling sum with a large
+  relative error: block scale / min_log are held to 2e-2 absolute (log2 units),
+  or, for a block beyond that, to the step-1 GEMM error envelope (at step 1) or
+  its width (later steps, whose EMA remembers step 1).
 * M codes: at most 2% differ, by at most 2.  Block scales within rtol 1e-5.
 * Parameters (fp32): within 1e-5 relative plus 2e-3 of the largest
   displacement the reference's own steps made.  A flipped code moves one
@@ -116,6 +125,54 @@ def _al_decode(q, scale, min_log):
 AL_STATS = ("v_low", "res_low", "conf_row_low", "conf_col_low")
 
 
+class _GemmCond:
+    """Per-element conditioning of g_low over a fixture's steps: for an APOLLO
+    matrix with projection P^T and step-s gradient G, x = G P^T (or P^T G) in
+    float64, b = 2 (3K + 2) u sum |g||p| (the HIP and the CPU GEMM each within
+    (3K + 2) u sum |g||p|), and rel = min(b / |x|, 1), the largest relative error
+    either GEMM can leave in an element.  ``cond`` keeps its maximum over the
+    steps seen so far; ``v1_envelope`` gives, per AL block of g_low^2 * beta_v at
+    step 1, the interval l_min and scale can take."""
+
+    def __init__(self):
+        self.cond, self.first = {}, {}
+
+    def add(self, key, g, pt):
+        G = _f32(_t2np(g)).astype(np.float64) if g.dtype == torch.bfloat16 else g.double().numpy()
+        P = pt.double().cpu().numpy()
+        R, C = G.shape
+        right = R >= C
+        K = C if right else R
+        x = G @ P if right else P @ G
+        b = 2 * (3 * K + 2) * 2.0 ** -24 * (np.abs(G) @ np.abs(P) if right else np.abs(P) @ np.abs(G))
+        rel = np.minimum(b / np.maximum(np.abs(x), 1e-300), 1.0).reshape(-1)
+        self.cond[key] = rel if key not in self.cond else np.maximum(self.cond[key], rel)
+        if key not in self.first:
+            self.first[key] = (np.abs(x).reshape(-1), b.reshape(-1))
+
+    def v1_envelope(self, key, bs, bv):
+        x, b = self.first[key]
+        lo = (np.maximum(x - b, 0.0) ** 2 * bv).reshape(-1, bs)
+        hi = ((x + b) ** 2 * bv).reshape(-1, bs)
+        with np.errstate(divide="ignore"):
+            lmin = (np.log2(lo.min(axis=1)), np.log2(hi.min(axis=1)))
+            lmax = (np.log2(lo.max(axis=1)), np.log2(hi.max(axis=1)))
+        return lmin, (lmax[0] - lmin[1], lmax[1] - lmin[0])
+
+
+def _close(mine, ref, rtol, atol, msg, cond=None):
+    """|mine - ref| <= rtol |ref| + atol (+ 4 cond |ref| for elements of an
+    ill-conditioned g_low, cond from _GemmCond)."""
+    m, r = np.asarray(mine, np.float64).reshape(-1), np.asarray(ref, np.float64).reshape(-1)
+    tol = rtol * np.abs(r) + atol
+    if cond is not None and cond.size == r.size:
+        tol = tol + 4.0 * cond * np.abs(r)
+    bad = ~(np.abs(m - r) <= tol)
+    if bad.any():
+        i = int(np.argmax(np.where(bad, np.abs(m - r) - tol, -np.inf)))
+        raise AssertionError(f"{msg}: {int(bad.sum())} of {r.size} beyond tolerance, e.g. {m[i]!r} vs {r[i]!r}")
+
+
 def _cmp_params(name, key, mine, ref, init, frac=1e-2):
     disp = float(np.abs(_f32(ref).astype(np.float64) - _f32(init)).max())
     if ref.dtype == np.int16:
@@ -135,7 +192,7 @@ def _cmp_params(name, key, mine, ref, init, frac=1e-2):
         np.testing.assert_allclose(mine, ref, rtol=1e-5, atol=1e-8 + 2e-3 * disp, err_msg=f"{name} {key} param")
 
 
-def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None):
+def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None, gc=None, pkey=None, step=None, bv1=None):
     extended = name.startswith(("apollo_came", "apollo_fact"))
     if norm_rtol is None:
         norm_rtol = 1e-4 if (extended or name.startswith("apollo_fp16")) else 3e-5
@@ -157,11 +214,30 @@ def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None):
             pre = k[:-2]
             dm, levels = _al_decode(mine, st[pre + "_scale"].cpu().numpy(), st[pre + "_min_log"].cpu().numpy())
             dr, _ = _al_decode(ref, z[f"{key}/{pre}_scale"], z[f"{key}/{pre}_min_log"])
-            step2 = np.exp2(2.0 * z[f"{key}/{pre}_scale"].astype(np.float64) / (levels - 2))[:, None] - 1.0
+            # two code steps of the reference's block, widened by the difference of the two
+            # block ranges (log2 v = l_min + (q - 1) s / L moves by at most |dl| + |ds|)
+            sref = z[f"{key}/{pre}_scale"].astype(np.float64)
+            drange = (np.abs(st[pre + "_scale"].cpu().numpy().astype(np.float64) - sref)
+                      + np.abs(st[pre + "_min_log"].cpu().numpy().astype(np.float64)
+                               - z[f"{key}/{pre}_min_log"].astype(np.float64)))
+            step2 = np.exp2(2.0 * sref / (levels - 2) + drange)[:, None] - 1.0
             slack = 1e-3 if extended else 0.0
-            assert np.all(np.abs(dm - dr) <= (step2 + slack) * np.abs(dr) + 1e-37), f"{msg}: decoded values"
+            if gc is not None and pkey in gc.cond and gc.cond[pkey].size == dr.size:
+                slack = slack + 4.0 * gc.cond[pkey].reshape(dr.shape)   # V = EMA of g_low^2
+            bad = ~(np.abs(dm - dr) <= (step2 + slack) * np.abs(dr) + 1e-37)
+            if bad.any():
+                i = np.argwhere(bad)[0]
+                c = gc.cond[pkey].reshape(dr.shape)[tuple(i)] if (gc is not None and pkey in gc.cond) else None
+                raise AssertionError(f"{msg}: decoded values: {int(bad.sum())} beyond, e.g. at {tuple(i)} "
+                                     f"{dm[tuple(i)]!r} vs {dr[tuple(i)]!r} (codes {int(np.asarray(mine).reshape(dr.shape)[tuple(i)])} "
+                                     f"vs {int(np.asarray(ref).reshape(dr.shape)[tuple(i)])}, cond {c})")
             if pre == "v_low" and levels == 256:
-                frac, mx = gu.code_mismatch(mine, ref)
+                # the share of differing codes counts blocks whose ranges agree to half a code
+                # step; a block whose range moved shifts its codes together (decoded check above)
+                _, mx = gu.code_mismatch(mine, ref)
+                keep = drange < 0.5 * sref / 254.0
+                qa, qb = np.asarray(mine).reshape(sref.size, -1), np.asarray(ref).reshape(sref.size, -1)
+                frac = gu.code_mismatch(qa[keep], qb[keep])[0] if keep.any() else 0.0
                 assert mx <= 2 and frac <= 2e-2, f"{msg}: {frac:.2e} codes differ, max {mx}"
         elif k.endswith("_q"):
             frac, mx = gu.code_mismatch(mine, ref)
@@ -169,7 +245,22 @@ def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None):
             allowed = 2e-2 if low_rank else 1e-4 + 1.0 / max(mine.size, 1)
             assert mx <= 2 and frac <= allowed, f"{msg}: {frac:.2e} codes differ, max {mx}"
         elif k.startswith("v_low_") and (k.endswith("_scale") or k.endswith("_min_log")):
-            np.testing.assert_allclose(mine, ref, rtol=0, atol=2e-2, err_msg=msg)
+            off = np.abs(mine.astype(np.float64) - ref) > 2e-2
+            if off.any() and gc is not None and pkey in gc.first:
+                # a block whose range moved further: at step 1 both ranges lie in the GEMM
+                # error envelope; later steps (an EMA that remembers step 1) stay within its width
+                bs = ref.size and gc.first[pkey][0].size // ref.size
+                env = gc.v1_envelope(pkey, bs, bv1)[0 if k.endswith("_min_log") else 1]
+                if step == 1:
+                    for v in (mine.astype(np.float64), ref.astype(np.float64)):
+                        assert np.all((v[off] >= env[0][off] - 1e-5) & (v[off] <= env[1][off] + 1e-5)), \
+                            f"{msg}: outside the GEMM error envelope"
+                else:
+                    width = (env[1] - env[0])[off]
+                    assert np.all(np.abs(mine.astype(np.float64) - ref)[off] <= width + 1e-5), \
+                        f"{msg}: beyond the step-1 GEMM envelope's width"
+            else:
+                np.testing.assert_allclose(mine, ref, rtol=0, atol=2e-2, err_msg=msg)
         elif k.startswith(AL_STATS[1:]) and (k.endswith("_scale") or k.endswith("_min_log")):
             pass   # a block of equal values: see the module doc (decoded values are checked)
         elif k == "m_low_scale":
@@ -182,7 +273,7 @@ def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None):
             assert int(mine) == int(ref), msg
         elif extended:
             floor = 1e-5 * float(np.abs(ref).max()) if ref.size else 0.0
-            np.testing.assert_allclose(mine, ref, rtol=1e-3, atol=1e-30 + floor, err_msg=msg)
+            _close(mine, ref, 1e-3, 1e-30 + floor, msg, gc.cond.get(pkey) if gc is not None else None)
         else:
             floor = 1e-6 * float(np.abs(ref).max()) if ref.size else 0.0
             np.testing.assert_allclose(mine, ref, rtol=fp32_rtol.get(k, 2e-6), atol=1e-30 + floor, err_msg=msg)
@@ -197,10 +288,18 @@ def test_apollo_matches_golden(name, multi, det_proj):
     print(f"[apollo golden] {name} multi={multi}", flush=True)
     params = gu.init_params(meta, device="cuda")
     opt = Adafactor8Bit(params if multi else [{"params": [p]} for p in params], **kw)
+    gc = _GemmCond()
+    beta2, bdec = kw.get("beta2"), kw.get("beta2_decay", -0.8)
+    bv1 = float(np.float32(1.0 - beta2)) if beta2 is not None else 1.0   # step 1: 1^beta2_decay
     for t in range(1, meta["steps"] + 1):
-        for p, g in zip(params, gu.grads_for(meta, params, t)):
+        grads = gu.grads_for(meta, params, t)
+        for p, g in zip(params, grads):
             p.grad = g.cuda()
         opt.step()
+        for i, (p, g) in enumerate(zip(params, grads)):
+            pt = opt.state[p].get("apollo_proj_matrix_T")
+            if p.dim() == 2 and pt is not None:
+                gc.add(i, g.float() if g.dtype == torch.float16 else g, pt)
         if t not in meta["save_steps"]:
             continue
         torch.cuda.synchronize()
@@ -210,7 +309,7 @@ def test_apollo_matches_golden(name, multi, det_proj):
             frac = 0.1 if (p.dim() == 1 and kw.get("weight_decay", 0.0)) else 1e-2
             _cmp_params(name, key, _t2np(p), z[f"{key}/param"], z[f"init/p{i}"], frac)
             zkeys = [k[len(key) + 1:] for k in z.files if k.startswith(key + "/") and not k.endswith("/param")]
-            _cmp_state(name, key, opt.state[p], z, zkeys)
+            _cmp_state(name, key, opt.state[p], z, zkeys, gc=gc, pkey=i, step=t, bv1=bv1)
 
 
 def _apollo_kw(**over):

@@ -14,7 +14,7 @@ the host schedule (stable_randn); later refreshes use the device generator
   those within one fp32 ulp: double log / cos of two libraries);
 * at C4's settings (rank 256, B_V 2048, B_M 256, UF8 / AL8, channel scale, Fira,
   bf16 parameters with SR, one right-side and one left-side matrix plus an fp32-
-  state vector, apollo_update_proj_gap=3), graph replays across two projection
+  state vector, apollo_update_proj_gap=3; fp32 parameters too), graph replays across two projection
   refreshes equal eager capturable steps bit for bit, P^T after a device refresh
   is the generator's for the new seed, and the schedule's state (apollo_seed,
   current_proj_seed, last_proj_step) equals the default path's;
@@ -76,9 +76,9 @@ def test_device_projection_generator_matches_oracle(rows, cols, rank):
     _assert_ulp1(pt.cpu().numpy(), ref, f"{rows}x{cols} r{rank}")
 
 
-def _setup(capturable):
+def _setup(capturable, dtype=torch.bfloat16):
     from adafactor8bit import Adafactor8Bit
-    ps = [torch.nn.Parameter(make_param(s, i, 29).to("cuda", torch.bfloat16)) for i, s in enumerate(SHAPES)]
+    ps = [torch.nn.Parameter(make_param(s, i, 29).to("cuda", dtype)) for i, s in enumerate(SHAPES)]
     for p in ps:
         p.grad = torch.zeros_like(p)   # static gradient buffers
     return ps, Adafactor8Bit(ps, **dict(C4_CAP, capturable=capturable))
@@ -86,7 +86,7 @@ def _setup(capturable):
 
 def _load(ps, t):
     for i, p in enumerate(ps):
-        p.grad.copy_(make_grad(tuple(p.shape), i, t, 29, zero_frac=0.0).to(torch.bfloat16))
+        p.grad.copy_(make_grad(tuple(p.shape), i, t, 29, zero_frac=0.0).to(p.dtype))
 
 
 def _same(oa, ob, pa, pb, what):
@@ -107,10 +107,11 @@ def _schedule(opt, ps):
 
 
 @pytest.mark.gpu
-def test_apollo_graph_replays_equal_eager_steps_across_refreshes():
-    print("[apollo capture] C4 settings, gap 3", flush=True)
-    pa, oa = _setup(True)   # replayed
-    pb, ob = _setup(True)   # eager
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_apollo_graph_replays_equal_eager_steps_across_refreshes(dtype):
+    print(f"[apollo capture] C4 settings, gap 3, {dtype}", flush=True)
+    pa, oa = _setup(True, dtype)   # replayed
+    pb, ob = _setup(True, dtype)   # eager
     for t in (1, 2):
         for ps, o in ((pa, oa), (pb, ob)):
             _load(ps, t)

@@ -168,9 +168,9 @@ def test_tensor_lr_scheduled_between_replays(name, kw, shapes):
 
 @pytest.mark.gpu
 def test_capturable_rejects_paths_with_host_scalars():
-    print("[capturable] APOLLO rejected", flush=True)
-    ps, o = _setup(dict(ADAMW, apollo_rank=8, block_size=128, m_block_size=32), [(64, 96)], torch.float32,
-                   capturable=True)
+    print("[capturable] factorised APOLLO rejected", flush=True)
+    ps, o = _setup(dict(ADAMW, apollo_rank=8, apollo_factorize=True, block_size=128, m_block_size=32), [(64, 96)],
+                   torch.float32, capturable=True)
     ps[0].grad.copy_(make_grad((64, 96), 0, 1, 17))
     with pytest.raises(NotImplementedError, match="APOLLO"):
         o.step()

@@ -37,7 +37,9 @@ namespace a8 {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kApTile = 64;     // G rows (right) / G columns (left) per projection tile
+constexpr int kApTile = 64;     // G columns per left-side projection tile (and fp32 G's right-side tile)
+constexpr int kApRB = 3;        // 32-row blocks per right-side bf16 projection tile
+constexpr int kApTileR = 32 * kApRB;   // G rows per right-side bf16 projection tile
 constexpr int kApPass = 256;    // low-rank outputs per projection pass (4 waves x 64)
 constexpr int kApUnit = 2048;   // low-rank elements per k_ap_low workgroup (8 per lane)
 constexpr int kApScR = 16;      // right side: g_low rows per k_ap_scale workgroup
@@ -51,7 +53,8 @@ struct ApL {
   int64_t glow, u, ngsq, fin, scal, gpart, ppart, spart, psplit, total;
 };
 
-__host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
+// trows: G rows per right-side projection tile (kApTileR for bf16 G, kApTile for fp32 G).
+__host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r, int64_t trows) {
   ApL w;
   const bool right = R >= C;
   w.n_low = (right ? R : C) * r;
@@ -59,7 +62,8 @@ __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r) {
   w.K = right ? C : R;                     // reduction length of the projection
   w.Kp = (w.K + 63) / 64 * 64;
   w.rp = (r + 31) / 32 * 32;
-  w.ntr = (w.nchg + kApTile - 1) / kApTile;
+  const int64_t tile = right ? trows : kApTile;
+  w.ntr = (w.nchg + tile - 1) / tile;
   w.npass = (w.rp + kApPass - 1) / kApPass;
   w.ntile = w.ntr * w.npass;
   w.nunit = (w.n_low + kApUnit - 1) / kApUnit;
@@ -102,6 +106,8 @@ struct ApDesc {
   int32_t first, has_prev, valign;
   int32_t rtile_begin, ltile_begin, unit_begin, sc_begin, app_begin, gap;
   int64_t* pstate;   // device projection schedule {last_proj_step, seed, current seed, fresh}, or null
+  int32_t trows;     // G rows per right-side projection tile (kApTileR: bf16 G; kApTile: fp32 G)
+  int32_t pad_;
 };
 static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
 
@@ -352,7 +358,7 @@ __global__ __launch_bounds__(256) void k_ap_pgen(ApDesc one, const ApDesc* tab, 
   if (!D.pstate) return;
   const int64_t fresh = gp(D.pstate)[3];
   if (fresh == 0) return;
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const bool right = D.R >= D.C;
   const int64_t r = D.r, K = L.K, nblk = L.rp / 32, nkc = L.Kp / 32, nu = nblk * nkc * 128;
   u32x4* out = reinterpret_cast<u32x4*>(D.ws + L.psplit);
@@ -429,41 +435,50 @@ __device__ __forceinline__ float sq8f(u32x4 q) {
 constexpr int kApGS = 72;   // LDS row stride (halves) of the right side's 64-row x 64-k G slab
 constexpr int kApTS = 40;   // LDS row stride (halves) of the left side's transposed 32-row slab
 
-// Right side: tile = 64 rows of G x 256 outputs (one pass); wave w owns outputs
-// [64w, 64w + 64) of the pass as two 32-column blocks (NB of them active).
-// Each 64-k slab of the tile's G rows is loaded once per workgroup with row
-// loads (eight lanes per 128-byte row segment, two rows per lane), scrubbed,
-// squared into the row norms and stored to LDS (double buffered); the MFMA A
-// fragments come from LDS, the B fragments (P) from the fragment-ordered split.
-// FULL: all 64 rows exist, K % 64 == 0 and rows are 16-byte aligned.
+// Right side: tile = kApTileR rows of G (kApRB blocks of 32) x 256 outputs (one
+// pass); wave w owns outputs [64w, 64w + 64) of the pass as two 32-column blocks
+// (NB of them active), for every row block of the tile.  Each 64-k slab of the
+// tile's G rows is loaded once per workgroup with row loads (eight lanes per
+// 128-byte row segment, kApRB rows per lane), scrubbed, squared into the row
+// norms and stored to LDS (double buffered); the MFMA A fragments come from LDS,
+// the B fragments (P) from the fragment-ordered split.  A wave's B fragments
+// serve all kApRB row blocks, so the split P streamed through L1 per MFMA falls
+// as the tile grows.  FULL: all rows exist, K % 64 == 0 and rows are 16-byte
+// aligned.
 template <bool FULL, int NB>
 __device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int tile, uint16_t* lds, double* sred) {
+  constexpr int RB = kApRB;
   const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
   const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
   const int pass = (int)(tile / L.ntr);
   const int64_t rt = tile - (int64_t)pass * L.ntr;
   const int64_t R = D.R, C = D.C, r = D.r, K = C;
-  const int64_t row0 = rt * kApTile;
+  const int64_t row0 = rt * kApTileR;
   const int64_t cb0 = (int64_t)pass * kApPass + w * 64;
   constexpr bool act1 = NB >= 2;
   const int64_t nblk = L.rp / 32, nkc = L.Kp / 32;
   const int64_t blk0 = cb0 / 32;
   const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
   const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
-  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: rows lr and lr + 32, k chunk lc
-  const int64_t ga = row0 + lr, gb = row0 + lr + 32;
+  const int lr = lane >> 3, lc = (lane & 7) * 8;   // loader: rows lr + 32 q, k chunk lc
   const bool pass0 = pass == 0;
-  f32x16 a00 = {}, a01 = {}, a10 = {}, a11 = {};
-  double na = 0.0, nb = 0.0;
-  auto ldG = [&](int64_t k0, u32x4& x, u32x4& y) {
-    if constexpr (FULL) {
-      x = ldu(G + k0, (uint32_t)((ga * C + lc) * 2));
-      y = ldu(G + k0, (uint32_t)((gb * C + lc) * 2));
-    } else {
-      const int64_t k = k0 + lc;
-      const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
-      x = ldg8(G, ga * C + k, ga < R ? cnt : 0, D.valign);
-      y = ldg8(G, gb * C + k, gb < R ? cnt : 0, D.valign);
+  f32x16 acc0[RB], acc1[RB];
+#pragma unroll
+  for (int q = 0; q < RB; ++q) { acc0[q] = f32x16{}; acc1[q] = f32x16{}; }
+  double nr[RB];
+#pragma unroll
+  for (int q = 0; q < RB; ++q) nr[q] = 0.0;
+  auto ldG = [&](int64_t k0, u32x4* x) {
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int64_t ga = row0 + lr + 32 * q;
+      if constexpr (FULL) {
+        x[q] = ldu(G + k0, (uint32_t)((ga * C + lc) * 2));
+      } else {
+        const int64_t k = k0 + lc;
+        const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
+        x[q] = ldg8(G, ga * C + k, ga < R ? cnt : 0, D.valign);
+      }
     }
   };
   auto ldB = [&](int64_t kc, int t, u32x4* x0, u32x4* x1) {
@@ -473,31 +488,34 @@ __device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int ti
       if constexpr (act1) x1[j] = gp(Ps)[psw_unit(t, blk0 + 1, kc, j, l, nblk, nkc)];
     }
   };
-  u32x4 fx, fy;   // the next slab's G, prefetched
-  ldG(0, fx, fy);
+  u32x4 f[RB];   // the next slab's G, prefetched
+  ldG(0, f);
   u32x4 b0[2], b1[2], c0[2], c1[2];
   if constexpr (NB > 0) ldB(0, 0, b0, b1);
   int buf = 0;
   for (int64_t k0 = 0; k0 < K; k0 += 64) {
-    const u32x4 x = scrub8(fx), y = scrub8(fy);
-    if (k0 + 64 < K) ldG(k0 + 64, fx, fy);
+    u32x4 x[RB];
+#pragma unroll
+    for (int q = 0; q < RB; ++q) x[q] = scrub8(f[q]);
+    if (k0 + 64 < K) ldG(k0 + 64, f);
     if (pass0) {
-      na += (double)sq8f(x);
-      nb += (double)sq8f(y);
+#pragma unroll
+      for (int q = 0; q < RB; ++q) nr[q] += (double)sq8f(x[q]);
     }
-    uint16_t* sl = lds + buf * (kApTile * kApGS);
-    *reinterpret_cast<u32x4*>(&sl[lr * kApGS + lc]) = x;
-    *reinterpret_cast<u32x4*>(&sl[(lr + 32) * kApGS + lc]) = y;
+    uint16_t* sl = lds + buf * (kApTileR * kApGS);
+#pragma unroll
+    for (int q = 0; q < RB; ++q) *reinterpret_cast<u32x4*>(&sl[(lr + 32 * q) * kApGS + lc]) = x[q];
     __syncthreads();   // the slab is in LDS; the other buffer's readers finished a barrier ago
     if constexpr (NB > 0) {
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
         const int64_t kcg = k0 / 32 + kc;
-        u32x4 ar0[2], ar1[2];
+        u32x4 ar[RB][2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          ar0[j] = *reinterpret_cast<const u32x4*>(&sl[l32 * kApGS + 32 * kc + 16 * hi + 8 * j]);
-          ar1[j] = *reinterpret_cast<const u32x4*>(&sl[(32 + l32) * kApGS + 32 * kc + 16 * hi + 8 * j]);
+        for (int q = 0; q < RB; ++q) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            ar[q][j] = *reinterpret_cast<const u32x4*>(&sl[(32 * q + l32) * kApGS + 32 * kc + 16 * hi + 8 * j]);
         }
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
@@ -508,11 +526,10 @@ __device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int ti
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            a00 = mfma(as_bf8(ar0[j]), as_bf8(b0[j]), a00);
-            a10 = mfma(as_bf8(ar1[j]), as_bf8(b0[j]), a10);
-            if constexpr (act1) {
-              a01 = mfma(as_bf8(ar0[j]), as_bf8(b1[j]), a01);
-              a11 = mfma(as_bf8(ar1[j]), as_bf8(b1[j]), a11);
+#pragma unroll
+            for (int q = 0; q < RB; ++q) {
+              acc0[q] = mfma(as_bf8(ar[q][j]), as_bf8(b0[j]), acc0[q]);
+              if constexpr (act1) acc1[q] = mfma(as_bf8(ar[q][j]), as_bf8(b1[j]), acc1[q]);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -527,26 +544,22 @@ __device__ __forceinline__ void proj_right(const ApDesc& D, const ApL& L, int ti
     buf ^= 1;
   }
   float* glow = D.ws + L.glow;
-  if constexpr (NB > 0) {
-    store_acc(a00, glow, r, row0, cb0 + l32, R, r, hi);
-    store_acc(a10, glow, r, row0 + 32, cb0 + l32, R, r, hi);
-  }
-  if constexpr (act1) {
-    store_acc(a01, glow, r, row0, cb0 + 32 + l32, R, r, hi);
-    store_acc(a11, glow, r, row0 + 32, cb0 + 32 + l32, R, r, hi);
+#pragma unroll
+  for (int q = 0; q < RB; ++q) {
+    if constexpr (NB > 0) store_acc(acc0[q], glow, r, row0 + 32 * q, cb0 + l32, R, r, hi);
+    if constexpr (act1) store_acc(acc1[q], glow, r, row0 + 32 * q, cb0 + 32 + l32, R, r, hi);
   }
   if (!pass0) return;
   // row norms: the eight lanes of a row (consecutive lanes) combine
-  na += __shfl_xor(na, 1, 64);
-  na += __shfl_xor(na, 2, 64);
-  na += __shfl_xor(na, 4, 64);
-  nb += __shfl_xor(nb, 1, 64);
-  nb += __shfl_xor(nb, 2, 64);
-  nb += __shfl_xor(nb, 4, 64);
   double t = 0.0;
-  if ((lane & 7) == 0) {
-    if (ga < R) { gp(D.ws + L.ngsq)[ga] = norm_sq(na); t += na; }
-    if (gb < R) { gp(D.ws + L.ngsq)[gb] = norm_sq(nb); t += nb; }
+#pragma unroll
+  for (int q = 0; q < RB; ++q) {
+    double nq = nr[q];
+    nq += __shfl_xor(nq, 1, 64);
+    nq += __shfl_xor(nq, 2, 64);
+    nq += __shfl_xor(nq, 4, 64);
+    const int64_t ga = row0 + lr + 32 * q;
+    if ((lane & 7) == 0 && ga < R) { gp(D.ws + L.ngsq)[ga] = norm_sq(nq); t += nq; }
   }
   t = ap_wg_sum(t, sred);
   if (lane == 0) ws_d_set(D.ws, L.gpart, rt, t);
@@ -994,13 +1007,13 @@ __device__ __forceinline__ int xcd_order(int b, int nwg) {
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void k_ap_proj_r(ApDesc one, const ApDesc* tab, int ntab) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kApTile * kApGS];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kApTileR * kApGS];
   __shared__ double sred[8];
   int local;
   const ApDesc D = ap_pick(one, tab, ntab, 0, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
-  const ApL L = ap_layout(D.R, D.C, D.r);
-  const int64_t row0 = (local % L.ntr) * kApTile;
-  const bool full = D.valign && row0 + kApTile <= D.R && D.C % 64 == 0;
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
+  const int64_t row0 = (local % L.ntr) * kApTileR;
+  const bool full = D.valign && row0 + kApTileR <= D.R && D.C % 64 == 0;
   const int64_t cb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
   const int nb = cb0 + 32 < L.rp ? 2 : (cb0 < L.rp ? 1 : 0);   // uniform per wave
   // every wave runs the slab loop (it holds the workgroup barriers)
@@ -1021,7 +1034,7 @@ void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
   __shared__ double sred[4 * 64 + 4];
   int local;
   const ApDesc D = ap_pick(one, tab, ntab, 1, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t n0 = (local % L.ntr) * kApTile;
   const bool full = D.valign && n0 + kApTile <= D.C && D.R % 32 == 0;
   const int64_t mb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
@@ -1043,7 +1056,7 @@ void k_ap_proj_r32(ApDesc one, const ApDesc* tab, int ntab) {
   __shared__ double sred[8];
   int local;
   const ApDesc D = ap_pick(one, tab, ntab, 0, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t row0 = (local % L.ntr) * kApTile;
   const bool full = D.valign && row0 + kApTile <= D.R && D.C % 64 == 0;
   const int64_t cb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
@@ -1065,7 +1078,7 @@ void k_ap_proj_l32(ApDesc one, const ApDesc* tab, int ntab) {
   __shared__ double sred[4 * 64 + 4];
   int local;
   const ApDesc D = ap_pick(one, tab, ntab, 1, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t n0 = (local % L.ntr) * kApTile;
   const bool full = D.valign && n0 + kApTile <= D.C && D.R % 32 == 0;
   const int64_t mb0 = (int64_t)(local / L.ntr) * kApPass + (threadIdx.x >> 6) * 64;
@@ -1087,7 +1100,7 @@ void k_ap_proj_l32(ApDesc one, const ApDesc* tab, int ntab) {
 template <typename T>
 __global__ __launch_bounds__(256) void k_ap_psq(ApDesc D) {
   __shared__ double sd[4];
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t n = D.R * D.C;
   const int64_t chunk = (n + L.ntr - 1) / L.ntr;
   const int64_t b = (int64_t)blockIdx.x * chunk, e = b + chunk < n ? b + chunk : n;
@@ -1379,7 +1392,7 @@ __global__ __launch_bounds__(256) void k_ap_low(ApDesc one, const ApDesc* tab, i
   __shared__ float dtab[4 * 256];
   int unit;
   const ApDesc D = ap_pick(one, tab, ntab, 2, (int)blockIdx.x, unit);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   ApHyp hh = h;
   if (hh.dsc) hh.bv = (float)load_step_scalars(hh.dsc).beta_val;
   if ((int64_t)(unit + 1) * kApUnit <= L.n_low && (L.u & 3) == 0) ap_low_unit<VB, MK, true>(D, L, unit, hh, xw, dtab);
@@ -1397,7 +1410,7 @@ __global__ __launch_bounds__(256) void k_ap_scale(ApDesc one, const ApDesc* tab,
   __shared__ double sd[2 * 256 + 4];
   int wg;
   const ApDesc D = ap_pick(one, tab, ntab, 3, (int)blockIdx.x, wg);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t R = D.R, C = D.C, r = D.r;
   const float* U = D.ws + L.u;
   const float* GL = D.ws + L.glow;
@@ -1491,7 +1504,7 @@ __global__ __launch_bounds__(256) void k_ap_scalars(ApDesc one, const ApDesc* ta
     __builtin_memcpy(&D, buf, sizeof(ApDesc));
   }
   (void)ntab;
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   float* ws = D.ws;
   const int lane = threadIdx.x;
   double pg = 0.0, pp = 0.0, s0 = 0.0, s1 = 0.0, s2 = 0.0;
@@ -1587,7 +1600,7 @@ template <typename T, bool SR, typename GT = T>
 __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab, int ntab, ApHyp h) {
   int unit;
   const ApDesc D = ap_pick(one, tab, ntab, 4, (int)blockIdx.x, unit);
-  const ApL L = ap_layout(D.R, D.C, D.r);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const uint32_t R = (uint32_t)D.R, C = (uint32_t)D.C, n = R * C;   // n < 2^31
   const bool right = R >= C;
   const float* ws = D.ws;
@@ -1780,9 +1793,11 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       return set_error(A8_ERR_ARG, "APOLLO with step_scalars needs each record's proj_state and proj_gap > 0");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.workspace))
       return set_error(A8_ERR_ALIGN, "APOLLO param, grad and workspace must be 16-byte aligned");
-    const ApL L = ap_layout(t.rows, t.cols, t.rank);
+    const int64_t trows = dtype == A8_BF16 ? kApTileR : kApTile;
+    const ApL L = ap_layout(t.rows, t.cols, t.rank, trows);
     ApDesc& D = tab[(size_t)i];
     D.grad = t.grad; D.param = t.param; D.ws = t.workspace; D.proj_t = t.proj_t;
+    D.trows = (int32_t)trows; D.pad_ = 0;
     D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_fp32 = t.v_fp32;
     D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
     D.fira_prev = t.fira_prev; D.lr = t.lr;
@@ -1846,7 +1861,7 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     for (int i = 0; i < n && !dsc; ++i) {
       if (!ts[i].proj_fresh) continue;
       const ApDesc& D = tab[(size_t)i];
-      const ApL L = ap_layout(D.R, D.C, D.r);
+      const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
       const int64_t nb = (L.rp * L.Kp / 8 + 255) / 256;
       hipLaunchKernelGGL(k_ap_split, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, D.proj_t, D.r, L.K,
                          (int)(D.R >= D.C), L.rp, L.Kp, reinterpret_cast<u32x4*>(D.ws + L.psplit));
@@ -1867,7 +1882,7 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     if (h.scale_param) {   // ||p||^2 of the parameter (fp64 parameters refuse scale_parameter above)
       for (int i = 0; i < n; ++i) {
         const ApDesc& D = tab[(size_t)i];
-        const dim3 grid((unsigned)ap_layout(D.R, D.C, D.r).ntr);
+        const dim3 grid((unsigned)ap_layout(D.R, D.C, D.r, D.trows).ntr);
         if (dtype == A8_BF16) hipLaunchKernelGGL(k_ap_psq<__hip_bfloat16>, grid, dim3(256), 0, st, D);
         else if (dtype == A8_F16) hipLaunchKernelGGL(k_ap_psq<__half>, grid, dim3(256), 0, st, D);
         else hipLaunchKernelGGL(k_ap_psq<float>, grid, dim3(256), 0, st, D);
@@ -1911,7 +1926,9 @@ extern "C" {
 int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int channel) {
   (void)channel;
   if (rows <= 0 || cols <= 0 || rank <= 0) return 0;
-  return ap_layout(rows, cols, rank).total;
+  // either tile height (the dtype is not known here): the larger workspace
+  const int64_t a = ap_layout(rows, cols, rank, kApTileR).total, b = ap_layout(rows, cols, rank, kApTile).total;
+  return a > b ? a : b;
 }
 
 int64_t a8_apollo_table_bytes(int ntensors) { return ntensors > 0 ? table_bytes(ntensors) : 0; }

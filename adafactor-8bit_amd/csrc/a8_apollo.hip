@@ -47,13 +47,24 @@ constexpr int kApScL = 64;      // left side: g_low columns per k_ap_scale workg
 constexpr int kApRuns = 2;      // runs of eight elements per k_ap_apply lane (4 measured slower)
 constexpr int kApApp = 2048 * kApRuns;   // matrix elements per k_ap_apply workgroup
 
+constexpr int kApWide = 256;     // channels per wide projection tile (bf16 G, rank % 256 == 0)
+static_assert(kApWide == kApPass, "a wide tile covers one output pass");
+
+// G channels per projection tile of a matrix: wide tiles for bf16 G at ranks
+// that are a multiple of 256, else kApTileR rows (bf16, right side) or kApTile.
+__host__ __device__ inline int64_t ap_tile(bool g16, int64_t R, int64_t C, int64_t r) {
+  if (g16 && r % kApWide == 0) return kApWide;
+  return (g16 && R >= C) ? kApTileR : kApTile;
+}
+
 // Workspace of one matrix (offsets in floats; partial arrays hold doubles).
 struct ApL {
   int64_t n_low, nchg, K, Kp, rp, ntr, npass, ntile, nunit, nsc, napp;
   int64_t glow, u, ngsq, fin, scal, gpart, ppart, spart, psplit, total;
 };
 
-// trows: G rows per right-side projection tile (kApTileR for bf16 G, kApTile for fp32 G).
+// trows: G channels (rows on the right side, columns on the left) per projection
+// tile, as ap_tile picks it.
 __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r, int64_t trows) {
   ApL w;
   const bool right = R >= C;
@@ -62,7 +73,7 @@ __host__ __device__ inline ApL ap_layout(int64_t R, int64_t C, int64_t r, int64_
   w.K = right ? C : R;                     // reduction length of the projection
   w.Kp = (w.K + 63) / 64 * 64;
   w.rp = (r + 31) / 32 * 32;
-  const int64_t tile = right ? trows : kApTile;
+  const int64_t tile = trows;
   w.ntr = (w.nchg + tile - 1) / tile;
   w.npass = (w.rp + kApPass - 1) / kApPass;
   w.ntile = w.ntr * w.npass;
@@ -106,8 +117,8 @@ struct ApDesc {
   int32_t first, has_prev, valign;
   int32_t rtile_begin, ltile_begin, unit_begin, sc_begin, app_begin, gap;
   int64_t* pstate;   // device projection schedule {last_proj_step, seed, current seed, fresh}, or null
-  int32_t trows;     // G rows per right-side projection tile (kApTileR: bf16 G; kApTile: fp32 G)
-  int32_t pad_;
+  int32_t trows;     // G channels per projection tile (see ap_tile)
+  int32_t wtile_begin;
 };
 static_assert(sizeof(ApDesc) % 8 == 0, "descriptor is loaded as 64-bit words");
 
@@ -226,14 +237,16 @@ __device__ __forceinline__ float norm_sq(double s) {
 // The projection's P operand (rows of P: output index n, reduction index k) in
 // three bf16 terms hi + mid + lo = the fp32 value exactly, stored in MFMA
 // fragment order so that one wave's fragment load is 1 KB of contiguous memory:
-// 16-byte unit u = (((t * nblk + blk) * nkc + kc) * 2 + j) * 64 + l holds
+// 16-byte unit u = (((kc * 3 + t) * nblk + blk) * 2 + j) * 64 + l holds
 // P[32 blk + l % 32][32 kc + 16 (l / 32) + 8 j .. +8] of term t (zero padded to
 // rp x Kp).  With lane half hi = l / 32 holding k = 16 hi + 8 j, sub-step j of
 // a 32-k chunk takes the same k permutation on both operands, which leaves the
-// sum unchanged.
+// sum unchanged.  A 32-k chunk's units are contiguous per term, so a wide tile
+// copies a chunk's eight output blocks as three 16 KB runs.
 __device__ __forceinline__ int64_t psw_unit(int64_t t, int64_t blk, int64_t kc, int j, int l, int64_t nblk,
                                             int64_t nkc) {
-  return (((t * nblk + blk) * nkc + kc) * 2 + j) * 64 + l;
+  (void)nkc;
+  return (((kc * 3 + t) * nblk + blk) * 2 + j) * 64 + l;
 }
 
 // One 16-byte unit u of the split (three terms), from P^T values pv(row, k).
@@ -692,6 +705,209 @@ __device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int til
   if (lane == 0) ws_d_set(D.ws, L.gpart, ct, t);
 }
 
+// ------------------------------------------------------------ MFMA projection, wide tiles
+// bf16 G at ranks that are a multiple of 256 (C4's rank 256): a workgroup
+// computes a 256-channel x 256-output tile of g_low (channels: G rows on the
+// right side, G columns on the left), each wave a 128 x 128 quarter as 4 x 4
+// MFMA blocks in accumulator registers.  Per 32-k slab the workgroup stages both
+// operands in LDS, double buffered: G, scrubbed, as [channel][k] rows, and the
+// chunk's split P for the tile's eight output blocks (fragment order, a plain
+// copy).  A wave then issues 48 MFMAs per 16 fragment reads, and each P unit is
+// fetched from L2 once per 256 channels: 6 bytes of split P per G element (the
+// narrower tiles above fetch it per wave, 16 bytes per element at 96 rows).  The
+// global loads of slab s + 1 are in flight while slab s is multiplied; one
+// barrier per slab publishes the next.  Lane i also sums the squares of channel
+// i from the staged slab (k order, double), for the channel norms.  FULL: all
+// 256 channels exist, K % 32 == 0 and rows are 16-byte aligned.
+constexpr int kApW = kApWide;             // channels and outputs of a wide tile
+constexpr int kApWS = 40;                 // LDS row stride (halves) of the G slab: 32 k + 8 pad
+constexpr int kApWGh = kApW * kApWS;      // halves per G slab buffer (20 KB)
+constexpr int kApWPu = 3 * 8 * 2 * 64;    // 16-byte P units per slab: 3 terms x 8 blocks x 2 j x 64 lanes (48 KB)
+
+template <bool RIGHT, bool FULL>
+__device__ __forceinline__ void proj_wide(const ApDesc& D, const ApL& L, int tile, uint16_t* gsl, u32x4* psl,
+                                          double* sred) {
+  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
+  const int gh = w >> 1, oh = w & 1;   // the wave's channel half and output half
+  const int pass = (int)(tile / L.ntr);
+  const int64_t gt = tile - (int64_t)pass * L.ntr;
+  const int64_t R = D.R, C = D.C, r = D.r;
+  const int64_t K = RIGHT ? C : R, nch = RIGHT ? R : C;
+  const int64_t ch0 = gt * kApW;
+  const int64_t nblk = L.rp / 32;
+  const int64_t nslab = (K + 31) / 32;
+  const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const bool pass0 = pass == 0;
+  // G loader.  Right: rows (lane >> 2) + 64 i, eight k at 8 (lane & 3).  Left:
+  // k rows 2 (lane & 15) and + 1, eight columns at 8 ((lane >> 4) + 16 i), stored
+  // transposed as pairs of k in one 32-bit word.
+  auto ldG1 = [&](int64_t k0, int i) -> u32x4 {
+    if constexpr (RIGHT) {
+      const int64_t row = ch0 + (lane >> 2) + 64 * i, k = k0 + 8 * (lane & 3);
+      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + k) * 2));
+      const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
+      return ldg8(G, row * C + k, row < R ? cnt : 0, D.valign);
+    } else {
+      const int64_t row = k0 + 2 * (lane & 15) + (i & 1), col = ch0 + 8 * ((lane >> 4) + 16 * (i >> 1));
+      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + col) * 2));
+      const int cnt = C - col >= 8 ? 8 : (C - col > 0 ? (int)(C - col) : 0);
+      return ldg8(G, row * C + col, row < K ? cnt : 0, D.valign);
+    }
+  };
+  auto stG = [&](const u32x4* f, uint16_t* sl) {
+    if constexpr (RIGHT) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4*>(&sl[((lane >> 2) + 64 * i) * kApWS + 8 * (lane & 3)]) = scrub8(f[i]);
+    } else {
+      const int kp = 2 * (lane & 15);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 a = scrub8(f[2 * h]), b = scrub8(f[2 * h + 1]);   // k rows kp, kp + 1
+        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+        const int c0 = 8 * ((lane >> 4) + 16 * h);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t lo = (e & 1) ? (wa[e >> 1] >> 16) : (wa[e >> 1] & 0xFFFFu);
+          const uint32_t hv = (e & 1) ? (wb[e >> 1] & 0xFFFF0000u) : (wb[e >> 1] << 16);
+          *reinterpret_cast<uint32_t*>(&sl[(c0 + e) * kApWS + kp]) = lo | hv;
+        }
+      }
+    }
+  };
+  // P: units lane + 256 i of the slab's 3072 (term i / 4)
+  auto ldP1 = [&](int64_t kc, int i) -> u32x4 {
+    return gp(Ps)[((kc * 3 + (i >> 2)) * nblk + 8 * pass) * 128 + lane + 256 * (i & 3)];
+  };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[q][c] = f32x16{};
+  double nsq = 0.0;   // squares of channel ch0 + lane
+  u32x4 fg[4], fp[12];   // the next slab, between its loads and its LDS stores
+  // One slab from LDS buffer b, 96 MFMAs.  With one wave per SIMD nothing else
+  // fills the MFMA pipe, so the wave's other instructions are spread one or two
+  // per MFMA in a fixed order (scheduling fences): a burst of loads or LDS
+  // accesses would stall the in-order instruction stream and drain the pipe.
+  //   before MFMA 0: the fragments MFMAs 0-3 need and the first channel-row read;
+  //   sub-step 0 (MFMAs 0-47): after MFMA m, the square of channel element m
+  //     (m < 32); after even m an LDS read (the remaining P fragments, channel-row
+  //     reads, sub-step 1's P fragments, G fragment 0 of sub-step 1), after odd m
+  //     one of the next slab's 16 global loads (NEXT), then sub-step 1's G reads;
+  //   sub-step 1 (MFMAs 48-95): after every third MFMA one of the next slab's
+  //     16 LDS stores (the 12 P units, then the G rows).
+  auto slab = [&](const int b, const int64_t kn, auto next) {
+    constexpr bool NEXT = decltype(next)::value;
+    const uint16_t* gs = gsl + b * kApWGh;
+    const u32x4* ps = psl + b * kApWPu;
+    uint16_t* gn = gsl + (b ^ 1) * kApWGh;
+    u32x4* pn = psl + (b ^ 1) * kApWPu;
+    u32x4 ga[2][4], pb[3][4], pc1[3][4], cr[2];
+    auto rdG = [&](int j, int q) {
+      return *reinterpret_cast<const u32x4*>(&gs[(gh * 128 + 32 * q + l32) * kApWS + 16 * hi + 8 * j]);
+    };
+    auto rdP = [&](int j, int t, int c) { return ps[((t * 8 + oh * 4 + c) * 2 + j) * 64 + l]; };
+    auto rdC = [&](int g) { return *reinterpret_cast<const u32x4*>(&gs[lane * kApWS + 8 * g]); };
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ga[0][q] = rdG(0, q);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) pb[0][c] = rdP(0, 0, c);
+    cr[0] = rdC(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < 48; ++m) {
+      const int t = m / 16, c = (m / 4) % 4, q = m % 4;
+      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[0][q]), as_bf8(pb[t][c]), acc[q][c]);
+      else acc[q][c] = mfma(as_bf8(pb[t][c]), as_bf8(ga[0][q]), acc[q][c]);
+      if (m < 32) {
+        const uint32_t wv = cr[(m / 8) & 1][(m / 2) % 4];
+        const float x = __uint_as_float((m & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
+        nsq += (double)(x * x);
+      }
+      const int a = m / 2;
+      if (m % 2 == 0) {
+        // even slots: cr1, P(t=1) x4, cr2, P(t=2) x4, cr3, sub-step 1's P x12, its G 0
+        if (a == 0) cr[1] = rdC(1);
+        else if (a <= 4) pb[1][a - 1] = rdP(0, 1, a - 1);
+        else if (a == 5) cr[0] = rdC(2);
+        else if (a <= 9) pb[2][a - 6] = rdP(0, 2, a - 6);
+        else if (a == 10) cr[1] = rdC(3);
+        else if (a <= 22) pc1[(a - 11) / 4][(a - 11) % 4] = rdP(1, (a - 11) / 4, (a - 11) % 4);
+        else ga[1][0] = rdG(1, 0);
+      } else {
+        // odd slots: the next slab's P units and G chunks, then sub-step 1's G 1-3
+        if (a < 12) {
+          if constexpr (NEXT) fp[a] = ldP1(kn, a);
+        } else if (a < 16) {
+          if constexpr (NEXT) fg[a - 12] = ldG1(32 * kn, a - 12);
+        } else if (a < 19) {
+          ga[1][a - 15] = rdG(1, a - 15);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int m = 0; m < 48; ++m) {
+      const int t = m / 16, c = (m / 4) % 4, q = m % 4;
+      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[1][q]), as_bf8(pc1[t][c]), acc[q][c]);
+      else acc[q][c] = mfma(as_bf8(pc1[t][c]), as_bf8(ga[1][q]), acc[q][c]);
+      if constexpr (NEXT) {
+        if (m % 3 == 0) {
+          const int pc = m / 3;
+          if (pc < 12) {
+            pn[lane + 256 * pc] = fp[pc];
+          } else if constexpr (RIGHT) {
+            const int i = pc - 12;
+            *reinterpret_cast<u32x4*>(&gn[((lane >> 2) + 64 * i) * kApWS + 8 * (lane & 3)]) = scrub8(fg[i]);
+          } else {
+            const int h = (pc - 12) >> 1, eh = (pc - 12) & 1, kp = 2 * (lane & 15);
+            const u32x4 a = scrub8(fg[2 * h]), bq = scrub8(fg[2 * h + 1]);   // k rows kp, kp + 1
+            const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {bq.x, bq.y, bq.z, bq.w};
+            const int c0 = 8 * ((lane >> 4) + 16 * h);
+#pragma unroll
+            for (int e = 4 * eh; e < 4 * eh + 4; ++e) {
+              const uint32_t lo = (e & 1) ? (wa[e >> 1] >> 16) : (wa[e >> 1] & 0xFFFFu);
+              const uint32_t hv = (e & 1) ? (wb[e >> 1] & 0xFFFF0000u) : (wb[e >> 1] << 16);
+              *reinterpret_cast<uint32_t*>(&gn[(c0 + e) * kApWS + kp]) = lo | hv;
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fg[i] = ldG1(0, i);
+#pragma unroll
+  for (int i = 0; i < 12; ++i) psl[lane + 256 * i] = ldP1(0, i);
+  stG(fg, gsl);
+  __syncthreads();
+  // slab s's LDS stores go to the other buffer, whose readers finished slab s - 1
+  // before the last barrier
+  for (int64_t s = 0; s + 1 < nslab; ++s) {
+    slab((int)(s & 1), s + 1, std::true_type{});
+    __syncthreads();
+  }
+  slab((int)((nslab - 1) & 1), nslab, std::false_type{});
+  float* glow = D.ws + L.glow;
+  const int64_t gx0 = ch0 + gh * 128, ox0 = (int64_t)pass * kApW + oh * 128;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (RIGHT) store_acc(acc[q][c], glow, r, gx0 + 32 * q, ox0 + 32 * c + l32, R, r, hi);
+      else store_acc(acc[q][c], glow, C, ox0 + 32 * c, gx0 + 32 * q + l32, r, C, hi);
+    }
+  if (!pass0) return;
+  const int64_t ch = ch0 + lane;
+  if (ch < nch) gp(D.ws + L.ngsq)[ch] = norm_sq(nsq);
+  const double t = ap_wg_sum(ch < nch ? nsq : 0.0, sred);
+  if (lane == 0) ws_d_set(D.ws, L.gpart, gt, t);
+}
+
 // ------------------------------------------------------------ MFMA projection (fp32 G)
 // fp32 G (fp32 parameters; fp16 / fp64 ones project grad.float()) takes the same
 // tiles with G split as P is: hi + mid + lo bf16 terms that sum to the fp32 value
@@ -1047,6 +1263,24 @@ void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
     if (nb == 2) proj_left<false, 2>(D, L, local, ldsT, sred);
     else if (nb == 1) proj_left<false, 1>(D, L, local, ldsT, sred);
     else proj_left<false, 0>(D, L, local, ldsT, sred);
+  }
+}
+
+// Wide tiles of both sides (one workgroup per CU: 136 KB of LDS).
+__global__ __launch_bounds__(256) void k_ap_proj_w(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t gsl[2 * kApWGh];
+  __shared__ u32x4 psl[2 * kApWPu];
+  __shared__ double sred[8];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 5, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
+  const int64_t ch0 = (local % L.ntr) * kApW;
+  if (D.R >= D.C) {
+    if (D.valign && ch0 + kApW <= D.R && D.C % 32 == 0) proj_wide<true, true>(D, L, local, gsl, psl, sred);
+    else proj_wide<true, false>(D, L, local, gsl, psl, sred);
+  } else {
+    if (D.valign && ch0 + kApW <= D.C && D.R % 32 == 0) proj_wide<false, true>(D, L, local, gsl, psl, sred);
+    else proj_wide<false, false>(D, L, local, gsl, psl, sred);
   }
 }
 
@@ -1748,7 +1982,7 @@ static void launch_low(int mkt, unsigned nb, const ApDesc& one, const ApDesc* ta
   }
 }
 
-static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 5 * sizeof(int32_t)); }
+static int64_t table_bytes(int n) { return (int64_t)n * (int64_t)(sizeof(ApDesc) + 6 * sizeof(int32_t)); }
 
 // phase 0: the whole step; 1: projection (and the norms of G) only, leaving
 // g_low in workspace[0, n_low); 2: scale, scalars and writeback from the update
@@ -1777,8 +2011,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     return set_error(A8_ERR_ARG, "scale_parameter is not available for fp64 APOLLO parameters");
   if (stochastic && (dtype == A8_F32 || dtype == A8_F64)) stochastic = 0;
   std::vector<ApDesc> tab((size_t)n);
-  std::vector<int32_t> first((size_t)5 * n);
-  int64_t nrt = 0, nlt = 0, nunit = 0, nsc = 0, napp = 0;
+  std::vector<int32_t> first((size_t)6 * n);
+  int64_t nrt = 0, nlt = 0, nwt = 0, nunit = 0, nsc = 0, napp = 0;
   for (int i = 0; i < n; ++i) {
     const a8_apollo_tensor& t = ts[i];
     if (!t.param || !t.grad || !t.proj_t || !t.workspace) return set_error(A8_ERR_ARG, "null pointer");
@@ -1793,11 +2027,11 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       return set_error(A8_ERR_ARG, "APOLLO with step_scalars needs each record's proj_state and proj_gap > 0");
     if (!aligned16(t.param) || !aligned16(t.grad) || !aligned16(t.workspace))
       return set_error(A8_ERR_ALIGN, "APOLLO param, grad and workspace must be 16-byte aligned");
-    const int64_t trows = dtype == A8_BF16 ? kApTileR : kApTile;
+    const int64_t trows = ap_tile(dtype == A8_BF16, t.rows, t.cols, t.rank);
     const ApL L = ap_layout(t.rows, t.cols, t.rank, trows);
     ApDesc& D = tab[(size_t)i];
     D.grad = t.grad; D.param = t.param; D.ws = t.workspace; D.proj_t = t.proj_t;
-    D.trows = (int32_t)trows; D.pad_ = 0;
+    D.trows = (int32_t)trows;
     D.v_q = t.v_q; D.v_scale = t.v_scale; D.v_min_log = t.v_min_log; D.v_fp32 = t.v_fp32;
     D.m_q = t.m_q; D.m_scale = t.m_scale; D.m_fp32 = t.m_fp32;
     D.fira_prev = t.fira_prev; D.lr = t.lr;
@@ -1813,9 +2047,13 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     first[(size_t)2 * n + i] = D.unit_begin;
     first[(size_t)3 * n + i] = D.sc_begin;
     first[(size_t)4 * n + i] = D.app_begin;
-    if (t.rows >= t.cols) nrt += L.ntile; else nlt += L.ntile;
+    D.wtile_begin = (int32_t)nwt;
+    first[(size_t)5 * n + i] = D.wtile_begin;
+    if (trows == kApWide) nwt += L.ntile;
+    else if (t.rows >= t.cols) nrt += L.ntile;
+    else nlt += L.ntile;
     nunit += L.nunit; nsc += L.nsc; napp += L.napp;
-    if (nrt > 0x7FFFFFFF || nlt > 0x7FFFFFFF || nunit > 0x7FFFFFFF || nsc > 0x7FFFFFFF || napp > 0x7FFFFFFF)
+    if (nrt > 0x7FFFFFFF || nlt > 0x7FFFFFFF || nwt > 0x7FFFFFFF || nunit > 0x7FFFFFFF || nsc > 0x7FFFFFFF || napp > 0x7FFFFFFF)
       return set_error(A8_ERR_SIZE, "too many workgroups");
   }
   hipStream_t st = (hipStream_t)stream;
@@ -1824,7 +2062,7 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
     if (upload) {
       std::vector<char> blob((size_t)table_bytes(n));
       std::memcpy(blob.data(), tab.data(), sizeof(ApDesc) * (size_t)n);
-      std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 5 * (size_t)n);
+      std::memcpy(blob.data() + sizeof(ApDesc) * (size_t)n, first.data(), sizeof(int32_t) * 6 * (size_t)n);
       if (upload_table(table_dev, blob.data(), blob.size(), st) != hipSuccess)
         return set_error(A8_ERR_HIP, "table upload failed");
     }
@@ -1879,6 +2117,10 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       else hipLaunchKernelGGL(k_ap_proj_l32, dim3((unsigned)nlt), dim3(256), 0, st, one, dtab, n);
       if ((rc = check_launch("k_ap_proj_l"))) return rc;
     }
+    if (nwt > 0) {
+      hipLaunchKernelGGL(k_ap_proj_w, dim3((unsigned)nwt), dim3(256), 0, st, one, dtab, n);
+      if ((rc = check_launch("k_ap_proj_w"))) return rc;
+    }
     if (h.scale_param) {   // ||p||^2 of the parameter (fp64 parameters refuse scale_parameter above)
       for (int i = 0; i < n; ++i) {
         const ApDesc& D = tab[(size_t)i];
@@ -1927,8 +2169,12 @@ int64_t a8_apollo_workspace_floats(int64_t rows, int64_t cols, int64_t rank, int
   (void)channel;
   if (rows <= 0 || cols <= 0 || rank <= 0) return 0;
   // either tile height (the dtype is not known here): the larger workspace
-  const int64_t a = ap_layout(rows, cols, rank, kApTileR).total, b = ap_layout(rows, cols, rank, kApTile).total;
-  return a > b ? a : b;
+  int64_t m = 0;
+  for (int g16 = 0; g16 < 2; ++g16) {
+    const int64_t a = ap_layout(rows, cols, rank, ap_tile(g16 != 0, rows, cols, rank)).total;
+    m = a > m ? a : m;
+  }
+  return m;
 }
 
 int64_t a8_apollo_table_bytes(int ntensors) { return ntensors > 0 ? table_bytes(ntensors) : 0; }

@@ -353,17 +353,17 @@ def test_apollo_projection_error_bound(shape, dtype, det_proj):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", [(128, 96), (64, 160)])
+@pytest.mark.parametrize("shape,rank", [((128, 96), 16), ((64, 160), 16), ((600, 300), 256), ((300, 520), 256)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_apollo_nonfinite_grad_equals_scrubbed(shape, dtype, det_proj):
+def test_apollo_nonfinite_grad_equals_scrubbed(shape, rank, dtype, det_proj):
     """NaN / +-Inf gradient entries count as zero (optimizer.py:2606): fp32 through
     the flag and recompute pass, bf16 scrubbed inside the projection kernel."""
     from adafactor8bit import Adafactor8Bit
-    print(f"[apollo nonfinite] {shape} {dtype}", flush=True)
+    print(f"[apollo nonfinite] {shape} r={rank} {dtype}", flush=True)
     res = []
     for bad in (True, False):
         p = torch.nn.Parameter(inputs.make_param(shape, 0, 5).to("cuda", dtype))
-        opt = Adafactor8Bit([p], **_apollo_kw(apollo_rank=16))
+        opt = Adafactor8Bit([p], **_apollo_kw(apollo_rank=rank))
         for t in range(1, 4):
             g = inputs.make_grad(shape, 0, t, 5).to(dtype)
             flat = g.view(-1)
@@ -515,9 +515,13 @@ C4_KW = dict(lr=1e-3, beta1=0.9, beta2=0.999, beta2_decay=None, beta3=None, fact
              m_quant_type="uf8", v_quant_type="al8")
 
 # (shape, rank): right side (R >= C, K = C) and left side (K = R).  Rank 320 takes
-# two 256-wide output passes.
+# two 256-wide output passes.  bf16 G at ranks 256 and 512 takes the wide tiles
+# (256 channels x 256 outputs): whole tiles (1024 x 512, 512 x 1536), a partial
+# last tile with K % 32 != 0 and rows that are not 16-byte aligned (700 x 390,
+# 390 x 1100: C % 8 == 6 and 4), and two passes (1100 x 600, 600 x 1300).
 GEMM_RANKS = [((1024, 512), 64), ((700, 384), 96), ((1024, 512), 256), ((700, 384), 320),
-              ((512, 1536), 256), ((384, 900), 320), ((300, 700), 64), ((200, 900), 96)]
+              ((512, 1536), 256), ((384, 900), 320), ((300, 700), 64), ((200, 900), 96),
+              ((700, 390), 256), ((390, 1100), 256), ((1100, 600), 512), ((600, 1300), 512)]
 
 
 @pytest.mark.gpu

@@ -58,13 +58,24 @@ struct HyperFull {
 constexpr int kFLanes = 256;
 constexpr int kFElems = kFLanes * 8;
 
-__device__ __forceinline__ const DescFull* find_full(const DescFull* tab, int n, int64_t wg) {
+// The tensor table is uniform per workgroup and read-only during the launch:
+// it is read through the scalar cache (constant address space), the search
+// probing each descriptor's wg_begin, the descriptor landing in SGPRs.
+__device__ __forceinline__ DescFull load_full(const DescFull* tab, int n, int64_t wg) {
+  const A8_C DescFull* ct = cp(tab);
   int lo = 0, hi = n - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;
-    if (tab[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
+    if (ct[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
   }
-  return tab + lo;
+  static_assert(sizeof(DescFull) % 8 == 0, "descriptor is loaded as 64-bit words");
+  const A8_C uint64_t* w = (const A8_C uint64_t*)(ct + lo);
+  uint64_t buf[sizeof(DescFull) / 8];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(DescFull) / 8); ++i) buf[i] = w[i];
+  DescFull d;
+  __builtin_memcpy(&d, buf, sizeof(DescFull));
+  return d;
 }
 
 // MODE: 0 single pass, 1 NORM (writes V, sums u^2 or U^2), 2 APPLY (reads V,
@@ -86,7 +97,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
     h.decay_val = sc.decay;
     h.sr_step = sc.step;
   }
-  const DescFull D = table ? *find_full(table, ntab, (int64_t)blockIdx.x) : one;
+  const DescFull D = table ? load_full(table, ntab, (int64_t)blockIdx.x) : one;
   const int64_t wl = (int64_t)blockIdx.x - D.wg_begin;
   const int lane = threadIdx.x;
   const int64_t n = D.numel;
@@ -122,25 +133,43 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
     const int cnt = (n - e0) < 8 ? (int)(n - e0) : 8;
     const T* G = reinterpret_cast<const T*>(D.grad);
     T* P = reinterpret_cast<T*>(D.param);
-    for (int k = 0; k < cnt; ++k) {
+    // every input of the lane's elements is loaded before any store: the stores
+    // could alias the loads as far as the compiler knows, so loads interleaved
+    // with them would run one memory round trip per element
+    constexpr bool kNeedP = MODE != 1 && MODE != 4;
+    T graw[8], praw[8];
+    float vin[8], min_[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k < cnt) {
+        const int64_t i = e0 + k;
+        graw[k] = G[i];
+        if (kNeedP || (MODE == 1 && h.scale_param)) praw[k] = P[i];
+        vin[k] = D.v[i];
+        if (D.m) min_[k] = D.m[i];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k >= cnt) break;
       const int64_t i = e0 + k;
-      const float g = scrub(to_f<T>(G[i]));
+      const float g = scrub(to_f<T>(graw[k]));
       if (MODE == 1 && h.scale_param) {
-        const float pv = to_f<T>(P[i]);
+        const float pv = to_f<T>(praw[k]);
         psum += pv * pv;
       }
       float v;
       if (MODE == 2 || MODE == 4 || h.v_ready) {
-        v = D.v[i];
+        v = vin[k];
       } else {
-        v = __builtin_fmaf(h.bv * g, g, D.v[i] * h.v_keep);
+        v = __builtin_fmaf(h.bv * g, g, vin[k] * h.v_keep);
         if (h.has_eps_add) v = v + h.eps_add;
         D.v[i] = v;
       }
       float inv = h.adam_denom ? 1.0f / (sqrtf(v) + h.eps_d) : 1.0f / sqrtf(fmaxf(v, h.eps_sq));
       float u;
       if (D.m) {
-        float mo = D.m[i];
+        float mo = min_[k];
         if (h.momentum_only) {
           const float ut = g * inv;
           if (MODE == 1 || MODE == 3) sq += ut * ut;
@@ -168,7 +197,7 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
         if (MODE == 1 || MODE == 3) sq += u * u;
       }
       if (MODE != 1 && MODE != 4) {
-        pval_t<T> p = pv_of<T>(P[i]);
+        pval_t<T> p = pv_of<T>(praw[k]);
         if constexpr (SR) {
           const float dec = D.decay ? *D.decay : (h.has_decay ? h.decay_val : (h.wd_mode ? wdec : 1.0f));
           P[i] = sr_round<T>(p * dec - step * u, D.sr_seed, h.sr_step, (uint64_t)i);

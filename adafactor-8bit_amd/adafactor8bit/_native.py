@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libadafactor8bit_amd.so")
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 MODE_NOCLIP, MODE_NORM, MODE_APPLY, MODE_LAG, MODE_MNORM = 0, 1, 2, 3, 4
+AL_KERNEL_RULE = 0x100   # A8_AL_KERNEL_RULE: OR'd into v_bits of the 1-D quantised steps
 
 _c_vp = ctypes.c_void_p
 _c_i = ctypes.c_int

@@ -6,9 +6,13 @@ that name (optimizer.py:85-98; bindings kernels.cu:3089-3150) and calls it as
 positional signatures, converts tensors to device pointers and launches the
 HIP kernels of ``libadafactor8bit_amd.so`` on the current stream.
 
-Numerics follow the reference's PyTorch path (optimizer.py:299-353, 504-532):
-the AL floor of the 1-D kernels is the CPU quantiser's -126, so the
+Numerics follow the reference's PyTorch path (optimizer.py:299-353, 504-532) by
+default: the AL floor of the 1-D kernels is the CPU quantiser's -126, so the
 ``log_eps_sq`` argument only supplies eps1 for the Adam denominator's momentum clamp.
+``set_refit_rule("kernel")`` switches the fused 1-D functions (fused_update_1d_*,
+fused_update_1d_vonly_*) to the refit rule of the reference's own CUDA kernels
+(kernels.cu:686-687, 772-791): the block minimum includes zeros and is floored at
+``log_eps_sq``, l_max is capped at 126 (A8_AL_KERNEL_RULE).
 
 Every one of the reference module's 61 functions is provided.
 """
@@ -44,6 +48,21 @@ __all__ = [
 
 _AL_FLOOR = -126.0
 _EPS_FLOOR = 1.17549435e-38
+_RULE = {"kernel": False}
+
+
+def set_refit_rule(rule):
+    """The V refit rule of the fused 1-D functions: "fallback" (the reference's CPU
+    quantiser, optimizer.py:299-325; the default) or "kernel" (the reference's fused
+    CUDA kernels, kernels.cu:686-687, 772-791, whose floor is the log_eps_sq argument).
+    Process-wide for this module; the optimizer's own switch is al_refit_rule."""
+    if rule not in ("fallback", "kernel"):
+        raise ValueError(f"refit rule must be 'fallback' or 'kernel', got {rule!r}")
+    _RULE["kernel"] = rule == "kernel"
+
+
+def refit_rule():
+    return "kernel" if _RULE["kernel"] else "fallback"
 
 
 def _stream(t):
@@ -95,9 +114,11 @@ def _u1d(mode, sr, param, grad, m_q, m_scale, v_q, v_scale, v_min_log, v_buf, no
         mode, int(sr), nat.dtype_code(ref.dtype), nat.ptr(param), nat.ptr(grad), nat.ptr(m_q),
         nat.ptr(m_scale), nat.ptr(v_q), nat.ptr(v_scale), nat.ptr(v_min_log), nat.ptr(v_buf),
         nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha), nat.ptr(prev_norm), nat.ptr(dec), int(sr_seed), int(sr_step),
-        float(beta1), float(beta_val), float(eps_for_denom), int(bool(use_adam_denom)), _AL_FLOOR,
+        float(beta1), float(beta_val), float(eps_for_denom), int(bool(use_adam_denom)),
+        float(log_eps_sq) if _RULE["kernel"] else _AL_FLOOR,
         float(eps_for_grad_sq), eps_sq, int(numel),
-        int(block_size), int(m_block_size), int(m_bits), int(m_mode), float(d), int(v_bits),
+        int(block_size), int(m_block_size), int(m_bits), int(m_mode), float(d),
+        int(v_bits) | (nat.AL_KERNEL_RULE if _RULE["kernel"] else 0),
         int(bool(momentum_only)), 0.0, 1.0, 0, _stream(ref))
     nat.check(rc, "fused_update_1d")
 

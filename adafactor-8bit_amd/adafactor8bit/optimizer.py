@@ -121,6 +121,7 @@ class Adafactor8Bit(Optimizer):
         bias_correction: Optional[bool] = None,
         warmup_multiplier: float = 0.0,
         capturable: bool = False,
+        al_refit_rule: str = "fallback",
     ):
         # argument validation: optimizer.py:1362-1432 (same conditions and messages)
         if lr < 0.0:
@@ -185,6 +186,8 @@ class Adafactor8Bit(Optimizer):
                 raise ValueError("CAME (beta3) requires factored=True (2D row/col factorization). It is "
                                  "not supported for 1D full-rank paths.")
 
+        if al_refit_rule not in ("fallback", "kernel"):
+            raise ValueError(f"al_refit_rule must be 'fallback' or 'kernel', got {al_refit_rule!r}")
         defaults = dict(
             lr=lr, beta1=beta1, beta2=beta2, beta2_decay=beta2_decay, beta3=beta3, eps_came=eps_came,
             eps=eps, weight_decay=weight_decay, d=d, maximize=maximize,
@@ -201,7 +204,7 @@ class Adafactor8Bit(Optimizer):
             scale_weight_decay=scale_weight_decay,
             enable_fira_for_adafactor=enable_fira_for_adafactor, fira_margin=fira_margin,
             lag_norm=lag_norm, momentum_only_1d=momentum_only_1d, bias_correction=bias_correction,
-            warmup_multiplier=warmup_multiplier, capturable=capturable,
+            warmup_multiplier=warmup_multiplier, capturable=capturable, al_refit_rule=al_refit_rule,
         )
         super().__init__(params, defaults)
         self._apollo_seed_counter = 1
@@ -524,7 +527,8 @@ class _Plan:
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
-                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep", "dsc")
+                 "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep", "dsc",
+                 "al_floor", "al_vbits")
 
     def batch_key(self):
         if self.path == "factored":
@@ -547,7 +551,7 @@ class _Plan:
         if self.path == "q1d" and (self.d > 0 or self.fira):
             if self.lag:
                 return None
-            return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
+            return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt, self.al_vbits,
                     self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                     self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.d, self.fira, self.margin)
@@ -558,7 +562,7 @@ class _Plan:
             return ("sgd", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m, mq,
                     self.mqt if mq else None, self.mbs if mq else 0, self.beta1, self.alpha_val, self.decay_val)
         return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
-                self.vbuf is not None,
+                self.vbuf is not None, self.al_vbits,
                 self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                 self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                 self.alpha_val, self.decay_val)
@@ -579,6 +583,12 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P.eps1, P.eps2 = eps1, eps2
     P.eps_sq = max(eps1 * eps1, _LOG_QUANT_FLOOR)
     P.log_eps_sq = math.log2(P.eps_sq)
+    # the V refit of the fused 1-D step: the CPU quantiser's rule (floor -126), or with
+    # al_refit_rule="kernel" the reference's fused CUDA kernels' rule, whose floor is
+    # log_eps_sq (optimizer.py:1961-1962 passes it to kernels.cu:772-774)
+    krule = group.get("al_refit_rule", "fallback") == "kernel"
+    P.al_floor = _f32(P.log_eps_sq) if krule else _AL_FLOOR
+    P.al_vbits = (16 if st.get("v_quant_type", "al8") == "al16" else 8) | (nat.AL_KERNEL_RULE if krule else 0)
     P.adam_denom = (not factored) and (beta2 is not None) and (beta3 is None)
     P.eps_d = eps1 if P.adam_denom else 0.0
     P.eps_g = eps1 if not P.adam_denom else 0.0
@@ -817,8 +827,8 @@ def _launch_1d(opt, P, mode, alpha_t, alpha_val, norm_buf=None, prev_norm=None, 
             nat.ptr(m_scale), nat.ptr(vq), nat.ptr(st["variance_scale"]), nat.ptr(st["variance_min_log"]),
             nat.ptr(v_buf), nat.ptr(norm_buf), nat.ptr(parts), nat.ptr(alpha_t), nat.ptr(prev_norm),
             nat.ptr(dec_t), int(st.get("sr_seed", 0)), int(P.step), P.beta1 if P.has_m else 0.0, P.beta_val, P.eps_d,
-            int(P.adam_denom), _AL_FLOOR, P.eps_g, P.eps_sq, p.numel(), P.bs,
-            P.mbs if P.has_m else P.bs, m_bits, m_mode, P.d, 16 if P.vqt == "al16" else 8,
+            int(P.adam_denom), P.al_floor, P.eps_g, P.eps_sq, p.numel(), P.bs,
+            P.mbs if P.has_m else P.bs, m_bits, m_mode, P.d, P.al_vbits,
             int(P.mom_only), float(alpha_val), float(dec_val), int(has_dec),
             nat.stream_of(p.device))
         nat.check(rc, "a8_fused_update_1d")
@@ -953,6 +963,10 @@ def _prep_q1d_fp32m(opt, P):
     with that V' (v_ready), as the reference feeds _v_fp32 to _fallback_1d_update."""
     st, p, g = P.st, P.p, P.g
     dev = p.device
+    if P.al_vbits & nat.AL_KERNEL_RULE:
+        raise NotImplementedError(
+            "adafactor8bit: al_refit_rule='kernel' covers the fused 1-D step (quantised or no momentum); "
+            "quantised V with fp32 momentum is refitted by fused_log_quantize_lerp's own rule in the reference")
     if "m" not in st:
         st["m"] = torch.zeros_like(g, dtype=torch.float32)
     if not st["m"].is_contiguous():
@@ -1264,10 +1278,10 @@ def _run_batch_q1dc(opt, key, plans):
         _no_upload_in_capture(up)
         rc = L.a8_fused_update_1d_multi(
             mode, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), table.numel(),
-            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), P0.al_floor,
             P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
             S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
-            16 if P0.vqt == "al16" else 8, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
+            P0.al_vbits, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
             float(dec_val), has_dec, up, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_fused_update_1d_multi")
         ent["arrs"][mode][2] = 0
@@ -1386,10 +1400,10 @@ def _run_batch(opt, key, plans):
     elif path == "q1d":
         rc = L.a8_fused_update_1d_multi(
             nat.MODE_NOCLIP, int(P0.sr), nat.dtype_code(P0.p.dtype), arr, n, table.data_ptr(), nbytes,
-            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), _AL_FLOOR,
+            P0.beta1 if P0.has_m else 0.0, P0.beta_val, P0.eps_d, int(P0.adam_denom), P0.al_floor,
             P0.eps_g, P0.eps_sq, P0.bs, P0.mbs if P0.has_m else P0.bs,
             S.m_bits(P0.mqt) if P0.has_m else 0, S.m_mode(P0.mqt) if P0.has_m else 0, P0.d,
-            16 if P0.vqt == "al16" else 8, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
+            P0.al_vbits, int(P0.mom_only), int(P0.step), float(P0.alpha_val),
             float(dec_val), has_dec, upload, nat.ptr(P0.dsc), strm)
         nat.check(rc, "a8_fused_update_1d_multi")
         for pl in plans:

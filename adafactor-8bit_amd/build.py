@@ -18,7 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "adafactor8bit", "libadafactor8bit_amd.so")
-SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_full1d.hip", "a8_factored.hip", "a8_apollo.hip",
+SOURCES = ["a8_abi.cpp", "a8_update1d.hip", "a8_update1d_k.hip", "a8_full1d.hip", "a8_factored.hip", "a8_apollo.hip",
            "a8_decode.hip", "a8_sgd.hip", "a8_prims.hip", "a8_apollo_x.hip", "a8_step.hip"]
 LIBS = ["-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = os.environ.get("A8_OFFLOAD_ARCH", "gfx950")

@@ -113,4 +113,5 @@ hipError_t apollo_upload_qmap(const float* q8, const float* q4);
 hipError_t decode_upload_qmap(const float* q8, const float* q4);
 hipError_t sgd_upload_qmap(const float* q8, const float* q4);
 hipError_t prims_upload_qmap(const float* q8, const float* q4);
+hipError_t update1d_k_upload_qmap(const float* q8, const float* q4);
 }  // namespace a8

@@ -165,13 +165,42 @@ __device__ __forceinline__ ALFit al_refit(float vmax, float vmin_nz, float floor
 // one call per wave: even lanes take log2 of the block max, odd lanes of the
 // block min, and every lane reads its block's pair back.  Requires that the
 // block's lanes hold the same (vmax, vmin_nz) and span at least two lanes.
+// ---- the reference's fused-kernel AL rule (kernels.cu:318-326, 686-687, 772-791)
+// The fused 1-D CUDA kernels refit differently from the CPU quantiser above:
+// l = log2(v) with log2(0) = -inf (no 1e-38 clamp); lmax = min(max l, 126), -1e30
+// for a block without a non-zero v; lmin = max(min(126, min l), floor) where the
+// minimum includes zeros, so a block holding a zero takes the floor (the caller's
+// log2(max(eps1^2, FLT_MIN))); lmin := lmax - 1 if lmin >= lmax; s = max(lmax -
+// lmin, 1e-12).  Codes: 0 for v == 0, else clamp(rint((l - lmin) * RN((L-2)/s)) + 1,
+// 1, L-1); decode 2^(((q-1) * RN(1/(L-2))) * s + lmin).  A call selects it with
+// krule; the default is the CPU rule.
+__device__ __forceinline__ float al_klog(float x, float lo) { return x > 0.0f ? log2_exact(x) : lo; }
+__device__ __forceinline__ void al_kfit(float lmax_raw, float lmin_raw, float floor_, float levels_m2, ALFit& f) {
+  const float lmax = fminf(lmax_raw, 126.0f);
+  float lmin = fmaxf(fminf(lmin_raw, 126.0f), floor_);
+  if (lmin >= lmax) lmin = lmax - 1.0f;
+  f.lmin = lmin;
+  f.s = fmaxf(lmax - lmin, 1e-12f);
+  al_fit_consts(f, levels_m2);
+}
+// The decode exponent of code c >= 1 (c1 = c - 1) under either rule.
+template <int LM2>
+__device__ __forceinline__ float al_dec_log(float c1, float s, float lm, bool krule) {
+  return krule ? (c1 * (1.0f / (float)LM2)) * s + lm : (c1 * s) / (float)LM2 + lm;
+}
+
+// krule: vmin_nz is the block minimum including zeros, and the fit is al_kfit's.
 __device__ __forceinline__ ALFit al_refit_pair(float vmax, float vmin_nz, float floor_, float levels_m2,
-                                               int lane) {
+                                               int lane, bool krule = false) {
   const float x = (lane & 1) ? vmin_nz : vmax;   // inf (no non-zero entry) stays inf
-  const float l = log2_exact(fmaxf(x, kLogClampIn));
+  const float l = krule ? al_klog(x, (lane & 1) ? -__builtin_inff() : -1e30f) : log2_exact(fmaxf(x, kLogClampIn));
   const float lmax = __shfl(l, lane & ~1, 64);
   float lmin = __shfl(l, lane | 1, 64);
   ALFit f;
+  if (krule) {
+    al_kfit(lmax, lmin, floor_, levels_m2, f);
+    return f;
+  }
   lmin = fmaxf(lmin, floor_);
   if (lmin >= lmax) lmin = lmax - 1.0f;
   const float s = fmaxf(lmax - lmin, 1e-12f);
@@ -188,6 +217,17 @@ template <int LM2>
 __device__ __forceinline__ float al_round_exact(float v, const ALFit& f) {
   const float le = log2_exact(fmaxf(v, kLogClampIn));
   return rintf(((le - f.lmin) / f.s) * (float)LM2) + 1.0f;
+}
+// The same under the kernels' rule (kernels.cu:322-326, 783-787): (l - lmin) times
+// the rounded (L-2)/s, no clamp of v (v > 0; v == 0 is code 0 before this matters).
+template <int LM2>
+__device__ __forceinline__ float al_round_exact_k(float v, const ALFit& f) {
+  const float le = log2_exact(v);
+  return rintf((le - f.lmin) * ((float)LM2 / f.s)) + 1.0f;
+}
+template <int LM2>
+__device__ __forceinline__ float al_round_exact(float v, const ALFit& f, bool krule) {
+  return krule ? al_round_exact_k<LM2>(v, f) : al_round_exact<LM2>(v, f);
 }
 
 // Fast AL8 code argument from the hardware log2 (faithful: |error| <= |l|*2^-23,
@@ -221,8 +261,11 @@ __device__ __forceinline__ uint32_t al_finish(float v, float r1) {
 // AL codes of N values under one block fit, equal to al_round_exact's: AL8 takes
 // the fast argument and re-decides only the values inside its margin; AL16,
 // whose margin would cover most values, always rounds exactly.
+// The fast argument approximates the real (l - lmin) * (L-2)/s + 1 of both rules;
+// each rule's own roundings stay inside the margin, so krule changes only the
+// exact re-decision.
 template <int LM2, int N>
-__device__ __forceinline__ void al_codes(const float* v, const ALFit& f, uint32_t* q) {
+__device__ __forceinline__ void al_codes(const float* v, const ALFit& f, uint32_t* q, bool krule = false) {
   float r[N];
   if constexpr (LM2 == 254) {
     bool bad[N];
@@ -230,10 +273,10 @@ __device__ __forceinline__ void al_codes(const float* v, const ALFit& f, uint32_
     for (int i = 0; i < N; ++i) r[i] = al8_round_fast(v[i], f, bad[i]);
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if (bad[i]) r[i] = al_round_exact<254>(v[i], f);
+      if (bad[i]) r[i] = al_round_exact<254>(v[i], f, krule);
   } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) r[i] = al_round_exact<LM2>(v[i], f);
+    for (int i = 0; i < N; ++i) r[i] = al_round_exact<LM2>(v[i], f, krule);
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) q[i] = al_finish<LM2>(v[i], r[i]);

@@ -46,6 +46,20 @@ extern "C" {
  * norm of a float64 tensor); no stochastic rounding. */
 #define A8_F64 3
 
+/* OR'd into v_bits of the 1-D quantised steps (a8_fused_update_1d, its _multi and
+ * _multi_noalloc forms): refit and code V by the rule of the reference's fused 1-D
+ * CUDA kernels (kernels.cu:686-687, 772-791, 318-326) instead of its CPU quantiser's
+ * (optimizer.py:299-353, the default, which the reference's CPU path and this
+ * library's parity tests follow).  The kernels' block minimum includes zeros and is
+ * floored at log_floor (pass log2(max(eps1^2, FLT_MIN)), the kernels' log_eps_sq;
+ * a block holding a zero V therefore takes the floor); l_max is capped at 126; a
+ * block without a non-zero V gets scale 1e-12 and min_log -1e30; codes are
+ * rint((log2 v - l_min) * ((L-2)/s)) + 1 and decode 2^(((q-1) * (1/(L-2))) * s +
+ * l_min), each product and quotient rounded to fp32 in that order.  The logarithm
+ * and power are correctly rounded, where the CUDA build uses log2f/exp2f, and the
+ * element arithmetic (the V and M EMAs, M codes) stays the CPU path's. */
+#define A8_AL_KERNEL_RULE 0x100
+
 /* kernel modes (kernels.cu:19-24): single pass, norm pass, apply pass, lagged norm */
 #define A8_MODE_NOCLIP 0
 #define A8_MODE_NORM 1
@@ -87,7 +101,9 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
  *               the update, the decoupled weight decay of optimizer.py:2034-2039)
  *   beta1, beta_val  EMA coefficients as the host's doubles: the lerp weights are
  *               (float)(1 - beta1) and (float)beta_val, as torch.lerp_ receives them
- *   log_floor   lower bound of a block's l_min (-126 for the reference numerics)
+ *   log_floor   lower bound of a block's l_min (-126 for the reference's CPU rule;
+ *               log2(max(eps1^2, FLT_MIN)) with A8_AL_KERNEL_RULE)
+ *   v_bits      8 (AL8) or 16 (AL16), optionally | A8_AL_KERNEL_RULE
  * block_size: a multiple of 128 up to 65536; m_block_size: a multiple of 4, at least
  * 32, dividing block_size (the reference's rules, optimizer.py:1395-1416).  Powers of
  * two (block_size <= 2048) run the 2048-element unit layout, other sizes one

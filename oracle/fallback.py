@@ -18,11 +18,15 @@ Pinning (see tests/test_oracle_*.py):
     monotonicity), plus the golden trajectories;
   * step functions: the golden fixtures written by tests/golden/gen_golden.py
     from the reference itself, bit-exact;
-  * Fira scalar: truth table over first step / reset / growth / non-finite.
+  * Fira scalar: truth table over first step / reset / growth / non-finite;
+  * the fused 1-D CUDA kernels' AL rule (al_quantize_kernel, al_refit_rule
+    "kernel"): kernels.cu cannot run here, so it is pinned by closed forms read
+    from kernels.cu:686-687, 772-791, 318-326 (tests/test_oracle_kernel_rule.py).
 """
 import math
 from typing import Any, Dict, Optional
 
+import numpy as np
 import torch
 
 LOG_QUANT_FLOOR = 1.17549435e-38  # optimizer.py:22
@@ -127,6 +131,78 @@ def al_dequantize(q: torch.Tensor, scale: torch.Tensor, min_log: torch.Tensor, n
     out = torch.pow(2.0, logs)
     out[zero] = 0.0
     return out.reshape(-1)[:numel]
+
+
+# --------------------------------------------------------------------------
+# AL codec, the reference's fused 1-D CUDA kernels' rule   kernels.cu:318-326, 686-687, 772-791
+# --------------------------------------------------------------------------
+FLT_MIN = 1.17549435e-38
+LOG_ZERO, LOG_MAX, MIN_SCALE = -1e30, 126.0, 1e-12     # kernels.cu:15-17
+
+
+def kernel_floor(eps1: float) -> float:
+    """The kernels' floor: log_eps_sq = log2(max(eps1^2, FLT_MIN)) (optimizer.py:1961-1962)."""
+    return float(np.float32(math.log2(max(eps1 * eps1, FLT_MIN))))
+
+
+def al_quantize_kernel(v: torch.Tensor, block_size: int, floor: float, levels: int = 256):
+    """The fused 1-D kernels' refit and codes (kernels.cu:686-687, 772-791, 322-326).
+
+    Per block of the tensor's elements (no padding enters the statistics):
+    l = log2(v), log2(0) = -inf; lmax = min(max(-1e30, max l), 126); lmin =
+    max(min(126, min l), floor) with zeros in the minimum; lmin := lmax - 1 if
+    lmin >= lmax; s = max(lmax - lmin, 1e-12); code 0 for v == 0, else
+    clamp(rint((l - lmin) * fp32((levels-2)/s)) + 1, 1, levels-1), every operation
+    rounded to fp32.  log2 is correctly rounded here (CUDA's log2f is within an ulp
+    or two).  Returns (codes, scale, min_log, pad) as :func:`al_quantize`.
+    """
+    flat = v.reshape(-1).to(torch.float32).numpy().astype(np.float32)
+    n = flat.size
+    pad = (block_size - n % block_size) % block_size
+    nb = (n + pad) // block_size
+    lm2 = np.float32(levels - 2)
+    codes = np.zeros(n + pad, dtype=np.int64)
+    scale = np.zeros(nb, dtype=np.float32)
+    minlog = np.zeros(nb, dtype=np.float32)
+    with np.errstate(divide="ignore"):
+        logs = np.where(flat > 0, np.log2(flat.astype(np.float64)), -np.inf).astype(np.float32)
+    f32 = np.float32
+    for b in range(nb):
+        lo, hi = b * block_size, min((b + 1) * block_size, n)
+        lb = logs[lo:hi]
+        lmax = min(max(f32(LOG_ZERO), lb.max()), f32(LOG_MAX))
+        lmin = max(min(f32(LOG_MAX), lb.min()), f32(floor))
+        if lmin >= lmax:
+            lmin = f32(lmax - f32(1.0))
+        s = max(f32(lmax - lmin), f32(MIN_SCALE))
+        inv = f32(lm2 / s)
+        x = np.rint((lb - lmin).astype(np.float32) * inv).astype(np.float64) + 1.0
+        q = np.clip(x, 1.0, levels - 1.0)
+        q[flat[lo:hi] == 0] = 0.0
+        codes[lo:hi] = q.astype(np.int64)
+        scale[b], minlog[b] = s, lmin
+    dt = torch.uint8 if levels <= 256 else torch.int16
+    out = codes.astype(np.uint8) if levels <= 256 else codes.astype(np.uint16).view(np.int16)
+    return torch.from_numpy(out.copy()).to(dt), torch.from_numpy(scale), torch.from_numpy(minlog), pad
+
+
+def al_dequantize_kernel(q: torch.Tensor, scale: torch.Tensor, min_log: torch.Tensor, numel: int):
+    """dequant_v (kernels.cu:318-320; AL16 kernels.cu:442): 0 for q = 0, else
+    2^(((q-1) * fp32(1/(levels-2))) * s + min_log) rounded to fp32 at each step; the
+    power correctly rounded."""
+    qf = q.reshape(-1)
+    levels = 256 if qf.dtype == torch.uint8 else 65536
+    x = qf.numpy().astype(np.int64)
+    if levels == 65536:
+        x = np.where(x < 0, x + 65536, x)
+    bs = x.size // scale.numel()
+    s = np.repeat(scale.numpy().astype(np.float32), bs)
+    lm = np.repeat(min_log.numpy().astype(np.float32), bs)
+    inv = np.float32(1.0) / np.float32(levels - 2)
+    arg = ((np.float32(x - 1).astype(np.float32) * inv).astype(np.float32) * s).astype(np.float32) + lm
+    out = np.exp2(arg.astype(np.float64)).astype(np.float32)
+    out[x == 0] = 0.0
+    return torch.from_numpy(out[:numel].copy())
 
 
 # --------------------------------------------------------------------------
@@ -292,15 +368,17 @@ def init_m(st, numel, shape, m_block, mqt, quantize):
     st["m_quant_type"] = mqt
 
 
-def deq_v(st, prefix):
+def deq_v(st, prefix, krule=False):
     q = st[f"{prefix}_q"]
     shape = st[f"{prefix}_shape"]
     numel = math.prod(shape)
-    return al_dequantize(q, st[f"{prefix}_scale"], st[f"{prefix}_min_log"], numel).view(shape)
+    deq = al_dequantize_kernel if krule else al_dequantize
+    return deq(q, st[f"{prefix}_scale"], st[f"{prefix}_min_log"], numel).view(shape)
 
 
-def quant_v(st, prefix, v, block_size, vqt, floor=-126.0):
-    q, s, ml, pad = al_quantize(v, block_size, floor, 256 if vqt == "al8" else 65536)
+def quant_v(st, prefix, v, block_size, vqt, floor=-126.0, krule=False):
+    qfn = al_quantize_kernel if krule else al_quantize
+    q, s, ml, pad = qfn(v, block_size, floor, 256 if vqt == "al8" else 65536)
     st[f"{prefix}_q"], st[f"{prefix}_scale"], st[f"{prefix}_min_log"] = q, s, ml
     st[f"{prefix}_shape"], st[f"{prefix}_pad"] = tuple(v.shape), pad
 
@@ -387,7 +465,7 @@ DEFAULTS = dict(lr=1e-2, beta1=None, beta2=None, beta2_decay=-0.8, beta3=None, e
                 apollo_rank=0, apollo_update_proj_gap=200, apollo_scale_type="channel",
                 apollo_scale=1.0, apollo_scale_front=False, apollo_eps=1e-6, apollo_factorize=False,
                 apollo_cache_proj=False, enable_fira_for_apollo=True,
-                stochastic_round_writeback=False)
+                stochastic_round_writeback=False, al_refit_rule="fallback")
 
 ADV_DEFAULT = 0xF   # optimizer.py:26
 
@@ -577,10 +655,16 @@ class OracleOptimizer:
 
         if full_rank:  # optimizer.py:2082-2190
             if quant and vqt != "fp32":
+                # al_refit_rule "kernel": the V refit and codes of the fused 1-D CUDA
+                # kernels (floor log_eps_sq, kernels.cu:772-774); "fallback": the CPU rule
+                kr = h.get("al_refit_rule", "fallback") == "kernel" and not sgd
                 gsq = g32.square().add_(eps_g)
-                var = deq_v(st, "variance")
+                var = deq_v(st, "variance", kr)
                 var.lerp_(gsq, bv)
-                quant_v(st, "variance", var, bs, vqt)
+                if kr:
+                    quant_v(st, "variance", var, bs, vqt, floor=kernel_floor(eps1), krule=True)
+                else:
+                    quant_v(st, "variance", var, bs, vqt)
             else:
                 var = st["variance"]
                 var.mul_(1.0 - bv).addcmul_(g32, g32, value=bv)

@@ -462,62 +462,32 @@ def _check_block_sizes(group):
     """Raise ValueError if a parameter of ``group`` would reach a kernel that cannot
     run its block sizes.  The constructor already enforces the reference's own
     rules (optimizer.py:1395-1416: B_V a multiple of 128, B_M a multiple of 4 and
-    at least 32, B_V % B_M == 0).  The kernels here take:
-      * quantised 1-D V (AL8/AL16) with coded momentum or none: every size those
-        rules allow, up to B_V = 65536 (powers of two in [128, 2048] take the unit
-        layout, the others one workgroup per V block);
-      * coded momentum on the SGD route and with fp32 V on the 1-D route: any
-        multiple of 4 from 32 to 65536;
-      * quantised 1-D V with fp32 momentum (the stand-alone AL EMA): any multiple
-        of 128 up to 65536;
-      * coded momentum on the factored route: any multiple of 4 from 32 to 65536
-        (powers of two up to 2048 take the tiled / unit layouts, the others whole
-        M blocks per workgroup);
-      * the APOLLO route: every size those rules allow, up to 65536 (powers of
-        two, B_V in [128, 2048] and B_M in [32, 2048], take the fused low-rank
-        stage, the others the stage of a8_apollo_lowrank_x).
+    at least 32, B_V % B_M == 0).  Every route takes every size those rules allow
+    up to 2^30 (the kernels' block sizes are 32-bit ints):
+      * quantised 1-D V (AL8/AL16) with coded momentum or none: powers of two in
+        [128, 2048] take the unit layout, the others one workgroup per V block
+        (a V block of more than 2048 M blocks in segments of 2048);
+      * coded momentum on the SGD route and with fp32 V on the 1-D route, and on
+        the factored route: powers of two up to 2048 take the unit / tiled
+        layouts, the others whole M blocks per workgroup;
+      * quantised 1-D V with fp32 momentum (the stand-alone AL EMA) and the
+        APOLLO route's low-rank V: one workgroup per V block beyond the unit
+        layout's sizes.
     The factored row / column statistics take any B_V."""
     if not group.get("quantize", True):
         return
     bs, mbs = group.get("block_size", 2048), group.get("m_block_size", 256)
     vqt, mqt = group.get("v_quant_type", "al8"), group.get("m_quant_type", "uf8")
-    cqt = group.get("c_quant_type") or vqt
-    beta1, beta3 = group.get("beta1"), group.get("beta3")
-    sgd = group.get("beta2") is None and group.get("beta2_decay") is None
-    min8 = group.get("min_8bit_size", 4096)
-    coded_m = beta1 is not None and mqt != "fp32"
+    coded_m = group.get("beta1") is not None and mqt != "fp32"
+    if not any(p.numel() >= group.get("min_8bit_size", 4096) for p in group["params"]):
+        return
+    if vqt != "fp32" and bs > _MAX_BLOCK:
+        raise ValueError(f"block_size={bs}: the kernels of this build take at most {_MAX_BLOCK}.")
+    if coded_m and mbs > _MAX_BLOCK:
+        raise ValueError(f"m_block_size={mbs}: the kernels of this build take at most {_MAX_BLOCK}.")
 
-    def need(ok, what, size, rule):
-        if not ok:
-            raise ValueError(f"{what}={size}: the {route} kernels of this build need {rule} "
-                             f"(parameter of shape {tuple(p.shape)}).")
 
-    for p in group["params"]:
-        if p.numel() < min8:
-            continue
-        any_m = 32 <= mbs <= 65536 and mbs % 4 == 0
-        if sgd:
-            route = "SGD"
-            if coded_m:
-                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
-        elif group.get("apollo_rank", 0) > 0 and p.dim() >= 2:
-            route = "APOLLO"
-            if vqt != "fp32" or (beta3 is not None and cqt != "fp32"):
-                need(bs <= 65536, "block_size", bs, "at most 65536")
-            if coded_m:
-                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
-        elif p.dim() >= 2 and group.get("factored", True):
-            route = "factored"
-            if coded_m:
-                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
-        else:
-            route = "full-rank"
-            if vqt != "fp32" and (coded_m or beta1 is None):
-                need(bs <= 65536, "block_size", bs, "at most 65536")
-            elif vqt != "fp32":   # fp32 momentum: the stand-alone AL EMA
-                need(bs <= 65536, "block_size", bs, "at most 65536")
-            elif coded_m:         # fp32 V: the stand-alone momentum EMA
-                need(any_m, "m_block_size", mbs, "a multiple of 4 in [32, 65536]")
+_MAX_BLOCK = 1 << 30
 
 
 # ====================================================================== planning

@@ -725,15 +725,15 @@ static int x_check(const a8_apollo_x_args* a) {
     return set_error(A8_ERR_SIZE, "u_rowsums: cols_low must be a power of two in [8, 512]");
   const bool v_coded = !a->factorize && a->v_bits;
   const bool c_coded = a->came && a->c_bits;
-  if ((v_coded || c_coded) && !(a->block_size >= 128 && a->block_size <= 65536 && a->block_size % 128 == 0))
-    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
+  if ((v_coded || c_coded) && !(a->block_size >= 128 && a->block_size <= (1 << 30) && a->block_size % 128 == 0))
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 2^30]");
   if ((v_coded && a->v_bits != 8 && a->v_bits != 16) || (c_coded && a->c_bits != 8 && a->c_bits != 16))
     return set_error(A8_ERR_ARG, "v_bits / c_bits must be 0, 8 or 16");
   if (a->has_m) {
     if (a->m_fp32 == nullptr) {
       if (!a->m_q || !a->m_scale) return set_error(A8_ERR_ARG, "momentum state missing");
-      if (!(a->m_block_size >= 32 && a->m_block_size <= 65536 && a->m_block_size % 4 == 0))
-        return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
+      if (!(a->m_block_size >= 32 && a->m_block_size <= (1 << 30) && a->m_block_size % 4 == 0))
+        return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 2^30]");
     }
   }
   if (a->factorize) {

@@ -1069,7 +1069,7 @@ __global__ __launch_bounds__(256) void k_fupdate(const DescF* __restrict__ table
 }
 
 // k_fupdate for coded momentum whose block size the unit layout cannot take
-// (B_M a multiple of 4 in [32, 65536], not a power of two up to 2048).  One
+// (B_M a multiple of 4 in [32, 2^30], not a power of two up to 2048).  One
 // workgroup covers h.unit = B_M * ceil(2048 / B_M) elements, a whole number of M
 // blocks and at least kUnit, so a tensor takes no more workgroups than its
 // W.nunit norm-partial slots; its last workgroup zeroes the slots it does not
@@ -1714,8 +1714,8 @@ int a8_factored_step(int dtype, int stochastic, const a8_tensor2d* tensors, int 
   if (has_m && !m32) {
     if (!((m_bits == 8 || m_bits == 4) && (m_mode == 0 || m_mode == 1)))
       return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");
-    if (m_block_size < 32 || m_block_size > 65536 || (m_block_size & 3))
-      return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
+    if (m_block_size < 32 || m_block_size > (1 << 30) || (m_block_size & 3))
+      return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 2^30]");
     if (m_block_size <= kUnit && !(m_block_size & (m_block_size - 1))) {
       lbm = 0;
       while ((1 << lbm) < m_block_size) ++lbm;

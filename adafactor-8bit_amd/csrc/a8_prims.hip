@@ -633,8 +633,8 @@ __global__ __launch_bounds__(256) void k_vema_gen(VemaDesc one, const VemaDesc* 
 }
 
 // AL block sizes: powers of two in [128, 2048] take the unit layout; other
-// multiples of 128 up to 65536 take k_vema_gen.
-static bool al_gen_ok(int64_t bs) { return bs >= 128 && bs % 128 == 0 && bs <= 65536; }
+// multiples of 128 (up to 2^30: block_size is a 32-bit int) take k_vema_gen.
+static bool al_gen_ok(int64_t bs) { return bs >= 128 && bs % 128 == 0 && bs <= (1 << 30); }
 
 static int lb_of(int64_t bs, int lo, int hi, int& lb, const char* what) {
   if (bs < lo || bs > hi || (bs & (bs - 1)) != 0) {
@@ -677,7 +677,7 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
   int lbv = 0;
   const bool gen = lb_of(block_size, 128, kPElems, lbv, "block_size") != 0;
   if (gen && !al_gen_ok(block_size))
-    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 2^30]");
   std::vector<VemaDesc> tab((size_t)n);
   int64_t wg = 0;
   for (int i = 0; i < n; ++i) {
@@ -1087,7 +1087,7 @@ int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, i
   int lbv = 0;
   const bool gen = lb_of(block_size, 128, kPElems, lbv, "block_size") != 0;
   if (gen && !al_gen_ok(block_size))
-    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 65536]");
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 in [128, 2^30]");
   const int64_t nblk = (numel + block_size - 1) / block_size;
   const int64_t nwg = gen ? nblk : (nblk * block_size + kPElems - 1) / kPElems;
   if (nwg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "numel too large");

@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
 
 // Coded momentum with a block size the reference accepts but the unit layout
 // cannot take (B_M a multiple of 4, at least 32, not a power of two in
-// [32, 2048]; up to 65536).  One workgroup covers `unit` elements: floor(2048 /
+// [32, 2048]; up to 2^30).  One workgroup covers `unit` elements: floor(2048 /
 // B_M) whole M blocks (one block when B_M > 2048).  Lanes take quads (a quad never
 // straddles a block, B_M % 4 == 0); each block's absmax meets in LDS (an exact
 // max).  Pass 1 forms m' and u and writes p (or m_out); pass 2, after the
@@ -406,11 +406,11 @@ static int m_codec(int m_bits, int m_mode, int& mk) {
 }
 
 // The momentum block: a power of two in [32, 2048] takes the unit layout (lbm);
-// any other multiple of 4 from 32 to 65536 takes k_sgd_gen (gen, bm, unit).
+// any other multiple of 4 from 32 to 2^30 takes k_sgd_gen (gen, bm, unit).
 static int block_log2(int bs, SgdHyp& h) {
   const bool pow2 = bs >= 32 && bs <= kSElems && (bs & (bs - 1)) == 0;
-  if (!pow2 && !(bs >= 32 && bs % 4 == 0 && bs <= 65536))
-    return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 65536]");
+  if (!pow2 && !(bs >= 32 && bs % 4 == 0 && bs <= (1 << 30)))
+    return set_error(A8_ERR_BLOCK, "m_block_size must be a multiple of 4 in [32, 2^30]");
   h.gen = pow2 ? 0 : 1;
   h.bm = bs;
   h.unit = pow2 ? kSElems : bs * (bs < kSElems ? kSElems / bs : 1);

@@ -56,7 +56,7 @@ static int check_common(int dtype, int64_t numel, int bv, int bm, int mbits, int
   if (vbits != 8 && vbits != 16) return set_error(A8_ERR_ARG, "v_bits must be 8 or 16");
   if (!has_m) bm = bv;
   if (!fast_shape_ok(bv, bm) && !gen_shape_ok(bv, bm))
-    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 (at most 65536) and m_block_size a "
+    return set_error(A8_ERR_BLOCK, "block_size must be a multiple of 128 (at most 2^30) and m_block_size a "
                                    "multiple of 4, at least 32, that divides block_size");
   if (has_m && !((mbits == 8 || mbits == 4) && (mmode == 0 || mmode == 1)))
     return set_error(A8_ERR_ARG, "m_bits must be 4/8 and m_mode 0/1");

@@ -654,9 +654,13 @@ void k_update1d(Desc1D one, const Desc1D* __restrict__ table, int ntab, Hyper1D 
 // exact max/min).  Pass 1 forms v', m', u, writes p (and v_buf in NORM) and the
 // statistics; pass 2, after the block fit, forms v' and m' again from the same
 // inputs (the same bits) and writes the codes.  The element arithmetic is
-// unit_step's, element for element.
-constexpr int kGenMaxBV = 65536;
-constexpr int kGenMaxMB = kGenMaxBV / 32;
+// unit_step's, element for element.  A V block holding more than kGenMaxMB M
+// blocks (B_V / B_M > 2048, so B_V > 65536) is taken in segments of kGenMaxMB M
+// blocks: pass 1 and then the M codes and scales segment by segment (a segment's
+// old scales are read only by its own quads), and after the last segment a pass
+// that writes the V codes.
+constexpr int kGenMaxMB = 2048;           // M blocks whose absmax LDS holds at once
+constexpr int kGenMaxBV = 1 << 30;        // block_size is a 32-bit int
 
 template <typename T, int VB, int MODE, bool SR, int MK, int KR>
 __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1D* __restrict__ table, int ntab,
@@ -685,13 +689,16 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
   const int64_t n = D.numel, base = blk * BV;
   const int nq = BV >> 2;
   const int mpb = kHasM ? BV / BM : 0;                        // M blocks per V block
+  constexpr bool kSegM = kWrite && kHasM;                      // M codes written, absmaxes in LDS
+  const int nseg = kSegM ? (mpb + kGenMaxMB - 1) / kGenMaxMB : 1;
+  const int segq = nseg > 1 ? kGenMaxMB * (BM >> 2) : nq;      // quads per segment (< 2^28 when nseg > 1)
   const int64_t nmb = kHasM ? (n + BM - 1) / BM : 0;          // M blocks of the tensor
   const int mk = (MK == 1) ? 1 : h.mk;
   const T* G = reinterpret_cast<const T*>(D.grad);
   T* P = reinterpret_cast<T*>(D.param);
   const float s_old = kVbuf ? 0.0f : gp(D.v_scale)[blk], lm_old = kVbuf ? 0.0f : gp(D.v_min_log)[blk];
   if (lane == 0) { s_st[0] = 0u; s_st[1] = 0xFFFFFFFFu; }
-  for (int i = lane; i < mpb; i += kLanes) s_mab[i] = 0u;
+  for (int i = lane; i < (mpb < kGenMaxMB ? mpb : kGenMaxMB); i += kLanes) s_mab[i] = 0u;
   if (VB == 8 && !kVbuf) s_tab[lane] = lane ? exp2_exact(al_dec_log<254>((float)(lane - 1), s_old, lm_old, KR)) : 0.0f;
   __syncthreads();
 
@@ -719,7 +726,10 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
   const bool mom = kHasM && h.momentum_only;
 
   // v' and m' of quad q (elements beyond the tensor: zero), and the quad's M block
-  auto quad_state = [&](int q, float* g, float* vn, float* mn, float* inv, int& cnt, int& mb, bool& m_ok) {
+  // need_m = false: v' only (the V-code pass after segmented M codes, whose M
+  // state is already the new one)
+  auto quad_state = [&](int q, float* g, float* vn, float* mn, float* inv, int& cnt, int& mb, bool& m_ok,
+                        bool need_m = true) {
     const int64_t i0 = base + 4 * q;
     cnt = i0 >= n ? 0 : (n - i0 >= 4 ? 4 : (int)(n - i0));
     load4n<T>(G, i0, n, g);
@@ -749,7 +759,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
       else inv[k] = __builtin_amdgcn_rsqf(fmaxf(vn[k], h.eps_sq));
     }
     mb = kHasM ? (4 * q) / BM : 0;
-    m_ok = kHasM && blk * mpb + mb < nmb;
+    m_ok = kHasM && need_m && blk * mpb + mb < nmb;
     if constexpr (kHasM) {
       float mo[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (m_ok) {
@@ -783,55 +793,94 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
       if (k >= cnt) { vn[k] = 0.0f; mn[k] = 0.0f; }
   };
 
-  // ---- pass 1: update, parameter, statistics
+  // the M codes of a quad from its M block's absmax bits
+  auto write_m = [&](int64_t i0, const float* mn, float ab) {
+    const float am = fmaxf(ab, 1e-12f);
+    const float ram = fast_rcp(am);
+    if (mk == 2 || mk == 4) {
+      const uint32_t w = ((m_encode(mk, mn[0], am, ram) << 4) | m_encode(mk, mn[1], am, ram)) |
+                         (((m_encode(mk, mn[2], am, ram) << 4) | m_encode(mk, mn[3], am, ram)) << 8);
+      *gp(reinterpret_cast<uint16_t*>(D.m_q + (i0 >> 1))) = (uint16_t)w;
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w |= m_encode(mk, mn[k], am, ram) << (8 * k);
+      *gp(reinterpret_cast<uint32_t*>(D.m_q + i0)) = w;
+    }
+  };
+
+  // ---- pass 1: update, parameter, statistics (by segments, see above)
   float sq = 0.0f;
   uint32_t vmax = 0u, vkey = 0xFFFFFFFFu;
   const uint32_t koff = KR ? 0u : 1u;   // block minimum keys, as unit_step
-  for (int q = lane; q < nq; q += kLanes) {
-    float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4], uu[4];
-    int cnt, mb;
-    bool m_ok;
-    quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
-    const int64_t i0 = base + 4 * q;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uu[k] = kHasM ? (mom ? mn[k] : mn[k] * inv[k]) : g[k] * inv[k];
-      if (k >= cnt) uu[k] = 0.0f;
-      if constexpr (kSq) {
-        const float t = (MODE == 4) ? mn[k] : ((mom && k < cnt) ? g[k] * inv[k] : uu[k]);
-        sq = __builtin_fmaf(t, t, sq);
-      }
-      vmax = max(vmax, __float_as_uint(vn[k]));
-      vkey = min(vkey, k < cnt ? __float_as_uint(vn[k]) - koff : 0xFFFFFFFFu);
-    }
-    if constexpr (MODE == 1) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (k < cnt) gp(D.v_buf)[i0 + k] = vn[k];
-    }
-    if constexpr (kWrite && kHasM) {
-      uint32_t ab = 0u;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) ab = max(ab, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
-      if (m_ok) atomicMax(&s_mab[mb], ab);
-    }
-    if constexpr (kWrite) {
-      const bool has_dec = D.decay || h.has_decay;
-      const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
+  for (int seg = 0; seg < nseg; ++seg) {
+    const int qb = seg * segq, qe = (nq - qb < segq) ? nq : qb + segq, mb0 = seg * kGenMaxMB;
+    for (int q = qb + lane; q < qe; q += kLanes) {
+      float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4], uu[4];
+      int cnt, mb;
+      bool m_ok;
+      quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
+      const int64_t i0 = base + 4 * q;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        if (k >= cnt) continue;
-        if constexpr (SR) {
-          const float pv = ld1<T>(P, i0 + k);
-          const T r = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(i0 + k));
-          uint16_t bits;
-          __builtin_memcpy(&bits, &r, 2);
-          gp(reinterpret_cast<uint16_t*>(P))[i0 + k] = bits;
-        } else {
-          pval_t<T> pv = ld1<T, pval_t<T>>(P, i0 + k);
-          if (has_dec) pv = pdec(pv, dec);
-          st1<T>(P, i0 + k, pupd(step, uu[k], pv));
+        uu[k] = kHasM ? (mom ? mn[k] : mn[k] * inv[k]) : g[k] * inv[k];
+        if (k >= cnt) uu[k] = 0.0f;
+        if constexpr (kSq) {
+          const float t = (MODE == 4) ? mn[k] : ((mom && k < cnt) ? g[k] * inv[k] : uu[k]);
+          sq = __builtin_fmaf(t, t, sq);
         }
+        vmax = max(vmax, __float_as_uint(vn[k]));
+        vkey = min(vkey, k < cnt ? __float_as_uint(vn[k]) - koff : 0xFFFFFFFFu);
+      }
+      if constexpr (MODE == 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (k < cnt) gp(D.v_buf)[i0 + k] = vn[k];
+      }
+      if constexpr (kWrite && kHasM) {
+        uint32_t ab = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ab = max(ab, __float_as_uint(mn[k]) & 0x7FFFFFFFu);
+        if (m_ok) atomicMax(&s_mab[mb - mb0], ab);
+      }
+      if constexpr (kWrite) {
+        const bool has_dec = D.decay || h.has_decay;
+        const float dec = D.decay ? *gp(D.decay) : (h.has_decay ? h.decay_val : 1.0f);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (k >= cnt) continue;
+          if constexpr (SR) {
+            const float pv = ld1<T>(P, i0 + k);
+            const T r = sr_round<T>(pv * dec - step * uu[k], D.sr_seed, h.sr_step, (uint64_t)(i0 + k));
+            uint16_t bits;
+            __builtin_memcpy(&bits, &r, 2);
+            gp(reinterpret_cast<uint16_t*>(P))[i0 + k] = bits;
+          } else {
+            pval_t<T> pv = ld1<T, pval_t<T>>(P, i0 + k);
+            if (has_dec) pv = pdec(pv, dec);
+            st1<T>(P, i0 + k, pupd(step, uu[k], pv));
+          }
+        }
+      }
+    }
+    if (nseg > 1) {
+      if constexpr (kSegM) {
+        __syncthreads();   // the segment's absmaxes are complete
+        for (int q = qb + lane; q < qe; q += kLanes) {
+          float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4];
+          int cnt, mb;
+          bool m_ok;
+          quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
+          if (m_ok) write_m(base + 4 * q, mn, __uint_as_float(s_mab[mb - mb0]));
+        }
+        __syncthreads();   // every lane has read the segment's old scales
+        const int nm = (mpb - mb0 < kGenMaxMB) ? mpb - mb0 : kGenMaxMB;
+        for (int i = lane; i < nm; i += kLanes) {
+          if (blk * mpb + mb0 + i < nmb)
+            gp(D.m_scale)[blk * mpb + mb0 + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+          s_mab[i] = 0u;
+        }
+        __syncthreads();
       }
     }
   }
@@ -850,6 +899,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
   }
   __syncthreads();
   if constexpr (kVbuf && !(kWrite && kHasM)) return;   // MNORM: no state written
+  if (kVbuf && nseg > 1) return;   // APPLY in segments: M codes and scales are written, V has none
 
   // ---- block fit (one lane pair) and pass 2: codes
   ALFit f{};
@@ -869,7 +919,7 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
     float g[4], vn[4], mn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, inv[4];
     int cnt, mb;
     bool m_ok;
-    quad_state(q, g, vn, mn, inv, cnt, mb, m_ok);
+    quad_state(q, g, vn, mn, inv, cnt, mb, m_ok, nseg == 1);
     const int64_t i0 = base + 4 * q;
     if constexpr (!kVbuf) {
       uint32_t code[4];
@@ -882,38 +932,26 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
             u32x2{code[0] | (code[1] << 16), code[2] | (code[3] << 16)};
       }
     }
-    if constexpr (kWrite && kHasM) {
-      if (m_ok) {
-        const float am = fmaxf(__uint_as_float(s_mab[mb]), 1e-12f);
-        const float ram = fast_rcp(am);
-        if (mk == 2 || mk == 4) {
-          const uint32_t w = ((m_encode(mk, mn[0], am, ram) << 4) | m_encode(mk, mn[1], am, ram)) |
-                             (((m_encode(mk, mn[2], am, ram) << 4) | m_encode(mk, mn[3], am, ram)) << 8);
-          *gp(reinterpret_cast<uint16_t*>(D.m_q + (i0 >> 1))) = (uint16_t)w;
-        } else {
-          uint32_t w = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) w |= m_encode(mk, mn[k], am, ram) << (8 * k);
-          *gp(reinterpret_cast<uint32_t*>(D.m_q + i0)) = w;
-        }
-      }
+    if constexpr (kSegM) {
+      if (m_ok) write_m(i0, mn, __uint_as_float(s_mab[mb]));   // one segment: mb0 = 0
     }
   }
   __syncthreads();   // every lane has read the old block metadata
   if (!kVbuf && lane == 0) { gp(D.v_scale)[blk] = f.s; gp(D.v_min_log)[blk] = f.lmin; }
-  if constexpr (kWrite && kHasM) {
-    for (int i = lane; i < mpb; i += kLanes)
-      if (blk * mpb + i < nmb) gp(D.m_scale)[blk * mpb + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+  if constexpr (kSegM) {
+    if (nseg == 1) {
+      for (int i = lane; i < mpb; i += kLanes)
+        if (blk * mpb + i < nmb) gp(D.m_scale)[blk * mpb + i] = fmaxf(__uint_as_float(s_mab[i]), 1e-12f);
+    }
   }
 }
 
-// ------------------------------------------------------------ norm finish
 // ------------------------------------------------------------ launch glue
 static bool fast_shape_ok(int bv, int bm) {
   auto pow2 = [](int x) { return x > 0 && (x & (x - 1)) == 0; };
   return pow2(bv) && bv >= 128 && bv <= 2048 && pow2(bm) && bm >= 32 && bm <= bv;
 }
-// The reference's rules (optimizer.py:1395-1416), up to kGenMaxBV.
+// The reference's rules (optimizer.py:1395-1416).
 static bool gen_shape_ok(int bv, int bm) {
   return bv >= 128 && bv % 128 == 0 && bv <= kGenMaxBV && bm >= 32 && bm % 4 == 0 && bv % bm == 0;
 }

@@ -104,7 +104,7 @@ int a8_set_qmap(const float* qmap8_host, const float* qmap4_host);
  *   log_floor   lower bound of a block's l_min (-126 for the reference's CPU rule;
  *               log2(max(eps1^2, FLT_MIN)) with A8_AL_KERNEL_RULE)
  *   v_bits      8 (AL8) or 16 (AL16), optionally | A8_AL_KERNEL_RULE
- * block_size: a multiple of 128 up to 65536; m_block_size: a multiple of 4, at least
+ * block_size: a multiple of 128 up to 2^30; m_block_size: a multiple of 4, at least
  * 32, dividing block_size (the reference's rules, optimizer.py:1395-1416).  Powers of
  * two (block_size <= 2048) run the 2048-element unit layout, other sizes one
  * workgroup per V block. */
@@ -335,7 +335,7 @@ typedef struct a8_tensor2d {
  * bias_mode: 0 none, 1 alpha *= bias_factor, 2 alpha /= bias_factor.
  * wd_mode: 0 none, 1 decay uses alpha, 2 decay uses lr.
  * v_bits: 8 / 16 (codes) or 0 (fp32 row_var/col_var).  block_size: V block
- * (any positive size).  m_block_size: a multiple of 4 in [32, 65536] (powers of
+ * (any positive size).  m_block_size: a multiple of 4 in [32, 2^30] (powers of
  * two up to 2048 take the tiled / unit layouts, other sizes whole M blocks per
  * workgroup).
  * table_dev: device buffer of a8_table_bytes_2d(ntensors) bytes (uploaded when upload != 0).
@@ -542,8 +542,8 @@ typedef struct a8_apollo_x_args {
  * momentum EMA, residual / confidence EMAs, and the update u = update_low.
  * With neither flag, the plain stage (optimizer.py:2759-2799): V EMA, momentum
  * EMA, u = x / (sqrt(v) + apollo_eps).  block_size (coded V, residual or
- * confidence): a multiple of 128 up to 65536; m_block_size (coded momentum): a
- * multiple of 4 in [32, 65536]. */
+ * confidence): a multiple of 128 up to 2^30; m_block_size (coded momentum): a
+ * multiple of 4 in [32, 2^30]. */
 int a8_apollo_lowrank_x(const a8_apollo_x_args* args, void* stream);
 int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low);
 
@@ -607,7 +607,7 @@ int a8_al_encode(void* q, float* scale, float* min_log, const float* x, int64_t 
  * apply=1) when Fira is on (else null); a non-finite norm then zeroes the update
  * (optimizer.py:797-800).  Momentum: m_q/m_scale (codes padded to whole
  * m_block_size blocks, m_bits/m_mode as in a8_fused_update_1d; m_block_size a
- * multiple of 4 in [32, 65536]), or fp32 m, or neither.  stochastic: 16-bit params
+ * multiple of 4 in [32, 2^30]), or fp32 m, or neither.  stochastic: 16-bit params
  * written with the kernels.cu:48-87 stream. */
 int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* grad, uint8_t* m_q, float* m_scale,
                 float* m, float* norm_buf, double* norm_parts, const float* fira, const float* alpha, const float* decay, int64_t numel,
@@ -647,7 +647,7 @@ int64_t a8_norm_parts_sgd(int64_t numel, int m_block_size);
  * _m_ema_pytorch (optimizer.py:690-701): m' = lerp(deq(m), x, 1 - beta) per
  * element (non-finite x read as 0), then one absmax per block and requantised
  * codes; fp32_out (optional) receives m'.  x: x_dtype (A8_F32/BF16/F16).
- * block_size: a multiple of 4 in [32, 65536]. */
+ * block_size: a multiple of 4 in [32, 2^30]. */
 int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype, float* fp32_out, double beta,
                        int block_size, int64_t numel, int m_bits, int m_mode, void* stream);
 
@@ -660,7 +660,7 @@ int a8_m_quantize_lerp(uint8_t* m_q, float* m_scale, const void* x, int x_dtype,
  * optimizer.py:677-685) with the arithmetic of its twin _deq_v -> lerp_ -> _quant_v
  * (optimizer.py:2232-2238): x = square_input ? x*x + eps1 : x (non-finite read as
  * 0); v' = lerp(deq(v), x, beta); per block of block_size (a multiple of 128 up to
- * 65536) the AL range is refit from the non-zero v' with floor log_floor;
+ * 2^30) the AL range is refit from the non-zero v' with floor log_floor;
  * fp32_out (optional) receives v'.  Codes past numel in the last block become 0.
  * q: uint8 (v_bits 8) or int16 (v_bits 16) codes padded to whole blocks. */
 int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, int x_dtype, float* fp32_out,

@@ -3,8 +3,7 @@
 The reference accepts any V block (B_V) that is a multiple of 128 and any momentum
 block (B_M) that is a multiple of 4, at least 32 and a divisor of B_V
 (optimizer.py:1395-1416).  Powers of two in [128, 2048] take the unit layout of
-k_update1d; every other size (and B_V up to 65536) takes k_update1d_gen, one
-workgroup per V block.  Against the oracle over 5 steps, to the parity bar of
+k_update1d; every other size takes k_update1d_gen, one workgroup per V block.  Against the oracle over 5 steps, to the parity bar of
 the reference-written fixtures: codes equal at step 1, later at most 1e-4 of
 codes (+1 per tensor) differ, by at most 2; block metadata within rtol 1e-5;
 parameters within rtol 1e-5 except the elements whose codes differed at some
@@ -59,13 +58,42 @@ CASES += [
 SHAPES = [(300, 77), (5000,), (4096,), (9000,)]
 
 
+# Blocks beyond 65536 (the reference's rules put no bound on B_V): a V block of
+# more than 2048 M blocks runs its M codes in segments of 2048 M blocks (B_V
+# 131200 at B_M 32: 4100 M blocks, three segments, the last of four; a tensor of
+# 70000 elements: one partial block of two segments), a power of two above 2048
+# at AL16 / UF4, the clip + Fira NORM / APPLY passes, no momentum, SGD's momentum
+# at B_M 70000, and the stand-alone AL EMA of fp32 momentum at B_V 131200.
+BIG_SHAPES = [(300000,), (70000,)]
+BIG_CASES = [
+    ("adamw_bv131200_bm32", dict(ADAMW, block_size=131200, m_block_size=32)),
+    ("adamw_bv262144_bm64_uf4_al16", dict(ADAMW, block_size=262144, m_block_size=64, m_quant_type="uf4",
+                                          v_quant_type="al16")),
+    ("adamw_bv131200_bm32_clip_fira", dict(ADAMW, block_size=131200, m_block_size=32, d=1.0,
+                                           enable_fira_for_adafactor=True)),
+    ("rmsprop_bv131200", dict(ADAMW, beta1=None, beta2=0.99, block_size=131200)),
+    ("sgd_bv560000_bm70000", dict(SGD, block_size=560000, m_block_size=70000)),
+    ("adamw_fp32m_bv131200", dict(ADAMW, m_quant_type="fp32", block_size=131200)),
+]
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
 def test_general_block_sizes_match_oracle(name, kw):
+    _general_vs_oracle(name, kw, SHAPES)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw", BIG_CASES, ids=[c[0] for c in BIG_CASES])
+def test_blocks_beyond_65536_match_oracle(name, kw):
+    _general_vs_oracle(name, kw, BIG_SHAPES)
+
+
+def _general_vs_oracle(name, kw, shapes):
     from adafactor8bit import Adafactor8Bit
     from oracle.fallback import OracleOptimizer
     print(f"[block sizes] {name}", flush=True)
-    pc = [torch.nn.Parameter(make_param(s, i, 9)) for i, s in enumerate(SHAPES)]
+    pc = [torch.nn.Parameter(make_param(s, i, 9)) for i, s in enumerate(shapes)]
     pg = [torch.nn.Parameter(p.detach().clone().cuda()) for p in pc]
     p0 = [p.detach().clone() for p in pc]
     oc, og = OracleOptimizer(pc, **kw), Adafactor8Bit(pg, **kw)

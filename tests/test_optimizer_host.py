@@ -18,10 +18,12 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
     (dict(ADAMW, block_size=384, m_block_size=128), [(64, 64)], True),      # quantised 1-D V: any size
     (dict(ADAMW, block_size=1152, m_block_size=36), [(64, 64)], True),
     (dict(ADAMW, block_size=6400, m_block_size=100, m_quant_type="uf4"), [(64, 64)], True),
-    (dict(ADAMW, block_size=131072, m_block_size=256), [(64, 64)], False),   # beyond 65536
+    (dict(ADAMW, block_size=131072, m_block_size=256), [(64, 64)], True),    # one workgroup per V block
+    (dict(ADAMW, block_size=(1 << 30) + 128, m_block_size=128), [(64, 64)], False),   # beyond 2^30
     (dict(ADAMW, block_size=384, m_block_size=128, m_quant_type="fp32"), [(64, 64)], True),   # fp32 M: AL EMA
     (dict(ADAMW, apollo_rank=4, block_size=384, m_block_size=128), [(64, 64)], True),         # APOLLO low-rank V
-    (dict(ADAMW, apollo_rank=4, block_size=131072, m_block_size=128), [(64, 64)], False),     # beyond 65536
+    (dict(ADAMW, apollo_rank=4, block_size=131072, m_block_size=128), [(64, 64)], True),
+    (dict(ADAMW, apollo_rank=4, block_size=(1 << 30) + 128, m_block_size=128), [(64, 64)], False),   # beyond 2^30
     (dict(ADAMW, block_size=384, m_block_size=128), [(63, 64)], True),      # below min_8bit_size
     (dict(ADAMW, block_size=384, m_block_size=128, quantize=False), [(64, 64)], True),
     (dict(ADAMW, block_size=384, m_block_size=128, v_quant_type="fp32", m_quant_type="fp32"), [(64, 64)], True),
@@ -37,7 +39,8 @@ ADAMW = dict(lr=1e-3, beta1=0.9, beta2=0.999, factored=False, relative_step=Fals
     (dict(lr=1e-2, beta1=0.9, beta2=None, beta2_decay=None, relative_step=False, block_size=1152,
           m_block_size=36), [(64, 64)], True),                                # SGD with coded momentum
     (dict(ADAMW, v_quant_type="fp32", block_size=6400, m_block_size=100), [(64, 64)], True),  # fp32 V, coded M
-    (dict(ADAMW, v_quant_type="fp32", block_size=131072, m_block_size=131072), [(64, 64)], False)
+    (dict(ADAMW, v_quant_type="fp32", block_size=131072, m_block_size=131072), [(64, 64)], True),
+    (dict(ADAMW, v_quant_type="fp32", block_size=(1 << 30) + 128, m_block_size=(1 << 30) + 128), [(64, 64)], False)
 ])
 def test_block_sizes_checked_at_construction(kw, shapes, ok):
     if ok:
@@ -49,7 +52,7 @@ def test_block_sizes_checked_at_construction(kw, shapes, ok):
 
 def test_add_param_group_rejects_and_leaves_groups_unchanged():
     opt, _ = _opt([(64, 64)], **dict(ADAMW))
-    bad = {"params": [torch.nn.Parameter(torch.zeros(5000))], "block_size": 131072, "m_block_size": 128}
+    bad = {"params": [torch.nn.Parameter(torch.zeros(5000))], "block_size": (1 << 30) + 128, "m_block_size": 128}
     with pytest.raises(ValueError):
         opt.add_param_group(bad)
     assert len(opt.param_groups) == 1

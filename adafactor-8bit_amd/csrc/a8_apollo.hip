@@ -908,6 +908,185 @@ __device__ __forceinline__ void proj_wide(const ApDesc& D, const ApL& L, int til
   if (lane == 0) ws_d_set(D.ws, L.gpart, gt, t);
 }
 
+// Eight waves per wide tile, two per SIMD: waves (channel half gh, output quarter
+// oq) each own a 128 x 64 block (4 x 2 MFMA tiles, 128 accumulators), so one
+// wave's MFMAs issue while the other of its SIMD waits on LDS or staging.  The
+// staging of the next slab is split over 512 lanes (8 loads and 8 LDS stores
+// each), and a channel's squares over two lanes (k 0-15 and 16-31 of every slab),
+// added once at the end.
+template <bool RIGHT, bool FULL>
+__device__ __forceinline__ void proj_wide8(const ApDesc& D, const ApL& L, int tile, uint16_t* gsl, u32x4* psl,
+                                           double* sred) {
+  const int tid = threadIdx.x, l = tid & 63, l32 = l & 31, hi = l >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gh = w >> 2, oq = w & 3;   // the wave's channel half and output quarter
+  const int pass = (int)(tile / L.ntr);
+  const int64_t gt = tile - (int64_t)pass * L.ntr;
+  const int64_t R = D.R, C = D.C, r = D.r;
+  const int64_t K = RIGHT ? C : R, nch = RIGHT ? R : C;
+  const int64_t ch0 = gt * kApW;
+  const int64_t nblk = L.rp / 32;
+  const int64_t nslab = (K + 31) / 32;
+  const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
+  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
+  const bool pass0 = pass == 0;
+  // G loader.  Right: rows (tid >> 2) + 128 i, eight k at 8 (tid & 3).  Left: k
+  // rows 2 (tid & 15) + i, eight columns at 8 (tid >> 4), stored transposed as
+  // pairs of k in one 32-bit word.
+  auto ldG1 = [&](int64_t k0, int i) -> u32x4 {
+    if constexpr (RIGHT) {
+      const int64_t row = ch0 + (tid >> 2) + 128 * i, k = k0 + 8 * (tid & 3);
+      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + k) * 2));
+      const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
+      return ldg8(G, row * C + k, row < R ? cnt : 0, D.valign);
+    } else {
+      const int64_t row = k0 + 2 * (tid & 15) + i, col = ch0 + 8 * (tid >> 4);
+      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + col) * 2));
+      const int cnt = C - col >= 8 ? 8 : (C - col > 0 ? (int)(C - col) : 0);
+      return ldg8(G, row * C + col, row < K ? cnt : 0, D.valign);
+    }
+  };
+  // G store, piece i of 2: right, row piece i; left, columns 4 i .. 4 i + 3 of the
+  // lane's eight (both k rows)
+  auto stG1 = [&](const u32x4* f, uint16_t* sl, int i) {
+    if constexpr (RIGHT) {
+      *reinterpret_cast<u32x4*>(&sl[((tid >> 2) + 128 * i) * kApWS + 8 * (tid & 3)]) = scrub8(f[i]);
+    } else {
+      const int kp = 2 * (tid & 15), c0 = 8 * (tid >> 4);
+      const u32x4 a = scrub8(f[0]), b = scrub8(f[1]);   // k rows kp, kp + 1
+      const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 4 * i; e < 4 * i + 4; ++e) {
+        const uint32_t lo = (e & 1) ? (wa[e >> 1] >> 16) : (wa[e >> 1] & 0xFFFFu);
+        const uint32_t hv = (e & 1) ? (wb[e >> 1] & 0xFFFF0000u) : (wb[e >> 1] << 16);
+        *reinterpret_cast<uint32_t*>(&sl[(c0 + e) * kApWS + kp]) = lo | hv;
+      }
+    }
+  };
+  // P: units tid + 512 i of the slab's 3072 (term i / 2)
+  auto ldP1 = [&](int64_t kc, int i) -> u32x4 {
+    return gp(Ps)[((kc * 3 + (i >> 1)) * nblk + 8 * pass) * 128 + tid + 512 * (i & 1)];
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[q][c] = f32x16{};
+  double nsq = 0.0;   // squares of channel ch0 + (tid & 255), k half tid >> 8
+  u32x4 fg[2], fp[6];   // the next slab, between its loads and its LDS stores
+  // One slab from LDS buffer b, 48 MFMAs, the other instructions placed between
+  // them in a fixed order (scheduling fences):
+  //   before MFMA 0: sub-step 0's G fragments, its first P term, the two
+  //     channel-row reads;
+  //   sub-step 0 (MFMAs 0-23): after MFMA m the square of channel element m
+  //     (m < 16); P terms 1-2 (m 0-3), the next slab's 8 global loads (m 4-11),
+  //     sub-step 1's G fragments (m 12-15), its P terms 0-1 (m 16-19, into the
+  //     registers of sub-step 0's dead terms);
+  //   sub-step 1 (MFMAs 24-47): its P term 2 (m 0-1), then after every third
+  //     MFMA one of the next slab's 8 LDS stores (6 P units, 2 G pieces).
+  auto slab = [&](const int b, const int64_t kn, auto next) {
+    constexpr bool NEXT = decltype(next)::value;
+    const uint16_t* gs = gsl + b * kApWGh;
+    const u32x4* ps = psl + b * kApWPu;
+    uint16_t* gn = gsl + (b ^ 1) * kApWGh;
+    u32x4* pn = psl + (b ^ 1) * kApWPu;
+    u32x4 ga[4], gb[4], pa[3][2], pb[3][2], cr[2];
+    auto rdG = [&](int j, int q) {
+      return *reinterpret_cast<const u32x4*>(&gs[(gh * 128 + 32 * q + l32) * kApWS + 16 * hi + 8 * j]);
+    };
+    auto rdP = [&](int j, int t, int c) { return ps[((t * 8 + oq * 2 + c) * 2 + j) * 64 + l]; };
+    auto rdC = [&](int g) {
+      return *reinterpret_cast<const u32x4*>(&gs[(tid & 255) * kApWS + 16 * (tid >> 8) + 8 * g]);
+    };
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ga[q] = rdG(0, q);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) pa[0][c] = rdP(0, 0, c);
+    cr[0] = rdC(0);
+    cr[1] = rdC(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < 24; ++m) {
+      const int t = m / 8, c = (m / 4) % 2, q = m % 4;
+      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[q]), as_bf8(pa[t][c]), acc[q][c]);
+      else acc[q][c] = mfma(as_bf8(pa[t][c]), as_bf8(ga[q]), acc[q][c]);
+      if (m < 16) {
+        const uint32_t wv = cr[m / 8][(m / 2) % 4];
+        const float x = __uint_as_float((m & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
+        nsq += (double)(x * x);
+      }
+      if (m < 4) {
+        pa[1 + m / 2][m % 2] = rdP(0, 1 + m / 2, m % 2);
+      } else if (m < 12) {
+        if constexpr (NEXT) {
+          if (m < 10) fp[m - 4] = ldP1(kn, m - 4);
+          else fg[m - 10] = ldG1(32 * kn, m - 10);
+        }
+      } else if (m < 16) {
+        gb[m - 12] = rdG(1, m - 12);
+      } else if (m < 20) {
+        pb[(m - 16) / 2][m % 2] = rdP(1, (m - 16) / 2, m % 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int m = 0; m < 24; ++m) {
+      const int t = m / 8, c = (m / 4) % 2, q = m % 4;
+      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(gb[q]), as_bf8(pb[t][c]), acc[q][c]);
+      else acc[q][c] = mfma(as_bf8(pb[t][c]), as_bf8(gb[q]), acc[q][c]);
+      if (m < 2) pb[2][m] = rdP(1, 2, m);
+      if constexpr (NEXT) {
+        if (m % 3 == 2) {
+          const int pc = m / 3;
+          if (pc < 6) pn[tid + 512 * pc] = fp[pc];
+          else stG1(fg, gn, pc - 6);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < 2; ++i) fg[i] = ldG1(0, i);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) psl[tid + 512 * i] = ldP1(0, i);
+  stG1(fg, gsl, 0);
+  stG1(fg, gsl, 1);
+  __syncthreads();
+  // slab s's LDS stores go to the other buffer, whose readers finished slab s - 1
+  // before the last barrier
+  for (int64_t s = 0; s + 1 < nslab; ++s) {
+    slab((int)(s & 1), s + 1, std::true_type{});
+    __syncthreads();
+  }
+  slab((int)((nslab - 1) & 1), nslab, std::false_type{});
+  float* glow = D.ws + L.glow;
+  const int64_t gx0 = ch0 + gh * 128, ox0 = (int64_t)pass * kApW + oq * 64;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if constexpr (RIGHT) store_acc(acc[q][c], glow, r, gx0 + 32 * q, ox0 + 32 * c + l32, R, r, hi);
+      else store_acc(acc[q][c], glow, C, ox0 + 32 * c, gx0 + 32 * q + l32, r, C, hi);
+    }
+  if (!pass0) return;
+  // a channel's two k halves, then the tile's channels in the order of four waves
+  double* half1 = sred + 8;
+  if (tid >= kApW) half1[tid - kApW] = nsq;
+  __syncthreads();
+  double tot = 0.0;
+  if (tid < kApW) {
+    const int64_t ch = ch0 + tid;
+    if (ch < nch) {
+      tot = nsq + half1[tid];
+      gp(D.ws + L.ngsq)[ch] = norm_sq(tot);
+    }
+  }
+  tot = grp_sum_d(tot, 64);
+  if ((tid & 63) == 0) sred[tid >> 6] = tot;
+  __syncthreads();
+  if (tid == 0) ws_d_set(D.ws, L.gpart, gt, ((sred[0] + sred[1]) + sred[2]) + sred[3]);
+}
+
 // ------------------------------------------------------------ MFMA projection (fp32 G)
 // fp32 G (fp32 parameters; fp16 / fp64 ones project grad.float()) takes the same
 // tiles with G split as P is: hi + mid + lo bf16 terms that sum to the fp32 value
@@ -1263,6 +1442,24 @@ void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
     if (nb == 2) proj_left<false, 2>(D, L, local, ldsT, sred);
     else if (nb == 1) proj_left<false, 1>(D, L, local, ldsT, sred);
     else proj_left<false, 0>(D, L, local, ldsT, sred);
+  }
+}
+
+// Wide tiles of both sides, eight waves (one workgroup per CU: 138 KB of LDS).
+__global__ __launch_bounds__(512) void k_ap_proj_w8(ApDesc one, const ApDesc* tab, int ntab) {
+  __shared__ __attribute__((aligned(16))) uint16_t gsl[2 * kApWGh];
+  __shared__ u32x4 psl[2 * kApWPu];
+  __shared__ double sred[8 + kApW];
+  int local;
+  const ApDesc D = ap_pick(one, tab, ntab, 5, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
+  const int64_t ch0 = (local % L.ntr) * kApW;
+  if (D.R >= D.C) {
+    if (D.valign && ch0 + kApW <= D.R && D.C % 32 == 0) proj_wide8<true, true>(D, L, local, gsl, psl, sred);
+    else proj_wide8<true, false>(D, L, local, gsl, psl, sred);
+  } else {
+    if (D.valign && ch0 + kApW <= D.C && D.R % 32 == 0) proj_wide8<false, true>(D, L, local, gsl, psl, sred);
+    else proj_wide8<false, false>(D, L, local, gsl, psl, sred);
   }
 }
 
@@ -2118,8 +2315,8 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       if ((rc = check_launch("k_ap_proj_l"))) return rc;
     }
     if (nwt > 0) {
-      hipLaunchKernelGGL(k_ap_proj_w, dim3((unsigned)nwt), dim3(256), 0, st, one, dtab, n);
-      if ((rc = check_launch("k_ap_proj_w"))) return rc;
+      hipLaunchKernelGGL(k_ap_proj_w8, dim3((unsigned)nwt), dim3(512), 0, st, one, dtab, n);
+      if ((rc = check_launch("k_ap_proj_w8"))) return rc;
     }
     if (h.scale_param) {   // ||p||^2 of the parameter (fp64 parameters refuse scale_parameter above)
       for (int i = 0; i < n; ++i) {

@@ -35,6 +35,7 @@
 namespace a8 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kApTile = 64;     // G columns per left-side projection tile (and fp32 G's right-side tile)
@@ -194,11 +195,15 @@ __device__ __forceinline__ u32x4 ldg8(const uint16_t* base, int64_t off, int cnt
     if (j < cnt) w[j >> 1] |= (uint32_t)gp(base)[off + j] << (16 * (j & 1));
   return u32x4{w[0], w[1], w[2], w[3]};
 }
-// NaN / Inf (exponent all ones) -> +0 in both halves of a word.
+// NaN / Inf (exponent all ones) -> +0 in both halves of a word.  A half's
+// exponent field plus 0x0080 reaches bit 15 only when it is all ones (0x7F80 ->
+// 0x8000; the low half cannot carry into the high one), and a 16-bit arithmetic
+// shift by 15 turns that bit into the half's mask: four instructions a word.
+typedef short i16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t scrub2(uint32_t w) {
-  const uint32_t lo = ((w & 0x7F80u) == 0x7F80u) ? 0u : (w & 0xFFFFu);
-  const uint32_t hi = ((w & 0x7F800000u) == 0x7F800000u) ? 0u : (w & 0xFFFF0000u);
-  return lo | hi;
+  const uint32_t u = (w & 0x7F807F80u) + 0x00800080u;
+  const i16x2 m = __builtin_bit_cast(i16x2, u) >> (i16x2){15, 15};
+  return w & ~__builtin_bit_cast(uint32_t, m);
 }
 __device__ __forceinline__ u32x4 scrub8(u32x4 q) {
   return u32x4{scrub2(q.x), scrub2(q.y), scrub2(q.z), scrub2(q.w)};
@@ -913,7 +918,9 @@ __device__ __forceinline__ void proj_wide(const ApDesc& D, const ApL& L, int til
 // wave's MFMAs issue while the other of its SIMD waits on LDS or staging.  The
 // staging of the next slab is split over 512 lanes (8 loads and 8 LDS stores
 // each), and a channel's squares over two lanes (k 0-15 and 16-31 of every slab),
-// added once at the end.
+// added once at the end.  A lane's 16 squares of a slab are exact products summed
+// in fp32 by v_dot2_f32_bf16 (its rounding is the hardware's, within an ulp of
+// the fp32 sum); the slabs' sums accumulate in double.
 template <bool RIGHT, bool FULL>
 __device__ __forceinline__ void proj_wide8(const ApDesc& D, const ApL& L, int tile, uint16_t* gsl, u32x4* psl,
                                            double* sred) {
@@ -978,8 +985,8 @@ __device__ __forceinline__ void proj_wide8(const ApDesc& D, const ApL& L, int ti
   // them in a fixed order (scheduling fences):
   //   before MFMA 0: sub-step 0's G fragments, its first P term, the two
   //     channel-row reads;
-  //   sub-step 0 (MFMAs 0-23): after MFMA m the square of channel element m
-  //     (m < 16); P terms 1-2 (m 0-3), the next slab's 8 global loads (m 4-11),
+  //   sub-step 0 (MFMAs 0-23): after MFMA m the squares of channel elements
+  //     2m, 2m + 1 (m < 8, one v_dot2); P terms 1-2 (m 0-3), the next slab's 8 global loads (m 4-11),
   //     sub-step 1's G fragments (m 12-15), its P terms 0-1 (m 16-19, into the
   //     registers of sub-step 0's dead terms);
   //   sub-step 1 (MFMAs 24-47): its P term 2 (m 0-1), then after every third
@@ -991,6 +998,7 @@ __device__ __forceinline__ void proj_wide8(const ApDesc& D, const ApL& L, int ti
     uint16_t* gn = gsl + (b ^ 1) * kApWGh;
     u32x4* pn = psl + (b ^ 1) * kApWPu;
     u32x4 ga[4], gb[4], pa[3][2], pb[3][2], cr[2];
+    float sq16 = 0.0f;
     auto rdG = [&](int j, int q) {
       return *reinterpret_cast<const u32x4*>(&gs[(gh * 128 + 32 * q + l32) * kApWS + 16 * hi + 8 * j]);
     };
@@ -1010,10 +1018,11 @@ __device__ __forceinline__ void proj_wide8(const ApDesc& D, const ApL& L, int ti
       const int t = m / 8, c = (m / 4) % 2, q = m % 4;
       if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[q]), as_bf8(pa[t][c]), acc[q][c]);
       else acc[q][c] = mfma(as_bf8(pa[t][c]), as_bf8(ga[q]), acc[q][c]);
-      if (m < 16) {
-        const uint32_t wv = cr[m / 8][(m / 2) % 4];
-        const float x = __uint_as_float((m & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
-        nsq += (double)(x * x);
+      if (m < 8) {   // two squares per MFMA (v_dot2), the slab's 16 in fp32, then into double
+        const uint32_t wv = cr[m / 4][m % 4];
+        sq16 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wv), __builtin_bit_cast(bf16x2, wv), sq16,
+                                               false);
+        if (m == 7) nsq += (double)sq16;
       }
       if (m < 4) {
         pa[1 + m / 2][m % 2] = rdP(0, 1 + m / 2, m % 2);

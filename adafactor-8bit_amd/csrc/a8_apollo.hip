@@ -2124,12 +2124,14 @@ __global__ __launch_bounds__(256) void k_ap_apply(ApDesc one, const ApDesc* tab,
         for (int k = 0; k < 8; ++k) amax = max(amax, __float_as_uint(xv[k]) & 0x7FFFFFFFu);
         if (amax < 0x7F7F0000u) {
           // all eight finite and below the largest value that can round up:
-          // sr_bf16_hi without its guards
+          // sr_bf16_hi without its guards.  It rounds up when (hv >> 16) < (b &
+          // 0xFFFF), which is when b + (0xFFFF - (hv >> 16)) carries into the high
+          // half; the two high halves of a pair then make one word (v_perm).
+          uint32_t sv[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const uint32_t b = __float_as_uint(xv[k]);
-            w[k >> 1] |= ((b >> 16) + (uint32_t)(hv[k] < (b << 16))) << (16 * (k & 1));
-          }
+          for (int k = 0; k < 8; ++k) sv[k] = __float_as_uint(xv[k]) + (~hv[k] >> 16);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = __builtin_amdgcn_perm(sv[2 * j + 1], sv[2 * j], 0x07060302u);
         } else {
 #pragma unroll
           for (int k = 0; k < 8; ++k) w[k >> 1] |= (uint32_t)sr_bf16_hi(xv[k], hv[k]) << (16 * (k & 1));

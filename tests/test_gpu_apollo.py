@@ -18,13 +18,15 @@ that bound (_GemmCond), everything else to the fixed tolerances:
   (2^(2 s / 254) - 1, relative) of the reference's decoded value, widened by
   the difference of the two block ranges (|dl_min| + |ds| in log2 units), and by
   4 rel for elements of an ill-conditioned g_low.  Codes differ by at most 2,
-  and on at most 2% of the elements of blocks whose ranges agree to half a code
-  step (a moved range shifts its block's codes together).  The block's range is
+  and on at most 1% of the elements of blocks whose ranges agree to half a code
+  step (a moved range shifts its block's codes together; measured: at most
+  8.2e-3 on the bf16 fixtures, 9.8e-4 on the others).  The block's range is
   set by its smallest nonzero g_low^2, which can be a cancelling sum with a large
   relative error: block scale / min_log are held to 2e-2 absolute (log2 units),
   or, for a block beyond that, to the step-1 GEMM error envelope (at step 1) or
   its width (later steps, whose EMA remembers step 1).
-* M codes: at most 2% differ, by at most 2.  Block scales within rtol 1e-5.
+* M codes: at most 1% differ, by at most 2 (measured: at most 6.3e-3, by 1).
+  Block scales within rtol 1e-5.
 * Parameters (fp32): within 1e-5 relative plus 2e-3 of the largest
   displacement the reference's own steps made.  A flipped code moves one
   element of the low-rank update by a code step.  That moves its channel's
@@ -238,11 +240,16 @@ def _cmp_state(name, key, st, z, zkeys, norm_rtol=None, fp32_rtol=None, gc=None,
                 keep = drange < 0.5 * sref / 254.0
                 qa, qb = np.asarray(mine).reshape(sref.size, -1), np.asarray(ref).reshape(sref.size, -1)
                 frac = gu.code_mismatch(qa[keep], qb[keep])[0] if keep.any() else 0.0
-                assert mx <= 2 and frac <= 2e-2, f"{msg}: {frac:.2e} codes differ, max {mx}"
+                allf = gu.code_mismatch(mine, ref)[0]
+                print(f"  {msg}: {allf:.2e} of codes differ ({frac:.2e} in blocks whose range agrees), max {mx}",
+                      flush=True)
+                assert mx <= 2 and frac <= 1e-2, f"{msg}: {frac:.2e} codes differ, max {mx}"
         elif k.endswith("_q"):
             frac, mx = gu.code_mismatch(mine, ref)
             low_rank = k.startswith(("v_low", "m_low"))
-            allowed = 2e-2 if low_rank else 1e-4 + 1.0 / max(mine.size, 1)
+            allowed = 1e-2 if low_rank else 1e-4 + 1.0 / max(mine.size, 1)
+            if low_rank:
+                print(f"  {msg}: {frac:.2e} of codes differ, max {mx}", flush=True)
             assert mx <= 2 and frac <= allowed, f"{msg}: {frac:.2e} codes differ, max {mx}"
         elif k.startswith("v_low_") and (k.endswith("_scale") or k.endswith("_min_log")):
             off = np.abs(mine.astype(np.float64) - ref) > 2e-2

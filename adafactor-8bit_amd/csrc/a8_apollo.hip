@@ -713,205 +713,19 @@ __device__ __forceinline__ void proj_left(const ApDesc& D, const ApL& L, int til
 // ------------------------------------------------------------ MFMA projection, wide tiles
 // bf16 G at ranks that are a multiple of 256 (C4's rank 256): a workgroup
 // computes a 256-channel x 256-output tile of g_low (channels: G rows on the
-// right side, G columns on the left), each wave a 128 x 128 quarter as 4 x 4
-// MFMA blocks in accumulator registers.  Per 32-k slab the workgroup stages both
+// right side, G columns on the left).  Per 32-k slab the workgroup stages both
 // operands in LDS, double buffered: G, scrubbed, as [channel][k] rows, and the
 // chunk's split P for the tile's eight output blocks (fragment order, a plain
-// copy).  A wave then issues 48 MFMAs per 16 fragment reads, and each P unit is
-// fetched from L2 once per 256 channels: 6 bytes of split P per G element (the
-// narrower tiles above fetch it per wave, 16 bytes per element at 96 rows).  The
-// global loads of slab s + 1 are in flight while slab s is multiplied; one
-// barrier per slab publishes the next.  Lane i also sums the squares of channel
-// i from the staged slab (k order, double), for the channel norms.  FULL: all
-// 256 channels exist, K % 32 == 0 and rows are 16-byte aligned.
+// copy).  Each P unit is then fetched from L2 once per 256 channels: 6 bytes of
+// split P per G element (the narrower tiles above fetch it per wave, 16 bytes
+// per element at 96 rows).  The global loads of slab s + 1 are in flight while
+// slab s is multiplied; one barrier per slab publishes the next.  The squares
+// of each channel are summed from the staged slab for the channel norms.
+// FULL: all 256 channels exist, K % 32 == 0 and rows are 16-byte aligned.
 constexpr int kApW = kApWide;             // channels and outputs of a wide tile
 constexpr int kApWS = 40;                 // LDS row stride (halves) of the G slab: 32 k + 8 pad
 constexpr int kApWGh = kApW * kApWS;      // halves per G slab buffer (20 KB)
 constexpr int kApWPu = 3 * 8 * 2 * 64;    // 16-byte P units per slab: 3 terms x 8 blocks x 2 j x 64 lanes (48 KB)
-
-template <bool RIGHT, bool FULL>
-__device__ __forceinline__ void proj_wide(const ApDesc& D, const ApL& L, int tile, uint16_t* gsl, u32x4* psl,
-                                          double* sred) {
-  const int lane = threadIdx.x, l = lane & 63, l32 = l & 31, hi = l >> 5;
-  const int w = __builtin_amdgcn_readfirstlane(lane >> 6);
-  const int gh = w >> 1, oh = w & 1;   // the wave's channel half and output half
-  const int pass = (int)(tile / L.ntr);
-  const int64_t gt = tile - (int64_t)pass * L.ntr;
-  const int64_t R = D.R, C = D.C, r = D.r;
-  const int64_t K = RIGHT ? C : R, nch = RIGHT ? R : C;
-  const int64_t ch0 = gt * kApW;
-  const int64_t nblk = L.rp / 32;
-  const int64_t nslab = (K + 31) / 32;
-  const uint16_t* G = reinterpret_cast<const uint16_t*>(D.grad);
-  const u32x4* Ps = reinterpret_cast<const u32x4*>(D.ws + L.psplit);
-  const bool pass0 = pass == 0;
-  // G loader.  Right: rows (lane >> 2) + 64 i, eight k at 8 (lane & 3).  Left:
-  // k rows 2 (lane & 15) and + 1, eight columns at 8 ((lane >> 4) + 16 i), stored
-  // transposed as pairs of k in one 32-bit word.
-  auto ldG1 = [&](int64_t k0, int i) -> u32x4 {
-    if constexpr (RIGHT) {
-      const int64_t row = ch0 + (lane >> 2) + 64 * i, k = k0 + 8 * (lane & 3);
-      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + k) * 2));
-      const int cnt = K - k >= 8 ? 8 : (K - k > 0 ? (int)(K - k) : 0);
-      return ldg8(G, row * C + k, row < R ? cnt : 0, D.valign);
-    } else {
-      const int64_t row = k0 + 2 * (lane & 15) + (i & 1), col = ch0 + 8 * ((lane >> 4) + 16 * (i >> 1));
-      if constexpr (FULL) return ldu(G, (uint32_t)((row * C + col) * 2));
-      const int cnt = C - col >= 8 ? 8 : (C - col > 0 ? (int)(C - col) : 0);
-      return ldg8(G, row * C + col, row < K ? cnt : 0, D.valign);
-    }
-  };
-  auto stG = [&](const u32x4* f, uint16_t* sl) {
-    if constexpr (RIGHT) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<u32x4*>(&sl[((lane >> 2) + 64 * i) * kApWS + 8 * (lane & 3)]) = scrub8(f[i]);
-    } else {
-      const int kp = 2 * (lane & 15);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x4 a = scrub8(f[2 * h]), b = scrub8(f[2 * h + 1]);   // k rows kp, kp + 1
-        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-        const int c0 = 8 * ((lane >> 4) + 16 * h);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t lo = (e & 1) ? (wa[e >> 1] >> 16) : (wa[e >> 1] & 0xFFFFu);
-          const uint32_t hv = (e & 1) ? (wb[e >> 1] & 0xFFFF0000u) : (wb[e >> 1] << 16);
-          *reinterpret_cast<uint32_t*>(&sl[(c0 + e) * kApWS + kp]) = lo | hv;
-        }
-      }
-    }
-  };
-  // P: units lane + 256 i of the slab's 3072 (term i / 4)
-  auto ldP1 = [&](int64_t kc, int i) -> u32x4 {
-    return gp(Ps)[((kc * 3 + (i >> 2)) * nblk + 8 * pass) * 128 + lane + 256 * (i & 3)];
-  };
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[q][c] = f32x16{};
-  double nsq = 0.0;   // squares of channel ch0 + lane
-  u32x4 fg[4], fp[12];   // the next slab, between its loads and its LDS stores
-  // One slab from LDS buffer b, 96 MFMAs.  With one wave per SIMD nothing else
-  // fills the MFMA pipe, so the wave's other instructions are spread one or two
-  // per MFMA in a fixed order (scheduling fences): a burst of loads or LDS
-  // accesses would stall the in-order instruction stream and drain the pipe.
-  //   before MFMA 0: the fragments MFMAs 0-3 need and the first channel-row read;
-  //   sub-step 0 (MFMAs 0-47): after MFMA m, the square of channel element m
-  //     (m < 32); after even m an LDS read (the remaining P fragments, channel-row
-  //     reads, sub-step 1's P fragments, G fragment 0 of sub-step 1), after odd m
-  //     one of the next slab's 16 global loads (NEXT), then sub-step 1's G reads;
-  //   sub-step 1 (MFMAs 48-95): after every third MFMA one of the next slab's
-  //     16 LDS stores (the 12 P units, then the G rows).
-  auto slab = [&](const int b, const int64_t kn, auto next) {
-    constexpr bool NEXT = decltype(next)::value;
-    const uint16_t* gs = gsl + b * kApWGh;
-    const u32x4* ps = psl + b * kApWPu;
-    uint16_t* gn = gsl + (b ^ 1) * kApWGh;
-    u32x4* pn = psl + (b ^ 1) * kApWPu;
-    u32x4 ga[2][4], pb[3][4], pc1[3][4], cr[2];
-    auto rdG = [&](int j, int q) {
-      return *reinterpret_cast<const u32x4*>(&gs[(gh * 128 + 32 * q + l32) * kApWS + 16 * hi + 8 * j]);
-    };
-    auto rdP = [&](int j, int t, int c) { return ps[((t * 8 + oh * 4 + c) * 2 + j) * 64 + l]; };
-    auto rdC = [&](int g) { return *reinterpret_cast<const u32x4*>(&gs[lane * kApWS + 8 * g]); };
-#pragma unroll
-    for (int q = 0; q < 4; ++q) ga[0][q] = rdG(0, q);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) pb[0][c] = rdP(0, 0, c);
-    cr[0] = rdC(0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int m = 0; m < 48; ++m) {
-      const int t = m / 16, c = (m / 4) % 4, q = m % 4;
-      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[0][q]), as_bf8(pb[t][c]), acc[q][c]);
-      else acc[q][c] = mfma(as_bf8(pb[t][c]), as_bf8(ga[0][q]), acc[q][c]);
-      if (m < 32) {
-        const uint32_t wv = cr[(m / 8) & 1][(m / 2) % 4];
-        const float x = __uint_as_float((m & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
-        nsq += (double)(x * x);
-      }
-      const int a = m / 2;
-      if (m % 2 == 0) {
-        // even slots: cr1, P(t=1) x4, cr2, P(t=2) x4, cr3, sub-step 1's P x12, its G 0
-        if (a == 0) cr[1] = rdC(1);
-        else if (a <= 4) pb[1][a - 1] = rdP(0, 1, a - 1);
-        else if (a == 5) cr[0] = rdC(2);
-        else if (a <= 9) pb[2][a - 6] = rdP(0, 2, a - 6);
-        else if (a == 10) cr[1] = rdC(3);
-        else if (a <= 22) pc1[(a - 11) / 4][(a - 11) % 4] = rdP(1, (a - 11) / 4, (a - 11) % 4);
-        else ga[1][0] = rdG(1, 0);
-      } else {
-        // odd slots: the next slab's P units and G chunks, then sub-step 1's G 1-3
-        if (a < 12) {
-          if constexpr (NEXT) fp[a] = ldP1(kn, a);
-        } else if (a < 16) {
-          if constexpr (NEXT) fg[a - 12] = ldG1(32 * kn, a - 12);
-        } else if (a < 19) {
-          ga[1][a - 15] = rdG(1, a - 15);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int m = 0; m < 48; ++m) {
-      const int t = m / 16, c = (m / 4) % 4, q = m % 4;
-      if constexpr (RIGHT) acc[q][c] = mfma(as_bf8(ga[1][q]), as_bf8(pc1[t][c]), acc[q][c]);
-      else acc[q][c] = mfma(as_bf8(pc1[t][c]), as_bf8(ga[1][q]), acc[q][c]);
-      if constexpr (NEXT) {
-        if (m % 3 == 0) {
-          const int pc = m / 3;
-          if (pc < 12) {
-            pn[lane + 256 * pc] = fp[pc];
-          } else if constexpr (RIGHT) {
-            const int i = pc - 12;
-            *reinterpret_cast<u32x4*>(&gn[((lane >> 2) + 64 * i) * kApWS + 8 * (lane & 3)]) = scrub8(fg[i]);
-          } else {
-            const int h = (pc - 12) >> 1, eh = (pc - 12) & 1, kp = 2 * (lane & 15);
-            const u32x4 a = scrub8(fg[2 * h]), bq = scrub8(fg[2 * h + 1]);   // k rows kp, kp + 1
-            const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {bq.x, bq.y, bq.z, bq.w};
-            const int c0 = 8 * ((lane >> 4) + 16 * h);
-#pragma unroll
-            for (int e = 4 * eh; e < 4 * eh + 4; ++e) {
-              const uint32_t lo = (e & 1) ? (wa[e >> 1] >> 16) : (wa[e >> 1] & 0xFFFFu);
-              const uint32_t hv = (e & 1) ? (wb[e >> 1] & 0xFFFF0000u) : (wb[e >> 1] << 16);
-              *reinterpret_cast<uint32_t*>(&gn[(c0 + e) * kApWS + kp]) = lo | hv;
-            }
-          }
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-#pragma unroll
-  for (int i = 0; i < 4; ++i) fg[i] = ldG1(0, i);
-#pragma unroll
-  for (int i = 0; i < 12; ++i) psl[lane + 256 * i] = ldP1(0, i);
-  stG(fg, gsl);
-  __syncthreads();
-  // slab s's LDS stores go to the other buffer, whose readers finished slab s - 1
-  // before the last barrier
-  for (int64_t s = 0; s + 1 < nslab; ++s) {
-    slab((int)(s & 1), s + 1, std::true_type{});
-    __syncthreads();
-  }
-  slab((int)((nslab - 1) & 1), nslab, std::false_type{});
-  float* glow = D.ws + L.glow;
-  const int64_t gx0 = ch0 + gh * 128, ox0 = (int64_t)pass * kApW + oh * 128;
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if constexpr (RIGHT) store_acc(acc[q][c], glow, r, gx0 + 32 * q, ox0 + 32 * c + l32, R, r, hi);
-      else store_acc(acc[q][c], glow, C, ox0 + 32 * c, gx0 + 32 * q + l32, r, C, hi);
-    }
-  if (!pass0) return;
-  const int64_t ch = ch0 + lane;
-  if (ch < nch) gp(D.ws + L.ngsq)[ch] = norm_sq(nsq);
-  const double t = ap_wg_sum(ch < nch ? nsq : 0.0, sred);
-  if (lane == 0) ws_d_set(D.ws, L.gpart, gt, t);
-}
 
 // Eight waves per wide tile, two per SIMD: waves (channel half gh, output quarter
 // oq) each own a 128 x 64 block (4 x 2 MFMA tiles, 128 accumulators), so one
@@ -1455,12 +1269,24 @@ void k_ap_proj_l(ApDesc one, const ApDesc* tab, int ntab) {
 }
 
 // Wide tiles of both sides, eight waves (one workgroup per CU: 138 KB of LDS).
-__global__ __launch_bounds__(512) void k_ap_proj_w8(ApDesc one, const ApDesc* tab, int ntab) {
+// Workgroups are dealt to the 8 XCDs round-robin by index; XCD x takes the
+// contiguous tile range [start[x], start[x + 1]) in order (its L2 then holds
+// the P split of one or two matrices at a time).  The host cuts the ranges at
+// equal cost (slabs of K) rather than equal tile counts: K differs between
+// matrices (k / v against the rest), and count-equal ranges left one XCD with
+// 12% more work than the average.  Slots past an XCD's range exit at once.
+struct ApXcd {
+  int32_t start[9];
+};
+__global__ __launch_bounds__(512) void k_ap_proj_w8(ApDesc one, const ApDesc* tab, int ntab, ApXcd xs) {
   __shared__ __attribute__((aligned(16))) uint16_t gsl[2 * kApWGh];
   __shared__ u32x4 psl[2 * kApWPu];
   __shared__ double sred[8 + kApW];
+  const int x = (int)blockIdx.x % 8;
+  const int wg = xs.start[x] + (int)blockIdx.x / 8;
+  if (wg >= xs.start[x + 1]) return;
   int local;
-  const ApDesc D = ap_pick(one, tab, ntab, 5, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
+  const ApDesc D = ap_pick(one, tab, ntab, 5, wg, local);
   const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
   const int64_t ch0 = (local % L.ntr) * kApW;
   if (D.R >= D.C) {
@@ -1469,24 +1295,6 @@ __global__ __launch_bounds__(512) void k_ap_proj_w8(ApDesc one, const ApDesc* ta
   } else {
     if (D.valign && ch0 + kApW <= D.C && D.R % 32 == 0) proj_wide8<false, true>(D, L, local, gsl, psl, sred);
     else proj_wide8<false, false>(D, L, local, gsl, psl, sred);
-  }
-}
-
-// Wide tiles of both sides (one workgroup per CU: 136 KB of LDS).
-__global__ __launch_bounds__(256) void k_ap_proj_w(ApDesc one, const ApDesc* tab, int ntab) {
-  __shared__ __attribute__((aligned(16))) uint16_t gsl[2 * kApWGh];
-  __shared__ u32x4 psl[2 * kApWPu];
-  __shared__ double sred[8];
-  int local;
-  const ApDesc D = ap_pick(one, tab, ntab, 5, xcd_order((int)blockIdx.x, (int)gridDim.x), local);
-  const ApL L = ap_layout(D.R, D.C, D.r, D.trows);
-  const int64_t ch0 = (local % L.ntr) * kApW;
-  if (D.R >= D.C) {
-    if (D.valign && ch0 + kApW <= D.R && D.C % 32 == 0) proj_wide<true, true>(D, L, local, gsl, psl, sred);
-    else proj_wide<true, false>(D, L, local, gsl, psl, sred);
-  } else {
-    if (D.valign && ch0 + kApW <= D.C && D.R % 32 == 0) proj_wide<false, true>(D, L, local, gsl, psl, sred);
-    else proj_wide<false, false>(D, L, local, gsl, psl, sred);
   }
 }
 
@@ -2326,7 +2134,28 @@ static int apollo_run(int phase, int dtype, int stochastic, const a8_apollo_tens
       if ((rc = check_launch("k_ap_proj_l"))) return rc;
     }
     if (nwt > 0) {
-      hipLaunchKernelGGL(k_ap_proj_w8, dim3((unsigned)nwt), dim3(512), 0, st, one, dtab, n);
+      // cost-balanced XCD ranges over the wide tiles in table order (cost of a
+      // tile: its slabs of K plus a few for the prologue and epilogue)
+      ApXcd xs{};
+      int64_t total = 0;
+      for (int i = 0; i < n; ++i)
+        if (tab[(size_t)i].trows == kApWide) {
+          const ApL L = ap_layout(tab[(size_t)i].R, tab[(size_t)i].C, tab[(size_t)i].r, kApWide);
+          total += L.ntile * ((L.K + 31) / 32 + 4);
+        }
+      int xi = 1;
+      int64_t cum = 0, wg = 0;
+      for (int i = 0; i < n; ++i) {
+        if (tab[(size_t)i].trows != kApWide) continue;
+        const ApL L = ap_layout(tab[(size_t)i].R, tab[(size_t)i].C, tab[(size_t)i].r, kApWide);
+        const int64_t c = (L.K + 31) / 32 + 4;
+        for (int64_t j = 0; j < L.ntile; ++j, ++wg, cum += c)
+          while (xi < 8 && cum * 8 >= total * xi) xs.start[xi++] = (int32_t)wg;
+      }
+      while (xi <= 8) xs.start[xi++] = (int32_t)wg;
+      int32_t most = 0;
+      for (int k = 0; k < 8; ++k) most = std::max(most, xs.start[k + 1] - xs.start[k]);
+      hipLaunchKernelGGL(k_ap_proj_w8, dim3((unsigned)(8 * most)), dim3(512), 0, st, one, dtab, n, xs);
       if ((rc = check_launch("k_ap_proj_w8"))) return rc;
     }
     if (h.scale_param) {   // ||p||^2 of the parameter (fp64 parameters refuse scale_parameter above)

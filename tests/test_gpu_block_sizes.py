@@ -231,6 +231,9 @@ ACASES = [
     ("apollo_came_bv640_bm160", dict(APOLLO_BASE, beta3=0.9999, d=1.0, eps_came=1e-16, block_size=640,
                                      m_block_size=160)),
     ("apollo_fact_bm36", dict(APOLLO_BASE, apollo_factorize=True, block_size=1152, m_block_size=36)),
+    # a V block beyond 65536 (2188 M blocks each: the segmented general kernel) on the low-rank
+    # state of a 3000 x 200 matrix (96,000 low-rank elements: one whole block and a ragged one)
+    ("apollo_plain_bv70016_bm32", dict(APOLLO_BASE, block_size=70016, m_block_size=32)),
     # power-of-two blocks: the fused low-rank tails (k_fact_tail, k_came_tail) in each state form
     ("apollo_fact_fp32m", dict(APOLLO_BASE, apollo_factorize=True, m_quant_type="fp32")),
     ("apollo_fact_uf4", dict(APOLLO_BASE, apollo_factorize=True, m_quant_type="uf4", m_block_size=64)),
@@ -240,6 +243,7 @@ ACASES = [
     ("apollo_came_fp32m_d0", dict(APOLLO_BASE, beta3=0.9999, d=0.0, eps_came=1e-16, m_quant_type="fp32")),
 ]
 ASHAPES = [(300, 200), (160, 420)]
+BIG_ASHAPES = [(3000, 200), (160, 420)]
 
 
 class _Z(dict):
@@ -262,18 +266,19 @@ def test_apollo_general_blocks_match_oracle(name, kw, monkeypatch):
     monkeypatch.setattr(F, "stable_randn", inputs.make_proj)
     old = F.set_exact_reductions(True)
     plain = name.startswith("apollo_plain")
+    shapes = BIG_ASHAPES if kw.get("block_size", 2048) > 65536 else ASHAPES
     try:
         print(f"[block sizes] {name}", flush=True)
-        init = [inputs.make_param(s, i, 17) for i, s in enumerate(ASHAPES)]
+        init = [inputs.make_param(s, i, 17) for i, s in enumerate(shapes)]
         pg = [torch.nn.Parameter(x.clone().cuda()) for x in init]
         pc = [torch.nn.Parameter(x.clone()) for x in init]
         og, oc = Adafactor8Bit(pg, **kw), F.OracleOptimizer(pc, **kw)
-        lows = [(R, 32) if R >= C else (32, C) for R, C in ASHAPES]
+        lows = [(R, 32) if R >= C else (32, C) for R, C in shapes]
         glows = {}
         oc.glow_hook = lambda p, _g, _pt: glows[id(p)]
         for t in range(1, 6):
             for i, (a, b) in enumerate(zip(pc, pg)):
-                g = inputs.make_grad(ASHAPES[i], i, t, 17, zero_frac=0.0)
+                g = inputs.make_grad(shapes[i], i, t, 17, zero_frac=0.0)
                 a.grad, b.grad = g.clone(), g.cuda()
             og.step()
             torch.cuda.synchronize()

@@ -355,7 +355,7 @@ class Adafactor8Bit(Optimizer):
                 bkey, rec, fin = _apollo_prep(self, p, g, st, group, dsc)
                 ap_batches.setdefault(bkey, []).append((rec, fin))
                 continue
-            plan = _plan_param(p, g, st, group)
+            plan = _plan_param(p, _grad_work(self, p, g, g.dtype, group["maximize"]), st, group)
             plan.dsc = dsc
             if plan.path == "q1d_fp32m":
                 _prep_q1d_fp32m(self, plan)
@@ -508,7 +508,7 @@ class _Plan:
             return None
         if self.alpha_t is not None or self.decay_t is not None:
             return None
-        if self.maximize or self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
+        if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
         if self.path == "f1d" and (self.d > 0 or self.fira or self.rms_kernel):
             if self.lag:
@@ -538,6 +538,29 @@ class _Plan:
                 self.alpha_val, self.decay_val)
 
 
+def _grad_work(opt, p, grad, dtype, negate):
+    """The gradient the kernels read.  p.grad itself when it is contiguous, of
+    ``dtype`` and not negated; otherwise a copy -- contiguous, converted (fp32 for
+    fp16 / fp64 APOLLO, as the reference's grad.float(), optimizer.py:2601) and/or
+    negated (maximize, optimizer.py:1971-1973, 2604-2605) -- in a buffer kept per
+    parameter, so that its address is the same every step: multi-tensor tables stay
+    valid and a captured step reads the buffer its copy kernel refills."""
+    if grad.is_contiguous() and grad.dtype == dtype and not negate:
+        return grad
+    key = (p.device, "gwork", id(p))
+    buf = opt._ws.get(key)
+    if buf is None or buf.shape != grad.shape or buf.dtype != dtype:
+        buf = torch.empty(grad.shape, dtype=dtype, device=grad.device)
+        opt._ws[key] = buf
+    if negate and grad.dtype == dtype:
+        torch.neg(grad, out=buf)
+    else:
+        buf.copy_(grad)
+        if negate:
+            buf.neg_()
+    return buf
+
+
 def _plan_param(p, grad, st, group) -> _Plan:
     P = _Plan()
     P.p, P.st, P.group = p, st, group
@@ -564,11 +587,8 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P.eps_g = eps1 if not P.adam_denom else 0.0
     mo = group.get("momentum_only_1d")
     P.mom_only = (not P.adam_denom) if mo is None else bool(mo)
-    P.maximize = group["maximize"]
-    g = grad if grad.is_contiguous() else grad.contiguous()
-    if P.maximize:
-        g = g.neg()
-    P.g = g
+    P.maximize = group["maximize"]   # the caller hands the negated gradient (_grad_work)
+    P.g = grad if grad.is_contiguous() else grad.contiguous()
     P.quant = st.get("is_quantized", False)
     P.vqt = st.get("v_quant_type", "al8")
     P.bs = st.get("block_size", group.get("block_size", 2048))
@@ -1477,17 +1497,16 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
         torch.linalg.vector_norm(p, ord=2, dtype=torch.float32)
     if not p.is_contiguous():
         raise NotImplementedError("adafactor8bit: non-contiguous parameters are not supported")
-    g = grad if grad.is_contiguous() else grad.contiguous()
     if p.dtype in (torch.float16, torch.float64):
         # the projection runs on fp32 G, as the reference's grad.float() (optimizer.py:2601)
-        g = g.float()
-    elif g.dtype != p.dtype:
-        if p.dtype == torch.float32:
-            g = g.float()
-        else:
+        gdt = torch.float32
+    elif grad.dtype != p.dtype:
+        if p.dtype != torch.float32:
             raise NotImplementedError("adafactor8bit: gradient dtype must match the parameter dtype")
-    if group["maximize"]:
-        g = g.neg()
+        gdt = torch.float32
+    else:
+        gdt = grad.dtype
+    g = _grad_work(opt, p, grad, gdt, group["maximize"])
     dev = p.device
     R = p.shape[0]
     C = p.numel() // R
@@ -1615,16 +1634,11 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
 
 
 def _apollo_capturable_check(p, group, factorize, came):
-    """What a capturable APOLLO step covers: bf16 and fp32 parameters (fp16 and fp64
-    ones project an fp32 copy of the gradient made each step), the plain low-rank
-    stage, no maximize (a negated gradient copy)."""
-    if p.dtype not in (torch.bfloat16, torch.float32):
-        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO on bf16 and fp32 parameters")
+    """What a capturable APOLLO step covers: the plain low-rank stage (the factorised
+    and CAME stages take host scalars)."""
     if factorize or came:
         raise NotImplementedError("adafactor8bit: capturable=True does not cover the factorised or CAME APOLLO "
                                   "stages (apollo_factorize, beta3)")
-    if group["maximize"]:
-        raise NotImplementedError("adafactor8bit: capturable=True does not cover APOLLO with maximize=True")
 
 
 def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, first, vbits, vqt, bs, has_m,

@@ -76,12 +76,12 @@ def test_device_projection_generator_matches_oracle(rows, cols, rank):
     _assert_ulp1(pt.cpu().numpy(), ref, f"{rows}x{cols} r{rank}")
 
 
-def _setup(capturable, dtype=torch.bfloat16):
+def _setup(capturable, dtype=torch.bfloat16, **extra):
     from adafactor8bit import Adafactor8Bit
     ps = [torch.nn.Parameter(make_param(s, i, 29).to("cuda", dtype)) for i, s in enumerate(SHAPES)]
     for p in ps:
         p.grad = torch.zeros_like(p)   # static gradient buffers
-    return ps, Adafactor8Bit(ps, **dict(C4_CAP, capturable=capturable))
+    return ps, Adafactor8Bit(ps, **dict(C4_CAP, capturable=capturable, **extra))
 
 
 def _load(ps, t):
@@ -107,11 +107,14 @@ def _schedule(opt, ps):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_apollo_graph_replays_equal_eager_steps_across_refreshes(dtype):
-    print(f"[apollo capture] C4 settings, gap 3, {dtype}", flush=True)
-    pa, oa = _setup(True, dtype)   # replayed
-    pb, ob = _setup(True, dtype)   # eager
+@pytest.mark.parametrize("dtype,maximize", [(torch.bfloat16, False), (torch.float32, False),
+                                            (torch.float16, False), (torch.bfloat16, True)])
+def test_apollo_graph_replays_equal_eager_steps_across_refreshes(dtype, maximize):
+    """fp16 parameters project an fp32 copy of G, and maximize a negated one: both are
+    refilled by the captured step in a buffer kept per parameter."""
+    print(f"[apollo capture] C4 settings, gap 3, {dtype}, maximize={maximize}", flush=True)
+    pa, oa = _setup(True, dtype, maximize=maximize)   # replayed
+    pb, ob = _setup(True, dtype, maximize=maximize)   # eager
     for t in (1, 2):
         for ps, o in ((pa, oa), (pb, ob)):
             _load(ps, t)

@@ -5,10 +5,10 @@ starts with a8_step_advance (count + 1, this step's scalars) and runs only
 multi-tensor kernels that read those scalars, so ``step()`` captured once in a
 graph replays as a real next step every time.  For the benchmark configurations
 (C1 AdamW UF8/AL8, C2 factored Adafactor with its fp32-state vectors, C3 CAME with
-Fira) and four more (weight decay with bias correction; bf16 with stochastic
+Fira) and more (weight decay with bias correction; bf16 with stochastic
 rounding; a clipped, Fira-limited quantised AdamW group and an fp32-state
 Adafactor group with scale_parameter, clip and Fira, on tensors of hundreds of
-workgroups, whose sums of squares are fixed-order sums):
+workgroups, whose sums of squares are fixed-order sums; SGD; maximize):
 
 * N graph replays leave parameters and every state tensor bit-identical to N
   eager steps of a second capturable optimizer on the same gradients, with eager
@@ -50,6 +50,11 @@ CASES = [
     ("adafactor1d_fp32_scale_clip_fira", FP32S, [(700, 1100), (2048,), (5000,)], torch.float32, "student_t"),
     # SGD (beta2 = beta2_decay = None): coded momentum with weight decay, bf16 with SR
     ("sgd_uf8_wd_bf16_sr", SGD, [(300, 260), (5000,), (2048,)], torch.bfloat16, "normal_zeros"),
+    # maximize: the kernels read a negated copy of the gradient kept per parameter, which the
+    # captured step refills (bf16 SR quantised AdamW, and factored CAME with its vectors)
+    ("adamw_bf16_sr_maximize", dict(ADAMW, stochastic_round_writeback=True, lr=1e-3, maximize=True),
+     [(300, 260), (1000,), (5000,)], torch.bfloat16, "normal_zeros"),
+    ("c3_came_fira_maximize", dict(C3, maximize=True), [(256, 300), (2048,)], torch.float32, "logscale"),
 ]
 
 

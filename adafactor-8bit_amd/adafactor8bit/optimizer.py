@@ -357,6 +357,8 @@ class Adafactor8Bit(Optimizer):
                 continue
             plan = _plan_param(p, _grad_work(self, p, g, g.dtype, group["maximize"]), st, group)
             plan.dsc = dsc
+            if plan.path == "q1d" and plan.alpha_t is not None and plan.mbuf is None and not plan.lag:
+                _persist_scale(self, plan, group, dsc)
             if plan.path == "q1d_fp32m":
                 _prep_q1d_fp32m(self, plan)
             elif plan.path == "f1d_qm":
@@ -498,7 +500,7 @@ class _Plan:
                  "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
                  "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep", "dsc",
-                 "al_floor", "al_vbits")
+                 "al_floor", "al_vbits", "pers")
 
     def batch_key(self):
         if self.path == "factored":
@@ -506,7 +508,7 @@ class _Plan:
                     self.vqt, self.bs, self.has_m, self.mqt, self.mbs, self.sr, self.beta3)
         if self.path not in ("q1d", "f1d", "sgd") or self.mbuf is not None:
             return None
-        if self.alpha_t is not None or self.decay_t is not None:
+        if (self.alpha_t is not None or self.decay_t is not None) and not self.pers:
             return None
         if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
@@ -521,7 +523,8 @@ class _Plan:
         if self.path == "q1d" and (self.d > 0 or self.fira):
             if self.lag:
                 return None
-            return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt, self.al_vbits,
+            return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.pers, self.vqt,
+                    self.al_vbits,
                     self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                     self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.d, self.fira, self.margin)
@@ -532,7 +535,7 @@ class _Plan:
             return ("sgd", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m, mq,
                     self.mqt if mq else None, self.mbs if mq else 0, self.beta1, self.alpha_val, self.decay_val)
         return (self.path, self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.vqt,
-                self.vbuf is not None, self.al_vbits,
+                self.vbuf is not None, self.al_vbits, self.pers,
                 self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                 self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                 self.alpha_val, self.decay_val)
@@ -564,6 +567,7 @@ def _grad_work(opt, p, grad, dtype, negate):
 def _plan_param(p, grad, st, group) -> _Plan:
     P = _Plan()
     P.p, P.st, P.group = p, st, group
+    P.pers = False
     P.vbuf = None
     P.mbuf = None
     beta1, beta2, beta2_decay, beta3 = group.get("beta1"), group["beta2"], group["beta2_decay"], group.get("beta3")
@@ -1057,6 +1061,48 @@ def _materialize_alpha(P):
     P.rms_kernel, P.kwd = False, 0
 
 
+def _persist_scale(opt, P, group, dsc):
+    """A quantised 1-D plan whose step size is a tensor -- scale_parameter's
+    max(rms(p), eps2) * rho, bias corrected (optimizer.py:851-855, 2020-2030), or a
+    tensor learning rate -- keeps it, and its weight-decay factor 1 - alpha * wd
+    (optimizer.py:2032-2039), in two floats kept per parameter: their addresses go
+    into the multi-tensor table (per-tensor alpha and decay, read before the
+    launch's scalars), so the plan joins the group's launch and a captured step
+    refills them.  Under capturable=True rho and the bias factor are the device
+    step block's (its rho and bias_factor: the same values, the same operation
+    order as the host path)."""
+    dev = P.p.device
+    key = (dev, "alpha", id(P.p))
+    buf = opt._ws.get(key)
+    if buf is None:
+        buf = torch.empty(2, dtype=torch.float32, device=dev)
+        opt._ws[key] = buf
+    a_buf, d_buf = buf[0:1], buf[1:2]
+    if dsc is not None:
+        # the plan's alpha used the placeholder lr: re-form it from the step block
+        beta1, beta2 = group.get("beta1"), group["beta2"]
+        sgd = beta2 is None and group["beta2_decay"] is None
+        rms = torch.linalg.vector_norm(P.p, ord=2, dtype=torch.float32) / math.sqrt(P.p.numel())
+        a = torch.clamp(rms, min=P.eps2) * dsc[6]   # rho
+        bc = group.get("bias_correction")
+        if beta1 is not None and not group["relative_step"] and not sgd and \
+                bool(P.adam_denom if bc is None else bc):
+            a = a * dsc[5] if beta2 is not None else a / dsc[5]   # sqrt(bc2) / bc1, or bc1
+        a_buf.copy_(a.reshape(1))
+        wd = group["weight_decay"]
+        if wd != 0 and group.get("scale_weight_decay", True):
+            d_buf.copy_((1.0 - (a * wd)).reshape(1))
+            P.decay_t = d_buf
+        else:
+            P.decay_t = None   # the block's decay (1 - rho * wd, or none)
+    else:
+        a_buf.copy_(P.alpha_t.reshape(1).to(torch.float32))
+        if P.decay_t is not None:
+            d_buf.copy_(P.decay_t.reshape(1).to(torch.float32))
+            P.decay_t = d_buf
+    P.alpha_t, P.alpha_val, P.pers = a_buf, 0.0, True
+
+
 def _run_single(opt, P):
     _materialize_alpha(P)
     if P.path == "factored":
@@ -1214,8 +1260,9 @@ def _run_batch_q1dc(opt, key, plans):
     fira = bool(P0.fira)
     mnorm = fira and P0.has_m and P0.mom_only
     ws = opt._ws.setdefault((dev, "q1dc"), {})
-    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr(), pl.st["variance_q"].data_ptr()) for pl in plans), P0.sr,
-          P0.has_m, fira, mnorm)
+    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr(), pl.st["variance_q"].data_ptr(),
+                 nat.ptr(pl.alpha_t if pl.pers else None), nat.ptr(pl.decay_t if pl.pers else None))
+                for pl in plans), P0.sr, P0.has_m, fira, mnorm)
     refs = [tuple(v.data_ptr() for k, v in pl.st.items() if torch.is_tensor(v) and k != "fira_prev_norm")
             for pl in plans]
     ent = ws.get(ck)
@@ -1247,12 +1294,13 @@ def _run_batch_q1dc(opt, key, plans):
                     fs = f0 + 4 * i
                     if not mnorm:   # the update clip reads the Fira launch's finite sum
                         nb = f0 + 4 * (2 * n + i)
+                ap = mode == nat.MODE_APPLY and pl.pers
                 arr[i] = nat.Tensor1D(
                     pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(st.get("m_q") if pl.has_m else None),
                     nat.ptr(st.get("m_scale") if pl.has_m else None), st["variance_q"].data_ptr(),
                     st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), v0 + 4 * offs[i], nb,
-                    None, prev, None, pl.p.numel(), int(st.get("sr_seed", 0)), fs,
-                    parts.data_ptr() + 8 * poffs[i])
+                    nat.ptr(pl.alpha_t if ap else None), prev, nat.ptr(pl.decay_t if ap else None),
+                    pl.p.numel(), int(st.get("sr_seed", 0)), fs, parts.data_ptr() + 8 * poffs[i])
             arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_1d(n)), dtype=torch.uint8, device=dev), 1]
         ent = {"refs": refs, "acc": acc, "fout": fout, "vbuf": vbuf, "parts": parts, "arrs": arrs}
         if len(ws) > 16:
@@ -1325,7 +1373,8 @@ def _run_batch(opt, key, plans):
     dev = P0.p.device
     L = nat.lib()
     n = len(plans)
-    ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(pl.vbuf)) for pl in plans)
+    ptrs = tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(pl.vbuf), nat.ptr(pl.alpha_t if pl.pers else None),
+                  nat.ptr(pl.decay_t if pl.pers else None)) for pl in plans)
     # The table holds only pointers, sizes and seeds; step-dependent scalars go
     # to the launch, so one upload serves every later step.
     cache_key = (path, dev, key[5], ptrs)   # key[5]: stochastic rounding (seeds in the table)
@@ -1348,8 +1397,9 @@ def _run_batch(opt, key, plans):
                 arr[i] = nat.Tensor1D(
                     pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(st.get("m_q") if pl.has_m else None),
                     nat.ptr(st.get("m_scale") if pl.has_m else None), st["variance_q"].data_ptr(),
-                    st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), None, None, None,
-                    None, None, pl.p.numel(), int(st.get("sr_seed", 0)))
+                    st["variance_scale"].data_ptr(), st["variance_min_log"].data_ptr(), None, None,
+                    nat.ptr(pl.alpha_t if pl.pers else None), None, nat.ptr(pl.decay_t if pl.pers else None),
+                    pl.p.numel(), int(st.get("sr_seed", 0)))
             nbytes = L.a8_table_bytes_1d(n)
         else:
             arr = (nat.TensorFull * n)()

@@ -55,6 +55,14 @@ CASES = [
     ("adamw_bf16_sr_maximize", dict(ADAMW, stochastic_round_writeback=True, lr=1e-3, maximize=True),
      [(300, 260), (1000,), (5000,)], torch.bfloat16, "normal_zeros"),
     ("c3_came_fira_maximize", dict(C3, maximize=True), [(256, 300), (2048,)], torch.float32, "logscale"),
+    # scale_parameter on quantised 1-D tensors (>= min_8bit_size): alpha = max(rms(p), eps2) * rho
+    # per tensor, from the device block's rho and bias factor, with 1 - alpha * wd; AdamW with
+    # bias correction, and Adafactor's defaults (relative step, scale_parameter) with a clip
+    ("adamw_q1d_scale_param_wd", dict(ADAMW, scale_parameter=True, weight_decay=0.1, scale_weight_decay=True,
+                                      lr=1e-3), [(300, 260), (5000,), (8192,)], torch.float32, "student_t"),
+    ("adafactor_q1d_relative_scale_clip", dict(C2, factored=False, relative_step=True, scale_parameter=True,
+                                               d=1.0, lr=1e-2), [(6000,), (8192,), (300, 260)], torch.float32,
+     "student_t"),
 ]
 
 

@@ -357,7 +357,7 @@ class Adafactor8Bit(Optimizer):
                 continue
             plan = _plan_param(p, _grad_work(self, p, g, g.dtype, group["maximize"]), st, group)
             plan.dsc = dsc
-            if plan.path == "q1d" and plan.alpha_t is not None and plan.mbuf is None and not plan.lag:
+            if plan.path == "q1d" and plan.alpha_t is not None and plan.mbuf is None:
                 _persist_scale(self, plan, group, dsc)
             if plan.path == "q1d_fp32m":
                 _prep_q1d_fp32m(self, plan)
@@ -497,7 +497,7 @@ class _Plan:
     """Host-side scalar preparation of one parameter's step (optimizer.py:1944-2040)."""
     __slots__ = ("p", "g", "st", "group", "path", "step", "beta_val", "alpha_val", "alpha_t",
                  "rho_val", "rho_t", "eps1", "eps2", "eps_sq", "log_eps_sq", "adam_denom", "eps_d",
-                 "eps_g", "mom_only", "beta1", "d", "fira", "margin", "lag", "decay_val", "decay_t",
+                 "eps_g", "mom_only", "beta1", "d", "fira", "margin", "decay_val", "decay_t",
                  "sr", "quant", "vqt", "mqt", "bs", "mbs", "has_m", "maximize", "beta3", "scale_param",
                  "bias_mode", "bias_fac", "wd", "wd_mode", "rms_kernel", "kwd", "vbuf", "mbuf", "_keep", "dsc",
                  "al_floor", "al_vbits", "pers")
@@ -513,16 +513,12 @@ class _Plan:
         if self.p.data_ptr() % 16 or self.g.data_ptr() % 16:
             return None
         if self.path == "f1d" and (self.d > 0 or self.fira or self.rms_kernel):
-            if self.lag:
-                return None
             return ("f1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m,
                     self.vbuf is not None,
                     self.beta1, self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.kwd, self.group["weight_decay"], self.d, self.fira,
                     self.margin, self.rms_kernel, self.eps2)
         if self.path == "q1d" and (self.d > 0 or self.fira):
-            if self.lag:
-                return None
             return ("q1dc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.pers, self.vqt,
                     self.al_vbits,
                     self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
@@ -603,7 +599,9 @@ def _plan_param(p, grad, st, group) -> _Plan:
     P.d = d
     P.fira = group.get("enable_fira_for_adafactor", False)
     P.margin = group.get("fira_margin", 0.01)
-    P.lag = group.get("lag_norm", False)
+    # lag_norm: the PyTorch branches clip by this step's norm whatever lag_norm says
+    # (the one-pass lagged clip, _dispatch_cuda_clip optimizer.py:1048-1073, is a CUDA-
+    # branch approximation); this build follows them, as for every other rule
 
     P.beta3 = beta3
     if sgd:
@@ -869,19 +867,6 @@ def _fira_apply(opt, st, norm_buf, alpha_t, alpha_val, margin, device):
     return out[0].view(()), out[2].view(1)
 
 
-def _fira_scale_only(opt, st, x, margin, device, key):
-    prev = st.get(key)
-    out = torch.empty(3, dtype=torch.float32, device=device)
-    x1 = x.reshape(1).to(torch.float32)
-    if prev is not None and not torch.is_tensor(prev):
-        prev = torch.tensor(prev, dtype=torch.float32, device=device)
-    rc = nat.lib().a8_fira_scalar(nat.ptr(x1), nat.ptr(prev), None, nat.ptr(out), 1,
-                                  int(prev is not None), 0, _f32(1.0 + margin), nat.stream_of(device))
-    nat.check(rc, "a8_fira_scalar")
-    st[key] = out[1].view(x.shape if prev is not None else ())
-    return out[0].view(())
-
-
 def _sgd_momentum(P):
     """Momentum buffers of an SGD step: (m_q, m_scale, m_fp32, kind) with kind 0
     none, 1 quantised, 2 fp32 (optimizer.py:2046-2068)."""
@@ -1120,20 +1105,6 @@ def _run_single(opt, P):
         _launch_1d(opt, P, nat.MODE_NOCLIP, alpha_t, alpha_val)
         return
     st = P.st
-    if P.lag:  # _dispatch_cuda_clip, lag branch (optimizer.py:1057-1073)
-        if "prev_update_norm" not in st:
-            st["prev_update_norm"] = torch.zeros(1, device=dev, dtype=torch.float32)
-        if P.fira and st.get("lag_fira_scale") is not None:
-            if alpha_t is None:
-                alpha_t = _dev_scalar(opt, dev, "lag_alpha", alpha_val)
-            alpha_t = alpha_t * st["lag_fira_scale"]
-        nb = _norm_buf(opt, dev)
-        _launch_1d(opt, P, nat.MODE_LAG, alpha_t, alpha_val, norm_buf=nb, prev_norm=st["prev_update_norm"])
-        curr = nb.sqrt()
-        st["prev_update_norm"] = curr
-        if P.fira:
-            st["lag_fira_scale"] = _fira_scale_only(opt, st, curr.view(()), P.margin, dev, "fira_prev_norm")
-        return
     nb = _norm_buf(opt, dev)
     vb = _v_buf(opt, dev, P.p.numel()) if P.path == "q1d" else None
     _launch_1d(opt, P, nat.MODE_NORM, None, 0.0, norm_buf=nb, v_buf=vb)

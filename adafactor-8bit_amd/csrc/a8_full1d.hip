@@ -120,7 +120,9 @@ __global__ __launch_bounds__(kFLanes) void k_update1d_full(DescFull one, const D
                           : (MODE == 4 ? sqrtf(*D.prev_norm) : *D.prev_norm);
         // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
         // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
-        if (h.momentum_only && D.m)
+        if (MODE == 3)   // LAG has no CPU branch: the CUDA kernels' pn / (sqrtf(numel) * d) in fp32 (kernels.cu:651-655)
+          denom = fmaxf(1.0f, nrm / (sqrtf((float)n) * h.d));
+        else if (h.momentum_only && D.m)
           denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
         else
           denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));

@@ -233,7 +233,9 @@ __device__ __forceinline__ void unit_step(const Desc1D& D, const Hyper1D& h, int
                           : (MODE == 4 ? sqrtf(*gp(D.prev_norm)) : *gp(D.prev_norm));
         // U-clip of momentum_only divides by sqrt(n) then d (optimizer.py:894-895);
         // the update clip divides by sqrt(n)*d (optimizer.py:859-863)
-        if (h.momentum_only && kHasM)
+        if (MODE == 3)   // LAG has no CPU branch: the CUDA kernels' pn / (sqrtf(numel) * d) in fp32 (kernels.cu:651-655)
+          denom = fmaxf(1.0f, nrm / (sqrtf((float)n) * h.d));
+        else if (h.momentum_only && kHasM)
           denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
         else
           denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));
@@ -714,7 +716,9 @@ __global__ __launch_bounds__(kLanes) void k_update1d_gen(Desc1D one, const Desc1
       if (h.d > 0.0f) {
         const float nrm = (MODE == 2) ? sqrtf(*gp(D.norm_buf))
                           : (MODE == 4 ? sqrtf(*gp(D.prev_norm)) : *gp(D.prev_norm));
-        if (h.momentum_only && kHasM)
+        if (MODE == 3)   // LAG has no CPU branch: the CUDA kernels' pn / (sqrtf(numel) * d) in fp32 (kernels.cu:651-655)
+          denom = fmaxf(1.0f, nrm / (sqrtf((float)n) * h.d));
+        else if (h.momentum_only && kHasM)
           denom = fmaxf(1.0f, (nrm / (float)sqrt((double)n)) / h.d);
         else
           denom = fmaxf(1.0f, nrm / (float)(sqrt((double)n) * (double)h.d));

@@ -180,6 +180,24 @@ def test_tensor_lr_scheduled_between_replays(name, kw, shapes):
 
 
 @pytest.mark.gpu
+def test_lag_norm_clips_by_this_steps_norm():
+    """lag_norm=True follows the PyTorch branches, which clip by this step's norm (the
+    one-pass lagged clip is the CUDA branch's approximation, kept as the module's
+    fused_update_*_lag): the same bits as lag_norm=False, in a captured step too."""
+    print("[capture] lag_norm", flush=True)
+    kw = dict(ADAMW, d=1.0, enable_fira_for_adafactor=True, lr=1e-3)
+    shapes = [(700, 1100), (5000,), (2048,)]
+    pa, oa = _setup(kw, shapes, torch.float32, lag_norm=True, capturable=True)
+    pb, ob = _setup(kw, shapes, torch.float32, lag_norm=False)
+    for t in range(1, 4):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load_grads(ps, t, "logscale", torch.float32)
+            o.step()
+    torch.cuda.synchronize()
+    _same_state(oa, ob, pa, pb, "lag_norm")
+
+
+@pytest.mark.gpu
 def test_capturable_rejects_paths_with_host_scalars():
     print("[capturable] factorised APOLLO rejected", flush=True)
     ps, o = _setup(dict(ADAMW, apollo_rank=8, apollo_factorize=True, block_size=128, m_block_size=32), [(64, 96)],

@@ -88,3 +88,85 @@ def test_module_rejects_wrong_code_dtype():
     with pytest.raises(RuntimeError, match="v_bits=16"):
         K.fused_update_1d_vonly_noclip(z, z, vq, one, one, one, 0.001, 1e-8, True, -53.0, 0.0,
                                        4096, 2048, 16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("full", [False, True])
+def test_module_lag_is_noclip_at_the_lagged_scale(full):
+    """fused_update_1d_lag / fused_update_1d_full_lag (kernels.cu:651-655, 1305-1309): the
+    step is alpha / max(1, prev_norm / (sqrtf(numel) * d)) in fp32 and the pass sums this
+    step's u^2.  The reference has no CPU branch for the lagged clip, so it is pinned by
+    equivalences: parameters, codes and block metadata equal a NOCLIP step whose alpha is
+    that fp32 quotient, and the sum equals the NORM pass's; momentum-only with a zero
+    previous norm (a clip factor of 1) equals momentum-only NOCLIP."""
+    from adafactor8bit import adafactor8bit_cuda as K
+    from adafactor8bit import _state as S
+    print(f"[module] lag full={full}", flush=True)
+    shape, bs, mbs, d = (61, 1003), 2048, 256, 1.0
+    n = shape[0] * shape[1]
+    K.set_qmap(*[q.cuda() for q in K.qmaps()])
+    g = make_grad(shape, 0, 1, 5).cuda()
+    p0 = make_param(shape, 0, 5).cuda()
+    bc1, bc2 = 1.0 - 0.9, 1.0 - 0.999
+    eps1 = 1e-8
+    alpha = (torch.tensor(1e-3, dtype=torch.float32) * (math.sqrt(bc2) / bc1)).reshape(1).cuda()
+    lfl = math.log2(max(eps1 * eps1, 1.17549435e-38))
+
+    def fresh():
+        st = {"p": p0.clone()}
+        if full:
+            st["v"] = torch.full(shape, 1e-6, dtype=torch.float32, device="cuda")
+            st["m"] = torch.full(shape, 1e-4, dtype=torch.float32, device="cuda")
+        else:
+            S.new_al_slot(st, "variance", shape, bs, "al8", "cuda")
+            S.new_momentum_codes(st, "m", n, mbs, "uf8", "cuda")
+        return st
+
+    def run(mode, st, a=None, prev=None, nb=None, mom_only=False):
+        adam = not mom_only
+        eps_d = eps1 * math.sqrt(bc2) if adam else 0.0
+        eps_g = 0.0 if adam else eps1
+        if full:
+            common = (0.9, 1.0 - 0.999, max(eps1 * eps1, 1.17549435e-38), eps_d, adam, eps_g, n)
+            if mode == "lag":
+                K.fused_update_1d_full_lag(st["p"], g, st["v"], st["m"], nb, a, prev, *common, d, mom_only)
+            elif mode == "noclip":
+                K.fused_update_1d_full_noclip(st["p"], g, st["v"], st["m"], a, *common, mom_only)
+            else:
+                K.fused_update_1d_full_norm(g, st["v"], st["m"], nb, *common, mom_only)
+            return
+        q = (st["m_q"], st["m_scale"], st["variance_q"], st["variance_scale"], st["variance_min_log"])
+        tail = (0.9, 1.0 - 0.999, eps_d, adam, lfl, eps_g, n, bs, mbs, 8, 0)
+        if mode == "lag":
+            K.fused_update_1d_lag(st["p"], g, *q, nb, a, prev, *tail, d, 8, mom_only)
+        elif mode == "noclip":
+            K.fused_update_1d_noclip(st["p"], g, *q, a, *tail, 8, mom_only)
+        else:
+            vb = torch.empty(n, dtype=torch.float32, device="cuda")
+            K.fused_update_1d_norm(g, *q, vb, nb, *tail, 8, mom_only)
+
+    keys = ("p", "v", "m") if full else ("p", "m_q", "m_scale", "variance_q", "variance_scale",
+                                         "variance_min_log")
+    prev = torch.tensor([7.5 * math.sqrt(n)], dtype=torch.float32, device="cuda")
+    denom = max(np.float32(1.0), np.float32(prev.item()) / (np.sqrt(np.float32(n)) * np.float32(d)))
+    assert denom > 7.0
+    a2 = torch.tensor([np.float32(alpha.item()) / np.float32(denom)], dtype=torch.float32, device="cuda")
+    sl, sn, sm = fresh(), fresh(), fresh()
+    nbl = torch.zeros(1, dtype=torch.float32, device="cuda")
+    nbn = torch.zeros(1, dtype=torch.float32, device="cuda")
+    run("lag", sl, alpha, prev, nbl)
+    run("noclip", sn, a2)
+    run("norm", sm, nb=nbn)
+    torch.cuda.synchronize()
+    for k in keys:
+        assert torch.equal(sl[k], sn[k]), k
+    assert not torch.equal(sl["p"], p0)
+    assert torch.equal(nbl, nbn) and nbl.item() > 0.0
+    # momentum-only, zero previous norm: U is not clipped, the step is alpha
+    sl, sn = fresh(), fresh()
+    zero = torch.zeros(1, dtype=torch.float32, device="cuda")
+    run("lag", sl, alpha, zero, torch.zeros(1, dtype=torch.float32, device="cuda"), mom_only=True)
+    run("noclip", sn, alpha, mom_only=True)
+    torch.cuda.synchronize()
+    for k in keys:
+        assert torch.equal(sl[k], sn[k]), ("momentum-only", k)

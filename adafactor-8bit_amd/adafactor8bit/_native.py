@@ -156,11 +156,11 @@ _SIGS = {
     "a8_apollo_step_multi_phase": (_c_i, [_c_i, _c_i, _c_i, ctypes.POINTER(ApolloTensor), _c_i, _c_vp, _c_i64,
                                           _c_d, _c_d, _c_i, _c_f, _c_f, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i,
                                           _c_i, _c_f, _c_i, _c_i, _c_f, _c_f, _c_f, _c_f, _c_i, _c_i, _c_f,
-                                          _c_i, _c_vp]),
+                                          _c_i, _c_i, _c_vp, _c_vp]),
     "a8_apollo_lowrank_x": (_c_i, [ctypes.POINTER(ApolloXArgs), _c_vp]),
     "a8_vema_fp32": (_c_i, [_c_vp, _c_vp, _c_i, _c_d, _c_f, _c_i64, _c_vp]),
     "a8_apollo_x_workspace_floats": (_c_i64, [_c_i64, _c_i64]),
-    "a8_apollo_lowrank_x_multi": (_c_i, [ctypes.POINTER(ApolloXArgs), _c_i, _c_vp, _c_i64, _c_vp]),
+    "a8_apollo_lowrank_x_multi": (_c_i, [ctypes.POINTER(ApolloXArgs), _c_i, _c_vp, _c_i64, _c_i, _c_vp, _c_vp]),
     "a8_apollo_x_table_bytes": (_c_i64, [_c_i]),
     "a8_dequantize_log_nonneg": (_c_i, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),
     "a8_dequantize_dynamic": (_c_i, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i, _c_i, _c_vp]),

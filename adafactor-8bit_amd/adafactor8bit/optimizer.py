@@ -1510,6 +1510,8 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
     came = group.get("beta3") is not None
     if came and beta1 is None:
         raise ValueError("CAME (beta3) strictly requires momentum (beta1) to compute update instability.")
+    if dsc is not None and int(st["apollo_update_proj_gap"]) <= 0:
+        raise NotImplementedError("adafactor8bit: capturable APOLLO needs apollo_update_proj_gap > 0")
     if p.dtype not in (torch.float32, torch.bfloat16, torch.float16, torch.float64):
         raise NotImplementedError("adafactor8bit: APOLLO needs fp32, bf16, fp16 or fp64 parameters")
     if p.dtype == torch.float64 and group["scale_parameter"]:
@@ -1550,7 +1552,6 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
     right = R >= C
     pstate = None
     if dsc is not None:
-        _apollo_capturable_check(p, group, factorize, came)
         proj_T, pstate = _apollo_proj_device(opt, st, (R, C), step, dev, group)
         fresh = False
     else:
@@ -1570,9 +1571,6 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
     # run the plain stage of a8_apollo_lowrank_x
     xmode = bool(factorize or came or (vbits and not _pow2_in(bs, 128, 2048))) or \
         (has_m and not m_fp32 and not _pow2_in(mbs, 32, 2048))
-    if dsc is not None and xmode:
-        raise NotImplementedError("adafactor8bit: capturable=True covers APOLLO with power-of-two block sizes "
-                                  "(V 128..2048, momentum 32..2048); this matrix needs the host-scalar low-rank stage")
     low_shape = (R, rank) if right else (rank, C)
     if factorize:   # optimizer.py:2693-2699 creates the row / column EMAs on the first step
         if first:
@@ -1618,9 +1616,15 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
         fresh = True
     ent["proj"] = (proj_T.data_ptr(), proj_T._version)
     sr = bool(group.get("stochastic_round_writeback", False)) and p.dtype in (torch.bfloat16, torch.float16)
+    if dsc is not None:
+        # the device block supplies step, bias factor, V weight and lr: the records
+        # (and so the uploaded tables) stay the same from step to step
+        step_rec, bias_rec, beta_key, rho_key = 0, 0.0, 0.0, 0.0
+    else:
+        step_rec, bias_rec, beta_key, rho_key = int(step), float(bias_fac), float(beta_val), float(rho_val)
     if xmode:
         xargs, xkeep = _apollo_x_args(opt, st, group, dev, ent["ws"], low_shape, n_low, factorize, came, first,
-                                      vbits, vqt, bs, has_m, m_fp32, mqt, mbs, quant, beta_val, beta1)
+                                      vbits, vqt, bs, has_m, m_fp32, mqt, mbs, quant, beta_key, beta1)
         # the stage leaves the per-row sums of u^2 and g_low^2 where the finish phase
         # reads them (right side, rank a power of two in [8, 512]: phase 3)
         xargs.u_rowsums = int(right and _pow2_in(rank, 8, 512))
@@ -1628,16 +1632,11 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
             p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank, None, None, None, None, None, None, None,
             nat.ptr(st.get("scaled_grad_norm_prev")) if fira else None, has_prev,
             nat.ptr(rho_t), ent["ws"].data_ptr(), int(st.get("sr_seed", 0)),
-            int(first), int(fresh), int(step), float(bias_fac))
-        bkey = (p.dtype, sr, "x", has_m, True, mqt, 0, 0, float(beta_val), float(rho_val), bias_mode)
-        keep = (g, proj_T, rho_t, xkeep)
+            int(first), int(fresh), step_rec, bias_rec, nat.ptr(pstate),
+            int(st["apollo_update_proj_gap"]) if pstate is not None else 0)
+        bkey = (p.dtype, sr, "x", has_m, True, mqt, 0, 0, beta_key, rho_key, bias_mode)
+        keep = (g, proj_T, rho_t, xkeep, pstate)
         return bkey, t, (st, "x", bs, keep, xargs)
-    if dsc is not None:
-        # the device block supplies step, bias factor, V weight and lr: the record
-        # (and so the uploaded table) stays the same from step to step
-        step_rec, bias_rec, beta_key, rho_key = 0, 0.0, 0.0, 0.0
-    else:
-        step_rec, bias_rec, beta_key, rho_key = int(step), float(bias_fac), float(beta_val), float(rho_val)
     t = nat.ApolloTensor(
         p.data_ptr(), g.data_ptr(), R, C, proj_T.data_ptr(), rank,
         nat.ptr(st.get("v_low_q")) if vbits else None, nat.ptr(st.get("v_low_scale")) if vbits else None,
@@ -1652,14 +1651,6 @@ def _apollo_prep(opt, p, grad, st, group, dsc=None):
     bkey = (p.dtype, sr, vbits, has_m, m_fp32, mqt, int(mbs), int(bs), beta_key, rho_key, bias_mode)
     keep = (g, proj_T, rho_t, pstate)   # alive until the launch is queued
     return bkey, t, (st, vbits, bs, keep, None)
-
-
-def _apollo_capturable_check(p, group, factorize, came):
-    """What a capturable APOLLO step covers: the plain low-rank stage (the factorised
-    and CAME stages take host scalars)."""
-    if factorize or came:
-        raise NotImplementedError("adafactor8bit: capturable=True does not cover the factorised or CAME APOLLO "
-                                  "stages (apollo_factorize, beta3)")
 
 
 def _apollo_x_args(opt, st, group, dev, ws, low_shape, n_low, factorize, came, first, vbits, vqt, bs, has_m,
@@ -1769,21 +1760,37 @@ def _run_apollo_batch(opt, group, bkey, items, dsc=None):
             int(bool(group.get("apollo_scale_front", False))), int(fira), float(group.get("fira_margin", 0.01)),
             float(group["d"]), float(rho_val), _f32(group["eps"][1]), int(bool(group["scale_parameter"])),
             bias_mode, _f32(wd), wd_mode, stream)
+    if dsc is not None:
+        beta_val, tail = 0.0, tail[:6] + (0.0,) + tail[7:]   # from the device block
     if vbits == "x":
-        # projection, the factorised / CAME low-rank stage per matrix, then scale and writeback
+        # projection, the factorised / CAME low-rank stage per matrix, then scale and
+        # writeback; phase 3 reads the table phase 1 left.  Capturable groups keep the
+        # stage's tables per group and upload them only when a record changes.
         head = (nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
                 float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), 0, 2048, 8, 0, 1,
                 256)
-        nat.check(L.a8_apollo_step_multi_phase(1, *head, *tail), "a8_apollo_step_multi_phase(1)")
+        dptr = nat.ptr(dsc)
+        nat.check(L.a8_apollo_step_multi_phase(1, *head, *tail[:-1], upload, dptr, tail[-1]),
+                  "a8_apollo_step_multi_phase(1)")
         xarr = (nat.ApolloXArgs * n)(*[it[1][4] for it in items])
         xneed = int(L.a8_apollo_x_table_bytes(n))
-        xtab = opt._ws.get((pdev, "apx_table"))
+        xkey = (pdev, "apx_table", id(group), bkey) if dsc is not None else (pdev, "apx_table")
+        xtab = opt._ws.get(xkey)
         if xtab is None or xtab.numel() < xneed:
             xtab = torch.empty(max(xneed, 4096), dtype=torch.uint8, device=pdev)
-            opt._ws[(pdev, "apx_table")] = xtab
-        nat.check(L.a8_apollo_lowrank_x_multi(xarr, n, xtab.data_ptr(), xtab.numel(), stream),
+            opt._ws[xkey] = xtab
+        xupload = 1
+        if dsc is not None:
+            xblob = bytes(xarr)
+            xbk = (pdev, "apx_table_blob", id(group), bkey)
+            if opt._ws.get(xbk) == (xtab.data_ptr(), xblob):
+                xupload = 0
+            _no_upload_in_capture(xupload)
+            opt._ws[xbk] = (xtab.data_ptr(), xblob)
+        nat.check(L.a8_apollo_lowrank_x_multi(xarr, n, xtab.data_ptr(), xtab.numel(), xupload, dptr, stream),
                   "a8_apollo_lowrank_x_multi")
-        nat.check(L.a8_apollo_step_multi_phase(3, *head, *tail), "a8_apollo_step_multi_phase(3)")
+        nat.check(L.a8_apollo_step_multi_phase(3, *head, *tail[:-1], 0, dptr, tail[-1]),
+                  "a8_apollo_step_multi_phase(3)")
         for _, (st, _vb, bsz, keep, xargs) in items:
             if xargs.v_bits:
                 _block_view(st, "v_low", bsz)
@@ -1793,8 +1800,6 @@ def _run_apollo_batch(opt, group, bkey, items, dsc=None):
                 _block_view(st, "conf_row_low", bsz)
                 _block_view(st, "conf_col_low", bsz)
         return
-    if dsc is not None:
-        beta_val, tail = 0.0, tail[:6] + (0.0,) + tail[7:]   # from the device block
     rc = L.a8_apollo_step_multi(
         nat.dtype_code(pdt), int(sr), arr, n, tab.data_ptr(), tab.numel(), float(beta_val),
         float(beta1) if has_m else 0.0, int(has_m), _f32(aeps), _f32(math.log2(eps_sq)), vbits, int(bs),

@@ -48,8 +48,11 @@ struct MEmaItem {   // momentum: m' = lerp(deq(m), x, 1 - beta), re-encoded; out
   int64_t n;
 };
 int64_t m_ema_table_bytes(int n);
+// upload == 0 (in each of these table forms): the table from an earlier call with
+// the same items is still in table_dev, and no copy is made (a captured graph's
+// launches then read it as it stands)
 int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int block_size, int m_bits, int m_mode,
-                hipStream_t st);
+                hipStream_t st, int upload = 1);
 
 struct CameTailItem {   // non-factorised CAME APOLLO after the RMS clip (k_came_tail)
   const float* U;         // U before the clip division
@@ -70,7 +73,7 @@ bool came_tail_ok(int m_fp32, int m_block_size, int c_bits, int block_size);
 int64_t came_tail_table_bytes(int n);
 int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1, double beta3, float eps_came,
                     float eps_sq, int m_fp32, int m_bits, int m_mode, int m_block_size, int c_bits, int block_size,
-                    hipStream_t st);
+                    hipStream_t st, int upload = 1);
 
 struct FactTailItem {   // factorised APOLLO momentum EMA and update (k_fact_tail)
   const float* g;         // g_low
@@ -86,7 +89,7 @@ struct FactTailItem {   // factorised APOLLO momentum EMA and update (k_fact_tai
 };
 int64_t fact_tail_table_bytes(int n);
 int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1, float apollo_eps, int m_fp32,
-                    int m_bits, int m_mode, int m_block_size, hipStream_t st);
+                    int m_bits, int m_mode, int m_block_size, hipStream_t st, int upload = 1);
 
 // Row sums of u^2 and g^2 (double, summed from fp32 squares) over the rows of C
 // elements of an n-element row-major matrix (C a power of two in [8, 512]), two
@@ -104,8 +107,10 @@ struct VEmaItem {   // AL state: v' = lerp(deq(v), x (or x^2 + eps1), w), re-enc
   int64_t n;
 };
 int64_t v_ema_table_bytes(int n);
+// w_dev: the lerp weight is (float) w_dev->beta_val, read on the device, in place of w
 int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_size, int square, float eps1,
-                float log_floor, int v_bits, hipStream_t st);
+                float log_floor, int v_bits, hipStream_t st, int upload = 1,
+                const a8_step_scalars* w_dev = nullptr);
 
 // Codebook upload of the factored-step translation unit (called by a8_set_qmap).
 hipError_t factored_upload_qmap(const float* q8, const float* q4);

@@ -2270,13 +2270,14 @@ int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_ap
                                float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits, int m_mode,
                                int m_fp32, int m_block_size, int channel, float apollo_scale, int scale_front,
                                int fira, float fira_margin, float d, float lr_val, float eps2, int scale_parameter,
-                               int bias_mode, float weight_decay, int wd_mode, void* stream) {
+                               int bias_mode, float weight_decay, int wd_mode, int upload, const void* step_scalars,
+                               void* stream) {
   if (phase < 1 || phase > 3)
     return set_error(A8_ERR_ARG, "phase must be 1 (projection), 2 or 3 (finish)");
   return apollo_run(phase, dtype, stochastic, ts, ntensors, table_dev, table_bytes_, beta_val, beta1, has_m,
                     apollo_eps, log_floor, v_bits, block_size, m_bits, m_mode, m_fp32, m_block_size, channel,
                     apollo_scale, scale_front, fira, fira_margin, d, lr_val, eps2, scale_parameter, bias_mode,
-                    weight_decay, wd_mode, 1, nullptr, stream);
+                    weight_decay, wd_mode, upload, reinterpret_cast<const a8_step_scalars*>(step_scalars), stream);
 }
 
 }  // extern "C"

@@ -96,12 +96,25 @@ struct XD {
   int64_t wb[XW_N];
 };
 
-// Where a launch finds its matrices: a device table, or one matrix by value.
+// Where a launch finds its matrices: a device table, or one matrix by value;
+// dsc: the device step block, whose V weight replaces the descriptors' bv.
 struct XT {
   XD one;
   const XD* tab;
   int ntab;
+  const a8_step_scalars* dsc;
 };
+
+// The V lerp weight bv and 1 - bv (derived in double, as the descriptor's are).
+__device__ __forceinline__ void x_bv(const XT& t, const XK& k, float& bv, float& omb) {
+  bv = k.bv;
+  omb = k.omb;
+  if (t.dsc) {
+    const double b = load_step_scalars(t.dsc).beta_val;
+    bv = (float)b;
+    omb = (float)(1.0 - b);
+  }
+}
 
 // The matrix that owns workgroup blockIdx.x of a launch of kind KIND, and the
 // workgroup's index within that matrix.
@@ -178,6 +191,8 @@ __global__ __launch_bounds__(256) void k_ax_el(XT t) {
   const float clip = (OP == XE_DIV) ? gp(ws)[L.scal] : 1.0f;
   const float rmean = (OP == XE_FCU || OP == XE_FU) ? gp(ws)[L.scal + 1] : 1.0f;
   const float cmean = (OP == XE_FUC) ? gp(ws)[L.scal + 2] : 1.0f;
+  float bv = 0.0f, omb = 0.0f;
+  if constexpr (OP == XE_SQB || OP == XE_V32) x_bv(t, k, bv, omb);
   double acc = 0.0;
   const int64_t stride = (int64_t)k.np * 1024;
   for (int64_t i = (lb * 256 + threadIdx.x) * 4; i < k.n; i += stride) {
@@ -185,7 +200,7 @@ __global__ __launch_bounds__(256) void k_ax_el(XT t) {
     if constexpr (OP == XE_SQB) {
       x_ld4(k.g, i, k.n, k.v4, a);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (a[e] * a[e]) * k.bv;
+      for (int e = 0; e < 4; ++e) o[e] = (a[e] * a[e]) * bv;
       x_st4(ws + L.xv, i, k.n, k.v4, o);
     } else if constexpr (OP == XE_V32) {
       x_ld4(k.g, i, k.n, k.v4, a);
@@ -193,7 +208,7 @@ __global__ __launch_bounds__(256) void k_ax_el(XT t) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float g2 = a[e] * a[e];
-        o[e] = k.first ? g2 * k.bv : lerp_ref(b[e], g2, k.bv);
+        o[e] = k.first ? g2 * bv : lerp_ref(b[e], g2, bv);
       }
       x_st4(k.v, i, k.n, k.v4, o);
     } else if constexpr (OP == XE_U) {
@@ -399,7 +414,9 @@ __global__ __launch_bounds__(256) void k_ax_vec(XT t) {
   const float mean = gp(k.ws)[(row ? L.rowm : L.colm) + i];
   if constexpr (OP == XV_VAR) {
     float* s = row ? k.rv : k.cv;
-    gp(s)[i] = k.first ? mean * k.bv : __builtin_fmaf(k.bv, mean, gp(s)[i] * k.omb);
+    float bv, omb;
+    x_bv(t, k, bv, omb);
+    gp(s)[i] = k.first ? mean * bv : __builtin_fmaf(bv, mean, gp(s)[i] * omb);
   } else {
     float* s = row ? k.cr : k.cc;
     gp(s)[i] = lerp_ref(gp(s)[i], mean, k.w3);
@@ -458,26 +475,35 @@ static void x_counts(const XK& k, int64_t* cnt) {
 // A batch of matrices that share every flag and hyper-parameter of the stage:
 // their descriptors (wb filled in), the total grid of each launch kind, the
 // device tables (null for a single matrix), and the arguments.
+// The descriptors change within a stage (the momentum pass sets src and m): each
+// version has a slot of its own in the table, so that a later call with the same
+// arguments finds all of them in place and need not upload (upload == 0).
+constexpr int kXSync = 3;
 struct XB {
   std::vector<XD> d;
   std::vector<const a8_apollo_x_args*> a;
   int64_t total[XW_N];
-  XD* tab_dev;          // n descriptors
+  XD* tab_dev;          // kXSync slots of n descriptors
   void* mema_dev;       // m_ema_table_bytes(n)
   void* vema_dev;       // v_ema_table_bytes(2 n)
   void* tail_dev;       // the larger of came_tail_table_bytes(n) and fact_tail_table_bytes(n)
   hipStream_t st;
   int tail_rs;          // a fused tail wrote the row sums of u_rowsums matrices
+  int upload;           // copy the tables (0: an earlier call with the same arguments left them)
+  int slot;             // the next descriptor slot
+  const XD* cur;        // the current descriptor version
+  const a8_step_scalars* dsc;   // device step block (the V weight), or null
 };
 
 static XT x_tab(const XB& b) {
   XT t{};
   if (b.tab_dev) {
-    t.tab = b.tab_dev;
+    t.tab = b.cur;
     t.ntab = (int)b.d.size();
   } else {
     t.one = b.d[0];
   }
+  t.dsc = b.dsc;
   return t;
 }
 
@@ -522,10 +548,15 @@ static int x_clip(const XB& b) {
   return x_el<XE_DIV>(b);
 }
 
-// Re-uploads the descriptors after a change of the per-matrix pointers.
+// Publishes the descriptors (first, and after a change of the per-matrix
+// pointers) in the next slot.
 static int x_sync(XB& b) {
   if (!b.tab_dev) return 0;
-  if (upload_table(b.tab_dev, b.d.data(), sizeof(XD) * b.d.size(), b.st) != hipSuccess)
+  if (b.slot >= kXSync) return set_error(A8_ERR_ARG, "low-rank stage: descriptor slots exhausted");
+  XD* dst = b.tab_dev + (size_t)b.slot * b.d.size();
+  ++b.slot;
+  b.cur = dst;
+  if (b.upload && upload_table(dst, b.d.data(), sizeof(XD) * b.d.size(), b.st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   return 0;
 }
@@ -545,7 +576,8 @@ static int x_momentum(XB& b, bool from_u) {
   if (a0->m_fp32) return x_el<XE_M32>(b);
   std::vector<MEmaItem> it(n);
   for (size_t i = 0; i < n; ++i) it[i] = MEmaItem{b.a[i]->m_q, b.a[i]->m_scale, b.d[i].k.src, b.d[i].k.m, b.d[i].k.n};
-  return m_ema_multi(it.data(), (int)n, b.mema_dev, a0->beta1, a0->m_block_size, a0->m_bits, a0->m_mode, b.st);
+  return m_ema_multi(it.data(), (int)n, b.mema_dev, a0->beta1, a0->m_block_size, a0->m_bits, a0->m_mode, b.st,
+                     b.upload);
 }
 
 static int x_stage(XB& b) {
@@ -575,7 +607,7 @@ static int x_stage(XB& b) {
           }
           b.tail_rs = 1;
           return fact_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->apollo_eps, a0->m_fp32 != nullptr,
-                                 a0->m_bits, a0->m_mode, a0->m_block_size, b.st);
+                                 a0->m_bits, a0->m_mode, a0->m_block_size, b.st, b.upload);
         }
         if ((rc = x_momentum(b, false))) return rc;
         for (auto& e : b.d) e.k.src = e.k.m;
@@ -602,7 +634,7 @@ static int x_stage(XB& b) {
                                  k.C};
       }
       if ((rc = v_ema_multi(it.data(), (int)(2 * n), b.vema_dev, 1.0 - a0->beta3, a0->block_size, 0, 0.0f,
-                            -126.0f, a0->c_bits, b.st)))
+                            -126.0f, a0->c_bits, b.st, b.upload)))
         return rc;
     } else if ((rc = x_vec<XV_CONF>(b))) {
       return rc;
@@ -622,10 +654,10 @@ static int x_stage(XB& b) {
     if (a0->first_step) {
       if ((rc = x_el<XE_SQB>(b))) return rc;
       if ((rc = v_ema_multi(it.data(), (int)n, b.vema_dev, 1.0, a0->block_size, 0, 0.0f, -126.0f, a0->v_bits,
-                            b.st)))
+                            b.st, b.upload)))
         return rc;
     } else if ((rc = v_ema_multi(it.data(), (int)n, b.vema_dev, a0->beta_v, a0->block_size, 1, 0.0f, a0->log_floor,
-                                 a0->v_bits, b.st))) {
+                                 a0->v_bits, b.st, b.upload, b.dsc))) {
       return rc;
     }
   } else if ((rc = x_el<XE_V32>(b))) {
@@ -659,7 +691,7 @@ static int x_stage(XB& b) {
     b.tail_rs = 1;
     return came_tail_multi(it.data(), (int)n, b.tail_dev, a0->beta1, a0->beta3, a0->eps_came, a0->eps_sq,
                            a0->m_fp32 != nullptr, a0->m_bits, a0->m_mode, a0->m_block_size, a0->c_bits,
-                           a0->block_size, b.st);
+                           a0->block_size, b.st, b.upload);
   }
   if ((rc = x_clip(b))) return rc;
   if (!a0->has_m) return 0;   // unreachable through the optimizer (beta3 needs beta1): u = clipped U
@@ -676,7 +708,7 @@ static int x_stage(XB& b) {
     }
     char* vt = b.vema_dev ? static_cast<char*>(b.vema_dev) + v_ema_table_bytes((int)n) : nullptr;
     if ((rc = v_ema_multi(it.data(), (int)n, vt, 1.0 - a0->beta3, a0->block_size, 0, 0.0f, -126.0f, a0->c_bits,
-                          b.st)))
+                          b.st, b.upload)))
       return rc;
   }
   return x_el<XE_UCAME>(b);
@@ -787,8 +819,8 @@ static int64_t x_round(int64_t b) { return (b + 255) / 256 * 256; }
 static int64_t x_bytes(int n) {
   const int64_t tail = came_tail_table_bytes(n) > fact_tail_table_bytes(n) ? came_tail_table_bytes(n)
                                                                            : fact_tail_table_bytes(n);
-  return x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) + x_round(v_ema_table_bytes(2 * n)) +
-         x_round(tail);
+  return kXSync * x_round((int64_t)sizeof(XD) * n) + x_round(m_ema_table_bytes(n)) +
+         x_round(v_ema_table_bytes(2 * n)) + x_round(tail);
 }
 
 }  // namespace a8
@@ -813,15 +845,26 @@ int a8_apollo_lowrank_x(const a8_apollo_x_args* a, void* stream) {
   b.d[0].k = x_desc(a);
   x_counts(b.d[0].k, b.total);
   b.st = (hipStream_t)stream;
+  b.upload = 1;
   return x_run(b);
 }
 
 int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* table_dev, int64_t table_bytes,
-                              void* stream) {
+                              int upload, const void* step_scalars, void* stream) {
   if (nmat <= 0) return 0;
   if (!args) return set_error(A8_ERR_ARG, "null pointer");
   if (!table_dev || table_bytes < x_bytes(nmat))
     return set_error(A8_ERR_SIZE, "table_dev too small: need a8_apollo_x_table_bytes(nmat)");
+  if (upload) {
+    // a captured copy would replay from the library's host staging as it is at
+    // replay time: the tables are uploaded by an eager call, and a captured one
+    // passes upload == 0
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess)
+      return set_error(A8_ERR_HIP, "hipStreamIsCapturing failed");
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(A8_ERR_ARG, "a8_apollo_lowrank_x_multi: upload != 0 on a capturing stream");
+  }
   for (int i = 0; i < nmat; ++i) {
     const int rc = x_check(args + i);
     if (rc) return rc;
@@ -834,6 +877,8 @@ int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* tabl
     if (batch_of[(size_t)i] >= 0) continue;
     XB b{};
     b.st = (hipStream_t)stream;
+    b.upload = upload ? 1 : 0;
+    b.dsc = reinterpret_cast<const a8_step_scalars*>(step_scalars);
     for (int j = i; j < nmat; ++j) {
       if (batch_of[(size_t)j] >= 0 || !x_same(args + i, args + j)) continue;
       batch_of[(size_t)j] = i;
@@ -854,7 +899,7 @@ int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* tabl
     for (int e = 0; e < XW_N; ++e)
       if (b.total[e] > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "low-rank batch too large");
     b.tab_dev = reinterpret_cast<XD*>(base);
-    b.mema_dev = base + x_round((int64_t)sizeof(XD) * n);
+    b.mema_dev = base + kXSync * x_round((int64_t)sizeof(XD) * n);
     b.vema_dev = static_cast<char*>(b.mema_dev) + x_round(m_ema_table_bytes(n));
     b.tail_dev = static_cast<char*>(b.vema_dev) + x_round(v_ema_table_bytes(2 * n));
     base += x_bytes(n);

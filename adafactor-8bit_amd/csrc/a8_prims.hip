@@ -193,7 +193,9 @@ struct VemaDesc {
 
 template <int VB>
 __global__ __launch_bounds__(256) void k_vema_multi(VemaDesc one, const VemaDesc* __restrict__ tab, int ntab,
-                                                    int lbv, float w, int square, float eps1, float floor_) {
+                                                    int lbv, float w, int square, float eps1, float floor_,
+                                                    const a8_step_scalars* w_dev) {
+  if (w_dev) w = (float)load_step_scalars(w_dev).beta_val;   // the device step's V weight
   __shared__ float xw[8];
   __shared__ float dtab[4 * 256];
   const int64_t wg = blockIdx.x;
@@ -533,7 +535,9 @@ hipError_t prims_upload_qmap(const float* q8, const float* q4) { return upload_q
 // writes the codes (and dec).  vema_unit's arithmetic, element for element.
 template <int VB, typename T>
 __global__ __launch_bounds__(256) void k_vema_gen(VemaDesc one, const VemaDesc* __restrict__ tab, int ntab, int bs,
-                                                  float w, int square, float eps1, float floor_) {
+                                                  float w, int square, float eps1, float floor_,
+                                                  const a8_step_scalars* w_dev) {
+  if (w_dev) w = (float)load_step_scalars(w_dev).beta_val;   // the device step's V weight
   __shared__ float s_tab[256];   // decode table of the old fit (both passes read it)
   __shared__ float s_new[256];   // decode table of the new fit (dec)
   __shared__ uint32_t s_st[2];
@@ -664,11 +668,11 @@ static void launch_f2d_t(int op, unsigned nwg, hipStream_t st, const F2& a) {
 int64_t v_ema_table_bytes(int n) { return (int64_t)sizeof(VemaDesc) * (int64_t)n; }
 
 int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_size, int square, float eps1,
-                float log_floor, int v_bits, hipStream_t st) {
+                float log_floor, int v_bits, hipStream_t st, int upload, const a8_step_scalars* w_dev) {
   if (n <= 0) return 0;
   if (!table_dev && n > 1) {   // no table: one launch per tensor
     for (int i = 0; i < n; ++i) {
-      const int rc = v_ema_multi(it + i, 1, nullptr, w, block_size, square, eps1, log_floor, v_bits, st);
+      const int rc = v_ema_multi(it + i, 1, nullptr, w, block_size, square, eps1, log_floor, v_bits, st, 1, w_dev);
       if (rc) return rc;
     }
     return 0;
@@ -695,7 +699,7 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
   if (wg > 0x7FFFFFFF) return set_error(A8_ERR_SIZE, "AL EMA: too many elements");
   const VemaDesc* dt = nullptr;
   if (table_dev) {
-    if (upload_table(table_dev, tab.data(), sizeof(VemaDesc) * (size_t)n, st) != hipSuccess)
+    if (upload && upload_table(table_dev, tab.data(), sizeof(VemaDesc) * (size_t)n, st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
     dt = reinterpret_cast<const VemaDesc*>(table_dev);
   }
@@ -703,18 +707,18 @@ int v_ema_multi(const VEmaItem* it, int n, void* table_dev, double w, int block_
   if (gen) {
     if (v_bits == 8)
       hipLaunchKernelGGL((k_vema_gen<8, float>), dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, block_size,
-                         (float)w, square, eps1, log_floor);
+                         (float)w, square, eps1, log_floor, w_dev);
     else
       hipLaunchKernelGGL((k_vema_gen<16, float>), dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, block_size,
-                         (float)w, square, eps1, log_floor);
+                         (float)w, square, eps1, log_floor, w_dev);
     return check_launch("k_vema_gen");
   }
   if (v_bits == 8)
     hipLaunchKernelGGL(k_vema_multi<8>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
-                       eps1, log_floor);
+                       eps1, log_floor, w_dev);
   else
     hipLaunchKernelGGL(k_vema_multi<16>, dim3((unsigned)wg), dim3(256), 0, st, one, dt, n, lbv, (float)w, square,
-                       eps1, log_floor);
+                       eps1, log_floor, w_dev);
   return check_launch("k_vema_multi");
 }
 
@@ -952,7 +956,7 @@ __global__ __launch_bounds__(256) void k_fact_tail(FactTailDesc one, const FactT
 int64_t fact_tail_table_bytes(int n) { return (int64_t)sizeof(FactTailDesc) * (int64_t)n; }
 
 int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1, float apollo_eps, int m_fp32,
-                    int m_bits, int m_mode, int m_block_size, hipStream_t st) {
+                    int m_bits, int m_mode, int m_block_size, hipStream_t st, int upload) {
   if (n <= 0) return 0;
   if (!m_fp32 && !(m_block_size >= 32 && m_block_size <= 2048 && (m_block_size & (m_block_size - 1)) == 0))
     return set_error(A8_ERR_BLOCK, "factorised tail: m_block_size must be a power of two in [32, 2048]");
@@ -988,7 +992,7 @@ int fact_tail_multi(const FactTailItem* it, int n, void* table_dev, double beta1
   const FactTailDesc* dt = nullptr;
   if (n > 1) {
     if (!table_dev) return set_error(A8_ERR_ARG, "factorised tail: a table is needed for several matrices");
-    if (upload_table(table_dev, tab.data(), sizeof(FactTailDesc) * (size_t)n, st) != hipSuccess)
+    if (upload && upload_table(table_dev, tab.data(), sizeof(FactTailDesc) * (size_t)n, st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
     dt = reinterpret_cast<const FactTailDesc*>(table_dev);
   }
@@ -1008,7 +1012,7 @@ int64_t came_tail_table_bytes(int n) { return (int64_t)sizeof(CameTailDesc) * (i
 
 int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1, double beta3, float eps_came,
                     float eps_sq, int m_fp32, int m_bits, int m_mode, int m_block_size, int c_bits, int block_size,
-                    hipStream_t st) {
+                    hipStream_t st, int upload) {
   if (n <= 0) return 0;
   if (!came_tail_ok(m_fp32, m_block_size, c_bits, block_size))
     return set_error(A8_ERR_BLOCK, "CAME tail: block sizes must be powers of two");
@@ -1051,7 +1055,7 @@ int came_tail_multi(const CameTailItem* it, int n, void* table_dev, double beta1
   const CameTailDesc* dt = nullptr;
   if (n > 1) {
     if (!table_dev) return set_error(A8_ERR_ARG, "CAME tail: a table is needed for several matrices");
-    if (upload_table(table_dev, tab.data(), sizeof(CameTailDesc) * (size_t)n, st) != hipSuccess)
+    if (upload && upload_table(table_dev, tab.data(), sizeof(CameTailDesc) * (size_t)n, st) != hipSuccess)
       return set_error(A8_ERR_HIP, "table upload failed");
     dt = reinterpret_cast<const CameTailDesc*>(table_dev);
   }
@@ -1099,7 +1103,7 @@ int a8_log_quantize_lerp(void* q, float* scale, float* min_log, const void* x, i
     one.out = fp32_out; one.n = numel; one.nblk = nblk;
 #define A8_VEMAG(VB, T)                                                                                        \
   hipLaunchKernelGGL((k_vema_gen<VB, T>), dim3((unsigned)nwg), dim3(256), 0, st, one, nullptr, 1, block_size, w, \
-                     square_input, eps1, log_floor)
+                     square_input, eps1, log_floor, nullptr)
     switch (x_dtype) {
       case A8_F32: if (v_bits == 8) A8_VEMAG(8, float); else A8_VEMAG(16, float); break;
       case A8_BF16: if (v_bits == 8) A8_VEMAG(8, __hip_bfloat16); else A8_VEMAG(16, __hip_bfloat16); break;

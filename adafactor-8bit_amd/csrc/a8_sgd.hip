@@ -431,7 +431,7 @@ int64_t m_ema_table_bytes(int n) { return (int64_t)sizeof(SgdDesc) * (int64_t)n;
 // a8_m_quantize_lerp).  table_dev: m_ema_table_bytes(n) of device memory, or null
 // for one launch per tensor (the descriptor then travels as a kernel argument).
 int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int block_size, int m_bits, int m_mode,
-                hipStream_t st) {
+                hipStream_t st, int upload) {
   if (n <= 0) return 0;
   if (!table_dev && n > 1) {   // no table: one launch per tensor
     for (int i = 0; i < n; ++i) {
@@ -457,7 +457,7 @@ int m_ema_multi(const MEmaItem* it, int n, void* table_dev, double beta, int blo
     wg += units_of(it[i].n, h);
   }
   if (!table_dev) return launch_sgd(A8_F32, 0, 3, 1, wg, st, tab[0], nullptr, 0, h);
-  if (upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)n, st) != hipSuccess)
+  if (upload && upload_table(table_dev, tab.data(), sizeof(SgdDesc) * (size_t)n, st) != hipSuccess)
     return set_error(A8_ERR_HIP, "table upload failed");
   SgdDesc none{};
   return launch_sgd(A8_F32, 0, 3, 1, wg, st, none, reinterpret_cast<const SgdDesc*>(table_dev), n, h);

@@ -477,13 +477,17 @@ int64_t a8_apollo_table_bytes(int ntensors);
  * matrices with rows >= cols and rank a power of two in [8, 512]: their row
  * sums of u^2 and g_low^2 are read in place of u and g_low (the two norms of
  * compute_apollo_norms, kernels.cu:2410-2453, per channel); u_rowsums on any
- * other matrix, or phase 3 without it, reads the wrong values. */
+ * other matrix, or phase 3 without it, reads the wrong values.  upload and
+ * step_scalars as for a8_apollo_step_multi: phase 1 runs the device projection
+ * schedule, phases 2 and 3 read lr, the bias factor and the SR step from the
+ * block; a phase after phase 1 of the same records may pass upload == 0. */
 int a8_apollo_step_multi_phase(int phase, int dtype, int stochastic, const a8_apollo_tensor* tensors,
                                int ntensors, void* table_dev, int64_t table_bytes, double beta_val, double beta1,
                                int has_m, float apollo_eps, float log_floor, int v_bits, int block_size, int m_bits,
                                int m_mode, int m_fp32, int m_block_size, int channel, float apollo_scale,
                                int scale_front, int fira, float fira_margin, float d, float lr_val, float eps2,
-                               int scale_parameter, int bias_mode, float weight_decay, int wd_mode, void* stream);
+                               int scale_parameter, int bias_mode, float weight_decay, int wd_mode, int upload,
+                               const void* step_scalars, void* stream);
 
 /* Low-rank state and hyper-parameters of one matrix for a8_apollo_lowrank_x.
  * Coded states are AL8 (uint8) / AL16 (int16) codes with per-block scale and
@@ -549,11 +553,16 @@ int64_t a8_apollo_x_workspace_floats(int64_t rows_low, int64_t cols_low);
 
 /* The same stage for nmat matrices at once (the reference steps them one by one
  * in _update_param_apollo, optimizer.py:2587-3084): matrices that agree on every
- * flag and hyper-parameter of their records share one launch per pass, over a
- * descriptor table in table_dev (a8_apollo_x_table_bytes(nmat) bytes of device
- * memory, written on the stream).  Each record needs its own xws. */
+ * flag and hyper-parameter of their records share one launch per pass, over
+ * descriptor tables in table_dev (a8_apollo_x_table_bytes(nmat) bytes of device
+ * memory, written on the stream when `upload` is non-zero; with upload == 0 the
+ * tables of an earlier call with the same records are used, and upload != 0 on a
+ * capturing stream is refused).  Each record needs its own xws.
+ * step_scalars (NULL: the records' beta_v): the device block of a8_step_advance,
+ * whose beta_val is the V lerp weight (the records' beta_v is then not read), so
+ * that the stage can be captured in a HIP graph with the phases around it. */
 int a8_apollo_lowrank_x_multi(const a8_apollo_x_args* args, int nmat, void* table_dev, int64_t table_bytes,
-                              void* stream);
+                              int upload, const void* step_scalars, void* stream);
 int64_t a8_apollo_x_table_bytes(int nmat);
 
 /* Replaces dequantize_log_nonneg (kernels.cu:2593-2632; called by

@@ -93,7 +93,7 @@ def test_apollo_lowrank_and_phase_argument_errors_without_gpu():
     assert L.a8_apollo_x_workspace_floats(0, 8) == 0
     assert L.a8_apollo_x_workspace_floats(5632, 256) > 4 * 5632 * 256
     rc = L.a8_apollo_step_multi_phase(4, 0, 0, None, 1, None, 0, 0.001, 0.9, 1, 1e-6, -39.9, 0, 2048, 8, 0, 1,
-                                      256, 1, 1.0, 0, 1, 0.01, 0.0, 1e-3, 1e-3, 0, 0, 0.0, 0, None)
+                                      256, 1, 1.0, 0, 1, 0.01, 0.0, 1e-3, 1e-3, 0, 0, 0.0, 0, 1, None, None)
     assert rc == -1 and b"phase" in L.a8_last_error()
     assert L.a8_vema_fp32(None, None, 0, 0.001, 0.0, 4, None) == -1
     assert L.a8_vema_fp32(256, 256, 9, 0.001, 0.0, 4, None) == -2

@@ -824,7 +824,7 @@ def _per_matrix_stage(L):
     import ctypes
     from adafactor8bit import _native as nat
 
-    def run(xarr, n, tab, nbytes, stream):
+    def run(xarr, n, tab, nbytes, upload, dsc, stream):
         recs = ctypes.cast(xarr, ctypes.POINTER(nat.ApolloXArgs))
         for i in range(n):
             rc = L.a8_apollo_lowrank_x(ctypes.byref(recs[i]), stream)

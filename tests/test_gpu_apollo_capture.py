@@ -19,7 +19,12 @@ the host schedule (stable_randn); later refreshes use the device generator
   is the generator's for the new seed, and the schedule's state (apollo_seed,
   current_proj_seed, last_proj_step) equals the default path's;
 * before the first device refresh, capturable eager steps equal the default
-  path's bit for bit.
+  path's bit for bit;
+* the same two properties for the low-rank stages that run between the phases
+  of a8_apollo_step_multi_phase: factorised (with and without momentum, the
+  latter with the step-dependent V weight t^-0.8), CAME (AL8, AL16 with UF4
+  momentum, fp32), factorised CAME (AL8, fp32), and the plain stage at block
+  sizes the fused kernel does not take (B_V 384, B_M 96).
 """
 import numpy as np
 import pytest
@@ -167,3 +172,61 @@ def test_apollo_capturable_schedule_matches_default_path():
                 ref = ap.proj_t(p.shape[0], p.shape[1], 256, int(st["current_proj_seed"])).reshape(-1)
                 _assert_ulp1(pt, ref, f"step 4 refresh, matrix {i}")
         print(f"[apollo capturable eager] step {t}", flush=True)
+
+
+# Low-rank stages between the projection and finish phases (a8_apollo_lowrank_x_multi)
+X_CAP = {
+    "fact_uf8": dict(apollo_factorize=True),
+    "fact_nomom": dict(apollo_factorize=True, beta1=None, beta2=None, beta2_decay=-0.8, d=1.0),
+    "came_al8_clip": dict(beta3=0.9999, d=1.0, eps_came=1e-16),
+    "came_al16_uf4": dict(beta3=0.99, d=1.0, eps_came=1e-16, v_quant_type="al16", c_quant_type="al16",
+                          m_quant_type="uf4"),
+    "came_fp32": dict(beta3=0.9999, d=1.0, eps_came=1e-16, quantize=False),
+    "fact_came_al8": dict(apollo_factorize=True, beta3=0.9999, d=1.0, eps_came=1e-16),
+    "fact_came_fp32": dict(apollo_factorize=True, beta3=0.999, d=1.0, eps_came=1e-16, quantize=False),
+    "plain_bv384_bm96": dict(block_size=384, m_block_size=96),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", sorted(X_CAP))
+def test_apollo_variant_graph_replays_equal_eager_steps(variant):
+    """The variant's low-rank stage reads the V weight from the device block and
+    uploads its tables only when a record changes (never under capture)."""
+    print(f"[apollo capture] {variant}", flush=True)
+    extra = X_CAP[variant]
+    pa, oa = _setup(True, **extra)   # replayed
+    pb, ob = _setup(True, **extra)   # eager
+    pc, oc = _setup(False, **extra)  # default path
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob), (pc, oc)):
+            _load(ps, t)
+            o.step()
+    torch.cuda.synchronize()
+    _same(ob, oc, pb, pc, f"{variant}: capturable eager vs default, step 2")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load(pa, 3)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    _same(oa, ob, pa, pb, f"{variant}: after capture (nothing ran)")
+    for t in range(3, 9):   # device refreshes at steps 4 and 7
+        _load(pa, t)
+        graph.replay()
+        _load(pb, t)
+        ob.step()
+        if t == 3:
+            _load(pc, t)
+            oc.step()
+        junk = torch.randn(4096, device="cuda").sum()
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        _same(oa, ob, pa, pb, f"{variant}: step {t}")
+        if t == 3:
+            _same(ob, oc, pb, pc, f"{variant}: capturable eager vs default, step 3")
+    assert _schedule(oa, pa) == _schedule(ob, pb)
+    print(f"[apollo capture] {variant}: 6 replays equal", flush=True)

@@ -199,10 +199,12 @@ def test_lag_norm_clips_by_this_steps_norm():
 
 @pytest.mark.gpu
 def test_capturable_rejects_paths_with_host_scalars():
-    print("[capturable] factorised APOLLO rejected", flush=True)
-    ps, o = _setup(dict(ADAMW, apollo_rank=8, apollo_factorize=True, block_size=128, m_block_size=32), [(64, 96)],
-                   torch.float32, capturable=True)
+    """APOLLO without a projection gap refreshes P on the host schedule only: refused
+    before the step touches the state."""
+    print("[capturable] APOLLO with apollo_update_proj_gap=0 rejected", flush=True)
+    ps, o = _setup(dict(ADAMW, apollo_rank=8, apollo_factorize=True, apollo_update_proj_gap=0, block_size=128,
+                        m_block_size=32), [(64, 96)], torch.float32, capturable=True)
     ps[0].grad.copy_(make_grad((64, 96), 0, 1, 17))
-    with pytest.raises(NotImplementedError, match="APOLLO"):
+    with pytest.raises(NotImplementedError, match="apollo_update_proj_gap"):
         o.step()
     assert o.state[ps[0]]["step"] == 0

@@ -26,9 +26,9 @@ kernels): ``adafactor`` (C2: factored AL8, B_V 256, no beta1, Student-t grads,
 bf16 params and grads 1e-3*N(0,1), the reference's apollo preset at rank 256,
 gap 200, channel scale, Fira, UF8 M / AL8 V low-rank states, SR writeback).
 For those the roofline is the whole step's algorithmic bytes over its GPU time
-(HIP events around each step); adafactor, came and apollo are timed, like the
-headline, eagerly and then as graph replays of one captured ``step()`` (``value``
-from the replays); apollo also reports the projection's flops.
+(HIP events around each step); every workload is timed, like the headline,
+eagerly and then as graph replays of one captured ``step()`` (``value`` from the
+replays); apollo also reports the projection's flops.
 ``apollo_factorize`` and ``apollo_came`` time C4 with the factorised (row /
 column low-rank second moment) and CAME (beta3 0.9999, RMS clip d=1) low-rank
 stages; their roofline counts C4's bytes only (a lower bound).
@@ -385,11 +385,9 @@ def main():
 def bench_factored(args, params, nparams, shapes, Adafactor8Bit):
     apollo = args.workload.startswith("apollo")
     kw = APOLLO_VARIANTS[args.workload] if apollo else {"adafactor": ADAFACTOR, "came": CAME}[args.workload]
-    # adafactor, came and plain APOLLO run capturable (device step count and, for
-    # APOLLO, the device projection schedule): timed eagerly, then as replays of one
-    # captured step; the factorised and CAME APOLLO stages take host scalars and
-    # run eagerly only
-    graphable = args.workload in ("adafactor", "came", "apollo", "apollo_fp32")
+    # every workload runs capturable (device step count and, for APOLLO, the device
+    # projection schedule): timed eagerly, then as replays of one captured step
+    graphable = True
     opt = Adafactor8Bit(params, **(dict(kw, capturable=True) if graphable else kw))
     for _ in range(args.warmup):
         opt.step()

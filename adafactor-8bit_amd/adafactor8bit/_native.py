@@ -55,7 +55,7 @@ class TensorSgd(ctypes.Structure):
     """Mirror of ``a8_tensor_sgd``."""
     _fields_ = [("param", _c_vp), ("grad", _c_vp), ("m_q", _c_vp), ("m_scale", _c_vp), ("m", _c_vp),
                 ("norm_buf", _c_vp), ("fira", _c_vp), ("alpha", _c_vp), ("decay", _c_vp),
-                ("numel", _c_i64), ("sr_seed", _c_u64), ("norm_parts", _c_vp)]
+                ("numel", _c_i64), ("sr_seed", _c_u64), ("norm_parts", _c_vp), ("fira_sum", _c_vp)]
 
 
 class FactoredPrimArgs(ctypes.Structure):

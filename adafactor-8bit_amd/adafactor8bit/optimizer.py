@@ -524,6 +524,11 @@ class _Plan:
                     self.mqt if self.has_m else None, self.bs, self.mbs, self.has_m, self.beta1,
                     self.beta_val, self.eps_d, self.eps_g, self.eps_sq, self.adam_denom, self.mom_only,
                     self.alpha_val, self.decay_val, self.d, self.fira, self.margin)
+        if self.path == "sgd" and (self.d > 0 or self.fira):
+            mq = self.has_m and self.quant and self.mqt != "fp32" and "m_q" in self.st
+            return ("sgdc", self.p.device, self.p.dtype, self.g.dtype, self.step, self.sr, self.has_m, mq,
+                    self.mqt if mq else None, self.mbs if mq else 0, self.beta1, self.alpha_val, self.decay_val,
+                    self.d, self.fira, self.margin)
         if self.d > 0 or self.fira:
             return None
         if self.path == "sgd":
@@ -1326,6 +1331,88 @@ def _run_batch_q1dc(opt, key, plans):
     launch(nat.MODE_APPLY)
 
 
+def _run_batch_sgdc(opt, key, plans):
+    """SGD tensors with an RMS clip or Fira as one group: NORM (each tensor's sum of
+    u^2 in its own slot, its partials added in index order) -> one Fira launch over
+    all tensors -> APPLY, each one multi-tensor launch (the per-tensor sequence of
+    _run_sgd, optimizer.py:2045-2077, 796-810).  APPLY reads each tensor's Fira
+    scale and finite sum from that launch's output (a8_tensor_sgd.fira, fira_sum)."""
+    P0 = plans[0]
+    dev = P0.p.device
+    L = nat.lib()
+    n = len(plans)
+    fira = bool(P0.fira)
+    moms = [_sgd_momentum(pl) for pl in plans]
+    kind = moms[0][3]
+    ws = opt._ws.setdefault((dev, "sgdc"), {})
+    ck = (tuple((pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(mo[0]), nat.ptr(mo[2])) for pl, mo in zip(plans, moms)),
+          P0.sr, kind, fira)
+    refs = [tuple(v.data_ptr() for k, v in pl.st.items() if torch.is_tensor(v) and k != "fira_prev_norm")
+            for pl in plans]
+    ent = ws.get(ck)
+    if ent is None or ent["refs"] != refs:
+        poffs, ptot = [], 0
+        for pl in plans:   # per-tensor slices of the NORM pass's partial-sum workspace
+            poffs.append(ptot)
+            ptot += _parts_of(pl)
+        parts = torch.empty(max(ptot, 1), dtype=torch.float64, device=dev)
+        acc = torch.zeros(n, dtype=torch.float32, device=dev)        # sum u^2
+        fout = torch.zeros(3 * n, dtype=torch.float32, device=dev)   # Fira: scale | prev norm | finite sum
+        a0, f0 = acc.data_ptr(), fout.data_ptr()
+        arrs = {}
+        for mode in (nat.MODE_NORM, nat.MODE_APPLY):
+            arr = (nat.TensorSgd * n)()
+            for i, (pl, (m_q, m_scale, m, _)) in enumerate(zip(plans, moms)):
+                fs = f0 + 4 * i if (mode == nat.MODE_APPLY and fira) else None
+                arr[i] = nat.TensorSgd(pl.p.data_ptr(), pl.g.data_ptr(), nat.ptr(m_q), nat.ptr(m_scale), nat.ptr(m),
+                                       a0 + 4 * i, fs, None, None, pl.p.numel(), int(pl.st.get("sr_seed", 0)),
+                                       parts.data_ptr() + 8 * poffs[i], f0 + 4 * (2 * n + i) if fs else None)
+            arrs[mode] = [arr, torch.empty(int(L.a8_table_bytes_sgd(n)), dtype=torch.uint8, device=dev), 1]
+        ent = {"refs": refs, "acc": acc, "fout": fout, "parts": parts, "arrs": arrs}
+        if len(ws) > 16:
+            ws.clear()
+        ws[ck] = ent
+    acc, fout = ent["acc"], ent["fout"]
+    strm = nat.stream_of(dev)
+    has_dec = int(P0.decay_val is not None)
+    dec_val = P0.decay_val if has_dec else 1.0
+    mbs = P0.mbs if kind == 1 else 32
+
+    def launch(mode):
+        arr, table, up = ent["arrs"][mode]
+        _no_upload_in_capture(up)
+        rc = L.a8_sgd_step_multi(
+            mode, nat.dtype_code(P0.p.dtype), int(P0.sr), arr, n, table.data_ptr(), table.numel(),
+            P0.beta1 if P0.has_m else 0.0, kind, S.m_bits(P0.mqt) if kind == 1 else 0,
+            S.m_mode(P0.mqt) if kind == 1 else 0, mbs, P0.d, float(P0.alpha_val), float(dec_val), has_dec,
+            int(P0.step), up, nat.ptr(P0.dsc), strm)
+        nat.check(rc, "a8_sgd_step_multi")
+        ent["arrs"][mode][2] = 0
+
+    acc.zero_()
+    launch(nat.MODE_NORM)
+    if fira:
+        # as in _run_batch_q1dc: a tensor without a previous norm takes 0 (scale 1,
+        # next = current), so every slot has one
+        prev_ok = all(torch.is_tensor(pl.st.get("fira_prev_norm")) and
+                      pl.st["fira_prev_norm"].data_ptr() == fout.data_ptr() + 4 * (n + i)
+                      for i, pl in enumerate(plans))
+        if not prev_ok:
+            vals = []
+            for pl in plans:
+                pv = pl.st.get("fira_prev_norm")
+                vals.append(torch.zeros((), dtype=torch.float32, device=dev) if pv is None else
+                            torch.as_tensor(pv, dtype=torch.float32).to(dev).reshape(()))
+            fout[n:2 * n].copy_(torch.stack(vals))
+        rc = L.a8_fira_scalar(acc.data_ptr(), fout.data_ptr() + 4 * n, None, fout.data_ptr(), n, 1, 2,
+                              _f32(1.0 + P0.margin), strm)
+        nat.check(rc, "a8_fira_scalar")
+        if not prev_ok:
+            for i, pl in enumerate(plans):
+                pl.st["fira_prev_norm"] = fout[n + i].view(())
+    launch(nat.MODE_APPLY)
+
+
 def _run_batch(opt, key, plans):
     path = key[0]
     if path == "factored":
@@ -1339,6 +1426,9 @@ def _run_batch(opt, key, plans):
         return
     if path == "q1dc":
         _run_batch_q1dc(opt, key, plans)
+        return
+    if path == "sgdc":
+        _run_batch_sgdc(opt, key, plans)
         return
     P0 = plans[0]
     dev = P0.p.device

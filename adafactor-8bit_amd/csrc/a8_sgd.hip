@@ -32,7 +32,8 @@ struct SgdDesc {
   float* m;             // fp32 momentum
   float* m_out;         // optional fp32 copy of m' (standalone EMA)
   float* norm_buf;      // sum of u^2 (NORM), read by APPLY
-  const float* fira;    // Fira scalar output [scale, prev', finite sum], or null
+  const float* fira;    // Fira's scale (the first of its [scale, prev', finite sum]), or null
+  const float* fira_sum;   // Fira's finite sum of u^2 (with fira)
   const float* alpha;
   const float* decay;
   int64_t numel;
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd(SgdDesc one, const SgdDesc* __r
           // a non-finite norm zeroes the update (optimizer.py:797-800)
           const bool fin = __builtin_isfinite(sqrtf(sum));
           const float sc = fin ? D.fira[0] : 0.0f;
-          sum = D.fira[2];
+          sum = *D.fira_sum;
 #pragma unroll
           for (int k = 0; k < 8; ++k) u[k] = u[k] * sc;
         }
@@ -235,7 +236,7 @@ __global__ __launch_bounds__(kSLanes) void k_sgd_gen(SgdDesc one, const SgdDesc*
       if (D.fira) {
         const bool fin = __builtin_isfinite(sqrtf(sum));   // a non-finite norm zeroes the update
         fsc = fin ? D.fira[0] : 0.0f;
-        sum = D.fira[2];
+        sum = *D.fira_sum;
       }
       if (h.d > 0.0f) step = a / fmaxf(1.0f, sqrtf(sum) / (float)(sqrt((double)n) * (double)h.d));
     }
@@ -501,7 +502,8 @@ int a8_sgd_step(int mode, int dtype, int stochastic, void* param, const void* gr
   }
   SgdDesc D{};
   D.param = param; D.grad = grad; D.m_q = m_q; D.m_scale = m_scale; D.m = m; D.norm_buf = norm_buf;
-  D.fira = fira; D.alpha = alpha; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
+  D.fira = fira; D.fira_sum = fira ? fira + 2 : nullptr;
+  D.alpha = alpha; D.decay = decay; D.numel = numel; D.sr_seed = sr_seed;
   D.norm_part = norm_parts;
   return launch_sgd(dtype, stochastic, mode, kind, units_of(numel, h), (hipStream_t)stream, D,
                     nullptr, 0, h);
@@ -542,6 +544,7 @@ int a8_sgd_step_multi(int mode, int dtype, int stochastic, const a8_tensor_sgd* 
       return set_error(A8_ERR_ALIGN, "param, grad and momentum must be 16-byte aligned");
     SgdDesc& D = tab[(size_t)i];
     D.param = t.param; D.grad = t.grad; D.norm_buf = t.norm_buf; D.fira = t.fira; D.norm_part = t.norm_parts;
+    D.fira_sum = t.fira ? (t.fira_sum ? t.fira_sum : t.fira + 2) : nullptr;
     D.alpha = t.alpha; D.decay = t.decay; D.numel = t.numel; D.sr_seed = t.sr_seed;
     if (m_kind == 1) { D.m_q = t.m_q; D.m_scale = t.m_scale; }
     if (m_kind == 2) D.m = t.m;

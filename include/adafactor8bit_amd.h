@@ -636,6 +636,10 @@ typedef struct a8_tensor_sgd {
   int64_t numel;
   uint64_t sr_seed;
   double* norm_parts;      /* NORM: a8_norm_parts_sgd(numel, ...) doubles of workspace */
+  const float* fira_sum;   /* APPLY with fira: Fira's finite sum of u^2 (NULL: fira + 2, the
+                              layout of a one-tensor a8_fira_scalar output); fira itself is
+                              read for the scale only, so a batch can point each tensor at
+                              out[i] and out[2n + i] of one n-tensor a8_fira_scalar */
 } a8_tensor_sgd;
 
 /* Multi-tensor form of a8_sgd_step: one launch per group.  m_kind: 0 none,

@@ -50,6 +50,12 @@ CASES = [
     ("adafactor1d_fp32_scale_clip_fira", FP32S, [(700, 1100), (2048,), (5000,)], torch.float32, "student_t"),
     # SGD (beta2 = beta2_decay = None): coded momentum with weight decay, bf16 with SR
     ("sgd_uf8_wd_bf16_sr", SGD, [(300, 260), (5000,), (2048,)], torch.bfloat16, "normal_zeros"),
+    # SGD with an RMS clip and Fira (one NORM launch, one Fira launch and one APPLY launch for the
+    # group), coded momentum with bf16 SR, and fp32 momentum with a clip only
+    ("sgd_uf8_clip_fira_bf16_sr", dict(SGD, d=1.0, enable_fira_for_adafactor=True),
+     [(700, 1100), (300, 260), (5000,)], torch.bfloat16, "logscale"),
+    ("sgd_fp32m_clip", dict(SGD, d=0.5, m_quant_type="fp32", stochastic_round_writeback=False),
+     [(700, 1100), (5000,)], torch.float32, "student_t"),
     # maximize: the kernels read a negated copy of the gradient kept per parameter, which the
     # captured step refills (bf16 SR quantised AdamW, and factored CAME with its vectors)
     ("adamw_bf16_sr_maximize", dict(ADAMW, stochastic_round_writeback=True, lr=1e-3, maximize=True),

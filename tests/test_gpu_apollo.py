@@ -864,3 +864,36 @@ def test_apollo_x_batched_equals_per_matrix(variant, rank, det_proj):
         for k, v in sa.items():
             if torch.is_tensor(v):
                 assert torch.equal(v, sb[k]), f"{variant} p{i}: state {k} differs"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,big", [((1024, 512), (4096, 2048)), ((512, 1536), (2048, 4096))],
+                         ids=["right", "left"])
+def test_apollo_step_is_the_same_alone_or_batched(shape, big):
+    """A matrix's APOLLO step does not depend on what else its group holds: the
+    wide projection's XCD ranges, the batched low-rank stage and the finish put
+    a 4-tile matrix stepped alone (each tile the only one of its XCD range) and
+    beside a 16-tile matrix (its tiles sharing a range with the big one's) on
+    different workgroups, but every output sums its K terms in the same order,
+    so the parameters and every state come out bit for bit the same (C4 settings,
+    bf16 SR, three steps)."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[apollo alone vs batched] {shape} beside {big}", flush=True)
+    kw = dict(C4_KW, stochastic_round_writeback=True)
+    runs = []
+    for with_big in (False, True):
+        shapes = [shape, big] if with_big else [shape]
+        ps = [torch.nn.Parameter(inputs.make_param(s, i, 23).to("cuda", torch.bfloat16)) for i, s in enumerate(shapes)]
+        opt = Adafactor8Bit(ps, **kw)
+        for t in range(1, 4):
+            for i, p in enumerate(ps):
+                p.grad = inputs.make_grad(shapes[i], i, t, 23, zero_frac=0.0).to("cuda", torch.bfloat16)
+            opt.step()
+        torch.cuda.synchronize()
+        runs.append((ps[0], opt))
+    (pa, oa), (pb, ob) = runs
+    assert torch.equal(pa, pb), "parameters differ"
+    sa, sb = oa.state[pa], ob.state[pb]
+    for k, v in sa.items():
+        if torch.is_tensor(v):
+            assert torch.equal(v, sb[k]), k

@@ -230,3 +230,52 @@ def test_apollo_variant_graph_replays_equal_eager_steps(variant):
             _same(ob, oc, pb, pc, f"{variant}: capturable eager vs default, step 3")
     assert _schedule(oa, pa) == _schedule(ob, pb)
     print(f"[apollo capture] {variant}: 6 replays equal", flush=True)
+
+
+@pytest.mark.gpu
+def test_apollo_checkpoint_of_replayed_steps_resumes():
+    """state_dict() after graph replays across a device projection refresh (steps 3-7,
+    refresh at 4 and 7) carries the step, the schedule and the cached P^T: a fresh
+    optimizer, capturable or default, that loads it continues (steps 8-9, no refresh)
+    with the bits of the uninterrupted capturable run."""
+    print("[apollo capture checkpoint]", flush=True)
+    pa, oa = _setup(True)   # replayed, then checkpointed
+    pr, orf = _setup(True)  # uninterrupted, eager
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pr, orf)):
+            _load(ps, t)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load(pa, 3)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for t in range(3, 8):
+        _load(pa, t)
+        graph.replay()
+        _load(pr, t)
+        orf.step()
+    torch.cuda.synchronize()
+    _same(oa, orf, pa, pr, "before the checkpoint")
+    sd = oa.state_dict()
+    assert {s["step"] for s in sd["state"].values()} == {7}
+    resumed = []
+    for capturable in (False, True):
+        pb, ob = _setup(capturable)
+        with torch.no_grad():
+            for a, b in zip(pa, pb):
+                b.copy_(a)
+        ob.load_state_dict(sd)
+        resumed.append((pb, ob))
+    for t in (8, 9):
+        for ps, o in [(pr, orf)] + resumed:
+            _load(ps, t)
+            o.step()
+    torch.cuda.synchronize()
+    for pb, ob in resumed:
+        _same(orf, ob, pr, pb, "resumed vs uninterrupted, step 9")
+    assert _schedule(orf, pr) == _schedule(resumed[0][1], resumed[0][0])

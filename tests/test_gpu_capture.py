@@ -214,3 +214,52 @@ def test_capturable_rejects_paths_with_host_scalars():
     with pytest.raises(NotImplementedError, match="apollo_update_proj_gap"):
         o.step()
     assert o.state[ps[0]]["step"] == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["c1_adamw", "c3_came_fira", "adamw_clip_fira_q1d", "sgd_uf8_clip_fira_bf16_sr"])
+def test_checkpoint_of_replayed_steps_resumes(name):
+    """state_dict() after graph replays (the step count lives on the device) loads
+    into a fresh optimizer, default or capturable, and the next two eager steps
+    give the bits of an uninterrupted default run (capturable steps equal default
+    ones on these paths)."""
+    _, kw, shapes, dtype, gkind = next(c for c in CASES if c[0] == name)
+    print(f"[capture checkpoint] {name}", flush=True)
+    pa, oa = _setup(kw, shapes, dtype, capturable=True)
+    pr, orf = _setup(kw, shapes, dtype)   # uninterrupted default run
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pr, orf)):
+            _load_grads(ps, t, gkind, dtype)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load_grads(pa, 3, gkind, dtype)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for t in (3, 4, 5):
+        _load_grads(pa, t, gkind, dtype)
+        graph.replay()
+        _load_grads(pr, t, gkind, dtype)
+        orf.step()
+    torch.cuda.synchronize()
+    sd = oa.state_dict()
+    assert {st["step"] for st in sd["state"].values()} == {5}
+    resumed = []
+    for extra in ({}, {"capturable": True}):
+        pb, ob = _setup(kw, shapes, dtype, **extra)
+        with torch.no_grad():
+            for a, b in zip(pa, pb):
+                b.copy_(a)
+        ob.load_state_dict(sd)
+        resumed.append((pb, ob))
+    for t in (6, 7):
+        for ps, o in [(pr, orf)] + resumed:
+            _load_grads(ps, t, gkind, dtype)
+            o.step()
+    torch.cuda.synchronize()
+    for pb, ob in resumed:
+        _same_state(orf, ob, pr, pb, f"{name}: resumed vs uninterrupted, step 7")

@@ -1962,8 +1962,10 @@ def _run_factored(opt, plans):
                  tuple(v.data_ptr() for v in pl.st.values() if torch.is_tensor(v)))
                 for pl, hp in zip(plans, has_prev))
     wsd = opt._ws.setdefault((dev, "tables2d"), {})
-    shapes = tuple(tuple(pl.g.shape) for pl in plans)
-    ent = wsd.get(shapes)
+    # one table per batch of parameters (two groups whose batches have the same
+    # shapes, an embedding and a head say, must not take turns re-uploading one)
+    tkey = tuple((pl.p.data_ptr(), tuple(pl.g.shape)) for pl in plans)
+    ent = wsd.get(tkey)
     upload = 0
     if ent is None or ent["sig"] != sig:
         sizes = []
@@ -2011,7 +2013,7 @@ def _run_factored(opt, plans):
         ent = {"sig": sig, "arr": arr, "ws": wbuf, "table": table, "n": n}
         if len(wsd) > 64:
             wsd.clear()
-        wsd[shapes] = ent
+        wsd[tkey] = ent
         upload = 1
     arr, table = ent["arr"], ent["table"]
     _no_upload_in_capture(upload)

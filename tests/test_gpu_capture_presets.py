@@ -7,7 +7,9 @@ full-rank fallback -- with the automatic quantisation profile (coded and fp32
 states side by side).  One optimizer over all of them runs with capturable=True:
 after two eager steps one step() is captured, and its replays must equal the
 eager steps of a twin optimizer bit for bit, parameters and every state, across
-APOLLO projection refreshes (apollo_update_proj_gap=3).
+APOLLO projection refreshes (apollo_update_proj_gap=3), for fp32 and for bf16
+parameters with stochastic rounding.  The same model also shows that parameters
+without a gradient take no step and leave the others' steps unchanged.
 """
 import pytest
 import torch
@@ -59,24 +61,27 @@ class _Model(nn.Module):
         self.lm_head = nn.Linear(H, V, bias=False)
 
 
-def _build(preset, capturable):
+def _build(preset, capturable, dtype=torch.float32, grads=True):
+    """The model in dtype (bf16: stochastic rounding on), its groups and the optimizer."""
     from adafactor8bit import Adafactor8Bit, build_param_groups
     model = _Model()
     with torch.no_grad():
         for i, p in enumerate(model.parameters()):
             p.copy_(make_param(tuple(p.shape), i, 37))
-    model = model.cuda()
+    model = model.to("cuda", dtype)
     params = list(model.parameters())
-    for p in params:
-        p.grad = torch.zeros_like(p)   # static gradient buffers: the graph reads these addresses
+    if grads:
+        for p in params:
+            p.grad = torch.zeros_like(p)   # static gradient buffers: the graph reads these addresses
     over = {"apollo_update_proj_gap": 3} if preset == "apollo" else {}
     groups = build_param_groups(model, preset, **over)
-    return params, Adafactor8Bit(groups, lr=1e-3, capturable=capturable)
+    return params, Adafactor8Bit(groups, lr=1e-3, capturable=capturable,
+                                 stochastic_round_writeback=dtype == torch.bfloat16)
 
 
 def _load(params, t):
     for i, p in enumerate(params):
-        p.grad.copy_(make_grad(tuple(p.shape), i, t, 37, zero_frac=0.0))
+        p.grad.copy_(make_grad(tuple(p.shape), i, t, 37, zero_frac=0.0).to(p.dtype))
 
 
 def _same(oa, ob, pa, pb, what):
@@ -90,11 +95,12 @@ def _same(oa, ob, pa, pb, what):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16_sr"])
 @pytest.mark.parametrize("preset", ["adafactor", "adamw", "rmsprop", "came", "sgd", "apollo"])
-def test_model_step_captured_for_every_preset(preset):
-    print(f"[capture preset] {preset}", flush=True)
-    pa, oa = _build(preset, True)   # replayed
-    pb, ob = _build(preset, True)   # eager
+def test_model_step_captured_for_every_preset(preset, dtype):
+    print(f"[capture preset] {preset} {dtype}", flush=True)
+    pa, oa = _build(preset, True, dtype)   # replayed
+    pb, ob = _build(preset, True, dtype)   # eager
     routes = sorted({tuple(sorted((k, str(v)) for k, v in g.items() if k != "params")) for g in oa.param_groups})
     print(f"  {len(oa.param_groups)} groups, {len(routes)} distinct option sets", flush=True)
     for t in (1, 2):
@@ -122,3 +128,43 @@ def test_model_step_captured_for_every_preset(preset):
         _same(oa, ob, pa, pb, f"{preset}: step {t}")
     sd = oa.state_dict()
     assert {st["step"] for st in sd["state"].values()} == {8}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("preset", ["adafactor", "came", "apollo"])
+def test_parameters_without_gradients_are_skipped(preset):
+    """A parameter whose .grad is None takes no step: its value and state stay as
+    they were, its step count included.  The others step exactly as in a run where
+    every parameter has its gradient (each parameter's update depends only on its
+    own state).  Here the layer-1 MLP has no gradient at steps 2 and 3."""
+    print(f"[no grad] {preset}", flush=True)
+    pa, oa = _build(preset, False, grads=False)   # layer-1 MLP skipped at steps 2, 3
+    pb, ob = _build(preset, False, grads=False)   # every parameter, every step
+    names = [n for n, _ in _Model().named_parameters()]
+    skip = {i for i, n in enumerate(names) if n.startswith("layers.1.mlp.")}
+    assert len(skip) == 3
+    for t in range(1, 5):
+        drop = t in (2, 3)
+        for ps, d in ((pa, drop), (pb, False)):
+            for i, p in enumerate(ps):
+                p.grad = None if (d and i in skip) else make_grad(tuple(p.shape), i, t, 37, zero_frac=0.0).cuda()
+        if drop:
+            before = {i: (pa[i].detach().clone(), oa.state[pa[i]]["step"],
+                          {k: v.clone() for k, v in oa.state[pa[i]].items() if torch.is_tensor(v)}) for i in skip}
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        if drop:
+            for i, (pv, stp, sv) in before.items():
+                assert torch.equal(pa[i], pv), (t, i)
+                assert oa.state[pa[i]]["step"] == stp, (t, i)
+                for k, v in sv.items():
+                    assert torch.equal(oa.state[pa[i]][k], v), (t, i, k)
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        if i in skip:
+            assert oa.state[a]["step"] == 2 and ob.state[b]["step"] == 4, i
+            continue
+        assert torch.equal(a, b), f"param {i} {names[i]}"
+        for k, v in oa.state[a].items():
+            if torch.is_tensor(v):
+                assert torch.equal(v, ob.state[b][k]), (i, k)

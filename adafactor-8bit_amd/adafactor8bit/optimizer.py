@@ -340,6 +340,11 @@ class Adafactor8Bit(Optimizer):
         ap_batches: Dict[tuple, list] = {}
         copy_back = []
         for p, g, st in zip(params, grads, states):
+            if p.numel() == 0:
+                # the reference's update of an empty tensor is a sequence of no-op tensor
+                # ops: the step is counted, nothing is launched
+                st["step"] = st.get("step", 0) + 1
+                continue
             if not p.is_contiguous():
                 # the reference steps a contiguous copy and writes it back (optimizer.py:2002-2007,
                 # 2608-2614); the copy is kept so workspaces keyed by the tensor stay valid

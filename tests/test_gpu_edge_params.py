@@ -1,0 +1,96 @@
+"""Edge-case parameter sets on the GPU.
+
+* Empty parameters (numel 0: shapes (0,), (0, 8), (8, 0), (2, 0, 3)) sit in a
+  group with ordinary ones under every update path -- quantised and fp32 1-D,
+  factored Adafactor and CAME, SGD, APOLLO -- and take steps without a launch
+  error, while the others step exactly as in an optimizer without them.
+* One optimizer holding bf16 matrices beside fp32 vectors (a model cast to bf16
+  with its norms kept in fp32) steps each parameter as an optimizer holding
+  only parameters of its dtype would.
+"""
+import pytest
+import torch
+
+from inputs import make_grad, make_param
+
+PATHS = {
+    "adamw_q1d": dict(beta1=0.9, beta2=0.999, beta2_decay=None, factored=False, relative_step=False,
+                      scale_parameter=False, d=0.0, lr=1e-3, block_size=256, m_block_size=64),
+    "adamw_fp32": dict(beta1=0.9, beta2=0.999, beta2_decay=None, factored=False, relative_step=False,
+                       scale_parameter=False, d=1.0, lr=1e-3, quantize=False),
+    "adafactor_factored": dict(beta1=None, beta2=None, beta2_decay=-0.8, factored=True, lr=1e-3, block_size=256),
+    "came": dict(beta1=0.9, beta2=0.999, beta2_decay=None, beta3=0.9999, factored=True, relative_step=False,
+                 lr=1e-3, block_size=256, d=1.0, enable_fira_for_adafactor=True),
+    "sgd_clip": dict(beta1=0.9, beta2=None, beta2_decay=None, factored=False, relative_step=False,
+                     scale_parameter=False, d=1.0, lr=1e-2, block_size=256, m_block_size=64),
+    "apollo": dict(beta1=0.9, beta2=0.999, beta2_decay=None, factored=False, relative_step=False,
+                   scale_parameter=False, d=0.0, lr=1e-3, apollo_rank=16, block_size=256, m_block_size=64),
+}
+SHAPES = [(300, 200), (1000,), (64, 96)]
+EMPTY = [(0,), (0, 8), (8, 0), (2, 0, 3)]
+
+
+def _params(shapes, seed, dtype=torch.float32):
+    return [torch.nn.Parameter(make_param(s, i, seed).to("cuda", dtype)) if 0 not in s else
+            torch.nn.Parameter(torch.zeros(s, device="cuda", dtype=dtype)) for i, s in enumerate(shapes)]
+
+
+def _grads(ps, t, seed):
+    for i, p in enumerate(ps):
+        p.grad = (make_grad(tuple(p.shape), i, t, seed, zero_frac=0.0).to("cuda", p.dtype) if p.numel() else
+                  torch.zeros_like(p))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_empty_parameters_step_beside_ordinary_ones(path):
+    from adafactor8bit import Adafactor8Bit
+    print(f"[empty params] {path}", flush=True)
+    kw = PATHS[path]
+    pa = _params(SHAPES + EMPTY, 41)
+    pb = _params(SHAPES, 41)
+    oa = Adafactor8Bit(pa, **kw)
+    ob = Adafactor8Bit(pb, **kw)
+    for t in range(1, 4):
+        _grads(pa, t, 41)
+        _grads(pb, t, 41)
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(pa[:len(SHAPES)], pb)):
+        assert torch.equal(a, b), f"{path}: param {i}"
+    for p in pa[len(SHAPES):]:
+        assert p.numel() == 0 and oa.state[p]["step"] == 3
+    # the state of the mixed set round-trips through a checkpoint and steps on
+    sd = oa.state_dict()
+    oc = Adafactor8Bit(pa, **kw)
+    oc.load_state_dict(sd)
+    _grads(pa, 4, 41)
+    _grads(pb, 4, 41)
+    oc.step()
+    ob.step()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(pa[:len(SHAPES)], pb)):
+        assert torch.equal(a, b), f"{path}: param {i} after the checkpoint"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["adamw_q1d", "adafactor_factored", "apollo"])
+def test_bf16_matrices_beside_fp32_vectors(path):
+    """Matrices in bf16 (stochastic rounding) and vectors in fp32 in one group; each
+    steps as in an optimizer holding only its own dtype's parameters."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[mixed dtypes] {path}", flush=True)
+    kw = dict(PATHS[path], stochastic_round_writeback=True)
+    mats, vecs = [(300, 200), (64, 96)], [(1000,), (256,)]
+    m1, v1 = _params(mats, 43, torch.bfloat16), _params(vecs, 44)
+    m2, v2 = _params(mats, 43, torch.bfloat16), _params(vecs, 44)
+    both = Adafactor8Bit(m1 + v1, **kw)
+    only_m, only_v = Adafactor8Bit(m2, **kw), Adafactor8Bit(v2, **kw)
+    for t in range(1, 4):
+        _grads(m1, t, 43); _grads(v1, t, 44)
+        _grads(m2, t, 43); _grads(v2, t, 44)
+        both.step(); only_m.step(); only_v.step()
+    torch.cuda.synchronize()
+    for a, b in zip(m1 + v1, m2 + v2):
+        assert a.dtype == b.dtype and torch.equal(a, b), tuple(a.shape)

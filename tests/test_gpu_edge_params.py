@@ -7,6 +7,7 @@
 * One optimizer holding bf16 matrices beside fp32 vectors (a model cast to bf16
   with its norms kept in fp32) steps each parameter as an optimizer holding
   only parameters of its dtype would.
+* A quantised 1-D tensor past 2^31 elements steps as its two halves do.
 """
 import pytest
 import torch
@@ -94,3 +95,37 @@ def test_bf16_matrices_beside_fp32_vectors(path):
     torch.cuda.synchronize()
     for a, b in zip(m1 + v1, m2 + v2):
         assert a.dtype == b.dtype and torch.equal(a, b), tuple(a.shape)
+
+
+@pytest.mark.gpu
+def test_quantised_1d_step_past_2_31_elements():
+    """A tensor of 2^31 + 8192 elements (AdamW UF8 / AL8, B_V 2048, B_M 256) steps as
+    its two block-aligned halves stepped as separate tensors do: the update is
+    elementwise inside blocks, so the bits must agree whatever the element index's
+    width.  (About 40 GB of device memory.)"""
+    from adafactor8bit import Adafactor8Bit
+    n1 = 1 << 31
+    n = n1 + 8192
+    print(f"[2^31] one tensor of {n} elements against two halves", flush=True)
+    kw = dict(PATHS["adamw_q1d"], block_size=2048, m_block_size=256)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    big = torch.nn.Parameter(torch.randn(n, device="cuda", generator=gen) * 0.02)
+    halves = [torch.nn.Parameter(big.detach()[:n1].clone()), torch.nn.Parameter(big.detach()[n1:].clone())]
+    oa = Adafactor8Bit([big], **kw)
+    ob = Adafactor8Bit(halves, **kw)
+    for t in range(2):
+        g = torch.randn(n, device="cuda", generator=gen) * 1e-3
+        big.grad = g
+        halves[0].grad = g[:n1].clone()
+        halves[1].grad = g[n1:].clone()
+        del g
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        assert torch.equal(big.detach()[:n1], halves[0].detach()), f"step {t + 1}: first half"
+        assert torch.equal(big.detach()[n1:], halves[1].detach()), f"step {t + 1}: second half"
+    sa, sb0, sb1 = oa.state[big], ob.state[halves[0]], ob.state[halves[1]]
+    for k in ("variance_q", "m_q"):   # codes, stored as [blocks, block] views
+        assert torch.equal(sa[k].reshape(-1), torch.cat([sb0[k].reshape(-1), sb1[k].reshape(-1)])), k
+    print("[2^31] equal after two steps", flush=True)

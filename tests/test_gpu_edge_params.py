@@ -129,3 +129,37 @@ def test_quantised_1d_step_past_2_31_elements():
     for k in ("variance_q", "m_q"):   # codes, stored as [blocks, block] views
         assert torch.equal(sa[k].reshape(-1), torch.cat([sb0[k].reshape(-1), sb1[k].reshape(-1)])), k
     print("[2^31] equal after two steps", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["adamw_q1d", "adamw_fp32", "came", "sgd_clip", "apollo"])
+def test_hyperparameter_changes_take_effect(path):
+    """group["lr"] and group["weight_decay"] changed between steps reach the next
+    launch (no cached table or batch keeps the old ones): the run equals one that
+    resumes from the step-2 checkpoint in a new optimizer built with the new values."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[hyper change] {path}", flush=True)
+    kw = dict(PATHS[path], weight_decay=0.01)
+    new = dict(lr=kw["lr"] * 0.37, weight_decay=0.05)
+    pa = _params(SHAPES, 45)
+    pb = _params(SHAPES, 45)
+    oa = Adafactor8Bit(pa, **kw)
+    ob = Adafactor8Bit(pb, **kw)
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _grads(ps, t, 45)
+            o.step()
+    for g in oa.param_groups:
+        g.update(new)
+    sd = ob.state_dict()
+    oc = Adafactor8Bit(pb, **dict(kw, **new))
+    oc.load_state_dict(sd)
+    for g in oc.param_groups:   # a loaded checkpoint brings its own group options back
+        g.update(new)
+    for t in (3, 4):
+        for ps, o in ((pa, oa), (pb, oc)):
+            _grads(ps, t, 45)
+            o.step()
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        assert torch.equal(a, b), f"{path}: param {i}"

@@ -8,6 +8,9 @@
   with its norms kept in fp32) steps each parameter as an optimizer holding
   only parameters of its dtype would.
 * A quantised 1-D tensor past 2^31 elements steps as its two halves do.
+* lr and weight decay changed between steps reach the next launch.
+* A group added with add_param_group mid-run steps on its own count and can be
+  captured together with the first group.
 """
 import pytest
 import torch
@@ -163,3 +166,57 @@ def test_hyperparameter_changes_take_effect(path):
     torch.cuda.synchronize()
     for i, (a, b) in enumerate(zip(pa, pb)):
         assert torch.equal(a, b), f"{path}: param {i}"
+
+
+@pytest.mark.gpu
+def test_group_added_mid_run_steps_and_captures():
+    """add_param_group after two steps: the new group starts its own count and state,
+    the old group is unaffected, and once both have taken an eager step a capturable
+    optimizer's step (both groups) is captured and replays bit-identically to eager
+    steps of a twin."""
+    from adafactor8bit import Adafactor8Bit
+    print("[add_param_group]", flush=True)
+    kw = dict(PATHS["adamw_q1d"], capturable=True)
+    runs = []
+    for _ in range(2):
+        p0 = _params([(300, 200), (1000,)], 47)
+        p1 = _params([(64, 96), (2048,)], 48)
+        for p in p0 + p1:
+            p.grad = torch.zeros_like(p)
+        o = Adafactor8Bit(p0, **kw)
+        for t in (1, 2):
+            _fill(p0, t, 47)
+            o.step()
+        o.add_param_group({"params": p1, "lr": 5e-4})
+        _fill(p0, 3, 47)
+        _fill(p1, 3, 48)
+        o.step()
+        runs.append((p0, p1, o))
+    (a0, a1, oa), (b0, b1, ob) = runs
+    assert {oa.state[p]["step"] for p in a0} == {3} and {oa.state[p]["step"] for p in a1} == {1}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _fill(a0, 4, 47)
+        _fill(a1, 4, 48)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    for t in range(4, 7):
+        _fill(a0, t, 47)
+        _fill(a1, t, 48)
+        graph.replay()
+        _fill(b0, t, 47)
+        _fill(b1, t, 48)
+        ob.step()
+        torch.cuda.synchronize()
+        for a, b in zip(a0 + a1, b0 + b1):
+            assert torch.equal(a, b), (t, tuple(a.shape))
+    sd = oa.state_dict()["state"]
+    assert sorted({s["step"] for s in sd.values()}) == [4, 6]
+
+
+def _fill(ps, t, seed):
+    for i, p in enumerate(ps):
+        p.grad.copy_(make_grad(tuple(p.shape), i, t, seed, zero_frac=0.0).to(p.dtype))

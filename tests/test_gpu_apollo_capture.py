@@ -279,3 +279,39 @@ def test_apollo_checkpoint_of_replayed_steps_resumes():
     for pb, ob in resumed:
         _same(orf, ob, pr, pb, "resumed vs uninterrupted, step 9")
     assert _schedule(orf, pr) == _schedule(resumed[0][1], resumed[0][0])
+
+
+@pytest.mark.gpu
+def test_apollo_replays_interleaved_with_eager_steps_and_checkpoints():
+    """C4 APOLLO replays mixed with eager steps and a state_dict() between them (it
+    copies the device schedule back), across the device refreshes at steps 4 and 7:
+    the run equals eager steps of a twin."""
+    print("[apollo capture interleaved]", flush=True)
+    pa, oa = _setup(True)
+    pb, ob = _setup(True)
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load(ps, t)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load(pa, 3)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    for t in range(3, 10):
+        _load(pa, t)
+        if t % 2:
+            graph.replay()
+        else:
+            oa.step()
+        if t in (4, 7):
+            sd = oa.state_dict()["state"]
+            assert {s["step"] for s in sd.values()} == {t}
+        _load(pb, t)
+        ob.step()
+        torch.cuda.synchronize()
+        _same(oa, ob, pa, pb, f"step {t}")
+    assert _schedule(oa, pa) == _schedule(ob, pb)

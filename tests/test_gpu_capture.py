@@ -263,3 +263,39 @@ def test_checkpoint_of_replayed_steps_resumes(name):
     torch.cuda.synchronize()
     for pb, ob in resumed:
         _same_state(orf, ob, pr, pb, f"{name}: resumed vs uninterrupted, step 7")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["c1_adamw", "c3_came_fira", "adamw_clip_fira_q1d"])
+def test_replays_interleaved_with_eager_steps_and_checkpoints(name):
+    """Replays of a captured step mixed with eager step() calls of the same optimizer,
+    with state_dict() taken in between (it reads the device count back): every step
+    advances the one device count, and the run equals six eager steps of a twin."""
+    _, kw, shapes, dtype, gkind = next(c for c in CASES if c[0] == name)
+    print(f"[capture interleaved] {name}", flush=True)
+    pa, oa = _setup(kw, shapes, dtype, capturable=True)
+    pb, ob = _setup(kw, shapes, dtype, capturable=True)
+    for t in (1, 2):
+        for ps, o in ((pa, oa), (pb, ob)):
+            _load_grads(ps, t, gkind, dtype)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _load_grads(pa, 3, gkind, dtype)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    for t in range(3, 7):
+        _load_grads(pa, t, gkind, dtype)
+        if t % 2:
+            graph.replay()
+        else:
+            oa.step()
+        if t == 4:
+            assert {st["step"] for st in oa.state_dict()["state"].values()} == {4}
+        _load_grads(pb, t, gkind, dtype)
+        ob.step()
+        torch.cuda.synchronize()
+        _same_state(oa, ob, pa, pb, f"{name}: step {t}")

@@ -74,9 +74,13 @@ class Adafactor8Bit(Optimizer):
     and launches only multi-tensor kernels that read them, so ``step()`` can be
     captured in a CUDA/HIP graph after one eager step and replayed; eager and
     replayed steps run the same kernels on the same inputs, so they give the same
-    bits.  Paths that need host-side scalars (APOLLO, LAG, per-tensor launches,
-    tensor learning rates) raise in this mode.  ``state_dict()`` reads the device
-    counts back.
+    bits.  APOLLO schedules its projection refreshes on the device (it needs
+    apollo_update_proj_gap > 0), and a tensor learning rate is read on the device
+    at every replay.  Parameters that need a per-tensor launch raise in this mode.
+    ``state_dict()`` reads the device counts and schedules back.  A graph holds the
+    addresses of the state and buffers it was captured with: after
+    ``load_state_dict()``, ``add_param_group()`` or a parameter's first step, run
+    one eager step and capture again instead of replaying the old graph.
     """
 
     def __init__(

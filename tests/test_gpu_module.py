@@ -170,3 +170,60 @@ def test_module_lag_is_noclip_at_the_lagged_scale(full):
     torch.cuda.synchronize()
     for k in keys:
         assert torch.equal(sl[k], sn[k]), ("momentum-only", k)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("full", [False, True], ids=["quantised", "fp32_state"])
+def test_module_momentum_only_lag_divides_u(full):
+    """Momentum-only LAG (kernels.cu:651-655, 1305-1309): the lagged factor divides U
+    before the momentum EMA, and the step stays alpha.  With numel 4096 (sqrtf(numel)
+    = 64 exactly), d = 1 and a previous norm of 512 the factor is 8 exactly, which is
+    APPLY's factor for norm_buf = 512^2: the two passes give the same bits."""
+    from adafactor8bit import adafactor8bit_cuda as K
+    from adafactor8bit import _state as S
+    print(f"[module] momentum-only lag full={full}", flush=True)
+    shape, bs, mbs = (64, 64), 2048, 256
+    n = 4096
+    K.set_qmap(*[q.cuda() for q in K.qmaps()])
+    g = make_grad(shape, 0, 1, 6).cuda()
+    p0 = make_param(shape, 0, 6).cuda()
+    alpha = torch.tensor([1e-3], dtype=torch.float32, device="cuda")
+    eps1 = 1e-8
+    eps_sq = max(eps1 * eps1, 1.17549435e-38)
+    lfl = math.log2(eps_sq)
+
+    def fresh():
+        st = {"p": p0.clone()}
+        if full:
+            st["v"] = torch.full(shape, 1e-6, dtype=torch.float32, device="cuda")
+            st["m"] = torch.full(shape, 1e-4, dtype=torch.float32, device="cuda")
+        else:
+            S.new_al_slot(st, "variance", shape, bs, "al8", "cuda")
+            S.new_momentum_codes(st, "m", n, mbs, "uf8", "cuda")
+        return st
+
+    prev = torch.tensor([512.0], dtype=torch.float32, device="cuda")
+    nb_apply = torch.tensor([512.0 * 512.0], dtype=torch.float32, device="cuda")
+    sl, sa = fresh(), fresh()
+    nbl = torch.zeros(1, dtype=torch.float32, device="cuda")
+    if full:
+        common = (0.9, 1.0 - 0.999, eps_sq, 0.0, False, eps1, n)
+        K.fused_update_1d_full_lag(sl["p"], g, sl["v"], sl["m"], nbl, alpha, prev, *common, 1.0, True)
+        # the three-pass flow: NORM writes V (and, momentum-only, leaves M), APPLY reads it
+        K.fused_update_1d_full_norm(g, sa["v"], sa["m"], torch.zeros(1, dtype=torch.float32, device="cuda"),
+                                    *common, True)
+        K.fused_update_1d_full_apply(sa["p"], g, sa["v"], sa["m"], nb_apply, alpha, *common, 1.0, True)
+        keys = ("p", "v", "m")
+    else:
+        tail = (0.9, 1.0 - 0.999, 0.0, False, lfl, eps1, n, bs, mbs, 8, 0)
+        ql = (sl["m_q"], sl["m_scale"], sl["variance_q"], sl["variance_scale"], sl["variance_min_log"])
+        qa = (sa["m_q"], sa["m_scale"], sa["variance_q"], sa["variance_scale"], sa["variance_min_log"])
+        K.fused_update_1d_lag(sl["p"], g, *ql, nbl, alpha, prev, *tail, 1.0, 8, True)
+        vb = torch.empty(n, dtype=torch.float32, device="cuda")
+        K.fused_update_1d_norm(g, *qa, vb, torch.zeros(1, dtype=torch.float32, device="cuda"), *tail, 8, True)
+        K.fused_update_1d_apply(sa["p"], g, *qa, vb, nb_apply, alpha, *tail, 1.0, 8, True)
+        keys = ("p", "m_q", "m_scale", "variance_q", "variance_scale", "variance_min_log")
+    torch.cuda.synchronize()
+    for k in keys:
+        assert torch.equal(sl[k], sa[k]), k
+    assert not torch.equal(sl["p"], p0)

@@ -240,6 +240,7 @@ struct F2 {
   float eps_came;
   float d;
   float sqrt_nd;    // (float)(sqrt(n) * d)
+  float sqrt_nf;    // sqrtf((float)n): the CUDA kernels' sqrt_numel (the lagged clip)
   int mq;           // momentum: 0 none, 1 quantised, 2 fp32
   int mk;           // codec of quantised momentum (1 UF8, 2 UF4, 3 D8, 4 D4)
   int lbm;          // log2 of the momentum block
@@ -405,7 +406,8 @@ __global__ __launch_bounds__(256) void k_f2d(F2 a) {
     if constexpr (OP == F_APPLY) {
       if (a.d > 0.0f) step = al / fmaxf(1.0f, sqrtf(*a.norm_buf) / a.sqrt_nd);
     } else if constexpr (OP == F_LAG) {
-      if (a.d > 0.0f) step = al / fmaxf(1.0f, *a.prev_norm / a.sqrt_nd);
+      // LAG has no CPU branch: the CUDA kernels' pn / (sqrt_numel * d) in fp32 (kernels.cu:1562-1565)
+      if (a.d > 0.0f) step = al / fmaxf(1.0f, *a.prev_norm / (a.sqrt_nf * a.d));
     }
     f2_write<T>(a, e0, cnt, step, u);
     if (a.mq == 2 && OP != F_CAME2) store8<float>(a.m, e0, n, m);
@@ -1140,6 +1142,7 @@ int a8_factored_prim(int op, int dtype, int stochastic, const a8_factored_prim_a
   a.R = p.rows; a.C = p.cols; a.n = p.numel; a.sr_seed = p.sr_seed; a.sr_step = p.sr_step;
   a.w_m = (float)(1.0 - p.beta1); a.eps_came = p.eps_came; a.d = p.d;
   a.sqrt_nd = (float)(sqrt((double)p.numel) * (double)p.d);
+  a.sqrt_nf = sqrtf((float)p.numel);
   a.sr = stochastic && dtype != A8_F32;
   a.lbm = 5;
   const bool writes_p = op == F_NOCLIP || op == F_APPLY || op == F_LAG || op == F_CAME2;

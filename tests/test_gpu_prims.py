@@ -171,7 +171,8 @@ def test_update_2d_lag_and_sums():
     K.fused_update_2d_full_lag(pg.view(-1), gg, None, row.cuda(), col.cuda(), rmean.cuda(), nb, a_t, prev, 0.0, R,
                                C, n, 256, 1.0)
     u = (g * inv_row) * inv_col
-    denom = max(1.0, 3.0e3 / (math.sqrt(n) * 1.0))
+    # the CUDA kernels' fp32 denominator pn / (sqrtf(numel) * d) (kernels.cu:1562-1565)
+    denom = max(np.float32(1.0), np.float32(3.0e3) / (np.sqrt(np.float32(n)) * np.float32(1.0)))
     want = p.add(u, alpha=-(torch.tensor(0.01) / torch.tensor(denom, dtype=torch.float32)).item())
     torch.cuda.synchronize()
     np.testing.assert_allclose(pg.cpu().numpy(), want.numpy(), rtol=1e-6, atol=1e-9)

@@ -299,3 +299,44 @@ def test_replays_interleaved_with_eager_steps_and_checkpoints(name):
         ob.step()
         torch.cuda.synchronize()
         _same_state(oa, ob, pa, pb, f"{name}: step {t}")
+
+
+@pytest.mark.gpu
+def test_two_optimizers_in_two_graphs():
+    """Two capturable optimizers (AdamW quantised 1-D and CAME factored) captured in
+    two graphs and replayed alternately: each equals the eager steps of its twin
+    (the library's table staging, codebooks and step blocks are shared by none of
+    their captured launches)."""
+    print("[capture] two optimizers, two graphs", flush=True)
+    c1 = next(c for c in CASES if c[0] == "c1_adamw")
+    c3 = next(c for c in CASES if c[0] == "c3_came_fira")
+    sets = []
+    for _, kw, shapes, dtype, gkind in (c1, c3):
+        pa, oa = _setup(kw, shapes, dtype, capturable=True)
+        pb, ob = _setup(kw, shapes, dtype, capturable=True)
+        sets.append((pa, oa, pb, ob, dtype, gkind))
+    for t in (1, 2):
+        for pa, oa, pb, ob, dtype, gkind in sets:
+            for ps, o in ((pa, oa), (pb, ob)):
+                _load_grads(ps, t, gkind, dtype)
+                o.step()
+    graphs = []
+    for pa, oa, _, _, dtype, gkind in sets:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            _load_grads(pa, 3, gkind, dtype)
+            with torch.cuda.graph(graph):
+                oa.step()
+        torch.cuda.current_stream().wait_stream(side)
+        graphs.append(graph)
+    for t in range(3, 7):
+        for (pa, oa, pb, ob, dtype, gkind), graph in zip(sets, graphs):
+            _load_grads(pa, t, gkind, dtype)
+            graph.replay()
+            _load_grads(pb, t, gkind, dtype)
+            ob.step()
+        torch.cuda.synchronize()
+        for pa, oa, pb, ob, _, _ in sets:
+            _same_state(oa, ob, pa, pb, f"step {t}")

@@ -349,9 +349,20 @@ class Adafactor8Bit(Optimizer):
                 # ops: the step is counted, nothing is launched
                 st["step"] = st.get("step", 0) + 1
                 continue
-            if not p.is_contiguous():
+            if g.data_ptr() % 16:
+                # the kernels load 16 bytes at a time: a gradient that starts off a 16-byte
+                # boundary (a slice of a flat buffer) is copied to one kept per parameter
+                key = (g.device, "galign", id(p))
+                gw = self._ws.get(key)
+                if gw is None or gw.shape != g.shape or gw.dtype != g.dtype:
+                    gw = torch.empty(g.shape, dtype=g.dtype, device=g.device)
+                    self._ws[key] = gw
+                gw.copy_(g)
+                g = gw
+            if not p.is_contiguous() or p.data_ptr() % 16:
                 # the reference steps a contiguous copy and writes it back (optimizer.py:2002-2007,
-                # 2608-2614); the copy is kept so workspaces keyed by the tensor stay valid
+                # 2608-2614); the copy is kept so workspaces keyed by the tensor stay valid.  A
+                # parameter that starts off a 16-byte boundary steps an aligned copy the same way
                 key = (p.device, "contig", id(p))
                 work = self._ws.get(key)
                 if work is None or work.shape != p.shape or work.dtype != p.dtype:

@@ -11,6 +11,8 @@
 * lr and weight decay changed between steps reach the next launch.
 * A group added with add_param_group mid-run steps on its own count and can be
   captured together with the first group.
+* Parameters and gradients that are views into flat buffers starting off a 16-byte
+  boundary step as aligned copies of them do, eagerly and captured.
 """
 import pytest
 import torch
@@ -220,3 +222,96 @@ def test_group_added_mid_run_steps_and_captures():
 def _fill(ps, t, seed):
     for i, p in enumerate(ps):
         p.grad.copy_(make_grad(tuple(p.shape), i, t, seed, zero_frac=0.0).to(p.dtype))
+
+
+def _flat_views(shapes, dtype, seed=None):
+    """Views into one flat buffer, each starting one element past a 16-byte boundary
+    (element offsets 1 mod 8: off for fp32 and for bf16), with gaps between them."""
+    offs, o = [], 1
+    for s in shapes:
+        offs.append(o)
+        o += (torch.Size(s).numel() + 7) // 8 * 8 + 8
+    flat = torch.zeros(o, device="cuda", dtype=dtype)
+    views = [flat[a:a + torch.Size(s).numel()].view(s) for a, s in zip(offs, shapes)]
+    if seed is not None:
+        for i, (v, s) in enumerate(zip(views, shapes)):
+            v.copy_(make_param(s, i, seed).to(v.dtype))
+    return flat, views
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16_sr"])
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_parameters_off_16_byte_boundaries(path, dtype):
+    """Parameters and gradients that are views into flat buffers starting off a 16-byte
+    boundary step exactly as aligned copies of them do; the results land in the flat
+    parameter buffer and its gaps stay untouched."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[misaligned] {path} {dtype}", flush=True)
+    kw = dict(PATHS[path], stochastic_round_writeback=dtype == torch.bfloat16)
+    pflat, views = _flat_views(SHAPES, dtype, seed=49)
+    gflat, gviews = _flat_views(SHAPES, dtype)
+    pa = [torch.nn.Parameter(v) for v in views]
+    assert all(p.data_ptr() % 16 for p in pa) and all(p.data_ptr() == v.data_ptr() for p, v in zip(pa, views))
+    pb = _params(SHAPES, 49, dtype)
+    oa, ob = Adafactor8Bit(pa, **kw), Adafactor8Bit(pb, **kw)
+    for t in range(1, 4):
+        for i, (p, gv) in enumerate(zip(pa, gviews)):
+            gv.copy_(make_grad(tuple(p.shape), i, t, 49, zero_frac=0.0).to(dtype))
+            p.grad = gv
+        _grads(pb, t, 49)
+        oa.step()
+        ob.step()
+    torch.cuda.synchronize()
+    gaps = torch.ones_like(pflat, dtype=torch.bool)
+    for i, (a, b, v) in enumerate(zip(pa, pb, views)):
+        assert torch.equal(a, b) and torch.equal(v, b), f"{path}: param {i}"
+        for k, s in oa.state[a].items():
+            if torch.is_tensor(s):
+                assert torch.equal(s, ob.state[b][k]), f"{path}: param {i} {k}"
+        a0 = (v.data_ptr() - pflat.data_ptr()) // pflat.element_size()
+        gaps[a0:a0 + v.numel()] = False
+    assert not pflat[gaps].any(), "a write outside the parameters"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["adamw_q1d", "came", "sgd_clip", "apollo"])
+def test_parameters_off_16_byte_boundaries_capture(path):
+    """Misaligned bf16 views (parameters and gradients) in a capturable optimizer: the
+    aligned copies are kept per parameter, so the step is captured and its replays
+    equal eager steps of a twin on the same views."""
+    from adafactor8bit import Adafactor8Bit
+    print(f"[misaligned capture] {path}", flush=True)
+    kw = dict(PATHS[path], stochastic_round_writeback=True, capturable=True)
+    sets = []
+    for _ in range(2):
+        _, views = _flat_views(SHAPES, torch.bfloat16, seed=51)
+        _, gviews = _flat_views(SHAPES, torch.bfloat16)
+        ps = [torch.nn.Parameter(v) for v in views]
+        for p, gv in zip(ps, gviews):
+            p.grad = gv
+        sets.append((ps, Adafactor8Bit(ps, **kw)))
+    (pa, oa), (pb, ob) = sets
+    for t in (1, 2):
+        for ps, o in sets:
+            _fill(ps, t, 51)
+            o.step()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        _fill(pa, 3, 51)
+        with torch.cuda.graph(graph):
+            oa.step()
+    torch.cuda.current_stream().wait_stream(side)
+    for t in range(3, 7):
+        _fill(pa, t, 51)
+        graph.replay()
+        _fill(pb, t, 51)
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            assert torch.equal(a, b), (path, t, i)
+            for k, s in oa.state[a].items():
+                if torch.is_tensor(s):
+                    assert torch.equal(s, ob.state[b][k]), (path, t, i, k)
